@@ -1,0 +1,89 @@
+/*
+ * nsq_hip.h - C ABI of the MI355X (gfx950) Hyena long-convolution library.
+ *
+ * Plain C: pointers, sizes and an opaque stream handle (a hipStream_t passed as
+ * void*; NULL = the default stream).  Every call is asynchronous on that stream,
+ * performs no host synchronisation and no device allocation: the caller owns
+ * every input, output and workspace buffer (size the workspace with the
+ * matching *_workspace_bytes call).  The library owns only an immutable
+ * per-device twiddle table built by nsq_init() or lazily on first use.
+ *
+ * Status: 0 (NSQ_OK) on success, otherwise an NSQ_ERR_* code with a message
+ * available from nsq_last_error() (thread-local).
+ *
+ * Tensor layouts are row-major and contiguous:
+ *   x, y, g, gx : [B, H, L]  in `dtype` (NSQ_DTYPE_*)
+ *   k, gk       : [H, K]     float32 (a shared filter; the Python layer
+ *                            squeezes the reference's [1, H, K])
+ *   shortcut    : [H]        in `dtype` (may be NULL: no shortcut term)
+ *   gs          : [H]        float32 (may be NULL when shortcut is NULL)
+ */
+#ifndef NSQ_HIP_H_
+#define NSQ_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSQ_ABI_VERSION 1
+
+enum {
+  NSQ_OK = 0,
+  NSQ_ERR_INVALID_ARGUMENT = 1,
+  NSQ_ERR_UNSUPPORTED = 2,
+  NSQ_ERR_HIP = 3
+};
+
+enum { NSQ_DTYPE_F32 = 0, NSQ_DTYPE_BF16 = 1, NSQ_DTYPE_F16 = 2 };
+
+enum { NSQ_DIR_FWD = 0, NSQ_DIR_BWD = 1 };
+
+/* Library version of this ABI (NSQ_ABI_VERSION). */
+int nsq_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* nsq_last_error(void);
+
+/* Builds the twiddle table for the current device (optional: done lazily). */
+int nsq_init(void);
+
+/*
+ * 1D causal FFT convolution (+ per-channel shortcut), fused
+ *   pad -> real FFT -> x filter spectrum -> inverse FFT -> crop -> cast -> + s*x.
+ *
+ * Replaces the native kernel the reference binds at
+ *   nvsubquadratic/ops/fftconv_custom.py:286-304  (_subq_causal_conv1d_bhl ->
+ *   subquadratic_ops_torch.fft_causal_conv1d(x, w)) together with the shortcut
+ *   epilogue of causal_fftconv1d_bhl, fftconv_custom.py:307-335.
+ * Results follow the reference torch.fft path
+ *   nvsubquadratic/ops/fftconv.py:546-600 (causal_fftconv1d_fp32_bhl):
+ *   y[b,h,n] = sum_m k[h,m] x[b,h,n-m] over the FFT length min(L+K, 2L), i.e.
+ *   including the circular wrap-around that length implies when K > L+1.
+ * Requires 1 <= K <= 2L.
+ */
+size_t nsq_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int direction);
+
+int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype,
+                             int64_t B, int64_t H, int64_t L, int64_t K, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
+ * Backward of nsq_fftconv1d_causal_fwd given the upstream gradient g:
+ *   gx = cast(corr(g, k)) + s*g,  gk[h] = sum_b corr(g_b, x_b)[0:K] (fp32),
+ *   gs[h] = sum_{b,n} g*x (fp32).
+ * This is the adjoint autograd derives for the reference path
+ *   (nvsubquadratic/ops/fftconv.py:583-599; the external kernel's autograd
+ *   exercised by tests/ops/test_fftconv_custom_1d.py:183-200).
+ */
+int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
+                             float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSQ_HIP_H_ */

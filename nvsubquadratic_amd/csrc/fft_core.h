@@ -1,0 +1,284 @@
+// Device building blocks for LDS-resident Stockham FFTs on gfx950.
+//
+// Design (CDNA4, wave64):
+//  * A workgroup holds a tile of M independent power-of-two transforms in LDS
+//    and each thread owns E = M*N/T complex points per pass (E = 16 in every
+//    kernel of this library, i.e. 32 VGPRs of data).
+//  * Each Stockham pass reads R points per butterfly, multiplies by the pass
+//    twiddles, runs an in-register radix-R DFT (R <= 16, unrolled radix-2
+//    DIT with trivial roots special-cased) and writes the autosorted result.
+//    The output of the last pass is in natural order, so no bit reversal.
+//  * The first pass may read from global memory and the last pass may write
+//    to global memory through functors, so a transform that starts and ends
+//    in HBM costs only (passes - 1) LDS round trips.
+//  * Twiddles come from the table built in twiddle.hip (double-precision
+//    roots rounded once); no sin/cos evaluation and no recurrences on device.
+#pragma once
+
+#include <type_traits>
+
+#include "nsq_common.h"
+
+namespace nsq {
+
+// ---------------------------------------------------------------------------
+// Complex helpers (float2 = re, im)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+  return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+// a * conj(b)
+__device__ __forceinline__ float2 cmulc(float2 a, float2 b) {
+  return make_float2(a.x * b.x + a.y * b.y, a.y * b.x - a.x * b.y);
+}
+__device__ __forceinline__ float2 cconj(float2 a) { return make_float2(a.x, -a.y); }
+__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
+__device__ __forceinline__ float2 mul_i(float2 a) { return make_float2(-a.y, a.x); }
+__device__ __forceinline__ float2 mul_neg_i(float2 a) { return make_float2(a.y, -a.x); }
+
+// ---------------------------------------------------------------------------
+// Roots of unity from the table.  W_{2^LOGB}^m, forward sign.
+// ---------------------------------------------------------------------------
+template <int LOGB>
+__device__ __forceinline__ float2 root(const float2* __restrict__ tw, uint32_t m) {
+  static_assert(LOGB >= 0 && LOGB <= 28, "root: size out of range");
+  if constexpr (LOGB <= 14) {
+    return tw[m << (14 - LOGB)];
+  } else {
+    uint32_t idx = m << (28 - LOGB);
+    return cmul(tw[idx >> 14], tw[(1u << 14) + (idx & ((1u << 14) - 1))]);
+  }
+}
+
+// Runtime-size variant (logb in [0, 28]).
+__device__ __forceinline__ float2 root_rt(const float2* __restrict__ tw, uint32_t m, int logb) {
+  if (logb <= 14) return tw[m << (14 - logb)];
+  uint32_t idx = m << (28 - logb);
+  return cmul(tw[idx >> 14], tw[(1u << 14) + (idx & ((1u << 14) - 1))]);
+}
+
+// ---------------------------------------------------------------------------
+// Compile-time loop
+// ---------------------------------------------------------------------------
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Multiply by the constant root W_R^K (forward) or its conjugate (INV).
+template <int R, int K, bool INV>
+__device__ __forceinline__ float2 const_twiddle(float2 a) {
+  constexpr int K16 = K * (16 / R);  // angle in units of 2*pi/16, K16 in [0, 8)
+  static_assert(K16 >= 0 && K16 < 8, "const_twiddle: K out of range");
+  constexpr float r2 = 0.70710678118654752440f;  // cos(pi/4)
+  if constexpr (K16 == 0) {
+    return a;
+  } else if constexpr (K16 == 4) {
+    return INV ? mul_i(a) : mul_neg_i(a);
+  } else if constexpr (K16 == 2) {
+    // forward (1 - i)/sqrt2, inverse (1 + i)/sqrt2
+    return INV ? make_float2(r2 * (a.x - a.y), r2 * (a.y + a.x))
+               : make_float2(r2 * (a.x + a.y), r2 * (a.y - a.x));
+  } else if constexpr (K16 == 6) {
+    // forward (-1 - i)/sqrt2, inverse (-1 + i)/sqrt2
+    return INV ? make_float2(-r2 * (a.x + a.y), r2 * (a.x - a.y))
+               : make_float2(r2 * (a.y - a.x), -r2 * (a.x + a.y));
+  } else {
+    // cos/sin of k*pi/8 for k = 1, 3, 5, 7
+    constexpr float c = (K16 == 1) ? 0.92387953251128675613f
+                      : (K16 == 3) ? 0.38268343236508977173f
+                      : (K16 == 5) ? -0.38268343236508977173f
+                                   : -0.92387953251128675613f;
+    constexpr float s = (K16 == 1 || K16 == 7) ? 0.38268343236508977173f : 0.92387953251128675613f;
+    // forward multiplies by (c - i s), inverse by (c + i s)
+    return INV ? make_float2(a.x * c - a.y * s, a.y * c + a.x * s)
+               : make_float2(a.x * c + a.y * s, a.y * c - a.x * s);
+  }
+}
+
+// In-register DFT of R = 2, 4, 8 or 16 points, natural order in and out.
+// Forward: X[k] = sum_n v[n] W_R^{nk}; INV uses conjugate roots (unscaled).
+template <int R, bool INV>
+__device__ __forceinline__ void dft(float2* v) {
+  if constexpr (R == 1) {
+    return;
+  } else if constexpr (R == 2) {
+    float2 a = v[0], b = v[1];
+    v[0] = cadd(a, b);
+    v[1] = csub(a, b);
+  } else if constexpr (R == 4) {
+    float2 t0 = cadd(v[0], v[2]);
+    float2 t1 = csub(v[0], v[2]);
+    float2 t2 = cadd(v[1], v[3]);
+    float2 d = csub(v[1], v[3]);
+    float2 t3 = INV ? mul_i(d) : mul_neg_i(d);
+    v[0] = cadd(t0, t2);
+    v[2] = csub(t0, t2);
+    v[1] = cadd(t1, t3);
+    v[3] = csub(t1, t3);
+  } else {
+    float2 e[R / 2], o[R / 2];
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) {
+      e[i] = v[2 * i];
+      o[i] = v[2 * i + 1];
+    }
+    dft<R / 2, INV>(e);
+    dft<R / 2, INV>(o);
+    static_for<0, R / 2>([&](auto kk) {
+      constexpr int k = decltype(kk)::value;
+      float2 t = const_twiddle<R, k, INV>(o[k]);
+      v[k] = cadd(e[k], t);
+      v[k + R / 2] = csub(e[k], t);
+    });
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One radix-2^LOGR Stockham pass over M transforms of length 2^LOGN executed by
+// T threads.  LD(m, n) -> float2 reads input element n of transform m; ST(m, n,
+// v) writes output element n.  LOGNS = log2 of the sub-transform length already
+// done (0 for the first pass).  Barriers bracket the write phase so LD and ST
+// may alias the same LDS buffer.
+// ---------------------------------------------------------------------------
+template <int LOGN, int LOGR, int LOGNS, bool INV, int M, int T, class LD, class ST>
+__device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __restrict__ tw) {
+  constexpr int R = 1 << LOGR;
+  constexpr int NR = 1 << (LOGN - LOGR);
+  constexpr int NS = 1 << LOGNS;
+  constexpr int PER = (M * NR) / T;
+  static_assert((M * NR) % T == 0, "stockham_pass: tile not divisible by threads");
+  static_assert(LOGNS + LOGR <= 14, "stockham_pass: transform too long for the coarse table");
+  const int tid = threadIdx.x;
+  float2 v[PER][R];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int bf = tid + i * T;
+    const int m = bf >> (LOGN - LOGR);
+    const int j = bf & (NR - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[i][r] = ld(m, j + r * NR);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int bf = tid + i * T;
+    const int m = bf >> (LOGN - LOGR);
+    const int j = bf & (NR - 1);
+    const int k = j & (NS - 1);
+    if constexpr (LOGNS > 0) {
+#pragma unroll
+      for (int r = 1; r < R; ++r) {
+        float2 w = tw[(r * k) << (14 - LOGNS - LOGR)];
+        if (INV) w.y = -w.y;
+        v[i][r] = cmul(v[i][r], w);
+      }
+    }
+    dft<R, INV>(v[i]);
+    const int base = ((j - k) << LOGR) + k;
+#pragma unroll
+    for (int r = 0; r < R; ++r) st(m, base + r * NS, v[i][r]);
+  }
+  __syncthreads();
+}
+
+template <int LOGN, int LOGNS, bool INV, int M, int T, class LDF, class STL, class LDL, class STF>
+__device__ __forceinline__ void fft_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last,
+                                        const float2* __restrict__ tw) {
+  constexpr int REM = LOGN - LOGNS;
+  constexpr int LOGR = REM < 4 ? REM : 4;
+  constexpr bool FIRST = (LOGNS == 0);
+  constexpr bool LAST = (LOGNS + LOGR == LOGN);
+  if constexpr (FIRST && LAST) {
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_first, st_last, tw);
+  } else if constexpr (FIRST) {
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_first, st_lds, tw);
+    fft_rec<LOGN, LOGNS + LOGR, INV, M, T>(ld_first, st_lds, ld_lds, st_last, tw);
+  } else if constexpr (LAST) {
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_lds, st_last, tw);
+  } else {
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_lds, st_lds, tw);
+    fft_rec<LOGN, LOGNS + LOGR, INV, M, T>(ld_first, st_lds, ld_lds, st_last, tw);
+  }
+}
+
+// Full transform of M length-2^LOGN sequences.  Passes 2..n-1 run in `lds`
+// (transform m at lds[m*S ...]); the first pass reads through ld_first and the
+// last pass writes through st_last.  Ends with a barrier.
+template <int LOGN, bool INV, int M, int T, int S, class LDF, class STF>
+__device__ __forceinline__ void fft(float2* lds, LDF& ld_first, STF& st_last, const float2* __restrict__ tw) {
+  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + n]; };
+  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + n] = v; };
+  fft_rec<LOGN, 0, INV, M, T>(ld_first, st_lds, ld_lds, st_last, tw);
+}
+
+// Transform that starts and ends in LDS.
+template <int LOGN, bool INV, int M, int T, int S>
+__device__ __forceinline__ void fft_lds(float2* lds, const float2* __restrict__ tw) {
+  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + n]; };
+  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + n] = v; };
+  fft_rec<LOGN, 0, INV, M, T>(ld_lds, st_lds, ld_lds, st_lds, tw);
+}
+
+// ---------------------------------------------------------------------------
+// Real-FFT packing.  A real sequence u[0, 2N) is packed as z[n] = u[2n] +
+// i*u[2n+1]; Z = FFT_N(z).  The real spectrum U[0..N] is handled in "slots":
+//   slot p in [1, N/2): (A, Bc) = (U[p], conj(U[N-p]))
+//   slot 0:             A = (U[0], U[N]) (two reals), Bc = U[N/2]
+// With this representation forward products are slot-wise A1*A2, Bc1*Bc2 and
+// correlations A1*conj(A2), Bc1*conj(Bc2), except slot 0's A whose two reals
+// multiply separately.
+// ---------------------------------------------------------------------------
+// zp = Z[p], zq = Z[N-p] (for p = 0: zp = Z[0], zq = Z[N/2]); w = W_{2N}^p.
+__device__ __forceinline__ void real_unpack(bool slot0, float2 zp, float2 zq, float2 w, float2& A, float2& Bc) {
+  if (slot0) {
+    A = make_float2(zp.x + zp.y, zp.x - zp.y);
+    Bc = cconj(zq);
+  } else {
+    float2 bc = cconj(zq);
+    float2 fe = cscale(cadd(zp, bc), 0.5f);
+    float2 fo = mul_neg_i(cscale(csub(zp, bc), 0.5f));
+    float2 wfo = cmul(w, fo);
+    A = cadd(fe, wfo);
+    Bc = csub(fe, wfo);
+  }
+}
+
+// Inverse of real_unpack for a Hermitian spectrum given in slot form; returns
+// the values to place at Z[p] and Z[N-p] (slot 0: Z[0] and Z[N/2]) so that the
+// unscaled inverse FFT_N gives N * (u[2n] + i u[2n+1]).
+__device__ __forceinline__ void real_repack(bool slot0, float2 A, float2 Bc, float2 w, float2& zp, float2& zq) {
+  if (slot0) {
+    zp = make_float2(0.5f * (A.x + A.y), 0.5f * (A.x - A.y));
+    zq = cconj(Bc);
+  } else {
+    float2 fe = cscale(cadd(A, Bc), 0.5f);
+    float2 fo = cmulc(cscale(csub(A, Bc), 0.5f), w);  // * conj(w)
+    zp = cadd(fe, mul_i(fo));
+    zq = cadd(cconj(fe), mul_i(cconj(fo)));
+  }
+}
+
+__device__ __forceinline__ float2 slot_mul(bool slot0_a, float2 a, float2 b) {
+  return slot0_a ? make_float2(a.x * b.x, a.y * b.y) : cmul(a, b);
+}
+__device__ __forceinline__ float2 slot_mulc(bool slot0_a, float2 a, float2 b) {
+  return slot0_a ? make_float2(a.x * b.x, a.y * b.y) : cmulc(a, b);
+}
+
+// ---------------------------------------------------------------------------
+// Pair load of a real row: (u[i], u[i+1]) with zeros outside [0, valid).
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float2 load_pair(const typename Elem<DT>::T* __restrict__ row, int64_t i, int64_t valid) {
+  float a = (i < valid) ? Elem<DT>::load(row, i) : 0.f;
+  float b = (i + 1 < valid) ? Elem<DT>::load(row, i + 1) : 0.f;
+  return make_float2(a, b);
+}
+
+}  // namespace nsq

@@ -1,0 +1,108 @@
+// C ABI entry points of the causal 1D FFT convolution (see include/nsq_hip.h).
+// Kernels and plans live in fftconv1d_impl.h; the per-dtype instantiations are
+// compiled in fftconv1d_f32.hip / fftconv1d_bf16.hip / fftconv1d_f16.hip.
+#include "fftconv1d_impl.h"
+
+namespace nsq {
+
+static int validate(const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H, int64_t L,
+                    int64_t K, Plan1D& p) {
+  NSQ_CHECK_ARG(a && b && k, "fftconv1d_causal: null tensor pointer");
+  NSQ_CHECK_ARG(valid_dtype(dtype), "fftconv1d_causal: unsupported dtype code %d", dtype);
+  NSQ_CHECK_ARG(B >= 1 && H >= 1 && L >= 1 && K >= 1, "fftconv1d_causal: sizes must be positive (B=%lld H=%lld L=%lld K=%lld)",
+                (long long)B, (long long)H, (long long)L, (long long)K);
+  NSQ_CHECK_ARG(K <= 2 * L, "fftconv1d_causal: kernel length %lld exceeds 2*seq_len=%lld", (long long)K,
+                (long long)(2 * L));
+  NSQ_CHECK_ARG(B * H <= 0x7fffffff && L <= (int64_t(1) << 30), "fftconv1d_causal: tensor too large");
+  if (!make_plan(L, K, p)) {
+    set_error("fftconv1d_causal: unsupported (L=%lld, K=%lld): FFT length beyond 2^23 or K > L+1 above the fused size",
+              (long long)L, (long long)K);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  return NSQ_OK;
+}
+
+}  // namespace nsq
+
+using namespace nsq;
+
+extern "C" {
+
+size_t nsq_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int direction) {
+  Plan1D p;
+  if (!make_plan(L, K, p) || p.fused) return 0;
+  const int64_t N = int64_t(1) << p.logN;
+  const int64_t rows = (direction == NSQ_DIR_BWD) ? (2 * B * H + H) : (B * H + H);
+  return size_t(rows * N) * sizeof(float2);
+}
+
+int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                             int64_t H, int64_t L, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  Plan1D p;
+  int rc = validate(x, y, k, dtype, B, H, L, K, p);
+  if (rc) return rc;
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  float2* ws = nullptr;
+  if (!p.fused) {
+    const size_t need = nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, NSQ_DIR_FWD);
+    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv1d_causal_fwd: workspace of %zu bytes required, got %zu",
+                  need, workspace_bytes);
+    ws = (float2*)workspace;
+  }
+  bool ok = false;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      ok = run_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, tw, st);
+      break;
+    case NSQ_DTYPE_BF16:
+      ok = run_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, tw, st);
+      break;
+    default:
+      ok = run_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, tw, st);
+      break;
+  }
+  NSQ_CHECK_ARG(ok, "fftconv1d_causal_fwd: no kernel for logN=%d", p.logN);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                             float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  clear_error();
+  Plan1D p;
+  int rc = validate(g, x, k, dtype, B, H, L, K, p);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(gx && gk, "fftconv1d_causal_bwd: null gradient output pointer");
+  NSQ_CHECK_ARG(!shortcut || gs, "fftconv1d_causal_bwd: gs required when a shortcut is given");
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  float2* ws = nullptr;
+  if (!p.fused) {
+    const size_t need = nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, NSQ_DIR_BWD);
+    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv1d_causal_bwd: workspace of %zu bytes required, got %zu",
+                  need, workspace_bytes);
+    ws = (float2*)workspace;
+  }
+  bool ok = false;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      ok = run_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, tw, st);
+      break;
+    case NSQ_DTYPE_BF16:
+      ok = run_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, tw, st);
+      break;
+    default:
+      ok = run_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, tw, st);
+      break;
+  }
+  NSQ_CHECK_ARG(ok, "fftconv1d_causal_bwd: no kernel for logN=%d", p.logN);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+}  // extern "C"

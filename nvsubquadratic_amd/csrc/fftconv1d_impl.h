@@ -1,0 +1,737 @@
+// Causal 1D FFT convolution (forward and backward) for gfx950.
+//
+// Semantics: nvsubquadratic/ops/fftconv.py:546-600 (causal_fftconv1d_fp32_bhl)
+// with the wrapper epilogue of nvsubquadratic/ops/fftconv_custom.py:307-335.
+//
+// Two execution plans, chosen by the FFT length F (a power of two, real):
+//
+//  * fused  (F <= 16384): one workgroup owns M channels.  It transforms the
+//    filter once (spectrum kept in registers, slot-owned by each thread), then
+//    for each batch row: real FFT of x in LDS -> spectral product -> inverse
+//    FFT -> crop/cast/shortcut epilogue straight to HBM.  HBM traffic is the
+//    algorithmic minimum (x, k read once; y written once).
+//  * 4-step (2^15 <= F <= 2^23): the packed complex length N = F/2 is split as
+//    N = N1 x N2 (Cooley-Tukey).  Three kernels:
+//      col_fwd  : length-N1 DFTs down the columns of each signal (x, k, g),
+//                 times the twiddle W_N^{n2 k1}, to a workspace;
+//      row      : length-N2 DFTs along rows k1 and N1-k1 (the rows that hold
+//                 the Hermitian partners k and N-k), real-spectrum unpack,
+//                 spectral product / correlation, repack, inverse row DFT,
+//                 times W_N^{-n2 k1}, written back in place;
+//      col_inv  : inverse length-N1 DFTs down the columns, crop and epilogue.
+//
+// Real signals of length F are packed as z[n] = u[2n] + i u[2n+1] (N = F/2
+// complex points); see real_unpack/real_repack in fft_core.h.
+#pragma once
+
+#include "fft_core.h"
+
+namespace nsq {
+
+// ===========================================================================
+// Plan selection
+// ===========================================================================
+struct Plan1D {
+  int logF;   // real FFT length 2^logF
+  int logN;   // packed complex length, logF - 1
+  bool fold;  // K > L+1: reference length 2L wraps; fold full[n + 2L] into y[n]
+  bool fused;
+  int logN1, logN2;  // 4-step split (fused == false)
+};
+
+inline bool make_plan(int64_t L, int64_t K, Plan1D& p) {
+  if (L < 1 || K < 1 || K > 2 * L) return false;
+  p.fold = K > L + 1;
+  int64_t need = p.fold ? 3 * L : L + K - 1;
+  int logF = ilog2_ceil(need);
+  if (logF < 4) logF = 4;
+  p.logF = logF;
+  p.logN = logF - 1;
+  p.fused = p.logN <= 13;
+  if (!p.fused) {
+    if (p.fold || p.logN > 22) return false;
+    p.logN1 = p.logN / 2 < 10 ? p.logN / 2 : 10;
+    p.logN2 = p.logN - p.logN1;
+  } else {
+    p.logN1 = p.logN2 = 0;
+  }
+  return true;
+}
+
+// ===========================================================================
+// Fused plan
+// ===========================================================================
+template <int LOGN>
+struct FusedCfg {
+  static constexpr int N = 1 << LOGN;
+  static constexpr int M = LOGN >= 11 ? 1 : (2048 >> LOGN);  // channels per workgroup
+  static constexpr int TILE = M * N;
+  static constexpr int T = TILE / 16;                          // threads
+  static constexpr int E = 16;                                 // points per thread
+  static constexpr int SLOTS = E / 2;                          // spectral slots per thread
+};
+
+// Slot s of the tile -> (transform m, slot p within the transform).
+template <int LOGN>
+__device__ __forceinline__ void slot_of(int s, int& m, int& p) {
+  m = s >> (LOGN - 1);
+  p = s & ((1 << (LOGN - 1)) - 1);
+}
+
+// Reads the packed real spectrum of transform m / slot p out of `z` (natural
+// order, stride N per transform) in slot form.
+template <int LOGN>
+__device__ __forceinline__ void lds_unpack(const float2* z, int m, int p, const float2* __restrict__ tw,
+                                           float2& A, float2& Bc) {
+  constexpr int N = 1 << LOGN;
+  const float2* zz = z + m * N;
+  const bool s0 = (p == 0);
+  float2 zp = zz[p];
+  float2 zq = zz[s0 ? N / 2 : N - p];
+  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p);
+  real_unpack(s0, zp, zq, w, A, Bc);
+}
+
+template <int LOGN>
+__device__ __forceinline__ void lds_repack(float2* z, int m, int p, const float2* __restrict__ tw, float2 A,
+                                           float2 Bc) {
+  constexpr int N = 1 << LOGN;
+  float2* zz = z + m * N;
+  const bool s0 = (p == 0);
+  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p);
+  float2 zp, zq;
+  real_repack(s0, A, Bc, w, zp, zq);
+  zz[p] = zp;
+  zz[s0 ? N / 2 : N - p] = zq;
+}
+
+// Filter spectrum of channels h0..h0+M-1 into per-thread slot registers.
+// `lds` must hold a tile; leaves it free (ends with a barrier).
+template <int LOGN>
+__device__ __forceinline__ void filter_spectrum(float2* lds, const float* __restrict__ k, int h0, int H, int K,
+                                                const float2* __restrict__ tw, float2* hA, float2* hB) {
+  using C = FusedCfg<LOGN>;
+  auto ld = [&](int m, int n) -> float2 {
+    const int h = h0 + m;
+    if (h >= H) return make_float2(0.f, 0.f);
+    return load_pair<NSQ_DTYPE_F32>(k + int64_t(h) * K, 2 * int64_t(n), K);
+  };
+  auto st = [&](int m, int n, float2 v) { lds[m * C::N + n] = v; };
+  fft<LOGN, false, C::M, C::T, C::N>(lds, ld, st, tw);
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    int m, p;
+    slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+    lds_unpack<LOGN>(lds, m, p, tw, hA[i], hB[i]);
+  }
+  __syncthreads();
+}
+
+// Forward, fused plan.  grid = (ceil(H/M), nb_split); each workgroup handles
+// batch rows [b0, b0 + b_per_wg).
+template <int LOGN, int DT, bool FOLD>
+__global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
+    const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ k,
+    const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ y, int B, int H, int L,
+    int K, int b_per_wg, const float2* __restrict__ tw) {
+  using C = FusedCfg<LOGN>;
+  __shared__ float2 lds[C::TILE];
+  const int h0 = blockIdx.x * C::M;
+  const int b0 = blockIdx.y * b_per_wg;
+  const int b1 = min(B, b0 + b_per_wg);
+
+  float2 hA[C::SLOTS], hB[C::SLOTS];
+  filter_spectrum<LOGN>(lds, k, h0, H, K, tw, hA, hB);
+
+  const float scale = 1.f / float(C::N);
+  for (int b = b0; b < b1; ++b) {
+    auto ld = [&](int m, int n) -> float2 {
+      const int h = h0 + m;
+      if (h >= H) return make_float2(0.f, 0.f);
+      return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
+    };
+    auto st = [&](int m, int n, float2 v) { lds[m * C::N + n] = v; };
+    fft<LOGN, false, C::M, C::T, C::N>(lds, ld, st, tw);
+#pragma unroll
+    for (int i = 0; i < C::SLOTS; ++i) {
+      int m, p;
+      slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+      float2 A, Bc;
+      lds_unpack<LOGN>(lds, m, p, tw, A, Bc);
+      A = slot_mul(p == 0, A, hA[i]);
+      Bc = cmul(Bc, hB[i]);
+      lds_repack<LOGN>(lds, m, p, tw, A, Bc);
+    }
+    __syncthreads();
+
+    auto epi = [&](int m, int n, float2 v) {
+      const int h = h0 + m;
+      if (h >= H) return;
+      const int64_t row = (int64_t(b) * H + h) * L;
+      const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
+      const int64_t i0 = 2 * int64_t(n);
+      if (i0 < L) Elem<DT>::store(y, row + i0, epilogue<DT>(v.x * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0) : 0.f));
+      if (i0 + 1 < L)
+        Elem<DT>::store(y, row + i0 + 1,
+                        epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0 + 1) : 0.f));
+    };
+    if constexpr (!FOLD) {
+      auto ldl = [&](int m, int n) -> float2 { return lds[m * C::N + n]; };
+      fft<LOGN, true, C::M, C::T, C::N>(lds, ldl, epi, tw);
+    } else {
+      fft_lds<LOGN, true, C::M, C::T, C::N>(lds, tw);
+      // y[j] = full[j] + full[j + 2L]; in packed units index n and n + L.
+      for (int e = threadIdx.x; e < C::TILE; e += C::T) {
+        const int m = e >> LOGN, n = e & (C::N - 1);
+        if (2 * n >= L) continue;
+        float2 v = lds[m * C::N + n];
+        if (n + L < C::N) v = cadd(v, lds[m * C::N + n + L]);
+        epi(m, n, v);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Backward, fused plan.  grid = ceil(H/M); each workgroup loops over all
+// batch rows (the filter gradient sums over the batch in a fixed order).
+template <int LOGN, int DT, bool FOLD>
+__global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
+    const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x,
+    const float* __restrict__ k, const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ gx,
+    float* __restrict__ gk, float* __restrict__ gs, int B, int H, int L, int K, const float2* __restrict__ tw) {
+  using C = FusedCfg<LOGN>;
+  __shared__ float2 ldsG[C::TILE];
+  __shared__ float2 ldsX[C::TILE];
+  const int h0 = blockIdx.x * C::M;
+
+  float2 hA[C::SLOTS], hB[C::SLOTS];
+  filter_spectrum<LOGN>(ldsG, k, h0, H, K, tw, hA, hB);
+  float2 qA[C::SLOTS], qB[C::SLOTS];
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) qA[i] = qB[i] = make_float2(0.f, 0.f);
+
+  const float scale = 1.f / float(C::N);
+  for (int b = 0; b < B; ++b) {
+    // g extended by its adjoint fold copy at offset 2L (FOLD only).
+    auto ldg = [&](int m, int n) -> float2 {
+      const int h = h0 + m;
+      if (h >= H) return make_float2(0.f, 0.f);
+      const typename Elem<DT>::T* row = g + (int64_t(b) * H + h) * L;
+      const int64_t i0 = 2 * int64_t(n);
+      if (FOLD && i0 >= 2 * int64_t(L)) return load_pair<DT>(row, i0 - 2 * int64_t(L), L);
+      return load_pair<DT>(row, i0, L);
+    };
+    auto ldx = [&](int m, int n) -> float2 {
+      const int h = h0 + m;
+      if (h >= H) return make_float2(0.f, 0.f);
+      return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
+    };
+    auto stG = [&](int m, int n, float2 v) { ldsG[m * C::N + n] = v; };
+    auto stX = [&](int m, int n, float2 v) { ldsX[m * C::N + n] = v; };
+    fft<LOGN, false, C::M, C::T, C::N>(ldsG, ldg, stG, tw);
+    fft<LOGN, false, C::M, C::T, C::N>(ldsX, ldx, stX, tw);
+#pragma unroll
+    for (int i = 0; i < C::SLOTS; ++i) {
+      int m, p;
+      slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+      float2 GA, GB, XA, XB;
+      lds_unpack<LOGN>(ldsG, m, p, tw, GA, GB);
+      lds_unpack<LOGN>(ldsX, m, p, tw, XA, XB);
+      const bool s0 = (p == 0);
+      qA[i] = cadd(qA[i], slot_mulc(s0, GA, XA));
+      qB[i] = cadd(qB[i], cmulc(GB, XB));
+      lds_repack<LOGN>(ldsG, m, p, tw, slot_mulc(s0, GA, hA[i]), cmulc(GB, hB[i]));
+    }
+    __syncthreads();
+    auto epi = [&](int m, int n, float2 v) {
+      const int h = h0 + m;
+      if (h >= H) return;
+      const int64_t row = (int64_t(b) * H + h) * L;
+      const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
+      const int64_t i0 = 2 * int64_t(n);
+      if (i0 < L)
+        Elem<DT>::store(gx, row + i0, epilogue<DT>(v.x * scale, s != nullptr, sv, s ? Elem<DT>::load(g, row + i0) : 0.f));
+      if (i0 + 1 < L)
+        Elem<DT>::store(gx, row + i0 + 1,
+                        epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(g, row + i0 + 1) : 0.f));
+    };
+    auto ldl = [&](int m, int n) -> float2 { return ldsG[m * C::N + n]; };
+    fft<LOGN, true, C::M, C::T, C::N>(ldsG, ldl, epi, tw);
+  }
+
+  // Filter gradient (and shortcut gradient = its lag-0 value).
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    int m, p;
+    slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+    lds_repack<LOGN>(ldsX, m, p, tw, qA[i], qB[i]);
+  }
+  __syncthreads();
+  auto epik = [&](int m, int n, float2 v) {
+    const int h = h0 + m;
+    if (h >= H) return;
+    const int64_t i0 = 2 * int64_t(n);
+    if (i0 < K) gk[int64_t(h) * K + i0] = v.x * scale;
+    if (i0 + 1 < K) gk[int64_t(h) * K + i0 + 1] = v.y * scale;
+    if (n == 0 && gs) gs[h] = v.x * scale;
+  };
+  auto ldl = [&](int m, int n) -> float2 { return ldsX[m * C::N + n]; };
+  fft<LOGN, true, C::M, C::T, C::N>(ldsX, ldl, epik, tw);
+}
+
+// ===========================================================================
+// 4-step plan
+// ===========================================================================
+// Column kernels: a workgroup owns COLS adjacent columns of one signal row.
+constexpr int kCols = 16;
+
+template <int LOGN1>
+struct ColCfg {
+  static constexpr int N1 = 1 << LOGN1;
+  static constexpr int S = N1 + 1;  // padded column stride in LDS
+  static constexpr int TILE = kCols * N1;
+  static constexpr int T = TILE / 16;
+};
+
+// Description of a real input signal set: `rows` rows of `valid` samples with
+// row stride `stride` (elements), zero-extended to length F.
+template <int DT>
+struct RealRows {
+  const typename Elem<DT>::T* p;
+  int64_t stride;
+  int64_t valid;
+};
+
+// col_fwd: A[row][k1][n2] = W_N^{n2 k1} * sum_{n1} z[N2 n1 + n2] W_{N1}^{n1 k1}
+// grid = (rows, N2 / kCols).
+template <int LOGN1, int LOGN, int DT>
+__global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_fwd_kernel(RealRows<DT> src, float2* __restrict__ ws,
+                                                                    const float2* __restrict__ tw) {
+  using C = ColCfg<LOGN1>;
+  constexpr int LOGN2 = LOGN - LOGN1;
+  constexpr int N2 = 1 << LOGN2;
+  __shared__ float2 lds[kCols * C::S];
+  const int c0 = blockIdx.y * kCols;
+  const int64_t row = blockIdx.x;
+  const typename Elem<DT>::T* in = src.p + row * src.stride;
+  // Coalesced load: consecutive threads take consecutive columns of one n1.
+  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
+    const int c = e % kCols, n1 = e / kCols;
+    const int64_t m = int64_t(n1) * N2 + c0 + c;  // packed index
+    lds[c * C::S + n1] = load_pair<DT>(in, 2 * m, src.valid);
+  }
+  __syncthreads();
+  fft_lds<LOGN1, false, kCols, C::T, C::S>(lds, tw);
+  float2* out = ws + row * (int64_t(1) << LOGN);
+  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
+    const int c = e % kCols, k1 = e / kCols;
+    const uint32_t n2 = c0 + c;
+    float2 v = cmul(lds[c * C::S + k1], root<LOGN>(tw, n2 * uint32_t(k1)));
+    out[int64_t(k1) * N2 + n2] = v;
+  }
+}
+
+// col_inv: z[N2 n1 + n2] = sum_{k1} B[row][k1][n2] W_{N1}^{-n1 k1}, then the
+// epilogue functor consumes packed output index m = N2 n1 + n2.
+template <int LOGN1, int LOGN, class EPI>
+__device__ __forceinline__ void col_inv_body(const float2* __restrict__ ws_row, int c0, EPI& epi,
+                                             const float2* __restrict__ tw, float2* lds) {
+  using C = ColCfg<LOGN1>;
+  constexpr int N2 = 1 << (LOGN - LOGN1);
+  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
+    const int c = e % kCols, k1 = e / kCols;
+    lds[c * C::S + k1] = ws_row[int64_t(k1) * N2 + c0 + c];
+  }
+  __syncthreads();
+  fft_lds<LOGN1, true, kCols, C::T, C::S>(lds, tw);
+  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
+    const int c = e % kCols, n1 = e / kCols;
+    epi(int64_t(n1) * N2 + c0 + c, lds[c * C::S + n1]);
+  }
+}
+
+// Output epilogue for y (forward) or gx (backward): out = epi(conv, s, aux)
+// where aux is x (forward) or g (backward).  grid = (B*H, N2/kCols).
+template <int LOGN1, int LOGN, int DT>
+__global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_inv_out_kernel(
+    const float2* __restrict__ ws, const typename Elem<DT>::T* __restrict__ aux,
+    const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ out, int H, int L,
+    const float2* __restrict__ tw) {
+  using C = ColCfg<LOGN1>;
+  __shared__ float2 lds[kCols * C::S];
+  const int64_t row = blockIdx.x;
+  const int h = int(row % H);
+  const float scale = 1.f / float(int64_t(1) << LOGN);
+  const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
+  const int64_t base = row * L;
+  auto epi = [&](int64_t m, float2 v) {
+    const int64_t i0 = 2 * m;
+    if (i0 < L) Elem<DT>::store(out, base + i0, epilogue<DT>(v.x * scale, s != nullptr, sv, s ? Elem<DT>::load(aux, base + i0) : 0.f));
+    if (i0 + 1 < L)
+      Elem<DT>::store(out, base + i0 + 1,
+                      epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(aux, base + i0 + 1) : 0.f));
+  };
+  col_inv_body<LOGN1, LOGN>(ws + row * (int64_t(1) << LOGN), blockIdx.y * kCols, epi, tw, lds);
+}
+
+// Filter-gradient epilogue: gk[h, 0:K] fp32, gs[h] = lag-0 value.  grid = (H, N2/kCols).
+template <int LOGN1, int LOGN>
+__global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_inv_gk_kernel(const float2* __restrict__ ws,
+                                                                       float* __restrict__ gk, float* __restrict__ gs,
+                                                                       int K, const float2* __restrict__ tw) {
+  using C = ColCfg<LOGN1>;
+  __shared__ float2 lds[kCols * C::S];
+  const int64_t h = blockIdx.x;
+  const float scale = 1.f / float(int64_t(1) << LOGN);
+  auto epi = [&](int64_t m, float2 v) {
+    const int64_t i0 = 2 * m;
+    if (i0 < K) gk[h * K + i0] = v.x * scale;
+    if (i0 + 1 < K) gk[h * K + i0 + 1] = v.y * scale;
+    if (m == 0 && gs) gs[h] = v.x * scale;
+  };
+  col_inv_body<LOGN1, LOGN>(ws + h * (int64_t(1) << LOGN), blockIdx.y * kCols, epi, tw, lds);
+}
+
+// Row kernels.  Workgroup q handles the row pair {q, N1-q} (q >= 1) or the two
+// self-paired rows {0, N1/2} (q == 0) of one channel; a tile is 2 rows of N2.
+template <int LOGN2>
+struct RowCfg {
+  static constexpr int N2 = 1 << LOGN2;
+  static constexpr int TILE = 2 * N2;
+  static constexpr int T = TILE / 16;
+  static constexpr int SLOTS = 8;  // N2 slots per workgroup / T threads
+};
+
+// Slot s in [0, N2) of row-pair q -> LDS positions (tile-relative) of the two
+// bins, the bin index kA = k of the first (for the twiddle W_F^k), and the
+// special slot flag (bins 0/N and N/2).
+template <int LOGN1, int LOGN2>
+__device__ __forceinline__ void row_slot(int q, int s, int& posA, int& posB, uint32_t& kA, bool& s0) {
+  constexpr int N1 = 1 << LOGN1, N2 = 1 << LOGN2;
+  s0 = false;
+  if (q > 0) {
+    posA = s;                      // row q, k2 = s
+    posB = N2 + (N2 - 1 - s);      // row N1-q, k2 = N2-1-s
+    kA = uint32_t(q) + uint32_t(N1) * uint32_t(s);
+  } else if (s < N2 / 2) {
+    // row 0: bins N1*k2, partner N1*(N2-k2)
+    if (s == 0) {
+      s0 = true;
+      posA = 0;        // bin 0
+      posB = N2 / 2;   // bin N/2 = N1 * N2/2
+      kA = 0;
+    } else {
+      posA = s;
+      posB = N2 - s;
+      kA = uint32_t(N1) * uint32_t(s);
+    }
+  } else {
+    // row N1/2: bins N1/2 + N1*k2, partner k2' = N2-1-k2
+    const int s2 = s - N2 / 2;
+    posA = N2 + s2;
+    posB = N2 + (N2 - 1 - s2);
+    kA = uint32_t(N1 / 2) + uint32_t(N1) * uint32_t(s2);
+  }
+}
+
+// Loads the two rows of the pair into a tile: tile row 0 = row q (or 0), tile
+// row 1 = row N1-q (or N1/2), then forward row DFTs; spectrum in natural order.
+template <int LOGN1, int LOGN2>
+__device__ __forceinline__ void row_pair_fft(float2* lds, const float2* __restrict__ sig, int q,
+                                             const float2* __restrict__ tw) {
+  using C = RowCfg<LOGN2>;
+  constexpr int N1 = 1 << LOGN1;
+  const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
+  auto ld = [&](int m, int n) -> float2 { return sig[int64_t(m == 0 ? ra : rb) * C::N2 + n]; };
+  auto st = [&](int m, int n, float2 v) { lds[m * C::N2 + n] = v; };
+  fft<LOGN2, false, 2, C::T, C::N2>(lds, ld, st, tw);
+}
+
+// Inverse row DFT of the tile, twiddle W_N^{-n2 k1}, store to sig rows.
+template <int LOGN1, int LOGN2>
+__device__ __forceinline__ void row_pair_ifft_store(float2* lds, float2* __restrict__ sig, int q,
+                                                    const float2* __restrict__ tw) {
+  using C = RowCfg<LOGN2>;
+  constexpr int N1 = 1 << LOGN1;
+  constexpr int LOGN = LOGN1 + LOGN2;
+  const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
+  auto ld = [&](int m, int n) -> float2 { return lds[m * C::N2 + n]; };
+  auto st = [&](int m, int n, float2 v) {
+    const int k1 = (m == 0) ? ra : rb;
+    float2 w = root<LOGN>(tw, uint32_t(n) * uint32_t(k1));
+    sig[int64_t(k1) * C::N2 + n] = cmulc(v, w);
+  };
+  fft<LOGN2, true, 2, C::T, C::N2>(lds, ld, st, tw);
+}
+
+template <int LOGN1, int LOGN2>
+__device__ __forceinline__ void row_unpack(const float2* lds, int q, int s, const float2* __restrict__ tw,
+                                           float2& A, float2& Bc) {
+  int pa, pb;
+  uint32_t kA;
+  bool s0;
+  row_slot<LOGN1, LOGN2>(q, s, pa, pb, kA, s0);
+  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN1 + LOGN2 + 1>(tw, kA);
+  real_unpack(s0, lds[pa], lds[pb], w, A, Bc);
+}
+
+template <int LOGN1, int LOGN2>
+__device__ __forceinline__ void row_repack(float2* lds, int q, int s, const float2* __restrict__ tw, float2 A,
+                                           float2 Bc) {
+  int pa, pb;
+  uint32_t kA;
+  bool s0;
+  row_slot<LOGN1, LOGN2>(q, s, pa, pb, kA, s0);
+  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN1 + LOGN2 + 1>(tw, kA);
+  float2 zp, zq;
+  real_repack(s0, A, Bc, w, zp, zq);
+  lds[pa] = zp;
+  lds[pb] = zq;
+}
+
+// Forward row kernel.  grid = H * N1/2 (block = h * N1/2 + q).  wsx rows are
+// [B*H][N], wsk [H][N].
+template <int LOGN1, int LOGN2>
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(float2* __restrict__ wsx,
+                                                                    const float2* __restrict__ wsk, int B, int H,
+                                                                    const float2* __restrict__ tw) {
+  using C = RowCfg<LOGN2>;
+  constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
+  __shared__ float2 lds[C::TILE];
+  const int q = blockIdx.x % ((1 << LOGN1) / 2);
+  const int h = blockIdx.x / ((1 << LOGN1) / 2);
+  float2 hA[C::SLOTS], hB[C::SLOTS];
+  row_pair_fft<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) row_unpack<LOGN1, LOGN2>(lds, q, threadIdx.x + i * C::T, tw, hA[i], hB[i]);
+  __syncthreads();
+  for (int b = 0; b < B; ++b) {
+    float2* sig = wsx + (int64_t(b) * H + h) * N;
+    row_pair_fft<LOGN1, LOGN2>(lds, sig, q, tw);
+#pragma unroll
+    for (int i = 0; i < C::SLOTS; ++i) {
+      const int s = threadIdx.x + i * C::T;
+      float2 A, Bc;
+      row_unpack<LOGN1, LOGN2>(lds, q, s, tw, A, Bc);
+      const bool s0 = (q == 0 && s == 0);
+      row_repack<LOGN1, LOGN2>(lds, q, s, tw, slot_mul(s0, A, hA[i]), cmul(Bc, hB[i]));
+    }
+    __syncthreads();
+    row_pair_ifft_store<LOGN1, LOGN2>(lds, sig, q, tw);
+  }
+}
+
+// Backward row kernel.  wsg rows [B*H][N] (in: column-transformed g; out:
+// gx pre-image), wsx rows [B*H][N] (column-transformed x), wsk [H][N] (in:
+// column-transformed k; out: gk pre-image).  grid = H * N1/2.
+template <int LOGN1, int LOGN2>
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_bwd_kernel(float2* __restrict__ wsg,
+                                                                    const float2* __restrict__ wsx,
+                                                                    float2* __restrict__ wsk, int B, int H,
+                                                                    const float2* __restrict__ tw) {
+  using C = RowCfg<LOGN2>;
+  constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
+  __shared__ float2 ldsG[C::TILE];
+  __shared__ float2 ldsX[C::TILE];
+  const int q = blockIdx.x % ((1 << LOGN1) / 2);
+  const int h = blockIdx.x / ((1 << LOGN1) / 2);
+  float2 hA[C::SLOTS], hB[C::SLOTS], qA[C::SLOTS], qB[C::SLOTS];
+  row_pair_fft<LOGN1, LOGN2>(ldsG, wsk + int64_t(h) * N, q, tw);
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    row_unpack<LOGN1, LOGN2>(ldsG, q, threadIdx.x + i * C::T, tw, hA[i], hB[i]);
+    qA[i] = qB[i] = make_float2(0.f, 0.f);
+  }
+  __syncthreads();
+  for (int b = 0; b < B; ++b) {
+    float2* sigg = wsg + (int64_t(b) * H + h) * N;
+    const float2* sigx = wsx + (int64_t(b) * H + h) * N;
+    row_pair_fft<LOGN1, LOGN2>(ldsG, sigg, q, tw);
+    row_pair_fft<LOGN1, LOGN2>(ldsX, sigx, q, tw);
+#pragma unroll
+    for (int i = 0; i < C::SLOTS; ++i) {
+      const int s = threadIdx.x + i * C::T;
+      const bool s0 = (q == 0 && s == 0);
+      float2 GA, GB, XA, XB;
+      row_unpack<LOGN1, LOGN2>(ldsG, q, s, tw, GA, GB);
+      row_unpack<LOGN1, LOGN2>(ldsX, q, s, tw, XA, XB);
+      qA[i] = cadd(qA[i], slot_mulc(s0, GA, XA));
+      qB[i] = cadd(qB[i], cmulc(GB, XB));
+      row_repack<LOGN1, LOGN2>(ldsG, q, s, tw, slot_mulc(s0, GA, hA[i]), cmulc(GB, hB[i]));
+    }
+    __syncthreads();
+    row_pair_ifft_store<LOGN1, LOGN2>(ldsG, sigg, q, tw);
+  }
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) row_repack<LOGN1, LOGN2>(ldsX, q, threadIdx.x + i * C::T, tw, qA[i], qB[i]);
+  __syncthreads();
+  row_pair_ifft_store<LOGN1, LOGN2>(ldsX, wsk + int64_t(h) * N, q, tw);
+}
+
+// ===========================================================================
+// Host launchers
+// ===========================================================================
+template <int LOGN, int DT>
+static void launch_fused_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void* y, int B, int H,
+                             int L, int K, const float2* tw, hipStream_t st) {
+  using C = FusedCfg<LOGN>;
+  using ET = typename Elem<DT>::T;
+  const int gh = int(ceil_div(H, C::M));
+  int nb = int(ceil_div(2048, gh));
+  nb = nb < 1 ? 1 : (nb > B ? B : nb);
+  const int bpw = int(ceil_div(B, nb));
+  nb = int(ceil_div(B, bpw));
+  dim3 grid(gh, nb);
+  if (p.fold)
+    hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
+                       (ET*)y, B, H, L, K, bpw, tw);
+  else
+    hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
+                       (ET*)y, B, H, L, K, bpw, tw);
+}
+
+template <int LOGN, int DT>
+static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, const float* k, const void* s, void* gx,
+                             float* gk, float* gs, int B, int H, int L, int K, const float2* tw, hipStream_t st) {
+  using C = FusedCfg<LOGN>;
+  using ET = typename Elem<DT>::T;
+  dim3 grid(int(ceil_div(H, C::M)));
+  if (p.fold)
+    hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw);
+  else
+    hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw);
+}
+
+template <int LOGN1, int LOGN2, int DT>
+static void launch_4step_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
+                             float2* ws, const float2* tw, hipStream_t st) {
+  constexpr int LOGN = LOGN1 + LOGN2;
+  constexpr int64_t N = int64_t(1) << LOGN;
+  using ET = typename Elem<DT>::T;
+  float2* wsx = ws;
+  float2* wsk = ws + int64_t(B) * H * N;
+  const int ncb = (1 << LOGN2) / kCols;
+  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
+                     RealRows<DT>{(const ET*)x, L, L}, wsx, tw);
+  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
+                     RealRows<NSQ_DTYPE_F32>{k, K, K}, wsk, tw);
+  hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st, wsx,
+                     (const float2*)wsk, B, H, tw);
+  hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
+                     (const float2*)wsx, (const ET*)x, (const ET*)s, (ET*)y, H, L, tw);
+}
+
+template <int LOGN1, int LOGN2, int DT>
+static void launch_4step_bwd(const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
+                             float* gs, int B, int H, int L, int K, float2* ws, const float2* tw, hipStream_t st) {
+  constexpr int LOGN = LOGN1 + LOGN2;
+  constexpr int64_t N = int64_t(1) << LOGN;
+  using ET = typename Elem<DT>::T;
+  float2* wsg = ws;
+  float2* wsx = ws + int64_t(B) * H * N;
+  float2* wsk = ws + 2 * int64_t(B) * H * N;
+  const int ncb = (1 << LOGN2) / kCols;
+  dim3 ct(ColCfg<LOGN1>::T);
+  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, RealRows<DT>{(const ET*)g, L, L},
+                     wsg, tw);
+  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, RealRows<DT>{(const ET*)x, L, L},
+                     wsx, tw);
+  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), ct, 0, st,
+                     RealRows<NSQ_DTYPE_F32>{k, K, K}, wsk, tw);
+  hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st, wsg,
+                     (const float2*)wsx, wsk, B, H, tw);
+  hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, (const float2*)wsg,
+                     (const ET*)g, (const ET*)s, (ET*)gx, H, L, tw);
+  hipLaunchKernelGGL((col_inv_gk_kernel<LOGN1, LOGN>), dim3(H, ncb), ct, 0, st, (const float2*)wsk, gk, gs, K, tw);
+}
+
+// Runtime -> compile-time dispatch helpers.
+template <template <int> class F, int LO, int HI, class... A>
+static bool dispatch_int(int v, A&&... a) {
+  if constexpr (LO > HI) {
+    return false;
+  } else {
+    if (v == LO) {
+      F<LO>::run(static_cast<A&&>(a)...);
+      return true;
+    }
+    return dispatch_int<F, LO + 1, HI>(v, static_cast<A&&>(a)...);
+  }
+}
+
+template <int DT>
+struct FusedFwd {
+  template <int LOGN>
+  struct At {
+    template <class... A>
+    static void run(A&&... a) {
+      launch_fused_fwd<LOGN, DT>(static_cast<A&&>(a)...);
+    }
+  };
+};
+
+template <int DT>
+struct FusedBwd {
+  template <int LOGN>
+  struct At {
+    template <class... A>
+    static void run(A&&... a) {
+      launch_fused_bwd<LOGN, DT>(static_cast<A&&>(a)...);
+    }
+  };
+};
+
+// 4-step instantiations: logN in [14, 22] with logN1 = min(logN/2, 10).
+template <int DT, bool BWD>
+struct FourStep {
+  template <int LOGN>
+  struct At {
+    static constexpr int L1 = (LOGN / 2) < 10 ? (LOGN / 2) : 10;
+    static constexpr int L2 = LOGN - L1;
+    template <class... A>
+    static void run(A&&... a) {
+      if constexpr (BWD)
+        launch_4step_bwd<L1, L2, DT>(static_cast<A&&>(a)...);
+      else
+        launch_4step_fwd<L1, L2, DT>(static_cast<A&&>(a)...);
+    }
+  };
+};
+
+// Per-dtype entry used by the C ABI; explicitly instantiated once per dtype in
+// fftconv1d_<dtype>.hip so the three instantiation sets compile in parallel.
+template <int DT>
+bool run_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
+             float2* ws, const float2* tw, hipStream_t st) {
+  if (p.fused) return dispatch_int<FusedFwd<DT>::template At, 3, 13>(p.logN, p, x, k, s, y, B, H, L, K, tw, st);
+  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, ws, tw, st);
+}
+
+template <int DT>
+bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
+             float* gs, int B, int H, int L, int K, float2* ws, const float2* tw, hipStream_t st) {
+  if (p.fused)
+    return dispatch_int<FusedBwd<DT>::template At, 3, 13>(p.logN, p, g, x, k, s, gx, gk, gs, B, H, L, K, tw, st);
+  return dispatch_int<FourStep<DT, true>::template At, 14, 22>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, ws, tw, st);
+}
+
+#define NSQ_DECLARE_FFTCONV1D(DT)                                                                               \
+  extern template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
+                                   int, float2*, const float2*, hipStream_t);                                   \
+  extern template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
+                                   float*, float*, int, int, int, int, float2*, const float2*, hipStream_t);
+
+#define NSQ_INSTANTIATE_FFTCONV1D(DT)                                                                    \
+  template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
+                            int, float2*, const float2*, hipStream_t);                                   \
+  template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
+                            float*, float*, int, int, int, int, float2*, const float2*, hipStream_t);
+
+NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_F32)
+NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_BF16)
+NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_F16)
+
+}  // namespace nsq

@@ -1,0 +1,85 @@
+// Twiddle table and error plumbing for the nvsubquadratic_amd C ABI.
+//
+// One immutable table per device, built on first use and kept for the life of
+// the process: the library's only device allocation outside caller-provided
+// buffers.  Layout (float2 = (cos, -sin), i.e. forward-transform roots):
+//   [0,      2^14): W_{2^14}^j            coarse roots  exp(-2*pi*i*j/2^14)
+//   [2^14, 2^15):   W_{2^28}^j            fine roots    exp(-2*pi*i*j/2^28)
+// A root of unity W_{2^b}^m with b <= 14 is one load (coarse[m << (14-b)]);
+// for 14 < b <= 28 it is coarse[idx >> 14] * fine[idx & (2^14-1)] with
+// idx = m << (28-b).  Values are computed on the host in double precision and
+// rounded once to float, so every twiddle is within 1 ulp (coarse) or 2 ulp
+// (coarse*fine) of the exact root; no recurrences are used.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <vector>
+
+#include "nsq_common.h"
+
+namespace nsq {
+
+namespace {
+thread_local char g_err[1024] = {0};
+std::mutex g_tw_mutex;
+constexpr int kMaxDevices = 64;
+float2* g_tw[kMaxDevices] = {nullptr};
+}  // namespace
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+const float2* twiddle_table() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("twiddle_table: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_tw_mutex);
+  if (g_tw[dev]) return g_tw[dev];
+  constexpr int kN = 1 << 14;
+  std::vector<float2> host(2 * kN);
+  const double two_pi = 6.283185307179586476925286766559;
+  for (int j = 0; j < kN; ++j) {
+    double a = two_pi * double(j) / double(kN);
+    host[j] = make_float2(float(std::cos(a)), float(-std::sin(a)));
+    double b = two_pi * double(j) / double(1 << 28);
+    host[kN + j] = make_float2(float(std::cos(b)), float(-std::sin(b)));
+  }
+  float2* d = nullptr;
+  hipError_t e = hipMalloc(&d, host.size() * sizeof(float2));
+  if (e != hipSuccess) {
+    set_error("twiddle_table: hipMalloc failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  e = hipMemcpy(d, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    set_error("twiddle_table: hipMemcpy failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  g_tw[dev] = d;
+  return d;
+}
+
+}  // namespace nsq
+
+extern "C" {
+
+const char* nsq_last_error(void) { return nsq::g_err; }
+
+int nsq_abi_version(void) { return NSQ_ABI_VERSION; }
+
+int nsq_init(void) {
+  nsq::clear_error();
+  return nsq::twiddle_table() ? NSQ_OK : NSQ_ERR_HIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,270 @@
+r"""HIP (gfx950) FFT long-convolution ops with the ``nvsubquadratic.ops`` call signatures.
+
+This module is the ``fft_backend="hip"`` counterpart of the reference's
+``nvsubquadratic/ops/fftconv_custom.py`` (the ``"subq_ops"`` backend).  Every
+public function keeps the reference name, argument order, accepted shapes,
+dtype behaviour and error types, so a caller switches backends by changing the
+import (or ``CKConvND(fft_backend=...)``, see :mod:`nvsubquadratic_amd.dispatch`).
+
+Semantics (reference ``nvsubquadratic/ops/fftconv_custom.py:307-335`` on top of
+``nvsubquadratic/ops/fftconv.py:546-600``):
+
+* the op accepts any input dtype, computes in float32 and returns ``x.dtype``;
+* ``y = conv(x, kernel).to(x.dtype)``, then ``y = y + shortcut.to(x.dtype) * x``;
+* 1D kernels are shared: ``[1, H, K]`` or ``[H, K]``; per-sample ``[B, H, K]``
+  with ``B != 1`` raises ``NotImplementedError`` like the reference wrapper
+  (``fftconv_custom.py:294-300``).
+
+Differences in *how*: the whole chain (pad, real FFT, spectral product,
+inverse FFT, crop, cast and shortcut) runs inside hand-written HIP kernels
+(``csrc/fftconv1d.hip``) with a fused backward; nothing is computed on the CPU.
+"""
+
+from __future__ import annotations
+
+import torch
+from einops import rearrange
+
+from . import _lib
+
+
+__all__ = [
+    "causal_fftconv1d_bhl",
+    "causal_fftconv1d_bhl_chunked",
+    "causal_fftconv1d_bhl_w_reshape",
+    "causal_fftconv1d_bhl_w_reshape_chunked",
+    "causal_fftconv1d_blh",
+    "causal_fftconv1d_blh_chunked",
+    "causal_fftconv1d_fwd_raw",
+    "causal_fftconv1d_bwd_raw",
+]
+
+_DEFAULT_CHUNK_SIZE = 128
+
+
+# ---------------------------------------------------------------------------
+# Raw launches (preallocated outputs; used by the autograd Function and bench)
+# ---------------------------------------------------------------------------
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def causal_fftconv1d_fwd_raw(
+    x: torch.Tensor,
+    k: torch.Tensor,
+    s: torch.Tensor | None,
+    y: torch.Tensor,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Launch the forward kernel on the current stream.
+
+    ``x``/``y``: contiguous ``[B, H, L]`` (float32/bfloat16/float16, same dtype);
+    ``k``: contiguous float32 ``[H, K]``; ``s``: ``[H]`` in ``x.dtype`` or None.
+    """
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, H, L = x.shape
+    K = k.shape[-1]
+    need = lib.nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, _lib.NSQ_DIR_FWD)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = _workspace(x.device, need)
+    rc = lib.nsq_fftconv1d_causal_fwd(
+        x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype),
+        B, H, L, K, _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
+        _lib.stream_ptr(x.device),
+    )
+    _lib.check(rc)
+    return y
+
+
+def causal_fftconv1d_bwd_raw(
+    g: torch.Tensor,
+    x: torch.Tensor,
+    k: torch.Tensor,
+    s: torch.Tensor | None,
+    gx: torch.Tensor,
+    gk: torch.Tensor,
+    gs: torch.Tensor | None,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """Launch the backward kernels on the current stream (see include/nsq_hip.h)."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, H, L = x.shape
+    K = k.shape[-1]
+    need = lib.nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, _lib.NSQ_DIR_BWD)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = _workspace(x.device, need)
+    rc = lib.nsq_fftconv1d_causal_bwd(
+        g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
+        _lib.dtype_code(x.dtype), B, H, L, K, _lib.ptr(workspace),
+        0 if workspace is None else workspace.numel(), _lib.stream_ptr(x.device),
+    )
+    _lib.check(rc)
+
+
+class _CausalFFTConv1d(torch.autograd.Function):
+    """Fused causal FFT conv; inputs already validated and cast.
+
+    x: [B, H, L] contiguous (f32/bf16/f16); k: [H, K] contiguous float32;
+    s: [H] in x.dtype or None.
+    """
+
+    @staticmethod
+    def forward(ctx, x, k, s):
+        y = torch.empty_like(x)
+        causal_fftconv1d_fwd_raw(x, k, s, y)
+        ctx.save_for_backward(x, k, s)
+        ctx.has_s = s is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, k, s = ctx.saved_tensors
+        g = gy.to(x.dtype).contiguous()
+        gx = torch.empty_like(x)
+        gk = torch.empty(k.shape, dtype=torch.float32, device=x.device)
+        gs = torch.empty(k.shape[0], dtype=torch.float32, device=x.device) if ctx.has_s else None
+        causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs)
+        return gx, gk, (gs.to(s.dtype) if ctx.has_s else None)
+
+
+# ---------------------------------------------------------------------------
+# Argument normalisation shared by every public function
+# ---------------------------------------------------------------------------
+def _kernel_2d(kernel: torch.Tensor) -> torch.Tensor:
+    """``[1, H, K]`` / ``[H, K]`` -> ``[H, K]``; FiLM ``[B, H, K]`` rejected.
+
+    Mirrors ``_subq_causal_conv1d_bhl`` (``nvsubquadratic/ops/fftconv_custom.py:286-304``).
+    """
+    if kernel.ndim == 3:
+        if kernel.shape[0] != 1:
+            raise NotImplementedError(
+                "fft_backend='hip' causal_fftconv1d does not accept per-sample "
+                f"FiLM weights. Got kernel shape {tuple(kernel.shape)} with batch={kernel.shape[0]}; "
+                "expected shared kernel [1, H, K] or [H, K]."
+            )
+        return kernel.squeeze(0)
+    if kernel.ndim == 2:
+        return kernel
+    raise ValueError(f"Unexpected kernel shape: {tuple(kernel.shape)}.")
+
+
+def _causal_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None) -> torch.Tensor:
+    if x.ndim != 3:
+        raise ValueError(f"x must be [B, H, L]; got shape {tuple(x.shape)}")
+    _B, H, L = x.shape
+    k2 = _kernel_2d(kernel)
+    if k2.shape[0] != H:
+        raise ValueError(f"kernel has {k2.shape[0]} channels, x has {H}")
+    if k2.shape[-1] > 2 * L:
+        raise ValueError(f"Kernel length must be less than or equal to 2 * seq_len. Got {k2.shape[-1]}.")
+    input_dtype = x.dtype
+    compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
+    xc = x.to(compute_dtype).contiguous()
+    kc = k2.float().contiguous()
+    sc = None
+    if shortcut is not None:
+        if shortcut.shape != (H,):
+            raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
+        # Reference casts the shortcut to the input dtype before the product.
+        sc = shortcut.to(input_dtype).to(compute_dtype).contiguous()
+    y = _CausalFFTConv1d.apply(xc, kc, sc)
+    return y.to(input_dtype)
+
+
+# ---------------------------------------------------------------------------
+# Public API (names and signatures of nvsubquadratic/ops/fftconv_custom.py)
+# ---------------------------------------------------------------------------
+def causal_fftconv1d_bhl(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """1D causal FFT convolution on the HIP backend, BHL layout ``[B, H, L]``.
+
+    Drop-in for ``nvsubquadratic.ops.fftconv_custom.causal_fftconv1d_bhl``
+    (``fftconv_custom.py:307-335``) and, numerically, for
+    ``nvsubquadratic.ops.fftconv.causal_fftconv1d_fp32_bhl`` (``fftconv.py:546-600``).
+
+    Args:
+        x: Input ``[B, H, L]``, any floating dtype.
+        kernel: ``[1, H, K]`` or ``[H, K]`` with ``K <= 2L``.
+        shortcut: Optional ``[H]`` per-channel scale.
+
+    Returns:
+        ``[B, H, L]`` in ``x.dtype``.
+    """
+    return _causal_core(x, kernel, shortcut)
+
+
+def causal_fftconv1d_bhl_w_reshape(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """BLH inputs ``[B, L, H]`` with kernel ``[1, K, H]`` (``fftconv_custom.py:338-350``)."""
+    x_bhl = rearrange(x, "b l h -> b h l")
+    kernel_bhl = rearrange(kernel, "b l h -> b h l")
+    y_bhl = causal_fftconv1d_bhl(x_bhl, kernel_bhl, shortcut)
+    return rearrange(y_bhl, "b h l -> b l h")
+
+
+def causal_fftconv1d_blh(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Alias for :func:`causal_fftconv1d_bhl_w_reshape` (``fftconv_custom.py:353-359``)."""
+    return causal_fftconv1d_bhl_w_reshape(x, kernel, shortcut)
+
+
+def causal_fftconv1d_bhl_chunked(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+    chunk_size: int | None = None,
+) -> torch.Tensor:
+    """Channel-chunked variant (``fftconv_custom.py:362-389``).
+
+    Channels are independent in every HIP kernel, so the result is bitwise
+    identical to :func:`causal_fftconv1d_bhl`; chunking only bounds the size of
+    the 4-step plan's workspace.
+    """
+    if chunk_size is None:
+        chunk_size = _DEFAULT_CHUNK_SIZE
+    _B, H, _L = x.shape
+    if H <= chunk_size:
+        return causal_fftconv1d_bhl(x, kernel, shortcut)
+    k2 = _kernel_2d(kernel)
+    chunks = []
+    for start in range(0, H, chunk_size):
+        end = min(start + chunk_size, H)
+        s_c = None if shortcut is None else shortcut[start:end]
+        chunks.append(causal_fftconv1d_bhl(x[:, start:end], k2[start:end], s_c))
+    return torch.cat(chunks, dim=1)
+
+
+def causal_fftconv1d_bhl_w_reshape_chunked(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+    chunk_size: int | None = None,
+) -> torch.Tensor:
+    """Chunked BLH variant (``fftconv_custom.py:392-402``)."""
+    x_bhl = rearrange(x, "b l h -> b h l")
+    kernel_bhl = rearrange(kernel, "b l h -> b h l")
+    y_bhl = causal_fftconv1d_bhl_chunked(x_bhl, kernel_bhl, shortcut, chunk_size)
+    return rearrange(y_bhl, "b h l -> b l h")
+
+
+def causal_fftconv1d_blh_chunked(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+    chunk_size: int | None = None,
+) -> torch.Tensor:
+    """Alias for :func:`causal_fftconv1d_bhl_w_reshape_chunked` (``fftconv_custom.py:405-412``)."""
+    return causal_fftconv1d_bhl_w_reshape_chunked(x, kernel, shortcut, chunk_size)

@@ -1,0 +1,83 @@
+"""CPU tests of the drop-in boundary: library exports, host-side validation.
+
+No kernel is launched here (no GPU in the CPU suite): the library is loaded
+with ctypes and its exported symbols are compared with include/nsq_hip.h; the
+Python layer's argument checks are exercised with CPU tensors, which must be
+rejected loudly rather than computed on the CPU.
+"""
+
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from nvsubquadratic_amd import _lib
+from nvsubquadratic_amd import fftconv_hip as F
+
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nsq_hip.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nsq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_what_python_binds():
+    assert _header_functions() == _lib.library_exports()
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT (nsq_[a-z0-9_]+)$", out.stdout, flags=re.M))
+    missing = [f for f in _header_functions() if f not in exported]
+    assert not missing, missing
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_library_loads_and_reports_abi():
+    lib = _lib.get_lib()
+    assert lib.nsq_abi_version() == _lib.ABI_VERSION
+    assert isinstance(lib.nsq_last_error(), bytes)
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_workspace_query_needs_no_gpu():
+    lib = _lib.get_lib()
+    # fused plan (F <= 16384): no workspace
+    assert lib.nsq_fftconv1d_causal_workspace_bytes(2, 128, 4096, 4096, 0) == 0
+    # 4-step plan at config 3: one complex64 row per signal
+    n = 1 << 18
+    assert lib.nsq_fftconv1d_causal_workspace_bytes(1, 4096, 262144, 262144, 0) == (4096 + 4096) * n * 8
+    assert lib.nsq_fftconv1d_causal_workspace_bytes(1, 4096, 262144, 262144, 1) == (2 * 4096 + 4096) * n * 8
+
+
+def test_per_sample_film_weights_rejected():
+    """Mirror of tests/ops/test_fftconv_custom_1d.py:231-239."""
+    x = torch.randn(2, 32, 128)
+    k = torch.randn(2, 32, 5)
+    with pytest.raises(NotImplementedError, match="per-sample FiLM weights"):
+        F.causal_fftconv1d_bhl(x, k)
+
+
+def test_kernel_longer_than_two_l_rejected():
+    with pytest.raises(ValueError, match="2 \\* seq_len"):
+        F.causal_fftconv1d_bhl(torch.randn(1, 2, 8), torch.randn(1, 2, 17))
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_cpu_tensors_fail_loudly_no_cpu_fallback():
+    with pytest.raises(_lib.HipLibraryError, match="no CPU fallback"):
+        F.causal_fftconv1d_bhl(torch.randn(1, 2, 8), torch.randn(1, 2, 3))
+
+
+def test_missing_library_raises_at_call_time(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(_lib.HipLibraryError, match="not found"):
+        _lib.get_lib()

@@ -1,0 +1,286 @@
+"""GPU parity of the HIP causal 1D FFT conv against the CPU oracle.
+
+Mirrors the reference's own test matrix (tests/ops/test_fftconv_custom_1d.py:
+shapes :106-113, BLH :133-144, shortcut :146-156, chunked :159-180, backward
+:183-200, dtypes :203-212, long kernels :215-228) and adds the BASELINE
+configs: config 1 whole, config 3 on a channel sample at full length, and
+size-independent properties (adjoint identity, delta filter) at full size.
+
+Tolerances: rel-L2 <= 1e-4 for fp32, <= 2e-2 for bf16
+I/O; the reference tests' own elementwise bounds are also applied where they
+mirror a reference test.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from nvsubquadratic_amd import fftconv_hip as F
+from nvsubquadratic_amd.workloads import causal1d_case
+from oracle.fftconv_ref import causal_fftconv1d_np, causal_fftconv1d_torch, rel_l2
+
+
+pytestmark = pytest.mark.gpu
+
+RTOL_F32_L2 = 1e-4
+RTOL_BF16_L2 = 2e-2
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "causal1d.npz")
+
+SHARED_SHAPES = [
+    (2, 64, 256, 7),
+    (4, 128, 512, 7),
+    (1, 256, 1024, 15),
+    (2, 32, 128, 3),
+    (1, 96, 2048, 65),
+    (2, 64, 64, 64),  # K == L
+]
+
+
+def _ref(x, k, s=None):
+    return causal_fftconv1d_torch(x.detach().cpu(), k.detach().cpu(), None if s is None else s.detach().cpu())
+
+
+@pytest.mark.parametrize("B,H,L,K", SHARED_SHAPES)
+def test_bhl_shared_kernel(B, H, L, K):
+    torch.manual_seed(42)
+    x = torch.randn(B, H, L)
+    k = torch.randn(1, H, K)
+    y = F.causal_fftconv1d_bhl(x.cuda(), k.cuda())
+    y_ref = _ref(x, k)
+    torch.testing.assert_close(y.cpu(), y_ref, atol=1e-3, rtol=1e-4)
+    assert rel_l2(y_ref, y) < RTOL_F32_L2
+
+
+@pytest.mark.parametrize("B,H,L,K", SHARED_SHAPES)
+def test_blh_shared_kernel(B, H, L, K):
+    torch.manual_seed(42)
+    x = torch.randn(B, L, H)
+    k = torch.randn(1, K, H)
+    y = F.causal_fftconv1d_bhl_w_reshape(x.cuda(), k.cuda())
+    xb = x.permute(0, 2, 1)
+    kb = k.permute(0, 2, 1)
+    y_ref = _ref(xb, kb).permute(0, 2, 1)
+    torch.testing.assert_close(y.cpu(), y_ref, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("B,H,L,K", SHARED_SHAPES[:3])
+def test_shortcut_semantics(B, H, L, K):
+    torch.manual_seed(42)
+    x = torch.randn(B, H, L)
+    k = torch.randn(1, H, K)
+    s = torch.randn(H)
+    y = F.causal_fftconv1d_bhl(x.cuda(), k.cuda(), s.cuda())
+    torch.testing.assert_close(y.cpu(), _ref(x, k, s), atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("B,H,L,K", SHARED_SHAPES[:4])
+@pytest.mark.parametrize("chunk_size", [16, 32, 128])
+def test_chunked_matches_bitwise(B, H, L, K, chunk_size):
+    torch.manual_seed(42)
+    x = torch.randn(B, H, L, device="cuda")
+    k = torch.randn(1, H, K, device="cuda")
+    s = torch.randn(H, device="cuda")
+    y = F.causal_fftconv1d_bhl(x, k, s)
+    yc = F.causal_fftconv1d_bhl_chunked(x, k, s, chunk_size)
+    assert torch.equal(y, yc)
+
+
+def test_blh_chunked_matches():
+    torch.manual_seed(42)
+    x = torch.randn(2, 256, 64, device="cuda")
+    k = torch.randn(1, 7, 64, device="cuda")
+    y = F.causal_fftconv1d_bhl_w_reshape(x, k)
+    yc = F.causal_fftconv1d_blh_chunked(x, k, chunk_size=32)
+    assert torch.equal(y, yc)
+
+
+@pytest.mark.parametrize("B,H,L,K", [(2, 64, 256, 7), (4, 32, 128, 5), (2, 16, 64, 64), (1, 8, 1024, 1024)])
+def test_grad_matches_reference(B, H, L, K):
+    torch.manual_seed(42)
+    x = torch.randn(B, H, L, requires_grad=True)
+    k = torch.randn(1, H, K, requires_grad=True)
+    s = torch.randn(H, requires_grad=True)
+    y_ref = causal_fftconv1d_torch(x, k, s)
+    gy = torch.randn_like(y_ref)
+    y_ref.backward(gy)
+    xg = x.detach().cuda().requires_grad_(True)
+    kg = k.detach().cuda().requires_grad_(True)
+    sg = s.detach().cuda().requires_grad_(True)
+    y = F.causal_fftconv1d_bhl(xg, kg, sg)
+    y.backward(gy.cuda())
+    torch.testing.assert_close(xg.grad.cpu(), x.grad, atol=1e-2, rtol=1e-3)
+    torch.testing.assert_close(kg.grad.cpu(), k.grad, atol=1e-2, rtol=1e-3)
+    torch.testing.assert_close(sg.grad.cpu(), s.grad, atol=1e-2, rtol=1e-3)
+    assert rel_l2(x.grad, xg.grad) < RTOL_F32_L2
+    assert rel_l2(k.grad, kg.grad) < RTOL_F32_L2
+    assert rel_l2(s.grad, sg.grad) < RTOL_F32_L2
+
+
+@pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dtype_preserved(in_dtype):
+    torch.manual_seed(0)
+    x = torch.randn(2, 32, 128, device="cuda", dtype=in_dtype)
+    k = torch.randn(1, 32, 5, device="cuda", dtype=in_dtype)
+    y = F.causal_fftconv1d_bhl(x, k)
+    assert y.dtype == in_dtype
+    assert torch.isfinite(y).all()
+    y_ref = _ref(x, k)
+    assert rel_l2(y_ref, y) < (RTOL_F32_L2 if in_dtype == torch.float32 else RTOL_BF16_L2)
+
+
+@pytest.mark.parametrize("K", [128, 512, 2048])
+def test_long_kernel_matches_reference(K):
+    torch.manual_seed(42)
+    B, H, L = 1, 32, max(K, 256)
+    x = torch.randn(B, H, L)
+    k = torch.randn(1, H, K)
+    y = F.causal_fftconv1d_bhl(x.cuda(), k.cuda())
+    torch.testing.assert_close(y.cpu(), _ref(x, k), atol=1e-3, rtol=1e-4)
+
+
+def test_golden_fixtures_forward_and_backward():
+    d = np.load(GOLDEN)
+    for i in range(int(d["n_causal"])):
+        x = torch.tensor(d[f"c{i}_x"], dtype=torch.float32, device="cuda", requires_grad=True)
+        k = torch.tensor(d[f"c{i}_k"], dtype=torch.float32, device="cuda", requires_grad=True)
+        s = torch.tensor(d[f"c{i}_s"], dtype=torch.float32, device="cuda", requires_grad=True)
+        y = F.causal_fftconv1d_bhl(x, k[None], s)
+        assert rel_l2(d[f"c{i}_y"], y) < 1e-5, f"case {i} y"
+        y.backward(torch.tensor(d[f"c{i}_g"], dtype=torch.float32, device="cuda"))
+        assert rel_l2(d[f"c{i}_gx"], x.grad) < 1e-5, f"case {i} gx"
+        assert rel_l2(d[f"c{i}_gk"], k.grad) < 1e-5, f"case {i} gk"
+        assert rel_l2(d[f"c{i}_gs"], s.grad) < 1e-5, f"case {i} gs"
+
+
+@pytest.mark.parametrize("B,H,L,K", [(1, 4, 100, 150), (2, 3, 1000, 2000), (1, 2, 4096, 8192), (2, 2, 33, 60)])
+def test_kernel_longer_than_l_plus_one_wraps_like_reference(B, H, L, K):
+    torch.manual_seed(3)
+    x = torch.randn(B, H, L, requires_grad=True)
+    k = torch.randn(1, H, K, requires_grad=True)
+    y_ref = causal_fftconv1d_torch(x, k)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg = x.detach().cuda().requires_grad_(True)
+    kg = k.detach().cuda().requires_grad_(True)
+    y = F.causal_fftconv1d_bhl(xg, kg)
+    y.backward(g.cuda())
+    assert rel_l2(y_ref, y) < RTOL_F32_L2
+    assert rel_l2(x.grad, xg.grad) < RTOL_F32_L2
+    assert rel_l2(k.grad, kg.grad) < RTOL_F32_L2
+
+
+@pytest.mark.parametrize("L,K", [(3, 3), (1, 1), (1, 2), (5, 1), (257, 3), (8191, 8191)])
+def test_ragged_and_tiny_lengths(L, K):
+    torch.manual_seed(5)
+    x = torch.randn(3, 5, L)
+    k = torch.randn(5, K)
+    s = torch.randn(5)
+    y = F.causal_fftconv1d_bhl(x.cuda(), k.cuda(), s.cuda())
+    assert rel_l2(_ref(x, k, s), y) < RTOL_F32_L2
+
+
+# ---------------------------------------------------------------------------
+# 4-step plan (FFT length >= 2^15) and the BASELINE configs
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("L,K", [(16384, 16384), (20000, 9000), (65536, 65536), (131072, 1000)])
+def test_four_step_fp32_fwd_bwd(L, K):
+    torch.manual_seed(7)
+    B, H = 2, 3
+    x = torch.randn(B, H, L, requires_grad=True)
+    k = torch.randn(1, H, K, requires_grad=True)
+    s = torch.randn(H, requires_grad=True)
+    y_ref = causal_fftconv1d_torch(x, k, s)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg = x.detach().cuda().requires_grad_(True)
+    kg = k.detach().cuda().requires_grad_(True)
+    sg = s.detach().cuda().requires_grad_(True)
+    y = F.causal_fftconv1d_bhl(xg, kg, sg)
+    y.backward(g.cuda())
+    assert rel_l2(y_ref, y) < RTOL_F32_L2
+    assert rel_l2(x.grad, xg.grad) < RTOL_F32_L2
+    assert rel_l2(k.grad, kg.grad) < RTOL_F32_L2
+    assert rel_l2(s.grad, sg.grad) < RTOL_F32_L2
+
+
+def test_config1_fp32_fwd_bwd():
+    """B=2, D=128, L=4096, fp32, decaying filter a~U(1,10)."""
+    c = causal1d_case(2, 128, 4096, torch.float32, (1.0, 10.0))
+    x = c.x.clone().requires_grad_(True)
+    k = c.k[None].clone().requires_grad_(True)
+    s = c.s.clone().requires_grad_(True)
+    y_ref = causal_fftconv1d_torch(x, k, s)
+    y_ref.backward(c.g)
+    xg = c.x.cuda().requires_grad_(True)
+    kg = c.k[None].cuda().requires_grad_(True)
+    sg = c.s.cuda().requires_grad_(True)
+    y = F.causal_fftconv1d_bhl(xg, kg, sg)
+    y.backward(c.g.cuda())
+    assert rel_l2(y_ref, y) < RTOL_F32_L2
+    assert rel_l2(x.grad, xg.grad) < RTOL_F32_L2
+    assert rel_l2(k.grad, kg.grad) < RTOL_F32_L2
+    assert rel_l2(s.grad, sg.grad) < RTOL_F32_L2
+
+
+def test_config3_channel_sample_bf16_fwd_bwd():
+    """BASELINE config 3 at full length L=262144 on a 4-channel sample (bf16 I/O)."""
+    L = 262144
+    c = causal1d_case(1, 4096, L, torch.bfloat16, (1.0, 50.0), channels=slice(1000, 1004))
+    x = c.x.clone().requires_grad_(True)
+    k = c.k[None].clone().requires_grad_(True)
+    s = c.s.clone().requires_grad_(True)
+    y_ref = causal_fftconv1d_torch(x, k, s)
+    y_ref.backward(c.g)
+    xg = c.x.cuda().requires_grad_(True)
+    kg = c.k[None].cuda().requires_grad_(True)
+    sg = c.s.cuda().requires_grad_(True)
+    y = F.causal_fftconv1d_bhl(xg, kg, sg)
+    y.backward(c.g.cuda())
+    assert y.dtype == torch.bfloat16
+    assert rel_l2(y_ref, y) < RTOL_BF16_L2
+    assert rel_l2(x.grad, xg.grad) < RTOL_BF16_L2
+    assert rel_l2(k.grad, kg.grad) < RTOL_BF16_L2
+    assert rel_l2(s.grad, sg.grad) < RTOL_BF16_L2
+    # the fp32 spectrum path itself is far tighter than the bf16 budget
+    y64 = causal_fftconv1d_np(c.x.float().numpy(), c.k.numpy(), c.s.float().numpy())
+    assert rel_l2(y64, y) < 5e-3
+
+
+def test_config3_full_size_properties():
+    """Full config-3 shape (B=1, D=4096, L=262144): size-independent checks.
+
+    * adjoint identity <conv(x), g> == <x, conv^T(g)> and <conv(x), g> == <k, gk>
+      (float32 I/O so no output rounding enters);
+    * a delta filter reproduces the input exactly (up to fp32 FFT error);
+    * the bf16 forward agrees with the CPU oracle on 3 sampled channels.
+    """
+    H, L = 4096, 262144
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    x = torch.randn(1, H, L, device="cuda", generator=gen)
+    a = torch.rand(H, 1, device="cuda", generator=gen) * 49 + 1
+    k = torch.randn(H, L, device="cuda", generator=gen)
+    k *= torch.exp(-a * torch.arange(L, device="cuda").float().view(1, L) / L)
+    g = torch.randn(1, H, L, device="cuda", generator=gen)
+    y = F.causal_fftconv1d_bhl(x, k)
+    gx = torch.empty_like(x)
+    gk = torch.empty_like(k)
+    F.causal_fftconv1d_bwd_raw(g, x, k, None, gx, gk, None)
+    lhs = torch.dot(y.flatten().double(), g.flatten().double()).item()
+    rhs1 = torch.dot(x.flatten().double(), gx.flatten().double()).item()
+    rhs2 = torch.dot(k.flatten().double(), gk.flatten().double()).item()
+    scale = y.double().norm().item() * g.double().norm().item()
+    assert abs(lhs - rhs1) / scale < 1e-5
+    assert abs(lhs - rhs2) / scale < 1e-5
+    # sampled channels vs oracle
+    for h in (0, 1777, 4095):
+        y_ref = causal_fftconv1d_np(x[:, h:h + 1].cpu().numpy(), k[h:h + 1].cpu().numpy())
+        assert rel_l2(y_ref, y[:, h:h + 1]) < RTOL_F32_L2
+    del gx, gk
+    # delta filter
+    kd = torch.zeros_like(k)
+    kd[:, 0] = 1.0
+    yd = F.causal_fftconv1d_bhl(x, kd)
+    assert rel_l2(x, yd) < 1e-5
