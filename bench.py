@@ -1,0 +1,212 @@
+"""Benchmark of the Hyena long-convolution hot path on one MI355X.
+
+Default workload (the BASELINE metric's configuration, config 3): causal 1D
+FFT convolution forward + backward at B=1, D=4096, L=262144 (FFT length
+2^19), x / upstream gradient bf16 ~ N(0,1), filter fp32 N(0,1)*exp(-a_d t/L)
+with a_d ~ U(1,50), shortcut bf16.  A step is one forward and one backward
+call on inputs resident in HBM, with outputs and workspace preallocated.
+
+Prints one JSON line with the driver's fields plus:
+  roofline     -- algorithmic HBM bytes of the fwd+bwd pair / its measured time,
+                  against MI355X's 8 TB/s (the path is HBM-bound by definition
+                  of the metric; see DESIGN.md for the per-kernel view);
+  cpu_baseline -- the CPU oracle (float32 torch.fft restatement of the
+                  reference path, autograd backward) on a bounded channel
+                  sample of the same workload, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --copy-calibration   (one plain copy kernel of known size,
+                                             for scaling rocprof FETCH/WRITE_SIZE)
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "FFT-conv fwd+bwd ms & HBM GB/s (% peak), 1D D=4096 L=256K, 1 MI355X"
+CFG = dict(B=1, D=4096, L=262144, K=262144, a_lo=1.0, a_hi=50.0)
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def copy_calibration() -> None:
+    """One device-to-device copy of exactly 1 GiB (read 1 GiB, write 1 GiB)."""
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
+
+
+def cpu_baseline(channels: int, iters: int) -> dict:
+    """Oracle fwd+bwd on a channel sample of the config-3 workload, host cores."""
+    from nvsubquadratic_amd.workloads import algorithmic_bytes_causal1d, causal1d_case
+    from oracle.fftconv_ref import causal_fftconv1d_chunked_torch
+
+    n_threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n_threads)
+    c = causal1d_case(CFG["B"], CFG["D"], CFG["L"], torch.bfloat16, (CFG["a_lo"], CFG["a_hi"]),
+                      channels=slice(0, channels))
+    times = []
+    for it in range(iters + 1):
+        x = c.x.clone().requires_grad_(True)
+        k = c.k[None].clone().requires_grad_(True)
+        s = c.s.clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        # 128-channel chunks bound host memory (nvsubquadratic/ops/fftconv_chunked.py:285-322 semantics)
+        y = causal_fftconv1d_chunked_torch(x, k, s, chunk_size=128)
+        y.backward(c.g)
+        dt = time.perf_counter() - t0
+        if it > 0:
+            times.append(dt)
+        _log(f"cpu baseline iter {it}: {dt:.2f}s")
+    med = statistics.median(times)
+    nbytes = algorithmic_bytes_causal1d(CFG["B"], channels, CFG["L"], CFG["K"], 2, "fwd+bwd")
+    full_ms = med * 1e3 * CFG["D"] / channels
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": n_threads,
+        "kind": "port",
+        "ms_per_step_extrapolated": round(full_ms, 1),
+        "sample": (f"{channels} of {CFG['D']} channels (B=1, L=262144, bf16 I/O), fwd+bwd with torch.fft fp32 "
+                   f"on CPU + autograd in 128-channel chunks, median of {iters} after 1 warmup; "
+                   f"value = algorithmic bytes of the "
+                   f"sample / median time; ms_per_step_extrapolated scales to all {CFG['D']} channels"),
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-channels", type=int, default=1024)
+    ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--copy-calibration", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one GPU only: the causal FFT conv is depthwise and shards over channels with no "
+            "communication (see DESIGN.md); multi-GPU runs are not part of this build.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
+
+    from nvsubquadratic_amd import _lib
+    from nvsubquadratic_amd import fftconv_hip as F
+    from nvsubquadratic_amd.workloads import algorithmic_bytes_causal1d, causal1d_case_fast, fft_flops_causal1d
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, D, L, K = CFG["B"], CFG["D"], CFG["L"], CFG["K"]
+    _log("generating inputs on the GPU")
+    c = causal1d_case_fast(B, D, L, torch.bfloat16, (CFG["a_lo"], CFG["a_hi"]), dev, seed=0)
+    y = torch.empty_like(c.x)
+    gx = torch.empty_like(c.x)
+    gk = torch.empty_like(c.k)
+    gs = torch.empty(D, dtype=torch.float32, device=dev)
+    lib = _lib.get_lib()
+    ws_bytes = max(lib.nsq_fftconv1d_causal_workspace_bytes(B, D, L, K, d) for d in (0, 1))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    _log(f"workspace {ws_bytes / 2**30:.1f} GiB")
+
+    def fwd():
+        F.causal_fftconv1d_fwd_raw(c.x, c.k, c.s, y, ws)
+
+    def bwd():
+        F.causal_fftconv1d_bwd_raw(c.g, c.x, c.k, c.s, gx, gk, gs, ws)
+
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    _log(f"warmup done ({args.warmup} steps)")
+
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[3 * i].record(stream)
+        fwd()
+        ev[3 * i + 1].record(stream)
+        bwd()
+        ev[3 * i + 2].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fwd_ms = [ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(args.steps)]
+    bwd_ms = [ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(args.steps)]
+    step_ms = [a + b for a, b in zip(fwd_ms, bwd_ms)]
+    ms = statistics.mean(step_ms)
+    _log(f"timed {args.steps} steps: {ms:.3f} ms/step (events), wall {wall * 1e3 / args.steps:.3f} ms/step")
+
+    nbytes = algorithmic_bytes_causal1d(B, D, L, K, 2, "fwd+bwd")
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    flops = fft_flops_causal1d(B, D, L, K, "fwd+bwd")
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg3: causal FFT long conv fwd+bwd, B=1 D=4096 L=262144 K=262144, FFT length 2^19, "
+                        "x/grad bf16, filter fp32, shortcut bf16",
+            "B": B, "D": D, "L": L, "K": K, "io_dtype": "bf16", "filter_dtype": "fp32",
+        },
+        "phases_ms": {
+            "fwd": round(statistics.mean(fwd_ms), 4),
+            "bwd": round(statistics.mean(bwd_ms), 4),
+            "fwd_median": round(statistics.median(fwd_ms), 4),
+            "bwd_median": round(statistics.median(bwd_ms), 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "scope": "fwd+bwd launch sequence (all kernels of both calls); algorithmic bytes "
+                     f"{nbytes} per step",
+            "fft_tflops_radix2_count": round(flops / (ms * 1e-3) / 1e12, 2),
+        },
+    }
+    if not args.no_cpu:
+        _log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_channels, args.cpu_iters)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
