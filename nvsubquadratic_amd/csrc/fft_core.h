@@ -11,8 +11,9 @@
 //  * The first pass may read from global memory and the last pass may write
 //    to global memory through functors, so a transform that starts and ends
 //    in HBM costs only (passes - 1) LDS round trips.
-//  * Twiddles come from the table built in twiddle.hip (double-precision
-//    roots rounded once); no sin/cos evaluation and no recurrences on device.
+//  * Twiddles of transforms up to 2^14 come from the table built in
+//    twiddle.hip (double-precision roots rounded once); longer-period roots
+//    use the hardware sin/cos (see root<> below).  No recurrences on device.
 #pragma once
 
 #include <type_traits>
@@ -39,24 +40,36 @@ __device__ __forceinline__ float2 mul_i(float2 a) { return make_float2(-a.y, a.x
 __device__ __forceinline__ float2 mul_neg_i(float2 a) { return make_float2(a.y, -a.x); }
 
 // ---------------------------------------------------------------------------
-// Roots of unity from the table.  W_{2^LOGB}^m, forward sign.
+// Roots of unity W_{2^LOGB}^m (forward sign).
+//  * LOGB <= 14: one load from the coarse table (correctly rounded roots).
+//  * LOGB > 14 (the long-transform twiddles of the 4-step plan and the real
+//    unpack): the hardware sin/cos of gfx950, whose argument is in revolutions,
+//    on the exact fraction m / 2^LOGB.  Measured on MI355X against double
+//    precision over 2^20 arguments: max abs error 1.25e-7, rms 3.5e-8 (a
+//    correctly rounded float table: 3.0e-8), i.e. ~2 ulp, far inside the 1e-4
+//    rel-L2 budget of the fp32 path, and with no scattered table loads.
 // ---------------------------------------------------------------------------
 template <int LOGB>
 __device__ __forceinline__ float2 root(const float2* __restrict__ tw, uint32_t m) {
-  static_assert(LOGB >= 0 && LOGB <= 28, "root: size out of range");
+  static_assert(LOGB >= 0 && LOGB <= 24, "root: size out of range");
   if constexpr (LOGB <= 14) {
     return tw[m << (14 - LOGB)];
   } else {
-    uint32_t idx = m << (28 - LOGB);
-    return cmul(tw[idx >> 14], tw[(1u << 14) + (idx & ((1u << 14) - 1))]);
+    const float a = float(m & ((1u << LOGB) - 1u)) * (1.0f / float(1u << LOGB));
+    return make_float2(__builtin_amdgcn_cosf(a), -__builtin_amdgcn_sinf(a));
   }
 }
 
-// Runtime-size variant (logb in [0, 28]).
-__device__ __forceinline__ float2 root_rt(const float2* __restrict__ tw, uint32_t m, int logb) {
-  if (logb <= 14) return tw[m << (14 - logb)];
-  uint32_t idx = m << (28 - logb);
-  return cmul(tw[idx >> 14], tw[(1u << 14) + (idx & ((1u << 14) - 1))]);
+
+// Thread index hidden from loop-invariant code motion.  Pass twiddles and
+// addresses depend only on the thread index; inside a batch loop the compiler
+// would otherwise hoist all of them out of the loop and keep them live across
+// it, tripling the register footprint (and halving occupancy).  Recomputing
+// them per use is cheaper than the lost occupancy.
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
 }
 
 // ---------------------------------------------------------------------------
@@ -144,9 +157,13 @@ __device__ __forceinline__ void dft(float2* v) {
 // T threads.  LD(m, n) -> float2 reads input element n of transform m; ST(m, n,
 // v) writes output element n.  LOGNS = log2 of the sub-transform length already
 // done (0 for the first pass).  Barriers bracket the write phase so LD and ST
-// may alias the same LDS buffer.
+// may alias the same LDS buffer.  Butterfly b of the tile is owned by thread
+// b % T; TMAJOR selects whether consecutive butterflies step through the
+// transforms first (m = b % M: consecutive lanes touch consecutive transforms,
+// i.e. consecutive columns of a row-major matrix in global memory) or through
+// the elements of one transform first (m = b / (N/R)).
 // ---------------------------------------------------------------------------
-template <int LOGN, int LOGR, int LOGNS, bool INV, int M, int T, class LD, class ST>
+template <int LOGN, int LOGR, int LOGNS, bool INV, int M, int T, bool TMAJOR, class LD, class ST>
 __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __restrict__ tw) {
   constexpr int R = 1 << LOGR;
   constexpr int NR = 1 << (LOGN - LOGR);
@@ -154,13 +171,13 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
   constexpr int PER = (M * NR) / T;
   static_assert((M * NR) % T == 0, "stockham_pass: tile not divisible by threads");
   static_assert(LOGNS + LOGR <= 14, "stockham_pass: transform too long for the coarse table");
-  const int tid = threadIdx.x;
+  const int tid = opaque_tid();
   float2 v[PER][R];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int bf = tid + i * T;
-    const int m = bf >> (LOGN - LOGR);
-    const int j = bf & (NR - 1);
+    const int m = TMAJOR ? (bf % M) : (bf >> (LOGN - LOGR));
+    const int j = TMAJOR ? (bf / M) : (bf & (NR - 1));
 #pragma unroll
     for (int r = 0; r < R; ++r) v[i][r] = ld(m, j + r * NR);
   }
@@ -168,8 +185,8 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int bf = tid + i * T;
-    const int m = bf >> (LOGN - LOGR);
-    const int j = bf & (NR - 1);
+    const int m = TMAJOR ? (bf % M) : (bf >> (LOGN - LOGR));
+    const int j = TMAJOR ? (bf / M) : (bf & (NR - 1));
     const int k = j & (NS - 1);
     if constexpr (LOGNS > 0) {
 #pragma unroll
@@ -187,7 +204,7 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
   __syncthreads();
 }
 
-template <int LOGN, int LOGNS, bool INV, int M, int T, class LDF, class STL, class LDL, class STF>
+template <int LOGN, int LOGNS, bool INV, int M, int T, bool TMAJOR, class LDF, class STL, class LDL, class STF>
 __device__ __forceinline__ void fft_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last,
                                         const float2* __restrict__ tw) {
   constexpr int REM = LOGN - LOGNS;
@@ -195,34 +212,45 @@ __device__ __forceinline__ void fft_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds,
   constexpr bool FIRST = (LOGNS == 0);
   constexpr bool LAST = (LOGNS + LOGR == LOGN);
   if constexpr (FIRST && LAST) {
-    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_first, st_last, tw);
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_first, st_last, tw);
   } else if constexpr (FIRST) {
-    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_first, st_lds, tw);
-    fft_rec<LOGN, LOGNS + LOGR, INV, M, T>(ld_first, st_lds, ld_lds, st_last, tw);
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_first, st_lds, tw);
+    fft_rec<LOGN, LOGNS + LOGR, INV, M, T, TMAJOR>(ld_first, st_lds, ld_lds, st_last, tw);
   } else if constexpr (LAST) {
-    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_lds, st_last, tw);
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_lds, st_last, tw);
   } else {
-    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T>(ld_lds, st_lds, tw);
-    fft_rec<LOGN, LOGNS + LOGR, INV, M, T>(ld_first, st_lds, ld_lds, st_last, tw);
+    stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_lds, st_lds, tw);
+    fft_rec<LOGN, LOGNS + LOGR, INV, M, T, TMAJOR>(ld_first, st_lds, ld_lds, st_last, tw);
   }
 }
 
 // Full transform of M length-2^LOGN sequences.  Passes 2..n-1 run in `lds`
-// (transform m at lds[m*S ...]); the first pass reads through ld_first and the
-// last pass writes through st_last.  Ends with a barrier.
-template <int LOGN, bool INV, int M, int T, int S, class LDF, class STF>
+// (transform m at lds[m*S ...], element n at pad16(n) for element-major tiles,
+// at n for TMAJOR tiles whose odd stride S already spreads the banks); the
+// first pass reads through ld_first and the last pass writes through st_last.
+// Ends with a barrier.
+// LDS position of element n in an element-major tile: one pad slot per 16
+// elements, so the stride-R writes of a Stockham pass (lanes j -> j*R + r)
+// spread over the 64 banks instead of hitting two of them.
+__device__ __forceinline__ constexpr int pad16(int n) { return n + (n >> 4); }
+template <int N>
+struct Padded {
+  static constexpr int SIZE = N + N / 16;  // padded length of one transform
+};
+
+template <int LOGN, bool INV, int M, int T, int S, bool TMAJOR = false, class LDF, class STF>
 __device__ __forceinline__ void fft(float2* lds, LDF& ld_first, STF& st_last, const float2* __restrict__ tw) {
-  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + n]; };
-  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + n] = v; };
-  fft_rec<LOGN, 0, INV, M, T>(ld_first, st_lds, ld_lds, st_last, tw);
+  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + (TMAJOR ? n : pad16(n))]; };
+  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + (TMAJOR ? n : pad16(n))] = v; };
+  fft_rec<LOGN, 0, INV, M, T, TMAJOR>(ld_first, st_lds, ld_lds, st_last, tw);
 }
 
 // Transform that starts and ends in LDS.
-template <int LOGN, bool INV, int M, int T, int S>
+template <int LOGN, bool INV, int M, int T, int S, bool TMAJOR = false>
 __device__ __forceinline__ void fft_lds(float2* lds, const float2* __restrict__ tw) {
-  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + n]; };
-  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + n] = v; };
-  fft_rec<LOGN, 0, INV, M, T>(ld_lds, st_lds, ld_lds, st_lds, tw);
+  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + (TMAJOR ? n : pad16(n))]; };
+  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + (TMAJOR ? n : pad16(n))] = v; };
+  fft_rec<LOGN, 0, INV, M, T, TMAJOR>(ld_lds, st_lds, ld_lds, st_lds, tw);
 }
 
 // ---------------------------------------------------------------------------
@@ -272,13 +300,46 @@ __device__ __forceinline__ float2 slot_mulc(bool slot0_a, float2 a, float2 b) {
 }
 
 // ---------------------------------------------------------------------------
-// Pair load of a real row: (u[i], u[i+1]) with zeros outside [0, valid).
+// Pair load/store of a real row: (u[i], u[i+1]) with zeros outside [0, valid).
+// Uses one 2-element vector access when the pair is in range and aligned
+// (always the case for even row strides), else two scalar accesses.
 // ---------------------------------------------------------------------------
 template <int DT>
 __device__ __forceinline__ float2 load_pair(const typename Elem<DT>::T* __restrict__ row, int64_t i, int64_t valid) {
+  using ET = typename Elem<DT>::T;
+  const ET* p = row + i;
+  if (i + 1 < valid && (reinterpret_cast<uintptr_t>(p) & (2 * sizeof(ET) - 1)) == 0) {
+    if constexpr (DT == NSQ_DTYPE_F32) {
+      return *reinterpret_cast<const float2*>(p);
+    } else if constexpr (DT == NSQ_DTYPE_BF16) {
+      const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+      return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+    } else {
+      return __half22float2(*reinterpret_cast<const __half2*>(p));
+    }
+  }
   float a = (i < valid) ? Elem<DT>::load(row, i) : 0.f;
   float b = (i + 1 < valid) ? Elem<DT>::load(row, i + 1) : 0.f;
   return make_float2(a, b);
+}
+
+// Stores (v.x, v.y) at row[i], row[i+1] for the indices below `valid`.
+template <int DT>
+__device__ __forceinline__ void store_pair(typename Elem<DT>::T* __restrict__ row, int64_t i, int64_t valid, float2 v) {
+  using ET = typename Elem<DT>::T;
+  ET* p = row + i;
+  if (i + 1 < valid && (reinterpret_cast<uintptr_t>(p) & (2 * sizeof(ET) - 1)) == 0) {
+    if constexpr (DT == NSQ_DTYPE_F32) {
+      *reinterpret_cast<float2*>(p) = v;
+    } else if constexpr (DT == NSQ_DTYPE_BF16) {
+      *reinterpret_cast<uint32_t*>(p) = uint32_t(f32_to_bf16_bits(v.x)) | (uint32_t(f32_to_bf16_bits(v.y)) << 16);
+    } else {
+      *reinterpret_cast<__half2*>(p) = __floats2half2_rn(v.x, v.y);
+    }
+    return;
+  }
+  if (i < valid) Elem<DT>::store(row, i, v.x);
+  if (i + 1 < valid) Elem<DT>::store(row, i + 1, v.y);
 }
 
 }  // namespace nsq

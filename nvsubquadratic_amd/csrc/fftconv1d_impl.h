@@ -28,6 +28,10 @@
 
 namespace nsq {
 
+// Keeps the scheduler from hoisting the loads of every unrolled spectral slot
+// ahead of the first one, which otherwise multiplies the live registers.
+#define NSQ_SLOT_FENCE() __builtin_amdgcn_sched_barrier(0)
+
 // ===========================================================================
 // Plan selection
 // ===========================================================================
@@ -38,6 +42,12 @@ struct Plan1D {
   bool fused;
   int logN1, logN2;  // 4-step split (fused == false)
 };
+
+// 4-step split N = N1 x N2: columns of N1 <= 256 points (two LDS passes) and
+// rows of N2 <= 4096 points; N1 grows beyond 256 only when N2 would exceed 4096.
+__host__ __device__ constexpr int split_log_n1(int logN) {
+  return (logN - 12 > ((logN / 2) < 8 ? (logN / 2) : 8)) ? (logN - 12) : ((logN / 2) < 8 ? (logN / 2) : 8);
+}
 
 inline bool make_plan(int64_t L, int64_t K, Plan1D& p) {
   if (L < 1 || K < 1 || K > 2 * L) return false;
@@ -50,7 +60,7 @@ inline bool make_plan(int64_t L, int64_t K, Plan1D& p) {
   p.fused = p.logN <= 13;
   if (!p.fused) {
     if (p.fold || p.logN > 22) return false;
-    p.logN1 = p.logN / 2 < 10 ? p.logN / 2 : 10;
+    p.logN1 = split_log_n1(p.logN);
     p.logN2 = p.logN - p.logN1;
   } else {
     p.logN1 = p.logN2 = 0;
@@ -66,6 +76,8 @@ struct FusedCfg {
   static constexpr int N = 1 << LOGN;
   static constexpr int M = LOGN >= 11 ? 1 : (2048 >> LOGN);  // channels per workgroup
   static constexpr int TILE = M * N;
+  static constexpr int SP = Padded<N>::SIZE;                   // padded LDS stride per transform
+  static constexpr int TILE_P = M * SP;                        // LDS elements of a tile
   static constexpr int T = TILE / 16;                          // threads
   static constexpr int E = 16;                                 // points per thread
   static constexpr int SLOTS = E / 2;                          // spectral slots per thread
@@ -84,10 +96,10 @@ template <int LOGN>
 __device__ __forceinline__ void lds_unpack(const float2* z, int m, int p, const float2* __restrict__ tw,
                                            float2& A, float2& Bc) {
   constexpr int N = 1 << LOGN;
-  const float2* zz = z + m * N;
+  const float2* zz = z + m * Padded<N>::SIZE;
   const bool s0 = (p == 0);
-  float2 zp = zz[p];
-  float2 zq = zz[s0 ? N / 2 : N - p];
+  float2 zp = zz[pad16(p)];
+  float2 zq = zz[pad16(s0 ? N / 2 : N - p)];
   float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p);
   real_unpack(s0, zp, zq, w, A, Bc);
 }
@@ -96,13 +108,13 @@ template <int LOGN>
 __device__ __forceinline__ void lds_repack(float2* z, int m, int p, const float2* __restrict__ tw, float2 A,
                                            float2 Bc) {
   constexpr int N = 1 << LOGN;
-  float2* zz = z + m * N;
+  float2* zz = z + m * Padded<N>::SIZE;
   const bool s0 = (p == 0);
   float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p);
   float2 zp, zq;
   real_repack(s0, A, Bc, w, zp, zq);
-  zz[p] = zp;
-  zz[s0 ? N / 2 : N - p] = zq;
+  zz[pad16(p)] = zp;
+  zz[pad16(s0 ? N / 2 : N - p)] = zq;
 }
 
 // Filter spectrum of channels h0..h0+M-1 into per-thread slot registers.
@@ -116,12 +128,13 @@ __device__ __forceinline__ void filter_spectrum(float2* lds, const float* __rest
     if (h >= H) return make_float2(0.f, 0.f);
     return load_pair<NSQ_DTYPE_F32>(k + int64_t(h) * K, 2 * int64_t(n), K);
   };
-  auto st = [&](int m, int n, float2 v) { lds[m * C::N + n] = v; };
-  fft<LOGN, false, C::M, C::T, C::N>(lds, ld, st, tw);
+  auto st = [&](int m, int n, float2 v) { lds[m * C::SP + pad16(n)] = v; };
+  fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
     int m, p;
-    slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+    slot_of<LOGN>(opaque_tid() + i * C::T, m, p);
     lds_unpack<LOGN>(lds, m, p, tw, hA[i], hB[i]);
   }
   __syncthreads();
@@ -135,7 +148,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
     const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ y, int B, int H, int L,
     int K, int b_per_wg, const float2* __restrict__ tw) {
   using C = FusedCfg<LOGN>;
-  __shared__ float2 lds[C::TILE];
+  __shared__ float2 lds[C::TILE_P];
   const int h0 = blockIdx.x * C::M;
   const int b0 = blockIdx.y * b_per_wg;
   const int b1 = min(B, b0 + b_per_wg);
@@ -150,12 +163,13 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
       if (h >= H) return make_float2(0.f, 0.f);
       return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
     };
-    auto st = [&](int m, int n, float2 v) { lds[m * C::N + n] = v; };
-    fft<LOGN, false, C::M, C::T, C::N>(lds, ld, st, tw);
+    auto st = [&](int m, int n, float2 v) { lds[m * C::SP + pad16(n)] = v; };
+    fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
       int m, p;
-      slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+      slot_of<LOGN>(opaque_tid() + i * C::T, m, p);
       float2 A, Bc;
       lds_unpack<LOGN>(lds, m, p, tw, A, Bc);
       A = slot_mul(p == 0, A, hA[i]);
@@ -176,16 +190,16 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
                         epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0 + 1) : 0.f));
     };
     if constexpr (!FOLD) {
-      auto ldl = [&](int m, int n) -> float2 { return lds[m * C::N + n]; };
-      fft<LOGN, true, C::M, C::T, C::N>(lds, ldl, epi, tw);
+      auto ldl = [&](int m, int n) -> float2 { return lds[m * C::SP + pad16(n)]; };
+      fft<LOGN, true, C::M, C::T, C::SP>(lds, ldl, epi, tw);
     } else {
-      fft_lds<LOGN, true, C::M, C::T, C::N>(lds, tw);
+      fft_lds<LOGN, true, C::M, C::T, C::SP>(lds, tw);
       // y[j] = full[j] + full[j + 2L]; in packed units index n and n + L.
       for (int e = threadIdx.x; e < C::TILE; e += C::T) {
         const int m = e >> LOGN, n = e & (C::N - 1);
         if (2 * n >= L) continue;
-        float2 v = lds[m * C::N + n];
-        if (n + L < C::N) v = cadd(v, lds[m * C::N + n + L]);
+        float2 v = lds[m * C::SP + pad16(n)];
+        if (n + L < C::N) v = cadd(v, lds[m * C::SP + pad16(n + L)]);
         epi(m, n, v);
       }
       __syncthreads();
@@ -201,8 +215,8 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     const float* __restrict__ k, const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ gx,
     float* __restrict__ gk, float* __restrict__ gs, int B, int H, int L, int K, const float2* __restrict__ tw) {
   using C = FusedCfg<LOGN>;
-  __shared__ float2 ldsG[C::TILE];
-  __shared__ float2 ldsX[C::TILE];
+  __shared__ float2 ldsG[C::TILE_P];
+  __shared__ float2 ldsX[C::TILE_P];
   const int h0 = blockIdx.x * C::M;
 
   float2 hA[C::SLOTS], hB[C::SLOTS];
@@ -227,14 +241,15 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
       if (h >= H) return make_float2(0.f, 0.f);
       return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
     };
-    auto stG = [&](int m, int n, float2 v) { ldsG[m * C::N + n] = v; };
-    auto stX = [&](int m, int n, float2 v) { ldsX[m * C::N + n] = v; };
-    fft<LOGN, false, C::M, C::T, C::N>(ldsG, ldg, stG, tw);
-    fft<LOGN, false, C::M, C::T, C::N>(ldsX, ldx, stX, tw);
+    auto stG = [&](int m, int n, float2 v) { ldsG[m * C::SP + pad16(n)] = v; };
+    auto stX = [&](int m, int n, float2 v) { ldsX[m * C::SP + pad16(n)] = v; };
+    fft<LOGN, false, C::M, C::T, C::SP>(ldsG, ldg, stG, tw);
+    fft<LOGN, false, C::M, C::T, C::SP>(ldsX, ldx, stX, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
       int m, p;
-      slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+      slot_of<LOGN>(opaque_tid() + i * C::T, m, p);
       float2 GA, GB, XA, XB;
       lds_unpack<LOGN>(ldsG, m, p, tw, GA, GB);
       lds_unpack<LOGN>(ldsX, m, p, tw, XA, XB);
@@ -256,15 +271,16 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
         Elem<DT>::store(gx, row + i0 + 1,
                         epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(g, row + i0 + 1) : 0.f));
     };
-    auto ldl = [&](int m, int n) -> float2 { return ldsG[m * C::N + n]; };
-    fft<LOGN, true, C::M, C::T, C::N>(ldsG, ldl, epi, tw);
+    auto ldl = [&](int m, int n) -> float2 { return ldsG[m * C::SP + pad16(n)]; };
+    fft<LOGN, true, C::M, C::T, C::SP>(ldsG, ldl, epi, tw);
   }
 
   // Filter gradient (and shortcut gradient = its lag-0 value).
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
     int m, p;
-    slot_of<LOGN>(threadIdx.x + i * C::T, m, p);
+    slot_of<LOGN>(opaque_tid() + i * C::T, m, p);
     lds_repack<LOGN>(ldsX, m, p, tw, qA[i], qB[i]);
   }
   __syncthreads();
@@ -276,26 +292,29 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     if (i0 + 1 < K) gk[int64_t(h) * K + i0 + 1] = v.y * scale;
     if (n == 0 && gs) gs[h] = v.x * scale;
   };
-  auto ldl = [&](int m, int n) -> float2 { return ldsX[m * C::N + n]; };
-  fft<LOGN, true, C::M, C::T, C::N>(ldsX, ldl, epik, tw);
+  auto ldl = [&](int m, int n) -> float2 { return ldsX[m * C::SP + pad16(n)]; };
+  fft<LOGN, true, C::M, C::T, C::SP>(ldsX, ldl, epik, tw);
 }
 
 // ===========================================================================
 // 4-step plan
 // ===========================================================================
-// Column kernels: a workgroup owns COLS adjacent columns of one signal row.
-constexpr int kCols = 16;
-
+// Column kernels: a workgroup owns C adjacent columns (n2) of one signal row
+// and runs their length-N1 transforms.  Thread lanes map to consecutive columns
+// (TMAJOR passes), so the first pass reads row segments of C consecutive packed
+// samples straight from HBM and the last pass writes row segments of C complex
+// values straight to the workspace: no separate staging copies.
 template <int LOGN1>
 struct ColCfg {
   static constexpr int N1 = 1 << LOGN1;
-  static constexpr int S = N1 + 1;  // padded column stride in LDS
-  static constexpr int TILE = kCols * N1;
+  static constexpr int M = (8192 >> LOGN1) < 8 ? 8 : ((8192 >> LOGN1) > 32 ? 32 : (8192 >> LOGN1));  // columns
+  static constexpr int S = N1 + 1;  // odd transform stride: consecutive columns hit distinct LDS banks
+  static constexpr int TILE = M * N1;
   static constexpr int T = TILE / 16;
 };
 
-// Description of a real input signal set: `rows` rows of `valid` samples with
-// row stride `stride` (elements), zero-extended to length F.
+// Description of a real input signal set: rows of `valid` samples with row
+// stride `stride` (elements), zero-extended to length F.
 template <int DT>
 struct RealRows {
   const typename Elem<DT>::T* p;
@@ -303,94 +322,83 @@ struct RealRows {
   int64_t valid;
 };
 
-// col_fwd: A[row][k1][n2] = W_N^{n2 k1} * sum_{n1} z[N2 n1 + n2] W_{N1}^{n1 k1}
-// grid = (rows, N2 / kCols).
+// col_fwd: A[row][k1][n2] = W_N^{n2 k1} * sum_{n1} z[N2 n1 + n2] W_{N1}^{n1 k1}.
+// grid = (rows, N2 / C).
 template <int LOGN1, int LOGN, int DT>
 __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_fwd_kernel(RealRows<DT> src, float2* __restrict__ ws,
                                                                     const float2* __restrict__ tw) {
   using C = ColCfg<LOGN1>;
-  constexpr int LOGN2 = LOGN - LOGN1;
-  constexpr int N2 = 1 << LOGN2;
-  __shared__ float2 lds[kCols * C::S];
-  const int c0 = blockIdx.y * kCols;
+  constexpr int N2 = 1 << (LOGN - LOGN1);
+  __shared__ float2 lds[C::M * C::S];
+  const int c0 = blockIdx.y * C::M;
   const int64_t row = blockIdx.x;
   const typename Elem<DT>::T* in = src.p + row * src.stride;
-  // Coalesced load: consecutive threads take consecutive columns of one n1.
-  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
-    const int c = e % kCols, n1 = e / kCols;
-    const int64_t m = int64_t(n1) * N2 + c0 + c;  // packed index
-    lds[c * C::S + n1] = load_pair<DT>(in, 2 * m, src.valid);
-  }
-  __syncthreads();
-  fft_lds<LOGN1, false, kCols, C::T, C::S>(lds, tw);
   float2* out = ws + row * (int64_t(1) << LOGN);
-  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
-    const int c = e % kCols, k1 = e / kCols;
-    const uint32_t n2 = c0 + c;
-    float2 v = cmul(lds[c * C::S + k1], root<LOGN>(tw, n2 * uint32_t(k1)));
-    out[int64_t(k1) * N2 + n2] = v;
-  }
+  auto ld = [&](int m, int n) -> float2 {
+    return load_pair<DT>(in, 2 * (int64_t(n) * N2 + c0 + m), src.valid);
+  };
+  auto st = [&](int m, int k1, float2 v) {
+    const uint32_t n2 = uint32_t(c0 + m);
+    out[int64_t(k1) * N2 + n2] = cmul(v, root<LOGN>(tw, n2 * uint32_t(k1)));
+  };
+  fft<LOGN1, false, C::M, C::T, C::S, true>(lds, ld, st, tw);
 }
 
-// col_inv: z[N2 n1 + n2] = sum_{k1} B[row][k1][n2] W_{N1}^{-n1 k1}, then the
-// epilogue functor consumes packed output index m = N2 n1 + n2.
+// col_inv: z[N2 n1 + n2] = sum_{k1} B[row][k1][n2] W_{N1}^{-n1 k1}; the
+// epilogue functor consumes (packed output index m = N2 n1 + n2, value).
 template <int LOGN1, int LOGN, class EPI>
 __device__ __forceinline__ void col_inv_body(const float2* __restrict__ ws_row, int c0, EPI& epi,
                                              const float2* __restrict__ tw, float2* lds) {
   using C = ColCfg<LOGN1>;
   constexpr int N2 = 1 << (LOGN - LOGN1);
-  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
-    const int c = e % kCols, k1 = e / kCols;
-    lds[c * C::S + k1] = ws_row[int64_t(k1) * N2 + c0 + c];
-  }
-  __syncthreads();
-  fft_lds<LOGN1, true, kCols, C::T, C::S>(lds, tw);
-  for (int e = threadIdx.x; e < C::TILE; e += C::T) {
-    const int c = e % kCols, n1 = e / kCols;
-    epi(int64_t(n1) * N2 + c0 + c, lds[c * C::S + n1]);
-  }
+  auto ld = [&](int m, int k1) -> float2 { return ws_row[int64_t(k1) * N2 + c0 + m]; };
+  auto st = [&](int m, int n1, float2 v) { epi(int64_t(n1) * N2 + c0 + m, v); };
+  fft<LOGN1, true, C::M, C::T, C::S, true>(lds, ld, st, tw);
 }
 
 // Output epilogue for y (forward) or gx (backward): out = epi(conv, s, aux)
-// where aux is x (forward) or g (backward).  grid = (B*H, N2/kCols).
+// where aux is x (forward) or g (backward).  grid = (B*H, N2/C).
 template <int LOGN1, int LOGN, int DT>
 __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_inv_out_kernel(
     const float2* __restrict__ ws, const typename Elem<DT>::T* __restrict__ aux,
     const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ out, int H, int L,
     const float2* __restrict__ tw) {
   using C = ColCfg<LOGN1>;
-  __shared__ float2 lds[kCols * C::S];
+  __shared__ float2 lds[C::M * C::S];
   const int64_t row = blockIdx.x;
   const int h = int(row % H);
   const float scale = 1.f / float(int64_t(1) << LOGN);
-  const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
-  const int64_t base = row * L;
+  const bool has_s = s != nullptr;
+  const float sv = has_s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
+  typename Elem<DT>::T* orow = out + row * L;
+  const typename Elem<DT>::T* arow = aux + row * L;
   auto epi = [&](int64_t m, float2 v) {
     const int64_t i0 = 2 * m;
-    if (i0 < L) Elem<DT>::store(out, base + i0, epilogue<DT>(v.x * scale, s != nullptr, sv, s ? Elem<DT>::load(aux, base + i0) : 0.f));
-    if (i0 + 1 < L)
-      Elem<DT>::store(out, base + i0 + 1,
-                      epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(aux, base + i0 + 1) : 0.f));
+    if (i0 >= L) return;
+    float2 a = has_s ? load_pair<DT>(arow, i0, L) : make_float2(0.f, 0.f);
+    float2 o = make_float2(epilogue<DT>(v.x * scale, has_s, sv, a.x), epilogue<DT>(v.y * scale, has_s, sv, a.y));
+    store_pair<DT>(orow, i0, L, o);
   };
-  col_inv_body<LOGN1, LOGN>(ws + row * (int64_t(1) << LOGN), blockIdx.y * kCols, epi, tw, lds);
+  col_inv_body<LOGN1, LOGN>(ws + row * (int64_t(1) << LOGN), blockIdx.y * C::M, epi, tw, lds);
 }
 
-// Filter-gradient epilogue: gk[h, 0:K] fp32, gs[h] = lag-0 value.  grid = (H, N2/kCols).
+// Filter-gradient epilogue: gk[h, 0:K] fp32, gs[h] = lag-0 value.  grid = (H, N2/C).
 template <int LOGN1, int LOGN>
 __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_inv_gk_kernel(const float2* __restrict__ ws,
                                                                        float* __restrict__ gk, float* __restrict__ gs,
                                                                        int K, const float2* __restrict__ tw) {
   using C = ColCfg<LOGN1>;
-  __shared__ float2 lds[kCols * C::S];
+  __shared__ float2 lds[C::M * C::S];
   const int64_t h = blockIdx.x;
   const float scale = 1.f / float(int64_t(1) << LOGN);
+  float* grow = gk + h * K;
   auto epi = [&](int64_t m, float2 v) {
     const int64_t i0 = 2 * m;
-    if (i0 < K) gk[h * K + i0] = v.x * scale;
-    if (i0 + 1 < K) gk[h * K + i0 + 1] = v.y * scale;
+    if (i0 >= K) return;
+    store_pair<NSQ_DTYPE_F32>(grow, i0, K, make_float2(v.x * scale, v.y * scale));
     if (m == 0 && gs) gs[h] = v.x * scale;
   };
-  col_inv_body<LOGN1, LOGN>(ws + h * (int64_t(1) << LOGN), blockIdx.y * kCols, epi, tw, lds);
+  col_inv_body<LOGN1, LOGN>(ws + h * (int64_t(1) << LOGN), blockIdx.y * C::M, epi, tw, lds);
 }
 
 // Row kernels.  Workgroup q handles the row pair {q, N1-q} (q >= 1) or the two
@@ -398,7 +406,9 @@ __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_inv_gk_kernel(const floa
 template <int LOGN2>
 struct RowCfg {
   static constexpr int N2 = 1 << LOGN2;
+  static constexpr int N2P = Padded<N2>::SIZE;  // padded LDS stride of a row
   static constexpr int TILE = 2 * N2;
+  static constexpr int TILE_P = 2 * N2P;
   static constexpr int T = TILE / 16;
   static constexpr int SLOTS = 8;  // N2 slots per workgroup / T threads
 };
@@ -433,6 +443,10 @@ __device__ __forceinline__ void row_slot(int q, int s, int& posA, int& posB, uin
     posB = N2 + (N2 - 1 - s2);
     kA = uint32_t(N1 / 2) + uint32_t(N1) * uint32_t(s2);
   }
+  // tile-relative (row, element) -> padded LDS position
+  constexpr int N2P = Padded<N2>::SIZE;
+  posA = (posA >= N2) ? N2P + pad16(posA - N2) : pad16(posA);
+  posB = (posB >= N2) ? N2P + pad16(posB - N2) : pad16(posB);
 }
 
 // Loads the two rows of the pair into a tile: tile row 0 = row q (or 0), tile
@@ -444,8 +458,8 @@ __device__ __forceinline__ void row_pair_fft(float2* lds, const float2* __restri
   constexpr int N1 = 1 << LOGN1;
   const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
   auto ld = [&](int m, int n) -> float2 { return sig[int64_t(m == 0 ? ra : rb) * C::N2 + n]; };
-  auto st = [&](int m, int n, float2 v) { lds[m * C::N2 + n] = v; };
-  fft<LOGN2, false, 2, C::T, C::N2>(lds, ld, st, tw);
+  auto st = [&](int m, int n, float2 v) { lds[m * C::N2P + pad16(n)] = v; };
+  fft<LOGN2, false, 2, C::T, C::N2P>(lds, ld, st, tw);
 }
 
 // Inverse row DFT of the tile, twiddle W_N^{-n2 k1}, store to sig rows.
@@ -456,13 +470,13 @@ __device__ __forceinline__ void row_pair_ifft_store(float2* lds, float2* __restr
   constexpr int N1 = 1 << LOGN1;
   constexpr int LOGN = LOGN1 + LOGN2;
   const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
-  auto ld = [&](int m, int n) -> float2 { return lds[m * C::N2 + n]; };
+  auto ld = [&](int m, int n) -> float2 { return lds[m * C::N2P + pad16(n)]; };
   auto st = [&](int m, int n, float2 v) {
     const int k1 = (m == 0) ? ra : rb;
     float2 w = root<LOGN>(tw, uint32_t(n) * uint32_t(k1));
     sig[int64_t(k1) * C::N2 + n] = cmulc(v, w);
   };
-  fft<LOGN2, true, 2, C::T, C::N2>(lds, ld, st, tw);
+  fft<LOGN2, true, 2, C::T, C::N2P>(lds, ld, st, tw);
 }
 
 template <int LOGN1, int LOGN2>
@@ -498,20 +512,24 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(float2* __res
                                                                     const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
   constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
-  __shared__ float2 lds[C::TILE];
+  __shared__ float2 lds[C::TILE_P];
   const int q = blockIdx.x % ((1 << LOGN1) / 2);
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 hA[C::SLOTS], hB[C::SLOTS];
   row_pair_fft<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) row_unpack<LOGN1, LOGN2>(lds, q, threadIdx.x + i * C::T, tw, hA[i], hB[i]);
+  for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
+    row_unpack<LOGN1, LOGN2>(lds, q, opaque_tid() + i * C::T, tw, hA[i], hB[i]);
+  }
   __syncthreads();
   for (int b = 0; b < B; ++b) {
     float2* sig = wsx + (int64_t(b) * H + h) * N;
     row_pair_fft<LOGN1, LOGN2>(lds, sig, q, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
-      const int s = threadIdx.x + i * C::T;
+    NSQ_SLOT_FENCE();
+      const int s = opaque_tid() + i * C::T;
       float2 A, Bc;
       row_unpack<LOGN1, LOGN2>(lds, q, s, tw, A, Bc);
       const bool s0 = (q == 0 && s == 0);
@@ -532,15 +550,16 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_bwd_kernel(float2* __res
                                                                     const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
   constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
-  __shared__ float2 ldsG[C::TILE];
-  __shared__ float2 ldsX[C::TILE];
+  __shared__ float2 ldsG[C::TILE_P];
+  __shared__ float2 ldsX[C::TILE_P];
   const int q = blockIdx.x % ((1 << LOGN1) / 2);
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 hA[C::SLOTS], hB[C::SLOTS], qA[C::SLOTS], qB[C::SLOTS];
   row_pair_fft<LOGN1, LOGN2>(ldsG, wsk + int64_t(h) * N, q, tw);
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
-    row_unpack<LOGN1, LOGN2>(ldsG, q, threadIdx.x + i * C::T, tw, hA[i], hB[i]);
+    NSQ_SLOT_FENCE();
+    row_unpack<LOGN1, LOGN2>(ldsG, q, opaque_tid() + i * C::T, tw, hA[i], hB[i]);
     qA[i] = qB[i] = make_float2(0.f, 0.f);
   }
   __syncthreads();
@@ -551,7 +570,8 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_bwd_kernel(float2* __res
     row_pair_fft<LOGN1, LOGN2>(ldsX, sigx, q, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
-      const int s = threadIdx.x + i * C::T;
+    NSQ_SLOT_FENCE();
+      const int s = opaque_tid() + i * C::T;
       const bool s0 = (q == 0 && s == 0);
       float2 GA, GB, XA, XB;
       row_unpack<LOGN1, LOGN2>(ldsG, q, s, tw, GA, GB);
@@ -564,7 +584,10 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_bwd_kernel(float2* __res
     row_pair_ifft_store<LOGN1, LOGN2>(ldsG, sigg, q, tw);
   }
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) row_repack<LOGN1, LOGN2>(ldsX, q, threadIdx.x + i * C::T, tw, qA[i], qB[i]);
+  for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
+    row_repack<LOGN1, LOGN2>(ldsX, q, opaque_tid() + i * C::T, tw, qA[i], qB[i]);
+  }
   __syncthreads();
   row_pair_ifft_store<LOGN1, LOGN2>(ldsX, wsk + int64_t(h) * N, q, tw);
 }
@@ -613,7 +636,7 @@ static void launch_4step_fwd(const void* x, const float* k, const void* s, void*
   using ET = typename Elem<DT>::T;
   float2* wsx = ws;
   float2* wsk = ws + int64_t(B) * H * N;
-  const int ncb = (1 << LOGN2) / kCols;
+  const int ncb = (1 << LOGN2) / ColCfg<LOGN1>::M;
   hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
                      RealRows<DT>{(const ET*)x, L, L}, wsx, tw);
   hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
@@ -633,7 +656,7 @@ static void launch_4step_bwd(const void* g, const void* x, const float* k, const
   float2* wsg = ws;
   float2* wsx = ws + int64_t(B) * H * N;
   float2* wsk = ws + 2 * int64_t(B) * H * N;
-  const int ncb = (1 << LOGN2) / kCols;
+  const int ncb = (1 << LOGN2) / ColCfg<LOGN1>::M;
   dim3 ct(ColCfg<LOGN1>::T);
   hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, RealRows<DT>{(const ET*)g, L, L},
                      wsg, tw);
@@ -684,12 +707,12 @@ struct FusedBwd {
   };
 };
 
-// 4-step instantiations: logN in [14, 22] with logN1 = min(logN/2, 10).
+// 4-step instantiations: logN in [14, 22] split by split_log_n1.
 template <int DT, bool BWD>
 struct FourStep {
   template <int LOGN>
   struct At {
-    static constexpr int L1 = (LOGN / 2) < 10 ? (LOGN / 2) : 10;
+    static constexpr int L1 = split_log_n1(LOGN);
     static constexpr int L2 = LOGN - L1;
     template <class... A>
     static void run(A&&... a) {

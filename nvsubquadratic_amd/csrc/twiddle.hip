@@ -3,13 +3,10 @@
 // One immutable table per device, built on first use and kept for the life of
 // the process: the library's only device allocation outside caller-provided
 // buffers.  Layout (float2 = (cos, -sin), i.e. forward-transform roots):
-//   [0,      2^14): W_{2^14}^j            coarse roots  exp(-2*pi*i*j/2^14)
-//   [2^14, 2^15):   W_{2^28}^j            fine roots    exp(-2*pi*i*j/2^28)
-// A root of unity W_{2^b}^m with b <= 14 is one load (coarse[m << (14-b)]);
-// for 14 < b <= 28 it is coarse[idx >> 14] * fine[idx & (2^14-1)] with
-// idx = m << (28-b).  Values are computed on the host in double precision and
-// rounded once to float, so every twiddle is within 1 ulp (coarse) or 2 ulp
-// (coarse*fine) of the exact root; no recurrences are used.
+//   [0, 2^14): W_{2^14}^j = exp(-2*pi*i*j/2^14)
+// A root of unity W_{2^b}^m with b <= 14 is one load (table[m << (14-b)]).
+// Values are computed on the host in double precision and rounded once to
+// float (within 0.5 ulp of the exact root).
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -45,13 +42,11 @@ const float2* twiddle_table() {
   std::lock_guard<std::mutex> lock(g_tw_mutex);
   if (g_tw[dev]) return g_tw[dev];
   constexpr int kN = 1 << 14;
-  std::vector<float2> host(2 * kN);
+  std::vector<float2> host(kN);
   const double two_pi = 6.283185307179586476925286766559;
   for (int j = 0; j < kN; ++j) {
     double a = two_pi * double(j) / double(kN);
     host[j] = make_float2(float(std::cos(a)), float(-std::sin(a)));
-    double b = two_pi * double(j) / double(1 << 28);
-    host[kN + j] = make_float2(float(std::cos(b)), float(-std::sin(b)));
   }
   float2* d = nullptr;
   hipError_t e = hipMalloc(&d, host.size() * sizeof(float2));
