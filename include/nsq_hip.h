@@ -82,6 +82,50 @@ int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const
                              float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Depthwise causal direct convolution, nn.Conv1d tap order with left padding
+ * K-1 (tests/ops/test_causal_conv1d_custom.py:65-72):
+ *   y[b,c,n] = act( sum_{j<K} w[c,j] x[b,c,n-K+1+j] + bias[c] ),  1 <= K <= 256,
+ *   act = identity (activation 0) or silu (activation 1).
+ * x, y, gy, gx: [B, C, L] in `dtype`; weight, gweight: [C, K] float32;
+ * bias, gbias: [C] float32 (may be NULL; gbias NULL skips its gradient).
+ * Replaces subquadratic_ops_torch.causal_conv1d bound at
+ *   nvsubquadratic/ops/causal_conv1d_custom.py:81-98 (its autograd backward
+ *   included), used by nvsubquadratic/modules/subq_ops_causal_conv1d.py:77-83.
+ */
+enum { NSQ_ACT_IDENTITY = 0, NSQ_ACT_SILU = 1 };
+
+int nsq_causal_conv1d_fwd(const void* x, const float* weight, const float* bias, void* y, int dtype, int activation,
+                          int64_t B, int64_t C, int64_t L, int64_t K, void* stream);
+
+size_t nsq_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t K, int activation);
+
+int nsq_causal_conv1d_bwd(const void* gy, const void* x, const float* weight, const float* bias, void* gx,
+                          float* gweight, float* gbias, int dtype, int activation, int64_t B, int64_t C, int64_t L,
+                          int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Back-to-back striped-Hyena short-conv block ("projection conv, pre-gate,
+ * mixer conv with skip, post-gate"; nvsubquadratic/ops/causal_conv1d_custom.py:101-121,
+ * which binds subquadratic_ops_torch.b2b_causal_conv1d):
+ *   p = causal_conv(x; weight_proj) over 3C channels;  q, k, v = p split in three;
+ *   z = k*v;  h = causal_conv(z; weight_mixer) + skip*z;  y = q*h.
+ * Both convs use the nn.Conv1d tap order above; fp32 throughout, y rounded once.
+ * x, gx: [B, 3C, L]; y, gy: [B, C, L] in `dtype`; weight_proj [3C, Kp],
+ * weight_mixer [C, Km], skip_bias [C] float32 (skip may be NULL = 0); gradients
+ * float32 of the same shapes (gskip may be NULL).  1 <= Kp, Km <= 256.
+ */
+int nsq_b2b_causal_conv1d_fwd(const void* x, const float* weight_proj, const float* weight_mixer,
+                              const float* skip_bias, void* y, int dtype, int64_t B, int64_t C, int64_t L, int64_t Kp,
+                              int64_t Km, void* stream);
+
+size_t nsq_b2b_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t Kp, int64_t Km);
+
+int nsq_b2b_causal_conv1d_bwd(const void* gy, const void* x, const float* weight_proj, const float* weight_mixer,
+                              const float* skip_bias, void* gx, float* gweight_proj, float* gweight_mixer,
+                              float* gskip, int dtype, int64_t B, int64_t C, int64_t L, int64_t Kp, int64_t Km,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

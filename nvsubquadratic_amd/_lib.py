@@ -65,6 +65,31 @@ _SIGNATURES = {
             _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p,
         ],
     ),
+    "nsq_causal_conv1d_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p],
+    ),
+    "nsq_causal_conv1d_bwd_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "nsq_causal_conv1d_bwd": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p,
+        ],
+    ),
+    "nsq_b2b_causal_conv1d_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_void_p],
+    ),
+    "nsq_b2b_causal_conv1d_bwd_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "nsq_b2b_causal_conv1d_bwd": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+            _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p,
+        ],
+    ),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,295 @@
+// Back-to-back striped-Hyena short-conv block, forward and backward (gfx950).
+//
+// Replaces subquadratic_ops_torch.b2b_causal_conv1d bound at
+// nvsubquadratic/ops/causal_conv1d_custom.py:101-121 ("projection conv,
+// pre-gate, mixer conv with skip, post-gate").  The reference does not state
+// the exact algorithm (its only test checks shape and finiteness,
+// tests/ops/test_causal_conv1d_custom.py:112-133), so this build fixes it as
+// follows, in fp32 throughout with one rounding of the output:
+//   p   = causal_conv(x; w_proj)   on all 3C channels (nn.Conv1d tap order)
+//   q, k, v = p[:, 0:C], p[:, C:2C], p[:, 2C:3C]
+//   z   = k * v                                   (pre-gate)
+//   h   = causal_conv(z; w_mixer) + skip * z      (mixer conv with skip)
+//   out = q * h                                   (post-gate)
+// The forward is one pass over HBM: 3 input rows read, 1 output row written.
+#include "direct_conv.h"
+
+namespace nsq {
+
+// grid = (B*C, ceil(L / kConvTile)).  xs_*: staged input rows; zs: z with the
+// mixer halo.
+template <int DT>
+__global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                                const float* __restrict__ wp,
+                                                                const float* __restrict__ wm,
+                                                                const float* __restrict__ skip,
+                                                                typename Elem<DT>::T* __restrict__ y, int C, int L,
+                                                                int Kp, int Km) {
+  constexpr int TF = conv_tile_floats(2 * kConvMaxK);
+  __shared__ float xs_q[conv_tile_floats(kConvMaxK)];
+  __shared__ float xs_k[TF];
+  __shared__ float xs_v[TF];
+  __shared__ float zs[conv_tile_floats(kConvMaxK)];
+  const int64_t row = blockIdx.x;  // b*C + c
+  const int b = int(row / C), c = int(row % C);
+  const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
+  const int64_t xq = (int64_t(b) * 3 * C + c) * L;
+  const int64_t xk = xq + int64_t(C) * L;
+  const int64_t xv = xk + int64_t(C) * L;
+  const int hz = Km - 1, hp = Kp - 1;
+  // q needs [n0 - hp, n0 + tile); k, v need [n0 - hz - hp, n0 + tile).
+  stage_row<DT>(xs_q, x + xq, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+  stage_row<DT>(xs_k, x + xk, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+  stage_row<DT>(xs_v, x + xv, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+  const float* wq = wp + int64_t(c) * Kp;
+  const float* wk = wp + int64_t(C + c) * Kp;
+  const float* wv = wp + int64_t(2 * C + c) * Kp;
+  // z[n] for n in [n0 - hz, n0 + tile): zs[i] = z[n0 - hz + i]; z of positions
+  // before the sequence start is 0 (the mixer conv's causal padding).
+  const int zcount = kConvTile + hz + 2 * kConvPer;
+  for (int i = threadIdx.x; i < zcount; i += kConvThreads) {
+    const int64_t n = n0 - hz + i;
+    float kk = 0.f, vv = 0.f;
+    if (n >= 0 && n < L) {
+      for (int j = 0; j < Kp; ++j) {
+        kk = fmaf(wk[j], xs_k[i + j], kk);
+        vv = fmaf(wv[j], xs_v[i + j], vv);
+      }
+    }
+    zs[i] = kk * vv;
+  }
+  __syncthreads();
+  const int base = threadIdx.x * kConvPer;
+  float qa[kConvPer], ha[kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) qa[e] = ha[e] = 0.f;
+  slide_fma(qa, xs_q, base, Kp, [&](int j) { return wq[j]; });
+  slide_fma(ha, zs, base, Km, [&](int j) { return wm[int64_t(c) * Km + j]; });
+  const float sk = skip ? skip[c] : 0.f;
+  typename Elem<DT>::T* yr = y + row * L;
+#pragma unroll
+  for (int e = 0; e < kConvPer; e += 2) {
+    const int64_t n = n0 + base + e;
+    if (n < L) {
+      const float h0 = fmaf(sk, zs[base + e + hz], ha[e]);
+      const float h1 = fmaf(sk, zs[base + e + 1 + hz], ha[e + 1]);
+      store_pair<DT>(yr, n, L, make_float2(qa[e] * h0, qa[e + 1] * h1));
+    }
+  }
+}
+
+// Backward step 1: recompute q, z, h; write gq = g*h into gp (q rows),
+// gh = g*q and z (fp32 workspaces).  grid as forward.
+template <int DT>
+__global__ __launch_bounds__(kConvThreads) void b2b_bwd1_kernel(const typename Elem<DT>::T* __restrict__ g,
+                                                                 const typename Elem<DT>::T* __restrict__ x,
+                                                                 const float* __restrict__ wp,
+                                                                 const float* __restrict__ wm,
+                                                                 const float* __restrict__ skip,
+                                                                 float* __restrict__ gp, float* __restrict__ gh,
+                                                                 float* __restrict__ zw, int C, int L, int Kp, int Km) {
+  constexpr int TF = conv_tile_floats(2 * kConvMaxK);
+  __shared__ float xs_q[conv_tile_floats(kConvMaxK)];
+  __shared__ float xs_k[TF];
+  __shared__ float xs_v[TF];
+  __shared__ float zs[conv_tile_floats(kConvMaxK)];
+  const int64_t row = blockIdx.x;
+  const int b = int(row / C), c = int(row % C);
+  const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
+  const int64_t xq = (int64_t(b) * 3 * C + c) * L;
+  const int64_t xk = xq + int64_t(C) * L;
+  const int64_t xv = xk + int64_t(C) * L;
+  const int hz = Km - 1, hp = Kp - 1;
+  stage_row<DT>(xs_q, x + xq, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+  stage_row<DT>(xs_k, x + xk, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+  stage_row<DT>(xs_v, x + xv, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+  const float* wq = wp + int64_t(c) * Kp;
+  const float* wk = wp + int64_t(C + c) * Kp;
+  const float* wv = wp + int64_t(2 * C + c) * Kp;
+  const int zcount = kConvTile + hz + 2 * kConvPer;
+  for (int i = threadIdx.x; i < zcount; i += kConvThreads) {
+    const int64_t n = n0 - hz + i;
+    float kk = 0.f, vv = 0.f;
+    if (n >= 0 && n < L) {
+      for (int j = 0; j < Kp; ++j) {
+        kk = fmaf(wk[j], xs_k[i + j], kk);
+        vv = fmaf(wv[j], xs_v[i + j], vv);
+      }
+    }
+    zs[i] = kk * vv;
+  }
+  __syncthreads();
+  const int base = threadIdx.x * kConvPer;
+  float qa[kConvPer], ha[kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) qa[e] = ha[e] = 0.f;
+  slide_fma(qa, xs_q, base, Kp, [&](int j) { return wq[j]; });
+  slide_fma(ha, zs, base, Km, [&](int j) { return wm[int64_t(c) * Km + j]; });
+  const float sk = skip ? skip[c] : 0.f;
+  const int64_t orow = row * L;                           // [B, C, L] rows
+  const int64_t prow = (int64_t(b) * 3 * C + c) * L;      // q rows of gp [B, 3C, L]
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) {
+    const int64_t n = n0 + base + e;
+    if (n < L) {
+      const float zv = zs[base + e + hz];
+      const float hv = fmaf(sk, zv, ha[e]);
+      const float gv = Elem<DT>::load(g, orow + n);
+      gp[prow + n] = gv * hv;
+      gh[orow + n] = gv * qa[e];
+      zw[orow + n] = zv;
+    }
+  }
+}
+
+// Backward step 2: gz = corr(gh, w_mixer) + skip*gh; recompute k, v;
+// gk = gz*v, gv = gz*k into gp (k and v rows).  grid as forward.
+template <int DT>
+__global__ __launch_bounds__(kConvThreads) void b2b_bwd2_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                                 const float* __restrict__ wp,
+                                                                 const float* __restrict__ wm,
+                                                                 const float* __restrict__ skip,
+                                                                 const float* __restrict__ gh, float* __restrict__ gp,
+                                                                 int C, int L, int Kp, int Km) {
+  __shared__ float ghs[conv_tile_floats(kConvMaxK)];
+  __shared__ float xs_k[conv_tile_floats(kConvMaxK)];
+  __shared__ float xs_v[conv_tile_floats(kConvMaxK)];
+  const int64_t row = blockIdx.x;
+  const int b = int(row / C), c = int(row % C);
+  const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
+  const int64_t xk = (int64_t(b) * 3 * C + C + c) * L;
+  const int64_t xv = xk + int64_t(C) * L;
+  const int hp = Kp - 1;
+  stage_row<NSQ_DTYPE_F32>(ghs, gh + row * L, n0, kConvTile + Km - 1 + 2 * kConvPer, L);
+  stage_row<DT>(xs_k, x + xk, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+  stage_row<DT>(xs_v, x + xv, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+  const float* wmr = wm + int64_t(c) * Km;
+  const int base = threadIdx.x * kConvPer;
+  float gz[kConvPer], ka[kConvPer], va[kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) gz[e] = ka[e] = va[e] = 0.f;
+  slide_fma(gz, ghs, base, Km, [&](int m) { return wmr[Km - 1 - m]; });
+  slide_fma(ka, xs_k, base, Kp, [&](int j) { return wp[int64_t(C + c) * Kp + j]; });
+  slide_fma(va, xs_v, base, Kp, [&](int j) { return wp[int64_t(2 * C + c) * Kp + j]; });
+  const float sk = skip ? skip[c] : 0.f;
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) {
+    const int64_t n = n0 + base + e;
+    if (n < L) {
+      const float gzv = fmaf(sk, ghs[base + e], gz[e]);
+      gp[xk + n] = gzv * va[e];
+      gp[xv + n] = gzv * ka[e];
+    }
+  }
+}
+
+__global__ void copy_column_kernel(const float* __restrict__ src, int ld, int col, float* __restrict__ dst, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[int64_t(i) * ld + col];
+}
+
+template <int DT>
+static void launch_b2b_fwd(const void* x, const float* wp, const float* wm, const float* skip, void* y, int B, int C,
+                           int L, int Kp, int Km, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
+  hipLaunchKernelGGL((b2b_fwd_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)x, wp, wm, skip, (ET*)y, C, L,
+                     Kp, Km);
+}
+
+template <int DT>
+static void launch_b2b_bwd(const void* g, const void* x, const float* wp, const float* wm, const float* skip, void* gx,
+                           float* gwp, float* gwm, float* gskip, int B, int C, int L, int Kp, int Km, float* ws,
+                           hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  const int64_t E = int64_t(B) * C * L;
+  float* gp = ws;            // [B, 3C, L]
+  float* gh = ws + 3 * E;    // [B, C, L]
+  float* zw = ws + 4 * E;    // [B, C, L]
+  dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
+  hipLaunchKernelGGL((b2b_bwd1_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)g, (const ET*)x, wp, wm, skip,
+                     gp, gh, zw, C, L, Kp, Km);
+  hipLaunchKernelGGL((b2b_bwd2_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)x, wp, wm, skip,
+                     (const float*)gh, gp, C, L, Kp, Km);
+  // input gradient and projection-weight gradient over all 3C channels
+  dim3 grid3(B * 3 * C, unsigned(ceil_div(L, kConvTile)));
+  hipLaunchKernelGGL((cconv_gx_kernel<DT, NSQ_DTYPE_F32>), grid3, dim3(kConvThreads), 0, st, (const float*)gp, wp, (ET*)gx,
+                     3 * C, L, Kp);
+  hipLaunchKernelGGL((cconv_wgrad_kernel<DT, NSQ_DTYPE_F32>), dim3(3 * C), dim3(kConvThreads), 0, st,
+                     (const float*)gp, (const ET*)x, gwp, (float*)nullptr, B, 3 * C, L, Kp);
+  // mixer-weight gradient: sum_n gh[n] z[n-Km+1+j]; its lag Km-1 is the skip gradient
+  hipLaunchKernelGGL((cconv_wgrad_kernel<NSQ_DTYPE_F32, NSQ_DTYPE_F32>), dim3(C), dim3(kConvThreads), 0, st,
+                     (const float*)gh, (const float*)zw, gwm, (float*)nullptr, B, C, L, Km);
+  if (gskip)
+    hipLaunchKernelGGL(copy_column_kernel, dim3(unsigned(ceil_div(C, 256))), dim3(256), 0, st, (const float*)gwm, Km,
+                       Km - 1, gskip, C);
+}
+
+static int validate_b2b(const void* a, const void* b, const float* wp, const float* wm, int dtype, int64_t B, int64_t C,
+                        int64_t L, int64_t Kp, int64_t Km) {
+  NSQ_CHECK_ARG(a && b && wp && wm, "b2b_causal_conv1d: null tensor pointer");
+  NSQ_CHECK_ARG(valid_dtype(dtype), "b2b_causal_conv1d: unsupported dtype code %d", dtype);
+  NSQ_CHECK_ARG(B >= 1 && C >= 1 && L >= 1, "b2b_causal_conv1d: sizes must be positive");
+  NSQ_CHECK_ARG(Kp >= 1 && Kp <= kConvMaxK && Km >= 1 && Km <= kConvMaxK,
+                "b2b_causal_conv1d: kernel sizes (%lld, %lld) outside [1, %d]", (long long)Kp, (long long)Km, kConvMaxK);
+  NSQ_CHECK_ARG(B * 3 * C <= 0x7fffffff && L <= 0x7fffffff, "b2b_causal_conv1d: tensor too large");
+  return NSQ_OK;
+}
+
+}  // namespace nsq
+
+using namespace nsq;
+
+extern "C" {
+
+int nsq_b2b_causal_conv1d_fwd(const void* x, const float* weight_proj, const float* weight_mixer,
+                              const float* skip_bias, void* y, int dtype, int64_t B, int64_t C, int64_t L, int64_t Kp,
+                              int64_t Km, void* stream) {
+  clear_error();
+  int rc = validate_b2b(x, y, weight_proj, weight_mixer, dtype, B, C, L, Kp, Km);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case NSQ_DTYPE_F32: launch_b2b_fwd<NSQ_DTYPE_F32>(x, weight_proj, weight_mixer, skip_bias, y, int(B), int(C), int(L), int(Kp), int(Km), st); break;
+    case NSQ_DTYPE_BF16: launch_b2b_fwd<NSQ_DTYPE_BF16>(x, weight_proj, weight_mixer, skip_bias, y, int(B), int(C), int(L), int(Kp), int(Km), st); break;
+    default: launch_b2b_fwd<NSQ_DTYPE_F16>(x, weight_proj, weight_mixer, skip_bias, y, int(B), int(C), int(L), int(Kp), int(Km), st); break;
+  }
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+size_t nsq_b2b_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t Kp, int64_t Km) {
+  (void)Kp;
+  (void)Km;
+  return size_t(5 * B * C * L) * sizeof(float);
+}
+
+int nsq_b2b_causal_conv1d_bwd(const void* gy, const void* x, const float* weight_proj, const float* weight_mixer,
+                              const float* skip_bias, void* gx, float* gweight_proj, float* gweight_mixer,
+                              float* gskip, int dtype, int64_t B, int64_t C, int64_t L, int64_t Kp, int64_t Km,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = validate_b2b(gy, x, weight_proj, weight_mixer, dtype, B, C, L, Kp, Km);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(gx && gweight_proj && gweight_mixer, "b2b_causal_conv1d_bwd: null gradient output pointer");
+  const size_t need = nsq_b2b_causal_conv1d_bwd_workspace_bytes(B, C, L, Kp, Km);
+  NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "b2b_causal_conv1d_bwd: workspace of %zu bytes required, got %zu",
+                need, workspace_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  float* ws = (float*)workspace;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      launch_b2b_bwd<NSQ_DTYPE_F32>(gy, x, weight_proj, weight_mixer, skip_bias, gx, gweight_proj, gweight_mixer, gskip, int(B), int(C), int(L), int(Kp), int(Km), ws, st);
+      break;
+    case NSQ_DTYPE_BF16:
+      launch_b2b_bwd<NSQ_DTYPE_BF16>(gy, x, weight_proj, weight_mixer, skip_bias, gx, gweight_proj, gweight_mixer, gskip, int(B), int(C), int(L), int(Kp), int(Km), ws, st);
+      break;
+    default:
+      launch_b2b_bwd<NSQ_DTYPE_F16>(gy, x, weight_proj, weight_mixer, skip_bias, gx, gweight_proj, gweight_mixer, gskip, int(B), int(C), int(L), int(Kp), int(Km), ws, st);
+      break;
+  }
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+}  // extern "C"

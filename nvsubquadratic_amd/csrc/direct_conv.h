@@ -1,0 +1,190 @@
+// Depthwise causal direct convolution building blocks (gfx950).
+//
+// Tap convention of nn.Conv1d with left padding K-1
+// (nvsubquadratic/modules/causal_conv1d.py:113-139, and the reference test
+// helper tests/ops/test_causal_conv1d_custom.py:65-72):
+//   y[b,c,n] = act( sum_{j<K} w[c,j] * x[b,c,n-K+1+j] + bias[c] )
+//
+// Work decomposition: a workgroup owns a tile of kTile outputs of one (b, c)
+// row.  The input tile plus its K-1 halo is staged once in LDS as fp32; each
+// thread produces kPer consecutive outputs from a register sliding window
+// (kPer new values per kPer taps), so LDS traffic is 2 reads per kPer^2 FMAs.
+// Weights are wave-uniform and are read through the scalar cache.
+#pragma once
+
+#include "fft_core.h"
+
+namespace nsq {
+
+constexpr int kConvThreads = 256;
+constexpr int kConvPer = 8;                            // outputs per thread
+constexpr int kConvTile = kConvThreads * kConvPer;    // outputs per workgroup
+constexpr int kConvMaxK = 256;
+
+// Activation codes NSQ_ACT_IDENTITY / NSQ_ACT_SILU come from include/nsq_hip.h.
+
+__device__ __forceinline__ float sigmoidf_(float v) { return 1.f / (1.f + __expf(-v)); }
+
+template <int ACT>
+__device__ __forceinline__ float act_fwd(float v) {
+  if constexpr (ACT == NSQ_ACT_SILU) return v * sigmoidf_(v);
+  return v;
+}
+
+// d silu(p) / dp = s(p) * (1 + p * (1 - s(p)))
+__device__ __forceinline__ float dsilu(float p) {
+  const float s = sigmoidf_(p);
+  return s * (1.f + p * (1.f - s));
+}
+
+// Stage src[row_off + first + i] for i in [0, count) into LDS as fp32 (zeros
+// outside [0, len)).  All threads participate; ends with a barrier.
+template <int DT>
+__device__ __forceinline__ void stage_row(float* dst, const typename Elem<DT>::T* __restrict__ row, int64_t first,
+                                          int count, int64_t len) {
+  for (int i = threadIdx.x; i < count; i += blockDim.x) {
+    const int64_t n = first + i;
+    dst[i] = (n >= 0 && n < len) ? Elem<DT>::load(row, n) : 0.f;
+  }
+  __syncthreads();
+}
+
+// acc[e] += sum_{j<K} wt(j) * xs[base + e + j], e < kConvPer, using a
+// register window; wt(j) must be wave-uniform.  xs must hold base + K + 7
+// valid entries (the caller's tile has kConvPer slack at the end).
+template <class WT>
+__device__ __forceinline__ void slide_fma(float (&acc)[kConvPer], const float* xs, int base, int K, WT wt) {
+  float win[2 * kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) win[e] = xs[base + e];
+  for (int jb = 0; jb < K; jb += kConvPer) {
+#pragma unroll
+    for (int e = 0; e < kConvPer; ++e) win[kConvPer + e] = xs[base + jb + kConvPer + e];
+#pragma unroll
+    for (int jj = 0; jj < kConvPer; ++jj) {
+      const float w = (jb + jj < K) ? wt(jb + jj) : 0.f;
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) acc[e] = fmaf(w, win[e + jj], acc[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < kConvPer; ++e) win[e] = win[kConvPer + e];
+  }
+}
+
+// LDS floats needed for a tile with halo K-1 plus the window's read-ahead.
+constexpr int conv_tile_floats(int kmax) { return kConvTile + kmax - 1 + 2 * kConvPer; }
+
+// Per-channel reduction for depthwise weight / bias gradients:
+//   gw[c, j] += sum_n gp[n] * x[n - K + 1 + j],  gb[c] += sum_n gp[n]
+// over one staged tile: gps[i] = gp[n0 + i] (i < kConvTile), xs[i] = x[n0 - K + 1 + i].
+// Thread t owns lag block lb = t % LB (lags 8*lb .. 8*lb+7) and the output
+// chunk nc = t / LB; acc and bacc persist across tiles.
+__device__ __forceinline__ void wgrad_tile(float (&acc)[kConvPer], float& bacc, const float* gps, const float* xs,
+                                           int K, int count) {
+  const int LB = (K + kConvPer - 1) / kConvPer;
+  const int NC = kConvThreads / LB;
+  const int t = threadIdx.x;
+  const int lb = t % LB, nc = t / LB;
+  if (nc >= NC) return;
+  const int chunk = (kConvTile + NC - 1) / NC;
+  const int nb = nc * chunk;
+  const int ne = min(count, nb + chunk);
+  if (nb >= ne) return;
+  float win[kConvPer];
+#pragma unroll
+  for (int jj = 0; jj < kConvPer; ++jj) win[jj] = xs[nb + lb * kConvPer + jj];
+  for (int n = nb; n < ne; ++n) {
+    const float g = gps[n];
+#pragma unroll
+    for (int jj = 0; jj < kConvPer; ++jj) acc[jj] = fmaf(g, win[jj], acc[jj]);
+    if (lb == 0) bacc += g;
+#pragma unroll
+    for (int jj = 0; jj < kConvPer - 1; ++jj) win[jj] = win[jj + 1];
+    win[kConvPer - 1] = xs[n + 1 + lb * kConvPer + kConvPer - 1];
+  }
+}
+
+// Fixed-order reduction of the wgrad_tile accumulators over the output
+// chunks (deterministic), then the store of gw[c, 0:K] and gb[c].
+__device__ __forceinline__ void wgrad_finish(float (&acc)[kConvPer], float bacc, float* red, float* gw_row, float* gb,
+                                             int K) {
+  const int LB = (K + kConvPer - 1) / kConvPer;
+  const int NC = kConvThreads / LB;
+  const int t = threadIdx.x;
+  const int lb = t % LB, nc = t / LB;
+  __syncthreads();
+  // red layout: [NC][LB*8] then [NC] for the bias partials
+  if (nc < NC) {
+#pragma unroll
+    for (int jj = 0; jj < kConvPer; ++jj) red[nc * LB * kConvPer + lb * kConvPer + jj] = acc[jj];
+    if (lb == 0) red[NC * LB * kConvPer + nc] = bacc;
+  }
+  __syncthreads();
+  for (int j = t; j < K; j += kConvThreads) {
+    float s = 0.f;
+    for (int c = 0; c < NC; ++c) s += red[c * LB * kConvPer + j];
+    gw_row[j] = s;
+  }
+  if (t == 0 && gb) {
+    float s = 0.f;
+    for (int c = 0; c < NC; ++c) s += red[NC * LB * kConvPer + c];
+    *gb = s;
+  }
+}
+
+// Kernels shared by the causal conv and B2B backward passes.
+// gx[i] = sum_j w[j] gp[i + K - 1 - j]  (gp = gpre in GT precision).  grid as forward.
+template <int DT, int GT>
+__global__ __launch_bounds__(kConvThreads) void cconv_gx_kernel(const typename Elem<GT>::T* __restrict__ gp,
+                                                                 const float* __restrict__ w,
+                                                                 typename Elem<DT>::T* __restrict__ gx, int C, int L,
+                                                                 int K) {
+  __shared__ float gs[conv_tile_floats(kConvMaxK)];
+  const int64_t row = blockIdx.x;
+  const int c = int(row % C);
+  const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
+  stage_row<GT>(gs, gp + row * L, n0, kConvTile + K - 1 + 2 * kConvPer, L);
+  const float* wr = w + int64_t(c) * K;
+  float acc[kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) acc[e] = 0.f;
+  const int base = threadIdx.x * kConvPer;
+  // acc[e] = sum_m w[K-1-m] gs[base + e + m]
+  slide_fma(acc, gs, base, K, [&](int m) { return wr[K - 1 - m]; });
+  typename Elem<DT>::T* gr = gx + row * L;
+#pragma unroll
+  for (int e = 0; e < kConvPer; e += 2) {
+    const int64_t n = n0 + base + e;
+    if (n < L) store_pair<DT>(gr, n, L, make_float2(acc[e], acc[e + 1]));
+  }
+}
+
+// Weight / bias gradients, one workgroup per channel (fixed-order sums over
+// batch and length).  grid = C.
+template <int DT, int GT>
+__global__ __launch_bounds__(kConvThreads) void cconv_wgrad_kernel(const typename Elem<GT>::T* __restrict__ gp,
+                                                                    const typename Elem<DT>::T* __restrict__ x,
+                                                                    float* __restrict__ gw, float* __restrict__ gb,
+                                                                    int B, int C, int L, int K) {
+  __shared__ float xs[conv_tile_floats(kConvMaxK)];
+  __shared__ float gps[kConvTile + 2 * kConvPer];
+  __shared__ float red[kConvThreads * kConvPer + kConvThreads];
+  const int c = blockIdx.x;
+  float acc[kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) acc[e] = 0.f;
+  float bacc = 0.f;
+  for (int b = 0; b < B; ++b) {
+    const int64_t row = int64_t(b) * C + c;
+    for (int64_t n0 = 0; n0 < L; n0 += kConvTile) {
+      const int count = int((L - n0) < kConvTile ? (L - n0) : kConvTile);
+      stage_row<DT>(xs, x + row * L, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
+      stage_row<GT>(gps, gp + row * L, n0, kConvTile + 2 * kConvPer, L);
+      wgrad_tile(acc, bacc, gps, xs, K, count);
+      __syncthreads();
+    }
+  }
+  wgrad_finish(acc, bacc, red, gw + int64_t(c) * K, gb ? gb + c : nullptr, K);
+}
+
+}  // namespace nsq

@@ -40,6 +40,43 @@ def _f32(a):
     return a.astype(np.float32).astype(np.float64)
 
 
+# (B, C, L, K) for the direct depthwise causal conv; K up to the 256-tap limit
+DIRECT_CASES = [(2, 16, 64, 3), (2, 36, 256, 3), (2, 64, 128, 7), (1, 3, 40, 64), (1, 2, 300, 256), (3, 2, 5, 9)]
+# (B, C, L, Kp, Km) for the B2B block
+B2B_CASES = [(2, 4, 64, 3, 3), (1, 3, 100, 4, 16), (2, 2, 70, 8, 128)]
+
+
+def _silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def direct_fixtures(rng) -> dict:
+    out = {}
+    for i, (B, C, L, K) in enumerate(DIRECT_CASES):
+        x = _f32(rng.standard_normal((B, C, L)))
+        w = _f32(rng.standard_normal((C, K)) / np.sqrt(K))
+        b = _f32(rng.standard_normal(C))
+        pre = direct.direct_causal_conv1d(x, w, b)
+        for name, v in dict(x=x, w=w, b=b, y=pre, y_silu=_silu(pre)).items():
+            out[f"d{i}_{name}"] = v
+        out[f"d{i}_shape"] = np.array([B, C, L, K])
+    out["n_direct"] = np.array(len(DIRECT_CASES))
+    for i, (B, C, L, Kp, Km) in enumerate(B2B_CASES):
+        x = _f32(rng.standard_normal((B, 3 * C, L)))
+        wp = _f32(rng.standard_normal((3 * C, Kp)) / np.sqrt(Kp))
+        wm = _f32(rng.standard_normal((C, Km)) / np.sqrt(Km))
+        sk = _f32(rng.standard_normal(C))
+        p = direct.direct_causal_conv1d(x, wp)
+        q, k, v = p[:, :C], p[:, C:2 * C], p[:, 2 * C:]
+        z = k * v
+        y = q * (direct.direct_causal_conv1d(z, wm) + sk[None, :, None] * z)
+        for name, val in dict(x=x, wp=wp, wm=wm, skip=sk, y=y).items():
+            out[f"b{i}_{name}"] = val
+        out[f"b{i}_shape"] = np.array([B, C, L, Kp, Km])
+    out["n_b2b"] = np.array(len(B2B_CASES))
+    return out
+
+
 def main() -> None:
     rng = np.random.default_rng(1234)
     out = {}
@@ -58,6 +95,9 @@ def main() -> None:
     out["n_causal"] = np.array(len(CAUSAL_CASES))
     np.savez_compressed(os.path.join(HERE, "causal1d.npz"), **out)
     print("wrote", os.path.join(HERE, "causal1d.npz"), len(CAUSAL_CASES), "cases")
+    d = direct_fixtures(np.random.default_rng(4321))
+    np.savez_compressed(os.path.join(HERE, "direct1d.npz"), **d)
+    print("wrote", os.path.join(HERE, "direct1d.npz"), len(DIRECT_CASES), "direct +", len(B2B_CASES), "b2b cases")
 
 
 if __name__ == "__main__":

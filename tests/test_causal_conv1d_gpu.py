@@ -1,0 +1,130 @@
+"""GPU parity of the HIP direct causal conv and B2B block against the CPU oracle.
+
+Mirrors tests/ops/test_causal_conv1d_custom.py (forward :63-110 incl. bias and
+silu; B2B shape/finite :112-133, here extended to values) and
+tests/modules/test_subq_ops_causal_conv1d.py (module forward/backward and the
+construction errors :74-148).  Tolerances: the reference's atol=1e-3/rtol=1e-4
+elementwise for fp32 plus rel-L2 <= 1e-4 (fp32) / 2e-2 (bf16).
+"""
+
+import numpy as np
+import os
+import pytest
+import torch
+
+from nvsubquadratic_amd.causal_conv1d_hip import b2b_causal_conv1d, causal_conv1d
+from nvsubquadratic_amd.modules import HipCausalConv1d
+from oracle.direct_ref import b2b_causal_conv1d_torch, causal_conv1d_torch
+from oracle.fftconv_ref import rel_l2
+
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "direct1d.npz")
+
+
+@pytest.mark.parametrize("C,L,K", [(16, 64, 3), (36, 256, 3), (64, 128, 7), (8, 5000, 128), (4, 3000, 256), (3, 7, 9)])
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("act", ["identity", "silu"])
+def test_forward_backward_vs_reference(C, L, K, with_bias, act):
+    torch.manual_seed(42)
+    x = torch.randn(2, C, L, requires_grad=True)
+    w = torch.randn(C, K, requires_grad=True)
+    b = torch.randn(C, requires_grad=True) if with_bias else None
+    y_ref = causal_conv1d_torch(x, w, b, act)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg = x.detach().cuda().requires_grad_(True)
+    wg = w.detach().cuda().requires_grad_(True)
+    bg = b.detach().cuda().requires_grad_(True) if with_bias else None
+    y = causal_conv1d(xg, wg, bg, act)
+    y.backward(g.cuda())
+    torch.testing.assert_close(y.cpu(), y_ref, atol=1e-3, rtol=1e-4)
+    assert rel_l2(y_ref, y) < 1e-4
+    assert rel_l2(x.grad, xg.grad) < 1e-4
+    assert rel_l2(w.grad, wg.grad) < 1e-4
+    if with_bias:
+        assert rel_l2(b.grad, bg.grad) < 1e-4
+
+
+def test_golden_fixtures():
+    d = np.load(GOLDEN)
+    for i in range(int(d["n_direct"])):
+        x, w, b = (torch.tensor(d[f"d{i}_{n}"], dtype=torch.float32, device="cuda") for n in ("x", "w", "b"))
+        assert rel_l2(d[f"d{i}_y"], causal_conv1d(x, w, b)) < 1e-5
+        assert rel_l2(d[f"d{i}_y_silu"], causal_conv1d(x, w, b, "silu")) < 1e-5
+    for i in range(int(d["n_b2b"])):
+        x, wp, wm, sk = (torch.tensor(d[f"b{i}_{n}"], dtype=torch.float32, device="cuda")
+                         for n in ("x", "wp", "wm", "skip"))
+        assert rel_l2(d[f"b{i}_y"], b2b_causal_conv1d(x, wp, wm, sk)) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_low_precision_io(dtype):
+    torch.manual_seed(1)
+    x = torch.randn(2, 32, 700, dtype=dtype)
+    w = torch.randn(32, 4)
+    y = causal_conv1d(x.cuda(), w.cuda(), None, "silu")
+    assert y.dtype == dtype
+    assert rel_l2(causal_conv1d_torch(x.float(), w, None, "silu"), y) < 2e-2
+
+
+def test_batch_and_tile_independence_bitwise():
+    torch.manual_seed(2)
+    x = torch.randn(3, 8, 5000, device="cuda")
+    w = torch.randn(8, 31, device="cuda")
+    y = causal_conv1d(x, w)
+    y1 = causal_conv1d(x[1:2].contiguous(), w)
+    assert torch.equal(y[1:2], y1)
+
+
+# --------------------------------------------------------------------------- B2B
+@pytest.mark.parametrize("B,C,L,Kp,Km", [(2, 16, 64, 3, 3), (4, 32, 128, 4, 4), (2, 16, 128, 8, 8),
+                                         (1, 8, 3000, 3, 128), (2, 4, 257, 5, 256)])
+def test_b2b_forward_backward(B, C, L, Kp, Km):
+    torch.manual_seed(42)
+    x = torch.randn(B, 3 * C, L, requires_grad=True)
+    wp = (torch.randn(3 * C, Kp) / Kp ** 0.5).requires_grad_(True)
+    wm = (torch.randn(C, Km) / Km ** 0.5).requires_grad_(True)
+    sk = torch.randn(C, requires_grad=True)
+    y_ref = b2b_causal_conv1d_torch(x, wp, wm, sk)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    args = [t.detach().cuda().requires_grad_(True) for t in (x, wp, wm, sk)]
+    y = b2b_causal_conv1d(*args)
+    assert y.shape == (B, C, L) and torch.isfinite(y).all()
+    y.backward(g.cuda())
+    assert rel_l2(y_ref, y) < 1e-4
+    for ref, got in zip((x, wp, wm, sk), args):
+        assert rel_l2(ref.grad, got.grad) < 1e-4
+
+
+def test_b2b_config2_shape_bf16_sample():
+    """Config 2 (B=4, L=8192, 3*4096 channels, k=3 then k=128) on a channel sample, bf16 I/O."""
+    torch.manual_seed(3)
+    B, C, L = 4, 64, 8192
+    x = torch.randn(B, 3 * C, L).to(torch.bfloat16)
+    wp = torch.randn(3 * C, 3)
+    wm = torch.randn(C, 128) / 128 ** 0.5
+    sk = torch.zeros(C)
+    y = b2b_causal_conv1d(x.cuda(), wp.cuda(), wm.cuda(), sk.cuda())
+    assert y.dtype == torch.bfloat16
+    assert rel_l2(b2b_causal_conv1d_torch(x.float(), wp, wm, sk), y) < 2e-2
+
+
+# --------------------------------------------------------------------------- module
+@pytest.mark.parametrize("C,L,K", [(36, 256, 3), (64, 512, 7), (16, 128, 4)])
+def test_module_matches_reference_conv(C, L, K):
+    torch.manual_seed(42)
+    ref = torch.nn.Conv1d(C, C, K, groups=C, bias=True)
+    fast = HipCausalConv1d(C, C, K, groups=C, bias=True).cuda()
+    fast.load_state_dict(ref.state_dict())
+    x = torch.randn(2, C, L, requires_grad=True)
+    y_ref = causal_conv1d_torch(x, ref.weight.squeeze(1), ref.bias)
+    y_ref.sum().backward()
+    xg = x.detach().cuda().requires_grad_(True)
+    y = fast(xg)
+    y.sum().backward()
+    torch.testing.assert_close(y.cpu(), y_ref, atol=1e-3, rtol=1e-4)
+    torch.testing.assert_close(xg.grad.cpu(), x.grad, atol=1e-2, rtol=1e-3)
+    torch.testing.assert_close(fast.weight.grad.cpu(), ref.weight.grad, atol=1e-2, rtol=1e-3)
+    torch.testing.assert_close(fast.bias.grad.cpu(), ref.bias.grad, atol=1e-2, rtol=1e-3)

@@ -1,0 +1,56 @@
+"""Construction checks of the module drop-ins and the fft_backend dispatch (CPU)."""
+
+import pytest
+import torch
+
+from nvsubquadratic_amd import dispatch
+from nvsubquadratic_amd.modules import HipCausalConv1d
+
+
+def test_rejects_non_depthwise():
+    with pytest.raises(ValueError, match="depthwise-only"):
+        HipCausalConv1d(in_channels=16, out_channels=16, kernel_size=3, groups=4)
+
+
+def test_rejects_in_neq_out():
+    with pytest.raises(ValueError, match="depthwise-only"):
+        HipCausalConv1d(in_channels=16, out_channels=32, kernel_size=3, groups=16)
+
+
+def test_rejects_invalid_activation():
+    with pytest.raises(ValueError, match="activation"):
+        HipCausalConv1d(in_channels=16, out_channels=16, kernel_size=3, groups=16, activation="relu")
+
+
+def test_is_nn_conv1d_subclass_with_reference_state_dict_layout():
+    m = HipCausalConv1d(in_channels=16, out_channels=16, kernel_size=3, groups=16, bias=True)
+    assert isinstance(m, torch.nn.Conv1d)
+    sd = m.state_dict()
+    assert sd["weight"].shape == (16, 1, 3) and sd["bias"].shape == (16,)
+
+
+def test_backend_name_validation():
+    dispatch.validate_fft_backend("hip")
+    with pytest.raises(AssertionError, match="Invalid fft_backend"):
+        dispatch.validate_fft_backend("cufft")
+
+
+def test_hip_constraints_mirror_reference_messages():
+    with pytest.raises(AssertionError, match="requires is_causal=True"):
+        dispatch.validate_hip_backend(1, False, "zero")
+    with pytest.raises(AssertionError, match="does not support causal"):
+        dispatch.validate_hip_backend(2, True, "zero")
+    with pytest.raises(AssertionError, match="only supports zero-padded"):
+        dispatch.validate_hip_backend(3, False, "circular")
+    with pytest.raises(ValueError, match="per-axis fft_padding"):
+        dispatch.validate_hip_backend(2, False, ["zero", "circular"])
+    with pytest.raises(AssertionError, match="data_dim"):
+        dispatch.validate_hip_backend(4, False, "zero")
+
+
+def test_hip_fn_selection():
+    from nvsubquadratic_amd import fftconv_hip as F
+
+    assert dispatch.hip_fftconv_fns(1, True) == (F.causal_fftconv1d_bhl_w_reshape, F.causal_fftconv1d_bhl)
+    assert dispatch.hip_fftconv_fns(1, True, use_chunked_fftconv=True) == (
+        F.causal_fftconv1d_bhl_w_reshape_chunked, F.causal_fftconv1d_bhl_chunked)
