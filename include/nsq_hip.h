@@ -126,6 +126,31 @@ int nsq_b2b_causal_conv1d_bwd(const void* gy, const void* x, const float* weight
                               float* gskip, int dtype, int64_t B, int64_t C, int64_t L, int64_t Kp, int64_t Km,
                               void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Non-causal "same" 2D / 3D FFT convolution (+ shortcut), nd = 2 or 3:
+ *   y = crop_{K_d//2}( x (*) k ).to(dtype) + shortcut * x
+ * x, y, g, gx: [B, H, S_0, .., S_{nd-1}] in `dtype`; k, gk: [kbatch*H, K_0, ..] float32
+ * with kbatch = 1 (shared) or B (per-sample FiLM kernels); shortcut [H] in `dtype`
+ * (may be NULL); gs: [kbatch*H] float32 per-kernel-row shortcut-gradient partials
+ * (the caller sums over kbatch).  S, K: host arrays of nd sizes, K_d <= 2 S_d, and
+ * every axis must fit an FFT length of 1024.
+ * Results follow nvsubquadratic/ops/fftconv.py:662-733 (fftconv2d_fp32_bhl) and
+ * :736-812 (fftconv3d_fp32_bhl); the 2D call replaces the native kernel bound at
+ * nvsubquadratic/ops/fftconv_custom.py:117-125 (subquadratic_ops_torch.fft_conv2d)
+ * plus the shortcut epilogue of fftconv2d_bhl (:133-160).  The reference has no
+ * native 3D kernel (nvsubquadratic/modules/ckconv_nd.py:721-724).
+ */
+size_t nsq_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
+                                      int64_t kbatch, int direction);
+
+int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                       int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                       float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -90,6 +90,18 @@ _SIGNATURES = {
             _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p,
         ],
     ),
+    "nsq_fftconv_nd_workspace_bytes": (
+        _c_size, [_c_int, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_int]),
+    "nsq_fftconv_nd_fwd": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, ctypes.POINTER(_c_i64),
+         ctypes.POINTER(_c_i64), _c_i64, _c_void_p, _c_size, _c_void_p],
+    ),
+    "nsq_fftconv_nd_bwd": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64,
+         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_void_p, _c_size, _c_void_p],
+    ),
 }
 
 _lock = threading.Lock()
@@ -165,6 +177,12 @@ def dtype_code(dt: torch.dtype) -> int:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def i64_array(values) -> ctypes.Array:
+    """Host int64 array argument (sizes of the N-d ops)."""
+    vals = [int(v) for v in values]
+    return (ctypes.c_int64 * len(vals))(*vals)
 
 
 def stream_ptr(device: torch.device) -> int:

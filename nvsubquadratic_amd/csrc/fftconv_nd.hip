@@ -1,0 +1,263 @@
+// Host plans and C ABI of the 2D / 3D non-causal FFT convolution (see
+// fftconv_nd_impl.h for the kernels and the pass structure).
+#include "fftconv_nd_impl.h"
+
+namespace nsq {
+
+struct NdPlan {
+  int nd;
+  int64_t B, H, kb;      // kb = kernel batch: 1 (shared) or B (per-sample FiLM)
+  int S[3], K[3];        // padded to 3 axes: (S0, S1, S2) with S1 = K1 = 1 for 2D
+  int lF[3], F[3], c[3];
+  int FH;
+  int64_t spec;
+};
+
+static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kb, NdPlan& p) {
+  if (nd != 2 && nd != 3) return false;
+  p.nd = nd;
+  p.B = B;
+  p.H = H;
+  p.kb = kb;
+  int s[3] = {1, 1, 1}, k[3] = {1, 1, 1};
+  if (nd == 2) {
+    s[0] = int(S[0]); s[2] = int(S[1]);
+    k[0] = int(K[0]); k[2] = int(K[1]);
+  } else {
+    for (int d = 0; d < 3; ++d) { s[d] = int(S[d]); k[d] = int(K[d]); }
+  }
+  for (int d = 0; d < 3; ++d) {
+    p.S[d] = s[d];
+    p.K[d] = k[d];
+    if (nd == 2 && d == 1) {
+      p.lF[d] = 0; p.F[d] = 1; p.c[d] = 0;
+      continue;
+    }
+    if (s[d] < 1 || k[d] < 1 || k[d] > 2 * s[d]) return false;
+    int lf = ilog2_ceil(int64_t(s[d]) + (k[d] + 1) / 2);
+    if (lf < 4) lf = 4;
+    if (lf > kNdMaxLogF) return false;
+    p.lF[d] = lf;
+    p.F[d] = 1 << lf;
+    p.c[d] = k[d] / 2;
+  }
+  p.FH = p.F[2] / 2 + 1;
+  p.spec = int64_t(p.F[0]) * p.F[1] * p.FH;
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Compile-time dispatch of the row / column passes on their log2 sizes.
+// ---------------------------------------------------------------------------
+template <int LO, int HI, class F>
+static bool with_log(int v, F&& f) {
+  if constexpr (LO > HI) {
+    return false;
+  } else {
+    if (v == LO) {
+      f(std::integral_constant<int, LO>{});
+      return true;
+    }
+    return with_log<LO + 1, HI>(v, f);
+  }
+}
+
+template <int DT>
+static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, float2* ws,
+                    const float2* tw, hipStream_t st) {
+  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.FH};
+  return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
+    constexpr int LOGN = decltype(L)::value;
+    using C = RowNdCfg<LOGN>;
+    hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0, st,
+                       (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+  });
+}
+
+template <int DT, int MODE>
+static bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int n1, RowInvOut o, const float2* tw,
+                    hipStream_t st) {
+  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.FH};
+  return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
+    constexpr int LOGN = decltype(L)::value;
+    using C = RowNdCfg<LOGN>;
+    hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0,
+                       st, ws, rg, o, tw);
+  });
+}
+
+// Column pass along axis d (0 or 1) of `nbh` blocks whose valid extent along
+// axis 0 is n_valid0 (used as the middle-row count of axis-1 passes).
+template <bool INV>
+static bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_valid0, int in_cnt, int out_off,
+                     int out_cnt, const float2* tw, hipStream_t st) {
+  ColGeom cg;
+  if (axis == 1) {
+    cg = ColGeom{n_valid0, int64_t(p.F[1]) * p.FH, p.spec, int64_t(p.FH), p.FH};
+  } else {
+    cg = ColGeom{1, 0, p.spec, int64_t(p.F[1]) * p.FH, p.F[1] * p.FH};
+  }
+  const int64_t n_outer = nbh * cg.n_mid;
+  return with_log<4, kNdMaxLogF>(p.lF[axis], [&](auto L) {
+    constexpr int LOGF = decltype(L)::value;
+    using C = ColNdCfg<LOGF>;
+    dim3 grid(unsigned(n_outer), unsigned(ceil_div(cg.inner_count, C::M)));
+    hipLaunchKernelGGL((nd_col_kernel<LOGF, INV>), grid, dim3(C::T), 0, st, ws, cg, in_cnt, out_off, out_cnt, tw);
+  });
+}
+
+static ColGeom axis0_geom(const NdPlan& p) { return ColGeom{1, 0, p.spec, int64_t(p.F[1]) * p.FH, p.F[1] * p.FH}; }
+
+// Filter spectrum: kb*H blocks of the [kb*H][K0][K1][K2] float32 kernel.
+static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {
+  const int64_t nk = p.kb * p.H;
+  if (!row_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], wsk, tw, st)) return false;
+  if (p.nd == 3 && !col_pass<false>(p, wsk, nk, 1, p.K[0], p.K[1], 0, p.F[1], tw, st)) return false;
+  return col_pass<false>(p, wsk, nk, 0, 1, p.K[0], 0, p.F[0], tw, st);
+}
+
+template <int DT>
+static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws,
+                       const float2* tw, hipStream_t st) {
+  const int64_t BH = p.B * p.H;
+  float2* wsx = ws;
+  float2* wsk = ws + BH * p.spec;
+  if (!filter_spectrum(p, k, wsk, tw, st)) return false;
+  if (!row_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
+  if (p.nd == 3 && !col_pass<false>(p, wsx, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
+  const ColGeom cg = axis0_geom(p);
+  bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
+    constexpr int LOGF = decltype(L)::value;
+    using C = ColNdCfg<LOGF>;
+    dim3 grid(unsigned(BH), unsigned(ceil_div(cg.inner_count, C::M)));
+    hipLaunchKernelGGL((nd_col_mul_kernel<LOGF>), grid, dim3(C::T), 0, st, wsx, (const float2*)wsk, cg, int(p.H),
+                       int(p.kb != 1), p.S[0], p.c[0], tw);
+  });
+  if (!ok) return false;
+  if (p.nd == 3 && !col_pass<true>(p, wsx, BH, 1, p.S[0], p.F[1], p.c[1], p.S[1], tw, st)) return false;
+  RowInvOut o{y, x, s, nullptr, int(p.H), p.c[2], p.S[2], 0, 0, 0,
+              1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2))};
+  return row_inv<DT, ND_OUT_Y>(p, wsx, BH, p.S[0], p.S[1], o, tw, st);
+}
+
+template <int DT>
+static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const float* k, const void* s, void* gx,
+                       float* gk, float* gs, float2* ws, const float2* tw, hipStream_t st) {
+  const int64_t BH = p.B * p.H, NK = p.kb * p.H;
+  float2* wsg = ws;
+  float2* wsx = wsg + BH * p.spec;
+  float2* wsk = wsx + BH * p.spec;
+  float2* wsq = wsk + NK * p.spec;
+  if (!filter_spectrum(p, k, wsk, tw, st)) return false;
+  if (!row_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
+  if (!row_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
+  if (p.nd == 3) {
+    if (!col_pass<false>(p, wsg, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
+    if (!col_pass<false>(p, wsx, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
+  }
+  const ColGeom cg = axis0_geom(p);
+  const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
+  bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
+    constexpr int LOGF = decltype(L)::value;
+    using C = ColNdBwdCfg<LOGF>;
+    dim3 grid(unsigned(NK), unsigned(ceil_div(cg.inner_count, C::M)));
+    hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF>), grid, dim3(C::T), 0, st, wsg, (const float2*)wsx,
+                       (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.K[0], rp, tw);
+  });
+  if (!ok) return false;
+  if (p.nd == 3) {
+    if (!col_pass<true>(p, wsg, BH, 1, p.S[0], p.F[1], 0, p.S[1], tw, st)) return false;
+    if (!col_pass<true>(p, wsq, NK, 1, p.K[0], p.F[1], 0, p.K[1], tw, st)) return false;
+  }
+  const float scale = 1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2));
+  RowInvOut og{gx, g, s, nullptr, int(p.H), 0, p.S[2], 0, 0, 0, scale};
+  if (!row_inv<DT, ND_OUT_Y>(p, wsg, BH, p.S[0], p.S[1], og, tw, st)) return false;
+  RowInvOut ok_{gk, nullptr, nullptr, gs, int(p.H), 0, p.K[2], p.c[0], p.c[1], p.c[2], scale};
+  return row_inv<NSQ_DTYPE_F32, ND_OUT_GK>(p, wsq, NK, p.K[0], p.K[1], ok_, tw, st);
+}
+
+static int validate_nd(int nd, const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H,
+                       const int64_t* S, const int64_t* K, int64_t kb, NdPlan& p) {
+  NSQ_CHECK_ARG(a && b && k && S && K, "fftconv_nd: null pointer argument");
+  NSQ_CHECK_ARG(nd == 2 || nd == 3, "fftconv_nd: nd must be 2 or 3 (got %d)", nd);
+  NSQ_CHECK_ARG(valid_dtype(dtype), "fftconv_nd: unsupported dtype code %d", dtype);
+  NSQ_CHECK_ARG(B >= 1 && H >= 1, "fftconv_nd: sizes must be positive");
+  NSQ_CHECK_ARG(kb == 1 || kb == B, "fftconv_nd: kernel batch must be 1 or B (got %lld, B=%lld)", (long long)kb,
+                (long long)B);
+  for (int d = 0; d < nd; ++d)
+    NSQ_CHECK_ARG(S[d] >= 1 && K[d] >= 1 && K[d] <= 2 * S[d],
+                  "fftconv_nd: axis %d: kernel size %lld must be in [1, 2*%lld]", d, (long long)K[d], (long long)S[d]);
+  if (!make_nd_plan(nd, B, H, S, K, kb, p)) {
+    set_error("fftconv_nd: unsupported shape: every axis needs an FFT length <= %d", 1 << kNdMaxLogF);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  return NSQ_OK;
+}
+
+}  // namespace nsq
+
+using namespace nsq;
+
+extern "C" {
+
+size_t nsq_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
+                                      int64_t kbatch, int direction) {
+  NdPlan p;
+  if (!S || !K || !make_nd_plan(nd, B, H, S, K, kbatch, p)) return 0;
+  const int64_t blocks = direction == NSQ_DIR_BWD ? (2 * B * H + 2 * kbatch * H) : (B * H + kbatch * H);
+  return size_t(blocks * p.spec) * sizeof(float2);
+}
+
+int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                       int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  NdPlan p;
+  int rc = validate_nd(nd, x, y, k, dtype, B, H, S, K, kbatch, p);
+  if (rc) return rc;
+  const size_t need = nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, NSQ_DIR_FWD);
+  NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv_nd_fwd: workspace of %zu bytes required, got %zu", need,
+                workspace_bytes);
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  float2* ws = (float2*)workspace;
+  bool ok;
+  switch (dtype) {
+    case NSQ_DTYPE_F32: ok = run_nd_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, ws, tw, st); break;
+    case NSQ_DTYPE_BF16: ok = run_nd_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, ws, tw, st); break;
+    default: ok = run_nd_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, ws, tw, st); break;
+  }
+  NSQ_CHECK_ARG(ok, "fftconv_nd_fwd: no kernel instantiated for this shape");
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                       float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  NdPlan p;
+  int rc = validate_nd(nd, g, x, k, dtype, B, H, S, K, kbatch, p);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(gx && gk, "fftconv_nd_bwd: null gradient output pointer");
+  NSQ_CHECK_ARG(!shortcut || gs, "fftconv_nd_bwd: gs required when a shortcut is given");
+  const size_t need = nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, NSQ_DIR_BWD);
+  NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv_nd_bwd: workspace of %zu bytes required, got %zu", need,
+                workspace_bytes);
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  float2* ws = (float2*)workspace;
+  bool ok;
+  switch (dtype) {
+    case NSQ_DTYPE_F32: ok = run_nd_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, ws, tw, st); break;
+    case NSQ_DTYPE_BF16: ok = run_nd_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, ws, tw, st); break;
+    default: ok = run_nd_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, ws, tw, st); break;
+  }
+  NSQ_CHECK_ARG(ok, "fftconv_nd_bwd: no kernel instantiated for this shape");
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+}  // extern "C"

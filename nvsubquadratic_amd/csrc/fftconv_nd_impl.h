@@ -1,0 +1,342 @@
+// Non-causal "same" 2D / 3D FFT convolution (forward and backward), gfx950.
+//
+// Semantics: nvsubquadratic/ops/fftconv.py:662-733 (fftconv2d_fp32_bhl) and
+// :736-812 (fftconv3d_fp32_bhl): zero-padded linear convolution, crop
+// [K_d//2, K_d//2 + S_d) per axis, cast to x.dtype, + shortcut * x.  Any FFT
+// length F_d >= S_d + ceil(K_d/2) gives the reference's result exactly (no
+// aliasing reaches the cropped window), so each axis uses the next power of two.
+//
+// Plan: the spectrum of one (b, h) image / volume is laid out in a workspace
+// block as [F0][F1][FH] (3D) or [F0][FH] (2D, F1 = 1), FH = F2/2 + 1 for the
+// last (contiguous, real) axis.  Passes:
+//   nd_row_fwd : real FFT along the last axis of the valid rows;
+//   nd_col     : complex FFT along axis 0 or 1 (strided), reading only the valid
+//                input rows (the rest is implicit zero padding) and writing
+//                either all F_d outputs (forward) or a cropped window moved to
+//                the front of the column (inverse);
+//   nd_col_mul : forward FFT along axis 0, spectral product, inverse FFT along
+//                axis 0 and crop, in one kernel (forward conv);
+//   nd_col_bwd : the same for the adjoint: P = G conj(K) R, Q = sum_b G conj(X) R,
+//                R = exp(-2 pi i sum_d c_d k_d / F_d) places g at the crop
+//                offset c_d (shift theorem), so gx and gk come out at window 0;
+//   nd_row_inv : inverse real FFT along the last axis, crop and epilogue.
+// Column passes map lanes to consecutive inner indices (coalesced row segments).
+#pragma once
+
+#include "fft_core.h"
+
+namespace nsq {
+
+// ---------------------------------------------------------------------------
+// Real row passes along the last axis (element-major tiles, M rows per WG).
+// ---------------------------------------------------------------------------
+template <int LOGN>
+struct RowNdCfg {
+  static constexpr int N = 1 << LOGN;  // packed complex length = F2 / 2
+  static constexpr int M = LOGN >= 11 ? 1 : (2048 >> LOGN);
+  static constexpr int SP = Padded<N>::SIZE;
+  static constexpr int T = (M * N) / 16;
+  static constexpr int SLOTS = 8;
+};
+
+// Rows are flattened over (bh, a0 < n0, a1 < n1).
+struct RowIdx {
+  int64_t bh;
+  int a0, a1;
+};
+__device__ __forceinline__ RowIdx row_index(int64_t r, int n0, int n1) {
+  RowIdx o;
+  o.a1 = int(r % n1);
+  const int64_t t = r / n1;
+  o.a0 = int(t % n0);
+  o.bh = t / n0;
+  return o;
+}
+
+// Row block geometry shared by the row passes.
+struct RowGeom {
+  int64_t rows;  // bh * n0 * n1
+  int n0, n1;    // valid counts of axes 0 and 1 for these rows
+  int64_t spec;  // spectrum block size (complex elements)
+  int F1, FH;
+};
+
+// Forward real FFT of rows of a contiguous [BH][n0][n1][len] real tensor,
+// zero-padded to F2 = 2N, into workspace bins [0, FH) of row (a0, a1).
+template <int LOGN, int DT>
+__global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typename Elem<DT>::T* __restrict__ src,
+                                                                        int len, RowGeom rg, float2* __restrict__ ws,
+                                                                        const float2* __restrict__ tw) {
+  using C = RowNdCfg<LOGN>;
+  __shared__ float2 lds[C::M * C::SP];
+  const int64_t r0 = int64_t(blockIdx.x) * C::M;
+  auto ld = [&](int m, int n) -> float2 {
+    const int64_t r = r0 + m;
+    if (r >= rg.rows) return make_float2(0.f, 0.f);
+    return load_pair<DT>(src + r * len, 2 * int64_t(n), len);
+  };
+  auto st = [&](int m, int n, float2 v) { lds[m * C::SP + pad16(n)] = v; };
+  fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
+  for (int i = 0; i < C::SLOTS; ++i) {
+    const int s = opaque_tid() + i * C::T;
+    const int m = s >> (LOGN - 1), p = s & (C::N / 2 - 1);
+    const int64_t r = r0 + m;
+    if (r >= rg.rows) continue;
+    const float2* zz = lds + m * C::SP;
+    const bool slot0 = (p == 0);
+    float2 A, Bc;
+    real_unpack(slot0, zz[pad16(p)], zz[pad16(slot0 ? C::N / 2 : C::N - p)],
+                slot0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p), A, Bc);
+    const RowIdx q = row_index(r, rg.n0, rg.n1);
+    float2* out = ws + q.bh * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+    if (slot0) {
+      out[0] = make_float2(A.x, 0.f);
+      out[C::N] = make_float2(A.y, 0.f);
+      out[C::N / 2] = Bc;
+    } else {
+      out[p] = A;
+      out[C::N - p] = cconj(Bc);
+    }
+  }
+}
+
+// Output epilogues of the inverse row pass.
+enum { ND_OUT_Y = 0, ND_OUT_GK = 1 };
+
+struct RowInvOut {
+  void* out;           // [rows][w2] (dtype for ND_OUT_Y, float for ND_OUT_GK)
+  const void* aux;     // x (forward) or g (backward) with the layout of `out` (ND_OUT_Y)
+  const void* s;       // shortcut [H] (ND_OUT_Y, may be null)
+  float* gs;           // [rows / (n0*n1)] lag-c value (ND_OUT_GK, may be null)
+  int H;               // channels (shortcut index = bh % H)
+  int off2, w2;        // last-axis window [off2, off2 + w2)
+  int ga0, ga1, ga2;   // lag whose value is the shortcut gradient (ND_OUT_GK)
+  float scale;         // 1 / (F0 * F1 * F2/2)
+};
+
+template <int LOGN, int DT, int MODE>
+__global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const float2* __restrict__ ws, RowGeom rg,
+                                                                        RowInvOut o, const float2* __restrict__ tw) {
+  using C = RowNdCfg<LOGN>;
+  using ET = typename Elem<DT>::T;
+  __shared__ float2 lds[C::M * C::SP];
+  const int64_t r0 = int64_t(blockIdx.x) * C::M;
+  for (int i = 0; i < C::SLOTS; ++i) {
+    const int s = opaque_tid() + i * C::T;
+    const int m = s >> (LOGN - 1), p = s & (C::N / 2 - 1);
+    const int64_t r = r0 + m;
+    const bool slot0 = (p == 0);
+    float2 zp = make_float2(0.f, 0.f), zq = zp;
+    if (r < rg.rows) {
+      const RowIdx q = row_index(r, rg.n0, rg.n1);
+      const float2* in = ws + q.bh * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+      float2 A, Bc;
+      if (slot0) {
+        A = make_float2(in[0].x, in[C::N].x);
+        Bc = in[C::N / 2];
+      } else {
+        A = in[p];
+        Bc = cconj(in[C::N - p]);
+      }
+      real_repack(slot0, A, Bc, slot0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p), zp, zq);
+    }
+    float2* zz = lds + m * C::SP;
+    zz[pad16(p)] = zp;
+    zz[pad16(slot0 ? C::N / 2 : C::N - p)] = zq;
+  }
+  __syncthreads();
+  auto ld = [&](int m, int n) -> float2 { return lds[m * C::SP + pad16(n)]; };
+  auto st = [&](int m, int n, float2 v) {
+    const int64_t r = r0 + m;
+    if (r >= rg.rows) return;
+    const int e0 = 2 * n - o.off2;  // output index of the even sample
+    const int h = int((r / (int64_t(rg.n0) * rg.n1)) % o.H);
+    const float vv[2] = {v.x * o.scale, v.y * o.scale};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e = e0 + t;
+      if (e < 0 || e >= o.w2) continue;
+      const int64_t idx = r * o.w2 + e;
+      if constexpr (MODE == ND_OUT_Y) {
+        const bool has_s = o.s != nullptr;
+        const float sv = has_s ? Elem<DT>::round(Elem<DT>::load((const ET*)o.s, h)) : 0.f;
+        const float a = has_s ? Elem<DT>::load((const ET*)o.aux, idx) : 0.f;
+        Elem<DT>::store((ET*)o.out, idx, epilogue<DT>(vv[t], has_s, sv, a));
+      } else {
+        ((float*)o.out)[idx] = vv[t];
+        if (o.gs && e == o.ga2) {
+          const RowIdx q = row_index(r, rg.n0, rg.n1);
+          if (q.a0 == o.ga0 && q.a1 == o.ga1) o.gs[q.bh] = vv[t];
+        }
+      }
+    }
+  };
+  fft<LOGN, true, C::M, C::T, C::SP>(lds, ld, st, tw);
+}
+
+// ---------------------------------------------------------------------------
+// Column passes along axis 0 or 1 (strided; TMAJOR tiles of M columns).
+// ---------------------------------------------------------------------------
+// M columns per workgroup (tile of about TARGET points), 16 points per thread.
+template <int LOGF, int TARGET = 8192>
+struct ColNdCfg {
+  static constexpr int F = 1 << LOGF;
+  static constexpr int M = (TARGET >> LOGF) < 4 ? 4 : ((TARGET >> LOGF) > 16 ? 16 : (TARGET >> LOGF));
+  static constexpr int S = F + 1;
+  static constexpr int TILE = M * F;
+  static constexpr int T = TILE / 16;
+};
+constexpr int kNdBwdTile = 4096;  // three tiles in LDS for the adjoint pass
+template <int LOGF>
+using ColNdBwdCfg = ColNdCfg<LOGF, kNdBwdTile>;
+constexpr int kNdMaxLogF = 10;    // 2D/3D axes: FFT length <= 1024
+
+// Column block geometry: column (o, j) with o = bh * n_mid + mid and inner
+// index j < inner_count starts at ws + bh*spec + mid*mid_stride + j; element
+// n of the column is at stride axis_stride.
+struct ColGeom {
+  int n_mid;
+  int64_t mid_stride;
+  int64_t spec;
+  int64_t axis_stride;
+  int inner_count;
+};
+
+__device__ __forceinline__ int64_t col_base(const ColGeom& cg, int64_t o) {
+  return (o / cg.n_mid) * cg.spec + (o % cg.n_mid) * cg.mid_stride;
+}
+
+// Generic pass: reads elements [0, in_cnt) (rest zero), transforms, writes
+// outputs [out_off, out_off + out_cnt) to positions [0, out_cnt).
+// grid = (n_outer, ceil(inner_count / M)).
+template <int LOGF, bool INV>
+__global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_kernel(float2* __restrict__ ws, ColGeom cg, int in_cnt,
+                                                                    int out_off, int out_cnt,
+                                                                    const float2* __restrict__ tw) {
+  using C = ColNdCfg<LOGF>;
+  __shared__ float2 lds[C::M * C::S];
+  float2* base = ws + col_base(cg, blockIdx.x);
+  const int j0 = blockIdx.y * C::M;
+  auto ld = [&](int m, int n) -> float2 {
+    if (j0 + m >= cg.inner_count || n >= in_cnt) return make_float2(0.f, 0.f);
+    return base[int64_t(n) * cg.axis_stride + j0 + m];
+  };
+  auto st = [&](int m, int k, float2 v) {
+    const int e = k - out_off;
+    if (j0 + m >= cg.inner_count || e < 0 || e >= out_cnt) return;
+    base[int64_t(e) * cg.axis_stride + j0 + m] = v;
+  };
+  fft<LOGF, INV, C::M, C::T, C::S, true>(lds, ld, st, tw);
+}
+
+// Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0).
+// grid = (B*H, ceil(inner_count / M)); Khat block index = bh (FiLM) or bh % H.
+template <int LOGF>
+__global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(float2* __restrict__ wsx,
+                                                                        const float2* __restrict__ wsk, ColGeom cg,
+                                                                        int H, int kfilm, int S0, int c0,
+                                                                        const float2* __restrict__ tw) {
+  using C = ColNdCfg<LOGF>;
+  __shared__ float2 lds[C::M * C::S];
+  const int64_t bh = blockIdx.x;
+  const int64_t hk = kfilm ? bh : (bh % H);
+  float2* base = wsx + bh * cg.spec;
+  const float2* kb = wsk + hk * cg.spec;
+  const int j0 = blockIdx.y * C::M;
+  auto ld = [&](int m, int n) -> float2 {
+    if (j0 + m >= cg.inner_count || n >= S0) return make_float2(0.f, 0.f);
+    return base[int64_t(n) * cg.axis_stride + j0 + m];
+  };
+  auto st_lds = [&](int m, int n, float2 v) { lds[m * C::S + n] = v; };
+  fft<LOGF, false, C::M, C::T, C::S, true>(lds, ld, st_lds, tw);
+  for (int e = opaque_tid(); e < C::TILE; e += C::T) {
+    const int m = e % C::M, k = e / C::M;
+    if (j0 + m < cg.inner_count) lds[m * C::S + k] = cmul(lds[m * C::S + k], kb[int64_t(k) * cg.axis_stride + j0 + m]);
+  }
+  __syncthreads();
+  auto ldl = [&](int m, int n) -> float2 { return lds[m * C::S + n]; };
+  auto st = [&](int m, int k, float2 v) {
+    const int e = k - c0;
+    if (j0 + m >= cg.inner_count || e < 0 || e >= S0) return;
+    base[int64_t(e) * cg.axis_stride + j0 + m] = v;
+  };
+  fft<LOGF, true, C::M, C::T, C::S, true>(lds, ldl, st, tw);
+}
+
+// Shift ramp parameters of the adjoint (3 axes; unused axes have c = 0).
+struct Ramp {
+  int c0, c1, c2;
+  int lF0, lF1, lF2;  // log2 sizes (lF1 = 0 for 2D)
+  int FH;             // inner index j -> (k1, k2) = (j / FH, j % FH) on axis-0 passes
+};
+
+__device__ __forceinline__ float2 shift_ramp(const Ramp& rp, int k0, int j) {
+  const int k1 = j / rp.FH, k2 = j % rp.FH;
+  const uint32_t m0 = (uint32_t(rp.c0) * uint32_t(k0)) & ((1u << rp.lF0) - 1u);
+  const uint32_t m1 = (uint32_t(rp.c1) * uint32_t(k1)) & ((1u << rp.lF1) - 1u);
+  const uint32_t m2 = (uint32_t(rp.c2) * uint32_t(k2)) & ((1u << rp.lF2) - 1u);
+  float a = float(m0) / float(1u << rp.lF0) + float(m1) / float(1u << rp.lF1) + float(m2) / float(1u << rp.lF2);
+  a = a - floorf(a);
+  return make_float2(__builtin_amdgcn_cosf(a), -__builtin_amdgcn_sinf(a));
+}
+
+// Adjoint, axis 0.  Shared kernel (kfilm = 0): grid.x = H, loops b; FiLM:
+// grid.x = B*H, one b.  Writes P (gx pre-image, window [0, S0)) into wsg and
+// Q (gk pre-image, window [0, K0)) into wsq.
+template <int LOGF>
+__global__ __launch_bounds__(ColNdBwdCfg<LOGF>::T) void nd_col_bwd_kernel(float2* __restrict__ wsg,
+                                                                        const float2* __restrict__ wsx,
+                                                                        const float2* __restrict__ wsk,
+                                                                        float2* __restrict__ wsq, ColGeom cg, int B,
+                                                                        int H, int kfilm, int S0, int K0, Ramp rp,
+                                                                        const float2* __restrict__ tw) {
+  using C = ColNdBwdCfg<LOGF>;
+  __shared__ float2 ldsG[C::M * C::S];
+  __shared__ float2 ldsX[C::M * C::S];
+  __shared__ float2 ldsQ[C::M * C::S];
+  const int64_t hk = blockIdx.x;
+  const int j0 = blockIdx.y * C::M;
+  const float2* kb = wsk + hk * cg.spec;
+  for (int e = threadIdx.x; e < C::TILE; e += C::T) ldsQ[(e % C::M) * C::S + e / C::M] = make_float2(0.f, 0.f);
+  const int nb = kfilm ? 1 : B;
+  for (int bi = 0; bi < nb; ++bi) {
+    const int64_t bh = kfilm ? hk : (int64_t(bi) * H + hk);
+    float2* gb = wsg + bh * cg.spec;
+    const float2* xb = wsx + bh * cg.spec;
+    auto ldg = [&](int m, int n) -> float2 {
+      if (j0 + m >= cg.inner_count || n >= S0) return make_float2(0.f, 0.f);
+      return gb[int64_t(n) * cg.axis_stride + j0 + m];
+    };
+    auto ldx = [&](int m, int n) -> float2 {
+      if (j0 + m >= cg.inner_count || n >= S0) return make_float2(0.f, 0.f);
+      return xb[int64_t(n) * cg.axis_stride + j0 + m];
+    };
+    auto stG = [&](int m, int n, float2 v) { ldsG[m * C::S + n] = v; };
+    auto stX = [&](int m, int n, float2 v) { ldsX[m * C::S + n] = v; };
+    fft<LOGF, false, C::M, C::T, C::S, true>(ldsG, ldg, stG, tw);
+    fft<LOGF, false, C::M, C::T, C::S, true>(ldsX, ldx, stX, tw);
+    for (int e = opaque_tid(); e < C::TILE; e += C::T) {
+      const int m = e % C::M, k = e / C::M;
+      if (j0 + m >= cg.inner_count) continue;
+      const float2 gsh = cmul(ldsG[m * C::S + k], shift_ramp(rp, k, j0 + m));
+      ldsQ[m * C::S + k] = cadd(ldsQ[m * C::S + k], cmulc(gsh, ldsX[m * C::S + k]));
+      ldsG[m * C::S + k] = cmulc(gsh, kb[int64_t(k) * cg.axis_stride + j0 + m]);
+    }
+    __syncthreads();
+    auto ldl = [&](int m, int n) -> float2 { return ldsG[m * C::S + n]; };
+    auto st = [&](int m, int k, float2 v) {
+      if (j0 + m >= cg.inner_count || k >= S0) return;
+      gb[int64_t(k) * cg.axis_stride + j0 + m] = v;
+    };
+    fft<LOGF, true, C::M, C::T, C::S, true>(ldsG, ldl, st, tw);
+  }
+  float2* qb = wsq + hk * cg.spec;
+  auto ldq = [&](int m, int n) -> float2 { return ldsQ[m * C::S + n]; };
+  auto stq = [&](int m, int k, float2 v) {
+    if (j0 + m >= cg.inner_count || k >= K0) return;
+    qb[int64_t(k) * cg.axis_stride + j0 + m] = v;
+  };
+  fft<LOGF, true, C::M, C::T, C::S, true>(ldsQ, ldq, stq, tw);
+}
+
+}  // namespace nsq

@@ -37,6 +37,20 @@ __all__ = [
     "causal_fftconv1d_blh_chunked",
     "causal_fftconv1d_fwd_raw",
     "causal_fftconv1d_bwd_raw",
+    "fftconv2d_bhl",
+    "fftconv2d_bhl_chunked",
+    "fftconv2d_bhl_w_reshape",
+    "fftconv2d_bhl_w_reshape_chunked",
+    "fftconv2d_blh",
+    "fftconv2d_blh_chunked",
+    "fftconv3d_bhl",
+    "fftconv3d_bhl_chunked",
+    "fftconv3d_bhl_w_reshape",
+    "fftconv3d_bhl_w_reshape_chunked",
+    "fftconv3d_blh",
+    "fftconv3d_blh_chunked",
+    "fftconv_nd_bwd_raw",
+    "fftconv_nd_fwd_raw",
 ]
 
 _DEFAULT_CHUNK_SIZE = 128
@@ -268,3 +282,189 @@ def causal_fftconv1d_blh_chunked(
 ) -> torch.Tensor:
     """Alias for :func:`causal_fftconv1d_bhl_w_reshape_chunked` (``fftconv_custom.py:405-412``)."""
     return causal_fftconv1d_bhl_w_reshape_chunked(x, kernel, shortcut, chunk_size)
+
+
+# ===========================================================================
+# 2D / 3D non-causal (zero-padded, "same") FFT convolution
+# ===========================================================================
+def fftconv_nd_fwd_raw(x, k, s, y, kbatch: int, workspace: torch.Tensor | None = None):
+    """Launch the N-d forward on the current stream.
+
+    ``x``/``y``: contiguous ``[B, H, *S]``; ``k``: contiguous float32
+    ``[kbatch*H, *K]``; ``s``: ``[H]`` in ``x.dtype`` or None.
+    """
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    nd = x.ndim - 2
+    B, H = x.shape[:2]
+    S = _lib.i64_array(x.shape[2:])
+    K = _lib.i64_array(k.shape[1:])
+    need = lib.nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, _lib.NSQ_DIR_FWD)
+    if need == 0:
+        raise NotImplementedError(f"fft_backend='hip' {nd}D: unsupported shape x={tuple(x.shape)} k={tuple(k.shape)}")
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(x.device, need)
+    _lib.check(lib.nsq_fftconv_nd_fwd(
+        nd, x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype), B, H, S, K, kbatch,
+        workspace.data_ptr(), workspace.numel(), _lib.stream_ptr(x.device)))
+    return y
+
+
+def fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, workspace: torch.Tensor | None = None):
+    """Launch the N-d backward (gs: ``[kbatch*H]`` partials or None)."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    nd = x.ndim - 2
+    B, H = x.shape[:2]
+    S = _lib.i64_array(x.shape[2:])
+    K = _lib.i64_array(k.shape[1:])
+    need = lib.nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, _lib.NSQ_DIR_BWD)
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(x.device, need)
+    _lib.check(lib.nsq_fftconv_nd_bwd(
+        nd, g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
+        _lib.dtype_code(x.dtype), B, H, S, K, kbatch, workspace.data_ptr(), workspace.numel(),
+        _lib.stream_ptr(x.device)))
+
+
+class _FFTConvND(torch.autograd.Function):
+    """x: [B, H, *S] contiguous; k: [kbatch*H, *K] contiguous float32; s: [H] in x.dtype or None."""
+
+    @staticmethod
+    def forward(ctx, x, k, s, kbatch):
+        y = torch.empty_like(x)
+        fftconv_nd_fwd_raw(x, k, s, y, kbatch)
+        ctx.save_for_backward(x, k, s)
+        ctx.kbatch = kbatch
+        ctx.has_s = s is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, k, s = ctx.saved_tensors
+        g = gy.to(x.dtype).contiguous()
+        gx = torch.empty_like(x)
+        gk = torch.empty_like(k)
+        H = x.shape[1]
+        gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
+        fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch)
+        gsum = gs.view(ctx.kbatch, H).sum(0).to(s.dtype) if ctx.has_s else None
+        return gx, gk, gsum, None
+
+
+def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, nd: int) -> torch.Tensor:
+    if x.ndim != nd + 2:
+        raise ValueError(f"x must be [B, H, {', '.join('S%d' % i for i in range(nd))}]; got {tuple(x.shape)}")
+    B, H = x.shape[:2]
+    if kernel.ndim == nd + 1:
+        kernel = kernel.unsqueeze(0)
+    assert kernel.ndim == nd + 2, f"Unexpected kernel shape: {tuple(kernel.shape)}."
+    assert kernel.shape[0] in (1, B), (
+        f"Leading dimension must be 1 or batch_size ({B}). Got kernel.shape={tuple(kernel.shape)}."
+    )
+    assert kernel.shape[1] == H, "Input and kernel must have the same number of channels (H)."
+    for d in range(nd):
+        assert kernel.shape[2 + d] <= 2 * x.shape[2 + d], (
+            f"Kernel size must be less than 2 * S_{d}. Got {kernel.shape[2 + d]}."
+        )
+    kbatch = kernel.shape[0]
+    input_dtype = x.dtype
+    compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
+    xc = x.to(compute_dtype).contiguous()
+    kc = kernel.float().reshape(kbatch * H, *kernel.shape[2:]).contiguous()
+    sc = None
+    if shortcut is not None:
+        if shortcut.shape != (H,):
+            raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
+        sc = shortcut.to(input_dtype).to(compute_dtype).contiguous()
+    return _FFTConvND.apply(xc, kc, sc, kbatch).to(input_dtype)
+
+
+def _chunked(fn, x, kernel, shortcut, chunk_size, nd):
+    if chunk_size is None:
+        chunk_size = _DEFAULT_CHUNK_SIZE
+    H = x.shape[1]
+    if H <= chunk_size:
+        return fn(x, kernel, shortcut)
+    k = kernel if kernel.ndim == nd + 2 else kernel.unsqueeze(0)
+    outs = []
+    for start in range(0, H, chunk_size):
+        end = min(start + chunk_size, H)
+        outs.append(fn(x[:, start:end], k[:, start:end], None if shortcut is None else shortcut[start:end]))
+    return torch.cat(outs, dim=1)
+
+
+def fftconv2d_bhl(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None = None) -> torch.Tensor:
+    """2D zero-padded FFT conv, BHL ``[B, H, X, Y]`` (``fftconv_custom.py:133-160``).
+
+    Kernel ``[1|B, H, Kx, Ky]`` or ``[H, Kx, Ky]`` (per-sample FiLM kernels are
+    supported as in ``_subq_conv2d_bhl``, ``fftconv_custom.py:117-125``).
+    Numerically matches ``nvsubquadratic.ops.fftconv.fftconv2d_fp32_bhl``
+    (``fftconv.py:662-733``).
+    """
+    return _nd_core(x, kernel, shortcut, 2)
+
+
+def fftconv2d_bhl_w_reshape(x, kernel, shortcut=None):
+    """BLH ``[B, X, Y, H]`` input, kernel ``[1|B, Kx, Ky, H]`` (``fftconv_custom.py:163-175``)."""
+    y = fftconv2d_bhl(rearrange(x, "b x y h -> b h x y"), rearrange(kernel, "b x y h -> b h x y"), shortcut)
+    return rearrange(y, "b h x y -> b x y h")
+
+
+def fftconv2d_blh(x, kernel, shortcut=None):
+    """Alias for :func:`fftconv2d_bhl_w_reshape` (``fftconv_custom.py:178-184``)."""
+    return fftconv2d_bhl_w_reshape(x, kernel, shortcut)
+
+
+def fftconv2d_bhl_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Channel-chunked 2D (``fftconv_custom.py:194-234``); bitwise equal to unchunked."""
+    return _chunked(fftconv2d_bhl, x, kernel, shortcut, chunk_size, 2)
+
+
+def fftconv2d_bhl_w_reshape_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Chunked BLH 2D (``fftconv_custom.py:237-250``)."""
+    y = fftconv2d_bhl_chunked(rearrange(x, "b x y h -> b h x y"), rearrange(kernel, "b x y h -> b h x y"),
+                              shortcut, chunk_size)
+    return rearrange(y, "b h x y -> b x y h")
+
+
+def fftconv2d_blh_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Alias for :func:`fftconv2d_bhl_w_reshape_chunked` (``fftconv_custom.py:253-260``)."""
+    return fftconv2d_bhl_w_reshape_chunked(x, kernel, shortcut, chunk_size)
+
+
+def fftconv3d_bhl(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None = None) -> torch.Tensor:
+    """3D zero-padded FFT conv, BHL ``[B, H, X, Y, Z]``.
+
+    Numerically matches ``nvsubquadratic.ops.fftconv.fftconv3d_fp32_bhl``
+    (``fftconv.py:736-812``); the reference has no accelerated 3D kernel.
+    """
+    return _nd_core(x, kernel, shortcut, 3)
+
+
+def fftconv3d_bhl_w_reshape(x, kernel, shortcut=None):
+    """BLH ``[B, X, Y, Z, H]`` input (mirrors ``fftconv.py:522-538``)."""
+    y = fftconv3d_bhl(rearrange(x, "b x y z h -> b h x y z"), rearrange(kernel, "b x y z h -> b h x y z"), shortcut)
+    return rearrange(y, "b h x y z -> b x y z h")
+
+
+def fftconv3d_blh(x, kernel, shortcut=None):
+    """Alias for :func:`fftconv3d_bhl_w_reshape`."""
+    return fftconv3d_bhl_w_reshape(x, kernel, shortcut)
+
+
+def fftconv3d_bhl_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Channel-chunked 3D (``fftconv_chunked.py`` semantics); bitwise equal to unchunked."""
+    return _chunked(fftconv3d_bhl, x, kernel, shortcut, chunk_size, 3)
+
+
+def fftconv3d_bhl_w_reshape_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Chunked BLH 3D."""
+    y = fftconv3d_bhl_chunked(rearrange(x, "b x y z h -> b h x y z"), rearrange(kernel, "b x y z h -> b h x y z"),
+                              shortcut, chunk_size)
+    return rearrange(y, "b h x y z -> b x y z h")
+
+
+def fftconv3d_blh_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Alias for :func:`fftconv3d_bhl_w_reshape_chunked`."""
+    return fftconv3d_bhl_w_reshape_chunked(x, kernel, shortcut, chunk_size)

@@ -134,3 +134,50 @@ def causal_fftconv1d_bwd_np(g, x, k, with_shortcut: bool, shortcut=None):
         gx = gx + np.asarray(shortcut, dtype=np.float64)[None, :, None] * g
         gs = (g * x).sum(axis=(0, 2))
     return gx, gk, gs
+
+
+# ---------------------------------------------------------------------------
+# 2D / 3D non-causal ("same") restatements
+# ---------------------------------------------------------------------------
+def fftconv_nd_torch(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None = None) -> torch.Tensor:
+    """nvsubquadratic/ops/fftconv.py:662-733 (2D) and :736-812 (3D) on CPU float32.
+
+    F_d = min(S_d + ceil(K_d/2), 2 S_d) per axis (:699-702 / :774-778),
+    rfftn -> multiply -> irfftn -> crop [K_d//2, K_d//2 + S_d) (:714-725 /
+    :789-805) -> cast to x.dtype -> + shortcut * x (shortcut cast to x.dtype as
+    in the subq wrapper, fftconv_custom.py:157-158).
+    """
+    nd = x.ndim - 2
+    if kernel.ndim == nd + 1:
+        kernel = kernel.unsqueeze(0)
+    H = x.shape[1]
+    S = x.shape[2:]
+    K = kernel.shape[2:]
+    dims = tuple(range(2, 2 + nd))
+    fft_shape = tuple(min(S[d] + (K[d] + 1) // 2, 2 * S[d]) for d in range(nd))
+    fx = torch.fft.rfftn(x.to(torch.float32), s=fft_shape, dim=dims)
+    fk = torch.fft.rfftn(kernel.to(torch.float32), s=fft_shape, dim=dims)
+    y = torch.fft.irfftn(fx * fk, s=fft_shape, dim=dims)
+    sl = [slice(None), slice(None)] + [slice(K[d] // 2, K[d] // 2 + S[d]) for d in range(nd)]
+    y = y[tuple(sl)].to(x.dtype)
+    if shortcut is not None:
+        y = y + shortcut.to(x.dtype).view(1, H, *([1] * nd)) * x
+    return y
+
+
+def fftconv_nd_np(x, kernel, shortcut=None) -> np.ndarray:
+    """float64 numpy version of :func:`fftconv_nd_torch` (power-of-two FFT sizes)."""
+    x = np.asarray(x, dtype=np.float64)
+    k = np.asarray(kernel, dtype=np.float64)
+    nd = x.ndim - 2
+    if k.ndim == nd + 1:
+        k = k[None]
+    S, K = x.shape[2:], k.shape[2:]
+    axes = tuple(range(2, 2 + nd))
+    fs = tuple(1 << int(np.ceil(np.log2(S[d] + (K[d] + 1) // 2))) for d in range(nd))
+    y = np.fft.irfftn(np.fft.rfftn(x, s=fs, axes=axes) * np.fft.rfftn(k, s=fs, axes=axes), s=fs, axes=axes)
+    sl = (slice(None), slice(None)) + tuple(slice(K[d] // 2, K[d] // 2 + S[d]) for d in range(nd))
+    y = y[sl]
+    if shortcut is not None:
+        y = y + np.asarray(shortcut, dtype=np.float64).reshape((1, -1) + (1,) * nd) * x
+    return y

@@ -46,6 +46,24 @@ DIRECT_CASES = [(2, 16, 64, 3), (2, 36, 256, 3), (2, 64, 128, 7), (1, 3, 40, 64)
 B2B_CASES = [(2, 4, 64, 3, 3), (1, 3, 100, 4, 16), (2, 2, 70, 8, 128)]
 
 
+# (B, H, S..., K...) for the 2D / 3D non-causal "same" conv
+ND_CASES = [((2, 3, 9, 7), (5, 3)), ((1, 2, 16, 16), (16, 16)), ((1, 2, 6, 5), (12, 9)),
+            ((1, 2, 5, 6, 7), (3, 4, 5)), ((2, 1, 4, 4, 4), (8, 1, 7))]
+
+
+def nd_fixtures(rng) -> dict:
+    out = {}
+    for i, (xs, ks) in enumerate(ND_CASES):
+        x = _f32(rng.standard_normal(xs))
+        k = _f32(rng.standard_normal((xs[1],) + ks))
+        s = _f32(rng.standard_normal(xs[1]))
+        y = direct.conv_same_nd(x, k) + s.reshape((1, -1) + (1,) * len(ks)) * x
+        for name, v in dict(x=x, k=k, s=s, y=y).items():
+            out[f"n{i}_{name}"] = v
+    out["n_nd"] = np.array(len(ND_CASES))
+    return out
+
+
 def _silu(v):
     return v / (1.0 + np.exp(-v))
 
@@ -98,6 +116,9 @@ def main() -> None:
     d = direct_fixtures(np.random.default_rng(4321))
     np.savez_compressed(os.path.join(HERE, "direct1d.npz"), **d)
     print("wrote", os.path.join(HERE, "direct1d.npz"), len(DIRECT_CASES), "direct +", len(B2B_CASES), "b2b cases")
+    n = nd_fixtures(np.random.default_rng(99))
+    np.savez_compressed(os.path.join(HERE, "nd.npz"), **n)
+    print("wrote", os.path.join(HERE, "nd.npz"), len(ND_CASES), "2D/3D cases")
 
 
 if __name__ == "__main__":
