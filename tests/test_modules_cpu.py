@@ -54,3 +54,11 @@ def test_hip_fn_selection():
     assert dispatch.hip_fftconv_fns(1, True) == (F.causal_fftconv1d_bhl_w_reshape, F.causal_fftconv1d_bhl)
     assert dispatch.hip_fftconv_fns(1, True, use_chunked_fftconv=True) == (
         F.causal_fftconv1d_bhl_w_reshape_chunked, F.causal_fftconv1d_bhl_chunked)
+
+
+def test_hip_fn_selection_2d_3d():
+    from nvsubquadratic_amd import fftconv_hip as F
+
+    assert dispatch.hip_fftconv_fns(2, False) == (F.fftconv2d_bhl_w_reshape, F.fftconv2d_bhl)
+    assert dispatch.hip_fftconv_fns(3, False, use_chunked_fftconv=True) == (
+        F.fftconv3d_bhl_w_reshape_chunked, F.fftconv3d_bhl_chunked)
