@@ -133,11 +133,13 @@ def main() -> None:
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     _log(f"workspace {ws_bytes / 2**30:.1f} GiB")
 
+    # The forward gets the backward-sized workspace, so it keeps its transformed
+    # x and k there and the backward reuses them (as autograd would).
     def fwd():
         F.causal_fftconv1d_fwd_raw(c.x, c.k, c.s, y, ws)
 
     def bwd():
-        F.causal_fftconv1d_bwd_raw(c.g, c.x, c.k, c.s, gx, gk, gs, ws)
+        F.causal_fftconv1d_bwd_raw(c.g, c.x, c.k, c.s, gx, gk, gs, ws, fwd_state=True)
 
     for _ in range(args.warmup):
         fwd()

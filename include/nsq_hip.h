@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 1
+#define NSQ_ABI_VERSION 2
 
 enum {
   NSQ_OK = 0,
@@ -63,6 +63,15 @@ int nsq_init(void);
  *   y[b,h,n] = sum_m k[h,m] x[b,h,n-m] over the FFT length min(L+K, 2L), i.e.
  *   including the circular wrap-around that length implies when K > L+1.
  * Requires 1 <= K <= 2L.
+ *
+ * Workspace: FFT lengths above 16384 use a workspace of complex64 rows.
+ * nsq_fftconv1d_causal_workspace_bytes(.., NSQ_DIR_FWD) is the minimum for the
+ * forward; (.., NSQ_DIR_BWD) is the size the backward needs.  A forward given a
+ * workspace of at least the NSQ_DIR_BWD size keeps its transformed x and k in
+ * it ("forward state"), and a backward called with fwd_state = 1 on that same,
+ * untouched workspace (same x, k) reuses them instead of transforming x and k
+ * again.  The backward consumes the state: call it once per forward.
+ * Shorter FFT lengths need no workspace (0 bytes; the pointer may be NULL).
  */
 size_t nsq_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int direction);
 
@@ -80,7 +89,7 @@ int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut
  */
 int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
                              float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
-                             void* workspace, size_t workspace_bytes, void* stream);
+                             void* workspace, size_t workspace_bytes, int fwd_state, void* stream);
 
 /*
  * Depthwise causal direct convolution, nn.Conv1d tap order with left padding

@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class HipLibraryError(RuntimeError):
@@ -62,7 +62,7 @@ _SIGNATURES = {
         _c_int,
         [
             _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
-            _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_int, _c_void_p,
         ],
     ),
     "nsq_causal_conv1d_fwd": (

@@ -46,22 +46,24 @@ int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
   float2* ws = nullptr;
+  bool save = false;
   if (!p.fused) {
     const size_t need = nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, NSQ_DIR_FWD);
     NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv1d_causal_fwd: workspace of %zu bytes required, got %zu",
                   need, workspace_bytes);
     ws = (float2*)workspace;
+    save = workspace_bytes >= nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, NSQ_DIR_BWD);
   }
   bool ok = false;
   switch (dtype) {
     case NSQ_DTYPE_F32:
-      ok = run_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, tw, st);
+      ok = run_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, save, tw, st);
       break;
     case NSQ_DTYPE_BF16:
-      ok = run_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, tw, st);
+      ok = run_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, save, tw, st);
       break;
     default:
-      ok = run_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, tw, st);
+      ok = run_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, save, tw, st);
       break;
   }
   NSQ_CHECK_ARG(ok, "fftconv1d_causal_fwd: no kernel for logN=%d", p.logN);
@@ -71,7 +73,7 @@ int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut
 
 int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
                              float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             size_t workspace_bytes, int fwd_state, void* stream) {
   clear_error();
   Plan1D p;
   int rc = validate(g, x, k, dtype, B, H, L, K, p);
@@ -91,13 +93,13 @@ int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const
   bool ok = false;
   switch (dtype) {
     case NSQ_DTYPE_F32:
-      ok = run_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, tw, st);
+      ok = run_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, fwd_state != 0, tw, st);
       break;
     case NSQ_DTYPE_BF16:
-      ok = run_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, tw, st);
+      ok = run_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, fwd_state != 0, tw, st);
       break;
     default:
-      ok = run_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, tw, st);
+      ok = run_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, fwd_state != 0, tw, st);
       break;
   }
   NSQ_CHECK_ARG(ok, "fftconv1d_causal_bwd: no kernel for logN=%d", p.logN);

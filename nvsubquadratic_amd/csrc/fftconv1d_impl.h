@@ -505,10 +505,13 @@ __device__ __forceinline__ void row_repack(float2* lds, int q, int s, const floa
 }
 
 // Forward row kernel.  grid = H * N1/2 (block = h * N1/2 + q).  wsx rows are
-// [B*H][N], wsk [H][N].
+// [B*H][N] (column-transformed x), wsk [H][N] (column-transformed k); the
+// product's inverse rows go to wsy (== wsx for in-place, or a separate region
+// so that wsx and wsk survive for the backward).
 template <int LOGN1, int LOGN2>
-__global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(float2* __restrict__ wsx,
-                                                                    const float2* __restrict__ wsk, int B, int H,
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(const float2* __restrict__ wsx,
+                                                                    const float2* __restrict__ wsk,
+                                                                    float2* __restrict__ wsy, int B, int H,
                                                                     const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
   constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
@@ -524,7 +527,7 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(float2* __res
   }
   __syncthreads();
   for (int b = 0; b < B; ++b) {
-    float2* sig = wsx + (int64_t(b) * H + h) * N;
+    const float2* sig = wsx + (int64_t(b) * H + h) * N;
     row_pair_fft<LOGN1, LOGN2>(lds, sig, q, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
@@ -536,7 +539,7 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(float2* __res
       row_repack<LOGN1, LOGN2>(lds, q, s, tw, slot_mul(s0, A, hA[i]), cmul(Bc, hB[i]));
     }
     __syncthreads();
-    row_pair_ifft_store<LOGN1, LOGN2>(lds, sig, q, tw);
+    row_pair_ifft_store<LOGN1, LOGN2>(lds, wsy + (int64_t(b) * H + h) * N, q, tw);
   }
 }
 
@@ -628,42 +631,51 @@ static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, cons
                        (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw);
 }
 
+// Workspace layout of the 4-step plan (rows of N complex64):
+//   [0, BH)          column-transformed x  (X')
+//   [BH, BH+H)       column-transformed k  (K')
+//   [BH+H, 2BH+H)    forward: inverse-row product (Y') when `save`; backward: G'
+// With `save`, X' and K' survive the forward so the backward can reuse them.
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
-                             float2* ws, const float2* tw, hipStream_t st) {
+                             float2* ws, bool save, const float2* tw, hipStream_t st) {
   constexpr int LOGN = LOGN1 + LOGN2;
   constexpr int64_t N = int64_t(1) << LOGN;
   using ET = typename Elem<DT>::T;
   float2* wsx = ws;
   float2* wsk = ws + int64_t(B) * H * N;
+  float2* wsy = save ? ws + (int64_t(B) * H + H) * N : wsx;
   const int ncb = (1 << LOGN2) / ColCfg<LOGN1>::M;
   hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
                      RealRows<DT>{(const ET*)x, L, L}, wsx, tw);
   hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
                      RealRows<NSQ_DTYPE_F32>{k, K, K}, wsk, tw);
-  hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st, wsx,
-                     (const float2*)wsk, B, H, tw);
+  hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st,
+                     (const float2*)wsx, (const float2*)wsk, wsy, B, H, tw);
   hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
-                     (const float2*)wsx, (const ET*)x, (const ET*)s, (ET*)y, H, L, tw);
+                     (const float2*)wsy, (const ET*)x, (const ET*)s, (ET*)y, H, L, tw);
 }
 
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_bwd(const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
-                             float* gs, int B, int H, int L, int K, float2* ws, const float2* tw, hipStream_t st) {
+                             float* gs, int B, int H, int L, int K, float2* ws, bool fwd_state, const float2* tw,
+                             hipStream_t st) {
   constexpr int LOGN = LOGN1 + LOGN2;
   constexpr int64_t N = int64_t(1) << LOGN;
   using ET = typename Elem<DT>::T;
-  float2* wsg = ws;
-  float2* wsx = ws + int64_t(B) * H * N;
-  float2* wsk = ws + 2 * int64_t(B) * H * N;
+  float2* wsx = ws;
+  float2* wsk = ws + int64_t(B) * H * N;
+  float2* wsg = ws + (int64_t(B) * H + H) * N;
   const int ncb = (1 << LOGN2) / ColCfg<LOGN1>::M;
   dim3 ct(ColCfg<LOGN1>::T);
   hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, RealRows<DT>{(const ET*)g, L, L},
                      wsg, tw);
-  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, RealRows<DT>{(const ET*)x, L, L},
-                     wsx, tw);
-  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), ct, 0, st,
-                     RealRows<NSQ_DTYPE_F32>{k, K, K}, wsk, tw);
+  if (!fwd_state) {
+    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st,
+                       RealRows<DT>{(const ET*)x, L, L}, wsx, tw);
+    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), ct, 0, st,
+                       RealRows<NSQ_DTYPE_F32>{k, K, K}, wsk, tw);
+  }
   hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st, wsg,
                      (const float2*)wsx, wsk, B, H, tw);
   hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, (const float2*)wsg,
@@ -728,30 +740,31 @@ struct FourStep {
 // fftconv1d_<dtype>.hip so the three instantiation sets compile in parallel.
 template <int DT>
 bool run_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
-             float2* ws, const float2* tw, hipStream_t st) {
+             float2* ws, bool save, const float2* tw, hipStream_t st) {
   if (p.fused) return dispatch_int<FusedFwd<DT>::template At, 3, 13>(p.logN, p, x, k, s, y, B, H, L, K, tw, st);
-  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, ws, tw, st);
+  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, ws, save, tw, st);
 }
 
 template <int DT>
 bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
-             float* gs, int B, int H, int L, int K, float2* ws, const float2* tw, hipStream_t st) {
+             float* gs, int B, int H, int L, int K, float2* ws, bool fwd_state, const float2* tw, hipStream_t st) {
   if (p.fused)
     return dispatch_int<FusedBwd<DT>::template At, 3, 13>(p.logN, p, g, x, k, s, gx, gk, gs, B, H, L, K, tw, st);
-  return dispatch_int<FourStep<DT, true>::template At, 14, 22>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, ws, tw, st);
+  return dispatch_int<FourStep<DT, true>::template At, 14, 22>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, ws,
+                                                                fwd_state, tw, st);
 }
 
 #define NSQ_DECLARE_FFTCONV1D(DT)                                                                               \
   extern template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
-                                   int, float2*, const float2*, hipStream_t);                                   \
+                                   int, float2*, bool, const float2*, hipStream_t);                             \
   extern template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
-                                   float*, float*, int, int, int, int, float2*, const float2*, hipStream_t);
+                                   float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t);
 
 #define NSQ_INSTANTIATE_FFTCONV1D(DT)                                                                    \
   template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
-                            int, float2*, const float2*, hipStream_t);                                   \
+                            int, float2*, bool, const float2*, hipStream_t);                             \
   template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
-                            float*, float*, int, int, int, int, float2*, const float2*, hipStream_t);
+                            float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t);
 
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_F32)
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_BF16)

@@ -102,8 +102,14 @@ def causal_fftconv1d_bwd_raw(
     gk: torch.Tensor,
     gs: torch.Tensor | None,
     workspace: torch.Tensor | None = None,
+    fwd_state: bool = False,
 ) -> None:
-    """Launch the backward kernels on the current stream (see include/nsq_hip.h)."""
+    """Launch the backward kernels on the current stream (see include/nsq_hip.h).
+
+    ``fwd_state=True`` reuses the transformed x and k that a forward call left
+    in ``workspace`` (a forward given a workspace of the backward's size keeps
+    them); the workspace must be untouched since that forward.
+    """
     lib = _lib.get_lib()
     _lib.check_device(x)
     B, H, L = x.shape
@@ -111,10 +117,11 @@ def causal_fftconv1d_bwd_raw(
     need = lib.nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, _lib.NSQ_DIR_BWD)
     if need and (workspace is None or workspace.numel() < need):
         workspace = _workspace(x.device, need)
+        fwd_state = False
     rc = lib.nsq_fftconv1d_causal_bwd(
         g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
         _lib.dtype_code(x.dtype), B, H, L, K, _lib.ptr(workspace),
-        0 if workspace is None else workspace.numel(), _lib.stream_ptr(x.device),
+        0 if workspace is None else workspace.numel(), int(bool(fwd_state)), _lib.stream_ptr(x.device),
     )
     _lib.check(rc)
 
@@ -129,8 +136,16 @@ class _CausalFFTConv1d(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, k, s):
         y = torch.empty_like(x)
-        causal_fftconv1d_fwd_raw(x, k, s, y)
+        ws = None
+        if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, k, s)):
+            # Backward-sized workspace: the forward keeps its transformed x and k
+            # in it for the backward (like autograd keeping rfft outputs).
+            B, H, L = x.shape
+            need = _lib.get_lib().nsq_fftconv1d_causal_workspace_bytes(B, H, L, k.shape[-1], _lib.NSQ_DIR_BWD)
+            ws = _workspace(x.device, need)
+        causal_fftconv1d_fwd_raw(x, k, s, y, ws)
         ctx.save_for_backward(x, k, s)
+        ctx.ws = ws
         ctx.has_s = s is not None
         return y
 
@@ -141,7 +156,8 @@ class _CausalFFTConv1d(torch.autograd.Function):
         gx = torch.empty_like(x)
         gk = torch.empty(k.shape, dtype=torch.float32, device=x.device)
         gs = torch.empty(k.shape[0], dtype=torch.float32, device=x.device) if ctx.has_s else None
-        causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs)
+        ws, ctx.ws = ctx.ws, None  # the backward consumes the forward state
+        causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ws, fwd_state=ws is not None)
         return gx, gk, (gs.to(s.dtype) if ctx.has_s else None)
 
 

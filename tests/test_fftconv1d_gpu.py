@@ -284,3 +284,44 @@ def test_config3_full_size_properties():
     kd[:, 0] = 1.0
     yd = F.causal_fftconv1d_bhl(x, kd)
     assert rel_l2(x, yd) < 1e-5
+
+
+@pytest.mark.parametrize("L", [16384, 65536])
+def test_backward_reusing_forward_state_is_bitwise_equal(L):
+    """The forward keeps its transformed x, k in a backward-sized workspace; reuse == recompute."""
+    from nvsubquadratic_amd import _lib
+
+    torch.manual_seed(8)
+    B, H = 2, 3
+    x = torch.randn(B, H, L, device="cuda").to(torch.bfloat16)
+    k = torch.randn(H, L, device="cuda")
+    s = torch.randn(H, device="cuda").to(torch.bfloat16)
+    g = torch.randn(B, H, L, device="cuda").to(torch.bfloat16)
+    need = _lib.get_lib().nsq_fftconv1d_causal_workspace_bytes(B, H, L, L, _lib.NSQ_DIR_BWD)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    F.causal_fftconv1d_fwd_raw(x, k, s, y, ws)
+    outs = []
+    for state, w in ((True, ws), (False, None)):
+        gx, gk, gs = torch.empty_like(x), torch.empty_like(k), torch.empty(H, device="cuda")
+        F.causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, w, fwd_state=state)
+        outs.append((gx, gk, gs))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    y2 = torch.empty_like(x)
+    F.causal_fftconv1d_fwd_raw(x, k, s, y2)  # minimum workspace, in-place plan
+    assert torch.equal(y, y2)
+
+
+def test_retain_graph_second_backward_matches_first():
+    torch.manual_seed(9)
+    x = torch.randn(1, 2, 20000, device="cuda", requires_grad=True)
+    k = torch.randn(1, 2, 20000, device="cuda", requires_grad=True)
+    g = torch.randn(1, 2, 20000, device="cuda")
+    y = F.causal_fftconv1d_bhl(x, k)
+    y.backward(g, retain_graph=True)
+    gx1, gk1 = x.grad.clone(), k.grad.clone()
+    x.grad = None
+    k.grad = None
+    y.backward(g)
+    assert torch.equal(gx1, x.grad) and torch.equal(gk1, k.grad)
