@@ -263,40 +263,42 @@ __device__ __forceinline__ void fft_lds(float2* lds, const float2* __restrict__ 
 // multiply separately.
 // ---------------------------------------------------------------------------
 // zp = Z[p], zq = Z[N-p] (for p = 0: zp = Z[0], zq = Z[N/2]); w = W_{2N}^p.
+// Branch-free: both the regular and the slot-0 forms are computed and one is
+// selected, so a slot loop has no divergent control flow.
 __device__ __forceinline__ void real_unpack(bool slot0, float2 zp, float2 zq, float2 w, float2& A, float2& Bc) {
-  if (slot0) {
-    A = make_float2(zp.x + zp.y, zp.x - zp.y);
-    Bc = cconj(zq);
-  } else {
-    float2 bc = cconj(zq);
-    float2 fe = cscale(cadd(zp, bc), 0.5f);
-    float2 fo = mul_neg_i(cscale(csub(zp, bc), 0.5f));
-    float2 wfo = cmul(w, fo);
-    A = cadd(fe, wfo);
-    Bc = csub(fe, wfo);
-  }
+  const float2 bc = cconj(zq);
+  const float2 fe = cscale(cadd(zp, bc), 0.5f);
+  const float2 fo = mul_neg_i(cscale(csub(zp, bc), 0.5f));
+  const float2 wfo = cmul(w, fo);
+  const float2 a_reg = cadd(fe, wfo);
+  const float2 b_reg = csub(fe, wfo);
+  A.x = slot0 ? zp.x + zp.y : a_reg.x;
+  A.y = slot0 ? zp.x - zp.y : a_reg.y;
+  Bc.x = slot0 ? bc.x : b_reg.x;
+  Bc.y = slot0 ? bc.y : b_reg.y;
 }
 
 // Inverse of real_unpack for a Hermitian spectrum given in slot form; returns
 // the values to place at Z[p] and Z[N-p] (slot 0: Z[0] and Z[N/2]) so that the
-// unscaled inverse FFT_N gives N * (u[2n] + i u[2n+1]).
+// unscaled inverse FFT_N gives N * (u[2n] + i u[2n+1]).  Branch-free.
 __device__ __forceinline__ void real_repack(bool slot0, float2 A, float2 Bc, float2 w, float2& zp, float2& zq) {
-  if (slot0) {
-    zp = make_float2(0.5f * (A.x + A.y), 0.5f * (A.x - A.y));
-    zq = cconj(Bc);
-  } else {
-    float2 fe = cscale(cadd(A, Bc), 0.5f);
-    float2 fo = cmulc(cscale(csub(A, Bc), 0.5f), w);  // * conj(w)
-    zp = cadd(fe, mul_i(fo));
-    zq = cadd(cconj(fe), mul_i(cconj(fo)));
-  }
+  const float2 fe = cscale(cadd(A, Bc), 0.5f);
+  const float2 fo = cmulc(cscale(csub(A, Bc), 0.5f), w);  // * conj(w)
+  const float2 p_reg = cadd(fe, mul_i(fo));
+  const float2 q_reg = cadd(cconj(fe), mul_i(cconj(fo)));
+  zp.x = slot0 ? 0.5f * (A.x + A.y) : p_reg.x;
+  zp.y = slot0 ? 0.5f * (A.x - A.y) : p_reg.y;
+  zq.x = slot0 ? Bc.x : q_reg.x;
+  zq.y = slot0 ? -Bc.y : q_reg.y;
 }
 
 __device__ __forceinline__ float2 slot_mul(bool slot0_a, float2 a, float2 b) {
-  return slot0_a ? make_float2(a.x * b.x, a.y * b.y) : cmul(a, b);
+  const float2 c = cmul(a, b);
+  return make_float2(slot0_a ? a.x * b.x : c.x, slot0_a ? a.y * b.y : c.y);
 }
 __device__ __forceinline__ float2 slot_mulc(bool slot0_a, float2 a, float2 b) {
-  return slot0_a ? make_float2(a.x * b.x, a.y * b.y) : cmulc(a, b);
+  const float2 c = cmulc(a, b);
+  return make_float2(slot0_a ? a.x * b.x : c.x, slot0_a ? a.y * b.y : c.y);
 }
 
 // ---------------------------------------------------------------------------

@@ -100,8 +100,7 @@ __device__ __forceinline__ void lds_unpack(const float2* z, int m, int p, const 
   const bool s0 = (p == 0);
   float2 zp = zz[pad16(p)];
   float2 zq = zz[pad16(s0 ? N / 2 : N - p)];
-  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p);
-  real_unpack(s0, zp, zq, w, A, Bc);
+  real_unpack(s0, zp, zq, root<LOGN + 1>(tw, p), A, Bc);  // W^0 = 1 for slot 0
 }
 
 template <int LOGN>
@@ -110,9 +109,8 @@ __device__ __forceinline__ void lds_repack(float2* z, int m, int p, const float2
   constexpr int N = 1 << LOGN;
   float2* zz = z + m * Padded<N>::SIZE;
   const bool s0 = (p == 0);
-  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p);
   float2 zp, zq;
-  real_repack(s0, A, Bc, w, zp, zq);
+  real_repack(s0, A, Bc, root<LOGN + 1>(tw, p), zp, zq);
   zz[pad16(p)] = zp;
   zz[pad16(s0 ? N / 2 : N - p)] = zq;
 }
@@ -419,34 +417,21 @@ struct RowCfg {
 template <int LOGN1, int LOGN2>
 __device__ __forceinline__ void row_slot(int q, int s, int& posA, int& posB, uint32_t& kA, bool& s0) {
   constexpr int N1 = 1 << LOGN1, N2 = 1 << LOGN2;
-  s0 = false;
-  if (q > 0) {
-    posA = s;                      // row q, k2 = s
-    posB = N2 + (N2 - 1 - s);      // row N1-q, k2 = N2-1-s
-    kA = uint32_t(q) + uint32_t(N1) * uint32_t(s);
-  } else if (s < N2 / 2) {
-    // row 0: bins N1*k2, partner N1*(N2-k2)
-    if (s == 0) {
-      s0 = true;
-      posA = 0;        // bin 0
-      posB = N2 / 2;   // bin N/2 = N1 * N2/2
-      kA = 0;
-    } else {
-      posA = s;
-      posB = N2 - s;
-      kA = uint32_t(N1) * uint32_t(s);
-    }
-  } else {
-    // row N1/2: bins N1/2 + N1*k2, partner k2' = N2-1-k2
-    const int s2 = s - N2 / 2;
-    posA = N2 + s2;
-    posB = N2 + (N2 - 1 - s2);
-    kA = uint32_t(N1 / 2) + uint32_t(N1) * uint32_t(s2);
-  }
-  // tile-relative (row, element) -> padded LDS position
   constexpr int N2P = Padded<N2>::SIZE;
-  posA = (posA >= N2) ? N2P + pad16(posA - N2) : pad16(posA);
-  posB = (posB >= N2) ? N2P + pad16(posB - N2) : pad16(posB);
+  // q > 0: (row q, s) <-> (row N1-q, N2-1-s); q == 0: row 0 pairs (s, N2-s)
+  // for s < N2/2 (s == 0 pairs bin 0 with bin N/2 at s = N2/2), and the
+  // second tile row (k1 = N1/2) pairs (s2, N2-1-s2) with s2 = s - N2/2.
+  const bool second = (q == 0) && (s >= N2 / 2);
+  const int s2 = second ? s - N2 / 2 : s;
+  s0 = (q == 0) && (s == 0);
+  const int eA = s2;                                                        // element of row A
+  const int eB = (q == 0 && !second) ? (s0 ? N2 / 2 : N2 - s) : (N2 - 1 - s2);
+  const bool rowA1 = second;                                                // tile row of A
+  const bool rowB1 = (q != 0) || second;                                    // tile row of B
+  posA = (rowA1 ? N2P : 0) + pad16(eA);
+  posB = (rowB1 ? N2P : 0) + pad16(eB);
+  const uint32_t k1A = second ? uint32_t(N1 / 2) : uint32_t(q);
+  kA = k1A + uint32_t(N1) * uint32_t(s2);
 }
 
 // Loads the two rows of the pair into a tile: tile row 0 = row q (or 0), tile
@@ -486,8 +471,7 @@ __device__ __forceinline__ void row_unpack(const float2* lds, int q, int s, cons
   uint32_t kA;
   bool s0;
   row_slot<LOGN1, LOGN2>(q, s, pa, pb, kA, s0);
-  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN1 + LOGN2 + 1>(tw, kA);
-  real_unpack(s0, lds[pa], lds[pb], w, A, Bc);
+  real_unpack(s0, lds[pa], lds[pb], root<LOGN1 + LOGN2 + 1>(tw, kA), A, Bc);
 }
 
 template <int LOGN1, int LOGN2>
@@ -497,9 +481,8 @@ __device__ __forceinline__ void row_repack(float2* lds, int q, int s, const floa
   uint32_t kA;
   bool s0;
   row_slot<LOGN1, LOGN2>(q, s, pa, pb, kA, s0);
-  float2 w = s0 ? make_float2(1.f, 0.f) : root<LOGN1 + LOGN2 + 1>(tw, kA);
   float2 zp, zq;
-  real_repack(s0, A, Bc, w, zp, zq);
+  real_repack(s0, A, Bc, root<LOGN1 + LOGN2 + 1>(tw, kA), zp, zq);
   lds[pa] = zp;
   lds[pb] = zq;
 }
@@ -509,7 +492,7 @@ __device__ __forceinline__ void row_repack(float2* lds, int q, int s, const floa
 // product's inverse rows go to wsy (== wsx for in-place, or a separate region
 // so that wsx and wsk survive for the backward).
 template <int LOGN1, int LOGN2>
-__global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(const float2* __restrict__ wsx,
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(4))) void row_fwd_kernel(const float2* __restrict__ wsx,
                                                                     const float2* __restrict__ wsk,
                                                                     float2* __restrict__ wsy, int B, int H,
                                                                     const float2* __restrict__ tw) {
@@ -547,7 +530,7 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_fwd_kernel(const float2*
 // gx pre-image), wsx rows [B*H][N] (column-transformed x), wsk [H][N] (in:
 // column-transformed k; out: gk pre-image).  grid = H * N1/2.
 template <int LOGN1, int LOGN2>
-__global__ __launch_bounds__(RowCfg<LOGN2>::T) void row_bwd_kernel(float2* __restrict__ wsg,
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(3))) void row_bwd_kernel(float2* __restrict__ wsg,
                                                                     const float2* __restrict__ wsx,
                                                                     float2* __restrict__ wsk, int B, int H,
                                                                     const float2* __restrict__ tw) {

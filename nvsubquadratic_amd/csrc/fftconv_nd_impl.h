@@ -86,7 +86,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
     const bool slot0 = (p == 0);
     float2 A, Bc;
     real_unpack(slot0, zz[pad16(p)], zz[pad16(slot0 ? C::N / 2 : C::N - p)],
-                slot0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p), A, Bc);
+                root<LOGN + 1>(tw, p), A, Bc);
     const RowIdx q = row_index(r, rg.n0, rg.n1);
     float2* out = ws + q.bh * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
     if (slot0) {
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
         A = in[p];
         Bc = cconj(in[C::N - p]);
       }
-      real_repack(slot0, A, Bc, slot0 ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, p), zp, zq);
+      real_repack(slot0, A, Bc, root<LOGN + 1>(tw, p), zp, zq);
     }
     float2* zz = lds + m * C::SP;
     zz[pad16(p)] = zp;
