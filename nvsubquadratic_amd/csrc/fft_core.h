@@ -41,7 +41,8 @@ __device__ __forceinline__ float2 mul_neg_i(float2 a) { return make_float2(a.y, 
 
 // ---------------------------------------------------------------------------
 // Roots of unity W_{2^LOGB}^m (forward sign).
-//  * LOGB <= 14: one load from the coarse table (correctly rounded roots).
+//  * LOGB <= 14: one load from the table segment of size 2^LOGB (correctly
+//    rounded roots; segment b starts at entry 2^b).
 //  * LOGB > 14 (the long-transform twiddles of the 4-step plan and the real
 //    unpack): the hardware sin/cos of gfx950, whose argument is in revolutions,
 //    on the exact fraction m / 2^LOGB.  Measured on MI355X against double
@@ -53,7 +54,7 @@ template <int LOGB>
 __device__ __forceinline__ float2 root(const float2* __restrict__ tw, uint32_t m) {
   static_assert(LOGB >= 0 && LOGB <= 24, "root: size out of range");
   if constexpr (LOGB <= 14) {
-    return tw[m << (14 - LOGB)];
+    return tw[(1u << LOGB) + (m & ((1u << LOGB) - 1u))];
   } else {
     const float a = float(m & ((1u << LOGB) - 1u)) * (1.0f / float(1u << LOGB));
     return make_float2(__builtin_amdgcn_cosf(a), -__builtin_amdgcn_sinf(a));
@@ -170,8 +171,21 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
   constexpr int NS = 1 << LOGNS;
   constexpr int PER = (M * NR) / T;
   static_assert((M * NR) % T == 0, "stockham_pass: tile not divisible by threads");
-  static_assert(LOGNS + LOGR <= 14, "stockham_pass: transform too long for the coarse table");
+  static_assert(LOGNS + LOGR <= 14, "stockham_pass: transform too long for the twiddle table");
   const int tid = opaque_tid();
+  // Twiddles first: their loads depend only on the thread index, so they are
+  // in flight while the pass reads its inputs and waits at the barrier.
+  float2 w[PER][R];
+  if constexpr (LOGNS > 0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int bf = tid + i * T;
+      const int j = TMAJOR ? (bf / M) : (bf & (NR - 1));
+      const int k = j & (NS - 1);
+#pragma unroll
+      for (int r = 1; r < R; ++r) w[i][r] = tw[(1 << (LOGNS + LOGR)) + r * k];
+    }
+  }
   float2 v[PER][R];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -190,11 +204,7 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
     const int k = j & (NS - 1);
     if constexpr (LOGNS > 0) {
 #pragma unroll
-      for (int r = 1; r < R; ++r) {
-        float2 w = tw[(r * k) << (14 - LOGNS - LOGR)];
-        if (INV) w.y = -w.y;
-        v[i][r] = cmul(v[i][r], w);
-      }
+      for (int r = 1; r < R; ++r) v[i][r] = INV ? cmulc(v[i][r], w[i][r]) : cmul(v[i][r], w[i][r]);
     }
     dft<R, INV>(v[i]);
     const int base = ((j - k) << LOGR) + k;

@@ -41,12 +41,15 @@ const float2* twiddle_table() {
   }
   std::lock_guard<std::mutex> lock(g_tw_mutex);
   if (g_tw[dev]) return g_tw[dev];
-  constexpr int kN = 1 << 14;
-  std::vector<float2> host(kN);
+  constexpr int kLogMax = 14;
+  std::vector<float2> host(size_t(2) << kLogMax, make_float2(1.f, 0.f));
   const double two_pi = 6.283185307179586476925286766559;
-  for (int j = 0; j < kN; ++j) {
-    double a = two_pi * double(j) / double(kN);
-    host[j] = make_float2(float(std::cos(a)), float(-std::sin(a)));
+  for (int b = 0; b <= kLogMax; ++b) {
+    const int n = 1 << b;
+    for (int j = 0; j < n; ++j) {
+      const double a = two_pi * double(j) / double(n);
+      host[size_t(n) + j] = make_float2(float(std::cos(a)), float(-std::sin(a)));
+    }
   }
   float2* d = nullptr;
   hipError_t e = hipMalloc(&d, host.size() * sizeof(float2));
