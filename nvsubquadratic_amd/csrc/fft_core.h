@@ -335,6 +335,140 @@ __device__ __forceinline__ float2 load_pair(const typename Elem<DT>::T* __restri
   return make_float2(a, b);
 }
 
+// Branch-free pair access for streaming kernels.  The load is always issued,
+// from a clamped in-bounds address (row[0] for out-of-range pairs, so `valid`
+// must be >= 1 for generic rows and >= 2 when ALIGNED), and out-of-range lanes
+// select zero afterwards: a run of these loads stays in flight together
+// instead of each waiting behind a branch.  ALIGNED means `valid` is even and
+// the row base is 2-element aligned (even row stride, aligned pointer; the
+// host checks), so a pair at an even index is one vector access that lies
+// wholly inside or wholly outside the row.
+template <int DT>
+__device__ __forceinline__ float2 load2(const typename Elem<DT>::T* __restrict__ p) {
+  if constexpr (DT == NSQ_DTYPE_F32) {
+    return *reinterpret_cast<const float2*>(p);
+  } else if constexpr (DT == NSQ_DTYPE_BF16) {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+    return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+  } else {
+    return __half22float2(*reinterpret_cast<const __half2*>(p));
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store2(typename Elem<DT>::T* __restrict__ p, float2 v) {
+  if constexpr (DT == NSQ_DTYPE_F32) {
+    *reinterpret_cast<float2*>(p) = v;
+  } else if constexpr (DT == NSQ_DTYPE_BF16) {
+    *reinterpret_cast<uint32_t*>(p) = f32x2_to_bf16x2_bits(v.x, v.y);
+  } else {
+    *reinterpret_cast<__half2*>(p) = __floats2half2_rn(v.x, v.y);
+  }
+}
+
+template <int DT, bool ALIGNED>
+__device__ __forceinline__ float2 load_pair_nb(const typename Elem<DT>::T* __restrict__ row, int64_t i,
+                                               int64_t valid) {
+  if constexpr (ALIGNED) {
+    const bool in = i < valid;
+    const float2 v = load2<DT>(row + (in ? i : 0));
+    return make_float2(in ? v.x : 0.f, in ? v.y : 0.f);
+  } else {
+    const bool ina = i < valid, inb = i + 1 < valid;
+    const float a = Elem<DT>::load(row, ina ? i : 0);
+    const float b = Elem<DT>::load(row, inb ? i + 1 : 0);
+    return make_float2(ina ? a : 0.f, inb ? b : 0.f);
+  }
+}
+
+template <int DT, bool ALIGNED>
+__device__ __forceinline__ void store_pair_nb(typename Elem<DT>::T* __restrict__ row, int64_t i, int64_t valid,
+                                              float2 v) {
+  if constexpr (ALIGNED) {
+    if (i < valid) store2<DT>(row + i, v);
+  } else {
+    if (i < valid) Elem<DT>::store(row, i, v.x);
+    if (i + 1 < valid) Elem<DT>::store(row, i + 1, v.y);
+  }
+}
+
+// A real row of `valid` elements as a raw buffer resource.  The hardware range
+// check returns 0 for loads past the end and drops stores past it, so row
+// accesses need no branches, a run of loads stays in flight together, and the
+// zero padding of a transform costs no memory traffic.  Offsets are 32-bit
+// byte offsets from the row start (rows here are at most 2^23 elements).
+// ALIGNED: see load_pair_nb; a pair at an even index is then one access.
+template <int DT, bool ALIGNED>
+struct RowBuf {
+  using ET = typename Elem<DT>::T;
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ RowBuf(const ET* row, int64_t valid)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<ET*>(row), 0, int(valid * int64_t(sizeof(ET))),
+                                            0x00020000)) {}
+  __device__ __forceinline__ float elem(int64_t i) const {
+    const int off = int(i) * int(sizeof(ET));
+    if constexpr (DT == NSQ_DTYPE_F32) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    } else if constexpr (DT == NSQ_DTYPE_BF16) {
+      return bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    } else {
+      return __half2float(__builtin_bit_cast(__half, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+    }
+  }
+  __device__ __forceinline__ void store_elem(int64_t i, float v) const {
+    const int off = int(i) * int(sizeof(ET));
+    if constexpr (DT == NSQ_DTYPE_F32) {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+    } else if constexpr (DT == NSQ_DTYPE_BF16) {
+      __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), r, off, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, __float2half_rn(v)), r, off, 0, 0);
+    }
+  }
+  // (u[i], u[i+1]); i even when ALIGNED.
+  __device__ __forceinline__ float2 load_pair(int64_t i) const {
+    if constexpr (ALIGNED) {
+      const int off = int(i) * int(sizeof(ET));
+      if constexpr (DT == NSQ_DTYPE_F32) {
+        return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+      } else if constexpr (DT == NSQ_DTYPE_BF16) {
+        const uint32_t u = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+        return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+      } else {
+        return __half22float2(__builtin_bit_cast(__half2, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)));
+      }
+    } else {
+      return make_float2(elem(i), elem(i + 1));
+    }
+  }
+  __device__ __forceinline__ void store_pair(int64_t i, float2 v) const {
+    if constexpr (ALIGNED) {
+      const int off = int(i) * int(sizeof(ET));
+      if constexpr (DT == NSQ_DTYPE_F32) {
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uint32_t __attribute__((ext_vector_type(2))), v), r,
+                                              off, 0, 0);
+      } else if constexpr (DT == NSQ_DTYPE_BF16) {
+        __builtin_amdgcn_raw_buffer_store_b32(f32x2_to_bf16x2_bits(v.x, v.y), r, off, 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, __floats2half2_rn(v.x, v.y)), r, off, 0,
+                                              0);
+      }
+    } else {
+      store_elem(i, v.x);
+      store_elem(i + 1, v.y);
+    }
+  }
+};
+
+// True when a row set with this base pointer and row stride (elements) can use
+// the ALIGNED pair accesses for rows of `valid` elements.
+template <int DT>
+inline bool pairs_aligned(const void* base, int64_t stride, int64_t valid) {
+  using ET = typename Elem<DT>::T;
+  return base != nullptr && (reinterpret_cast<uintptr_t>(base) % (2 * sizeof(ET))) == 0 && stride % 2 == 0 &&
+         valid % 2 == 0 && valid >= 2;
+}
+
 // Stores (v.x, v.y) at row[i], row[i+1] for the indices below `valid`.
 template <int DT>
 __device__ __forceinline__ void store_pair(typename Elem<DT>::T* __restrict__ row, int64_t i, int64_t valid, float2 v) {
@@ -344,7 +478,7 @@ __device__ __forceinline__ void store_pair(typename Elem<DT>::T* __restrict__ ro
     if constexpr (DT == NSQ_DTYPE_F32) {
       *reinterpret_cast<float2*>(p) = v;
     } else if constexpr (DT == NSQ_DTYPE_BF16) {
-      *reinterpret_cast<uint32_t*>(p) = uint32_t(f32_to_bf16_bits(v.x)) | (uint32_t(f32_to_bf16_bits(v.y)) << 16);
+      *reinterpret_cast<uint32_t*>(p) = f32x2_to_bf16x2_bits(v.x, v.y);
     } else {
       *reinterpret_cast<__half2*>(p) = __floats2half2_rn(v.x, v.y);
     }

@@ -19,6 +19,9 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
               (long long)L, (long long)K);
     return NSQ_ERR_UNSUPPORTED;
   }
+  // 4-step column grids are B*H * (N2 / columns per workgroup) <= B*H * 512.
+  NSQ_CHECK_ARG(p.fused || B * H <= (int64_t(1) << 22), "fftconv1d_causal: B*H=%lld too large for the 4-step plan",
+                (long long)(B * H));
   return NSQ_OK;
 }
 

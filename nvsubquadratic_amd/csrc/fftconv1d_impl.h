@@ -321,20 +321,20 @@ struct RealRows {
 };
 
 // col_fwd: A[row][k1][n2] = W_N^{n2 k1} * sum_{n1} z[N2 n1 + n2] W_{N1}^{n1 k1}.
-// grid = (rows, N2 / C).
-template <int LOGN1, int LOGN, int DT>
+// grid = rows * (N2 / M), column block fastest so that the workgroups running
+// together cover whole rows of the signal and of the workspace.
+template <int LOGN1, int LOGN, int DT, bool AL>
 __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_fwd_kernel(RealRows<DT> src, float2* __restrict__ ws,
                                                                     const float2* __restrict__ tw) {
   using C = ColCfg<LOGN1>;
   constexpr int N2 = 1 << (LOGN - LOGN1);
+  constexpr int NCB = N2 / C::M;
   __shared__ float2 lds[C::M * C::S];
-  const int c0 = blockIdx.y * C::M;
-  const int64_t row = blockIdx.x;
-  const typename Elem<DT>::T* in = src.p + row * src.stride;
+  const int c0 = int(blockIdx.x % NCB) * C::M;
+  const int64_t row = blockIdx.x / NCB;
+  const RowBuf<DT, AL> in(src.p + row * src.stride, src.valid);
   float2* out = ws + row * (int64_t(1) << LOGN);
-  auto ld = [&](int m, int n) -> float2 {
-    return load_pair<DT>(in, 2 * (int64_t(n) * N2 + c0 + m), src.valid);
-  };
+  auto ld = [&](int m, int n) -> float2 { return in.load_pair(2 * (int64_t(n) * N2 + c0 + m)); };
   auto st = [&](int m, int k1, float2 v) {
     const uint32_t n2 = uint32_t(c0 + m);
     out[int64_t(k1) * N2 + n2] = cmul(v, root<LOGN>(tw, n2 * uint32_t(k1)));
@@ -355,48 +355,56 @@ __device__ __forceinline__ void col_inv_body(const float2* __restrict__ ws_row, 
 }
 
 // Output epilogue for y (forward) or gx (backward): out = epi(conv, s, aux)
-// where aux is x (forward) or g (backward).  grid = (B*H, N2/C).
-template <int LOGN1, int LOGN, int DT>
+// where aux is x (forward) or g (backward).  grid = B*H * (N2/M), column block
+// fastest.  Without a shortcut the aux row is an empty buffer (reads 0, no
+// traffic).
+template <int LOGN1, int LOGN, int DT, bool AL>
 __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_inv_out_kernel(
     const float2* __restrict__ ws, const typename Elem<DT>::T* __restrict__ aux,
     const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ out, int H, int L,
     const float2* __restrict__ tw) {
   using C = ColCfg<LOGN1>;
+  constexpr int NCB = (1 << (LOGN - LOGN1)) / C::M;
   __shared__ float2 lds[C::M * C::S];
-  const int64_t row = blockIdx.x;
+  const int64_t row = blockIdx.x / NCB;
+  const int c0 = int(blockIdx.x % NCB) * C::M;
   const int h = int(row % H);
   const float scale = 1.f / float(int64_t(1) << LOGN);
   const bool has_s = s != nullptr;
   const float sv = has_s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
-  typename Elem<DT>::T* orow = out + row * L;
-  const typename Elem<DT>::T* arow = aux + row * L;
+  const RowBuf<DT, AL> orow(out + row * L, L);
+  const RowBuf<DT, AL> arow(aux + row * L, has_s ? L : 0);
   auto epi = [&](int64_t m, float2 v) {
     const int64_t i0 = 2 * m;
-    if (i0 >= L) return;
-    float2 a = has_s ? load_pair<DT>(arow, i0, L) : make_float2(0.f, 0.f);
-    float2 o = make_float2(epilogue<DT>(v.x * scale, has_s, sv, a.x), epilogue<DT>(v.y * scale, has_s, sv, a.y));
-    store_pair<DT>(orow, i0, L, o);
+    const float2 a = arow.load_pair(i0);
+    orow.store_pair(i0, make_float2(epilogue<DT>(v.x * scale, has_s, sv, a.x),
+                                    epilogue<DT>(v.y * scale, has_s, sv, a.y)));
   };
-  col_inv_body<LOGN1, LOGN>(ws + row * (int64_t(1) << LOGN), blockIdx.y * C::M, epi, tw, lds);
+  col_inv_body<LOGN1, LOGN>(ws + row * (int64_t(1) << LOGN), c0, epi, tw, lds);
 }
 
-// Filter-gradient epilogue: gk[h, 0:K] fp32, gs[h] = lag-0 value.  grid = (H, N2/C).
-template <int LOGN1, int LOGN>
+// Filter-gradient epilogue: gk[h, 0:K] fp32, gs[h] = lag-0 value.
+// grid = H * (N2/M), column block fastest.
+template <int LOGN1, int LOGN, bool AL>
 __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_inv_gk_kernel(const float2* __restrict__ ws,
                                                                        float* __restrict__ gk, float* __restrict__ gs,
                                                                        int K, const float2* __restrict__ tw) {
   using C = ColCfg<LOGN1>;
+  constexpr int NCB = (1 << (LOGN - LOGN1)) / C::M;
   __shared__ float2 lds[C::M * C::S];
-  const int64_t h = blockIdx.x;
+  const int64_t h = blockIdx.x / NCB;
+  const int c0 = int(blockIdx.x % NCB) * C::M;
   const float scale = 1.f / float(int64_t(1) << LOGN);
-  float* grow = gk + h * K;
+  const RowBuf<NSQ_DTYPE_F32, AL> grow(gk + h * K, K);
+  bool has0 = false;  // this thread produced lag 0 (selects, not a branch per element)
+  float g0 = 0.f;
   auto epi = [&](int64_t m, float2 v) {
-    const int64_t i0 = 2 * m;
-    if (i0 >= K) return;
-    store_pair<NSQ_DTYPE_F32>(grow, i0, K, make_float2(v.x * scale, v.y * scale));
-    if (m == 0 && gs) gs[h] = v.x * scale;
+    grow.store_pair(2 * m, make_float2(v.x * scale, v.y * scale));
+    has0 = has0 || (m == 0);
+    g0 = (m == 0) ? v.x * scale : g0;
   };
-  col_inv_body<LOGN1, LOGN>(ws + h * (int64_t(1) << LOGN), blockIdx.y * C::M, epi, tw, lds);
+  col_inv_body<LOGN1, LOGN>(ws + h * (int64_t(1) << LOGN), c0, epi, tw, lds);
+  if (gs && has0) gs[h] = g0;
 }
 
 // Row kernels.  Workgroup q handles the row pair {q, N1-q} (q >= 1) or the two
@@ -619,6 +627,43 @@ static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, cons
 //   [BH, BH+H)       column-transformed k  (K')
 //   [BH+H, 2BH+H)    forward: inverse-row product (Y') when `save`; backward: G'
 // With `save`, X' and K' survive the forward so the backward can reuse them.
+// Column-pass launches; `al` selects the aligned-pair row access.
+template <int LOGN1, int LOGN, int DT>
+static void launch_col_fwd(RealRows<DT> src, int64_t rows, float2* out, const float2* tw, hipStream_t st) {
+  const int64_t nb = rows * ((int64_t(1) << (LOGN - LOGN1)) / ColCfg<LOGN1>::M);
+  if (pairs_aligned<DT>(src.p, src.stride, src.valid))
+    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, true>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0, st,
+                       src, out, tw);
+  else
+    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, false>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0, st,
+                       src, out, tw);
+}
+
+template <int LOGN1, int LOGN, int DT>
+static void launch_col_inv_out(const float2* ws, const void* aux, const void* s, void* out, int64_t rows, int H,
+                               int L, const float2* tw, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  const int64_t nb = rows * ((int64_t(1) << (LOGN - LOGN1)) / ColCfg<LOGN1>::M);
+  if (pairs_aligned<DT>(out, L, L) && pairs_aligned<DT>(aux, L, L))
+    hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT, true>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0,
+                       st, ws, (const ET*)aux, (const ET*)s, (ET*)out, H, L, tw);
+  else
+    hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT, false>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0,
+                       st, ws, (const ET*)aux, (const ET*)s, (ET*)out, H, L, tw);
+}
+
+template <int LOGN1, int LOGN>
+static void launch_col_inv_gk(const float2* ws, float* gk, float* gs, int H, int K, const float2* tw,
+                              hipStream_t st) {
+  const int64_t nb = int64_t(H) * ((int64_t(1) << (LOGN - LOGN1)) / ColCfg<LOGN1>::M);
+  if (pairs_aligned<NSQ_DTYPE_F32>(gk, K, K))
+    hipLaunchKernelGGL((col_inv_gk_kernel<LOGN1, LOGN, true>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0, st, ws,
+                       gk, gs, K, tw);
+  else
+    hipLaunchKernelGGL((col_inv_gk_kernel<LOGN1, LOGN, false>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0, st,
+                       ws, gk, gs, K, tw);
+}
+
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
                              float2* ws, bool save, const float2* tw, hipStream_t st) {
@@ -628,15 +673,11 @@ static void launch_4step_fwd(const void* x, const float* k, const void* s, void*
   float2* wsx = ws;
   float2* wsk = ws + int64_t(B) * H * N;
   float2* wsy = save ? ws + (int64_t(B) * H + H) * N : wsx;
-  const int ncb = (1 << LOGN2) / ColCfg<LOGN1>::M;
-  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
-                     RealRows<DT>{(const ET*)x, L, L}, wsx, tw);
-  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
-                     RealRows<NSQ_DTYPE_F32>{k, K, K}, wsk, tw);
+  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, int64_t(B) * H, wsx, tw, st);
+  launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, H, wsk, tw, st);
   hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st,
                      (const float2*)wsx, (const float2*)wsk, wsy, B, H, tw);
-  hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), dim3(ColCfg<LOGN1>::T), 0, st,
-                     (const float2*)wsy, (const ET*)x, (const ET*)s, (ET*)y, H, L, tw);
+  launch_col_inv_out<LOGN1, LOGN, DT>(wsy, x, s, y, int64_t(B) * H, H, L, tw, st);
 }
 
 template <int LOGN1, int LOGN2, int DT>
@@ -649,21 +690,15 @@ static void launch_4step_bwd(const void* g, const void* x, const float* k, const
   float2* wsx = ws;
   float2* wsk = ws + int64_t(B) * H * N;
   float2* wsg = ws + (int64_t(B) * H + H) * N;
-  const int ncb = (1 << LOGN2) / ColCfg<LOGN1>::M;
-  dim3 ct(ColCfg<LOGN1>::T);
-  hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, RealRows<DT>{(const ET*)g, L, L},
-                     wsg, tw);
+  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)g, L, L}, int64_t(B) * H, wsg, tw, st);
   if (!fwd_state) {
-    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st,
-                       RealRows<DT>{(const ET*)x, L, L}, wsx, tw);
-    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, NSQ_DTYPE_F32>), dim3(H, ncb), ct, 0, st,
-                       RealRows<NSQ_DTYPE_F32>{k, K, K}, wsk, tw);
+    launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, int64_t(B) * H, wsx, tw, st);
+    launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, H, wsk, tw, st);
   }
   hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st, wsg,
                      (const float2*)wsx, wsk, B, H, tw);
-  hipLaunchKernelGGL((col_inv_out_kernel<LOGN1, LOGN, DT>), dim3(B * H, ncb), ct, 0, st, (const float2*)wsg,
-                     (const ET*)g, (const ET*)s, (ET*)gx, H, L, tw);
-  hipLaunchKernelGGL((col_inv_gk_kernel<LOGN1, LOGN>), dim3(H, ncb), ct, 0, st, (const float2*)wsk, gk, gs, K, tw);
+  launch_col_inv_out<LOGN1, LOGN, DT>(wsg, g, s, gx, int64_t(B) * H, H, L, tw, st);
+  launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, gs, H, K, tw, st);
 }
 
 // Runtime -> compile-time dispatch helpers.

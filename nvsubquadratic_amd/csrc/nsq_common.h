@@ -74,11 +74,19 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(uint32_t(b) << 16);
 }
 
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32): round to nearest even,
+// NaN stays NaN.  Branch-free, and a pair packs in one instruction.
+typedef __bf16 nsq_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float nsq_f32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);  // NaN stays NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// (bf16(a) | bf16(b) << 16)
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+  const nsq_f32x2_t f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, nsq_bf16x2_t));
 }
 
 template <int DT>
@@ -115,12 +123,10 @@ struct Elem<NSQ_DTYPE_F16> {
 // the product s*x and the sum are rounded separately here as well.
 template <int DT>
 __device__ __forceinline__ float epilogue(float conv, bool has_s, float s_rounded, float xv) {
-  float y = Elem<DT>::round(conv);
-  if (has_s) {
-    float sx = Elem<DT>::round(s_rounded * xv);
-    y = Elem<DT>::round(y + sx);
-  }
-  return y;
+  const float y = Elem<DT>::round(conv);
+  const float sx = Elem<DT>::round(s_rounded * xv);
+  const float ys = Elem<DT>::round(y + sx);
+  return has_s ? ys : y;  // select, not a branch: keeps streaming epilogues branch-free
 }
 
 }  // namespace nsq
