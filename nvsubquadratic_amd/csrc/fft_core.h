@@ -153,6 +153,46 @@ __device__ __forceinline__ void dft(float2* v) {
   }
 }
 
+// LDS position of element n in an element-major tile: one pad slot per 16
+// elements, so the stride-R writes of a Stockham pass (lanes j -> j*R + r)
+// spread over the 64 banks instead of hitting two of them.
+__device__ __forceinline__ constexpr int pad16(int n) { return n + (n >> 4); }
+template <int N>
+struct Padded {
+  static constexpr int SIZE = N + N / 16;  // padded length of one transform
+};
+
+// A tile of transforms in LDS: transform m at p[m*S ...], element n at
+// pad16(n) (PAD, element-major tiles) or at n (TMAJOR tiles, whose odd stride
+// S already spreads the banks).  For every access pattern of a power-of-two
+// Stockham pass -- element j + r*NR read, element base + r*NS written --
+// pad16(x + r*D) == pad16(x) + pad16(r*D) (checked exhaustively for all
+// transform lengths <= 2^14), so a pass computes one address per butterfly
+// and reaches its R elements through compile-time offsets.
+template <int S, bool PAD>
+struct LdsTile {
+  float2* p;
+  __device__ __forceinline__ float2* at(int m, int n) const { return p + m * S + (PAD ? pad16(n) : n); }
+  static constexpr int off(int d) { return PAD ? pad16(d) : d; }
+};
+template <class X>
+struct IsLdsTile : std::false_type {};
+template <int S, bool PAD>
+struct IsLdsTile<LdsTile<S, PAD>> : std::true_type {};
+
+// Twiddle-table loads through a raw buffer resource: 32-bit offsets from one
+// scalar base, so a butterfly's R-1 twiddle addresses are a multiply each.
+struct TwTable {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ explicit TwTable(const float2* tw)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<float2*>(tw), 0, int((2 << 14) * sizeof(float2)), 0x00020000)) {}
+  // entry seg + idx of the table (seg = 2^b selects the W_{2^b} segment)
+  __device__ __forceinline__ float2 load(int seg, int idx) const {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, idx * int(sizeof(float2)),
+                                                                          seg * int(sizeof(float2)), 0));
+  }
+};
+
 // ---------------------------------------------------------------------------
 // One radix-2^LOGR Stockham pass over M transforms of length 2^LOGN executed by
 // T threads.  LD(m, n) -> float2 reads input element n of transform m; ST(m, n,
@@ -177,13 +217,14 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
   // in flight while the pass reads its inputs and waits at the barrier.
   float2 w[PER][R];
   if constexpr (LOGNS > 0) {
+    const TwTable tt(tw);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int bf = tid + i * T;
       const int j = TMAJOR ? (bf / M) : (bf & (NR - 1));
       const int k = j & (NS - 1);
 #pragma unroll
-      for (int r = 1; r < R; ++r) w[i][r] = tw[(1 << (LOGNS + LOGR)) + r * k];
+      for (int r = 1; r < R; ++r) w[i][r] = tt.load(1 << (LOGNS + LOGR), r * k);
     }
   }
   float2 v[PER][R];
@@ -192,8 +233,14 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
     const int bf = tid + i * T;
     const int m = TMAJOR ? (bf % M) : (bf >> (LOGN - LOGR));
     const int j = TMAJOR ? (bf / M) : (bf & (NR - 1));
+    if constexpr (IsLdsTile<LD>::value) {
+      const float2* q = ld.at(m, j);
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[i][r] = ld(m, j + r * NR);
+      for (int r = 0; r < R; ++r) v[i][r] = q[LD::off(r * NR)];
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[i][r] = ld(m, j + r * NR);
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -208,8 +255,14 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
     }
     dft<R, INV>(v[i]);
     const int base = ((j - k) << LOGR) + k;
+    if constexpr (IsLdsTile<ST>::value) {
+      float2* q = st.at(m, base);
 #pragma unroll
-    for (int r = 0; r < R; ++r) st(m, base + r * NS, v[i][r]);
+      for (int r = 0; r < R; ++r) q[ST::off(r * NS)] = v[i][r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) st(m, base + r * NS, v[i][r]);
+    }
   }
   __syncthreads();
 }
@@ -235,32 +288,21 @@ __device__ __forceinline__ void fft_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds,
 }
 
 // Full transform of M length-2^LOGN sequences.  Passes 2..n-1 run in `lds`
-// (transform m at lds[m*S ...], element n at pad16(n) for element-major tiles,
-// at n for TMAJOR tiles whose odd stride S already spreads the banks); the
-// first pass reads through ld_first and the last pass writes through st_last.
-// Ends with a barrier.
-// LDS position of element n in an element-major tile: one pad slot per 16
-// elements, so the stride-R writes of a Stockham pass (lanes j -> j*R + r)
-// spread over the 64 banks instead of hitting two of them.
-__device__ __forceinline__ constexpr int pad16(int n) { return n + (n >> 4); }
-template <int N>
-struct Padded {
-  static constexpr int SIZE = N + N / 16;  // padded length of one transform
-};
-
+// (an LdsTile: transform m at lds[m*S ...], padded element-major unless
+// TMAJOR); the first pass reads through ld_first and the last pass writes
+// through st_last, each either a functor (m, n[, v]) or an LdsTile of the
+// same layout.  Ends with a barrier.
 template <int LOGN, bool INV, int M, int T, int S, bool TMAJOR = false, class LDF, class STF>
 __device__ __forceinline__ void fft(float2* lds, LDF& ld_first, STF& st_last, const float2* __restrict__ tw) {
-  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + (TMAJOR ? n : pad16(n))]; };
-  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + (TMAJOR ? n : pad16(n))] = v; };
-  fft_rec<LOGN, 0, INV, M, T, TMAJOR>(ld_first, st_lds, ld_lds, st_last, tw);
+  LdsTile<S, !TMAJOR> tile{lds};
+  fft_rec<LOGN, 0, INV, M, T, TMAJOR>(ld_first, tile, tile, st_last, tw);
 }
 
 // Transform that starts and ends in LDS.
 template <int LOGN, bool INV, int M, int T, int S, bool TMAJOR = false>
 __device__ __forceinline__ void fft_lds(float2* lds, const float2* __restrict__ tw) {
-  auto ld_lds = [&](int m, int n) -> float2 { return lds[m * S + (TMAJOR ? n : pad16(n))]; };
-  auto st_lds = [&](int m, int n, float2 v) { lds[m * S + (TMAJOR ? n : pad16(n))] = v; };
-  fft_rec<LOGN, 0, INV, M, T, TMAJOR>(ld_lds, st_lds, ld_lds, st_lds, tw);
+  LdsTile<S, !TMAJOR> tile{lds};
+  fft_rec<LOGN, 0, INV, M, T, TMAJOR>(tile, tile, tile, tile, tw);
 }
 
 // ---------------------------------------------------------------------------

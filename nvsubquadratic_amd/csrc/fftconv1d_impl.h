@@ -126,7 +126,7 @@ __device__ __forceinline__ void filter_spectrum(float2* lds, const float* __rest
     if (h >= H) return make_float2(0.f, 0.f);
     return load_pair<NSQ_DTYPE_F32>(k + int64_t(h) * K, 2 * int64_t(n), K);
   };
-  auto st = [&](int m, int n, float2 v) { lds[m * C::SP + pad16(n)] = v; };
+  LdsTile<C::SP, true> st{lds};
   fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
       if (h >= H) return make_float2(0.f, 0.f);
       return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
     };
-    auto st = [&](int m, int n, float2 v) { lds[m * C::SP + pad16(n)] = v; };
+    LdsTile<C::SP, true> st{lds};
     fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
                         epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0 + 1) : 0.f));
     };
     if constexpr (!FOLD) {
-      auto ldl = [&](int m, int n) -> float2 { return lds[m * C::SP + pad16(n)]; };
+      LdsTile<C::SP, true> ldl{lds};
       fft<LOGN, true, C::M, C::T, C::SP>(lds, ldl, epi, tw);
     } else {
       fft_lds<LOGN, true, C::M, C::T, C::SP>(lds, tw);
@@ -239,8 +239,8 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
       if (h >= H) return make_float2(0.f, 0.f);
       return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
     };
-    auto stG = [&](int m, int n, float2 v) { ldsG[m * C::SP + pad16(n)] = v; };
-    auto stX = [&](int m, int n, float2 v) { ldsX[m * C::SP + pad16(n)] = v; };
+    LdsTile<C::SP, true> stG{ldsG};
+    LdsTile<C::SP, true> stX{ldsX};
     fft<LOGN, false, C::M, C::T, C::SP>(ldsG, ldg, stG, tw);
     fft<LOGN, false, C::M, C::T, C::SP>(ldsX, ldx, stX, tw);
 #pragma unroll
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
         Elem<DT>::store(gx, row + i0 + 1,
                         epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(g, row + i0 + 1) : 0.f));
     };
-    auto ldl = [&](int m, int n) -> float2 { return ldsG[m * C::SP + pad16(n)]; };
+    LdsTile<C::SP, true> ldl{ldsG};
     fft<LOGN, true, C::M, C::T, C::SP>(ldsG, ldl, epi, tw);
   }
 
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     if (i0 + 1 < K) gk[int64_t(h) * K + i0 + 1] = v.y * scale;
     if (n == 0 && gs) gs[h] = v.x * scale;
   };
-  auto ldl = [&](int m, int n) -> float2 { return ldsX[m * C::SP + pad16(n)]; };
+  LdsTile<C::SP, true> ldl{ldsX};
   fft<LOGN, true, C::M, C::T, C::SP>(ldsX, ldl, epik, tw);
 }
 
@@ -451,7 +451,7 @@ __device__ __forceinline__ void row_pair_fft(float2* lds, const float2* __restri
   constexpr int N1 = 1 << LOGN1;
   const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
   auto ld = [&](int m, int n) -> float2 { return sig[int64_t(m == 0 ? ra : rb) * C::N2 + n]; };
-  auto st = [&](int m, int n, float2 v) { lds[m * C::N2P + pad16(n)] = v; };
+  LdsTile<C::N2P, true> st{lds};
   fft<LOGN2, false, 2, C::T, C::N2P>(lds, ld, st, tw);
 }
 
@@ -463,7 +463,7 @@ __device__ __forceinline__ void row_pair_ifft_store(float2* lds, float2* __restr
   constexpr int N1 = 1 << LOGN1;
   constexpr int LOGN = LOGN1 + LOGN2;
   const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
-  auto ld = [&](int m, int n) -> float2 { return lds[m * C::N2P + pad16(n)]; };
+  LdsTile<C::N2P, true> ld{lds};
   auto st = [&](int m, int n, float2 v) {
     const int k1 = (m == 0) ? ra : rb;
     float2 w = root<LOGN>(tw, uint32_t(n) * uint32_t(k1));

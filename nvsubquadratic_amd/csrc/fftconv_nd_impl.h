@@ -75,7 +75,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
     if (r >= rg.rows) return make_float2(0.f, 0.f);
     return load_pair<DT>(src + r * len, 2 * int64_t(n), len);
   };
-  auto st = [&](int m, int n, float2 v) { lds[m * C::SP + pad16(n)] = v; };
+  LdsTile<C::SP, true> st{lds};
   fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
   for (int i = 0; i < C::SLOTS; ++i) {
     const int s = opaque_tid() + i * C::T;
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
     zz[pad16(slot0 ? C::N / 2 : C::N - p)] = zq;
   }
   __syncthreads();
-  auto ld = [&](int m, int n) -> float2 { return lds[m * C::SP + pad16(n)]; };
+  LdsTile<C::SP, true> ld{lds};
   auto st = [&](int m, int n, float2 v) {
     const int64_t r = r0 + m;
     if (r >= rg.rows) return;
