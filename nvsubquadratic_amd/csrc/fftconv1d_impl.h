@@ -534,9 +534,11 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
   }
 }
 
-// Backward row kernel.  wsg rows [B*H][N] (in: column-transformed g; out:
-// gx pre-image), wsx rows [B*H][N] (column-transformed x), wsk [H][N] (in:
-// column-transformed k; out: gk pre-image).  grid = H * N1/2.
+// Backward row kernel, any batch.  wsg rows [B*H][N] (in: column-transformed
+// g; out: gx pre-image), wsx rows [B*H][N] (column-transformed x), wsk [H][N]
+// (in: column-transformed k; out: gk pre-image).  grid = H * N1/2.  Two LDS
+// tiles: G and X of one batch row are transformed side by side and the gk
+// correlation accumulates over the batch in registers.
 template <int LOGN1, int LOGN2>
 __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(3))) void row_bwd_kernel(float2* __restrict__ wsg,
                                                                     const float2* __restrict__ wsx,
@@ -584,6 +586,57 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
   }
   __syncthreads();
   row_pair_ifft_store<LOGN1, LOGN2>(ldsX, wsk + int64_t(h) * N, q, tw);
+}
+
+// Backward row kernel for a single batch row (B == 1), one LDS tile.  Same
+// buffers as row_bwd_kernel.  Order K -> G -> X: the K slots live in registers
+// while G is transformed; unpacking G forms the gx product (repacked in place)
+// and the G slots replace the K slots; unpacking X forms the gk correlation
+// G*conj(X).  One spectrum's slots are live per transform, as in the forward.
+template <int LOGN1, int LOGN2>
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(4))) void row_bwd1_kernel(
+    float2* __restrict__ wsg, const float2* __restrict__ wsx, float2* __restrict__ wsk, int H,
+    const float2* __restrict__ tw) {
+  using C = RowCfg<LOGN2>;
+  constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
+  __shared__ float2 lds[C::TILE_P];
+  const int q = blockIdx.x % ((1 << LOGN1) / 2);
+  const int h = blockIdx.x / ((1 << LOGN1) / 2);
+  float2 sA[C::SLOTS], sB[C::SLOTS];  // K slots, then G slots
+  row_pair_fft<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
+    row_unpack<LOGN1, LOGN2>(lds, q, opaque_tid() + i * C::T, tw, sA[i], sB[i]);
+  }
+  __syncthreads();
+  float2* sigg = wsg + int64_t(h) * N;
+  row_pair_fft<LOGN1, LOGN2>(lds, sigg, q, tw);
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
+    const int s = opaque_tid() + i * C::T;
+    const bool s0 = (q == 0 && s == 0);
+    float2 GA, GB;
+    row_unpack<LOGN1, LOGN2>(lds, q, s, tw, GA, GB);
+    row_repack<LOGN1, LOGN2>(lds, q, s, tw, slot_mulc(s0, GA, sA[i]), cmulc(GB, sB[i]));
+    sA[i] = GA;
+    sB[i] = GB;
+  }
+  __syncthreads();
+  row_pair_ifft_store<LOGN1, LOGN2>(lds, sigg, q, tw);
+  row_pair_fft<LOGN1, LOGN2>(lds, wsx + int64_t(h) * N, q, tw);
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    NSQ_SLOT_FENCE();
+    const int s = opaque_tid() + i * C::T;
+    const bool s0 = (q == 0 && s == 0);
+    float2 XA, XB;
+    row_unpack<LOGN1, LOGN2>(lds, q, s, tw, XA, XB);
+    row_repack<LOGN1, LOGN2>(lds, q, s, tw, slot_mulc(s0, sA[i], XA), cmulc(sB[i], XB));
+  }
+  __syncthreads();
+  row_pair_ifft_store<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
 }
 
 // ===========================================================================
@@ -695,8 +748,12 @@ static void launch_4step_bwd(const void* g, const void* x, const float* k, const
     launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, int64_t(B) * H, wsx, tw, st);
     launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, H, wsk, tw, st);
   }
-  hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st, wsg,
-                     (const float2*)wsx, wsk, B, H, tw);
+  if (B == 1)
+    hipLaunchKernelGGL((row_bwd1_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st,
+                       wsg, (const float2*)wsx, wsk, H, tw);
+  else
+    hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st,
+                       wsg, (const float2*)wsx, wsk, B, H, tw);
   launch_col_inv_out<LOGN1, LOGN, DT>(wsg, g, s, gx, int64_t(B) * H, H, L, tw, st);
   launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, gs, H, K, tw, st);
 }

@@ -184,10 +184,11 @@ def test_ragged_and_tiny_lengths(L, K):
 # ---------------------------------------------------------------------------
 # 4-step plan (FFT length >= 2^15) and the BASELINE configs
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B", [1, 2])
 @pytest.mark.parametrize("L,K", [(16384, 16384), (20000, 9000), (65536, 65536), (131072, 1000)])
-def test_four_step_fp32_fwd_bwd(L, K):
+def test_four_step_fp32_fwd_bwd(L, K, B):
     torch.manual_seed(7)
-    B, H = 2, 3
+    H = 3
     x = torch.randn(B, H, L, requires_grad=True)
     k = torch.randn(1, H, K, requires_grad=True)
     s = torch.randn(H, requires_grad=True)
@@ -286,13 +287,14 @@ def test_config3_full_size_properties():
     assert rel_l2(x, yd) < 1e-5
 
 
+@pytest.mark.parametrize("B", [1, 2])
 @pytest.mark.parametrize("L", [16384, 65536])
-def test_backward_reusing_forward_state_is_bitwise_equal(L):
+def test_backward_reusing_forward_state_is_bitwise_equal(L, B):
     """The forward keeps its transformed x, k in a backward-sized workspace; reuse == recompute."""
     from nvsubquadratic_amd import _lib
 
     torch.manual_seed(8)
-    B, H = 2, 3
+    H = 3
     x = torch.randn(B, H, L, device="cuda").to(torch.bfloat16)
     k = torch.randn(H, L, device="cuda")
     s = torch.randn(H, device="cuda").to(torch.bfloat16)
@@ -311,6 +313,33 @@ def test_backward_reusing_forward_state_is_bitwise_equal(L):
     y2 = torch.empty_like(x)
     F.causal_fftconv1d_fwd_raw(x, k, s, y2)  # minimum workspace, in-place plan
     assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("L", [16384, 65536])
+def test_single_row_backward_matches_batched(L):
+    """B == 1 runs its own backward row kernel: per-row gx and gk agree with the batched call.
+
+    The two kernels may contract products into FMAs differently, so agreement is to
+    rounding (bf16 gx: a last-bit flip here and there), not bitwise.
+    """
+    torch.manual_seed(10)
+    B, H = 2, 3
+    x = torch.randn(B, H, L, device="cuda").to(torch.bfloat16)
+    k = torch.randn(H, L, device="cuda")
+    s = torch.randn(H, device="cuda").to(torch.bfloat16)
+    g = torch.randn(B, H, L, device="cuda").to(torch.bfloat16)
+    gx, gk, gs = torch.empty_like(x), torch.empty_like(k), torch.empty(H, device="cuda")
+    F.causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs)
+    gk_sum = torch.zeros_like(k)
+    gs_sum = torch.zeros(H, device="cuda")
+    for b in range(B):
+        gx1, gk1, gs1 = torch.empty_like(x[b:b + 1]), torch.empty_like(k), torch.empty(H, device="cuda")
+        F.causal_fftconv1d_bwd_raw(g[b:b + 1].contiguous(), x[b:b + 1].contiguous(), k, s, gx1, gk1, gs1)
+        assert rel_l2(gx[b], gx1[0]) < 2e-3
+        gk_sum += gk1
+        gs_sum += gs1
+    torch.testing.assert_close(gk_sum, gk, rtol=1e-5, atol=1e-5 * gk.abs().max().item())
+    torch.testing.assert_close(gs_sum, gs, rtol=1e-5, atol=1e-5 * gs.abs().max().item())
 
 
 def test_retain_graph_second_backward_matches_first():
