@@ -15,6 +15,9 @@ Prints one JSON line with the driver's fields plus:
                   sample of the same workload, on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --workload cfg1|cfg2|cfg4|cfg5   (the other benchmark
+           configurations, for the per-config report; same JSON fields, value =
+           algorithmic GB/s of the phase BASELINE.md quotes for that config)
        python bench.py --copy-calibration   (one plain copy kernel of known size,
                                              for scaling rocprof FETCH/WRITE_SIZE)
 """
@@ -93,6 +96,91 @@ def cpu_baseline(channels: int, iters: int) -> dict:
     }
 
 
+def _time_steps(step, steps: int, warmup: int) -> list[float]:
+    """Event-timed steps on the current stream (ms each) after untimed warmup."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        step()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+
+
+def other_workload(name: str, steps: int, warmup: int) -> None:
+    """Configs 1, 2, 4, 5 of the benchmark set (inputs resident in HBM)."""
+    from nvsubquadratic_amd import causal_conv1d_hip as CC
+    from nvsubquadratic_amd import fftconv_hip as F
+    from nvsubquadratic_amd.workloads import (algorithmic_bytes_b2b, algorithmic_bytes_causal1d,
+                                              algorithmic_bytes_nd, causal1d_case_fast, radial_filter)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    if name == "cfg1":
+        B, D, L = 2, 128, 4096
+        c = causal1d_case_fast(B, D, L, torch.float32, (1.0, 10.0), dev, seed=0)
+        y = torch.empty_like(c.x)
+        phase, dtype = "fwd", "f32"
+        nbytes = algorithmic_bytes_causal1d(B, D, L, L, 4, "fwd")
+        desc = "cfg1: causal FFT long conv fwd, B=2 D=128 L=4096 K=4096, FFT length 8192, fp32 I/O"
+
+        def step():
+            F.causal_fftconv1d_fwd_raw(c.x, c.k, c.s, y)
+    elif name == "cfg2":
+        B, C, L, Kp, Km = 4, 4096, 8192, 3, 128
+        x = torch.randn(B, 3 * C, L, device=dev, generator=gen).to(torch.bfloat16)
+        wp = torch.randn(3 * C, Kp, device=dev, generator=gen)
+        wm = torch.randn(C, Km, device=dev, generator=gen) / Km ** 0.5
+        phase, dtype = "fwd", "f32"
+        nbytes = algorithmic_bytes_b2b(B, C, L, Kp, Km, 2)
+        desc = "cfg2: B2B short-conv block fwd (k=3 proj -> gate -> k=128 mixer -> gate), B=4 L=8192 D=4096, bf16 I/O"
+
+        def step():
+            with torch.no_grad():
+                CC.b2b_causal_conv1d(x, wp, wm, None)
+    elif name in ("cfg4", "cfg5"):
+        nd = 2 if name == "cfg4" else 3
+        B, C, size, sig = (16, 384, 128, (4.0, 64.0)) if nd == 2 else (2, 128, 64, (2.0, 32.0))
+        x = torch.randn(B, C, *([size] * nd), device=dev, generator=gen).to(torch.bfloat16)
+        k = radial_filter(C, size, sig[0], sig[1], nd, gen, dev)
+        s = torch.randn(C, device=dev, generator=gen).to(torch.bfloat16)
+        fn = F.fftconv2d_bhl if nd == 2 else F.fftconv3d_bhl
+        phase, dtype = ("fwd", "f32") if nd == 2 else ("fwd+bwd", "f32")
+        nbytes = algorithmic_bytes_nd(B, C, [size] * nd, [size] * nd, 2, phase)
+        desc = (f"cfg{4 if nd == 2 else 5}: {nd}D non-causal FFT conv {phase}, B={B} C={C} {size}^{nd}, "
+                f"filter {size}^{nd} fp32, FFT {2 * size}^{nd} per axis, bf16 I/O")
+        if nd == 2:
+            def step():
+                with torch.no_grad():
+                    fn(x, k, s)
+        else:
+            xg, kg, sg = (t.detach().requires_grad_(True) for t in (x, k, s))
+            g = torch.randn(x.shape, device=dev, generator=gen).to(torch.bfloat16)
+
+            def step():
+                xg.grad = kg.grad = sg.grad = None
+                fn(xg, kg, sg).backward(g)
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    ms_list = _time_steps(step, steps, warmup)
+    ms = statistics.mean(ms_list)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": f"{name} {phase} algorithmic HBM GB/s, 1 MI355X",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 4), "ms_median": round(statistics.median(ms_list), 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic", "config": {"workload": desc},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes},
+    }), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,6 +190,7 @@ def main() -> None:
     ap.add_argument("--cpu-channels", type=int, default=1024)
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -113,6 +202,9 @@ def main() -> None:
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.workload != "cfg3":
+        other_workload(args.workload, args.steps, args.warmup)
         return
 
     from nvsubquadratic_amd import _lib

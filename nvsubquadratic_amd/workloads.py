@@ -17,11 +17,14 @@ import torch
 
 __all__ = [
     "Causal1DCase",
+    "algorithmic_bytes_b2b",
     "algorithmic_bytes_causal1d",
+    "algorithmic_bytes_nd",
     "causal1d_case",
     "causal1d_case_fast",
     "decaying_filter_1d",
     "fft_flops_causal1d",
+    "radial_filter",
 ]
 
 
@@ -137,4 +140,40 @@ def fft_flops_causal1d(B: int, H: int, L: int, K: int, phase: str) -> float:
         return (3 * B * H + 2 * H) * per
     if phase == "fwd+bwd":
         return (5 * B * H + 3 * H) * per
+    raise ValueError(phase)
+
+
+def radial_filter(C: int, size: int, sig_lo: float, sig_hi: float, nd: int, gen: torch.Generator,
+                  device="cpu") -> torch.Tensor:
+    """Per-channel ND filter N(0,1) * exp(-r / sigma_c), r = distance from the
+    centre (size // 2 along each axis), sigma_c ~ U(sig_lo, sig_hi); float32
+    [C, size, ..., size] (configs 4 and 5)."""
+    sig = torch.empty(C, device=device).uniform_(sig_lo, sig_hi, generator=gen)
+    ax = torch.arange(size, device=device).float() - size // 2
+    grids = torch.meshgrid(*([ax] * nd), indexing="ij")
+    r = torch.sqrt(sum(g ** 2 for g in grids))
+    h = torch.randn(C, *([size] * nd), device=device, generator=gen)
+    return h * torch.exp(-r[None] / sig.view(-1, *([1] * nd)))
+
+
+def algorithmic_bytes_b2b(B: int, C: int, L: int, Kp: int, Km: int, itemsize: int) -> int:
+    """Forward of the fused B2B block: x [B, 3C, L] read, y [B, C, L] written
+    (itemsize each), fp32 depthwise weights [3C, Kp] and [C, Km] read.
+    Config 2 (B=4, C=4096, L=8192, Kp=3, Km=128, bf16): 1,075,986,432 B."""
+    return B * 3 * C * L * itemsize + B * C * L * itemsize + (3 * C * Kp + C * Km) * 4
+
+
+def algorithmic_bytes_nd(B: int, C: int, S, K, itemsize: int, phase: str) -> int:
+    """Compulsory HBM bytes of one 2D/3D FFT-conv call with a shared fp32
+    filter [C, *K] and a shortcut [C] in the I/O dtype (same accounting as
+    :func:`algorithmic_bytes_causal1d`).  Config 4 forward: 427,819,776 B;
+    config 5 forward + backward: 1,073,742,592 B."""
+    E = B * C * math.prod(S)
+    KK = C * math.prod(K)
+    if phase == "fwd":
+        return E * 2 * itemsize + KK * 4 + C * itemsize
+    if phase == "bwd":
+        return E * 3 * itemsize + KK * 8 + 2 * C * itemsize
+    if phase == "fwd+bwd":
+        return algorithmic_bytes_nd(B, C, S, K, itemsize, "fwd") + algorithmic_bytes_nd(B, C, S, K, itemsize, "bwd")
     raise ValueError(phase)
