@@ -69,8 +69,12 @@ static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
     constexpr int LOGN = decltype(L)::value;
     using C = RowNdCfg<LOGN>;
-    hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0, st,
-                       (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+    if (pairs_aligned<DT>(src, len, len))
+      hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, true>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0,
+                         st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+    else
+      hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, false>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0,
+                         st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
   });
 }
 
@@ -81,8 +85,12 @@ static bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int 
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
     constexpr int LOGN = decltype(L)::value;
     using C = RowNdCfg<LOGN>;
-    hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0,
-                       st, ws, rg, o, tw);
+    if (MODE == ND_OUT_Y && o.s)
+      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, true>), dim3(unsigned(ceil_div(rg.rows, C::M))),
+                         dim3(C::T), 0, st, ws, rg, o, tw);
+    else
+      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, false>), dim3(unsigned(ceil_div(rg.rows, C::M))),
+                         dim3(C::T), 0, st, ws, rg, o, tw);
   });
 }
 
@@ -129,9 +137,9 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
     using C = ColNdCfg<LOGF>;
-    dim3 grid(unsigned(BH), unsigned(ceil_div(cg.inner_count, C::M)));
-    hipLaunchKernelGGL((nd_col_mul_kernel<LOGF>), grid, dim3(C::T), 0, st, wsx, (const float2*)wsk, cg, int(p.H),
-                       int(p.kb != 1), p.S[0], p.c[0], tw);
+    dim3 grid(unsigned(p.kb != 1 ? BH : p.H), unsigned(ceil_div(cg.inner_count, C::M)));
+    hipLaunchKernelGGL((nd_col_mul_kernel<LOGF>), grid, dim3(C::T), 0, st, wsx, (const float2*)wsk, cg, int(p.B),
+                       int(p.H), int(p.kb != 1), p.S[0], p.c[0], tw);
   });
   if (!ok) return false;
   if (p.nd == 3 && !col_pass<true>(p, wsx, BH, 1, p.S[0], p.F[1], p.c[1], p.S[1], tw, st)) return false;
@@ -189,6 +197,11 @@ static int validate_nd(int nd, const void* a, const void* b, const float* k, int
                   "fftconv_nd: axis %d: kernel size %lld must be in [1, 2*%lld]", d, (long long)K[d], (long long)S[d]);
   if (!make_nd_plan(nd, B, H, S, K, kb, p)) {
     set_error("fftconv_nd: unsupported shape: every axis needs an FFT length <= %d", 1 << kNdMaxLogF);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  if (B * H * int64_t(p.F[0]) * p.F[1] >= (int64_t(1) << 31)) {  // row passes index rows in 32 bits
+    set_error("fftconv_nd: unsupported shape: B*H*F0*F1 = %lld rows exceeds 2^31 - 1",
+              (long long)(B * H * int64_t(p.F[0]) * p.F[1]));
     return NSQ_ERR_UNSUPPORTED;
   }
   return NSQ_OK;

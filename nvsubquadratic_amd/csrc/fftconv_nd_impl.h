@@ -39,17 +39,20 @@ struct RowNdCfg {
   static constexpr int SLOTS = 8;
 };
 
-// Rows are flattened over (bh, a0 < n0, a1 < n1).
+// Rows are flattened over (bh, a0 < n0, a1 < n1).  The host keeps the row
+// count of a pass below 2^31, so the decomposition is 32-bit arithmetic (a
+// 64-bit division is a long instruction sequence, and it runs per slot).
 struct RowIdx {
-  int64_t bh;
+  int bh;
   int a0, a1;
 };
-__device__ __forceinline__ RowIdx row_index(int64_t r, int n0, int n1) {
+__device__ __forceinline__ RowIdx row_index(int64_t r64, int n0, int n1) {
+  const uint32_t r = uint32_t(r64);
+  const uint32_t t = r / uint32_t(n1);
   RowIdx o;
-  o.a1 = int(r % n1);
-  const int64_t t = r / n1;
-  o.a0 = int(t % n0);
-  o.bh = t / n0;
+  o.a1 = int(r - t * uint32_t(n1));
+  o.bh = int(t / uint32_t(n0));
+  o.a0 = int(t - uint32_t(o.bh) * uint32_t(n0));
   return o;
 }
 
@@ -63,7 +66,8 @@ struct RowGeom {
 
 // Forward real FFT of rows of a contiguous [BH][n0][n1][len] real tensor,
 // zero-padded to F2 = 2N, into workspace bins [0, FH) of row (a0, a1).
-template <int LOGN, int DT>
+// AL: aligned pair access (even len, aligned base; see load_pair_nb).
+template <int LOGN, int DT, bool AL>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typename Elem<DT>::T* __restrict__ src,
                                                                         int len, RowGeom rg, float2* __restrict__ ws,
                                                                         const float2* __restrict__ tw) {
@@ -72,8 +76,8 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
   const int64_t r0 = int64_t(blockIdx.x) * C::M;
   auto ld = [&](int m, int n) -> float2 {
     const int64_t r = r0 + m;
-    if (r >= rg.rows) return make_float2(0.f, 0.f);
-    return load_pair<DT>(src + r * len, 2 * int64_t(n), len);
+    const bool rok = r < rg.rows;  // tail rows read row 0 and select zero
+    return load_pair_nb<DT, AL>(src + (rok ? r : 0) * len, 2 * int64_t(n), rok ? len : 0);
   };
   LdsTile<C::SP, true> st{lds};
   fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
@@ -88,7 +92,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
     real_unpack(slot0, zz[pad16(p)], zz[pad16(slot0 ? C::N / 2 : C::N - p)],
                 root<LOGN + 1>(tw, p), A, Bc);
     const RowIdx q = row_index(r, rg.n0, rg.n1);
-    float2* out = ws + q.bh * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+    float2* out = ws + int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
     if (slot0) {
       out[0] = make_float2(A.x, 0.f);
       out[C::N] = make_float2(A.y, 0.f);
@@ -114,56 +118,70 @@ struct RowInvOut {
   float scale;         // 1 / (F0 * F1 * F2/2)
 };
 
-template <int LOGN, int DT, int MODE>
+// HAS_S: a shortcut is given (ND_OUT_Y); its term reads aux.  Loads are
+// branch-free (clamped indices, zero selected) so they overlap; only stores
+// are predicated.
+template <int LOGN, int DT, int MODE, bool HAS_S>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const float2* __restrict__ ws, RowGeom rg,
                                                                         RowInvOut o, const float2* __restrict__ tw) {
   using C = RowNdCfg<LOGN>;
   using ET = typename Elem<DT>::T;
   __shared__ float2 lds[C::M * C::SP];
   const int64_t r0 = int64_t(blockIdx.x) * C::M;
+#pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
     const int s = opaque_tid() + i * C::T;
     const int m = s >> (LOGN - 1), p = s & (C::N / 2 - 1);
     const int64_t r = r0 + m;
+    const bool rok = r < rg.rows;
     const bool slot0 = (p == 0);
-    float2 zp = make_float2(0.f, 0.f), zq = zp;
-    if (r < rg.rows) {
-      const RowIdx q = row_index(r, rg.n0, rg.n1);
-      const float2* in = ws + q.bh * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
-      float2 A, Bc;
-      if (slot0) {
-        A = make_float2(in[0].x, in[C::N].x);
-        Bc = in[C::N / 2];
-      } else {
-        A = in[p];
-        Bc = cconj(in[C::N - p]);
-      }
-      real_repack(slot0, A, Bc, root<LOGN + 1>(tw, p), zp, zq);
-    }
+    const RowIdx q = row_index(rok ? r : 0, rg.n0, rg.n1);
+    const float2* in = ws + int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+    const float2 u0 = in[slot0 ? 0 : p];
+    const float2 u1 = in[slot0 ? C::N : C::N - p];
+    const float2 u2 = in[C::N / 2];
+    float2 A = slot0 ? make_float2(u0.x, u1.x) : u0;
+    float2 Bc = slot0 ? u2 : cconj(u1);
+    A = make_float2(rok ? A.x : 0.f, rok ? A.y : 0.f);
+    Bc = make_float2(rok ? Bc.x : 0.f, rok ? Bc.y : 0.f);
+    float2 zp, zq;
+    real_repack(slot0, A, Bc, root<LOGN + 1>(tw, p), zp, zq);
     float2* zz = lds + m * C::SP;
     zz[pad16(p)] = zp;
     zz[pad16(slot0 ? C::N / 2 : C::N - p)] = zq;
   }
   __syncthreads();
   LdsTile<C::SP, true> ld{lds};
+  const ET* __restrict__ aux = (const ET*)o.aux;
+  const ET* __restrict__ sh = (const ET*)o.s;
   auto st = [&](int m, int n, float2 v) {
     const int64_t r = r0 + m;
-    if (r >= rg.rows) return;
+    const bool rok = r < rg.rows;
     const int e0 = 2 * n - o.off2;  // output index of the even sample
-    const int h = int((r / (int64_t(rg.n0) * rg.n1)) % o.H);
     const float vv[2] = {v.x * o.scale, v.y * o.scale};
+    if constexpr (MODE == ND_OUT_Y) {
+      const int h = int((uint32_t(rok ? r : 0) / uint32_t(rg.n0 * rg.n1)) % uint32_t(o.H));
+      float sv = 0.f, a[2] = {0.f, 0.f};
+      if constexpr (HAS_S) {
+        sv = Elem<DT>::round(Elem<DT>::load(sh, h));
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int e = e0 + t;
-      if (e < 0 || e >= o.w2) continue;
-      const int64_t idx = r * o.w2 + e;
-      if constexpr (MODE == ND_OUT_Y) {
-        const bool has_s = o.s != nullptr;
-        const float sv = has_s ? Elem<DT>::round(Elem<DT>::load((const ET*)o.s, h)) : 0.f;
-        const float a = has_s ? Elem<DT>::load((const ET*)o.aux, idx) : 0.f;
-        Elem<DT>::store((ET*)o.out, idx, epilogue<DT>(vv[t], has_s, sv, a));
-      } else {
-        ((float*)o.out)[idx] = vv[t];
+        for (int t = 0; t < 2; ++t) {
+          const int e = e0 + t;
+          const bool ok = rok && e >= 0 && e < o.w2;
+          a[t] = Elem<DT>::load(aux, ok ? r * o.w2 + e : 0);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int e = e0 + t;
+        if (rok && e >= 0 && e < o.w2) Elem<DT>::store((ET*)o.out, r * o.w2 + e, epilogue<DT>(vv[t], HAS_S, sv, a[t]));
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int e = e0 + t;
+        if (!rok || e < 0 || e >= o.w2) continue;
+        ((float*)o.out)[r * o.w2 + e] = vv[t];
         if (o.gs && e == o.ga2) {
           const RowIdx q = row_index(r, rg.n0, rg.n1);
           if (q.a0 == o.ga0 && q.a1 == o.ga1) o.gs[q.bh] = vv[t];
@@ -206,6 +224,16 @@ __device__ __forceinline__ int64_t col_base(const ColGeom& cg, int64_t o) {
   return (o / cg.n_mid) * cg.spec + (o % cg.n_mid) * cg.mid_stride;
 }
 
+// Element n of inner column j of a column group, zero for j >= inner_count or
+// n >= valid.  Branch-free: the load is always issued (from the group's first
+// element when out of range), so a pass's loads stay in flight together.
+__device__ __forceinline__ float2 col_load(const float2* __restrict__ base, const ColGeom& cg, int j, int n,
+                                           int valid) {
+  const bool ok = (j < cg.inner_count) && (n < valid);
+  const float2 v = base[ok ? int64_t(n) * cg.axis_stride + j : 0];
+  return make_float2(ok ? v.x : 0.f, ok ? v.y : 0.f);
+}
+
 // Generic pass: reads elements [0, in_cnt) (rest zero), transforms, writes
 // outputs [out_off, out_off + out_cnt) to positions [0, out_cnt).
 // grid = (n_outer, ceil(inner_count / M)).
@@ -217,10 +245,7 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_kernel(float2* __res
   __shared__ float2 lds[C::M * C::S];
   float2* base = ws + col_base(cg, blockIdx.x);
   const int j0 = blockIdx.y * C::M;
-  auto ld = [&](int m, int n) -> float2 {
-    if (j0 + m >= cg.inner_count || n >= in_cnt) return make_float2(0.f, 0.f);
-    return base[int64_t(n) * cg.axis_stride + j0 + m];
-  };
+  auto ld = [&](int m, int n) -> float2 { return col_load(base, cg, j0 + m, n, in_cnt); };
   auto st = [&](int m, int k, float2 v) {
     const int e = k - out_off;
     if (j0 + m >= cg.inner_count || e < 0 || e >= out_cnt) return;
@@ -230,37 +255,48 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_kernel(float2* __res
 }
 
 // Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0).
-// grid = (B*H, ceil(inner_count / M)); Khat block index = bh (FiLM) or bh % H.
+// Shared filter (kfilm = 0): grid.x = H and the workgroup loops over the batch,
+// so its slice of Khat is read once per channel, not once per image; FiLM:
+// grid.x = B*H, one image each.  grid.y = ceil(inner_count / M).
 template <int LOGF>
 __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(float2* __restrict__ wsx,
                                                                         const float2* __restrict__ wsk, ColGeom cg,
-                                                                        int H, int kfilm, int S0, int c0,
+                                                                        int B, int H, int kfilm, int S0, int c0,
                                                                         const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF>;
   __shared__ float2 lds[C::M * C::S];
-  const int64_t bh = blockIdx.x;
-  const int64_t hk = kfilm ? bh : (bh % H);
-  float2* base = wsx + bh * cg.spec;
+  const int64_t hk = blockIdx.x;
   const float2* kb = wsk + hk * cg.spec;
   const int j0 = blockIdx.y * C::M;
-  auto ld = [&](int m, int n) -> float2 {
-    if (j0 + m >= cg.inner_count || n >= S0) return make_float2(0.f, 0.f);
-    return base[int64_t(n) * cg.axis_stride + j0 + m];
-  };
-  auto st_lds = [&](int m, int n, float2 v) { lds[m * C::S + n] = v; };
-  fft<LOGF, false, C::M, C::T, C::S, true>(lds, ld, st_lds, tw);
-  for (int e = opaque_tid(); e < C::TILE; e += C::T) {
-    const int m = e % C::M, k = e / C::M;
-    if (j0 + m < cg.inner_count) lds[m * C::S + k] = cmul(lds[m * C::S + k], kb[int64_t(k) * cg.axis_stride + j0 + m]);
+  // Filter spectrum of this column block (element e -> column e % M,
+  // frequency e / M), loaded before the first transform so its latency hides.
+  constexpr int PT = C::TILE / C::T;
+  float2 kv[PT];
+#pragma unroll
+  for (int it = 0; it < PT; ++it) {
+    const int e = opaque_tid() + it * C::T;
+    kv[it] = col_load(kb, cg, j0 + e % C::M, e / C::M, C::F);
   }
-  __syncthreads();
-  auto ldl = [&](int m, int n) -> float2 { return lds[m * C::S + n]; };
-  auto st = [&](int m, int k, float2 v) {
-    const int e = k - c0;
-    if (j0 + m >= cg.inner_count || e < 0 || e >= S0) return;
-    base[int64_t(e) * cg.axis_stride + j0 + m] = v;
-  };
-  fft<LOGF, true, C::M, C::T, C::S, true>(lds, ldl, st, tw);
+  const int nb = kfilm ? 1 : B;
+  for (int bi = 0; bi < nb; ++bi) {
+    float2* base = wsx + (kfilm ? hk : int64_t(bi) * H + hk) * cg.spec;
+    auto ld = [&](int m, int n) -> float2 { return col_load(base, cg, j0 + m, n, S0); };
+    LdsTile<C::S, false> tile{lds};
+    fft<LOGF, false, C::M, C::T, C::S, true>(lds, ld, tile, tw);
+#pragma unroll
+    for (int it = 0; it < PT; ++it) {
+      const int e = opaque_tid() + it * C::T;
+      float2& z = lds[(e % C::M) * C::S + e / C::M];
+      z = cmul(z, kv[it]);
+    }
+    __syncthreads();
+    auto st = [&](int m, int k, float2 v) {
+      const int e = k - c0;
+      if (j0 + m >= cg.inner_count || e < 0 || e >= S0) return;
+      base[int64_t(e) * cg.axis_stride + j0 + m] = v;
+    };
+    fft<LOGF, true, C::M, C::T, C::S, true>(lds, tile, st, tw);
+  }
 }
 
 // Shift ramp parameters of the adjoint (3 axes; unused axes have c = 0).
@@ -303,27 +339,30 @@ __global__ __launch_bounds__(ColNdBwdCfg<LOGF>::T) void nd_col_bwd_kernel(float2
     const int64_t bh = kfilm ? hk : (int64_t(bi) * H + hk);
     float2* gb = wsg + bh * cg.spec;
     const float2* xb = wsx + bh * cg.spec;
-    auto ldg = [&](int m, int n) -> float2 {
-      if (j0 + m >= cg.inner_count || n >= S0) return make_float2(0.f, 0.f);
-      return gb[int64_t(n) * cg.axis_stride + j0 + m];
-    };
-    auto ldx = [&](int m, int n) -> float2 {
-      if (j0 + m >= cg.inner_count || n >= S0) return make_float2(0.f, 0.f);
-      return xb[int64_t(n) * cg.axis_stride + j0 + m];
-    };
-    auto stG = [&](int m, int n, float2 v) { ldsG[m * C::S + n] = v; };
-    auto stX = [&](int m, int n, float2 v) { ldsX[m * C::S + n] = v; };
+    constexpr int PT = C::TILE / C::T;
+    float2 kv[PT];
+#pragma unroll
+    for (int it = 0; it < PT; ++it) {
+      const int e = opaque_tid() + it * C::T;
+      kv[it] = col_load(kb, cg, j0 + e % C::M, e / C::M, C::F);
+    }
+    auto ldg = [&](int m, int n) -> float2 { return col_load(gb, cg, j0 + m, n, S0); };
+    auto ldx = [&](int m, int n) -> float2 { return col_load(xb, cg, j0 + m, n, S0); };
+    LdsTile<C::S, false> stG{ldsG};
+    LdsTile<C::S, false> stX{ldsX};
     fft<LOGF, false, C::M, C::T, C::S, true>(ldsG, ldg, stG, tw);
     fft<LOGF, false, C::M, C::T, C::S, true>(ldsX, ldx, stX, tw);
-    for (int e = opaque_tid(); e < C::TILE; e += C::T) {
+#pragma unroll
+    for (int it = 0; it < PT; ++it) {
+      const int e = opaque_tid() + it * C::T;
       const int m = e % C::M, k = e / C::M;
-      if (j0 + m >= cg.inner_count) continue;
-      const float2 gsh = cmul(ldsG[m * C::S + k], shift_ramp(rp, k, j0 + m));
-      ldsQ[m * C::S + k] = cadd(ldsQ[m * C::S + k], cmulc(gsh, ldsX[m * C::S + k]));
-      ldsG[m * C::S + k] = cmulc(gsh, kb[int64_t(k) * cg.axis_stride + j0 + m]);
+      const int a = m * C::S + k;
+      const float2 gsh = cmul(ldsG[a], shift_ramp(rp, k, j0 + m));
+      ldsQ[a] = cadd(ldsQ[a], cmulc(gsh, ldsX[a]));
+      ldsG[a] = cmulc(gsh, kv[it]);
     }
     __syncthreads();
-    auto ldl = [&](int m, int n) -> float2 { return ldsG[m * C::S + n]; };
+    LdsTile<C::S, false> ldl{ldsG};
     auto st = [&](int m, int k, float2 v) {
       if (j0 + m >= cg.inner_count || k >= S0) return;
       gb[int64_t(k) * cg.axis_stride + j0 + m] = v;
@@ -331,7 +370,7 @@ __global__ __launch_bounds__(ColNdBwdCfg<LOGF>::T) void nd_col_bwd_kernel(float2
     fft<LOGF, true, C::M, C::T, C::S, true>(ldsG, ldl, st, tw);
   }
   float2* qb = wsq + hk * cg.spec;
-  auto ldq = [&](int m, int n) -> float2 { return ldsQ[m * C::S + n]; };
+  LdsTile<C::S, false> ldq{ldsQ};
   auto stq = [&](int m, int k, float2 v) {
     if (j0 + m >= cg.inner_count || k >= K0) return;
     qb[int64_t(k) * cg.axis_stride + j0 + m] = v;
