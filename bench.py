@@ -96,6 +96,29 @@ def cpu_baseline(channels: int, iters: int) -> dict:
     }
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "fftconv1d_causal_cfg3_fwd_bwd_traffic.txt")
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes of one config-3 step from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary, each scaled by its copy-kernel calibration factor."""
+    try:
+        lines = open(TRAFFIC_PROFILE).read().splitlines()
+    except OSError:
+        return None
+    ff = wf = None
+    total = 0.0
+    for ln in lines:
+        t = ln.split()
+        if not t or t[0].startswith("#"):
+            continue
+        if t[0] == "calibration":
+            ff, wf = float(t[1]), float(t[2])
+        elif t[0] == "kernel" and ff is not None:
+            total += float(t[2]) * 1024 * ff + float(t[3]) * 1024 * wf
+    return int(round(total)) if total else None
+
+
 def _time_steps(step, steps: int, warmup: int) -> list[float]:
     """Event-timed steps on the current stream (ms each) after untimed warmup."""
     for _ in range(warmup):
@@ -290,9 +313,10 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "scope": "fwd+bwd launch sequence (all kernels of both calls); algorithmic bytes "
-                     f"{nbytes} per step",
+                     f"{nbytes} per step; traffic = HBM bytes per step from "
+                     "profiles/fftconv1d_causal_cfg3_fwd_bwd_traffic.txt",
             "fft_tflops_radix2_count": round(flops / (ms * 1e-3) / 1e12, 2),
         },
     }
