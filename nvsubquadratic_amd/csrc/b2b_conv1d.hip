@@ -16,6 +16,26 @@
 
 namespace nsq {
 
+// Dynamic LDS layout of b2b_fwd_kernel / b2b_bwd1_kernel, sized by the actual
+// tap counts (a static layout for 256 taps would cost a workgroup per CU).
+// Float offsets, each a multiple of 8 so the sliding-window reads stay aligned.
+struct B2BLds {
+  int q, k, v, z, wq, wk, wv, wm, total;
+  __host__ __device__ static int up8(int n) { return (n + 7) & ~7; }
+  __host__ __device__ B2BLds(int Kp, int Km) {
+    const int hp = Kp - 1, hz = Km - 1;
+    q = 0;
+    k = q + up8(kConvTile + hp + 2 * kConvPer);
+    v = k + up8(kConvTile + hz + hp + 2 * kConvPer);
+    z = v + up8(kConvTile + hz + hp + 2 * kConvPer);
+    wq = z + up8(kConvTile + hz + 2 * kConvPer);
+    wk = wq + up8(Kp);
+    wv = wk + up8(Kp);
+    wm = wv + up8(Kp);
+    total = wm + up8(Km);
+  }
+};
+
 // grid = (B*C, ceil(L / kConvTile)).  xs_*: staged input rows; zs: z with the
 // mixer halo.
 template <int DT>
@@ -26,10 +46,16 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename El
                                                                 typename Elem<DT>::T* __restrict__ y, int C, int L,
                                                                 int Kp, int Km) {
   constexpr int TF = conv_tile_floats(2 * kConvMaxK);
-  __shared__ float xs_q[conv_tile_floats(kConvMaxK)];
-  __shared__ float xs_k[TF];
-  __shared__ float xs_v[TF];
-  __shared__ float zs[conv_tile_floats(kConvMaxK)];
+  extern __shared__ float smem[];
+  const B2BLds lay(Kp, Km);
+  float* xs_q = smem + lay.q;
+  float* xs_k = smem + lay.k;
+  float* xs_v = smem + lay.v;
+  float* zs = smem + lay.z;
+  float* wlq = smem + lay.wq;
+  float* wlk = smem + lay.wk;
+  float* wlv = smem + lay.wv;
+  float* wlm = smem + lay.wm;
   const int64_t row = blockIdx.x;  // b*C + c
   const int b = int(row / C), c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
@@ -38,12 +64,22 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename El
   const int64_t xv = xk + int64_t(C) * L;
   const int hz = Km - 1, hp = Kp - 1;
   // q needs [n0 - hp, n0 + tile); k, v need [n0 - hz - hp, n0 + tile).
-  stage_row<DT>(xs_q, x + xq, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
-  stage_row<DT>(xs_k, x + xk, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
-  stage_row<DT>(xs_v, x + xv, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
-  const float* wq = wp + int64_t(c) * Kp;
-  const float* wk = wp + int64_t(C + c) * Kp;
-  const float* wv = wp + int64_t(2 * C + c) * Kp;
+  stage_weights<false>(wlq, wp + int64_t(c) * Kp, Kp);
+  stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
+  stage_weights<false>(wlv, wp + int64_t(2 * C + c) * Kp, Kp);
+  stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
+  {
+    // all three rows' loads in flight together, then the LDS stores
+    RowStage<DT, conv_tile_floats(kConvMaxK)> sq;
+    RowStage<DT, TF> sk, sv;
+    sq.load(x + xq, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+    sk.load(x + xk, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+    sv.load(x + xv, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+    sq.store(xs_q, kConvTile + hp + 2 * kConvPer);
+    sk.store(xs_k, kConvTile + hz + hp + 2 * kConvPer);
+    sv.store(xs_v, kConvTile + hz + hp + 2 * kConvPer);
+    __syncthreads();
+  }
   // z[n] for n in [n0 - hz, n0 + tile): zs[i] = z[n0 - hz + i]; z of positions
   // before the sequence start is 0 (the mixer conv's causal padding).
   const int zcount = kConvTile + hz + 2 * kConvPer;
@@ -52,8 +88,8 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename El
     float kk = 0.f, vv = 0.f;
     if (n >= 0 && n < L) {
       for (int j = 0; j < Kp; ++j) {
-        kk = fmaf(wk[j], xs_k[i + j], kk);
-        vv = fmaf(wv[j], xs_v[i + j], vv);
+        kk = fmaf(wlk[j], xs_k[i + j], kk);
+        vv = fmaf(wlv[j], xs_v[i + j], vv);
       }
     }
     zs[i] = kk * vv;
@@ -63,8 +99,8 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename El
   float qa[kConvPer], ha[kConvPer];
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) qa[e] = ha[e] = 0.f;
-  slide_fma(qa, xs_q, base, Kp, [&](int j) { return wq[j]; });
-  slide_fma(ha, zs, base, Km, [&](int j) { return wm[int64_t(c) * Km + j]; });
+  slide_fma(qa, xs_q, base, Kp, wlq);
+  slide_fma(ha, zs, base, Km, wlm);
   const float sk = skip ? skip[c] : 0.f;
   typename Elem<DT>::T* yr = y + row * L;
 #pragma unroll
@@ -89,10 +125,16 @@ __global__ __launch_bounds__(kConvThreads) void b2b_bwd1_kernel(const typename E
                                                                  float* __restrict__ gp, float* __restrict__ gh,
                                                                  float* __restrict__ zw, int C, int L, int Kp, int Km) {
   constexpr int TF = conv_tile_floats(2 * kConvMaxK);
-  __shared__ float xs_q[conv_tile_floats(kConvMaxK)];
-  __shared__ float xs_k[TF];
-  __shared__ float xs_v[TF];
-  __shared__ float zs[conv_tile_floats(kConvMaxK)];
+  extern __shared__ float smem[];
+  const B2BLds lay(Kp, Km);
+  float* xs_q = smem + lay.q;
+  float* xs_k = smem + lay.k;
+  float* xs_v = smem + lay.v;
+  float* zs = smem + lay.z;
+  float* wlq = smem + lay.wq;
+  float* wlk = smem + lay.wk;
+  float* wlv = smem + lay.wv;
+  float* wlm = smem + lay.wm;
   const int64_t row = blockIdx.x;
   const int b = int(row / C), c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
@@ -100,20 +142,30 @@ __global__ __launch_bounds__(kConvThreads) void b2b_bwd1_kernel(const typename E
   const int64_t xk = xq + int64_t(C) * L;
   const int64_t xv = xk + int64_t(C) * L;
   const int hz = Km - 1, hp = Kp - 1;
-  stage_row<DT>(xs_q, x + xq, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
-  stage_row<DT>(xs_k, x + xk, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
-  stage_row<DT>(xs_v, x + xv, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
-  const float* wq = wp + int64_t(c) * Kp;
-  const float* wk = wp + int64_t(C + c) * Kp;
-  const float* wv = wp + int64_t(2 * C + c) * Kp;
+  stage_weights<false>(wlq, wp + int64_t(c) * Kp, Kp);
+  stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
+  stage_weights<false>(wlv, wp + int64_t(2 * C + c) * Kp, Kp);
+  stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
+  {
+    // all three rows' loads in flight together, then the LDS stores
+    RowStage<DT, conv_tile_floats(kConvMaxK)> sq;
+    RowStage<DT, TF> sk, sv;
+    sq.load(x + xq, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+    sk.load(x + xk, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+    sv.load(x + xv, n0 - hz - hp, kConvTile + hz + hp + 2 * kConvPer, L);
+    sq.store(xs_q, kConvTile + hp + 2 * kConvPer);
+    sk.store(xs_k, kConvTile + hz + hp + 2 * kConvPer);
+    sv.store(xs_v, kConvTile + hz + hp + 2 * kConvPer);
+    __syncthreads();
+  }
   const int zcount = kConvTile + hz + 2 * kConvPer;
   for (int i = threadIdx.x; i < zcount; i += kConvThreads) {
     const int64_t n = n0 - hz + i;
     float kk = 0.f, vv = 0.f;
     if (n >= 0 && n < L) {
       for (int j = 0; j < Kp; ++j) {
-        kk = fmaf(wk[j], xs_k[i + j], kk);
-        vv = fmaf(wv[j], xs_v[i + j], vv);
+        kk = fmaf(wlk[j], xs_k[i + j], kk);
+        vv = fmaf(wlv[j], xs_v[i + j], vv);
       }
     }
     zs[i] = kk * vv;
@@ -123,20 +175,25 @@ __global__ __launch_bounds__(kConvThreads) void b2b_bwd1_kernel(const typename E
   float qa[kConvPer], ha[kConvPer];
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) qa[e] = ha[e] = 0.f;
-  slide_fma(qa, xs_q, base, Kp, [&](int j) { return wq[j]; });
-  slide_fma(ha, zs, base, Km, [&](int j) { return wm[int64_t(c) * Km + j]; });
+  slide_fma(qa, xs_q, base, Kp, wlq);
+  slide_fma(ha, zs, base, Km, wlm);
   const float sk = skip ? skip[c] : 0.f;
   const int64_t orow = row * L;                           // [B, C, L] rows
   const int64_t prow = (int64_t(b) * 3 * C + c) * L;      // q rows of gp [B, 3C, L]
+  float gva[kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) {  // all loads first (clamped), then predicated stores
+    const int64_t n = n0 + base + e;
+    gva[e] = Elem<DT>::load(g, orow + (n < L ? n : 0));
+  }
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) {
     const int64_t n = n0 + base + e;
     if (n < L) {
       const float zv = zs[base + e + hz];
       const float hv = fmaf(sk, zv, ha[e]);
-      const float gv = Elem<DT>::load(g, orow + n);
-      gp[prow + n] = gv * hv;
-      gh[orow + n] = gv * qa[e];
+      gp[prow + n] = gva[e] * hv;
+      gh[orow + n] = gva[e] * qa[e];
       zw[orow + n] = zv;
     }
   }
@@ -154,23 +211,36 @@ __global__ __launch_bounds__(kConvThreads) void b2b_bwd2_kernel(const typename E
   __shared__ float ghs[conv_tile_floats(kConvMaxK)];
   __shared__ float xs_k[conv_tile_floats(kConvMaxK)];
   __shared__ float xs_v[conv_tile_floats(kConvMaxK)];
+  __shared__ float wlm[kConvWeightFloats];
+  __shared__ float wlk[kConvWeightFloats];
+  __shared__ float wlv[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int b = int(row / C), c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
+  stage_weights<true>(wlm, wm + int64_t(c) * Km, Km);
+  stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
+  stage_weights<false>(wlv, wp + int64_t(2 * C + c) * Kp, Kp);
   const int64_t xk = (int64_t(b) * 3 * C + C + c) * L;
   const int64_t xv = xk + int64_t(C) * L;
   const int hp = Kp - 1;
-  stage_row<NSQ_DTYPE_F32>(ghs, gh + row * L, n0, kConvTile + Km - 1 + 2 * kConvPer, L);
-  stage_row<DT>(xs_k, x + xk, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
-  stage_row<DT>(xs_v, x + xv, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
-  const float* wmr = wm + int64_t(c) * Km;
+  {
+    RowStage<NSQ_DTYPE_F32, conv_tile_floats(kConvMaxK)> sh;
+    RowStage<DT, conv_tile_floats(kConvMaxK)> sk, sv;
+    sh.load(gh + row * L, n0, kConvTile + Km - 1 + 2 * kConvPer, L);
+    sk.load(x + xk, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+    sv.load(x + xv, n0 - hp, kConvTile + hp + 2 * kConvPer, L);
+    sh.store(ghs, kConvTile + Km - 1 + 2 * kConvPer);
+    sk.store(xs_k, kConvTile + hp + 2 * kConvPer);
+    sv.store(xs_v, kConvTile + hp + 2 * kConvPer);
+    __syncthreads();
+  }
   const int base = threadIdx.x * kConvPer;
   float gz[kConvPer], ka[kConvPer], va[kConvPer];
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) gz[e] = ka[e] = va[e] = 0.f;
-  slide_fma(gz, ghs, base, Km, [&](int m) { return wmr[Km - 1 - m]; });
-  slide_fma(ka, xs_k, base, Kp, [&](int j) { return wp[int64_t(C + c) * Kp + j]; });
-  slide_fma(va, xs_v, base, Kp, [&](int j) { return wp[int64_t(2 * C + c) * Kp + j]; });
+  slide_fma(gz, ghs, base, Km, wlm);
+  slide_fma(ka, xs_k, base, Kp, wlk);
+  slide_fma(va, xs_v, base, Kp, wlv);
   const float sk = skip ? skip[c] : 0.f;
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) {
@@ -193,7 +263,7 @@ static void launch_b2b_fwd(const void* x, const float* wp, const float* wm, cons
                            int L, int Kp, int Km, hipStream_t st) {
   using ET = typename Elem<DT>::T;
   dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
-  hipLaunchKernelGGL((b2b_fwd_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)x, wp, wm, skip, (ET*)y, C, L,
+  hipLaunchKernelGGL((b2b_fwd_kernel<DT>), grid, dim3(kConvThreads), size_t(B2BLds(Kp, Km).total) * sizeof(float), st, (const ET*)x, wp, wm, skip, (ET*)y, C, L,
                      Kp, Km);
 }
 
@@ -207,7 +277,7 @@ static void launch_b2b_bwd(const void* g, const void* x, const float* wp, const 
   float* gh = ws + 3 * E;    // [B, C, L]
   float* zw = ws + 4 * E;    // [B, C, L]
   dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
-  hipLaunchKernelGGL((b2b_bwd1_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)g, (const ET*)x, wp, wm, skip,
+  hipLaunchKernelGGL((b2b_bwd1_kernel<DT>), grid, dim3(kConvThreads), size_t(B2BLds(Kp, Km).total) * sizeof(float), st, (const ET*)g, (const ET*)x, wp, wm, skip,
                      gp, gh, zw, C, L, Kp, Km);
   hipLaunchKernelGGL((b2b_bwd2_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)x, wp, wm, skip,
                      (const float*)gh, gp, C, L, Kp, Km);

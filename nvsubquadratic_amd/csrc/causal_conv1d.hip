@@ -16,18 +16,19 @@ __global__ __launch_bounds__(kConvThreads) void cconv_fwd_kernel(const typename 
                                                                   typename Elem<DT>::T* __restrict__ y, int C, int L,
                                                                   int K) {
   __shared__ float xs[conv_tile_floats(kConvMaxK)];
+  __shared__ float wl[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
   const typename Elem<DT>::T* xr = x + row * L;
-  stage_row<DT>(xs, xr, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
-  const float* wr = w + int64_t(c) * K;
+  stage_weights<false>(wl, w + int64_t(c) * K, K);
+  stage_row<DT, conv_tile_floats(kConvMaxK)>(xs, xr, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
   const float b0 = bias ? bias[c] : 0.f;
   float acc[kConvPer];
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) acc[e] = b0;
   const int base = threadIdx.x * kConvPer;
-  slide_fma(acc, xs, base, K, [&](int j) { return wr[j]; });
+  slide_fma(acc, xs, base, K, wl);
   typename Elem<DT>::T* yr = y + row * L;
 #pragma unroll
   for (int e = 0; e < kConvPer; e += 2) {
@@ -44,17 +45,18 @@ __global__ __launch_bounds__(kConvThreads) void cconv_gpre_silu_kernel(const typ
                                                                         const float* __restrict__ bias,
                                                                         float* __restrict__ gpre, int C, int L, int K) {
   __shared__ float xs[conv_tile_floats(kConvMaxK)];
+  __shared__ float wl[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
-  stage_row<DT>(xs, x + row * L, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
-  const float* wr = w + int64_t(c) * K;
+  stage_weights<false>(wl, w + int64_t(c) * K, K);
+  stage_row<DT, conv_tile_floats(kConvMaxK)>(xs, x + row * L, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
   const float b0 = bias ? bias[c] : 0.f;
   float acc[kConvPer];
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) acc[e] = b0;
   const int base = threadIdx.x * kConvPer;
-  slide_fma(acc, xs, base, K, [&](int j) { return wr[j]; });
+  slide_fma(acc, xs, base, K, wl);
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) {
     const int64_t n = n0 + base + e;

@@ -37,42 +37,90 @@ __device__ __forceinline__ float dsilu(float p) {
   return s * (1.f + p * (1.f - s));
 }
 
-// Stage src[row_off + first + i] for i in [0, count) into LDS as fp32 (zeros
-// outside [0, len)).  All threads participate; ends with a barrier.
-template <int DT>
+// LDS floats needed for a tile with halo K-1 plus the window's read-ahead.
+constexpr int conv_tile_floats(int kmax) { return kConvTile + kmax - 1 + 2 * kConvPer; }
+
+// Staging of row[first + i], i in [0, count <= MAXC), as fp32 with zeros
+// outside [0, len).  load() issues every element load of the thread at once
+// (fixed trip count, clamped in-bounds indices, zero selected afterwards), so
+// they are in flight together; store() writes them to LDS.  Several rows can
+// be loaded before any is stored.
+template <int DT, int MAXC>
+struct RowStage {
+  static constexpr int IT = (MAXC + kConvThreads - 1) / kConvThreads;
+  float v[IT];
+  __device__ __forceinline__ void load(const typename Elem<DT>::T* __restrict__ row, int64_t first, int count,
+                                       int64_t len) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int i = int(threadIdx.x) + it * kConvThreads;
+      const int64_t n = first + i;
+      const bool ok = i < count && n >= 0 && n < len;
+      const float a = Elem<DT>::load(row, ok ? n : 0);
+      v[it] = ok ? a : 0.f;
+    }
+  }
+  __device__ __forceinline__ void store(float* dst, int count) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int i = int(threadIdx.x) + it * kConvThreads;
+      if (i < count) dst[i] = v[it];
+    }
+  }
+};
+
+// One row staged into LDS; ends with a barrier.
+template <int DT, int MAXC>
 __device__ __forceinline__ void stage_row(float* dst, const typename Elem<DT>::T* __restrict__ row, int64_t first,
                                           int count, int64_t len) {
-  for (int i = threadIdx.x; i < count; i += blockDim.x) {
-    const int64_t n = first + i;
-    dst[i] = (n >= 0 && n < len) ? Elem<DT>::load(row, n) : 0.f;
-  }
+  RowStage<DT, MAXC> rs;
+  rs.load(row, first, count, len);
+  rs.store(dst, count);
   __syncthreads();
 }
 
-// acc[e] += sum_{j<K} wt(j) * xs[base + e + j], e < kConvPer, using a
-// register window; wt(j) must be wave-uniform.  xs must hold base + K + 7
-// valid entries (the caller's tile has kConvPer slack at the end).
-template <class WT>
-__device__ __forceinline__ void slide_fma(float (&acc)[kConvPer], const float* xs, int base, int K, WT wt) {
+// LDS floats of a staged weight row (K <= kConvMaxK, zero-padded to a
+// multiple of kConvPer).
+constexpr int kConvWeightFloats = kConvMaxK;
+static_assert(kConvMaxK == kConvThreads && kConvMaxK % kConvPer == 0, "stage_weights: one tap per thread");
+
+// One channel's depthwise weights staged in LDS for slide_fma: wl[j] = w[j]
+// (w[K-1-j] when REV, the correlation of the adjoints) for j < K, zero up to
+// the next multiple of kConvPer.  The caller's staging barrier must follow.
+template <bool REV>
+__device__ __forceinline__ void stage_weights(float* wl, const float* __restrict__ w, int K) {
+  const int j = int(threadIdx.x);
+  const int kp = (K + kConvPer - 1) / kConvPer * kConvPer;
+  const bool ok = j < K;
+  const float v = w[ok ? (REV ? K - 1 - j : j) : 0];
+  if (j < kp) wl[j] = ok ? v : 0.f;
+}
+
+// acc[e] += sum_{j<K} wl[j] * xs[base + e + j], e < kConvPer, using a
+// register window.  wl: weights staged by stage_weights (all lanes read the
+// same LDS words: broadcast, and no per-tap branch or scalar-load wait).  xs
+// must hold base + K + 7 valid entries (the caller's tile has kConvPer slack).
+__device__ __forceinline__ void slide_fma(float (&acc)[kConvPer], const float* xs, int base, int K,
+                                          const float* wl) {
   float win[2 * kConvPer];
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) win[e] = xs[base + e];
   for (int jb = 0; jb < K; jb += kConvPer) {
+    float w[kConvPer];
 #pragma unroll
-    for (int e = 0; e < kConvPer; ++e) win[kConvPer + e] = xs[base + jb + kConvPer + e];
+    for (int e = 0; e < kConvPer; ++e) {
+      win[kConvPer + e] = xs[base + jb + kConvPer + e];
+      w[e] = wl[jb + e];
+    }
 #pragma unroll
     for (int jj = 0; jj < kConvPer; ++jj) {
-      const float w = (jb + jj < K) ? wt(jb + jj) : 0.f;
 #pragma unroll
-      for (int e = 0; e < kConvPer; ++e) acc[e] = fmaf(w, win[e + jj], acc[e]);
+      for (int e = 0; e < kConvPer; ++e) acc[e] = fmaf(w[jj], win[e + jj], acc[e]);
     }
 #pragma unroll
     for (int e = 0; e < kConvPer; ++e) win[e] = win[kConvPer + e];
   }
 }
-
-// LDS floats needed for a tile with halo K-1 plus the window's read-ahead.
-constexpr int conv_tile_floats(int kmax) { return kConvTile + kmax - 1 + 2 * kConvPer; }
 
 // Per-channel reduction for depthwise weight / bias gradients:
 //   gw[c, j] += sum_n gp[n] * x[n - K + 1 + j],  gb[c] += sum_n gp[n]
@@ -140,17 +188,18 @@ __global__ __launch_bounds__(kConvThreads) void cconv_gx_kernel(const typename E
                                                                  typename Elem<DT>::T* __restrict__ gx, int C, int L,
                                                                  int K) {
   __shared__ float gs[conv_tile_floats(kConvMaxK)];
+  __shared__ float wl[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
-  stage_row<GT>(gs, gp + row * L, n0, kConvTile + K - 1 + 2 * kConvPer, L);
-  const float* wr = w + int64_t(c) * K;
+  stage_weights<true>(wl, w + int64_t(c) * K, K);
+  stage_row<GT, conv_tile_floats(kConvMaxK)>(gs, gp + row * L, n0, kConvTile + K - 1 + 2 * kConvPer, L);
   float acc[kConvPer];
 #pragma unroll
   for (int e = 0; e < kConvPer; ++e) acc[e] = 0.f;
   const int base = threadIdx.x * kConvPer;
   // acc[e] = sum_m w[K-1-m] gs[base + e + m]
-  slide_fma(acc, gs, base, K, [&](int m) { return wr[K - 1 - m]; });
+  slide_fma(acc, gs, base, K, wl);
   typename Elem<DT>::T* gr = gx + row * L;
 #pragma unroll
   for (int e = 0; e < kConvPer; e += 2) {
@@ -178,8 +227,8 @@ __global__ __launch_bounds__(kConvThreads) void cconv_wgrad_kernel(const typenam
     const int64_t row = int64_t(b) * C + c;
     for (int64_t n0 = 0; n0 < L; n0 += kConvTile) {
       const int count = int((L - n0) < kConvTile ? (L - n0) : kConvTile);
-      stage_row<DT>(xs, x + row * L, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
-      stage_row<GT>(gps, gp + row * L, n0, kConvTile + 2 * kConvPer, L);
+      stage_row<DT, conv_tile_floats(kConvMaxK)>(xs, x + row * L, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
+      stage_row<GT, conv_tile_floats(1)>(gps, gp + row * L, n0, kConvTile + 2 * kConvPer, L);
       wgrad_tile(acc, bacc, gps, xs, K, count);
       __syncthreads();
     }
