@@ -46,7 +46,7 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename El
                                                                 typename Elem<DT>::T* __restrict__ y, int C, int L,
                                                                 int Kp, int Km) {
   constexpr int TF = conv_tile_floats(2 * kConvMaxK);
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   const B2BLds lay(Kp, Km);
   float* xs_q = smem + lay.q;
   float* xs_k = smem + lay.k;
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kConvThreads) void b2b_bwd1_kernel(const typename E
                                                                  float* __restrict__ gp, float* __restrict__ gh,
                                                                  float* __restrict__ zw, int C, int L, int Kp, int Km) {
   constexpr int TF = conv_tile_floats(2 * kConvMaxK);
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   const B2BLds lay(Kp, Km);
   float* xs_q = smem + lay.q;
   float* xs_k = smem + lay.k;
@@ -208,12 +208,12 @@ __global__ __launch_bounds__(kConvThreads) void b2b_bwd2_kernel(const typename E
                                                                  const float* __restrict__ skip,
                                                                  const float* __restrict__ gh, float* __restrict__ gp,
                                                                  int C, int L, int Kp, int Km) {
-  __shared__ float ghs[conv_tile_floats(kConvMaxK)];
-  __shared__ float xs_k[conv_tile_floats(kConvMaxK)];
-  __shared__ float xs_v[conv_tile_floats(kConvMaxK)];
-  __shared__ float wlm[kConvWeightFloats];
-  __shared__ float wlk[kConvWeightFloats];
-  __shared__ float wlv[kConvWeightFloats];
+  __shared__ __align__(16) float ghs[conv_tile_floats(kConvMaxK)];
+  __shared__ __align__(16) float xs_k[conv_tile_floats(kConvMaxK)];
+  __shared__ __align__(16) float xs_v[conv_tile_floats(kConvMaxK)];
+  __shared__ __align__(16) float wlm[kConvWeightFloats];
+  __shared__ __align__(16) float wlk[kConvWeightFloats];
+  __shared__ __align__(16) float wlv[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int b = int(row / C), c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
@@ -302,7 +302,7 @@ static int validate_b2b(const void* a, const void* b, const float* wp, const flo
   NSQ_CHECK_ARG(B >= 1 && C >= 1 && L >= 1, "b2b_causal_conv1d: sizes must be positive");
   NSQ_CHECK_ARG(Kp >= 1 && Kp <= kConvMaxK && Km >= 1 && Km <= kConvMaxK,
                 "b2b_causal_conv1d: kernel sizes (%lld, %lld) outside [1, %d]", (long long)Kp, (long long)Km, kConvMaxK);
-  NSQ_CHECK_ARG(B * 3 * C <= 0x7fffffff && L <= 0x7fffffff, "b2b_causal_conv1d: tensor too large");
+  NSQ_CHECK_ARG(B * 3 * C <= 0x7fffffff && L < (int64_t(1) << 28), "b2b_causal_conv1d: tensor too large (rows are staged through 32-bit byte offsets: L < 2^28)");
   return NSQ_OK;
 }
 

@@ -15,8 +15,8 @@ __global__ __launch_bounds__(kConvThreads) void cconv_fwd_kernel(const typename 
                                                                   const float* __restrict__ bias,
                                                                   typename Elem<DT>::T* __restrict__ y, int C, int L,
                                                                   int K) {
-  __shared__ float xs[conv_tile_floats(kConvMaxK)];
-  __shared__ float wl[kConvWeightFloats];
+  __shared__ __align__(16) float xs[conv_tile_floats(kConvMaxK)];
+  __shared__ __align__(16) float wl[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
@@ -44,8 +44,8 @@ __global__ __launch_bounds__(kConvThreads) void cconv_gpre_silu_kernel(const typ
                                                                         const float* __restrict__ w,
                                                                         const float* __restrict__ bias,
                                                                         float* __restrict__ gpre, int C, int L, int K) {
-  __shared__ float xs[conv_tile_floats(kConvMaxK)];
-  __shared__ float wl[kConvWeightFloats];
+  __shared__ __align__(16) float xs[conv_tile_floats(kConvMaxK)];
+  __shared__ __align__(16) float wl[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
@@ -103,7 +103,7 @@ static int validate_cconv(const void* a, const void* b, const float* w, int dtyp
   NSQ_CHECK_ARG(act == NSQ_ACT_IDENTITY || act == NSQ_ACT_SILU, "causal_conv1d: activation code %d not in {0, 1}", act);
   NSQ_CHECK_ARG(B >= 1 && C >= 1 && L >= 1, "causal_conv1d: sizes must be positive");
   NSQ_CHECK_ARG(K >= 1 && K <= kConvMaxK, "causal_conv1d: kernel size %lld outside [1, %d]", (long long)K, kConvMaxK);
-  NSQ_CHECK_ARG(B * C <= 0x7fffffff && L <= 0x7fffffff, "causal_conv1d: tensor too large");
+  NSQ_CHECK_ARG(B * C <= 0x7fffffff && L < (int64_t(1) << 28), "causal_conv1d: tensor too large (rows are staged through 32-bit byte offsets: L < 2^28)");
   return NSQ_OK;
 }
 

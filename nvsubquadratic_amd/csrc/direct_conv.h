@@ -42,23 +42,22 @@ constexpr int conv_tile_floats(int kmax) { return kConvTile + kmax - 1 + 2 * kCo
 
 // Staging of row[first + i], i in [0, count <= MAXC), as fp32 with zeros
 // outside [0, len).  load() issues every element load of the thread at once
-// (fixed trip count, clamped in-bounds indices, zero selected afterwards), so
-// they are in flight together; store() writes them to LDS.  Several rows can
-// be loaded before any is stored.
+// (fixed trip count), so they are in flight together; store() writes them to
+// LDS.  Several rows can be loaded before any is stored.  The row is a raw
+// buffer of len elements (its pointer is uniform: one (b, c) row per
+// workgroup): positions at or beyond len read as zero through the hardware
+// range check, positions before 0 through RowBuf::elem_halo.
 template <int DT, int MAXC>
 struct RowStage {
   static constexpr int IT = (MAXC + kConvThreads - 1) / kConvThreads;
   float v[IT];
   __device__ __forceinline__ void load(const typename Elem<DT>::T* __restrict__ row, int64_t first, int count,
                                        int64_t len) {
+    (void)count;
+    const RowBuf<DT, false> rb(row, len);
+    const int f = int(first);  // first >= -(2 * kConvMaxK); rows are < 2^31 elements
 #pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int i = int(threadIdx.x) + it * kConvThreads;
-      const int64_t n = first + i;
-      const bool ok = i < count && n >= 0 && n < len;
-      const float a = Elem<DT>::load(row, ok ? n : 0);
-      v[it] = ok ? a : 0.f;
-    }
+    for (int it = 0; it < IT; ++it) v[it] = rb.elem_halo(f + int(threadIdx.x) + it * kConvThreads);
   }
   __device__ __forceinline__ void store(float* dst, int count) const {
 #pragma unroll
@@ -100,18 +99,27 @@ __device__ __forceinline__ void stage_weights(float* wl, const float* __restrict
 // register window.  wl: weights staged by stage_weights (all lanes read the
 // same LDS words: broadcast, and no per-tap branch or scalar-load wait).  xs
 // must hold base + K + 7 valid entries (the caller's tile has kConvPer slack).
+// xs, wl and base are 16-byte aligned (base a multiple of kConvPer), and the
+// window / weight refills are explicit 16-byte LDS reads: as pairs of 4-byte
+// reads at the 32-byte lane stride of `base` they conflicted on the banks.
 __device__ __forceinline__ void slide_fma(float (&acc)[kConvPer], const float* xs, int base, int K,
                                           const float* wl) {
+  static_assert(kConvPer == 8, "slide_fma: two 16-byte refills per step");
   float win[2 * kConvPer];
-#pragma unroll
-  for (int e = 0; e < kConvPer; ++e) win[e] = xs[base + e];
+  {
+    const float4 a = *reinterpret_cast<const float4*>(xs + base);
+    const float4 b = *reinterpret_cast<const float4*>(xs + base + 4);
+    win[0] = a.x; win[1] = a.y; win[2] = a.z; win[3] = a.w;
+    win[4] = b.x; win[5] = b.y; win[6] = b.z; win[7] = b.w;
+  }
   for (int jb = 0; jb < K; jb += kConvPer) {
-    float w[kConvPer];
-#pragma unroll
-    for (int e = 0; e < kConvPer; ++e) {
-      win[kConvPer + e] = xs[base + jb + kConvPer + e];
-      w[e] = wl[jb + e];
-    }
+    const float4 a = *reinterpret_cast<const float4*>(xs + base + jb + kConvPer);
+    const float4 b = *reinterpret_cast<const float4*>(xs + base + jb + kConvPer + 4);
+    const float4 wa = *reinterpret_cast<const float4*>(wl + jb);
+    const float4 wb = *reinterpret_cast<const float4*>(wl + jb + 4);
+    win[8] = a.x; win[9] = a.y; win[10] = a.z; win[11] = a.w;
+    win[12] = b.x; win[13] = b.y; win[14] = b.z; win[15] = b.w;
+    const float w[kConvPer] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
     for (int jj = 0; jj < kConvPer; ++jj) {
 #pragma unroll
@@ -187,8 +195,8 @@ __global__ __launch_bounds__(kConvThreads) void cconv_gx_kernel(const typename E
                                                                  const float* __restrict__ w,
                                                                  typename Elem<DT>::T* __restrict__ gx, int C, int L,
                                                                  int K) {
-  __shared__ float gs[conv_tile_floats(kConvMaxK)];
-  __shared__ float wl[kConvWeightFloats];
+  __shared__ __align__(16) float gs[conv_tile_floats(kConvMaxK)];
+  __shared__ __align__(16) float wl[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
   const int64_t n0 = int64_t(blockIdx.y) * kConvTile;

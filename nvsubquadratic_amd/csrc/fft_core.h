@@ -438,7 +438,8 @@ __device__ __forceinline__ void store_pair_nb(typename Elem<DT>::T* __restrict__
 // check returns 0 for loads past the end and drops stores past it, so row
 // accesses need no branches, a run of loads stays in flight together, and the
 // zero padding of a transform costs no memory traffic.  Offsets are 32-bit
-// byte offsets from the row start (rows here are at most 2^23 elements).
+// byte offsets from the row start (rows here are below 2^28 elements); every
+// offset is non-negative (see elem_halo for positions before the row).
 // ALIGNED: see load_pair_nb; a pair at an even index is then one access.
 template <int DT, bool ALIGNED>
 struct RowBuf {
@@ -449,6 +450,23 @@ struct RowBuf {
                                             0x00020000)) {}
   __device__ __forceinline__ float elem(int64_t i) const {
     const int off = int(i) * int(sizeof(ET));
+    if constexpr (DT == NSQ_DTYPE_F32) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    } else if constexpr (DT == NSQ_DTYPE_BF16) {
+      return bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    } else {
+      return __half2float(__builtin_bit_cast(__half, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+    }
+  }
+  // Element at a position that may be negative (a halo before the row start),
+  // zero there.  A negative byte offset is not safe on its own: the compiler
+  // may fold a constant of the index into the instruction's immediate offset,
+  // and the 32-bit sum can wrap back into range.  Positions before 0 therefore
+  // use offset 2^31, which no immediate brings into range, and the offset is
+  // hidden from further folding.
+  __device__ __forceinline__ float elem_halo(int n) const {
+    int off = n < 0 ? int(0x80000000u) : n * int(sizeof(ET));
+    asm volatile("" : "+v"(off));
     if constexpr (DT == NSQ_DTYPE_F32) {
       return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
     } else if constexpr (DT == NSQ_DTYPE_BF16) {

@@ -77,6 +77,51 @@ def test_batch_and_tile_independence_bitwise():
     assert torch.equal(y[1:2], y1)
 
 
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 8, 9, 17, 33, 128, 256])
+def test_halo_before_row_start_reads_zero(K):
+    """Outputs whose window reaches before position 0 see only the zero padding.
+
+    Rows are staged through raw buffers; positions before the row start must read
+    as zero however the compiler splits the element offset (a negative offset plus
+    a folded immediate can wrap back into range).
+    """
+    torch.manual_seed(11)
+    B, C, L = 3, 5, 300
+    x = torch.randn(B, C, L, requires_grad=True)
+    w = torch.randn(C, K, requires_grad=True)
+    y_ref = causal_conv1d_torch(x, w, None)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, wg = x.detach().cuda().requires_grad_(True), w.detach().cuda().requires_grad_(True)
+    y = causal_conv1d(xg, wg)
+    y.backward(g.cuda())
+    assert rel_l2(y_ref[..., :K], y[..., :K]) < 1e-5
+    assert rel_l2(y_ref, y) < 1e-5
+    assert rel_l2(x.grad, xg.grad) < 1e-5
+    assert rel_l2(w.grad, wg.grad) < 1e-5
+
+
+@pytest.mark.parametrize("Kp,Km", [(2, 3), (4, 4), (5, 7), (8, 1), (1, 9), (7, 33)])
+def test_b2b_halo_before_row_start_reads_zero(Kp, Km):
+    """B2B forward and backward near the row start for several halo widths."""
+    torch.manual_seed(12)
+    B, C, L = 2, 3, 200
+    x = torch.randn(B, 3 * C, L, requires_grad=True)
+    wp = torch.randn(3 * C, Kp, requires_grad=True)
+    wm = torch.randn(C, Km, requires_grad=True)
+    sk = torch.randn(C, requires_grad=True)
+    y_ref = b2b_causal_conv1d_torch(x, wp, wm, sk)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    args = [t.detach().cuda().requires_grad_(True) for t in (x, wp, wm, sk)]
+    y = b2b_causal_conv1d(*args)
+    y.backward(g.cuda())
+    assert rel_l2(y_ref, y) < 1e-4
+    assert rel_l2(x.grad[..., :Kp + Km], args[0].grad[..., :Kp + Km]) < 1e-4
+    for ref, got in zip((x, wp, wm, sk), args):
+        assert rel_l2(ref.grad, got.grad) < 1e-4
+
+
 # --------------------------------------------------------------------------- B2B
 @pytest.mark.parametrize("B,C,L,Kp,Km", [(2, 16, 64, 3, 3), (4, 32, 128, 4, 4), (2, 16, 128, 8, 8),
                                          (1, 8, 3000, 3, 128), (2, 4, 257, 5, 256)])
