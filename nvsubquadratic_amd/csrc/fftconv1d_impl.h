@@ -419,28 +419,55 @@ struct RowCfg {
   static constexpr int SLOTS = 8;  // N2 slots per workgroup / T threads
 };
 
-// Slot s in [0, N2) of row-pair q -> LDS positions (tile-relative) of the two
-// bins, the bin index kA = k of the first (for the twiddle W_F^k), and the
-// special slot flag (bins 0/N and N/2).
+// Spectral slots of the row-pair tile.  Slot s = t + i*T (thread t, i <
+// SLOTS) pairs two bins of the real spectrum:
+//  * q > 0: element s of tile row 0 (row q) with element N2-1-s of tile row 1
+//    (row N1-q);
+//  * q == 0, i < SLOTS/2: row 0 with itself, s <-> N2-s (slot 0 holds bins 0,
+//    N and N/2);
+//  * q == 0, i >= SLOTS/2: tile row 1 (k1 = N1/2) with itself, s2 <-> N2-1-s2,
+//    s2 = s - N2/2.
+// The unpack root of the slot is W_2N^{k1 + N1 s2}.  Since T is a multiple of
+// 16, pad16(x + c) = pad16(x) + pad16(c) for c a multiple of 16 and
+// pad16(c - x) = pad16(c) - pad16(x) for c = 15 mod 16, so each LDS position
+// is a per-thread base plus a compile-time offset plus a per-workgroup
+// constant; and the root factors as a per-workgroup root W_2N^{k1} (times i
+// on the second q == 0 half) times the table root W_{2 N2}^s.  (All formulas
+// were checked against the direct index arithmetic for every slot of N1 in
+// [2^7, 2^10], N2 in [2^7, 2^12].)
 template <int LOGN1, int LOGN2>
-__device__ __forceinline__ void row_slot(int q, int s, int& posA, int& posB, uint32_t& kA, bool& s0) {
-  constexpr int N1 = 1 << LOGN1, N2 = 1 << LOGN2;
-  constexpr int N2P = Padded<N2>::SIZE;
-  // q > 0: (row q, s) <-> (row N1-q, N2-1-s); q == 0: row 0 pairs (s, N2-s)
-  // for s < N2/2 (s == 0 pairs bin 0 with bin N/2 at s = N2/2), and the
-  // second tile row (k1 = N1/2) pairs (s2, N2-1-s2) with s2 = s - N2/2.
-  const bool second = (q == 0) && (s >= N2 / 2);
-  const int s2 = second ? s - N2 / 2 : s;
-  s0 = (q == 0) && (s == 0);
-  const int eA = s2;                                                        // element of row A
-  const int eB = (q == 0 && !second) ? (s0 ? N2 / 2 : N2 - s) : (N2 - 1 - s2);
-  const bool rowA1 = second;                                                // tile row of A
-  const bool rowB1 = (q != 0) || second;                                    // tile row of B
-  posA = (rowA1 ? N2P : 0) + pad16(eA);
-  posB = (rowB1 ? N2P : 0) + pad16(eB);
-  const uint32_t k1A = second ? uint32_t(N1 / 2) : uint32_t(q);
-  kA = k1A + uint32_t(N1) * uint32_t(s2);
-}
+struct RowSlots {
+  using C = RowCfg<LOGN2>;
+  static constexpr int N1 = 1 << LOGN1, N2 = 1 << LOGN2, N2P = C::N2P, T = C::T;
+  static_assert(T % 16 == 0 && 2 * N2 <= (1 << 14), "RowSlots: tile shape");
+  TwTable tt;
+  int t;
+  bool qz;     // q == 0
+  int base;    // pad16(t)
+  int corr;    // q == 0 first half: pad16(N2 - s) = pad16(N2 - 1) - pad16(s) + 1 + (s % 16 == 0)
+  float2 u0;   // W_2N^q (q > 0), 1 (q == 0)
+  float2 u1;   // W_2N^{N1/2} * i (q == 0, second half)
+  __device__ __forceinline__ RowSlots(int q, const float2* __restrict__ tw) : tt(tw) {
+    constexpr int LOGN = LOGN1 + LOGN2;
+    t = opaque_tid();
+    qz = (q == 0);
+    base = pad16(t);
+    corr = (t & 15) == 0 ? 1 : 0;
+    u0 = qz ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, uint32_t(q));
+    u1 = mul_i(root<LOGN + 1>(tw, uint32_t(N1 / 2)));
+  }
+  __device__ __forceinline__ bool s0(int i) const { return qz && i == 0 && t == 0; }
+  __device__ __forceinline__ void at(int i, int& pa, int& pb, float2& w) const {
+    const bool sec = qz && (i >= C::SLOTS / 2);
+    const bool f0 = qz && (i < C::SLOTS / 2);
+    const int oi = pad16(i * T);
+    pa = base + oi + (sec ? N2P - pad16(N2 / 2) : 0);
+    const int ub = !qz ? N2P + pad16(N2 - 1) : (sec ? N2P + pad16(3 * N2 / 2 - 1) : pad16(N2 - 1) + 1);
+    pb = ub - base - oi + (f0 ? corr : 0);
+    pb = s0(i) ? pad16(N2 / 2) : pb;
+    w = cmul(sec ? u1 : u0, tt.load(2 * N2, t + i * T));
+  }
+};
 
 // Loads the two rows of the pair into a tile: tile row 0 = row q (or 0), tile
 // row 1 = row N1-q (or N1/2), then forward row DFTs; spectrum in natural order.
@@ -473,24 +500,22 @@ __device__ __forceinline__ void row_pair_ifft_store(float2* lds, float2* __restr
 }
 
 template <int LOGN1, int LOGN2>
-__device__ __forceinline__ void row_unpack(const float2* lds, int q, int s, const float2* __restrict__ tw,
-                                           float2& A, float2& Bc) {
+__device__ __forceinline__ void row_unpack(const float2* lds, const RowSlots<LOGN1, LOGN2>& rs, int i, float2& A,
+                                           float2& Bc) {
   int pa, pb;
-  uint32_t kA;
-  bool s0;
-  row_slot<LOGN1, LOGN2>(q, s, pa, pb, kA, s0);
-  real_unpack(s0, lds[pa], lds[pb], root<LOGN1 + LOGN2 + 1>(tw, kA), A, Bc);
+  float2 w;
+  rs.at(i, pa, pb, w);
+  real_unpack(rs.s0(i), lds[pa], lds[pb], w, A, Bc);
 }
 
 template <int LOGN1, int LOGN2>
-__device__ __forceinline__ void row_repack(float2* lds, int q, int s, const float2* __restrict__ tw, float2 A,
+__device__ __forceinline__ void row_repack(float2* lds, const RowSlots<LOGN1, LOGN2>& rs, int i, float2 A,
                                            float2 Bc) {
   int pa, pb;
-  uint32_t kA;
-  bool s0;
-  row_slot<LOGN1, LOGN2>(q, s, pa, pb, kA, s0);
+  float2 w;
+  rs.at(i, pa, pb, w);
   float2 zp, zq;
-  real_repack(s0, A, Bc, root<LOGN1 + LOGN2 + 1>(tw, kA), zp, zq);
+  real_repack(rs.s0(i), A, Bc, w, zp, zq);
   lds[pa] = zp;
   lds[pb] = zq;
 }
@@ -498,36 +523,38 @@ __device__ __forceinline__ void row_repack(float2* lds, int q, int s, const floa
 // Forward row kernel.  grid = H * N1/2 (block = h * N1/2 + q).  wsx rows are
 // [B*H][N] (column-transformed x), wsk [H][N] (column-transformed k); the
 // product's inverse rows go to wsy (== wsx for in-place, or a separate region
-// so that wsx and wsk survive for the backward).
+// so that wsx and wsk survive for the backward).  The slot geometry (RowSlots)
+// is rebuilt per loop so that none of it stays live across the transforms.
 template <int LOGN1, int LOGN2>
-__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(4))) void row_fwd_kernel(const float2* __restrict__ wsx,
-                                                                    const float2* __restrict__ wsk,
-                                                                    float2* __restrict__ wsy, int B, int H,
-                                                                    const float2* __restrict__ tw) {
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(4))) void row_fwd_kernel(
+    const float2* __restrict__ wsx, const float2* __restrict__ wsk, float2* __restrict__ wsy, int B, int H,
+    const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
+  using RS = RowSlots<LOGN1, LOGN2>;
   constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
   __shared__ float2 lds[C::TILE_P];
   const int q = blockIdx.x % ((1 << LOGN1) / 2);
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 hA[C::SLOTS], hB[C::SLOTS];
   row_pair_fft<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
+  {
+    const RS rs(q, tw);
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-    row_unpack<LOGN1, LOGN2>(lds, q, opaque_tid() + i * C::T, tw, hA[i], hB[i]);
+    for (int i = 0; i < C::SLOTS; ++i) {
+      NSQ_SLOT_FENCE();
+      row_unpack(lds, rs, i, hA[i], hB[i]);
+    }
   }
   __syncthreads();
   for (int b = 0; b < B; ++b) {
-    const float2* sig = wsx + (int64_t(b) * H + h) * N;
-    row_pair_fft<LOGN1, LOGN2>(lds, sig, q, tw);
+    row_pair_fft<LOGN1, LOGN2>(lds, wsx + (int64_t(b) * H + h) * N, q, tw);
+    const RS rs(q, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-      const int s = opaque_tid() + i * C::T;
+      NSQ_SLOT_FENCE();
       float2 A, Bc;
-      row_unpack<LOGN1, LOGN2>(lds, q, s, tw, A, Bc);
-      const bool s0 = (q == 0 && s == 0);
-      row_repack<LOGN1, LOGN2>(lds, q, s, tw, slot_mul(s0, A, hA[i]), cmul(Bc, hB[i]));
+      row_unpack(lds, rs, i, A, Bc);
+      row_repack(lds, rs, i, slot_mul(rs.s0(i), A, hA[i]), cmul(Bc, hB[i]));
     }
     __syncthreads();
     row_pair_ifft_store<LOGN1, LOGN2>(lds, wsy + (int64_t(b) * H + h) * N, q, tw);
@@ -540,11 +567,11 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
 // tiles: G and X of one batch row are transformed side by side and the gk
 // correlation accumulates over the batch in registers.
 template <int LOGN1, int LOGN2>
-__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(3))) void row_bwd_kernel(float2* __restrict__ wsg,
-                                                                    const float2* __restrict__ wsx,
-                                                                    float2* __restrict__ wsk, int B, int H,
-                                                                    const float2* __restrict__ tw) {
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(3))) void row_bwd_kernel(
+    float2* __restrict__ wsg, const float2* __restrict__ wsx, float2* __restrict__ wsk, int B, int H,
+    const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
+  using RS = RowSlots<LOGN1, LOGN2>;
   constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
   __shared__ float2 ldsG[C::TILE_P];
   __shared__ float2 ldsX[C::TILE_P];
@@ -552,37 +579,42 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 hA[C::SLOTS], hB[C::SLOTS], qA[C::SLOTS], qB[C::SLOTS];
   row_pair_fft<LOGN1, LOGN2>(ldsG, wsk + int64_t(h) * N, q, tw);
+  {
+    const RS rs(q, tw);
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-    row_unpack<LOGN1, LOGN2>(ldsG, q, opaque_tid() + i * C::T, tw, hA[i], hB[i]);
-    qA[i] = qB[i] = make_float2(0.f, 0.f);
+    for (int i = 0; i < C::SLOTS; ++i) {
+      NSQ_SLOT_FENCE();
+      row_unpack(ldsG, rs, i, hA[i], hB[i]);
+      qA[i] = qB[i] = make_float2(0.f, 0.f);
+    }
   }
   __syncthreads();
   for (int b = 0; b < B; ++b) {
     float2* sigg = wsg + (int64_t(b) * H + h) * N;
-    const float2* sigx = wsx + (int64_t(b) * H + h) * N;
     row_pair_fft<LOGN1, LOGN2>(ldsG, sigg, q, tw);
-    row_pair_fft<LOGN1, LOGN2>(ldsX, sigx, q, tw);
+    row_pair_fft<LOGN1, LOGN2>(ldsX, wsx + (int64_t(b) * H + h) * N, q, tw);
+    const RS rs(q, tw);
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-      const int s = opaque_tid() + i * C::T;
-      const bool s0 = (q == 0 && s == 0);
+      NSQ_SLOT_FENCE();
+      const bool s0 = rs.s0(i);
       float2 GA, GB, XA, XB;
-      row_unpack<LOGN1, LOGN2>(ldsG, q, s, tw, GA, GB);
-      row_unpack<LOGN1, LOGN2>(ldsX, q, s, tw, XA, XB);
+      row_unpack(ldsG, rs, i, GA, GB);
+      row_unpack(ldsX, rs, i, XA, XB);
       qA[i] = cadd(qA[i], slot_mulc(s0, GA, XA));
       qB[i] = cadd(qB[i], cmulc(GB, XB));
-      row_repack<LOGN1, LOGN2>(ldsG, q, s, tw, slot_mulc(s0, GA, hA[i]), cmulc(GB, hB[i]));
+      row_repack(ldsG, rs, i, slot_mulc(s0, GA, hA[i]), cmulc(GB, hB[i]));
     }
     __syncthreads();
     row_pair_ifft_store<LOGN1, LOGN2>(ldsG, sigg, q, tw);
   }
+  {
+    const RS rs(q, tw);
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-    row_repack<LOGN1, LOGN2>(ldsX, q, opaque_tid() + i * C::T, tw, qA[i], qB[i]);
+    for (int i = 0; i < C::SLOTS; ++i) {
+      NSQ_SLOT_FENCE();
+      row_repack(ldsX, rs, i, qA[i], qB[i]);
+    }
   }
   __syncthreads();
   row_pair_ifft_store<LOGN1, LOGN2>(ldsX, wsk + int64_t(h) * N, q, tw);
@@ -598,42 +630,48 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
     float2* __restrict__ wsg, const float2* __restrict__ wsx, float2* __restrict__ wsk, int H,
     const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
+  using RS = RowSlots<LOGN1, LOGN2>;
   constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
   __shared__ float2 lds[C::TILE_P];
   const int q = blockIdx.x % ((1 << LOGN1) / 2);
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 sA[C::SLOTS], sB[C::SLOTS];  // K slots, then G slots
   row_pair_fft<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
+  {
+    const RS rs(q, tw);
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-    row_unpack<LOGN1, LOGN2>(lds, q, opaque_tid() + i * C::T, tw, sA[i], sB[i]);
+    for (int i = 0; i < C::SLOTS; ++i) {
+      NSQ_SLOT_FENCE();
+      row_unpack(lds, rs, i, sA[i], sB[i]);
+    }
   }
   __syncthreads();
   float2* sigg = wsg + int64_t(h) * N;
   row_pair_fft<LOGN1, LOGN2>(lds, sigg, q, tw);
+  {
+    const RS rs(q, tw);
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-    const int s = opaque_tid() + i * C::T;
-    const bool s0 = (q == 0 && s == 0);
-    float2 GA, GB;
-    row_unpack<LOGN1, LOGN2>(lds, q, s, tw, GA, GB);
-    row_repack<LOGN1, LOGN2>(lds, q, s, tw, slot_mulc(s0, GA, sA[i]), cmulc(GB, sB[i]));
-    sA[i] = GA;
-    sB[i] = GB;
+    for (int i = 0; i < C::SLOTS; ++i) {
+      NSQ_SLOT_FENCE();
+      float2 GA, GB;
+      row_unpack(lds, rs, i, GA, GB);
+      row_repack(lds, rs, i, slot_mulc(rs.s0(i), GA, sA[i]), cmulc(GB, sB[i]));
+      sA[i] = GA;
+      sB[i] = GB;
+    }
   }
   __syncthreads();
   row_pair_ifft_store<LOGN1, LOGN2>(lds, sigg, q, tw);
   row_pair_fft<LOGN1, LOGN2>(lds, wsx + int64_t(h) * N, q, tw);
+  {
+    const RS rs(q, tw);
 #pragma unroll
-  for (int i = 0; i < C::SLOTS; ++i) {
-    NSQ_SLOT_FENCE();
-    const int s = opaque_tid() + i * C::T;
-    const bool s0 = (q == 0 && s == 0);
-    float2 XA, XB;
-    row_unpack<LOGN1, LOGN2>(lds, q, s, tw, XA, XB);
-    row_repack<LOGN1, LOGN2>(lds, q, s, tw, slot_mulc(s0, sA[i], XA), cmulc(sB[i], XB));
+    for (int i = 0; i < C::SLOTS; ++i) {
+      NSQ_SLOT_FENCE();
+      float2 XA, XB;
+      row_unpack(lds, rs, i, XA, XB);
+      row_repack(lds, rs, i, slot_mulc(rs.s0(i), sA[i], XA), cmulc(sB[i], XB));
+    }
   }
   __syncthreads();
   row_pair_ifft_store<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
