@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 2
+#define NSQ_ABI_VERSION 3
 
 enum {
   NSQ_OK = 0,
@@ -151,6 +151,9 @@ int nsq_b2b_causal_conv1d_bwd(const void* gy, const void* x, const float* weight
  */
 size_t nsq_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
                                       int64_t kbatch, int direction);
+/* A forward given a workspace of the backward's size keeps the transformed x
+ * and the filter spectrum in it; a backward called on that untouched workspace
+ * with fwd_state = 1 reuses them (results identical to fwd_state = 0). */
 
 int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
                        int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, void* workspace,
@@ -158,7 +161,7 @@ int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortc
 
 int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
                        float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       void* workspace, size_t workspace_bytes, int fwd_state, void* stream);
 
 #ifdef __cplusplus
 }

@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class HipLibraryError(RuntimeError):
@@ -100,7 +100,7 @@ _SIGNATURES = {
     "nsq_fftconv_nd_bwd": (
         _c_int,
         [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64,
-         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_void_p, _c_size, _c_void_p],
+         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_void_p, _c_size, _c_int, _c_void_p],
     ),
 }
 

@@ -124,12 +124,19 @@ static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const 
   return col_pass<false>(p, wsk, nk, 0, 1, p.K[0], 0, p.F[0], tw, st);
 }
 
+// Workspace layout (spectrum blocks of p.spec complex64):
+//   backward: [G: BH | X: BH | Khat: NK | Q: NK]
+//   forward with `save` (a backward-sized workspace): X after the inner-axis
+//     passes and Khat at the backward's positions, the product in the G region;
+//     the backward called with fwd_state then starts from them.
+//   forward without `save`: [X (product in place): BH | Khat: NK].
 template <int DT>
-static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws,
+static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws, bool save,
                        const float2* tw, hipStream_t st) {
   const int64_t BH = p.B * p.H;
-  float2* wsx = ws;
-  float2* wsk = ws + BH * p.spec;
+  float2* wsx = save ? ws + BH * p.spec : ws;
+  float2* wsk = wsx + BH * p.spec;
+  float2* wsy = save ? ws : wsx;
   if (!filter_spectrum(p, k, wsk, tw, st)) return false;
   if (!row_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
   if (p.nd == 3 && !col_pass<false>(p, wsx, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
@@ -138,31 +145,31 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
     constexpr int LOGF = decltype(L)::value;
     using C = ColNdCfg<LOGF>;
     dim3 grid(unsigned(p.kb != 1 ? BH : p.H), unsigned(ceil_div(cg.inner_count, C::M)));
-    hipLaunchKernelGGL((nd_col_mul_kernel<LOGF>), grid, dim3(C::T), 0, st, wsx, (const float2*)wsk, cg, int(p.B),
-                       int(p.H), int(p.kb != 1), p.S[0], p.c[0], tw);
+    hipLaunchKernelGGL((nd_col_mul_kernel<LOGF>), grid, dim3(C::T), 0, st, (const float2*)wsx, wsy,
+                       (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.c[0], tw);
   });
   if (!ok) return false;
-  if (p.nd == 3 && !col_pass<true>(p, wsx, BH, 1, p.S[0], p.F[1], p.c[1], p.S[1], tw, st)) return false;
+  if (p.nd == 3 && !col_pass<true>(p, wsy, BH, 1, p.S[0], p.F[1], p.c[1], p.S[1], tw, st)) return false;
   RowInvOut o{y, x, s, nullptr, int(p.H), p.c[2], p.S[2], 0, 0, 0,
               1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2))};
-  return row_inv<DT, ND_OUT_Y>(p, wsx, BH, p.S[0], p.S[1], o, tw, st);
+  return row_inv<DT, ND_OUT_Y>(p, wsy, BH, p.S[0], p.S[1], o, tw, st);
 }
 
 template <int DT>
 static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const float* k, const void* s, void* gx,
-                       float* gk, float* gs, float2* ws, const float2* tw, hipStream_t st) {
+                       float* gk, float* gs, float2* ws, bool fwd_state, const float2* tw, hipStream_t st) {
   const int64_t BH = p.B * p.H, NK = p.kb * p.H;
   float2* wsg = ws;
   float2* wsx = wsg + BH * p.spec;
   float2* wsk = wsx + BH * p.spec;
   float2* wsq = wsk + NK * p.spec;
-  if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-  if (!row_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
-  if (!row_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
-  if (p.nd == 3) {
-    if (!col_pass<false>(p, wsg, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
-    if (!col_pass<false>(p, wsx, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
+  if (!fwd_state) {
+    if (!filter_spectrum(p, k, wsk, tw, st)) return false;
+    if (!row_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
+    if (p.nd == 3 && !col_pass<false>(p, wsx, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
   }
+  if (!row_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
+  if (p.nd == 3 && !col_pass<false>(p, wsg, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
@@ -235,11 +242,12 @@ int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortc
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
   float2* ws = (float2*)workspace;
+  const bool save = workspace_bytes >= nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, NSQ_DIR_BWD);
   bool ok;
   switch (dtype) {
-    case NSQ_DTYPE_F32: ok = run_nd_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, ws, tw, st); break;
-    case NSQ_DTYPE_BF16: ok = run_nd_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, ws, tw, st); break;
-    default: ok = run_nd_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, ws, tw, st); break;
+    case NSQ_DTYPE_F32: ok = run_nd_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, ws, save, tw, st); break;
+    case NSQ_DTYPE_BF16: ok = run_nd_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, ws, save, tw, st); break;
+    default: ok = run_nd_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, ws, save, tw, st); break;
   }
   NSQ_CHECK_ARG(ok, "fftconv_nd_fwd: no kernel instantiated for this shape");
   NSQ_CHECK_LAUNCH();
@@ -248,7 +256,7 @@ int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortc
 
 int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
                        float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
-                       void* workspace, size_t workspace_bytes, void* stream) {
+                       void* workspace, size_t workspace_bytes, int fwd_state, void* stream) {
   clear_error();
   NdPlan p;
   int rc = validate_nd(nd, g, x, k, dtype, B, H, S, K, kbatch, p);
@@ -264,9 +272,9 @@ int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, con
   float2* ws = (float2*)workspace;
   bool ok;
   switch (dtype) {
-    case NSQ_DTYPE_F32: ok = run_nd_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, ws, tw, st); break;
-    case NSQ_DTYPE_BF16: ok = run_nd_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, ws, tw, st); break;
-    default: ok = run_nd_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, ws, tw, st); break;
+    case NSQ_DTYPE_F32: ok = run_nd_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, ws, fwd_state != 0, tw, st); break;
+    case NSQ_DTYPE_BF16: ok = run_nd_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, ws, fwd_state != 0, tw, st); break;
+    default: ok = run_nd_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, ws, fwd_state != 0, tw, st); break;
   }
   NSQ_CHECK_ARG(ok, "fftconv_nd_bwd: no kernel instantiated for this shape");
   NSQ_CHECK_LAUNCH();

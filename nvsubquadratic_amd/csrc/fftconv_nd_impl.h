@@ -254,12 +254,13 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_kernel(float2* __res
   fft<LOGF, INV, C::M, C::T, C::S, true>(lds, ld, st, tw);
 }
 
-// Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0).
+// Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0),
+// read from wsx and written to wsy (the same buffer for an in-place product).
 // Shared filter (kfilm = 0): grid.x = H and the workgroup loops over the batch,
 // so its slice of Khat is read once per channel, not once per image; FiLM:
 // grid.x = B*H, one image each.  grid.y = ceil(inner_count / M).
 template <int LOGF>
-__global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(float2* __restrict__ wsx,
+__global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
                                                                         const float2* __restrict__ wsk, ColGeom cg,
                                                                         int B, int H, int kfilm, int S0, int c0,
                                                                         const float2* __restrict__ tw) {
@@ -279,7 +280,9 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(float2* _
   }
   const int nb = kfilm ? 1 : B;
   for (int bi = 0; bi < nb; ++bi) {
-    float2* base = wsx + (kfilm ? hk : int64_t(bi) * H + hk) * cg.spec;
+    const int64_t blk = (kfilm ? hk : int64_t(bi) * H + hk) * cg.spec;
+    const float2* base = wsx + blk;  // may equal out (in place): a block is read before it is written
+    float2* out = wsy + blk;
     auto ld = [&](int m, int n) -> float2 { return col_load(base, cg, j0 + m, n, S0); };
     LdsTile<C::S, false> tile{lds};
     fft<LOGF, false, C::M, C::T, C::S, true>(lds, ld, tile, tw);
@@ -293,7 +296,7 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(float2* _
     auto st = [&](int m, int k, float2 v) {
       const int e = k - c0;
       if (j0 + m >= cg.inner_count || e < 0 || e >= S0) return;
-      base[int64_t(e) * cg.axis_stride + j0 + m] = v;
+      out[int64_t(e) * cg.axis_stride + j0 + m] = v;
     };
     fft<LOGF, true, C::M, C::T, C::S, true>(lds, tile, st, tw);
   }

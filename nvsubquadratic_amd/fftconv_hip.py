@@ -137,7 +137,7 @@ class _CausalFFTConv1d(torch.autograd.Function):
     def forward(ctx, x, k, s):
         y = torch.empty_like(x)
         ws = None
-        if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, k, s)):
+        if any(ctx.needs_input_grad[:3]):  # (grad mode is off inside forward; this flag is not)
             # Backward-sized workspace: the forward keeps its transformed x and k
             # in it for the backward (like autograd keeping rfft outputs).
             B, H, L = x.shape
@@ -326,8 +326,13 @@ def fftconv_nd_fwd_raw(x, k, s, y, kbatch: int, workspace: torch.Tensor | None =
     return y
 
 
-def fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, workspace: torch.Tensor | None = None):
-    """Launch the N-d backward (gs: ``[kbatch*H]`` partials or None)."""
+def fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, workspace: torch.Tensor | None = None,
+                       fwd_state: bool = False):
+    """Launch the N-d backward (gs: ``[kbatch*H]`` partials or None).
+
+    ``fwd_state=True`` reuses the transformed x and filter spectrum that a forward
+    given a backward-sized ``workspace`` left there (untouched since).
+    """
     lib = _lib.get_lib()
     _lib.check_device(x)
     nd = x.ndim - 2
@@ -337,9 +342,10 @@ def fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, workspace: torch.Ten
     need = lib.nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, _lib.NSQ_DIR_BWD)
     if workspace is None or workspace.numel() < need:
         workspace = _workspace(x.device, need)
+        fwd_state = False
     _lib.check(lib.nsq_fftconv_nd_bwd(
         nd, g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
-        _lib.dtype_code(x.dtype), B, H, S, K, kbatch, workspace.data_ptr(), workspace.numel(),
+        _lib.dtype_code(x.dtype), B, H, S, K, kbatch, workspace.data_ptr(), workspace.numel(), int(bool(fwd_state)),
         _lib.stream_ptr(x.device)))
 
 
@@ -349,10 +355,20 @@ class _FFTConvND(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, k, s, kbatch):
         y = torch.empty_like(x)
-        fftconv_nd_fwd_raw(x, k, s, y, kbatch)
+        ws = None
+        if any(ctx.needs_input_grad[:3]):  # (grad mode is off inside forward; this flag is not)
+            # Backward-sized workspace: the forward keeps its transformed x and
+            # filter spectrum there for the backward.
+            lib = _lib.get_lib()
+            nd = x.ndim - 2
+            need = lib.nsq_fftconv_nd_workspace_bytes(nd, x.shape[0], x.shape[1], _lib.i64_array(x.shape[2:]),
+                                                      _lib.i64_array(k.shape[1:]), kbatch, _lib.NSQ_DIR_BWD)
+            ws = _workspace(x.device, need) if need else None
+        fftconv_nd_fwd_raw(x, k, s, y, kbatch, ws)
         ctx.save_for_backward(x, k, s)
         ctx.kbatch = kbatch
         ctx.has_s = s is not None
+        ctx.ws = ws
         return y
 
     @staticmethod
@@ -363,7 +379,8 @@ class _FFTConvND(torch.autograd.Function):
         gk = torch.empty_like(k)
         H = x.shape[1]
         gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
-        fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch)
+        ws, ctx.ws = ctx.ws, None  # the backward consumes the forward state
+        fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch, ws, fwd_state=ws is not None)
         gsum = gs.view(ctx.kbatch, H).sum(0).to(s.dtype) if ctx.has_s else None
         return gx, gk, gsum, None
 

@@ -126,6 +126,62 @@ def test_golden_fixtures():
         assert rel_l2(d[f"n{i}_y"], fn(x, k, s)) < 1e-5, f"case {i}"
 
 
+@pytest.mark.parametrize("xs,ks,kb", [((2, 3, 40, 24), (3, 17, 9), 1), ((2, 2, 12, 10, 14), (2, 5, 7, 6), 1),
+                                       ((2, 2, 20, 16), (2 * 2, 9, 5), 2)])
+def test_backward_reusing_forward_state_is_bitwise_equal(xs, ks, kb):
+    """A forward given a backward-sized workspace keeps x's transform and the filter
+    spectrum; the backward reusing them equals the one that recomputes them, bitwise."""
+    from nvsubquadratic_amd import _lib
+
+    torch.manual_seed(21)
+    nd = len(xs) - 2
+    x = torch.randn(*xs, device="cuda")
+    k = torch.randn(*ks, device="cuda")
+    s = torch.randn(xs[1], device="cuda")
+    g = torch.randn(*xs, device="cuda")
+    lib = _lib.get_lib()
+    S, K = _lib.i64_array(xs[2:]), _lib.i64_array(ks[1:])
+    need = lib.nsq_fftconv_nd_workspace_bytes(nd, xs[0], xs[1], S, K, kb, _lib.NSQ_DIR_BWD)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    F.fftconv_nd_fwd_raw(x, k, s, y, kb, ws)
+    outs = []
+    for state, w in ((True, ws), (False, None)):
+        gx, gk, gs = torch.empty_like(x), torch.empty_like(k), torch.empty(kb * xs[1], device="cuda")
+        F.fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kb, w, fwd_state=state)
+        outs.append((gx, gk, gs))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    y2 = torch.empty_like(x)
+    F.fftconv_nd_fwd_raw(x, k, s, y2, kb)  # minimum workspace: product in place
+    assert torch.equal(y, y2)
+
+
+def test_autograd_backward_receives_forward_state(monkeypatch):
+    """Through autograd, the forward keeps its transforms and the backward reuses them
+    (1D and ND): the backward launch is called with fwd_state=True."""
+    seen = []
+    real_1d, real_nd = F.causal_fftconv1d_bwd_raw, F.fftconv_nd_bwd_raw
+
+    def spy_1d(*a, **kw):
+        seen.append(("1d", kw.get("fwd_state")))
+        return real_1d(*a, **kw)
+
+    def spy_nd(*a, **kw):
+        seen.append(("nd", kw.get("fwd_state")))
+        return real_nd(*a, **kw)
+
+    monkeypatch.setattr(F, "causal_fftconv1d_bwd_raw", spy_1d)
+    monkeypatch.setattr(F, "fftconv_nd_bwd_raw", spy_nd)
+    x1 = torch.randn(1, 2, 20000, device="cuda", requires_grad=True)
+    k1 = torch.randn(1, 2, 20000, device="cuda", requires_grad=True)
+    F.causal_fftconv1d_bhl(x1, k1).sum().backward()
+    x2 = torch.randn(2, 3, 16, 12, device="cuda", requires_grad=True)
+    k2 = torch.randn(3, 5, 7, device="cuda", requires_grad=True)
+    F.fftconv2d_bhl(x2, k2).sum().backward()
+    assert seen == [("1d", True), ("nd", True)]
+
+
 def _radial_filter(C, size, sig_lo, sig_hi, nd, gen):
     sig = torch.empty(C).uniform_(sig_lo, sig_hi, generator=gen)
     ax = torch.arange(size).float() - size // 2
