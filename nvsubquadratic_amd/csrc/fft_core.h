@@ -175,10 +175,22 @@ struct LdsTile {
   __device__ __forceinline__ float2* at(int m, int n) const { return p + m * S + (PAD ? pad16(n) : n); }
   static constexpr int off(int d) { return PAD ? pad16(d) : d; }
 };
+// Columns of a row-major LDS matrix with padded rows of stride RS (complex):
+// transform m is column j0 + m, its element n at p[pad16(j0 + m) + n*RS].
+template <int RS>
+struct LdsCols {
+  float2* p;
+  int j0;
+  __device__ __forceinline__ float2* at(int m, int n) const { return p + pad16(j0 + m) + n * RS; }
+  static constexpr int off(int d) { return d * RS; }
+};
+
 template <class X>
 struct IsLdsTile : std::false_type {};
 template <int S, bool PAD>
 struct IsLdsTile<LdsTile<S, PAD>> : std::true_type {};
+template <int RS>
+struct IsLdsTile<LdsCols<RS>> : std::true_type {};
 
 // Twiddle-table loads through a raw buffer resource: 32-bit offsets from one
 // scalar base, so a butterfly's R-1 twiddle addresses are a multiply each.

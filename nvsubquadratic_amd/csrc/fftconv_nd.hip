@@ -114,13 +114,82 @@ static bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_v
   });
 }
 
+// Plane passes (3D, a (b, h, a0) plane fits in LDS): both inner axes in one
+// kernel.  plane_ok mirrors PlaneCfg::OK for the plan's sizes.
+static bool plane_ok(const NdPlan& p) {
+  if (p.nd != 3) return false;
+  const int logn = p.lF[2] - 1, logf1 = p.lF[1];
+  if (logn < 4 || logn > 9 || logf1 < 4 || logf1 > kNdMaxLogF) return false;
+  const int n = 1 << logn, f1 = 1 << logf1, mr = 4096 >> logn, mc = 4096 >> logf1;
+  return mr >= 1 && mr <= f1 && mc >= 1 && mc <= n && int64_t(f1) * (n + n / 16) * 8 <= 80 * 1024;
+}
+
+template <class F>
+static bool with_plane(const NdPlan& p, F&& f) {
+  bool launched = false;
+  with_log<4, 9>(p.lF[2] - 1, [&](auto LN) {
+    constexpr int LOGN = decltype(LN)::value;
+    with_log<4, kNdMaxLogF>(p.lF[1], [&](auto LF) {
+      constexpr int LOGF1 = decltype(LF)::value;
+      if constexpr (PlaneCfg<LOGN, LOGF1>::OK) {
+        f(std::integral_constant<int, LOGN>{}, std::integral_constant<int, LOGF1>{});
+        launched = true;
+      }
+    });
+  });
+  return launched;
+}
+
+// Forward inner-axis transforms of nbh blocks of [n0][n1][len] real rows.
+template <int DT>
+static bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, float2* ws,
+                      const float2* tw, hipStream_t st) {
+  if (plane_ok(p)) {
+    using ET = typename Elem<DT>::T;
+    const bool al = pairs_aligned<DT>(src, len, len);
+    return with_plane(p, [&](auto LN, auto LF) {
+      constexpr int LOGN = decltype(LN)::value, LOGF1 = decltype(LF)::value;
+      const dim3 grid(unsigned(nbh * n0));
+      if (al)
+        hipLaunchKernelGGL((nd_plane_fwd_kernel<LOGN, LOGF1, DT, true>), grid, dim3(256), 0, st, (const ET*)src, n0,
+                           n1, len, ws, p.spec, tw);
+      else
+        hipLaunchKernelGGL((nd_plane_fwd_kernel<LOGN, LOGF1, DT, false>), grid, dim3(256), 0, st, (const ET*)src, n0,
+                           n1, len, ws, p.spec, tw);
+    });
+  }
+  if (!row_fwd<DT>(p, src, nbh, n0, n1, len, ws, tw, st)) return false;
+  return p.nd != 3 || col_pass<false>(p, ws, nbh, 1, n0, n1, 0, p.F[1], tw, st);
+}
+
+// Inverse inner-axis transforms, crop (axis 1: [off1, off1 + n1out); axis 2:
+// RowInvOut) and epilogue, for nbh blocks whose axis-0 extent is n0.
+template <int DT, int MODE>
+static bool inner_inv(const NdPlan& p, float2* ws, int64_t nbh, int n0, int off1, int n1out, RowInvOut o,
+                      const float2* tw, hipStream_t st) {
+  if (plane_ok(p)) {
+    const bool has_s = MODE == ND_OUT_Y && o.s;
+    return with_plane(p, [&](auto LN, auto LF) {
+      constexpr int LOGN = decltype(LN)::value, LOGF1 = decltype(LF)::value;
+      const dim3 grid(unsigned(nbh * n0));
+      if (has_s)
+        hipLaunchKernelGGL((nd_plane_inv_kernel<LOGN, LOGF1, DT, MODE, true>), grid, dim3(256), 0, st,
+                           (const float2*)ws, p.spec, n0, off1, n1out, o, tw);
+      else
+        hipLaunchKernelGGL((nd_plane_inv_kernel<LOGN, LOGF1, DT, MODE, false>), grid, dim3(256), 0, st,
+                           (const float2*)ws, p.spec, n0, off1, n1out, o, tw);
+    });
+  }
+  if (p.nd == 3 && !col_pass<true>(p, ws, nbh, 1, n0, p.F[1], off1, n1out, tw, st)) return false;
+  return row_inv<DT, MODE>(p, ws, nbh, n0, n1out, o, tw, st);
+}
+
 static ColGeom axis0_geom(const NdPlan& p) { return ColGeom{1, 0, p.spec, int64_t(p.F[1]) * p.FH, p.F[1] * p.FH}; }
 
 // Filter spectrum: kb*H blocks of the [kb*H][K0][K1][K2] float32 kernel.
 static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {
   const int64_t nk = p.kb * p.H;
-  if (!row_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], wsk, tw, st)) return false;
-  if (p.nd == 3 && !col_pass<false>(p, wsk, nk, 1, p.K[0], p.K[1], 0, p.F[1], tw, st)) return false;
+  if (!inner_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], wsk, tw, st)) return false;
   return col_pass<false>(p, wsk, nk, 0, 1, p.K[0], 0, p.F[0], tw, st);
 }
 
@@ -138,8 +207,7 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
   float2* wsk = wsx + BH * p.spec;
   float2* wsy = save ? ws : wsx;
   if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-  if (!row_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
-  if (p.nd == 3 && !col_pass<false>(p, wsx, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
+  if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
@@ -149,10 +217,9 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
                        (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.c[0], tw);
   });
   if (!ok) return false;
-  if (p.nd == 3 && !col_pass<true>(p, wsy, BH, 1, p.S[0], p.F[1], p.c[1], p.S[1], tw, st)) return false;
   RowInvOut o{y, x, s, nullptr, int(p.H), p.c[2], p.S[2], 0, 0, 0,
               1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2))};
-  return row_inv<DT, ND_OUT_Y>(p, wsy, BH, p.S[0], p.S[1], o, tw, st);
+  return inner_inv<DT, ND_OUT_Y>(p, wsy, BH, p.S[0], p.c[1], p.S[1], o, tw, st);
 }
 
 template <int DT>
@@ -165,11 +232,9 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
   float2* wsq = wsk + NK * p.spec;
   if (!fwd_state) {
     if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-    if (!row_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
-    if (p.nd == 3 && !col_pass<false>(p, wsx, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
+    if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
   }
-  if (!row_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
-  if (p.nd == 3 && !col_pass<false>(p, wsg, BH, 1, p.S[0], p.S[1], 0, p.F[1], tw, st)) return false;
+  if (!inner_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
@@ -180,15 +245,11 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
                        (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.K[0], rp, tw);
   });
   if (!ok) return false;
-  if (p.nd == 3) {
-    if (!col_pass<true>(p, wsg, BH, 1, p.S[0], p.F[1], 0, p.S[1], tw, st)) return false;
-    if (!col_pass<true>(p, wsq, NK, 1, p.K[0], p.F[1], 0, p.K[1], tw, st)) return false;
-  }
   const float scale = 1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2));
   RowInvOut og{gx, g, s, nullptr, int(p.H), 0, p.S[2], 0, 0, 0, scale};
-  if (!row_inv<DT, ND_OUT_Y>(p, wsg, BH, p.S[0], p.S[1], og, tw, st)) return false;
+  if (!inner_inv<DT, ND_OUT_Y>(p, wsg, BH, p.S[0], 0, p.S[1], og, tw, st)) return false;
   RowInvOut ok_{gk, nullptr, nullptr, gs, int(p.H), 0, p.K[2], p.c[0], p.c[1], p.c[2], scale};
-  return row_inv<NSQ_DTYPE_F32, ND_OUT_GK>(p, wsq, NK, p.K[0], p.K[1], ok_, tw, st);
+  return inner_inv<NSQ_DTYPE_F32, ND_OUT_GK>(p, wsq, NK, p.K[0], 0, p.K[1], ok_, tw, st);
 }
 
 static int validate_nd(int nd, const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H,

@@ -193,6 +193,177 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
 }
 
 // ---------------------------------------------------------------------------
+// Plane passes (3D): the two inner axes of one (b, h, a0) plane in LDS, used
+// when a plane fits (PlaneCfg::OK).  A plane is F1 rows of a packed real-row
+// spectrum: row a1 holds V[0..N), V[p] = U[p] for 1 <= p < N and V[0] =
+// U[0] + i U[N] (the row's real DC and Nyquist bins packed in one complex).
+// Along axis 1 the packed column transforms to Z = A + i B (A, B the
+// transforms of the real columns U[0], U[N]), separated with the Hermitian
+// pairing A[k] = (Z[k] + conj Z[-k]) / 2, B[k] = (Z[k] - conj Z[-k]) / 2i.
+// The forward pass replaces nd_row_fwd + the axis-1 nd_col pass, the inverse
+// the axis-1 inverse nd_col pass + nd_row_inv: one spectrum round trip each
+// instead of two.
+// ---------------------------------------------------------------------------
+template <int LOGN, int LOGF1>
+struct PlaneCfg {
+  static constexpr int N = 1 << LOGN;          // packed row length F2 / 2
+  static constexpr int F1 = 1 << LOGF1;
+  static constexpr int FH = N + 1;
+  static constexpr int RS = Padded<N>::SIZE;   // LDS row stride
+  static constexpr int T = 256;
+  static constexpr int MR = (16 * T) >> LOGN;  // rows per row-transform tile
+  static constexpr int MC = (16 * T) >> LOGF1; // columns per column-transform tile
+  static constexpr int SLOTS = 8;              // MR * N / 2 slots per tile / T
+  static constexpr bool OK = LOGN >= 4 && LOGF1 >= 4 && MR >= 1 && MR <= F1 && MC >= 1 && MC <= N &&
+                             F1 * RS * 8 <= 80 * 1024;
+};
+
+template <int LOGN, int LOGF1, int DT, bool AL>
+__global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<DT>::T* __restrict__ src, int n0,
+                                                           int n1, int len, float2* __restrict__ ws, int64_t spec,
+                                                           const float2* __restrict__ tw) {
+  using C = PlaneCfg<LOGN, LOGF1>;
+  static_assert(C::OK, "nd_plane_fwd_kernel: plane does not fit");
+  constexpr int N = C::N, RS = C::RS;
+  __shared__ float2 P[C::F1 * RS];
+  const int64_t plane = blockIdx.x;  // bh * n0 + a0
+  const typename Elem<DT>::T* xs = src + plane * n1 * len;
+  // Axis 2: real transforms of the valid rows, unpacked in place to V.
+  for (int r0 = 0; r0 < n1; r0 += C::MR) {
+    LdsTile<RS, true> rows{P + r0 * RS};
+    auto ld = [&](int m, int n) -> float2 {
+      const int a1 = r0 + m;
+      const bool ok = a1 < n1;
+      return load_pair_nb<DT, AL>(xs + int64_t(ok ? a1 : 0) * len, 2 * int64_t(n), ok ? len : 0);
+    };
+    fft_rec<LOGN, 0, false, C::MR, C::T, false>(ld, rows, rows, rows, tw);
+#pragma unroll
+    for (int i = 0; i < C::SLOTS; ++i) {
+      const int s = opaque_tid() + i * C::T;
+      const int m = s >> (LOGN - 1), p = s & (N / 2 - 1);
+      const bool p0 = (p == 0);
+      float2* z = P + (r0 + m) * RS;
+      const int pb = pad16(p0 ? N / 2 : N - p);
+      float2 A, Bc;
+      real_unpack(p0, z[pad16(p)], z[pb], root<LOGN + 1>(tw, uint32_t(p)), A, Bc);
+      z[pad16(p)] = A;                          // p = 0: U[0] + i U[N]
+      z[pb] = p0 ? Bc : cconj(Bc);              // U[N/2] or U[N-p]
+    }
+    __syncthreads();
+  }
+  // Axis 1: complex transforms of the N packed columns; rows >= n1 are zero.
+  for (int j0 = 0; j0 < N; j0 += C::MC) {
+    LdsCols<RS> cols{P, j0};
+    auto ld = [&](int m, int n) -> float2 {
+      const bool ok = n < n1;
+      const float2 v = P[(ok ? n : 0) * RS + pad16(j0 + m)];
+      return make_float2(ok ? v.x : 0.f, ok ? v.y : 0.f);
+    };
+    fft_rec<LOGF1, 0, false, C::MC, C::T, true>(ld, cols, cols, cols, tw);
+  }
+  // Store [F1][FH]; column 0 separates into the DC (j = 0) and Nyquist (j = N) bins.
+  float2* out = ws + (plane / n0) * spec + (plane % n0) * int64_t(C::F1) * C::FH;
+  for (int e = opaque_tid(); e < C::F1 * C::FH; e += C::T) {
+    const int k1 = e / C::FH, j = e - k1 * C::FH;
+    const bool edge = (j == 0) || (j == N);
+    const float2 v = P[k1 * RS + pad16(edge ? 0 : j)];
+    const float2 zc = cconj(P[((C::F1 - k1) & (C::F1 - 1)) * RS]);
+    const float2 dc = cscale(cadd(v, zc), 0.5f);
+    const float2 ny = mul_neg_i(cscale(csub(v, zc), 0.5f));
+    out[int64_t(k1) * C::FH + j] = (j == 0) ? dc : ((j == N) ? ny : v);
+  }
+}
+
+// Inverse: plane [F1][FH] of the spectrum (after the axis-0 pass) -> inverse
+// along axis 1, rows [off1, off1 + n1out) -> inverse real transforms along
+// axis 2, crop and epilogue (RowInvOut; output rows [plane][n1out][w2]).
+template <int LOGN, int LOGF1, int DT, int MODE, bool HAS_S>
+__global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restrict__ ws, int64_t spec, int n0,
+                                                           int off1, int n1out, RowInvOut o,
+                                                           const float2* __restrict__ tw) {
+  using C = PlaneCfg<LOGN, LOGF1>;
+  static_assert(C::OK, "nd_plane_inv_kernel: plane does not fit");
+  using ET = typename Elem<DT>::T;
+  constexpr int N = C::N, RS = C::RS;
+  __shared__ float2 P[C::F1 * RS];
+  const int64_t plane = blockIdx.x;  // bh * n0 + a0
+  const int64_t bh = plane / n0;
+  const int a0 = int(plane % n0);
+  const float2* in = ws + bh * spec + int64_t(a0) * C::F1 * C::FH;
+  // Load, packing DC + i * Nyquist into column 0.
+  for (int e = opaque_tid(); e < C::F1 * N; e += C::T) {
+    const int k1 = e >> LOGN, j = e & (N - 1);
+    const float2 v = in[int64_t(k1) * C::FH + j];
+    const float2 w = in[int64_t(k1) * C::FH + (j == 0 ? N : j)];
+    P[k1 * RS + pad16(j)] = (j == 0) ? make_float2(v.x - w.y, v.y + w.x) : v;
+  }
+  __syncthreads();
+  // Axis 1 inverse; the last pass keeps rows [off1, off1 + n1out), moved to the front.
+  for (int j0 = 0; j0 < N; j0 += C::MC) {
+    LdsCols<RS> cols{P, j0};
+    auto st = [&](int m, int k, float2 v) {
+      const int r = k - off1;
+      if (r >= 0 && r < n1out) P[r * RS + pad16(j0 + m)] = v;
+    };
+    fft_rec<LOGF1, 0, true, C::MC, C::T, true>(cols, cols, cols, st, tw);
+  }
+  // Axis 2: repack each kept row and invert it; epilogue to the output rows.
+  const ET* __restrict__ aux = (const ET*)o.aux;
+  const ET* __restrict__ sh = (const ET*)o.s;
+  const int h = int(bh % o.H);
+  const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load(sh, h)) : 0.f;
+  for (int r0 = 0; r0 < n1out; r0 += C::MR) {
+#pragma unroll
+    for (int i = 0; i < C::SLOTS; ++i) {
+      const int s = opaque_tid() + i * C::T;
+      const int m = s >> (LOGN - 1), p = s & (N / 2 - 1);
+      const bool p0 = (p == 0);
+      float2* z = P + (r0 + m) * RS;
+      const int pb = pad16(p0 ? N / 2 : N - p);
+      const float2 b = z[pb];
+      float2 zp, zq;
+      real_repack(p0, z[pad16(p)], p0 ? b : cconj(b), root<LOGN + 1>(tw, uint32_t(p)), zp, zq);
+      z[pad16(p)] = zp;
+      z[pb] = zq;
+    }
+    __syncthreads();
+    LdsTile<RS, true> rows{P + r0 * RS};
+    auto st = [&](int m, int n, float2 v) {
+      const int a1 = r0 + m;
+      const bool rok = a1 < n1out;
+      const int64_t r = plane * n1out + (rok ? a1 : 0);
+      const int e0 = 2 * n - o.off2;
+      const float vv[2] = {v.x * o.scale, v.y * o.scale};
+      if constexpr (MODE == ND_OUT_Y) {
+        float a[2] = {0.f, 0.f};
+        if constexpr (HAS_S) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int e = e0 + t;
+            const bool ok = rok && e >= 0 && e < o.w2;
+            a[t] = Elem<DT>::load(aux, ok ? r * o.w2 + e : 0);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int e = e0 + t;
+          if (rok && e >= 0 && e < o.w2) Elem<DT>::store((ET*)o.out, r * o.w2 + e, epilogue<DT>(vv[t], HAS_S, sv, a[t]));
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int e = e0 + t;
+          if (!rok || e < 0 || e >= o.w2) continue;
+          ((float*)o.out)[r * o.w2 + e] = vv[t];
+          if (o.gs && e == o.ga2 && a0 == o.ga0 && a1 == o.ga1) o.gs[bh] = vv[t];
+        }
+      }
+    };
+    fft_rec<LOGN, 0, true, C::MR, C::T, false>(rows, rows, rows, st, tw);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Column passes along axis 0 or 1 (strided; TMAJOR tiles of M columns).
 // ---------------------------------------------------------------------------
 // M columns per workgroup (tile of about TARGET points), 16 points per thread.

@@ -108,6 +108,22 @@ def test_3d_fwd_bwd(xs, ks):
     _grad_check(xs, ks, F.fftconv3d_bhl)
 
 
+# Shapes whose two inner axes fit one LDS plane (plane passes): F1 * F2/2 in
+# {4096, 8192} with F1 >= 16, F2/2 >= 16; odd sizes, kernels longer than half the
+# axis, and a kernel as long as twice the axis.
+PLANE_3D = [((2, 3, 6, 100, 50), (5, 21, 27)), ((1, 2, 9, 64, 64), (4, 64, 64)), ((2, 2, 5, 33, 120), (3, 17, 9)),
+            ((1, 2, 4, 20, 200), (3, 40, 5))]
+
+
+@pytest.mark.parametrize("xs,ks", PLANE_3D)
+def test_3d_plane_passes_fwd_bwd(xs, ks):
+    _grad_check(xs, ks, F.fftconv3d_bhl)
+
+
+def test_3d_plane_passes_film():
+    _grad_check((2, 2, 6, 100, 50), (5, 21, 27), F.fftconv3d_bhl, kb=2)
+
+
 def test_3d_film_and_chunked():
     _grad_check((2, 3, 8, 8, 8), (5, 5, 5), F.fftconv3d_bhl, kb=2)
     torch.manual_seed(6)
@@ -127,7 +143,7 @@ def test_golden_fixtures():
 
 
 @pytest.mark.parametrize("xs,ks,kb", [((2, 3, 40, 24), (3, 17, 9), 1), ((2, 2, 12, 10, 14), (2, 5, 7, 6), 1),
-                                       ((2, 2, 20, 16), (2 * 2, 9, 5), 2)])
+                                       ((2, 2, 20, 16), (2 * 2, 9, 5), 2), ((2, 2, 6, 100, 50), (2, 5, 21, 27), 1)])
 def test_backward_reusing_forward_state_is_bitwise_equal(xs, ks, kb):
     """A forward given a backward-sized workspace keeps x's transform and the filter
     spectrum; the backward reusing them equals the one that recomputes them, bitwise."""
