@@ -81,8 +81,9 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
   };
   LdsTile<C::SP, true> st{lds};
   fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
+  const int tslot = opaque_tid();  // once: the asm statement would order the unrolled loads
   for (int i = 0; i < C::SLOTS; ++i) {
-    const int s = opaque_tid() + i * C::T;
+    const int s = tslot + i * C::T;
     const int m = s >> (LOGN - 1), p = s & (C::N / 2 - 1);
     const int64_t r = r0 + m;
     if (r >= rg.rows) continue;
@@ -128,9 +129,10 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
   using ET = typename Elem<DT>::T;
   __shared__ float2 lds[C::M * C::SP];
   const int64_t r0 = int64_t(blockIdx.x) * C::M;
+  const int tslot = opaque_tid();  // once: the asm statement would order the unrolled loads
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
-    const int s = opaque_tid() + i * C::T;
+    const int s = tslot + i * C::T;
     const int m = s >> (LOGN - 1), p = s & (C::N / 2 - 1);
     const int64_t r = r0 + m;
     const bool rok = r < rg.rows;
@@ -237,9 +239,10 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
       return load_pair_nb<DT, AL>(xs + int64_t(ok ? a1 : 0) * len, 2 * int64_t(n), ok ? len : 0);
     };
     fft_rec<LOGN, 0, false, C::MR, C::T, false>(ld, rows, rows, rows, tw);
+    const int tslot = opaque_tid();  // once: the asm statement would order the unrolled loads
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
-      const int s = opaque_tid() + i * C::T;
+      const int s = tslot + i * C::T;
       const int m = s >> (LOGN - 1), p = s & (N / 2 - 1);
       const bool p0 = (p == 0);
       float2* z = P + (r0 + m) * RS;
@@ -263,7 +266,9 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
   }
   // Store [F1][FH]; column 0 separates into the DC (j = 0) and Nyquist (j = N) bins.
   float2* out = ws + (plane / n0) * spec + (plane % n0) * int64_t(C::F1) * C::FH;
-  for (int e = opaque_tid(); e < C::F1 * C::FH; e += C::T) {
+  const int tst = opaque_tid();
+#pragma unroll 4
+  for (int e = tst; e < C::F1 * C::FH; e += C::T) {
     const int k1 = e / C::FH, j = e - k1 * C::FH;
     const bool edge = (j == 0) || (j == N);
     const float2 v = P[k1 * RS + pad16(edge ? 0 : j)];
@@ -290,12 +295,23 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
   const int64_t bh = plane / n0;
   const int a0 = int(plane % n0);
   const float2* in = ws + bh * spec + int64_t(a0) * C::F1 * C::FH;
-  // Load, packing DC + i * Nyquist into column 0.
-  for (int e = opaque_tid(); e < C::F1 * N; e += C::T) {
+  // Load the plane (unrolled so that the loads of a batch are in flight
+  // together), then pack DC + i * Nyquist into column 0.
+  static_assert((C::F1 * N) % (8 * C::T) == 0, "nd_plane_inv_kernel: load batches");
+  // One read of the thread index for the batched loops: opaque_tid is an asm
+  // statement, which the scheduler does not move loads across.
+  const int t = opaque_tid();
+#pragma unroll 8
+  for (int it = 0; it < C::F1 * N / C::T; ++it) {
+    const int e = t + it * C::T;
     const int k1 = e >> LOGN, j = e & (N - 1);
-    const float2 v = in[int64_t(k1) * C::FH + j];
-    const float2 w = in[int64_t(k1) * C::FH + (j == 0 ? N : j)];
-    P[k1 * RS + pad16(j)] = (j == 0) ? make_float2(v.x - w.y, v.y + w.x) : v;
+    P[k1 * RS + pad16(j)] = in[int64_t(k1) * C::FH + j];
+  }
+  __syncthreads();
+  for (int k1 = t; k1 < C::F1; k1 += C::T) {
+    const float2 w = in[int64_t(k1) * C::FH + N];
+    const float2 v = P[k1 * RS];
+    P[k1 * RS] = make_float2(v.x - w.y, v.y + w.x);
   }
   __syncthreads();
   // Axis 1 inverse; the last pass keeps rows [off1, off1 + n1out), moved to the front.
@@ -307,7 +323,9 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
     };
     fft_rec<LOGF1, 0, true, C::MC, C::T, true>(cols, cols, cols, st, tw);
   }
-  // Axis 2: repack each kept row and invert it; epilogue to the output rows.
+  // Axis 2: repack each kept row, invert it in LDS, then the epilogue reads the
+  // real samples back (u[2n], u[2n+1]) = (z[n].x, z[n].y), crops, and stores;
+  // all of a thread's shortcut loads are issued before its stores.
   const ET* __restrict__ aux = (const ET*)o.aux;
   const ET* __restrict__ sh = (const ET*)o.s;
   const int h = int(bh % o.H);
@@ -315,7 +333,7 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
   for (int r0 = 0; r0 < n1out; r0 += C::MR) {
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
-      const int s = opaque_tid() + i * C::T;
+      const int s = t + i * C::T;
       const int m = s >> (LOGN - 1), p = s & (N / 2 - 1);
       const bool p0 = (p == 0);
       float2* z = P + (r0 + m) * RS;
@@ -328,38 +346,39 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
     }
     __syncthreads();
     LdsTile<RS, true> rows{P + r0 * RS};
-    auto st = [&](int m, int n, float2 v) {
-      const int a1 = r0 + m;
-      const bool rok = a1 < n1out;
-      const int64_t r = plane * n1out + (rok ? a1 : 0);
-      const int e0 = 2 * n - o.off2;
-      const float vv[2] = {v.x * o.scale, v.y * o.scale};
-      if constexpr (MODE == ND_OUT_Y) {
-        float a[2] = {0.f, 0.f};
-        if constexpr (HAS_S) {
+    fft_rec<LOGN, 0, true, C::MR, C::T, false>(rows, rows, rows, rows, tw);
+    // Epilogue over the tile's real samples: MR rows x w2 kept samples.
+    const int nrows = (n1out - r0) < C::MR ? (n1out - r0) : C::MR;
+    for (int eb = 0; eb < C::MR * o.w2; eb += 8 * C::T) {
+      float a[8], v[8];
+      int64_t idx[8];
+      bool ok[8];
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const int e = e0 + t;
-            const bool ok = rok && e >= 0 && e < o.w2;
-            a[t] = Elem<DT>::load(aux, ok ? r * o.w2 + e : 0);
-          }
-        }
+      for (int u = 0; u < 8; ++u) {
+        const int e = eb + t + u * C::T;
+        const int m = e / o.w2, c = e - m * o.w2;
+        ok[u] = m < nrows;
+        const int sidx = c + o.off2;  // sample index in the row
+        const float2 zz = P[(r0 + (ok[u] ? m : 0)) * RS + pad16(sidx >> 1)];
+        v[u] = ((sidx & 1) ? zz.y : zz.x) * o.scale;
+        idx[u] = (plane * n1out + r0 + (ok[u] ? m : 0)) * o.w2 + c;
+        a[u] = 0.f;
+        if constexpr (HAS_S) a[u] = Elem<DT>::load(aux, ok[u] ? idx[u] : 0);
+      }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int e = e0 + t;
-          if (rok && e >= 0 && e < o.w2) Elem<DT>::store((ET*)o.out, r * o.w2 + e, epilogue<DT>(vv[t], HAS_S, sv, a[t]));
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int e = e0 + t;
-          if (!rok || e < 0 || e >= o.w2) continue;
-          ((float*)o.out)[r * o.w2 + e] = vv[t];
-          if (o.gs && e == o.ga2 && a0 == o.ga0 && a1 == o.ga1) o.gs[bh] = vv[t];
+      for (int u = 0; u < 8; ++u) {
+        if (!ok[u]) continue;
+        if constexpr (MODE == ND_OUT_Y) {
+          Elem<DT>::store((ET*)o.out, idx[u], epilogue<DT>(v[u], HAS_S, sv, a[u]));
+        } else {
+          ((float*)o.out)[idx[u]] = v[u];
+          const int e = eb + t + u * C::T;
+          const int m = e / o.w2, c = e - m * o.w2;
+          if (o.gs && c == o.ga2 && a0 == o.ga0 && r0 + m == o.ga1) o.gs[bh] = v[u];
         }
       }
-    };
-    fft_rec<LOGN, 0, true, C::MR, C::T, false>(rows, rows, rows, st, tw);
+    }
+    __syncthreads();
   }
 }
 
@@ -444,9 +463,10 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(const flo
   // frequency e / M), loaded before the first transform so its latency hides.
   constexpr int PT = C::TILE / C::T;
   float2 kv[PT];
+  const int tk = opaque_tid();
 #pragma unroll
   for (int it = 0; it < PT; ++it) {
-    const int e = opaque_tid() + it * C::T;
+    const int e = tk + it * C::T;
     kv[it] = col_load(kb, cg, j0 + e % C::M, e / C::M, C::F);
   }
   const int nb = kfilm ? 1 : B;
@@ -457,9 +477,10 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(const flo
     auto ld = [&](int m, int n) -> float2 { return col_load(base, cg, j0 + m, n, S0); };
     LdsTile<C::S, false> tile{lds};
     fft<LOGF, false, C::M, C::T, C::S, true>(lds, ld, tile, tw);
+    const int tp = opaque_tid();
 #pragma unroll
     for (int it = 0; it < PT; ++it) {
-      const int e = opaque_tid() + it * C::T;
+      const int e = tp + it * C::T;
       float2& z = lds[(e % C::M) * C::S + e / C::M];
       z = cmul(z, kv[it]);
     }
@@ -515,9 +536,10 @@ __global__ __launch_bounds__(ColNdBwdCfg<LOGF>::T) void nd_col_bwd_kernel(float2
     const float2* xb = wsx + bh * cg.spec;
     constexpr int PT = C::TILE / C::T;
     float2 kv[PT];
+    const int tk = opaque_tid();
 #pragma unroll
     for (int it = 0; it < PT; ++it) {
-      const int e = opaque_tid() + it * C::T;
+      const int e = tk + it * C::T;
       kv[it] = col_load(kb, cg, j0 + e % C::M, e / C::M, C::F);
     }
     auto ldg = [&](int m, int n) -> float2 { return col_load(gb, cg, j0 + m, n, S0); };
@@ -526,9 +548,10 @@ __global__ __launch_bounds__(ColNdBwdCfg<LOGF>::T) void nd_col_bwd_kernel(float2
     LdsTile<C::S, false> stX{ldsX};
     fft<LOGF, false, C::M, C::T, C::S, true>(ldsG, ldg, stG, tw);
     fft<LOGF, false, C::M, C::T, C::S, true>(ldsX, ldx, stX, tw);
+    const int tp = opaque_tid();
 #pragma unroll
     for (int it = 0; it < PT; ++it) {
-      const int e = opaque_tid() + it * C::T;
+      const int e = tp + it * C::T;
       const int m = e % C::M, k = e / C::M;
       const int a = m * C::S + k;
       const float2 gsh = cmul(ldsG[a], shift_ramp(rp, k, j0 + m));
