@@ -114,6 +114,203 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename El
   }
 }
 
+// The same forward with the mixer conv on the matrix cores (ToeplitzMfma, NS
+// steps, Km <= 4*NS - 15).  A workgroup walks a segment of up to kB2BSegTiles
+// consecutive tiles of one (b, c) row, so the mixer's weight band is built
+// once per segment and z is computed once per position: the Km - 1 values of
+// z before a tile are the last ones of the previous tile (the first tile of a
+// segment computes them from its staged halo).  Per tile, with a barrier
+// after each phase:
+//   1. the staged rows (registers, loaded during the previous tile) go to LDS,
+//      and the next tile's loads are issued;
+//   2. z = k*v for the tile's 2048 positions into the padded window buffer
+//      (zero at positions >= L), q into qs;
+//   3. MFMA: two interleaved 16-block M-tiles per wave; out = q*(y + skip*z)
+//      into qs;
+//   4. row stores; the last Km - 1 z values move to the window's front.
+constexpr int kB2BSegTiles = 4;
+
+template <int NS>
+struct B2BMfmaLds {
+  int q, k, v, qs, z, wq, wk, wv, wm, total, hk;
+  __host__ __device__ static int up8(int n) { return (n + 7) & ~7; }
+  __host__ __device__ B2BMfmaLds(int Kp, int Km) {
+    const int hp = Kp - 1, hz = Km - 1;
+    hk = hp + up8(hz);  // k, v rows are staged from n0 - hk (aligned window bases)
+    q = 0;
+    k = q + up8(kConvTile + hp + 2 * kConvPer);
+    v = k + up8(kConvTile + hk + 2 * kConvPer);
+    qs = v + up8(kConvTile + hk + 2 * kConvPer);
+    z = qs + kConvTile + kConvTile / 4;  // qs_pad
+    wq = z + up8(conv_pad_words(mfma_src_count<NS>()));
+    wk = wq + up8(Kp);
+    wv = wk + up8(Kp);
+    wm = wv + up8(Kp);
+    total = wm + up8(Km);
+  }
+};
+
+// Output-tile slot of position p: 16 words of pad per 64 so that the four
+// 64-word-apart lane groups of an MFMA epilogue use distinct banks; runs of 8
+// from a multiple of 8 stay contiguous.
+__device__ __forceinline__ int qs_pad(int p) { return p + 16 * (p >> 6); }
+
+// acc[e] += sum_{j<4} wl[j] xs[base + e + j] (taps >= K are zero in wl).
+__device__ __forceinline__ void slide_fma4(float (&acc)[kConvPer], const float* xs, int base, const float* wl) {
+  const float4 a = *reinterpret_cast<const float4*>(xs + base);
+  const float4 b = *reinterpret_cast<const float4*>(xs + base + 4);
+  const float4 c = *reinterpret_cast<const float4*>(xs + base + 8);
+  const float4 w = *reinterpret_cast<const float4*>(wl);
+  const float win[12] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w};
+  const float ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+    for (int e = 0; e < kConvPer; ++e) acc[e] = fmaf(ww[jj], win[e + jj], acc[e]);
+  }
+}
+
+template <bool SHORT>
+__device__ __forceinline__ void slide_proj(float (&acc)[kConvPer], const float* xs, int base, int K, const float* wl) {
+  if constexpr (SHORT) {
+    slide_fma4(acc, xs, base, wl);
+  } else {
+    slide_fma(acc, xs, base, K, wl);
+  }
+}
+
+// SHORT: projection taps Kp <= 4.
+template <int DT, int NS, bool SHORT>
+__global__ __launch_bounds__(kConvThreads) void b2b_fwd_mfma_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                                     const float* __restrict__ wp,
+                                                                     const float* __restrict__ wm,
+                                                                     const float* __restrict__ skip,
+                                                                     typename Elem<DT>::T* __restrict__ y, int C, int L,
+                                                                     int Kp, int Km) {
+  constexpr int TF = conv_tile_floats(2 * kConvMaxK);
+  extern __shared__ __align__(16) float smem[];
+  const B2BMfmaLds<NS> lay(Kp, Km);
+  float* xs_q = smem + lay.q;
+  float* xs_k = smem + lay.k;
+  float* xs_v = smem + lay.v;
+  float* qs = smem + lay.qs;
+  float* zp = smem + lay.z;
+  float* wlq = smem + lay.wq;
+  float* wlk = smem + lay.wk;
+  float* wlv = smem + lay.wv;
+  float* wlm = smem + lay.wm;
+  const int64_t row = blockIdx.x;  // b*C + c
+  const int b = int(row / C), c = int(row % C);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int t_begin = int(blockIdx.y) * kB2BSegTiles;
+  const int t_end = min(ntiles, t_begin + kB2BSegTiles);
+  const typename Elem<DT>::T* xq = x + (int64_t(b) * 3 * C + c) * L;
+  const typename Elem<DT>::T* xk = xq + int64_t(C) * L;
+  const typename Elem<DT>::T* xv = xk + int64_t(C) * L;
+  const int hz = Km - 1, hp = Kp - 1, hk = lay.hk;
+  const int t = int(threadIdx.x);
+  stage_weights<false>(wlq, wp + int64_t(c) * Kp, Kp);
+  stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
+  stage_weights<false>(wlv, wp + int64_t(2 * C + c) * Kp, Kp);
+  stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
+  // the window's tail beyond the tile's last use meets zero taps: keep it finite
+  constexpr int ZW = mfma_src_count<NS>();
+  for (int m = kConvTile + t; m < ZW; m += kConvThreads) zp[conv_pad(m)] = 0.f;
+  RowStage<DT, conv_tile_floats(kConvMaxK)> sq;
+  RowStage<DT, TF> sk, sv;
+  {
+    const int64_t n0 = int64_t(t_begin) * kConvTile;
+    sq.load(xq, n0 - hp, 0, L);
+    sk.load(xk, n0 - hk, 0, L);
+    sv.load(xv, n0 - hk, 0, L);
+  }
+  __syncthreads();  // weights staged
+  ToeplitzMfma<NS> tm;
+  tm.load_weights(wlm, Km);
+  const float sk_c = skip ? skip[c] : 0.f;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+  const int base = t * kConvPer;
+  for (int ti = t_begin; ti < t_end; ++ti) {
+    const int64_t n0 = int64_t(ti) * kConvTile;
+    // 1. staged rows to LDS, next tile's loads in flight
+    sq.store(xs_q, kConvTile + hp + 2 * kConvPer);
+    sk.store(xs_k, kConvTile + hk + 2 * kConvPer);
+    sv.store(xs_v, kConvTile + hk + 2 * kConvPer);
+    __syncthreads();
+    if (ti + 1 < t_end) {
+      sq.load(xq, n0 + kConvTile - hp, 0, L);
+      sk.load(xk, n0 + kConvTile - hk, 0, L);
+      sv.load(xv, n0 + kConvTile - hk, 0, L);
+    }
+    // 2. z at n0 + base + e -> window word hz + base + e; q -> qs
+    {
+      float ka[kConvPer], va[kConvPer], qa[kConvPer];
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) ka[e] = va[e] = qa[e] = 0.f;
+      const int bz = hk - hp + base;  // xs_k[bz + e + j] = x_k[n0 + base + e - hp + j]
+      slide_proj<SHORT>(ka, xs_k, bz, Kp, wlk);
+      slide_proj<SHORT>(va, xs_v, bz, Kp, wlv);
+      slide_proj<SHORT>(qa, xs_q, base, Kp, wlq);
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) zp[conv_pad(hz + base + e)] = (n0 + base + e < L) ? ka[e] * va[e] : 0.f;
+      float* qd = qs + qs_pad(base);
+      *reinterpret_cast<float4*>(qd) = make_float4(qa[0], qa[1], qa[2], qa[3]);
+      *reinterpret_cast<float4*>(qd + 4) = make_float4(qa[4], qa[5], qa[6], qa[7]);
+      if (ti == t_begin) {
+        // z at n0 - hz + m (m < hz): the causal zero padding before the row
+        // start, else recomputed from the staged halo
+        for (int m = t; m < hz; m += kConvThreads) {
+          const int64_t n = n0 - hz + m;
+          float kv = 0.f, vv = 0.f;
+          if (n >= 0) {
+            const int i0 = hk - hp - hz + m;  // xs_k[i0 + j] = x_k[n - hp + j]
+            for (int j = 0; j < Kp; ++j) {
+              kv = fmaf(wlk[j], xs_k[i0 + j], kv);
+              vv = fmaf(wlv[j], xs_v[i0 + j], vv);
+            }
+          }
+          zp[conv_pad(m)] = kv * vv;
+        }
+      }
+    }
+    __syncthreads();
+    // 3. MFMA tiles (wave w: M-tiles w and w + 4), epilogue into qs
+    {
+      static_assert(kMfmaTiles == 2 * kConvWaves, "b2b MFMA: two M-tiles per wave");
+      nsq_f32x4_t acc0, acc1;
+      tm.run2(zp, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int mt = wave + h * kConvWaves;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = 16 * (16 * mt + 4 * (l >> 4) + r) + (l & 15);
+          const float yv = h ? acc1[r] : acc0[r];
+          const float hv = fmaf(sk_c, zp[conv_pad(p + hz)], yv);
+          float& qv = qs[qs_pad(p)];
+          qv = qv * hv;
+        }
+      }
+    }
+    __syncthreads();
+    // 4. row stores; z of the next tile's halo to the window front
+    {
+      const float* od = qs + qs_pad(base);
+      const float4 o0 = *reinterpret_cast<const float4*>(od);
+      const float4 o1 = *reinterpret_cast<const float4*>(od + 4);
+      const float ov[kConvPer] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+      typename Elem<DT>::T* yr = y + row * L;
+#pragma unroll
+      for (int e = 0; e < kConvPer; e += 2) {
+        const int64_t n = n0 + base + e;
+        if (n < L) store_pair<DT>(yr, n, L, make_float2(ov[e], ov[e + 1]));
+      }
+      for (int m = t; m < hz; m += kConvThreads) zp[conv_pad(m)] = zp[conv_pad(kConvTile + m)];
+    }
+    // the next iteration's first barrier orders these LDS writes before its reads
+  }
+}
+
 // Backward step 1: recompute q, z, h; write gq = g*h into gp (q rows),
 // gh = g*q and z (fp32 workspaces).  grid as forward.
 template <int DT>
@@ -258,10 +455,31 @@ __global__ void copy_column_kernel(const float* __restrict__ src, int ld, int co
   if (i < n) dst[i] = src[int64_t(i) * ld + col];
 }
 
+template <int DT, int NS>
+static void launch_b2b_fwd_mfma(const void* x, const float* wp, const float* wm, const float* skip, void* y, int B,
+                                int C, int L, int Kp, int Km, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  dim3 grid(B * C, unsigned(ceil_div(ceil_div(L, kConvTile), kB2BSegTiles)));
+  const size_t lds = size_t(B2BMfmaLds<NS>(Kp, Km).total) * sizeof(float);
+  if (Kp <= 4)
+    hipLaunchKernelGGL((b2b_fwd_mfma_kernel<DT, NS, true>), grid, dim3(kConvThreads), lds, st, (const ET*)x, wp, wm,
+                       skip, (ET*)y, C, L, Kp, Km);
+  else
+    hipLaunchKernelGGL((b2b_fwd_mfma_kernel<DT, NS, false>), grid, dim3(kConvThreads), lds, st, (const ET*)x, wp, wm,
+                       skip, (ET*)y, C, L, Kp, Km);
+}
+
 template <int DT>
 static void launch_b2b_fwd(const void* x, const float* wp, const float* wm, const float* skip, void* y, int B, int C,
                            int L, int Kp, int Km, hipStream_t st) {
   using ET = typename Elem<DT>::T;
+  switch (mfma_steps_for(Km)) {  // mixer conv on the matrix cores from 16 taps up
+    case 12: return launch_b2b_fwd_mfma<DT, 12>(x, wp, wm, skip, y, B, C, L, Kp, Km, st);
+    case 20: return launch_b2b_fwd_mfma<DT, 20>(x, wp, wm, skip, y, B, C, L, Kp, Km, st);
+    case 36: return launch_b2b_fwd_mfma<DT, 36>(x, wp, wm, skip, y, B, C, L, Kp, Km, st);
+    case 68: return launch_b2b_fwd_mfma<DT, 68>(x, wp, wm, skip, y, B, C, L, Kp, Km, st);
+    default: break;
+  }
   dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
   hipLaunchKernelGGL((b2b_fwd_kernel<DT>), grid, dim3(kConvThreads), size_t(B2BLds(Kp, Km).total) * sizeof(float), st, (const ET*)x, wp, wm, skip, (ET*)y, C, L,
                      Kp, Km);

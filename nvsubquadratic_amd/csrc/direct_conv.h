@@ -50,20 +50,20 @@ constexpr int conv_tile_floats(int kmax) { return kConvTile + kmax - 1 + 2 * kCo
 template <int DT, int MAXC>
 struct RowStage {
   static constexpr int IT = (MAXC + kConvThreads - 1) / kConvThreads;
-  float v[IT];
+  uint32_t v[IT];  // raw element bits; converted to fp32 by store()
   __device__ __forceinline__ void load(const typename Elem<DT>::T* __restrict__ row, int64_t first, int count,
                                        int64_t len) {
     (void)count;
     const RowBuf<DT, false> rb(row, len);
     const int f = int(first);  // first >= -(2 * kConvMaxK); rows are < 2^31 elements
 #pragma unroll
-    for (int it = 0; it < IT; ++it) v[it] = rb.elem_halo(f + int(threadIdx.x) + it * kConvThreads);
+    for (int it = 0; it < IT; ++it) v[it] = rb.elem_halo_bits(f + int(threadIdx.x) + it * kConvThreads);
   }
   __device__ __forceinline__ void store(float* dst, int count) const {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int i = int(threadIdx.x) + it * kConvThreads;
-      if (i < count) dst[i] = v[it];
+      if (i < count) dst[i] = RowBuf<DT, false>::bits_to_f32(v[it]);
     }
   }
 };
@@ -186,6 +186,111 @@ __device__ __forceinline__ void wgrad_finish(float (&acc)[kConvPer], float bacc,
     for (int c = 0; c < NC; ++c) s += red[NC * LB * kConvPer + c];
     *gb = s;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Depthwise conv on the matrix cores: v_mfma_f32_16x16x4_f32 (fp32 products,
+// fp32 accumulation; the same arithmetic as the FMA loop up to summation
+// order).  Over a staged tile, output block a (tile outputs 16a .. 16a+15) is
+// row a of
+//     Y = Xw T,   Xw[a][t] = src[16a + t],   T[t][i] = w[t - i] (0 outside [0, K)),
+// t < 4*NS, i.e. y[16a + i] = sum_j w[j] src[16a + i + j]: a banded Toeplitz
+// GEMM whose window is 16 + K - 1 wide, so the MFMA does (4*NS) / K <= 1.125x
+// the multiply-adds of the tap loop (K = 128), at twice the VALU FMA rate.
+//
+// MFMA lane layout (wave64, 16x16x4): lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16] and receives D[4 (l / 16) + r][l % 16] in accumulator r.
+// The window column of step s and k-slot kk = l / 16 is
+//     t = 16 (s / 4) + 4 kk + (s % 4),
+// so a lane's A values of four consecutive steps are four consecutive src
+// words: one 16-byte LDS read.  T follows the same column order and lives in
+// NS registers per lane for the whole tile.
+//
+// src is laid out in LDS with a 4-word pad after every 16 words,
+// conv_pad(m) = m + 4 (m / 16): the 16 lanes of one read phase (blocks a ..
+// a+15, stride 20 words) then cover all 64 banks exactly once.
+// ---------------------------------------------------------------------------
+typedef float nsq_f32x4_t __attribute__((ext_vector_type(4)));
+
+__host__ __device__ __forceinline__ constexpr int conv_pad(int m) { return m + 4 * (m >> 4); }
+// Padded LDS words holding src[0, count).
+constexpr int conv_pad_words(int count) { return conv_pad(((count + 15) / 16) * 16); }
+
+// Steps for K taps: 4*NS >= K + 15 window columns, NS a multiple of 4.
+template <int NS>
+struct ToeplitzMfma {
+  static_assert(NS % 4 == 0 && NS >= 4, "ToeplitzMfma: NS must be a multiple of 4");
+  static constexpr int KMAX = 4 * NS - 15;  // largest tap count this NS covers
+  float b[NS];
+  // wl: the K taps in LDS (conv orientation: y[n] = sum_j wl[j] src[n + j]).
+  __device__ __forceinline__ void load_weights(const float* wl, int K) {
+    const int l = int(threadIdx.x) & 63, kk = l >> 4, i = l & 15;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int j = 16 * (s >> 2) + 4 * kk + (s & 3) - i;
+      const bool ok = j >= 0 && j < K;
+      const float v = wl[ok ? j : 0];
+      b[s] = ok ? v : 0.f;
+    }
+  }
+  // The lane's four outputs of the 16 blocks starting at block a0:
+  // out[r] = y of block a0 + 4 (l / 16) + r, position l % 16 in the block.
+  // srcp: padded src; reads src[16 a0, 16 (a0 + 16) + 4 NS - 16).
+  __device__ __forceinline__ nsq_f32x4_t run(const float* srcp, int a0) const {
+    const int l = int(threadIdx.x) & 63, kk = l >> 4, a = l & 15;
+    const float* p = srcp + 20 * (a0 + a) + 4 * kk;
+    nsq_f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NS / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(p + 20 * q);
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, b[4 * q + 0], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(v.y, b[4 * q + 1], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(v.z, b[4 * q + 2], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(v.w, b[4 * q + 3], c, 0, 0, 0);
+    }
+    return c;
+  }
+  // Two M-tiles (blocks a0.. and a1..) with their steps interleaved: two
+  // independent accumulation chains keep the matrix pipeline busy.
+  __device__ __forceinline__ void run2(const float* srcp, int a0, int a1, nsq_f32x4_t& c0, nsq_f32x4_t& c1) const {
+    const int l = int(threadIdx.x) & 63, kk = l >> 4, a = l & 15;
+    const float* p0 = srcp + 20 * (a0 + a) + 4 * kk;
+    const float* p1 = srcp + 20 * (a1 + a) + 4 * kk;
+    c0 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    c1 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NS / 4; ++q) {
+      const float4 u = *reinterpret_cast<const float4*>(p0 + 20 * q);
+      const float4 v = *reinterpret_cast<const float4*>(p1 + 20 * q);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(u.x, b[4 * q + 0], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, b[4 * q + 0], c1, 0, 0, 0);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(u.y, b[4 * q + 1], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(v.y, b[4 * q + 1], c1, 0, 0, 0);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(u.z, b[4 * q + 2], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(v.z, b[4 * q + 2], c1, 0, 0, 0);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(u.w, b[4 * q + 3], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(v.w, b[4 * q + 3], c1, 0, 0, 0);
+    }
+  }
+};
+
+// Tile geometry of the MFMA path: kConvTile outputs = kConvTile / 16 blocks,
+// in M-tiles of 16 blocks spread over the workgroup's waves.
+constexpr int kMfmaBlocks = kConvTile / 16;
+constexpr int kMfmaTiles = kMfmaBlocks / 16;
+constexpr int kConvWaves = kConvThreads / 64;
+static_assert(kMfmaTiles % kConvWaves == 0, "MFMA conv: M-tiles per wave");
+// src words read by a tile with NS steps (window of the last block).
+template <int NS>
+constexpr int mfma_src_count() { return kConvTile + 4 * NS - 16; }
+
+// Smallest supported step count for K taps (0: use the FMA path).
+inline int mfma_steps_for(int K) {
+  if (K < 16) return 0;
+  if (K <= ToeplitzMfma<12>::KMAX) return 12;
+  if (K <= ToeplitzMfma<20>::KMAX) return 20;
+  if (K <= ToeplitzMfma<36>::KMAX) return 36;
+  return 68;  // K <= 257
 }
 
 // Kernels shared by the causal conv and B2B backward passes.

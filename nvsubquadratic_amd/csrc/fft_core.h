@@ -476,15 +476,26 @@ struct RowBuf {
   // and the 32-bit sum can wrap back into range.  Positions before 0 therefore
   // use offset 2^31, which no immediate brings into range, and the offset is
   // hidden from further folding.
-  __device__ __forceinline__ float elem_halo(int n) const {
+  __device__ __forceinline__ float elem_halo(int n) const { return bits_to_f32(elem_halo_bits(n)); }
+  // The element's raw bits (zero-extended), for loaders that convert later:
+  // converting each value right after its load would hold the next load
+  // behind the previous one's completion.
+  __device__ __forceinline__ uint32_t elem_halo_bits(int n) const {
     int off = n < 0 ? int(0x80000000u) : n * int(sizeof(ET));
     asm volatile("" : "+v"(off));
     if constexpr (DT == NSQ_DTYPE_F32) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-    } else if constexpr (DT == NSQ_DTYPE_BF16) {
-      return bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+      return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
     } else {
-      return __half2float(__builtin_bit_cast(__half, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+      return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    }
+  }
+  __device__ __forceinline__ static float bits_to_f32(uint32_t b) {
+    if constexpr (DT == NSQ_DTYPE_F32) {
+      return __builtin_bit_cast(float, b);
+    } else if constexpr (DT == NSQ_DTYPE_BF16) {
+      return __uint_as_float(b << 16);
+    } else {
+      return __half2float(__builtin_bit_cast(__half, uint16_t(b)));
     }
   }
   __device__ __forceinline__ void store_elem(int64_t i, float v) const {

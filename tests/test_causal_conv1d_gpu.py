@@ -143,6 +143,33 @@ def test_b2b_forward_backward(B, C, L, Kp, Km):
         assert rel_l2(ref.grad, got.grad) < 1e-4
 
 
+@pytest.mark.parametrize("Km", [15, 16, 17, 33, 34, 65, 66, 128, 129, 130, 256])
+def test_b2b_mixer_tap_counts_across_matrix_core_plans(Km):
+    """Mixer tap counts on both sides of each matrix-core step-count boundary.
+
+    From 16 taps the mixer conv runs as a banded Toeplitz product on the matrix
+    cores with 12, 20, 36 or 68 steps (up to 33, 65, 129, 257 taps); 15 taps
+    stay on the FMA loop.  Ragged length (not a multiple of the 2048-output
+    tile), several batches, nonzero skip.
+    """
+    torch.manual_seed(100 + Km)
+    B, C, L = 3, 5, 4500
+    x = torch.randn(B, 3 * C, L, dtype=torch.float64)
+    wp = torch.randn(3 * C, 3, dtype=torch.float64) / 3 ** 0.5
+    wm = torch.randn(C, Km, dtype=torch.float64) / Km ** 0.5
+    sk = torch.randn(C, dtype=torch.float64)
+    # the B2B composition of the oracle's conv, in float64
+    p = causal_conv1d_torch(x, wp)
+    q, k, v = p[:, :C], p[:, C:2 * C], p[:, 2 * C:]
+    z = k * v
+    y_ref = q * (causal_conv1d_torch(z, wm) + sk.view(1, C, 1) * z)
+    y = b2b_causal_conv1d(*(t.float().cuda() for t in (x, wp, wm, sk))).double().cpu()
+    assert rel_l2(y_ref, y) < 1e-5
+    # the first outputs of a row and of a tile see the causal zero padding / the tile halo
+    assert rel_l2(y_ref[..., :Km + 3], y[..., :Km + 3]) < 1e-5
+    assert rel_l2(y_ref[..., 2048:2048 + Km], y[..., 2048:2048 + Km]) < 1e-5
+
+
 def test_b2b_config2_shape_bf16_sample():
     """Config 2 (B=4, L=8192, 3*4096 channels, k=3 then k=128) on a channel sample, bf16 I/O."""
     torch.manual_seed(3)
