@@ -138,10 +138,12 @@ struct B2BMfmaLds {
     const int hp = Kp - 1, hz = Km - 1;
     hk = hp + up8(hz);  // k, v rows are staged from n0 - hk (aligned window bases)
     q = 0;
-    k = q + up8(kConvTile + hp + 2 * kConvPer);
+    qs = 0;  // q values (qs_pad layout) replace the staged q row once it is consumed
+    const int qwords = kConvTile + kConvTile / 4 > kConvTile + hp + 2 * kConvPer ? kConvTile + kConvTile / 4
+                                                                                   : kConvTile + hp + 2 * kConvPer;
+    k = up8(qwords);
     v = k + up8(kConvTile + hk + 2 * kConvPer);
-    qs = v + up8(kConvTile + hk + 2 * kConvPer);
-    z = qs + kConvTile + kConvTile / 4;  // qs_pad
+    z = v + up8(kConvTile + hk + 2 * kConvPer);
     wq = z + up8(conv_pad_words(mfma_src_count<NS>()));
     wk = wq + up8(Kp);
     wv = wk + up8(Kp);
@@ -180,14 +182,24 @@ __device__ __forceinline__ void slide_proj(float (&acc)[kConvPer], const float* 
 }
 
 // SHORT: projection taps Kp <= 4.
-template <int DT, int NS, bool SHORT>
-__global__ __launch_bounds__(kConvThreads) void b2b_fwd_mfma_kernel(const typename Elem<DT>::T* __restrict__ x,
+// Staged words of the k, v rows: the tile, the mixer halo (aligned) and the
+// projection halo, plus the window read-ahead.
+template <int NS, bool SHORT>
+constexpr int b2b_kv_stage_words() {
+  return kConvTile + (SHORT ? 3 : kConvMaxK - 1) + ((4 * NS - 16 + 7) & ~7) + 2 * kConvPer;
+}
+
+// PF: the next tile's rows are loaded into registers during the current tile
+// (fewer waves fit); without it each tile loads at its start and the other
+// resident workgroups cover the latency.
+template <int DT, int NS, bool SHORT, bool PF>
+__global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF ? 3 : 4))) void b2b_fwd_mfma_kernel(const typename Elem<DT>::T* __restrict__ x,
                                                                      const float* __restrict__ wp,
                                                                      const float* __restrict__ wm,
                                                                      const float* __restrict__ skip,
                                                                      typename Elem<DT>::T* __restrict__ y, int C, int L,
                                                                      int Kp, int Km) {
-  constexpr int TF = conv_tile_floats(2 * kConvMaxK);
+  constexpr int TF = b2b_kv_stage_words<NS, SHORT>();
   extern __shared__ __align__(16) float smem[];
   const B2BMfmaLds<NS> lay(Kp, Km);
   float* xs_q = smem + lay.q;
@@ -216,9 +228,9 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_mfma_kernel(const typena
   // the window's tail beyond the tile's last use meets zero taps: keep it finite
   constexpr int ZW = mfma_src_count<NS>();
   for (int m = kConvTile + t; m < ZW; m += kConvThreads) zp[conv_pad(m)] = 0.f;
-  RowStage<DT, conv_tile_floats(kConvMaxK)> sq;
+  RowStage<DT, kConvTile + (SHORT ? 3 : kConvMaxK - 1) + 2 * kConvPer> sq;
   RowStage<DT, TF> sk, sv;
-  {
+  if constexpr (PF) {
     const int64_t n0 = int64_t(t_begin) * kConvTile;
     sq.load(xq, n0 - hp, 0, L);
     sk.load(xk, n0 - hk, 0, L);
@@ -226,18 +238,23 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_mfma_kernel(const typena
   }
   __syncthreads();  // weights staged
   ToeplitzMfma<NS> tm;
-  tm.load_weights(wlm, Km);
-  const float sk_c = skip ? skip[c] : 0.f;
+  tm.load_weights(wlm, Km, skip ? skip[c] : 0.f);  // h = conv(z) + skip*z: skip joins the last tap
+  const RowBuf<DT, false> yb(y + row * L, L);
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
   const int base = t * kConvPer;
   for (int ti = t_begin; ti < t_end; ++ti) {
     const int64_t n0 = int64_t(ti) * kConvTile;
     // 1. staged rows to LDS, next tile's loads in flight
+    if constexpr (!PF) {
+      sq.load(xq, n0 - hp, 0, L);
+      sk.load(xk, n0 - hk, 0, L);
+      sv.load(xv, n0 - hk, 0, L);
+    }
     sq.store(xs_q, kConvTile + hp + 2 * kConvPer);
     sk.store(xs_k, kConvTile + hk + 2 * kConvPer);
     sv.store(xs_v, kConvTile + hk + 2 * kConvPer);
     __syncthreads();
-    if (ti + 1 < t_end) {
+    if (PF && ti + 1 < t_end) {
       sq.load(xq, n0 + kConvTile - hp, 0, L);
       sk.load(xk, n0 + kConvTile - hk, 0, L);
       sv.load(xv, n0 + kConvTile - hk, 0, L);
@@ -253,9 +270,6 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_mfma_kernel(const typena
       slide_proj<SHORT>(qa, xs_q, base, Kp, wlq);
 #pragma unroll
       for (int e = 0; e < kConvPer; ++e) zp[conv_pad(hz + base + e)] = (n0 + base + e < L) ? ka[e] * va[e] : 0.f;
-      float* qd = qs + qs_pad(base);
-      *reinterpret_cast<float4*>(qd) = make_float4(qa[0], qa[1], qa[2], qa[3]);
-      *reinterpret_cast<float4*>(qd + 4) = make_float4(qa[4], qa[5], qa[6], qa[7]);
       if (ti == t_begin) {
         // z at n0 - hz + m (m < hz): the causal zero padding before the row
         // start, else recomputed from the staged halo
@@ -272,9 +286,15 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_mfma_kernel(const typena
           zp[conv_pad(m)] = kv * vv;
         }
       }
+      __syncthreads();  // the q stage is consumed: q takes its place
+      float* qd = qs + qs_pad(base);
+      *reinterpret_cast<float4*>(qd) = make_float4(qa[0], qa[1], qa[2], qa[3]);
+      *reinterpret_cast<float4*>(qd + 4) = make_float4(qa[4], qa[5], qa[6], qa[7]);
     }
     __syncthreads();
-    // 3. MFMA tiles (wave w: M-tiles w and w + 4), epilogue into qs
+    // 3. MFMA tiles (wave w: M-tiles w and w + 4); out = q * h stored from the
+    //    accumulator layout (16 consecutive outputs per lane group; the row
+    //    buffer's range check drops positions >= L)
     {
       static_assert(kMfmaTiles == 2 * kConvWaves, "b2b MFMA: two M-tiles per wave");
       nsq_f32x4_t acc0, acc1;
@@ -285,29 +305,237 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_mfma_kernel(const typena
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p = 16 * (16 * mt + 4 * (l >> 4) + r) + (l & 15);
-          const float yv = h ? acc1[r] : acc0[r];
-          const float hv = fmaf(sk_c, zp[conv_pad(p + hz)], yv);
-          float& qv = qs[qs_pad(p)];
-          qv = qv * hv;
+          const float hv = h ? acc1[r] : acc0[r];
+          yb.store_elem(n0 + p, qs[qs_pad(p)] * hv);
         }
       }
     }
     __syncthreads();
-    // 4. row stores; z of the next tile's halo to the window front
-    {
-      const float* od = qs + qs_pad(base);
-      const float4 o0 = *reinterpret_cast<const float4*>(od);
-      const float4 o1 = *reinterpret_cast<const float4*>(od + 4);
-      const float ov[kConvPer] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
-      typename Elem<DT>::T* yr = y + row * L;
+    // 4. z of the next tile's halo to the window front (ordered before the
+    //    next tile's reads by its first barrier)
+    for (int m = t; m < hz; m += kConvThreads) zp[conv_pad(m)] = zp[conv_pad(kConvTile + m)];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wave-specialized matrix-core forward for projection taps Kp <= 4 (the
+// striped-Hyena short conv).  A workgroup of 8 waves owns one channel c and
+// walks kB2BWsSegTiles consecutive tiles of the channel's (batch, tile)
+// sequence, g = b * ntiles + tile (one weight set for all of them):
+//   * waves 4..7 (producers) build tile u+1: each thread reads its 12-sample
+//     windows of the q, k, v rows straight from HBM (vector loads, issued a
+//     tile ahead), runs the 4-tap projection convs in registers and writes
+//     z = k*v and q to the LDS buffers of tile u+1;
+//   * waves 0..3 (consumers) run the mixer conv of tile u on the matrix cores
+//     (ToeplitzMfma, two M-tiles per wave) and store out = q * h.
+// One barrier per tile hands the double-buffered z/q over; on each SIMD a
+// producer wave's VALU work overlaps a consumer wave's MFMA chain.
+// The mixer band gets `d` leading zero taps so that its halo hz = Km - 1 + d
+// is a multiple of 4: z of a tile then starts at a 16-byte boundary of the
+// padded window buffer.
+constexpr int kB2BWsThreads = 512;
+constexpr int kB2BWsSegTiles = 8;
+
+template <int NS>
+struct B2BWsLds {
+  static constexpr int ZWORDS = (conv_pad_words(mfma_src_count<NS>()) + 7) & ~7;
+  static constexpr int QWORDS = kConvTile + kConvTile / 4;  // qs_pad layout
+  static constexpr int z0 = 0, q0 = 2 * ZWORDS, wm = 2 * ZWORDS + 2 * QWORDS;
+  static constexpr int total = wm + kConvMaxK;
+};
+
+// Samples x[n - 4 + i], i < 12, of one row as raw bits.  AL (16-bit types:
+// len % 8 == 0; fp32: len % 4 == 0; 16-byte aligned rows): n is a multiple of
+// 8 and the window is three aligned vector loads that lie wholly inside or
+// wholly outside [0, len); otherwise twelve element loads.  Positions before
+// the row read as zero (offset 2^31, see RowBuf::elem_halo).
+template <int DT, bool AL>
+struct Win12 {
+  static constexpr bool HALF = DT != NSQ_DTYPE_F32;
+  static constexpr int W = (HALF && AL) ? 6 : 12;
+  uint32_t w[W];
+  __device__ __forceinline__ void load(const RowBuf<DT, false>& rb, int n) {
+    if constexpr (AL) {
+      constexpr int ES = HALF ? 2 : 4;
+      int off_h = n < 4 ? int(0x80000000u) : (n - 4) * ES;
+      asm volatile("" : "+v"(off_h));
+      const int off_m = n * ES;
+      if constexpr (HALF) {
+        const auto h = __builtin_amdgcn_raw_buffer_load_b64(rb.r, off_h, 0, 0);
+        const auto m = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_m, 0, 0);
+        w[0] = h[0]; w[1] = h[1];
+        w[2] = m[0]; w[3] = m[1]; w[4] = m[2]; w[5] = m[3];
+      } else {
+        const auto h = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_h, 0, 0);
+        const auto m0 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_m, 0, 0);
+        const auto m1 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_m + 16, 0, 0);
 #pragma unroll
-      for (int e = 0; e < kConvPer; e += 2) {
-        const int64_t n = n0 + base + e;
-        if (n < L) store_pair<DT>(yr, n, L, make_float2(ov[e], ov[e + 1]));
+        for (int i = 0; i < 4; ++i) { w[i] = h[i]; w[4 + i] = m0[i]; w[8 + i] = m1[i]; }
       }
-      for (int m = t; m < hz; m += kConvThreads) zp[conv_pad(m)] = zp[conv_pad(kConvTile + m)];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 12; ++i) w[i] = rb.elem_halo_bits(n - 4 + i);
     }
-    // the next iteration's first barrier orders these LDS writes before its reads
+  }
+  __device__ __forceinline__ float at(int i) const {  // i is a compile-time constant after unrolling
+    if constexpr (HALF && AL) {
+      const uint32_t v = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
+      return RowBuf<DT, false>::bits_to_f32(v);
+    } else {
+      return RowBuf<DT, false>::bits_to_f32(w[i]);
+    }
+  }
+};
+
+// out[e] = sum_{j<4} w4[j] x[n + e - 3 + j], e < 8, from a window at n.
+template <int DT, bool AL>
+__device__ __forceinline__ void conv4_from_window(float (&out)[kConvPer], const Win12<DT, AL>& win, const float (&w4)[4]) {
+  float xv[12];
+#pragma unroll
+  for (int i = 0; i < 12; ++i) xv[i] = win.at(i);
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a = fmaf(w4[j], xv[e + 1 + j], a);
+    out[e] = a;
+  }
+}
+
+// Projection taps left-padded to 4: w4[j] = w[j - (4 - Kp)].
+__device__ __forceinline__ void load_taps4(float (&w4)[4], const float* __restrict__ w, int Kp) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s = j - (4 - Kp);
+    w4[j] = s >= 0 ? w[s >= 0 ? s : 0] : 0.f;
+  }
+}
+
+template <int DT, int NS, bool AL>
+__global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                                    const float* __restrict__ wp,
+                                                                    const float* __restrict__ wm,
+                                                                    const float* __restrict__ skip,
+                                                                    typename Elem<DT>::T* __restrict__ y, int B, int C,
+                                                                    int L, int Kp, int Km) {
+  using LY = B2BWsLds<NS>;
+  using ET = typename Elem<DT>::T;
+  extern __shared__ __align__(16) float smem[];
+  float* const zbuf = smem + LY::z0;  // buffer u: zbuf + u * ZWORDS
+  float* const qbuf = smem + LY::q0;  // buffer u: qbuf + u * QWORDS
+  float* const wlm = smem + LY::wm;
+  const int c = int(blockIdx.x);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int g_begin = int(blockIdx.y) * kB2BWsSegTiles;
+  const int g_end = min(B * ntiles, g_begin + kB2BWsSegTiles);
+  const int d = ((Km - 1 + 3) & ~3) + 1 - Km;  // leading zero taps of the band
+  const int hz = Km - 1 + d;
+  const int t = int(threadIdx.x);
+  const bool producer = t >= kB2BWsThreads / 2;
+  constexpr int ZW = mfma_src_count<NS>();
+  if (t < kConvThreads) stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
+  for (int m = kConvTile + hz + t; m < ZW; m += kB2BWsThreads) {
+    zbuf[conv_pad(m)] = 0.f;
+    zbuf[LY::ZWORDS + conv_pad(m)] = 0.f;
+  }
+  // q row of batch b; k and v rows follow at C*L and 2*C*L
+  auto qrow = [&](int b) -> const ET* { return x + (int64_t(b) * 3 * C + c) * L; };
+  if (producer) {
+    const int pt = t - kB2BWsThreads / 2;
+    float wq4[4], wk4[4], wv4[4];
+    load_taps4(wq4, wp + int64_t(c) * Kp, Kp);
+    load_taps4(wk4, wp + int64_t(C + c) * Kp, Kp);
+    load_taps4(wv4, wp + int64_t(2 * C + c) * Kp, Kp);
+    Win12<DT, AL> cq, ck, cv;
+    auto load_tile = [&](int g, Win12<DT, AL>& wq_, Win12<DT, AL>& wk_, Win12<DT, AL>& wv_) {
+      const int b = g / ntiles, ti = g - b * ntiles;
+      const ET* xq = qrow(b);
+      const int n = ti * kConvTile + 8 * pt;
+      wq_.load(RowBuf<DT, false>(xq, L), n);
+      wk_.load(RowBuf<DT, false>(xq + int64_t(C) * L, L), n);
+      wv_.load(RowBuf<DT, false>(xq + 2 * int64_t(C) * L, L), n);
+    };
+    load_tile(g_begin, cq, ck, cv);
+    // builds tile g into buffer nb from the windows in cq/ck/cv; the z halo is
+    // zero at a row start, recomputed from the row at the segment start, else
+    // carried over from buffer ob
+    auto produce = [&](int g, int nb, int ob) {
+      const int b = g / ntiles, ti = g - b * ntiles;
+      const int n0 = ti * kConvTile;
+      Win12<DT, AL> nq, nk, nv;
+      const bool more = g + 1 < g_end;
+      if (more) load_tile(g + 1, nq, nk, nv);
+      float* zb = zbuf + nb * LY::ZWORDS;
+      float* qb = qbuf + nb * LY::QWORDS;
+      float ka[kConvPer], va[kConvPer], qa[kConvPer];
+      conv4_from_window(ka, ck, wk4);
+      conv4_from_window(va, cv, wv4);
+      conv4_from_window(qa, cq, wq4);
+      const int n = n0 + 8 * pt;
+      float zv[kConvPer];
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) zv[e] = (n + e < L) ? ka[e] * va[e] : 0.f;
+      *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt)) = make_float4(zv[0], zv[1], zv[2], zv[3]);
+      *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt + 4)) = make_float4(zv[4], zv[5], zv[6], zv[7]);
+      float* qd = qb + qs_pad(8 * pt);
+      *reinterpret_cast<float4*>(qd) = make_float4(qa[0], qa[1], qa[2], qa[3]);
+      *reinterpret_cast<float4*>(qd + 4) = make_float4(qa[4], qa[5], qa[6], qa[7]);
+      if (ti == 0) {
+        if (pt < hz) zb[conv_pad(pt)] = 0.f;  // causal padding before the row start
+      } else if (g == g_begin) {
+        if (8 * pt < hz) {  // z at n0 - hz + m, m < hz
+          const ET* xq = qrow(b);
+          Win12<DT, false> hk, hv;
+          const int nh = n0 - hz + 8 * pt;
+          hk.load(RowBuf<DT, false>(xq + int64_t(C) * L, L), nh);
+          hv.load(RowBuf<DT, false>(xq + 2 * int64_t(C) * L, L), nh);
+          float kh[kConvPer], vh[kConvPer];
+          conv4_from_window(kh, hk, wk4);
+          conv4_from_window(vh, hv, wv4);
+#pragma unroll
+          for (int e = 0; e < kConvPer; ++e)
+            if (8 * pt + e < hz) zb[conv_pad(8 * pt + e)] = kh[e] * vh[e];
+        }
+      } else {
+        const float* zo = zbuf + ob * LY::ZWORDS;
+        if (pt < hz) zb[conv_pad(pt)] = zo[conv_pad(kConvTile + pt)];
+      }
+      if (more) {
+        cq = nq; ck = nk; cv = nv;
+      }
+    };
+    produce(g_begin, 0, 1);
+    __syncthreads();
+    for (int g = g_begin; g < g_end; ++g) {
+      const int cb = (g - g_begin) & 1;
+      if (g + 1 < g_end) produce(g + 1, cb ^ 1, cb);
+      __syncthreads();
+    }
+  } else {
+    __syncthreads();  // weights staged, first tile produced
+    ToeplitzMfma<NS> tm;
+    tm.load_weights(wlm, Km, skip ? skip[c] : 0.f, d);
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+    for (int g = g_begin; g < g_end; ++g) {
+      const int cb = (g - g_begin) & 1;
+      const int b = g / ntiles, ti = g - b * ntiles;
+      const RowBuf<DT, false> yb(y + (int64_t(b) * C + c) * L, L);
+      const float* zb = zbuf + cb * LY::ZWORDS;
+      const float* qb = qbuf + cb * LY::QWORDS;
+      nsq_f32x4_t acc0, acc1;
+      tm.run2(zb, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      const int n0 = ti * kConvTile;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int mt = wave + h * kConvWaves;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = 16 * (16 * mt + 4 * (l >> 4) + r) + (l & 15);
+          yb.store_elem(n0 + p, qb[qs_pad(p)] * (h ? acc1[r] : acc0[r]));
+        }
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -461,12 +689,23 @@ static void launch_b2b_fwd_mfma(const void* x, const float* wp, const float* wm,
   using ET = typename Elem<DT>::T;
   dim3 grid(B * C, unsigned(ceil_div(ceil_div(L, kConvTile), kB2BSegTiles)));
   const size_t lds = size_t(B2BMfmaLds<NS>(Kp, Km).total) * sizeof(float);
-  if (Kp <= 4)
-    hipLaunchKernelGGL((b2b_fwd_mfma_kernel<DT, NS, true>), grid, dim3(kConvThreads), lds, st, (const ET*)x, wp, wm,
-                       skip, (ET*)y, C, L, Kp, Km);
-  else
-    hipLaunchKernelGGL((b2b_fwd_mfma_kernel<DT, NS, false>), grid, dim3(kConvThreads), lds, st, (const ET*)x, wp, wm,
-                       skip, (ET*)y, C, L, Kp, Km);
+  if (Kp <= 4) {
+    // wave-specialized kernel; vector window loads when every row starts 16-byte aligned
+    constexpr int ES = int(sizeof(ET));
+    const bool al = L % (DT == NSQ_DTYPE_F32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    dim3 gws(C, unsigned(ceil_div(int64_t(B) * ceil_div(L, kConvTile), kB2BWsSegTiles)));
+    const size_t lws = size_t(B2BWsLds<NS>::total) * sizeof(float);
+    (void)ES;
+    if (al)
+      hipLaunchKernelGGL((b2b_fwd_ws_kernel<DT, NS, true>), gws, dim3(kB2BWsThreads), lws, st, (const ET*)x, wp, wm,
+                         skip, (ET*)y, B, C, L, Kp, Km);
+    else
+      hipLaunchKernelGGL((b2b_fwd_ws_kernel<DT, NS, false>), gws, dim3(kB2BWsThreads), lws, st, (const ET*)x, wp, wm,
+                         skip, (ET*)y, B, C, L, Kp, Km);
+  } else {
+    hipLaunchKernelGGL((b2b_fwd_mfma_kernel<DT, NS, false, true>), grid, dim3(kConvThreads), lds, st, (const ET*)x,
+                       wp, wm, skip, (ET*)y, C, L, Kp, Km);
+  }
 }
 
 template <int DT>

@@ -223,13 +223,16 @@ struct ToeplitzMfma {
   static constexpr int KMAX = 4 * NS - 15;  // largest tap count this NS covers
   float b[NS];
   // wl: the K taps in LDS (conv orientation: y[n] = sum_j wl[j] src[n + j]).
-  __device__ __forceinline__ void load_weights(const float* wl, int K) {
+  // last_add is added to tap K-1 (a skip term c * src[n + K - 1] folded into
+  // the band).
+  // shift: zero taps prepended to the band (tap j of the band is wl[j - shift]).
+  __device__ __forceinline__ void load_weights(const float* wl, int K, float last_add = 0.f, int shift = 0) {
     const int l = int(threadIdx.x) & 63, kk = l >> 4, i = l & 15;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int j = 16 * (s >> 2) + 4 * kk + (s & 3) - i;
+      const int j = 16 * (s >> 2) + 4 * kk + (s & 3) - i - shift;
       const bool ok = j >= 0 && j < K;
-      const float v = wl[ok ? j : 0];
+      const float v = wl[ok ? j : 0] + (j == K - 1 ? last_add : 0.f);
       b[s] = ok ? v : 0.f;
     }
   }
@@ -258,10 +261,16 @@ struct ToeplitzMfma {
     const float* p1 = srcp + 20 * (a1 + a) + 4 * kk;
     c0 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
     c1 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // operands of step group q+1 are read before the MFMAs of group q issue
+    float4 un = *reinterpret_cast<const float4*>(p0);
+    float4 vn = *reinterpret_cast<const float4*>(p1);
 #pragma unroll
     for (int q = 0; q < NS / 4; ++q) {
-      const float4 u = *reinterpret_cast<const float4*>(p0 + 20 * q);
-      const float4 v = *reinterpret_cast<const float4*>(p1 + 20 * q);
+      const float4 u = un, v = vn;
+      if (q + 1 < NS / 4) {
+        un = *reinterpret_cast<const float4*>(p0 + 20 * (q + 1));
+        vn = *reinterpret_cast<const float4*>(p1 + 20 * (q + 1));
+      }
       c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(u.x, b[4 * q + 0], c0, 0, 0, 0);
       c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, b[4 * q + 0], c1, 0, 0, 0);
       c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(u.y, b[4 * q + 1], c0, 0, 0, 0);
