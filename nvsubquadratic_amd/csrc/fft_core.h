@@ -185,6 +185,15 @@ struct LdsCols {
   static constexpr int off(int d) { return d * RS; }
 };
 
+// Store functors of a last pass may take a butterfly's R outputs at once,
+// run<R, NS>(m, base, v) for outputs base + r*NS (r < R) of transform m,
+// e.g. to step a twiddle from one output to the next instead of computing
+// each.  Marked by a member `static constexpr bool kRunStore = true`.
+template <class X, class = void>
+struct HasRunStore : std::false_type {};
+template <class X>
+struct HasRunStore<X, std::void_t<decltype(X::kRunStore)>> : std::true_type {};
+
 template <class X>
 struct IsLdsTile : std::false_type {};
 template <int S, bool PAD>
@@ -271,6 +280,8 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
       float2* q = st.at(m, base);
 #pragma unroll
       for (int r = 0; r < R; ++r) q[ST::off(r * NS)] = v[i][r];
+    } else if constexpr (HasRunStore<ST>::value) {
+      st.template run<R, NS>(m, base, v[i]);
     } else {
 #pragma unroll
       for (int r = 0; r < R; ++r) st(m, base + r * NS, v[i][r]);

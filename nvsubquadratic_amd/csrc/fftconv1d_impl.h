@@ -320,6 +320,29 @@ struct RealRows {
   int64_t valid;
 };
 
+// Last-pass store of col_fwd: out[k1][n2] = v * W_N^{n2 k1}.  A butterfly's
+// outputs k1 = base + r*NS share n2, so the twiddle starts at W_N^{n2 base}
+// and steps by W_N^{n2 NS}: two hardware sin/cos pairs per butterfly instead
+// of one per output (the recurrence adds at most R-1 roundings, ~1e-6).
+template <int LOGN, int N2>
+struct TwiddledColumnStore {
+  static constexpr bool kRunStore = true;
+  float2* out;
+  int c0;
+  const float2* tw;
+  template <int R, int NS>
+  __device__ __forceinline__ void run(int m, int base, const float2 (&v)[R]) const {
+    const uint32_t n2 = uint32_t(c0 + m);
+    float2 w = root<LOGN>(tw, n2 * uint32_t(base));
+    const float2 step = root<LOGN>(tw, n2 * uint32_t(NS));
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      out[int64_t(base + r * NS) * N2 + n2] = cmul(v[r], w);
+      if (r + 1 < R) w = cmul(w, step);
+    }
+  }
+};
+
 // col_fwd: A[row][k1][n2] = W_N^{n2 k1} * sum_{n1} z[N2 n1 + n2] W_{N1}^{n1 k1}.
 // grid = rows * (N2 / M), column block fastest so that the workgroups running
 // together cover whole rows of the signal and of the workspace.
@@ -335,10 +358,7 @@ __global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_fwd_kernel(RealRows<DT> 
   const RowBuf<DT, AL> in(src.p + row * src.stride, src.valid);
   float2* out = ws + row * (int64_t(1) << LOGN);
   auto ld = [&](int m, int n) -> float2 { return in.load_pair(2 * (int64_t(n) * N2 + c0 + m)); };
-  auto st = [&](int m, int k1, float2 v) {
-    const uint32_t n2 = uint32_t(c0 + m);
-    out[int64_t(k1) * N2 + n2] = cmul(v, root<LOGN>(tw, n2 * uint32_t(k1)));
-  };
+  TwiddledColumnStore<LOGN, N2> st{out, c0, tw};
   fft<LOGN1, false, C::M, C::T, C::S, true>(lds, ld, st, tw);
 }
 
@@ -482,6 +502,28 @@ __device__ __forceinline__ void row_pair_fft(float2* lds, const float2* __restri
   fft<LOGN2, false, 2, C::T, C::N2P>(lds, ld, st, tw);
 }
 
+// Last-pass store of an inverse row pair: sig[k1][n] = v * W_N^{-n k1}, k1 =
+// ra (tile row 0) or rb (tile row 1); the twiddle steps along a butterfly's
+// outputs n = base + r*NS as in TwiddledColumnStore.
+template <int LOGN, int N2>
+struct TwiddledRowStore {
+  static constexpr bool kRunStore = true;
+  float2* sig;
+  int ra, rb;
+  const float2* tw;
+  template <int R, int NS>
+  __device__ __forceinline__ void run(int m, int base, const float2 (&v)[R]) const {
+    const int k1 = (m == 0) ? ra : rb;
+    float2 w = root<LOGN>(tw, uint32_t(base) * uint32_t(k1));
+    const float2 step = root<LOGN>(tw, uint32_t(NS) * uint32_t(k1));
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      sig[int64_t(k1) * N2 + base + r * NS] = cmulc(v[r], w);
+      if (r + 1 < R) w = cmul(w, step);
+    }
+  }
+};
+
 // Inverse row DFT of the tile, twiddle W_N^{-n2 k1}, store to sig rows.
 template <int LOGN1, int LOGN2>
 __device__ __forceinline__ void row_pair_ifft_store(float2* lds, float2* __restrict__ sig, int q,
@@ -491,11 +533,7 @@ __device__ __forceinline__ void row_pair_ifft_store(float2* lds, float2* __restr
   constexpr int LOGN = LOGN1 + LOGN2;
   const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
   LdsTile<C::N2P, true> ld{lds};
-  auto st = [&](int m, int n, float2 v) {
-    const int k1 = (m == 0) ? ra : rb;
-    float2 w = root<LOGN>(tw, uint32_t(n) * uint32_t(k1));
-    sig[int64_t(k1) * C::N2 + n] = cmulc(v, w);
-  };
+  TwiddledRowStore<LOGN, C::N2> st{sig, ra, rb, tw};
   fft<LOGN2, true, 2, C::T, C::N2P>(lds, ld, st, tw);
 }
 
