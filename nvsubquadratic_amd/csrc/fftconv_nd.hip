@@ -94,6 +94,20 @@ static bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int 
   });
 }
 
+// Column blocks of a pass: full blocks of the kernel's regular width, then the
+// remainder in blocks of kNdTailTile's 4 columns at column offset jbase (a 2D
+// spectrum has FH = F2/2 + 1 columns, so one regular block would otherwise
+// run almost empty).  launch(tile, grid_y, jbase) launches one instance.
+constexpr int kNdTailTile = 1;  // ColNdCfg clamps this to 4 columns
+template <int LOGF, int TARGET, class LAUNCH>
+static void col_blocks(int inner, LAUNCH&& launch) {
+  using CM = ColNdCfg<LOGF, TARGET>;
+  using CT = ColNdCfg<LOGF, kNdTailTile>;
+  const int full = inner / CM::M, rem = inner - full * CM::M;
+  if (full) launch(std::integral_constant<int, TARGET>{}, full, 0);
+  if (rem) launch(std::integral_constant<int, kNdTailTile>{}, int(ceil_div(rem, CT::M)), full * CM::M);
+}
+
 // Column pass along axis d (0 or 1) of `nbh` blocks whose valid extent along
 // axis 0 is n_valid0 (used as the middle-row count of axis-1 passes).
 template <bool INV>
@@ -108,9 +122,11 @@ static bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_v
   const int64_t n_outer = nbh * cg.n_mid;
   return with_log<4, kNdMaxLogF>(p.lF[axis], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
-    using C = ColNdCfg<LOGF>;
-    dim3 grid(unsigned(n_outer), unsigned(ceil_div(cg.inner_count, C::M)));
-    hipLaunchKernelGGL((nd_col_kernel<LOGF, INV>), grid, dim3(C::T), 0, st, ws, cg, in_cnt, out_off, out_cnt, tw);
+    col_blocks<LOGF, 8192>(cg.inner_count, [&](auto tile, int gy, int jbase) {
+      constexpr int TGT = decltype(tile)::value;
+      hipLaunchKernelGGL((nd_col_kernel<LOGF, INV, TGT>), dim3(unsigned(n_outer), unsigned(gy)),
+                         dim3(ColNdCfg<LOGF, TGT>::T), 0, st, ws, cg, in_cnt, out_off, out_cnt, jbase, tw);
+    });
   });
 }
 
@@ -211,10 +227,12 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
   const ColGeom cg = axis0_geom(p);
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
-    using C = ColNdCfg<LOGF>;
-    dim3 grid(unsigned(p.kb != 1 ? BH : p.H), unsigned(ceil_div(cg.inner_count, C::M)));
-    hipLaunchKernelGGL((nd_col_mul_kernel<LOGF>), grid, dim3(C::T), 0, st, (const float2*)wsx, wsy,
-                       (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.c[0], tw);
+    col_blocks<LOGF, 8192>(cg.inner_count, [&](auto tile, int gy, int jbase) {
+      constexpr int TGT = decltype(tile)::value;
+      hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT>), dim3(unsigned(p.kb != 1 ? BH : p.H), unsigned(gy)),
+                         dim3(ColNdCfg<LOGF, TGT>::T), 0, st, (const float2*)wsx, wsy, (const float2*)wsk, cg,
+                         int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.c[0], jbase, tw);
+    });
   });
   if (!ok) return false;
   RowInvOut o{y, x, s, nullptr, int(p.H), p.c[2], p.S[2], 0, 0, 0,
@@ -239,10 +257,12 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
   const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
-    using C = ColNdBwdCfg<LOGF>;
-    dim3 grid(unsigned(NK), unsigned(ceil_div(cg.inner_count, C::M)));
-    hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF>), grid, dim3(C::T), 0, st, wsg, (const float2*)wsx,
-                       (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.K[0], rp, tw);
+    col_blocks<LOGF, kNdBwdTile>(cg.inner_count, [&](auto tile, int gy, int jbase) {
+      constexpr int TGT = decltype(tile)::value;
+      hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT>), dim3(unsigned(NK), unsigned(gy)),
+                         dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg, (const float2*)wsx, (const float2*)wsk, wsq, cg,
+                         int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.K[0], rp, jbase, tw);
+    });
   });
   if (!ok) return false;
   const float scale = 1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2));

@@ -128,8 +128,16 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
   using C = RowNdCfg<LOGN>;
   using ET = typename Elem<DT>::T;
   __shared__ float2 lds[C::M * C::SP];
+  __shared__ int64_t rowoff[C::M];  // spectrum row of each tile row (one index decomposition per row)
   const int64_t r0 = int64_t(blockIdx.x) * C::M;
   const int tslot = opaque_tid();  // once: the asm statement would order the unrolled loads
+  // every tile row (short rows give tiles of more rows than threads)
+  for (int m = tslot; m < C::M; m += C::T) {
+    const int64_t r = r0 + m;
+    const RowIdx q = row_index(r < rg.rows ? r : 0, rg.n0, rg.n1);
+    rowoff[m] = int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+  }
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
     const int s = tslot + i * C::T;
@@ -137,8 +145,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
     const int64_t r = r0 + m;
     const bool rok = r < rg.rows;
     const bool slot0 = (p == 0);
-    const RowIdx q = row_index(rok ? r : 0, rg.n0, rg.n1);
-    const float2* in = ws + int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+    const float2* in = ws + rowoff[m];
     const float2 u0 = in[slot0 ? 0 : p];
     const float2 u1 = in[slot0 ? C::N : C::N - p];
     const float2 u2 = in[C::N / 2];
@@ -153,45 +160,66 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
     zz[pad16(slot0 ? C::N / 2 : C::N - p)] = zq;
   }
   __syncthreads();
-  LdsTile<C::SP, true> ld{lds};
+  // Inverse in place, then a batched epilogue: the real samples of row m are
+  // (u[2n], u[2n+1]) = (z[n].x, z[n].y); a thread issues the shortcut loads of
+  // 8 outputs before their stores (in a store functor of the last pass each
+  // load would wait behind the previous stores).
+  LdsTile<C::SP, true> tile{lds};
+  fft_rec<LOGN, 0, true, C::M, C::T, false>(tile, tile, tile, tile, tw);
+  __shared__ float svs[C::M];  // shortcut value of each tile row
   const ET* __restrict__ aux = (const ET*)o.aux;
-  const ET* __restrict__ sh = (const ET*)o.s;
-  auto st = [&](int m, int n, float2 v) {
-    const int64_t r = r0 + m;
-    const bool rok = r < rg.rows;
-    const int e0 = 2 * n - o.off2;  // output index of the even sample
-    const float vv[2] = {v.x * o.scale, v.y * o.scale};
-    if constexpr (MODE == ND_OUT_Y) {
-      const int h = int((uint32_t(rok ? r : 0) / uint32_t(rg.n0 * rg.n1)) % uint32_t(o.H));
-      float sv = 0.f, a[2] = {0.f, 0.f};
-      if constexpr (HAS_S) {
-        sv = Elem<DT>::round(Elem<DT>::load(sh, h));
+  if constexpr (MODE == ND_OUT_Y && HAS_S) {
+    for (int m = tslot; m < C::M; m += C::T) {
+      const int64_t r = r0 + m;
+      const RowIdx q = row_index(r < rg.rows ? r : 0, rg.n0, rg.n1);
+      svs[m] = Elem<DT>::round(Elem<DT>::load((const ET*)o.s, q.bh % o.H));
+    }
+    __syncthreads();
+  }
+  const int nrows = (rg.rows - r0) < C::M ? int(rg.rows - r0) : C::M;
+  const int nvalid = nrows * o.w2;  // the tile's outputs are e in [0, nvalid), row-major
+  const int64_t tbase = r0 * o.w2;   // 32-bit offsets from here (M * w2 is small)
+  const ET* aux_t = aux + (HAS_S ? tbase : 0);
+  // (row, column) of output e = eb + tslot + u*T for the LDS read, stepped without division
+  int m_next = tslot / o.w2, c_next = tslot - m_next * o.w2;
+  for (int eb = 0; eb < C::M * o.w2; eb += 8 * C::T) {
+    float a[8], v[8];
+    int mm[8], cc[8];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int e = e0 + t;
-          const bool ok = rok && e >= 0 && e < o.w2;
-          a[t] = Elem<DT>::load(aux, ok ? r * o.w2 + e : 0);
-        }
+    for (int u = 0; u < 8; ++u) {
+      mm[u] = m_next;
+      cc[u] = c_next;
+      c_next += C::T;
+      while (c_next >= o.w2) {
+        c_next -= o.w2;
+        ++m_next;
       }
+    }
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int e = e0 + t;
-        if (rok && e >= 0 && e < o.w2) Elem<DT>::store((ET*)o.out, r * o.w2 + e, epilogue<DT>(vv[t], HAS_S, sv, a[t]));
-      }
-    } else {
+    for (int u = 0; u < 8; ++u) {
+      const int e = eb + tslot + u * C::T;
+      const bool ok = e < nvalid;
+      const int sidx = cc[u] + o.off2;  // sample index in the row
+      const float2 zz = lds[(ok ? mm[u] : 0) * C::SP + pad16(sidx >> 1)];
+      v[u] = ((sidx & 1) ? zz.y : zz.x) * o.scale;
+      a[u] = 0.f;
+      if constexpr (MODE == ND_OUT_Y && HAS_S) a[u] = Elem<DT>::load(aux_t, ok ? e : 0);
+    }
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int e = e0 + t;
-        if (!rok || e < 0 || e >= o.w2) continue;
-        ((float*)o.out)[r * o.w2 + e] = vv[t];
-        if (o.gs && e == o.ga2) {
-          const RowIdx q = row_index(r, rg.n0, rg.n1);
-          if (q.a0 == o.ga0 && q.a1 == o.ga1) o.gs[q.bh] = vv[t];
+    for (int u = 0; u < 8; ++u) {
+      const int e = eb + tslot + u * C::T;
+      if (e >= nvalid) continue;
+      if constexpr (MODE == ND_OUT_Y) {
+        Elem<DT>::store((ET*)o.out + tbase, e, epilogue<DT>(v[u], HAS_S, HAS_S ? svs[mm[u]] : 0.f, a[u]));
+      } else {
+        ((float*)o.out + tbase)[e] = v[u];
+        if (o.gs && cc[u] == o.ga2) {
+          const RowIdx q = row_index(r0 + mm[u], rg.n0, rg.n1);
+          if (q.a0 == o.ga0 && q.a1 == o.ga1) o.gs[q.bh] = v[u];
         }
       }
     }
-  };
-  fft<LOGN, true, C::M, C::T, C::SP>(lds, ld, st, tw);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -427,14 +455,14 @@ __device__ __forceinline__ float2 col_load(const float2* __restrict__ base, cons
 // Generic pass: reads elements [0, in_cnt) (rest zero), transforms, writes
 // outputs [out_off, out_off + out_cnt) to positions [0, out_cnt).
 // grid = (n_outer, ceil(inner_count / M)).
-template <int LOGF, bool INV>
-__global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_kernel(float2* __restrict__ ws, ColGeom cg, int in_cnt,
-                                                                    int out_off, int out_cnt,
-                                                                    const float2* __restrict__ tw) {
-  using C = ColNdCfg<LOGF>;
+template <int LOGF, bool INV, int TARGET = 8192>
+__global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_kernel(float2* __restrict__ ws, ColGeom cg,
+                                                                            int in_cnt, int out_off, int out_cnt,
+                                                                            int jbase, const float2* __restrict__ tw) {
+  using C = ColNdCfg<LOGF, TARGET>;
   __shared__ float2 lds[C::M * C::S];
   float2* base = ws + col_base(cg, blockIdx.x);
-  const int j0 = blockIdx.y * C::M;
+  const int j0 = jbase + blockIdx.y * C::M;
   auto ld = [&](int m, int n) -> float2 { return col_load(base, cg, j0 + m, n, in_cnt); };
   auto st = [&](int m, int k, float2 v) {
     const int e = k - out_off;
@@ -449,16 +477,17 @@ __global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_kernel(float2* __res
 // Shared filter (kfilm = 0): grid.x = H and the workgroup loops over the batch,
 // so its slice of Khat is read once per channel, not once per image; FiLM:
 // grid.x = B*H, one image each.  grid.y = ceil(inner_count / M).
-template <int LOGF>
-__global__ __launch_bounds__(ColNdCfg<LOGF>::T) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
-                                                                        const float2* __restrict__ wsk, ColGeom cg,
-                                                                        int B, int H, int kfilm, int S0, int c0,
-                                                                        const float2* __restrict__ tw) {
-  using C = ColNdCfg<LOGF>;
+template <int LOGF, int TARGET = 8192>
+__global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
+                                                                                const float2* __restrict__ wsk,
+                                                                                ColGeom cg, int B, int H, int kfilm,
+                                                                                int S0, int c0, int jbase,
+                                                                                const float2* __restrict__ tw) {
+  using C = ColNdCfg<LOGF, TARGET>;
   __shared__ float2 lds[C::M * C::S];
   const int64_t hk = blockIdx.x;
   const float2* kb = wsk + hk * cg.spec;
-  const int j0 = blockIdx.y * C::M;
+  const int j0 = jbase + blockIdx.y * C::M;
   // Filter spectrum of this column block (element e -> column e % M,
   // frequency e / M), loaded before the first transform so its latency hides.
   constexpr int PT = C::TILE / C::T;
@@ -514,19 +543,20 @@ __device__ __forceinline__ float2 shift_ramp(const Ramp& rp, int k0, int j) {
 // Adjoint, axis 0.  Shared kernel (kfilm = 0): grid.x = H, loops b; FiLM:
 // grid.x = B*H, one b.  Writes P (gx pre-image, window [0, S0)) into wsg and
 // Q (gk pre-image, window [0, K0)) into wsq.
-template <int LOGF>
-__global__ __launch_bounds__(ColNdBwdCfg<LOGF>::T) void nd_col_bwd_kernel(float2* __restrict__ wsg,
-                                                                        const float2* __restrict__ wsx,
-                                                                        const float2* __restrict__ wsk,
-                                                                        float2* __restrict__ wsq, ColGeom cg, int B,
-                                                                        int H, int kfilm, int S0, int K0, Ramp rp,
-                                                                        const float2* __restrict__ tw) {
-  using C = ColNdBwdCfg<LOGF>;
+template <int LOGF, int TARGET = kNdBwdTile>
+__global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel(float2* __restrict__ wsg,
+                                                                                const float2* __restrict__ wsx,
+                                                                                const float2* __restrict__ wsk,
+                                                                                float2* __restrict__ wsq, ColGeom cg,
+                                                                                int B, int H, int kfilm, int S0,
+                                                                                int K0, Ramp rp, int jbase,
+                                                                                const float2* __restrict__ tw) {
+  using C = ColNdCfg<LOGF, TARGET>;
   __shared__ float2 ldsG[C::M * C::S];
   __shared__ float2 ldsX[C::M * C::S];
   __shared__ float2 ldsQ[C::M * C::S];
   const int64_t hk = blockIdx.x;
-  const int j0 = blockIdx.y * C::M;
+  const int j0 = jbase + blockIdx.y * C::M;
   const float2* kb = wsk + hk * cg.spec;
   for (int e = threadIdx.x; e < C::TILE; e += C::T) ldsQ[(e % C::M) * C::S + e / C::M] = make_float2(0.f, 0.f);
   const int nb = kfilm ? 1 : B;
