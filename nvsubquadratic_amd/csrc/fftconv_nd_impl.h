@@ -73,7 +73,14 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
                                                                         const float2* __restrict__ tw) {
   using C = RowNdCfg<LOGN>;
   __shared__ float2 lds[C::M * C::SP];
+  __shared__ int64_t rowoff[C::M];  // spectrum row of each tile row (one index decomposition per row)
   const int64_t r0 = int64_t(blockIdx.x) * C::M;
+  const int tslot = opaque_tid();  // once: the asm statement would order the unrolled loads
+  for (int m = tslot; m < C::M; m += C::T) {  // ordered before its use by the transform's barriers
+    const int64_t r = r0 + m;
+    const RowIdx q = row_index(r < rg.rows ? r : 0, rg.n0, rg.n1);
+    rowoff[m] = int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+  }
   auto ld = [&](int m, int n) -> float2 {
     const int64_t r = r0 + m;
     const bool rok = r < rg.rows;  // tail rows read row 0 and select zero
@@ -81,7 +88,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
   };
   LdsTile<C::SP, true> st{lds};
   fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
-  const int tslot = opaque_tid();  // once: the asm statement would order the unrolled loads
+#pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
     const int s = tslot + i * C::T;
     const int m = s >> (LOGN - 1), p = s & (C::N / 2 - 1);
@@ -92,8 +99,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
     float2 A, Bc;
     real_unpack(slot0, zz[pad16(p)], zz[pad16(slot0 ? C::N / 2 : C::N - p)],
                 root<LOGN + 1>(tw, p), A, Bc);
-    const RowIdx q = row_index(r, rg.n0, rg.n1);
-    float2* out = ws + int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+    float2* out = ws + rowoff[m];
     if (slot0) {
       out[0] = make_float2(A.x, 0.f);
       out[C::N] = make_float2(A.y, 0.f);
@@ -474,18 +480,20 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_kernel(flo
 
 // Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0),
 // read from wsx and written to wsy (the same buffer for an in-place product).
-// Shared filter (kfilm = 0): grid.x = H and the workgroup loops over the batch,
-// so its slice of Khat is read once per channel, not once per image; FiLM:
-// grid.x = B*H, one image each.  grid.y = ceil(inner_count / M).
+// Shared filter (kfilm = 0): grid.x = H * bsplit and a workgroup loops over
+// its share of the batch, so its slice of Khat is read once per channel (per
+// bsplit share), not once per image; FiLM: grid.x = B*H, one image each.
+// grid.y = column blocks.
 template <int LOGF, int TARGET = 8192>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
                                                                                 const float2* __restrict__ wsk,
                                                                                 ColGeom cg, int B, int H, int kfilm,
-                                                                                int S0, int c0, int jbase,
+                                                                                int S0, int c0, int jbase, int bsplit,
                                                                                 const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
   __shared__ float2 lds[C::M * C::S];
-  const int64_t hk = blockIdx.x;
+  const int64_t hk = blockIdx.x / bsplit;  // filter (channel, or FiLM image)
+  const int part = int(blockIdx.x % bsplit);
   const float2* kb = wsk + hk * cg.spec;
   const int j0 = jbase + blockIdx.y * C::M;
   // Filter spectrum of this column block (element e -> column e % M,
@@ -499,7 +507,8 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
     kv[it] = col_load(kb, cg, j0 + e % C::M, e / C::M, C::F);
   }
   const int nb = kfilm ? 1 : B;
-  for (int bi = 0; bi < nb; ++bi) {
+  // bsplit > 1: this workgroup takes batches [part * nb / bsplit, (part + 1) * nb / bsplit)
+  for (int bi = part * nb / bsplit; bi < (part + 1) * nb / bsplit; ++bi) {
     const int64_t blk = (kfilm ? hk : int64_t(bi) * H + hk) * cg.spec;
     const float2* base = wsx + blk;  // may equal out (in place): a block is read before it is written
     float2* out = wsy + blk;
