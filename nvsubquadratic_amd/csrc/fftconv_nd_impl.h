@@ -539,15 +539,6 @@ struct Ramp {
   int FH;             // inner index j -> (k1, k2) = (j / FH, j % FH) on axis-0 passes
 };
 
-__device__ __forceinline__ float2 shift_ramp(const Ramp& rp, int k0, int j) {
-  const int k1 = j / rp.FH, k2 = j % rp.FH;
-  const uint32_t m0 = (uint32_t(rp.c0) * uint32_t(k0)) & ((1u << rp.lF0) - 1u);
-  const uint32_t m1 = (uint32_t(rp.c1) * uint32_t(k1)) & ((1u << rp.lF1) - 1u);
-  const uint32_t m2 = (uint32_t(rp.c2) * uint32_t(k2)) & ((1u << rp.lF2) - 1u);
-  float a = float(m0) / float(1u << rp.lF0) + float(m1) / float(1u << rp.lF1) + float(m2) / float(1u << rp.lF2);
-  a = a - floorf(a);
-  return make_float2(__builtin_amdgcn_cosf(a), -__builtin_amdgcn_sinf(a));
-}
 
 // Adjoint, axis 0.  Shared kernel (kfilm = 0): grid.x = H, loops b; FiLM:
 // grid.x = B*H, one b.  Writes P (gx pre-image, window [0, S0)) into wsg and
@@ -561,57 +552,73 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
                                                                                 int K0, Ramp rp, int jbase,
                                                                                 const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
+  static_assert(C::T % C::M == 0, "nd_col_bwd_kernel: a thread's elements share one column");
+  constexpr int PT = C::TILE / C::T;
   __shared__ float2 ldsG[C::M * C::S];
-  __shared__ float2 ldsX[C::M * C::S];
-  __shared__ float2 ldsQ[C::M * C::S];
+  __shared__ float2 ldsX[C::M * C::S];  // X of the current image; at the end, Q
   const int64_t hk = blockIdx.x;
   const int j0 = jbase + blockIdx.y * C::M;
   const float2* kb = wsk + hk * cg.spec;
-  for (int e = threadIdx.x; e < C::TILE; e += C::T) ldsQ[(e % C::M) * C::S + e / C::M] = make_float2(0.f, 0.f);
+  // Element it of a thread is column m = tp % M (fixed), frequency k = tp / M
+  // + it * T / M.  Its filter value and shift ramp
+  //   R = W_F0^{c0 k} * W_F1^{c1 k1} * W_F2^{c2 k2},  (k1, k2) = (j / FH, j % FH),
+  // do not depend on the image: built once, the column factor once per thread
+  // (table roots; every axis length here is <= 2^10).
+  const int tp = opaque_tid();
+  const int m = tp % C::M, kfirst = tp / C::M;
+  const int j = j0 + m;
+  const TwTable tt(tw);
+  float2 r12;
+  {
+    const int jj = j < cg.inner_count ? j : 0;
+    const int k1 = jj / rp.FH, k2 = jj - k1 * rp.FH;
+    const int f1 = 1 << rp.lF1, f2 = 1 << rp.lF2;
+    r12 = cmul(tt.load(f1, (rp.c1 * k1) & (f1 - 1)), tt.load(f2, (rp.c2 * k2) & (f2 - 1)));
+  }
+  float2 kv[PT], rr[PT], q[PT];
+#pragma unroll
+  for (int it = 0; it < PT; ++it) {
+    const int k = kfirst + it * (C::T / C::M);
+    kv[it] = col_load(kb, cg, j, k, C::F);
+    rr[it] = cmul(r12, tt.load(C::F, (rp.c0 * k) & (C::F - 1)));
+    q[it] = make_float2(0.f, 0.f);
+  }
   const int nb = kfilm ? 1 : B;
   for (int bi = 0; bi < nb; ++bi) {
     const int64_t bh = kfilm ? hk : (int64_t(bi) * H + hk);
     float2* gb = wsg + bh * cg.spec;
     const float2* xb = wsx + bh * cg.spec;
-    constexpr int PT = C::TILE / C::T;
-    float2 kv[PT];
-    const int tk = opaque_tid();
-#pragma unroll
-    for (int it = 0; it < PT; ++it) {
-      const int e = tk + it * C::T;
-      kv[it] = col_load(kb, cg, j0 + e % C::M, e / C::M, C::F);
-    }
-    auto ldg = [&](int m, int n) -> float2 { return col_load(gb, cg, j0 + m, n, S0); };
-    auto ldx = [&](int m, int n) -> float2 { return col_load(xb, cg, j0 + m, n, S0); };
+    auto ldg = [&](int mm, int n) -> float2 { return col_load(gb, cg, j0 + mm, n, S0); };
+    auto ldx = [&](int mm, int n) -> float2 { return col_load(xb, cg, j0 + mm, n, S0); };
     LdsTile<C::S, false> stG{ldsG};
     LdsTile<C::S, false> stX{ldsX};
     fft<LOGF, false, C::M, C::T, C::S, true>(ldsG, ldg, stG, tw);
     fft<LOGF, false, C::M, C::T, C::S, true>(ldsX, ldx, stX, tw);
-    const int tp = opaque_tid();
 #pragma unroll
     for (int it = 0; it < PT; ++it) {
-      const int e = tp + it * C::T;
-      const int m = e % C::M, k = e / C::M;
-      const int a = m * C::S + k;
-      const float2 gsh = cmul(ldsG[a], shift_ramp(rp, k, j0 + m));
-      ldsQ[a] = cadd(ldsQ[a], cmulc(gsh, ldsX[a]));
+      const int a = m * C::S + kfirst + it * (C::T / C::M);
+      const float2 gsh = cmul(ldsG[a], rr[it]);
+      q[it] = cadd(q[it], cmulc(gsh, ldsX[a]));
       ldsG[a] = cmulc(gsh, kv[it]);
     }
     __syncthreads();
     LdsTile<C::S, false> ldl{ldsG};
-    auto st = [&](int m, int k, float2 v) {
-      if (j0 + m >= cg.inner_count || k >= S0) return;
-      gb[int64_t(k) * cg.axis_stride + j0 + m] = v;
+    auto st = [&](int mm, int k, float2 v) {
+      if (j0 + mm >= cg.inner_count || k >= S0) return;
+      gb[int64_t(k) * cg.axis_stride + j0 + mm] = v;
     };
-    fft<LOGF, true, C::M, C::T, C::S, true>(ldsG, ldl, st, tw);
+    fft<LOGF, true, C::M, C::T, C::S, true>(ldsG, ldl, st, tw);  // ends with a barrier: ldsX is free
   }
+#pragma unroll
+  for (int it = 0; it < PT; ++it) ldsX[m * C::S + kfirst + it * (C::T / C::M)] = q[it];
+  __syncthreads();
   float2* qb = wsq + hk * cg.spec;
-  LdsTile<C::S, false> ldq{ldsQ};
-  auto stq = [&](int m, int k, float2 v) {
-    if (j0 + m >= cg.inner_count || k >= K0) return;
-    qb[int64_t(k) * cg.axis_stride + j0 + m] = v;
+  LdsTile<C::S, false> ldq{ldsX};
+  auto stq = [&](int mm, int k, float2 v) {
+    if (j0 + mm >= cg.inner_count || k >= K0) return;
+    qb[int64_t(k) * cg.axis_stride + j0 + mm] = v;
   };
-  fft<LOGF, true, C::M, C::T, C::S, true>(ldsQ, ldq, stq, tw);
+  fft<LOGF, true, C::M, C::T, C::S, true>(ldsX, ldq, stq, tw);
 }
 
 }  // namespace nsq
