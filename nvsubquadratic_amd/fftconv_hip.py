@@ -381,7 +381,10 @@ class _FFTConvND(torch.autograd.Function):
         gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
         ws, ctx.ws = ctx.ws, None  # the backward consumes the forward state
         fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch, ws, fwd_state=ws is not None)
-        gsum = gs.view(ctx.kbatch, H).sum(0).to(s.dtype) if ctx.has_s else None
+        gsum = None
+        if ctx.has_s:
+            # per-filter partial sums only for FiLM kernels; a shared kernel's gs is complete
+            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
         return gx, gk, gsum, None
 
 
