@@ -318,6 +318,322 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
 }
 
 // ---------------------------------------------------------------------------
+// Backward with the mixer on the matrix cores (Km >= 16), three kernels:
+//  bwd1 (row walker like the forward): z into the window, q; h = conv(z) +
+//       skip*z on the MFMA band; gq = g*h -> gp (q rows), gh = g*q -> gh
+//       workspace; and the mixer weight gradient of each tile as an MFMA
+//       product over the same windows,
+//         D[i][t] += sum_a gh[16a + i] * zwin[16a + t],  gw[j] = sum_i D[i][i + j]
+//       (zwin[m] = z[n0 - hz + m]; t = i + j < 4 NS), kept in registers over
+//       the workgroup's tiles and reduced in a fixed order (waves, then the
+//       diagonal) into a per-workgroup partial;
+//  bwd2: gz = corr(gh; w_mixer) + skip*gh on the reversed band over a forward
+//       window of gh; k, v recomputed; gk = gz*v, gv = gz*k -> gp (k, v rows);
+//  reduce: the partials of a channel summed in a fixed order -> gw_mixer, and
+//       its lag Km-1 -> gskip.
+// ---------------------------------------------------------------------------
+template <int NS>
+struct B2BBwd1Lds {
+  B2BMfmaLds<NS> f;
+  int gh, total;
+  __host__ __device__ B2BBwd1Lds(int Kp, int Km) : f(Kp, Km) {
+    gh = f.total;  // gh of the tile, qs_pad layout
+    total = gh + kConvTile + kConvTile / 4;
+    const int red = 16 * 4 * NS;  // end-of-segment reduction (aliases the start)
+    if (total < red) total = red;
+  }
+};
+
+template <int DT, int NS, bool SHORT>
+__global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2))) void b2b_bwd1_mfma_kernel(
+    const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ wp,
+    const float* __restrict__ wm, const float* __restrict__ skip, float* __restrict__ gp, float* __restrict__ ghw,
+    float* __restrict__ gw_part, int B, int C, int L, int Kp, int Km) {
+  constexpr int TF = b2b_kv_stage_words<NS, SHORT>();
+  constexpr int TG = NS / 4;  // 16-column groups of the window
+  extern __shared__ __align__(16) float smem[];
+  const B2BBwd1Lds<NS> lay(Kp, Km);
+  float* xs_q = smem + lay.f.q;
+  float* xs_k = smem + lay.f.k;
+  float* xs_v = smem + lay.f.v;
+  float* qs = smem + lay.f.qs;
+  float* zp = smem + lay.f.z;
+  float* wlq = smem + lay.f.wq;
+  float* wlk = smem + lay.f.wk;
+  float* wlv = smem + lay.f.wv;
+  float* wlm = smem + lay.f.wm;
+  float* ghs = smem + lay.gh;
+  const int64_t row = blockIdx.x;  // b*C + c
+  const int b = int(row / C), c = int(row % C);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int t_begin = int(blockIdx.y) * kB2BSegTiles;
+  const int t_end = min(ntiles, t_begin + kB2BSegTiles);
+  const typename Elem<DT>::T* xq = x + (int64_t(b) * 3 * C + c) * L;
+  const typename Elem<DT>::T* xk = xq + int64_t(C) * L;
+  const typename Elem<DT>::T* xv = xk + int64_t(C) * L;
+  const int hz = Km - 1, hp = Kp - 1, hk = lay.f.hk;
+  const int t = int(threadIdx.x);
+  stage_weights<false>(wlq, wp + int64_t(c) * Kp, Kp);
+  stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
+  stage_weights<false>(wlv, wp + int64_t(2 * C + c) * Kp, Kp);
+  stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
+  constexpr int ZW = mfma_src_count<NS>();
+  for (int m = kConvTile + t; m < ZW; m += kConvThreads) zp[conv_pad(m)] = 0.f;
+  RowStage<DT, kConvTile + (SHORT ? 3 : kConvMaxK - 1) + 2 * kConvPer> sq;
+  RowStage<DT, TF> sk, sv;
+  {
+    const int64_t n0 = int64_t(t_begin) * kConvTile;
+    sq.load(xq, n0 - hp, 0, L);
+    sk.load(xk, n0 - hk, 0, L);
+    sv.load(xv, n0 - hk, 0, L);
+  }
+  __syncthreads();  // weights staged
+  ToeplitzMfma<NS> tm;
+  tm.load_weights(wlm, Km, skip ? skip[c] : 0.f);  // h = conv(z) + skip*z
+  const RowBuf<DT, false> gb(g + row * L, L);
+  const RowBuf<NSQ_DTYPE_F32, false> gqb(gp + (int64_t(b) * 3 * C + c) * L, L);
+  const RowBuf<NSQ_DTYPE_F32, false> ghb(ghw + row * L, L);
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+  const int kk = l >> 4, li = l & 15;
+  const int base = t * kConvPer;
+  nsq_f32x4_t D[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) D[tg] = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int ti = t_begin; ti < t_end; ++ti) {
+    const int64_t n0 = int64_t(ti) * kConvTile;
+    // 1. staged rows to LDS, next tile's loads in flight
+    sq.store(xs_q, kConvTile + hp + 2 * kConvPer);
+    sk.store(xs_k, kConvTile + hk + 2 * kConvPer);
+    sv.store(xs_v, kConvTile + hk + 2 * kConvPer);
+    __syncthreads();
+    if (ti + 1 < t_end) {
+      sq.load(xq, n0 + kConvTile - hp, 0, L);
+      sk.load(xk, n0 + kConvTile - hk, 0, L);
+      sv.load(xv, n0 + kConvTile - hk, 0, L);
+    }
+    // 2. z and q as in the forward
+    {
+      float ka[kConvPer], va[kConvPer], qa[kConvPer];
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) ka[e] = va[e] = qa[e] = 0.f;
+      const int bz = hk - hp + base;
+      slide_proj<SHORT>(ka, xs_k, bz, Kp, wlk);
+      slide_proj<SHORT>(va, xs_v, bz, Kp, wlv);
+      slide_proj<SHORT>(qa, xs_q, base, Kp, wlq);
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) zp[conv_pad(hz + base + e)] = (n0 + base + e < L) ? ka[e] * va[e] : 0.f;
+      if (ti == t_begin) {
+        for (int m = t; m < hz; m += kConvThreads) {
+          const int64_t n = n0 - hz + m;
+          float kv = 0.f, vv = 0.f;
+          if (n >= 0) {
+            const int i0 = hk - hp - hz + m;
+            for (int j = 0; j < Kp; ++j) {
+              kv = fmaf(wlk[j], xs_k[i0 + j], kv);
+              vv = fmaf(wlv[j], xs_v[i0 + j], vv);
+            }
+          }
+          zp[conv_pad(m)] = kv * vv;
+        }
+      }
+      __syncthreads();  // the q stage is consumed: q takes its place
+      float* qd = qs + qs_pad(base);
+      *reinterpret_cast<float4*>(qd) = make_float4(qa[0], qa[1], qa[2], qa[3]);
+      *reinterpret_cast<float4*>(qd + 4) = make_float4(qa[4], qa[5], qa[6], qa[7]);
+    }
+    __syncthreads();
+    // 3. h on the MFMA band; gq = g*h, gh = g*q (positions >= L: g reads 0)
+    {
+      nsq_f32x4_t acc0, acc1;
+      tm.run2(zp, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      float gv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = 16 * (16 * (wave + h * kConvWaves) + 4 * kk + r) + li;
+          gv[4 * h + r] = gb.elem(n0 + p);
+        }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = 16 * (16 * (wave + h * kConvWaves) + 4 * kk + r) + li;
+          const float hv = h ? acc1[r] : acc0[r];
+          const float ghv = gv[4 * h + r] * qs[qs_pad(p)];
+          gqb.store_elem(n0 + p, gv[4 * h + r] * hv);
+          ghb.store_elem(n0 + p, ghv);
+          ghs[qs_pad(p)] = ghv;
+        }
+      }
+    }
+    __syncthreads();
+    // 4. mixer weight gradient of the tile: wave w takes blocks [32w, 32w + 32)
+#pragma unroll 2
+    for (int a0 = 32 * wave; a0 < 32 * wave + 32; a0 += 4) {
+      const float av = ghs[qs_pad(16 * (a0 + kk) + li)];
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg) {
+        const float bv = zp[20 * (a0 + kk + tg) + li];
+        D[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, D[tg], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    // 5. z of the next tile's halo to the window front
+    for (int m = t; m < hz; m += kConvThreads) zp[conv_pad(m)] = zp[conv_pad(kConvTile + m)];
+  }
+  // Fixed-order reduction: D of waves 0..3 summed into red[i][t], then
+  // gw[j] = sum_i red[i][i + j].
+  __syncthreads();
+  float* red = smem;
+  constexpr int RW = 4 * NS;
+  for (int w = 0; w < kConvWaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float& dst = red[(4 * kk + r) * RW + 16 * tg + li];
+          dst = (w == 0 ? 0.f : dst) + D[tg][r];
+        }
+    }
+    __syncthreads();
+  }
+  if (t < Km) {
+    float sacc = 0.f;
+    for (int i = 0; i < 16; ++i) sacc += red[i * RW + i + t];
+    const int nparts = B * int(gridDim.y);
+    const int part = b * int(gridDim.y) + int(blockIdx.y);
+    gw_part[(int64_t(c) * nparts + part) * Km + t] = sacc;
+  }
+}
+
+template <int DT, int NS, bool SHORT>
+struct B2BBwd2Lds {
+  static constexpr int GWORDS = (conv_pad_words(mfma_src_count<NS>()) + 7) & ~7;
+  int gw, k, v, ks, vs, wk, wv, wr, total;
+  __host__ __device__ static int up8(int n) { return (n + 7) & ~7; }
+  __host__ __device__ B2BBwd2Lds(int Kp, int Km) {
+    const int hp = Kp - 1;
+    gw = 0;
+    k = GWORDS;
+    v = k + up8(kConvTile + hp + 2 * kConvPer);
+    ks = v + up8(kConvTile + hp + 2 * kConvPer);
+    vs = ks + kConvTile + kConvTile / 4;
+    wk = vs + kConvTile + kConvTile / 4;
+    wv = wk + up8(Kp);
+    wr = wv + up8(Kp);
+    total = wr + up8(Km);
+  }
+};
+
+template <int DT, int NS, bool SHORT>
+__global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3))) void b2b_bwd2_mfma_kernel(
+    const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ wp, const float* __restrict__ wm,
+    const float* __restrict__ skip, const float* __restrict__ ghw, float* __restrict__ gp, int C, int L, int Kp,
+    int Km) {
+  constexpr int ZW = mfma_src_count<NS>();
+  constexpr int GIT = (ZW + kConvThreads - 1) / kConvThreads;
+  extern __shared__ __align__(16) float smem[];
+  const B2BBwd2Lds<DT, NS, SHORT> lay(Kp, Km);
+  float* gwin = smem + lay.gw;
+  float* xs_k = smem + lay.k;
+  float* xs_v = smem + lay.v;
+  float* ks = smem + lay.ks;
+  float* vs = smem + lay.vs;
+  float* wlk = smem + lay.wk;
+  float* wlv = smem + lay.wv;
+  float* wlr = smem + lay.wr;
+  const int64_t row = blockIdx.x;  // b*C + c
+  const int b = int(row / C), c = int(row % C);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int t_begin = int(blockIdx.y) * kB2BSegTiles;
+  const int t_end = min(ntiles, t_begin + kB2BSegTiles);
+  const typename Elem<DT>::T* xk = x + (int64_t(b) * 3 * C + C + c) * L;
+  const typename Elem<DT>::T* xv = xk + int64_t(C) * L;
+  const float* ghr = ghw + row * L;
+  const int hp = Kp - 1;
+  const int t = int(threadIdx.x);
+  stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
+  stage_weights<false>(wlv, wp + int64_t(2 * C + c) * Kp, Kp);
+  stage_weights<true>(wlr, wm + int64_t(c) * Km, Km);  // wlr[j] = w[Km-1-j]: gz[n] = sum_j wlr[j] gh[n + j]
+  RowStage<DT, kConvTile + (SHORT ? 3 : kConvMaxK - 1) + 2 * kConvPer> sk, sv;
+  float gstage[GIT];
+  auto load_tile = [&](int64_t n0) {
+    sk.load(xk, n0 - hp, 0, L);
+    sv.load(xv, n0 - hp, 0, L);
+    const RowBuf<NSQ_DTYPE_F32, false> rb(ghr, L);
+#pragma unroll
+    for (int it = 0; it < GIT; ++it) gstage[it] = rb.elem(n0 + t + it * kConvThreads);  // n0 >= 0
+  };
+  load_tile(int64_t(t_begin) * kConvTile);
+  __syncthreads();  // weights staged
+  ToeplitzMfma<NS> tm;
+  tm.load_weights(wlr, Km, 0.f, 0, skip ? skip[c] : 0.f);  // + skip*gh[n]: tap 0
+  const RowBuf<NSQ_DTYPE_F32, false> gkb(gp + (int64_t(b) * 3 * C + C + c) * L, L);
+  const RowBuf<NSQ_DTYPE_F32, false> gvb(gp + (int64_t(b) * 3 * C + 2 * C + c) * L, L);
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+  const int kk = l >> 4, li = l & 15;
+  const int base = t * kConvPer;
+  for (int ti = t_begin; ti < t_end; ++ti) {
+    const int64_t n0 = int64_t(ti) * kConvTile;
+    // 1. staged rows to LDS (gh window: word m = gh[n0 + m], m < ZW)
+    sk.store(xs_k, kConvTile + hp + 2 * kConvPer);
+    sv.store(xs_v, kConvTile + hp + 2 * kConvPer);
+#pragma unroll
+    for (int it = 0; it < GIT; ++it) {
+      const int m = t + it * kConvThreads;
+      if (m < ZW) gwin[conv_pad(m)] = gstage[it];
+    }
+    __syncthreads();
+    if (ti + 1 < t_end) load_tile(n0 + kConvTile);
+    // 2. k, v of the tile
+    {
+      float ka[kConvPer], va[kConvPer];
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) ka[e] = va[e] = 0.f;
+      slide_proj<SHORT>(ka, xs_k, base, Kp, wlk);
+      slide_proj<SHORT>(va, xs_v, base, Kp, wlv);
+      float* kd = ks + qs_pad(base);
+      float* vd = vs + qs_pad(base);
+      *reinterpret_cast<float4*>(kd) = make_float4(ka[0], ka[1], ka[2], ka[3]);
+      *reinterpret_cast<float4*>(kd + 4) = make_float4(ka[4], ka[5], ka[6], ka[7]);
+      *reinterpret_cast<float4*>(vd) = make_float4(va[0], va[1], va[2], va[3]);
+      *reinterpret_cast<float4*>(vd + 4) = make_float4(va[4], va[5], va[6], va[7]);
+    }
+    __syncthreads();
+    // 3. gz on the reversed band; gk = gz*v, gv = gz*k
+    {
+      nsq_f32x4_t acc0, acc1;
+      tm.run2(gwin, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = 16 * (16 * (wave + h * kConvWaves) + 4 * kk + r) + li;
+          const float gz = h ? acc1[r] : acc0[r];
+          gkb.store_elem(n0 + p, gz * vs[qs_pad(p)]);
+          gvb.store_elem(n0 + p, gz * ks[qs_pad(p)]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// gw_mixer[c, j] = sum over the channel's partials (fixed order); gskip[c] = its lag Km-1.
+__global__ void b2b_wgrad_reduce_kernel(const float* __restrict__ part, int nparts, int Km, float* __restrict__ gw,
+                                        float* __restrict__ gskip) {
+  const int c = blockIdx.x, j = threadIdx.x;
+  if (j >= Km) return;
+  const float* pc = part + int64_t(c) * nparts * Km + j;
+  float sacc = 0.f;
+  for (int p = 0; p < nparts; ++p) sacc += pc[int64_t(p) * Km];
+  gw[int64_t(c) * Km + j] = sacc;
+  if (gskip && j == Km - 1) gskip[c] = sacc;
+}
+
+// ---------------------------------------------------------------------------
 // Wave-specialized matrix-core forward for projection taps Kp <= 4 (the
 // striped-Hyena short conv).  A workgroup of 8 waves owns one channel c and
 // walks kB2BWsSegTiles consecutive tiles of the channel's (batch, tile)
@@ -724,6 +1040,33 @@ static void launch_b2b_fwd(const void* x, const float* wp, const float* wm, cons
                      Kp, Km);
 }
 
+// Partials of the matrix-core mixer weight gradient: [C][B * segments][Km].
+static int64_t b2b_wgrad_parts(int64_t B, int64_t L) { return B * ceil_div(ceil_div(L, kConvTile), kB2BSegTiles); }
+
+template <int DT, int NS>
+static void launch_b2b_bwd_mfma(const void* g, const void* x, const float* wp, const float* wm, const float* skip,
+                                float* gwm, float* gskip, int B, int C, int L, int Kp, int Km, float* gp, float* gh,
+                                float* part, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  dim3 grid(B * C, unsigned(ceil_div(ceil_div(L, kConvTile), kB2BSegTiles)));
+  const size_t l1 = size_t(B2BBwd1Lds<NS>(Kp, Km).total) * sizeof(float);
+  if (Kp <= 4) {
+    const size_t l2 = size_t(B2BBwd2Lds<DT, NS, true>(Kp, Km).total) * sizeof(float);
+    hipLaunchKernelGGL((b2b_bwd1_mfma_kernel<DT, NS, true>), grid, dim3(kConvThreads), l1, st, (const ET*)g,
+                       (const ET*)x, wp, wm, skip, gp, gh, part, B, C, L, Kp, Km);
+    hipLaunchKernelGGL((b2b_bwd2_mfma_kernel<DT, NS, true>), grid, dim3(kConvThreads), l2, st, (const ET*)x, wp, wm,
+                       skip, (const float*)gh, gp, C, L, Kp, Km);
+  } else {
+    const size_t l2 = size_t(B2BBwd2Lds<DT, NS, false>(Kp, Km).total) * sizeof(float);
+    hipLaunchKernelGGL((b2b_bwd1_mfma_kernel<DT, NS, false>), grid, dim3(kConvThreads), l1, st, (const ET*)g,
+                       (const ET*)x, wp, wm, skip, gp, gh, part, B, C, L, Kp, Km);
+    hipLaunchKernelGGL((b2b_bwd2_mfma_kernel<DT, NS, false>), grid, dim3(kConvThreads), l2, st, (const ET*)x, wp, wm,
+                       skip, (const float*)gh, gp, C, L, Kp, Km);
+  }
+  hipLaunchKernelGGL(b2b_wgrad_reduce_kernel, dim3(C), dim3(kConvThreads), 0, st, (const float*)part,
+                     int(b2b_wgrad_parts(B, L)), Km, gwm, gskip);
+}
+
 template <int DT>
 static void launch_b2b_bwd(const void* g, const void* x, const float* wp, const float* wm, const float* skip, void* gx,
                            float* gwp, float* gwm, float* gskip, int B, int C, int L, int Kp, int Km, float* ws,
@@ -732,7 +1075,22 @@ static void launch_b2b_bwd(const void* g, const void* x, const float* wp, const 
   const int64_t E = int64_t(B) * C * L;
   float* gp = ws;            // [B, 3C, L]
   float* gh = ws + 3 * E;    // [B, C, L]
-  float* zw = ws + 4 * E;    // [B, C, L]
+  float* zw = ws + 4 * E;    // [B, C, L] (FMA path), or the weight-gradient partials (MFMA path)
+  const int ns = mfma_steps_for(Km);
+  if (ns) {
+    switch (ns) {
+      case 12: launch_b2b_bwd_mfma<DT, 12>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+      case 20: launch_b2b_bwd_mfma<DT, 20>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+      case 36: launch_b2b_bwd_mfma<DT, 36>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+      default: launch_b2b_bwd_mfma<DT, 68>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+    }
+    dim3 grid3(B * 3 * C, unsigned(ceil_div(L, kConvTile)));
+    hipLaunchKernelGGL((cconv_gx_kernel<DT, NSQ_DTYPE_F32>), grid3, dim3(kConvThreads), 0, st, (const float*)gp, wp,
+                       (ET*)gx, 3 * C, L, Kp);
+    hipLaunchKernelGGL((cconv_wgrad_kernel<DT, NSQ_DTYPE_F32>), dim3(3 * C), dim3(kConvThreads), 0, st,
+                       (const float*)gp, (const ET*)x, gwp, (float*)nullptr, B, 3 * C, L, Kp);
+    return;
+  }
   dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
   hipLaunchKernelGGL((b2b_bwd1_kernel<DT>), grid, dim3(kConvThreads), size_t(B2BLds(Kp, Km).total) * sizeof(float), st, (const ET*)g, (const ET*)x, wp, wm, skip,
                      gp, gh, zw, C, L, Kp, Km);
@@ -787,8 +1145,11 @@ int nsq_b2b_causal_conv1d_fwd(const void* x, const float* weight_proj, const flo
 
 size_t nsq_b2b_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t Kp, int64_t Km) {
   (void)Kp;
-  (void)Km;
-  return size_t(5 * B * C * L) * sizeof(float);
+  // gp [B,3C,L], gh [B,C,L], then z [B,C,L] (FMA path) or the weight-gradient
+  // partials [C][B * segments][Km] (matrix-core path, Km >= 16)
+  const int64_t E = B * C * L;
+  const int64_t tail = Km >= 16 ? C * b2b_wgrad_parts(B, L) * Km : E;
+  return size_t(4 * E + (tail > E ? tail : E)) * sizeof(float);
 }
 
 int nsq_b2b_causal_conv1d_bwd(const void* gy, const void* x, const float* weight_proj, const float* weight_mixer,

@@ -225,14 +225,16 @@ struct ToeplitzMfma {
   // wl: the K taps in LDS (conv orientation: y[n] = sum_j wl[j] src[n + j]).
   // last_add is added to tap K-1 (a skip term c * src[n + K - 1] folded into
   // the band).
-  // shift: zero taps prepended to the band (tap j of the band is wl[j - shift]).
-  __device__ __forceinline__ void load_weights(const float* wl, int K, float last_add = 0.f, int shift = 0) {
+  // shift: zero taps prepended to the band (tap j of the band is wl[j - shift]);
+  // first_add joins tap 0 (a skip term c * src[n] of a correlation).
+  __device__ __forceinline__ void load_weights(const float* wl, int K, float last_add = 0.f, int shift = 0,
+                                               float first_add = 0.f) {
     const int l = int(threadIdx.x) & 63, kk = l >> 4, i = l & 15;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int j = 16 * (s >> 2) + 4 * kk + (s & 3) - i - shift;
       const bool ok = j >= 0 && j < K;
-      const float v = wl[ok ? j : 0] + (j == K - 1 ? last_add : 0.f);
+      const float v = wl[ok ? j : 0] + (j == K - 1 ? last_add : 0.f) + (j == 0 ? first_add : 0.f);
       b[s] = ok ? v : 0.f;
     }
   }

@@ -147,27 +147,38 @@ def test_b2b_forward_backward(B, C, L, Kp, Km):
 def test_b2b_mixer_tap_counts_across_matrix_core_plans(Km):
     """Mixer tap counts on both sides of each matrix-core step-count boundary.
 
-    From 16 taps the mixer conv runs as a banded Toeplitz product on the matrix
-    cores with 12, 20, 36 or 68 steps (up to 33, 65, 129, 257 taps); 15 taps
-    stay on the FMA loop.  Ragged length (not a multiple of the 2048-output
-    tile), several batches, nonzero skip.
+    From 16 taps the mixer conv (forward), its adjoint correlation and its
+    weight gradient run as banded Toeplitz products on the matrix cores with
+    12, 20, 36 or 68 steps (up to 33, 65, 129, 257 taps); 15 taps stay on the
+    FMA loop.  Ragged length (not a multiple of the 2048-output tile), several
+    batches, nonzero skip; forward and all four gradients against float64.
     """
     torch.manual_seed(100 + Km)
     B, C, L = 3, 5, 4500
-    x = torch.randn(B, 3 * C, L, dtype=torch.float64)
-    wp = torch.randn(3 * C, 3, dtype=torch.float64) / 3 ** 0.5
-    wm = torch.randn(C, Km, dtype=torch.float64) / Km ** 0.5
-    sk = torch.randn(C, dtype=torch.float64)
+    x = torch.randn(B, 3 * C, L, dtype=torch.float64, requires_grad=True)
+    wp = (torch.randn(3 * C, 3, dtype=torch.float64) / 3 ** 0.5).requires_grad_(True)
+    wm = (torch.randn(C, Km, dtype=torch.float64) / Km ** 0.5).requires_grad_(True)
+    sk = torch.randn(C, dtype=torch.float64, requires_grad=True)
     # the B2B composition of the oracle's conv, in float64
     p = causal_conv1d_torch(x, wp)
     q, k, v = p[:, :C], p[:, C:2 * C], p[:, 2 * C:]
     z = k * v
     y_ref = q * (causal_conv1d_torch(z, wm) + sk.view(1, C, 1) * z)
-    y = b2b_causal_conv1d(*(t.float().cuda() for t in (x, wp, wm, sk))).double().cpu()
+    gy = torch.randn_like(y_ref)
+    y_ref.backward(gy)
+    args = [t.detach().float().cuda().requires_grad_(True) for t in (x, wp, wm, sk)]
+    y = b2b_causal_conv1d(*args)
+    y.backward(gy.float().cuda())
+    y = y.detach().double().cpu()
     assert rel_l2(y_ref, y) < 1e-5
     # the first outputs of a row and of a tile see the causal zero padding / the tile halo
     assert rel_l2(y_ref[..., :Km + 3], y[..., :Km + 3]) < 1e-5
     assert rel_l2(y_ref[..., 2048:2048 + Km], y[..., 2048:2048 + Km]) < 1e-5
+    for ref, got in zip((x, wp, wm, sk), args):
+        assert rel_l2(ref.grad, got.grad.double()) < 1e-5
+    # gradients near the row end and across a tile boundary
+    assert rel_l2(x.grad[..., -Km - 3:], args[0].grad[..., -Km - 3:].double()) < 1e-5
+    assert rel_l2(x.grad[..., 2040:2060], args[0].grad[..., 2040:2060].double()) < 1e-5
 
 
 def test_b2b_config2_shape_bf16_sample():
