@@ -317,6 +317,15 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
   }
 }
 
+// Projection taps left-padded to 4: w4[j] = w[j - (4 - Kp)].
+__device__ __forceinline__ void load_taps4(float (&w4)[4], const float* __restrict__ w, int Kp) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s = j - (4 - Kp);
+    w4[j] = s >= 0 ? w[s >= 0 ? s : 0] : 0.f;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Backward with the mixer on the matrix cores (Km >= 16), three kernels:
 //  bwd1 (row walker like the forward): z into the window, q; h = conv(z) +
@@ -621,6 +630,258 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
   }
 }
 
+// bwd2 for projection taps Kp <= 4, fused with the input gradient and the
+// projection weight gradient: per tile, gz on the reversed band (and by a
+// short dot product at the Kp - 1 positions past the tile), gk = gz*v and
+// gv = gz*k into LDS, gq from the workspace; then
+//   gx_c[n] = sum_j w_c[j] gc[n + Kp - 1 - j]   (c = q, k, v)
+// stored directly, and gw_c[j] += sum_n gc[n] x_c[n - Kp + 1 + j] kept per
+// thread over the workgroup's tiles, reduced in a fixed order into a
+// per-workgroup partial [3][4].  (Neither gk, gv nor gx need a workspace pass.)
+constexpr int kB2BBwdExtra = 4;  // positions past the tile with gk, gv (>= Kp - 1, keeps 16-byte alignment)
+
+template <int NS>
+struct B2BBwd2fLds {
+  static constexpr int GWORDS = (conv_pad_words(mfma_src_count<NS>() + kB2BBwdExtra) + 7) & ~7;
+  static constexpr int XW = kConvTile + 3 + kB2BBwdExtra + 2 * kConvPer;  // staged x / g words per row
+  static constexpr int XS = (XW + 7) & ~7;
+  int gw, xq, xk, xv, gq, gk, gv, ks, vs, wq, wk, wv, wr, total;
+  __host__ __device__ B2BBwd2fLds(int Km) {
+    gw = 0;
+    xq = GWORDS;
+    xk = xq + XS;
+    xv = xk + XS;
+    gq = xv + XS;
+    gk = gq + XS;
+    gv = gk + XS;
+    ks = gv + XS;  // k, v at tile positions p (+ the extra ones), index p
+    vs = ks + XS;
+    wq = vs + XS;  // three reversed 4-tap sets (padded to 8), then the reversed mixer
+    wk = wq + 8;
+    wv = wk + 8;
+    wr = wv + 8;
+    total = wr + ((Km + 7) & ~7);
+    if (total < 12 * kConvThreads) total = 12 * kConvThreads;  // end-of-segment reduction
+  }
+};
+
+template <int DT, int NS>
+__global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2))) void b2b_bwd2f_mfma_kernel(
+    const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ wp, const float* __restrict__ wm,
+    const float* __restrict__ skip, const float* __restrict__ ghw, const float* __restrict__ gpw,
+    typename Elem<DT>::T* __restrict__ gx, float* __restrict__ gwp_part, int B, int C, int L, int Kp, int Km) {
+  using ET = typename Elem<DT>::T;
+  constexpr int ZW = mfma_src_count<NS>() + kB2BBwdExtra;
+  constexpr int GIT = (ZW + kConvThreads - 1) / kConvThreads;
+  using LY = B2BBwd2fLds<NS>;
+  extern __shared__ __align__(16) float smem[];
+  const LY lay(Km);
+  float* gwin = smem + lay.gw;
+  float* xs[3] = {smem + lay.xq, smem + lay.xk, smem + lay.xv};
+  float* gs_q = smem + lay.gq;
+  float* gs_k = smem + lay.gk;
+  float* gs_v = smem + lay.gv;
+  float* ks = smem + lay.ks;
+  float* vs = smem + lay.vs;
+  float* wl[3] = {smem + lay.wq, smem + lay.wk, smem + lay.wv};
+  float* wlr = smem + lay.wr;
+  const int64_t row = blockIdx.x;  // b*C + c
+  const int b = int(row / C), c = int(row % C);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int t_begin = int(blockIdx.y) * kB2BSegTiles;
+  const int t_end = min(ntiles, t_begin + kB2BSegTiles);
+  const ET* xrow[3];
+  xrow[0] = x + (int64_t(b) * 3 * C + c) * L;
+  xrow[1] = xrow[0] + int64_t(C) * L;
+  xrow[2] = xrow[1] + int64_t(C) * L;
+  const float* ghr = ghw + row * L;
+  const float* gqr = gpw + (int64_t(b) * 3 * C + c) * L;
+  const int hp = Kp - 1;
+  const int t = int(threadIdx.x);
+  // 4-tap sets, left-padded as in the forward (w4[j] = w[j - (4 - Kp)]) for
+  // the projection convs, and reversed (wr4[j] = w[Kp - 1 - j], zero for j >=
+  // Kp) for the input-gradient correlations
+  if (t < 24) {
+    const int set = t / 8, j = t % 8;
+    const int ch = set * C + c;
+    wl[set][j] = (j < Kp) ? wp[int64_t(ch) * Kp + (Kp - 1 - j)] : 0.f;
+  }
+  float w4[3][4];
+#pragma unroll
+  for (int set = 0; set < 3; ++set) load_taps4(w4[set], wp + int64_t(set * C + c) * Kp, Kp);
+  stage_weights<true>(wlr, wm + int64_t(c) * Km, Km);
+  // staged words: x rows and gq from n0 - 3 (xs index i <-> position n0 - 3 + i)
+  constexpr int XW = LY::XW;
+  RowStage<DT, XW> sx0, sx1, sx2;
+  RowStage<NSQ_DTYPE_F32, XW> sgq;
+  float gstage[GIT];
+  auto load_tile = [&](int64_t n0) {
+    sx0.load(xrow[0], n0 - 3, 0, L);
+    sx1.load(xrow[1], n0 - 3, 0, L);
+    sx2.load(xrow[2], n0 - 3, 0, L);
+    sgq.load(gqr, n0 - 3, 0, L);
+    const RowBuf<NSQ_DTYPE_F32, false> rb(ghr, L);
+#pragma unroll
+    for (int it = 0; it < GIT; ++it) gstage[it] = rb.elem(n0 + t + it * kConvThreads);
+  };
+  __syncthreads();  // weights staged
+  ToeplitzMfma<NS> tm;
+  const float skv = skip ? skip[c] : 0.f;
+  tm.load_weights(wlr, Km, 0.f, 0, skv);
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+  const int kk = l >> 4, li = l & 15;
+  const int base = t * kConvPer;
+  float wacc[3][4];  // projection weight-gradient partials of this thread
+#pragma unroll
+  for (int cc = 0; cc < 3; ++cc)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wacc[cc][j] = 0.f;
+  for (int ti = t_begin; ti < t_end; ++ti) {
+    const int64_t n0 = int64_t(ti) * kConvTile;
+    // 1. stage (loaded here: holding the next tile in registers would spill)
+    load_tile(n0);
+    sx0.store(xs[0], XW);
+    sx1.store(xs[1], XW);
+    sx2.store(xs[2], XW);
+    sgq.store(gs_q, XW);
+#pragma unroll
+    for (int it = 0; it < GIT; ++it) {
+      const int m = t + it * kConvThreads;
+      if (m < ZW) gwin[conv_pad(m)] = gstage[it];
+    }
+    // k, v at the tile positions p = base + e (4-tap convs over xs index p + j, x at n0 + p - 3 + j)
+    {
+      float ka[kConvPer], va[kConvPer];
+#pragma unroll
+      for (int e = 0; e < kConvPer; ++e) ka[e] = va[e] = 0.f;
+      slide_fma4(ka, xs[1], base, w4[1]);
+      slide_fma4(va, xs[2], base, w4[2]);
+      *reinterpret_cast<float4*>(ks + base) = make_float4(ka[0], ka[1], ka[2], ka[3]);
+      *reinterpret_cast<float4*>(ks + base + 4) = make_float4(ka[4], ka[5], ka[6], ka[7]);
+      *reinterpret_cast<float4*>(vs + base) = make_float4(va[0], va[1], va[2], va[3]);
+      *reinterpret_cast<float4*>(vs + base + 4) = make_float4(va[4], va[5], va[6], va[7]);
+      if (t < kB2BBwdExtra) {  // the positions past the tile
+        const int p = kConvTile + t;
+        float kv = 0.f, vv = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          kv = fmaf(w4[1][j], xs[1][p + j], kv);
+          vv = fmaf(w4[2][j], xs[2][p + j], vv);
+        }
+        ks[p] = kv;
+        vs[p] = vv;
+      }
+    }
+    __syncthreads();
+    // 2. gz on the band; gk = gz*v, gv = gz*k at tile positions p (LDS index p + 3)
+    {
+      nsq_f32x4_t acc0, acc1;
+      tm.run2(gwin, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = 16 * (16 * (wave + h * kConvWaves) + 4 * kk + r) + li;
+          const float gz = h ? acc1[r] : acc0[r];
+          gs_k[p + 3] = gz * vs[p];
+          gs_v[p + 3] = gz * ks[p];
+        }
+      }
+      // the kB2BBwdExtra positions past the tile: wave w takes position 2048 + w,
+      // its lanes split the taps, and a fixed shuffle tree sums them
+      static_assert(kB2BBwdExtra == kConvWaves, "b2b bwd2: one wave per extra position");
+      {
+        const int p = kConvTile + wave;
+        float part = 0.f;
+        for (int j = l; j < Km; j += 64) part = fmaf(wlr[j], gwin[conv_pad(p + j)], part);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
+        if (l == 0) {
+          const float gz = fmaf(skv, gwin[conv_pad(p)], part);
+          gs_k[p + 3] = gz * vs[p];
+          gs_v[p + 3] = gz * ks[p];
+        }
+      }
+    }
+    __syncthreads();
+    // 3. input gradients and weight-gradient partials at n0 + base + e
+    {
+      const float* gsrc[3] = {gs_q, gs_k, gs_v};
+#pragma unroll
+      for (int cc = 0; cc < 3; ++cc) {
+        // window gc[n0 + base - 3 + i], i < 16 (LDS index base + i); x at the same offsets
+        float gw_[16], xw_[12];
+        {
+          const float4 a = *reinterpret_cast<const float4*>(gsrc[cc] + base);
+          const float4 b4 = *reinterpret_cast<const float4*>(gsrc[cc] + base + 4);
+          const float4 c4 = *reinterpret_cast<const float4*>(gsrc[cc] + base + 8);
+          const float4 d4 = *reinterpret_cast<const float4*>(gsrc[cc] + base + 12);
+          const float tmp[16] = {a.x, a.y, a.z, a.w, b4.x, b4.y, b4.z, b4.w,
+                                 c4.x, c4.y, c4.z, c4.w, d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int i = 0; i < 16; ++i) gw_[i] = tmp[i];
+          const float4 xa = *reinterpret_cast<const float4*>(xs[cc] + base);
+          const float4 xb = *reinterpret_cast<const float4*>(xs[cc] + base + 4);
+          const float4 xc = *reinterpret_cast<const float4*>(xs[cc] + base + 8);
+          const float xt[12] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w, xc.x, xc.y, xc.z, xc.w};
+#pragma unroll
+          for (int i = 0; i < 12; ++i) xw_[i] = xt[i];
+        }
+        const float4 wr4 = *reinterpret_cast<const float4*>(wl[cc]);
+        const float wr[4] = {wr4.x, wr4.y, wr4.z, wr4.w};
+        float out[kConvPer];
+#pragma unroll
+        for (int e = 0; e < kConvPer; ++e) {
+          // gx[n] = sum_j w[Kp-1-j] gc[n + j], n = n0 + base + e -> window index e + 3 + j
+          float a = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a = fmaf(wr[j], gw_[e + 3 + j], a);
+          out[e] = a;
+          // gw[j] += gc[n] x[n - Kp + 1 + j], x window index e + 3 - hp + j
+          const float gcv = (n0 + base + e < L) ? gw_[e + 3] : 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int xi = e + 3 - hp + j;  // 0 <= xi < 12 for hp <= 3, j <= 3
+            wacc[cc][j] = fmaf(gcv, (j < Kp) ? xw_[xi < 0 ? 0 : (xi > 11 ? 11 : xi)] : 0.f, wacc[cc][j]);
+          }
+        }
+        ET* gr = gx + (int64_t(b) * 3 * C + cc * C + c) * L;
+#pragma unroll
+        for (int e = 0; e < kConvPer; e += 2) {
+          const int64_t n = n0 + base + e;
+          if (n < L) store_pair<DT>(gr, n, L, make_float2(out[e], out[e + 1]));
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // Fixed-order reduction of the weight-gradient partials: red[v][t], v < 12.
+  float* red = smem;
+#pragma unroll
+  for (int cc = 0; cc < 3; ++cc)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[(cc * 4 + j) * kConvThreads + t] = wacc[cc][j];
+  __syncthreads();
+  if (t < 12) {
+    float sacc = 0.f;
+    for (int i = 0; i < kConvThreads; ++i) sacc += red[t * kConvThreads + i];
+    const int nparts = B * int(gridDim.y);
+    const int part = b * int(gridDim.y) + int(blockIdx.y);
+    gwp_part[(int64_t(c) * nparts + part) * 12 + t] = sacc;
+  }
+}
+
+// gw_proj[set*C + c, j] = sum of the channel's partials (fixed order), j < Kp.
+__global__ void b2b_pwgrad_reduce_kernel(const float* __restrict__ part, int nparts, int C, int Kp,
+                                         float* __restrict__ gw) {
+  const int c = blockIdx.x, v = threadIdx.x;  // v = set * 4 + j
+  if (v >= 12 || (v % 4) >= Kp) return;
+  const float* pc = part + int64_t(c) * nparts * 12 + v;
+  float sacc = 0.f;
+  for (int p = 0; p < nparts; ++p) sacc += pc[int64_t(p) * 12];
+  gw[int64_t((v / 4) * C + c) * Kp + (v % 4)] = sacc;
+}
+
 // gw_mixer[c, j] = sum over the channel's partials (fixed order); gskip[c] = its lag Km-1.
 __global__ void b2b_wgrad_reduce_kernel(const float* __restrict__ part, int nparts, int Km, float* __restrict__ gw,
                                         float* __restrict__ gskip) {
@@ -715,15 +976,6 @@ __device__ __forceinline__ void conv4_from_window(float (&out)[kConvPer], const 
 #pragma unroll
     for (int j = 0; j < 4; ++j) a = fmaf(w4[j], xv[e + 1 + j], a);
     out[e] = a;
-  }
-}
-
-// Projection taps left-padded to 4: w4[j] = w[j - (4 - Kp)].
-__device__ __forceinline__ void load_taps4(float (&w4)[4], const float* __restrict__ w, int Kp) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int s = j - (4 - Kp);
-    w4[j] = s >= 0 ? w[s >= 0 ? s : 0] : 0.f;
   }
 }
 
@@ -1045,17 +1297,21 @@ static int64_t b2b_wgrad_parts(int64_t B, int64_t L) { return B * ceil_div(ceil_
 
 template <int DT, int NS>
 static void launch_b2b_bwd_mfma(const void* g, const void* x, const float* wp, const float* wm, const float* skip,
-                                float* gwm, float* gskip, int B, int C, int L, int Kp, int Km, float* gp, float* gh,
-                                float* part, hipStream_t st) {
+                                void* gx, float* gwp, float* gwm, float* gskip, int B, int C, int L, int Kp, int Km,
+                                float* gp, float* gh, float* part, hipStream_t st) {
   using ET = typename Elem<DT>::T;
   dim3 grid(B * C, unsigned(ceil_div(ceil_div(L, kConvTile), kB2BSegTiles)));
   const size_t l1 = size_t(B2BBwd1Lds<NS>(Kp, Km).total) * sizeof(float);
   if (Kp <= 4) {
-    const size_t l2 = size_t(B2BBwd2Lds<DT, NS, true>(Kp, Km).total) * sizeof(float);
     hipLaunchKernelGGL((b2b_bwd1_mfma_kernel<DT, NS, true>), grid, dim3(kConvThreads), l1, st, (const ET*)g,
                        (const ET*)x, wp, wm, skip, gp, gh, part, B, C, L, Kp, Km);
-    hipLaunchKernelGGL((b2b_bwd2_mfma_kernel<DT, NS, true>), grid, dim3(kConvThreads), l2, st, (const ET*)x, wp, wm,
-                       skip, (const float*)gh, gp, C, L, Kp, Km);
+    // fused: gz, gk, gv, the input gradient and the projection weight-gradient partials
+    float* ppart = part + int64_t(C) * b2b_wgrad_parts(B, L) * Km;
+    const size_t l2 = size_t(B2BBwd2fLds<NS>(Km).total) * sizeof(float);
+    hipLaunchKernelGGL((b2b_bwd2f_mfma_kernel<DT, NS>), grid, dim3(kConvThreads), l2, st, (const ET*)x, wp, wm, skip,
+                       (const float*)gh, (const float*)gp, (ET*)gx, ppart, B, C, L, Kp, Km);
+    hipLaunchKernelGGL(b2b_pwgrad_reduce_kernel, dim3(C), dim3(64), 0, st, (const float*)ppart,
+                       int(b2b_wgrad_parts(B, L)), C, Kp, gwp);
   } else {
     const size_t l2 = size_t(B2BBwd2Lds<DT, NS, false>(Kp, Km).total) * sizeof(float);
     hipLaunchKernelGGL((b2b_bwd1_mfma_kernel<DT, NS, false>), grid, dim3(kConvThreads), l1, st, (const ET*)g,
@@ -1079,11 +1335,12 @@ static void launch_b2b_bwd(const void* g, const void* x, const float* wp, const 
   const int ns = mfma_steps_for(Km);
   if (ns) {
     switch (ns) {
-      case 12: launch_b2b_bwd_mfma<DT, 12>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
-      case 20: launch_b2b_bwd_mfma<DT, 20>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
-      case 36: launch_b2b_bwd_mfma<DT, 36>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
-      default: launch_b2b_bwd_mfma<DT, 68>(g, x, wp, wm, skip, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+      case 12: launch_b2b_bwd_mfma<DT, 12>(g, x, wp, wm, skip, gx, gwp, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+      case 20: launch_b2b_bwd_mfma<DT, 20>(g, x, wp, wm, skip, gx, gwp, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+      case 36: launch_b2b_bwd_mfma<DT, 36>(g, x, wp, wm, skip, gx, gwp, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
+      default: launch_b2b_bwd_mfma<DT, 68>(g, x, wp, wm, skip, gx, gwp, gwm, gskip, B, C, L, Kp, Km, gp, gh, zw, st); break;
     }
+    if (Kp <= 4) return;  // input and projection gradients came with bwd2
     dim3 grid3(B * 3 * C, unsigned(ceil_div(L, kConvTile)));
     hipLaunchKernelGGL((cconv_gx_kernel<DT, NSQ_DTYPE_F32>), grid3, dim3(kConvThreads), 0, st, (const float*)gp, wp,
                        (ET*)gx, 3 * C, L, Kp);
@@ -1146,9 +1403,10 @@ int nsq_b2b_causal_conv1d_fwd(const void* x, const float* weight_proj, const flo
 size_t nsq_b2b_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t Kp, int64_t Km) {
   (void)Kp;
   // gp [B,3C,L], gh [B,C,L], then z [B,C,L] (FMA path) or the weight-gradient
-  // partials [C][B * segments][Km] (matrix-core path, Km >= 16)
+  // partials [C][B * segments][Km] and [C][B * segments][12] (matrix-core
+  // path, Km >= 16)
   const int64_t E = B * C * L;
-  const int64_t tail = Km >= 16 ? C * b2b_wgrad_parts(B, L) * Km : E;
+  const int64_t tail = Km >= 16 ? C * b2b_wgrad_parts(B, L) * (Km + 12) : E;
   return size_t(4 * E + (tail > E ? tail : E)) * sizeof(float);
 }
 
