@@ -18,6 +18,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --workload cfg1|cfg2|cfg4|cfg5   (the other benchmark
            configurations, for the per-config report; same JSON fields, value =
            algorithmic GB/s of the phase BASELINE.md quotes for that config)
+       python bench.py --workload cfg2-fwd-bwd   (config 2's block with its
+           backward, report-only)
        python bench.py --copy-calibration   (one plain copy kernel of known size,
                                              for scaling rocprof FETCH/WRITE_SIZE)
 """
@@ -166,6 +168,22 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
         def step():
             with torch.no_grad():
                 CC.b2b_causal_conv1d(x, wp, wm, None)
+    elif name == "cfg2-fwd-bwd":
+        # report-only: the config-2 block with its backward (autograd), skip = 0 as in config 2
+        B, C, L, Kp, Km = 4, 4096, 8192, 3, 128
+        x = torch.randn(B, 3 * C, L, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+        wp = torch.randn(3 * C, Kp, device=dev, generator=gen).requires_grad_(True)
+        wm = (torch.randn(C, Km, device=dev, generator=gen) / Km ** 0.5).requires_grad_(True)
+        sk = torch.zeros(C, device=dev, requires_grad=True)
+        g = torch.randn(B, C, L, device=dev, generator=gen).to(torch.bfloat16)
+        phase, dtype = "fwd+bwd", "f32"
+        nbytes = algorithmic_bytes_b2b(B, C, L, Kp, Km, 2, "fwd+bwd")
+        desc = ("cfg2-fwd-bwd: B2B short-conv block fwd+bwd (k=3 proj -> gate -> k=128 mixer -> gate), "
+                "B=4 L=8192 D=4096, bf16 I/O")
+
+        def step():
+            x.grad = wp.grad = wm.grad = sk.grad = None
+            CC.b2b_causal_conv1d(x, wp, wm, sk).backward(g)
     elif name in ("cfg4", "cfg5"):
         nd = 2 if name == "cfg4" else 3
         B, C, size, sig = (16, 384, 128, (4.0, 64.0)) if nd == 2 else (2, 128, 64, (2.0, 32.0))
@@ -213,7 +231,7 @@ def main() -> None:
     ap.add_argument("--cpu-channels", type=int, default=1024)
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -156,11 +156,24 @@ def radial_filter(C: int, size: int, sig_lo: float, sig_hi: float, nd: int, gen:
     return h * torch.exp(-r[None] / sig.view(-1, *([1] * nd)))
 
 
-def algorithmic_bytes_b2b(B: int, C: int, L: int, Kp: int, Km: int, itemsize: int) -> int:
-    """Forward of the fused B2B block: x [B, 3C, L] read, y [B, C, L] written
-    (itemsize each), fp32 depthwise weights [3C, Kp] and [C, Km] read.
-    Config 2 (B=4, C=4096, L=8192, Kp=3, Km=128, bf16): 1,075,986,432 B."""
-    return B * 3 * C * L * itemsize + B * C * L * itemsize + (3 * C * Kp + C * Km) * 4
+def algorithmic_bytes_b2b(B: int, C: int, L: int, Kp: int, Km: int, itemsize: int, phase: str = "fwd") -> int:
+    """Compulsory HBM bytes of the fused B2B block.
+
+    Forward: x [B, 3C, L] read, y [B, C, L] written (itemsize each), fp32
+    depthwise weights [3C, Kp] and [C, Km] read.  Config 2 (B=4, C=4096,
+    L=8192, Kp=3, Km=128, bf16): 1,075,986,432 B.  Backward: g [B, C, L] and x
+    read, gx [B, 3C, L] written, the weights and the skip [C] read and their
+    fp32 gradients written."""
+    E = B * C * L
+    W = 3 * C * Kp + C * Km
+    if phase == "fwd":
+        return 3 * E * itemsize + E * itemsize + W * 4
+    if phase == "bwd":
+        return E * itemsize + 3 * E * itemsize + 3 * E * itemsize + 2 * (W + C) * 4
+    if phase == "fwd+bwd":
+        return algorithmic_bytes_b2b(B, C, L, Kp, Km, itemsize, "fwd") + algorithmic_bytes_b2b(
+            B, C, L, Kp, Km, itemsize, "bwd")
+    raise ValueError(phase)
 
 
 def algorithmic_bytes_nd(B: int, C: int, S, K, itemsize: int, phase: str) -> int:
