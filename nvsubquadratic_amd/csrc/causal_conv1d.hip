@@ -64,10 +64,241 @@ __global__ __launch_bounds__(kConvThreads) void cconv_gpre_silu_kernel(const typ
   }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core path for K >= 16 taps: a workgroup walks a segment of
+// kConvSegTiles tiles of one (b, c) row; per tile the source window (fp32,
+// padded as ToeplitzMfma reads it) is staged from registers loaded during the
+// previous tile, the MFMA band gives acc[p] for the tile's 2048 outputs, and
+// the epilogue stores from the accumulator layout through a range-checked row
+// buffer.  Modes:
+//   FWD (ACT identity / silu): src = x from n0 - K + 1, y = act(acc + bias);
+//   GPRE: the same conv, out (fp32) = gy * silu'(acc + bias);
+//   CORR: src = gp from n0 on the reversed band, gx = acc
+//         (gx[n] = sum_j w[j] gp[n + K - 1 - j]).
+// ---------------------------------------------------------------------------
+enum { CC_FWD_ID = 0, CC_FWD_SILU = 1, CC_GPRE = 2, CC_CORR = 3 };
+constexpr int kConvSegTiles = 4;
+
+template <int DS, int DO, int NS, int MODE>
+__global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3))) void cconv_mfma_kernel(
+    const typename Elem<DS>::T* __restrict__ src, const float* __restrict__ w, const float* __restrict__ bias,
+    const typename Elem<DO>::T* __restrict__ gy, void* __restrict__ out, int C, int L, int K) {
+  constexpr int ZW = mfma_src_count<NS>();
+  constexpr int ZWORDS = (conv_pad_words(ZW) + 7) & ~7;
+  __shared__ __align__(16) float zp[ZWORDS];
+  __shared__ __align__(16) float wl[kConvWeightFloats];
+  const int64_t row = blockIdx.x;
+  const int c = int(row % C);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int t_begin = int(blockIdx.y) * kConvSegTiles;
+  const int t_end = min(ntiles, t_begin + kConvSegTiles);
+  const int t = int(threadIdx.x);
+  constexpr bool CORR = MODE == CC_CORR;
+  if (CORR)
+    stage_weights<true>(wl, w + int64_t(c) * K, K);
+  else
+    stage_weights<false>(wl, w + int64_t(c) * K, K);
+  const int shift = CORR ? 0 : K - 1;  // window word m is src[n0 - shift + m]
+  RowStage<DS, ZW> sw;
+  sw.load(src + row * L, int64_t(t_begin) * kConvTile - shift, 0, L);
+  __syncthreads();  // weights staged
+  ToeplitzMfma<NS> tm;
+  tm.load_weights(wl, K);
+  const float b0 = (!CORR && bias) ? bias[c] : 0.f;
+  const RowBuf<DO, false> ob((typename Elem<DO>::T*)out + row * L, L);
+  const RowBuf<NSQ_DTYPE_F32, false> ofb((float*)out + row * L, L);
+  const RowBuf<DO, false> gyb(gy + row * L, L);
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+  for (int ti = t_begin; ti < t_end; ++ti) {
+    const int64_t n0 = int64_t(ti) * kConvTile;
+#pragma unroll
+    for (int it = 0; it < RowStage<DS, ZW>::IT; ++it) {
+      const int m = t + it * kConvThreads;
+      if (m < ZW) zp[conv_pad(m)] = RowBuf<DS, false>::bits_to_f32(sw.v[it]);
+    }
+    __syncthreads();
+    if (ti + 1 < t_end) sw.load(src + row * L, n0 + kConvTile - shift, 0, L);
+    nsq_f32x4_t acc0, acc1;
+    tm.run2(zp, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = 16 * (16 * (wave + h * kConvWaves) + 4 * (l >> 4) + r) + (l & 15);
+        const float a = (h ? acc1[r] : acc0[r]) + b0;
+        if constexpr (MODE == CC_FWD_ID) {
+          ob.store_elem(n0 + p, a);
+        } else if constexpr (MODE == CC_FWD_SILU) {
+          ob.store_elem(n0 + p, act_fwd<NSQ_ACT_SILU>(a));
+        } else if constexpr (MODE == CC_GPRE) {
+          ofb.store_elem(n0 + p, gyb.elem(n0 + p) * dsilu(a));
+        } else {
+          ob.store_elem(n0 + p, a);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Weight / bias gradients on the matrix cores (K >= 16): per tile,
+//   D[i][t] += sum_a gp[16a + i] * xwin[16a + t],  xwin[m] = x[n0 - K + 1 + m],
+// gw[j] = sum_i D[i][i + j] over the workgroup's tiles (one channel, a segment
+// of its (b, tile) sequence), gb = sum gp; fixed-order reduction into a
+// per-workgroup partial [K + 1], summed by cconv_wgrad_reduce_kernel.
+template <int DG, int DX, int NS>
+__global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2))) void cconv_wgrad_mfma_kernel(
+    const typename Elem<DG>::T* __restrict__ gp, const typename Elem<DX>::T* __restrict__ x, float* __restrict__ part,
+    int B, int C, int L, int K) {
+  constexpr int ZW = mfma_src_count<NS>();
+  constexpr int ZWORDS = (conv_pad_words(ZW) + 7) & ~7;
+  constexpr int TG = NS / 4;
+  constexpr int RW = 4 * NS;
+  static_assert(16 * RW <= ZWORDS + kConvTile, "cconv_wgrad_mfma_kernel: reduction area");
+  __shared__ __align__(16) float sm[ZWORDS + kConvTile];
+  float* zp = sm;
+  float* gs = sm + ZWORDS;  // gp of the tile, plain
+  const int c = int(blockIdx.x);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int g_begin = int(blockIdx.y) * kConvSegTiles;
+  const int g_end = min(B * ntiles, g_begin + kConvSegTiles);
+  const int t = int(threadIdx.x);
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+  const int kk = l >> 4, li = l & 15;
+  nsq_f32x4_t D[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) D[tg] = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float bacc = 0.f;
+  for (int g = g_begin; g < g_end; ++g) {
+    const int b = g / ntiles, ti = g - b * ntiles;
+    const int64_t row = int64_t(b) * C + c;
+    const int64_t n0 = int64_t(ti) * kConvTile;
+    {
+      RowStage<DX, ZW> sx;
+      RowStage<DG, kConvTile> sg;
+      sx.load(x + row * L, n0 - (K - 1), 0, L);
+      sg.load(gp + row * L, n0, 0, L);
+#pragma unroll
+      for (int it = 0; it < RowStage<DX, ZW>::IT; ++it) {
+        const int m = t + it * kConvThreads;
+        if (m < ZW) zp[conv_pad(m)] = RowBuf<DX, false>::bits_to_f32(sx.v[it]);
+      }
+      sg.store(gs, kConvTile);
+#pragma unroll
+      for (int it = 0; it < RowStage<DG, kConvTile>::IT; ++it) bacc += RowBuf<DG, false>::bits_to_f32(sg.v[it]);
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (int a0 = 32 * wave; a0 < 32 * wave + 32; a0 += 4) {
+      const float av = gs[16 * (a0 + kk) + li];
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg) {
+        const float bv = zp[20 * (a0 + kk + tg) + li];
+        D[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, D[tg], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  float* red = sm;
+  for (int w = 0; w < kConvWaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float& dst = red[(4 * kk + r) * RW + 16 * tg + li];
+          dst = (w == 0 ? 0.f : dst) + D[tg][r];
+        }
+    }
+    __syncthreads();
+  }
+  const int nparts = int(gridDim.y);
+  float* pw = part + (int64_t(c) * nparts + blockIdx.y) * (K + 1);
+  if (t < K) {
+    float sacc = 0.f;
+    for (int i = 0; i < 16; ++i) sacc += red[i * RW + i + t];
+    pw[t] = sacc;
+  }
+  __syncthreads();
+  red[t] = bacc;  // bias partial: fixed-order sum over the threads
+  __syncthreads();
+  if (t == 0) {
+    float sacc = 0.f;
+    for (int i = 0; i < kConvThreads; ++i) sacc += red[i];
+    pw[K] = sacc;
+  }
+}
+
+__global__ void cconv_wgrad_reduce_kernel(const float* __restrict__ part, int nparts, int K, float* __restrict__ gw,
+                                          float* __restrict__ gb) {
+  const int c = blockIdx.x, j = threadIdx.x;
+  if (j > K) return;
+  const float* pc = part + int64_t(c) * nparts * (K + 1) + j;
+  float sacc = 0.f;
+  for (int p = 0; p < nparts; ++p) sacc += pc[int64_t(p) * (K + 1)];
+  if (j < K)
+    gw[int64_t(c) * K + j] = sacc;
+  else if (gb)
+    gb[c] = sacc;
+}
+
+static int64_t cconv_wgrad_parts(int64_t B, int64_t L) {
+  return ceil_div(B * ceil_div(L, kConvTile), kConvSegTiles);
+}
+
+template <int DT, int NS>
+static void launch_fwd_mfma(const void* x, const float* w, const float* bias, void* y, int act, int B, int C, int L,
+                            int K, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  dim3 grid(B * C, unsigned(ceil_div(ceil_div(L, kConvTile), kConvSegTiles)));
+  if (act == NSQ_ACT_SILU)
+    hipLaunchKernelGGL((cconv_mfma_kernel<DT, DT, NS, CC_FWD_SILU>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w,
+                       bias, (const ET*)nullptr, y, C, L, K);
+  else
+    hipLaunchKernelGGL((cconv_mfma_kernel<DT, DT, NS, CC_FWD_ID>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w,
+                       bias, (const ET*)nullptr, y, C, L, K);
+}
+
+template <int DT, int NS>
+static void launch_bwd_mfma(const void* gy, const void* x, const float* w, const float* bias, void* gx, float* gw,
+                            float* gb, int act, int B, int C, int L, int K, float* ws, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  dim3 grid(B * C, unsigned(ceil_div(ceil_div(L, kConvTile), kConvSegTiles)));
+  const int64_t nparts = cconv_wgrad_parts(B, L);
+  dim3 wgrid(C, unsigned(nparts));
+  if (act == NSQ_ACT_SILU) {
+    float* gpre = ws;
+    float* part = ws + int64_t(B) * C * L;
+    hipLaunchKernelGGL((cconv_mfma_kernel<DT, DT, NS, CC_GPRE>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w,
+                       bias, (const ET*)gy, (void*)gpre, C, L, K);
+    hipLaunchKernelGGL((cconv_mfma_kernel<NSQ_DTYPE_F32, DT, NS, CC_CORR>), grid, dim3(kConvThreads), 0, st,
+                       (const float*)gpre, w, (const float*)nullptr, (const ET*)nullptr, gx, C, L, K);
+    hipLaunchKernelGGL((cconv_wgrad_mfma_kernel<NSQ_DTYPE_F32, DT, NS>), wgrid, dim3(kConvThreads), 0, st,
+                       (const float*)gpre, (const ET*)x, part, B, C, L, K);
+    hipLaunchKernelGGL(cconv_wgrad_reduce_kernel, dim3(C), dim3(kConvThreads + 64), 0, st, (const float*)part,
+                       int(nparts), K, gw, gb);
+  } else {
+    float* part = ws;
+    hipLaunchKernelGGL((cconv_mfma_kernel<DT, DT, NS, CC_CORR>), grid, dim3(kConvThreads), 0, st, (const ET*)gy, w,
+                       (const float*)nullptr, (const ET*)nullptr, gx, C, L, K);
+    hipLaunchKernelGGL((cconv_wgrad_mfma_kernel<DT, DT, NS>), wgrid, dim3(kConvThreads), 0, st, (const ET*)gy,
+                       (const ET*)x, part, B, C, L, K);
+    hipLaunchKernelGGL(cconv_wgrad_reduce_kernel, dim3(C), dim3(kConvThreads + 64), 0, st, (const float*)part,
+                       int(nparts), K, gw, gb);
+  }
+}
+
 template <int DT>
 static void launch_fwd(const void* x, const float* w, const float* bias, void* y, int act, int B, int C, int L, int K,
                        hipStream_t st) {
   using ET = typename Elem<DT>::T;
+  switch (mfma_steps_for(K)) {  // matrix cores from 16 taps up
+    case 12: return launch_fwd_mfma<DT, 12>(x, w, bias, y, act, B, C, L, K, st);
+    case 20: return launch_fwd_mfma<DT, 20>(x, w, bias, y, act, B, C, L, K, st);
+    case 36: return launch_fwd_mfma<DT, 36>(x, w, bias, y, act, B, C, L, K, st);
+    case 68: return launch_fwd_mfma<DT, 68>(x, w, bias, y, act, B, C, L, K, st);
+    default: break;
+  }
   dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
   if (act == NSQ_ACT_SILU)
     hipLaunchKernelGGL((cconv_fwd_kernel<DT, NSQ_ACT_SILU>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w, bias,
@@ -81,6 +312,13 @@ template <int DT>
 static void launch_bwd(const void* gy, const void* x, const float* w, const float* bias, void* gx, float* gw,
                        float* gb, int act, int B, int C, int L, int K, float* ws, hipStream_t st) {
   using ET = typename Elem<DT>::T;
+  switch (mfma_steps_for(K)) {
+    case 12: return launch_bwd_mfma<DT, 12>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
+    case 20: return launch_bwd_mfma<DT, 20>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
+    case 36: return launch_bwd_mfma<DT, 36>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
+    case 68: return launch_bwd_mfma<DT, 68>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
+    default: break;
+  }
   dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
   if (act == NSQ_ACT_SILU) {
     hipLaunchKernelGGL((cconv_gpre_silu_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)gy, (const ET*)x, w,
@@ -114,8 +352,11 @@ using namespace nsq;
 extern "C" {
 
 size_t nsq_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t K, int activation) {
-  (void)K;
-  return activation == NSQ_ACT_SILU ? size_t(B * C * L) * sizeof(float) : 0;
+  // silu: gy * silu'(pre) [B, C, L]; K >= 16 (matrix cores): then the weight /
+  // bias gradient partials [C][parts][K + 1]
+  const int64_t pre = activation == NSQ_ACT_SILU ? B * C * L : 0;
+  const int64_t parts = (K >= 16 && K <= kConvMaxK) ? C * cconv_wgrad_parts(B, L) * (K + 1) : 0;
+  return size_t(pre + parts) * sizeof(float);
 }
 
 int nsq_causal_conv1d_fwd(const void* x, const float* weight, const float* bias, void* y, int dtype, int activation,

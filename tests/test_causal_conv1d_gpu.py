@@ -101,6 +101,31 @@ def test_halo_before_row_start_reads_zero(K):
     assert rel_l2(w.grad, wg.grad) < 1e-5
 
 
+@pytest.mark.parametrize("K", [15, 16, 17, 33, 34, 65, 66, 129, 130, 256])
+@pytest.mark.parametrize("act", ["identity", "silu"])
+def test_tap_counts_across_matrix_core_plans(K, act):
+    """Direct conv from 16 taps runs as banded Toeplitz MFMA products (forward,
+    the silu pre-activation gradient, the input-gradient correlation and the
+    weight gradient); 15 taps stay on the FMA loop.  Ragged length, bias, two
+    batches; forward and gradients against a float64 reference."""
+    torch.manual_seed(200 + K)
+    B, C, L = 2, 3, 4700
+    x = torch.randn(B, C, L, dtype=torch.float64, requires_grad=True)
+    w = (torch.randn(C, K, dtype=torch.float64) / K ** 0.5).requires_grad_(True)
+    b = torch.randn(C, dtype=torch.float64, requires_grad=True)
+    y_ref = causal_conv1d_torch(x, w, b, act)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, wg, bg = (t.detach().float().cuda().requires_grad_(True) for t in (x, w, b))
+    y = causal_conv1d(xg, wg, bg, act)
+    y.backward(g.float().cuda())
+    assert rel_l2(y_ref, y.detach().double()) < 1e-5
+    assert rel_l2(y_ref[..., :K + 2], y.detach()[..., :K + 2].double()) < 1e-5
+    for ref, got in ((x, xg), (w, wg), (b, bg)):
+        assert rel_l2(ref.grad, got.grad.double()) < 1e-5
+    assert rel_l2(x.grad[..., -K - 2:], xg.grad[..., -K - 2:].double()) < 1e-5
+
+
 @pytest.mark.parametrize("Kp,Km", [(2, 3), (4, 4), (5, 7), (8, 1), (1, 9), (7, 33)])
 def test_b2b_halo_before_row_start_reads_zero(Kp, Km):
     """B2B forward and backward near the row start for several halo widths."""
