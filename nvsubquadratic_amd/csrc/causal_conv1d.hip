@@ -288,6 +288,120 @@ static void launch_bwd_mfma(const void* gy, const void* x, const float* w, const
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward for K <= 4 taps in one register-resident pass (the Hyena short-conv
+// case).  Thread t of a tile owns outputs n = n0 + 8t + e, e < 8; its x and gy
+// windows [n0 + 8t - 4, n0 + 8t + 16) come straight from HBM (two Win12 each).
+// With the taps left-padded to 4 (w4[j] = w[j - (4 - K)]):
+//   pre[n]  = bias + sum_j w4[j] x[n - 3 + j],  gpre = gy * silu'(pre) (or gy)
+//   gx[n]   = sum_s wr4[s] gpre[n + s],          wr4[s] = w[K - 1 - s] (s < K)
+//   gw4[j] += gpre[n] x[n - 3 + j],              gb += gpre[n]
+// gpre is recomputed at the 3 positions past the thread's 8 (its neighbour
+// owns them); the weight / bias sums stay in registers over the workgroup's
+// tiles (one channel, a segment of its (b, tile) sequence) and are reduced in
+// a fixed order into a per-workgroup partial [K + 1].
+// ---------------------------------------------------------------------------
+template <int DT, bool AL, int ACT>
+__global__ __launch_bounds__(kConvThreads) void cconv_bwd_short_kernel(
+    const typename Elem<DT>::T* __restrict__ gy, const typename Elem<DT>::T* __restrict__ x,
+    const float* __restrict__ w, const float* __restrict__ bias, typename Elem<DT>::T* __restrict__ gx,
+    float* __restrict__ part, int B, int C, int L, int K) {
+  __shared__ float red[5 * kConvThreads];
+  const int c = int(blockIdx.x);
+  const int ntiles = (L + kConvTile - 1) / kConvTile;
+  const int g_begin = int(blockIdx.y) * kConvSegTiles;
+  const int g_end = min(B * ntiles, g_begin + kConvSegTiles);
+  const int t = int(threadIdx.x);
+  float w4[4], wr4[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int sl = j - (4 - K);
+    w4[j] = sl >= 0 ? w[int64_t(c) * K + (sl >= 0 ? sl : 0)] : 0.f;
+    wr4[j] = j < K ? w[int64_t(c) * K + (j < K ? K - 1 - j : 0)] : 0.f;
+  }
+  const float b0 = bias ? bias[c] : 0.f;
+  float gw4[4] = {0.f, 0.f, 0.f, 0.f};
+  float gbs = 0.f;
+  for (int g = g_begin; g < g_end; ++g) {
+    const int b = g / ntiles, ti = g - b * ntiles;
+    const int64_t row = int64_t(b) * C + c;
+    const int base = ti * kConvTile + kConvPer * t;
+    const RowBuf<DT, false> xb(x + row * L, L), gb(gy + row * L, L);
+    Win12<DT, AL> x0, x1, g0, g1;
+    x0.load(xb, base);
+    x1.load(xb, base + 8);
+    g0.load(gb, base);
+    g1.load(gb, base + 8);
+    float xw[20], gw[20];  // index i <-> position base - 4 + i
+#pragma unroll
+    for (int i = 0; i < 20; ++i) {
+      xw[i] = i < 12 ? x0.at(i) : x1.at(i - 8);
+      gw[i] = i < 12 ? g0.at(i) : g1.at(i - 8);
+    }
+    float gp[kConvPer + 3];  // gpre at base + e, e < 11
+#pragma unroll
+    for (int e = 0; e < kConvPer + 3; ++e) {
+      float pre = b0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pre = fmaf(w4[j], xw[e + 1 + j], pre);
+      gp[e] = (ACT == NSQ_ACT_SILU) ? gw[e + 4] * dsilu(pre) : gw[e + 4];
+    }
+    float out[kConvPer];
+#pragma unroll
+    for (int e = 0; e < kConvPer; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int sidx = 0; sidx < 4; ++sidx) a = fmaf(wr4[sidx], gp[e + sidx], a);
+      out[e] = a;
+      gbs += gp[e];  // positions >= L have gy = 0, so gpre = 0
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gw4[j] = fmaf(gp[e], xw[e + 1 + j], gw4[j]);
+    }
+    const RowBuf<DT, AL> ob(gx + row * L, L);
+#pragma unroll
+    for (int e = 0; e < kConvPer; e += 2) ob.store_pair(base + e, make_float2(out[e], out[e + 1]));
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) red[j * kConvThreads + t] = gw4[j];
+  red[4 * kConvThreads + t] = gbs;
+  __syncthreads();
+  if (t < 5) {
+    float sacc = 0.f;
+    for (int i = 0; i < kConvThreads; ++i) sacc += red[t * kConvThreads + i];
+    // left-padded tap t -> weight index t - (4 - K); slot 4 -> the bias
+    const int nparts = int(gridDim.y);
+    float* pw = part + (int64_t(c) * nparts + blockIdx.y) * (K + 1);
+    if (t == 4)
+      pw[K] = sacc;
+    else if (t >= 4 - K)
+      pw[t - (4 - K)] = sacc;
+  }
+}
+
+template <int DT>
+static void launch_bwd_short(const void* gy, const void* x, const float* w, const float* bias, void* gx, float* gw,
+                             float* gb, int act, int B, int C, int L, int K, float* ws, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  const int64_t nparts = cconv_wgrad_parts(B, L);
+  dim3 grid(C, unsigned(nparts));
+  const bool al = L % (DT == NSQ_DTYPE_F32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(gy) & 15) == 0 && (reinterpret_cast<uintptr_t>(gx) & 15) == 0;
+  auto go = [&](auto al_c, auto act_c) {
+    hipLaunchKernelGGL((cconv_bwd_short_kernel<DT, decltype(al_c)::value, decltype(act_c)::value>), grid,
+                       dim3(kConvThreads), 0, st, (const ET*)gy, (const ET*)x, w, bias, (ET*)gx, ws, B, C, L, K);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using SILU = std::integral_constant<int, NSQ_ACT_SILU>;
+  using IDN = std::integral_constant<int, NSQ_ACT_IDENTITY>;
+  if (al)
+    act == NSQ_ACT_SILU ? go(T_{}, SILU{}) : go(T_{}, IDN{});
+  else
+    act == NSQ_ACT_SILU ? go(F_{}, SILU{}) : go(F_{}, IDN{});
+  hipLaunchKernelGGL(cconv_wgrad_reduce_kernel, dim3(C), dim3(kConvThreads + 64), 0, st, (const float*)ws,
+                     int(nparts), K, gw, gb);
+}
+
 template <int DT>
 static void launch_fwd(const void* x, const float* w, const float* bias, void* y, int act, int B, int C, int L, int K,
                        hipStream_t st) {
@@ -312,6 +426,7 @@ template <int DT>
 static void launch_bwd(const void* gy, const void* x, const float* w, const float* bias, void* gx, float* gw,
                        float* gb, int act, int B, int C, int L, int K, float* ws, hipStream_t st) {
   using ET = typename Elem<DT>::T;
+  if (K <= 4) return launch_bwd_short<DT>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
   switch (mfma_steps_for(K)) {
     case 12: return launch_bwd_mfma<DT, 12>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
     case 20: return launch_bwd_mfma<DT, 20>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
@@ -352,8 +467,10 @@ using namespace nsq;
 extern "C" {
 
 size_t nsq_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t K, int activation) {
-  // silu: gy * silu'(pre) [B, C, L]; K >= 16 (matrix cores): then the weight /
-  // bias gradient partials [C][parts][K + 1]
+  // K <= 4 (one fused pass): the weight / bias gradient partials
+  // [C][parts][K + 1] only; otherwise silu: gy * silu'(pre) [B, C, L], and for
+  // K >= 16 (matrix cores) the partials after it
+  if (K >= 1 && K <= 4) return size_t(C * cconv_wgrad_parts(B, L) * (K + 1)) * sizeof(float);
   const int64_t pre = activation == NSQ_ACT_SILU ? B * C * L : 0;
   const int64_t parts = (K >= 16 && K <= kConvMaxK) ? C * cconv_wgrad_parts(B, L) * (K + 1) : 0;
   return size_t(pre + parts) * sizeof(float);

@@ -304,6 +304,49 @@ inline int mfma_steps_for(int K) {
   return 68;  // K <= 257
 }
 
+// Samples x[n - 4 + i], i < 12, of one row as raw bits.  AL (16-bit types:
+// len % 8 == 0; fp32: len % 4 == 0; 16-byte aligned rows): n is a multiple of
+// 8 and the window is three aligned vector loads that lie wholly inside or
+// wholly outside [0, len); otherwise twelve element loads.  Positions before
+// the row read as zero (offset 2^31, see RowBuf::elem_halo).
+template <int DT, bool AL>
+struct Win12 {
+  static constexpr bool HALF = DT != NSQ_DTYPE_F32;
+  static constexpr int W = (HALF && AL) ? 6 : 12;
+  uint32_t w[W];
+  __device__ __forceinline__ void load(const RowBuf<DT, false>& rb, int n) {
+    if constexpr (AL) {
+      constexpr int ES = HALF ? 2 : 4;
+      int off_h = n < 4 ? int(0x80000000u) : (n - 4) * ES;
+      asm volatile("" : "+v"(off_h));
+      const int off_m = n * ES;
+      if constexpr (HALF) {
+        const auto h = __builtin_amdgcn_raw_buffer_load_b64(rb.r, off_h, 0, 0);
+        const auto m = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_m, 0, 0);
+        w[0] = h[0]; w[1] = h[1];
+        w[2] = m[0]; w[3] = m[1]; w[4] = m[2]; w[5] = m[3];
+      } else {
+        const auto h = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_h, 0, 0);
+        const auto m0 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_m, 0, 0);
+        const auto m1 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off_m + 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { w[i] = h[i]; w[4 + i] = m0[i]; w[8 + i] = m1[i]; }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 12; ++i) w[i] = rb.elem_halo_bits(n - 4 + i);
+    }
+  }
+  __device__ __forceinline__ float at(int i) const {  // i is a compile-time constant after unrolling
+    if constexpr (HALF && AL) {
+      const uint32_t v = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
+      return RowBuf<DT, false>::bits_to_f32(v);
+    } else {
+      return RowBuf<DT, false>::bits_to_f32(w[i]);
+    }
+  }
+};
+
 // Kernels shared by the causal conv and B2B backward passes.
 // gx[i] = sum_j w[j] gp[i + K - 1 - j]  (gp = gpre in GT precision).  grid as forward.
 template <int DT, int GT>

@@ -101,6 +101,54 @@ def test_halo_before_row_start_reads_zero(K):
     assert rel_l2(w.grad, wg.grad) < 1e-5
 
 
+@pytest.mark.parametrize("K", [1, 2, 3, 4])
+@pytest.mark.parametrize("L", [1, 13, 4103, 18432])
+def test_short_taps_backward_across_tiles_and_batches(K, L):
+    """Up to 4 taps the whole backward is one register-resident pass whose
+    weight/bias partials cover runs of (batch, tile) pairs; with 3 batches and
+    up to 9 tiles per row those runs cross row ends.  Ragged lengths take the
+    element-load path, multiples of 8 the vector path."""
+    torch.manual_seed(100 + K)
+    B, C = 3, 6
+    x = torch.randn(B, C, L, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(C, K, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(C, dtype=torch.float64, requires_grad=True)
+    y_ref = causal_conv1d_torch(x, w, b, "silu")
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg = x.detach().float().cuda().requires_grad_(True)
+    wg = w.detach().float().cuda().requires_grad_(True)
+    bg = b.detach().float().cuda().requires_grad_(True)
+    y = causal_conv1d(xg, wg, bg, "silu")
+    y.backward(g.float().cuda())
+    assert rel_l2(y_ref, y.double()) < 1e-5
+    assert rel_l2(x.grad, xg.grad.double()) < 1e-5
+    assert rel_l2(w.grad, wg.grad.double()) < 1e-5
+    assert rel_l2(b.grad, bg.grad.double()) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_short_taps_backward_low_precision_io(dtype):
+    torch.manual_seed(5)
+    x = torch.randn(2, 16, 3000).to(dtype)
+    w = torch.randn(16, 4)
+    b = torch.randn(16)
+    xr = x.float().requires_grad_(True)
+    wr, br = w.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    y_ref = causal_conv1d_torch(xr, wr, br, "silu")
+    g = torch.randn_like(y_ref).to(dtype)
+    y_ref.backward(g.float())
+    xg = x.cuda().requires_grad_(True)
+    wg, bg = w.cuda().requires_grad_(True), b.cuda().requires_grad_(True)
+    y = causal_conv1d(xg, wg, bg, "silu")
+    y.backward(g.cuda())
+    assert xg.grad.dtype == dtype
+    assert rel_l2(y_ref, y.float()) < 2e-2
+    assert rel_l2(xr.grad, xg.grad.float()) < 2e-2
+    assert rel_l2(wr.grad, wg.grad) < 2e-2
+    assert rel_l2(br.grad, bg.grad) < 2e-2
+
+
 @pytest.mark.parametrize("K", [15, 16, 17, 33, 34, 65, 66, 129, 130, 256])
 @pytest.mark.parametrize("act", ["identity", "silu"])
 def test_tap_counts_across_matrix_core_plans(K, act):
