@@ -290,6 +290,17 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
   __syncthreads();
 }
 
+// First-pass loader over values already in registers: the pass calls its
+// loader in a fixed, fully unrolled order (butterfly i, then point r), so the
+// values are handed out in that order and every index is a constant after
+// unrolling.
+template <int NV>
+struct RegStream {
+  const float2 (&v)[NV];
+  int k = 0;
+  __device__ __forceinline__ float2 operator()(int, int) { return v[k++]; }
+};
+
 template <int LOGN, int LOGNS, bool INV, int M, int T, bool TMAJOR, class LDF, class STL, class LDL, class STF>
 __device__ __forceinline__ void fft_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last,
                                         const float2* __restrict__ tw) {
@@ -533,6 +544,35 @@ struct RowBuf {
       }
     } else {
       return make_float2(elem(i), elem(i + 1));
+    }
+  }
+  // load_pair split into the access and the conversion, so that a loader can
+  // keep a pair's raw bits in flight across other work (a prefetch).
+  struct PairBits {
+    uint32_t a, b;
+  };
+  __device__ __forceinline__ PairBits load_pair_bits(int64_t i) const {
+    const int off = int(i) * int(sizeof(ET));
+    if constexpr (ALIGNED && DT == NSQ_DTYPE_F32) {
+      const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+      return PairBits{u[0], u[1]};
+    } else if constexpr (ALIGNED) {
+      return PairBits{__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0), 0u};
+    } else if constexpr (DT == NSQ_DTYPE_F32) {
+      return PairBits{__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0),
+                      __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, 0)};
+    } else {
+      return PairBits{__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0),
+                      __builtin_amdgcn_raw_buffer_load_b16(r, off + 2, 0, 0)};
+    }
+  }
+  __device__ __forceinline__ static float2 pair_from_bits(PairBits p) {
+    if constexpr (ALIGNED && DT == NSQ_DTYPE_BF16) {
+      return make_float2(__uint_as_float(p.a << 16), __uint_as_float(p.a & 0xffff0000u));
+    } else if constexpr (ALIGNED && DT == NSQ_DTYPE_F16) {
+      return __half22float2(__builtin_bit_cast(__half2, p.a));
+    } else {
+      return make_float2(bits_to_f32(p.a), bits_to_f32(p.b));
     }
   }
   __device__ __forceinline__ void store_pair(int64_t i, float2 v) const {

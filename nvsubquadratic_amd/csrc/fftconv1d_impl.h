@@ -343,23 +343,52 @@ struct TwiddledColumnStore {
   }
 };
 
+// Column tiles per workgroup.  Workgroup w runs tiles w, w + G, w + 2G, ...
+// (G = grid size), so the workgroups resident together still cover adjacent
+// column blocks of the same rows, and each prefetches its next tile's
+// first-pass inputs while it transforms the current one.
+constexpr int kColTilesPerWG = 8;
+
 // col_fwd: A[row][k1][n2] = W_N^{n2 k1} * sum_{n1} z[N2 n1 + n2] W_{N1}^{n1 k1}.
-// grid = rows * (N2 / M), column block fastest so that the workgroups running
-// together cover whole rows of the signal and of the workspace.
+// Tile t = row * (N2 / M) + column block: column block fastest.  The first
+// pass is one radix-R butterfly per thread (T = M * N1 / R); its R input
+// pairs for the next tile are loaded as raw bits before the current tile's
+// passes run and converted when that tile starts.
 template <int LOGN1, int LOGN, int DT, bool AL>
-__global__ __launch_bounds__(ColCfg<LOGN1>::T) void col_fwd_kernel(RealRows<DT> src, float2* __restrict__ ws,
-                                                                    const float2* __restrict__ tw) {
+__global__ __launch_bounds__(ColCfg<LOGN1>::T) __attribute__((amdgpu_waves_per_eu(4))) void col_fwd_kernel(
+    RealRows<DT> src, float2* __restrict__ ws, const float2* __restrict__ tw, int64_t ntiles) {
   using C = ColCfg<LOGN1>;
+  using RB = RowBuf<DT, AL>;
   constexpr int N2 = 1 << (LOGN - LOGN1);
   constexpr int NCB = N2 / C::M;
+  constexpr int R = 1 << (LOGN1 < 4 ? LOGN1 : 4);  // first-pass radix, as chosen by fft_rec
+  constexpr int NR = C::N1 / R;
+  static_assert(C::M * NR == C::T, "col_fwd: one first-pass butterfly per thread");
   __shared__ float2 lds[C::M * C::S];
-  const int c0 = int(blockIdx.x % NCB) * C::M;
-  const int64_t row = blockIdx.x / NCB;
-  const RowBuf<DT, AL> in(src.p + row * src.stride, src.valid);
-  float2* out = ws + row * (int64_t(1) << LOGN);
-  auto ld = [&](int m, int n) -> float2 { return in.load_pair(2 * (int64_t(n) * N2 + c0 + m)); };
-  TwiddledColumnStore<LOGN, N2> st{out, c0, tw};
-  fft<LOGN1, false, C::M, C::T, C::S, true>(lds, ld, st, tw);
+  const int tid = threadIdx.x;
+  const int m = tid % C::M, j = tid / C::M;  // the first pass's (transform, butterfly) of this thread
+  typename RB::PairBits raw[R];
+  auto issue = [&](int64_t t) {
+    const int c0 = int(t % NCB) * C::M;
+    const RB in(src.p + (t / NCB) * src.stride, src.valid);
+#pragma unroll
+    for (int r = 0; r < R; ++r) raw[r] = in.load_pair_bits(2 * (int64_t(j + r * NR) * N2 + c0 + m));
+  };
+  int64_t t = blockIdx.x;  // grid <= ntiles
+  issue(t);
+  for (;;) {
+    float2 v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = RB::pair_from_bits(raw[r]);
+    const int64_t tn = t + gridDim.x;
+    if (tn < ntiles) issue(tn);
+    RegStream<R> ld{v};
+    LdsTile<C::S, false> tile{lds};
+    TwiddledColumnStore<LOGN, N2> st{ws + (t / NCB) * (int64_t(1) << LOGN), int(t % NCB) * C::M, tw};
+    fft_rec<LOGN1, 0, false, C::M, C::T, true>(ld, tile, tile, st, tw);
+    if (tn >= ntiles) break;
+    t = tn;
+  }
 }
 
 // col_inv: z[N2 n1 + n2] = sum_{k1} B[row][k1][n2] W_{N1}^{-n1 k1}; the
@@ -760,12 +789,13 @@ static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, cons
 template <int LOGN1, int LOGN, int DT>
 static void launch_col_fwd(RealRows<DT> src, int64_t rows, float2* out, const float2* tw, hipStream_t st) {
   const int64_t nb = rows * ((int64_t(1) << (LOGN - LOGN1)) / ColCfg<LOGN1>::M);
+  const unsigned grid = unsigned(ceil_div(nb, kColTilesPerWG));
   if (pairs_aligned<DT>(src.p, src.stride, src.valid))
-    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, true>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0, st,
-                       src, out, tw);
+    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, true>), dim3(grid), dim3(ColCfg<LOGN1>::T), 0, st, src, out,
+                       tw, nb);
   else
-    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, false>), dim3(unsigned(nb)), dim3(ColCfg<LOGN1>::T), 0, st,
-                       src, out, tw);
+    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, false>), dim3(grid), dim3(ColCfg<LOGN1>::T), 0, st, src, out,
+                       tw, nb);
 }
 
 template <int LOGN1, int LOGN, int DT>
