@@ -17,8 +17,9 @@
 //      row      : length-N2 DFTs along rows k1 and N1-k1 (the rows that hold
 //                 the Hermitian partners k and N-k), real-spectrum unpack,
 //                 spectral product / correlation, repack, inverse row DFT,
-//                 times W_N^{-n2 k1}, written back in place;
-//      col_inv  : inverse length-N1 DFTs down the columns, crop and epilogue.
+//                 written back in place;
+//      col_inv  : times W_N^{-n2 k1} as loaded, inverse length-N1 DFTs down
+//                 the columns, crop and epilogue.
 //
 // Real signals of length F are packed as z[n] = u[2n] + i u[2n+1] (N = F/2
 // complex points); see real_unpack/real_repack in fft_core.h.
@@ -391,14 +392,42 @@ __global__ __launch_bounds__(ColCfg<LOGN1>::T) __attribute__((amdgpu_waves_per_e
   }
 }
 
-// col_inv: z[N2 n1 + n2] = sum_{k1} B[row][k1][n2] W_{N1}^{-n1 k1}; the
-// epilogue functor consumes (packed output index m = N2 n1 + n2, value).
+// First-pass loader of the inverse column pass: B[k1][n2] * W_N^{-n2 k1}, the
+// 4-step twiddle of the inverse row outputs.  The pass calls it R times per
+// butterfly with k1 = j + r*NR (r = 0..R-1, n2 fixed), so the twiddle starts at
+// W_N^{-n2 j} and steps by W_N^{-n2 NR}: two hardware sin/cos pairs per
+// butterfly (the recurrence adds at most R-1 roundings, ~1e-6).
+template <int LOGN, int N2, int R, int NR>
+struct TwiddledColumnLoad {
+  const float2* ws_row;
+  int c0;
+  const float2* tw;
+  int q = 0;
+  float2 w, step;
+  __device__ __forceinline__ float2 operator()(int m, int k1) {
+    const uint32_t n2 = uint32_t(c0 + m);
+    if (q % R == 0) {  // a butterfly's first input (q is a constant after unrolling)
+      w = root<LOGN>(tw, n2 * uint32_t(k1));
+      step = root<LOGN>(tw, n2 * uint32_t(NR));
+    }
+    const float2 v = cmulc(ws_row[int64_t(k1) * N2 + c0 + m], w);
+    if (q % R != R - 1) w = cmul(w, step);
+    ++q;
+    return v;
+  }
+};
+
+// col_inv: z[N2 n1 + n2] = sum_{k1} (B[row][k1][n2] W_N^{-n2 k1}) W_{N1}^{-n1 k1};
+// the epilogue functor consumes (packed output index m = N2 n1 + n2, value).
 template <int LOGN1, int LOGN, class EPI>
 __device__ __forceinline__ void col_inv_body(const float2* __restrict__ ws_row, int c0, EPI& epi,
                                              const float2* __restrict__ tw, float2* lds) {
   using C = ColCfg<LOGN1>;
   constexpr int N2 = 1 << (LOGN - LOGN1);
-  auto ld = [&](int m, int k1) -> float2 { return ws_row[int64_t(k1) * N2 + c0 + m]; };
+  constexpr int R = 1 << (LOGN1 < 4 ? LOGN1 : 4);  // first-pass radix, as chosen by fft_rec
+  constexpr int NR = C::N1 / R;
+  static_assert(C::M * NR == C::T, "col_inv: one first-pass butterfly per thread");
+  TwiddledColumnLoad<LOGN, N2, R, NR> ld{ws_row, c0, tw};
   auto st = [&](int m, int n1, float2 v) { epi(int64_t(n1) * N2 + c0 + m, v); };
   fft<LOGN1, true, C::M, C::T, C::S, true>(lds, ld, st, tw);
 }
@@ -531,38 +560,28 @@ __device__ __forceinline__ void row_pair_fft(float2* lds, const float2* __restri
   fft<LOGN2, false, 2, C::T, C::N2P>(lds, ld, st, tw);
 }
 
-// Last-pass store of an inverse row pair: sig[k1][n] = v * W_N^{-n k1}, k1 =
-// ra (tile row 0) or rb (tile row 1); the twiddle steps along a butterfly's
-// outputs n = base + r*NS as in TwiddledColumnStore.
-template <int LOGN, int N2>
-struct TwiddledRowStore {
-  static constexpr bool kRunStore = true;
+// Last-pass store of an inverse row pair: sig[k1][n] = v, k1 = ra (tile row
+// 0) or rb (tile row 1).  The 4-step twiddle W_N^{-n k1} of these values is
+// applied by the inverse column pass as it loads them (TwiddledColumnLoad):
+// the row kernels are bound by their VALU issue, the column pass is not.
+template <int N2>
+struct RowStore {
   float2* sig;
   int ra, rb;
-  const float2* tw;
-  template <int R, int NS>
-  __device__ __forceinline__ void run(int m, int base, const float2 (&v)[R]) const {
-    const int k1 = (m == 0) ? ra : rb;
-    float2 w = root<LOGN>(tw, uint32_t(base) * uint32_t(k1));
-    const float2 step = root<LOGN>(tw, uint32_t(NS) * uint32_t(k1));
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      sig[int64_t(k1) * N2 + base + r * NS] = cmulc(v[r], w);
-      if (r + 1 < R) w = cmul(w, step);
-    }
+  __device__ __forceinline__ void operator()(int m, int n, float2 v) const {
+    sig[int64_t(m == 0 ? ra : rb) * N2 + n] = v;
   }
 };
 
-// Inverse row DFT of the tile, twiddle W_N^{-n2 k1}, store to sig rows.
+// Inverse row DFT of the tile, stored to sig rows (untwiddled, see RowStore).
 template <int LOGN1, int LOGN2>
 __device__ __forceinline__ void row_pair_ifft_store(float2* lds, float2* __restrict__ sig, int q,
                                                     const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
   constexpr int N1 = 1 << LOGN1;
-  constexpr int LOGN = LOGN1 + LOGN2;
   const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
   LdsTile<C::N2P, true> ld{lds};
-  TwiddledRowStore<LOGN, C::N2> st{sig, ra, rb, tw};
+  RowStore<C::N2> st{sig, ra, rb};
   fft<LOGN2, true, 2, C::T, C::N2P>(lds, ld, st, tw);
 }
 
