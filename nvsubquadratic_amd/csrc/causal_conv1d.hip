@@ -37,33 +37,6 @@ __global__ __launch_bounds__(kConvThreads) void cconv_fwd_kernel(const typename 
   }
 }
 
-// gpre = gy * silu'(pre), pre recomputed; fp32 workspace.  grid as forward.
-template <int DT>
-__global__ __launch_bounds__(kConvThreads) void cconv_gpre_silu_kernel(const typename Elem<DT>::T* __restrict__ gy,
-                                                                        const typename Elem<DT>::T* __restrict__ x,
-                                                                        const float* __restrict__ w,
-                                                                        const float* __restrict__ bias,
-                                                                        float* __restrict__ gpre, int C, int L, int K) {
-  __shared__ __align__(16) float xs[conv_tile_floats(kConvMaxK)];
-  __shared__ __align__(16) float wl[kConvWeightFloats];
-  const int64_t row = blockIdx.x;
-  const int c = int(row % C);
-  const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
-  stage_weights<false>(wl, w + int64_t(c) * K, K);
-  stage_row<DT, conv_tile_floats(kConvMaxK)>(xs, x + row * L, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
-  const float b0 = bias ? bias[c] : 0.f;
-  float acc[kConvPer];
-#pragma unroll
-  for (int e = 0; e < kConvPer; ++e) acc[e] = b0;
-  const int base = threadIdx.x * kConvPer;
-  slide_fma(acc, xs, base, K, wl);
-#pragma unroll
-  for (int e = 0; e < kConvPer; ++e) {
-    const int64_t n = n0 + base + e;
-    if (n < L) gpre[row * L + n] = Elem<DT>::load(gy, row * L + n) * dsilu(acc[e]);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Matrix-core path for K >= 16 taps: a workgroup walks a segment of
 // kConvSegTiles tiles of one (b, c) row; per tile the source window (fp32,
@@ -289,92 +262,97 @@ static void launch_bwd_mfma(const void* gy, const void* x, const float* w, const
 }
 
 // ---------------------------------------------------------------------------
-// Backward for K <= 4 taps in one register-resident pass (the Hyena short-conv
-// case).  Thread t of a tile owns outputs n = n0 + 8t + e, e < 8; its x and gy
-// windows [n0 + 8t - 4, n0 + 8t + 16) come straight from HBM (two Win12 each).
-// With the taps left-padded to 4 (w4[j] = w[j - (4 - K)]):
-//   pre[n]  = bias + sum_j w4[j] x[n - 3 + j],  gpre = gy * silu'(pre) (or gy)
-//   gx[n]   = sum_s wr4[s] gpre[n + s],          wr4[s] = w[K - 1 - s] (s < K)
-//   gw4[j] += gpre[n] x[n - 3 + j],              gb += gpre[n]
-// gpre is recomputed at the 3 positions past the thread's 8 (its neighbour
-// owns them); the weight / bias sums stay in registers over the workgroup's
-// tiles (one channel, a segment of its (b, tile) sequence) and are reduced in
-// a fixed order into a per-workgroup partial [K + 1].
+// Backward for K <= 16 taps in one register-resident pass (the Hyena
+// short-conv case).  Thread t of a tile owns outputs n = n0 + 8t + e, e < 8.
+// With the taps left-padded to KP = 4, 8 or 16 (wk[j] = w[j - (KP - K)]):
+//   pre[n]  = bias + sum_j wk[j] x[n - KP + 1 + j],  gpre = gy * silu'(pre) (or gy)
+//   gx[n]   = sum_s wr[s] gpre[n + s],                wr[s] = w[K - 1 - s] (s < K)
+//   gwk[j] += gpre[n] x[n - KP + 1 + j],              gb += gpre[n]
+// gpre is recomputed at the KP - 1 positions past the thread's 8 (its
+// neighbour owns them).  x over [n0 + 8t - 8 XB, n0 + 8t + 8 XA) and gy over
+// [n0 + 8t, n0 + 8t + 8 XA) come straight from HBM in aligned chunks of 8
+// (Win8).  The weight / bias sums stay in registers over the workgroup's tiles
+// (one channel, a segment of its (b, tile) sequence) and are reduced in a fixed
+// order into a per-workgroup partial [K + 1].
 // ---------------------------------------------------------------------------
-template <int DT, bool AL, int ACT>
+template <int DT, bool AL, int ACT, int KP>
 __global__ __launch_bounds__(kConvThreads) void cconv_bwd_short_kernel(
     const typename Elem<DT>::T* __restrict__ gy, const typename Elem<DT>::T* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ bias, typename Elem<DT>::T* __restrict__ gx,
     float* __restrict__ part, int B, int C, int L, int K) {
-  __shared__ float red[5 * kConvThreads];
+  static_assert(KP == 4 || KP == 8 || KP == 16, "cconv_bwd_short: taps padded to 4, 8 or 16");
+  static_assert(kConvPer == 8, "cconv_bwd_short: 8 outputs per thread");
+  constexpr int NG = kConvPer + KP - 1;  // gpre positions per thread: [0, NG)
+  constexpr int XB = (KP - 1 + 7) / 8;   // x chunks before the outputs: positions >= 1 - KP
+  constexpr int XA = (NG + 7) / 8;       // x and gy chunks from the outputs on: positions < NG
+  __shared__ float red[(KP + 1) * kConvThreads];
   const int c = int(blockIdx.x);
   const int ntiles = (L + kConvTile - 1) / kConvTile;
   const int g_begin = int(blockIdx.y) * kConvSegTiles;
   const int g_end = min(B * ntiles, g_begin + kConvSegTiles);
   const int t = int(threadIdx.x);
-  float w4[4], wr4[4];
+  float wk[KP], wr[KP];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int sl = j - (4 - K);
-    w4[j] = sl >= 0 ? w[int64_t(c) * K + (sl >= 0 ? sl : 0)] : 0.f;
-    wr4[j] = j < K ? w[int64_t(c) * K + (j < K ? K - 1 - j : 0)] : 0.f;
+  for (int j = 0; j < KP; ++j) {
+    const int sl = j - (KP - K);
+    wk[j] = sl >= 0 ? w[int64_t(c) * K + (sl >= 0 ? sl : 0)] : 0.f;
+    wr[j] = j < K ? w[int64_t(c) * K + (j < K ? K - 1 - j : 0)] : 0.f;
   }
   const float b0 = bias ? bias[c] : 0.f;
-  float gw4[4] = {0.f, 0.f, 0.f, 0.f};
+  float gwk[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) gwk[j] = 0.f;
   float gbs = 0.f;
   for (int g = g_begin; g < g_end; ++g) {
     const int b = g / ntiles, ti = g - b * ntiles;
     const int64_t row = int64_t(b) * C + c;
     const int base = ti * kConvTile + kConvPer * t;
     const RowBuf<DT, false> xb(x + row * L, L), gb(gy + row * L, L);
-    Win12<DT, AL> x0, x1, g0, g1;
-    x0.load(xb, base);
-    x1.load(xb, base + 8);
-    g0.load(gb, base);
-    g1.load(gb, base + 8);
-    float xw[20], gw[20];  // index i <-> position base - 4 + i
+    Win8<DT, AL> xc[XB + XA], gc[XA];
 #pragma unroll
-    for (int i = 0; i < 20; ++i) {
-      xw[i] = i < 12 ? x0.at(i) : x1.at(i - 8);
-      gw[i] = i < 12 ? g0.at(i) : g1.at(i - 8);
-    }
-    float gp[kConvPer + 3];  // gpre at base + e, e < 11
+    for (int i = 0; i < XB + XA; ++i) xc[i].load(xb, base + 8 * (i - XB));
 #pragma unroll
-    for (int e = 0; e < kConvPer + 3; ++e) {
+    for (int i = 0; i < XA; ++i) gc[i].load(gb, base + 8 * i);
+    // x at position base + p for p in [-8 XB, 8 XA), gy at base + p for p in [0, 8 XA)
+    auto xat = [&](int p) { return xc[(p + 8 * XB) >> 3].at((p + 8 * XB) & 7); };
+    auto gat = [&](int p) { return gc[p >> 3].at(p & 7); };
+    float gp[NG];  // gpre at base + e
+#pragma unroll
+    for (int e = 0; e < NG; ++e) {
       float pre = b0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) pre = fmaf(w4[j], xw[e + 1 + j], pre);
-      gp[e] = (ACT == NSQ_ACT_SILU) ? gw[e + 4] * dsilu(pre) : gw[e + 4];
+      for (int j = 0; j < KP; ++j) pre = fmaf(wk[j], xat(e - KP + 1 + j), pre);
+      gp[e] = (ACT == NSQ_ACT_SILU) ? gat(e) * dsilu(pre) : gat(e);
     }
     float out[kConvPer];
 #pragma unroll
     for (int e = 0; e < kConvPer; ++e) {
       float a = 0.f;
 #pragma unroll
-      for (int sidx = 0; sidx < 4; ++sidx) a = fmaf(wr4[sidx], gp[e + sidx], a);
+      for (int sidx = 0; sidx < KP; ++sidx) a = fmaf(wr[sidx], gp[e + sidx], a);
       out[e] = a;
       gbs += gp[e];  // positions >= L have gy = 0, so gpre = 0
 #pragma unroll
-      for (int j = 0; j < 4; ++j) gw4[j] = fmaf(gp[e], xw[e + 1 + j], gw4[j]);
+      for (int j = 0; j < KP; ++j) gwk[j] = fmaf(gp[e], xat(e - KP + 1 + j), gwk[j]);
     }
     const RowBuf<DT, AL> ob(gx + row * L, L);
 #pragma unroll
     for (int e = 0; e < kConvPer; e += 2) ob.store_pair(base + e, make_float2(out[e], out[e + 1]));
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) red[j * kConvThreads + t] = gw4[j];
-  red[4 * kConvThreads + t] = gbs;
+  for (int j = 0; j < KP; ++j) red[j * kConvThreads + t] = gwk[j];
+  red[KP * kConvThreads + t] = gbs;
   __syncthreads();
-  if (t < 5) {
+  if (t <= KP) {
     float sacc = 0.f;
     for (int i = 0; i < kConvThreads; ++i) sacc += red[t * kConvThreads + i];
-    // left-padded tap t -> weight index t - (4 - K); slot 4 -> the bias
+    // left-padded tap t -> weight index t - (KP - K); slot KP -> the bias
     const int nparts = int(gridDim.y);
     float* pw = part + (int64_t(c) * nparts + blockIdx.y) * (K + 1);
-    if (t == 4)
+    if (t == KP)
       pw[K] = sacc;
-    else if (t >= 4 - K)
-      pw[t - (4 - K)] = sacc;
+    else if (t >= KP - K)
+      pw[t - (KP - K)] = sacc;
   }
 }
 
@@ -387,8 +365,17 @@ static void launch_bwd_short(const void* gy, const void* x, const float* w, cons
   const bool al = L % (DT == NSQ_DTYPE_F32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(gy) & 15) == 0 && (reinterpret_cast<uintptr_t>(gx) & 15) == 0;
   auto go = [&](auto al_c, auto act_c) {
-    hipLaunchKernelGGL((cconv_bwd_short_kernel<DT, decltype(al_c)::value, decltype(act_c)::value>), grid,
-                       dim3(kConvThreads), 0, st, (const ET*)gy, (const ET*)x, w, bias, (ET*)gx, ws, B, C, L, K);
+    constexpr bool A = decltype(al_c)::value;
+    constexpr int F = decltype(act_c)::value;
+    if (K <= 4)
+      hipLaunchKernelGGL((cconv_bwd_short_kernel<DT, A, F, 4>), grid, dim3(kConvThreads), 0, st, (const ET*)gy,
+                         (const ET*)x, w, bias, (ET*)gx, ws, B, C, L, K);
+    else if (K <= 8)
+      hipLaunchKernelGGL((cconv_bwd_short_kernel<DT, A, F, 8>), grid, dim3(kConvThreads), 0, st, (const ET*)gy,
+                         (const ET*)x, w, bias, (ET*)gx, ws, B, C, L, K);
+    else
+      hipLaunchKernelGGL((cconv_bwd_short_kernel<DT, A, F, 16>), grid, dim3(kConvThreads), 0, st, (const ET*)gy,
+                         (const ET*)x, w, bias, (ET*)gx, ws, B, C, L, K);
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
@@ -425,27 +412,12 @@ static void launch_fwd(const void* x, const float* w, const float* bias, void* y
 template <int DT>
 static void launch_bwd(const void* gy, const void* x, const float* w, const float* bias, void* gx, float* gw,
                        float* gb, int act, int B, int C, int L, int K, float* ws, hipStream_t st) {
-  using ET = typename Elem<DT>::T;
-  if (K <= 4) return launch_bwd_short<DT>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
-  switch (mfma_steps_for(K)) {
+  if (K <= 16) return launch_bwd_short<DT>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
+  switch (mfma_steps_for(K)) {  // 17 <= K <= 256 (validated)
     case 12: return launch_bwd_mfma<DT, 12>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
     case 20: return launch_bwd_mfma<DT, 20>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
     case 36: return launch_bwd_mfma<DT, 36>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
-    case 68: return launch_bwd_mfma<DT, 68>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
-    default: break;
-  }
-  dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
-  if (act == NSQ_ACT_SILU) {
-    hipLaunchKernelGGL((cconv_gpre_silu_kernel<DT>), grid, dim3(kConvThreads), 0, st, (const ET*)gy, (const ET*)x, w,
-                       bias, ws, C, L, K);
-    hipLaunchKernelGGL((cconv_gx_kernel<DT, NSQ_DTYPE_F32>), grid, dim3(kConvThreads), 0, st, (const float*)ws, w,
-                       (ET*)gx, C, L, K);
-    hipLaunchKernelGGL((cconv_wgrad_kernel<DT, NSQ_DTYPE_F32>), dim3(C), dim3(kConvThreads), 0, st, (const float*)ws,
-                       (const ET*)x, gw, gb, B, C, L, K);
-  } else {
-    hipLaunchKernelGGL((cconv_gx_kernel<DT, DT>), grid, dim3(kConvThreads), 0, st, (const ET*)gy, w, (ET*)gx, C, L, K);
-    hipLaunchKernelGGL((cconv_wgrad_kernel<DT, DT>), dim3(C), dim3(kConvThreads), 0, st, (const ET*)gy, (const ET*)x,
-                       gw, gb, B, C, L, K);
+    default: return launch_bwd_mfma<DT, 68>(gy, x, w, bias, gx, gw, gb, act, B, C, L, K, ws, st);
   }
 }
 
@@ -467,12 +439,12 @@ using namespace nsq;
 extern "C" {
 
 size_t nsq_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, int64_t K, int activation) {
-  // K <= 4 (one fused pass): the weight / bias gradient partials
-  // [C][parts][K + 1] only; otherwise silu: gy * silu'(pre) [B, C, L], and for
-  // K >= 16 (matrix cores) the partials after it
-  if (K >= 1 && K <= 4) return size_t(C * cconv_wgrad_parts(B, L) * (K + 1)) * sizeof(float);
+  // K <= 16 (one fused pass): the weight / bias gradient partials
+  // [C][parts][K + 1] only; otherwise (matrix cores) silu: gy * silu'(pre)
+  // [B, C, L], then the partials
+  if (K >= 1 && K <= 16) return size_t(C * cconv_wgrad_parts(B, L) * (K + 1)) * sizeof(float);
   const int64_t pre = activation == NSQ_ACT_SILU ? B * C * L : 0;
-  const int64_t parts = (K >= 16 && K <= kConvMaxK) ? C * cconv_wgrad_parts(B, L) * (K + 1) : 0;
+  const int64_t parts = K <= kConvMaxK ? C * cconv_wgrad_parts(B, L) * (K + 1) : 0;
   return size_t(pre + parts) * sizeof(float);
 }
 

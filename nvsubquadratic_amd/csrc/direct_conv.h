@@ -347,6 +347,45 @@ struct Win12 {
   }
 };
 
+// Samples x[n + i], i < 8, of one row as raw bits.  AL as for Win12: n is a
+// multiple of 8 and the chunk is one (16-bit types) or two (fp32) aligned
+// 16-byte loads lying wholly inside or wholly outside [0, len); otherwise
+// eight element loads.  A chunk before the row (n < 0) reads as zero.
+template <int DT, bool AL>
+struct Win8 {
+  static constexpr bool HALF = DT != NSQ_DTYPE_F32;
+  static constexpr int W = (HALF && AL) ? 4 : 8;
+  uint32_t w[W];
+  __device__ __forceinline__ void load(const RowBuf<DT, false>& rb, int n) {
+    if constexpr (AL) {
+      constexpr int ES = HALF ? 2 : 4;
+      int off = n < 0 ? int(0x80000000u) : n * ES;
+      asm volatile("" : "+v"(off));
+      if constexpr (HALF) {
+        const auto m = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = m[i];
+      } else {
+        const auto m0 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off, 0, 0);
+        const auto m1 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off + 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { w[i] = m0[i]; w[4 + i] = m1[i]; }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w[i] = rb.elem_halo_bits(n + i);
+    }
+  }
+  __device__ __forceinline__ float at(int i) const {  // i is a compile-time constant after unrolling
+    if constexpr (HALF && AL) {
+      const uint32_t v = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
+      return RowBuf<DT, false>::bits_to_f32(v);
+    } else {
+      return RowBuf<DT, false>::bits_to_f32(w[i]);
+    }
+  }
+};
+
 // Kernels shared by the causal conv and B2B backward passes.
 // gx[i] = sum_j w[j] gp[i + K - 1 - j]  (gp = gpre in GT precision).  grid as forward.
 template <int DT, int GT>

@@ -101,10 +101,10 @@ def test_halo_before_row_start_reads_zero(K):
     assert rel_l2(w.grad, wg.grad) < 1e-5
 
 
-@pytest.mark.parametrize("K", [1, 2, 3, 4])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16])
 @pytest.mark.parametrize("L", [1, 13, 4103, 18432])
 def test_short_taps_backward_across_tiles_and_batches(K, L):
-    """Up to 4 taps the whole backward is one register-resident pass whose
+    """Up to 16 taps the whole backward is one register-resident pass whose
     weight/bias partials cover runs of (batch, tile) pairs; with 3 batches and
     up to 9 tiles per row those runs cross row ends.  Ragged lengths take the
     element-load path, multiples of 8 the vector path."""
@@ -128,10 +128,11 @@ def test_short_taps_backward_across_tiles_and_batches(K, L):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_short_taps_backward_low_precision_io(dtype):
+@pytest.mark.parametrize("K", [4, 7, 13])
+def test_short_taps_backward_low_precision_io(dtype, K):
     torch.manual_seed(5)
     x = torch.randn(2, 16, 3000).to(dtype)
-    w = torch.randn(16, 4)
+    w = torch.randn(16, K)
     b = torch.randn(16)
     xr = x.float().requires_grad_(True)
     wr, br = w.clone().requires_grad_(True), b.clone().requires_grad_(True)
