@@ -8,37 +8,49 @@
 
 namespace nsq {
 
-// grid = (B*C, ceil(L / kConvTile)).
-template <int DT, int ACT>
-__global__ __launch_bounds__(kConvThreads) void cconv_fwd_kernel(const typename Elem<DT>::T* __restrict__ x,
-                                                                  const float* __restrict__ w,
-                                                                  const float* __restrict__ bias,
-                                                                  typename Elem<DT>::T* __restrict__ y, int C, int L,
-                                                                  int K) {
-  __shared__ __align__(16) float xs[conv_tile_floats(kConvMaxK)];
-  __shared__ __align__(16) float wl[kConvWeightFloats];
+// Forward for K <= 16 taps from registers: thread t of a tile owns outputs
+// n = n0 + 8t + e, e < 8; with the taps left-padded to KP = 4, 8 or 16,
+// y[n] = act(bias + sum_j wk[j] x[n - KP + 1 + j]).  Its x window
+// [n0 + 8t - 8 XB, n0 + 8t + 8) comes straight from HBM in aligned chunks of 8
+// (Win8; the chunks before the thread's own are its neighbours', read again
+// from L2), so no LDS staging or barrier.  grid = (B*C, ceil(L / kConvTile)).
+template <int DT, bool AL, int ACT, int KP>
+__global__ __launch_bounds__(kConvThreads) void cconv_fwd_short_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                                        const float* __restrict__ w,
+                                                                        const float* __restrict__ bias,
+                                                                        typename Elem<DT>::T* __restrict__ y, int C,
+                                                                        int L, int K) {
+  static_assert(KP == 4 || KP == 8 || KP == 16, "cconv_fwd_short: taps padded to 4, 8 or 16");
+  static_assert(kConvPer == 8, "cconv_fwd_short: 8 outputs per thread");
+  constexpr int XB = (KP - 1 + 7) / 8;  // chunks before the outputs: positions >= 1 - KP
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
-  const int64_t n0 = int64_t(blockIdx.y) * kConvTile;
-  const typename Elem<DT>::T* xr = x + row * L;
-  stage_weights<false>(wl, w + int64_t(c) * K, K);
-  stage_row<DT, conv_tile_floats(kConvMaxK)>(xs, xr, n0 - (K - 1), kConvTile + K - 1 + 2 * kConvPer, L);
-  const float b0 = bias ? bias[c] : 0.f;
-  float acc[kConvPer];
+  const int base = int(blockIdx.y) * kConvTile + kConvPer * int(threadIdx.x);
+  float wk[KP];
 #pragma unroll
-  for (int e = 0; e < kConvPer; ++e) acc[e] = b0;
-  const int base = threadIdx.x * kConvPer;
-  slide_fma(acc, xs, base, K, wl);
-  typename Elem<DT>::T* yr = y + row * L;
-#pragma unroll
-  for (int e = 0; e < kConvPer; e += 2) {
-    const int64_t n = n0 + base + e;
-    if (n < L) store_pair<DT>(yr, n, L, make_float2(act_fwd<ACT>(acc[e]), act_fwd<ACT>(acc[e + 1])));
+  for (int j = 0; j < KP; ++j) {
+    const int sl = j - (KP - K);
+    wk[j] = sl >= 0 ? w[int64_t(c) * K + (sl >= 0 ? sl : 0)] : 0.f;
   }
+  const float b0 = bias ? bias[c] : 0.f;
+  const RowBuf<DT, false> xb(x + row * L, L);
+  Win8<DT, AL> xc[XB + 1];
+#pragma unroll
+  for (int i = 0; i <= XB; ++i) xc[i].load(xb, base + 8 * (i - XB));
+  auto xat = [&](int p) { return xc[(p + 8 * XB) >> 3].at((p + 8 * XB) & 7); };
+  float out[kConvPer];
+#pragma unroll
+  for (int e = 0; e < kConvPer; ++e) {
+    float a = b0;
+#pragma unroll
+    for (int j = 0; j < KP; ++j) a = fmaf(wk[j], xat(e - KP + 1 + j), a);
+    out[e] = act_fwd<ACT>(a);
+  }
+  store8<DT, AL>(RowBuf<DT, AL>(y + row * L, L), base, out);
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core path for K >= 16 taps: a workgroup walks a segment of
+// Matrix-core path (K >= 16; used above 16 taps): a workgroup walks a segment of
 // kConvSegTiles tiles of one (b, c) row; per tile the source window (fp32,
 // padded as ToeplitzMfma reads it) is staged from registers loaded during the
 // previous tile, the MFMA band gives acc[p] for the tile's 2048 outputs, and
@@ -114,7 +126,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
   }
 }
 
-// Weight / bias gradients on the matrix cores (K >= 16): per tile,
+// Weight / bias gradients on the matrix cores (K >= 16; used above 16 taps): per tile,
 //   D[i][t] += sum_a gp[16a + i] * xwin[16a + t],  xwin[m] = x[n0 - K + 1 + m],
 // gw[j] = sum_i D[i][i + j] over the workgroup's tiles (one channel, a segment
 // of its (b, tile) sequence), gb = sum gp; fixed-order reduction into a
@@ -393,20 +405,38 @@ template <int DT>
 static void launch_fwd(const void* x, const float* w, const float* bias, void* y, int act, int B, int C, int L, int K,
                        hipStream_t st) {
   using ET = typename Elem<DT>::T;
-  switch (mfma_steps_for(K)) {  // matrix cores from 16 taps up
-    case 12: return launch_fwd_mfma<DT, 12>(x, w, bias, y, act, B, C, L, K, st);
-    case 20: return launch_fwd_mfma<DT, 20>(x, w, bias, y, act, B, C, L, K, st);
-    case 36: return launch_fwd_mfma<DT, 36>(x, w, bias, y, act, B, C, L, K, st);
-    case 68: return launch_fwd_mfma<DT, 68>(x, w, bias, y, act, B, C, L, K, st);
-    default: break;
+  if (K > 16) {  // matrix cores; up to 16 taps the register kernel below is faster
+    switch (mfma_steps_for(K)) {  // 17 <= K <= 256 (validated)
+      case 12: return launch_fwd_mfma<DT, 12>(x, w, bias, y, act, B, C, L, K, st);
+      case 20: return launch_fwd_mfma<DT, 20>(x, w, bias, y, act, B, C, L, K, st);
+      case 36: return launch_fwd_mfma<DT, 36>(x, w, bias, y, act, B, C, L, K, st);
+      default: return launch_fwd_mfma<DT, 68>(x, w, bias, y, act, B, C, L, K, st);
+    }
   }
   dim3 grid(B * C, unsigned(ceil_div(L, kConvTile)));
-  if (act == NSQ_ACT_SILU)
-    hipLaunchKernelGGL((cconv_fwd_kernel<DT, NSQ_ACT_SILU>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w, bias,
-                       (ET*)y, C, L, K);
+  const bool al = L % (DT == NSQ_DTYPE_F32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  auto go = [&](auto al_c, auto act_c) {
+    constexpr bool A = decltype(al_c)::value;
+    constexpr int F = decltype(act_c)::value;
+    if (K <= 4)
+      hipLaunchKernelGGL((cconv_fwd_short_kernel<DT, A, F, 4>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w,
+                         bias, (ET*)y, C, L, K);
+    else if (K <= 8)
+      hipLaunchKernelGGL((cconv_fwd_short_kernel<DT, A, F, 8>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w,
+                         bias, (ET*)y, C, L, K);
+    else
+      hipLaunchKernelGGL((cconv_fwd_short_kernel<DT, A, F, 16>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w,
+                         bias, (ET*)y, C, L, K);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using SILU = std::integral_constant<int, NSQ_ACT_SILU>;
+  using IDN = std::integral_constant<int, NSQ_ACT_IDENTITY>;
+  if (al)
+    act == NSQ_ACT_SILU ? go(T_{}, SILU{}) : go(T_{}, IDN{});
   else
-    hipLaunchKernelGGL((cconv_fwd_kernel<DT, NSQ_ACT_IDENTITY>), grid, dim3(kConvThreads), 0, st, (const ET*)x, w,
-                       bias, (ET*)y, C, L, K);
+    act == NSQ_ACT_SILU ? go(F_{}, SILU{}) : go(F_{}, IDN{});
 }
 
 template <int DT>

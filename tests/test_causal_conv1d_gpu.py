@@ -153,10 +153,11 @@ def test_short_taps_backward_low_precision_io(dtype, K):
 @pytest.mark.parametrize("K", [15, 16, 17, 33, 34, 65, 66, 129, 130, 256])
 @pytest.mark.parametrize("act", ["identity", "silu"])
 def test_tap_counts_across_matrix_core_plans(K, act):
-    """Direct conv from 16 taps runs as banded Toeplitz MFMA products (forward,
+    """Direct conv above 16 taps runs as banded Toeplitz MFMA products (forward,
     the silu pre-activation gradient, the input-gradient correlation and the
-    weight gradient); 15 taps stay on the FMA loop.  Ragged length, bias, two
-    batches; forward and gradients against a float64 reference."""
+    weight gradient, on bands of 12, 20, 36 or 68 steps); up to 16 taps the
+    register-window kernels run.  Ragged length, bias, two batches; forward and
+    gradients against a float64 reference."""
     torch.manual_seed(200 + K)
     B, C, L = 2, 3, 4700
     x = torch.randn(B, C, L, dtype=torch.float64, requires_grad=True)
