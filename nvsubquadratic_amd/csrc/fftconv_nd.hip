@@ -9,7 +9,8 @@ struct NdPlan {
   int64_t B, H, kb;      // kb = kernel batch: 1 (shared) or B (per-sample FiLM)
   int S[3], K[3];        // padded to 3 axes: (S0, S1, S2) with S1 = K1 = 1 for 2D
   int lF[3], F[3], c[3];
-  int FH;
+  int FH;        // spectrum columns along the last axis, F2/2 + 1
+  int RS;        // spectrum row stride (complex elements), >= FH
   int64_t spec;
 };
 
@@ -42,7 +43,14 @@ static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
     p.c[d] = k[d] / 2;
   }
   p.FH = p.F[2] / 2 + 1;
-  p.spec = int64_t(p.F[0]) * p.F[1] * p.FH;
+  // 2D: rows padded to a multiple of 16 complex values, so the 16-column
+  // segments the axis-0 passes move per row start on a 128-byte line (an FH
+  // row stride puts every segment across two lines).  The pad is never read
+  // or written.  3D planes are F1 rows of FH: the axis-0 segments are aligned
+  // there already (the plane stride is a multiple of 16) and the plane passes
+  // keep their compile-time row stride.
+  p.RS = nd == 2 ? (p.FH + 15) / 16 * 16 : p.FH;
+  p.spec = int64_t(p.F[0]) * p.F[1] * p.RS;
   return true;
 }
 
@@ -65,7 +73,7 @@ static bool with_log(int v, F&& f) {
 template <int DT>
 static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, float2* ws,
                     const float2* tw, hipStream_t st) {
-  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.FH};
+  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.RS};
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
     constexpr int LOGN = decltype(L)::value;
     using C = RowNdCfg<LOGN>;
@@ -81,7 +89,7 @@ static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n
 template <int DT, int MODE>
 static bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int n1, RowInvOut o, const float2* tw,
                     hipStream_t st) {
-  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.FH};
+  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.RS};
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
     constexpr int LOGN = decltype(L)::value;
     using C = RowNdCfg<LOGN>;
@@ -108,6 +116,12 @@ static void col_blocks(int inner, LAUNCH&& launch) {
   if (rem) launch(std::integral_constant<int, kNdTailTile>{}, int(ceil_div(rem, CT::M)), full * CM::M);
 }
 
+// Axis-0 columns: the inner index j runs over a block's F1 rows of the last
+// axis; 3D packs them (RS = FH), 2D has one padded row (F1 = 1, j < FH).
+static ColGeom axis0_geom(const NdPlan& p) {
+  return ColGeom{1, 0, p.spec, int64_t(p.F[1]) * p.RS, p.F[1] * p.FH};
+}
+
 // Column pass along axis d (0 or 1) of `nbh` blocks whose valid extent along
 // axis 0 is n_valid0 (used as the middle-row count of axis-1 passes).
 template <bool INV>
@@ -115,9 +129,9 @@ static bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_v
                      int out_cnt, const float2* tw, hipStream_t st) {
   ColGeom cg;
   if (axis == 1) {
-    cg = ColGeom{n_valid0, int64_t(p.F[1]) * p.FH, p.spec, int64_t(p.FH), p.FH};
+    cg = ColGeom{n_valid0, int64_t(p.F[1]) * p.RS, p.spec, int64_t(p.RS), p.FH};
   } else {
-    cg = ColGeom{1, 0, p.spec, int64_t(p.F[1]) * p.FH, p.F[1] * p.FH};
+    cg = axis0_geom(p);
   }
   const int64_t n_outer = nbh * cg.n_mid;
   return with_log<4, kNdMaxLogF>(p.lF[axis], [&](auto L) {
@@ -200,7 +214,7 @@ static bool inner_inv(const NdPlan& p, float2* ws, int64_t nbh, int n0, int off1
   return row_inv<DT, MODE>(p, ws, nbh, n0, n1out, o, tw, st);
 }
 
-static ColGeom axis0_geom(const NdPlan& p) { return ColGeom{1, 0, p.spec, int64_t(p.F[1]) * p.FH, p.F[1] * p.FH}; }
+
 
 // Filter spectrum: kb*H blocks of the [kb*H][K0][K1][K2] float32 kernel.
 static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {

@@ -61,7 +61,7 @@ struct RowGeom {
   int64_t rows;  // bh * n0 * n1
   int n0, n1;    // valid counts of axes 0 and 1 for these rows
   int64_t spec;  // spectrum block size (complex elements)
-  int F1, FH;
+  int F1, RS;    // rows per axis-0 index; spectrum row stride (complex elements)
 };
 
 // Forward real FFT of rows of a contiguous [BH][n0][n1][len] real tensor,
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
   for (int m = tslot; m < C::M; m += C::T) {  // ordered before its use by the transform's barriers
     const int64_t r = r0 + m;
     const RowIdx q = row_index(r < rg.rows ? r : 0, rg.n0, rg.n1);
-    rowoff[m] = int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+    rowoff[m] = int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.RS;
   }
   auto ld = [&](int m, int n) -> float2 {
     const int64_t r = r0 + m;
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
   for (int m = tslot; m < C::M; m += C::T) {
     const int64_t r = r0 + m;
     const RowIdx q = row_index(r < rg.rows ? r : 0, rg.n0, rg.n1);
-    rowoff[m] = int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.FH;
+    rowoff[m] = int64_t(q.bh) * rg.spec + (int64_t(q.a0) * rg.F1 + q.a1) * rg.RS;
   }
   __syncthreads();
 #pragma unroll
@@ -448,15 +448,34 @@ __device__ __forceinline__ int64_t col_base(const ColGeom& cg, int64_t o) {
   return (o / cg.n_mid) * cg.spec + (o % cg.n_mid) * cg.mid_stride;
 }
 
-// Element n of inner column j of a column group, zero for j >= inner_count or
-// n >= valid.  Branch-free: the load is always issued (from the group's first
-// element when out of range), so a pass's loads stay in flight together.
-__device__ __forceinline__ float2 col_load(const float2* __restrict__ base, const ColGeom& cg, int j, int n,
-                                           int valid) {
-  const bool ok = (j < cg.inner_count) && (n < valid);
-  const float2 v = base[ok ? int64_t(n) * cg.axis_stride + j : 0];
-  return make_float2(ok ? v.x : 0.f, ok ? v.y : 0.f);
-}
+// A column group of one workspace block as a raw buffer resource: element n
+// of inner column j is at byte n * 8 * axis_stride + 8 j from the block base.
+// Offsets are 32-bit (a block spans < 2^31 bytes) and the n * stride product
+// is a 24-bit multiply (axis lengths <= 2^10, strides < 2^21 elements), so a
+// pass's address math is one multiply-add and one select per element.  An
+// access the caller marks invalid (column past inner_count, element outside
+// the read or write window) uses offset 2^31, past the range: loads read zero
+// and stores are dropped, with no branch, so a pass's loads stay in flight
+// together.
+struct ColBuf {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t stride8;
+  __device__ __forceinline__ ColBuf(const float2* base, const ColGeom& cg)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<float2*>(base), 0, 0x7fffffff, 0x00020000)),
+        stride8(uint32_t(cg.axis_stride) * 8u) {}
+  __device__ __forceinline__ int off(int n, int j, bool ok) const {
+    int o = ok ? int(__umul24(uint32_t(n), stride8) + 8u * uint32_t(j)) : int(0x80000000u);
+    asm volatile("" : "+v"(o));  // keep the offset whole (no constant folded into the immediate)
+    return o;
+  }
+  __device__ __forceinline__ float2 load(int n, int j, bool ok) const {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off(n, j, ok), 0, 0));
+  }
+  __device__ __forceinline__ void store(int n, int j, bool ok, float2 v) const {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uint32_t __attribute__((ext_vector_type(2))), v), r,
+                                          off(n, j, ok), 0, 0);
+  }
+};
 
 // Generic pass: reads elements [0, in_cnt) (rest zero), transforms, writes
 // outputs [out_off, out_off + out_cnt) to positions [0, out_cnt).
@@ -467,13 +486,12 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_kernel(flo
                                                                             int jbase, const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
   __shared__ float2 lds[C::M * C::S];
-  float2* base = ws + col_base(cg, blockIdx.x);
+  const ColBuf cb(ws + col_base(cg, blockIdx.x), cg);
   const int j0 = jbase + blockIdx.y * C::M;
-  auto ld = [&](int m, int n) -> float2 { return col_load(base, cg, j0 + m, n, in_cnt); };
+  auto ld = [&](int m, int n) -> float2 { return cb.load(n, j0 + m, j0 + m < cg.inner_count && n < in_cnt); };
   auto st = [&](int m, int k, float2 v) {
     const int e = k - out_off;
-    if (j0 + m >= cg.inner_count || e < 0 || e >= out_cnt) return;
-    base[int64_t(e) * cg.axis_stride + j0 + m] = v;
+    cb.store(e, j0 + m, j0 + m < cg.inner_count && uint32_t(e) < uint32_t(out_cnt), v);
   };
   fft<LOGF, INV, C::M, C::T, C::S, true>(lds, ld, st, tw);
 }
@@ -494,7 +512,7 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
   __shared__ float2 lds[C::M * C::S];
   const int64_t hk = blockIdx.x / bsplit;  // filter (channel, or FiLM image)
   const int part = int(blockIdx.x % bsplit);
-  const float2* kb = wsk + hk * cg.spec;
+  const ColBuf kb(wsk + hk * cg.spec, cg);
   const int j0 = jbase + blockIdx.y * C::M;
   // Filter spectrum of this column block (element e -> column e % M,
   // frequency e / M), loaded before the first transform so its latency hides.
@@ -504,15 +522,15 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
 #pragma unroll
   for (int it = 0; it < PT; ++it) {
     const int e = tk + it * C::T;
-    kv[it] = col_load(kb, cg, j0 + e % C::M, e / C::M, C::F);
+    kv[it] = kb.load(e / C::M, j0 + e % C::M, j0 + e % C::M < cg.inner_count);
   }
   const int nb = kfilm ? 1 : B;
   // bsplit > 1: this workgroup takes batches [part * nb / bsplit, (part + 1) * nb / bsplit)
   for (int bi = part * nb / bsplit; bi < (part + 1) * nb / bsplit; ++bi) {
     const int64_t blk = (kfilm ? hk : int64_t(bi) * H + hk) * cg.spec;
-    const float2* base = wsx + blk;  // may equal out (in place): a block is read before it is written
-    float2* out = wsy + blk;
-    auto ld = [&](int m, int n) -> float2 { return col_load(base, cg, j0 + m, n, S0); };
+    const ColBuf in(wsx + blk, cg);  // may be the output block (in place): a block is read before it is written
+    const ColBuf out(wsy + blk, cg);
+    auto ld = [&](int m, int n) -> float2 { return in.load(n, j0 + m, j0 + m < cg.inner_count && n < S0); };
     LdsTile<C::S, false> tile{lds};
     fft<LOGF, false, C::M, C::T, C::S, true>(lds, ld, tile, tw);
     const int tp = opaque_tid();
@@ -525,8 +543,7 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
     __syncthreads();
     auto st = [&](int m, int k, float2 v) {
       const int e = k - c0;
-      if (j0 + m >= cg.inner_count || e < 0 || e >= S0) return;
-      out[int64_t(e) * cg.axis_stride + j0 + m] = v;
+      out.store(e, j0 + m, j0 + m < cg.inner_count && uint32_t(e) < uint32_t(S0), v);
     };
     fft<LOGF, true, C::M, C::T, C::S, true>(lds, tile, st, tw);
   }
@@ -558,7 +575,7 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
   __shared__ float2 ldsX[C::M * C::S];  // X of the current image; at the end, Q
   const int64_t hk = blockIdx.x;
   const int j0 = jbase + blockIdx.y * C::M;
-  const float2* kb = wsk + hk * cg.spec;
+  const ColBuf kb(wsk + hk * cg.spec, cg);
   // Element it of a thread is column m = tp % M (fixed), frequency k = tp / M
   // + it * T / M.  Its filter value and shift ramp
   //   R = W_F0^{c0 k} * W_F1^{c1 k1} * W_F2^{c2 k2},  (k1, k2) = (j / FH, j % FH),
@@ -579,17 +596,17 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
 #pragma unroll
   for (int it = 0; it < PT; ++it) {
     const int k = kfirst + it * (C::T / C::M);
-    kv[it] = col_load(kb, cg, j, k, C::F);
+    kv[it] = kb.load(k, j, j < cg.inner_count);
     rr[it] = cmul(r12, tt.load(C::F, (rp.c0 * k) & (C::F - 1)));
     q[it] = make_float2(0.f, 0.f);
   }
   const int nb = kfilm ? 1 : B;
   for (int bi = 0; bi < nb; ++bi) {
     const int64_t bh = kfilm ? hk : (int64_t(bi) * H + hk);
-    float2* gb = wsg + bh * cg.spec;
-    const float2* xb = wsx + bh * cg.spec;
-    auto ldg = [&](int mm, int n) -> float2 { return col_load(gb, cg, j0 + mm, n, S0); };
-    auto ldx = [&](int mm, int n) -> float2 { return col_load(xb, cg, j0 + mm, n, S0); };
+    const ColBuf gb(wsg + bh * cg.spec, cg);
+    const ColBuf xb(wsx + bh * cg.spec, cg);
+    auto ldg = [&](int mm, int n) -> float2 { return gb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0); };
+    auto ldx = [&](int mm, int n) -> float2 { return xb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0); };
     LdsTile<C::S, false> stG{ldsG};
     LdsTile<C::S, false> stX{ldsX};
     fft<LOGF, false, C::M, C::T, C::S, true>(ldsG, ldg, stG, tw);
@@ -603,21 +620,15 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
     }
     __syncthreads();
     LdsTile<C::S, false> ldl{ldsG};
-    auto st = [&](int mm, int k, float2 v) {
-      if (j0 + mm >= cg.inner_count || k >= S0) return;
-      gb[int64_t(k) * cg.axis_stride + j0 + mm] = v;
-    };
+    auto st = [&](int mm, int k, float2 v) { gb.store(k, j0 + mm, j0 + mm < cg.inner_count && k < S0, v); };
     fft<LOGF, true, C::M, C::T, C::S, true>(ldsG, ldl, st, tw);  // ends with a barrier: ldsX is free
   }
 #pragma unroll
   for (int it = 0; it < PT; ++it) ldsX[m * C::S + kfirst + it * (C::T / C::M)] = q[it];
   __syncthreads();
-  float2* qb = wsq + hk * cg.spec;
+  const ColBuf qb(wsq + hk * cg.spec, cg);
   LdsTile<C::S, false> ldq{ldsX};
-  auto stq = [&](int mm, int k, float2 v) {
-    if (j0 + mm >= cg.inner_count || k >= K0) return;
-    qb[int64_t(k) * cg.axis_stride + j0 + mm] = v;
-  };
+  auto stq = [&](int mm, int k, float2 v) { qb.store(k, j0 + mm, j0 + mm < cg.inner_count && k < K0, v); };
   fft<LOGF, true, C::M, C::T, C::S, true>(ldsX, ldq, stq, tw);
 }
 
