@@ -347,77 +347,6 @@ struct Win12 {
   }
 };
 
-// Samples x[n + i], i < 8, of one row as raw bits.  AL as for Win12: n is a
-// multiple of 8 and the chunk is one (16-bit types) or two (fp32) aligned
-// 16-byte loads lying wholly inside or wholly outside [0, len); otherwise
-// eight element loads.  A chunk before the row (n < 0) reads as zero.
-template <int DT, bool AL>
-struct Win8 {
-  static constexpr bool HALF = DT != NSQ_DTYPE_F32;
-  static constexpr int W = (HALF && AL) ? 4 : 8;
-  uint32_t w[W];
-  __device__ __forceinline__ void load(const RowBuf<DT, false>& rb, int n) {
-    if constexpr (AL) {
-      constexpr int ES = HALF ? 2 : 4;
-      int off = n < 0 ? int(0x80000000u) : n * ES;
-      asm volatile("" : "+v"(off));
-      if constexpr (HALF) {
-        const auto m = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = m[i];
-      } else {
-        const auto m0 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off, 0, 0);
-        const auto m1 = __builtin_amdgcn_raw_buffer_load_b128(rb.r, off + 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { w[i] = m0[i]; w[4 + i] = m1[i]; }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) w[i] = rb.elem_halo_bits(n + i);
-    }
-  }
-  __device__ __forceinline__ float at(int i) const {  // i is a compile-time constant after unrolling
-    if constexpr (HALF && AL) {
-      const uint32_t v = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
-      return RowBuf<DT, false>::bits_to_f32(v);
-    } else {
-      return RowBuf<DT, false>::bits_to_f32(w[i]);
-    }
-  }
-};
-
-// Stores v[i] at positions n + i, i < 8, of one row.  AL as for Win8: n is a
-// multiple of 8 and the chunk goes out as one (16-bit types) or two (fp32)
-// 16-byte stores, dropped as a whole past the row end; otherwise pair stores.
-template <int DT, bool AL>
-__device__ __forceinline__ void store8(const RowBuf<DT, AL>& rb, int n, const float (&v)[8]) {
-  if constexpr (AL) {
-    using U4 = uint32_t __attribute__((ext_vector_type(4)));
-    const int off = n * int(sizeof(typename Elem<DT>::T));
-    if constexpr (DT == NSQ_DTYPE_F32) {
-      __builtin_amdgcn_raw_buffer_store_b128(U4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                                                __float_as_uint(v[3])},
-                                             rb.r, off, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b128(U4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
-                                                __float_as_uint(v[7])},
-                                             rb.r, off + 16, 0, 0);
-    } else {
-      uint32_t u[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if constexpr (DT == NSQ_DTYPE_BF16)
-          u[i] = f32x2_to_bf16x2_bits(v[2 * i], v[2 * i + 1]);
-        else
-          u[i] = __builtin_bit_cast(uint32_t, __floats2half2_rn(v[2 * i], v[2 * i + 1]));
-      }
-      __builtin_amdgcn_raw_buffer_store_b128(U4{u[0], u[1], u[2], u[3]}, rb.r, off, 0, 0);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) rb.store_pair(n + i, make_float2(v[i], v[i + 1]));
-  }
-}
-
 // Kernels shared by the causal conv and B2B backward passes.
 // gx[i] = sum_j w[j] gp[i + K - 1 - j]  (gp = gpre in GT precision).  grid as forward.
 template <int DT, int GT>

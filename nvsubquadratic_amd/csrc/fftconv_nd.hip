@@ -93,12 +93,23 @@ static bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int 
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
     constexpr int LOGN = decltype(L)::value;
     using C = RowNdCfg<LOGN>;
+    const dim3 grid(unsigned(ceil_div(rg.rows, C::M)));
+    const bool fast = MODE == ND_OUT_Y && o.off2 % 2 == 0 && o.w2 % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(o.out) & 15) == 0 && (reinterpret_cast<uintptr_t>(o.aux) & 15) == 0;
+    if constexpr (MODE == ND_OUT_Y) {
+      if (fast) {
+        if (o.s)
+          hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, true, true>), grid, dim3(C::T), 0, st, ws, rg, o, tw);
+        else
+          hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, false, true>), grid, dim3(C::T), 0, st, ws, rg, o,
+                             tw);
+        return;
+      }
+    }
     if (MODE == ND_OUT_Y && o.s)
-      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, true>), dim3(unsigned(ceil_div(rg.rows, C::M))),
-                         dim3(C::T), 0, st, ws, rg, o, tw);
+      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, true>), grid, dim3(C::T), 0, st, ws, rg, o, tw);
     else
-      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, false>), dim3(unsigned(ceil_div(rg.rows, C::M))),
-                         dim3(C::T), 0, st, ws, rg, o, tw);
+      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, false>), grid, dim3(C::T), 0, st, ws, rg, o, tw);
   });
 }
 

@@ -127,8 +127,10 @@ struct RowInvOut {
 
 // HAS_S: a shortcut is given (ND_OUT_Y); its term reads aux.  Loads are
 // branch-free (clamped indices, zero selected) so they overlap; only stores
-// are predicated.
-template <int LOGN, int DT, int MODE, bool HAS_S>
+// are predicated.  FAST (ND_OUT_Y; even off2, w2 a multiple of 8, out and aux
+// 16-byte aligned): the epilogue moves 8 consecutive kept samples per thread,
+// four complex values from LDS, one 16-byte aux load and one 16-byte store.
+template <int LOGN, int DT, int MODE, bool HAS_S, bool FAST = false>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const float2* __restrict__ ws, RowGeom rg,
                                                                         RowInvOut o, const float2* __restrict__ tw) {
   using C = RowNdCfg<LOGN>;
@@ -186,6 +188,30 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
   const int nvalid = nrows * o.w2;  // the tile's outputs are e in [0, nvalid), row-major
   const int64_t tbase = r0 * o.w2;   // 32-bit offsets from here (M * w2 is small)
   const ET* aux_t = aux + (HAS_S ? tbase : 0);
+  if constexpr (FAST) {
+    static_assert(MODE == ND_OUT_Y, "nd_row_inv_kernel: FAST epilogue writes y");
+    const int cpr = o.w2 >> 3;  // 8-sample chunks per row
+    const RowBuf<DT, false> ab(aux_t, HAS_S ? nvalid : 0);
+    const RowBuf<DT, true> ob((ET*)o.out + tbase, nvalid);
+    for (int ch = tslot; ch < C::M * cpr; ch += C::T) {
+      const int m = ch / cpr, c8 = (ch - m * cpr) * 8;
+      const bool ok = m < nrows;
+      const int e0 = ok ? m * o.w2 + c8 : nvalid;  // past the range: the aux load reads 0, the store is dropped
+      Win8<DT, true> a;
+      a.load(ab, e0);
+      const float2* zr = lds + (ok ? m : 0) * C::SP;
+      const int n0 = (c8 + o.off2) >> 1;
+      float y[8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float2 z = zr[pad16(n0 + u)];
+        y[2 * u] = epilogue<DT>(z.x * o.scale, HAS_S, HAS_S ? svs[m] : 0.f, a.at(2 * u));
+        y[2 * u + 1] = epilogue<DT>(z.y * o.scale, HAS_S, HAS_S ? svs[m] : 0.f, a.at(2 * u + 1));
+      }
+      store8<DT, true>(ob, e0, y);
+    }
+    return;
+  }
   // (row, column) of output e = eb + tslot + u*T for the LDS read, stepped without division
   int m_next = tslot / o.w2, c_next = tslot - m_next * o.w2;
   for (int eb = 0; eb < C::M * o.w2; eb += 8 * C::T) {
