@@ -257,10 +257,15 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
       // the narrow tail instance takes one image per workgroup (its work per
       // image is small, so a batch loop would leave the GPU idle)
       const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : 1;
-      hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT>),
-                         dim3(unsigned((p.kb != 1 ? BH : p.H) * bsplit), unsigned(gy)), dim3(ColNdCfg<LOGF, TGT>::T), 0,
-                         st, (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1),
-                         p.S[0], p.c[0], jbase, bsplit, tw);
+      const dim3 grid(unsigned((p.kb != 1 ? BH : p.H) * bsplit), unsigned(gy));
+      if (2 * p.S[0] <= p.F[0])
+        hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT, true>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st,
+                           (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1),
+                           p.S[0], p.c[0], jbase, bsplit, tw);
+      else
+        hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT, false>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st,
+                           (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1),
+                           p.S[0], p.c[0], jbase, bsplit, tw);
     });
   });
   if (!ok) return false;

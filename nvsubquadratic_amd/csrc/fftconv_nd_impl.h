@@ -527,14 +527,22 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_kernel(flo
 // Shared filter (kfilm = 0): grid.x = H * bsplit and a workgroup loops over
 // its share of the batch, so its slice of Khat is read once per channel (per
 // bsplit share), not once per image; FiLM: grid.x = B*H, one image each.
-// grid.y = column blocks.
-template <int LOGF, int TARGET = 8192>
+// grid.y = column blocks.  The first pass is one radix-R butterfly per thread
+// over elements j + r*NR of column m; the next image's inputs are loaded
+// before the current image's transforms.  HALF (S0 <= F/2, the zero padding
+// of a conv is at least half the axis): inputs r >= R/2 are zero, so only R/2
+// are loaded and the first pass's butterflies fold the zeros away.
+template <int LOGF, int TARGET = 8192, bool HALF = false>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
                                                                                 const float2* __restrict__ wsk,
                                                                                 ColGeom cg, int B, int H, int kfilm,
                                                                                 int S0, int c0, int jbase, int bsplit,
                                                                                 const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
+  constexpr int R = 1 << (LOGF < 4 ? LOGF : 4);  // first-pass radix, as chosen by fft_rec
+  constexpr int NR = C::F / R;
+  constexpr int RL = HALF ? R / 2 : R;           // first-pass inputs that can be nonzero
+  static_assert(C::M * NR == C::T, "nd_col_mul_kernel: one first-pass butterfly per thread");
   __shared__ float2 lds[C::M * C::S];
   const int64_t hk = blockIdx.x / bsplit;  // filter (channel, or FiLM image)
   const int part = int(blockIdx.x % bsplit);
@@ -552,11 +560,24 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
   }
   const int nb = kfilm ? 1 : B;
   // bsplit > 1: this workgroup takes batches [part * nb / bsplit, (part + 1) * nb / bsplit)
-  for (int bi = part * nb / bsplit; bi < (part + 1) * nb / bsplit; ++bi) {
-    const int64_t blk = (kfilm ? hk : int64_t(bi) * H + hk) * cg.spec;
-    const ColBuf in(wsx + blk, cg);  // may be the output block (in place): a block is read before it is written
-    const ColBuf out(wsy + blk, cg);
-    auto ld = [&](int m, int n) -> float2 { return in.load(n, j0 + m, j0 + m < cg.inner_count && n < S0); };
+  const int b_begin = part * nb / bsplit, b_end = (part + 1) * nb / bsplit;
+  const int m1 = int(threadIdx.x) % C::M, j1 = int(threadIdx.x) / C::M;  // first-pass butterfly of this thread
+  const bool colok = j0 + m1 < cg.inner_count;
+  auto block = [&](int bi) { return (kfilm ? hk : int64_t(bi) * H + hk) * cg.spec; };
+  float2 raw[RL];
+  auto issue = [&](int bi) {
+    const ColBuf in(wsx + block(bi), cg);
+#pragma unroll
+    for (int r = 0; r < RL; ++r) raw[r] = in.load(j1 + r * NR, j0 + m1, colok && j1 + r * NR < S0);
+  };
+  if (b_begin < b_end) issue(b_begin);
+  for (int bi = b_begin; bi < b_end; ++bi) {
+    float2 v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = r < RL ? raw[r] : make_float2(0.f, 0.f);
+    if (bi + 1 < b_end) issue(bi + 1);  // the block is read before the (in-place) output is written
+    const ColBuf out(wsy + block(bi), cg);
+    RegStream<R> ld{v};
     LdsTile<C::S, false> tile{lds};
     fft<LOGF, false, C::M, C::T, C::S, true>(lds, ld, tile, tw);
     const int tp = opaque_tid();
@@ -567,9 +588,9 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
       z = cmul(z, kv[it]);
     }
     __syncthreads();
-    auto st = [&](int m, int k, float2 v) {
+    auto st = [&](int m, int k, float2 val) {
       const int e = k - c0;
-      out.store(e, j0 + m, j0 + m < cg.inner_count && uint32_t(e) < uint32_t(S0), v);
+      out.store(e, j0 + m, j0 + m < cg.inner_count && uint32_t(e) < uint32_t(S0), val);
     };
     fft<LOGF, true, C::M, C::T, C::S, true>(lds, tile, st, tw);
   }
