@@ -354,8 +354,11 @@ constexpr int kColTilesPerWG = 8;
 // Tile t = row * (N2 / M) + column block: column block fastest.  The first
 // pass is one radix-R butterfly per thread (T = M * N1 / R); its R input
 // pairs for the next tile are loaded as raw bits before the current tile's
-// passes run and converted when that tile starts.
-template <int LOGN1, int LOGN, int DT, bool AL>
+// passes run and converted when that tile starts.  HALF (valid <= N real
+// samples, i.e. at least half the transform is zero padding, as in every
+// causal conv with K > 1): the inputs n1 >= N1/2 of a column are zero, so only
+// R/2 pairs are loaded and the first pass's butterflies fold the zeros away.
+template <int LOGN1, int LOGN, int DT, bool AL, bool HALF>
 __global__ __launch_bounds__(ColCfg<LOGN1>::T) __attribute__((amdgpu_waves_per_eu(4))) void col_fwd_kernel(
     RealRows<DT> src, float2* __restrict__ ws, const float2* __restrict__ tw, int64_t ntiles) {
   using C = ColCfg<LOGN1>;
@@ -364,23 +367,24 @@ __global__ __launch_bounds__(ColCfg<LOGN1>::T) __attribute__((amdgpu_waves_per_e
   constexpr int NCB = N2 / C::M;
   constexpr int R = 1 << (LOGN1 < 4 ? LOGN1 : 4);  // first-pass radix, as chosen by fft_rec
   constexpr int NR = C::N1 / R;
+  constexpr int RL = HALF ? R / 2 : R;             // inputs that can be nonzero
   static_assert(C::M * NR == C::T, "col_fwd: one first-pass butterfly per thread");
   __shared__ float2 lds[C::M * C::S];
   const int tid = threadIdx.x;
   const int m = tid % C::M, j = tid / C::M;  // the first pass's (transform, butterfly) of this thread
-  typename RB::PairBits raw[R];
+  typename RB::PairBits raw[RL];
   auto issue = [&](int64_t t) {
     const int c0 = int(t % NCB) * C::M;
     const RB in(src.p + (t / NCB) * src.stride, src.valid);
 #pragma unroll
-    for (int r = 0; r < R; ++r) raw[r] = in.load_pair_bits(2 * (int64_t(j + r * NR) * N2 + c0 + m));
+    for (int r = 0; r < RL; ++r) raw[r] = in.load_pair_bits(2 * (int64_t(j + r * NR) * N2 + c0 + m));
   };
   int64_t t = blockIdx.x;  // grid <= ntiles
   issue(t);
   for (;;) {
     float2 v[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[r] = RB::pair_from_bits(raw[r]);
+    for (int r = 0; r < R; ++r) v[r] = r < RL ? RB::pair_from_bits(raw[r < RL ? r : 0]) : make_float2(0.f, 0.f);
     const int64_t tn = t + gridDim.x;
     if (tn < ntiles) issue(tn);
     RegStream<R> ld{v};
@@ -809,12 +813,17 @@ template <int LOGN1, int LOGN, int DT>
 static void launch_col_fwd(RealRows<DT> src, int64_t rows, float2* out, const float2* tw, hipStream_t st) {
   const int64_t nb = rows * ((int64_t(1) << (LOGN - LOGN1)) / ColCfg<LOGN1>::M);
   const unsigned grid = unsigned(ceil_div(nb, kColTilesPerWG));
-  if (pairs_aligned<DT>(src.p, src.stride, src.valid))
-    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, true>), dim3(grid), dim3(ColCfg<LOGN1>::T), 0, st, src, out,
-                       tw, nb);
+  auto go = [&](auto al, auto half) {
+    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, decltype(al)::value, decltype(half)::value>), dim3(grid),
+                       dim3(ColCfg<LOGN1>::T), 0, st, src, out, tw, nb);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  const bool al = pairs_aligned<DT>(src.p, src.stride, src.valid);
+  if (src.valid <= (int64_t(1) << LOGN))  // packed samples [N/2, N) all zero
+    al ? go(T_{}, T_{}) : go(F_{}, T_{});
   else
-    hipLaunchKernelGGL((col_fwd_kernel<LOGN1, LOGN, DT, false>), dim3(grid), dim3(ColCfg<LOGN1>::T), 0, st, src, out,
-                       tw, nb);
+    al ? go(T_{}, F_{}) : go(F_{}, F_{});
 }
 
 template <int LOGN1, int LOGN, int DT>
