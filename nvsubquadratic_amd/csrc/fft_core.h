@@ -301,6 +301,22 @@ struct RegStream {
   __device__ __forceinline__ float2 operator()(int, int) { return v[k++]; }
 };
 
+// First-pass loader wrapper for zero-padded transforms: with HALF, the inputs
+// r >= R/2 of each radix-R first-pass butterfly (elements j + r*N/R >= N/2)
+// are zero, returned as constants (the call order is fixed and unrolled, so r
+// is a constant) and the butterflies fold them away; the rest go to LD.
+template <int R, bool HALF, class LD>
+struct HalfZeroLoad {
+  LD& ld;
+  int q = 0;
+  __device__ __forceinline__ float2 operator()(int m, int n) {
+    const int r = q % R;
+    ++q;
+    if (HALF && r >= R / 2) return make_float2(0.f, 0.f);
+    return ld(m, n);
+  }
+};
+
 template <int LOGN, int LOGNS, bool INV, int M, int T, bool TMAJOR, class LDF, class STL, class LDL, class STF>
 __device__ __forceinline__ void fft_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last,
                                         const float2* __restrict__ tw) {

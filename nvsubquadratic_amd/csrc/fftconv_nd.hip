@@ -77,12 +77,18 @@ static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
     constexpr int LOGN = decltype(L)::value;
     using C = RowNdCfg<LOGN>;
-    if (pairs_aligned<DT>(src, len, len))
-      hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, true>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0,
+    const dim3 grid{unsigned(ceil_div(rg.rows, C::M))};
+    auto go = [&](auto al, auto half) {
+      hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value>), grid, dim3(C::T), 0,
                          st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool al = pairs_aligned<DT>(src, len, len);
+    if (len <= C::N)  // packed samples [N/2, N) of every row are zero
+      al ? go(T_{}, T_{}) : go(F_{}, T_{});
     else
-      hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, false>), dim3(unsigned(ceil_div(rg.rows, C::M))), dim3(C::T), 0,
-                         st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+      al ? go(T_{}, F_{}) : go(F_{}, F_{});
   });
 }
 
@@ -191,12 +197,16 @@ static bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int
     return with_plane(p, [&](auto LN, auto LF) {
       constexpr int LOGN = decltype(LN)::value, LOGF1 = decltype(LF)::value;
       const dim3 grid(unsigned(nbh * n0));
-      if (al)
-        hipLaunchKernelGGL((nd_plane_fwd_kernel<LOGN, LOGF1, DT, true>), grid, dim3(256), 0, st, (const ET*)src, n0,
-                           n1, len, ws, p.spec, tw);
+      auto go = [&](auto alc, auto half) {
+        hipLaunchKernelGGL((nd_plane_fwd_kernel<LOGN, LOGF1, DT, decltype(alc)::value, decltype(half)::value>), grid,
+                           dim3(256), 0, st, (const ET*)src, n0, n1, len, ws, p.spec, tw);
+      };
+      using T_ = std::true_type;
+      using F_ = std::false_type;
+      if (len <= (1 << LOGN) && 2 * n1 <= (1 << LOGF1))  // rows and columns at least half zero padding
+        al ? go(T_{}, T_{}) : go(F_{}, T_{});
       else
-        hipLaunchKernelGGL((nd_plane_fwd_kernel<LOGN, LOGF1, DT, false>), grid, dim3(256), 0, st, (const ET*)src, n0,
-                           n1, len, ws, p.spec, tw);
+        al ? go(T_{}, F_{}) : go(F_{}, F_{});
     });
   }
   if (!row_fwd<DT>(p, src, nbh, n0, n1, len, ws, tw, st)) return false;
@@ -293,9 +303,15 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
     constexpr int LOGF = decltype(L)::value;
     col_blocks<LOGF, kNdBwdTile>(cg.inner_count, [&](auto tile, int gy, int jbase) {
       constexpr int TGT = decltype(tile)::value;
-      hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT>), dim3(unsigned(NK), unsigned(gy)),
-                         dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg, (const float2*)wsx, (const float2*)wsk, wsq, cg,
-                         int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.K[0], rp, jbase, tw);
+      const dim3 grid{unsigned(NK), unsigned(gy)};
+      if (2 * p.S[0] <= p.F[0])  // the g and x columns are at least half zero padding
+        hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, true>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg,
+                           (const float2*)wsx, (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1),
+                           p.S[0], p.K[0], rp, jbase, tw);
+      else
+        hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, false>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg,
+                           (const float2*)wsx, (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1),
+                           p.S[0], p.K[0], rp, jbase, tw);
     });
   });
   if (!ok) return false;

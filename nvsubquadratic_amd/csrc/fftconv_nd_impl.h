@@ -67,7 +67,9 @@ struct RowGeom {
 // Forward real FFT of rows of a contiguous [BH][n0][n1][len] real tensor,
 // zero-padded to F2 = 2N, into workspace bins [0, FH) of row (a0, a1).
 // AL: aligned pair access (even len, aligned base; see load_pair_nb).
-template <int LOGN, int DT, bool AL>
+// HALF: len <= N (at least half of each row is zero padding): the first pass
+// folds the zero half (HalfZeroLoad).
+template <int LOGN, int DT, bool AL, bool HALF = false>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typename Elem<DT>::T* __restrict__ src,
                                                                         int len, RowGeom rg, float2* __restrict__ ws,
                                                                         const float2* __restrict__ tw) {
@@ -86,8 +88,9 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
     const bool rok = r < rg.rows;  // tail rows read row 0 and select zero
     return load_pair_nb<DT, AL>(src + (rok ? r : 0) * len, 2 * int64_t(n), rok ? len : 0);
   };
+  HalfZeroLoad<(LOGN < 4 ? (1 << LOGN) : 16), HALF, decltype(ld)> ld1{ld};
   LdsTile<C::SP, true> st{lds};
-  fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
+  fft<LOGN, false, C::M, C::T, C::SP>(lds, ld1, st, tw);
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
     const int s = tslot + i * C::T;
@@ -280,7 +283,9 @@ struct PlaneCfg {
                              F1 * RS * 8 <= 80 * 1024;
 };
 
-template <int LOGN, int LOGF1, int DT, bool AL>
+// HALF: len <= N and n1 <= F1/2 (each row and each column at least half zero
+// padding): both first passes fold the zero half (HalfZeroLoad).
+template <int LOGN, int LOGF1, int DT, bool AL, bool HALF = false>
 __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<DT>::T* __restrict__ src, int n0,
                                                            int n1, int len, float2* __restrict__ ws, int64_t spec,
                                                            const float2* __restrict__ tw) {
@@ -298,7 +303,8 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
       const bool ok = a1 < n1;
       return load_pair_nb<DT, AL>(xs + int64_t(ok ? a1 : 0) * len, 2 * int64_t(n), ok ? len : 0);
     };
-    fft_rec<LOGN, 0, false, C::MR, C::T, false>(ld, rows, rows, rows, tw);
+    HalfZeroLoad<16, HALF, decltype(ld)> ld1{ld};  // LOGN >= 4: radix-16 first pass
+    fft_rec<LOGN, 0, false, C::MR, C::T, false>(ld1, rows, rows, rows, tw);
     const int tslot = opaque_tid();  // once: the asm statement would order the unrolled loads
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
@@ -322,7 +328,8 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
       const float2 v = P[(ok ? n : 0) * RS + pad16(j0 + m)];
       return make_float2(ok ? v.x : 0.f, ok ? v.y : 0.f);
     };
-    fft_rec<LOGF1, 0, false, C::MC, C::T, true>(ld, cols, cols, cols, tw);
+    HalfZeroLoad<16, HALF, decltype(ld)> ld1{ld};  // LOGF1 >= 4: radix-16 first pass
+    fft_rec<LOGF1, 0, false, C::MC, C::T, true>(ld1, cols, cols, cols, tw);
   }
   // Store [F1][FH]; column 0 separates into the DC (j = 0) and Nyquist (j = N) bins.
   float2* out = ws + (plane / n0) * spec + (plane % n0) * int64_t(C::F1) * C::FH;
@@ -607,7 +614,7 @@ struct Ramp {
 // Adjoint, axis 0.  Shared kernel (kfilm = 0): grid.x = H, loops b; FiLM:
 // grid.x = B*H, one b.  Writes P (gx pre-image, window [0, S0)) into wsg and
 // Q (gk pre-image, window [0, K0)) into wsq.
-template <int LOGF, int TARGET = kNdBwdTile>
+template <int LOGF, int TARGET = kNdBwdTile, bool HALF = false>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel(float2* __restrict__ wsg,
                                                                                 const float2* __restrict__ wsx,
                                                                                 const float2* __restrict__ wsk,
@@ -656,8 +663,11 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
     auto ldx = [&](int mm, int n) -> float2 { return xb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0); };
     LdsTile<C::S, false> stG{ldsG};
     LdsTile<C::S, false> stX{ldsX};
-    fft<LOGF, false, C::M, C::T, C::S, true>(ldsG, ldg, stG, tw);
-    fft<LOGF, false, C::M, C::T, C::S, true>(ldsX, ldx, stX, tw);
+    constexpr int R1 = 1 << (LOGF < 4 ? LOGF : 4);  // first-pass radix
+    HalfZeroLoad<R1, HALF, decltype(ldg)> ldg1{ldg};  // HALF: S0 <= F/2
+    HalfZeroLoad<R1, HALF, decltype(ldx)> ldx1{ldx};
+    fft<LOGF, false, C::M, C::T, C::S, true>(ldsG, ldg1, stG, tw);
+    fft<LOGF, false, C::M, C::T, C::S, true>(ldsX, ldx1, stX, tw);
 #pragma unroll
     for (int it = 0; it < PT; ++it) {
       const int a = m * C::S + kfirst + it * (C::T / C::M);
