@@ -20,8 +20,11 @@ from oracle.fftconv_ref import fftconv_nd_np, fftconv_nd_torch, rel_l2
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "nd.npz")
 
+# The last two shapes leave less than half of an axis as padding (S > F/2: 60 -> F = 64, 50 -> 64), so the
+# passes that fold a zero first-pass half run their unpruned variants too.
 SHAPES_2D = [(2, 64, 32, 32, 7, 7), (4, 128, 14, 14, 7, 7), (2, 256, 28, 28, 13, 13), (1, 64, 64, 64, 15, 15),
-             (1, 384, 14, 14, 14, 14), (2, 64, 14, 14, 28, 28), (2, 8, 32, 16, 7, 5), (1, 3, 5, 7, 10, 13)]
+             (1, 384, 14, 14, 14, 14), (2, 64, 14, 14, 28, 28), (2, 8, 32, 16, 7, 5), (1, 3, 5, 7, 10, 13),
+             (2, 8, 60, 50, 3, 5), (1, 16, 20, 60, 9, 3)]
 
 
 def _grad_check(xs, ks, fn, kb=1, dtype=torch.float32, tol=1e-4):
