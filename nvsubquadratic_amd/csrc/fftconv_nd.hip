@@ -342,6 +342,11 @@ static int validate_nd(int nd, const void* a, const void* b, const float* k, int
               (long long)(B * H * int64_t(p.F[0]) * p.F[1]));
     return NSQ_ERR_UNSUPPORTED;
   }
+  if (p.spec * int64_t(sizeof(float2)) >= (int64_t(1) << 31)) {  // column passes: 32-bit offsets in a block
+    set_error("fftconv_nd: unsupported shape: one spectrum block F0*F1*(F2/2+1) = %lld complex values exceeds 2 GiB",
+              (long long)p.spec);
+    return NSQ_ERR_UNSUPPORTED;
+  }
   return NSQ_OK;
 }
 

@@ -81,3 +81,17 @@ def test_missing_library_raises_at_call_time(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(_lib.HipLibraryError, match="not found"):
         _lib.get_lib()
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_nd_spectrum_block_over_2gib_rejected():
+    """The 2D/3D column passes address one spectrum block with 32-bit byte
+    offsets; a block of 2 GiB or more (F = 1024^3: 1024*1024*513 complex) must be
+    refused before any launch (validation runs before the device is touched)."""
+    lib = _lib.get_lib()
+    dummy = 16  # non-null; never dereferenced when validation fails
+    S, K = _lib.i64_array([1000, 1000, 1000]), _lib.i64_array([3, 3, 3])
+    rc = lib.nsq_fftconv_nd_fwd(3, dummy, dummy, None, dummy, _lib.NSQ_DTYPE[torch.float32], 1, 1, S, K, 1, dummy,
+                                1 << 40, None)
+    assert rc == 2  # NSQ_ERR_UNSUPPORTED
+    assert b"2 GiB" in lib.nsq_last_error()
