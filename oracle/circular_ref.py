@@ -1,0 +1,66 @@
+"""CPU restatement of the reference circular FFT convolution -- TEST INFRASTRUCTURE ONLY.
+
+* :func:`circular_fftconv_torch` follows nvsubquadratic/ops/circular_fftconv.py
+  step for step in float32 CPU torch (1D :310-404, 2D and 3D the same steps over
+  2 or 3 axes): cast to fp32, ``rfftn`` of x and of the kernel at the input's
+  own sizes (no padding; the kernel is zero-extended), multiply by the
+  phase ramp of the integer shift ``-((K_d - 1) // 2)`` per axis
+  (``_PhaseRampCache*.get``: ``exp(-2 pi i sum_d shift_d f_d)`` with
+  ``fftfreq`` / ``rfftfreq``), ``irfftn``, cast to ``x.dtype``, then
+  ``+ shortcut * x``.  Autograd-capable: its gradients are the reference's.
+* :func:`circular_conv_direct_np` is the brute-force float64 circular
+  convolution the reference's own tests compare against
+  (tests/ops/test_circular_fftconv.py:69-105: circular padding K//2 left,
+  K - 1 - K//2 right, flipped kernel, grouped conv), written out as
+  ``y[n] = sum_j k[j] x[(n + (K - 1)//2 - j) mod S]`` per axis.  It pins the
+  FFT restatement (tests/test_oracle_circular.py) with no FFT involved.
+"""
+
+from __future__ import annotations
+
+import itertools
+import math
+
+import numpy as np
+import torch
+
+
+def circular_fftconv_torch(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None = None) -> torch.Tensor:
+    """x ``[B, H, *S]`` (1 to 3 spatial axes), kernel ``[1|B, H, *K]`` (K_d <= S_d)."""
+    nd = x.dim() - 2
+    S = list(x.shape[2:])
+    K = list(kernel.shape[2:])
+    dims = tuple(range(2, 2 + nd))
+    xf = torch.fft.rfftn(x.to(torch.float32), s=S, dim=dims)
+    kf = torch.fft.rfftn(kernel.to(torch.float32), s=S, dim=dims)
+    # phase ramp of the shift -((K_d - 1) // 2) along every axis (circular_fftconv.py:_PhaseRampCache*)
+    phases = torch.zeros([S[d] if d < nd - 1 else S[d] // 2 + 1 for d in range(nd)], dtype=torch.float32)
+    for d in range(nd):
+        f = torch.fft.rfftfreq(S[d]) if d == nd - 1 else torch.fft.fftfreq(S[d])
+        shape = [1] * nd
+        shape[d] = -1
+        phases = phases + (-2.0 * math.pi * -((K[d] - 1) // 2)) * f.to(torch.float32).reshape(shape)
+    kf = kf * torch.complex(torch.cos(phases), torch.sin(phases))
+    y = torch.fft.irfftn(xf * kf, s=S, dim=dims).to(x.dtype)
+    if shortcut is not None:
+        y = y + shortcut.to(x.dtype).reshape([1, -1] + [1] * nd) * x
+    return y
+
+
+def circular_conv_direct_np(x, kernel, shortcut=None) -> np.ndarray:
+    """float64 brute force: y[b,h,n] = sum_j k[b|0,h,j] x[b,h,(n + c - j) mod S] per axis, c = (K-1)//2."""
+    x = np.asarray(x, dtype=np.float64)
+    k = np.asarray(kernel, dtype=np.float64)
+    nd = x.ndim - 2
+    S = x.shape[2:]
+    K = k.shape[2:]
+    c = [(kd - 1) // 2 for kd in K]
+    y = np.zeros_like(x)
+    for j in itertools.product(*[range(kd) for kd in K]):
+        # x[(n + c - j) mod S] = roll(x, shift = j - c)
+        shifted = np.roll(x, shift=[j[d] - c[d] for d in range(nd)], axis=tuple(range(2, 2 + nd)))
+        w = k[(slice(None), slice(None)) + tuple(j)]  # [1|B, H]
+        y += w.reshape(w.shape + (1,) * nd) * shifted
+    if shortcut is not None:
+        y += np.asarray(shortcut, dtype=np.float64).reshape([1, -1] + [1] * nd) * x
+    return y
