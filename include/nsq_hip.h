@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 3
+#define NSQ_ABI_VERSION 4
 
 enum {
   NSQ_OK = 0,
@@ -90,6 +90,25 @@ int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut
 int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
                              float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
                              void* workspace, size_t workspace_bytes, int fwd_state, void* stream);
+
+/*
+ * 1D circular (periodic) FFT convolution (+ shortcut), FFT length L (no padding):
+ *   y[b,h,n] = sum_{j<K} k[b|0,h,j] x[b,h,(n + (K-1)//2 - j) mod L],
+ *   y = y.to(dtype) + shortcut * x.
+ * k: [kbatch*H, K] float32, kbatch = 1 (shared) or B (per-sample FiLM kernels);
+ * gk likewise; gs: [kbatch*H] float32 partials (the caller sums over kbatch).
+ * 1 <= K <= L; L must be a power of two in [16, 16384] (NSQ_ERR_UNSUPPORTED
+ * otherwise).  No workspace.  Replaces nvsubquadratic/ops/circular_fftconv.py:310-404
+ * (circular_fftconv1d_fp32_bhl, torch.fft in the reference; its autograd for the
+ * backward): gx = corr(g, k) + s*g, gk[j] = sum_{b,n} g[n] x[(n + (K-1)//2 - j) mod L],
+ * gs = sum g*x.
+ */
+int nsq_circular_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                               int64_t H, int64_t L, int64_t K, int64_t kbatch, void* stream);
+
+int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
+                               float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
+                               int64_t kbatch, void* stream);
 
 /*
  * Depthwise causal direct convolution, nn.Conv1d tap order with left padding
@@ -162,6 +181,33 @@ int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortc
 int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
                        float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
                        void* workspace, size_t workspace_bytes, int fwd_state, void* stream);
+
+/*
+ * Circular and mixed-boundary 2D / 3D FFT convolution: the nsq_fftconv_nd_*
+ * calls above with a per-axis boundary condition.  Bit d of `periodic` set =
+ * axis d is periodic: no padding along it, K_d <= S_d, and
+ *   y[.., n_d, ..] = sum_j k[.., j_d, ..] x[.., (n_d + (K_d-1)//2 - j_d) mod S_d, ..]
+ * (the circular "same" alignment, shift -((K_d-1)//2) as a phase ramp on the
+ * filter spectrum).  Clear bits are zero-padded "same" axes exactly as above.
+ * Periodic lengths must be powers of two in [16, 1024] (NSQ_ERR_UNSUPPORTED
+ * otherwise).  periodic = 0 is nsq_fftconv_nd_*; all bits set is the circular
+ * conv.  Replaces nvsubquadratic/ops/circular_fftconv.py:406-483
+ * (circular_fftconv2d_fp32_bhl), :486-569 (circular_fftconv3d_fp32_bhl) and
+ * nvsubquadratic/ops/mixed_fftconv.py:504-630 (_mixed_fftconv_nd_fp32_bhl,
+ * behind mixed_fftconv{2,3}d_fp32_bhl :663-729), which are torch.fft code in
+ * the reference (no native kernel to bind).  Workspace and fwd_state as above.
+ */
+size_t nsq_mixed_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
+                                            int64_t kbatch, unsigned periodic, int direction);
+
+int nsq_mixed_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype,
+                             int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
+                             unsigned periodic, void* workspace, size_t workspace_bytes, void* stream);
+
+int nsq_mixed_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx,
+                             float* gk, float* gs, int dtype, int64_t B, int64_t H, const int64_t* S,
+                             const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace,
+                             size_t workspace_bytes, int fwd_state, void* stream);
 
 #ifdef __cplusplus
 }

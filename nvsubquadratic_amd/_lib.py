@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class HipLibraryError(RuntimeError):
@@ -46,6 +46,7 @@ class HipLibraryError(RuntimeError):
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
+_c_uint = ctypes.c_uint
 _c_size = ctypes.c_size_t
 
 # name -> (restype, argtypes).  Must match include/nsq_hip.h.
@@ -63,6 +64,17 @@ _SIGNATURES = {
         [
             _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
             _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_int, _c_void_p,
+        ],
+    ),
+    "nsq_circular_fftconv1d_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p],
+    ),
+    "nsq_circular_fftconv1d_bwd": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p,
         ],
     ),
     "nsq_causal_conv1d_fwd": (
@@ -101,6 +113,18 @@ _SIGNATURES = {
         _c_int,
         [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64,
          ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_void_p, _c_size, _c_int, _c_void_p],
+    ),
+    "nsq_mixed_fftconv_nd_workspace_bytes": (
+        _c_size, [_c_int, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_uint, _c_int]),
+    "nsq_mixed_fftconv_nd_fwd": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, ctypes.POINTER(_c_i64),
+         ctypes.POINTER(_c_i64), _c_i64, _c_uint, _c_void_p, _c_size, _c_void_p],
+    ),
+    "nsq_mixed_fftconv_nd_bwd": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64,
+         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_uint, _c_void_p, _c_size, _c_int, _c_void_p],
     ),
 }
 

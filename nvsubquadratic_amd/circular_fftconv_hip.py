@@ -1,0 +1,178 @@
+r"""HIP circular (periodic) FFT convolution with the ``nvsubquadratic.ops.circular_fftconv`` signatures.
+
+Reference: ``nvsubquadratic/ops/circular_fftconv.py`` (torch.fft only, no
+native kernel).  Per axis of length ``S_d`` with a kernel of ``K_d <= S_d``
+taps the output is the circular convolution aligned to "same":
+
+    y[n] = sum_j k[j] x[(n + (K_d - 1) // 2 - j) mod S_d]
+
+(the reference's ``rfftn(x) * rfftn(k) * phase_ramp`` with shift
+``-((K_d - 1) // 2)``, ``circular_fftconv.py:310-404``), cast to ``x.dtype``,
+then ``+ shortcut * x``.
+
+How: the 2D / 3D calls run the HIP N-d engine with every axis periodic
+(``nsq_mixed_fftconv_nd_*``): FFT length ``S_d`` (no padding), the shift as a
+ramp folded into the filter values of the product pass, no crop.  The 1D call
+runs the fused 1D kernels at FFT length ``L`` with the ramp on the filter's
+spectrum (``nsq_circular_fftconv1d_*``).  ``use_phase_shift`` is accepted for
+signature parity; both of the reference's branches give the same result and
+the kernels always apply the shift in the frequency domain.
+
+Sizes: periodic lengths must be powers of two (2D / 3D: 16..1024 per axis;
+1D: 16..16384); other sizes raise ``NotImplementedError`` (the product has no
+CPU fallback).
+"""
+
+from __future__ import annotations
+
+import torch
+from einops import rearrange
+
+from . import _lib
+from .fftconv_hip import _nd_core
+
+
+__all__ = [
+    "circular_fftconv1d_fp32_bhl",
+    "circular_fftconv1d_fp32_bhl_w_reshape",
+    "circular_fftconv2d_fp32_bhl",
+    "circular_fftconv2d_fp32_bhl_w_reshape",
+    "circular_fftconv3d_fp32_bhl",
+    "circular_fftconv3d_fp32_bhl_w_reshape",
+    "circular_fftconv1d_fwd_raw",
+    "circular_fftconv1d_bwd_raw",
+]
+
+
+def _check_common(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, nd: int) -> None:
+    """Argument checks of the reference (``circular_fftconv.py:363-369, 400-401, 440-447, 539-545``)."""
+    B, H = x.shape[:2]
+    assert len(kernel.shape) == nd + 2, f"Unexpected kernel shape: {kernel.shape}."
+    assert kernel.shape[0] in (1, B), (
+        f"Leading dimension must be 1 or batch_size ({B}). Got kernel.shape={kernel.shape}."
+    )
+    assert kernel.shape[1] == H, "Input and kernel must have the same number of channels (H)."
+    for d in range(nd):
+        assert kernel.shape[2 + d] <= x.shape[2 + d], (
+            f"Kernel must be <= input along each axis. Got K={tuple(kernel.shape[2:])}, S={tuple(x.shape[2:])}."
+        )
+    if shortcut is not None:
+        assert shortcut.dtype == x.dtype, f"shortcut.dtype ({shortcut.dtype}) must match x.dtype ({x.dtype})"
+        assert shortcut.shape == (H,)
+
+
+# ---------------------------------------------------------------------------
+# 1D: fused kernels at FFT length L
+# ---------------------------------------------------------------------------
+def circular_fftconv1d_fwd_raw(x, k, s, y, kbatch: int):
+    """Launch the 1D circular forward: x/y ``[B, H, L]``, k float32 ``[kbatch*H, K]``, s ``[H]`` or None."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, H, L = x.shape
+    _lib.check(lib.nsq_circular_fftconv1d_fwd(
+        x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype), B, H, L, k.shape[-1],
+        kbatch, _lib.stream_ptr(x.device)))
+    return y
+
+
+def circular_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int):
+    """Launch the 1D circular backward (gk ``[kbatch*H, K]``, gs ``[kbatch*H]`` partials or None)."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, H, L = x.shape
+    _lib.check(lib.nsq_circular_fftconv1d_bwd(
+        g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
+        _lib.dtype_code(x.dtype), B, H, L, k.shape[-1], kbatch, _lib.stream_ptr(x.device)))
+
+
+class _CircularFFTConv1d(torch.autograd.Function):
+    """x: [B, H, L] contiguous; k: [kbatch*H, K] contiguous float32; s: [H] in x.dtype or None."""
+
+    @staticmethod
+    def forward(ctx, x, k, s, kbatch):
+        y = torch.empty_like(x)
+        circular_fftconv1d_fwd_raw(x, k, s, y, kbatch)
+        ctx.save_for_backward(x, k, s)
+        ctx.kbatch = kbatch
+        ctx.has_s = s is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, k, s = ctx.saved_tensors
+        g = gy.to(x.dtype).contiguous()
+        gx = torch.empty_like(x)
+        gk = torch.empty_like(k)
+        H = x.shape[1]
+        gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
+        circular_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch)
+        gsum = None
+        if ctx.has_s:
+            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
+        return gx, gk, gsum, None
+
+
+def circular_fftconv1d_fp32_bhl(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+    use_phase_shift: bool = True,
+) -> torch.Tensor:
+    """1D circular conv, BHL ``[B, H, L]``, kernel ``[1|B, H, K]`` (``circular_fftconv.py:310-404``)."""
+    del use_phase_shift  # same result either way (see module docstring)
+    B, H, L = x.shape
+    _check_common(x, kernel, shortcut, 1)
+    kbatch = kernel.shape[0]
+    input_dtype = x.dtype
+    compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
+    xc = x.to(compute_dtype).contiguous()
+    kc = kernel.float().reshape(kbatch * H, kernel.shape[-1]).contiguous()
+    sc = None if shortcut is None else shortcut.to(compute_dtype).contiguous()
+    return _CircularFFTConv1d.apply(xc, kc, sc, kbatch).to(input_dtype)
+
+
+def circular_fftconv2d_fp32_bhl(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+    use_phase_shift: bool = True,
+) -> torch.Tensor:
+    """2D circular conv, ``[B, H, X, Y]``, kernel ``[1|B, H, Kx, Ky]`` (``circular_fftconv.py:406-483``)."""
+    del use_phase_shift
+    assert x.ndim == 4, f"x must be [B, H, X, Y]; got {tuple(x.shape)}"
+    _check_common(x, kernel, shortcut, 2)
+    return _nd_core(x, kernel, shortcut, 2, periodic=0b11)
+
+
+def circular_fftconv3d_fp32_bhl(
+    x: torch.Tensor,
+    kernel: torch.Tensor,
+    shortcut: torch.Tensor | None = None,
+    use_phase_shift: bool = True,
+) -> torch.Tensor:
+    """3D circular conv, ``[B, H, X, Y, Z]``, kernel ``[1|B, H, Kx, Ky, Kz]`` (``circular_fftconv.py:486-569``)."""
+    del use_phase_shift
+    assert x.ndim == 5, f"x must be [B, H, X, Y, Z]; got {tuple(x.shape)}"
+    _check_common(x, kernel, shortcut, 3)
+    return _nd_core(x, kernel, shortcut, 3, periodic=0b111)
+
+
+def circular_fftconv1d_fp32_bhl_w_reshape(x, kernel, shortcut=None, use_phase_shift=True):
+    """BLH ``[B, L, H]`` input, kernel ``[1|B, K, H]`` (``circular_fftconv.py:585-607``)."""
+    y = circular_fftconv1d_fp32_bhl(rearrange(x, "b l h -> b h l"), rearrange(kernel, "b k h -> b h k"), shortcut,
+                                    use_phase_shift)
+    return rearrange(y, "b h l -> b l h")
+
+
+def circular_fftconv2d_fp32_bhl_w_reshape(x, kernel, shortcut=None, use_phase_shift=True):
+    """BLH ``[B, X, Y, H]`` input (``circular_fftconv.py:610-632``)."""
+    y = circular_fftconv2d_fp32_bhl(rearrange(x, "b x y h -> b h x y"), rearrange(kernel, "b kx ky h -> b h kx ky"),
+                                    shortcut, use_phase_shift)
+    return rearrange(y, "b h x y -> b x y h")
+
+
+def circular_fftconv3d_fp32_bhl_w_reshape(x, kernel, shortcut=None, use_phase_shift=True):
+    """BLH ``[B, X, Y, Z, H]`` input (``circular_fftconv.py:635-660``)."""
+    y = circular_fftconv3d_fp32_bhl(rearrange(x, "b x y z h -> b h x y z"),
+                                    rearrange(kernel, "b kx ky kz h -> b h kx ky kz"), shortcut, use_phase_shift)
+    return rearrange(y, "b h x y z -> b x y z h")

@@ -25,6 +25,28 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
   return NSQ_OK;
 }
 
+// Circular 1D: L a power of two in [16, 16384] (the fused plan at FFT length L),
+// 1 <= K <= L, kbatch 1 or B.
+static int validate_circ(const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H, int64_t L,
+                         int64_t K, int64_t kbatch, int& logN) {
+  NSQ_CHECK_ARG(a && b && k, "circular_fftconv1d: null tensor pointer");
+  NSQ_CHECK_ARG(valid_dtype(dtype), "circular_fftconv1d: unsupported dtype code %d", dtype);
+  NSQ_CHECK_ARG(B >= 1 && H >= 1 && L >= 1 && K >= 1,
+                "circular_fftconv1d: sizes must be positive (B=%lld H=%lld L=%lld K=%lld)", (long long)B, (long long)H,
+                (long long)L, (long long)K);
+  NSQ_CHECK_ARG(K <= L, "circular_fftconv1d: K must be <= L (K=%lld, L=%lld)", (long long)K, (long long)L);
+  NSQ_CHECK_ARG(kbatch == 1 || kbatch == B, "circular_fftconv1d: kernel batch must be 1 or B (got %lld, B=%lld)",
+                (long long)kbatch, (long long)B);
+  NSQ_CHECK_ARG(B * H <= 0x7fffffff && B <= 65535, "circular_fftconv1d: tensor too large");
+  if (L < 16 || L > 16384 || (L & (L - 1))) {
+    set_error("circular_fftconv1d: unsupported length L=%lld: the HIP kernels take powers of two in [16, 16384]",
+              (long long)L);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  logN = ilog2_ceil(L) - 1;
+  return NSQ_OK;
+}
+
 }  // namespace nsq
 
 using namespace nsq;
@@ -106,6 +128,63 @@ int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const
       break;
   }
   NSQ_CHECK_ARG(ok, "fftconv1d_causal_bwd: no kernel for logN=%d", p.logN);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+int nsq_circular_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                               int64_t H, int64_t L, int64_t K, int64_t kbatch, void* stream) {
+  clear_error();
+  int logN = 0;
+  int rc = validate_circ(x, y, k, dtype, B, H, L, K, kbatch, logN);
+  if (rc) return rc;
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  const int kf = kbatch != 1;
+  bool ok = false;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      ok = run_circ_fwd<NSQ_DTYPE_F32>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, tw, st);
+      break;
+    case NSQ_DTYPE_BF16:
+      ok = run_circ_fwd<NSQ_DTYPE_BF16>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, tw, st);
+      break;
+    default:
+      ok = run_circ_fwd<NSQ_DTYPE_F16>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, tw, st);
+      break;
+  }
+  NSQ_CHECK_ARG(ok, "circular_fftconv1d_fwd: no kernel for logN=%d", logN);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
+                               float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
+                               int64_t kbatch, void* stream) {
+  clear_error();
+  int logN = 0;
+  int rc = validate_circ(g, x, k, dtype, B, H, L, K, kbatch, logN);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(gx && gk, "circular_fftconv1d_bwd: null gradient output pointer");
+  NSQ_CHECK_ARG(!shortcut || gs, "circular_fftconv1d_bwd: gs required when a shortcut is given");
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  const int kf = kbatch != 1;
+  bool ok = false;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      ok = run_circ_bwd<NSQ_DTYPE_F32>(logN, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, tw, st);
+      break;
+    case NSQ_DTYPE_BF16:
+      ok = run_circ_bwd<NSQ_DTYPE_BF16>(logN, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, tw, st);
+      break;
+    default:
+      ok = run_circ_bwd<NSQ_DTYPE_F16>(logN, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, tw, st);
+      break;
+  }
+  NSQ_CHECK_ARG(ok, "circular_fftconv1d_bwd: no kernel for logN=%d", logN);
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
 }

@@ -116,11 +116,34 @@ __device__ __forceinline__ void lds_repack(float2* z, int m, int p, const float2
   zz[pad16(s0 ? N / 2 : N - p)] = zq;
 }
 
-// Filter spectrum of channels h0..h0+M-1 into per-thread slot registers.
-// `lds` must hold a tile; leaves it free (ends with a barrier).
+// Shift ramp of the circular conv on one spectral slot (slot form: see
+// real_unpack).  The real spectrum U[f], f in [0, N] (F = 2N), is multiplied by
+// rho(f) = e^{+2 pi i c f / F} = conj(W_F^{c f}):
+//   slot p > 0: A = U[p] -> A * conj(W^{cp});  Bc = conj(U[N-p]) -> Bc * W^{c(N-p)};
+//   slot 0:     A = (U[0], U[N]) -> (U[0], (-1)^c U[N]);  Bc = U[N/2] -> Bc * conj(W^{cN/2}).
 template <int LOGN>
+__device__ __forceinline__ void circ_ramp(int p, int c, const float2* __restrict__ tw, float2& A, float2& Bc) {
+  constexpr int N = 1 << LOGN, F = 2 * N;
+  const TwTable tt(tw);
+  const bool s0 = p == 0;
+  const float2 wa = tt.load(F, (c * p) & (F - 1));
+  const float2 wb = tt.load(F, (c * (s0 ? N / 2 : N - p)) & (F - 1));
+  const float2 a = cmulc(A, wa);
+  const float2 b = cmul(Bc, wb);
+  const float2 b0 = cmulc(Bc, wb);
+  A.x = s0 ? A.x : a.x;
+  A.y = s0 ? ((c & 1) ? -A.y : A.y) : a.y;
+  Bc.x = s0 ? b0.x : b.x;
+  Bc.y = s0 ? b0.y : b.y;
+}
+
+// Filter spectrum of channels h0..h0+M-1 into per-thread slot registers.
+// `lds` must hold a tile; leaves it free (ends with a barrier).  CIRC: the
+// spectrum is multiplied by the ramp e^{+2 pi i c f / F} (F = 2N, the real
+// FFT length), which rolls the circular conv's output by -c (see circ_ramp).
+template <int LOGN, bool CIRC = false>
 __device__ __forceinline__ void filter_spectrum(float2* lds, const float* __restrict__ k, int h0, int H, int K,
-                                                const float2* __restrict__ tw, float2* hA, float2* hB) {
+                                                const float2* __restrict__ tw, float2* hA, float2* hB, int c = 0) {
   using C = FusedCfg<LOGN>;
   auto ld = [&](int m, int n) -> float2 {
     const int h = h0 + m;
@@ -135,17 +158,21 @@ __device__ __forceinline__ void filter_spectrum(float2* lds, const float* __rest
     int m, p;
     slot_of<LOGN>(opaque_tid() + i * C::T, m, p);
     lds_unpack<LOGN>(lds, m, p, tw, hA[i], hB[i]);
+    if constexpr (CIRC) circ_ramp<LOGN>(p, c, tw, hA[i], hB[i]);
   }
   __syncthreads();
 }
 
 // Forward, fused plan.  grid = (ceil(H/M), nb_split); each workgroup handles
-// batch rows [b0, b0 + b_per_wg).
-template <int LOGN, int DT, bool FOLD>
+// batch rows [b0, b0 + b_per_wg).  CIRC: circular conv at FFT length 2N = L
+// (no padding, no crop) rolled by -c through the filter ramp.  kfilm: the
+// filter is per image ([B, H, K]); the launch then gives one image per
+// workgroup (b_per_wg = 1).
+template <int LOGN, int DT, bool FOLD, bool CIRC = false>
 __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
     const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ k,
     const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ y, int B, int H, int L,
-    int K, int b_per_wg, const float2* __restrict__ tw) {
+    int K, int b_per_wg, const float2* __restrict__ tw, int c, int kfilm) {
   using C = FusedCfg<LOGN>;
   __shared__ float2 lds[C::TILE_P];
   const int h0 = blockIdx.x * C::M;
@@ -153,7 +180,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
   const int b1 = min(B, b0 + b_per_wg);
 
   float2 hA[C::SLOTS], hB[C::SLOTS];
-  filter_spectrum<LOGN>(lds, k, h0, H, K, tw, hA, hB);
+  filter_spectrum<LOGN, CIRC>(lds, kfilm ? k + int64_t(b0) * H * K : k, h0, H, K, tw, hA, hB, c);
 
   const float scale = 1.f / float(C::N);
   for (int b = b0; b < b1; ++b) {
@@ -208,24 +235,35 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
 
 // Backward, fused plan.  grid = ceil(H/M); each workgroup loops over all
 // batch rows (the filter gradient sums over the batch in a fixed order).
-template <int LOGN, int DT, bool FOLD>
+// kfilm: grid = (ceil(H/M), B), one image per workgroup, whose filter and
+// filter-gradient rows are that image's.  CIRC: as the forward; the filter
+// gradient gk[j] = sum_n g[n] x[(n + c - j) mod L] is the correlation read at
+// lag (j - c) mod L.
+template <int LOGN, int DT, bool FOLD, bool CIRC = false>
 __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x,
     const float* __restrict__ k, const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ gx,
-    float* __restrict__ gk, float* __restrict__ gs, int B, int H, int L, int K, const float2* __restrict__ tw) {
+    float* __restrict__ gk, float* __restrict__ gs, int B, int H, int L, int K, const float2* __restrict__ tw, int c,
+    int kfilm) {
   using C = FusedCfg<LOGN>;
   __shared__ float2 ldsG[C::TILE_P];
   __shared__ float2 ldsX[C::TILE_P];
   const int h0 = blockIdx.x * C::M;
+  const int bb0 = kfilm ? int(blockIdx.y) : 0, bb1 = kfilm ? bb0 + 1 : B;
+  const int64_t koff = kfilm ? int64_t(bb0) * H * K : 0;
+  if (kfilm) {
+    gk += koff;
+    if (gs) gs += int64_t(bb0) * H;
+  }
 
   float2 hA[C::SLOTS], hB[C::SLOTS];
-  filter_spectrum<LOGN>(ldsG, k, h0, H, K, tw, hA, hB);
+  filter_spectrum<LOGN, CIRC>(ldsG, k + koff, h0, H, K, tw, hA, hB, c);
   float2 qA[C::SLOTS], qB[C::SLOTS];
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) qA[i] = qB[i] = make_float2(0.f, 0.f);
 
   const float scale = 1.f / float(C::N);
-  for (int b = 0; b < B; ++b) {
+  for (int b = bb0; b < bb1; ++b) {
     // g extended by its adjoint fold copy at offset 2L (FOLD only).
     auto ldg = [&](int m, int n) -> float2 {
       const int h = h0 + m;
@@ -286,9 +324,16 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
   auto epik = [&](int m, int n, float2 v) {
     const int h = h0 + m;
     if (h >= H) return;
-    const int64_t i0 = 2 * int64_t(n);
-    if (i0 < K) gk[int64_t(h) * K + i0] = v.x * scale;
-    if (i0 + 1 < K) gk[int64_t(h) * K + i0 + 1] = v.y * scale;
+    if constexpr (CIRC) {
+      constexpr int F = 2 * C::N;
+      const int j0 = (2 * n + c) & (F - 1), j1 = (2 * n + 1 + c) & (F - 1);
+      if (j0 < K) gk[int64_t(h) * K + j0] = v.x * scale;
+      if (j1 < K) gk[int64_t(h) * K + j1] = v.y * scale;
+    } else {
+      const int64_t i0 = 2 * int64_t(n);
+      if (i0 < K) gk[int64_t(h) * K + i0] = v.x * scale;
+      if (i0 + 1 < K) gk[int64_t(h) * K + i0 + 1] = v.y * scale;
+    }
     if (n == 0 && gs) gs[h] = v.x * scale;
   };
   LdsTile<C::SP, true> ldl{ldsX};
@@ -783,10 +828,10 @@ static void launch_fused_fwd(const Plan1D& p, const void* x, const float* k, con
   dim3 grid(gh, nb);
   if (p.fold)
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, 0);
   else
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, 0);
 }
 
 template <int LOGN, int DT>
@@ -797,10 +842,39 @@ static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, cons
   dim3 grid(int(ceil_div(H, C::M)));
   if (p.fold)
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0);
   else
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0);
+}
+
+// Circular 1D (fused plan at FFT length L = 2N): shift c = (K-1)/2; kfilm =
+// per-image filters [B, H, K] (one image per workgroup).
+template <int LOGN, int DT>
+static void launch_circ_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
+                            int kfilm, const float2* tw, hipStream_t st) {
+  using C = FusedCfg<LOGN>;
+  using ET = typename Elem<DT>::T;
+  const int gh = int(ceil_div(H, C::M));
+  int bpw = 1;
+  if (!kfilm) {
+    int nb = int(ceil_div(2048, gh));
+    nb = nb < 1 ? 1 : (nb > B ? B : nb);
+    bpw = int(ceil_div(B, nb));
+  }
+  const dim3 grid(gh, unsigned(ceil_div(B, bpw)));
+  hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)x, k,
+                     (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, (K - 1) / 2, kfilm);
+}
+
+template <int LOGN, int DT>
+static void launch_circ_bwd(const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
+                            float* gs, int B, int H, int L, int K, int kfilm, const float2* tw, hipStream_t st) {
+  using C = FusedCfg<LOGN>;
+  using ET = typename Elem<DT>::T;
+  const dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
+  hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
+                     (const ET*)x, k, (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, (K - 1) / 2, kfilm);
 }
 
 // Workspace layout of the 4-step plan (rows of N complex64):
@@ -928,6 +1002,20 @@ struct FusedBwd {
   };
 };
 
+template <int DT, bool BWD>
+struct CircFused {
+  template <int LOGN>
+  struct At {
+    template <class... A>
+    static void run(A&&... a) {
+      if constexpr (BWD)
+        launch_circ_bwd<LOGN, DT>(static_cast<A&&>(a)...);
+      else
+        launch_circ_fwd<LOGN, DT>(static_cast<A&&>(a)...);
+    }
+  };
+};
+
 // 4-step instantiations: logN in [14, 22] split by split_log_n1.
 template <int DT, bool BWD>
 struct FourStep {
@@ -963,17 +1051,39 @@ bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, cons
                                                                 fwd_state, tw, st);
 }
 
+// Circular 1D: logN = log2(L) - 1 in [3, 13] (L a power of two in [16, 16384]).
+template <int DT>
+bool run_circ_fwd(int logN, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
+                  int kfilm, const float2* tw, hipStream_t st) {
+  return dispatch_int<CircFused<DT, false>::template At, 3, 13>(logN, x, k, s, y, B, H, L, K, kfilm, tw, st);
+}
+
+template <int DT>
+bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
+                  float* gs, int B, int H, int L, int K, int kfilm, const float2* tw, hipStream_t st) {
+  return dispatch_int<CircFused<DT, true>::template At, 3, 13>(logN, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, tw,
+                                                               st);
+}
+
 #define NSQ_DECLARE_FFTCONV1D(DT)                                                                               \
   extern template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
                                    int, float2*, bool, const float2*, hipStream_t);                             \
   extern template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
-                                   float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t);
+                                   float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t); \
+  extern template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, \
+                                        int, const float2*, hipStream_t);                                       \
+  extern template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, \
+                                        float*, int, int, int, int, int, const float2*, hipStream_t);
 
 #define NSQ_INSTANTIATE_FFTCONV1D(DT)                                                                    \
   template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
                             int, float2*, bool, const float2*, hipStream_t);                             \
   template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
-                            float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t);
+                            float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t); \
+  template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, int, \
+                                 const float2*, hipStream_t);                                               \
+  template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, float*, \
+                                 int, int, int, int, int, const float2*, hipStream_t);
 
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_F32)
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_BF16)

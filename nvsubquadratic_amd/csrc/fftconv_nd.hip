@@ -4,34 +4,61 @@
 
 namespace nsq {
 
+// Boundary condition per axis (ops/mixed_fftconv.py:295-343, `_mixed_recipe`):
+//   zero-padded ("same"): F_d = 2^ceil(log2(S_d + ceil(K_d/2))) >= 16, output
+//     window [K_d/2, K_d/2 + S_d) of the linear conv (crop o_d = K_d/2);
+//   periodic (circular):  F_d = S_d (a power of two in [16, 2^kNdMaxLogF]),
+//     K_d <= S_d, output = the whole circular conv rolled by -(K_d-1)/2, done
+//     as a ramp on the filter spectrum (r_d = (K_d-1)/2, o_d = 0).
+// Either way y[n] = sum_j k[j] x[n + c_d - j] along the axis, c_d = o_d + r_d,
+// which is the shift the backward's ramp and its gs lag use.
 struct NdPlan {
   int nd;
   int64_t B, H, kb;      // kb = kernel batch: 1 (shared) or B (per-sample FiLM)
   int S[3], K[3];        // padded to 3 axes: (S0, S1, S2) with S1 = K1 = 1 for 2D
   int lF[3], F[3], c[3];
+  int o[3], r[3];        // forward crop offsets and forward ramp shifts (c = o + r)
+  bool ramp;             // some r_d != 0
   int FH;        // spectrum columns along the last axis, F2/2 + 1
   int RS;        // spectrum row stride (complex elements), >= FH
   int64_t spec;
 };
 
-static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kb, NdPlan& p) {
+// `periodic`: bit d set = axis d (of the nd given axes) is periodic.
+static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kb,
+                         unsigned periodic, NdPlan& p) {
   if (nd != 2 && nd != 3) return false;
+  if (periodic >> nd) return false;
   p.nd = nd;
   p.B = B;
   p.H = H;
   p.kb = kb;
+  p.ramp = false;
   int s[3] = {1, 1, 1}, k[3] = {1, 1, 1};
+  bool per[3] = {false, false, false};
   if (nd == 2) {
     s[0] = int(S[0]); s[2] = int(S[1]);
     k[0] = int(K[0]); k[2] = int(K[1]);
+    per[0] = periodic & 1u; per[2] = (periodic >> 1) & 1u;
   } else {
-    for (int d = 0; d < 3; ++d) { s[d] = int(S[d]); k[d] = int(K[d]); }
+    for (int d = 0; d < 3; ++d) { s[d] = int(S[d]); k[d] = int(K[d]); per[d] = (periodic >> d) & 1u; }
   }
   for (int d = 0; d < 3; ++d) {
     p.S[d] = s[d];
     p.K[d] = k[d];
     if (nd == 2 && d == 1) {
-      p.lF[d] = 0; p.F[d] = 1; p.c[d] = 0;
+      p.lF[d] = 0; p.F[d] = 1; p.c[d] = 0; p.o[d] = 0; p.r[d] = 0;
+      continue;
+    }
+    if (per[d]) {
+      if (k[d] < 1 || k[d] > s[d] || s[d] < 16 || (s[d] & (s[d] - 1))) return false;
+      const int lf = ilog2_ceil(s[d]);
+      if (lf > kNdMaxLogF) return false;
+      p.lF[d] = lf;
+      p.F[d] = s[d];
+      p.c[d] = p.r[d] = (k[d] - 1) / 2;
+      p.o[d] = 0;
+      p.ramp = p.ramp || p.r[d] != 0;
       continue;
     }
     if (s[d] < 1 || k[d] < 1 || k[d] > 2 * s[d]) return false;
@@ -40,7 +67,8 @@ static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
     if (lf > kNdMaxLogF) return false;
     p.lF[d] = lf;
     p.F[d] = 1 << lf;
-    p.c[d] = k[d] / 2;
+    p.c[d] = p.o[d] = k[d] / 2;
+    p.r[d] = 0;
   }
   p.FH = p.F[2] / 2 + 1;
   // 2D: rows padded to a multiple of 16 complex values, so the 16-column
@@ -260,6 +288,7 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
   if (!filter_spectrum(p, k, wsk, tw, st)) return false;
   if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
+  const Ramp rf{p.r[0], p.r[1], p.r[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
     col_blocks<LOGF, 8192>(cg.inner_count, [&](auto tile, int gy, int jbase) {
@@ -268,20 +297,23 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
       // image is small, so a batch loop would leave the GPU idle)
       const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : 1;
       const dim3 grid(unsigned((p.kb != 1 ? BH : p.H) * bsplit), unsigned(gy));
-      if (2 * p.S[0] <= p.F[0])
-        hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT, true>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st,
-                           (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1),
-                           p.S[0], p.c[0], jbase, bsplit, tw);
+      auto go = [&](auto half, auto ramp) {
+        hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT, decltype(half)::value, decltype(ramp)::value>), grid,
+                           dim3(ColNdCfg<LOGF, TGT>::T), 0, st, (const float2*)wsx, wsy, (const float2*)wsk, cg,
+                           int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.o[0], rf, jbase, bsplit, tw);
+      };
+      using T_ = std::true_type;
+      using F_ = std::false_type;
+      if (2 * p.S[0] <= p.F[0])  // the x columns are at least half zero padding
+        p.ramp ? go(T_{}, T_{}) : go(T_{}, F_{});
       else
-        hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT, false>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st,
-                           (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B), int(p.H), int(p.kb != 1),
-                           p.S[0], p.c[0], jbase, bsplit, tw);
+        p.ramp ? go(F_{}, T_{}) : go(F_{}, F_{});
     });
   });
   if (!ok) return false;
-  RowInvOut o{y, x, s, nullptr, int(p.H), p.c[2], p.S[2], 0, 0, 0,
+  RowInvOut o{y, x, s, nullptr, int(p.H), p.o[2], p.S[2], 0, 0, 0,
               1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2))};
-  return inner_inv<DT, ND_OUT_Y>(p, wsy, BH, p.S[0], p.c[1], p.S[1], o, tw, st);
+  return inner_inv<DT, ND_OUT_Y>(p, wsy, BH, p.S[0], p.o[1], p.S[1], o, tw, st);
 }
 
 template <int DT>
@@ -323,17 +355,32 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
 }
 
 static int validate_nd(int nd, const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H,
-                       const int64_t* S, const int64_t* K, int64_t kb, NdPlan& p) {
+                       const int64_t* S, const int64_t* K, int64_t kb, unsigned periodic, NdPlan& p) {
   NSQ_CHECK_ARG(a && b && k && S && K, "fftconv_nd: null pointer argument");
   NSQ_CHECK_ARG(nd == 2 || nd == 3, "fftconv_nd: nd must be 2 or 3 (got %d)", nd);
   NSQ_CHECK_ARG(valid_dtype(dtype), "fftconv_nd: unsupported dtype code %d", dtype);
   NSQ_CHECK_ARG(B >= 1 && H >= 1, "fftconv_nd: sizes must be positive");
   NSQ_CHECK_ARG(kb == 1 || kb == B, "fftconv_nd: kernel batch must be 1 or B (got %lld, B=%lld)", (long long)kb,
                 (long long)B);
-  for (int d = 0; d < nd; ++d)
-    NSQ_CHECK_ARG(S[d] >= 1 && K[d] >= 1 && K[d] <= 2 * S[d],
-                  "fftconv_nd: axis %d: kernel size %lld must be in [1, 2*%lld]", d, (long long)K[d], (long long)S[d]);
-  if (!make_nd_plan(nd, B, H, S, K, kb, p)) {
+  NSQ_CHECK_ARG((periodic >> nd) == 0, "fftconv_nd: periodic mask 0x%x names an axis >= nd=%d", periodic, nd);
+  for (int d = 0; d < nd; ++d) {
+    if ((periodic >> d) & 1u) {
+      NSQ_CHECK_ARG(S[d] >= 1 && K[d] >= 1 && K[d] <= S[d],
+                    "fftconv_nd: periodic axis %d: kernel size %lld must be in [1, %lld]", d, (long long)K[d],
+                    (long long)S[d]);
+      if (S[d] < 16 || S[d] > (1 << kNdMaxLogF) || (S[d] & (S[d] - 1))) {
+        set_error("fftconv_nd: unsupported shape: periodic axis %d has length %lld; the HIP kernels take periodic "
+                  "lengths that are powers of two in [16, %d]",
+                  d, (long long)S[d], 1 << kNdMaxLogF);
+        return NSQ_ERR_UNSUPPORTED;
+      }
+    } else {
+      NSQ_CHECK_ARG(S[d] >= 1 && K[d] >= 1 && K[d] <= 2 * S[d],
+                    "fftconv_nd: axis %d: kernel size %lld must be in [1, 2*%lld]", d, (long long)K[d],
+                    (long long)S[d]);
+    }
+  }
+  if (!make_nd_plan(nd, B, H, S, K, kb, periodic, p)) {
     set_error("fftconv_nd: unsupported shape: every axis needs an FFT length <= %d", 1 << kNdMaxLogF);
     return NSQ_ERR_UNSUPPORTED;
   }
@@ -350,35 +397,29 @@ static int validate_nd(int nd, const void* a, const void* b, const float* k, int
   return NSQ_OK;
 }
 
-}  // namespace nsq
-
-using namespace nsq;
-
-extern "C" {
-
-size_t nsq_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
-                                      int64_t kbatch, int direction) {
+static size_t nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
+                                 unsigned periodic, int direction) {
   NdPlan p;
-  if (!S || !K || !make_nd_plan(nd, B, H, S, K, kbatch, p)) return 0;
+  if (!S || !K || !make_nd_plan(nd, B, H, S, K, kbatch, periodic, p)) return 0;
   const int64_t blocks = direction == NSQ_DIR_BWD ? (2 * B * H + 2 * kbatch * H) : (B * H + kbatch * H);
   return size_t(blocks * p.spec) * sizeof(float2);
 }
 
-int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
-                       int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+static int nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                  int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace,
+                  size_t workspace_bytes, void* stream) {
   clear_error();
   NdPlan p;
-  int rc = validate_nd(nd, x, y, k, dtype, B, H, S, K, kbatch, p);
+  int rc = validate_nd(nd, x, y, k, dtype, B, H, S, K, kbatch, periodic, p);
   if (rc) return rc;
-  const size_t need = nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, NSQ_DIR_FWD);
+  const size_t need = nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_FWD);
   NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv_nd_fwd: workspace of %zu bytes required, got %zu", need,
                 workspace_bytes);
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
   float2* ws = (float2*)workspace;
-  const bool save = workspace_bytes >= nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, NSQ_DIR_BWD);
+  const bool save = workspace_bytes >= nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_BWD);
   bool ok;
   switch (dtype) {
     case NSQ_DTYPE_F32: ok = run_nd_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, ws, save, tw, st); break;
@@ -390,16 +431,16 @@ int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortc
   return NSQ_OK;
 }
 
-int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
-                       float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
-                       void* workspace, size_t workspace_bytes, int fwd_state, void* stream) {
+static int nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                  float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
+                  unsigned periodic, void* workspace, size_t workspace_bytes, int fwd_state, void* stream) {
   clear_error();
   NdPlan p;
-  int rc = validate_nd(nd, g, x, k, dtype, B, H, S, K, kbatch, p);
+  int rc = validate_nd(nd, g, x, k, dtype, B, H, S, K, kbatch, periodic, p);
   if (rc) return rc;
   NSQ_CHECK_ARG(gx && gk, "fftconv_nd_bwd: null gradient output pointer");
   NSQ_CHECK_ARG(!shortcut || gs, "fftconv_nd_bwd: gs required when a shortcut is given");
-  const size_t need = nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, NSQ_DIR_BWD);
+  const size_t need = nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_BWD);
   NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv_nd_bwd: workspace of %zu bytes required, got %zu", need,
                 workspace_bytes);
   const float2* tw = twiddle_table();
@@ -415,6 +456,49 @@ int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, con
   NSQ_CHECK_ARG(ok, "fftconv_nd_bwd: no kernel instantiated for this shape");
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
+}
+
+}  // namespace nsq
+
+using namespace nsq;
+
+extern "C" {
+
+size_t nsq_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
+                                      int64_t kbatch, int direction) {
+  return nd_workspace_bytes(nd, B, H, S, K, kbatch, 0u, direction);
+}
+
+int nsq_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                       int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  return nd_fwd(nd, x, k, shortcut, y, dtype, B, H, S, K, kbatch, 0u, workspace, workspace_bytes, stream);
+}
+
+int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                       float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
+                       void* workspace, size_t workspace_bytes, int fwd_state, void* stream) {
+  return nd_bwd(nd, g, x, k, shortcut, gx, gk, gs, dtype, B, H, S, K, kbatch, 0u, workspace, workspace_bytes,
+                fwd_state, stream);
+}
+
+size_t nsq_mixed_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
+                                            int64_t kbatch, unsigned periodic, int direction) {
+  return nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, direction);
+}
+
+int nsq_mixed_fftconv_nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype,
+                             int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
+                             unsigned periodic, void* workspace, size_t workspace_bytes, void* stream) {
+  return nd_fwd(nd, x, k, shortcut, y, dtype, B, H, S, K, kbatch, periodic, workspace, workspace_bytes, stream);
+}
+
+int nsq_mixed_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx,
+                             float* gk, float* gs, int dtype, int64_t B, int64_t H, const int64_t* S,
+                             const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace,
+                             size_t workspace_bytes, int fwd_state, void* stream) {
+  return nd_bwd(nd, g, x, k, shortcut, gx, gk, gs, dtype, B, H, S, K, kbatch, periodic, workspace, workspace_bytes,
+                fwd_state, stream);
 }
 
 }  // extern "C"

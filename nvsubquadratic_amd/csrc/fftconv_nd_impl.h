@@ -529,6 +529,21 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_kernel(flo
   fft<LOGF, INV, C::M, C::T, C::S, true>(lds, ld, st, tw);
 }
 
+// Shift ramp parameters (3 axes; unused axes have c = 0).
+struct Ramp {
+  int c0, c1, c2;
+  int lF0, lF1, lF2;  // log2 sizes (lF1 = 0 for 2D)
+  int FH;             // inner index j -> (k1, k2) = (j / FH, j % FH) on axis-0 passes
+};
+
+// Factor of the shift ramp at axis-0 frequency k of inner index j, without
+// the axis-0 term:  W_F1^{c1 k1} * W_F2^{c2 k2}  (table roots, W = e^{-2 pi i / F}).
+__device__ __forceinline__ float2 ramp_inner(const Ramp& rp, const TwTable& tt, int j) {
+  const int k1 = j / rp.FH, k2 = j - k1 * rp.FH;
+  const int f1 = 1 << rp.lF1, f2 = 1 << rp.lF2;
+  return cmul(tt.load(f1, (rp.c1 * k1) & (f1 - 1)), tt.load(f2, (rp.c2 * k2) & (f2 - 1)));
+}
+
 // Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0),
 // read from wsx and written to wsy (the same buffer for an in-place product).
 // Shared filter (kfilm = 0): grid.x = H * bsplit and a workgroup loops over
@@ -538,12 +553,16 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_kernel(flo
 // over elements j + r*NR of column m; the next image's inputs are loaded
 // before the current image's transforms.  HALF (S0 <= F/2, the zero padding
 // of a conv is at least half the axis): inputs r >= R/2 are zero, so only R/2
-// are loaded and the first pass's butterflies fold the zeros away.
-template <int LOGF, int TARGET = 8192, bool HALF = false>
+// are loaded and the first pass's butterflies fold the zeros away.  RAMP
+// (periodic axes): the filter values are multiplied by conj(R), R the shift
+// ramp of `rf`, as they are loaded, which rolls the output by -c_d along
+// every axis (the circular "same" alignment; c0 is then 0).
+template <int LOGF, int TARGET = 8192, bool HALF = false, bool RAMP = false>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
                                                                                 const float2* __restrict__ wsk,
                                                                                 ColGeom cg, int B, int H, int kfilm,
-                                                                                int S0, int c0, int jbase, int bsplit,
+                                                                                int S0, int c0, Ramp rf, int jbase,
+                                                                                int bsplit,
                                                                                 const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
   constexpr int R = 1 << (LOGF < 4 ? LOGF : 4);  // first-pass radix, as chosen by fft_rec
@@ -563,7 +582,13 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
 #pragma unroll
   for (int it = 0; it < PT; ++it) {
     const int e = tk + it * C::T;
-    kv[it] = kb.load(e / C::M, j0 + e % C::M, j0 + e % C::M < cg.inner_count);
+    const int jj = j0 + e % C::M, k = e / C::M;
+    kv[it] = kb.load(k, jj, jj < cg.inner_count);
+    if constexpr (RAMP) {
+      const TwTable tt(tw);
+      const float2 r = cmul(ramp_inner(rf, tt, jj < cg.inner_count ? jj : 0), tt.load(C::F, (rf.c0 * k) & (C::F - 1)));
+      kv[it] = cmulc(kv[it], r);
+    }
   }
   const int nb = kfilm ? 1 : B;
   // bsplit > 1: this workgroup takes batches [part * nb / bsplit, (part + 1) * nb / bsplit)
@@ -603,13 +628,6 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
   }
 }
 
-// Shift ramp parameters of the adjoint (3 axes; unused axes have c = 0).
-struct Ramp {
-  int c0, c1, c2;
-  int lF0, lF1, lF2;  // log2 sizes (lF1 = 0 for 2D)
-  int FH;             // inner index j -> (k1, k2) = (j / FH, j % FH) on axis-0 passes
-};
-
 
 // Adjoint, axis 0.  Shared kernel (kfilm = 0): grid.x = H, loops b; FiLM:
 // grid.x = B*H, one b.  Writes P (gx pre-image, window [0, S0)) into wsg and
@@ -639,13 +657,7 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
   const int m = tp % C::M, kfirst = tp / C::M;
   const int j = j0 + m;
   const TwTable tt(tw);
-  float2 r12;
-  {
-    const int jj = j < cg.inner_count ? j : 0;
-    const int k1 = jj / rp.FH, k2 = jj - k1 * rp.FH;
-    const int f1 = 1 << rp.lF1, f2 = 1 << rp.lF2;
-    r12 = cmul(tt.load(f1, (rp.c1 * k1) & (f1 - 1)), tt.load(f2, (rp.c2 * k2) & (f2 - 1)));
-  }
+  const float2 r12 = ramp_inner(rp, tt, j < cg.inner_count ? j : 0);
   float2 kv[PT], rr[PT], q[PT];
 #pragma unroll
   for (int it = 0; it < PT; ++it) {

@@ -303,11 +303,19 @@ def causal_fftconv1d_blh_chunked(
 # ===========================================================================
 # 2D / 3D non-causal (zero-padded, "same") FFT convolution
 # ===========================================================================
-def fftconv_nd_fwd_raw(x, k, s, y, kbatch: int, workspace: torch.Tensor | None = None):
+def _nd_workspace_bytes(lib, nd, B, H, S, K, kbatch, periodic, direction):
+    if periodic:
+        return lib.nsq_mixed_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, direction)
+    return lib.nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, direction)
+
+
+def fftconv_nd_fwd_raw(x, k, s, y, kbatch: int, workspace: torch.Tensor | None = None, periodic: int = 0):
     """Launch the N-d forward on the current stream.
 
     ``x``/``y``: contiguous ``[B, H, *S]``; ``k``: contiguous float32
-    ``[kbatch*H, *K]``; ``s``: ``[H]`` in ``x.dtype`` or None.
+    ``[kbatch*H, *K]``; ``s``: ``[H]`` in ``x.dtype`` or None.  ``periodic``:
+    bit d set = spatial axis d is circular (``nsq_mixed_fftconv_nd_fwd``);
+    0 = every axis zero-padded (``nsq_fftconv_nd_fwd``).
     """
     lib = _lib.get_lib()
     _lib.check_device(x)
@@ -315,19 +323,25 @@ def fftconv_nd_fwd_raw(x, k, s, y, kbatch: int, workspace: torch.Tensor | None =
     B, H = x.shape[:2]
     S = _lib.i64_array(x.shape[2:])
     K = _lib.i64_array(k.shape[1:])
-    need = lib.nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, _lib.NSQ_DIR_FWD)
+    need = _nd_workspace_bytes(lib, nd, B, H, S, K, kbatch, periodic, _lib.NSQ_DIR_FWD)
     if need == 0:
-        raise NotImplementedError(f"fft_backend='hip' {nd}D: unsupported shape x={tuple(x.shape)} k={tuple(k.shape)}")
+        raise NotImplementedError(
+            f"fft_backend='hip' {nd}D: unsupported shape x={tuple(x.shape)} k={tuple(k.shape)} periodic={periodic:#x} "
+            f"(periodic axes need a power-of-two length in [16, 1024] and K <= S; zero-padded axes an FFT length "
+            f"<= 1024)")
     if workspace is None or workspace.numel() < need:
         workspace = _workspace(x.device, need)
-    _lib.check(lib.nsq_fftconv_nd_fwd(
-        nd, x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype), B, H, S, K, kbatch,
-        workspace.data_ptr(), workspace.numel(), _lib.stream_ptr(x.device)))
+    args = (x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype), B, H, S, K, kbatch)
+    tail = (workspace.data_ptr(), workspace.numel(), _lib.stream_ptr(x.device))
+    if periodic:
+        _lib.check(lib.nsq_mixed_fftconv_nd_fwd(nd, *args, periodic, *tail))
+    else:
+        _lib.check(lib.nsq_fftconv_nd_fwd(nd, *args, *tail))
     return y
 
 
 def fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, workspace: torch.Tensor | None = None,
-                       fwd_state: bool = False):
+                       fwd_state: bool = False, periodic: int = 0):
     """Launch the N-d backward (gs: ``[kbatch*H]`` partials or None).
 
     ``fwd_state=True`` reuses the transformed x and filter spectrum that a forward
@@ -339,21 +353,24 @@ def fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, workspace: torch.Ten
     B, H = x.shape[:2]
     S = _lib.i64_array(x.shape[2:])
     K = _lib.i64_array(k.shape[1:])
-    need = lib.nsq_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, _lib.NSQ_DIR_BWD)
+    need = _nd_workspace_bytes(lib, nd, B, H, S, K, kbatch, periodic, _lib.NSQ_DIR_BWD)
     if workspace is None or workspace.numel() < need:
         workspace = _workspace(x.device, need)
         fwd_state = False
-    _lib.check(lib.nsq_fftconv_nd_bwd(
-        nd, g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
-        _lib.dtype_code(x.dtype), B, H, S, K, kbatch, workspace.data_ptr(), workspace.numel(), int(bool(fwd_state)),
-        _lib.stream_ptr(x.device)))
+    args = (g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
+            _lib.dtype_code(x.dtype), B, H, S, K, kbatch)
+    tail = (workspace.data_ptr(), workspace.numel(), int(bool(fwd_state)), _lib.stream_ptr(x.device))
+    if periodic:
+        _lib.check(lib.nsq_mixed_fftconv_nd_bwd(nd, *args, periodic, *tail))
+    else:
+        _lib.check(lib.nsq_fftconv_nd_bwd(nd, *args, *tail))
 
 
 class _FFTConvND(torch.autograd.Function):
     """x: [B, H, *S] contiguous; k: [kbatch*H, *K] contiguous float32; s: [H] in x.dtype or None."""
 
     @staticmethod
-    def forward(ctx, x, k, s, kbatch):
+    def forward(ctx, x, k, s, kbatch, periodic=0):
         y = torch.empty_like(x)
         ws = None
         if any(ctx.needs_input_grad[:3]):  # (grad mode is off inside forward; this flag is not)
@@ -361,12 +378,13 @@ class _FFTConvND(torch.autograd.Function):
             # filter spectrum there for the backward.
             lib = _lib.get_lib()
             nd = x.ndim - 2
-            need = lib.nsq_fftconv_nd_workspace_bytes(nd, x.shape[0], x.shape[1], _lib.i64_array(x.shape[2:]),
-                                                      _lib.i64_array(k.shape[1:]), kbatch, _lib.NSQ_DIR_BWD)
+            need = _nd_workspace_bytes(lib, nd, x.shape[0], x.shape[1], _lib.i64_array(x.shape[2:]),
+                                       _lib.i64_array(k.shape[1:]), kbatch, periodic, _lib.NSQ_DIR_BWD)
             ws = _workspace(x.device, need) if need else None
-        fftconv_nd_fwd_raw(x, k, s, y, kbatch, ws)
+        fftconv_nd_fwd_raw(x, k, s, y, kbatch, ws, periodic)
         ctx.save_for_backward(x, k, s)
         ctx.kbatch = kbatch
+        ctx.periodic = periodic
         ctx.has_s = s is not None
         ctx.ws = ws
         return y
@@ -380,15 +398,16 @@ class _FFTConvND(torch.autograd.Function):
         H = x.shape[1]
         gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
         ws, ctx.ws = ctx.ws, None  # the backward consumes the forward state
-        fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch, ws, fwd_state=ws is not None)
+        fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch, ws, fwd_state=ws is not None, periodic=ctx.periodic)
         gsum = None
         if ctx.has_s:
             # per-filter partial sums only for FiLM kernels; a shared kernel's gs is complete
             gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
-        return gx, gk, gsum, None
+        return gx, gk, gsum, None, None
 
 
-def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, nd: int) -> torch.Tensor:
+def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, nd: int,
+             periodic: int = 0) -> torch.Tensor:
     if x.ndim != nd + 2:
         raise ValueError(f"x must be [B, H, {', '.join('S%d' % i for i in range(nd))}]; got {tuple(x.shape)}")
     B, H = x.shape[:2]
@@ -400,9 +419,14 @@ def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | Non
     )
     assert kernel.shape[1] == H, "Input and kernel must have the same number of channels (H)."
     for d in range(nd):
-        assert kernel.shape[2 + d] <= 2 * x.shape[2 + d], (
-            f"Kernel size must be less than 2 * S_{d}. Got {kernel.shape[2 + d]}."
-        )
+        if (periodic >> d) & 1:
+            assert kernel.shape[2 + d] <= x.shape[2 + d], (
+                f"K must be <= N on periodic axis {d}: K={kernel.shape[2 + d]}, N={x.shape[2 + d]}."
+            )
+        else:
+            assert kernel.shape[2 + d] <= 2 * x.shape[2 + d], (
+                f"Kernel size must be less than 2 * S_{d}. Got {kernel.shape[2 + d]}."
+            )
     kbatch = kernel.shape[0]
     input_dtype = x.dtype
     compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
@@ -413,7 +437,7 @@ def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | Non
         if shortcut.shape != (H,):
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         sc = shortcut.to(input_dtype).to(compute_dtype).contiguous()
-    return _FFTConvND.apply(xc, kc, sc, kbatch).to(input_dtype)
+    return _FFTConvND.apply(xc, kc, sc, kbatch, periodic).to(input_dtype)
 
 
 def _chunked(fn, x, kernel, shortcut, chunk_size, nd):

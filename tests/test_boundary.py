@@ -95,3 +95,32 @@ def test_nd_spectrum_block_over_2gib_rejected():
                                 1 << 40, None)
     assert rc == 2  # NSQ_ERR_UNSUPPORTED
     assert b"2 GiB" in lib.nsq_last_error()
+
+
+def test_periodic_lengths_validated_before_launch():
+    """Circular / mixed entry points refuse non-power-of-two or out-of-range
+    periodic lengths (NSQ_ERR_UNSUPPORTED) and periodic kernels longer than the
+    axis (NSQ_ERR_INVALID_ARGUMENT) before the device is touched."""
+    lib = _lib.get_lib()
+    dummy = 16
+    f32 = _lib.NSQ_DTYPE[torch.float32]
+    assert lib.nsq_circular_fftconv1d_fwd(dummy, dummy, None, dummy, f32, 1, 1, 48, 5, 1, None) == 2
+    assert b"power" in lib.nsq_last_error()
+    assert lib.nsq_circular_fftconv1d_fwd(dummy, dummy, None, dummy, f32, 1, 1, 32768, 5, 1, None) == 2
+    assert lib.nsq_circular_fftconv1d_fwd(dummy, dummy, None, dummy, f32, 1, 1, 64, 65, 1, None) == 1
+    assert lib.nsq_circular_fftconv1d_bwd(dummy, dummy, dummy, None, dummy, dummy, None, f32, 2, 1, 64, 5, 3,
+                                          None) == 1  # kernel batch neither 1 nor B
+    S, K = _lib.i64_array([12, 16]), _lib.i64_array([3, 3])
+    assert lib.nsq_mixed_fftconv_nd_workspace_bytes(2, 1, 1, S, K, 1, 0b01, 0) == 0
+    rc = lib.nsq_mixed_fftconv_nd_fwd(2, dummy, dummy, None, dummy, f32, 1, 1, S, K, 1, 0b01, dummy, 1 << 40, None)
+    assert rc == 2 and b"periodic axis 0" in lib.nsq_last_error()
+    # axis 0 zero-padded is fine at 12; axis 1 periodic at 16 with K = 17 is not
+    S, K = _lib.i64_array([12, 16]), _lib.i64_array([3, 17])
+    rc = lib.nsq_mixed_fftconv_nd_fwd(2, dummy, dummy, None, dummy, f32, 1, 1, S, K, 1, 0b10, dummy, 1 << 40, None)
+    assert rc == 1
+    rc = lib.nsq_mixed_fftconv_nd_fwd(2, dummy, dummy, None, dummy, f32, 1, 1, S, K, 1, 0b100, dummy, 1 << 40, None)
+    assert rc == 1 and b"periodic mask" in lib.nsq_last_error()
+    S, K = _lib.i64_array([12, 16]), _lib.i64_array([3, 16])
+    spec_zero = lib.nsq_fftconv_nd_workspace_bytes(2, 1, 1, S, K, 1, 0)
+    spec_mixed = lib.nsq_mixed_fftconv_nd_workspace_bytes(2, 1, 1, S, K, 1, 0b10, 0)
+    assert 0 < spec_mixed < spec_zero  # the periodic axis is not padded: F1 = 16 instead of 32

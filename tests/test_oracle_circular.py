@@ -104,3 +104,53 @@ def test_gradients_are_adjoint_convolution():
             gk[0, :, j0, j1] = (g * np.roll(xn, (j0 - c[0], j1 - c[1]), axis=(2, 3))).sum(axis=(0, 2, 3))
     assert rel_l2(gx, x.grad.numpy()) < 1e-5
     assert rel_l2(gk, k.grad.numpy()) < 1e-5
+
+
+# --- mixed boundary conditions (ops/mixed_fftconv.py) -----------------------
+from oracle.circular_ref import mixed_conv_direct_np, mixed_fftconv_torch  # noqa: E402
+from oracle.fftconv_ref import fftconv_nd_np  # noqa: E402
+
+MIXED = [((2, 2, 16, 12), (1, 2, 5, 7), (True, False)), ((1, 3, 10, 16), (1, 3, 20, 3), (False, True)),
+         ((2, 2, 8, 6, 16), (2, 2, 3, 5, 4), (True, True, False)), ((1, 1, 6, 8, 5), (1, 1, 4, 8, 9), (False, True, False)),
+         ((1, 2, 12, 9), (1, 2, 4, 18), (True, False))]
+
+
+@pytest.mark.parametrize("xs,ks,per", MIXED)
+def test_mixed_restatement_matches_brute_force(xs, ks, per):
+    rng = np.random.default_rng(sum(xs) + 3 * sum(ks))
+    x = rng.standard_normal(xs)
+    k = rng.standard_normal(ks)
+    s = rng.standard_normal(xs[1])
+    ref = mixed_conv_direct_np(x, k, per, s)
+    yt = mixed_fftconv_torch(torch.tensor(x, dtype=torch.float32), torch.tensor(k, dtype=torch.float32), per,
+                             torch.tensor(s, dtype=torch.float32))
+    assert rel_l2(ref, yt) < 1e-5
+
+
+@pytest.mark.parametrize("xs,ks", [((2, 2, 9, 7), (1, 2, 5, 3)), ((1, 2, 5, 6, 4), (1, 2, 3, 4, 8))])
+def test_mixed_brute_force_uniform_cases(xs, ks):
+    """All periodic = the circular brute force; all zero = the zero-padded "same" restatement."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(xs)
+    k = rng.standard_normal(ks)
+    nd = len(xs) - 2
+    assert rel_l2(circular_conv_direct_np(x, k), mixed_conv_direct_np(x, k, (True,) * nd)) < 1e-14
+    assert rel_l2(fftconv_nd_np(x, k[0]), mixed_conv_direct_np(x, k, (False,) * nd)) < 1e-12
+
+
+def test_float32_ramp_error_grows_with_kernel_length():
+    """The reference computes its ramp angles 2*pi*c*f in float32 (circular_fftconv.py:_PhaseRampCache1D.get);
+    at K = L = 4096 the angles reach ~pi*2047 and their rounding costs ~1e-4 relative, while the float64
+    restatement matches the brute force.  The GPU parity tests therefore compare against float64."""
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((1, 2, 4096))
+    k = rng.standard_normal((1, 2, 4096))
+    ref = circular_conv_direct_np(x, k)
+    y64 = circular_fftconv_torch(torch.tensor(x), torch.tensor(k), compute_dtype=torch.float64)
+    y32 = circular_fftconv_torch(torch.tensor(x, dtype=torch.float32), torch.tensor(k, dtype=torch.float32))
+    assert rel_l2(ref, y64) < 1e-12
+    assert rel_l2(ref, y32) > 3e-5
+    # short kernels keep the float32 angles small: the reference arithmetic is then accurate
+    k7 = k[..., :7]
+    y32s = circular_fftconv_torch(torch.tensor(x, dtype=torch.float32), torch.tensor(k7, dtype=torch.float32))
+    assert rel_l2(circular_conv_direct_np(x, k7), y32s) < 2e-6
