@@ -20,6 +20,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
            algorithmic GB/s of the phase BASELINE.md quotes for that config)
        python bench.py --workload cfg2-fwd-bwd   (config 2's block with its
            backward, report-only)
+       python bench.py --workload cfg4-circular|well-rb   (periodic and
+           mixed boundaries, report-only: cfg4's shape with circular padding;
+           the rayleigh_benard Well config's layer, x periodic / y zero-padded)
        python bench.py --copy-calibration   (one plain copy kernel of known size,
                                              for scaling rocprof FETCH/WRITE_SIZE)
 """
@@ -206,6 +209,39 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
             def step():
                 xg.grad = kg.grad = sg.grad = None
                 fn(xg, kg, sg).backward(g)
+    elif name in ("cfg4-circular", "well-rb"):
+        # periodic boundaries (report-only): cfg4's shape with fft_padding="circular" (FFT 128^2, no padding),
+        # and the rayleigh_benard Hyena layer (examples/well/v2/rayleigh_benard/hyena.py: 512x128 / patch 8 =
+        # 64x16 tokens, H=384, batch 64, fft_padding=["circular", "zero"], kernel 64 x 31)
+        from nvsubquadratic_amd import circular_fftconv_hip as C
+        from nvsubquadratic_amd import mixed_fftconv_hip as M
+
+        if name == "cfg4-circular":
+            B, Ch, S, K, phase = 16, 384, (128, 128), (128, 128), "fwd"
+            fn = C.circular_fftconv2d_fp32_bhl
+            desc = ("cfg4-circular: 2D circular FFT conv fwd, B=16 C=384 128^2, filter 128^2 fp32, FFT 128^2, "
+                    "bf16 I/O")
+        else:
+            B, Ch, S, K, phase = 64, 384, (64, 16), (64, 31), "fwd+bwd"
+            fn = lambda x_, k_, s_: M.mixed_fftconv2d_fp32_bhl(x_, k_, (True, False), s_)  # noqa: E731
+            desc = ("well-rb: 2D mixed-boundary FFT conv fwd+bwd (x periodic, y zero-padded), B=64 C=384 64x16, "
+                    "filter 64x31 fp32, FFT 64x32, bf16 I/O")
+        x = torch.randn(B, Ch, *S, device=dev, generator=gen).to(torch.bfloat16)
+        k = torch.randn(1, Ch, *K, device=dev, generator=gen) / (K[0] * K[1]) ** 0.5
+        s = torch.randn(Ch, device=dev, generator=gen).to(torch.bfloat16)
+        dtype = "f32"
+        nbytes = algorithmic_bytes_nd(B, Ch, list(S), list(K), 2, phase)
+        if phase == "fwd":
+            def step():
+                with torch.no_grad():
+                    fn(x, k, s)
+        else:
+            xg, kg, sg = (t.detach().requires_grad_(True) for t in (x, k, s))
+            g = torch.randn(x.shape, device=dev, generator=gen).to(torch.bfloat16)
+
+            def step():
+                xg.grad = kg.grad = sg.grad = None
+                fn(xg, kg, sg).backward(g)
     else:
         raise SystemExit(f"unknown workload {name}")
     ms_list = _time_steps(step, steps, warmup)
@@ -231,7 +267,8 @@ def main() -> None:
     ap.add_argument("--cpu-channels", type=int, default=1024)
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
+                                                              "cfg4-circular", "well-rb"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

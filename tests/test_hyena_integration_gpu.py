@@ -62,3 +62,31 @@ def test_hyena_block_hip_vs_oracle(data_dim, spatial, kshape):
     assert rel_l2(y_ref, y) < 1e-4
     for ref_t, hip_t in zip((q, k, v, kernel, shortcut), args):
         assert rel_l2(ref_t.grad, hip_t.grad) < 1e-4
+
+
+@pytest.mark.parametrize("data_dim,spatial,kshape,fft_padding",
+                         [(1, (256,), (256,), "circular"), (2, (32, 16), (32, 16), "circular"),
+                          (2, (32, 16), (63, 16), ["zero", "circular"]),
+                          (3, (16, 16, 16), (16, 31, 16), ["circular", "zero", "circular"])])
+def test_hyena_block_periodic_boundaries(data_dim, spatial, kshape, fft_padding):
+    """The Well-style configs: fft_padding="circular" (grid_type "single": K = S) and per-axis lists."""
+    from oracle.circular_ref import mixed_fftconv_torch
+    from nvsubquadratic_amd.dispatch import resolve_periodic
+
+    torch.manual_seed(1)
+    B, C = 2, 8
+    q, k, v = (torch.randn(B, *spatial, C, requires_grad=True) for _ in range(3))
+    kernel = torch.randn(1, C, *kshape, requires_grad=True)
+    shortcut = torch.randn(C, requires_grad=True)
+    _, fft_bhl = hip_fftconv_fns(data_dim, False, fft_padding)
+    periodic = resolve_periodic(fft_padding, data_dim)
+    y_ref = _hyena(q, k, v, None, lambda x, kk, s: mixed_fftconv_torch(x, kk, periodic, s, torch.float64),
+                   kernel, shortcut)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    args = [t.detach().cuda().requires_grad_(True) for t in (q, k, v, kernel, shortcut)]
+    y = _hyena(args[0], args[1], args[2], None, fft_bhl, args[3], args[4])
+    y.backward(g.cuda())
+    assert rel_l2(y_ref, y) < 1e-4
+    for ref_t, hip_t in zip((q, k, v, kernel, shortcut), args):
+        assert rel_l2(ref_t.grad, hip_t.grad) < 1e-4

@@ -40,12 +40,26 @@ def test_hip_constraints_mirror_reference_messages():
         dispatch.validate_hip_backend(1, False, "zero")
     with pytest.raises(AssertionError, match="does not support causal"):
         dispatch.validate_hip_backend(2, True, "zero")
-    with pytest.raises(AssertionError, match="only supports zero-padded"):
-        dispatch.validate_hip_backend(3, False, "circular")
-    with pytest.raises(ValueError, match="per-axis fft_padding"):
-        dispatch.validate_hip_backend(2, False, ["zero", "circular"])
+    with pytest.raises(AssertionError, match="does not support causal"):
+        dispatch.validate_hip_backend(3, True, ["zero", "circular", "zero"])
+    with pytest.raises(AssertionError, match="not supported with fft_padding='circular'"):
+        dispatch.validate_hip_backend(2, False, "circular", use_chunked_fftconv=True)
     with pytest.raises(AssertionError, match="data_dim"):
         dispatch.validate_hip_backend(4, False, "zero")
+    dispatch.validate_hip_backend(1, False, "circular")
+    dispatch.validate_hip_backend(1, False, ["circular"])
+    dispatch.validate_hip_backend(3, False, "circular")
+    dispatch.validate_hip_backend(2, False, ["zero", "circular"], use_chunked_fftconv=True)
+
+
+def test_resolve_periodic_mirrors_reference_forms_and_errors():
+    assert dispatch.resolve_periodic("zero", 3) == (False, False, False)
+    assert dispatch.resolve_periodic(" Circular ", 2) == (True, True)
+    assert dispatch.resolve_periodic(["circular", "ZERO"], 2) == (True, False)
+    for bad, msg in ((True, "True/False"), ("circular, zero", "comma-separated"), ((True, False), "booleans"),
+                     (["circular"], "length data_dim"), (["periodic", "zero"], "Invalid padding mode"), (3, "single")):
+        with pytest.raises(ValueError, match=msg):
+            dispatch.resolve_periodic(bad, 2)
 
 
 def test_hip_fn_selection():
@@ -62,3 +76,18 @@ def test_hip_fn_selection_2d_3d():
     assert dispatch.hip_fftconv_fns(2, False) == (F.fftconv2d_bhl_w_reshape, F.fftconv2d_bhl)
     assert dispatch.hip_fftconv_fns(3, False, use_chunked_fftconv=True) == (
         F.fftconv3d_bhl_w_reshape_chunked, F.fftconv3d_bhl_chunked)
+
+
+def test_hip_fn_selection_circular_and_mixed():
+    from nvsubquadratic_amd import circular_fftconv_hip as C
+    from nvsubquadratic_amd import mixed_fftconv_hip as M
+
+    assert dispatch.hip_fftconv_fns(1, False, "circular") == (C.circular_fftconv1d_fp32_bhl_w_reshape,
+                                                              C.circular_fftconv1d_fp32_bhl)
+    assert dispatch.hip_fftconv_fns(3, False, "circular") == (C.circular_fftconv3d_fp32_bhl_w_reshape,
+                                                              C.circular_fftconv3d_fp32_bhl)
+    blh, bhl = dispatch.hip_fftconv_fns(2, False, ["circular", "zero"])
+    assert bhl.op is M.mixed_fftconv2d_fp32_bhl and bhl.periodic == (True, False)
+    assert blh.op is M.mixed_fftconv2d_fp32_bhl_w_reshape
+    blh, bhl = dispatch.hip_fftconv_fns(3, False, ["zero", "circular", "zero"], use_chunked_fftconv=True)
+    assert bhl.op is M.mixed_fftconv3d_fp32_bhl_chunked and bhl.periodic == (False, True, False)
