@@ -161,6 +161,28 @@ static void col_blocks(int inner, LAUNCH&& launch) {
   if (rem) launch(std::integral_constant<int, kNdTailTile>{}, int(ceil_div(rem, CT::M)), full * CM::M);
 }
 
+// Column-block workgroups per channel of an axis-0 pass with tile target
+// `target` (col_blocks: full blocks of M columns, then blocks of 4).
+static int64_t axis0_blocks(const NdPlan& p, int target) {
+  const int inner = p.F[1] * p.FH;
+  int m = target >> p.lF[0];
+  m = m < 4 ? 4 : (m > 16 ? 16 : m);
+  const int full = inner / m, rem = inner - full * m;
+  return full + (rem + 3) / 4;
+}
+
+// Batch split of the axis-0 product / adjoint passes for a shared kernel: a
+// workgroup per (channel, column block) loops over the batch, so few channels
+// and small spectra leave CUs idle; split the batch until about 3072
+// workgroups (12 per CU) are in flight.  FiLM kernels already launch B*H.
+static int axis0_batch_split(const NdPlan& p, int target) {
+  if (p.kb != 1) return 1;
+  const int64_t wgs = p.H * axis0_blocks(p, target);
+  if (wgs >= 1024) return 1;
+  const int64_t want = (3072 + wgs - 1) / wgs;
+  return int(want < p.B ? want : p.B);
+}
+
 // Axis-0 columns: the inner index j runs over a block's F1 rows of the last
 // axis; 3D packs them (RS = FH), 2D has one padded row (F1 = 1, j < FH).
 static ColGeom axis0_geom(const NdPlan& p) {
@@ -273,7 +295,8 @@ static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const 
 }
 
 // Workspace layout (spectrum blocks of p.spec complex64):
-//   backward: [G: BH | X: BH | Khat: NK | Q: NK]
+//   backward: [G: BH | X: BH | Khat: NK | Q: NK | (nz - 1) * NK partial Q]
+//     (nz = axis0_batch_split: the adjoint's batch split, 1 for most shapes)
 //   forward with `save` (a backward-sized workspace): X after the inner-axis
 //     passes and Khat at the backward's positions, the product in the G region;
 //     the backward called with fwd_state then starts from them.
@@ -295,7 +318,7 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
       constexpr int TGT = decltype(tile)::value;
       // the narrow tail instance takes one image per workgroup (its work per
       // image is small, so a batch loop would leave the GPU idle)
-      const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : 1;
+      const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : axis0_batch_split(p, 8192);
       const dim3 grid(unsigned((p.kb != 1 ? BH : p.H) * bsplit), unsigned(gy));
       auto go = [&](auto half, auto ramp) {
         hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT, decltype(half)::value, decltype(ramp)::value>), grid,
@@ -331,22 +354,29 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
   if (!inner_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
+  const int nz = axis0_batch_split(p, kNdBwdTile);  // partial Q blocks follow Q in the workspace
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
     col_blocks<LOGF, kNdBwdTile>(cg.inner_count, [&](auto tile, int gy, int jbase) {
       constexpr int TGT = decltype(tile)::value;
-      const dim3 grid{unsigned(NK), unsigned(gy)};
+      const dim3 grid{unsigned(NK), unsigned(gy), unsigned(nz)};
       if (2 * p.S[0] <= p.F[0])  // the g and x columns are at least half zero padding
         hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, true>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg,
                            (const float2*)wsx, (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1),
-                           p.S[0], p.K[0], rp, jbase, tw);
+                           p.S[0], p.K[0], rp, jbase, NK, tw);
       else
         hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, false>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg,
                            (const float2*)wsx, (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1),
-                           p.S[0], p.K[0], rp, jbase, tw);
+                           p.S[0], p.K[0], rp, jbase, NK, tw);
     });
   });
   if (!ok) return false;
+  if (nz > 1) {
+    const int64_t count = int64_t(p.K[0]) * p.F[1] * p.RS;  // rows [0, K0) of a block
+    const int64_t blocks = (NK * count + 255) / 256;
+    hipLaunchKernelGGL(nd_q_reduce_kernel, dim3(unsigned(blocks < 8192 ? blocks : 8192)), dim3(256), 0, st, wsq, NK,
+                       p.spec, count, nz);
+  }
   const float scale = 1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2));
   RowInvOut og{gx, g, s, nullptr, int(p.H), 0, p.S[2], 0, 0, 0, scale};
   if (!inner_inv<DT, ND_OUT_Y>(p, wsg, BH, p.S[0], 0, p.S[1], og, tw, st)) return false;
@@ -401,7 +431,9 @@ static size_t nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S,
                                  unsigned periodic, int direction) {
   NdPlan p;
   if (!S || !K || !make_nd_plan(nd, B, H, S, K, kbatch, periodic, p)) return 0;
-  const int64_t blocks = direction == NSQ_DIR_BWD ? (2 * B * H + 2 * kbatch * H) : (B * H + kbatch * H);
+  const int64_t blocks = direction == NSQ_DIR_BWD
+                             ? (2 * B * H + (1 + axis0_batch_split(p, kNdBwdTile)) * kbatch * H)
+                             : (B * H + kbatch * H);
   return size_t(blocks * p.spec) * sizeof(float2);
 }
 

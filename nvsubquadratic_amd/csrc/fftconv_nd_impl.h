@@ -631,7 +631,10 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
 
 // Adjoint, axis 0.  Shared kernel (kfilm = 0): grid.x = H, loops b; FiLM:
 // grid.x = B*H, one b.  Writes P (gx pre-image, window [0, S0)) into wsg and
-// Q (gk pre-image, window [0, K0)) into wsq.
+// Q (gk pre-image, window [0, K0)) into wsq.  grid.z > 1 (shared kernel, few
+// channels and column blocks for the CUs): workgroup z takes images
+// [z*B/nz, (z+1)*B/nz) and writes its partial Q to block z*qsplit + hk; the
+// partials are then summed into block hk by nd_q_reduce_kernel.
 template <int LOGF, int TARGET = kNdBwdTile, bool HALF = false>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel(float2* __restrict__ wsg,
                                                                                 const float2* __restrict__ wsx,
@@ -639,6 +642,7 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
                                                                                 float2* __restrict__ wsq, ColGeom cg,
                                                                                 int B, int H, int kfilm, int S0,
                                                                                 int K0, Ramp rp, int jbase,
+                                                                                int64_t qsplit,
                                                                                 const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
   static_assert(C::T % C::M == 0, "nd_col_bwd_kernel: a thread's elements share one column");
@@ -667,7 +671,8 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
     q[it] = make_float2(0.f, 0.f);
   }
   const int nb = kfilm ? 1 : B;
-  for (int bi = 0; bi < nb; ++bi) {
+  const int nz = int(gridDim.z), z = int(blockIdx.z);
+  for (int bi = z * nb / nz; bi < (z + 1) * nb / nz; ++bi) {
     const int64_t bh = kfilm ? hk : (int64_t(bi) * H + hk);
     const ColBuf gb(wsg + bh * cg.spec, cg);
     const ColBuf xb(wsx + bh * cg.spec, cg);
@@ -695,10 +700,26 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
 #pragma unroll
   for (int it = 0; it < PT; ++it) ldsX[m * C::S + kfirst + it * (C::T / C::M)] = q[it];
   __syncthreads();
-  const ColBuf qb(wsq + hk * cg.spec, cg);
+  const ColBuf qb(wsq + (z * qsplit + hk) * cg.spec, cg);
   LdsTile<C::S, false> ldq{ldsX};
   auto stq = [&](int mm, int k, float2 v) { qb.store(k, j0 + mm, j0 + mm < cg.inner_count && k < K0, v); };
   fft<LOGF, true, C::M, C::T, C::S, true>(ldsX, ldq, stq, tw);
+}
+
+// Sum of the batch-split partial Q blocks: for h < nk, block h += blocks
+// z*nk + h, z = 1..nz-1, over the first `count` complex values of each block
+// (the rows [0, K0) the adjoint wrote; padding columns are summed too and
+// never read).  One thread per complex value, fixed summation order.
+__global__ __launch_bounds__(256) void nd_q_reduce_kernel(float2* __restrict__ wsq, int64_t nk, int64_t spec,
+                                                          int64_t count, int nz) {
+  const int64_t total = nk * count;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
+    const int64_t h = i / count, e = i - h * count;
+    float2* q = wsq + h * spec + e;
+    float2 acc = *q;
+    for (int z = 1; z < nz; ++z) acc = cadd(acc, q[int64_t(z) * nk * spec]);
+    *q = acc;
+  }
 }
 
 }  // namespace nsq
