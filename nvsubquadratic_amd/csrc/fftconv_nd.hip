@@ -19,7 +19,8 @@ struct NdPlan {
   int lF[3], F[3], c[3];
   int o[3], r[3];        // forward crop offsets and forward ramp shifts (c = o + r)
   bool ramp;             // some r_d != 0
-  int FH;        // spectrum columns along the last axis, F2/2 + 1
+  bool pack;             // 2D: the DC and Nyquist bins share bin 0 (FH = F2/2)
+  int FH;        // spectrum columns along the last axis: F2/2 + 1, or F2/2 packed
   int RS;        // spectrum row stride (complex elements), >= FH
   int64_t spec;
 };
@@ -70,11 +71,14 @@ static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
     p.c[d] = p.o[d] = k[d] / 2;
     p.r[d] = 0;
   }
-  p.FH = p.F[2] / 2 + 1;
-  // 2D: rows padded to a multiple of 16 complex values, so the 16-column
-  // segments the axis-0 passes move per row start on a 128-byte line (an FH
-  // row stride puts every segment across two lines).  The pad is never read
-  // or written.  3D planes are F1 rows of FH: the axis-0 segments are aligned
+  // 2D rows store the real DC and Nyquist bins packed in bin 0 (N columns, a
+  // multiple of the axis-0 passes' column tiles, instead of N + 1 with a
+  // one-column tail); 3D keeps N + 1 (its axis-1 pass pairs across columns).
+  p.pack = nd == 2;
+  p.FH = p.pack ? p.F[2] / 2 : p.F[2] / 2 + 1;
+  // 2D: rows padded to a multiple of 16 complex values (a pad only for
+  // F2 = 16), so the 16-column segments the axis-0 passes move per row start
+  // on a 128-byte line.  The pad is never read or written.  3D planes are F1 rows of FH: the axis-0 segments are aligned
   // there already (the plane stride is a multiple of 16) and the plane passes
   // keep their compile-time row stride.
   p.RS = nd == 2 ? (p.FH + 15) / 16 * 16 : p.FH;
@@ -107,8 +111,12 @@ static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n
     using C = RowNdCfg<LOGN>;
     const dim3 grid{unsigned(ceil_div(rg.rows, C::M))};
     auto go = [&](auto al, auto half) {
-      hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value>), grid, dim3(C::T), 0,
-                         st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+      if (p.pack)
+        hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value, true>), grid,
+                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+      else
+        hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value, false>), grid,
+                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
@@ -130,27 +138,31 @@ static bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int 
     const dim3 grid(unsigned(ceil_div(rg.rows, C::M)));
     const bool fast = MODE == ND_OUT_Y && o.off2 % 2 == 0 && o.w2 % 8 == 0 &&
                       (reinterpret_cast<uintptr_t>(o.out) & 15) == 0 && (reinterpret_cast<uintptr_t>(o.aux) & 15) == 0;
+    auto go = [&](auto has_s, auto fst, auto pack) {
+      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, decltype(has_s)::value, decltype(fst)::value,
+                                            decltype(pack)::value>),
+                         grid, dim3(C::T), 0, st, ws, rg, o, tw);
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    auto go_pack = [&](auto has_s, auto fst) { p.pack ? go(has_s, fst, T_{}) : go(has_s, fst, F_{}); };
     if constexpr (MODE == ND_OUT_Y) {
       if (fast) {
-        if (o.s)
-          hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, true, true>), grid, dim3(C::T), 0, st, ws, rg, o, tw);
-        else
-          hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, false, true>), grid, dim3(C::T), 0, st, ws, rg, o,
-                             tw);
+        o.s ? go_pack(T_{}, T_{}) : go_pack(F_{}, T_{});
         return;
       }
+      o.s ? go_pack(T_{}, F_{}) : go_pack(F_{}, F_{});
+    } else {
+      go_pack(F_{}, F_{});
     }
-    if (MODE == ND_OUT_Y && o.s)
-      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, true>), grid, dim3(C::T), 0, st, ws, rg, o, tw);
-    else
-      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, false>), grid, dim3(C::T), 0, st, ws, rg, o, tw);
   });
 }
 
 // Column blocks of a pass: full blocks of the kernel's regular width, then the
-// remainder in blocks of kNdTailTile's 4 columns at column offset jbase (a 2D
-// spectrum has FH = F2/2 + 1 columns, so one regular block would otherwise
-// run almost empty).  launch(tile, grid_y, jbase) launches one instance.
+// remainder in blocks of kNdTailTile's 4 columns at column offset jbase (a
+// remainder exists for short 2D rows, FH = F2/2 < 16, and for 3D blocks whose
+// F1 * FH is not a multiple of the width).  launch(tile, grid_y, jbase)
+// launches one instance.
 constexpr int kNdTailTile = 1;  // ColNdCfg clamps this to 4 columns
 template <int LOGF, int TARGET, class LAUNCH>
 static void col_blocks(int inner, LAUNCH&& launch) {
@@ -173,15 +185,21 @@ static int64_t axis0_blocks(const NdPlan& p, int target) {
 
 // Batch split of the axis-0 product / adjoint passes for a shared kernel: a
 // workgroup per (channel, column block) loops over the batch, so few channels
-// and small spectra leave CUs idle; split the batch until about 3072
-// workgroups (12 per CU) are in flight.  FiLM kernels already launch B*H.
-static int axis0_batch_split(const NdPlan& p, int target) {
+// and small spectra leave CUs idle.  Below `lo` workgroups the batch is split
+// until about `want` are in flight.  The product pass splits for free (each
+// share re-reads only its filter columns): lo 4096, want 6144 (24 per CU);
+// the adjoint's shares each add a partial filter-gradient block and a reduce:
+// lo 1024, want 3072 (measured on MI355X: more shares cost more than they
+// hide there).  FiLM kernels already launch B*H workgroups.
+static int axis0_batch_split(const NdPlan& p, int target, int64_t lo, int64_t want_total) {
   if (p.kb != 1) return 1;
   const int64_t wgs = p.H * axis0_blocks(p, target);
-  if (wgs >= 1024) return 1;
-  const int64_t want = (3072 + wgs - 1) / wgs;
+  if (wgs >= lo) return 1;
+  const int64_t want = (want_total + wgs - 1) / wgs;
   return int(want < p.B ? want : p.B);
 }
+static int mul_batch_split(const NdPlan& p) { return axis0_batch_split(p, 8192, 4096, 6144); }
+static int bwd_batch_split(const NdPlan& p) { return axis0_batch_split(p, kNdBwdTile, 1024, 3072); }
 
 // Axis-0 columns: the inner index j runs over a block's F1 rows of the last
 // axis; 3D packs them (RS = FH), 2D has one padded row (F1 = 1, j < FH).
@@ -296,7 +314,7 @@ static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const 
 
 // Workspace layout (spectrum blocks of p.spec complex64):
 //   backward: [G: BH | X: BH | Khat: NK | Q: NK | (nz - 1) * NK partial Q]
-//     (nz = axis0_batch_split: the adjoint's batch split, 1 for most shapes)
+//     (nz = bwd_batch_split: the adjoint's batch split, 1 for most shapes)
 //   forward with `save` (a backward-sized workspace): X after the inner-axis
 //     passes and Khat at the backward's positions, the product in the G region;
 //     the backward called with fwd_state then starts from them.
@@ -318,12 +336,16 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
       constexpr int TGT = decltype(tile)::value;
       // the narrow tail instance takes one image per workgroup (its work per
       // image is small, so a batch loop would leave the GPU idle)
-      const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : axis0_batch_split(p, 8192);
+      const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : mul_batch_split(p);
       const dim3 grid(unsigned((p.kb != 1 ? BH : p.H) * bsplit), unsigned(gy));
       auto go = [&](auto half, auto ramp) {
-        hipLaunchKernelGGL((nd_col_mul_kernel<LOGF, TGT, decltype(half)::value, decltype(ramp)::value>), grid,
-                           dim3(ColNdCfg<LOGF, TGT>::T), 0, st, (const float2*)wsx, wsy, (const float2*)wsk, cg,
-                           int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.o[0], rf, jbase, bsplit, tw);
+        auto launch = [&](auto pack) {
+          hipLaunchKernelGGL(
+              (nd_col_mul_kernel<LOGF, TGT, decltype(half)::value, decltype(ramp)::value, decltype(pack)::value>),
+              grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B),
+              int(p.H), int(p.kb != 1), p.S[0], p.o[0], rf, jbase, bsplit, tw);
+        };
+        p.pack ? launch(std::true_type{}) : launch(std::false_type{});
       };
       using T_ = std::true_type;
       using F_ = std::false_type;
@@ -354,20 +376,23 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
   if (!inner_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
-  const int nz = axis0_batch_split(p, kNdBwdTile);  // partial Q blocks follow Q in the workspace
+  const int nz = bwd_batch_split(p);  // partial Q blocks follow Q in the workspace
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
     constexpr int LOGF = decltype(L)::value;
     col_blocks<LOGF, kNdBwdTile>(cg.inner_count, [&](auto tile, int gy, int jbase) {
       constexpr int TGT = decltype(tile)::value;
       const dim3 grid{unsigned(NK), unsigned(gy), unsigned(nz)};
+      auto go = [&](auto half, auto pack) {
+        hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, decltype(half)::value, decltype(pack)::value>), grid,
+                           dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg, (const float2*)wsx, (const float2*)wsk, wsq,
+                           cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.K[0], rp, jbase, NK, tw);
+      };
+      using T_ = std::true_type;
+      using F_ = std::false_type;
       if (2 * p.S[0] <= p.F[0])  // the g and x columns are at least half zero padding
-        hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, true>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg,
-                           (const float2*)wsx, (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1),
-                           p.S[0], p.K[0], rp, jbase, NK, tw);
+        p.pack ? go(T_{}, T_{}) : go(T_{}, F_{});
       else
-        hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, false>), grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg,
-                           (const float2*)wsx, (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1),
-                           p.S[0], p.K[0], rp, jbase, NK, tw);
+        p.pack ? go(F_{}, T_{}) : go(F_{}, F_{});
     });
   });
   if (!ok) return false;
@@ -432,7 +457,7 @@ static size_t nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S,
   NdPlan p;
   if (!S || !K || !make_nd_plan(nd, B, H, S, K, kbatch, periodic, p)) return 0;
   const int64_t blocks = direction == NSQ_DIR_BWD
-                             ? (2 * B * H + (1 + axis0_batch_split(p, kNdBwdTile)) * kbatch * H)
+                             ? (2 * B * H + (1 + bwd_batch_split(p)) * kbatch * H)
                              : (B * H + kbatch * H);
   return size_t(blocks * p.spec) * sizeof(float2);
 }

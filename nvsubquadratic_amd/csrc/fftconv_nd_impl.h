@@ -68,8 +68,10 @@ struct RowGeom {
 // zero-padded to F2 = 2N, into workspace bins [0, FH) of row (a0, a1).
 // AL: aligned pair access (even len, aligned base; see load_pair_nb).
 // HALF: len <= N (at least half of each row is zero padding): the first pass
-// folds the zero half (HalfZeroLoad).
-template <int LOGN, int DT, bool AL, bool HALF = false>
+// folds the zero half (HalfZeroLoad).  PACK (2D spectra): N bins per row, the
+// real DC and Nyquist values packed in bin 0 as U[0] + i U[N] (see
+// pack_split); otherwise N + 1 bins.
+template <int LOGN, int DT, bool AL, bool HALF = false, bool PACK = false>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typename Elem<DT>::T* __restrict__ src,
                                                                         int len, RowGeom rg, float2* __restrict__ ws,
                                                                         const float2* __restrict__ tw) {
@@ -104,8 +106,12 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
                 root<LOGN + 1>(tw, p), A, Bc);
     float2* out = ws + rowoff[m];
     if (slot0) {
-      out[0] = make_float2(A.x, 0.f);
-      out[C::N] = make_float2(A.y, 0.f);
+      if constexpr (PACK) {
+        out[0] = A;
+      } else {
+        out[0] = make_float2(A.x, 0.f);
+        out[C::N] = make_float2(A.y, 0.f);
+      }
       out[C::N / 2] = Bc;
     } else {
       out[p] = A;
@@ -133,7 +139,7 @@ struct RowInvOut {
 // are predicated.  FAST (ND_OUT_Y; even off2, w2 a multiple of 8, out and aux
 // 16-byte aligned): the epilogue moves 8 consecutive kept samples per thread,
 // four complex values from LDS, one 16-byte aux load and one 16-byte store.
-template <int LOGN, int DT, int MODE, bool HAS_S, bool FAST = false>
+template <int LOGN, int DT, int MODE, bool HAS_S, bool FAST = false, bool PACK = false>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const float2* __restrict__ ws, RowGeom rg,
                                                                         RowInvOut o, const float2* __restrict__ tw) {
   using C = RowNdCfg<LOGN>;
@@ -158,9 +164,9 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
     const bool slot0 = (p == 0);
     const float2* in = ws + rowoff[m];
     const float2 u0 = in[slot0 ? 0 : p];
-    const float2 u1 = in[slot0 ? C::N : C::N - p];
+    const float2 u1 = in[slot0 ? (PACK ? 0 : C::N) : C::N - p];  // PACK: no bin N (row stride may be N)
     const float2 u2 = in[C::N / 2];
-    float2 A = slot0 ? make_float2(u0.x, u1.x) : u0;
+    float2 A = slot0 ? (PACK ? u0 : make_float2(u0.x, u1.x)) : u0;
     float2 Bc = slot0 ? u2 : cconj(u1);
     A = make_float2(rok ? A.x : 0.f, rok ? A.y : 0.f);
     Bc = make_float2(rok ? Bc.x : 0.f, rok ? Bc.y : 0.f);
@@ -544,6 +550,51 @@ __device__ __forceinline__ float2 ramp_inner(const Ramp& rp, const TwTable& tt, 
   return cmul(tt.load(f1, (rp.c1 * k1) & (f1 - 1)), tt.load(f2, (rp.c2 * k2) & (f2 - 1)));
 }
 
+// Packed DC / Nyquist column of a 2D spectrum (PACK): bin 0 of every row holds
+// d + i n with d, n the rows' real DC and Nyquist values, so along axis 0 it
+// transforms to Cc = D + i Nq with D, Nq Hermitian (transforms of real
+// columns).  Separation by the pairing of k and F-k:
+//   D[k] = (Cc[k] + conj Cc[-k]) / 2,  Nq[k] = (Cc[k] - conj Cc[-k]) / 2i.
+// A product Y = X H per column becomes Yc = Xd Hd + i Xn Hn on this column
+// (H = filter times ramp; the Nyquist ramp is the DC one times (-1)^{c2}).
+__device__ __forceinline__ void pack_split(float2 c, float2 cm, float2& d, float2& n) {
+  const float2 cc = cconj(cm);
+  d = cscale(cadd(c, cc), 0.5f);
+  n = mul_neg_i(cscale(csub(c, cc), 0.5f));
+}
+
+// Column-0 filter factors of a PACK workgroup (j0 = 0) for the threads whose
+// elements are column 0 (pc0; their frequencies k = kf + it * step): kv[it]
+// holds the packed filter value Kc[k] on entry and fd * Kd[k] on exit, and
+// kcol[k] = fn * Kn[k], fd / fn the DC / Nyquist factors given by `fac`
+// (fac(it, k, fd, fn)).  Uses kcol for the exchange; all threads of the
+// workgroup must call it (it has barriers).
+template <int F, int PT, class FAC>
+__device__ __forceinline__ void pack_filter(bool pc0, int kf, int step, float2* kv, float2* kcol, FAC&& fac) {
+  if (pc0) {
+#pragma unroll
+    for (int it = 0; it < PT; ++it) kcol[kf + it * step] = kv[it];
+  }
+  __syncthreads();
+  float2 kn[PT];
+  if (pc0) {
+#pragma unroll
+    for (int it = 0; it < PT; ++it) {
+      const int k = kf + it * step;
+      float2 d, n, fd, fn;
+      pack_split(kv[it], kcol[(F - k) & (F - 1)], d, n);
+      fac(it, k, fd, fn);
+      kv[it] = cmul(d, fd);
+      kn[it] = cmul(n, fn);
+    }
+  }
+  __syncthreads();
+  if (pc0) {
+#pragma unroll
+    for (int it = 0; it < PT; ++it) kcol[kf + it * step] = kn[it];
+  }
+}
+
 // Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0),
 // read from wsx and written to wsy (the same buffer for an in-place product).
 // Shared filter (kfilm = 0): grid.x = H * bsplit and a workgroup loops over
@@ -556,8 +607,9 @@ __device__ __forceinline__ float2 ramp_inner(const Ramp& rp, const TwTable& tt, 
 // are loaded and the first pass's butterflies fold the zeros away.  RAMP
 // (periodic axes): the filter values are multiplied by conj(R), R the shift
 // ramp of `rf`, as they are loaded, which rolls the output by -c_d along
-// every axis (the circular "same" alignment; c0 is then 0).
-template <int LOGF, int TARGET = 8192, bool HALF = false, bool RAMP = false>
+// every axis (the circular "same" alignment; c0 is then 0).  PACK (2D): the
+// inner index j = 0 is the packed DC / Nyquist column (pack_split).
+template <int LOGF, int TARGET = 8192, bool HALF = false, bool RAMP = false, bool PACK = false>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
                                                                                 const float2* __restrict__ wsk,
                                                                                 ColGeom cg, int B, int H, int kfilm,
@@ -577,17 +629,34 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
   // Filter spectrum of this column block (element e -> column e % M,
   // frequency e / M), loaded before the first transform so its latency hides.
   constexpr int PT = C::TILE / C::T;
+  static_assert(C::T % C::M == 0, "nd_col_mul_kernel: a thread's elements share one column");
   float2 kv[PT];
   const int tk = opaque_tid();
+  // PACK: this thread's elements are the packed column (k = tk / M + it * T / M)
+  const bool pc0 = PACK && j0 == 0 && tk % C::M == 0;
+  __shared__ float2 kcol[PACK ? C::F : 1];
+  __shared__ float2 ycol[PACK ? C::F : 1];  // column-0 products (registers would cost occupancy)
 #pragma unroll
   for (int it = 0; it < PT; ++it) {
     const int e = tk + it * C::T;
     const int jj = j0 + e % C::M, k = e / C::M;
     kv[it] = kb.load(k, jj, jj < cg.inner_count);
     if constexpr (RAMP) {
-      const TwTable tt(tw);
-      const float2 r = cmul(ramp_inner(rf, tt, jj < cg.inner_count ? jj : 0), tt.load(C::F, (rf.c0 * k) & (C::F - 1)));
-      kv[it] = cmulc(kv[it], r);
+      if (!pc0) {
+        const TwTable tt(tw);
+        const float2 r =
+            cmul(ramp_inner(rf, tt, jj < cg.inner_count ? jj : 0), tt.load(C::F, (rf.c0 * k) & (C::F - 1)));
+        kv[it] = cmulc(kv[it], r);
+      }
+    }
+  }
+  if constexpr (PACK) {
+    if (j0 == 0) {  // (uniform) kv of pc0 threads -> conj(Rd) Kd, kcol -> conj(Rn) Kn
+      pack_filter<C::F, PT>(pc0, tk / C::M, C::T / C::M, kv, kcol, [&](int, int k, float2& fd, float2& fn) {
+        fd = make_float2(1.f, 0.f);
+        if constexpr (RAMP) fd = cconj(TwTable(tw).load(C::F, (rf.c0 * k) & (C::F - 1)));
+        fn = (RAMP && (rf.c2 & 1)) ? make_float2(-fd.x, -fd.y) : fd;
+      });
     }
   }
   const int nb = kfilm ? 1 : B;
@@ -617,7 +686,26 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
     for (int it = 0; it < PT; ++it) {
       const int e = tp + it * C::T;
       float2& z = lds[(e % C::M) * C::S + e / C::M];
-      z = cmul(z, kv[it]);
+      if (PACK && pc0) {  // column 0: Yc = Xd Hd + i Xn Hn, staged until every pair is read
+        const int k = e / C::M;
+        float2 xd, xn;
+        pack_split(z, lds[(C::F - k) & (C::F - 1)], xd, xn);
+        ycol[PACK ? k : 0] = cadd(cmul(xd, kv[it]), mul_i(cmul(xn, kcol[PACK ? k : 0])));
+      } else {
+        z = cmul(z, kv[it]);
+      }
+    }
+    if constexpr (PACK) {
+      if (j0 == 0) {
+        __syncthreads();
+        if (pc0) {
+#pragma unroll
+          for (int it = 0; it < PT; ++it) {
+            const int k = (tp + it * C::T) / C::M;
+            lds[k] = ycol[k];
+          }
+        }
+      }
     }
     __syncthreads();
     auto st = [&](int m, int k, float2 val) {
@@ -635,7 +723,7 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
 // channels and column blocks for the CUs): workgroup z takes images
 // [z*B/nz, (z+1)*B/nz) and writes its partial Q to block z*qsplit + hk; the
 // partials are then summed into block hk by nd_q_reduce_kernel.
-template <int LOGF, int TARGET = kNdBwdTile, bool HALF = false>
+template <int LOGF, int TARGET = kNdBwdTile, bool HALF = false, bool PACK = false>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel(float2* __restrict__ wsg,
                                                                                 const float2* __restrict__ wsx,
                                                                                 const float2* __restrict__ wsk,
@@ -670,6 +758,18 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
     rr[it] = cmul(r12, tt.load(C::F, (rp.c0 * k) & (C::F - 1)));
     q[it] = make_float2(0.f, 0.f);
   }
+  // PACK: column 0 is the packed DC / Nyquist column (pack_split): kv -> Kd,
+  // kcol -> Kn; the Nyquist ramp is the DC one (rr) times (-1)^{c2}.
+  const bool pc0 = PACK && j0 == 0 && m == 0;
+  __shared__ float2 kcol[PACK ? C::F : 1];
+  __shared__ float2 pcol[PACK ? C::F : 1];  // column-0 P values, staged until every pair is read
+  const float nys = (rp.c2 & 1) ? -1.f : 1.f;
+  if constexpr (PACK) {
+    if (j0 == 0)
+      pack_filter<C::F, PT>(pc0, kfirst, C::T / C::M, kv, kcol, [](int, int, float2& fd, float2& fn) {
+        fd = fn = make_float2(1.f, 0.f);
+      });
+  }
   const int nb = kfilm ? 1 : B;
   const int nz = int(gridDim.z), z = int(blockIdx.z);
   for (int bi = z * nb / nz; bi < (z + 1) * nb / nz; ++bi) {
@@ -688,9 +788,32 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
 #pragma unroll
     for (int it = 0; it < PT; ++it) {
       const int a = m * C::S + kfirst + it * (C::T / C::M);
-      const float2 gsh = cmul(ldsG[a], rr[it]);
-      q[it] = cadd(q[it], cmulc(gsh, ldsX[a]));
-      ldsG[a] = cmulc(gsh, kv[it]);
+      if (PACK && pc0) {
+        // column 0: P = Gd Rd conj(Kd) + i Gn Rn conj(Kn),  Q += Gd Rd conj(Xd) + i Gn Rn conj(Xn)
+        const int k = kfirst + it * (C::T / C::M), km = (C::F - k) & (C::F - 1);
+        float2 gd, gn, xd, xn;
+        pack_split(ldsG[k], ldsG[km], gd, gn);
+        pack_split(ldsX[k], ldsX[km], xd, xn);
+        const float2 gdr = cmul(gd, rr[it]), gnr = cscale(cmul(gn, rr[it]), nys);
+        q[it] = cadd(q[it], cadd(cmulc(gdr, xd), mul_i(cmulc(gnr, xn))));
+        pcol[PACK ? k : 0] = cadd(cmulc(gdr, kv[it]), mul_i(cmulc(gnr, kcol[PACK ? k : 0])));
+      } else {
+        const float2 gsh = cmul(ldsG[a], rr[it]);
+        q[it] = cadd(q[it], cmulc(gsh, ldsX[a]));
+        ldsG[a] = cmulc(gsh, kv[it]);
+      }
+    }
+    if constexpr (PACK) {
+      if (j0 == 0) {
+        __syncthreads();  // every column-0 pair read before it is overwritten
+        if (pc0) {
+#pragma unroll
+          for (int it = 0; it < PT; ++it) {
+            const int k = kfirst + it * (C::T / C::M);
+            ldsG[k] = pcol[k];
+          }
+        }
+      }
     }
     __syncthreads();
     LdsTile<C::S, false> ldl{ldsG};
