@@ -97,8 +97,8 @@ int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const
  *   y = y.to(dtype) + shortcut * x.
  * k: [kbatch*H, K] float32, kbatch = 1 (shared) or B (per-sample FiLM kernels);
  * gk likewise; gs: [kbatch*H] float32 partials (the caller sums over kbatch).
- * 1 <= K <= L; L must be a power of two in [16, 16384] (NSQ_ERR_UNSUPPORTED
- * otherwise).  No workspace.  Replaces nvsubquadratic/ops/circular_fftconv.py:310-404
+ * 1 <= K <= L; L must be a power of two <= 16384 (NSQ_ERR_UNSUPPORTED
+ * otherwise; L < 16 runs on its periodic extension at length 16).  No workspace.  Replaces nvsubquadratic/ops/circular_fftconv.py:310-404
  * (circular_fftconv1d_fp32_bhl, torch.fft in the reference; its autograd for the
  * backward): gx = corr(g, k) + s*g, gk[j] = sum_{b,n} g[n] x[(n + (K-1)//2 - j) mod L],
  * gs = sum g*x.
@@ -189,8 +189,8 @@ int nsq_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* k, con
  *   y[.., n_d, ..] = sum_j k[.., j_d, ..] x[.., (n_d + (K_d-1)//2 - j_d) mod S_d, ..]
  * (the circular "same" alignment, shift -((K_d-1)//2) as a phase ramp on the
  * filter spectrum).  Clear bits are zero-padded "same" axes exactly as above.
- * Periodic lengths must be powers of two in [16, 1024] (NSQ_ERR_UNSUPPORTED
- * otherwise).  periodic = 0 is nsq_fftconv_nd_*; all bits set is the circular
+ * Periodic lengths must be powers of two up to 1024 (NSQ_ERR_UNSUPPORTED
+ * otherwise; lengths below 16 run on their periodic extension at 16).  periodic = 0 is nsq_fftconv_nd_*; all bits set is the circular
  * conv.  Replaces nvsubquadratic/ops/circular_fftconv.py:406-483
  * (circular_fftconv2d_fp32_bhl), :486-569 (circular_fftconv3d_fp32_bhl) and
  * nvsubquadratic/ops/mixed_fftconv.py:504-630 (_mixed_fftconv_nd_fp32_bhl,

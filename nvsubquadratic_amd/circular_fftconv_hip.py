@@ -18,9 +18,10 @@ spectrum (``nsq_circular_fftconv1d_*``).  ``use_phase_shift`` is accepted for
 signature parity; both of the reference's branches give the same result and
 the kernels always apply the shift in the frequency domain.
 
-Sizes: periodic lengths must be powers of two (2D / 3D: 16..1024 per axis;
-1D: 16..16384); other sizes raise ``NotImplementedError`` (the product has no
-CPU fallback).
+Sizes: periodic lengths must be powers of two (2D / 3D: up to 1024 per axis;
+1D: up to 16384); lengths below 16 run on their periodic extension at FFT
+length 16.  Other sizes raise ``NotImplementedError`` (the product has no CPU
+fallback).
 """
 
 from __future__ import annotations

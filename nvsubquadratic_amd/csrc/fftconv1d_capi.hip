@@ -25,8 +25,8 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
   return NSQ_OK;
 }
 
-// Circular 1D: L a power of two in [16, 16384] (the fused plan at FFT length L),
-// 1 <= K <= L, kbatch 1 or B.
+// Circular 1D: L a power of two <= 16384 (the fused plan at FFT length
+// max(L, 16)), 1 <= K <= L, kbatch 1 or B.
 static int validate_circ(const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H, int64_t L,
                          int64_t K, int64_t kbatch, int& logN) {
   NSQ_CHECK_ARG(a && b && k, "circular_fftconv1d: null tensor pointer");
@@ -38,12 +38,12 @@ static int validate_circ(const void* a, const void* b, const float* k, int dtype
   NSQ_CHECK_ARG(kbatch == 1 || kbatch == B, "circular_fftconv1d: kernel batch must be 1 or B (got %lld, B=%lld)",
                 (long long)kbatch, (long long)B);
   NSQ_CHECK_ARG(B * H <= 0x7fffffff && B <= 65535, "circular_fftconv1d: tensor too large");
-  if (L < 16 || L > 16384 || (L & (L - 1))) {
-    set_error("circular_fftconv1d: unsupported length L=%lld: the HIP kernels take powers of two in [16, 16384]",
+  if (L > 16384 || (L & (L - 1))) {
+    set_error("circular_fftconv1d: unsupported length L=%lld: the HIP kernels take powers of two up to 16384",
               (long long)L);
     return NSQ_ERR_UNSUPPORTED;
   }
-  logN = ilog2_ceil(L) - 1;
+  logN = (L < 16 ? 4 : ilog2_ceil(L)) - 1;
   return NSQ_OK;
 }
 

@@ -165,14 +165,15 @@ __device__ __forceinline__ void filter_spectrum(float2* lds, const float* __rest
 
 // Forward, fused plan.  grid = (ceil(H/M), nb_split); each workgroup handles
 // batch rows [b0, b0 + b_per_wg).  CIRC: circular conv at FFT length 2N = L
-// (no padding, no crop) rolled by -c through the filter ramp.  kfilm: the
-// filter is per image ([B, H, K]); the launch then gives one image per
-// workgroup (b_per_wg = 1).
+// (no padding, no crop) rolled by -c through the filter ramp; a period L < 16
+// runs at length 16 on the periodic extension of x (sample i read at i & wm,
+// wm = L - 1; -1 otherwise).  kfilm: the filter is per image ([B, H, K]); the
+// launch then gives one image per workgroup (b_per_wg = 1).
 template <int LOGN, int DT, bool FOLD, bool CIRC = false>
 __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
     const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ k,
     const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ y, int B, int H, int L,
-    int K, int b_per_wg, const float2* __restrict__ tw, int c, int kfilm) {
+    int K, int b_per_wg, const float2* __restrict__ tw, int c, int kfilm, int wm) {
   using C = FusedCfg<LOGN>;
   __shared__ float2 lds[C::TILE_P];
   const int h0 = blockIdx.x * C::M;
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
     auto ld = [&](int m, int n) -> float2 {
       const int h = h0 + m;
       if (h >= H) return make_float2(0.f, 0.f);
-      return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
+      return load_pair<DT>(x + (int64_t(b) * H + h) * L, (2 * int64_t(n)) & wm, L);
     };
     LdsTile<C::SP, true> st{lds};
     fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
@@ -238,13 +239,14 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
 // kfilm: grid = (ceil(H/M), B), one image per workgroup, whose filter and
 // filter-gradient rows are that image's.  CIRC: as the forward; the filter
 // gradient gk[j] = sum_n g[n] x[(n + c - j) mod L] is the correlation read at
-// lag (j - c) mod L.
+// lag (j - c) mod L; on a periodic extension (wm = L - 1) every lag repeats
+// 2N / L times, so gk and gs are scaled by gks = L / 2N (1 otherwise).
 template <int LOGN, int DT, bool FOLD, bool CIRC = false>
 __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x,
     const float* __restrict__ k, const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ gx,
     float* __restrict__ gk, float* __restrict__ gs, int B, int H, int L, int K, const float2* __restrict__ tw, int c,
-    int kfilm) {
+    int kfilm, int wm, float gks) {
   using C = FusedCfg<LOGN>;
   __shared__ float2 ldsG[C::TILE_P];
   __shared__ float2 ldsX[C::TILE_P];
@@ -271,12 +273,12 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
       const typename Elem<DT>::T* row = g + (int64_t(b) * H + h) * L;
       const int64_t i0 = 2 * int64_t(n);
       if (FOLD && i0 >= 2 * int64_t(L)) return load_pair<DT>(row, i0 - 2 * int64_t(L), L);
-      return load_pair<DT>(row, i0, L);
+      return load_pair<DT>(row, i0 & wm, L);
     };
     auto ldx = [&](int m, int n) -> float2 {
       const int h = h0 + m;
       if (h >= H) return make_float2(0.f, 0.f);
-      return load_pair<DT>(x + (int64_t(b) * H + h) * L, 2 * int64_t(n), L);
+      return load_pair<DT>(x + (int64_t(b) * H + h) * L, (2 * int64_t(n)) & wm, L);
     };
     LdsTile<C::SP, true> stG{ldsG};
     LdsTile<C::SP, true> stX{ldsX};
@@ -327,14 +329,14 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     if constexpr (CIRC) {
       constexpr int F = 2 * C::N;
       const int j0 = (2 * n + c) & (F - 1), j1 = (2 * n + 1 + c) & (F - 1);
-      if (j0 < K) gk[int64_t(h) * K + j0] = v.x * scale;
-      if (j1 < K) gk[int64_t(h) * K + j1] = v.y * scale;
+      if (j0 < K) gk[int64_t(h) * K + j0] = v.x * scale * gks;
+      if (j1 < K) gk[int64_t(h) * K + j1] = v.y * scale * gks;
     } else {
       const int64_t i0 = 2 * int64_t(n);
       if (i0 < K) gk[int64_t(h) * K + i0] = v.x * scale;
       if (i0 + 1 < K) gk[int64_t(h) * K + i0 + 1] = v.y * scale;
     }
-    if (n == 0 && gs) gs[h] = v.x * scale;
+    if (n == 0 && gs) gs[h] = v.x * scale * gks;
   };
   LdsTile<C::SP, true> ldl{ldsX};
   fft<LOGN, true, C::M, C::T, C::SP>(ldsX, ldl, epik, tw);
@@ -828,10 +830,10 @@ static void launch_fused_fwd(const Plan1D& p, const void* x, const float* k, con
   dim3 grid(gh, nb);
   if (p.fold)
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw, 0, 0);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, 0, -1);
   else
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw, 0, 0);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, 0, -1);
 }
 
 template <int LOGN, int DT>
@@ -842,10 +844,10 @@ static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, cons
   dim3 grid(int(ceil_div(H, C::M)));
   if (p.fold)
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0, -1, 1.f);
   else
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0, -1, 1.f);
 }
 
 // Circular 1D (fused plan at FFT length L = 2N): shift c = (K-1)/2; kfilm =
@@ -863,8 +865,10 @@ static void launch_circ_fwd(const void* x, const float* k, const void* s, void* 
     bpw = int(ceil_div(B, nb));
   }
   const dim3 grid(gh, unsigned(ceil_div(B, bpw)));
+  // a period shorter than the transform: periodic extension (L = 1, K = 1: plain zero padding is exact)
+  const int wm = (L > 1 && L < 2 * C::N) ? L - 1 : -1;
   hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)x, k,
-                     (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, (K - 1) / 2, kfilm);
+                     (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, (K - 1) / 2, kfilm, wm);
 }
 
 template <int LOGN, int DT>
@@ -873,8 +877,10 @@ static void launch_circ_bwd(const void* g, const void* x, const float* k, const 
   using C = FusedCfg<LOGN>;
   using ET = typename Elem<DT>::T;
   const dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
+  const int wm = (L > 1 && L < 2 * C::N) ? L - 1 : -1;
   hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
-                     (const ET*)x, k, (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, (K - 1) / 2, kfilm);
+                     (const ET*)x, k, (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, (K - 1) / 2, kfilm, wm,
+                     wm == -1 ? 1.f : float(L) / float(2 * C::N));
 }
 
 // Workspace layout of the 4-step plan (rows of N complex64):
@@ -1051,7 +1057,8 @@ bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, cons
                                                                 fwd_state, tw, st);
 }
 
-// Circular 1D: logN = log2(L) - 1 in [3, 13] (L a power of two in [16, 16384]).
+// Circular 1D: logN = max(log2(L), 4) - 1 in [3, 13] (L a power of two <= 16384;
+// L < 16 runs at transform length 16 on the periodic extension).
 template <int DT>
 bool run_circ_fwd(int logN, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
                   int kfilm, const float2* tw, hipStream_t st) {

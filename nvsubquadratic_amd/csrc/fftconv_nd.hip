@@ -9,7 +9,13 @@ namespace nsq {
 //     window [K_d/2, K_d/2 + S_d) of the linear conv (crop o_d = K_d/2);
 //   periodic (circular):  F_d = S_d (a power of two in [16, 2^kNdMaxLogF]),
 //     K_d <= S_d, output = the whole circular conv rolled by -(K_d-1)/2, done
-//     as a ramp on the filter spectrum (r_d = (K_d-1)/2, o_d = 0).
+//     as a ramp on the filter spectrum (r_d = (K_d-1)/2, o_d = 0).  A shorter
+//     power-of-two period (2, 4, 8) is tiled: F_d = 16 and the first passes read
+//     x and g at index n & (S_d - 1) (their periodic extension, of which the
+//     period-16 circular conv restricted to [0, S_d) is the period-S_d one;
+//     the filter is not extended).  The extension repeats every product
+//     F_d / S_d times, so gk and gs are scaled by S_d / F_d.  A period of 1 is
+//     the zero-padded 1-tap case.
 // Either way y[n] = sum_j k[j] x[n + c_d - j] along the axis, c_d = o_d + r_d,
 // which is the shift the backward's ramp and its gs lag use.
 struct NdPlan {
@@ -19,6 +25,8 @@ struct NdPlan {
   int lF[3], F[3], c[3];
   int o[3], r[3];        // forward crop offsets and forward ramp shifts (c = o + r)
   bool ramp;             // some r_d != 0
+  int wm[3];             // index mask of x / g along the axis: -1, or S_d - 1 for a tiled periodic axis
+  float gk_scale;        // 1 / (product of F_d / S_d over tiled axes): gk, gs of the periodic extension
   bool pack;             // 2D: the DC and Nyquist bins share bin 0 (FH = F2/2)
   int FH;        // spectrum columns along the last axis: F2/2 + 1, or F2/2 packed
   int RS;        // spectrum row stride (complex elements), >= FH
@@ -35,6 +43,7 @@ static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
   p.H = H;
   p.kb = kb;
   p.ramp = false;
+  p.gk_scale = 1.f;
   int s[3] = {1, 1, 1}, k[3] = {1, 1, 1};
   bool per[3] = {false, false, false};
   if (nd == 2) {
@@ -47,16 +56,22 @@ static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
   for (int d = 0; d < 3; ++d) {
     p.S[d] = s[d];
     p.K[d] = k[d];
+    p.wm[d] = -1;
     if (nd == 2 && d == 1) {
       p.lF[d] = 0; p.F[d] = 1; p.c[d] = 0; p.o[d] = 0; p.r[d] = 0;
       continue;
     }
-    if (per[d]) {
-      if (k[d] < 1 || k[d] > s[d] || s[d] < 16 || (s[d] & (s[d] - 1))) return false;
-      const int lf = ilog2_ceil(s[d]);
+    if (per[d] && s[d] > 1) {
+      if (k[d] < 1 || k[d] > s[d] || (s[d] & (s[d] - 1))) return false;
+      int lf = ilog2_ceil(s[d]);
       if (lf > kNdMaxLogF) return false;
+      if (lf < 4) {  // tiled short period
+        p.wm[d] = s[d] - 1;
+        p.gk_scale *= float(s[d]) / 16.f;
+        lf = 4;
+      }
       p.lF[d] = lf;
-      p.F[d] = s[d];
+      p.F[d] = 1 << lf;
       p.c[d] = p.r[d] = (k[d] - 1) / 2;
       p.o[d] = 0;
       p.ramp = p.ramp || p.r[d] != 0;
@@ -102,10 +117,13 @@ static bool with_log(int v, F&& f) {
   }
 }
 
+// wrap: x / g (read through the plan's periodic extension masks); the filter
+// is never extended.
 template <int DT>
-static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, float2* ws,
+static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, bool wrap, float2* ws,
                     const float2* tw, hipStream_t st) {
   RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.RS};
+  const int wm = wrap ? p.wm[2] : -1;
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
     constexpr int LOGN = decltype(L)::value;
     using C = RowNdCfg<LOGN>;
@@ -113,15 +131,15 @@ static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n
     auto go = [&](auto al, auto half) {
       if (p.pack)
         hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value, true>), grid,
-                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, wm, rg, ws, tw);
       else
         hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value, false>), grid,
-                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, rg, ws, tw);
+                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, wm, rg, ws, tw);
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
     const bool al = pairs_aligned<DT>(src, len, len);
-    if (len <= C::N)  // packed samples [N/2, N) of every row are zero
+    if (len <= C::N && wm == -1)  // packed samples [N/2, N) of every row are zero
       al ? go(T_{}, T_{}) : go(F_{}, T_{});
     else
       al ? go(T_{}, F_{}) : go(F_{}, F_{});
@@ -211,7 +229,7 @@ static ColGeom axis0_geom(const NdPlan& p) {
 // axis 0 is n_valid0 (used as the middle-row count of axis-1 passes).
 template <bool INV>
 static bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_valid0, int in_cnt, int out_off,
-                     int out_cnt, const float2* tw, hipStream_t st) {
+                     int out_cnt, const float2* tw, hipStream_t st, int wm = -1) {
   ColGeom cg;
   if (axis == 1) {
     cg = ColGeom{n_valid0, int64_t(p.F[1]) * p.RS, p.spec, int64_t(p.RS), p.FH};
@@ -224,7 +242,7 @@ static bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_v
     col_blocks<LOGF, 8192>(cg.inner_count, [&](auto tile, int gy, int jbase) {
       constexpr int TGT = decltype(tile)::value;
       hipLaunchKernelGGL((nd_col_kernel<LOGF, INV, TGT>), dim3(unsigned(n_outer), unsigned(gy)),
-                         dim3(ColNdCfg<LOGF, TGT>::T), 0, st, ws, cg, in_cnt, out_off, out_cnt, jbase, tw);
+                         dim3(ColNdCfg<LOGF, TGT>::T), 0, st, ws, cg, in_cnt, wm, out_off, out_cnt, jbase, tw);
     });
   });
 }
@@ -255,10 +273,12 @@ static bool with_plane(const NdPlan& p, F&& f) {
   return launched;
 }
 
-// Forward inner-axis transforms of nbh blocks of [n0][n1][len] real rows.
+// Forward inner-axis transforms of nbh blocks of [n0][n1][len] real rows
+// (wrap: x / g, read through the periodic extension masks).
 template <int DT>
-static bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, float2* ws,
+static bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, bool wrap, float2* ws,
                       const float2* tw, hipStream_t st) {
+  const int wm1 = wrap ? p.wm[1] : -1, wm2 = wrap ? p.wm[2] : -1;
   if (plane_ok(p)) {
     using ET = typename Elem<DT>::T;
     const bool al = pairs_aligned<DT>(src, len, len);
@@ -267,18 +287,18 @@ static bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int
       const dim3 grid(unsigned(nbh * n0));
       auto go = [&](auto alc, auto half) {
         hipLaunchKernelGGL((nd_plane_fwd_kernel<LOGN, LOGF1, DT, decltype(alc)::value, decltype(half)::value>), grid,
-                           dim3(256), 0, st, (const ET*)src, n0, n1, len, ws, p.spec, tw);
+                           dim3(256), 0, st, (const ET*)src, n0, n1, len, wm1, wm2, ws, p.spec, tw);
       };
       using T_ = std::true_type;
       using F_ = std::false_type;
-      if (len <= (1 << LOGN) && 2 * n1 <= (1 << LOGF1))  // rows and columns at least half zero padding
+      if (len <= (1 << LOGN) && 2 * n1 <= (1 << LOGF1) && wm1 == -1 && wm2 == -1)  // at least half zero padding
         al ? go(T_{}, T_{}) : go(F_{}, T_{});
       else
         al ? go(T_{}, F_{}) : go(F_{}, F_{});
     });
   }
-  if (!row_fwd<DT>(p, src, nbh, n0, n1, len, ws, tw, st)) return false;
-  return p.nd != 3 || col_pass<false>(p, ws, nbh, 1, n0, n1, 0, p.F[1], tw, st);
+  if (!row_fwd<DT>(p, src, nbh, n0, n1, len, wrap, ws, tw, st)) return false;
+  return p.nd != 3 || col_pass<false>(p, ws, nbh, 1, n0, n1, 0, p.F[1], tw, st, wm1);
 }
 
 // Inverse inner-axis transforms, crop (axis 1: [off1, off1 + n1out); axis 2:
@@ -308,7 +328,7 @@ static bool inner_inv(const NdPlan& p, float2* ws, int64_t nbh, int n0, int off1
 // Filter spectrum: kb*H blocks of the [kb*H][K0][K1][K2] float32 kernel.
 static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {
   const int64_t nk = p.kb * p.H;
-  if (!inner_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], wsk, tw, st)) return false;
+  if (!inner_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], false, wsk, tw, st)) return false;
   return col_pass<false>(p, wsk, nk, 0, 1, p.K[0], 0, p.F[0], tw, st);
 }
 
@@ -327,7 +347,7 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
   float2* wsk = wsx + BH * p.spec;
   float2* wsy = save ? ws : wsx;
   if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-  if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
+  if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rf{p.r[0], p.r[1], p.r[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
   bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
@@ -343,13 +363,13 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
           hipLaunchKernelGGL(
               (nd_col_mul_kernel<LOGF, TGT, decltype(half)::value, decltype(ramp)::value, decltype(pack)::value>),
               grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B),
-              int(p.H), int(p.kb != 1), p.S[0], p.o[0], rf, jbase, bsplit, tw);
+              int(p.H), int(p.kb != 1), p.S[0], p.wm[0], p.o[0], rf, jbase, bsplit, tw);
         };
         p.pack ? launch(std::true_type{}) : launch(std::false_type{});
       };
       using T_ = std::true_type;
       using F_ = std::false_type;
-      if (2 * p.S[0] <= p.F[0])  // the x columns are at least half zero padding
+      if (2 * p.S[0] <= p.F[0] && p.wm[0] == -1)  // the x columns are at least half zero padding
         p.ramp ? go(T_{}, T_{}) : go(T_{}, F_{});
       else
         p.ramp ? go(F_{}, T_{}) : go(F_{}, F_{});
@@ -371,9 +391,9 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
   float2* wsq = wsk + NK * p.spec;
   if (!fwd_state) {
     if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-    if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], wsx, tw, st)) return false;
+    if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st)) return false;
   }
-  if (!inner_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], wsg, tw, st)) return false;
+  if (!inner_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], true, wsg, tw, st)) return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
   const int nz = bwd_batch_split(p);  // partial Q blocks follow Q in the workspace
@@ -385,11 +405,11 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
       auto go = [&](auto half, auto pack) {
         hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, decltype(half)::value, decltype(pack)::value>), grid,
                            dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg, (const float2*)wsx, (const float2*)wsk, wsq,
-                           cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.K[0], rp, jbase, NK, tw);
+                           cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.wm[0], p.K[0], rp, jbase, NK, tw);
       };
       using T_ = std::true_type;
       using F_ = std::false_type;
-      if (2 * p.S[0] <= p.F[0])  // the g and x columns are at least half zero padding
+      if (2 * p.S[0] <= p.F[0] && p.wm[0] == -1)  // the g and x columns are at least half zero padding
         p.pack ? go(T_{}, T_{}) : go(T_{}, F_{});
       else
         p.pack ? go(F_{}, T_{}) : go(F_{}, F_{});
@@ -405,7 +425,7 @@ static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const floa
   const float scale = 1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2));
   RowInvOut og{gx, g, s, nullptr, int(p.H), 0, p.S[2], 0, 0, 0, scale};
   if (!inner_inv<DT, ND_OUT_Y>(p, wsg, BH, p.S[0], 0, p.S[1], og, tw, st)) return false;
-  RowInvOut ok_{gk, nullptr, nullptr, gs, int(p.H), 0, p.K[2], p.c[0], p.c[1], p.c[2], scale};
+  RowInvOut ok_{gk, nullptr, nullptr, gs, int(p.H), 0, p.K[2], p.c[0], p.c[1], p.c[2], scale * p.gk_scale};
   return inner_inv<NSQ_DTYPE_F32, ND_OUT_GK>(p, wsq, NK, p.K[0], 0, p.K[1], ok_, tw, st);
 }
 
@@ -423,9 +443,9 @@ static int validate_nd(int nd, const void* a, const void* b, const float* k, int
       NSQ_CHECK_ARG(S[d] >= 1 && K[d] >= 1 && K[d] <= S[d],
                     "fftconv_nd: periodic axis %d: kernel size %lld must be in [1, %lld]", d, (long long)K[d],
                     (long long)S[d]);
-      if (S[d] < 16 || S[d] > (1 << kNdMaxLogF) || (S[d] & (S[d] - 1))) {
+      if (S[d] > (1 << kNdMaxLogF) || (S[d] & (S[d] - 1))) {
         set_error("fftconv_nd: unsupported shape: periodic axis %d has length %lld; the HIP kernels take periodic "
-                  "lengths that are powers of two in [16, %d]",
+                  "lengths that are powers of two up to %d",
                   d, (long long)S[d], 1 << kNdMaxLogF);
         return NSQ_ERR_UNSUPPORTED;
       }

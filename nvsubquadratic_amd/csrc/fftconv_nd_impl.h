@@ -70,10 +70,13 @@ struct RowGeom {
 // HALF: len <= N (at least half of each row is zero padding): the first pass
 // folds the zero half (HalfZeroLoad).  PACK (2D spectra): N bins per row, the
 // real DC and Nyquist values packed in bin 0 as U[0] + i U[N] (see
-// pack_split); otherwise N + 1 bins.
+// pack_split); otherwise N + 1 bins.  wm: sample index mask, -1, or len - 1
+// for a periodic row of a power-of-two length len < F2 read as its periodic
+// extension (sample i of the transform is row[i & wm]).
 template <int LOGN, int DT, bool AL, bool HALF = false, bool PACK = false>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typename Elem<DT>::T* __restrict__ src,
-                                                                        int len, RowGeom rg, float2* __restrict__ ws,
+                                                                        int len, int wm, RowGeom rg,
+                                                                        float2* __restrict__ ws,
                                                                         const float2* __restrict__ tw) {
   using C = RowNdCfg<LOGN>;
   __shared__ float2 lds[C::M * C::SP];
@@ -88,7 +91,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typ
   auto ld = [&](int m, int n) -> float2 {
     const int64_t r = r0 + m;
     const bool rok = r < rg.rows;  // tail rows read row 0 and select zero
-    return load_pair_nb<DT, AL>(src + (rok ? r : 0) * len, 2 * int64_t(n), rok ? len : 0);
+    return load_pair_nb<DT, AL>(src + (rok ? r : 0) * len, (2 * int64_t(n)) & wm, rok ? len : 0);
   };
   HalfZeroLoad<(LOGN < 4 ? (1 << LOGN) : 16), HALF, decltype(ld)> ld1{ld};
   LdsTile<C::SP, true> st{lds};
@@ -293,8 +296,8 @@ struct PlaneCfg {
 // padding): both first passes fold the zero half (HalfZeroLoad).
 template <int LOGN, int LOGF1, int DT, bool AL, bool HALF = false>
 __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<DT>::T* __restrict__ src, int n0,
-                                                           int n1, int len, float2* __restrict__ ws, int64_t spec,
-                                                           const float2* __restrict__ tw) {
+                                                           int n1, int len, int wm1, int wm2, float2* __restrict__ ws,
+                                                           int64_t spec, const float2* __restrict__ tw) {
   using C = PlaneCfg<LOGN, LOGF1>;
   static_assert(C::OK, "nd_plane_fwd_kernel: plane does not fit");
   constexpr int N = C::N, RS = C::RS;
@@ -307,7 +310,7 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
     auto ld = [&](int m, int n) -> float2 {
       const int a1 = r0 + m;
       const bool ok = a1 < n1;
-      return load_pair_nb<DT, AL>(xs + int64_t(ok ? a1 : 0) * len, 2 * int64_t(n), ok ? len : 0);
+      return load_pair_nb<DT, AL>(xs + int64_t(ok ? a1 : 0) * len, (2 * int64_t(n)) & wm2, ok ? len : 0);
     };
     HalfZeroLoad<16, HALF, decltype(ld)> ld1{ld};  // LOGN >= 4: radix-16 first pass
     fft_rec<LOGN, 0, false, C::MR, C::T, false>(ld1, rows, rows, rows, tw);
@@ -330,6 +333,7 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
   for (int j0 = 0; j0 < N; j0 += C::MC) {
     LdsCols<RS> cols{P, j0};
     auto ld = [&](int m, int n) -> float2 {
+      n &= wm1;  // periodic extension of a short axis 1
       const bool ok = n < n1;
       const float2 v = P[(ok ? n : 0) * RS + pad16(j0 + m)];
       return make_float2(ok ? v.x : 0.f, ok ? v.y : 0.f);
@@ -516,18 +520,23 @@ struct ColBuf {
   }
 };
 
-// Generic pass: reads elements [0, in_cnt) (rest zero), transforms, writes
+// Generic pass: reads elements [0, in_cnt) (rest zero; element n is read at
+// n & wm, wm = -1 or the mask of a short periodic axis), transforms, writes
 // outputs [out_off, out_off + out_cnt) to positions [0, out_cnt).
 // grid = (n_outer, ceil(inner_count / M)).
 template <int LOGF, bool INV, int TARGET = 8192>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_kernel(float2* __restrict__ ws, ColGeom cg,
-                                                                            int in_cnt, int out_off, int out_cnt,
-                                                                            int jbase, const float2* __restrict__ tw) {
+                                                                            int in_cnt, int wm, int out_off,
+                                                                            int out_cnt, int jbase,
+                                                                            const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
   __shared__ float2 lds[C::M * C::S];
   const ColBuf cb(ws + col_base(cg, blockIdx.x), cg);
   const int j0 = jbase + blockIdx.y * C::M;
-  auto ld = [&](int m, int n) -> float2 { return cb.load(n, j0 + m, j0 + m < cg.inner_count && n < in_cnt); };
+  auto ld = [&](int m, int n) -> float2 {
+    n &= wm;
+    return cb.load(n, j0 + m, j0 + m < cg.inner_count && n < in_cnt);
+  };
   auto st = [&](int m, int k, float2 v) {
     const int e = k - out_off;
     cb.store(e, j0 + m, j0 + m < cg.inner_count && uint32_t(e) < uint32_t(out_cnt), v);
@@ -607,14 +616,16 @@ __device__ __forceinline__ void pack_filter(bool pc0, int kf, int step, float2* 
 // are loaded and the first pass's butterflies fold the zeros away.  RAMP
 // (periodic axes): the filter values are multiplied by conj(R), R the shift
 // ramp of `rf`, as they are loaded, which rolls the output by -c_d along
-// every axis (the circular "same" alignment; c0 is then 0).  PACK (2D): the
+// every axis (the circular "same" alignment; c0 is then 0).  wm0: row index
+// mask of the x columns (-1, or S0 - 1 for a short periodic axis 0 read as
+// its periodic extension).  PACK (2D): the
 // inner index j = 0 is the packed DC / Nyquist column (pack_split).
 template <int LOGF, int TARGET = 8192, bool HALF = false, bool RAMP = false, bool PACK = false>
 __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
                                                                                 const float2* __restrict__ wsk,
                                                                                 ColGeom cg, int B, int H, int kfilm,
-                                                                                int S0, int c0, Ramp rf, int jbase,
-                                                                                int bsplit,
+                                                                                int S0, int wm0, int c0, Ramp rf,
+                                                                                int jbase, int bsplit,
                                                                                 const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
   constexpr int R = 1 << (LOGF < 4 ? LOGF : 4);  // first-pass radix, as chosen by fft_rec
@@ -669,7 +680,10 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel
   auto issue = [&](int bi) {
     const ColBuf in(wsx + block(bi), cg);
 #pragma unroll
-    for (int r = 0; r < RL; ++r) raw[r] = in.load(j1 + r * NR, j0 + m1, colok && j1 + r * NR < S0);
+    for (int r = 0; r < RL; ++r) {
+      const int n = (j1 + r * NR) & wm0;
+      raw[r] = in.load(n, j0 + m1, colok && n < S0);
+    }
   };
   if (b_begin < b_end) issue(b_begin);
   for (int bi = b_begin; bi < b_end; ++bi) {
@@ -729,7 +743,7 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
                                                                                 const float2* __restrict__ wsk,
                                                                                 float2* __restrict__ wsq, ColGeom cg,
                                                                                 int B, int H, int kfilm, int S0,
-                                                                                int K0, Ramp rp, int jbase,
+                                                                                int wm0, int K0, Ramp rp, int jbase,
                                                                                 int64_t qsplit,
                                                                                 const float2* __restrict__ tw) {
   using C = ColNdCfg<LOGF, TARGET>;
@@ -776,8 +790,14 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
     const int64_t bh = kfilm ? hk : (int64_t(bi) * H + hk);
     const ColBuf gb(wsg + bh * cg.spec, cg);
     const ColBuf xb(wsx + bh * cg.spec, cg);
-    auto ldg = [&](int mm, int n) -> float2 { return gb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0); };
-    auto ldx = [&](int mm, int n) -> float2 { return xb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0); };
+    auto ldg = [&](int mm, int n) -> float2 {
+      n &= wm0;
+      return gb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0);
+    };
+    auto ldx = [&](int mm, int n) -> float2 {
+      n &= wm0;
+      return xb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0);
+    };
     LdsTile<C::S, false> stG{ldsG};
     LdsTile<C::S, false> stX{ldsX};
     constexpr int R1 = 1 << (LOGF < 4 ? LOGF : 4);  // first-pass radix

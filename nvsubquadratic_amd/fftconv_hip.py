@@ -327,7 +327,7 @@ def fftconv_nd_fwd_raw(x, k, s, y, kbatch: int, workspace: torch.Tensor | None =
     if need == 0:
         raise NotImplementedError(
             f"fft_backend='hip' {nd}D: unsupported shape x={tuple(x.shape)} k={tuple(k.shape)} periodic={periodic:#x} "
-            f"(periodic axes need a power-of-two length in [16, 1024] and K <= S; zero-padded axes an FFT length "
+            f"(periodic axes need a power-of-two length <= 1024 and K <= S; zero-padded axes an FFT length "
             f"<= 1024)")
     if workspace is None or workspace.numel() < need:
         workspace = _workspace(x.device, need)

@@ -120,7 +120,10 @@ def test_periodic_lengths_validated_before_launch():
     assert rc == 1
     rc = lib.nsq_mixed_fftconv_nd_fwd(2, dummy, dummy, None, dummy, f32, 1, 1, S, K, 1, 0b100, dummy, 1 << 40, None)
     assert rc == 1 and b"periodic mask" in lib.nsq_last_error()
-    S, K = _lib.i64_array([12, 16]), _lib.i64_array([3, 16])
+    S, K = _lib.i64_array([12, 64]), _lib.i64_array([3, 64])
     spec_zero = lib.nsq_fftconv_nd_workspace_bytes(2, 1, 1, S, K, 1, 0)
     spec_mixed = lib.nsq_mixed_fftconv_nd_workspace_bytes(2, 1, 1, S, K, 1, 0b10, 0)
-    assert 0 < spec_mixed < spec_zero  # the periodic axis is not padded: F1 = 16 instead of 32
+    assert 0 < 2 * spec_mixed == spec_zero  # the periodic axis is not padded: F1 = 64 instead of 128
+    # short periods run on their periodic extension at length 16 (accepted, not refused)
+    S, K = _lib.i64_array([8, 4]), _lib.i64_array([3, 4])
+    assert lib.nsq_mixed_fftconv_nd_workspace_bytes(2, 1, 1, S, K, 1, 0b11, 0) > 0

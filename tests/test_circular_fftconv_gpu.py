@@ -4,9 +4,11 @@ Mirrors tests/ops/test_circular_fftconv.py (1D/2D/3D vs the spatial reference,
 shortcut, dtype preservation, BLH layout, batched kernel, backward) and
 tests/ops/test_mixed_fftconv.py (every per-axis combination, uniform cases
 routed to the zero-padded / circular ops, chunked, impulse and DC responses,
-backward).  Periodic lengths are powers of two >= 16 (the HIP kernels' range):
-the reference's 8- and 12-point and 48-point periodic cases are replaced by
-16- and 64-point ones, and the unsupported sizes are checked to raise.
+backward).  Periodic lengths are powers of two (the HIP kernels' range; below
+16 points on the periodic extension at FFT length 16, covered by the reference's
+own 8-point shapes and 1/2/4-point ones): the reference's 12- and 48-point
+periodic cases are replaced by 16- and 64-point ones, and non-power-of-two
+sizes are checked to raise.
 Tolerances: rel-L2 <= 1e-4 fp32, <= 2e-2 bf16 / fp16 I/O.
 """
 
@@ -60,11 +62,12 @@ def _circ64(x, k, s=None):
 
 # --- circular: forward vs the float64 brute force ---------------------------
 CIRC_1D = [(2, 16, 64, 7), (2, 32, 128, 32), (1, 8, 256, 256), (4, 16, 64, 15), (2, 8, 16, 1), (1, 4, 16384, 100),
-           (3, 5, 1024, 4)]
+           (3, 5, 1024, 4), (2, 3, 8, 8), (2, 3, 8, 3), (1, 2, 4, 4), (1, 2, 2, 2), (2, 2, 1, 1)]
 CIRC_2D = [(2, 8, 32, 32, 7, 7), (2, 16, 64, 64, 15, 15), (1, 8, 32, 32, 32, 32), (4, 8, 16, 16, 5, 5),
-           (1, 4, 16, 128, 4, 9), (2, 3, 256, 32, 1, 32)]
+           (1, 4, 16, 128, 4, 9), (2, 3, 256, 32, 1, 32), (4, 6, 8, 8, 5, 5), (2, 3, 8, 8, 8, 8), (1, 2, 2, 64, 2, 7),
+           (2, 2, 16, 4, 6, 3), (1, 2, 1, 16, 1, 5)]
 CIRC_3D = [(2, 4, 16, 16, 16, 5, 5, 5), (1, 8, 16, 16, 16, 3, 3, 3), (2, 4, 16, 16, 16, 16, 16, 16),
-           (1, 2, 32, 16, 64, 4, 7, 2)]
+           (1, 2, 32, 16, 64, 4, 7, 2), (1, 4, 8, 8, 8, 3, 3, 3), (2, 3, 8, 8, 8, 8, 8, 8), (1, 2, 4, 16, 2, 3, 5, 2)]
 
 
 @pytest.mark.parametrize("B,H,L,K", CIRC_1D)
@@ -100,12 +103,15 @@ def test_circular_3d_vs_brute_force(B, H, X, Y, Z, Kx, Ky, Kz):
 # --- circular: backward, shortcut, FiLM, dtypes -----------------------------
 @pytest.mark.parametrize("xs,ks", [((2, 8, 64), (15,)), ((1, 16, 128), (7,)), ((2, 4, 4096), (4096,)),
                                    ((2, 4, 16, 16), (5, 5)), ((1, 8, 32, 32), (7, 7)), ((2, 3, 64, 16), (6, 16)),
-                                   ((2, 4, 16, 16, 16), (5, 5, 5)), ((1, 2, 16, 32, 16), (4, 1, 16))])
+                                   ((2, 4, 16, 16, 16), (5, 5, 5)), ((1, 2, 16, 32, 16), (4, 1, 16)),
+                                   ((2, 3, 8), (5,)), ((2, 4, 8, 8), (5, 4)), ((2, 3, 8, 8, 8), (3, 3, 3)),
+                                   ((1, 4, 8, 8, 8), (3, 3, 3)), ((2, 2, 4, 32), (3, 9))])
 def test_circular_fwd_bwd_vs_oracle(xs, ks):
     _fwd_bwd_check(xs, ks, CIRC_FNS[len(xs) - 2], _circ64)
 
 
-@pytest.mark.parametrize("xs,ks", [((3, 8, 256), (9,)), ((2, 4, 32, 32), (5, 6)), ((2, 2, 16, 16, 32), (3, 4, 5))])
+@pytest.mark.parametrize("xs,ks", [((3, 8, 256), (9,)), ((2, 4, 32, 32), (5, 6)), ((2, 2, 16, 16, 32), (3, 4, 5)),
+                                   ((3, 2, 8), (4,)), ((2, 3, 8, 8, 8), (5, 4, 3))])
 def test_circular_film_per_sample_kernel(xs, ks):
     _fwd_bwd_check(xs, ks, CIRC_FNS[len(xs) - 2], _circ64, kb=xs[0])
 
@@ -153,8 +159,8 @@ def test_circular_rejects_mismatched_shortcut_dtype():
         C.circular_fftconv1d_fp32_bhl(x, k, torch.randn(4, device="cuda", dtype=torch.bfloat16))
 
 
-@pytest.mark.parametrize("xs,ks", [((1, 4, 48), (5,)), ((1, 4, 8), (3,)), ((1, 2, 12, 16), (3, 3)),
-                                   ((1, 2, 16, 16, 8), (3, 3, 3)), ((1, 2, 32768), (5,))])
+@pytest.mark.parametrize("xs,ks", [((1, 4, 48), (5,)), ((1, 4, 12), (3,)), ((1, 2, 12, 16), (3, 3)),
+                                   ((1, 2, 16, 16, 24), (3, 3, 3)), ((1, 2, 32768), (5,)), ((1, 2, 2048, 16), (3, 3))])
 def test_circular_unsupported_lengths_raise(xs, ks):
     """Non-power-of-two or out-of-range periodic lengths are refused, not approximated."""
     x = torch.randn(*xs, device="cuda")
@@ -182,7 +188,8 @@ def test_mixed_2d_vs_brute_force(periodic, B, H, X, Y, Kx, Ky):
 
 
 @pytest.mark.parametrize("periodic", COMBOS_3D)
-@pytest.mark.parametrize("B,H,X,Y,Z,Kx,Ky,Kz", [(2, 4, 16, 16, 16, 5, 5, 5), (1, 8, 16, 16, 32, 7, 7, 5)])
+@pytest.mark.parametrize("B,H,X,Y,Z,Kx,Ky,Kz", [(2, 4, 16, 16, 16, 5, 5, 5), (1, 8, 16, 16, 32, 7, 7, 5),
+                                                (1, 4, 8, 8, 8, 5, 5, 5)])
 def test_mixed_3d_vs_brute_force(periodic, B, H, X, Y, Z, Kx, Ky, Kz):
     rng = np.random.default_rng(X + Kx + Z)
     x = rng.standard_normal((B, H, X, Y, Z)).astype(np.float32)
@@ -237,8 +244,9 @@ def test_mixed_chunked_and_w_reshape_bitwise(periodic):
 
 @pytest.mark.parametrize("periodic", COMBOS_3D)
 def test_mixed_impulse_response_3d(periodic):
+    """tests/ops/test_mixed_fftconv.py:666-676 (8^3, K = 3 x 5 x 4)."""
     torch.manual_seed(0)
-    x = torch.zeros(1, 2, 16, 16, 16, device="cuda")
+    x = torch.zeros(1, 2, 8, 8, 8, device="cuda")
     x[..., 0, 0, 0] = 1.0
     k = torch.randn(1, 2, 3, 5, 4, device="cuda")
     y = M.mixed_fftconv3d_fp32_bhl(x, k, periodic)
@@ -250,3 +258,20 @@ def test_mixed_periodic_kernel_larger_than_axis_rejected():
     x = torch.randn(1, 2, 16, 16, device="cuda")
     with pytest.raises(AssertionError):
         M.mixed_fftconv2d_fp32_bhl(x, torch.randn(1, 2, 17, 3, device="cuda"), (True, False))
+
+
+@pytest.mark.parametrize("periodic", [(True, False), (False, True)])
+def test_mixed_2d_short_periodic_fwd_bwd(periodic):
+    """gray_scott / MHD-like token grids: an 8-point periodic axis beside a zero-padded one."""
+    xs = (2, 4, 8, 16) if periodic[0] else (2, 4, 16, 8)
+    ks = (5, 31) if periodic[0] else (31, 8)
+    _fwd_bwd_check(xs, ks, lambda x, k, s: M.mixed_fftconv2d_fp32_bhl(x, k, periodic, s),
+                   lambda x, k, s: mixed_fftconv_torch(x, k, periodic, s, compute_dtype=torch.float64))
+
+
+def test_dc_response_all_periodic_3d_short():
+    """tests/ops/test_mixed_fftconv.py:697: constant input -> sum(kernel) everywhere (8^3)."""
+    torch.manual_seed(0)
+    k = torch.randn(1, 2, 5, 5, 5, device="cuda")
+    y = M.mixed_fftconv3d_fp32_bhl(torch.ones(1, 2, 8, 8, 8, device="cuda"), k, (True, True, True))
+    torch.testing.assert_close(y, k.sum(dim=(-1, -2, -3)).view(1, 2, 1, 1, 1).expand_as(y), rtol=1e-5, atol=1e-5)
