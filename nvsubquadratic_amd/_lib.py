@@ -66,6 +66,19 @@ _SIGNATURES = {
             _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_int, _c_void_p,
         ],
     ),
+    "nsq_fftconv1d_causal_film_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "nsq_fftconv1d_causal_film_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p,
+         _c_size, _c_void_p],
+    ),
+    "nsq_fftconv1d_causal_film_bwd": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_int, _c_void_p,
+        ],
+    ),
     "nsq_circular_fftconv1d_fwd": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p],

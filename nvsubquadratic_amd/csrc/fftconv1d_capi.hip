@@ -6,7 +6,9 @@
 namespace nsq {
 
 static int validate(const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H, int64_t L,
-                    int64_t K, Plan1D& p) {
+                    int64_t K, int64_t kbatch, Plan1D& p) {
+  NSQ_CHECK_ARG(kbatch == 1 || kbatch == B, "fftconv1d_causal: kernel batch must be 1 or B (got %lld, B=%lld)",
+                (long long)kbatch, (long long)B);
   NSQ_CHECK_ARG(a && b && k, "fftconv1d_causal: null tensor pointer");
   NSQ_CHECK_ARG(valid_dtype(dtype), "fftconv1d_causal: unsupported dtype code %d", dtype);
   NSQ_CHECK_ARG(B >= 1 && H >= 1 && L >= 1 && K >= 1, "fftconv1d_causal: sizes must be positive (B=%lld H=%lld L=%lld K=%lld)",
@@ -19,9 +21,12 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
               (long long)L, (long long)K);
     return NSQ_ERR_UNSUPPORTED;
   }
-  // 4-step column grids are B*H * (N2 / columns per workgroup) <= B*H * 512.
-  NSQ_CHECK_ARG(p.fused || B * H <= (int64_t(1) << 22), "fftconv1d_causal: B*H=%lld too large for the 4-step plan",
-                (long long)(B * H));
+  // 4-step column grids are B*H * (N2 / columns per workgroup) <= B*H * 512; per-sample filters run the
+  // row passes over B*H channels, B*H * N1/2 <= B*H * 512 workgroups.
+  NSQ_CHECK_ARG(p.fused || B * H < (int64_t(1) << 22) + (kbatch == 1 ? 1 : 0),
+                "fftconv1d_causal: B*H=%lld too large for the 4-step plan", (long long)(B * H));
+  NSQ_CHECK_ARG(!p.fused || kbatch == 1 || B <= 65535, "fftconv1d_causal: B=%lld too large for per-sample filters",
+                (long long)B);
   return NSQ_OK;
 }
 
@@ -47,25 +52,20 @@ static int validate_circ(const void* a, const void* b, const float* k, int dtype
   return NSQ_OK;
 }
 
-}  // namespace nsq
-
-using namespace nsq;
-
-extern "C" {
-
-size_t nsq_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int direction) {
+static size_t causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, int direction) {
   Plan1D p;
   if (!make_plan(L, K, p) || p.fused) return 0;
   const int64_t N = int64_t(1) << p.logN;
-  const int64_t rows = (direction == NSQ_DIR_BWD) ? (2 * B * H + H) : (B * H + H);
+  const int64_t nk = kbatch * H;
+  const int64_t rows = (direction == NSQ_DIR_BWD) ? (2 * B * H + nk) : (B * H + nk);
   return size_t(rows * N) * sizeof(float2);
 }
 
-int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
-                             int64_t H, int64_t L, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+static int causal_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B, int64_t H,
+                      int64_t L, int64_t K, int64_t kbatch, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   Plan1D p;
-  int rc = validate(x, y, k, dtype, B, H, L, K, p);
+  int rc = validate(x, y, k, dtype, B, H, L, K, kbatch, p);
   if (rc) return rc;
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
@@ -73,22 +73,23 @@ int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut
   float2* ws = nullptr;
   bool save = false;
   if (!p.fused) {
-    const size_t need = nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, NSQ_DIR_FWD);
+    const size_t need = causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_FWD);
     NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv1d_causal_fwd: workspace of %zu bytes required, got %zu",
                   need, workspace_bytes);
     ws = (float2*)workspace;
-    save = workspace_bytes >= nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, NSQ_DIR_BWD);
+    save = workspace_bytes >= causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD);
   }
+  const int kf = kbatch != 1;
   bool ok = false;
   switch (dtype) {
     case NSQ_DTYPE_F32:
-      ok = run_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, save, tw, st);
+      ok = run_fwd<NSQ_DTYPE_F32>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, ws, save, tw, st);
       break;
     case NSQ_DTYPE_BF16:
-      ok = run_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, save, tw, st);
+      ok = run_fwd<NSQ_DTYPE_BF16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, ws, save, tw, st);
       break;
     default:
-      ok = run_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), ws, save, tw, st);
+      ok = run_fwd<NSQ_DTYPE_F16>(p, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, ws, save, tw, st);
       break;
   }
   NSQ_CHECK_ARG(ok, "fftconv1d_causal_fwd: no kernel for logN=%d", p.logN);
@@ -96,12 +97,12 @@ int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut
   return NSQ_OK;
 }
 
-int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
-                             float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, void* workspace,
-                             size_t workspace_bytes, int fwd_state, void* stream) {
+static int causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                      float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, void* workspace,
+                      size_t workspace_bytes, int fwd_state, void* stream) {
   clear_error();
   Plan1D p;
-  int rc = validate(g, x, k, dtype, B, H, L, K, p);
+  int rc = validate(g, x, k, dtype, B, H, L, K, kbatch, p);
   if (rc) return rc;
   NSQ_CHECK_ARG(gx && gk, "fftconv1d_causal_bwd: null gradient output pointer");
   NSQ_CHECK_ARG(!shortcut || gs, "fftconv1d_causal_bwd: gs required when a shortcut is given");
@@ -110,26 +111,68 @@ int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const
   hipStream_t st = (hipStream_t)stream;
   float2* ws = nullptr;
   if (!p.fused) {
-    const size_t need = nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, NSQ_DIR_BWD);
+    const size_t need = causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD);
     NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv1d_causal_bwd: workspace of %zu bytes required, got %zu",
                   need, workspace_bytes);
     ws = (float2*)workspace;
   }
+  const int kf = kbatch != 1;
+  const bool fs = fwd_state != 0;
   bool ok = false;
   switch (dtype) {
     case NSQ_DTYPE_F32:
-      ok = run_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, fwd_state != 0, tw, st);
+      ok = run_bwd<NSQ_DTYPE_F32>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, ws, fs, tw, st);
       break;
     case NSQ_DTYPE_BF16:
-      ok = run_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, fwd_state != 0, tw, st);
+      ok = run_bwd<NSQ_DTYPE_BF16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, ws, fs, tw, st);
       break;
     default:
-      ok = run_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), ws, fwd_state != 0, tw, st);
+      ok = run_bwd<NSQ_DTYPE_F16>(p, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, ws, fs, tw, st);
       break;
   }
   NSQ_CHECK_ARG(ok, "fftconv1d_causal_bwd: no kernel for logN=%d", p.logN);
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
+}
+
+}  // namespace nsq
+
+using namespace nsq;
+
+extern "C" {
+
+size_t nsq_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int direction) {
+  return causal_workspace_bytes(B, H, L, K, 1, direction);
+}
+
+int nsq_fftconv1d_causal_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                             int64_t H, int64_t L, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+  return causal_fwd(x, k, shortcut, y, dtype, B, H, L, K, 1, workspace, workspace_bytes, stream);
+}
+
+int nsq_fftconv1d_causal_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                             float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, void* workspace,
+                             size_t workspace_bytes, int fwd_state, void* stream) {
+  return causal_bwd(g, x, k, shortcut, gx, gk, gs, dtype, B, H, L, K, 1, workspace, workspace_bytes, fwd_state, stream);
+}
+
+size_t nsq_fftconv1d_causal_film_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                                                 int direction) {
+  return causal_workspace_bytes(B, H, L, K, kbatch, direction);
+}
+
+int nsq_fftconv1d_causal_film_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                                  int64_t H, int64_t L, int64_t K, int64_t kbatch, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  return causal_fwd(x, k, shortcut, y, dtype, B, H, L, K, kbatch, workspace, workspace_bytes, stream);
+}
+
+int nsq_fftconv1d_causal_film_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
+                                  float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
+                                  int64_t kbatch, void* workspace, size_t workspace_bytes, int fwd_state,
+                                  void* stream) {
+  return causal_bwd(g, x, k, shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, workspace, workspace_bytes, fwd_state,
+                    stream);
 }
 
 int nsq_circular_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,

@@ -817,37 +817,39 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
 // ===========================================================================
 // Host launchers
 // ===========================================================================
+// kfilm: per-sample filters [B*H, K]; one image per workgroup.
 template <int LOGN, int DT>
 static void launch_fused_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void* y, int B, int H,
-                             int L, int K, const float2* tw, hipStream_t st) {
+                             int L, int K, int kfilm, const float2* tw, hipStream_t st) {
   using C = FusedCfg<LOGN>;
   using ET = typename Elem<DT>::T;
   const int gh = int(ceil_div(H, C::M));
   int nb = int(ceil_div(2048, gh));
   nb = nb < 1 ? 1 : (nb > B ? B : nb);
-  const int bpw = int(ceil_div(B, nb));
+  const int bpw = kfilm ? 1 : int(ceil_div(B, nb));
   nb = int(ceil_div(B, bpw));
   dim3 grid(gh, nb);
   if (p.fold)
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw, 0, 0, -1);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1);
   else
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw, 0, 0, -1);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1);
 }
 
 template <int LOGN, int DT>
 static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, const float* k, const void* s, void* gx,
-                             float* gk, float* gs, int B, int H, int L, int K, const float2* tw, hipStream_t st) {
+                             float* gk, float* gs, int B, int H, int L, int K, int kfilm, const float2* tw,
+                             hipStream_t st) {
   using C = FusedCfg<LOGN>;
   using ET = typename Elem<DT>::T;
-  dim3 grid(int(ceil_div(H, C::M)));
+  dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
   if (p.fold)
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0, -1, 1.f);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f);
   else
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, 0, -1, 1.f);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f);
 }
 
 // Circular 1D (fused plan at FFT length L = 2N): shift c = (K-1)/2; kfilm =
@@ -883,11 +885,15 @@ static void launch_circ_bwd(const void* g, const void* x, const float* k, const 
                      wm == -1 ? 1.f : float(L) / float(2 * C::N));
 }
 
-// Workspace layout of the 4-step plan (rows of N complex64):
-//   [0, BH)          column-transformed x  (X')
-//   [BH, BH+H)       column-transformed k  (K')
-//   [BH+H, 2BH+H)    forward: inverse-row product (Y') when `save`; backward: G'
+// Workspace layout of the 4-step plan (rows of N complex64; NK = H, or B*H for
+// per-sample filters):
+//   [0, BH)            column-transformed x  (X')
+//   [BH, BH+NK)        column-transformed k  (K')
+//   [BH+NK, 2BH+NK)    forward: inverse-row product (Y') when `save`; backward: G'
 // With `save`, X' and K' survive the forward so the backward can reuse them.
+// Per-sample filters run the row passes as one image of B*H channels (every
+// row then has its own filter row); the epilogues still index the shortcut by
+// row % H.
 // Column-pass launches; `al` selects the aligned-pair row access.
 template <int LOGN1, int LOGN, int DT>
 static void launch_col_fwd(RealRows<DT> src, int64_t rows, float2* out, const float2* tw, hipStream_t st) {
@@ -933,43 +939,47 @@ static void launch_col_inv_gk(const float2* ws, float* gk, float* gs, int H, int
 
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
-                             float2* ws, bool save, const float2* tw, hipStream_t st) {
+                             int kfilm, float2* ws, bool save, const float2* tw, hipStream_t st) {
   constexpr int LOGN = LOGN1 + LOGN2;
   constexpr int64_t N = int64_t(1) << LOGN;
   using ET = typename Elem<DT>::T;
+  const int64_t BH = int64_t(B) * H, NK = kfilm ? BH : H;
+  const int rb = kfilm ? 1 : B, rh = kfilm ? int(BH) : H;  // row-pass images and channels
   float2* wsx = ws;
-  float2* wsk = ws + int64_t(B) * H * N;
-  float2* wsy = save ? ws + (int64_t(B) * H + H) * N : wsx;
-  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, int64_t(B) * H, wsx, tw, st);
-  launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, H, wsk, tw, st);
-  hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st,
-                     (const float2*)wsx, (const float2*)wsk, wsy, B, H, tw);
-  launch_col_inv_out<LOGN1, LOGN, DT>(wsy, x, s, y, int64_t(B) * H, H, L, tw, st);
+  float2* wsk = ws + BH * N;
+  float2* wsy = save ? ws + (BH + NK) * N : wsx;
+  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
+  launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
+  hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T),
+                     0, st, (const float2*)wsx, (const float2*)wsk, wsy, rb, rh, tw);
+  launch_col_inv_out<LOGN1, LOGN, DT>(wsy, x, s, y, BH, H, L, tw, st);
 }
 
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_bwd(const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
-                             float* gs, int B, int H, int L, int K, float2* ws, bool fwd_state, const float2* tw,
-                             hipStream_t st) {
+                             float* gs, int B, int H, int L, int K, int kfilm, float2* ws, bool fwd_state,
+                             const float2* tw, hipStream_t st) {
   constexpr int LOGN = LOGN1 + LOGN2;
   constexpr int64_t N = int64_t(1) << LOGN;
   using ET = typename Elem<DT>::T;
+  const int64_t BH = int64_t(B) * H, NK = kfilm ? BH : H;
+  const int rb = kfilm ? 1 : B, rh = kfilm ? int(BH) : H;  // row-pass images and channels
   float2* wsx = ws;
-  float2* wsk = ws + int64_t(B) * H * N;
-  float2* wsg = ws + (int64_t(B) * H + H) * N;
-  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)g, L, L}, int64_t(B) * H, wsg, tw, st);
+  float2* wsk = ws + BH * N;
+  float2* wsg = ws + (BH + NK) * N;
+  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)g, L, L}, BH, wsg, tw, st);
   if (!fwd_state) {
-    launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, int64_t(B) * H, wsx, tw, st);
-    launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, H, wsk, tw, st);
+    launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
+    launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
   }
-  if (B == 1)
-    hipLaunchKernelGGL((row_bwd1_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st,
-                       wsg, (const float2*)wsx, wsk, H, tw);
+  if (rb == 1)
+    hipLaunchKernelGGL((row_bwd1_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)),
+                       dim3(RowCfg<LOGN2>::T), 0, st, wsg, (const float2*)wsx, wsk, rh, tw);
   else
-    hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(H * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T), 0, st,
-                       wsg, (const float2*)wsx, wsk, B, H, tw);
-  launch_col_inv_out<LOGN1, LOGN, DT>(wsg, g, s, gx, int64_t(B) * H, H, L, tw, st);
-  launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, gs, H, K, tw, st);
+    hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)),
+                       dim3(RowCfg<LOGN2>::T), 0, st, wsg, (const float2*)wsx, wsk, rb, rh, tw);
+  launch_col_inv_out<LOGN1, LOGN, DT>(wsg, g, s, gx, BH, H, L, tw, st);
+  launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, gs, int(NK), K, tw, st);
 }
 
 // Runtime -> compile-time dispatch helpers.
@@ -1041,19 +1051,24 @@ struct FourStep {
 
 // Per-dtype entry used by the C ABI; explicitly instantiated once per dtype in
 // fftconv1d_<dtype>.hip so the three instantiation sets compile in parallel.
+// kfilm: per-sample filters (k, gk: [B*H, K]; gs: [B*H] partials).
 template <int DT>
 bool run_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
-             float2* ws, bool save, const float2* tw, hipStream_t st) {
-  if (p.fused) return dispatch_int<FusedFwd<DT>::template At, 3, 13>(p.logN, p, x, k, s, y, B, H, L, K, tw, st);
-  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, ws, save, tw, st);
+             int kfilm, float2* ws, bool save, const float2* tw, hipStream_t st) {
+  if (p.fused)
+    return dispatch_int<FusedFwd<DT>::template At, 3, 13>(p.logN, p, x, k, s, y, B, H, L, K, kfilm, tw, st);
+  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, kfilm, ws, save, tw,
+                                                                 st);
 }
 
 template <int DT>
 bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
-             float* gs, int B, int H, int L, int K, float2* ws, bool fwd_state, const float2* tw, hipStream_t st) {
+             float* gs, int B, int H, int L, int K, int kfilm, float2* ws, bool fwd_state, const float2* tw,
+             hipStream_t st) {
   if (p.fused)
-    return dispatch_int<FusedBwd<DT>::template At, 3, 13>(p.logN, p, g, x, k, s, gx, gk, gs, B, H, L, K, tw, st);
-  return dispatch_int<FourStep<DT, true>::template At, 14, 22>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, ws,
+    return dispatch_int<FusedBwd<DT>::template At, 3, 13>(p.logN, p, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, tw,
+                                                          st);
+  return dispatch_int<FourStep<DT, true>::template At, 14, 22>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, ws,
                                                                 fwd_state, tw, st);
 }
 
@@ -1074,9 +1089,10 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
 
 #define NSQ_DECLARE_FFTCONV1D(DT)                                                                               \
   extern template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
-                                   int, float2*, bool, const float2*, hipStream_t);                             \
+                                   int, int, float2*, bool, const float2*, hipStream_t);                        \
   extern template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
-                                   float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t); \
+                                   float*, float*, int, int, int, int, int, float2*, bool, const float2*,       \
+                                   hipStream_t);                                                                \
   extern template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, \
                                         int, const float2*, hipStream_t);                                       \
   extern template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, \
@@ -1084,9 +1100,10 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
 
 #define NSQ_INSTANTIATE_FFTCONV1D(DT)                                                                    \
   template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
-                            int, float2*, bool, const float2*, hipStream_t);                             \
+                            int, int, float2*, bool, const float2*, hipStream_t);                        \
   template bool run_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,   \
-                            float*, float*, int, int, int, int, float2*, bool, const float2*, hipStream_t); \
+                            float*, float*, int, int, int, int, int, float2*, bool, const float2*,       \
+                            hipStream_t);                                                                \
   template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, int, \
                                  const float2*, hipStream_t);                                               \
   template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, float*, \

@@ -11,9 +11,10 @@ Semantics (reference ``nvsubquadratic/ops/fftconv_custom.py:307-335`` on top of
 
 * the op accepts any input dtype, computes in float32 and returns ``x.dtype``;
 * ``y = conv(x, kernel).to(x.dtype)``, then ``y = y + shortcut.to(x.dtype) * x``;
-* 1D kernels are shared: ``[1, H, K]`` or ``[H, K]``; per-sample ``[B, H, K]``
-  with ``B != 1`` raises ``NotImplementedError`` like the reference wrapper
-  (``fftconv_custom.py:294-300``).
+* 1D kernels: shared ``[1, H, K]`` / ``[H, K]``, or per-sample (FiLM)
+  ``[B, H, K]``.  The reference's native wrapper raises ``NotImplementedError``
+  for the latter (``fftconv_custom.py:294-300``); its torch path accepts it
+  (``fftconv.py:546-600``), and so does this backend, with that path's results.
 
 Differences in *how*: the whole chain (pad, real FFT, spectral product,
 inverse FFT, crop, cast and shortcut) runs inside hand-written HIP kernels
@@ -65,30 +66,39 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
+def _causal_workspace_bytes(lib, B, H, L, K, kbatch, direction):
+    if kbatch != 1:
+        return lib.nsq_fftconv1d_causal_film_workspace_bytes(B, H, L, K, kbatch, direction)
+    return lib.nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, direction)
+
+
 def causal_fftconv1d_fwd_raw(
     x: torch.Tensor,
     k: torch.Tensor,
     s: torch.Tensor | None,
     y: torch.Tensor,
     workspace: torch.Tensor | None = None,
+    kbatch: int = 1,
 ) -> torch.Tensor:
     """Launch the forward kernel on the current stream.
 
     ``x``/``y``: contiguous ``[B, H, L]`` (float32/bfloat16/float16, same dtype);
-    ``k``: contiguous float32 ``[H, K]``; ``s``: ``[H]`` in ``x.dtype`` or None.
+    ``k``: contiguous float32 ``[kbatch*H, K]`` (kbatch 1, or B for per-sample
+    filters); ``s``: ``[H]`` in ``x.dtype`` or None.
     """
     lib = _lib.get_lib()
     _lib.check_device(x)
     B, H, L = x.shape
     K = k.shape[-1]
-    need = lib.nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, _lib.NSQ_DIR_FWD)
+    need = _causal_workspace_bytes(lib, B, H, L, K, kbatch, _lib.NSQ_DIR_FWD)
     if need and (workspace is None or workspace.numel() < need):
         workspace = _workspace(x.device, need)
-    rc = lib.nsq_fftconv1d_causal_fwd(
-        x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype),
-        B, H, L, K, _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
-        _lib.stream_ptr(x.device),
-    )
+    args = (x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype), B, H, L, K)
+    tail = (_lib.ptr(workspace), 0 if workspace is None else workspace.numel(), _lib.stream_ptr(x.device))
+    if kbatch != 1:
+        rc = lib.nsq_fftconv1d_causal_film_fwd(*args, kbatch, *tail)
+    else:
+        rc = lib.nsq_fftconv1d_causal_fwd(*args, *tail)
     _lib.check(rc)
     return y
 
@@ -103,49 +113,55 @@ def causal_fftconv1d_bwd_raw(
     gs: torch.Tensor | None,
     workspace: torch.Tensor | None = None,
     fwd_state: bool = False,
+    kbatch: int = 1,
 ) -> None:
     """Launch the backward kernels on the current stream (see include/nsq_hip.h).
 
     ``fwd_state=True`` reuses the transformed x and k that a forward call left
     in ``workspace`` (a forward given a workspace of the backward's size keeps
-    them); the workspace must be untouched since that forward.
+    them); the workspace must be untouched since that forward.  Per-sample
+    filters (``kbatch = B``): gk ``[B*H, K]``, gs ``[B*H]`` partials.
     """
     lib = _lib.get_lib()
     _lib.check_device(x)
     B, H, L = x.shape
     K = k.shape[-1]
-    need = lib.nsq_fftconv1d_causal_workspace_bytes(B, H, L, K, _lib.NSQ_DIR_BWD)
+    need = _causal_workspace_bytes(lib, B, H, L, K, kbatch, _lib.NSQ_DIR_BWD)
     if need and (workspace is None or workspace.numel() < need):
         workspace = _workspace(x.device, need)
         fwd_state = False
-    rc = lib.nsq_fftconv1d_causal_bwd(
-        g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
-        _lib.dtype_code(x.dtype), B, H, L, K, _lib.ptr(workspace),
-        0 if workspace is None else workspace.numel(), int(bool(fwd_state)), _lib.stream_ptr(x.device),
-    )
+    args = (g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
+            _lib.dtype_code(x.dtype), B, H, L, K)
+    tail = (_lib.ptr(workspace), 0 if workspace is None else workspace.numel(), int(bool(fwd_state)),
+            _lib.stream_ptr(x.device))
+    if kbatch != 1:
+        rc = lib.nsq_fftconv1d_causal_film_bwd(*args, kbatch, *tail)
+    else:
+        rc = lib.nsq_fftconv1d_causal_bwd(*args, *tail)
     _lib.check(rc)
 
 
 class _CausalFFTConv1d(torch.autograd.Function):
     """Fused causal FFT conv; inputs already validated and cast.
 
-    x: [B, H, L] contiguous (f32/bf16/f16); k: [H, K] contiguous float32;
+    x: [B, H, L] contiguous (f32/bf16/f16); k: [kbatch*H, K] contiguous float32;
     s: [H] in x.dtype or None.
     """
 
     @staticmethod
-    def forward(ctx, x, k, s):
+    def forward(ctx, x, k, s, kbatch=1):
         y = torch.empty_like(x)
         ws = None
         if any(ctx.needs_input_grad[:3]):  # (grad mode is off inside forward; this flag is not)
             # Backward-sized workspace: the forward keeps its transformed x and k
             # in it for the backward (like autograd keeping rfft outputs).
             B, H, L = x.shape
-            need = _lib.get_lib().nsq_fftconv1d_causal_workspace_bytes(B, H, L, k.shape[-1], _lib.NSQ_DIR_BWD)
+            need = _causal_workspace_bytes(_lib.get_lib(), B, H, L, k.shape[-1], kbatch, _lib.NSQ_DIR_BWD)
             ws = _workspace(x.device, need)
-        causal_fftconv1d_fwd_raw(x, k, s, y, ws)
+        causal_fftconv1d_fwd_raw(x, k, s, y, ws, kbatch)
         ctx.save_for_backward(x, k, s)
         ctx.ws = ws
+        ctx.kbatch = kbatch
         ctx.has_s = s is not None
         return y
 
@@ -157,38 +173,41 @@ class _CausalFFTConv1d(torch.autograd.Function):
         gk = torch.empty(k.shape, dtype=torch.float32, device=x.device)
         gs = torch.empty(k.shape[0], dtype=torch.float32, device=x.device) if ctx.has_s else None
         ws, ctx.ws = ctx.ws, None  # the backward consumes the forward state
-        causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ws, fwd_state=ws is not None)
-        return gx, gk, (gs.to(s.dtype) if ctx.has_s else None)
+        causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ws, fwd_state=ws is not None, kbatch=ctx.kbatch)
+        gsum = None
+        if ctx.has_s:
+            H = x.shape[1]
+            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
+        return gx, gk, gsum, None
 
 
 # ---------------------------------------------------------------------------
 # Argument normalisation shared by every public function
 # ---------------------------------------------------------------------------
-def _kernel_2d(kernel: torch.Tensor) -> torch.Tensor:
-    """``[1, H, K]`` / ``[H, K]`` -> ``[H, K]``; FiLM ``[B, H, K]`` rejected.
+def _kernel_3d(kernel: torch.Tensor, B: int) -> torch.Tensor:
+    """``[H, K]`` -> ``[1, H, K]``; ``[1|B, H, K]`` kept (per-sample FiLM filters ``[B, H, K]``).
 
-    Mirrors ``_subq_causal_conv1d_bhl`` (``nvsubquadratic/ops/fftconv_custom.py:286-304``).
+    The shape rule of ``causal_fftconv1d_fp32_bhl`` (``nvsubquadratic/ops/fftconv.py:571-574``).
     """
-    if kernel.ndim == 3:
-        if kernel.shape[0] != 1:
-            raise NotImplementedError(
-                "fft_backend='hip' causal_fftconv1d does not accept per-sample "
-                f"FiLM weights. Got kernel shape {tuple(kernel.shape)} with batch={kernel.shape[0]}; "
-                "expected shared kernel [1, H, K] or [H, K]."
-            )
-        return kernel.squeeze(0)
     if kernel.ndim == 2:
-        return kernel
-    raise ValueError(f"Unexpected kernel shape: {tuple(kernel.shape)}.")
+        return kernel.unsqueeze(0)
+    if kernel.ndim != 3:
+        raise ValueError(f"Unexpected kernel shape: {tuple(kernel.shape)}.")
+    assert kernel.shape[0] in (1, B), (
+        f"Leading dimension must be 1 or batch_size ({B}). Got kernel.shape={tuple(kernel.shape)}."
+    )
+    return kernel
 
 
 def _causal_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None) -> torch.Tensor:
     if x.ndim != 3:
         raise ValueError(f"x must be [B, H, L]; got shape {tuple(x.shape)}")
-    _B, H, L = x.shape
-    k2 = _kernel_2d(kernel)
-    if k2.shape[0] != H:
-        raise ValueError(f"kernel has {k2.shape[0]} channels, x has {H}")
+    B, H, L = x.shape
+    k3 = _kernel_3d(kernel, B)
+    kbatch = k3.shape[0]
+    k2 = k3.reshape(kbatch * k3.shape[1], k3.shape[2])
+    if k3.shape[1] != H:
+        raise ValueError(f"kernel has {k3.shape[1]} channels, x has {H}")
     if k2.shape[-1] > 2 * L:
         raise ValueError(f"Kernel length must be less than or equal to 2 * seq_len. Got {k2.shape[-1]}.")
     input_dtype = x.dtype
@@ -201,7 +220,7 @@ def _causal_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor |
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         # Reference casts the shortcut to the input dtype before the product.
         sc = shortcut.to(input_dtype).to(compute_dtype).contiguous()
-    y = _CausalFFTConv1d.apply(xc, kc, sc)
+    y = _CausalFFTConv1d.apply(xc, kc, sc, kbatch)
     return y.to(input_dtype)
 
 
@@ -221,7 +240,7 @@ def causal_fftconv1d_bhl(
 
     Args:
         x: Input ``[B, H, L]``, any floating dtype.
-        kernel: ``[1, H, K]`` or ``[H, K]`` with ``K <= 2L``.
+        kernel: ``[1, H, K]``, ``[H, K]`` or per-sample ``[B, H, K]``, with ``K <= 2L``.
         shortcut: Optional ``[H]`` per-channel scale.
 
     Returns:
@@ -265,15 +284,15 @@ def causal_fftconv1d_bhl_chunked(
     """
     if chunk_size is None:
         chunk_size = _DEFAULT_CHUNK_SIZE
-    _B, H, _L = x.shape
+    B, H, _L = x.shape
     if H <= chunk_size:
         return causal_fftconv1d_bhl(x, kernel, shortcut)
-    k2 = _kernel_2d(kernel)
+    k3 = _kernel_3d(kernel, B)
     chunks = []
     for start in range(0, H, chunk_size):
         end = min(start + chunk_size, H)
         s_c = None if shortcut is None else shortcut[start:end]
-        chunks.append(causal_fftconv1d_bhl(x[:, start:end], k2[start:end], s_c))
+        chunks.append(causal_fftconv1d_bhl(x[:, start:end], k3[:, start:end], s_c))
     return torch.cat(chunks, dim=1)
 
 

@@ -57,12 +57,22 @@ def test_workspace_query_needs_no_gpu():
     assert lib.nsq_fftconv1d_causal_workspace_bytes(1, 4096, 262144, 262144, 1) == (2 * 4096 + 4096) * n * 8
 
 
-def test_per_sample_film_weights_rejected():
-    """Mirror of tests/ops/test_fftconv_custom_1d.py:231-239."""
+def test_per_sample_film_kernel_batch_validated():
+    """tests/ops/test_fftconv_custom_1d.py:231-239 checks that the reference's native wrapper rejects [B, H, K];
+    this backend accepts it (the torch path's semantics, fftconv.py:546-600) and rejects only a kernel batch that
+    is neither 1 nor B, in Python (AssertionError, as fftconv.py:571-574) and in the C ABI (before the device)."""
     x = torch.randn(2, 32, 128)
-    k = torch.randn(2, 32, 5)
-    with pytest.raises(NotImplementedError, match="per-sample FiLM weights"):
-        F.causal_fftconv1d_bhl(x, k)
+    with pytest.raises(AssertionError, match="Leading dimension must be 1 or batch_size"):
+        F.causal_fftconv1d_bhl(x, torch.randn(3, 32, 5))
+    lib = _lib.get_lib()
+    dummy = 16
+    rc = lib.nsq_fftconv1d_causal_film_fwd(dummy, dummy, None, dummy, _lib.NSQ_DTYPE[torch.float32], 2, 32, 128, 5,
+                                           3, None, 0, None)
+    assert rc == 1 and b"kernel batch" in lib.nsq_last_error()
+    # per-sample filters size the 4-step workspace with B*H filter rows
+    shared = lib.nsq_fftconv1d_causal_workspace_bytes(2, 4, 65536, 65536, 1)
+    film = lib.nsq_fftconv1d_causal_film_workspace_bytes(2, 4, 65536, 65536, 2, 1)
+    assert film - shared == 4 * (shared // (2 * 2 * 4 + 4))
 
 
 def test_kernel_longer_than_two_l_rejected():

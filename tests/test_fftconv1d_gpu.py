@@ -354,3 +354,54 @@ def test_retain_graph_second_backward_matches_first():
     k.grad = None
     y.backward(g)
     assert torch.equal(gx1, x.grad) and torch.equal(gk1, k.grad)
+
+
+# --- per-sample (FiLM) filters [B, H, K] ---------------------
+@pytest.mark.parametrize("B,H,L,K", [(3, 16, 256, 7), (2, 8, 1000, 2000), (2, 5, 4096, 4096), (4, 3, 64, 64),
+                                     (2, 3, 16384, 16384), (3, 2, 65536, 1000), (2, 2, 20000, 9000)])
+def test_per_sample_filters_fwd_bwd(B, H, L, K):
+    """Fused plan (incl. the K > L+1 fold) and 4-step plan, against the oracle's [B, H, K] path
+    (fftconv.py:546-600 broadcasts the kernel batch); gk is per image, gs summed over images."""
+    torch.manual_seed(11)
+    x = torch.randn(B, H, L, requires_grad=True)
+    k = torch.randn(B, H, K, requires_grad=True)
+    s = torch.randn(H, requires_grad=True)
+    y_ref = causal_fftconv1d_torch(x, k, s)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, kg, sg = (t.detach().cuda().requires_grad_(True) for t in (x, k, s))
+    y = F.causal_fftconv1d_bhl(xg, kg, sg)
+    y.backward(g.cuda())
+    assert kg.grad.shape == (B, H, K)
+    assert rel_l2(y_ref, y) < RTOL_F32_L2
+    assert rel_l2(x.grad, xg.grad) < RTOL_F32_L2
+    assert rel_l2(k.grad, kg.grad) < RTOL_F32_L2
+    assert rel_l2(s.grad, sg.grad) < RTOL_F32_L2
+
+
+@pytest.mark.parametrize("L,K", [(512, 31), (32768, 32768)])
+def test_per_sample_filters_equal_per_image_shared_calls_bitwise(L, K):
+    torch.manual_seed(12)
+    B, H = 3, 4
+    x = torch.randn(B, H, L, device="cuda").to(torch.bfloat16)
+    k = torch.randn(B, H, K, device="cuda")
+    s = torch.randn(H, device="cuda").to(torch.bfloat16)
+    y = F.causal_fftconv1d_bhl(x, k, s)
+    for b in range(B):
+        assert torch.equal(y[b:b + 1], F.causal_fftconv1d_bhl(x[b:b + 1].contiguous(), k[b:b + 1].contiguous(), s))
+    yc = F.causal_fftconv1d_bhl_chunked(x, k, s, chunk_size=3)
+    assert torch.equal(yc, y)
+    y_blh = F.causal_fftconv1d_bhl_w_reshape(x.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous(), s)
+    assert torch.equal(y_blh, y.transpose(1, 2))
+
+
+def test_per_sample_filters_bf16_config3_shape_sample():
+    """Config 3's length with per-sample filters on a channel sample (bf16 I/O)."""
+    torch.manual_seed(13)
+    B, H, L = 2, 2, 262144
+    x = torch.randn(B, H, L).to(torch.bfloat16)
+    k = torch.randn(B, H, L) * torch.exp(-torch.linspace(0, 20, L))
+    y_ref = causal_fftconv1d_torch(x, k)
+    y = F.causal_fftconv1d_bhl(x.cuda(), k.cuda())
+    assert y.dtype == torch.bfloat16
+    assert rel_l2(y_ref, y) < RTOL_BF16_L2

@@ -185,3 +185,22 @@ def test_bf16_output_cast_and_shortcut_rounding():
     # fp32 FFT vs fp64 conv may flip a bf16 rounding: allow a 1-ulp difference
     diff = np.abs(y.float().numpy() - expect)
     assert (diff <= np.abs(expect) * 2 ** -7 + 1e-30).all()
+
+
+@pytest.mark.parametrize("B,H,L,K", [(3, 4, 64, 17), (2, 3, 50, 100), (2, 2, 33, 33)])
+def test_per_sample_filters_match_brute_force_per_image(B, H, L, K):
+    """Kernel [B, H, K] (fftconv.py:571-574 allows a leading batch): image b uses filter b -- the brute force
+    run image by image, and the autograd gradients are each image's own adjoint (gk per image, not summed)."""
+    rng = np.random.default_rng(B * 7 + K)
+    x = rng.standard_normal((B, H, L))
+    k = rng.standard_normal((B, H, K))
+    g = rng.standard_normal((B, H, L))
+    xt = torch.tensor(x, requires_grad=True)
+    kt = torch.tensor(k, requires_grad=True)
+    y = causal_fftconv1d_torch(xt, kt)
+    y.backward(torch.tensor(g))
+    for b in range(B):
+        assert rel_l2(direct.causal_conv1d(x[b:b + 1], k[b]), y[b:b + 1].detach()) < 1e-5
+        gx_bf, gk_bf = direct.causal_conv1d_bwd(g[b:b + 1], x[b:b + 1], k[b])
+        assert rel_l2(gx_bf, xt.grad[b:b + 1]) < 1e-5
+        assert rel_l2(gk_bf, kt.grad[b]) < 1e-5
