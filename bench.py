@@ -23,6 +23,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --workload cfg4-circular|well-rb   (periodic and
            mixed boundaries, report-only: cfg4's shape with circular padding;
            the rayleigh_benard Well config's layer, x periodic / y zero-padded)
+       python bench.py --workload hyena-gated   (report-only: the Hyena gates
+           fused into the causal conv, with the unfused composition's time)
        python bench.py --copy-calibration   (one plain copy kernel of known size,
                                              for scaling rocprof FETCH/WRITE_SIZE)
 """
@@ -149,6 +151,7 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev).manual_seed(0)
+    extra = {}
     if name == "cfg1":
         B, D, L = 2, 128, 4096
         c = causal1d_case_fast(B, D, L, torch.float32, (1.0, 10.0), dev, seed=0)
@@ -242,6 +245,45 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
             def step():
                 xg.grad = kg.grad = sg.grad = None
                 fn(xg, kg, sg).backward(g)
+    elif name == "hyena-gated":
+        # report-only (row F2): the Hyena layer's gated long conv, fused, against the same layer composed of torch
+        # gates around the HIP conv (hyena_nd.py:546,558,570), fwd+bwd
+        import torch.nn.functional as Fn
+
+        from nvsubquadratic_amd.gated_fftconv_hip import hyena_gated_causal_fftconv1d_bhl
+        from nvsubquadratic_amd.workloads import algorithmic_bytes_gated
+
+        B, Ch, L = 4, 1024, 8192
+        q, kk, v = (torch.randn(B, Ch, L, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+                    for _ in range(3))
+        w = (torch.randn(1, Ch, L, device=dev, generator=gen) / L ** 0.5).requires_grad_(True)
+        sh = torch.randn(Ch, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+        g = torch.randn(B, Ch, L, device=dev, generator=gen).to(torch.bfloat16)
+        phase, dtype = "fwd+bwd", "f32"
+        nbytes = algorithmic_bytes_gated(B, Ch, L, L, 2)
+        desc = ("hyena-gated: gated causal FFT conv fwd+bwd (z = q silu(k), y = (conv(z) + s z) sigmoid(v)), "
+                "B=4 D=1024 L=8192 K=8192, bf16 I/O; forward gates fused into the conv's first and last passes, "
+                "backward gates as elementwise kernels around the conv adjoint")
+
+        def clear():
+            for t in (q, kk, v, w, sh):
+                t.grad = None
+
+        def step():
+            clear()
+            hyena_gated_causal_fftconv1d_bhl(q, kk, v, w, sh, "silu", "sigmoid").backward(g)
+
+        def step_unfused():
+            clear()
+            z = q * Fn.silu(kk)
+            (F.causal_fftconv1d_bhl(z, w, sh) * torch.sigmoid(v)).backward(g)
+
+        def step_fused_bwd():
+            clear()
+            hyena_gated_causal_fftconv1d_bhl(q, kk, v, w, sh, "silu", "sigmoid", fuse_backward_gates=True).backward(g)
+
+        extra["unfused_ms_per_step"] = round(statistics.mean(_time_steps(step_unfused, steps, warmup)), 4)
+        extra["fused_backward_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_fused_bwd, steps, warmup)), 4)
     else:
         raise SystemExit(f"unknown workload {name}")
     ms_list = _time_steps(step, steps, warmup)
@@ -255,6 +297,7 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
         "data": "synthetic", "config": {"workload": desc},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes},
+        **extra,
     }), flush=True)
 
 
@@ -268,7 +311,7 @@ def main() -> None:
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
-                                                              "cfg4-circular", "well-rb"])
+                                                              "cfg4-circular", "well-rb", "hyena-gated"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -134,6 +134,44 @@ int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, con
                                int64_t kbatch, void* stream);
 
 /*
+ * Hyena-gated causal 1D FFT convolution (row F2 of the build plan): the long conv
+ * with the gates around it fused into its first and last passes,
+ *   z = q * act1(k_gate);  y1 = causal_conv(z; k) + shortcut * z;  y = y1 * act2(v),
+ * as nvsubquadratic/modules/hyena_nd.py:546 (first gate), :558 (CKConvND global
+ * conv with its shortcut, ckconv_nd.py:1054-1062) and :570 (second gate) compute
+ * it; each elementwise product rounded to `dtype` as those torch ops round.
+ * act codes: NSQ_GATE_IDENTITY, NSQ_GATE_SIGMOID, NSQ_GATE_SILU (torch.nn.Identity,
+ * Sigmoid, SiLU).  q, k_gate, v, y, y1, g, dq, dk_gate, dv: [B, H, L] in `dtype`;
+ * k, gk, gs, kbatch as nsq_fftconv1d_causal_film_*.  The forward writes y1 when
+ * y1 != NULL (the backward needs it).  The backward returns dq, dk_gate, dv, gk, gs.
+ * Forward: FFT lengths <= 16384 run one fused kernel (no workspace); longer ones
+ * run elementwise gate kernels around the multi-kernel conv.  Backward: the
+ * elementwise gate kernels around the plain conv adjoint, or, with fuse_gates = 1
+ * and FFT lengths <= 16384, one fused kernel (no workspace).  The fused adjoint
+ * carries five extra operand streams through a latency-bound kernel and measured
+ * slower on MI355X at B=4 D=1024 L=8192 (see the bench's hyena-gated line), so 0
+ * is the default of the Python layer.  Workspace: nsq_gated_fftconv1d_causal_
+ * workspace_bytes; the unfused paths need 16-byte aligned tensors.
+ * No counterpart in the reference: there the gates are separate torch ops
+ * around fft_causal_conv1d.
+ */
+enum { NSQ_GATE_IDENTITY = 0, NSQ_GATE_SIGMOID = 1, NSQ_GATE_SILU = 2 };
+
+size_t nsq_gated_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                                                  int dtype, int direction);
+
+int nsq_gated_fftconv1d_causal_fwd(const void* q, const void* k_gate, const void* v, const float* k,
+                                   const void* shortcut, void* y, void* y1, int dtype, int act1, int act2, int64_t B,
+                                   int64_t H, int64_t L, int64_t K, int64_t kbatch, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+int nsq_gated_fftconv1d_causal_bwd(const void* g, const void* q, const void* k_gate, const void* v, const void* y1,
+                                   const float* k, const void* shortcut, void* dq, void* dk_gate, void* dv, float* gk,
+                                   float* gs, int dtype, int act1, int act2, int64_t B, int64_t H, int64_t L,
+                                   int64_t K, int64_t kbatch, int fuse_gates, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
+/*
  * Depthwise causal direct convolution, nn.Conv1d tap order with left padding
  * K-1 (tests/ops/test_causal_conv1d_custom.py:65-72):
  *   y[b,c,n] = act( sum_{j<K} w[c,j] x[b,c,n-K+1+j] + bias[c] ),  1 <= K <= 256,

@@ -79,6 +79,18 @@ _SIGNATURES = {
             _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_int, _c_void_p,
         ],
     ),
+    "nsq_gated_fftconv1d_causal_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "nsq_gated_fftconv1d_causal_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p],
+    ),
+    "nsq_gated_fftconv1d_causal_bwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_void_p,
+         _c_size, _c_void_p],
+    ),
     "nsq_circular_fftconv1d_fwd": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p],

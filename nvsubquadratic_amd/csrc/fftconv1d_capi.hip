@@ -1,6 +1,8 @@
 // C ABI entry points of the causal 1D FFT convolution (see include/nsq_hip.h).
 // Kernels and plans live in fftconv1d_impl.h; the per-dtype instantiations are
 // compiled in fftconv1d_f32.hip / fftconv1d_bf16.hip / fftconv1d_f16.hip.
+#include <initializer_list>
+
 #include "fftconv1d_impl.h"
 
 namespace nsq {
@@ -135,6 +137,30 @@ static int causal_bwd(const void* g, const void* x, const float* k, const void* 
   return NSQ_OK;
 }
 
+// Gated (Hyena) causal conv: the plain conv's checks plus gate codes and, for
+// the elementwise kernels of the multi-kernel plan, 16-byte aligned tensors.
+static size_t gated_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, int dtype,
+                                    int direction) {
+  Plan1D p;
+  if (!make_plan(L, K, p) || !valid_dtype(dtype)) return 0;
+  if (p.fused && direction == NSQ_DIR_FWD) return 0;  // one fused kernel
+  const size_t conv = (causal_workspace_bytes(B, H, L, K, kbatch, direction) + 255) / 256 * 256;
+  const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
+  return conv + size_t(direction == NSQ_DIR_BWD ? 3 : 2) * size_t(B * H * L) * es;
+}
+
+static bool aligned16(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (p && (reinterpret_cast<uintptr_t>(p) & 15)) return false;
+  return true;
+}
+
+static int validate_gate(int act1, int act2) {
+  NSQ_CHECK_ARG(act1 >= 0 && act1 <= 2 && act2 >= 0 && act2 <= 2,
+                "gated_fftconv1d: gate codes must be 0 (identity), 1 (sigmoid) or 2 (silu); got %d, %d", act1, act2);
+  return NSQ_OK;
+}
+
 }  // namespace nsq
 
 using namespace nsq;
@@ -228,6 +254,105 @@ int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, con
       break;
   }
   NSQ_CHECK_ARG(ok, "circular_fftconv1d_bwd: no kernel for logN=%d", logN);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+size_t nsq_gated_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                                                  int dtype, int direction) {
+  return gated_workspace_bytes(B, H, L, K, kbatch, dtype, direction);
+}
+
+int nsq_gated_fftconv1d_causal_fwd(const void* q, const void* kgate, const void* v, const float* k,
+                                   const void* shortcut, void* y, void* y1, int dtype, int act1, int act2, int64_t B,
+                                   int64_t H, int64_t L, int64_t K, int64_t kbatch, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  clear_error();
+  Plan1D p;
+  int rc = validate(q, y, k, dtype, B, H, L, K, kbatch, p);
+  if (rc) return rc;
+  rc = validate_gate(act1, act2);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(kgate && v, "gated_fftconv1d_fwd: null gate input pointer");
+  NSQ_CHECK_ARG(p.fused || aligned16({q, kgate, v, y, y1}), "gated_fftconv1d_fwd: tensors must be 16-byte aligned");
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  float2* ws = nullptr;
+  void* gws = nullptr;
+  if (!p.fused) {
+    const size_t need = gated_workspace_bytes(B, H, L, K, kbatch, dtype, NSQ_DIR_FWD);
+    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv1d_fwd: workspace of %zu bytes required, got %zu",
+                  need, workspace_bytes);
+    ws = (float2*)workspace;
+    gws = (char*)workspace + (causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_FWD) + 255) / 256 * 256;
+  }
+  const GateArgs ga{kgate, v, y1, nullptr, nullptr, act1, act2};
+  const int kf = kbatch != 1;
+  bool ok = false;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      ok = run_gated_fwd<NSQ_DTYPE_F32>(p, q, k, shortcut, y, int(B), int(H), int(L), int(K), kf, ga, gws, ws, tw, st);
+      break;
+    case NSQ_DTYPE_BF16:
+      ok = run_gated_fwd<NSQ_DTYPE_BF16>(p, q, k, shortcut, y, int(B), int(H), int(L), int(K), kf, ga, gws, ws, tw, st);
+      break;
+    default:
+      ok = run_gated_fwd<NSQ_DTYPE_F16>(p, q, k, shortcut, y, int(B), int(H), int(L), int(K), kf, ga, gws, ws, tw, st);
+      break;
+  }
+  NSQ_CHECK_ARG(ok, "gated_fftconv1d_fwd: no kernel for logN=%d", p.logN);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+int nsq_gated_fftconv1d_causal_bwd(const void* g, const void* q, const void* kgate, const void* v, const void* y1,
+                                   const float* k, const void* shortcut, void* dq, void* dkgate, void* dv, float* gk,
+                                   float* gs, int dtype, int act1, int act2, int64_t B, int64_t H, int64_t L,
+                                   int64_t K, int64_t kbatch, int fuse_gates, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  clear_error();
+  Plan1D p;
+  int rc = validate(g, q, k, dtype, B, H, L, K, kbatch, p);
+  if (rc) return rc;
+  rc = validate_gate(act1, act2);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(kgate && v && y1, "gated_fftconv1d_bwd: null gate input pointer (y1 is required)");
+  NSQ_CHECK_ARG(dq && dkgate && dv && gk, "gated_fftconv1d_bwd: null gradient output pointer");
+  NSQ_CHECK_ARG(!shortcut || gs, "gated_fftconv1d_bwd: gs required when a shortcut is given");
+  const bool fused_gates = p.fused && fuse_gates;
+  NSQ_CHECK_ARG(fused_gates || aligned16({g, q, kgate, v, y1, dq, dkgate, dv}),
+                "gated_fftconv1d_bwd: tensors must be 16-byte aligned");
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  float2* ws = nullptr;
+  void* gws = nullptr;
+  if (!fused_gates) {
+    const size_t need = gated_workspace_bytes(B, H, L, K, kbatch, dtype, NSQ_DIR_BWD);
+    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv1d_bwd: workspace of %zu bytes required, got %zu",
+                  need, workspace_bytes);
+    ws = (float2*)workspace;
+    gws = (char*)workspace + (causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD) + 255) / 256 * 256;
+  }
+  const GateArgs ga{kgate, v, const_cast<void*>(y1), dkgate, dv, act1, act2};
+  const int kf = kbatch != 1;
+  bool ok = false;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      ok = run_gated_bwd<NSQ_DTYPE_F32>(p, g, q, k, shortcut, dq, gk, gs, int(B), int(H), int(L), int(K), kf, ga, gws,
+                                        ws, tw, st, fused_gates);
+      break;
+    case NSQ_DTYPE_BF16:
+      ok = run_gated_bwd<NSQ_DTYPE_BF16>(p, g, q, k, shortcut, dq, gk, gs, int(B), int(H), int(L), int(K), kf, ga, gws,
+                                         ws, tw, st, fused_gates);
+      break;
+    default:
+      ok = run_gated_bwd<NSQ_DTYPE_F16>(p, g, q, k, shortcut, dq, gk, gs, int(B), int(H), int(L), int(K), kf, ga, gws,
+                                        ws, tw, st, fused_gates);
+      break;
+  }
+  NSQ_CHECK_ARG(ok, "gated_fftconv1d_bwd: no kernel for logN=%d", p.logN);
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
 }

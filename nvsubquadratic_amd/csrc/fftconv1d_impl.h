@@ -26,6 +26,7 @@
 #pragma once
 
 #include "fft_core.h"
+#include "gate.h"
 
 namespace nsq {
 
@@ -168,12 +169,15 @@ __device__ __forceinline__ void filter_spectrum(float2* lds, const float* __rest
 // (no padding, no crop) rolled by -c through the filter ramp; a period L < 16
 // runs at length 16 on the periodic extension of x (sample i read at i & wm,
 // wm = L - 1; -1 otherwise).  kfilm: the filter is per image ([B, H, K]); the
-// launch then gives one image per workgroup (b_per_wg = 1).
-template <int LOGN, int DT, bool FOLD, bool CIRC = false>
+// launch then gives one image per workgroup (b_per_wg = 1).  GATE (Hyena
+// gates, gate.h): x is the query q; the transform reads z = q act1(k) and the
+// epilogue writes y = y1 act2(v), y1 = conv(z) + s z (kept in ga.y1 if given).
+template <int LOGN, int DT, bool FOLD, bool CIRC = false, bool GATE = false>
 __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
     const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ k,
     const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ y, int B, int H, int L,
-    int K, int b_per_wg, const float2* __restrict__ tw, int c, int kfilm, int wm) {
+    int K, int b_per_wg, const float2* __restrict__ tw, int c, int kfilm, int wm, GateArgs ga) {
+  using ET = typename Elem<DT>::T;
   using C = FusedCfg<LOGN>;
   __shared__ float2 lds[C::TILE_P];
   const int h0 = blockIdx.x * C::M;
@@ -188,7 +192,13 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
     auto ld = [&](int m, int n) -> float2 {
       const int h = h0 + m;
       if (h >= H) return make_float2(0.f, 0.f);
-      return load_pair<DT>(x + (int64_t(b) * H + h) * L, (2 * int64_t(n)) & wm, L);
+      const int64_t row = (int64_t(b) * H + h) * L, i = (2 * int64_t(n)) & wm;
+      const float2 q = load_pair<DT>(x + row, i, L);
+      if constexpr (GATE) {
+        const float2 kk = load_pair<DT>((const ET*)ga.kg + row, i, L);
+        return make_float2(gate1<DT>(ga.act1, q.x, kk.x), gate1<DT>(ga.act1, q.y, kk.y));
+      }
+      return q;
     };
     LdsTile<C::SP, true> st{lds};
     fft<LOGN, false, C::M, C::T, C::SP>(lds, ld, st, tw);
@@ -211,10 +221,19 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
       const int64_t row = (int64_t(b) * H + h) * L;
       const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
       const int64_t i0 = 2 * int64_t(n);
-      if (i0 < L) Elem<DT>::store(y, row + i0, epilogue<DT>(v.x * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0) : 0.f));
-      if (i0 + 1 < L)
-        Elem<DT>::store(y, row + i0 + 1,
-                        epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0 + 1) : 0.f));
+      auto out = [&](int64_t i, float conv) {
+        if constexpr (GATE) {
+          const float zi = s ? gate1<DT>(ga.act1, Elem<DT>::load(x, row + i), Elem<DT>::load((const ET*)ga.kg, row + i))
+                             : 0.f;
+          const float y1 = epilogue<DT>(conv, s != nullptr, sv, zi);
+          if (ga.y1) Elem<DT>::store((ET*)ga.y1, row + i, y1);
+          Elem<DT>::store(y, row + i, y1 * Elem<DT>::round(gate_act(ga.act2, Elem<DT>::load((const ET*)ga.v, row + i))));
+        } else {
+          Elem<DT>::store(y, row + i, epilogue<DT>(conv, s != nullptr, sv, s ? Elem<DT>::load(x, row + i) : 0.f));
+        }
+      };
+      if (i0 < L) out(i0, v.x * scale);
+      if (i0 + 1 < L) out(i0 + 1, v.y * scale);
     };
     if constexpr (!FOLD) {
       LdsTile<C::SP, true> ldl{lds};
@@ -240,13 +259,18 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
 // filter-gradient rows are that image's.  CIRC: as the forward; the filter
 // gradient gk[j] = sum_n g[n] x[(n + c - j) mod L] is the correlation read at
 // lag (j - c) mod L; on a periodic extension (wm = L - 1) every lag repeats
-// 2N / L times, so gk and gs are scaled by gks = L / 2N (1 otherwise).
-template <int LOGN, int DT, bool FOLD, bool CIRC = false>
+// 2N / L times, so gk and gs are scaled by gks = L / 2N (1 otherwise).  GATE:
+// g is the gradient of the gated output; the transform reads dy1 = g act2(v)
+// and writes dv = (g y1) act2'(v) as it loads; x is q (read as z = q act1(k));
+// the epilogue turns dz = conv^T(dy1) + s dy1 into gx = dq = dz act1(k) and
+// ga.dk = (dz q) act1'(k).
+template <int LOGN, int DT, bool FOLD, bool CIRC = false, bool GATE = false>
 __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x,
     const float* __restrict__ k, const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ gx,
     float* __restrict__ gk, float* __restrict__ gs, int B, int H, int L, int K, const float2* __restrict__ tw, int c,
-    int kfilm, int wm, float gks) {
+    int kfilm, int wm, float gks, GateArgs ga) {
+  using ET = typename Elem<DT>::T;
   using C = FusedCfg<LOGN>;
   __shared__ float2 ldsG[C::TILE_P];
   __shared__ float2 ldsX[C::TILE_P];
@@ -270,15 +294,35 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     auto ldg = [&](int m, int n) -> float2 {
       const int h = h0 + m;
       if (h >= H) return make_float2(0.f, 0.f);
-      const typename Elem<DT>::T* row = g + (int64_t(b) * H + h) * L;
+      const int64_t ro = (int64_t(b) * H + h) * L;
+      const typename Elem<DT>::T* row = g + ro;
       const int64_t i0 = 2 * int64_t(n);
-      if (FOLD && i0 >= 2 * int64_t(L)) return load_pair<DT>(row, i0 - 2 * int64_t(L), L);
-      return load_pair<DT>(row, i0 & wm, L);
+      const bool fold = FOLD && i0 >= 2 * int64_t(L);
+      const int64_t i = fold ? i0 - 2 * int64_t(L) : (i0 & wm);
+      const float2 gv = load_pair<DT>(row, i, L);
+      if constexpr (GATE) {
+        const float2 vv = load_pair<DT>((const ET*)ga.v + ro, i, L);
+        const float2 yv = load_pair<DT>((const ET*)ga.y1 + ro, i, L);
+        if (!fold) {  // dv once per sample (the fold re-reads samples)
+          if (i < L) Elem<DT>::store((ET*)ga.dv, ro + i, Elem<DT>::round(gv.x * yv.x) * gate_dact(ga.act2, vv.x));
+          if (i + 1 < L)
+            Elem<DT>::store((ET*)ga.dv, ro + i + 1, Elem<DT>::round(gv.y * yv.y) * gate_dact(ga.act2, vv.y));
+        }
+        return make_float2(Elem<DT>::round(gv.x * Elem<DT>::round(gate_act(ga.act2, vv.x))),
+                           Elem<DT>::round(gv.y * Elem<DT>::round(gate_act(ga.act2, vv.y))));
+      }
+      return gv;
     };
     auto ldx = [&](int m, int n) -> float2 {
       const int h = h0 + m;
       if (h >= H) return make_float2(0.f, 0.f);
-      return load_pair<DT>(x + (int64_t(b) * H + h) * L, (2 * int64_t(n)) & wm, L);
+      const int64_t ro = (int64_t(b) * H + h) * L, i = (2 * int64_t(n)) & wm;
+      const float2 q = load_pair<DT>(x + ro, i, L);
+      if constexpr (GATE) {
+        const float2 kk = load_pair<DT>((const ET*)ga.kg + ro, i, L);
+        return make_float2(gate1<DT>(ga.act1, q.x, kk.x), gate1<DT>(ga.act1, q.y, kk.y));
+      }
+      return q;
     };
     LdsTile<C::SP, true> stG{ldsG};
     LdsTile<C::SP, true> stX{ldsX};
@@ -304,11 +348,22 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
       const int64_t row = (int64_t(b) * H + h) * L;
       const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
       const int64_t i0 = 2 * int64_t(n);
-      if (i0 < L)
-        Elem<DT>::store(gx, row + i0, epilogue<DT>(v.x * scale, s != nullptr, sv, s ? Elem<DT>::load(g, row + i0) : 0.f));
-      if (i0 + 1 < L)
-        Elem<DT>::store(gx, row + i0 + 1,
-                        epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(g, row + i0 + 1) : 0.f));
+      auto out = [&](int64_t i, float conv) {
+        if constexpr (GATE) {
+          const float dy1 =
+              s ? Elem<DT>::round(Elem<DT>::load(g, row + i) *
+                                  Elem<DT>::round(gate_act(ga.act2, Elem<DT>::load((const ET*)ga.v, row + i))))
+                : 0.f;
+          const float dz = epilogue<DT>(conv, s != nullptr, sv, dy1);
+          const float q = Elem<DT>::load(x, row + i), kk = Elem<DT>::load((const ET*)ga.kg, row + i);
+          Elem<DT>::store(gx, row + i, dz * Elem<DT>::round(gate_act(ga.act1, kk)));
+          Elem<DT>::store((ET*)ga.dk, row + i, Elem<DT>::round(dz * q) * gate_dact(ga.act1, kk));
+        } else {
+          Elem<DT>::store(gx, row + i, epilogue<DT>(conv, s != nullptr, sv, s ? Elem<DT>::load(g, row + i) : 0.f));
+        }
+      };
+      if (i0 < L) out(i0, v.x * scale);
+      if (i0 + 1 < L) out(i0 + 1, v.y * scale);
     };
     LdsTile<C::SP, true> ldl{ldsG};
     fft<LOGN, true, C::M, C::T, C::SP>(ldsG, ldl, epi, tw);
@@ -831,10 +886,10 @@ static void launch_fused_fwd(const Plan1D& p, const void* x, const float* k, con
   dim3 grid(gh, nb);
   if (p.fold)
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1, GateArgs{});
   else
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)x, k, (const ET*)s,
-                       (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1);
+                       (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1, GateArgs{});
 }
 
 template <int LOGN, int DT>
@@ -846,10 +901,46 @@ static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, cons
   dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
   if (p.fold)
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, GateArgs{});
   else
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f);
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, GateArgs{});
+}
+
+// Gated (Hyena) fused plan: the GATE variants of the fused kernels.
+template <int LOGN, int DT>
+static void launch_gated_fused_fwd(const Plan1D& p, const void* q, const float* k, const void* s, void* y, int B,
+                                   int H, int L, int K, int kfilm, const GateArgs& ga, const float2* tw,
+                                   hipStream_t st) {
+  using C = FusedCfg<LOGN>;
+  using ET = typename Elem<DT>::T;
+  const int gh = int(ceil_div(H, C::M));
+  int nb = int(ceil_div(2048, gh));
+  nb = nb < 1 ? 1 : (nb > B ? B : nb);
+  const int bpw = kfilm ? 1 : int(ceil_div(B, nb));
+  nb = int(ceil_div(B, bpw));
+  const dim3 grid(gh, nb);
+  if (p.fold)
+    hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, true, false, true>), grid, dim3(C::T), 0, st, (const ET*)q, k,
+                       (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1, ga);
+  else
+    hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false, false, true>), grid, dim3(C::T), 0, st, (const ET*)q, k,
+                       (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1, ga);
+}
+
+template <int LOGN, int DT>
+static void launch_gated_fused_bwd(const Plan1D& p, const void* g, const void* q, const float* k, const void* s,
+                                   void* dq, float* gk, float* gs, int B, int H, int L, int K, int kfilm,
+                                   const GateArgs& ga, const float2* tw, hipStream_t st) {
+  using C = FusedCfg<LOGN>;
+  using ET = typename Elem<DT>::T;
+  const dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
+  if (p.fold)
+    hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
+                       (const ET*)q, k, (const ET*)s, (ET*)dq, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, ga);
+  else
+    hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
+                       (const ET*)q, k, (const ET*)s, (ET*)dq, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, ga);
 }
 
 // Circular 1D (fused plan at FFT length L = 2N): shift c = (K-1)/2; kfilm =
@@ -870,7 +961,7 @@ static void launch_circ_fwd(const void* x, const float* k, const void* s, void* 
   // a period shorter than the transform: periodic extension (L = 1, K = 1: plain zero padding is exact)
   const int wm = (L > 1 && L < 2 * C::N) ? L - 1 : -1;
   hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)x, k,
-                     (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, (K - 1) / 2, kfilm, wm);
+                     (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, (K - 1) / 2, kfilm, wm, GateArgs{});
 }
 
 template <int LOGN, int DT>
@@ -882,7 +973,7 @@ static void launch_circ_bwd(const void* g, const void* x, const float* k, const 
   const int wm = (L > 1 && L < 2 * C::N) ? L - 1 : -1;
   hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
                      (const ET*)x, k, (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, (K - 1) / 2, kfilm, wm,
-                     wm == -1 ? 1.f : float(L) / float(2 * C::N));
+                     wm == -1 ? 1.f : float(L) / float(2 * C::N), GateArgs{});
 }
 
 // Workspace layout of the 4-step plan (rows of N complex64; NK = H, or B*H for
@@ -1019,6 +1110,20 @@ struct FusedBwd {
 };
 
 template <int DT, bool BWD>
+struct GatedFused {
+  template <int LOGN>
+  struct At {
+    template <class... A>
+    static void run(A&&... a) {
+      if constexpr (BWD)
+        launch_gated_fused_bwd<LOGN, DT>(static_cast<A&&>(a)...);
+      else
+        launch_gated_fused_fwd<LOGN, DT>(static_cast<A&&>(a)...);
+    }
+  };
+};
+
+template <int DT, bool BWD>
 struct CircFused {
   template <int LOGN>
   struct At {
@@ -1072,6 +1177,53 @@ bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, cons
                                                                 fwd_state, tw, st);
 }
 
+// Gated (Hyena) causal conv.  Fused plan: one gated kernel each way.  4-step
+// plan: the elementwise gate kernels around the plain conv, with the
+// intermediates in `gws` (forward: z [, y1 when the caller keeps none];
+// backward: z, dy1, dz), the conv's own workspace in `ws`.
+// Forward: y = (conv(z) + s z) act2(v), z = q act1(k_gate); ga.y1 (optional)
+// receives conv(z) + s z.  Backward: needs ga.y1.
+template <int DT>
+bool run_gated_fwd(const Plan1D& p, const void* q, const float* k, const void* s, void* y, int B, int H, int L,
+                   int K, int kfilm, const GateArgs& ga, void* gws, float2* ws, const float2* tw, hipStream_t st) {
+  if (p.fused)
+    return dispatch_int<GatedFused<DT, false>::template At, 3, 13>(p.logN, p, q, k, s, y, B, H, L, K, kfilm, ga, tw,
+                                                                   st);
+  using ET = typename Elem<DT>::T;
+  const int64_t n = int64_t(B) * H * L;
+  ET* z = (ET*)gws;
+  ET* y1 = ga.y1 ? (ET*)ga.y1 : z + n;
+  launch_gate_ew<DT, GATE_OP_FWD1>(GateEw{q, ga.kg, nullptr, z, nullptr, ga.act1}, n, st);
+  if (!run_fwd<DT>(p, z, k, s, y1, B, H, L, K, kfilm, ws, false, tw, st)) return false;
+  launch_gate_ew<DT, GATE_OP_FWD2>(GateEw{y1, ga.v, nullptr, y, nullptr, ga.act2}, n, st);
+  return true;
+}
+
+// The backward runs the elementwise gate kernels around the plain conv adjoint
+// for every plan: the gated fused adjoint (GATE) is correct but, with one
+// 139 KB-LDS workgroup per CU at FFT length 16384, its five extra operand
+// streams add latency that occupancy cannot hide (measured on MI355X at
+// B=4 D=1024 L=8192 bf16: 1.01 ms against 0.66 ms for the plain adjoint plus
+// ~0.17 ms of gate kernels).  `fused_gate_bwd` selects it anyway (tests).
+template <int DT>
+bool run_gated_bwd(const Plan1D& p, const void* g, const void* q, const float* k, const void* s, void* dq, float* gk,
+                   float* gs, int B, int H, int L, int K, int kfilm, const GateArgs& ga, void* gws, float2* ws,
+                   const float2* tw, hipStream_t st, bool fused_gate_bwd) {
+  if (p.fused && fused_gate_bwd)
+    return dispatch_int<GatedFused<DT, true>::template At, 3, 13>(p.logN, p, g, q, k, s, dq, gk, gs, B, H, L, K,
+                                                                  kfilm, ga, tw, st);
+  using ET = typename Elem<DT>::T;
+  const int64_t n = int64_t(B) * H * L;
+  ET* z = (ET*)gws;
+  ET* dy1 = z + n;
+  ET* dz = dy1 + n;
+  launch_gate_ew<DT, GATE_OP_BWD2>(GateEw{g, ga.v, ga.y1, dy1, ga.dv, ga.act2}, n, st);
+  launch_gate_ew<DT, GATE_OP_FWD1>(GateEw{q, ga.kg, nullptr, z, nullptr, ga.act1}, n, st);
+  if (!run_bwd<DT>(p, dy1, z, k, s, dz, gk, gs, B, H, L, K, kfilm, ws, false, tw, st)) return false;
+  launch_gate_ew<DT, GATE_OP_BWD1>(GateEw{dz, q, ga.kg, dq, ga.dk, ga.act1}, n, st);
+  return true;
+}
+
 // Circular 1D: logN = max(log2(L), 4) - 1 in [3, 13] (L a power of two <= 16384;
 // L < 16 runs at transform length 16 on the periodic extension).
 template <int DT>
@@ -1096,7 +1248,13 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
   extern template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, \
                                         int, const float2*, hipStream_t);                                       \
   extern template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, \
-                                        float*, int, int, int, int, int, const float2*, hipStream_t);
+                                        float*, int, int, int, int, int, const float2*, hipStream_t);          \
+  extern template bool run_gated_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, \
+                                         int, int, int, const GateArgs&, void*, float2*, const float2*,         \
+                                         hipStream_t);                                                          \
+  extern template bool run_gated_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*,     \
+                                         void*, float*, float*, int, int, int, int, int, const GateArgs&, void*, \
+                                         float2*, const float2*, hipStream_t, bool);
 
 #define NSQ_INSTANTIATE_FFTCONV1D(DT)                                                                    \
   template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
@@ -1107,7 +1265,12 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
   template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, int, \
                                  const float2*, hipStream_t);                                               \
   template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, float*, \
-                                 int, int, int, int, int, const float2*, hipStream_t);
+                                 int, int, int, int, int, const float2*, hipStream_t);                         \
+  template bool run_gated_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, int, \
+                                  int, const GateArgs&, void*, float2*, const float2*, hipStream_t);             \
+  template bool run_gated_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,      \
+                                  float*, float*, int, int, int, int, int, const GateArgs&, void*, float2*,       \
+                                  const float2*, hipStream_t, bool);
 
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_F32)
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_BF16)

@@ -190,3 +190,13 @@ def algorithmic_bytes_nd(B: int, C: int, S, K, itemsize: int, phase: str) -> int
     if phase == "fwd+bwd":
         return algorithmic_bytes_nd(B, C, S, K, itemsize, "fwd") + algorithmic_bytes_nd(B, C, S, K, itemsize, "bwd")
     raise ValueError(phase)
+
+
+def algorithmic_bytes_gated(B: int, H: int, L: int, K: int, itemsize: int) -> int:
+    """Compulsory HBM bytes of one gated causal FFT-conv forward + backward (Hyena layer's
+    ``(conv(q act1(k)) + s z) act2(v)``): forward reads q, k, v and writes y and the kept
+    y1 (5 tensors); backward reads g, q, k, v, y1 and writes dq, dk, dv (8 tensors); the fp32
+    filter is read by both and its gradient written once; shortcut read twice, its
+    gradient written once."""
+    E = B * H * L
+    return E * itemsize * 13 + H * K * 4 * 3 + H * itemsize * 3

@@ -1,0 +1,73 @@
+"""GPU parity of the Hyena-gated causal FFT conv (fused gates) against the CPU oracle composition.
+
+Covers the fused plan (FFT length <= 16384, one kernel each way, including the K > L+1 fold), the multi-kernel plan
+(elementwise gate kernels around the 4-step conv), every gate pair the reference configs use (SiLU / Sigmoid,
+Identity), per-sample filters and bf16 I/O.  Tolerances: rel-L2 <= 1e-4 fp32, <= 2e-2 bf16.  The reference
+computes gradients with autograd through the composition; the oracle does the same on the CPU.
+"""
+
+import pytest
+import torch
+
+from nvsubquadratic_amd.gated_fftconv_hip import hyena_gated_causal_fftconv1d_bhl
+from oracle.fftconv_ref import rel_l2
+from oracle.gated_ref import gated_causal_fftconv1d_torch
+
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(B, H, L, K, g1, g2, kb=1, dtype=torch.float32, tol=1e-4, shortcut=True, fuse_bwd=False):
+    torch.manual_seed(B * 131 + L + K)
+    q, k, v = (torch.randn(B, H, L).to(dtype).requires_grad_(True) for _ in range(3))
+    w = (torch.randn(kb, H, K) / K ** 0.5).requires_grad_(True)
+    s = torch.randn(H).to(dtype).requires_grad_(True) if shortcut else None
+    y_ref = gated_causal_fftconv1d_torch(q, k, v, w, s, g1, g2)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    qg, kg, vg, wg = (t.detach().cuda().requires_grad_(True) for t in (q, k, v, w))
+    sg = s.detach().cuda().requires_grad_(True) if shortcut else None
+    y = hyena_gated_causal_fftconv1d_bhl(qg, kg, vg, wg, sg, g1, g2, fuse_backward_gates=fuse_bwd)
+    y.backward(g.cuda())
+    assert y.dtype == dtype
+    assert rel_l2(y_ref, y) < tol
+    for ref_t, hip_t in ((q, qg), (k, kg), (v, vg), (w, wg)) + (((s, sg),) if shortcut else ()):
+        assert rel_l2(ref_t.grad, hip_t.grad) < tol
+
+
+@pytest.mark.parametrize("g1,g2", [("silu", "sigmoid"), ("identity", "identity"), ("silu", "silu"),
+                                   ("sigmoid", "identity")])
+@pytest.mark.parametrize("B,H,L,K", [(2, 16, 1024, 1024), (3, 8, 300, 17), (2, 4, 100, 180), (1, 4, 8192, 8192)])
+def test_fused_plan(B, H, L, K, g1, g2):
+    _check(B, H, L, K, g1, g2)
+    _check(B, H, L, K, g1, g2, fuse_bwd=True)  # the one-kernel gated adjoint
+
+
+@pytest.mark.parametrize("g1,g2", [("silu", "sigmoid"), ("identity", "identity")])
+@pytest.mark.parametrize("B,H,L,K", [(2, 3, 16384, 16384), (1, 2, 65536, 4000), (2, 2, 20001, 9000)])
+def test_multi_kernel_plan(B, H, L, K, g1, g2):
+    _check(B, H, L, K, g1, g2)
+
+
+@pytest.mark.parametrize("L", [2048, 32768])
+def test_per_sample_filters_and_no_shortcut(L):
+    _check(3, 4, L, 257, "silu", "sigmoid", kb=3)
+    _check(2, 4, L, 64, "silu", "sigmoid", shortcut=False)
+    _check(3, 4, L, 257, "silu", "sigmoid", kb=3, fuse_bwd=True)
+
+
+@pytest.mark.parametrize("L", [4096, 65536])
+def test_bf16_io(L):
+    _check(2, 8, L, L, "silu", "sigmoid", dtype=torch.bfloat16, tol=2e-2)
+    _check(2, 8, L, L, "silu", "sigmoid", dtype=torch.bfloat16, tol=2e-2, fuse_bwd=True)
+
+
+def test_modules_as_gates_and_default_second_gate():
+    torch.manual_seed(3)
+    q, k, v = (torch.randn(2, 4, 512, device="cuda") for _ in range(3))
+    w = torch.randn(1, 4, 512, device="cuda") / 512 ** 0.5
+    a = hyena_gated_causal_fftconv1d_bhl(q, k, v, w, None, torch.nn.SiLU())
+    b = hyena_gated_causal_fftconv1d_bhl(q, k, v, w, None, "silu", "silu")
+    assert torch.equal(a, b)
+    with pytest.raises(NotImplementedError):
+        hyena_gated_causal_fftconv1d_bhl(q, k, v, w, None, torch.nn.GELU())
