@@ -354,8 +354,9 @@ static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const voi
     constexpr int LOGF = decltype(L)::value;
     col_blocks<LOGF, 8192>(cg.inner_count, [&](auto tile, int gy, int jbase) {
       constexpr int TGT = decltype(tile)::value;
-      // the narrow tail instance takes one image per workgroup (its work per
-      // image is small, so a batch loop would leave the GPU idle)
+      // a narrow tail instance (3D blocks whose F1 * FH is not a multiple of
+      // the column tile, or 2D rows shorter than 16 bins) takes one image per
+      // workgroup: its work per image is small
       const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : mul_batch_split(p);
       const dim3 grid(unsigned((p.kb != 1 ? BH : p.H) * bsplit), unsigned(gy));
       auto go = [&](auto half, auto ramp) {
@@ -465,7 +466,7 @@ static int validate_nd(int nd, const void* a, const void* b, const float* k, int
     return NSQ_ERR_UNSUPPORTED;
   }
   if (p.spec * int64_t(sizeof(float2)) >= (int64_t(1) << 31)) {  // column passes: 32-bit offsets in a block
-    set_error("fftconv_nd: unsupported shape: one spectrum block F0*F1*(F2/2+1) = %lld complex values exceeds 2 GiB",
+    set_error("fftconv_nd: unsupported shape: one spectrum block of %lld complex values exceeds 2 GiB",
               (long long)p.spec);
     return NSQ_ERR_UNSUPPORTED;
   }

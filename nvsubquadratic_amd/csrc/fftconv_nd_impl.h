@@ -6,9 +6,15 @@
 // length F_d >= S_d + ceil(K_d/2) gives the reference's result exactly (no
 // aliasing reaches the cropped window), so each axis uses the next power of two.
 //
+// Periodic axes (circular / mixed boundaries, nvsubquadratic/ops/
+// circular_fftconv.py, mixed_fftconv.py) use F_d = S_d, no crop, and a shift
+// ramp on the filter spectrum (nd_col_mul RAMP); see the plan in
+// fftconv_nd.hip.
+//
 // Plan: the spectrum of one (b, h) image / volume is laid out in a workspace
-// block as [F0][F1][FH] (3D) or [F0][FH] (2D, F1 = 1), FH = F2/2 + 1 for the
-// last (contiguous, real) axis.  Passes:
+// block as [F0][F1][F2/2 + 1] (3D) or [F0][F2/2] (2D, F1 = 1: the rows' real DC
+// and Nyquist bins packed in bin 0, see pack_split) for the last (contiguous,
+// real) axis.  Passes:
 //   nd_row_fwd : real FFT along the last axis of the valid rows;
 //   nd_col     : complex FFT along axis 0 or 1 (strided), reading only the valid
 //                input rows (the rest is implicit zero padding) and writing
