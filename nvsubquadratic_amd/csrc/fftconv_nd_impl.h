@@ -610,6 +610,16 @@ __device__ __forceinline__ void pack_filter(bool pc0, int kf, int step, float2* 
   }
 }
 
+// Occupancy target of nd_col_mul: 4 waves per SIMD (<= 128 VGPRs) where the
+// compiler reaches it without spilling (the HALF variants' first pass holds
+// half the inputs; with a ramp but no packed column the ramp factors push it
+// over), else no bound (150 VGPRs, 3 waves).  Checked with the compiler's
+// resource report for every instantiation.
+template <int LOGF, bool HALF, bool RAMP, bool PACK>
+struct ColMulOcc {
+  static constexpr int WAVES = (HALF && (PACK || !RAMP) && LOGF >= 6 && LOGF <= 8) ? 4 : 1;
+};
+
 // Forward conv, axis 0: FFT(x col) * Khat -> IFFT -> window [c0, c0 + S0),
 // read from wsx and written to wsy (the same buffer for an in-place product).
 // Shared filter (kfilm = 0): grid.x = H * bsplit and a workgroup loops over
@@ -627,7 +637,8 @@ __device__ __forceinline__ void pack_filter(bool pc0, int kf, int step, float2* 
 // its periodic extension).  PACK (2D): the
 // inner index j = 0 is the packed DC / Nyquist column (pack_split).
 template <int LOGF, int TARGET = 8192, bool HALF = false, bool RAMP = false, bool PACK = false>
-__global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
+__global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T))
+__attribute__((amdgpu_waves_per_eu(ColMulOcc<LOGF, HALF, RAMP, PACK>::WAVES))) void nd_col_mul_kernel(const float2* wsx, float2* wsy,
                                                                                 const float2* __restrict__ wsk,
                                                                                 ColGeom cg, int B, int H, int kfilm,
                                                                                 int S0, int wm0, int c0, Ramp rf,
