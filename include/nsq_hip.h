@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 4
+#define NSQ_ABI_VERSION 5
 
 enum {
   NSQ_OK = 0,
@@ -132,6 +132,26 @@ int nsq_circular_fftconv1d_fwd(const void* x, const float* k, const void* shortc
 int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
                                float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
                                int64_t kbatch, void* stream);
+
+/*
+ * Non-causal 1D FFT convolution with a per-axis boundary (periodic bit 0):
+ *   periodic = 0: zero-padded "same" conv, replaces the reference's
+ *     fftconv1d_fp32_bhl (nvsubquadratic/ops/fftconv.py:603-660) and
+ *     mixed_fftconv1d_fp32_bhl with periodic=(False,) (ops/mixed_fftconv.py:504-630,
+ *     recipe :295-342):  y[n] = sum_j k[j] x[n + K/2 - j], x zero outside
+ *     [0, L), n in [0, L); K <= 2L; L + ceil(K/2) <= 16384, else
+ *     NSQ_ERR_UNSUPPORTED.
+ *   periodic = 1: the circular conv, as nsq_circular_fftconv1d_fwd.
+ * Then y is rounded to the I/O dtype and shortcut * x added (as the causal op).
+ * kbatch 1 or B; no workspace.  The backward writes gx, gk ([kbatch*H, K]) and,
+ * with a shortcut, gs ([kbatch*H] partial sums).
+ */
+int nsq_mixed_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                            int64_t H, int64_t L, int64_t K, int64_t kbatch, unsigned periodic, void* stream);
+
+int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                            float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                            unsigned periodic, void* stream);
 
 /*
  * Hyena-gated causal 1D FFT convolution (row F2 of the build plan): the long conv

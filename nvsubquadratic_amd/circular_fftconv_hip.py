@@ -30,7 +30,7 @@ import torch
 from einops import rearrange
 
 from . import _lib
-from .fftconv_hip import _nd_core
+from .fftconv_hip import _nd_core, shifted_fftconv1d
 
 
 __all__ = [
@@ -86,33 +86,6 @@ def circular_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int):
         _lib.dtype_code(x.dtype), B, H, L, k.shape[-1], kbatch, _lib.stream_ptr(x.device)))
 
 
-class _CircularFFTConv1d(torch.autograd.Function):
-    """x: [B, H, L] contiguous; k: [kbatch*H, K] contiguous float32; s: [H] in x.dtype or None."""
-
-    @staticmethod
-    def forward(ctx, x, k, s, kbatch):
-        y = torch.empty_like(x)
-        circular_fftconv1d_fwd_raw(x, k, s, y, kbatch)
-        ctx.save_for_backward(x, k, s)
-        ctx.kbatch = kbatch
-        ctx.has_s = s is not None
-        return y
-
-    @staticmethod
-    def backward(ctx, gy):
-        x, k, s = ctx.saved_tensors
-        g = gy.to(x.dtype).contiguous()
-        gx = torch.empty_like(x)
-        gk = torch.empty_like(k)
-        H = x.shape[1]
-        gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
-        circular_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch)
-        gsum = None
-        if ctx.has_s:
-            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
-        return gx, gk, gsum, None
-
-
 def circular_fftconv1d_fp32_bhl(
     x: torch.Tensor,
     kernel: torch.Tensor,
@@ -121,15 +94,8 @@ def circular_fftconv1d_fp32_bhl(
 ) -> torch.Tensor:
     """1D circular conv, BHL ``[B, H, L]``, kernel ``[1|B, H, K]`` (``circular_fftconv.py:310-404``)."""
     del use_phase_shift  # same result either way (see module docstring)
-    B, H, L = x.shape
     _check_common(x, kernel, shortcut, 1)
-    kbatch = kernel.shape[0]
-    input_dtype = x.dtype
-    compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
-    xc = x.to(compute_dtype).contiguous()
-    kc = kernel.float().reshape(kbatch * H, kernel.shape[-1]).contiguous()
-    sc = None if shortcut is None else shortcut.to(compute_dtype).contiguous()
-    return _CircularFFTConv1d.apply(xc, kc, sc, kbatch).to(input_dtype)
+    return shifted_fftconv1d(x, kernel, shortcut, 1)
 
 
 def circular_fftconv2d_fp32_bhl(

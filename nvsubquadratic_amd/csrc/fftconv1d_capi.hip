@@ -34,20 +34,36 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
 
 // Circular 1D: L a power of two <= 16384 (the fused plan at FFT length
 // max(L, 16)), 1 <= K <= L, kbatch 1 or B.
-static int validate_circ(const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H, int64_t L,
-                         int64_t K, int64_t kbatch, int& logN) {
-  NSQ_CHECK_ARG(a && b && k, "circular_fftconv1d: null tensor pointer");
-  NSQ_CHECK_ARG(valid_dtype(dtype), "circular_fftconv1d: unsupported dtype code %d", dtype);
-  NSQ_CHECK_ARG(B >= 1 && H >= 1 && L >= 1 && K >= 1,
-                "circular_fftconv1d: sizes must be positive (B=%lld H=%lld L=%lld K=%lld)", (long long)B, (long long)H,
-                (long long)L, (long long)K);
-  NSQ_CHECK_ARG(K <= L, "circular_fftconv1d: K must be <= L (K=%lld, L=%lld)", (long long)K, (long long)L);
-  NSQ_CHECK_ARG(kbatch == 1 || kbatch == B, "circular_fftconv1d: kernel batch must be 1 or B (got %lld, B=%lld)",
+// Shifted 1D convs on the fused plan.  zpad = false: circular, K <= L, L a
+// power of two <= 16384 (FFT length L; below 16, its periodic extension at 16).
+// zpad = true: zero-padded "same", K <= 2L, FFT length pow2(L + ceil(K/2)) <=
+// 16384.  logN = log2(FFT length) - 1.
+static int validate_shifted(const char* op, const void* a, const void* b, const float* k, int dtype, int64_t B,
+                            int64_t H, int64_t L, int64_t K, int64_t kbatch, bool zpad, int& logN) {
+  NSQ_CHECK_ARG(a && b && k, "%s: null tensor pointer", op);
+  NSQ_CHECK_ARG(valid_dtype(dtype), "%s: unsupported dtype code %d", op, dtype);
+  NSQ_CHECK_ARG(B >= 1 && H >= 1 && L >= 1 && K >= 1, "%s: sizes must be positive (B=%lld H=%lld L=%lld K=%lld)",
+                op, (long long)B, (long long)H, (long long)L, (long long)K);
+  if (zpad)
+    NSQ_CHECK_ARG(K <= 2 * L, "%s: K must be <= 2*L on a zero-padded axis (K=%lld, L=%lld)", op, (long long)K,
+                  (long long)L);
+  else
+    NSQ_CHECK_ARG(K <= L, "%s: K must be <= L (K=%lld, L=%lld)", op, (long long)K, (long long)L);
+  NSQ_CHECK_ARG(kbatch == 1 || kbatch == B, "%s: kernel batch must be 1 or B (got %lld, B=%lld)", op,
                 (long long)kbatch, (long long)B);
-  NSQ_CHECK_ARG(B * H <= 0x7fffffff && B <= 65535, "circular_fftconv1d: tensor too large");
+  NSQ_CHECK_ARG(B * H <= 0x7fffffff && B <= 65535, "%s: tensor too large", op);
+  if (zpad) {
+    const int64_t F = L + (K + 1) / 2;
+    if (F > 16384) {
+      set_error("%s: zero-padded length L + ceil(K/2) = %lld exceeds the fused kernels' FFT length 16384", op,
+                (long long)F);
+      return NSQ_ERR_UNSUPPORTED;
+    }
+    logN = (F < 16 ? 4 : ilog2_ceil(F)) - 1;
+    return NSQ_OK;
+  }
   if (L > 16384 || (L & (L - 1))) {
-    set_error("circular_fftconv1d: unsupported length L=%lld: the HIP kernels take powers of two up to 16384",
-              (long long)L);
+    set_error("%s: unsupported length L=%lld: the HIP kernels take powers of two up to 16384", op, (long long)L);
     return NSQ_ERR_UNSUPPORTED;
   }
   logN = (L < 16 ? 4 : ilog2_ceil(L)) - 1;
@@ -201,61 +217,93 @@ int nsq_fftconv1d_causal_film_bwd(const void* g, const void* x, const float* k, 
                     stream);
 }
 
-int nsq_circular_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
-                               int64_t H, int64_t L, int64_t K, int64_t kbatch, void* stream) {
+static int shifted_fwd(const char* op, const void* x, const float* k, const void* shortcut, void* y, int dtype,
+                       int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, bool zpad, void* stream) {
   clear_error();
   int logN = 0;
-  int rc = validate_circ(x, y, k, dtype, B, H, L, K, kbatch, logN);
+  int rc = validate_shifted(op, x, y, k, dtype, B, H, L, K, kbatch, zpad, logN);
   if (rc) return rc;
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
   const int kf = kbatch != 1;
+  const int c = zpad ? int(K / 2) : int((K - 1) / 2);
   bool ok = false;
   switch (dtype) {
     case NSQ_DTYPE_F32:
-      ok = run_circ_fwd<NSQ_DTYPE_F32>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, tw, st);
+      ok = run_circ_fwd<NSQ_DTYPE_F32>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, c, zpad, tw, st);
       break;
     case NSQ_DTYPE_BF16:
-      ok = run_circ_fwd<NSQ_DTYPE_BF16>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, tw, st);
+      ok = run_circ_fwd<NSQ_DTYPE_BF16>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, c, zpad, tw, st);
       break;
     default:
-      ok = run_circ_fwd<NSQ_DTYPE_F16>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, tw, st);
+      ok = run_circ_fwd<NSQ_DTYPE_F16>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, c, zpad, tw, st);
       break;
   }
-  NSQ_CHECK_ARG(ok, "circular_fftconv1d_fwd: no kernel for logN=%d", logN);
+  NSQ_CHECK_ARG(ok, "%s: no kernel for logN=%d", op, logN);
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
+}
+
+static int shifted_bwd(const char* op, const void* g, const void* x, const float* k, const void* shortcut, void* gx,
+                       float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                       bool zpad, void* stream) {
+  clear_error();
+  int logN = 0;
+  int rc = validate_shifted(op, g, x, k, dtype, B, H, L, K, kbatch, zpad, logN);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(gx && gk, "%s: null gradient output pointer", op);
+  NSQ_CHECK_ARG(!shortcut || gs, "%s: gs required when a shortcut is given", op);
+  const float2* tw = twiddle_table();
+  if (!tw) return NSQ_ERR_HIP;
+  hipStream_t st = (hipStream_t)stream;
+  const int kf = kbatch != 1;
+  const int c = zpad ? int(K / 2) : int((K - 1) / 2);
+  const int b = int(B), h = int(H), l = int(L), kk = int(K);
+  bool ok = false;
+  switch (dtype) {
+    case NSQ_DTYPE_F32:
+      ok = run_circ_bwd<NSQ_DTYPE_F32>(logN, g, x, k, shortcut, gx, gk, gs, b, h, l, kk, kf, c, zpad, tw, st);
+      break;
+    case NSQ_DTYPE_BF16:
+      ok = run_circ_bwd<NSQ_DTYPE_BF16>(logN, g, x, k, shortcut, gx, gk, gs, b, h, l, kk, kf, c, zpad, tw, st);
+      break;
+    default:
+      ok = run_circ_bwd<NSQ_DTYPE_F16>(logN, g, x, k, shortcut, gx, gk, gs, b, h, l, kk, kf, c, zpad, tw, st);
+      break;
+  }
+  NSQ_CHECK_ARG(ok, "%s: no kernel for logN=%d", op, logN);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+int nsq_circular_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                               int64_t H, int64_t L, int64_t K, int64_t kbatch, void* stream) {
+  return shifted_fwd("circular_fftconv1d_fwd", x, k, shortcut, y, dtype, B, H, L, K, kbatch, false, stream);
 }
 
 int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
                                float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
                                int64_t kbatch, void* stream) {
+  return shifted_bwd("circular_fftconv1d_bwd", g, x, k, shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, false,
+                     stream);
+}
+
+int nsq_mixed_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+                            int64_t H, int64_t L, int64_t K, int64_t kbatch, unsigned periodic, void* stream) {
   clear_error();
-  int logN = 0;
-  int rc = validate_circ(g, x, k, dtype, B, H, L, K, kbatch, logN);
-  if (rc) return rc;
-  NSQ_CHECK_ARG(gx && gk, "circular_fftconv1d_bwd: null gradient output pointer");
-  NSQ_CHECK_ARG(!shortcut || gs, "circular_fftconv1d_bwd: gs required when a shortcut is given");
-  const float2* tw = twiddle_table();
-  if (!tw) return NSQ_ERR_HIP;
-  hipStream_t st = (hipStream_t)stream;
-  const int kf = kbatch != 1;
-  bool ok = false;
-  switch (dtype) {
-    case NSQ_DTYPE_F32:
-      ok = run_circ_bwd<NSQ_DTYPE_F32>(logN, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, tw, st);
-      break;
-    case NSQ_DTYPE_BF16:
-      ok = run_circ_bwd<NSQ_DTYPE_BF16>(logN, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, tw, st);
-      break;
-    default:
-      ok = run_circ_bwd<NSQ_DTYPE_F16>(logN, g, x, k, shortcut, gx, gk, gs, int(B), int(H), int(L), int(K), kf, tw, st);
-      break;
-  }
-  NSQ_CHECK_ARG(ok, "circular_fftconv1d_bwd: no kernel for logN=%d", logN);
-  NSQ_CHECK_LAUNCH();
-  return NSQ_OK;
+  NSQ_CHECK_ARG(periodic <= 1u, "mixed_fftconv1d_fwd: periodic mask 0x%x names an axis >= 1", periodic);
+  return shifted_fwd(periodic ? "mixed_fftconv1d_fwd (periodic)" : "mixed_fftconv1d_fwd (zero-padded)", x, k,
+                     shortcut, y, dtype, B, H, L, K, kbatch, periodic == 0, stream);
+}
+
+int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+                            float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                            unsigned periodic, void* stream) {
+  clear_error();
+  NSQ_CHECK_ARG(periodic <= 1u, "mixed_fftconv1d_bwd: periodic mask 0x%x names an axis >= 1", periodic);
+  return shifted_bwd(periodic ? "mixed_fftconv1d_bwd (periodic)" : "mixed_fftconv1d_bwd (zero-padded)", g, x, k,
+                     shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, periodic == 0, stream);
 }
 
 size_t nsq_gated_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,

@@ -943,11 +943,15 @@ static void launch_gated_fused_bwd(const Plan1D& p, const void* g, const void* q
                        (const ET*)q, k, (const ET*)s, (ET*)dq, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, ga);
 }
 
-// Circular 1D (fused plan at FFT length L = 2N): shift c = (K-1)/2; kfilm =
-// per-image filters [B, H, K] (one image per workgroup).
+// Shifted 1D convs on the fused plan, output rolled by -c through the filter
+// ramp (circ_ramp); kfilm = per-image filters [B, H, K] (one image per
+// workgroup).  zpad = false: circular conv at FFT length L = 2N (or its
+// periodic extension), c = (K-1)/2.  zpad = true: the zero-padded "same" conv,
+// x zero-extended from L to 2N >= L + ceil(K/2), c = K/2 (no sample wraps
+// into the output window [0, L), see nsq_mixed_fftconv1d_fwd).
 template <int LOGN, int DT>
 static void launch_circ_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
-                            int kfilm, const float2* tw, hipStream_t st) {
+                            int kfilm, int c, bool zpad, const float2* tw, hipStream_t st) {
   using C = FusedCfg<LOGN>;
   using ET = typename Elem<DT>::T;
   const int gh = int(ceil_div(H, C::M));
@@ -959,20 +963,21 @@ static void launch_circ_fwd(const void* x, const float* k, const void* s, void* 
   }
   const dim3 grid(gh, unsigned(ceil_div(B, bpw)));
   // a period shorter than the transform: periodic extension (L = 1, K = 1: plain zero padding is exact)
-  const int wm = (L > 1 && L < 2 * C::N) ? L - 1 : -1;
+  const int wm = (!zpad && L > 1 && L < 2 * C::N) ? L - 1 : -1;
   hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)x, k,
-                     (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, (K - 1) / 2, kfilm, wm, GateArgs{});
+                     (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, c, kfilm, wm, GateArgs{});
 }
 
 template <int LOGN, int DT>
 static void launch_circ_bwd(const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
-                            float* gs, int B, int H, int L, int K, int kfilm, const float2* tw, hipStream_t st) {
+                            float* gs, int B, int H, int L, int K, int kfilm, int c, bool zpad, const float2* tw,
+                            hipStream_t st) {
   using C = FusedCfg<LOGN>;
   using ET = typename Elem<DT>::T;
   const dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
-  const int wm = (L > 1 && L < 2 * C::N) ? L - 1 : -1;
+  const int wm = (!zpad && L > 1 && L < 2 * C::N) ? L - 1 : -1;
   hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
-                     (const ET*)x, k, (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, (K - 1) / 2, kfilm, wm,
+                     (const ET*)x, k, (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, c, kfilm, wm,
                      wm == -1 ? 1.f : float(L) / float(2 * C::N), GateArgs{});
 }
 
@@ -1228,15 +1233,17 @@ bool run_gated_bwd(const Plan1D& p, const void* g, const void* q, const float* k
 // L < 16 runs at transform length 16 on the periodic extension).
 template <int DT>
 bool run_circ_fwd(int logN, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
-                  int kfilm, const float2* tw, hipStream_t st) {
-  return dispatch_int<CircFused<DT, false>::template At, 3, 13>(logN, x, k, s, y, B, H, L, K, kfilm, tw, st);
+                  int kfilm, int c, bool zpad, const float2* tw, hipStream_t st) {
+  return dispatch_int<CircFused<DT, false>::template At, 3, 13>(logN, x, k, s, y, B, H, L, K, kfilm, c, zpad, tw,
+                                                                st);
 }
 
 template <int DT>
 bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
-                  float* gs, int B, int H, int L, int K, int kfilm, const float2* tw, hipStream_t st) {
-  return dispatch_int<CircFused<DT, true>::template At, 3, 13>(logN, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, tw,
-                                                               st);
+                  float* gs, int B, int H, int L, int K, int kfilm, int c, bool zpad, const float2* tw,
+                  hipStream_t st) {
+  return dispatch_int<CircFused<DT, true>::template At, 3, 13>(logN, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, c,
+                                                               zpad, tw, st);
 }
 
 #define NSQ_DECLARE_FFTCONV1D(DT)                                                                               \
@@ -1246,9 +1253,9 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
                                    float*, float*, int, int, int, int, int, float2*, bool, const float2*,       \
                                    hipStream_t);                                                                \
   extern template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, \
-                                        int, const float2*, hipStream_t);                                       \
+                                        int, int, bool, const float2*, hipStream_t);                            \
   extern template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, \
-                                        float*, int, int, int, int, int, const float2*, hipStream_t);          \
+                                        float*, int, int, int, int, int, int, bool, const float2*, hipStream_t); \
   extern template bool run_gated_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, \
                                          int, int, int, const GateArgs&, void*, float2*, const float2*,         \
                                          hipStream_t);                                                          \
@@ -1263,9 +1270,9 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
                             float*, float*, int, int, int, int, int, float2*, bool, const float2*,       \
                             hipStream_t);                                                                \
   template bool run_circ_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, int, \
-                                 const float2*, hipStream_t);                                               \
+                                 int, bool, const float2*, hipStream_t);                                    \
   template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, float*, \
-                                 int, int, int, int, int, const float2*, hipStream_t);                         \
+                                 int, int, int, int, int, int, bool, const float2*, hipStream_t);              \
   template bool run_gated_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, int, \
                                   int, const GateArgs&, void*, float2*, const float2*, hipStream_t);             \
   template bool run_gated_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,      \

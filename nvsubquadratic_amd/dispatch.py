@@ -9,8 +9,8 @@ with the same contract:
 
 * :data:`FFT_BACKENDS` extends the accepted set to ``("torch_fft", "subq_ops", "hip")``;
 * :func:`validate_hip_backend` raises the reference's exception types for the
-  combinations the HIP kernels do not cover: 1D must be causal or circular;
-  2D/3D must be non-causal (zero, circular or a per-axis list);
+  combinations the HIP kernels do not cover: 2D/3D must be non-causal (1D
+  takes causal, zero, circular or a per-axis list);
 * :func:`hip_fftconv_fns` returns ``(fftconv_fn, fftconv_fn_bhl_input)``, the
   pair CKConvND stores and calls in ``apply_convolution``
   (``ckconv_nd.py:1054-1062``): the causal / zero-padded ops of
@@ -88,7 +88,7 @@ def resolve_periodic(fft_padding, data_dim: int) -> tuple[bool, ...]:
 def validate_hip_backend(data_dim: int, is_causal: bool, fft_padding, use_chunked_fftconv: bool = False) -> None:
     """Constraint block of the hip backend (the checks of ``ckconv_nd.py:690-724`` for what HIP covers).
 
-    1D: ``is_causal=True``, or non-causal with ``fft_padding="circular"``;
+    1D: causal, or non-causal with ``"zero"``, ``"circular"`` or a per-axis list;
     2D and 3D: ``is_causal=False`` with ``"zero"``, ``"circular"`` or a per-axis
     list.  ``"circular"`` (string form) takes no chunked variant, as in the
     reference (``:695-699``).
@@ -101,12 +101,6 @@ def validate_hip_backend(data_dim: int, is_causal: bool, fft_padding, use_chunke
             "use_chunked_fftconv=True is not supported with fft_padding='circular'. Chunked FFT convolutions "
             "are only implemented for 'zero' padding (and 'causal' 1D).")
     if data_dim == 1:
-        if is_causal:
-            return
-        assert all(periodic), (
-            "fft_backend='hip' on 1D requires is_causal=True or fft_padding='circular' "
-            "(no non-causal zero-padded 1D HIP kernel is wired). Got is_causal=False."
-        )
         return
     assert not is_causal, (
         f"fft_backend='hip' on {data_dim}D does not support causal convolutions (causal is 1D only)."
@@ -155,6 +149,10 @@ def hip_fftconv_fns(data_dim: int, is_causal: bool, fft_padding="zero", use_chun
             2: (C.circular_fftconv2d_fp32_bhl_w_reshape, C.circular_fftconv2d_fp32_bhl),
             3: (C.circular_fftconv3d_fp32_bhl_w_reshape, C.circular_fftconv3d_fp32_bhl),
         }[data_dim]
+    if data_dim == 1:
+        if use_chunked_fftconv:
+            return F.fftconv1d_bhl_w_reshape_chunked, F.fftconv1d_bhl_chunked
+        return F.fftconv1d_bhl_w_reshape, F.fftconv1d_bhl
     if data_dim == 2:
         if use_chunked_fftconv:
             return F.fftconv2d_bhl_w_reshape_chunked, F.fftconv2d_bhl_chunked

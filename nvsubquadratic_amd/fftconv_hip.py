@@ -38,6 +38,14 @@ __all__ = [
     "causal_fftconv1d_blh_chunked",
     "causal_fftconv1d_fwd_raw",
     "causal_fftconv1d_bwd_raw",
+    "fftconv1d_bhl",
+    "fftconv1d_bhl_chunked",
+    "fftconv1d_bhl_w_reshape",
+    "fftconv1d_bhl_w_reshape_chunked",
+    "fftconv1d_blh",
+    "fftconv1d_blh_chunked",
+    "mixed_fftconv1d_fwd_raw",
+    "mixed_fftconv1d_bwd_raw",
     "fftconv2d_bhl",
     "fftconv2d_bhl_chunked",
     "fftconv2d_bhl_w_reshape",
@@ -471,6 +479,123 @@ def _chunked(fn, x, kernel, shortcut, chunk_size, nd):
         end = min(start + chunk_size, H)
         outs.append(fn(x[:, start:end], k[:, start:end], None if shortcut is None else shortcut[start:end]))
     return torch.cat(outs, dim=1)
+
+
+# ---------------------------------------------------------------------------
+# Non-causal 1D on the fused kernels: zero-padded "same" (periodic 0) or
+# circular (periodic 1), both an output shift through the filter's ramp.
+# ---------------------------------------------------------------------------
+def mixed_fftconv1d_fwd_raw(x, k, s, y, kbatch: int, periodic: int):
+    """Launch ``nsq_mixed_fftconv1d_fwd``: x/y ``[B, H, L]``, k float32 ``[kbatch*H, K]``, s ``[H]`` or None."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, H, L = x.shape
+    _lib.check(lib.nsq_mixed_fftconv1d_fwd(
+        x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype), B, H, L, k.shape[-1],
+        kbatch, int(periodic), _lib.stream_ptr(x.device)))
+    return y
+
+
+def mixed_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, periodic: int):
+    """Launch ``nsq_mixed_fftconv1d_bwd`` (gk ``[kbatch*H, K]``, gs ``[kbatch*H]`` partials or None)."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, H, L = x.shape
+    _lib.check(lib.nsq_mixed_fftconv1d_bwd(
+        g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
+        _lib.dtype_code(x.dtype), B, H, L, k.shape[-1], kbatch, int(periodic), _lib.stream_ptr(x.device)))
+
+
+class _ShiftedFFTConv1d(torch.autograd.Function):
+    """x: [B, H, L] contiguous; k: [kbatch*H, K] contiguous float32; s: [H] in x.dtype or None."""
+
+    @staticmethod
+    def forward(ctx, x, k, s, kbatch, periodic):
+        y = torch.empty_like(x)
+        mixed_fftconv1d_fwd_raw(x, k, s, y, kbatch, periodic)
+        ctx.save_for_backward(x, k, s)
+        ctx.kbatch, ctx.periodic = kbatch, periodic
+        ctx.has_s = s is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, k, s = ctx.saved_tensors
+        g = gy.to(x.dtype).contiguous()
+        gx = torch.empty_like(x)
+        gk = torch.empty_like(k)
+        H = x.shape[1]
+        gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
+        mixed_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch, ctx.periodic)
+        gsum = None
+        if ctx.has_s:
+            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
+        return gx, gk, gsum, None, None
+
+
+def shifted_fftconv1d(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, periodic: int):
+    """Cast and launch the 1D shifted conv (shapes already checked): kernel ``[1|B, H, K]``."""
+    B, H, L = x.shape
+    kbatch = kernel.shape[0]
+    input_dtype = x.dtype
+    compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
+    xc = x.to(compute_dtype).contiguous()
+    kc = kernel.float().reshape(kbatch * H, kernel.shape[-1]).contiguous()
+    sc = None if shortcut is None else shortcut.to(compute_dtype).contiguous()
+    return _ShiftedFFTConv1d.apply(xc, kc, sc, kbatch, int(periodic)).to(input_dtype)
+
+
+def fftconv1d_bhl(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None = None) -> torch.Tensor:
+    """1D zero-padded non-causal ("same") FFT conv, BHL ``[B, H, L]`` (``fftconv.py:603-660``).
+
+    ``y[n] = sum_j k[j] x[n + K//2 - j]`` with x zero outside ``[0, L)``, cast to
+    ``x.dtype``, then ``+ shortcut * x``.  Kernel ``[1|B, H, K]``, ``K <= 2L``.
+    Runs the fused 1D kernels (``nsq_mixed_fftconv1d_*`` with ``periodic=0``) at
+    FFT length ``pow2(L + ceil(K/2))`` (the reference's ``L + (K+1)//2`` is the
+    same result: every length from there on keeps the output window free of
+    wrap-around); lengths above 16384 raise ``NotImplementedError``.
+    """
+    batch_size, hidden_dim, seq_len = x.shape
+    assert len(kernel.shape) == 3, f"Unexpected kernel shape: {kernel.shape}."
+    assert kernel.shape[0] in (1, batch_size), (
+        f"Leading dimension must be 1 or batch_size ({batch_size}). Got kernel.shape={kernel.shape}."
+    )
+    kernel_len = kernel.shape[-1]
+    assert kernel_len <= 2 * seq_len, f"Kernel length must be less than or equal to 2 * seq_len. Got {kernel_len}."
+    if kernel.shape[1] != hidden_dim:
+        raise ValueError(f"kernel has {kernel.shape[1]} channels, x has {hidden_dim}")
+    if shortcut is not None:
+        assert shortcut.dtype == x.dtype, f"shortcut.dtype ({shortcut.dtype}) must match x.dtype ({x.dtype})"
+        assert shortcut.shape == (hidden_dim,)
+    return shifted_fftconv1d(x, kernel, shortcut, 0)
+
+
+def fftconv1d_bhl_w_reshape(x, kernel, shortcut=None):
+    """BLH ``[B, L, H]`` input, kernel ``[1|B, K, H]`` (``fftconv.py:476-500``)."""
+    y = fftconv1d_bhl(rearrange(x, "b l h -> b h l"), rearrange(kernel, "b l h -> b h l"), shortcut)
+    return rearrange(y, "b h l -> b l h")
+
+
+def fftconv1d_blh(x, kernel, shortcut=None):
+    """Alias for :func:`fftconv1d_bhl_w_reshape` (``fftconv.py:235``)."""
+    return fftconv1d_bhl_w_reshape(x, kernel, shortcut)
+
+
+def fftconv1d_bhl_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Channel-chunked zero-padded 1D (``fftconv_chunked.py:245-280``); bitwise equal to unchunked."""
+    return _chunked(fftconv1d_bhl, x, kernel, shortcut, chunk_size, 1)
+
+
+def fftconv1d_bhl_w_reshape_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Chunked BLH zero-padded 1D."""
+    y = fftconv1d_bhl_chunked(rearrange(x, "b l h -> b h l"), rearrange(kernel, "b l h -> b h l"), shortcut,
+                              chunk_size)
+    return rearrange(y, "b h l -> b l h")
+
+
+def fftconv1d_blh_chunked(x, kernel, shortcut=None, chunk_size=None):
+    """Alias for :func:`fftconv1d_bhl_w_reshape_chunked`."""
+    return fftconv1d_bhl_w_reshape_chunked(x, kernel, shortcut, chunk_size)
 
 
 def fftconv2d_bhl(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None = None) -> torch.Tensor:

@@ -9,9 +9,10 @@ route to the circular or zero-padded op exactly as the reference's
 ``_dispatch_legacy_if_uniform`` (``:445-501``).
 
 How: one call of the HIP N-d engine with the per-axis mask
-(``nsq_mixed_fftconv_nd_*``; bit d = axis d periodic).  1D supports
-``periodic=(True,)`` (the circular op); the zero-padded non-causal 1D op has no
-HIP kernel and raises ``NotImplementedError``.
+(``nsq_mixed_fftconv_nd_*``; bit d = axis d periodic).  1D runs the fused 1D
+kernels with the output shift on the filter's spectrum
+(``nsq_mixed_fftconv1d_*``): ``periodic=(True,)`` the circular op,
+``periodic=(False,)`` the zero-padded one (``fftconv_hip.fftconv1d_bhl``).
 """
 
 from __future__ import annotations
@@ -82,11 +83,7 @@ def _mixed_core(x, kernel, periodic_t, shortcut, use_phase_shift, data_dim):
               _circ.circular_fftconv3d_fp32_bhl)[data_dim - 1]
         return fn(x, kernel, shortcut, use_phase_shift=use_phase_shift)
     if not any(periodic_t):
-        if data_dim == 1:
-            raise NotImplementedError(
-                "fft_backend='hip' has no non-causal zero-padded 1D FFT conv (mixed periodic=(False,)); "
-                "1D is served causal (fftconv_hip.causal_fftconv1d_bhl) or circular.")
-        return (_zero.fftconv2d_bhl, _zero.fftconv3d_bhl)[data_dim - 2](x, kernel, shortcut)
+        return (_zero.fftconv1d_bhl, _zero.fftconv2d_bhl, _zero.fftconv3d_bhl)[data_dim - 1](x, kernel, shortcut)
     if shortcut is not None:
         assert shortcut.dtype == x.dtype, f"shortcut.dtype ({shortcut.dtype}) must match x.dtype ({x.dtype})"
         assert shortcut.shape == (H,), f"Expected shortcut shape ({H},), got {tuple(shortcut.shape)}"

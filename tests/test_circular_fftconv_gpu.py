@@ -221,8 +221,7 @@ def test_mixed_uniform_cases_route_to_zero_and_circular_ops():
     x1 = torch.randn(2, 8, 128, device="cuda")
     k1 = torch.randn(1, 8, 9, device="cuda")
     assert torch.equal(M.mixed_fftconv1d_fp32_bhl(x1, k1, (True,)), C.circular_fftconv1d_fp32_bhl(x1, k1))
-    with pytest.raises(NotImplementedError):
-        M.mixed_fftconv1d_fp32_bhl(x1, k1, (False,))
+    assert torch.equal(M.mixed_fftconv1d_fp32_bhl(x1, k1, (False,)), Z.fftconv1d_bhl(x1, k1))
 
 
 @pytest.mark.parametrize("periodic", COMBOS_2D)

@@ -36,8 +36,6 @@ def test_backend_name_validation():
 
 
 def test_hip_constraints_mirror_reference_messages():
-    with pytest.raises(AssertionError, match="requires is_causal=True"):
-        dispatch.validate_hip_backend(1, False, "zero")
     with pytest.raises(AssertionError, match="does not support causal"):
         dispatch.validate_hip_backend(2, True, "zero")
     with pytest.raises(AssertionError, match="does not support causal"):
@@ -46,6 +44,8 @@ def test_hip_constraints_mirror_reference_messages():
         dispatch.validate_hip_backend(2, False, "circular", use_chunked_fftconv=True)
     with pytest.raises(AssertionError, match="data_dim"):
         dispatch.validate_hip_backend(4, False, "zero")
+    dispatch.validate_hip_backend(1, False, "zero")
+    dispatch.validate_hip_backend(1, False, "zero", use_chunked_fftconv=True)
     dispatch.validate_hip_backend(1, False, "circular")
     dispatch.validate_hip_backend(1, False, ["circular"])
     dispatch.validate_hip_backend(3, False, "circular")
@@ -68,6 +68,10 @@ def test_hip_fn_selection():
     assert dispatch.hip_fftconv_fns(1, True) == (F.causal_fftconv1d_bhl_w_reshape, F.causal_fftconv1d_bhl)
     assert dispatch.hip_fftconv_fns(1, True, use_chunked_fftconv=True) == (
         F.causal_fftconv1d_bhl_w_reshape_chunked, F.causal_fftconv1d_bhl_chunked)
+    # non-causal 1D: FFT_FUNCTIONS["zero"][1] (ckconv_nd.py:208-211) and its chunked table entry
+    assert dispatch.hip_fftconv_fns(1, False, "zero") == (F.fftconv1d_bhl_w_reshape, F.fftconv1d_bhl)
+    assert dispatch.hip_fftconv_fns(1, False, "zero", use_chunked_fftconv=True) == (
+        F.fftconv1d_bhl_w_reshape_chunked, F.fftconv1d_bhl_chunked)
 
 
 def test_hip_fn_selection_2d_3d():

@@ -127,6 +127,27 @@ def test_mixed_restatement_matches_brute_force(xs, ks, per):
     assert rel_l2(ref, yt) < 1e-5
 
 
+@pytest.mark.parametrize("L,K", [(16, 5), (16, 6), (9, 18), (7, 1), (1, 2), (33, 20)])
+def test_mixed_1d_zero_padded_is_numpy_full_convolution_cropped(L, K):
+    """1D periodic=(False,) ("same", ops/fftconv.py:603-660): numpy's full linear convolution sliced at
+    [K//2, K//2 + L) (not numpy's own mode="same", which crops at (K-1)//2); the FFT restatement agrees."""
+    rng = np.random.default_rng(L * 31 + K)
+    x = rng.standard_normal((2, 3, L))
+    k = rng.standard_normal((1, 3, K))
+    s = rng.standard_normal(3)
+    ref = np.stack([[np.convolve(x[b, h], k[0, h])[K // 2:K // 2 + L] + s[h] * x[b, h] for h in range(3)]
+                    for b in range(2)])
+    assert rel_l2(ref, mixed_conv_direct_np(x, k, (False,), s)) < 1e-13
+    yt = mixed_fftconv_torch(torch.tensor(x), torch.tensor(k), (False,), torch.tensor(s), compute_dtype=torch.float64)
+    assert rel_l2(ref, yt) < 1e-12
+    # periodic=(True,) (K <= L) is the circular wrap of the same sum
+    if K <= L:
+        c = (K - 1) // 2
+        refc = np.stack([[sum(k[0, h, j] * np.roll(x[b, h], j - c) for j in range(K)) for h in range(3)]
+                         for b in range(2)])
+        assert rel_l2(refc, mixed_conv_direct_np(x, k, (True,))) < 1e-13
+
+
 @pytest.mark.parametrize("xs,ks", [((2, 2, 9, 7), (1, 2, 5, 3)), ((1, 2, 5, 6, 4), (1, 2, 3, 4, 8))])
 def test_mixed_brute_force_uniform_cases(xs, ks):
     """All periodic = the circular brute force; all zero = the zero-padded "same" restatement."""
