@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 5
+#define NSQ_ABI_VERSION 6
 
 enum {
   NSQ_OK = 0,
@@ -190,6 +190,31 @@ int nsq_gated_fftconv1d_causal_bwd(const void* g, const void* q, const void* k_g
                                    float* gs, int dtype, int act1, int act2, int64_t B, int64_t H, int64_t L,
                                    int64_t K, int64_t kbatch, int fuse_gates, void* workspace, size_t workspace_bytes,
                                    void* stream);
+
+/*
+ * Hyena-gated 2D/3D FFT convolution (row F2 for the N-d layers,
+ * nvsubquadratic/modules/hyena_nd.py:546-570 around the CKConvND global conv,
+ * ckconv_nd.py:1054-1062): z = q act1(k_gate), y1 = conv_nd(z) + shortcut z,
+ * y = y1 act2(v), with the N-d conv of nsq_mixed_fftconv_nd_fwd (periodic mask,
+ * 0 = zero-padded "same" on every axis).  The gates run as elementwise kernels
+ * around the conv; each product is rounded to the I/O dtype.  y1 (may be null)
+ * keeps the pre-gate output for the backward.  Tensors are 16-byte aligned.
+ * The backward recomputes z and writes dq, dk_gate, dv (I/O dtype), gk
+ * [kbatch*H, prod K] and, with a shortcut, gs [kbatch*H] partials.
+ */
+size_t nsq_gated_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
+                                            int64_t kbatch, unsigned periodic, int dtype, int direction);
+
+int nsq_gated_fftconv_nd_fwd(int nd, const void* q, const void* k_gate, const void* v, const float* k,
+                             const void* shortcut, void* y, void* y1, int dtype, int act1, int act2, int64_t B,
+                             int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, unsigned periodic,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+int nsq_gated_fftconv_nd_bwd(int nd, const void* g, const void* q, const void* k_gate, const void* v, const void* y1,
+                             const float* k, const void* shortcut, void* dq, void* dk_gate, void* dv, float* gk,
+                             float* gs, int dtype, int act1, int act2, int64_t B, int64_t H, const int64_t* S,
+                             const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 /*
  * Depthwise causal direct convolution, nn.Conv1d tap order with left padding

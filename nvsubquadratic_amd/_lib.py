@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class HipLibraryError(RuntimeError):
@@ -90,6 +90,19 @@ _SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_void_p,
          _c_size, _c_void_p],
+    ),
+    "nsq_gated_fftconv_nd_workspace_bytes": (
+        _c_size, [_c_int, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_uint, _c_int, _c_int]),
+    "nsq_gated_fftconv_nd_fwd": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_uint, _c_void_p, _c_size, _c_void_p],
+    ),
+    "nsq_gated_fftconv_nd_bwd": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_uint,
+         _c_void_p, _c_size, _c_void_p],
     ),
     "nsq_circular_fftconv1d_fwd": (
         _c_int,

@@ -26,10 +26,12 @@ import torch
 
 from . import _lib
 from .fftconv_hip import _kernel_3d, _workspace
+from .mixed_fftconv_hip import periodic_mask
 
 
 __all__ = ["GATE_CODES", "gate_code", "hyena_gated_causal_fftconv1d_bhl", "gated_causal_fftconv1d_fwd_raw",
-           "gated_causal_fftconv1d_bwd_raw"]
+           "gated_causal_fftconv1d_bwd_raw", "hyena_gated_fftconv2d_bhl", "hyena_gated_fftconv3d_bhl",
+           "hyena_gated_fftconv_nd_bhl"]
 
 GATE_CODES = {"identity": 0, "sigmoid": 1, "silu": 2}
 _MODULE_CODES = {torch.nn.Identity: 0, torch.nn.Sigmoid: 1, torch.nn.SiLU: 2}
@@ -151,3 +153,106 @@ def hyena_gated_causal_fftconv1d_bhl(
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         sc = shortcut.to(in_dtype).to(cdt).contiguous()
     return _GatedCausalFFTConv1d.apply(q, kg, v, kc, sc, act1, act2, kbatch, fuse_backward_gates).to(in_dtype)
+
+
+# ---------------------------------------------------------------------------
+# 2D / 3D: the gate kernels around the N-d conv (nsq_gated_fftconv_nd_*)
+# ---------------------------------------------------------------------------
+class _GatedFFTConvND(torch.autograd.Function):
+    """q, kg, v: [B, H, *S] contiguous; k: [kbatch*H, *K] contiguous float32; s: [H] or None."""
+
+    @staticmethod
+    def forward(ctx, q, kg, v, k, s, act1, act2, kbatch, periodic):
+        lib = _lib.get_lib()
+        _lib.check_device(q)
+        nd = q.ndim - 2
+        B, H = q.shape[:2]
+        S, K = _lib.i64_array(q.shape[2:]), _lib.i64_array(k.shape[1:])
+        dt = _lib.dtype_code(q.dtype)
+        y = torch.empty_like(q)
+        keep = any(ctx.needs_input_grad[:5])
+        y1 = torch.empty_like(q) if keep else None
+        ws = _workspace(q.device, lib.nsq_gated_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dt,
+                                                                            _lib.NSQ_DIR_FWD))
+        _lib.check(lib.nsq_gated_fftconv_nd_fwd(
+            nd, q.data_ptr(), kg.data_ptr(), v.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.ptr(y1), dt,
+            act1, act2, B, H, S, K, kbatch, periodic, _lib.ptr(ws), 0 if ws is None else ws.numel(),
+            _lib.stream_ptr(q.device)))
+        ctx.save_for_backward(q, kg, v, y1, k, s)
+        ctx.meta = (act1, act2, kbatch, periodic)
+        ctx.has_s = s is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        q, kg, v, y1, k, s = ctx.saved_tensors
+        act1, act2, kbatch, periodic = ctx.meta
+        lib = _lib.get_lib()
+        nd = q.ndim - 2
+        B, H = q.shape[:2]
+        S, K = _lib.i64_array(q.shape[2:]), _lib.i64_array(k.shape[1:])
+        dt = _lib.dtype_code(q.dtype)
+        g = gy.to(q.dtype).contiguous()
+        dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+        gk = torch.empty_like(k)
+        gs = torch.empty(kbatch * H, dtype=torch.float32, device=q.device) if ctx.has_s else None
+        ws = _workspace(q.device, lib.nsq_gated_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dt,
+                                                                            _lib.NSQ_DIR_BWD))
+        _lib.check(lib.nsq_gated_fftconv_nd_bwd(
+            nd, g.data_ptr(), q.data_ptr(), kg.data_ptr(), v.data_ptr(), y1.data_ptr(), k.data_ptr(), _lib.ptr(s),
+            dq.data_ptr(), dkg.data_ptr(), dv.data_ptr(), gk.data_ptr(), _lib.ptr(gs), dt, act1, act2, B, H, S, K,
+            kbatch, periodic, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_ptr(q.device)))
+        gsum = None
+        if ctx.has_s:
+            gsum = (gs if kbatch == 1 else gs.view(kbatch, H).sum(0)).to(s.dtype)
+        return dq, dkg, dv, gk, gsum, None, None, None, None
+
+
+def hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut=None, gate_nonlinear="silu",
+                               gate_nonlinear_2=None, periodic=None) -> torch.Tensor:
+    """``(conv(q*act1(k)) + s*(q*act1(k))) * act2(v)`` for ``[B, H, *S]`` q, k, v (2D or 3D), with the
+    non-causal N-d conv of CKConvND: ``periodic`` per axis (None = all zero-padded "same").
+
+    ``kernel``: ``[1|B, H, *K]`` or ``[H, *K]`` (``K_d <= 2 S_d`` zero-padded, ``K_d <= S_d`` periodic);
+    ``shortcut``: ``[H]`` or None.  Returns ``query.dtype``.
+    """
+    if query.ndim not in (4, 5) or key.shape != query.shape or value.shape != query.shape:
+        raise ValueError(f"query, key, value must share one [B, H, *S] shape (2D or 3D); got {tuple(query.shape)}, "
+                         f"{tuple(key.shape)}, {tuple(value.shape)}")
+    nd = query.ndim - 2
+    B, H = query.shape[:2]
+    per = (False,) * nd if periodic is None else tuple(bool(p) for p in periodic)
+    if len(per) != nd:
+        raise ValueError(f"periodic must have {nd} entries; got {per}")
+    act1 = gate_code(gate_nonlinear)
+    act2 = act1 if gate_nonlinear_2 is None else gate_code(gate_nonlinear_2)
+    k = kernel if kernel.ndim == nd + 2 else kernel.unsqueeze(0)
+    if k.ndim != nd + 2 or k.shape[0] not in (1, B) or k.shape[1] != H:
+        raise ValueError(f"kernel must be [1|B, H, *K] or [H, *K]; got {tuple(kernel.shape)}")
+    kbatch = k.shape[0]
+    in_dtype = query.dtype
+    cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
+    q, kg, v = (t.to(cdt).contiguous() for t in (query, key, value))
+    kc = k.float().reshape(kbatch * H, *k.shape[2:]).contiguous()
+    sc = None
+    if shortcut is not None:
+        if shortcut.shape != (H,):
+            raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
+        sc = shortcut.to(in_dtype).to(cdt).contiguous()
+    return _GatedFFTConvND.apply(q, kg, v, kc, sc, act1, act2, kbatch, periodic_mask(per)).to(in_dtype)
+
+
+def hyena_gated_fftconv2d_bhl(query, key, value, kernel, shortcut=None, gate_nonlinear="silu",
+                              gate_nonlinear_2=None, periodic=None) -> torch.Tensor:
+    """2D form of :func:`hyena_gated_fftconv_nd_bhl` (``[B, H, X, Y]``)."""
+    if query.ndim != 4:
+        raise ValueError(f"expected [B, H, X, Y]; got {tuple(query.shape)}")
+    return hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut, gate_nonlinear, gate_nonlinear_2, periodic)
+
+
+def hyena_gated_fftconv3d_bhl(query, key, value, kernel, shortcut=None, gate_nonlinear="silu",
+                              gate_nonlinear_2=None, periodic=None) -> torch.Tensor:
+    """3D form of :func:`hyena_gated_fftconv_nd_bhl` (``[B, H, X, Y, Z]``)."""
+    if query.ndim != 5:
+        raise ValueError(f"expected [B, H, X, Y, Z]; got {tuple(query.shape)}")
+    return hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut, gate_nonlinear, gate_nonlinear_2, periodic)

@@ -1,0 +1,82 @@
+"""GPU parity of the Hyena-gated 2D/3D FFT conv (``hyena_gated_fftconv{2,3}d_bhl``) against the CPU
+composition of the reference (``hyena_nd.py:546-570`` around CKConvND's N-d conv), restated in
+``oracle/gated_ref.py``: forward and the gradients of q, k, v, the filter and the shortcut.
+Tolerances: 1e-4 rel-L2 for fp32, 2e-2 for bf16 I/O."""
+
+import pytest
+import torch
+
+from nvsubquadratic_amd import gated_fftconv_hip as G
+from nvsubquadratic_amd import fftconv_hip as Z
+from oracle.gated_ref import gated_fftconv_nd_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(ref, out) -> float:
+    r = ref.detach().cpu().double()
+    o = out.detach().cpu().double()
+    return float((o - r).norm() / r.norm().clamp_min(1e-30))
+
+
+def _check(S, K, periodic, gate, gate_2, dtype=torch.float32, kb=1, B=2, H=6, tol=1e-4, shortcut=True):
+    torch.manual_seed(sum(S) + sum(K))
+    q, kg, v = (torch.randn(B, H, *S).to(dtype).requires_grad_(True) for _ in range(3))
+    k = torch.randn(kb, H, *K, requires_grad=True)
+    s = torch.randn(H).to(dtype).requires_grad_(True) if shortcut else None
+    per = (False,) * len(S) if periodic is None else periodic
+    y_ref = gated_fftconv_nd_torch(q, kg, v, k, per, s, gate, gate_2, compute_dtype=torch.float64)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    leaves = [q, kg, v, k] + ([s] if shortcut else [])
+    dev = [t.detach().cuda().requires_grad_(True) for t in leaves]
+    print(f"gated nd S={S} K={K} periodic={periodic} {gate}/{gate_2} {dtype} kb={kb}", flush=True)
+    y = G.hyena_gated_fftconv_nd_bhl(dev[0], dev[1], dev[2], dev[3], dev[4] if shortcut else None, gate, gate_2,
+                                     periodic)
+    y.backward(g.cuda())
+    assert y.dtype == dtype and y.shape == q.shape
+    assert rel_l2(y_ref, y) < tol
+    for a, b in zip(leaves, dev):
+        assert rel_l2(a.grad, b.grad) < tol
+
+
+@pytest.mark.parametrize("gate,gate_2", [("silu", None), ("sigmoid", "identity"), ("identity", "silu")])
+def test_gated_2d(gate, gate_2):
+    _check((16, 24), (5, 7), None, gate, gate_2)
+
+
+@pytest.mark.parametrize("periodic", [(True, False), (True, True)])
+def test_gated_2d_periodic_axes(periodic):
+    _check((32, 16), (5, 9), periodic, "silu", None)
+
+
+def test_gated_3d():
+    _check((8, 16, 12), (3, 5, 4), None, "silu", "sigmoid", H=4)
+
+
+def test_gated_3d_mixed_per_sample_filter():
+    _check((16, 8, 16), (5, 3, 4), (True, False, True), "sigmoid", None, kb=2, H=4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gated_2d_half_io(dtype):
+    _check((32, 32), (9, 9), None, "silu", None, dtype=dtype, tol=2e-2)
+
+
+def test_gated_2d_no_shortcut_identity_gates_equal_plain_conv():
+    torch.manual_seed(4)
+    x = torch.randn(2, 8, 24, 20, device="cuda")
+    k = torch.randn(1, 8, 7, 5, device="cuda")
+    one = torch.ones_like(x)
+    y = G.hyena_gated_fftconv2d_bhl(x, one, one, k, None, "identity", "identity")
+    assert rel_l2(Z.fftconv2d_bhl(x, k), y) < 1e-6
+
+
+def test_gated_nd_argument_errors():
+    q = torch.randn(1, 2, 8, 8, device="cuda")
+    with pytest.raises(ValueError, match="share one"):
+        G.hyena_gated_fftconv_nd_bhl(q, q, q[..., :4], torch.randn(1, 2, 3, 3, device="cuda"))
+    with pytest.raises(ValueError, match="periodic"):
+        G.hyena_gated_fftconv2d_bhl(q, q, q, torch.randn(1, 2, 3, 3, device="cuda"), periodic=(True,))
+    with pytest.raises(NotImplementedError):
+        G.hyena_gated_fftconv2d_bhl(q, q, q, torch.randn(1, 2, 3, 3, device="cuda"), gate_nonlinear=torch.nn.GELU())

@@ -46,3 +46,23 @@ def test_gradients_match_written_out_chain_rule():
     assert rel_l2(dq, qt.grad) < 1e-5 and rel_l2(dk, kt.grad) < 1e-5 and rel_l2(dv, vt.grad) < 1e-5
     assert rel_l2(dw, wt.grad[0]) < 1e-5
     assert rel_l2((dy1 * z).sum(axis=(0, 2)), st.grad) < 1e-5
+
+
+def test_nd_gates_around_a_centre_delta_filter():
+    """A centre delta (index K//2 on zero-padded axes, (K-1)//2 on periodic ones) makes the conv the identity, so
+    the gated op is (z + s z) * act2(v) with z = q * act1(k) -- a closed form independent of the FFT recipe."""
+    from oracle.gated_ref import gated_fftconv_nd_torch
+
+    torch.manual_seed(2)
+    for periodic, ks in (((False, False), (5, 4)), ((True, False, True), (3, 4, 5))):
+        S = (8, 6) if len(ks) == 2 else (8, 6, 8)
+        q, kg, v = (torch.randn(2, 3, *S, dtype=torch.float64) for _ in range(3))
+        s = torch.randn(3, dtype=torch.float64)
+        kernel = torch.zeros(1, 3, *ks, dtype=torch.float64)
+        centre = tuple((kd - 1) // 2 if p else kd // 2 for kd, p in zip(ks, periodic))
+        kernel[(0, slice(None)) + centre] = 1.0
+        y = gated_fftconv_nd_torch(q, kg, v, kernel, periodic, s, gate="sigmoid", gate_2="silu",
+                                   compute_dtype=torch.float64)
+        z = q * torch.sigmoid(kg)
+        ref = (z + s.view(1, 3, *([1] * len(S))) * z) * torch.nn.functional.silu(v)
+        assert torch.allclose(y, ref, atol=1e-12)
