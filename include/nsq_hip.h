@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 6
+#define NSQ_ABI_VERSION 7
 
 enum {
   NSQ_OK = 0,
@@ -139,19 +139,27 @@ int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, con
  *     fftconv1d_fp32_bhl (nvsubquadratic/ops/fftconv.py:603-660) and
  *     mixed_fftconv1d_fp32_bhl with periodic=(False,) (ops/mixed_fftconv.py:504-630,
  *     recipe :295-342):  y[n] = sum_j k[j] x[n + K/2 - j], x zero outside
- *     [0, L), n in [0, L); K <= 2L; L + ceil(K/2) <= 16384, else
+ *     [0, L), n in [0, L); K <= 2L; L + ceil(K/2) <= 2^23, else
  *     NSQ_ERR_UNSUPPORTED.
- *   periodic = 1: the circular conv, as nsq_circular_fftconv1d_fwd.
+ *   periodic = 1: the circular conv of nsq_circular_fftconv1d_fwd, for power-of-
+ *     two L <= 2^23.
  * Then y is rounded to the I/O dtype and shortcut * x added (as the causal op).
- * kbatch 1 or B; no workspace.  The backward writes gx, gk ([kbatch*H, K]) and,
- * with a shortcut, gs ([kbatch*H] partial sums).
+ * kbatch 1 or B.  FFT lengths <= 16384 run the fused kernels and need no
+ * workspace; longer ones the 4-step plan, with a workspace of
+ * nsq_mixed_fftconv1d_workspace_bytes (NSQ_DIR_FWD / NSQ_DIR_BWD).  The
+ * backward writes gx, gk ([kbatch*H, K]) and, with a shortcut, gs ([kbatch*H]
+ * partial sums).
  */
+size_t nsq_mixed_fftconv1d_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                                           unsigned periodic, int dtype, int direction);
+
 int nsq_mixed_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
-                            int64_t H, int64_t L, int64_t K, int64_t kbatch, unsigned periodic, void* stream);
+                            int64_t H, int64_t L, int64_t K, int64_t kbatch, unsigned periodic, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
                             float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
-                            unsigned periodic, void* stream);
+                            unsigned periodic, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Hyena-gated causal 1D FFT convolution (row F2 of the build plan): the long conv

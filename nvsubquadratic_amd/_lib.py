@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class HipLibraryError(RuntimeError):
@@ -115,16 +115,17 @@ _SIGNATURES = {
             _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p,
         ],
     ),
+    "nsq_mixed_fftconv1d_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_uint, _c_int, _c_int]),
     "nsq_mixed_fftconv1d_fwd": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_uint,
-         _c_void_p],
+         _c_void_p, _c_size, _c_void_p],
     ),
     "nsq_mixed_fftconv1d_bwd": (
         _c_int,
         [
             _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
-            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_uint, _c_void_p,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_uint, _c_void_p, _c_size, _c_void_p,
         ],
     ),
     "nsq_causal_conv1d_fwd": (

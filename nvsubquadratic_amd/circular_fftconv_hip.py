@@ -19,7 +19,8 @@ signature parity; both of the reference's branches give the same result and
 the kernels always apply the shift in the frequency domain.
 
 Sizes: periodic lengths must be powers of two (2D / 3D: up to 1024 per axis;
-1D: up to 16384); lengths below 16 run on their periodic extension at FFT
+1D: up to 2^23, the fused kernels up to 16384 and the 4-step plan beyond);
+lengths below 16 run on their periodic extension at FFT
 length 16.  Other sizes raise ``NotImplementedError`` (the product has no CPU
 fallback).
 """

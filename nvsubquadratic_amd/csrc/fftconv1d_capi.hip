@@ -34,12 +34,13 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
 
 // Circular 1D: L a power of two <= 16384 (the fused plan at FFT length
 // max(L, 16)), 1 <= K <= L, kbatch 1 or B.
-// Shifted 1D convs on the fused plan.  zpad = false: circular, K <= L, L a
-// power of two <= 16384 (FFT length L; below 16, its periodic extension at 16).
-// zpad = true: zero-padded "same", K <= 2L, FFT length pow2(L + ceil(K/2)) <=
-// 16384.  logN = log2(FFT length) - 1.
+// Shifted 1D convs.  zpad = false: circular, K <= L, L a power of two (FFT
+// length L; below 16, its periodic extension at 16).  zpad = true: zero-padded
+// "same", K <= 2L, FFT length pow2(L + ceil(K/2)).  logN = log2(FFT length) - 1:
+// the fused plan up to 13, the 4-step plan (with a workspace) up to max_logn.
 static int validate_shifted(const char* op, const void* a, const void* b, const float* k, int dtype, int64_t B,
-                            int64_t H, int64_t L, int64_t K, int64_t kbatch, bool zpad, int& logN) {
+                            int64_t H, int64_t L, int64_t K, int64_t kbatch, bool zpad, int& logN,
+                            int max_logn = 22) {
   NSQ_CHECK_ARG(a && b && k, "%s: null tensor pointer", op);
   NSQ_CHECK_ARG(valid_dtype(dtype), "%s: unsupported dtype code %d", op, dtype);
   NSQ_CHECK_ARG(B >= 1 && H >= 1 && L >= 1 && K >= 1, "%s: sizes must be positive (B=%lld H=%lld L=%lld K=%lld)",
@@ -52,22 +53,42 @@ static int validate_shifted(const char* op, const void* a, const void* b, const 
   NSQ_CHECK_ARG(kbatch == 1 || kbatch == B, "%s: kernel batch must be 1 or B (got %lld, B=%lld)", op,
                 (long long)kbatch, (long long)B);
   NSQ_CHECK_ARG(B * H <= 0x7fffffff && B <= 65535, "%s: tensor too large", op);
+  const int64_t maxF = int64_t(2) << max_logn;
   if (zpad) {
     const int64_t F = L + (K + 1) / 2;
-    if (F > 16384) {
-      set_error("%s: zero-padded length L + ceil(K/2) = %lld exceeds the fused kernels' FFT length 16384", op,
-                (long long)F);
+    if (F > maxF) {
+      set_error("%s: zero-padded length L + ceil(K/2) = %lld exceeds the largest FFT length %lld", op, (long long)F,
+                (long long)maxF);
       return NSQ_ERR_UNSUPPORTED;
     }
     logN = (F < 16 ? 4 : ilog2_ceil(F)) - 1;
     return NSQ_OK;
   }
-  if (L > 16384 || (L & (L - 1))) {
-    set_error("%s: unsupported length L=%lld: the HIP kernels take powers of two up to 16384", op, (long long)L);
+  if (L > maxF || (L & (L - 1))) {
+    set_error("%s: unsupported length L=%lld: the HIP kernels take powers of two up to %lld", op, (long long)L,
+              (long long)maxF);
     return NSQ_ERR_UNSUPPORTED;
   }
   logN = (L < 16 ? 4 : ilog2_ceil(L)) - 1;
   return NSQ_OK;
+}
+
+// Workspace of a shifted conv: none on the fused plan; on the 4-step plan the
+// 4-step blocks (forward: x and k; backward: x, k and g, N complex values
+// each), then the rolled rows (B*H rows of F = 2N I/O-dtype values).
+static size_t shifted_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, int dtype,
+                                      bool zpad, int direction) {
+  int logN = 0;
+  if (!valid_dtype(dtype) || B < 1 || H < 1 || L < 1 || K < 1 || K > (zpad ? 2 * L : L)) return 0;
+  const int64_t F = zpad ? L + (K + 1) / 2 : L;
+  if (F > (int64_t(2) << 22) || (!zpad && (L & (L - 1)))) return 0;
+  logN = (F < 16 ? 4 : ilog2_ceil(F)) - 1;
+  if (logN <= 13) return 0;
+  const int64_t N = int64_t(1) << logN;
+  const int64_t nk = kbatch * H;
+  const int64_t blocks = direction == NSQ_DIR_BWD ? 2 * B * H + nk : B * H + nk;
+  const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
+  return (size_t(blocks * N) * sizeof(float2) + 255) / 256 * 256 + size_t(B * H * 2 * N) * es;
 }
 
 static size_t causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, int direction) {
@@ -218,10 +239,11 @@ int nsq_fftconv1d_causal_film_bwd(const void* g, const void* x, const float* k, 
 }
 
 static int shifted_fwd(const char* op, const void* x, const float* k, const void* shortcut, void* y, int dtype,
-                       int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, bool zpad, void* stream) {
+                       int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, bool zpad, void* workspace,
+                       size_t workspace_bytes, int max_logn, void* stream) {
   clear_error();
   int logN = 0;
-  int rc = validate_shifted(op, x, y, k, dtype, B, H, L, K, kbatch, zpad, logN);
+  int rc = validate_shifted(op, x, y, k, dtype, B, H, L, K, kbatch, zpad, logN, max_logn);
   if (rc) return rc;
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
@@ -229,6 +251,28 @@ static int shifted_fwd(const char* op, const void* x, const float* k, const void
   const int kf = kbatch != 1;
   const int c = zpad ? int(K / 2) : int((K - 1) / 2);
   bool ok = false;
+  if (logN > 13) {
+    const size_t need = shifted_workspace_bytes(B, H, L, K, kbatch, dtype, zpad, NSQ_DIR_FWD);
+    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "%s: workspace of %zu bytes required, got %zu", op, need,
+                  workspace_bytes);
+    float2* ws = (float2*)workspace;
+    void* roll = (char*)workspace + (need - size_t(B * H * (int64_t(2) << logN)) * (dtype == NSQ_DTYPE_F32 ? 4 : 2));
+    const int b = int(B), h = int(H), l = int(L), kk = int(K);
+    switch (dtype) {
+      case NSQ_DTYPE_F32:
+        ok = run_shift4_fwd<NSQ_DTYPE_F32>(logN, x, k, shortcut, y, b, h, l, kk, kf, c, zpad, roll, ws, tw, st);
+        break;
+      case NSQ_DTYPE_BF16:
+        ok = run_shift4_fwd<NSQ_DTYPE_BF16>(logN, x, k, shortcut, y, b, h, l, kk, kf, c, zpad, roll, ws, tw, st);
+        break;
+      default:
+        ok = run_shift4_fwd<NSQ_DTYPE_F16>(logN, x, k, shortcut, y, b, h, l, kk, kf, c, zpad, roll, ws, tw, st);
+        break;
+    }
+    NSQ_CHECK_ARG(ok, "%s: no kernel for logN=%d", op, logN);
+    NSQ_CHECK_LAUNCH();
+    return NSQ_OK;
+  }
   switch (dtype) {
     case NSQ_DTYPE_F32:
       ok = run_circ_fwd<NSQ_DTYPE_F32>(logN, x, k, shortcut, y, int(B), int(H), int(L), int(K), kf, c, zpad, tw, st);
@@ -247,10 +291,10 @@ static int shifted_fwd(const char* op, const void* x, const float* k, const void
 
 static int shifted_bwd(const char* op, const void* g, const void* x, const float* k, const void* shortcut, void* gx,
                        float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
-                       bool zpad, void* stream) {
+                       bool zpad, void* workspace, size_t workspace_bytes, int max_logn, void* stream) {
   clear_error();
   int logN = 0;
-  int rc = validate_shifted(op, g, x, k, dtype, B, H, L, K, kbatch, zpad, logN);
+  int rc = validate_shifted(op, g, x, k, dtype, B, H, L, K, kbatch, zpad, logN, max_logn);
   if (rc) return rc;
   NSQ_CHECK_ARG(gx && gk, "%s: null gradient output pointer", op);
   NSQ_CHECK_ARG(!shortcut || gs, "%s: gs required when a shortcut is given", op);
@@ -261,6 +305,30 @@ static int shifted_bwd(const char* op, const void* g, const void* x, const float
   const int c = zpad ? int(K / 2) : int((K - 1) / 2);
   const int b = int(B), h = int(H), l = int(L), kk = int(K);
   bool ok = false;
+  if (logN > 13) {
+    const size_t need = shifted_workspace_bytes(B, H, L, K, kbatch, dtype, zpad, NSQ_DIR_BWD);
+    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "%s: workspace of %zu bytes required, got %zu", op, need,
+                  workspace_bytes);
+    float2* ws = (float2*)workspace;
+    void* roll = (char*)workspace + (need - size_t(B * H * (int64_t(2) << logN)) * (dtype == NSQ_DTYPE_F32 ? 4 : 2));
+    switch (dtype) {
+      case NSQ_DTYPE_F32:
+        ok = run_shift4_bwd<NSQ_DTYPE_F32>(logN, g, x, k, shortcut, gx, gk, gs, b, h, l, kk, kf, c, zpad, roll, ws,
+                                           tw, st);
+        break;
+      case NSQ_DTYPE_BF16:
+        ok = run_shift4_bwd<NSQ_DTYPE_BF16>(logN, g, x, k, shortcut, gx, gk, gs, b, h, l, kk, kf, c, zpad, roll, ws,
+                                            tw, st);
+        break;
+      default:
+        ok = run_shift4_bwd<NSQ_DTYPE_F16>(logN, g, x, k, shortcut, gx, gk, gs, b, h, l, kk, kf, c, zpad, roll, ws,
+                                           tw, st);
+        break;
+    }
+    NSQ_CHECK_ARG(ok, "%s: no kernel for logN=%d", op, logN);
+    NSQ_CHECK_LAUNCH();
+    return NSQ_OK;
+  }
   switch (dtype) {
     case NSQ_DTYPE_F32:
       ok = run_circ_bwd<NSQ_DTYPE_F32>(logN, g, x, k, shortcut, gx, gk, gs, b, h, l, kk, kf, c, zpad, tw, st);
@@ -279,31 +347,40 @@ static int shifted_bwd(const char* op, const void* g, const void* x, const float
 
 int nsq_circular_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
                                int64_t H, int64_t L, int64_t K, int64_t kbatch, void* stream) {
-  return shifted_fwd("circular_fftconv1d_fwd", x, k, shortcut, y, dtype, B, H, L, K, kbatch, false, stream);
+  return shifted_fwd("circular_fftconv1d_fwd", x, k, shortcut, y, dtype, B, H, L, K, kbatch, false, nullptr, 0, 13,
+                     stream);
 }
 
 int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx,
                                float* gk, float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K,
                                int64_t kbatch, void* stream) {
   return shifted_bwd("circular_fftconv1d_bwd", g, x, k, shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, false,
-                     stream);
+                     nullptr, 0, 13, stream);
+}
+
+size_t nsq_mixed_fftconv1d_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
+                                           unsigned periodic, int dtype, int direction) {
+  if (periodic > 1u) return 0;
+  return shifted_workspace_bytes(B, H, L, K, kbatch, dtype, periodic == 0, direction);
 }
 
 int nsq_mixed_fftconv1d_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
-                            int64_t H, int64_t L, int64_t K, int64_t kbatch, unsigned periodic, void* stream) {
+                            int64_t H, int64_t L, int64_t K, int64_t kbatch, unsigned periodic, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   clear_error();
   NSQ_CHECK_ARG(periodic <= 1u, "mixed_fftconv1d_fwd: periodic mask 0x%x names an axis >= 1", periodic);
   return shifted_fwd(periodic ? "mixed_fftconv1d_fwd (periodic)" : "mixed_fftconv1d_fwd (zero-padded)", x, k,
-                     shortcut, y, dtype, B, H, L, K, kbatch, periodic == 0, stream);
+                     shortcut, y, dtype, B, H, L, K, kbatch, periodic == 0, workspace, workspace_bytes, 22, stream);
 }
 
 int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
                             float* gs, int dtype, int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,
-                            unsigned periodic, void* stream) {
+                            unsigned periodic, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   NSQ_CHECK_ARG(periodic <= 1u, "mixed_fftconv1d_bwd: periodic mask 0x%x names an axis >= 1", periodic);
   return shifted_bwd(periodic ? "mixed_fftconv1d_bwd (periodic)" : "mixed_fftconv1d_bwd (zero-padded)", g, x, k,
-                     shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, periodic == 0, stream);
+                     shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, periodic == 0, workspace, workspace_bytes, 22,
+                     stream);
 }
 
 size_t nsq_gated_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch,

@@ -1078,6 +1078,91 @@ static void launch_4step_bwd(const void* g, const void* x, const float* k, const
   launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, gs, int(NK), K, tw, st);
 }
 
+// Shifted convs (circular, or zero-padded "same") beyond the fused plan, on
+// the 4-step plan at FFT length F = 2N.  The shift is moved into a rolled copy
+// of one operand (shift_rows_kernel): the forward transforms xr[t] = x[(t + c)
+// mod P] and the backward gr[t] = g[(t - c) mod P] (P = L circular, F zero-
+// padded; indices >= L read zero), so the plain 4-step circular products give
+//   y[i]  = sum_j k[j] xr[(i - j) mod F] = sum_j k[j] x[i + c - j],
+//   gx[i] = sum_t gr[t] k[(t - i) mod F],  gk[j] = sum_t gr[t] x[(t - j) mod F],
+// and the shortcut terms read the unshifted x and g; the shortcut gradient
+// sum_n g[n] x[n] = sum_t gr[t] x[t - c] is the filter gradient's lag c.
+// Zero-padded: F >= L + ceil(K/2) keeps every wrapped index out of the window
+// (no aliasing).
+template <int DT>
+__global__ __launch_bounds__(256) void shift_rows_kernel(const typename Elem<DT>::T* __restrict__ src,
+                                                         typename Elem<DT>::T* __restrict__ dst, int64_t rows, int L,
+                                                         int F, int off, int period) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * F) return;
+  const int64_t r = i / F;
+  const int t = int(i - r * F);
+  int idx = (t + off) % period;
+  if (idx < 0) idx += period;
+  Elem<DT>::store(dst, i, idx < L ? Elem<DT>::load(src, r * L + idx) : 0.f);
+}
+
+template <int UNUSED = 0>  // a template: one definition across the per-dtype translation units
+__global__ __launch_bounds__(256) void lag_gather_kernel(const float* __restrict__ gk, float* __restrict__ gs,
+                                                         int64_t rows, int K, int c) {
+  const int64_t r = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (r < rows) gs[r] = gk[r * K + c];
+}
+
+template <int LOGN1, int LOGN2, int DT>
+static void launch_4step_shift_fwd(const void* xr, const void* x, const float* k, const void* s, void* y, int B,
+                                   int H, int L, int K, int kfilm, float2* ws, const float2* tw, hipStream_t st) {
+  constexpr int LOGN = LOGN1 + LOGN2;
+  constexpr int64_t N = int64_t(1) << LOGN;
+  using ET = typename Elem<DT>::T;
+  const int64_t BH = int64_t(B) * H, NK = kfilm ? BH : H;
+  const int rb = kfilm ? 1 : B, rh = kfilm ? int(BH) : H;
+  float2* wsx = ws;
+  float2* wsk = ws + BH * N;
+  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)xr, 2 * N, 2 * N}, BH, wsx, tw, st);
+  launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
+  hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T),
+                     0, st, (const float2*)wsx, (const float2*)wsk, wsx, rb, rh, tw);
+  launch_col_inv_out<LOGN1, LOGN, DT>(wsx, x, s, y, BH, H, L, tw, st);
+}
+
+template <int LOGN1, int LOGN2, int DT>
+static void launch_4step_shift_bwd(const void* gr, const void* g, const void* x, const float* k, const void* s,
+                                   void* gx, float* gk, float* gs, int B, int H, int L, int K, int kfilm, int c,
+                                   float2* ws, const float2* tw, hipStream_t st) {
+  constexpr int LOGN = LOGN1 + LOGN2;
+  constexpr int64_t N = int64_t(1) << LOGN;
+  using ET = typename Elem<DT>::T;
+  const int64_t BH = int64_t(B) * H, NK = kfilm ? BH : H;
+  const int rb = kfilm ? 1 : B, rh = kfilm ? int(BH) : H;
+  float2* wsx = ws;
+  float2* wsk = ws + BH * N;
+  float2* wsg = ws + (BH + NK) * N;
+  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)gr, 2 * N, 2 * N}, BH, wsg, tw, st);
+  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
+  launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
+  if (rb == 1)
+    hipLaunchKernelGGL((row_bwd1_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)),
+                       dim3(RowCfg<LOGN2>::T), 0, st, wsg, (const float2*)wsx, wsk, rh, tw);
+  else
+    hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)),
+                       dim3(RowCfg<LOGN2>::T), 0, st, wsg, (const float2*)wsx, wsk, rb, rh, tw);
+  launch_col_inv_out<LOGN1, LOGN, DT>(wsg, g, s, gx, BH, H, L, tw, st);
+  launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, nullptr, int(NK), K, tw, st);
+  if (gs)
+    hipLaunchKernelGGL(lag_gather_kernel<0>, dim3(unsigned(ceil_div(NK, 256))), dim3(256), 0, st, (const float*)gk, gs, NK,
+                       K, c);
+}
+
+template <int DT>
+static void launch_shift_rows(const void* src, void* dst, int64_t rows, int L, int F, int off, int period,
+                              hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  const int64_t n = rows * F;
+  hipLaunchKernelGGL((shift_rows_kernel<DT>), dim3(unsigned(ceil_div(n, 256))), dim3(256), 0, st, (const ET*)src,
+                     (ET*)dst, rows, L, F, off, period);
+}
+
 // Runtime -> compile-time dispatch helpers.
 template <template <int> class F, int LO, int HI, class... A>
 static bool dispatch_int(int v, A&&... a) {
@@ -1138,6 +1223,22 @@ struct CircFused {
         launch_circ_bwd<LOGN, DT>(static_cast<A&&>(a)...);
       else
         launch_circ_fwd<LOGN, DT>(static_cast<A&&>(a)...);
+    }
+  };
+};
+
+template <int DT, bool BWD>
+struct FourStepShift {
+  template <int LOGN>
+  struct At {
+    static constexpr int L1 = split_log_n1(LOGN);
+    static constexpr int L2 = LOGN - L1;
+    template <class... A>
+    static void run(A&&... a) {
+      if constexpr (BWD)
+        launch_4step_shift_bwd<L1, L2, DT>(static_cast<A&&>(a)...);
+      else
+        launch_4step_shift_fwd<L1, L2, DT>(static_cast<A&&>(a)...);
     }
   };
 };
@@ -1246,6 +1347,29 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
                                                                zpad, tw, st);
 }
 
+// Shifted convs on the 4-step plan (logN in [14, 22]); `roll` holds B*H rows of
+// F = 2^(logN+1) I/O-dtype values, `ws` the 4-step workspace without `save`.
+template <int DT>
+bool run_shift4_fwd(int logN, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
+                    int kfilm, int c, bool zpad, void* roll, float2* ws, const float2* tw, hipStream_t st) {
+  if (logN < 14 || logN > 22) return false;
+  const int F = 2 << logN;
+  launch_shift_rows<DT>(x, roll, int64_t(B) * H, L, F, c, zpad ? F : L, st);
+  return dispatch_int<FourStepShift<DT, false>::template At, 14, 22>(logN, (const void*)roll, x, k, s, y, B, H, L, K,
+                                                                     kfilm, ws, tw, st);
+}
+
+template <int DT>
+bool run_shift4_bwd(int logN, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
+                    float* gs, int B, int H, int L, int K, int kfilm, int c, bool zpad, void* roll, float2* ws,
+                    const float2* tw, hipStream_t st) {
+  if (logN < 14 || logN > 22) return false;
+  const int F = 2 << logN;
+  launch_shift_rows<DT>(g, roll, int64_t(B) * H, L, F, -c, zpad ? F : L, st);
+  return dispatch_int<FourStepShift<DT, true>::template At, 14, 22>(logN, (const void*)roll, g, x, k, s, gx, gk, gs,
+                                                                    B, H, L, K, kfilm, c, ws, tw, st);
+}
+
 #define NSQ_DECLARE_FFTCONV1D(DT)                                                                               \
   extern template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
                                    int, int, float2*, bool, const float2*, hipStream_t);                        \
@@ -1256,6 +1380,11 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
                                         int, int, bool, const float2*, hipStream_t);                            \
   extern template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, \
                                         float*, int, int, int, int, int, int, bool, const float2*, hipStream_t); \
+  extern template bool run_shift4_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, \
+                                          int, int, bool, void*, float2*, const float2*, hipStream_t);          \
+  extern template bool run_shift4_bwd<DT>(int, const void*, const void*, const float*, const void*, void*,      \
+                                          float*, float*, int, int, int, int, int, int, bool, void*, float2*,   \
+                                          const float2*, hipStream_t);                                          \
   extern template bool run_gated_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, \
                                          int, int, int, const GateArgs&, void*, float2*, const float2*,         \
                                          hipStream_t);                                                          \
@@ -1273,6 +1402,11 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
                                  int, bool, const float2*, hipStream_t);                                    \
   template bool run_circ_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*, float*, \
                                  int, int, int, int, int, int, bool, const float2*, hipStream_t);              \
+  template bool run_shift4_fwd<DT>(int, const void*, const float*, const void*, void*, int, int, int, int, int, \
+                                   int, bool, void*, float2*, const float2*, hipStream_t);                     \
+  template bool run_shift4_bwd<DT>(int, const void*, const void*, const float*, const void*, void*, float*,    \
+                                   float*, int, int, int, int, int, int, bool, void*, float2*, const float2*,  \
+                                   hipStream_t);                                                               \
   template bool run_gated_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, int, \
                                   int, const GateArgs&, void*, float2*, const float2*, hipStream_t);             \
   template bool run_gated_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,      \

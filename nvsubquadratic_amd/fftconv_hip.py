@@ -490,9 +490,12 @@ def mixed_fftconv1d_fwd_raw(x, k, s, y, kbatch: int, periodic: int):
     lib = _lib.get_lib()
     _lib.check_device(x)
     B, H, L = x.shape
+    dt = _lib.dtype_code(x.dtype)
+    ws = _workspace(x.device, lib.nsq_mixed_fftconv1d_workspace_bytes(B, H, L, k.shape[-1], kbatch, int(periodic),
+                                                                       dt, _lib.NSQ_DIR_FWD))
     _lib.check(lib.nsq_mixed_fftconv1d_fwd(
-        x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.dtype_code(x.dtype), B, H, L, k.shape[-1],
-        kbatch, int(periodic), _lib.stream_ptr(x.device)))
+        x.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), dt, B, H, L, k.shape[-1], kbatch, int(periodic),
+        _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_ptr(x.device)))
     return y
 
 
@@ -501,9 +504,13 @@ def mixed_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, periodic: int):
     lib = _lib.get_lib()
     _lib.check_device(x)
     B, H, L = x.shape
+    dt = _lib.dtype_code(x.dtype)
+    ws = _workspace(x.device, lib.nsq_mixed_fftconv1d_workspace_bytes(B, H, L, k.shape[-1], kbatch, int(periodic),
+                                                                       dt, _lib.NSQ_DIR_BWD))
     _lib.check(lib.nsq_mixed_fftconv1d_bwd(
-        g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs),
-        _lib.dtype_code(x.dtype), B, H, L, k.shape[-1], kbatch, int(periodic), _lib.stream_ptr(x.device)))
+        g.data_ptr(), x.data_ptr(), k.data_ptr(), _lib.ptr(s), gx.data_ptr(), gk.data_ptr(), _lib.ptr(gs), dt, B, H,
+        L, k.shape[-1], kbatch, int(periodic), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+        _lib.stream_ptr(x.device)))
 
 
 class _ShiftedFFTConv1d(torch.autograd.Function):
@@ -550,10 +557,11 @@ def fftconv1d_bhl(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor 
 
     ``y[n] = sum_j k[j] x[n + K//2 - j]`` with x zero outside ``[0, L)``, cast to
     ``x.dtype``, then ``+ shortcut * x``.  Kernel ``[1|B, H, K]``, ``K <= 2L``.
-    Runs the fused 1D kernels (``nsq_mixed_fftconv1d_*`` with ``periodic=0``) at
-    FFT length ``pow2(L + ceil(K/2))`` (the reference's ``L + (K+1)//2`` is the
-    same result: every length from there on keeps the output window free of
-    wrap-around); lengths above 16384 raise ``NotImplementedError``.
+    Runs ``nsq_mixed_fftconv1d_*`` with ``periodic=0`` at FFT length
+    ``pow2(L + ceil(K/2))`` (the reference's ``L + (K+1)//2`` gives the same
+    result: every length from there on keeps the output window free of
+    wrap-around): the fused kernels up to 16384, the 4-step plan up to 2^23;
+    longer raises ``NotImplementedError``.
     """
     batch_size, hidden_dim, seq_len = x.shape
     assert len(kernel.shape) == 3, f"Unexpected kernel shape: {kernel.shape}."

@@ -160,7 +160,7 @@ def test_circular_rejects_mismatched_shortcut_dtype():
 
 
 @pytest.mark.parametrize("xs,ks", [((1, 4, 48), (5,)), ((1, 4, 12), (3,)), ((1, 2, 12, 16), (3, 3)),
-                                   ((1, 2, 16, 16, 24), (3, 3, 3)), ((1, 2, 32768), (5,)), ((1, 2, 2048, 16), (3, 3))])
+                                   ((1, 2, 16, 16, 24), (3, 3, 3)), ((1, 2, 2**24), (5,)), ((1, 2, 2048, 16), (3, 3))])
 def test_circular_unsupported_lengths_raise(xs, ks):
     """Non-power-of-two or out-of-range periodic lengths are refused, not approximated."""
     x = torch.randn(*xs, device="cuda")

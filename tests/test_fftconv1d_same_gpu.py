@@ -25,7 +25,7 @@ def rel_l2(ref, out) -> float:
 
 
 # (B, H, L, K): odd / even K, K = 2L, K = 1, L = 1, lengths that are not powers of two, and the largest
-# L + ceil(K/2) the fused kernels take (16384)
+# L + ceil(K/2) the fused kernels take (16384; longer ones run the 4-step plan, tested below)
 CASES = [(2, 16, 64, 7), (2, 8, 64, 8), (1, 8, 100, 200), (3, 4, 333, 1), (2, 3, 1, 2), (2, 4, 1000, 129),
          (1, 4, 4096, 4096), (1, 2, 12288, 8192), (2, 16, 2048, 33), (4, 32, 8192, 16)]
 
@@ -99,9 +99,9 @@ def test_same_1d_routing_chunking_and_layouts_bitwise():
 
 
 def test_same_1d_limits():
-    x = torch.randn(1, 2, 16000, device="cuda")
-    with pytest.raises(NotImplementedError, match="16384"):
-        Z.fftconv1d_bhl(x, torch.randn(1, 2, 800, device="cuda"))  # L + ceil(K/2) = 16400
+    x = torch.randn(1, 2, 2**23 - 100, device="cuda")
+    with pytest.raises(NotImplementedError, match="FFT length"):
+        Z.fftconv1d_bhl(x, torch.randn(1, 2, 400, device="cuda"))  # L + ceil(K/2) > 2^23
     with pytest.raises(AssertionError, match="2 \\* seq_len"):
         Z.fftconv1d_bhl(torch.randn(1, 2, 8, device="cuda"), torch.randn(1, 2, 17, device="cuda"))
     # the C-ABI's own checks: K > 2L and a mask naming axis 1
@@ -113,4 +113,48 @@ def test_same_1d_limits():
         Z.mixed_fftconv1d_fwd_raw(xs, k, None, y, 1, 0)
     with pytest.raises(ValueError, match="periodic mask"):
         _lib.check(lib.nsq_mixed_fftconv1d_fwd(xs.data_ptr(), k.data_ptr(), None, y.data_ptr(), 0, 1, 2, 8, 3, 1, 2,
-                                               _lib.stream_ptr(xs.device)))
+                                               None, 0, _lib.stream_ptr(xs.device)))
+
+
+# --- beyond the fused kernels: the 4-step plan with a rolled operand -------------
+LONG = [(1, 4, 20000, 3001, False), (2, 2, 40000, 80000, False), (1, 3, 32768, 31, True), (2, 2, 65536, 65536, True),
+        (1, 2, 131072, 1000, True), (1, 2, 100000, 17, False)]
+
+
+@pytest.mark.parametrize("B,H,L,K,periodic", LONG)
+def test_long_shifted_1d_fwd_bwd(B, H, L, K, periodic):
+    """Zero-padded "same" and circular 1D at FFT lengths 2^15..2^18 (4-step plan): forward and all gradients
+    against the float64 torch.fft restatement."""
+    from oracle.circular_ref import mixed_fftconv_torch
+
+    torch.manual_seed(L + K)
+    x = torch.randn(B, H, L, requires_grad=True)
+    k = (torch.randn(1, H, K) * torch.exp(-torch.arange(K) / (K / 4))).requires_grad_(True)
+    s = torch.randn(H, requires_grad=True)
+    y_ref = mixed_fftconv_torch(x, k, (periodic,), s, compute_dtype=torch.float64)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, kg, sg = (t.detach().cuda().requires_grad_(True) for t in (x, k, s))
+    print(f"long shifted 1d B={B} H={H} L={L} K={K} periodic={periodic}", flush=True)
+    y = M.mixed_fftconv1d_fp32_bhl(xg, kg, (periodic,), sg)
+    y.backward(g.cuda())
+    for ref, out in ((y_ref, y), (x.grad, xg.grad), (k.grad, kg.grad), (s.grad, sg.grad)):
+        assert rel_l2(ref, out) < 1e-4
+
+
+def test_long_shifted_1d_bf16_per_sample():
+    from oracle.circular_ref import mixed_fftconv_torch
+
+    torch.manual_seed(9)
+    B, H, L, K = 2, 3, 50000, 777
+    x = torch.randn(B, H, L).to(torch.bfloat16).requires_grad_(True)
+    k = (torch.randn(B, H, K) / K ** 0.5).requires_grad_(True)
+    y_ref = mixed_fftconv_torch(x, k, (False,), None, compute_dtype=torch.float64)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, kg = (t.detach().cuda().requires_grad_(True) for t in (x, k))
+    print("long shifted 1d bf16 per-sample", flush=True)
+    y = Z.fftconv1d_bhl(xg, kg)
+    y.backward(g.cuda())
+    for ref, out in ((y_ref, y), (x.grad, xg.grad), (k.grad, kg.grad)):
+        assert rel_l2(ref, out) < 2e-2
