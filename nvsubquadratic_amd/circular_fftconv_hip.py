@@ -13,8 +13,9 @@ then ``+ shortcut * x``.
 How: the 2D / 3D calls run the HIP N-d engine with every axis periodic
 (``nsq_mixed_fftconv_nd_*``): FFT length ``S_d`` (no padding), the shift as a
 ramp folded into the filter values of the product pass, no crop.  The 1D call
-runs the fused 1D kernels at FFT length ``L`` with the ramp on the filter's
-spectrum (``nsq_circular_fftconv1d_*``).  ``use_phase_shift`` is accepted for
+runs ``nsq_mixed_fftconv1d_*`` with ``periodic=1``: the fused 1D kernels at FFT
+length ``L`` with the ramp on the filter's spectrum, or beyond 16384 the 4-step
+plan on a rolled copy of x (g in the backward).  ``use_phase_shift`` is accepted for
 signature parity; both of the reference's branches give the same result and
 the kernels always apply the shift in the frequency domain.
 
