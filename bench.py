@@ -25,6 +25,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
            the rayleigh_benard Well config's layer, x periodic / y zero-padded)
        python bench.py --workload hyena-gated   (report-only: the Hyena gates
            fused into the causal conv, with the unfused composition's time)
+       python bench.py --workload hyena-gated-2d   (report-only: the gated 2D
+           conv at cfg4's shape, with torch gates around the same conv and the
+           conv alone)
        python bench.py --copy-calibration   (one plain copy kernel of known size,
                                              for scaling rocprof FETCH/WRITE_SIZE)
 """
@@ -284,6 +287,43 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
 
         extra["unfused_ms_per_step"] = round(statistics.mean(_time_steps(step_unfused, steps, warmup)), 4)
         extra["fused_backward_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_fused_bwd, steps, warmup)), 4)
+    elif name == "hyena-gated-2d":
+        # report-only (row F2, 2D): gate kernels around the N-d conv, against torch's gate ops around the same HIP
+        # conv (which keeps z for the backward) and the conv alone, fwd+bwd at cfg4's shape
+        import torch.nn.functional as Fn
+
+        from nvsubquadratic_amd.gated_fftconv_hip import hyena_gated_fftconv2d_bhl
+        from nvsubquadratic_amd.workloads import algorithmic_bytes_gated
+
+        B, Ch, X, K = 16, 384, 128, 128
+        q, kk, v = (torch.randn(B, Ch, X, X, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+                    for _ in range(3))
+        w = radial_filter(Ch, K, 4.0, 64.0, 2, gen, dev).unsqueeze(0).requires_grad_(True)
+        sh = torch.randn(Ch, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+        g = torch.randn(B, Ch, X, X, device=dev, generator=gen).to(torch.bfloat16)
+        phase, dtype = "fwd+bwd", "f32"
+        nbytes = algorithmic_bytes_gated(B, Ch, X * X, K * K, 2)
+        desc = ("hyena-gated-2d: gated 2D FFT conv fwd+bwd (z = q silu(k), y = (conv(z) + s z) silu(v)), "
+                "B=16 C=384 128^2, filter 128^2 fp32, FFT 256^2, bf16 I/O; gate kernels around the N-d conv")
+
+        def clear():
+            for t in (q, kk, v, w, sh):
+                t.grad = None
+
+        def step():
+            clear()
+            hyena_gated_fftconv2d_bhl(q, kk, v, w, sh, "silu").backward(g)
+
+        def step_torch_gates():
+            clear()
+            (F.fftconv2d_bhl(q * Fn.silu(kk), w, sh) * Fn.silu(v)).backward(g)
+
+        def step_conv_only():
+            clear()
+            F.fftconv2d_bhl(q, w, sh).backward(g)
+
+        extra["torch_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_torch_gates, steps, warmup)), 4)
+        extra["conv_only_ms_per_step"] = round(statistics.mean(_time_steps(step_conv_only, steps, warmup)), 4)
     else:
         raise SystemExit(f"unknown workload {name}")
     ms_list = _time_steps(step, steps, warmup)
@@ -311,7 +351,8 @@ def main() -> None:
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
-                                                              "cfg4-circular", "well-rb", "hyena-gated"])
+                                                              "cfg4-circular", "well-rb", "hyena-gated",
+                                                              "hyena-gated-2d"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
