@@ -749,6 +749,9 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
       const int m = t + it * kConvThreads;
       if (m < ZW) gwin[conv_pad(m)] = gstage[it];
     }
+    // The k / v windows below read x words that other waves staged: the
+    // stores above must be complete in every wave first.
+    __syncthreads();
     // k, v at the tile positions p = base + e (4-tap convs over xs index p + j, x at n0 + p - 3 + j)
     {
       float ka[kConvPer], va[kConvPer];

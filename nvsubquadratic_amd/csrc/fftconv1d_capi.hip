@@ -181,9 +181,9 @@ static size_t gated_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, 
   Plan1D p;
   if (!make_plan(L, K, p) || !valid_dtype(dtype)) return 0;
   if (p.fused && direction == NSQ_DIR_FWD) return 0;  // one fused kernel
-  const size_t conv = (causal_workspace_bytes(B, H, L, K, kbatch, direction) + 255) / 256 * 256;
+  const size_t conv = round256(causal_workspace_bytes(B, H, L, K, kbatch, direction));
   const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
-  return conv + size_t(direction == NSQ_DIR_BWD ? 3 : 2) * size_t(B * H * L) * es;
+  return conv + size_t(direction == NSQ_DIR_BWD ? 3 : 2) * round256(size_t(B * H * L) * es);
 }
 
 static bool aligned16(std::initializer_list<const void*> ps) {
@@ -410,7 +410,7 @@ int nsq_gated_fftconv1d_causal_fwd(const void* q, const void* kgate, const void*
     NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv1d_fwd: workspace of %zu bytes required, got %zu",
                   need, workspace_bytes);
     ws = (float2*)workspace;
-    gws = (char*)workspace + (causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_FWD) + 255) / 256 * 256;
+    gws = (char*)workspace + round256(causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_FWD));
   }
   const GateArgs ga{kgate, v, y1, nullptr, nullptr, act1, act2};
   const int kf = kbatch != 1;
@@ -458,7 +458,7 @@ int nsq_gated_fftconv1d_causal_bwd(const void* g, const void* q, const void* kga
     NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv1d_bwd: workspace of %zu bytes required, got %zu",
                   need, workspace_bytes);
     ws = (float2*)workspace;
-    gws = (char*)workspace + (causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD) + 255) / 256 * 256;
+    gws = (char*)workspace + round256(causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD));
   }
   const GateArgs ga{kgate, v, const_cast<void*>(y1), dkgate, dv, act1, act2};
   const int kf = kbatch != 1;

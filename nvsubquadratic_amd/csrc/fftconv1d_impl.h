@@ -1297,8 +1297,9 @@ bool run_gated_fwd(const Plan1D& p, const void* q, const float* k, const void* s
                                                                    st);
   using ET = typename Elem<DT>::T;
   const int64_t n = int64_t(B) * H * L;
+  const int64_t stride = int64_t(round256(size_t(n) * sizeof(ET)) / sizeof(ET));  // 256-byte aligned sub-buffers
   ET* z = (ET*)gws;
-  ET* y1 = ga.y1 ? (ET*)ga.y1 : z + n;
+  ET* y1 = ga.y1 ? (ET*)ga.y1 : z + stride;
   launch_gate_ew<DT, GATE_OP_FWD1>(GateEw{q, ga.kg, nullptr, z, nullptr, ga.act1}, n, st);
   if (!run_fwd<DT>(p, z, k, s, y1, B, H, L, K, kfilm, ws, false, tw, st)) return false;
   launch_gate_ew<DT, GATE_OP_FWD2>(GateEw{y1, ga.v, nullptr, y, nullptr, ga.act2}, n, st);
@@ -1320,9 +1321,10 @@ bool run_gated_bwd(const Plan1D& p, const void* g, const void* q, const float* k
                                                                   kfilm, ga, tw, st);
   using ET = typename Elem<DT>::T;
   const int64_t n = int64_t(B) * H * L;
+  const int64_t stride = int64_t(round256(size_t(n) * sizeof(ET)) / sizeof(ET));  // 256-byte aligned sub-buffers
   ET* z = (ET*)gws;
-  ET* dy1 = z + n;
-  ET* dz = dy1 + n;
+  ET* dy1 = z + stride;
+  ET* dz = dy1 + stride;
   launch_gate_ew<DT, GATE_OP_BWD2>(GateEw{g, ga.v, ga.y1, dy1, ga.dv, ga.act2}, n, st);
   launch_gate_ew<DT, GATE_OP_FWD1>(GateEw{q, ga.kg, nullptr, z, nullptr, ga.act1}, n, st);
   if (!run_bwd<DT>(p, dy1, z, k, s, dz, gk, gs, B, H, L, K, kfilm, ws, false, tw, st)) return false;

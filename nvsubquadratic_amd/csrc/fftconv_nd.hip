@@ -556,7 +556,7 @@ static size_t gated_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64
   const size_t conv = nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, direction);
   if (!conv || !valid_dtype(dtype)) return 0;
   const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
-  return (conv + 255) / 256 * 256 + size_t(direction == NSQ_DIR_BWD ? 3 : 2) * size_t(nd_numel(nd, B, H, S)) * es;
+  return round256(conv) + size_t(direction == NSQ_DIR_BWD ? 3 : 2) * round256(size_t(nd_numel(nd, B, H, S)) * es);
 }
 
 template <int DT>
@@ -598,11 +598,11 @@ static int gated_nd_fwd(int nd, const void* q, const void* kgate, const void* v,
   const size_t need = gated_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dtype, NSQ_DIR_FWD);
   NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv_nd_fwd: workspace of %zu bytes required, got %zu",
                 need, workspace_bytes);
-  const size_t conv = (nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_FWD) + 255) / 256 * 256;
+  const size_t conv = round256(nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_FWD));
   const int64_t n = nd_numel(nd, B, H, S);
   const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
   char* z = (char*)workspace + conv;
-  void* y1b = y1 ? y1 : (void*)(z + n * es);
+  void* y1b = y1 ? y1 : (void*)(z + round256(n * es));
   hipStream_t st = (hipStream_t)stream;
   gate_pass(dtype, GATE_OP_FWD1, GateEw{q, kgate, nullptr, z, nullptr, act1}, n, st);
   rc = nd_fwd(nd, z, k, shortcut, y1b, dtype, B, H, S, K, kbatch, periodic, workspace, conv, stream);
@@ -629,12 +629,12 @@ static int gated_nd_bwd(int nd, const void* g, const void* q, const void* kgate,
   const size_t need = gated_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dtype, NSQ_DIR_BWD);
   NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv_nd_bwd: workspace of %zu bytes required, got %zu",
                 need, workspace_bytes);
-  const size_t conv = (nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_BWD) + 255) / 256 * 256;
+  const size_t conv = round256(nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_BWD));
   const int64_t n = nd_numel(nd, B, H, S);
   const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
   char* z = (char*)workspace + conv;
-  char* dy1 = z + n * es;
-  char* dz = dy1 + n * es;
+  char* dy1 = z + round256(n * es);
+  char* dz = dy1 + round256(n * es);
   hipStream_t st = (hipStream_t)stream;
   gate_pass(dtype, GATE_OP_BWD2, GateEw{g, v, y1, dy1, dv, act2}, n, st);
   gate_pass(dtype, GATE_OP_FWD1, GateEw{q, kgate, nullptr, z, nullptr, act1}, n, st);

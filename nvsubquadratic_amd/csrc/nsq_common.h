@@ -60,6 +60,11 @@ inline bool valid_dtype(int dt) {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Sub-buffers carved out of one workspace start on 256-byte boundaries, so
+// every kernel that takes one may use 16-byte vector accesses whatever the
+// element counts before it.
+inline size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
 inline int ilog2_ceil(int64_t v) {
   int l = 0;
   while ((int64_t(1) << l) < v) ++l;

@@ -37,6 +37,13 @@ GATE_CODES = {"identity": 0, "sigmoid": 1, "silu": 2}
 _MODULE_CODES = {torch.nn.Identity: 0, torch.nn.Sigmoid: 1, torch.nn.SiLU: 2}
 
 
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """A copy of ``t`` when its data does not start on a 16-byte boundary (the gate kernels move
+    16-byte chunks).  Views into a larger tensor, such as the q / k / v that ``x.split(H, dim=1)``
+    gives at B = 1 with an odd H * L, may start anywhere."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def gate_code(gate) -> int:
     """``"identity" | "sigmoid" | "silu"`` or an ``nn.Identity / nn.Sigmoid / nn.SiLU`` instance -> C gate code."""
     if isinstance(gate, str):
@@ -102,7 +109,7 @@ class _GatedCausalFFTConv1d(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gy):
         q, kg, v, y1, k, s = ctx.saved_tensors
-        g = gy.to(q.dtype).contiguous()
+        g = _aligned16(gy.to(q.dtype).contiguous())
         dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
         gk = torch.empty_like(k)
         H = q.shape[1]
@@ -145,7 +152,7 @@ def hyena_gated_causal_fftconv1d_bhl(
     kbatch = k3.shape[0]
     in_dtype = query.dtype
     cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
-    q, kg, v = (t.to(cdt).contiguous() for t in (query, key, value))
+    q, kg, v = (_aligned16(t.to(cdt).contiguous()) for t in (query, key, value))
     kc = k3.float().reshape(kbatch * H, k3.shape[-1]).contiguous()
     sc = None
     if shortcut is not None:
@@ -192,7 +199,7 @@ class _GatedFFTConvND(torch.autograd.Function):
         B, H = q.shape[:2]
         S, K = _lib.i64_array(q.shape[2:]), _lib.i64_array(k.shape[1:])
         dt = _lib.dtype_code(q.dtype)
-        g = gy.to(q.dtype).contiguous()
+        g = _aligned16(gy.to(q.dtype).contiguous())
         dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
         gk = torch.empty_like(k)
         gs = torch.empty(kbatch * H, dtype=torch.float32, device=q.device) if ctx.has_s else None
@@ -232,7 +239,7 @@ def hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut=None, gate_no
     kbatch = k.shape[0]
     in_dtype = query.dtype
     cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
-    q, kg, v = (t.to(cdt).contiguous() for t in (query, key, value))
+    q, kg, v = (_aligned16(t.to(cdt).contiguous()) for t in (query, key, value))
     kc = k.float().reshape(kbatch * H, *k.shape[2:]).contiguous()
     sc = None
     if shortcut is not None:

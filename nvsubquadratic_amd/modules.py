@@ -1,11 +1,13 @@
-"""Module-level drop-ins for the Hyena short-conv slot.
+"""The Hyena short-conv slot as an ``nn.Conv1d`` on the HIP backend.
 
-:class:`HipCausalConv1d` mirrors ``SubqOpsCausalConv1d``
-(``nvsubquadratic/modules/subq_ops_causal_conv1d.py:36-83``): an
-``nn.Conv1d`` subclass (so ``Hyena``'s ``isinstance(short_conv, nn.Conv1d)``
-check at ``nvsubquadratic/modules/hyena_nd.py:258-271`` passes) with the same
-``weight [C, 1, K]`` / ``bias [C]`` state-dict layout, the same constructor
-checks and error messages, running :func:`nvsubquadratic_amd.causal_conv1d_hip.causal_conv1d`.
+Hyena accepts any ``nn.Conv1d`` for its short convolution
+(``nvsubquadratic/modules/hyena_nd.py:258-271`` checks the type), and the
+reference fills the slot with ``SubqOpsCausalConv1d``
+(``nvsubquadratic/modules/subq_ops_causal_conv1d.py:36-83``).
+:class:`HipCausalConv1d` takes the same constructor arguments and keeps the
+same parameters (``weight`` of shape ``[C, 1, K]``, optional ``bias`` of shape
+``[C]``), so checkpoints move between the two unchanged; its forward runs
+:func:`nvsubquadratic_amd.causal_conv1d_hip.causal_conv1d`.
 """
 
 from __future__ import annotations
@@ -17,9 +19,11 @@ from .causal_conv1d_hip import causal_conv1d
 
 __all__ = ["HipCausalConv1d"]
 
+_ACTIVATIONS = ("identity", "silu")
+
 
 class HipCausalConv1d(torch.nn.Conv1d):
-    """Depthwise causal 1D conv on the gfx950 HIP backend."""
+    """Per-channel causal convolution: output n sees inputs n-K+1 .. n of its own channel."""
 
     def __init__(
         self,
@@ -31,35 +35,31 @@ class HipCausalConv1d(torch.nn.Conv1d):
         bias: bool = False,
         activation: str = "identity",
     ) -> None:
-        """Build a depthwise causal conv with optional SiLU activation.
-
-        Args:
-            in_channels: Channel count (must equal ``out_channels`` and ``groups``).
-            out_channels: Output channels (depthwise: same as ``in_channels``).
-            kernel_size: Causal kernel length (1..256).
-            groups: Must equal ``in_channels`` for depthwise layout.
-            bias: Whether to include a per-channel bias.
-            activation: ``"identity"`` or ``"silu"`` applied inside the kernel.
         """
-        if not (groups == in_channels == out_channels):
+        Args:
+            in_channels: C, the number of channels.
+            out_channels: also C; each channel has its own filter.
+            kernel_size: K, the filter length (1 <= K <= 256 for the HIP kernels).
+            groups: also C (one group per channel).
+            bias: add a learned per-channel offset before the activation.
+            activation: ``"identity"`` or ``"silu"``, fused into the kernel's output.
+
+        Raises:
+            ValueError: when the three channel arguments differ (the layer is
+                depthwise-only) or the activation is not one of the two above.
+        """
+        if groups != in_channels or out_channels != in_channels:
             raise ValueError(
-                "HipCausalConv1d is depthwise-only: groups must equal "
-                f"in_channels must equal out_channels.  Got groups={groups}, "
-                f"in_channels={in_channels}, out_channels={out_channels}."
+                f"HipCausalConv1d is depthwise-only (one filter per channel), so in_channels, out_channels and "
+                f"groups have to agree; received in_channels={in_channels}, out_channels={out_channels}, "
+                f"groups={groups}."
             )
-        if activation not in ("identity", "silu"):
-            raise ValueError(f"activation must be 'identity' or 'silu'. Got {activation!r}.")
-        super().__init__(
-            in_channels=in_channels,
-            out_channels=out_channels,
-            kernel_size=kernel_size,
-            groups=groups,
-            bias=bias,
-            padding=0,
-        )
+        if activation not in _ACTIVATIONS:
+            raise ValueError(f"unsupported activation {activation!r}; choose one of {_ACTIVATIONS}.")
+        super().__init__(in_channels, out_channels, kernel_size, groups=groups, bias=bias, padding=0)
         self.activation = activation
 
     def forward(self, input: torch.Tensor) -> torch.Tensor:  # type: ignore[override]
-        """Run causal depthwise conv; input shape ``[B, C, L]``."""
-        # nn.Conv1d depthwise weight is [C, 1, K]; the kernel takes [C, K].
-        return causal_conv1d(input, self.weight.squeeze(1), self.bias, self.activation)
+        """``input`` is ``[B, C, L]``; returns ``[B, C, L]`` in the input's dtype."""
+        # The parameter keeps nn.Conv1d's [C, 1, K] layout; the op takes one filter row per channel.
+        return causal_conv1d(input, self.weight[:, 0, :], self.bias, self.activation)

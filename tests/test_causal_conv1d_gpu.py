@@ -218,6 +218,32 @@ def test_b2b_forward_backward(B, C, L, Kp, Km):
         assert rel_l2(ref.grad, got.grad) < 1e-4
 
 
+def test_b2b_backward_every_channel_many_workgroups():
+    """The fused adjoint (projection taps <= 4, matrix-core mixer) with many workgroups per CU in
+    flight, fp32, checked channel by channel: each thread's k / v windows read x words that
+    other waves stage, so a missing barrier there corrupts runs of positions in a few
+    channels only -- invisible in one rel-L2 over all channels, caught per row here."""
+    torch.manual_seed(7)
+    B, C, L, Kp, Km = 4, 512, 8192, 3, 128
+    x = torch.randn(B, 3 * C, L, requires_grad=True)
+    wp = (torch.randn(3 * C, Kp) / Kp ** 0.5).requires_grad_(True)
+    wm = (torch.randn(C, Km) / Km ** 0.5).requires_grad_(True)
+    sk = torch.randn(C, requires_grad=True)
+    y_ref = b2b_causal_conv1d_torch(x, wp, wm, sk)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    args = [t.detach().cuda().requires_grad_(True) for t in (x, wp, wm, sk)]
+    b2b_causal_conv1d(*args).backward(g.cuda())
+    gx = args[0].grad.cpu().double()
+    rx = x.grad.double()
+    err_x = ((gx - rx).norm(dim=2) / rx.norm(dim=2)).max().item()  # worst (batch, channel) row
+    err_wp = ((args[1].grad.cpu().double() - wp.grad.double()).norm(dim=1) / wp.grad.double().norm(dim=1)).max().item()
+    assert err_x < 1e-4, err_x
+    assert err_wp < 1e-4, err_wp
+    for ref, got in zip((wm, sk), args[2:]):
+        assert rel_l2(ref.grad, got.grad) < 1e-4
+
+
 @pytest.mark.parametrize("Km", [15, 16, 17, 33, 34, 65, 66, 128, 129, 130, 256])
 def test_b2b_mixer_tap_counts_across_matrix_core_plans(Km):
     """Mixer tap counts on both sides of each matrix-core step-count boundary.

@@ -71,3 +71,32 @@ def test_modules_as_gates_and_default_second_gate():
     assert torch.equal(a, b)
     with pytest.raises(NotImplementedError):
         hyena_gated_causal_fftconv1d_bhl(q, k, v, w, None, torch.nn.GELU())
+
+
+def test_multi_kernel_plan_odd_numel_bf16_and_split_views():
+    """4-step plan (elementwise gate kernels around the conv) with B*H*L odd: every workspace sub-buffer
+    must start 16-byte aligned.  q / k / v are x.split(H, dim=1) views at B = 1 (k and v start at odd
+    element offsets); a no-grad forward keeps y1 in the workspace."""
+    B, H, L, K = 1, 3, 20001, 9001
+    torch.manual_seed(13)
+    x = torch.randn(B, 3 * H, L).to(torch.bfloat16)
+    w = torch.randn(1, H, K) / K ** 0.5
+    s = torch.randn(H).to(torch.bfloat16)
+    xg = x.cuda().requires_grad_(True)
+    q, kk, v = xg.split(H, dim=1)
+    assert kk.data_ptr() % 16 != 0
+    wg, sg = w.cuda().requires_grad_(True), s.cuda().requires_grad_(True)
+    y = hyena_gated_causal_fftconv1d_bhl(q, kk, v, wg, sg, "silu", "sigmoid")
+    g = torch.randn(y.shape).to(torch.bfloat16)
+    y.backward(g.cuda())
+    xr = x.clone().requires_grad_(True)
+    qr, kr, vr = xr.split(H, dim=1)
+    wr, sr = w.clone().requires_grad_(True), s.clone().requires_grad_(True)
+    y_ref = gated_causal_fftconv1d_torch(qr, kr, vr, wr, sr, "silu", "sigmoid")
+    y_ref.backward(g)
+    assert rel_l2(y_ref, y) < 2e-2
+    for a, b in ((xr, xg), (wr, wg), (sr, sg)):
+        assert rel_l2(a.grad, b.grad) < 2e-2
+    with torch.no_grad():
+        y0 = hyena_gated_causal_fftconv1d_bhl(q, kk, v, wg, sg, "silu", "sigmoid")
+    assert torch.equal(y0, y)

@@ -80,3 +80,34 @@ def test_gated_nd_argument_errors():
         G.hyena_gated_fftconv2d_bhl(q, q, q, torch.randn(1, 2, 3, 3, device="cuda"), periodic=(True,))
     with pytest.raises(NotImplementedError):
         G.hyena_gated_fftconv2d_bhl(q, q, q, torch.randn(1, 2, 3, 3, device="cuda"), gate_nonlinear=torch.nn.GELU())
+
+
+def test_gated_2d_odd_numel_bf16_and_split_views():
+    """B*H*prod(S) odd: the workspace sub-buffers (z, y1, dy1, dz) follow one another and must each start
+    16-byte aligned for the vectorized gate kernels.  The q / k / v come from x.split(H, dim=1) at B = 1,
+    as Hyena takes them, so k and v start at odd element offsets; a no-grad forward keeps y1 in the
+    workspace."""
+    B, H, S, K = 1, 3, (15, 17), (5, 7)
+    torch.manual_seed(12)
+    x = torch.randn(B, 3 * H, *S).to(torch.bfloat16)
+    w = torch.randn(1, H, *K)
+    s = torch.randn(H).to(torch.bfloat16)
+    xg = x.cuda().requires_grad_(True)
+    q, kk, v = xg.split(H, dim=1)
+    assert kk.data_ptr() % 16 != 0
+    wg, sg = w.cuda().requires_grad_(True), s.cuda().requires_grad_(True)
+    y = G.hyena_gated_fftconv2d_bhl(q, kk, v, wg, sg, "silu", "sigmoid")
+    g = torch.randn(y.shape).to(torch.bfloat16)
+    y.backward(g.cuda())
+    xr = x.clone().requires_grad_(True)
+    qr, kr, vr = xr.split(H, dim=1)
+    wr, sr = w.clone().requires_grad_(True), s.clone().requires_grad_(True)
+    y_ref = gated_fftconv_nd_torch(qr, kr, vr, wr, (False, False), sr, "silu", "sigmoid",
+                                   compute_dtype=torch.float64)
+    y_ref.backward(g)
+    assert rel_l2(y_ref, y) < 2e-2
+    for a, b in ((xr, xg), (wr, wg), (sr, sg)):
+        assert rel_l2(a.grad, b.grad) < 2e-2
+    with torch.no_grad():
+        y0 = G.hyena_gated_fftconv2d_bhl(q, kk, v, wg, sg, "silu", "sigmoid")
+    assert torch.equal(y0, y)
