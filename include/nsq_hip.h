@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 7
+#define NSQ_ABI_VERSION 8
 
 enum {
   NSQ_OK = 0,
@@ -245,6 +245,26 @@ size_t nsq_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t C, int64_t L, in
 int nsq_causal_conv1d_bwd(const void* gy, const void* x, const float* weight, const float* bias, void* gx,
                           float* gweight, float* gbias, int dtype, int activation, int64_t B, int64_t C, int64_t L,
                           int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free variant of nsq_causal_conv1d_bwd: the same kernels and the
+ * same results (bitwise), with the scratch they need (the weight / bias
+ * gradient partials, and above 16 taps with silu the pre-activation gradient)
+ * in a fixed device buffer of NSQ_NOALLOC_SCRATCH_BYTES that the library holds
+ * on each GPU it runs on until the process ends, instead of a caller
+ * workspace.  It has no counterpart in the reference: it is for callers that
+ * cannot allocate device memory, such as code under HIP graph capture or a
+ * serving loop that forbids allocation.  It calls no hipMalloc / hipFree.
+ * Shapes whose scratch (nsq_causal_conv1d_bwd_workspace_bytes) exceeds the
+ * buffer return NSQ_ERR_UNSUPPORTED without launching anything.  Every call
+ * on one GPU shares that GPU's buffer: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.
+ */
+#define NSQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+int nsq_causal_conv1d_bwd_noalloc(const void* gy, const void* x, const float* weight, const float* bias, void* gx,
+                                  float* gweight, float* gbias, int dtype, int activation, int64_t B, int64_t C,
+                                  int64_t L, int64_t K, void* stream);
 
 /*
  * Back-to-back striped-Hyena short-conv block ("projection conv, pre-gate,

@@ -4,9 +4,19 @@
 // nvsubquadratic/ops/causal_conv1d_custom.py:81-98 (subquadratic_ops_torch
 // .causal_conv1d(x, w, bias, activation)), used by the Hyena short-conv slot
 // through nvsubquadratic/modules/subq_ops_causal_conv1d.py:77-83.
+#include <mutex>
+
 #include "direct_conv.h"
 
 namespace nsq {
+
+// Scratch of nsq_causal_conv1d_bwd_noalloc: one copy per GPU, resident from
+// module load to process exit.  In host code `scratch` names a host-side
+// stand-in, not device memory: the device address of each GPU's copy comes
+// from hipGetSymbolAddress (noalloc_scratch below) and only that address is
+// ever handed to kernels.
+constexpr size_t kNoAllocScratchBytes = NSQ_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 // Forward for K <= 16 taps from registers: thread t of a tile owns outputs
 // n = n0 + 8t + e, e < 8; with the taps left-padded to KP = 4, 8 or 16,
@@ -462,6 +472,44 @@ static int validate_cconv(const void* a, const void* b, const float* w, int dtyp
   return NSQ_OK;
 }
 
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxScratchDevices] = {nullptr};
+}  // namespace
+
+// Device address of the current GPU's scratch, looked up on the first call
+// made with that device current and kept for later calls.  nullptr on failure
+// (error recorded).
+static float* noalloc_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("causal_conv1d_bwd_noalloc: no current HIP device (or device index >= %d)", kMaxScratchDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("causal_conv1d_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  return g_scratch[dev];
+}
+
+template <class... A>
+static void launch_bwd_dtype(int dtype, A... a) {
+  switch (dtype) {
+    case NSQ_DTYPE_F32: launch_bwd<NSQ_DTYPE_F32>(a...); break;
+    case NSQ_DTYPE_BF16: launch_bwd<NSQ_DTYPE_BF16>(a...); break;
+    default: launch_bwd<NSQ_DTYPE_F16>(a...); break;
+  }
+}
+
 }  // namespace nsq
 
 using namespace nsq;
@@ -503,19 +551,36 @@ int nsq_causal_conv1d_bwd(const void* gy, const void* x, const float* weight, co
   const size_t need = nsq_causal_conv1d_bwd_workspace_bytes(B, C, L, K, activation);
   NSQ_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need),
                 "causal_conv1d_bwd: workspace of %zu bytes required, got %zu", need, workspace_bytes);
-  hipStream_t st = (hipStream_t)stream;
-  float* ws = (float*)workspace;
-  switch (dtype) {
-    case NSQ_DTYPE_F32:
-      launch_bwd<NSQ_DTYPE_F32>(gy, x, weight, bias, gx, gweight, gbias, activation, int(B), int(C), int(L), int(K), ws, st);
-      break;
-    case NSQ_DTYPE_BF16:
-      launch_bwd<NSQ_DTYPE_BF16>(gy, x, weight, bias, gx, gweight, gbias, activation, int(B), int(C), int(L), int(K), ws, st);
-      break;
-    default:
-      launch_bwd<NSQ_DTYPE_F16>(gy, x, weight, bias, gx, gweight, gbias, activation, int(B), int(C), int(L), int(K), ws, st);
-      break;
+  launch_bwd_dtype(dtype, gy, x, weight, bias, gx, gweight, gbias, activation, int(B), int(C), int(L), int(K),
+                   (float*)workspace, (hipStream_t)stream);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+// The scratch regions the backward uses (partials, the silu pre-activation
+// gradient) are written in full by one kernel before the next reads them, so
+// the buffer needs no clearing between calls.
+int nsq_causal_conv1d_bwd_noalloc(const void* gy, const void* x, const float* weight, const float* bias, void* gx,
+                                  float* gweight, float* gbias, int dtype, int activation, int64_t B, int64_t C,
+                                  int64_t L, int64_t K, void* stream) {
+  clear_error();
+  int rc = validate_cconv(gy, x, weight, dtype, activation, B, C, L, K);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(gx && gweight, "causal_conv1d_bwd_noalloc: null gradient output pointer");
+  const size_t need = nsq_causal_conv1d_bwd_workspace_bytes(B, C, L, K, activation);
+  if (need > kNoAllocScratchBytes) {
+    set_error("causal_conv1d_bwd_noalloc: B=%lld C=%lld L=%lld K=%lld needs %zu bytes of scratch, more than the "
+              "fixed %zu-byte device buffer; call nsq_causal_conv1d_bwd with a workspace instead",
+              (long long)B, (long long)C, (long long)L, (long long)K, need, kNoAllocScratchBytes);
+    return NSQ_ERR_UNSUPPORTED;
   }
+  float* ws = nullptr;
+  if (need) {
+    ws = noalloc_scratch();
+    if (!ws) return NSQ_ERR_HIP;
+  }
+  launch_bwd_dtype(dtype, gy, x, weight, bias, gx, gweight, gbias, activation, int(B), int(C), int(L), int(K), ws,
+                   (hipStream_t)stream);
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
 }

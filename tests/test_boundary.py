@@ -137,3 +137,20 @@ def test_periodic_lengths_validated_before_launch():
     # short periods run on their periodic extension at length 16 (accepted, not refused)
     S, K = _lib.i64_array([8, 4]), _lib.i64_array([3, 4])
     assert lib.nsq_mixed_fftconv_nd_workspace_bytes(2, 1, 1, S, K, 1, 0b11, 0) > 0
+
+
+def test_noalloc_scratch_size_matches_header():
+    m = re.search(r"#define NSQ_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NSQ_NOALLOC_SCRATCH_BYTES
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_noalloc_backward_refuses_oversize_scratch_on_the_host():
+    """A shape whose scratch exceeds the fixed device buffer is refused before anything touches the GPU."""
+    lib = _lib.get_lib()
+    B, C, L, K = 8, 8192, 1 << 20, 16
+    assert lib.nsq_causal_conv1d_bwd_workspace_bytes(B, C, L, K, 0) > _lib.NSQ_NOALLOC_SCRATCH_BYTES
+    fake = 1 << 20  # never dereferenced: the call returns before any launch
+    rc = lib.nsq_causal_conv1d_bwd_noalloc(fake, fake, fake, None, fake, fake, None, 0, 0, B, C, L, K, None)
+    assert rc == 2  # NSQ_ERR_UNSUPPORTED
+    assert b"scratch" in lib.nsq_last_error()
