@@ -631,9 +631,12 @@ struct RowSlots {
   int corr;    // q == 0 first half: pad16(N2 - s) = pad16(N2 - 1) - pad16(s) + 1 + (s % 16 == 0)
   float2 u0;   // W_2N^q (q > 0), 1 (q == 0)
   float2 u1;   // W_2N^{N1/2} * i (q == 0, second half)
-  __device__ __forceinline__ RowSlots(int q, const float2* __restrict__ tw) : tt(tw) {
+  __device__ __forceinline__ RowSlots(int q, const float2* __restrict__ tw) : RowSlots(q, tw, opaque_tid()) {}
+  // tl: the thread's index among the T threads of its row pair (a workgroup
+  // may run several row pairs side by side, each on its own 2-row sub-tile).
+  __device__ __forceinline__ RowSlots(int q, const float2* __restrict__ tw, int tl) : tt(tw) {
     constexpr int LOGN = LOGN1 + LOGN2;
-    t = opaque_tid();
+    t = tl;
     qz = (q == 0);
     base = pad16(t);
     corr = (t & 15) == 0 ? 1 : 0;
