@@ -17,7 +17,10 @@ gradients flow back through the cast).  There is no CPU path.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
+from torch.library import custom_op
 
 from . import _lib
 
@@ -32,38 +35,62 @@ def _io(x: torch.Tensor) -> tuple[torch.Tensor, torch.dtype]:
     return x.to(dt).contiguous(), dt
 
 
-class _CausalConv1d(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, w, bias, act):
-        lib = _lib.get_lib()
-        _lib.check_device(x)
-        B, C, L = x.shape
-        K = w.shape[-1]
-        y = torch.empty_like(x)
-        _lib.check(lib.nsq_causal_conv1d_fwd(
-            x.data_ptr(), w.data_ptr(), _lib.ptr(bias), y.data_ptr(), _lib.dtype_code(x.dtype), act,
-            B, C, L, K, _lib.stream_ptr(x.device)))
-        ctx.save_for_backward(x, w, bias)
-        ctx.act = act
-        ctx.has_bias = bias is not None
-        return y
+@custom_op("nsq_hip::causal_conv1d", mutates_args=())
+def causal_conv1d_op(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], act: int) -> torch.Tensor:
+    """Depthwise causal conv forward: x ``[B, C, L]`` contiguous (f32/bf16/f16), w ``[C, K]`` and bias ``[C]`` float32."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, C, L = x.shape
+    y = torch.empty_like(x)
+    _lib.check(lib.nsq_causal_conv1d_fwd(
+        x.data_ptr(), w.data_ptr(), _lib.ptr(bias), y.data_ptr(), _lib.dtype_code(x.dtype), act, B, C, L,
+        w.shape[-1], _lib.stream_ptr(x.device)))
+    return y
 
-    @staticmethod
-    def backward(ctx, gy):
-        x, w, bias = ctx.saved_tensors
-        lib = _lib.get_lib()
-        B, C, L = x.shape
-        K = w.shape[-1]
-        g = gy.to(x.dtype).contiguous()
-        gx = torch.empty_like(x)
-        gw = torch.empty_like(w)
-        gb = torch.empty_like(bias) if ctx.has_bias else None
-        need = lib.nsq_causal_conv1d_bwd_workspace_bytes(B, C, L, K, ctx.act)
-        ws = torch.empty(need, dtype=torch.uint8, device=x.device) if need else None
-        _lib.check(lib.nsq_causal_conv1d_bwd(
-            g.data_ptr(), x.data_ptr(), w.data_ptr(), _lib.ptr(bias), gx.data_ptr(), gw.data_ptr(), _lib.ptr(gb),
-            _lib.dtype_code(x.dtype), ctx.act, B, C, L, K, _lib.ptr(ws), need, _lib.stream_ptr(x.device)))
-        return gx, gw, gb, None
+
+@causal_conv1d_op.register_fake
+def _(x, w, bias, act):
+    return torch.empty_like(x)
+
+
+@custom_op("nsq_hip::causal_conv1d_backward", mutates_args=())
+def causal_conv1d_backward_op(g: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor],
+                              act: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(gx, gw, gbias)``; gbias is empty when there is no bias."""
+    lib = _lib.get_lib()
+    B, C, L = x.shape
+    K = w.shape[-1]
+    gx = torch.empty_like(x)
+    gw = torch.empty_like(w)
+    gb = torch.empty(C if bias is not None else 0, dtype=torch.float32, device=x.device)
+    need = lib.nsq_causal_conv1d_bwd_workspace_bytes(B, C, L, K, act)
+    ws = torch.empty(need, dtype=torch.uint8, device=x.device) if need else None
+    _lib.check(lib.nsq_causal_conv1d_bwd(
+        g.data_ptr(), x.data_ptr(), w.data_ptr(), _lib.ptr(bias), gx.data_ptr(), gw.data_ptr(),
+        gb.data_ptr() if bias is not None else None, _lib.dtype_code(x.dtype), act, B, C, L, K, _lib.ptr(ws), need,
+        _lib.stream_ptr(x.device)))
+    return gx, gw, gb
+
+
+@causal_conv1d_backward_op.register_fake
+def _(g, x, w, bias, act):
+    return torch.empty_like(x), torch.empty_like(w), x.new_empty(x.shape[1] if bias is not None else 0,
+                                                                 dtype=torch.float32)
+
+
+def _cc_setup(ctx, inputs, output):
+    x, w, bias, act = inputs
+    ctx.save_for_backward(x, w, bias)
+    ctx.act = act
+
+
+def _cc_backward(ctx, gy):
+    x, w, bias = ctx.saved_tensors
+    gx, gw, gb = causal_conv1d_backward_op(gy.to(x.dtype).contiguous(), x, w, bias, ctx.act)
+    return gx, gw, (gb if bias is not None else None), None
+
+
+causal_conv1d_op.register_autograd(_cc_backward, setup_context=_cc_setup)
 
 
 def causal_conv1d(
@@ -90,43 +117,68 @@ def causal_conv1d(
     xc, _ = _io(x)
     wc = weight.float().contiguous()
     bc = None if bias is None else bias.float().contiguous()
-    y = _CausalConv1d.apply(xc, wc, bc, _ACT[activation])
+    y = causal_conv1d_op(xc, wc, bc, _ACT[activation])
     return y.to(x.dtype)
 
 
-class _B2B(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, wp, wm, skip):
-        lib = _lib.get_lib()
-        _lib.check_device(x)
-        B, C3, L = x.shape
-        C = C3 // 3
-        y = torch.empty(B, C, L, dtype=x.dtype, device=x.device)
-        _lib.check(lib.nsq_b2b_causal_conv1d_fwd(
-            x.data_ptr(), wp.data_ptr(), wm.data_ptr(), _lib.ptr(skip), y.data_ptr(), _lib.dtype_code(x.dtype),
-            B, C, L, wp.shape[-1], wm.shape[-1], _lib.stream_ptr(x.device)))
-        ctx.save_for_backward(x, wp, wm, skip)
-        ctx.has_skip = skip is not None
-        return y
+@custom_op("nsq_hip::b2b_causal_conv1d", mutates_args=())
+def b2b_causal_conv1d_op(x: torch.Tensor, wp: torch.Tensor, wm: torch.Tensor,
+                         skip: Optional[torch.Tensor]) -> torch.Tensor:
+    """Fused B2B forward: x ``[B, 3C, L]`` contiguous, wp ``[3C, Kp]``, wm ``[C, Km]``, skip ``[C]`` float32 or None."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, C3, L = x.shape
+    C = C3 // 3
+    y = torch.empty(B, C, L, dtype=x.dtype, device=x.device)
+    _lib.check(lib.nsq_b2b_causal_conv1d_fwd(
+        x.data_ptr(), wp.data_ptr(), wm.data_ptr(), _lib.ptr(skip), y.data_ptr(), _lib.dtype_code(x.dtype),
+        B, C, L, wp.shape[-1], wm.shape[-1], _lib.stream_ptr(x.device)))
+    return y
 
-    @staticmethod
-    def backward(ctx, gy):
-        x, wp, wm, skip = ctx.saved_tensors
-        lib = _lib.get_lib()
-        B, C3, L = x.shape
-        C = C3 // 3
-        g = gy.to(x.dtype).contiguous()
-        gx = torch.empty_like(x)
-        gwp = torch.empty_like(wp)
-        gwm = torch.empty_like(wm)
-        gskip = torch.empty(C, dtype=torch.float32, device=x.device) if ctx.has_skip else None
-        need = lib.nsq_b2b_causal_conv1d_bwd_workspace_bytes(B, C, L, wp.shape[-1], wm.shape[-1])
-        ws = torch.empty(need, dtype=torch.uint8, device=x.device)
-        _lib.check(lib.nsq_b2b_causal_conv1d_bwd(
-            g.data_ptr(), x.data_ptr(), wp.data_ptr(), wm.data_ptr(), _lib.ptr(skip), gx.data_ptr(), gwp.data_ptr(),
-            gwm.data_ptr(), _lib.ptr(gskip), _lib.dtype_code(x.dtype), B, C, L, wp.shape[-1], wm.shape[-1],
-            ws.data_ptr(), need, _lib.stream_ptr(x.device)))
-        return gx, gwp, gwm, gskip
+
+@b2b_causal_conv1d_op.register_fake
+def _(x, wp, wm, skip):
+    return x.new_empty(x.shape[0], x.shape[1] // 3, x.shape[2])
+
+
+@custom_op("nsq_hip::b2b_causal_conv1d_backward", mutates_args=())
+def b2b_causal_conv1d_backward_op(g: torch.Tensor, x: torch.Tensor, wp: torch.Tensor, wm: torch.Tensor,
+                                  skip: Optional[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                         torch.Tensor]:
+    """``(gx, gwp, gwm, gskip)``; gskip is empty when there is no skip."""
+    lib = _lib.get_lib()
+    B, C3, L = x.shape
+    C = C3 // 3
+    gx = torch.empty_like(x)
+    gwp = torch.empty_like(wp)
+    gwm = torch.empty_like(wm)
+    gskip = torch.empty(C if skip is not None else 0, dtype=torch.float32, device=x.device)
+    need = lib.nsq_b2b_causal_conv1d_bwd_workspace_bytes(B, C, L, wp.shape[-1], wm.shape[-1])
+    ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _lib.check(lib.nsq_b2b_causal_conv1d_bwd(
+        g.data_ptr(), x.data_ptr(), wp.data_ptr(), wm.data_ptr(), _lib.ptr(skip), gx.data_ptr(), gwp.data_ptr(),
+        gwm.data_ptr(), gskip.data_ptr() if skip is not None else None, _lib.dtype_code(x.dtype), B, C, L,
+        wp.shape[-1], wm.shape[-1], ws.data_ptr(), need, _lib.stream_ptr(x.device)))
+    return gx, gwp, gwm, gskip
+
+
+@b2b_causal_conv1d_backward_op.register_fake
+def _(g, x, wp, wm, skip):
+    return (torch.empty_like(x), torch.empty_like(wp), torch.empty_like(wm),
+            x.new_empty(x.shape[1] // 3 if skip is not None else 0, dtype=torch.float32))
+
+
+def _b2b_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _b2b_backward(ctx, gy):
+    x, wp, wm, skip = ctx.saved_tensors
+    gx, gwp, gwm, gskip = b2b_causal_conv1d_backward_op(gy.to(x.dtype).contiguous(), x, wp, wm, skip)
+    return gx, gwp, gwm, (gskip if skip is not None else None)
+
+
+b2b_causal_conv1d_op.register_autograd(_b2b_backward, setup_context=_b2b_setup)
 
 
 def b2b_causal_conv1d(
@@ -157,7 +209,7 @@ def b2b_causal_conv1d(
     if skip_bias is not None and skip_bias.shape != (C,):
         raise ValueError(f"skip_bias must be [C] = [{C}]; got {tuple(skip_bias.shape)}")
     xc, _ = _io(x)
-    y = _B2B.apply(
+    y = b2b_causal_conv1d_op(
         xc,
         weight_proj.float().contiguous(),
         weight_mixer.float().contiguous(),

@@ -23,8 +23,11 @@ inverse FFT, crop, cast and shortcut) runs inside hand-written HIP kernels
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 from einops import rearrange
+from torch.library import custom_op
 
 from . import _lib
 
@@ -66,7 +69,7 @@ _DEFAULT_CHUNK_SIZE = 128
 
 
 # ---------------------------------------------------------------------------
-# Raw launches (preallocated outputs; used by the autograd Function and bench)
+# Raw launches (preallocated outputs; used by the custom ops below, tests and bench)
 # ---------------------------------------------------------------------------
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     if nbytes == 0:
@@ -149,44 +152,81 @@ def causal_fftconv1d_bwd_raw(
     _lib.check(rc)
 
 
-class _CausalFFTConv1d(torch.autograd.Function):
-    """Fused causal FFT conv; inputs already validated and cast.
+# ---------------------------------------------------------------------------
+# Operators.  Every HIP op is a torch.library custom op (namespace nsq_hip) with
+# a fake (meta) implementation and a registered autograd formula, so that
+# torch.compile traces through it (fullgraph) instead of breaking the graph at
+# an opaque ctypes call; eager calls dispatch to the same implementations.
+# ---------------------------------------------------------------------------
+def _grad_wanted(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
-    x: [B, H, L] contiguous (f32/bf16/f16); k: [kbatch*H, K] contiguous float32;
-    s: [H] in x.dtype or None.
-    """
 
-    @staticmethod
-    def forward(ctx, x, k, s, kbatch=1):
-        y = torch.empty_like(x)
-        ws = None
-        if any(ctx.needs_input_grad[:3]):  # (grad mode is off inside forward; this flag is not)
-            # Backward-sized workspace: the forward keeps its transformed x and k
-            # in it for the backward (like autograd keeping rfft outputs).
-            B, H, L = x.shape
-            need = _causal_workspace_bytes(_lib.get_lib(), B, H, L, k.shape[-1], kbatch, _lib.NSQ_DIR_BWD)
-            ws = _workspace(x.device, need)
-        causal_fftconv1d_fwd_raw(x, k, s, y, ws, kbatch)
-        ctx.save_for_backward(x, k, s)
-        ctx.ws = ws
-        ctx.kbatch = kbatch
-        ctx.has_s = s is not None
-        return y
+def _causal_state_bytes(x: torch.Tensor, k: torch.Tensor, kbatch: int, keep: bool) -> int:
+    if not keep:
+        return 0
+    B, H, L = (int(d) for d in x.shape)
+    return int(_causal_workspace_bytes(_lib.get_lib(), B, H, L, int(k.shape[-1]), kbatch, _lib.NSQ_DIR_BWD))
 
-    @staticmethod
-    def backward(ctx, gy):
-        x, k, s = ctx.saved_tensors
-        g = gy.to(x.dtype).contiguous()
-        gx = torch.empty_like(x)
-        gk = torch.empty(k.shape, dtype=torch.float32, device=x.device)
-        gs = torch.empty(k.shape[0], dtype=torch.float32, device=x.device) if ctx.has_s else None
-        ws, ctx.ws = ctx.ws, None  # the backward consumes the forward state
-        causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ws, fwd_state=ws is not None, kbatch=ctx.kbatch)
-        gsum = None
-        if ctx.has_s:
-            H = x.shape[1]
-            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
-        return gx, gk, gsum, None
+
+@custom_op("nsq_hip::causal_fftconv1d", mutates_args=())
+def causal_fftconv1d_op(x: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor], kbatch: int,
+                        keep: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Causal FFT conv forward; x ``[B, H, L]`` contiguous (f32/bf16/f16), k ``[kbatch*H, K]`` float32, s ``[H]``
+    in x.dtype or None.  Returns ``(y, state)``: with ``keep`` the state is a backward-sized workspace in which the
+    forward leaves its transformed x and k for the backward (like autograd keeping rfft outputs), else empty."""
+    y = torch.empty_like(x)
+    state = torch.empty(_causal_state_bytes(x, k, kbatch, keep), dtype=torch.uint8, device=x.device)
+    causal_fftconv1d_fwd_raw(x, k, s, y, state if keep else None, kbatch)
+    return y, state
+
+
+@causal_fftconv1d_op.register_fake
+def _(x, k, s, kbatch, keep):
+    return torch.empty_like(x), x.new_empty(_causal_state_bytes(x, k, kbatch, keep), dtype=torch.uint8)
+
+
+@custom_op("nsq_hip::causal_fftconv1d_backward", mutates_args=("state",))
+def causal_fftconv1d_backward_op(g: torch.Tensor, x: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor],
+                                 state: torch.Tensor, kbatch: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients ``(gx, gk, gs)`` (gs ``[kbatch*H]`` partial sums, empty without a shortcut); a non-empty ``state``
+    is the forward's workspace and is consumed (overwritten)."""
+    gx = torch.empty_like(x)
+    gk = torch.empty(k.shape, dtype=torch.float32, device=x.device)
+    gs = torch.empty(k.shape[0] if s is not None else 0, dtype=torch.float32, device=x.device)
+    has = state.numel() > 0
+    causal_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs if s is not None else None, state if has else None,
+                             fwd_state=has, kbatch=kbatch)
+    return gx, gk, gs
+
+
+@causal_fftconv1d_backward_op.register_fake
+def _(g, x, k, s, state, kbatch):
+    return (torch.empty_like(x), k.new_empty(k.shape, dtype=torch.float32),
+            x.new_empty(k.shape[0] if s is not None else 0, dtype=torch.float32))
+
+
+def _shortcut_grad(gs: torch.Tensor, s: torch.Tensor | None, kbatch: int, H: int):
+    """Per-filter partial shortcut gradients (per-sample filters) summed to ``[H]``, in the shortcut's dtype."""
+    if s is None:
+        return None
+    return (gs if kbatch == 1 else gs.view(kbatch, H).sum(0)).to(s.dtype)
+
+
+def _causal_setup(ctx, inputs, output):
+    x, k, s, kbatch, _keep = inputs
+    ctx.save_for_backward(x, k, s, output[1])
+    ctx.kbatch = kbatch
+
+
+def _causal_backward(ctx, gy, _gstate):
+    x, k, s, state = ctx.saved_tensors
+    g = gy.to(x.dtype).contiguous()
+    gx, gk, gs = causal_fftconv1d_backward_op(g, x, k, s, state, ctx.kbatch)
+    return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None
+
+
+causal_fftconv1d_op.register_autograd(_causal_backward, setup_context=_causal_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -228,7 +268,7 @@ def _causal_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor |
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         # Reference casts the shortcut to the input dtype before the product.
         sc = shortcut.to(input_dtype).to(compute_dtype).contiguous()
-    y = _CausalFFTConv1d.apply(xc, kc, sc, kbatch)
+    y, _ = causal_fftconv1d_op(xc, kc, sc, kbatch, _grad_wanted(xc, kc, sc))
     return y.to(input_dtype)
 
 
@@ -393,44 +433,65 @@ def fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, workspace: torch.Ten
         _lib.check(lib.nsq_fftconv_nd_bwd(nd, *args, *tail))
 
 
-class _FFTConvND(torch.autograd.Function):
-    """x: [B, H, *S] contiguous; k: [kbatch*H, *K] contiguous float32; s: [H] in x.dtype or None."""
+def _nd_state_bytes(x: torch.Tensor, k: torch.Tensor, kbatch: int, periodic: int, keep: bool) -> int:
+    if not keep:
+        return 0
+    nd = x.ndim - 2
+    return int(_nd_workspace_bytes(_lib.get_lib(), nd, int(x.shape[0]), int(x.shape[1]),
+                                   _lib.i64_array([int(d) for d in x.shape[2:]]),
+                                   _lib.i64_array([int(d) for d in k.shape[1:]]), kbatch, periodic, _lib.NSQ_DIR_BWD))
 
-    @staticmethod
-    def forward(ctx, x, k, s, kbatch, periodic=0):
-        y = torch.empty_like(x)
-        ws = None
-        if any(ctx.needs_input_grad[:3]):  # (grad mode is off inside forward; this flag is not)
-            # Backward-sized workspace: the forward keeps its transformed x and
-            # filter spectrum there for the backward.
-            lib = _lib.get_lib()
-            nd = x.ndim - 2
-            need = _nd_workspace_bytes(lib, nd, x.shape[0], x.shape[1], _lib.i64_array(x.shape[2:]),
-                                       _lib.i64_array(k.shape[1:]), kbatch, periodic, _lib.NSQ_DIR_BWD)
-            ws = _workspace(x.device, need) if need else None
-        fftconv_nd_fwd_raw(x, k, s, y, kbatch, ws, periodic)
-        ctx.save_for_backward(x, k, s)
-        ctx.kbatch = kbatch
-        ctx.periodic = periodic
-        ctx.has_s = s is not None
-        ctx.ws = ws
-        return y
 
-    @staticmethod
-    def backward(ctx, gy):
-        x, k, s = ctx.saved_tensors
-        g = gy.to(x.dtype).contiguous()
-        gx = torch.empty_like(x)
-        gk = torch.empty_like(k)
-        H = x.shape[1]
-        gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
-        ws, ctx.ws = ctx.ws, None  # the backward consumes the forward state
-        fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch, ws, fwd_state=ws is not None, periodic=ctx.periodic)
-        gsum = None
-        if ctx.has_s:
-            # per-filter partial sums only for FiLM kernels; a shared kernel's gs is complete
-            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
-        return gx, gk, gsum, None, None
+@custom_op("nsq_hip::fftconv_nd", mutates_args=())
+def fftconv_nd_op(x: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor], kbatch: int, periodic: int,
+                  keep: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """2D/3D non-causal FFT conv forward; x ``[B, H, *S]``, k ``[kbatch*H, *K]`` float32, s ``[H]`` or None,
+    ``periodic`` bit d = axis d circular.  ``(y, state)`` as :func:`causal_fftconv1d_op`."""
+    y = torch.empty_like(x)
+    state = torch.empty(_nd_state_bytes(x, k, kbatch, periodic, keep), dtype=torch.uint8, device=x.device)
+    fftconv_nd_fwd_raw(x, k, s, y, kbatch, state if keep and state.numel() else None, periodic)
+    return y, state
+
+
+@fftconv_nd_op.register_fake
+def _(x, k, s, kbatch, periodic, keep):
+    return torch.empty_like(x), x.new_empty(_nd_state_bytes(x, k, kbatch, periodic, keep), dtype=torch.uint8)
+
+
+@custom_op("nsq_hip::fftconv_nd_backward", mutates_args=("state",))
+def fftconv_nd_backward_op(g: torch.Tensor, x: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor],
+                           state: torch.Tensor, kbatch: int, periodic: int) -> tuple[torch.Tensor, torch.Tensor,
+                                                                                     torch.Tensor]:
+    """Gradients ``(gx, gk, gs)`` of :func:`fftconv_nd_op` (gs ``[kbatch*H]`` partials, empty without a shortcut)."""
+    gx = torch.empty_like(x)
+    gk = torch.empty_like(k)
+    gs = torch.empty(kbatch * x.shape[1] if s is not None else 0, dtype=torch.float32, device=x.device)
+    has = state.numel() > 0
+    fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs if s is not None else None, kbatch, state if has else None,
+                       fwd_state=has, periodic=periodic)
+    return gx, gk, gs
+
+
+@fftconv_nd_backward_op.register_fake
+def _(g, x, k, s, state, kbatch, periodic):
+    return torch.empty_like(x), torch.empty_like(k), x.new_empty(kbatch * x.shape[1] if s is not None else 0,
+                                                                 dtype=torch.float32)
+
+
+def _nd_setup(ctx, inputs, output):
+    x, k, s, kbatch, periodic, _keep = inputs
+    ctx.save_for_backward(x, k, s, output[1])
+    ctx.kbatch, ctx.periodic = kbatch, periodic
+
+
+def _nd_backward(ctx, gy, _gstate):
+    x, k, s, state = ctx.saved_tensors
+    g = gy.to(x.dtype).contiguous()
+    gx, gk, gs = fftconv_nd_backward_op(g, x, k, s, state, ctx.kbatch, ctx.periodic)
+    return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None, None
+
+
+fftconv_nd_op.register_autograd(_nd_backward, setup_context=_nd_setup)
 
 
 def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, nd: int,
@@ -464,7 +525,8 @@ def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | Non
         if shortcut.shape != (H,):
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         sc = shortcut.to(input_dtype).to(compute_dtype).contiguous()
-    return _FFTConvND.apply(xc, kc, sc, kbatch, periodic).to(input_dtype)
+    y, _ = fftconv_nd_op(xc, kc, sc, kbatch, int(periodic), _grad_wanted(xc, kc, sc))
+    return y.to(input_dtype)
 
 
 def _chunked(fn, x, kernel, shortcut, chunk_size, nd):
@@ -513,31 +575,52 @@ def mixed_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, kbatch: int, periodic: int):
         _lib.stream_ptr(x.device)))
 
 
-class _ShiftedFFTConv1d(torch.autograd.Function):
-    """x: [B, H, L] contiguous; k: [kbatch*H, K] contiguous float32; s: [H] in x.dtype or None."""
+@custom_op("nsq_hip::shifted_fftconv1d", mutates_args=())
+def shifted_fftconv1d_op(x: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor], kbatch: int,
+                         periodic: int) -> torch.Tensor:
+    """Non-causal 1D FFT conv (periodic 1: circular; 0: zero-padded "same"); x ``[B, H, L]``, k ``[kbatch*H, K]``
+    float32, s ``[H]`` or None."""
+    y = torch.empty_like(x)
+    mixed_fftconv1d_fwd_raw(x, k, s, y, kbatch, periodic)
+    return y
 
-    @staticmethod
-    def forward(ctx, x, k, s, kbatch, periodic):
-        y = torch.empty_like(x)
-        mixed_fftconv1d_fwd_raw(x, k, s, y, kbatch, periodic)
-        ctx.save_for_backward(x, k, s)
-        ctx.kbatch, ctx.periodic = kbatch, periodic
-        ctx.has_s = s is not None
-        return y
 
-    @staticmethod
-    def backward(ctx, gy):
-        x, k, s = ctx.saved_tensors
-        g = gy.to(x.dtype).contiguous()
-        gx = torch.empty_like(x)
-        gk = torch.empty_like(k)
-        H = x.shape[1]
-        gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=x.device) if ctx.has_s else None
-        mixed_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs, ctx.kbatch, ctx.periodic)
-        gsum = None
-        if ctx.has_s:
-            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
-        return gx, gk, gsum, None, None
+@shifted_fftconv1d_op.register_fake
+def _(x, k, s, kbatch, periodic):
+    return torch.empty_like(x)
+
+
+@custom_op("nsq_hip::shifted_fftconv1d_backward", mutates_args=())
+def shifted_fftconv1d_backward_op(g: torch.Tensor, x: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor],
+                                  kbatch: int, periodic: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients ``(gx, gk, gs)`` of :func:`shifted_fftconv1d_op` (gs partials, empty without a shortcut)."""
+    gx = torch.empty_like(x)
+    gk = torch.empty_like(k)
+    gs = torch.empty(kbatch * x.shape[1] if s is not None else 0, dtype=torch.float32, device=x.device)
+    mixed_fftconv1d_bwd_raw(g, x, k, s, gx, gk, gs if s is not None else None, kbatch, periodic)
+    return gx, gk, gs
+
+
+@shifted_fftconv1d_backward_op.register_fake
+def _(g, x, k, s, kbatch, periodic):
+    return torch.empty_like(x), torch.empty_like(k), x.new_empty(kbatch * x.shape[1] if s is not None else 0,
+                                                                 dtype=torch.float32)
+
+
+def _shifted_setup(ctx, inputs, output):
+    x, k, s, kbatch, periodic = inputs
+    ctx.save_for_backward(x, k, s)
+    ctx.kbatch, ctx.periodic = kbatch, periodic
+
+
+def _shifted_backward(ctx, gy):
+    x, k, s = ctx.saved_tensors
+    g = gy.to(x.dtype).contiguous()
+    gx, gk, gs = shifted_fftconv1d_backward_op(g, x, k, s, ctx.kbatch, ctx.periodic)
+    return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None
+
+
+shifted_fftconv1d_op.register_autograd(_shifted_backward, setup_context=_shifted_setup)
 
 
 def shifted_fftconv1d(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, periodic: int):
@@ -549,7 +632,7 @@ def shifted_fftconv1d(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Ten
     xc = x.to(compute_dtype).contiguous()
     kc = kernel.float().reshape(kbatch * H, kernel.shape[-1]).contiguous()
     sc = None if shortcut is None else shortcut.to(compute_dtype).contiguous()
-    return _ShiftedFFTConv1d.apply(xc, kc, sc, kbatch, int(periodic)).to(input_dtype)
+    return shifted_fftconv1d_op(xc, kc, sc, kbatch, int(periodic)).to(input_dtype)
 
 
 def fftconv1d_bhl(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None = None) -> torch.Tensor:

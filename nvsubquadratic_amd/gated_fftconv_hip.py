@@ -22,7 +22,10 @@ reference composition with each elementwise product rounded to the I/O dtype.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
+from torch.library import custom_op
 
 from . import _lib
 from .fftconv_hip import _kernel_3d, _workspace
@@ -92,33 +95,73 @@ def gated_causal_fftconv1d_bwd_raw(g, q, kg, v, y1, k, s, dq, dkg, dv, gk, gs, a
         int(bool(fuse_gates)), _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_ptr(q.device)))
 
 
-class _GatedCausalFFTConv1d(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, kg, v, k, s, act1, act2, kbatch, fuse_bwd=False):
-        y = torch.empty_like(q)
-        keep = any(ctx.needs_input_grad[:5])
-        y1 = torch.empty_like(q) if keep else None
-        gated_causal_fftconv1d_fwd_raw(q, kg, v, k, s, y, y1, act1, act2, kbatch)
-        ctx.save_for_backward(q, kg, v, y1, k, s)
-        ctx.acts = (act1, act2)
-        ctx.kbatch = kbatch
-        ctx.fuse_bwd = fuse_bwd
-        ctx.has_s = s is not None
-        return y
+def _grad_wanted(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
-    @staticmethod
-    def backward(ctx, gy):
-        q, kg, v, y1, k, s = ctx.saved_tensors
-        g = _aligned16(gy.to(q.dtype).contiguous())
-        dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-        gk = torch.empty_like(k)
-        H = q.shape[1]
-        gs = torch.empty(ctx.kbatch * H, dtype=torch.float32, device=q.device) if ctx.has_s else None
-        gated_causal_fftconv1d_bwd_raw(g, q, kg, v, y1, k, s, dq, dkg, dv, gk, gs, *ctx.acts, ctx.kbatch, ctx.fuse_bwd)
-        gsum = None
-        if ctx.has_s:
-            gsum = (gs if ctx.kbatch == 1 else gs.view(ctx.kbatch, H).sum(0)).to(s.dtype)
-        return dq, dkg, dv, gk, gsum, None, None, None, None
+
+def _shortcut_grad(gs, s, kbatch, H):
+    if s is None:
+        return None
+    return (gs if kbatch == 1 else gs.view(kbatch, H).sum(0)).to(s.dtype)
+
+
+@custom_op("nsq_hip::gated_causal_fftconv1d", mutates_args=())
+def gated_causal_fftconv1d_op(q: torch.Tensor, kg: torch.Tensor, v: torch.Tensor, k: torch.Tensor,
+                              s: Optional[torch.Tensor], act1: int, act2: int, kbatch: int, keep: bool,
+                              fuse_bwd: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Gated causal conv forward; returns ``(y, y1)``, y1 = conv(z) + s z kept for the backward when ``keep``
+    (else empty).  ``fuse_bwd`` selects the backward's one-kernel gated adjoint (recorded for the backward)."""
+    q, kg, v = (_aligned16(t) for t in (q, kg, v))
+    y = torch.empty_like(q)
+    y1 = torch.empty_like(q) if keep else q.new_empty(0)
+    gated_causal_fftconv1d_fwd_raw(q, kg, v, k, s, y, y1 if keep else None, act1, act2, kbatch)
+    return y, y1
+
+
+@gated_causal_fftconv1d_op.register_fake
+def _(q, kg, v, k, s, act1, act2, kbatch, keep, fuse_bwd):
+    return torch.empty_like(q), (torch.empty_like(q) if keep else q.new_empty(0))
+
+
+@custom_op("nsq_hip::gated_causal_fftconv1d_backward", mutates_args=())
+def gated_causal_fftconv1d_backward_op(g: torch.Tensor, q: torch.Tensor, kg: torch.Tensor, v: torch.Tensor,
+                                       y1: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor], act1: int,
+                                       act2: int, kbatch: int, fuse: bool) -> tuple[torch.Tensor, torch.Tensor,
+                                                                                   torch.Tensor, torch.Tensor,
+                                                                                   torch.Tensor]:
+    """``(dq, dkg, dv, gk, gs)``; gs ``[kbatch*H]`` partials, empty without a shortcut."""
+    g, q, kg, v = (_aligned16(t) for t in (g, q, kg, v))
+    dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    gk = torch.empty_like(k)
+    gs = torch.empty(kbatch * q.shape[1] if s is not None else 0, dtype=torch.float32, device=q.device)
+    gated_causal_fftconv1d_bwd_raw(g, q, kg, v, y1, k, s, dq, dkg, dv, gk, gs if s is not None else None, act1, act2,
+                                   kbatch, fuse)
+    return dq, dkg, dv, gk, gs
+
+
+@gated_causal_fftconv1d_backward_op.register_fake
+def _(g, q, kg, v, y1, k, s, act1, act2, kbatch, fuse):
+    return (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q), torch.empty_like(k),
+            q.new_empty(kbatch * q.shape[1] if s is not None else 0, dtype=torch.float32))
+
+
+def _gated1d_setup(ctx, inputs, output):
+    q, kg, v, k, s, act1, act2, kbatch, _keep, fuse_bwd = inputs
+    ctx.save_for_backward(q, kg, v, output[1], k, s)
+    ctx.meta = (act1, act2, kbatch)
+    ctx.fuse_bwd = fuse_bwd
+
+
+def _gated1d_backward(ctx, gy, _gy1):
+    q, kg, v, y1, k, s = ctx.saved_tensors
+    act1, act2, kbatch = ctx.meta
+    g = gy.to(q.dtype).contiguous()
+    dq, dkg, dv, gk, gs = gated_causal_fftconv1d_backward_op(g, q, kg, v, y1, k, s, act1, act2, kbatch,
+                                                             ctx.fuse_bwd)
+    return dq, dkg, dv, gk, _shortcut_grad(gs, s, kbatch, q.shape[1]), None, None, None, None, None
+
+
+gated_causal_fftconv1d_op.register_autograd(_gated1d_backward, setup_context=_gated1d_setup)
 
 
 def hyena_gated_causal_fftconv1d_bhl(
@@ -152,67 +195,102 @@ def hyena_gated_causal_fftconv1d_bhl(
     kbatch = k3.shape[0]
     in_dtype = query.dtype
     cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
-    q, kg, v = (_aligned16(t.to(cdt).contiguous()) for t in (query, key, value))
+    q, kg, v = (t.to(cdt).contiguous() for t in (query, key, value))
     kc = k3.float().reshape(kbatch * H, k3.shape[-1]).contiguous()
     sc = None
     if shortcut is not None:
         if shortcut.shape != (H,):
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         sc = shortcut.to(in_dtype).to(cdt).contiguous()
-    return _GatedCausalFFTConv1d.apply(q, kg, v, kc, sc, act1, act2, kbatch, fuse_backward_gates).to(in_dtype)
+    y, _ = gated_causal_fftconv1d_op(q, kg, v, kc, sc, act1, act2, kbatch, _grad_wanted(q, kg, v, kc, sc),
+                                     bool(fuse_backward_gates))
+    return y.to(in_dtype)
 
 
 # ---------------------------------------------------------------------------
 # 2D / 3D: the gate kernels around the N-d conv (nsq_gated_fftconv_nd_*)
 # ---------------------------------------------------------------------------
-class _GatedFFTConvND(torch.autograd.Function):
-    """q, kg, v: [B, H, *S] contiguous; k: [kbatch*H, *K] contiguous float32; s: [H] or None."""
+def _gated_nd_ws(q, k, kbatch, periodic, direction):
+    lib = _lib.get_lib()
+    nd = q.ndim - 2
+    return int(lib.nsq_gated_fftconv_nd_workspace_bytes(
+        nd, int(q.shape[0]), int(q.shape[1]), _lib.i64_array([int(d) for d in q.shape[2:]]),
+        _lib.i64_array([int(d) for d in k.shape[1:]]), kbatch, periodic, _lib.dtype_code(q.dtype), direction))
 
-    @staticmethod
-    def forward(ctx, q, kg, v, k, s, act1, act2, kbatch, periodic):
-        lib = _lib.get_lib()
-        _lib.check_device(q)
-        nd = q.ndim - 2
-        B, H = q.shape[:2]
-        S, K = _lib.i64_array(q.shape[2:]), _lib.i64_array(k.shape[1:])
-        dt = _lib.dtype_code(q.dtype)
-        y = torch.empty_like(q)
-        keep = any(ctx.needs_input_grad[:5])
-        y1 = torch.empty_like(q) if keep else None
-        ws = _workspace(q.device, lib.nsq_gated_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dt,
-                                                                            _lib.NSQ_DIR_FWD))
-        _lib.check(lib.nsq_gated_fftconv_nd_fwd(
-            nd, q.data_ptr(), kg.data_ptr(), v.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(), _lib.ptr(y1), dt,
-            act1, act2, B, H, S, K, kbatch, periodic, _lib.ptr(ws), 0 if ws is None else ws.numel(),
-            _lib.stream_ptr(q.device)))
-        ctx.save_for_backward(q, kg, v, y1, k, s)
-        ctx.meta = (act1, act2, kbatch, periodic)
-        ctx.has_s = s is not None
-        return y
 
-    @staticmethod
-    def backward(ctx, gy):
-        q, kg, v, y1, k, s = ctx.saved_tensors
-        act1, act2, kbatch, periodic = ctx.meta
-        lib = _lib.get_lib()
-        nd = q.ndim - 2
-        B, H = q.shape[:2]
-        S, K = _lib.i64_array(q.shape[2:]), _lib.i64_array(k.shape[1:])
-        dt = _lib.dtype_code(q.dtype)
-        g = _aligned16(gy.to(q.dtype).contiguous())
-        dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-        gk = torch.empty_like(k)
-        gs = torch.empty(kbatch * H, dtype=torch.float32, device=q.device) if ctx.has_s else None
-        ws = _workspace(q.device, lib.nsq_gated_fftconv_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dt,
-                                                                            _lib.NSQ_DIR_BWD))
-        _lib.check(lib.nsq_gated_fftconv_nd_bwd(
-            nd, g.data_ptr(), q.data_ptr(), kg.data_ptr(), v.data_ptr(), y1.data_ptr(), k.data_ptr(), _lib.ptr(s),
-            dq.data_ptr(), dkg.data_ptr(), dv.data_ptr(), gk.data_ptr(), _lib.ptr(gs), dt, act1, act2, B, H, S, K,
-            kbatch, periodic, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_ptr(q.device)))
-        gsum = None
-        if ctx.has_s:
-            gsum = (gs if kbatch == 1 else gs.view(kbatch, H).sum(0)).to(s.dtype)
-        return dq, dkg, dv, gk, gsum, None, None, None, None
+@custom_op("nsq_hip::gated_fftconv_nd", mutates_args=())
+def gated_fftconv_nd_op(q: torch.Tensor, kg: torch.Tensor, v: torch.Tensor, k: torch.Tensor,
+                        s: Optional[torch.Tensor], act1: int, act2: int, kbatch: int, periodic: int,
+                        keep: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Gated 2D/3D conv forward: q, kg, v ``[B, H, *S]`` contiguous, k ``[kbatch*H, *K]`` float32, s ``[H]`` or None;
+    returns ``(y, y1)`` with y1 kept when ``keep`` (else empty)."""
+    lib = _lib.get_lib()
+    _lib.check_device(q)
+    nd = q.ndim - 2
+    B, H = q.shape[:2]
+    S, K = _lib.i64_array(q.shape[2:]), _lib.i64_array(k.shape[1:])
+    dt = _lib.dtype_code(q.dtype)
+    q, kg, v = (_aligned16(t) for t in (q, kg, v))
+    y = torch.empty_like(q)
+    y1 = torch.empty_like(q) if keep else q.new_empty(0)
+    ws = _workspace(q.device, _gated_nd_ws(q, k, kbatch, periodic, _lib.NSQ_DIR_FWD))
+    _lib.check(lib.nsq_gated_fftconv_nd_fwd(
+        nd, q.data_ptr(), kg.data_ptr(), v.data_ptr(), k.data_ptr(), _lib.ptr(s), y.data_ptr(),
+        y1.data_ptr() if keep else None, dt, act1, act2, B, H, S, K, kbatch, periodic, _lib.ptr(ws),
+        0 if ws is None else ws.numel(), _lib.stream_ptr(q.device)))
+    return y, y1
+
+
+@gated_fftconv_nd_op.register_fake
+def _(q, kg, v, k, s, act1, act2, kbatch, periodic, keep):
+    return torch.empty_like(q), (torch.empty_like(q) if keep else q.new_empty(0))
+
+
+@custom_op("nsq_hip::gated_fftconv_nd_backward", mutates_args=())
+def gated_fftconv_nd_backward_op(g: torch.Tensor, q: torch.Tensor, kg: torch.Tensor, v: torch.Tensor,
+                                 y1: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor], act1: int, act2: int,
+                                 kbatch: int, periodic: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                      torch.Tensor, torch.Tensor]:
+    """``(dq, dkg, dv, gk, gs)``; gs ``[kbatch*H]`` partials, empty without a shortcut."""
+    lib = _lib.get_lib()
+    nd = q.ndim - 2
+    B, H = q.shape[:2]
+    S, K = _lib.i64_array(q.shape[2:]), _lib.i64_array(k.shape[1:])
+    dt = _lib.dtype_code(q.dtype)
+    g, q, kg, v = (_aligned16(t) for t in (g, q, kg, v))
+    dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    gk = torch.empty_like(k)
+    gs = torch.empty(kbatch * H if s is not None else 0, dtype=torch.float32, device=q.device)
+    ws = _workspace(q.device, _gated_nd_ws(q, k, kbatch, periodic, _lib.NSQ_DIR_BWD))
+    _lib.check(lib.nsq_gated_fftconv_nd_bwd(
+        nd, g.data_ptr(), q.data_ptr(), kg.data_ptr(), v.data_ptr(), y1.data_ptr(), k.data_ptr(), _lib.ptr(s),
+        dq.data_ptr(), dkg.data_ptr(), dv.data_ptr(), gk.data_ptr(), gs.data_ptr() if s is not None else None, dt,
+        act1, act2, B, H, S, K, kbatch, periodic, _lib.ptr(ws), 0 if ws is None else ws.numel(),
+        _lib.stream_ptr(q.device)))
+    return dq, dkg, dv, gk, gs
+
+
+@gated_fftconv_nd_backward_op.register_fake
+def _(g, q, kg, v, y1, k, s, act1, act2, kbatch, periodic):
+    return (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q), torch.empty_like(k),
+            q.new_empty(kbatch * q.shape[1] if s is not None else 0, dtype=torch.float32))
+
+
+def _gatednd_setup(ctx, inputs, output):
+    q, kg, v, k, s, act1, act2, kbatch, periodic, _keep = inputs
+    ctx.save_for_backward(q, kg, v, output[1], k, s)
+    ctx.meta = (act1, act2, kbatch, periodic)
+
+
+def _gatednd_backward(ctx, gy, _gy1):
+    q, kg, v, y1, k, s = ctx.saved_tensors
+    act1, act2, kbatch, periodic = ctx.meta
+    g = gy.to(q.dtype).contiguous()
+    dq, dkg, dv, gk, gs = gated_fftconv_nd_backward_op(g, q, kg, v, y1, k, s, act1, act2, kbatch, periodic)
+    return dq, dkg, dv, gk, _shortcut_grad(gs, s, kbatch, q.shape[1]), None, None, None, None, None
+
+
+gated_fftconv_nd_op.register_autograd(_gatednd_backward, setup_context=_gatednd_setup)
 
 
 def hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut=None, gate_nonlinear="silu",
@@ -239,14 +317,15 @@ def hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut=None, gate_no
     kbatch = k.shape[0]
     in_dtype = query.dtype
     cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
-    q, kg, v = (_aligned16(t.to(cdt).contiguous()) for t in (query, key, value))
+    q, kg, v = (t.to(cdt).contiguous() for t in (query, key, value))
     kc = k.float().reshape(kbatch * H, *k.shape[2:]).contiguous()
     sc = None
     if shortcut is not None:
         if shortcut.shape != (H,):
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         sc = shortcut.to(in_dtype).to(cdt).contiguous()
-    return _GatedFFTConvND.apply(q, kg, v, kc, sc, act1, act2, kbatch, periodic_mask(per)).to(in_dtype)
+    y, _ = gated_fftconv_nd_op(q, kg, v, kc, sc, act1, act2, kbatch, periodic_mask(per), _grad_wanted(q, kg, v, kc, sc))
+    return y.to(in_dtype)
 
 
 def hyena_gated_fftconv2d_bhl(query, key, value, kernel, shortcut=None, gate_nonlinear="silu",

@@ -154,3 +154,41 @@ def test_noalloc_backward_refuses_oversize_scratch_on_the_host():
     rc = lib.nsq_causal_conv1d_bwd_noalloc(fake, fake, fake, None, fake, fake, None, 0, 0, B, C, L, K, None)
     assert rc == 2  # NSQ_ERR_UNSUPPORTED
     assert b"scratch" in lib.nsq_last_error()
+
+
+_OPS = ["causal_fftconv1d", "fftconv_nd", "shifted_fftconv1d", "causal_conv1d", "b2b_causal_conv1d",
+        "gated_causal_fftconv1d", "gated_fftconv_nd"]
+
+
+def test_every_hip_op_is_a_registered_custom_op():
+    """Each op and its backward are torch.library custom ops (traceable by torch.compile)."""
+    import nvsubquadratic_amd.causal_conv1d_hip  # noqa: F401
+    import nvsubquadratic_amd.gated_fftconv_hip  # noqa: F401
+
+    for name in _OPS:
+        for n in (name, name + "_backward"):
+            schema = str(getattr(torch.ops.nsq_hip, n).default._schema)
+            assert schema.startswith(f"nsq_hip::{n}(")
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_fake_implementations_propagate_shapes_without_a_gpu():
+    """The fake (meta) implementations give the real ops' output shapes and the forward-state size the C ABI
+    reports, with no device code involved."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    lib = _lib.get_lib()
+    with FakeTensorMode():
+        x = torch.empty(2, 4, 50000)
+        k = torch.empty(4, 50000)
+        s = torch.empty(4)
+        y, state = torch.ops.nsq_hip.causal_fftconv1d(x, k, s, 1, True)
+        assert y.shape == x.shape and state.dtype == torch.uint8
+        assert state.numel() == lib.nsq_fftconv1d_causal_workspace_bytes(2, 4, 50000, 50000, _lib.NSQ_DIR_BWD)
+        gx, gk, gs = torch.ops.nsq_hip.causal_fftconv1d_backward(x, x, k, s, state, 1)
+        assert gx.shape == x.shape and gk.shape == k.shape and gs.shape == (4,)
+        x2 = torch.empty(2, 3, 16, 12)
+        y2, st2 = torch.ops.nsq_hip.fftconv_nd(x2, torch.empty(3, 5, 7), None, 1, 0, False)
+        assert y2.shape == x2.shape and st2.numel() == 0
+        yb = torch.ops.nsq_hip.b2b_causal_conv1d(torch.empty(2, 12, 64), torch.empty(12, 3), torch.empty(4, 9), None)
+        assert yb.shape == (2, 4, 64)
