@@ -129,6 +129,87 @@ def measured_traffic() -> int | None:
     return int(round(total)) if total else None
 
 
+def cpu_baseline_other(name: str, iters: int = 3) -> dict:
+    """The oracle (float32 torch on all the host cores) on the whole of config 1, 2, 4 or 5, the phase the GPU line
+    times: at least ``iters`` steps after a warmup, more while under ~10 s; the median step."""
+    from nvsubquadratic_amd.workloads import (algorithmic_bytes_b2b, algorithmic_bytes_causal1d,
+                                              algorithmic_bytes_nd, causal1d_case_fast, radial_filter)
+    from oracle.direct_ref import b2b_causal_conv1d_torch
+    from oracle.fftconv_ref import causal_fftconv1d_torch, fftconv_nd_torch
+
+    n_threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n_threads)
+    gen = torch.Generator().manual_seed(0)
+    if name == "cfg1":
+        B, D, L = 2, 128, 4096
+        c = causal1d_case_fast(B, D, L, torch.float32, (1.0, 10.0), "cpu", seed=0)
+        run = lambda: causal_fftconv1d_torch(c.x, c.k[None], c.s)  # noqa: E731
+        nbytes = algorithmic_bytes_causal1d(B, D, L, L, 4, "fwd")
+        what = "whole config (B=2 D=128 L=4096 fp32), forward, torch.fft"
+    elif name == "cfg2":
+        B, C, L = 4, 4096, 8192
+        x = torch.randn(B, 3 * C, L, generator=gen).to(torch.bfloat16)
+        wp = torch.randn(3 * C, 3, generator=gen)
+        wm = torch.randn(C, 128, generator=gen) / 128 ** 0.5
+        run = lambda: b2b_causal_conv1d_torch(x, wp, wm, None)  # noqa: E731
+        nbytes = algorithmic_bytes_b2b(B, C, L, 3, 128, 2)
+        what = "whole config (B=4 D=4096 L=8192, k=3 then k=128, bf16 I/O), forward, torch conv1d fp32"
+    elif name in ("cfg4", "cfg5"):
+        nd = 2 if name == "cfg4" else 3
+        B, C, size, sig = (16, 384, 128, (4.0, 64.0)) if nd == 2 else (2, 128, 64, (2.0, 32.0))
+        x = torch.randn(B, C, *([size] * nd), generator=gen).to(torch.bfloat16)
+        k = radial_filter(C, size, sig[0], sig[1], nd, gen)
+        sv = torch.randn(C, generator=gen).to(torch.bfloat16)
+        if nd == 2:
+            run = lambda: fftconv_nd_torch(x, k, sv)  # noqa: E731
+            phase = "fwd"
+        else:
+            g = torch.randn(x.shape, generator=gen).to(torch.bfloat16)
+
+            def run():
+                xx, kk, ss = (t.clone().requires_grad_(True) for t in (x, k, sv))
+                fftconv_nd_torch(xx, kk, ss).backward(g)
+            phase = "fwd+bwd"
+        nbytes = algorithmic_bytes_nd(B, C, [size] * nd, [size] * nd, 2, phase)
+        what = (f"whole config (B={B} C={C}, {size}^{nd}, bf16 I/O), {phase}, torch.fft fp32 at the reference's "
+                f"FFT size")
+    else:
+        return {}
+    times, t_start = [], time.perf_counter()
+    for it in range(1000):
+        t0 = time.perf_counter()
+        with torch.set_grad_enabled(name == "cfg5"):
+            run()
+        if it > 0:
+            times.append(time.perf_counter() - t0)
+        if len(times) >= iters and time.perf_counter() - t_start > 10.0:
+            break
+    med = statistics.median(times)
+    return {
+        "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": n_threads, "kind": "port",
+        "ms_per_step": round(med * 1e3, 2),
+        "sample": f"{what}; median of {len(times)} steps after 1 warmup (at least {iters}, ~10 s); value = algorithmic "
+                  f"bytes of the sample / median time",
+    }
+
+
+def counter_traffic(profile: str) -> int | None:
+    """HBM bytes of one step from a committed counter summary (its 'step total' read + write GB, already scaled
+    by the copy calibration)."""
+    try:
+        for ln in open(os.path.join(ROOT, "profiles", profile)):
+            t = ln.split()
+            if len(t) >= 4 and t[0] == "step" and t[1] == "total":
+                return int(round((float(t[3]) + float(t[4])) * 1e9))
+    except (OSError, ValueError, IndexError):
+        return None
+    return None
+
+
+_COUNTER_PROFILES = {"cfg1": "fftconv1d_causal_cfg1_fwd_counters.md", "cfg2": "b2b_cfg2_fwd_counters.md",
+                     "cfg4": "fftconv2d_cfg4_fwd_counters.md", "cfg5": "fftconv3d_cfg5_fwd_bwd_counters.md"}
+
+
 def _time_steps(step, steps: int, warmup: int) -> list[float]:
     """Event-timed steps on the current stream (ms each) after untimed warmup."""
     for _ in range(warmup):
@@ -144,7 +225,7 @@ def _time_steps(step, steps: int, warmup: int) -> list[float]:
     return [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
 
 
-def other_workload(name: str, steps: int, warmup: int) -> None:
+def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None:
     """Configs 1, 2, 4, 5 of the benchmark set (inputs resident in HBM)."""
     from nvsubquadratic_amd import causal_conv1d_hip as CC
     from nvsubquadratic_amd import fftconv_hip as F
@@ -329,6 +410,11 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
     ms_list = _time_steps(step, steps, warmup)
     ms = statistics.mean(ms_list)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    if name in _COUNTER_PROFILES:
+        extra["roofline_traffic_source"] = f"profiles/{_COUNTER_PROFILES[name]}"
+    if cpu and name in ("cfg1", "cfg2", "cfg4", "cfg5"):
+        _log("cpu baseline")
+        extra["cpu_baseline"] = cpu_baseline_other(name)
     print(json.dumps({
         "metric": f"{name} {phase} algorithmic HBM GB/s, 1 MI355X",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -336,7 +422,8 @@ def other_workload(name: str, steps: int, warmup: int) -> None:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic", "config": {"workload": desc},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+                     "traffic": counter_traffic(_COUNTER_PROFILES[name]) if name in _COUNTER_PROFILES else None},
         **extra,
     }), flush=True)
 
@@ -366,7 +453,7 @@ def main() -> None:
         copy_calibration()
         return
     if args.workload != "cfg3":
-        other_workload(args.workload, args.steps, args.warmup)
+        other_workload(args.workload, args.steps, args.warmup, cpu=not args.no_cpu)
         return
 
     from nvsubquadratic_amd import _lib
