@@ -12,7 +12,15 @@ Contents:
 * :mod:`oracle.direct` -- ctypes binding of ``direct_conv.c``: brute-force
   float64 direct convolutions that pin the FFT restatement independently of any
   FFT.
-* :mod:`oracle.inputs` -- seeded synthetic inputs for the BASELINE configs.
+* :mod:`oracle.direct_ref` -- torch restatements of the depthwise causal conv
+  (``CausalConv1D``) and of the B2B block's specification.
+* :mod:`oracle.circular_ref` -- circular and mixed-boundary restatements
+  (``ops/circular_fftconv.py``, ``ops/mixed_fftconv.py``) and their float64
+  brute forces.
+* :mod:`oracle.gated_ref` -- the Hyena gate compositions around the long conv.
+
+The seeded synthetic inputs of the benchmark configs are product-side
+(``nvsubquadratic_amd.workloads``): they are data, not a checker.
 
 Parity status of every function is listed in the module docstrings; a function
 with no independent check says "parity unpinned".
