@@ -12,8 +12,10 @@
 //    to global memory through functors, so a transform that starts and ends
 //    in HBM costs only (passes - 1) LDS round trips.
 //  * Twiddles of transforms up to 2^14 come from the table built in
-//    twiddle.hip (double-precision roots rounded once); longer-period roots
-//    use the hardware sin/cos (see root<> below).  No recurrences on device.
+//    twiddle.hip (double-precision roots rounded once), a pass loading the
+//    roots at r = 1, 2, 4, 8 and forming the others as products of two
+//    (pass_twiddles); longer-period roots use the hardware sin/cos (see root<>
+//    below).  No running recurrences on device.
 #pragma once
 
 #include <type_traits>
@@ -112,6 +114,31 @@ __device__ __forceinline__ float2 const_twiddle(float2 a) {
     // forward multiplies by (c - i s), inverse by (c + i s)
     return INV ? make_float2(a.x * c - a.y * s, a.y * c + a.x * s)
                : make_float2(a.x * c + a.y * s, a.y * c - a.x * s);
+  }
+}
+
+// Complex product with its two fused multiply-adds written out, so every
+// kernel that inlines it rounds identically (with contraction left to the
+// compiler, a*b - c*d may become fma(a, b, -c*d) in one kernel and
+// fma(-c, d, a*b) in another).  Used for the roots this file derives from
+// table roots, which kernels of different plans must reproduce bit for bit.
+__device__ __forceinline__ float2 cmul_fixed(float2 a, float2 b) {
+  return make_float2(__builtin_fmaf(a.x, b.x, -(a.y * b.y)), __builtin_fmaf(a.x, b.y, a.y * b.x));
+}
+
+// a * W_16^i for i in [0, 8); i is a constant after unrolling, so one case
+// remains.  The roots are the correctly rounded float constants.
+__device__ __forceinline__ float2 rot16(float2 a, int i) {
+  constexpr float c1 = 0.92387953251128675613f, s1 = 0.38268343236508977173f, r2 = 0.70710678118654752440f;
+  switch (i) {
+    case 1: return cmul_fixed(a, make_float2(c1, -s1));
+    case 2: return cmul_fixed(a, make_float2(r2, -r2));
+    case 3: return cmul_fixed(a, make_float2(s1, -c1));
+    case 4: return mul_neg_i(a);
+    case 5: return cmul_fixed(a, make_float2(-s1, -c1));
+    case 6: return cmul_fixed(a, make_float2(-r2, -r2));
+    case 7: return cmul_fixed(a, make_float2(-c1, -s1));
+    default: return a;
   }
 }
 
@@ -214,6 +241,35 @@ struct TwTable {
   }
 };
 
+// The R-1 twiddles W_S^{r k} (r = 1..R-1) of one butterfly, S = the segment
+// of this pass.  Only the roots at r = 1, 2, 4, 8 are table loads; the others
+// are products of two of them (r = 3 = 2+1, 5..7 = 4 + 1..3, 9..15 = 8 +
+// 1..7), at most three products deep (W^{15k} = W^{8k} (W^{4k} (W^{2k}
+// W^k))): a few ulp (measured 2.3e-7 rel-L2 over a 2^19-point transform
+// against all-table twiddles).  Measured on MI355X: each vector-memory load
+// of a pass waits, in issue order, behind the tile's HBM loads and stores, so
+// 4 loads and 11 complex products per radix-16 butterfly instead of 15 loads
+// take ~10% off the 4-step row kernels, whose VALU is far from busy.
+template <int R>
+__device__ __forceinline__ void pass_twiddles(const TwTable& tt, int seg, int k, float2* w) {
+  w[1] = tt.load(seg, k);
+  if constexpr (R >= 4) {
+    w[2] = tt.load(seg, 2 * k);
+    w[3] = cmul_fixed(w[2], w[1]);
+  }
+  if constexpr (R >= 8) {
+    w[4] = tt.load(seg, 4 * k);
+#pragma unroll
+    for (int r = 5; r < 8; ++r) w[r] = cmul_fixed(w[4], w[r - 4]);
+  }
+  if constexpr (R >= 16) {
+    w[8] = tt.load(seg, 8 * k);
+#pragma unroll
+    for (int r = 9; r < 16; ++r) w[r] = cmul_fixed(w[8], w[r - 8]);
+  }
+  static_assert(R <= 16, "pass_twiddles: radix up to 16");
+}
+
 // ---------------------------------------------------------------------------
 // One radix-2^LOGR Stockham pass over M transforms of length 2^LOGN executed by
 // T threads.  LD(m, n) -> float2 reads input element n of transform m; ST(m, n,
@@ -244,8 +300,7 @@ __device__ __forceinline__ void stockham_pass(LD& ld, ST& st, const float2* __re
       const int bf = tid + i * T;
       const int j = TMAJOR ? (bf / M) : (bf & (NR - 1));
       const int k = j & (NS - 1);
-#pragma unroll
-      for (int r = 1; r < R; ++r) w[i][r] = tt.load(1 << (LOGNS + LOGR), r * k);
+      pass_twiddles<R>(tt, 1 << (LOGNS + LOGR), k, w[i]);
     }
   }
   float2 v[PER][R];

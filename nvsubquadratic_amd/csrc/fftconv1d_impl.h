@@ -631,6 +631,7 @@ struct RowSlots {
   int corr;    // q == 0 first half: pad16(N2 - s) = pad16(N2 - 1) - pad16(s) + 1 + (s % 16 == 0)
   float2 u0;   // W_2N^q (q > 0), 1 (q == 0)
   float2 u1;   // W_2N^{N1/2} * i (q == 0, second half)
+  float2 wt;   // W_{2 N2}^t: slot i's table root W_{2 N2}^{t + i T} is wt * W_16^i (2 N2 = 16 T)
   __device__ __forceinline__ RowSlots(int q, const float2* __restrict__ tw) : RowSlots(q, tw, opaque_tid()) {}
   // tl: the thread's index among the T threads of its row pair (a workgroup
   // may run several row pairs side by side, each on its own 2-row sub-tile).
@@ -642,6 +643,7 @@ struct RowSlots {
     corr = (t & 15) == 0 ? 1 : 0;
     u0 = qz ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, uint32_t(q));
     u1 = mul_i(root<LOGN + 1>(tw, uint32_t(N1 / 2)));
+    wt = tt.load(2 * N2, t);
   }
   __device__ __forceinline__ bool s0(int i) const { return qz && i == 0 && t == 0; }
   __device__ __forceinline__ void at(int i, int& pa, int& pb, float2& w) const {
@@ -652,7 +654,8 @@ struct RowSlots {
     const int ub = !qz ? N2P + pad16(N2 - 1) : (sec ? N2P + pad16(3 * N2 / 2 - 1) : pad16(N2 - 1) + 1);
     pb = ub - base - oi + (f0 ? corr : 0);
     pb = s0(i) ? pad16(N2 / 2) : pb;
-    w = cmul(sec ? u1 : u0, tt.load(2 * N2, t + i * T));
+    static_assert(2 * N2 == 16 * T, "RowSlots: slot roots step by W_16");
+    w = cmul_fixed(sec ? u1 : u0, rot16(wt, i));
   }
 };
 

@@ -3,8 +3,9 @@
 // One immutable table per device, built on first use and kept for the life of
 // the process: the library's only device allocation outside caller-provided
 // buffers.  Layout (float2 = (cos, -sin), i.e. forward-transform roots):
-//   [0, 2^14): W_{2^14}^j = exp(-2*pi*i*j/2^14)
-// A root of unity W_{2^b}^m with b <= 14 is one load (table[m << (14-b)]).
+//   segment b (b = 0..14) at entries [2^b, 2^(b+1)): W_{2^b}^j = exp(-2*pi*i*j/2^b)
+// so a root of unity W_{2^b}^m with b <= 14 is one load, table[2^b + m], and a
+// pass of a length-2^b transform reads one contiguous 2^b-entry segment.
 // Values are computed on the host in double precision and rounded once to
 // float (within 0.5 ulp of the exact root).
 #include <cmath>

@@ -215,12 +215,27 @@ def _shortcut_grad(gs: torch.Tensor, s: torch.Tensor | None, kbatch: int, H: int
 
 def _causal_setup(ctx, inputs, output):
     x, k, s, kbatch, _keep = inputs
-    ctx.save_for_backward(x, k, s, output[1])
+    # the second output is internal (state kept for the backward): no gradient flows into it, and none is
+    # materialized for it (autograd would otherwise fill a zero tensor of its size before every backward)
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(x, k, s)
+    ctx.state = output[1]
     ctx.kbatch = kbatch
 
 
+def _take_state(ctx) -> torch.Tensor:
+    """The forward's state for this backward.  The backward consumes it (overwrites it in place), so a second
+    backward through the same graph (``retain_graph=True``) gets an empty state and recomputes the transforms.  The
+    state is kept on ctx, not saved: the in-place use would fail saved-tensor version checks."""
+    state = ctx.state
+    ctx.state = state.new_empty(0)
+    return state
+
+
 def _causal_backward(ctx, gy, _gstate):
-    x, k, s, state = ctx.saved_tensors
+    x, k, s = ctx.saved_tensors
+    state = _take_state(ctx)
     g = gy.to(x.dtype).contiguous()
     gx, gk, gs = causal_fftconv1d_backward_op(g, x, k, s, state, ctx.kbatch)
     return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None
@@ -480,12 +495,18 @@ def _(g, x, k, s, state, kbatch, periodic):
 
 def _nd_setup(ctx, inputs, output):
     x, k, s, kbatch, periodic, _keep = inputs
-    ctx.save_for_backward(x, k, s, output[1])
+    # the second output is internal (state kept for the backward): no gradient flows into it, and none is
+    # materialized for it (autograd would otherwise fill a zero tensor of its size before every backward)
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(x, k, s)
+    ctx.state = output[1]
     ctx.kbatch, ctx.periodic = kbatch, periodic
 
 
 def _nd_backward(ctx, gy, _gstate):
-    x, k, s, state = ctx.saved_tensors
+    x, k, s = ctx.saved_tensors
+    state = _take_state(ctx)
     g = gy.to(x.dtype).contiguous()
     gx, gk, gs = fftconv_nd_backward_op(g, x, k, s, state, ctx.kbatch, ctx.periodic)
     return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None, None

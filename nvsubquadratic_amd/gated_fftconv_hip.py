@@ -147,6 +147,10 @@ def _(g, q, kg, v, y1, k, s, act1, act2, kbatch, fuse):
 
 def _gated1d_setup(ctx, inputs, output):
     q, kg, v, k, s, act1, act2, kbatch, _keep, fuse_bwd = inputs
+    # the second output is internal (state kept for the backward): no gradient flows into it, and none is
+    # materialized for it (autograd would otherwise fill a zero tensor of its size before every backward)
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(q, kg, v, output[1], k, s)
     ctx.meta = (act1, act2, kbatch)
     ctx.fuse_bwd = fuse_bwd
@@ -278,6 +282,10 @@ def _(g, q, kg, v, y1, k, s, act1, act2, kbatch, periodic):
 
 def _gatednd_setup(ctx, inputs, output):
     q, kg, v, k, s, act1, act2, kbatch, periodic, _keep = inputs
+    # the second output is internal (state kept for the backward): no gradient flows into it, and none is
+    # materialized for it (autograd would otherwise fill a zero tensor of its size before every backward)
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(q, kg, v, output[1], k, s)
     ctx.meta = (act1, act2, kbatch, periodic)
 
