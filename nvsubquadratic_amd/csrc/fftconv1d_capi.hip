@@ -36,8 +36,7 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
                 (long long)(2 * L));
   NSQ_CHECK_ARG(B * H <= 0x7fffffff && L <= (int64_t(1) << 30), "fftconv1d_causal: tensor too large");
   if (!make_plan(L, K, p)) {
-    set_error("fftconv1d_causal: unsupported (L=%lld, K=%lld): FFT length beyond 2^23 or K > L+1 above the fused size",
-              (long long)L, (long long)K);
+    set_error("fftconv1d_causal: unsupported (L=%lld, K=%lld): FFT length beyond 2^23", (long long)L, (long long)K);
     return NSQ_ERR_UNSUPPORTED;
   }
   // 4-step column grids are B*H * (N2 / columns per workgroup) <= B*H * 512; per-sample filters run the
@@ -114,8 +113,10 @@ static size_t causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K,
   if (use_team_plan(p, B, kbatch)) return team_workspace_bytes(p, direction);
   const int64_t N = int64_t(1) << p.logN;
   const int64_t nk = kbatch * H;
+  // 4-step blocks of N complex values: x, k (forward: y in place of x, or in a third block kept with x and k for
+  // the backward); backward x, k, g.  K > L+1 adds one block for the wrap copy of x or g (fold_rows_kernel).
   const int64_t rows = (direction == NSQ_DIR_BWD) ? (2 * B * H + nk) : (B * H + nk);
-  return size_t(rows * N) * sizeof(float2);
+  return size_t(rows * N + (p.fold ? B * H * N : 0)) * sizeof(float2);
 }
 
 static int causal_fwd(const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B, int64_t H,

@@ -40,7 +40,8 @@ namespace nsq {
 struct Plan1D {
   int logF;   // real FFT length 2^logF
   int logN;   // packed complex length, logF - 1
-  bool fold;  // K > L+1: reference length 2L wraps; fold full[n + 2L] into y[n]
+  bool fold;  // K > L+1: the reference's FFT length 2L wraps (fused plan: full[n + 2L] folded into y[n];
+              // 4-step plan: a copy of x, or of g in the backward, at the wrap offset; see fold_rows_kernel)
   bool fused;
   int logN1, logN2;  // 4-step split (fused == false)
 };
@@ -61,7 +62,7 @@ inline bool make_plan(int64_t L, int64_t K, Plan1D& p) {
   p.logN = logF - 1;
   p.fused = p.logN <= 13;
   if (!p.fused) {
-    if (p.fold || p.logN > 22) return false;
+    if (p.logN > 22) return false;
     p.logN1 = split_log_n1(p.logN);
     p.logN2 = p.logN - p.logN1;
   } else {
@@ -1039,18 +1040,60 @@ static void launch_col_inv_gk(const float2* ws, float* gk, float* gs, int H, int
                        ws, gk, gs, K, tw);
 }
 
+// K > L+1 on the 4-step plan.  The reference's circular conv at length 2L
+// wraps: y[n] = sum_j k[j] x[(n - j) mod 2L], n < L, K <= 2L.  At the plan's
+// FFT length F >= 3L the same sums come out of the plain circular products
+// when one operand carries a copy of itself at the wrap offset:
+//  * forward: x_ext = x on [0, L) and x[t - (F - 2L)] on [F - 2L, F - L):
+//    for j > n, (n - j) mod F = F + n - j lands in the copy exactly when
+//    n - j + 2L is in [0, L), i.e. the wrapped term x[n - j + 2L];
+//  * backward: g_ext = g on [0, L) and g[t - 2L] on [2L, 3L) (the adjoint
+//    fold of the fused plan): gx[m] = sum_t g_ext[t] k[t - m] and gk[j] =
+//    sum_t g_ext[t] x[t - j] gain the wrapped terms g[n] k[n + 2L - m] and
+//    g[n] x[n + 2L - j].
+// The windows are disjoint (offset >= L) and every other index of [0, F) is
+// beyond both supports, so nothing aliases.  The copy goes to one workspace
+// block of B*H rows of F values (it fits: a block is B*H*N complex values).
+template <int DT>
+__global__ __launch_bounds__(256) void fold_rows_kernel(const typename Elem<DT>::T* __restrict__ src,
+                                                        typename Elem<DT>::T* __restrict__ dst, int64_t rows, int L,
+                                                        int F, int off) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * F) return;
+  const int64_t r = i / F;
+  const int t = int(i - r * F);
+  const int u = t < L ? t : t - off;
+  Elem<DT>::store(dst, i, (u >= 0 && u < L) ? Elem<DT>::load(src, r * L + u) : 0.f);
+}
+
+template <int DT>
+static const void* launch_fold_rows(const void* src, float2* block, int64_t rows, int L, int F, int off,
+                                    hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  const int64_t n = rows * F;
+  hipLaunchKernelGGL((fold_rows_kernel<DT>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, (const ET*)src,
+                     (ET*)block, rows, L, F, off);
+  return block;
+}
+
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
-                             int kfilm, float2* ws, bool save, const float2* tw, hipStream_t st) {
+                             int kfilm, float2* ws, bool save, const float2* tw, hipStream_t st, bool fold) {
   constexpr int LOGN = LOGN1 + LOGN2;
   constexpr int64_t N = int64_t(1) << LOGN;
+  constexpr int F = int(2 * N);
   using ET = typename Elem<DT>::T;
   const int64_t BH = int64_t(B) * H, NK = kfilm ? BH : H;
   const int rb = kfilm ? 1 : B, rh = kfilm ? int(BH) : H;  // row-pass images and channels
   float2* wsx = ws;
   float2* wsk = ws + BH * N;
   float2* wsy = save ? ws + (BH + NK) * N : wsx;
-  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
+  if (fold) {  // x with its wrap copy at F - 2L, in the block after x and k (save is off with a fold)
+    const void* xe = launch_fold_rows<DT>(x, ws + (BH + NK) * N, BH, L, F, F - 2 * L, st);
+    launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)xe, F, F}, BH, wsx, tw, st);
+  } else {
+    launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
+  }
   launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
   hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T),
                      0, st, (const float2*)wsx, (const float2*)wsk, wsy, rb, rh, tw);
@@ -1060,16 +1103,23 @@ static void launch_4step_fwd(const void* x, const float* k, const void* s, void*
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_bwd(const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
                              float* gs, int B, int H, int L, int K, int kfilm, float2* ws, bool fwd_state,
-                             const float2* tw, hipStream_t st) {
+                             const float2* tw, hipStream_t st, bool fold) {
   constexpr int LOGN = LOGN1 + LOGN2;
   constexpr int64_t N = int64_t(1) << LOGN;
+  constexpr int F = int(2 * N);
   using ET = typename Elem<DT>::T;
   const int64_t BH = int64_t(B) * H, NK = kfilm ? BH : H;
   const int rb = kfilm ? 1 : B, rh = kfilm ? int(BH) : H;  // row-pass images and channels
   float2* wsx = ws;
   float2* wsk = ws + BH * N;
   float2* wsg = ws + (BH + NK) * N;
-  launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)g, L, L}, BH, wsg, tw, st);
+  if (fold) {  // g with its adjoint copy at 2L, in the block after g; the forward's x block held x's copy: redo x
+    const void* ge = launch_fold_rows<DT>(g, ws + (2 * BH + NK) * N, BH, L, F, 2 * L, st);
+    launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)ge, F, F}, BH, wsg, tw, st);
+    fwd_state = false;
+  } else {
+    launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)g, L, L}, BH, wsg, tw, st);
+  }
   if (!fwd_state) {
     launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
     launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
@@ -1274,8 +1324,8 @@ bool run_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void
              int kfilm, float2* ws, bool save, const float2* tw, hipStream_t st) {
   if (p.fused)
     return dispatch_int<FusedFwd<DT>::template At, 3, 13>(p.logN, p, x, k, s, y, B, H, L, K, kfilm, tw, st);
-  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, kfilm, ws, save, tw,
-                                                                 st);
+  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, kfilm, ws,
+                                                                 save && !p.fold, tw, st, p.fold);
 }
 
 template <int DT>
@@ -1286,7 +1336,7 @@ bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, cons
     return dispatch_int<FusedBwd<DT>::template At, 3, 13>(p.logN, p, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, tw,
                                                           st);
   return dispatch_int<FourStep<DT, true>::template At, 14, 22>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, ws,
-                                                                fwd_state, tw, st);
+                                                                fwd_state && !p.fold, tw, st, p.fold);
 }
 
 // Gated (Hyena) causal conv.  Fused plan: one gated kernel each way.  4-step

@@ -55,6 +55,10 @@ def test_workspace_query_needs_no_gpu():
     n = 1 << 18
     assert lib.nsq_fftconv1d_causal_workspace_bytes(1, 4096, 262144, 262144, 0) == (4096 + 4096) * n * 8
     assert lib.nsq_fftconv1d_causal_workspace_bytes(1, 4096, 262144, 262144, 1) == (2 * 4096 + 4096) * n * 8
+    # K > L+1 on the 4-step plan (FFT length pow2(3L)): one more block of B*H*N complex values for the wrap copy
+    nf = 1 << 16  # L = 2^15: F = 2^17, N = 2^16
+    assert lib.nsq_fftconv1d_causal_workspace_bytes(2, 3, 32768, 65536, 0) == (6 + 3 + 6) * nf * 8
+    assert lib.nsq_fftconv1d_causal_workspace_bytes(2, 3, 32768, 65536, 1) == (2 * 6 + 3 + 6) * nf * 8
 
 
 def test_per_sample_film_kernel_batch_validated():

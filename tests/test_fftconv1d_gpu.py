@@ -206,6 +206,42 @@ def test_four_step_fp32_fwd_bwd(L, K, B):
     assert rel_l2(s.grad, sg.grad) < RTOL_F32_L2
 
 
+@pytest.mark.parametrize("B,H,L,K,kb", [(1, 3, 32768, 65536, 1), (2, 2, 20000, 30000, 1), (1, 2, 12000, 24000, 1),
+                                        (2, 2, 20000, 40000, 2), (1, 2, 40000, 40002, 1)])
+def test_four_step_kernel_longer_than_l_plus_one(B, H, L, K, kb):
+    """K > L+1 beyond the fused plan (FFT length >= 2^15): the reference's length-2L FFT wraps
+    (fftconv.py:576-580); the 4-step plan adds the wrap through a copy of x (forward) or g (backward)
+    at the wrap offset.  L = 2^15, K = 2L is the longest kernel the reference accepts at that length;
+    kb = B runs per-sample filters; K = L + 2 is the first length that wraps."""
+    torch.manual_seed(L + K)
+    x = torch.randn(B, H, L, requires_grad=True)
+    k = (torch.randn(kb, H, K) / K ** 0.5).requires_grad_(True)
+    s = torch.randn(H, requires_grad=True)
+    y_ref = causal_fftconv1d_torch(x, k, s)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, kg, sg = (t.detach().cuda().requires_grad_(True) for t in (x, k, s))
+    y = F.causal_fftconv1d_bhl(xg, kg, sg)
+    y.backward(g.cuda())
+    assert rel_l2(y_ref, y) < RTOL_F32_L2
+    assert rel_l2(x.grad, xg.grad) < RTOL_F32_L2
+    assert rel_l2(k.grad, kg.grad) < RTOL_F32_L2
+    assert rel_l2(s.grad, sg.grad) < RTOL_F32_L2
+    # no-grad forward (the conv runs in place of x's block, no kept state) gives the same y
+    with torch.no_grad():
+        assert torch.equal(F.causal_fftconv1d_bhl(xg, kg, sg), y)
+
+
+def test_four_step_fold_bf16_against_float64():
+    torch.manual_seed(12)
+    B, H, L, K = 1, 4, 32768, 65536
+    x = torch.randn(B, H, L).to(torch.bfloat16)
+    k = torch.randn(H, K) / K ** 0.5
+    y = F.causal_fftconv1d_bhl(x.cuda(), k.cuda())
+    y64 = causal_fftconv1d_np(x.float().numpy(), k.numpy())
+    assert rel_l2(y64, y) < 5e-3
+
+
 def test_config1_fp32_fwd_bwd():
     """B=2, D=128, L=4096, fp32, decaying filter a~U(1,10)."""
     c = causal1d_case(2, 128, 4096, torch.float32, (1.0, 10.0))

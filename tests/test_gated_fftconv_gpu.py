@@ -44,7 +44,8 @@ def test_fused_plan(B, H, L, K, g1, g2):
 
 
 @pytest.mark.parametrize("g1,g2", [("silu", "sigmoid"), ("identity", "identity")])
-@pytest.mark.parametrize("B,H,L,K", [(2, 3, 16384, 16384), (1, 2, 65536, 4000), (2, 2, 20001, 9000)])
+@pytest.mark.parametrize("B,H,L,K", [(2, 3, 16384, 16384), (1, 2, 65536, 4000), (2, 2, 20001, 9000),
+                                     (2, 2, 20000, 36000)])
 def test_multi_kernel_plan(B, H, L, K, g1, g2):
     _check(B, H, L, K, g1, g2)
 
