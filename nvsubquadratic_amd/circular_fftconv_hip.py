@@ -19,11 +19,15 @@ plan on a rolled copy of x (g in the backward).  ``use_phase_shift`` is accepted
 signature parity; both of the reference's branches give the same result and
 the kernels always apply the shift in the frequency domain.
 
-Sizes: periodic lengths must be powers of two (2D / 3D: up to 1024 per axis;
-1D: up to 2^23, the fused kernels up to 16384 and the 4-step plan beyond);
-lengths below 16 run on their periodic extension at FFT
-length 16.  Other sizes raise ``NotImplementedError`` (the product has no CPU
-fallback).
+Sizes: power-of-two periodic lengths run as above (2D / 3D: up to 1024 per
+axis; 1D: up to 2^23, the fused kernels up to 16384 and the 4-step plan
+beyond; lengths below 16 on their periodic extension at FFT length 16).  A
+periodic axis of any other length S runs as a zero-padded "same" axis on the
+periodic extension of x (:func:`periodic_by_extension`): the circular sums
+are exactly the linear ones over S + K - 1 extended samples, so the result is
+the reference's at FFT length pow2(S + K - 1 + ceil(K/2)) (2D / 3D: up to
+1024 per axis).  Sizes beyond that raise ``NotImplementedError`` (the product
+has no CPU fallback).
 """
 
 from __future__ import annotations
@@ -32,7 +36,7 @@ import torch
 from einops import rearrange
 
 from . import _lib
-from .fftconv_hip import _nd_core, shifted_fftconv1d
+from .fftconv_hip import _nd_core, fftconv1d_bhl, shifted_fftconv1d
 
 
 __all__ = [
@@ -45,6 +49,51 @@ __all__ = [
     "circular_fftconv1d_fwd_raw",
     "circular_fftconv1d_bwd_raw",
 ]
+
+
+def _pow2(n: int) -> bool:
+    return n > 0 and n & (n - 1) == 0
+
+
+def needs_extension(shape, periodic) -> bool:
+    """True if a periodic axis has a length the power-of-two periodic plans do not take."""
+    return any(p and not _pow2(int(n)) for n, p in zip(shape, periodic))
+
+
+def periodic_by_extension(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None,
+                          periodic) -> torch.Tensor:
+    """Mixed / circular conv whose periodic axes include lengths that are not powers of two.
+
+    On such an axis (length S, K <= S taps, c = (K - 1) // 2) the circular "same" output
+    ``y[n] = sum_j k[j] x[(n + c - j) mod S]`` equals the zero-padded "same" conv of the periodic
+    extension ``xe[t] = x[(t - (K - 1 - c)) mod S]``, t < S + K - 1, read at ``n + c``: every index
+    ``n + c + K//2 - j`` it sums over lies in [0, S + K - 1), so no zero padding enters the kept window
+    (and the extension wraps at most once, K <= S).  The other axes keep their own mode (power-of-two
+    periodic axes stay on the shift-ramp plan).  The extension is a gather (its gradient the
+    matching scatter-add, by autograd), the conv is the HIP op, and the shortcut is added afterwards as
+    the reference adds it (``y.to(x.dtype) + shortcut * x``, ``mixed_fftconv.py:616-623``).
+    """
+    nd = x.dim() - 2
+    xe = x
+    crops = []
+    mask = 0
+    for d, (n, kk, p) in enumerate(zip(x.shape[2:], kernel.shape[2:], periodic)):
+        if p and not _pow2(int(n)):
+            c = (kk - 1) // 2
+            idx = (torch.arange(n + kk - 1, device=x.device) - (kk - 1 - c)) % n
+            xe = xe.index_select(2 + d, idx)
+            crops.append(slice(c, c + n))
+        else:
+            mask |= (1 << d) if p else 0
+            crops.append(slice(None))
+    if nd == 1:  # the one axis was extended: zero-padded
+        y = fftconv1d_bhl(xe, kernel, None)
+    else:
+        y = _nd_core(xe, kernel, None, nd, periodic=mask)
+    y = y[(slice(None), slice(None), *crops)]
+    if shortcut is not None:
+        y = y + shortcut.view(1, -1, *([1] * nd)) * x
+    return y
 
 
 def _check_common(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | None, nd: int) -> None:
@@ -97,6 +146,8 @@ def circular_fftconv1d_fp32_bhl(
     """1D circular conv, BHL ``[B, H, L]``, kernel ``[1|B, H, K]`` (``circular_fftconv.py:310-404``)."""
     del use_phase_shift  # same result either way (see module docstring)
     _check_common(x, kernel, shortcut, 1)
+    if needs_extension(x.shape[2:], (True,)):
+        return periodic_by_extension(x, kernel, shortcut, (True,))
     return shifted_fftconv1d(x, kernel, shortcut, 1)
 
 
@@ -110,6 +161,8 @@ def circular_fftconv2d_fp32_bhl(
     del use_phase_shift
     assert x.ndim == 4, f"x must be [B, H, X, Y]; got {tuple(x.shape)}"
     _check_common(x, kernel, shortcut, 2)
+    if needs_extension(x.shape[2:], (True, True)):
+        return periodic_by_extension(x, kernel, shortcut, (True, True))
     return _nd_core(x, kernel, shortcut, 2, periodic=0b11)
 
 
@@ -123,6 +176,8 @@ def circular_fftconv3d_fp32_bhl(
     del use_phase_shift
     assert x.ndim == 5, f"x must be [B, H, X, Y, Z]; got {tuple(x.shape)}"
     _check_common(x, kernel, shortcut, 3)
+    if needs_extension(x.shape[2:], (True, True, True)):
+        return periodic_by_extension(x, kernel, shortcut, (True, True, True))
     return _nd_core(x, kernel, shortcut, 3, periodic=0b111)
 
 

@@ -13,6 +13,9 @@ How: one call of the HIP N-d engine with the per-axis mask
 kernels with the output shift on the filter's spectrum
 (``nsq_mixed_fftconv1d_*``): ``periodic=(True,)`` the circular op,
 ``periodic=(False,)`` the zero-padded one (``fftconv_hip.fftconv1d_bhl``).
+Periodic axes whose length is not a power of two run on the periodic
+extension of x as zero-padded axes
+(:func:`circular_fftconv_hip.periodic_by_extension`).
 """
 
 from __future__ import annotations
@@ -87,6 +90,8 @@ def _mixed_core(x, kernel, periodic_t, shortcut, use_phase_shift, data_dim):
     if shortcut is not None:
         assert shortcut.dtype == x.dtype, f"shortcut.dtype ({shortcut.dtype}) must match x.dtype ({x.dtype})"
         assert shortcut.shape == (H,), f"Expected shortcut shape ({H},), got {tuple(shortcut.shape)}"
+    if _circ.needs_extension(x.shape[2:], periodic_t):
+        return _circ.periodic_by_extension(x, kernel, shortcut, periodic_t)
     return _zero._nd_core(x, kernel, shortcut, data_dim, periodic=periodic_mask(periodic_t))
 
 

@@ -159,10 +159,10 @@ def test_circular_rejects_mismatched_shortcut_dtype():
         C.circular_fftconv1d_fp32_bhl(x, k, torch.randn(4, device="cuda", dtype=torch.bfloat16))
 
 
-@pytest.mark.parametrize("xs,ks", [((1, 4, 48), (5,)), ((1, 4, 12), (3,)), ((1, 2, 12, 16), (3, 3)),
-                                   ((1, 2, 16, 16, 24), (3, 3, 3)), ((1, 2, 2**24), (5,)), ((1, 2, 2048, 16), (3, 3))])
+@pytest.mark.parametrize("xs,ks", [((1, 2, 2**24), (5,)), ((1, 2, 2048, 16), (3, 3)), ((1, 2, 1000, 12), (101, 3))])
 def test_circular_unsupported_lengths_raise(xs, ks):
-    """Non-power-of-two or out-of-range periodic lengths are refused, not approximated."""
+    """Out-of-range periodic lengths are refused, not approximated (1000 with 101 taps: its periodic extension
+    needs FFT length 2048 on that axis)."""
     x = torch.randn(*xs, device="cuda")
     k = torch.randn(1, xs[1], *ks, device="cuda")
     with pytest.raises(NotImplementedError):
@@ -274,3 +274,41 @@ def test_dc_response_all_periodic_3d_short():
     k = torch.randn(1, 2, 5, 5, 5, device="cuda")
     y = M.mixed_fftconv3d_fp32_bhl(torch.ones(1, 2, 8, 8, 8, device="cuda"), k, (True, True, True))
     torch.testing.assert_close(y, k.sum(dim=(-1, -2, -3)).view(1, 2, 1, 1, 1).expand_as(y), rtol=1e-5, atol=1e-5)
+
+
+# --- periodic axes whose length is not a power of two ------------------------
+# Run as zero-padded axes on the periodic extension of x; the oracle (float64 and the reference's
+# float32 arithmetic) takes any length through torch.fft, and is pinned to the brute force on
+# non-power-of-two lengths by the CPU tests.
+NPOW2 = [((2, 3, 48), (1, 3, 5), (True,)), ((1, 2, 1000), (1, 2, 30), (True,)), ((2, 2, 12), (2, 2, 12), (True,)),
+         ((2, 3, 24, 20), (1, 3, 5, 6), (True, True)), ((1, 2, 48, 16), (1, 2, 7, 4), (True, True)),
+         ((2, 2, 12, 10, 8), (1, 2, 3, 4, 5), (True, True, True)),
+         ((2, 2, 24, 20), (1, 2, 5, 7), (True, False)), ((1, 3, 16, 12), (1, 3, 20, 5), (False, True)),
+         ((1, 2, 6, 16, 10), (1, 2, 3, 8, 4), (True, True, False)), ((1, 2, 224, 9), (1, 2, 31, 3), (True, False))]
+
+
+@pytest.mark.parametrize("xs,ks,per", NPOW2)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_periodic_non_power_of_two_fwd_bwd(xs, ks, per, dtype):
+    torch.manual_seed(sum(xs) + sum(ks))
+    x = torch.randn(*xs).to(dtype).requires_grad_(True)
+    k = torch.randn(*ks).requires_grad_(True)
+    s = torch.randn(xs[1]).to(dtype).requires_grad_(True)
+    y_ref = mixed_fftconv_torch(x, k, per, s)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, kg, sg = (t.detach().cuda().requires_grad_(True) for t in (x, k, s))
+    nd = len(xs) - 2
+    fn = CIRC_FNS[nd] if all(per) else None
+    y = fn(xg, kg, sg) if fn else (M.mixed_fftconv1d_fp32_bhl, M.mixed_fftconv2d_fp32_bhl,
+                                   M.mixed_fftconv3d_fp32_bhl)[nd - 1](xg, kg, per, sg)
+    y.backward(g.cuda())
+    assert y.dtype == dtype and y.shape == y_ref.shape
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert rel_l2(y_ref, y) < tol
+    for a, b in ((x, xg), (k, kg), (s, sg)):
+        assert rel_l2(a.grad, b.grad) < tol
+    if dtype == torch.float32:
+        y64 = mixed_fftconv_torch(x.detach().double(), k.detach().double(), per, s.detach().double(),
+                                  compute_dtype=torch.float64)
+        assert rel_l2(y64, y) < 1e-5
