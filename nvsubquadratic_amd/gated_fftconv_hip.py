@@ -29,6 +29,7 @@ from torch.library import custom_op
 
 from . import _lib
 from .fftconv_hip import _kernel_3d, _workspace
+from .circular_fftconv_hip import needs_extension, periodic_by_extension
 from .mixed_fftconv_hip import periodic_mask
 
 
@@ -38,6 +39,7 @@ __all__ = ["GATE_CODES", "gate_code", "hyena_gated_causal_fftconv1d_bhl", "gated
 
 GATE_CODES = {"identity": 0, "sigmoid": 1, "silu": 2}
 _MODULE_CODES = {torch.nn.Identity: 0, torch.nn.Sigmoid: 1, torch.nn.SiLU: 2}
+_TORCH_GATES = {0: lambda t: t, 1: torch.sigmoid, 2: torch.nn.functional.silu}
 
 
 def _aligned16(t: torch.Tensor) -> torch.Tensor:
@@ -332,6 +334,12 @@ def hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut=None, gate_no
         if shortcut.shape != (H,):
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         sc = shortcut.to(in_dtype).to(cdt).contiguous()
+    if needs_extension(q.shape[2:], per):
+        # a periodic axis of a length the periodic plans do not take: the gates as the reference computes them
+        # (hyena_nd.py:546,570) around the conv on the periodic extension
+        z = q * _TORCH_GATES[act1](kg)
+        y1 = periodic_by_extension(z, kc.view(kbatch, H, *kc.shape[1:]), sc, per)
+        return (y1 * _TORCH_GATES[act2](v)).to(in_dtype)
     y, _ = gated_fftconv_nd_op(q, kg, v, kc, sc, act1, act2, kbatch, periodic_mask(per), _grad_wanted(q, kg, v, kc, sc))
     return y.to(in_dtype)
 

@@ -50,6 +50,14 @@ def test_gated_2d_periodic_axes(periodic):
     _check((32, 16), (5, 9), periodic, "silu", None)
 
 
+@pytest.mark.parametrize("S,K,periodic", [((24, 20), (5, 7), (True, False)), ((24, 20), (5, 6), (True, True)),
+                                          ((12, 10, 8), (3, 4, 5), (True, True, False))])
+def test_gated_periodic_non_power_of_two(S, K, periodic):
+    """Periodic lengths that are not powers of two: torch gates around the conv on the periodic extension."""
+    _check(S, K, periodic, "silu", "sigmoid")
+    _check(S, K, periodic, "identity", None, dtype=torch.bfloat16, tol=2e-2)
+
+
 def test_gated_3d():
     _check((8, 16, 12), (3, 5, 4), None, "silu", "sigmoid", H=4)
 
