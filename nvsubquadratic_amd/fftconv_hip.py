@@ -25,6 +25,8 @@ from __future__ import annotations
 
 from typing import Optional
 
+import os
+
 import torch
 from einops import rearrange
 from torch.library import custom_op
@@ -162,11 +164,33 @@ def _grad_wanted(*ts) -> bool:
     return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
 
+def state_budget_bytes(device: torch.device) -> int:
+    """Largest forward state (transformed x and filter, kept for the backward) one call keeps.
+
+    ``NSQ_STATE_MAX_BYTES`` (bytes) sets it; by default an eighth of the device's memory (36 GB on one
+    MI355X: config 3's 24 GiB is kept).  A larger state is not kept and the backward recomputes the
+    transforms from x and the filter (config 3: two more column passes, ~4.5 ms)."""
+    env = os.environ.get("NSQ_STATE_MAX_BYTES")
+    if env is not None:
+        return int(env)
+    if device.type != "cuda" or not torch.cuda.is_available():  # shape propagation without a GPU
+        return 1 << 62
+    return torch.cuda.get_device_properties(device).total_memory // 8
+
+
+
+
+def _within_budget(nbytes: int, device: torch.device) -> int:
+    """``nbytes`` if that state fits :func:`state_budget_bytes`, else 0 (no state kept)."""
+    return nbytes if nbytes <= state_budget_bytes(device) else 0
+
+
 def _causal_state_bytes(x: torch.Tensor, k: torch.Tensor, kbatch: int, keep: bool) -> int:
     if not keep:
         return 0
     B, H, L = (int(d) for d in x.shape)
-    return int(_causal_workspace_bytes(_lib.get_lib(), B, H, L, int(k.shape[-1]), kbatch, _lib.NSQ_DIR_BWD))
+    return _within_budget(
+        int(_causal_workspace_bytes(_lib.get_lib(), B, H, L, int(k.shape[-1]), kbatch, _lib.NSQ_DIR_BWD)), x.device)
 
 
 @custom_op("nsq_hip::causal_fftconv1d", mutates_args=())
@@ -177,7 +201,7 @@ def causal_fftconv1d_op(x: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tens
     forward leaves its transformed x and k for the backward (like autograd keeping rfft outputs), else empty."""
     y = torch.empty_like(x)
     state = torch.empty(_causal_state_bytes(x, k, kbatch, keep), dtype=torch.uint8, device=x.device)
-    causal_fftconv1d_fwd_raw(x, k, s, y, state if keep else None, kbatch)
+    causal_fftconv1d_fwd_raw(x, k, s, y, state if state.numel() else None, kbatch)
     return y, state
 
 
@@ -452,9 +476,11 @@ def _nd_state_bytes(x: torch.Tensor, k: torch.Tensor, kbatch: int, periodic: int
     if not keep:
         return 0
     nd = x.ndim - 2
-    return int(_nd_workspace_bytes(_lib.get_lib(), nd, int(x.shape[0]), int(x.shape[1]),
-                                   _lib.i64_array([int(d) for d in x.shape[2:]]),
-                                   _lib.i64_array([int(d) for d in k.shape[1:]]), kbatch, periodic, _lib.NSQ_DIR_BWD))
+    return _within_budget(
+        int(_nd_workspace_bytes(_lib.get_lib(), nd, int(x.shape[0]), int(x.shape[1]),
+                                _lib.i64_array([int(d) for d in x.shape[2:]]),
+                                _lib.i64_array([int(d) for d in k.shape[1:]]), kbatch, periodic, _lib.NSQ_DIR_BWD)),
+        x.device)
 
 
 @custom_op("nsq_hip::fftconv_nd", mutates_args=())

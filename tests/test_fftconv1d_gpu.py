@@ -441,3 +441,26 @@ def test_per_sample_filters_bf16_config3_shape_sample():
     y = F.causal_fftconv1d_bhl(x.cuda(), k.cuda())
     assert y.dtype == torch.bfloat16
     assert rel_l2(y_ref, y) < RTOL_BF16_L2
+
+
+@pytest.mark.parametrize("L", [8192, 65536])
+def test_state_budget_zero_recomputes_bitwise(monkeypatch, L):
+    """A forward state above NSQ_STATE_MAX_BYTES is not kept; the backward then recomputes the transforms
+    and gives the same gradients bit for bit (fused plan: no state either way; 4-step plan: two column passes)."""
+    torch.manual_seed(21)
+    x = torch.randn(2, 3, L, device="cuda", requires_grad=True)
+    k = torch.randn(1, 3, L, device="cuda", requires_grad=True)
+    s = torch.randn(3, device="cuda", requires_grad=True)
+    g = torch.randn(2, 3, L, device="cuda")
+    grads = []
+    for budget in (None, "0"):
+        if budget is None:
+            monkeypatch.delenv("NSQ_STATE_MAX_BYTES", raising=False)
+        else:
+            monkeypatch.setenv("NSQ_STATE_MAX_BYTES", budget)
+        for t in (x, k, s):
+            t.grad = None
+        F.causal_fftconv1d_bhl(x, k, s).backward(g)
+        grads.append([t.grad.clone() for t in (x, k, s)])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)

@@ -240,3 +240,24 @@ def test_config5_3d_channel_sample_bf16_fwd_bwd():
     assert rel_l2(x.grad, xg.grad) < 2e-2
     assert rel_l2(k.grad, kg.grad) < 2e-2
     assert rel_l2(s.grad, sg.grad) < 2e-2
+
+
+def test_state_budget_zero_recomputes_bitwise(monkeypatch):
+    """N-d: the backward without a kept forward state recomputes x's and the filter's spectra, bitwise equal."""
+    torch.manual_seed(22)
+    x = torch.randn(2, 4, 24, 20, device="cuda", requires_grad=True)
+    k = torch.randn(1, 4, 7, 9, device="cuda", requires_grad=True)
+    s = torch.randn(4, device="cuda", requires_grad=True)
+    g = torch.randn(2, 4, 24, 20, device="cuda")
+    grads = []
+    for budget in (None, "0"):
+        if budget is None:
+            monkeypatch.delenv("NSQ_STATE_MAX_BYTES", raising=False)
+        else:
+            monkeypatch.setenv("NSQ_STATE_MAX_BYTES", budget)
+        for t in (x, k, s):
+            t.grad = None
+        F.fftconv2d_bhl(x, k, s).backward(g)
+        grads.append([t.grad.clone() for t in (x, k, s)])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
