@@ -405,6 +405,43 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
 
         extra["torch_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_torch_gates, steps, warmup)), 4)
         extra["conv_only_ms_per_step"] = round(statistics.mean(_time_steps(step_conv_only, steps, warmup)), 4)
+    elif name == "siren-1d":
+        # report-only (row F1): the SIREN filter of a long-context Hyena layer (kernels_nd.py:876, CKConvND's causal
+        # half): HIP hidden stack + one readout GEMM, fwd+bwd, against the reference's torch layers on the same GPU
+        import torch.nn.functional as Fn
+
+        from nvsubquadratic_amd.siren_hip import siren_filter, siren_grid
+
+        H, L, E, HD, nh = 4096, 262144, 32, 32, 2
+        grid = siren_grid((L,), (1.0,), (L,), dev)[L - 1:].contiguous()  # [L, 1]: the points the causal crop keeps
+        gen_c = torch.Generator().manual_seed(0)
+        mk = lambda *shape, b: ((torch.rand(*shape, generator=gen_c) * 2 - 1) * b).to(dev).requires_grad_(True)  # noqa
+        w0, b0 = mk(E, 1, b=2 * 3.14159 * 10.0), mk(E, b=1.0)
+        hw = [mk(HD, E, b=(6 / E) ** 0.5)] + [mk(HD, HD, b=(6 / HD) ** 0.5) for _ in range(nh - 1)]
+        hb = [mk(HD, b=1.0) for _ in range(nh)]
+        wo, bo = mk(H, HD, b=(6 / HD) ** 0.5 / 512), mk(H, b=0.1)
+        g = torch.randn(H, L, device=dev, generator=gen)
+        phase, dtype = "fwd+bwd", "f32"
+        nbytes = 2 * H * L * 4
+        desc = ("siren-1d: SIREN filter synthesis fwd+bwd (pos-emb 32, 2 hidden layers of 32, readout to 4096 "
+                "channels) on the 262144 causal points, fp32; writes k [H, L] and reads its gradient")
+
+        def clear():
+            for t in (w0, b0, *hw, *hb, wo, bo):
+                t.grad = None
+
+        def step():
+            clear()
+            siren_filter(grid, w0, b0, hw, hb, wo, bo).backward(g)
+
+        def step_torch():
+            clear()
+            h = torch.sin(Fn.linear(grid, w0, b0))
+            for w, b in zip(hw, hb):
+                h = torch.sin(Fn.linear(h, w, b))
+            Fn.linear(h, wo, bo).t().backward(g)
+
+        extra["torch_layers_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
     else:
         raise SystemExit(f"unknown workload {name}")
     ms_list = _time_steps(step, steps, warmup)
@@ -439,7 +476,7 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
                                                               "cfg4-circular", "well-rb", "hyena-gated",
-                                                              "hyena-gated-2d"])
+                                                              "hyena-gated-2d", "siren-1d"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 8
+#define NSQ_ABI_VERSION 9
 
 enum {
   NSQ_OK = 0,
@@ -342,6 +342,42 @@ int nsq_mixed_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* 
                              float* gk, float* gs, int dtype, int64_t B, int64_t H, const int64_t* S,
                              const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace,
                              size_t workspace_bytes, int fwd_state, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Implicit filter generation (SIREN MLP): the hidden stack (ABI 9).
+ *
+ * Replaces the hidden layers of nvsubquadratic/modules/kernels_nd.py:1149-1190
+ * (SIRENKernelND.forward without FiLM: the positional embedding and the
+ * sine-activated stack):
+ *   a_0[g] = sin(W0 x_g + b0)                       W0 [E, d], b0 [E]
+ *   a_i[g] = sin(W_i a_{i-1}[g] + b_i), i = 1..nh   W_1 [HD, E], W_i [HD, HD]
+ * for the G coordinates grid [G, d] (d = 1..3).  The forward writes
+ * act [HD + 1][lda] fp32 = [a_nh^T; 1]: the last activation transposed with a
+ * row of ones, so that the reference's readout k = W_out a_nh + b_out becomes
+ * one library GEMM [W_out | b_out] act writing the filter straight in the
+ * [H][G] layout the FFT convs read (the rearrange of modules/ckconv_nd.py:
+ * 1149-1164 never materialises).  The hidden weights are packed back to back in
+ * wh (W_1, W_2, ...), their biases in bh.  Bias pointers may be null
+ * (use_bias=False).  E, HD in {16, 32, 64, 128}; 1 <= nh <= 8.  fp32
+ * throughout, matrix cores for the products (fp32 in, fp32 accumulate).  Other
+ * sizes: NSQ_ERR_UNSUPPORTED.
+ *
+ * Backward: gact = dL/da_nh (= W_out^T gk, from the readout's gradient GEMM)
+ * in, element (j, g) at gact[j * gact_stride_j + g * gact_stride_g] (so both
+ * [HD][G] and [G][HD] layouts read in place); the gradients of W0, b0, wh, bh
+ * out (gb0 / gbh may be null when the biases are).  The layers are recomputed from the grid (no
+ * forward state); partial sums go to the workspace and are reduced in a fixed
+ * order (deterministic).
+ */
+int nsq_siren_mlp_fwd(const float* grid, int64_t G, int d, const float* w0, const float* b0, int E, const float* wh,
+                      const float* bh, int nh, int HD, float* act, int64_t lda, void* stream);
+
+size_t nsq_siren_mlp_bwd_workspace_bytes(int64_t G, int d, int E, int nh, int HD);
+
+int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_stride_g, const float* grid, int64_t G,
+                      int d, const float* w0, const float* b0, int E, const float* wh, const float* bh, int nh, int HD,
+                      float* gw0, float* gb0, float* gwh, float* gbh, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,595 @@
+// Implicit filter generation (SIREN MLP) for gfx950: the hidden stack.
+//
+// Semantics: nvsubquadratic/modules/kernels_nd.py:1149-1190 (SIRENKernelND
+// without FiLM):
+//   a_0[g] = sin(W0 x_g + b0),  a_i[g] = sin(W_i a_{i-1}[g] + b_i) (i = 1..nh),
+//   k[h][g] = W_out[h] . a_nh[g] + b_out[h].
+// These kernels produce the last activation transposed, A_ext = [a_nh^T; 1]
+// ([HD + 1][G]), and the hidden weights' gradients from dA = W_out^T gk; the
+// readout k = [W_out | b_out] A_ext (one GEMM of K = HD + 1 that writes the
+// filter straight in the [H][G] layout the FFT convs read, bias folded in) and
+// its two gradient GEMMs are plain library GEMMs (hipBLASLt), which this
+// shape (M = H, N = G, K = 33) feeds at its own HBM roofline.
+//
+// Design (MI355X):
+//  * A wave owns 16 grid points.  Every product is a v_mfma_f32_16x16x4_f32
+//    (fp32 in, fp32 accumulate: the reference's fp32 linear layers up to
+//    summation order).  Lane l supplies A[l % 16][s] and B[s][l % 16] for
+//    k-slot s = l / 16 and receives D[4 (l / 16) + r][l % 16].  The k index
+//    of slot s at step kb is K/4 * s + kb, so a lane's operands of one product
+//    are K/4 consecutive words of one row (vector loads) and the 16 points'
+//    activations (B) stay in registers across every output tile.
+//  * The hidden layers run out of a per-wave LDS tile; the forward writes
+//    only A_ext (HD + 1 floats per point) to HBM.
+//  * Backward: siren_bwd_delta_kernel reads dA for its 16 points, recomputes
+//    the layers and back-propagates, writing every layer's activations and
+//    deltas transposed ([rows][Gp]); siren_gram_kernel then forms each weight
+//    gradient X Y^T and bias row sums over the points as per-chunk partials,
+//    reduced in a fixed order (bitwise repeatable).
+#include <type_traits>
+
+#include "nsq_common.h"
+
+namespace nsq {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSirenWaves = 4;  // waves per workgroup, 16 grid points each
+constexpr int kSirenThreads = 64 * kSirenWaves;
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Keeps the compiler from moving LDS accesses of one wave across each other;
+// the LDS executes a wave's instructions in order, so no barrier is needed
+// between lanes of the same wave.
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Row stride (words) of a per-wave activation tile [16 points][D]: D + 4
+// spreads the 16 rows of a B-operand read over the 64 banks.
+template <int D>
+struct Tile {
+  static constexpr int S = D + 4;
+  static constexpr int WORDS = 16 * S;
+};
+
+// Layer geometry: layer i (i = 1..nh) maps IN -> HD, IN = E for i = 1.
+struct SirenNet {
+  const float* w0;  // [E][d]
+  const float* b0;  // [E] or null
+  const float* wh;  // packed W_1 [HD][E], W_2.. [HD][HD]
+  const float* bh;  // packed [nh][HD] or null
+  int d, nh;
+};
+
+__device__ __forceinline__ const float* layer_w(const SirenNet& n, int i, int E, int HD) {
+  return n.wh + (i == 1 ? 0 : int64_t(HD) * E + int64_t(i - 2) * HD * HD);
+}
+
+// Coordinates of point g (zeros past G), unrolled over the at most 3 axes.
+__device__ __forceinline__ void load_coords(const float* __restrict__ grid, int64_t G, int d, int64_t g, float* x) {
+#pragma unroll
+  for (int c = 0; c < 3; ++c) x[c] = (g < G && c < d) ? grid[g * d + c] : 0.f;
+}
+
+// Pre-activation of embedding feature e: W0[e] . x + b0[e].
+__device__ __forceinline__ float embed_pre(const SirenNet& n, int e, const float* x) {
+  float z = n.b0 ? n.b0[e] : 0.f;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    if (c < n.d) z = __builtin_fmaf(n.w0[e * n.d + c], x[c], z);
+  }
+  return z;
+}
+
+// Positional embedding of the wave's 16 points into tile a0 [16][E] (and the
+// pre-activation into z0 if given): lane l, point l % 16, features l / 16 + 4t.
+template <int E>
+__device__ __forceinline__ void pos_embed(const SirenNet& n, const float* __restrict__ grid, int64_t G, int64_t g0,
+                                          float* a0, float* z0) {
+  const int l = int(threadIdx.x) & 63, p = l & 15;
+  const int64_t g = g0 + p;
+  float x[3];
+  load_coords(grid, G, n.d, g, x);
+#pragma unroll
+  for (int t = 0; t < E / 4; ++t) {
+    const int e = (l >> 4) + 4 * t;
+    const float z = embed_pre(n, e, x);
+    a0[p * Tile<E>::S + e] = sinf(z);
+    if (z0) z0[p * Tile<E>::S + e] = z;
+  }
+}
+
+// One hidden layer on the matrix cores: out[p][o] = sin(W[o] . in[p] + b[o])
+// for the wave's 16 points; z (optional) keeps the pre-activation.
+// SIN / SOUT: row strides of the input and output tiles.
+template <int IN, int HD, int SIN = Tile<IN>::S, int SOUT = Tile<HD>::S>
+__device__ __forceinline__ void hidden_layer(const float* __restrict__ w, const float* __restrict__ b, const float* in,
+                                             float* out, float* z) {
+  constexpr int KB = IN / 4;
+  const int l = int(threadIdx.x) & 63, s = l >> 4, p = l & 15;
+  float bv[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) bv[kb] = in[p * SIN + KB * s + kb];
+#pragma unroll
+  for (int o0 = 0; o0 < HD; o0 += 16) {
+    const float* wr = w + (o0 + p) * IN + KB * s;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) acc = mfma4(wr[kb], bv[kb], acc);
+    // D[m = o0 + 4 s + r][n = point p]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = o0 + 4 * s + r;
+      const float zz = acc[r] + (b ? b[o] : 0.f);
+      out[p * SOUT + o] = sinf(zz);
+      if (z) z[p * SOUT + o] = zz;
+    }
+  }
+}
+
+// Layers 1..nh for the wave's tile; returns the tile holding a_nh.  fwd keeps
+// only two tiles (ping-pong); the backward passes per-layer tiles (act[i],
+// zt[i]) so every layer's activation and pre-activation survive.
+template <int E, int HD>
+__device__ __forceinline__ const float* run_layers(const SirenNet& n, float* const* act, float* const* zt) {
+  for (int i = 1; i <= n.nh; ++i) {
+    const float* w = layer_w(n, i, E, HD);
+    const float* b = n.bh ? n.bh + (i - 1) * HD : nullptr;
+    wave_lds_order();
+    if (i == 1)
+      hidden_layer<E, HD>(w, b, act[0], act[1], zt ? zt[1] : nullptr);
+    else
+      hidden_layer<HD, HD>(w, b, act[i - 1], act[i], zt ? zt[i] : nullptr);
+  }
+  wave_lds_order();
+  return act[n.nh];
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  grid = ceil(G / 64) workgroups of 4 waves (16 points each);
+// dynamic LDS per wave: a0 [16][E] and two ping-pong tiles [16][HD].  Writes
+// the last layer transposed, act[j][g] = a_nh[g][j] (j < HD), and the ones
+// row act[HD][g] = 1 that carries the readout bias through the readout GEMM.
+// ---------------------------------------------------------------------------
+template <int E, int HD>
+__global__ __launch_bounds__(kSirenThreads) void siren_mlp_fwd_kernel(const float* __restrict__ grid, int64_t G,
+                                                                      SirenNet n, float* __restrict__ act,
+                                                                      int64_t lda) {
+  extern __shared__ float lds[];
+  const int wv = int(threadIdx.x) >> 6, l = int(threadIdx.x) & 63, s = l >> 4, p = l & 15;
+  float* base = lds + wv * (Tile<E>::WORDS + 2 * Tile<HD>::WORDS);
+  float* t0 = base;
+  float* t1 = base + Tile<E>::WORDS;
+  float* t2 = t1 + Tile<HD>::WORDS;
+  const int64_t g0 = (int64_t(blockIdx.x) * kSirenWaves + wv) * 16;
+  pos_embed<E>(n, grid, G, g0, t0, nullptr);
+  // ping-pong: a_i in t1 for odd i, t2 for even i >= 2
+  float* tiles[9] = {t0, t1, t2, t1, t2, t1, t2, t1, t2};
+  const float* last = run_layers<E, HD>(n, tiles, nullptr);
+  const int64_t g = g0 + p;
+  if (g < G) {
+    for (int j = s; j < HD; j += 4) act[int64_t(j) * lda + g] = last[p * Tile<HD>::S + j];
+    if (s == 0) act[int64_t(HD) * lda + g] = 1.f;
+  }
+}
+
+template <int E, int HD>
+__global__ __launch_bounds__(kSirenThreads) void siren_bwd_delta_kernel(
+    const float* __restrict__ gact, int64_t sj, int64_t sg, const float* __restrict__ grid, int64_t G, int64_t Gp,
+    SirenNet n, float* __restrict__ act, float* __restrict__ del, float* __restrict__ gridT, int nwaves_wg) {
+  extern __shared__ float lds[];
+  constexpr int D = E > HD ? E : HD;
+  constexpr int TS = Tile<D>::S, TW = Tile<D>::WORDS;
+  const int wv = int(threadIdx.x) >> 6, l = int(threadIdx.x) & 63, s = l >> 4, p = l & 15;
+  const int per_wave = (2 * (n.nh + 1) + 2) * TW;
+  float* base = lds + wv * per_wave;
+  float* at[9];
+  float* zt[9];
+  for (int i = 0; i <= n.nh; ++i) {
+    at[i] = base + i * TW;
+    zt[i] = base + (n.nh + 1 + i) * TW;
+  }
+  float* dA = base + 2 * (n.nh + 1) * TW;
+  float* dB = dA + TW;
+  const int64_t g0 = (int64_t(blockIdx.x) * nwaves_wg + wv) * 16;
+  const int64_t g = g0 + p;
+  const bool gok = g < G;
+
+  // dA[p][j] = gact[j sj + (g0 + p) sg], the gradient of the last layer's output (the readout's W_out^T gk)
+  for (int j = s; j < HD; j += 4) dA[p * TS + j] = gok ? gact[int64_t(j) * sj + g * sg] : 0.f;
+
+  // forward recompute with pre-activations; every tile has the D-wide stride TS
+  {
+    float x[3];
+    load_coords(grid, G, n.d, g, x);
+    const float xs = s == 0 ? x[0] : (s == 1 ? x[1] : x[2]);
+    if (s < n.d && gok) gridT[int64_t(s) * Gp + g] = xs;
+#pragma unroll
+    for (int t = 0; t < E / 4; ++t) {
+      const int e = s + 4 * t;
+      const float z = embed_pre(n, e, x);
+      at[0][p * TS + e] = sinf(z);
+      zt[0][p * TS + e] = z;
+    }
+    for (int i = 1; i <= n.nh; ++i) {
+      const float* w = layer_w(n, i, E, HD);
+      const float* b = n.bh ? n.bh + (i - 1) * HD : nullptr;
+      wave_lds_order();
+      if (i == 1)
+        hidden_layer<E, HD, TS, TS>(w, b, at[0], at[1], zt[1]);
+      else
+        hidden_layer<HD, HD, TS, TS>(w, b, at[i - 1], at[i], zt[i]);
+    }
+    wave_lds_order();
+  }
+
+  // delta_nh = dA * cos(z_nh); for i = nh..1: delta_{i-1}[p][j] = (sum_o delta_i[p][o] W_i[o][j]) cos(z_{i-1}[p][j])
+  // (D[m = j][n = p] = sum_o W_i^T[j][o] delta_i^T[o][p]: A[m = j][k = o] = W_i[o][j], B[k = o][n = p]).
+  float* cur = dA;
+  float* nxt = dB;
+  for (int e = l; e < 16 * HD; e += 64) {
+    const int pp = e / HD, j = e - pp * HD;
+    cur[pp * TS + j] *= cosf(zt[n.nh][pp * TS + j]);
+  }
+  wave_lds_order();
+  for (int i = n.nh; i >= 0; --i) {
+    const int rows = i == 0 ? E : HD;
+    // write a_i^T and delta_i^T rows for these 16 points
+    const int64_t roff = i == 0 ? 0 : E + int64_t(i - 1) * HD;
+    for (int e = s; e < rows; e += 4) {
+      if (gok) {
+        act[(roff + e) * Gp + g] = at[i][p * TS + e];
+        del[(roff + e) * Gp + g] = cur[p * TS + e];
+      }
+    }
+    if (i == 0) break;
+    const int IN = i == 1 ? E : HD;
+    const float* w = layer_w(n, i, E, HD);
+    // B operand: delta_i^T[o][p] for o = (HD/4) s + kb
+    constexpr int KBO = HD / 4;
+    float bv[KBO];
+#pragma unroll
+    for (int kb = 0; kb < KBO; ++kb) bv[kb] = cur[p * TS + KBO * s + kb];
+    for (int j0 = 0; j0 < IN; j0 += 16) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KBO; ++kb) acc = mfma4(w[(KBO * s + kb) * IN + j0 + p], bv[kb], acc);
+      // D[m = j = j0 + 4 s + r][n = point p]
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = j0 + 4 * s + r;
+        nxt[p * TS + j] = acc[r] * cosf(zt[i - 1][p * TS + j]);
+      }
+    }
+    wave_lds_order();
+    float* t = cur;
+    cur = nxt;
+    nxt = t;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gram reduction over points: part[c][m][n] = sum_{g in chunk c} X[m][g] Y[n][g]
+// (n < N; rows n >= NY of Y read as zero) and rsum[c][m] = sum_g X[m][g].
+// X rows have stride ldx, Y rows stride ldy.  grid = (M / 16, chunks); the 4
+// waves split a chunk (chunk a multiple of 64) and are reduced through LDS.
+// Each wave loads the next 16 points' operands before the current products.
+// VEC: 16-byte loads (ldx, ldy multiples of 4 and 16-byte aligned bases).
+// ---------------------------------------------------------------------------
+template <int NT, bool VEC>
+__global__ __launch_bounds__(kSirenThreads) void siren_gram_kernel(const float* __restrict__ X, int64_t ldx,
+                                                                   const float* __restrict__ Y, int64_t ldy, int NY,
+                                                                   int64_t G, int M, int64_t chunk,
+                                                                   float* __restrict__ part, float* __restrict__ rsum) {
+  __shared__ float red[kSirenWaves][NT * 16 * 16 + 16];
+  const int wv = int(threadIdx.x) >> 6, l = int(threadIdx.x) & 63, s = l >> 4, p = l & 15;
+  const int m0 = int(blockIdx.x) * 16;
+  const int64_t gbeg = int64_t(blockIdx.y) * chunk + int64_t(wv) * (chunk / kSirenWaves);
+  const int64_t gend0 = gbeg + chunk / kSirenWaves;
+  const int64_t gend = gend0 < G ? gend0 : G;
+  const float* xr = X + int64_t(m0 + p) * ldx;
+  // slot s takes points gb + 4 s + i, i = 0..3 (one 16-byte segment per row)
+  auto ld4 = [&](const float* row, int64_t gs, float* v) {
+    if (VEC && gs + 3 < G) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(row + gs);
+      v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = gs + i < G ? row[gs + i] : 0.f;
+    }
+  };
+  float xv[4], yv[NT][4], xn[4], yn[NT][4];
+  auto load = [&](int64_t gb, float* x, float (*y)[4]) {
+    const int64_t gs = gb + 4 * s;
+    ld4(xr, gs, x);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int nrow = 16 * t + p;
+      if (nrow < NY) {
+        ld4(Y + int64_t(nrow) * ldy, gs, y[t]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[t][i] = 0.f;
+      }
+    }
+  };
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float rs = 0.f;
+  if (gbeg < gend) load(gbeg, xv, yv);
+  for (int64_t gb = gbeg; gb < gend; gb += 16) {
+    if (gb + 16 < gend) load(gb + 16, xn, yn);
+    rs += (xv[0] + xv[1]) + (xv[2] + xv[3]);
+    // A[m = p][k slot s] = X[m0 + p][gs + i], B[k][n = p] = Y[16 t + p][gs + i]
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t] = mfma4(xv[i], yv[t][i], acc[t]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xv[i] = xn[i];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) yv[t][i] = yn[t][i];
+    }
+  }
+  // D[m = 4 s + r][n = p] of tile t; row sums: lanes of slot s hold row p partials
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wv][t * 256 + (4 * s + r) * 16 + p] = acc[t][r];
+  }
+  rs += __shfl_xor(rs, 16);
+  rs += __shfl_xor(rs, 32);
+  if (s == 0) red[wv][NT * 256 + p] = rs;
+  __syncthreads();
+  const int64_t cidx = blockIdx.y;
+  for (int e = int(threadIdx.x); e < NT * 256; e += kSirenThreads) {
+    const float v = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
+    const int t = e / 256, mm = (e % 256) / 16, nn = e % 16;
+    part[(cidx * M + m0 + mm) * (NT * 16) + 16 * t + nn] = v;
+  }
+  if (threadIdx.x < 16) {
+    const int e = NT * 256 + int(threadIdx.x);
+    rsum[cidx * M + m0 + int(threadIdx.x)] = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
+  }
+}
+
+// out[m][n] (n < N) = sum_c part[c][m][n] (row stride NP) and rout[m] = sum_c
+// rpart[c][m] (if given): one wave per output, lanes take chunks c = lane,
+// lane + 64, ... and a fixed butterfly adds the lanes (deterministic).
+__global__ __launch_bounds__(256) void siren_reduce_kernel(const float* __restrict__ part, int64_t chunks, int M,
+                                                           int NP, int N, float* __restrict__ out,
+                                                           const float* __restrict__ rpart,
+                                                           float* __restrict__ rout) {
+  const int64_t e = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = int(threadIdx.x) & 63;
+  const int64_t nout = int64_t(M) * N;
+  const bool is_out = e < nout;
+  const bool is_row = !is_out && rout && e < nout + M;
+  if (!is_out && !is_row) return;  // a whole wave leaves together
+  float acc = 0.f;
+  if (is_out) {
+    const int m = int(e / N), nn = int(e % N);
+    for (int64_t c = lane; c < chunks; c += 64) acc += part[(c * M + m) * NP + nn];
+  } else {
+    const int64_t m = e - nout;
+    for (int64_t c = lane; c < chunks; c += 64) acc += rpart[c * M + m];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) {
+    if (is_out)
+      out[e] = acc;
+    else
+      rout[e - nout] = acc;
+  }
+}
+
+bool siren_dims_ok(int E, int HD) {
+  auto ok = [](int v) { return v == 16 || v == 32 || v == 64 || v == 128; };
+  return ok(E) && ok(HD);
+}
+
+template <template <int, int> class F, class... A>
+bool siren_dispatch(int E, int HD, A&&... a) {
+#define NSQ_SIREN_CASE(e, h) \
+  if (E == e && HD == h) return F<e, h>::run(static_cast<A&&>(a)...), true;
+  NSQ_SIREN_CASE(16, 16) NSQ_SIREN_CASE(16, 32) NSQ_SIREN_CASE(16, 64) NSQ_SIREN_CASE(16, 128)
+  NSQ_SIREN_CASE(32, 16) NSQ_SIREN_CASE(32, 32) NSQ_SIREN_CASE(32, 64) NSQ_SIREN_CASE(32, 128)
+  NSQ_SIREN_CASE(64, 16) NSQ_SIREN_CASE(64, 32) NSQ_SIREN_CASE(64, 64) NSQ_SIREN_CASE(64, 128)
+  NSQ_SIREN_CASE(128, 16) NSQ_SIREN_CASE(128, 32) NSQ_SIREN_CASE(128, 64) NSQ_SIREN_CASE(128, 128)
+#undef NSQ_SIREN_CASE
+  return false;
+}
+
+template <int E, int HD>
+struct SirenFwd {
+  static void run(const float* grid, int64_t G, const SirenNet& n, float* act, int64_t lda, hipStream_t st) {
+    const size_t lds = size_t(kSirenWaves) * (Tile<E>::WORDS + 2 * Tile<HD>::WORDS) * sizeof(float);
+    const dim3 grd(unsigned(ceil_div(G, 16 * kSirenWaves)));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&siren_mlp_fwd_kernel<E, HD>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    hipLaunchKernelGGL((siren_mlp_fwd_kernel<E, HD>), grd, dim3(kSirenThreads), lds, st, grid, G, n, act, lda);
+  }
+};
+
+constexpr int kSirenMaxLds = 160 * 1024;
+
+// LDS bytes per wave of the backward pass 1.
+inline int delta_lds_per_wave(int E, int HD, int nh) {
+  const int D = E > HD ? E : HD;
+  return (2 * (nh + 1) + 2) * 16 * (D + 4) * int(sizeof(float));
+}
+
+template <int E, int HD>
+struct SirenDelta {
+  static void run(const float* gact, int64_t sj, int64_t sg, const float* grid, int64_t G, int64_t Gp,
+                  const SirenNet& n, float* act, float* del, float* gridT, hipStream_t st) {
+    const int per = delta_lds_per_wave(E, HD, n.nh);
+    int waves = kSirenMaxLds / per;
+    waves = waves > kSirenWaves ? kSirenWaves : waves;
+    const dim3 grd(unsigned(ceil_div(G, 16 * waves)));
+    const size_t lds = size_t(per) * waves;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&siren_bwd_delta_kernel<E, HD>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    hipLaunchKernelGGL((siren_bwd_delta_kernel<E, HD>), grd, dim3(64 * waves), lds, st, gact, sj, sg, grid, G, Gp, n,
+                       act, del, gridT, waves);
+  }
+};
+
+// Points per Gram workgroup: enough chunks that M/16 x chunks reaches ~2048
+// workgroups (8 per CU), at least 64 points (16 per wave) and a multiple of 64.
+int64_t gram_chunk(int64_t G, int M) {
+  const int64_t tiles = M / 16;
+  int64_t chunks = ceil_div(2048, tiles);
+  const int64_t cmax = ceil_div(G, 64);
+  chunks = chunks < 1 ? 1 : (chunks > cmax ? cmax : chunks);
+  return ceil_div(ceil_div(G, chunks), 64) * 64;
+}
+int64_t gram_chunks(int64_t G, int M) { return ceil_div(G, gram_chunk(G, M)); }
+
+template <int NT>
+void launch_gram(const float* X, int64_t ldx, const float* Y, int64_t ldy, int NY, int64_t G, int M, float* part,
+                 float* rpart, hipStream_t st) {
+  const bool vec = ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+  const int64_t chunk = gram_chunk(G, M);
+  const dim3 grd(unsigned(M / 16), unsigned(gram_chunks(G, M)));
+  if (vec)
+    hipLaunchKernelGGL((siren_gram_kernel<NT, true>), grd, dim3(kSirenThreads), 0, st, X, ldx, Y, ldy, NY, G, M,
+                       chunk, part, rpart);
+  else
+    hipLaunchKernelGGL((siren_gram_kernel<NT, false>), grd, dim3(kSirenThreads), 0, st, X, ldx, Y, ldy, NY, G, M,
+                       chunk, part, rpart);
+}
+
+// Output tiles of 16 columns a Gram launch covers for NY columns: 1, 2, 4 or 8.
+int gram_nt(int NY) { return NY <= 16 ? 1 : (NY <= 32 ? 2 : (NY <= 64 ? 4 : 8)); }
+
+void gram(const float* X, int64_t ldx, const float* Y, int64_t ldy, int NY, int64_t G, int M, float* out, float* rout,
+          float* part, float* rpart, hipStream_t st) {
+  const int NT = gram_nt(NY);
+  switch (NT) {
+    case 1: launch_gram<1>(X, ldx, Y, ldy, NY, G, M, part, rpart, st); break;
+    case 2: launch_gram<2>(X, ldx, Y, ldy, NY, G, M, part, rpart, st); break;
+    case 4: launch_gram<4>(X, ldx, Y, ldy, NY, G, M, part, rpart, st); break;
+    default: launch_gram<8>(X, ldx, Y, ldy, NY, G, M, part, rpart, st); break;
+  }
+  const int NP = 16 * NT;
+  const int64_t nwaves = int64_t(M) * NY + M;
+  hipLaunchKernelGGL(siren_reduce_kernel, dim3(unsigned(ceil_div(nwaves, 4))), dim3(256), 0, st, part,
+                     gram_chunks(G, M), M, NP, NY, out, rpart, rout);
+}
+
+// Workspace layout (floats): act [E + nh HD][Gp], del [same], gridT [d][Gp],
+// part [chunks][max(E, HD)][max NT*16], rpart [chunks][max(E, HD)].
+struct SirenWs {
+  int64_t Gp, rows;
+  size_t act, del, gridT, part, rpart, total;  // float offsets / count
+};
+
+SirenWs siren_ws(int64_t G, int d, int E, int nh, int HD) {
+  SirenWs w;
+  w.Gp = (G + 15) / 16 * 16;
+  w.rows = E + int64_t(nh) * HD;
+  // partial sums of the largest Gram launch: hidden (M = HD, N = E or HD), embedding (M = E, N = d)
+  auto psz = [&](int64_t M, int NY) { return size_t(gram_chunks(G, int(M))) * M * 16 * gram_nt(NY); };
+  auto rsz = [&](int64_t M) { return size_t(gram_chunks(G, int(M))) * M; };
+  size_t pmax = psz(HD, E > HD ? E : HD);
+  pmax = psz(E, d) > pmax ? psz(E, d) : pmax;
+  size_t rmax = rsz(HD) > rsz(E) ? rsz(HD) : rsz(E);
+  auto al = [](size_t v) { return (v + 63) / 64 * 64; };  // 256-byte sub-buffers
+  w.act = 0;
+  w.del = al(w.act + size_t(w.rows) * w.Gp);
+  w.gridT = al(w.del + size_t(w.rows) * w.Gp);
+  w.part = al(w.gridT + size_t(d) * w.Gp);
+  w.rpart = al(w.part + pmax);
+  w.total = al(w.rpart + rmax);
+  return w;
+}
+
+int siren_validate(const float* grid, int64_t G, int d, const float* w0, int E, const float* wh, int nh, int HD) {
+  NSQ_CHECK_ARG(grid && w0 && wh, "siren_mlp: null weight or grid pointer");
+  NSQ_CHECK_ARG(G >= 1 && G <= (int64_t(1) << 30), "siren_mlp: G=%lld out of range", (long long)G);
+  NSQ_CHECK_ARG(d >= 1 && d <= 3, "siren_mlp: data_dim %d must be 1..3", d);
+  NSQ_CHECK_ARG(nh >= 1 && nh <= 8, "siren_mlp: hidden layer count %d must be 1..8", nh);
+  if (!siren_dims_ok(E, HD)) {
+    set_error("siren_mlp: embedding_dim %d and mlp_hidden_dim %d must each be 16, 32, 64 or 128", E, HD);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  return NSQ_OK;
+}
+
+}  // namespace
+}  // namespace nsq
+
+extern "C" {
+
+int nsq_siren_mlp_fwd(const float* grid, int64_t G, int d, const float* w0, const float* b0, int E, const float* wh,
+                      const float* bh, int nh, int HD, float* act, int64_t lda, void* stream) {
+  using namespace nsq;
+  clear_error();
+  int rc = siren_validate(grid, G, d, w0, E, wh, nh, HD);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(act && lda >= G, "siren_mlp_fwd: null output or row stride %lld < G", (long long)lda);
+  const SirenNet n{w0, b0, wh, bh, d, nh};
+  siren_dispatch<SirenFwd>(E, HD, grid, G, n, act, lda, (hipStream_t)stream);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+size_t nsq_siren_mlp_bwd_workspace_bytes(int64_t G, int d, int E, int nh, int HD) {
+  if (G < 1 || d < 1 || d > 3 || nh < 1 || nh > 8 || !nsq::siren_dims_ok(E, HD)) return 0;
+  return nsq::siren_ws(G, d, E, nh, HD).total * sizeof(float);
+}
+
+int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_stride_g, const float* grid, int64_t G,
+                      int d, const float* w0, const float* b0, int E, const float* wh, const float* bh, int nh, int HD,
+                      float* gw0, float* gb0, float* gwh, float* gbh, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  using namespace nsq;
+  clear_error();
+  int rc = siren_validate(grid, G, d, w0, E, wh, nh, HD);
+  if (rc) return rc;
+  NSQ_CHECK_ARG(gact && gw0 && gwh, "siren_mlp_bwd: null gradient pointer");
+  NSQ_CHECK_ARG(gact_stride_j >= 0 && gact_stride_g >= 0, "siren_mlp_bwd: negative gact stride");
+  NSQ_CHECK_ARG(!b0 || gb0, "siren_mlp_bwd: gb0 required with b0");
+  NSQ_CHECK_ARG(!bh || gbh, "siren_mlp_bwd: gbh required with bh");
+  const SirenWs w = siren_ws(G, d, E, nh, HD);
+  NSQ_CHECK_ARG(workspace && workspace_bytes >= w.total * sizeof(float),
+                "siren_mlp_bwd: workspace of %zu bytes required, got %zu", w.total * sizeof(float), workspace_bytes);
+  NSQ_CHECK_ARG(delta_lds_per_wave(E, HD, nh) <= kSirenMaxLds, "siren_mlp_bwd: %d hidden layers of %d too large", nh,
+                HD);
+  hipStream_t st = (hipStream_t)stream;
+  float* ws = static_cast<float*>(workspace);
+  float* act = ws + w.act;
+  float* del = ws + w.del;
+  float* gridT = ws + w.gridT;
+  float* part = ws + w.part;
+  float* rpart = ws + w.rpart;
+  const SirenNet n{w0, b0, wh, bh, d, nh};
+  siren_dispatch<SirenDelta>(E, HD, gact, gact_stride_j, gact_stride_g, grid, G, w.Gp, n, act, del, gridT, st);
+  // hidden layers i = nh..1: X = delta_i^T [HD], Y = a_{i-1}^T [IN]
+  for (int i = nh; i >= 1; --i) {
+    const int IN = i == 1 ? E : HD;
+    const int64_t xo = E + int64_t(i - 1) * HD, yo = i == 1 ? 0 : E + int64_t(i - 2) * HD;
+    float* gw = gwh + (i == 1 ? 0 : int64_t(HD) * E + int64_t(i - 2) * HD * HD);
+    gram(del + xo * w.Gp, w.Gp, act + yo * w.Gp, w.Gp, IN, G, HD, gw, gbh ? gbh + (i - 1) * HD : nullptr, part,
+         rpart, st);
+  }
+  // positional embedding: X = delta_0^T [E], Y = grid^T [d] (rows >= d read as zero)
+  gram(del, w.Gp, gridT, w.Gp, d, G, E, gw0, gb0, part, rpart, st);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+}  // extern "C"

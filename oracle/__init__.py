@@ -18,6 +18,9 @@ Contents:
   (``ops/circular_fftconv.py``, ``ops/mixed_fftconv.py``) and their float64
   brute forces.
 * :mod:`oracle.gated_ref` -- the Hyena gate compositions around the long conv.
+* :mod:`oracle.siren_ref` -- the SIREN implicit filter generator
+  (``modules/kernels_nd.py``, ``SIRENKernelND`` without FiLM) in float32 or
+  float64 torch.
 
 The seeded synthetic inputs of the benchmark configs are product-side
 (``nvsubquadratic_amd.workloads``): they are data, not a checker.

@@ -1,0 +1,123 @@
+"""GPU parity of the HIP SIREN filter generation (row F1) against the CPU restatement (oracle/siren_ref.py).
+
+The reference network (kernels_nd.py:876-1190 without FiLM) at the shapes its configs use (embedding and
+hidden width 32, 3 layers, 160-384 channels; examples/vit5_imagenet: KERNEL_* settings) and the long 1D
+grid of a Hyena layer (4096 channels).  Forward: rel-L2 <= 1e-5 against float64 and float32 evaluations.
+Backward: every weight and bias gradient against the restatement's autograd (float64), rel-L2 <= 1e-4;
+repeated backward calls are bitwise equal (fixed-order reductions).
+"""
+
+import pytest
+import torch
+
+from nvsubquadratic_amd.siren_hip import HipSIRENKernelND, siren_filter, siren_grid
+from oracle.fftconv_ref import rel_l2
+from oracle.siren_ref import siren_mlp_torch, siren_params
+
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # (d, grid shape, E, HD, nh, H, bias)
+    (1, (599,), 32, 32, 2, 160, True),
+    (2, (27, 27), 32, 32, 2, 384, True),
+    (3, (9, 7, 5), 16, 64, 1, 64, False),
+    (1, (4095,), 64, 16, 3, 256, True),
+    (2, (13, 11), 128, 128, 3, 32, True),
+    (1, (16383,), 32, 32, 2, 4096, True),
+]
+
+
+def _grid(shape):
+    return siren_grid([(s + 1) // 2 + 3 for s in shape], [1.0] * len(shape), [(s + 1) // 2 for s in shape])
+
+
+def _run(case, seed=0):
+    d, shape, E, HD, nh, H, bias = case
+    grid = _grid(shape).reshape(-1, d)
+    params = siren_params(d, E, HD, nh, H, bias=bias, seed=seed)
+    return grid, params
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_forward_matches_restatement(case):
+    grid, (w0, b0, hw, hb, wo, bo) = _run(case)
+    print(f"siren fwd {case}", flush=True)
+    dev = lambda t: None if t is None else t.cuda()  # noqa: E731
+    k = siren_filter(grid.cuda(), dev(w0), dev(b0), [w.cuda() for w in hw], None if hb is None else
+                     [b.cuda() for b in hb], dev(wo), dev(bo))
+    assert k.shape == (wo.shape[0], grid.shape[0]) and k.dtype == torch.float32
+    ref64 = siren_mlp_torch(grid, w0, b0, hw, hb, wo, bo, dtype=torch.float64).t()
+    ref32 = siren_mlp_torch(grid, w0, b0, hw, hb, wo, bo).t()
+    assert rel_l2(ref64, k) < 1e-5
+    assert rel_l2(ref32, k) < 1e-5
+
+
+# the last case is long enough for the readout's split weight-gradient product (16 slices + a remainder)
+BWD_CASES = CASES[:5] + [(1, (131071,), 32, 32, 2, 64, True)]
+
+
+@pytest.mark.parametrize("case", BWD_CASES)
+def test_backward_matches_restatement(case):
+    grid, (w0, b0, hw, hb, wo, bo) = _run(case, seed=1)
+    print(f"siren bwd {case}", flush=True)
+    leaves = [w0, b0, *hw, *(hb or []), wo, bo]
+    ref = [None if t is None else t.double().requires_grad_(True) for t in leaves]
+    nh = len(hw)
+
+    def split(ts):
+        w0_, b0_ = ts[0], ts[1]
+        hw_ = ts[2:2 + nh]
+        hb_ = ts[2 + nh:2 + 2 * nh] if hb is not None else None
+        return w0_, b0_, hw_, hb_, ts[-2], ts[-1]
+
+    y = siren_mlp_torch(grid.double(), *split(ref), dtype=torch.float64)
+    g = torch.randn(y.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(5))
+    y.backward(g)
+    hip = [None if t is None else t.cuda().requires_grad_(True) for t in leaves]
+    w0_, b0_, hw_, hb_, wo_, bo_ = split(hip)
+    k = siren_filter(grid.cuda(), w0_, b0_, hw_, hb_, wo_, bo_)
+    k.backward(g.t().float().cuda())
+    for r, h in zip(ref, hip):
+        if r is None:
+            continue
+        assert rel_l2(r.grad, h.grad) < 1e-4
+    first = [None if t is None else t.grad.clone() for t in hip]
+    for t in hip:
+        if t is not None:
+            t.grad = None
+    siren_filter(grid.cuda(), w0_, b0_, hw_, hb_, wo_, bo_).backward(g.t().float().cuda())
+    for a, t in zip(first, hip):
+        if t is not None:
+            assert torch.equal(a, t.grad)
+
+
+def test_module_forward_and_causal_half():
+    """HipSIRENKernelND.forward gives the reference's [1, *grid, H] (a view of the channel-first filter) and
+    kernel_bhl(causal=True) the half CKConvND keeps (kernel_len // 2 onwards)."""
+    torch.manual_seed(3)
+    m = HipSIRENKernelND(out_dim=96, data_dim=1, mlp_hidden_dim=32, num_layers=3, embedding_dim=32, omega_0=10.0,
+                         L_cache=512, use_bias=True).cuda()
+    with torch.no_grad():
+        for p in m.parameters():
+            if p.ndim == 1:
+                p.uniform_(-0.5, 0.5)  # nonzero biases
+    kernel, grid = m((300,))
+    assert kernel.shape == (1, 599, 96) and grid.shape == (1, 599, 1)
+    pe, hl = m.positional_embedding.linear, m.hidden_linears
+    ref = siren_mlp_torch(grid[0].cpu(), pe.weight.detach().cpu(), pe.bias.detach().cpu(),
+                          [lin.weight.detach().cpu() for lin in hl], [lin.bias.detach().cpu() for lin in hl],
+                          m.out_linear.weight.detach().cpu(), m.out_linear.bias.detach().cpu())
+    assert rel_l2(ref, kernel[0]) < 1e-5
+    assert kernel.movedim(-1, 1).is_contiguous()
+    causal = m.kernel_bhl((300,), causal=True)
+    assert causal.shape == (1, 96, 300)
+    # the readout GEMM over the half may tile differently from the full one: equal to fp32 rounding
+    torch.testing.assert_close(causal[0], kernel[0, 599 // 2:].t(), rtol=1e-6, atol=1e-6)
+
+
+def test_unsupported_widths_raise():
+    grid = torch.rand(10, 1, device="cuda")
+    w0, b0, hw, hb, wo, bo = siren_params(1, 24, 32, 1, 16)
+    with pytest.raises(NotImplementedError):
+        siren_filter(grid, w0.cuda(), b0.cuda(), [w.cuda() for w in hw], [b.cuda() for b in hb], wo.cuda(),
+                     bo.cuda())
