@@ -369,8 +369,8 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
         extra["unfused_ms_per_step"] = round(statistics.mean(_time_steps(step_unfused, steps, warmup)), 4)
         extra["fused_backward_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_fused_bwd, steps, warmup)), 4)
     elif name == "hyena-gated-2d":
-        # report-only (row F2, 2D): gate kernels around the N-d conv, against torch's gate ops around the same HIP
-        # conv (which keeps z for the backward) and the conv alone, fwd+bwd at cfg4's shape
+        # report-only (row F2, 2D): the gates inside the N-d conv's first and last passes, against torch's gate ops
+        # around the same HIP conv (which keeps z for the backward) and the conv alone, fwd+bwd at cfg4's shape
         import torch.nn.functional as Fn
 
         from nvsubquadratic_amd.gated_fftconv_hip import hyena_gated_fftconv2d_bhl
@@ -385,7 +385,7 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
         phase, dtype = "fwd+bwd", "f32"
         nbytes = algorithmic_bytes_gated(B, Ch, X * X, K * K, 2)
         desc = ("hyena-gated-2d: gated 2D FFT conv fwd+bwd (z = q silu(k), y = (conv(z) + s z) silu(v)), "
-                "B=16 C=384 128^2, filter 128^2 fp32, FFT 256^2, bf16 I/O; gate kernels around the N-d conv")
+                "B=16 C=384 128^2, filter 128^2 fp32, FFT 256^2, bf16 I/O; gates in the N-d conv's first and last passes")
 
         def clear():
             for t in (q, kk, v, w, sh):

@@ -1,492 +1,10 @@
-// Host plans and C ABI of the 2D / 3D non-causal FFT convolution (see
-// fftconv_nd_impl.h for the kernels and the pass structure).
-#include "fftconv_nd_impl.h"
-#include "gate.h"
-
-#include <initializer_list>
+// C ABI of the plain and mixed-boundary 2D / 3D non-causal FFT convolution
+// (host plans in fftconv_nd_plan.h, kernels in fftconv_nd_impl.h).
+#include "fftconv_nd_plan.h"
 
 namespace nsq {
 
-// Boundary condition per axis (ops/mixed_fftconv.py:295-343, `_mixed_recipe`):
-//   zero-padded ("same"): F_d = 2^ceil(log2(S_d + ceil(K_d/2))) >= 16, output
-//     window [K_d/2, K_d/2 + S_d) of the linear conv (crop o_d = K_d/2);
-//   periodic (circular):  F_d = S_d (a power of two in [16, 2^kNdMaxLogF]),
-//     K_d <= S_d, output = the whole circular conv rolled by -(K_d-1)/2, done
-//     as a ramp on the filter spectrum (r_d = (K_d-1)/2, o_d = 0).  A shorter
-//     power-of-two period (2, 4, 8) is tiled: F_d = 16 and the first passes read
-//     x and g at index n & (S_d - 1) (their periodic extension, of which the
-//     period-16 circular conv restricted to [0, S_d) is the period-S_d one;
-//     the filter is not extended).  The extension repeats every product
-//     F_d / S_d times, so gk and gs are scaled by S_d / F_d.  A period of 1 is
-//     the zero-padded 1-tap case.
-// Either way y[n] = sum_j k[j] x[n + c_d - j] along the axis, c_d = o_d + r_d,
-// which is the shift the backward's ramp and its gs lag use.
-struct NdPlan {
-  int nd;
-  int64_t B, H, kb;      // kb = kernel batch: 1 (shared) or B (per-sample FiLM)
-  int S[3], K[3];        // padded to 3 axes: (S0, S1, S2) with S1 = K1 = 1 for 2D
-  int lF[3], F[3], c[3];
-  int o[3], r[3];        // forward crop offsets and forward ramp shifts (c = o + r)
-  bool ramp;             // some r_d != 0
-  int wm[3];             // index mask of x / g along the axis: -1, or S_d - 1 for a tiled periodic axis
-  float gk_scale;        // 1 / (product of F_d / S_d over tiled axes): gk, gs of the periodic extension
-  bool pack;             // 2D: the DC and Nyquist bins share bin 0 (FH = F2/2)
-  int FH;        // spectrum columns along the last axis: F2/2 + 1, or F2/2 packed
-  int RS;        // spectrum row stride (complex elements), >= FH
-  int64_t spec;
-};
-
-// `periodic`: bit d set = axis d (of the nd given axes) is periodic.
-static bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kb,
-                         unsigned periodic, NdPlan& p) {
-  if (nd != 2 && nd != 3) return false;
-  if (periodic >> nd) return false;
-  p.nd = nd;
-  p.B = B;
-  p.H = H;
-  p.kb = kb;
-  p.ramp = false;
-  p.gk_scale = 1.f;
-  int s[3] = {1, 1, 1}, k[3] = {1, 1, 1};
-  bool per[3] = {false, false, false};
-  if (nd == 2) {
-    s[0] = int(S[0]); s[2] = int(S[1]);
-    k[0] = int(K[0]); k[2] = int(K[1]);
-    per[0] = periodic & 1u; per[2] = (periodic >> 1) & 1u;
-  } else {
-    for (int d = 0; d < 3; ++d) { s[d] = int(S[d]); k[d] = int(K[d]); per[d] = (periodic >> d) & 1u; }
-  }
-  for (int d = 0; d < 3; ++d) {
-    p.S[d] = s[d];
-    p.K[d] = k[d];
-    p.wm[d] = -1;
-    if (nd == 2 && d == 1) {
-      p.lF[d] = 0; p.F[d] = 1; p.c[d] = 0; p.o[d] = 0; p.r[d] = 0;
-      continue;
-    }
-    if (per[d] && s[d] > 1) {
-      if (k[d] < 1 || k[d] > s[d] || (s[d] & (s[d] - 1))) return false;
-      int lf = ilog2_ceil(s[d]);
-      if (lf > kNdMaxLogF) return false;
-      if (lf < 4) {  // tiled short period
-        p.wm[d] = s[d] - 1;
-        p.gk_scale *= float(s[d]) / 16.f;
-        lf = 4;
-      }
-      p.lF[d] = lf;
-      p.F[d] = 1 << lf;
-      p.c[d] = p.r[d] = (k[d] - 1) / 2;
-      p.o[d] = 0;
-      p.ramp = p.ramp || p.r[d] != 0;
-      continue;
-    }
-    if (s[d] < 1 || k[d] < 1 || k[d] > 2 * s[d]) return false;
-    int lf = ilog2_ceil(int64_t(s[d]) + (k[d] + 1) / 2);
-    if (lf < 4) lf = 4;
-    if (lf > kNdMaxLogF) return false;
-    p.lF[d] = lf;
-    p.F[d] = 1 << lf;
-    p.c[d] = p.o[d] = k[d] / 2;
-    p.r[d] = 0;
-  }
-  // 2D rows store the real DC and Nyquist bins packed in bin 0 (N columns, a
-  // multiple of the axis-0 passes' column tiles, instead of N + 1 with a
-  // one-column tail); 3D keeps N + 1 (its axis-1 pass pairs across columns).
-  p.pack = nd == 2;
-  p.FH = p.pack ? p.F[2] / 2 : p.F[2] / 2 + 1;
-  // 2D: rows padded to a multiple of 16 complex values (a pad only for
-  // F2 = 16), so the 16-column segments the axis-0 passes move per row start
-  // on a 128-byte line.  The pad is never read or written.  3D planes are F1 rows of FH: the axis-0 segments are aligned
-  // there already (the plane stride is a multiple of 16) and the plane passes
-  // keep their compile-time row stride.
-  p.RS = nd == 2 ? (p.FH + 15) / 16 * 16 : p.FH;
-  p.spec = int64_t(p.F[0]) * p.F[1] * p.RS;
-  return true;
-}
-
-// ---------------------------------------------------------------------------
-// Compile-time dispatch of the row / column passes on their log2 sizes.
-// ---------------------------------------------------------------------------
-template <int LO, int HI, class F>
-static bool with_log(int v, F&& f) {
-  if constexpr (LO > HI) {
-    return false;
-  } else {
-    if (v == LO) {
-      f(std::integral_constant<int, LO>{});
-      return true;
-    }
-    return with_log<LO + 1, HI>(v, f);
-  }
-}
-
-// wrap: x / g (read through the plan's periodic extension masks); the filter
-// is never extended.
-template <int DT>
-static bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, bool wrap, float2* ws,
-                    const float2* tw, hipStream_t st) {
-  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.RS};
-  const int wm = wrap ? p.wm[2] : -1;
-  return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
-    constexpr int LOGN = decltype(L)::value;
-    using C = RowNdCfg<LOGN>;
-    const dim3 grid{unsigned(ceil_div(rg.rows, C::M))};
-    auto go = [&](auto al, auto half) {
-      if (p.pack)
-        hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value, true>), grid,
-                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, wm, rg, ws, tw);
-      else
-        hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, decltype(al)::value, decltype(half)::value, false>), grid,
-                           dim3(C::T), 0, st, (const typename Elem<DT>::T*)src, len, wm, rg, ws, tw);
-    };
-    using T_ = std::true_type;
-    using F_ = std::false_type;
-    const bool al = pairs_aligned<DT>(src, len, len);
-    if (len <= C::N && wm == -1)  // packed samples [N/2, N) of every row are zero
-      al ? go(T_{}, T_{}) : go(F_{}, T_{});
-    else
-      al ? go(T_{}, F_{}) : go(F_{}, F_{});
-  });
-}
-
-template <int DT, int MODE>
-static bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int n1, RowInvOut o, const float2* tw,
-                    hipStream_t st) {
-  RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.RS};
-  return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
-    constexpr int LOGN = decltype(L)::value;
-    using C = RowNdCfg<LOGN>;
-    const dim3 grid(unsigned(ceil_div(rg.rows, C::M)));
-    const bool fast = MODE == ND_OUT_Y && o.off2 % 2 == 0 && o.w2 % 8 == 0 &&
-                      (reinterpret_cast<uintptr_t>(o.out) & 15) == 0 && (reinterpret_cast<uintptr_t>(o.aux) & 15) == 0;
-    auto go = [&](auto has_s, auto fst, auto pack) {
-      hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, decltype(has_s)::value, decltype(fst)::value,
-                                            decltype(pack)::value>),
-                         grid, dim3(C::T), 0, st, ws, rg, o, tw);
-    };
-    using T_ = std::true_type;
-    using F_ = std::false_type;
-    auto go_pack = [&](auto has_s, auto fst) { p.pack ? go(has_s, fst, T_{}) : go(has_s, fst, F_{}); };
-    if constexpr (MODE == ND_OUT_Y) {
-      if (fast) {
-        o.s ? go_pack(T_{}, T_{}) : go_pack(F_{}, T_{});
-        return;
-      }
-      o.s ? go_pack(T_{}, F_{}) : go_pack(F_{}, F_{});
-    } else {
-      go_pack(F_{}, F_{});
-    }
-  });
-}
-
-// Column blocks of a pass: full blocks of the kernel's regular width, then the
-// remainder in blocks of kNdTailTile's 4 columns at column offset jbase (a
-// remainder exists for short 2D rows, FH = F2/2 < 16, and for 3D blocks whose
-// F1 * FH is not a multiple of the width).  launch(tile, grid_y, jbase)
-// launches one instance.
-constexpr int kNdTailTile = 1;  // ColNdCfg clamps this to 4 columns
-template <int LOGF, int TARGET, class LAUNCH>
-static void col_blocks(int inner, LAUNCH&& launch) {
-  using CM = ColNdCfg<LOGF, TARGET>;
-  using CT = ColNdCfg<LOGF, kNdTailTile>;
-  const int full = inner / CM::M, rem = inner - full * CM::M;
-  if (full) launch(std::integral_constant<int, TARGET>{}, full, 0);
-  if (rem) launch(std::integral_constant<int, kNdTailTile>{}, int(ceil_div(rem, CT::M)), full * CM::M);
-}
-
-// Column-block workgroups per channel of an axis-0 pass with tile target
-// `target` (col_blocks: full blocks of M columns, then blocks of 4).
-static int64_t axis0_blocks(const NdPlan& p, int target) {
-  const int inner = p.F[1] * p.FH;
-  int m = target >> p.lF[0];
-  m = m < 4 ? 4 : (m > 16 ? 16 : m);
-  const int full = inner / m, rem = inner - full * m;
-  return full + (rem + 3) / 4;
-}
-
-// Batch split of the axis-0 product / adjoint passes for a shared kernel: a
-// workgroup per (channel, column block) loops over the batch, so few channels
-// and small spectra leave CUs idle.  Below `lo` workgroups the batch is split
-// until about `want` are in flight.  The product pass splits for free (each
-// share re-reads only its filter columns): lo 4096, want 6144 (24 per CU);
-// the adjoint's shares each add a partial filter-gradient block and a reduce:
-// lo 1024, want 3072 (measured on MI355X: more shares cost more than they
-// hide there).  FiLM kernels already launch B*H workgroups.
-static int axis0_batch_split(const NdPlan& p, int target, int64_t lo, int64_t want_total) {
-  if (p.kb != 1) return 1;
-  const int64_t wgs = p.H * axis0_blocks(p, target);
-  if (wgs >= lo) return 1;
-  const int64_t want = (want_total + wgs - 1) / wgs;
-  return int(want < p.B ? want : p.B);
-}
-static int mul_batch_split(const NdPlan& p) { return axis0_batch_split(p, 8192, 4096, 6144); }
-static int bwd_batch_split(const NdPlan& p) { return axis0_batch_split(p, kNdBwdTile, 1024, 3072); }
-
-// Axis-0 columns: the inner index j runs over a block's F1 rows of the last
-// axis; 3D packs them (RS = FH), 2D has one padded row (F1 = 1, j < FH).
-static ColGeom axis0_geom(const NdPlan& p) {
-  return ColGeom{1, 0, p.spec, int64_t(p.F[1]) * p.RS, p.F[1] * p.FH};
-}
-
-// Column pass along axis d (0 or 1) of `nbh` blocks whose valid extent along
-// axis 0 is n_valid0 (used as the middle-row count of axis-1 passes).
-template <bool INV>
-static bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_valid0, int in_cnt, int out_off,
-                     int out_cnt, const float2* tw, hipStream_t st, int wm = -1) {
-  ColGeom cg;
-  if (axis == 1) {
-    cg = ColGeom{n_valid0, int64_t(p.F[1]) * p.RS, p.spec, int64_t(p.RS), p.FH};
-  } else {
-    cg = axis0_geom(p);
-  }
-  const int64_t n_outer = nbh * cg.n_mid;
-  return with_log<4, kNdMaxLogF>(p.lF[axis], [&](auto L) {
-    constexpr int LOGF = decltype(L)::value;
-    col_blocks<LOGF, 8192>(cg.inner_count, [&](auto tile, int gy, int jbase) {
-      constexpr int TGT = decltype(tile)::value;
-      hipLaunchKernelGGL((nd_col_kernel<LOGF, INV, TGT>), dim3(unsigned(n_outer), unsigned(gy)),
-                         dim3(ColNdCfg<LOGF, TGT>::T), 0, st, ws, cg, in_cnt, wm, out_off, out_cnt, jbase, tw);
-    });
-  });
-}
-
-// Plane passes (3D, a (b, h, a0) plane fits in LDS): both inner axes in one
-// kernel.  plane_ok mirrors PlaneCfg::OK for the plan's sizes.
-static bool plane_ok(const NdPlan& p) {
-  if (p.nd != 3) return false;
-  const int logn = p.lF[2] - 1, logf1 = p.lF[1];
-  if (logn < 4 || logn > 9 || logf1 < 4 || logf1 > kNdMaxLogF) return false;
-  const int n = 1 << logn, f1 = 1 << logf1, mr = 4096 >> logn, mc = 4096 >> logf1;
-  return mr >= 1 && mr <= f1 && mc >= 1 && mc <= n && int64_t(f1) * (n + n / 16) * 8 <= 80 * 1024;
-}
-
-template <class F>
-static bool with_plane(const NdPlan& p, F&& f) {
-  bool launched = false;
-  with_log<4, 9>(p.lF[2] - 1, [&](auto LN) {
-    constexpr int LOGN = decltype(LN)::value;
-    with_log<4, kNdMaxLogF>(p.lF[1], [&](auto LF) {
-      constexpr int LOGF1 = decltype(LF)::value;
-      if constexpr (PlaneCfg<LOGN, LOGF1>::OK) {
-        f(std::integral_constant<int, LOGN>{}, std::integral_constant<int, LOGF1>{});
-        launched = true;
-      }
-    });
-  });
-  return launched;
-}
-
-// Forward inner-axis transforms of nbh blocks of [n0][n1][len] real rows
-// (wrap: x / g, read through the periodic extension masks).
-template <int DT>
-static bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, bool wrap, float2* ws,
-                      const float2* tw, hipStream_t st) {
-  const int wm1 = wrap ? p.wm[1] : -1, wm2 = wrap ? p.wm[2] : -1;
-  if (plane_ok(p)) {
-    using ET = typename Elem<DT>::T;
-    const bool al = pairs_aligned<DT>(src, len, len);
-    return with_plane(p, [&](auto LN, auto LF) {
-      constexpr int LOGN = decltype(LN)::value, LOGF1 = decltype(LF)::value;
-      const dim3 grid(unsigned(nbh * n0));
-      auto go = [&](auto alc, auto half) {
-        hipLaunchKernelGGL((nd_plane_fwd_kernel<LOGN, LOGF1, DT, decltype(alc)::value, decltype(half)::value>), grid,
-                           dim3(256), 0, st, (const ET*)src, n0, n1, len, wm1, wm2, ws, p.spec, tw);
-      };
-      using T_ = std::true_type;
-      using F_ = std::false_type;
-      if (len <= (1 << LOGN) && 2 * n1 <= (1 << LOGF1) && wm1 == -1 && wm2 == -1)  // at least half zero padding
-        al ? go(T_{}, T_{}) : go(F_{}, T_{});
-      else
-        al ? go(T_{}, F_{}) : go(F_{}, F_{});
-    });
-  }
-  if (!row_fwd<DT>(p, src, nbh, n0, n1, len, wrap, ws, tw, st)) return false;
-  return p.nd != 3 || col_pass<false>(p, ws, nbh, 1, n0, n1, 0, p.F[1], tw, st, wm1);
-}
-
-// Inverse inner-axis transforms, crop (axis 1: [off1, off1 + n1out); axis 2:
-// RowInvOut) and epilogue, for nbh blocks whose axis-0 extent is n0.
-template <int DT, int MODE>
-static bool inner_inv(const NdPlan& p, float2* ws, int64_t nbh, int n0, int off1, int n1out, RowInvOut o,
-                      const float2* tw, hipStream_t st) {
-  if (plane_ok(p)) {
-    const bool has_s = MODE == ND_OUT_Y && o.s;
-    return with_plane(p, [&](auto LN, auto LF) {
-      constexpr int LOGN = decltype(LN)::value, LOGF1 = decltype(LF)::value;
-      const dim3 grid(unsigned(nbh * n0));
-      if (has_s)
-        hipLaunchKernelGGL((nd_plane_inv_kernel<LOGN, LOGF1, DT, MODE, true>), grid, dim3(256), 0, st,
-                           (const float2*)ws, p.spec, n0, off1, n1out, o, tw);
-      else
-        hipLaunchKernelGGL((nd_plane_inv_kernel<LOGN, LOGF1, DT, MODE, false>), grid, dim3(256), 0, st,
-                           (const float2*)ws, p.spec, n0, off1, n1out, o, tw);
-    });
-  }
-  if (p.nd == 3 && !col_pass<true>(p, ws, nbh, 1, n0, p.F[1], off1, n1out, tw, st)) return false;
-  return row_inv<DT, MODE>(p, ws, nbh, n0, n1out, o, tw, st);
-}
-
-
-
-// Filter spectrum: kb*H blocks of the [kb*H][K0][K1][K2] float32 kernel.
-static bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {
-  const int64_t nk = p.kb * p.H;
-  if (!inner_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], false, wsk, tw, st)) return false;
-  return col_pass<false>(p, wsk, nk, 0, 1, p.K[0], 0, p.F[0], tw, st);
-}
-
-// Workspace layout (spectrum blocks of p.spec complex64):
-//   backward: [G: BH | X: BH | Khat: NK | Q: NK | (nz - 1) * NK partial Q]
-//     (nz = bwd_batch_split: the adjoint's batch split, 1 for most shapes)
-//   forward with `save` (a backward-sized workspace): X after the inner-axis
-//     passes and Khat at the backward's positions, the product in the G region;
-//     the backward called with fwd_state then starts from them.
-//   forward without `save`: [X (product in place): BH | Khat: NK].
-template <int DT>
-static bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws, bool save,
-                       const float2* tw, hipStream_t st) {
-  const int64_t BH = p.B * p.H;
-  float2* wsx = save ? ws + BH * p.spec : ws;
-  float2* wsk = wsx + BH * p.spec;
-  float2* wsy = save ? ws : wsx;
-  if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-  if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st)) return false;
-  const ColGeom cg = axis0_geom(p);
-  const Ramp rf{p.r[0], p.r[1], p.r[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
-  bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
-    constexpr int LOGF = decltype(L)::value;
-    col_blocks<LOGF, 8192>(cg.inner_count, [&](auto tile, int gy, int jbase) {
-      constexpr int TGT = decltype(tile)::value;
-      // a narrow tail instance (3D blocks whose F1 * FH is not a multiple of
-      // the column tile, or 2D rows shorter than 16 bins) takes one image per
-      // workgroup: its work per image is small
-      const int bsplit = (TGT == kNdTailTile && p.kb == 1) ? int(p.B) : mul_batch_split(p);
-      const dim3 grid(unsigned((p.kb != 1 ? BH : p.H) * bsplit), unsigned(gy));
-      auto go = [&](auto half, auto ramp) {
-        auto launch = [&](auto pack) {
-          hipLaunchKernelGGL(
-              (nd_col_mul_kernel<LOGF, TGT, decltype(half)::value, decltype(ramp)::value, decltype(pack)::value>),
-              grid, dim3(ColNdCfg<LOGF, TGT>::T), 0, st, (const float2*)wsx, wsy, (const float2*)wsk, cg, int(p.B),
-              int(p.H), int(p.kb != 1), p.S[0], p.wm[0], p.o[0], rf, jbase, bsplit, tw);
-        };
-        p.pack ? launch(std::true_type{}) : launch(std::false_type{});
-      };
-      using T_ = std::true_type;
-      using F_ = std::false_type;
-      if (2 * p.S[0] <= p.F[0] && p.wm[0] == -1)  // the x columns are at least half zero padding
-        p.ramp ? go(T_{}, T_{}) : go(T_{}, F_{});
-      else
-        p.ramp ? go(F_{}, T_{}) : go(F_{}, F_{});
-    });
-  });
-  if (!ok) return false;
-  RowInvOut o{y, x, s, nullptr, int(p.H), p.o[2], p.S[2], 0, 0, 0,
-              1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2))};
-  return inner_inv<DT, ND_OUT_Y>(p, wsy, BH, p.S[0], p.o[1], p.S[1], o, tw, st);
-}
-
-template <int DT>
-static bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const float* k, const void* s, void* gx,
-                       float* gk, float* gs, float2* ws, bool fwd_state, const float2* tw, hipStream_t st) {
-  const int64_t BH = p.B * p.H, NK = p.kb * p.H;
-  float2* wsg = ws;
-  float2* wsx = wsg + BH * p.spec;
-  float2* wsk = wsx + BH * p.spec;
-  float2* wsq = wsk + NK * p.spec;
-  if (!fwd_state) {
-    if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-    if (!inner_fwd<DT>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st)) return false;
-  }
-  if (!inner_fwd<DT>(p, g, BH, p.S[0], p.S[1], p.S[2], true, wsg, tw, st)) return false;
-  const ColGeom cg = axis0_geom(p);
-  const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
-  const int nz = bwd_batch_split(p);  // partial Q blocks follow Q in the workspace
-  bool ok = with_log<4, kNdMaxLogF>(p.lF[0], [&](auto L) {
-    constexpr int LOGF = decltype(L)::value;
-    col_blocks<LOGF, kNdBwdTile>(cg.inner_count, [&](auto tile, int gy, int jbase) {
-      constexpr int TGT = decltype(tile)::value;
-      const dim3 grid{unsigned(NK), unsigned(gy), unsigned(nz)};
-      auto go = [&](auto half, auto pack) {
-        hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, decltype(half)::value, decltype(pack)::value>), grid,
-                           dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg, (const float2*)wsx, (const float2*)wsk, wsq,
-                           cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.wm[0], p.K[0], rp, jbase, NK, tw);
-      };
-      using T_ = std::true_type;
-      using F_ = std::false_type;
-      if (2 * p.S[0] <= p.F[0] && p.wm[0] == -1)  // the g and x columns are at least half zero padding
-        p.pack ? go(T_{}, T_{}) : go(T_{}, F_{});
-      else
-        p.pack ? go(F_{}, T_{}) : go(F_{}, F_{});
-    });
-  });
-  if (!ok) return false;
-  if (nz > 1) {
-    const int64_t count = int64_t(p.K[0]) * p.F[1] * p.RS;  // rows [0, K0) of a block
-    const int64_t blocks = (NK * count + 255) / 256;
-    hipLaunchKernelGGL(nd_q_reduce_kernel, dim3(unsigned(blocks < 8192 ? blocks : 8192)), dim3(256), 0, st, wsq, NK,
-                       p.spec, count, nz);
-  }
-  const float scale = 1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2));
-  RowInvOut og{gx, g, s, nullptr, int(p.H), 0, p.S[2], 0, 0, 0, scale};
-  if (!inner_inv<DT, ND_OUT_Y>(p, wsg, BH, p.S[0], 0, p.S[1], og, tw, st)) return false;
-  RowInvOut ok_{gk, nullptr, nullptr, gs, int(p.H), 0, p.K[2], p.c[0], p.c[1], p.c[2], scale * p.gk_scale};
-  return inner_inv<NSQ_DTYPE_F32, ND_OUT_GK>(p, wsq, NK, p.K[0], 0, p.K[1], ok_, tw, st);
-}
-
-static int validate_nd(int nd, const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H,
-                       const int64_t* S, const int64_t* K, int64_t kb, unsigned periodic, NdPlan& p) {
-  NSQ_CHECK_ARG(a && b && k && S && K, "fftconv_nd: null pointer argument");
-  NSQ_CHECK_ARG(nd == 2 || nd == 3, "fftconv_nd: nd must be 2 or 3 (got %d)", nd);
-  NSQ_CHECK_ARG(valid_dtype(dtype), "fftconv_nd: unsupported dtype code %d", dtype);
-  NSQ_CHECK_ARG(B >= 1 && H >= 1, "fftconv_nd: sizes must be positive");
-  NSQ_CHECK_ARG(kb == 1 || kb == B, "fftconv_nd: kernel batch must be 1 or B (got %lld, B=%lld)", (long long)kb,
-                (long long)B);
-  NSQ_CHECK_ARG((periodic >> nd) == 0, "fftconv_nd: periodic mask 0x%x names an axis >= nd=%d", periodic, nd);
-  for (int d = 0; d < nd; ++d) {
-    if ((periodic >> d) & 1u) {
-      NSQ_CHECK_ARG(S[d] >= 1 && K[d] >= 1 && K[d] <= S[d],
-                    "fftconv_nd: periodic axis %d: kernel size %lld must be in [1, %lld]", d, (long long)K[d],
-                    (long long)S[d]);
-      if (S[d] > (1 << kNdMaxLogF) || (S[d] & (S[d] - 1))) {
-        set_error("fftconv_nd: unsupported shape: periodic axis %d has length %lld; the HIP kernels take periodic "
-                  "lengths that are powers of two up to %d",
-                  d, (long long)S[d], 1 << kNdMaxLogF);
-        return NSQ_ERR_UNSUPPORTED;
-      }
-    } else {
-      NSQ_CHECK_ARG(S[d] >= 1 && K[d] >= 1 && K[d] <= 2 * S[d],
-                    "fftconv_nd: axis %d: kernel size %lld must be in [1, 2*%lld]", d, (long long)K[d],
-                    (long long)S[d]);
-    }
-  }
-  if (!make_nd_plan(nd, B, H, S, K, kb, periodic, p)) {
-    set_error("fftconv_nd: unsupported shape: every axis needs an FFT length <= %d", 1 << kNdMaxLogF);
-    return NSQ_ERR_UNSUPPORTED;
-  }
-  if (B * H * int64_t(p.F[0]) * p.F[1] >= (int64_t(1) << 31)) {  // row passes index rows in 32 bits
-    set_error("fftconv_nd: unsupported shape: B*H*F0*F1 = %lld rows exceeds 2^31 - 1",
-              (long long)(B * H * int64_t(p.F[0]) * p.F[1]));
-    return NSQ_ERR_UNSUPPORTED;
-  }
-  if (p.spec * int64_t(sizeof(float2)) >= (int64_t(1) << 31)) {  // column passes: 32-bit offsets in a block
-    set_error("fftconv_nd: unsupported shape: one spectrum block of %lld complex values exceeds 2 GiB",
-              (long long)p.spec);
-    return NSQ_ERR_UNSUPPORTED;
-  }
-  return NSQ_OK;
-}
-
-static size_t nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
-                                 unsigned periodic, int direction) {
-  NdPlan p;
-  if (!S || !K || !make_nd_plan(nd, B, H, S, K, kbatch, periodic, p)) return 0;
-  const int64_t blocks = direction == NSQ_DIR_BWD
-                             ? (2 * B * H + (1 + bwd_batch_split(p)) * kbatch * H)
-                             : (B * H + kbatch * H);
-  return size_t(blocks * p.spec) * sizeof(float2);
-}
-
-static int nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
+int nd_fwd(int nd, const void* x, const float* k, const void* shortcut, void* y, int dtype, int64_t B,
                   int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace,
                   size_t workspace_bytes, void* stream) {
   clear_error();
@@ -512,7 +30,7 @@ static int nd_fwd(int nd, const void* x, const float* k, const void* shortcut, v
   return NSQ_OK;
 }
 
-static int nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
+int nd_bwd(int nd, const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
                   float* gs, int dtype, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch,
                   unsigned periodic, void* workspace, size_t workspace_bytes, int fwd_state, void* stream) {
   clear_error();
@@ -539,139 +57,11 @@ static int nd_bwd(int nd, const void* g, const void* x, const float* k, const vo
   return NSQ_OK;
 }
 
-// ---------------------------------------------------------------------------
-// Hyena-gated 2D/3D conv: the elementwise gate kernels (gate.h) around the
-// N-d conv.  Workspace: the conv's (rounded up to 256 bytes), then I/O-dtype
-// buffers of B*H*prod(S) values: forward z and (when the caller keeps none) y1;
-// backward z, dy1 and dz.
-// ---------------------------------------------------------------------------
-static int64_t nd_numel(int nd, int64_t B, int64_t H, const int64_t* S) {
-  int64_t n = B * H;
-  for (int d = 0; d < nd; ++d) n *= S[d];
-  return n;
-}
-
-static size_t gated_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
-                                       int64_t kbatch, unsigned periodic, int dtype, int direction) {
-  const size_t conv = nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, direction);
-  if (!conv || !valid_dtype(dtype)) return 0;
-  const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
-  return round256(conv) + size_t(direction == NSQ_DIR_BWD ? 3 : 2) * round256(size_t(nd_numel(nd, B, H, S)) * es);
-}
-
-template <int DT>
-static void gate_pass(int op, const GateEw& g, int64_t n, hipStream_t st) {
-  switch (op) {
-    case GATE_OP_FWD1: launch_gate_ew<DT, GATE_OP_FWD1>(g, n, st); break;
-    case GATE_OP_FWD2: launch_gate_ew<DT, GATE_OP_FWD2>(g, n, st); break;
-    case GATE_OP_BWD2: launch_gate_ew<DT, GATE_OP_BWD2>(g, n, st); break;
-    default: launch_gate_ew<DT, GATE_OP_BWD1>(g, n, st); break;
-  }
-}
-
-static void gate_pass(int dtype, int op, const GateEw& g, int64_t n, hipStream_t st) {
-  switch (dtype) {
-    case NSQ_DTYPE_F32: gate_pass<NSQ_DTYPE_F32>(op, g, n, st); break;
-    case NSQ_DTYPE_BF16: gate_pass<NSQ_DTYPE_BF16>(op, g, n, st); break;
-    default: gate_pass<NSQ_DTYPE_F16>(op, g, n, st); break;
-  }
-}
-
-static bool aligned16_nd(std::initializer_list<const void*> ps) {
-  for (const void* p : ps)
-    if (p && (reinterpret_cast<uintptr_t>(p) & 15)) return false;
-  return true;
-}
-
-static int gated_nd_fwd(int nd, const void* q, const void* kgate, const void* v, const float* k, const void* shortcut,
-                        void* y, void* y1, int dtype, int act1, int act2, int64_t B, int64_t H, const int64_t* S,
-                        const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace, size_t workspace_bytes,
-                        void* stream) {
-  clear_error();
-  NdPlan p;
-  int rc = validate_nd(nd, q, y, k, dtype, B, H, S, K, kbatch, periodic, p);
-  if (rc) return rc;
-  NSQ_CHECK_ARG(kgate && v, "gated_fftconv_nd_fwd: null gate operand");
-  NSQ_CHECK_ARG(act1 >= 0 && act1 <= 2 && act2 >= 0 && act2 <= 2,
-                "gated_fftconv_nd: gate codes must be 0 (identity), 1 (sigmoid) or 2 (silu); got %d, %d", act1, act2);
-  NSQ_CHECK_ARG(aligned16_nd({q, kgate, v, y, y1, workspace}), "gated_fftconv_nd_fwd: tensors must be 16-byte aligned");
-  const size_t need = gated_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dtype, NSQ_DIR_FWD);
-  NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv_nd_fwd: workspace of %zu bytes required, got %zu",
-                need, workspace_bytes);
-  const size_t conv = round256(nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_FWD));
-  const int64_t n = nd_numel(nd, B, H, S);
-  const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
-  char* z = (char*)workspace + conv;
-  void* y1b = y1 ? y1 : (void*)(z + round256(n * es));
-  hipStream_t st = (hipStream_t)stream;
-  gate_pass(dtype, GATE_OP_FWD1, GateEw{q, kgate, nullptr, z, nullptr, act1}, n, st);
-  rc = nd_fwd(nd, z, k, shortcut, y1b, dtype, B, H, S, K, kbatch, periodic, workspace, conv, stream);
-  if (rc) return rc;
-  gate_pass(dtype, GATE_OP_FWD2, GateEw{y1b, v, nullptr, y, nullptr, act2}, n, st);
-  NSQ_CHECK_LAUNCH();
-  return NSQ_OK;
-}
-
-static int gated_nd_bwd(int nd, const void* g, const void* q, const void* kgate, const void* v, const void* y1,
-                        const float* k, const void* shortcut, void* dq, void* dkgate, void* dv, float* gk, float* gs,
-                        int dtype, int act1, int act2, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
-                        int64_t kbatch, unsigned periodic, void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  NdPlan p;
-  int rc = validate_nd(nd, g, q, k, dtype, B, H, S, K, kbatch, periodic, p);
-  if (rc) return rc;
-  NSQ_CHECK_ARG(kgate && v && y1 && dq && dkgate && dv && gk, "gated_fftconv_nd_bwd: null tensor pointer");
-  NSQ_CHECK_ARG(!shortcut || gs, "gated_fftconv_nd_bwd: gs required when a shortcut is given");
-  NSQ_CHECK_ARG(act1 >= 0 && act1 <= 2 && act2 >= 0 && act2 <= 2,
-                "gated_fftconv_nd: gate codes must be 0 (identity), 1 (sigmoid) or 2 (silu); got %d, %d", act1, act2);
-  NSQ_CHECK_ARG(aligned16_nd({g, q, kgate, v, y1, dq, dkgate, dv, workspace}),
-                "gated_fftconv_nd_bwd: tensors must be 16-byte aligned");
-  const size_t need = gated_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dtype, NSQ_DIR_BWD);
-  NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv_nd_bwd: workspace of %zu bytes required, got %zu",
-                need, workspace_bytes);
-  const size_t conv = round256(nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, NSQ_DIR_BWD));
-  const int64_t n = nd_numel(nd, B, H, S);
-  const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
-  char* z = (char*)workspace + conv;
-  char* dy1 = z + round256(n * es);
-  char* dz = dy1 + round256(n * es);
-  hipStream_t st = (hipStream_t)stream;
-  gate_pass(dtype, GATE_OP_BWD2, GateEw{g, v, y1, dy1, dv, act2}, n, st);
-  gate_pass(dtype, GATE_OP_FWD1, GateEw{q, kgate, nullptr, z, nullptr, act1}, n, st);
-  rc = nd_bwd(nd, dy1, z, k, shortcut, dz, gk, gs, dtype, B, H, S, K, kbatch, periodic, workspace, conv, 0, stream);
-  if (rc) return rc;
-  gate_pass(dtype, GATE_OP_BWD1, GateEw{dz, q, kgate, dq, dkgate, act1}, n, st);
-  NSQ_CHECK_LAUNCH();
-  return NSQ_OK;
-}
-
 }  // namespace nsq
 
 using namespace nsq;
 
 extern "C" {
-
-size_t nsq_gated_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
-                                            int64_t kbatch, unsigned periodic, int dtype, int direction) {
-  return gated_nd_workspace_bytes(nd, B, H, S, K, kbatch, periodic, dtype, direction);
-}
-
-int nsq_gated_fftconv_nd_fwd(int nd, const void* q, const void* kgate, const void* v, const float* k,
-                             const void* shortcut, void* y, void* y1, int dtype, int act1, int act2, int64_t B,
-                             int64_t H, const int64_t* S, const int64_t* K, int64_t kbatch, unsigned periodic,
-                             void* workspace, size_t workspace_bytes, void* stream) {
-  return gated_nd_fwd(nd, q, kgate, v, k, shortcut, y, y1, dtype, act1, act2, B, H, S, K, kbatch, periodic, workspace,
-                      workspace_bytes, stream);
-}
-
-int nsq_gated_fftconv_nd_bwd(int nd, const void* g, const void* q, const void* kgate, const void* v, const void* y1,
-                             const float* k, const void* shortcut, void* dq, void* dkgate, void* dv, float* gk,
-                             float* gs, int dtype, int act1, int act2, int64_t B, int64_t H, const int64_t* S,
-                             const int64_t* K, int64_t kbatch, unsigned periodic, void* workspace,
-                             size_t workspace_bytes, void* stream) {
-  return gated_nd_bwd(nd, g, q, kgate, v, y1, k, shortcut, dq, dkgate, dv, gk, gs, dtype, act1, act2, B, H, S, K,
-                      kbatch, periodic, workspace, workspace_bytes, stream);
-}
 
 size_t nsq_fftconv_nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K,
                                       int64_t kbatch, int direction) {

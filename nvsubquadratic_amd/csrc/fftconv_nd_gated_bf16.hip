@@ -1,0 +1,6 @@
+// bf16 instances of the 2D / 3D conv's host runs (Hyena-gated).
+#include "fftconv_nd_plan.h"
+
+namespace nsq {
+NSQ_ND_RUN_INSTANCES(, NSQ_DTYPE_BF16, true)
+}  // namespace nsq

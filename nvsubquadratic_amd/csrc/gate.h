@@ -13,16 +13,25 @@
 
 namespace nsq {
 
-__device__ __forceinline__ float gate_sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+// The gate arithmetic is not contracted into FMAs (`fp contract(off)`): each
+// product and sum rounds on its own, as the reference's separate elementwise ops
+// do, and identically in every kernel that inlines it (the fused loaders and
+// epilogues and the gate kernels give the same bits).
+__device__ __forceinline__ float gate_sigmoid(float x) {
+#pragma clang fp contract(off)
+  return 1.f / (1.f + __expf(-x));
+}
 
 // act(x) for act in {identity, sigmoid, silu}
 __device__ __forceinline__ float gate_act(int act, float x) {
+#pragma clang fp contract(off)
   const float s = gate_sigmoid(x);
   return act == NSQ_GATE_SIGMOID ? s : (act == NSQ_GATE_SILU ? x * s : x);
 }
 
 // d act / dx
 __device__ __forceinline__ float gate_dact(int act, float x) {
+#pragma clang fp contract(off)
   const float s = gate_sigmoid(x);
   return act == NSQ_GATE_SIGMOID ? s * (1.f - s) : (act == NSQ_GATE_SILU ? s * (1.f + x * (1.f - s)) : 1.f);
 }
@@ -41,6 +50,7 @@ struct GateArgs {
 
 template <int DT>
 __device__ __forceinline__ float gate1(int act, float q, float k) {
+#pragma clang fp contract(off)
   return Elem<DT>::round(q * Elem<DT>::round(gate_act(act, k)));
 }
 
@@ -110,6 +120,7 @@ __device__ __forceinline__ void ew_store8(void* p, int64_t i, bool whole, int64_
 
 template <int DT, int OP>
 __global__ __launch_bounds__(256) void gate_ew_kernel(GateEw g, int64_t n) {
+#pragma clang fp contract(off)
   const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 8;
   if (i >= n) return;
   const bool whole = i + 8 <= n;  // base pointers are 16-byte aligned (checked by the host)

@@ -128,6 +128,7 @@ struct Elem<NSQ_DTYPE_F16> {
 // the product s*x and the sum are rounded separately here as well.
 template <int DT>
 __device__ __forceinline__ float epilogue(float conv, bool has_s, float s_rounded, float xv) {
+#pragma clang fp contract(off)  // s*x and the sum rounded apart in every kernel (fp32 rounding is the identity)
   const float y = Elem<DT>::round(conv);
   const float sx = Elem<DT>::round(s_rounded * xv);
   const float ys = Elem<DT>::round(y + sx);

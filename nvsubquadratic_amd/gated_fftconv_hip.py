@@ -1,4 +1,4 @@
-r"""Hyena-gated causal 1D FFT convolution on the HIP backend (build-plan row F2).
+r"""Hyena-gated FFT convolution (causal 1D, 2D / 3D) on the HIP backend (build-plan row F2).
 
 The reference computes a Hyena layer's gated long convolution as separate ops
 (``nvsubquadratic/modules/hyena_nd.py:546`` first gate, ``:558`` the CKConvND
@@ -14,7 +14,11 @@ to 16384: one kernel), or as elementwise HIP kernels around the multi-kernel
 conv (longer sequences).  The backward runs elementwise gate kernels around the
 plain conv adjoint by default; the one-kernel gated adjoint
 (``fuse_backward_gates=True``) measured slower on MI355X (a latency-bound kernel
-at one workgroup per CU gains five operand streams).  Gates: ``"identity"``, ``"sigmoid"``, ``"silu"`` or the
+at one workgroup per CU gains five operand streams).  2D / 3D: both directions
+run the gates inside the N-d conv's first and last passes (z, or dy1 and dv, as
+the first pass loads; gate 2, or dq and dk, in the last pass's epilogue) where
+the plan has packed 2D rows with the vector epilogue or 3D plane passes, else as
+gate kernels around the conv; both give the same bits.  Gates: ``"identity"``, ``"sigmoid"``, ``"silu"`` or the
 matching ``torch.nn`` modules; ``gate_nonlinear_2=None`` reuses the first gate,
 as ``Hyena.__init__`` does (``hyena_nd.py:274-278``).  Results follow the
 reference composition with each elementwise product rounded to the I/O dtype.
@@ -214,7 +218,8 @@ def hyena_gated_causal_fftconv1d_bhl(
 
 
 # ---------------------------------------------------------------------------
-# 2D / 3D: the gate kernels around the N-d conv (nsq_gated_fftconv_nd_*)
+# 2D / 3D (nsq_gated_fftconv_nd_*): the gates inside the N-d conv's first and last passes (packed 2D rows
+# with the vector epilogue, 3D plane passes), else the gate kernels around it
 # ---------------------------------------------------------------------------
 def _gated_nd_ws(q, k, kbatch, periodic, direction):
     lib = _lib.get_lib()

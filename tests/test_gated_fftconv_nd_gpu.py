@@ -1,11 +1,16 @@
 """GPU parity of the Hyena-gated 2D/3D FFT conv (``hyena_gated_fftconv{2,3}d_bhl``) against the CPU
 composition of the reference (``hyena_nd.py:546-570`` around CKConvND's N-d conv), restated in
 ``oracle/gated_ref.py``: forward and the gradients of q, k, v, the filter and the shortcut.
-Tolerances: 1e-4 rel-L2 for fp32, 2e-2 for bf16 I/O."""
+Tolerances: 1e-4 rel-L2 for fp32, 2e-2 for bf16 I/O.  Plans with the gates fused into the conv's first and
+last passes are also checked bitwise against the gate kernels composed around the plain conv
+(``NSQ_ND_GATES_FUSED=0``)."""
+
+import os
 
 import pytest
 import torch
 
+from nvsubquadratic_amd import _lib
 from nvsubquadratic_amd import gated_fftconv_hip as G
 from nvsubquadratic_amd import fftconv_hip as Z
 from oracle.gated_ref import gated_fftconv_nd_torch
@@ -119,3 +124,62 @@ def test_gated_2d_odd_numel_bf16_and_split_views():
     with torch.no_grad():
         y0 = G.hyena_gated_fftconv2d_bhl(q, kk, v, wg, sg, "silu", "sigmoid")
     assert torch.equal(y0, y)
+
+
+# Plans whose gates run inside the conv's passes: packed 2D rows with the vector epilogue (even crop offset
+# along the last axis, its length a multiple of 8) and 3D plane passes (F1 * F2/2 >= 4096).
+FUSED_CASES = [  # (S, K, periodic, gate, gate_2, dtype, kb, shortcut)
+    ((32, 32), (9, 9), None, "silu", None, torch.float32, 1, True),
+    ((32, 32), (9, 9), None, "sigmoid", "silu", torch.bfloat16, 1, True),
+    ((32, 16), (5, 9), (True, False), "identity", "sigmoid", torch.float16, 1, False),
+    ((24, 40), (7, 13), None, "silu", "identity", torch.bfloat16, 2, True),
+    ((8, 8), (3, 3), (False, True), "silu", "silu", torch.float32, 1, True),  # tiled period 8 on the last axis
+    ((8, 64, 64), (3, 9, 9), None, "silu", "sigmoid", torch.bfloat16, 1, True),
+    ((8, 64, 64), (3, 9, 8), (False, True, False), "sigmoid", None, torch.float32, 2, True),
+]
+
+
+def _gated_run(S, K, periodic, gate, gate_2, dtype, kb, shortcut, fused):
+    old = os.environ.get("NSQ_ND_GATES_FUSED")
+    os.environ["NSQ_ND_GATES_FUSED"] = "1" if fused else "0"
+    try:
+        torch.manual_seed(7)
+        B, H = 2, 4
+        leaves = [torch.randn(B, H, *S, device="cuda").to(dtype) for _ in range(3)]
+        leaves.append(torch.randn(kb, H, *K, device="cuda"))
+        if shortcut:
+            leaves.append(torch.randn(H, device="cuda").to(dtype))
+        leaves = [t.requires_grad_(True) for t in leaves]
+        y = G.hyena_gated_fftconv_nd_bhl(leaves[0], leaves[1], leaves[2], leaves[3],
+                                         leaves[4] if shortcut else None, gate, gate_2, periodic)
+        g = torch.randn(y.shape, device="cuda", generator=torch.Generator("cuda").manual_seed(3)).to(dtype)
+        y.backward(g)
+        with torch.no_grad():  # a forward that keeps no y1
+            y_ng = G.hyena_gated_fftconv_nd_bhl(*[t.detach() for t in leaves[:4]],
+                                                leaves[4].detach() if shortcut else None, gate, gate_2, periodic)
+        per = 0 if periodic is None else sum(1 << d for d, f in enumerate(periodic) if f)
+        ws = G._gated_nd_ws(leaves[0], torch.empty(kb * H, *K), kb, per, _lib.NSQ_DIR_BWD)
+        torch.cuda.synchronize()
+        return [y, y_ng] + [t.grad for t in leaves], ws
+    finally:
+        if old is None:
+            del os.environ["NSQ_ND_GATES_FUSED"]
+        else:
+            os.environ["NSQ_ND_GATES_FUSED"] = old
+
+
+@pytest.mark.parametrize("case", FUSED_CASES)
+def test_gates_fused_into_passes_equal_gate_kernels(case):
+    """The fused loaders and epilogues round as the gate kernels do, so every output is bitwise equal; the fused
+    plan also needs only the conv's workspace (checks that the fused path is the one that ran)."""
+    print(f"gated fused vs composed {case}", flush=True)
+    fused, ws_f = _gated_run(*case, fused=True)
+    comp, ws_c = _gated_run(*case, fused=False)
+    assert ws_f < ws_c
+    for a, b in zip(fused, comp):
+        assert torch.equal(a, b)
+
+
+def test_gated_3d_plane_fused_against_oracle():
+    _check((8, 64, 64), (3, 9, 9), None, "silu", "sigmoid", H=3, B=2)
+    _check((8, 64, 64), (3, 9, 9), None, "sigmoid", None, dtype=torch.bfloat16, H=3, B=2, tol=2e-2)
