@@ -85,7 +85,7 @@ static int gated_nd_fwd(int nd, const void* q, const void* kgate, const void* v,
   if (gated_fused_ok(p)) {
     const float2* tw = twiddle_table();
     if (!tw) return NSQ_ERR_HIP;
-    const NdGateIO gi{q, kgate, v, nullptr, y1, nullptr, nullptr, act1, act2};
+    const GatedIO gi{q, kgate, v, nullptr, y1, nullptr, nullptr, act1, act2};
     float2* ws = (float2*)workspace;
     bool ok;
     switch (dtype) {
@@ -131,7 +131,7 @@ static int gated_nd_bwd(int nd, const void* g, const void* q, const void* kgate,
   if (gated_fused_ok(p)) {
     const float2* tw = twiddle_table();
     if (!tw) return NSQ_ERR_HIP;
-    const NdGateIO gi{q, kgate, v, y1, nullptr, dv, dkgate, act1, act2};
+    const GatedIO gi{q, kgate, v, y1, nullptr, dv, dkgate, act1, act2};
     float2* ws = (float2*)workspace;
     bool ok;
     switch (dtype) {

@@ -35,73 +35,26 @@
 namespace nsq {
 
 // ---------------------------------------------------------------------------
-// Hyena gates inside the first and last passes (the gated ops of
-// fftconv_nd_gated.hip): z = q act1(kg) formed as the forward's first pass
-// loads, out = y1 act2(v) in its epilogue; in the backward dy1 = g act2(v)
-// formed as the g-side first pass loads, and dq, dkg, dv in the gx epilogue
-// (16-byte operand windows there, where dv's scattered stores from the loader
-// cost more than its extra y1 window).  Roundings as gate_ew_kernel's
-// (gate.h), so the results equal the gate kernels composed around the plain
-// conv.
+// Hyena gates inside the first and last passes (GATED_* of gate.h; the gated
+// ops of fftconv_nd_gated.hip): z = q act1(kg), or dy1 = g act2(v), formed as
+// the first pass loads its sample pairs; gate 2, or dq, dkg, dv, in the last
+// pass's epilogue (16-byte operand windows there: dv's scattered stores from
+// the loader cost more than its extra y1 window).
 // ---------------------------------------------------------------------------
-enum { ND_GATE_NONE = 0, ND_GATE_FWD = 1, ND_GATE_BWD = 2 };
-
-struct NdGateIO {
-  const void* q;   // gate-1 operand (the forward's x; the backward's x-side and dq, dkg)
-  const void* kg;  // gate-1 input
-  const void* v;   // gate-2 input
-  const void* y1;  // backward: the conv output before gate 2 (for dv)
-  void* y1out;     // forward: y1 kept for the backward (may be null)
-  void* dv;        // backward: written by the gx epilogue
-  void* dkg;       // backward: written by the gx epilogue
-  int act1, act2;
-};
-
 // Sample pair (i, i + 1) of the row at element offset roff of the first pass's
-// source: GL = NONE src itself, FWD z = gate1(q = src, kg), BWD dy1 = g act2(v)
-// with g = src.  Samples at or past `valid` read zero, and every gate maps zero
-// to zero.
+// source (src, then q or g; the second operand kg or v from gi).  Samples at
+// or past `valid` read zero, and every gate maps zero to zero.
 template <int DT, bool AL, int GL>
-__device__ __forceinline__ float2 gated_pair(const typename Elem<DT>::T* __restrict__ src, const NdGateIO& gi,
+__device__ __forceinline__ float2 gated_pair(const typename Elem<DT>::T* __restrict__ src, const GatedIO& gi,
                                              int64_t roff, int64_t i, int64_t valid) {
-#pragma clang fp contract(off)
   using ET = typename Elem<DT>::T;
   const float2 a = load_pair_nb<DT, AL>(src + roff, i, valid);
-  if constexpr (GL == ND_GATE_NONE) {
+  if constexpr (GL == GATED_NONE) {
     return a;
-  } else if constexpr (GL == ND_GATE_FWD) {
-    const float2 k = load_pair_nb<DT, AL>((const ET*)gi.kg + roff, i, valid);
-    return make_float2(gate1<DT>(gi.act1, a.x, k.x), gate1<DT>(gi.act1, a.y, k.y));
   } else {
-    const float2 v = load_pair_nb<DT, AL>((const ET*)gi.v + roff, i, valid);
-    return make_float2(Elem<DT>::round(a.x * Elem<DT>::round(gate_act(gi.act2, v.x))),
-                       Elem<DT>::round(a.y * Elem<DT>::round(gate_act(gi.act2, v.y))));
-  }
-}
-
-// Epilogue of one output sample of a gated last pass.  `conv` is the scaled
-// transform value, `a` / `b` the operands of the first gate formed here (FWD:
-// q, kg -> z, the shortcut term's input; BWD: g, v -> dy1 and dv), `c` / `d` /
-// `e` the others (FWD: v; BWD: q, kg, y1).  Returns the stored output (FWD: out;
-// BWD: dq) and sets o2 (FWD: y1; BWD: dkg) and o3 (BWD: dv).
-template <int DT, int GE>
-__device__ __forceinline__ float gated_epilogue(float conv, bool has_s, float sv, float a, float b, float c, float d,
-                                                float e, const NdGateIO& gi, float& o2, float& o3) {
-#pragma clang fp contract(off)
-  o3 = 0.f;
-  if constexpr (GE == ND_GATE_NONE) {
-    o2 = 0.f;
-    return epilogue<DT>(conv, has_s, sv, a);
-  } else if constexpr (GE == ND_GATE_FWD) {
-    const float y1 = epilogue<DT>(conv, has_s, sv, gate1<DT>(gi.act1, a, b));
-    o2 = y1;
-    return y1 * Elem<DT>::round(gate_act(gi.act2, c));
-  } else {
-    const float dy1 = Elem<DT>::round(a * Elem<DT>::round(gate_act(gi.act2, b)));
-    o3 = Elem<DT>::round(a * e) * gate_dact(gi.act2, b);
-    const float dz = epilogue<DT>(conv, has_s, sv, dy1);
-    o2 = Elem<DT>::round(dz * c) * gate_dact(gi.act1, d);
-    return dz * Elem<DT>::round(gate_act(gi.act1, d));
+    const float2 b = load_pair_nb<DT, AL>((const ET*)(GL == GATED_FWD ? gi.kg : gi.v) + roff, i, valid);
+    return make_float2(gated_input<DT, GL>(gi.act1, gi.act2, a.x, b.x),
+                       gated_input<DT, GL>(gi.act1, gi.act2, a.y, b.y));
   }
 }
 
@@ -152,11 +105,11 @@ struct RowGeom {
 // for a periodic row of a power-of-two length len < F2 read as its periodic
 // extension (sample i of the transform is row[i & wm]).
 // GL: gate formed as the pairs are loaded (gated_pair; src is then q or g).
-template <int LOGN, int DT, bool AL, bool HALF = false, bool PACK = false, int GL = ND_GATE_NONE>
+template <int LOGN, int DT, bool AL, bool HALF = false, bool PACK = false, int GL = GATED_NONE>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_fwd_kernel(const typename Elem<DT>::T* __restrict__ src,
                                                                         int len, int wm, RowGeom rg,
                                                                         float2* __restrict__ ws,
-                                                                        const float2* __restrict__ tw, NdGateIO gi) {
+                                                                        const float2* __restrict__ tw, GatedIO gi) {
   using C = RowNdCfg<LOGN>;
   __shared__ float2 lds[C::M * C::SP];
   __shared__ int64_t rowoff[C::M];  // spectrum row of each tile row (one index decomposition per row)
@@ -214,7 +167,7 @@ struct RowInvOut {
   int off2, w2;        // last-axis window [off2, off2 + w2)
   int ga0, ga1, ga2;   // lag whose value is the shortcut gradient (ND_OUT_GK)
   float scale;         // 1 / (F0 * F1 * F2/2)
-  NdGateIO gio;        // gated epilogues (GE != ND_GATE_NONE; aux is then q or g)
+  GatedIO gio;        // gated epilogues (GE != GATED_NONE; aux is then q or g)
 };
 
 // HAS_S: a shortcut is given (ND_OUT_Y); its term reads aux.  Loads are
@@ -222,9 +175,9 @@ struct RowInvOut {
 // are predicated.  FAST (ND_OUT_Y; even off2, w2 a multiple of 8, out and aux
 // 16-byte aligned): the epilogue moves 8 consecutive kept samples per thread,
 // four complex values from LDS, one 16-byte aux load and one 16-byte store.
-// GE (FAST only): gated epilogue (gated_epilogue; o.aux is q or g, the other
+// GE (FAST only): gated epilogue (gated_output; o.aux is q or g, the other
 // operands and the second output in o.gio, all with the layout of `out`).
-template <int LOGN, int DT, int MODE, bool HAS_S, bool FAST = false, bool PACK = false, int GE = ND_GATE_NONE>
+template <int LOGN, int DT, int MODE, bool HAS_S, bool FAST = false, bool PACK = false, int GE = GATED_NONE>
 __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const float2* __restrict__ ws, RowGeom rg,
                                                                         RowInvOut o, const float2* __restrict__ tw) {
   using C = RowNdCfg<LOGN>;
@@ -282,24 +235,24 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
   const int nvalid = nrows * o.w2;  // the tile's outputs are e in [0, nvalid), row-major
   const int64_t tbase = r0 * o.w2;   // 32-bit offsets from here (M * w2 is small)
   const ET* aux_t = aux + (HAS_S ? tbase : 0);
-  static_assert(GE == ND_GATE_NONE || (FAST && MODE == ND_OUT_Y), "nd_row_inv_kernel: gates need the FAST epilogue");
+  static_assert(GE == GATED_NONE || (FAST && MODE == ND_OUT_Y), "nd_row_inv_kernel: gates need the FAST epilogue");
   if constexpr (FAST) {
     static_assert(MODE == ND_OUT_Y, "nd_row_inv_kernel: FAST epilogue writes y");
     const int cpr = o.w2 >> 3;  // 8-sample chunks per row
     // operands of the gate formed here (a: aux, q or g; b: kg or v), the others (c: v or q; d: kg; e: y1); the
     // forward reads a and b only for the shortcut term, the backward always (dv)
-    constexpr bool BWD = GE == ND_GATE_BWD;
+    constexpr bool BWD = GE == GATED_BWD;
     const bool need_ab = HAS_S || BWD;
     const ET* a_t = aux + tbase;
-    const ET* gb = (const ET*)(GE == ND_GATE_FWD ? o.gio.kg : o.gio.v);
-    const ET* gc = (const ET*)(GE == ND_GATE_FWD ? o.gio.v : o.gio.q);
+    const ET* gb = (const ET*)(GE == GATED_FWD ? o.gio.kg : o.gio.v);
+    const ET* gc = (const ET*)(GE == GATED_FWD ? o.gio.v : o.gio.q);
     const RowBuf<DT, false> ab(need_ab ? a_t : aux_t, need_ab ? nvalid : 0);
-    const RowBuf<DT, false> bb(GE != ND_GATE_NONE && need_ab ? gb + tbase : aux_t,
-                               GE != ND_GATE_NONE && need_ab ? nvalid : 0);
-    const RowBuf<DT, false> cb(GE != ND_GATE_NONE ? gc + tbase : aux_t, GE != ND_GATE_NONE ? nvalid : 0);
+    const RowBuf<DT, false> bb(GE != GATED_NONE && need_ab ? gb + tbase : aux_t,
+                               GE != GATED_NONE && need_ab ? nvalid : 0);
+    const RowBuf<DT, false> cb(GE != GATED_NONE ? gc + tbase : aux_t, GE != GATED_NONE ? nvalid : 0);
     const RowBuf<DT, false> db(BWD ? (const ET*)o.gio.kg + tbase : aux_t, BWD ? nvalid : 0);
     const RowBuf<DT, false> eb(BWD ? (const ET*)o.gio.y1 + tbase : aux_t, BWD ? nvalid : 0);
-    void* out2 = GE == ND_GATE_FWD ? o.gio.y1out : o.gio.dkg;
+    void* out2 = GE == GATED_FWD ? o.gio.y1out : o.gio.dkg;
     const RowBuf<DT, true> ob((ET*)o.out + tbase, nvalid);
     const RowBuf<DT, true> ob2(out2 ? (ET*)out2 + tbase : (ET*)o.out + tbase, out2 ? nvalid : 0);
     const RowBuf<DT, true> ob3(BWD ? (ET*)o.gio.dv + tbase : (ET*)o.out + tbase, BWD ? nvalid : 0);
@@ -309,7 +262,7 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
       const int e0 = ok ? m * o.w2 + c8 : nvalid;  // past the range: the aux load reads 0, the store is dropped
       Win8<DT, true> a, b, c, d, ew;
       a.load(ab, e0);
-      if constexpr (GE != ND_GATE_NONE) {
+      if constexpr (GE != GATED_NONE) {
         b.load(bb, e0);
         c.load(cb, e0);
       }
@@ -327,16 +280,17 @@ __global__ __launch_bounds__(RowNdCfg<LOGN>::T) void nd_row_inv_kernel(const flo
         for (int h = 0; h < 2; ++h) {
           const int i = 2 * u + h;
           const float cv = (h ? z.y : z.x) * o.scale;
-          if constexpr (GE == ND_GATE_NONE) {
+          if constexpr (GE == GATED_NONE) {
             y[i] = epilogue<DT>(cv, HAS_S, HAS_S ? svs[m] : 0.f, a.at(i));
           } else {
-            y[i] = gated_epilogue<DT, GE>(cv, HAS_S, HAS_S ? svs[m] : 0.f, a.at(i), b.at(i), c.at(i),
-                                          BWD ? d.at(i) : 0.f, BWD ? ew.at(i) : 0.f, o.gio, y2[i], y3[i]);
+            y[i] = gated_output<DT, GE>(cv, HAS_S, HAS_S ? svs[m] : 0.f, a.at(i), b.at(i), c.at(i),
+                                        BWD ? d.at(i) : 0.f, BWD ? ew.at(i) : 0.f, o.gio.act1, o.gio.act2, y2[i],
+                                        y3[i]);
           }
         }
       }
       store8<DT, true>(ob, e0, y);
-      if constexpr (GE != ND_GATE_NONE) {
+      if constexpr (GE != GATED_NONE) {
         if (out2) store8<DT, true>(ob2, e0, y2);
       }
       if constexpr (BWD) store8<DT, true>(ob3, e0, y3);
@@ -414,10 +368,10 @@ struct PlaneCfg {
 // HALF: len <= N and n1 <= F1/2 (each row and each column at least half zero
 // padding): both first passes fold the zero half (HalfZeroLoad).  GL: gate
 // formed as the pairs are loaded (gated_pair; src is then q or g).
-template <int LOGN, int LOGF1, int DT, bool AL, bool HALF = false, int GL = ND_GATE_NONE>
+template <int LOGN, int LOGF1, int DT, bool AL, bool HALF = false, int GL = GATED_NONE>
 __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<DT>::T* __restrict__ src, int n0,
                                                            int n1, int len, int wm1, int wm2, float2* __restrict__ ws,
-                                                           int64_t spec, const float2* __restrict__ tw, NdGateIO gi) {
+                                                           int64_t spec, const float2* __restrict__ tw, GatedIO gi) {
   using C = PlaneCfg<LOGN, LOGF1>;
   static_assert(C::OK, "nd_plane_fwd_kernel: plane does not fit");
   constexpr int N = C::N, RS = C::RS;
@@ -480,9 +434,9 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
 // Inverse: plane [F1][FH] of the spectrum (after the axis-0 pass) -> inverse
 // along axis 1, rows [off1, off1 + n1out) -> inverse real transforms along
 // axis 2, crop and epilogue (RowInvOut; output rows [plane][n1out][w2]).
-// GE: gated epilogue (gated_epilogue; o.aux is q or g, the other operands and
+// GE: gated epilogue (gated_output; o.aux is q or g, the other operands and
 // the second output in o.gio).
-template <int LOGN, int LOGF1, int DT, int MODE, bool HAS_S, int GE = ND_GATE_NONE>
+template <int LOGN, int LOGF1, int DT, int MODE, bool HAS_S, int GE = GATED_NONE>
 __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restrict__ ws, int64_t spec, int n0,
                                                            int off1, int n1out, RowInvOut o,
                                                            const float2* __restrict__ tw) {
@@ -549,13 +503,13 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
     fft_rec<LOGN, 0, true, C::MR, C::T, false>(rows, rows, rows, rows, tw);
     // Epilogue over the tile's real samples: MR rows x w2 kept samples.
     const int nrows = (n1out - r0) < C::MR ? (n1out - r0) : C::MR;
-    static_assert(GE == ND_GATE_NONE || MODE == ND_OUT_Y, "nd_plane_inv_kernel: gates on y only");
-    constexpr bool BWD = GE == ND_GATE_BWD;
-    const ET* __restrict__ gb = (const ET*)(GE == ND_GATE_FWD ? o.gio.kg : o.gio.v);
-    const ET* __restrict__ gc = (const ET*)(GE == ND_GATE_FWD ? o.gio.v : o.gio.q);
+    static_assert(GE == GATED_NONE || MODE == ND_OUT_Y, "nd_plane_inv_kernel: gates on y only");
+    constexpr bool BWD = GE == GATED_BWD;
+    const ET* __restrict__ gb = (const ET*)(GE == GATED_FWD ? o.gio.kg : o.gio.v);
+    const ET* __restrict__ gc = (const ET*)(GE == GATED_FWD ? o.gio.v : o.gio.q);
     const ET* __restrict__ gd = (const ET*)o.gio.kg;
     const ET* __restrict__ ge = (const ET*)o.gio.y1;
-    ET* out2 = (ET*)(GE == ND_GATE_FWD ? o.gio.y1out : o.gio.dkg);
+    ET* out2 = (ET*)(GE == GATED_FWD ? o.gio.y1out : o.gio.dkg);
     for (int eb = 0; eb < C::MR * o.w2; eb += 8 * C::T) {
       float a[8], v[8], b[8], c2[8], d[8], e2[8];
       int64_t idx[8];
@@ -572,7 +526,7 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
         const int64_t li = ok[u] ? idx[u] : 0;
         a[u] = b[u] = c2[u] = d[u] = e2[u] = 0.f;
         if constexpr (HAS_S || BWD) a[u] = Elem<DT>::load(aux, li);
-        if constexpr (GE != ND_GATE_NONE) {
+        if constexpr (GE != GATED_NONE) {
           if constexpr (HAS_S || BWD) b[u] = Elem<DT>::load(gb, li);
           c2[u] = Elem<DT>::load(gc, li);
         }
@@ -585,12 +539,13 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
       for (int u = 0; u < 8; ++u) {
         if (!ok[u]) continue;
         if constexpr (MODE == ND_OUT_Y) {
-          if constexpr (GE == ND_GATE_NONE) {
+          if constexpr (GE == GATED_NONE) {
             Elem<DT>::store((ET*)o.out, idx[u], epilogue<DT>(v[u], HAS_S, sv, a[u]));
           } else {
             float y2, y3;
             Elem<DT>::store((ET*)o.out, idx[u],
-                            gated_epilogue<DT, GE>(v[u], HAS_S, sv, a[u], b[u], c2[u], d[u], e2[u], o.gio, y2, y3));
+                            gated_output<DT, GE>(v[u], HAS_S, sv, a[u], b[u], c2[u], d[u], e2[u], o.gio.act1,
+                                                 o.gio.act2, y2, y3));
             if (out2) Elem<DT>::store(out2, idx[u], y2);
             if constexpr (BWD) Elem<DT>::store((ET*)o.gio.dv, idx[u], y3);
           }

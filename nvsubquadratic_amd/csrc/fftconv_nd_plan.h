@@ -122,11 +122,11 @@ bool with_log(int v, F&& f) {
 }
 
 // wrap: x / g (read through the plan's periodic extension masks); the filter
-// is never extended.  GL: gate formed by the loads (ND_GATE_*, packed 2D rows
+// is never extended.  GL: gate formed by the loads (GATED_*, packed 2D rows
 // only; gi holds its operands).
-template <int DT, int GL = ND_GATE_NONE>
+template <int DT, int GL = GATED_NONE>
 bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, bool wrap, float2* ws,
-             const float2* tw, hipStream_t st, const NdGateIO& gi = NdGateIO{}) {
+             const float2* tw, hipStream_t st, const GatedIO& gi = GatedIO{}) {
   RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.RS};
   const int wm = wrap ? p.wm[2] : -1;
   return with_log<3, kNdMaxLogF - 1>(p.lF[2] - 1, [&](auto L) {
@@ -139,7 +139,7 @@ bool row_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int 
       if (p.pack)
         hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, A, H, true, GL>), grid, dim3(C::T), 0, st, (const ET*)src,
                            len, wm, rg, ws, tw, gi);
-      else if constexpr (GL == ND_GATE_NONE)  // gated_fused_ok: gates only on packed rows
+      else if constexpr (GL == GATED_NONE)  // gated_fused_ok: gates only on packed rows
         hipLaunchKernelGGL((nd_row_fwd_kernel<LOGN, DT, A, H, false>), grid, dim3(C::T), 0, st, (const ET*)src, len,
                            wm, rg, ws, tw, gi);
     };
@@ -160,8 +160,8 @@ inline bool row_inv_fast(const RowInvOut& o) {
          (reinterpret_cast<uintptr_t>(o.aux) & 15) == 0;
 }
 
-// GE: gated epilogue (ND_GATE_*; packed rows with row_inv_fast(o) only).
-template <int DT, int MODE, int GE = ND_GATE_NONE>
+// GE: gated epilogue (GATED_*; packed rows with row_inv_fast(o) only).
+template <int DT, int MODE, int GE = GATED_NONE>
 bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int n1, RowInvOut o, const float2* tw,
              hipStream_t st) {
   RowGeom rg{nbh * n0 * n1, n0, n1, p.spec, p.F[1], p.RS};
@@ -178,7 +178,7 @@ bool row_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int n1, Row
     using T_ = std::true_type;
     using F_ = std::false_type;
     auto go_pack = [&](auto has_s, auto fst) { p.pack ? go(has_s, fst, T_{}) : go(has_s, fst, F_{}); };
-    if constexpr (MODE == ND_OUT_Y && GE != ND_GATE_NONE) {
+    if constexpr (MODE == ND_OUT_Y && GE != GATED_NONE) {
       auto gated = [&](auto has_s) {  // gated_fused_ok: packed rows, fast epilogue
         hipLaunchKernelGGL((nd_row_inv_kernel<LOGN, DT, MODE, decltype(has_s)::value, true, true, GE>), grid,
                            dim3(C::T), 0, st, ws, rg, o, tw);
@@ -295,11 +295,11 @@ bool with_plane(const NdPlan& p, F&& f) {
 
 // Forward inner-axis transforms of nbh blocks of [n0][n1][len] real rows
 // (wrap: x / g, read through the periodic extension masks).
-// GL: gate formed by the first pass's loads (ND_GATE_*; the packed 2D rows or
+// GL: gate formed by the first pass's loads (GATED_*; the packed 2D rows or
 // the 3D plane pass only, see gated_fused_ok).
-template <int DT, int GL = ND_GATE_NONE>
+template <int DT, int GL = GATED_NONE>
 bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, bool wrap, float2* ws,
-               const float2* tw, hipStream_t st, const NdGateIO& gi = NdGateIO{}) {
+               const float2* tw, hipStream_t st, const GatedIO& gi = GatedIO{}) {
   const int wm1 = wrap ? p.wm[1] : -1, wm2 = wrap ? p.wm[2] : -1;
   if (plane_ok(p)) {
     using ET = typename Elem<DT>::T;
@@ -326,9 +326,9 @@ bool inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, in
 
 // Inverse inner-axis transforms, crop (axis 1: [off1, off1 + n1out); axis 2:
 // RowInvOut) and epilogue, for nbh blocks whose axis-0 extent is n0.
-// GE: gated epilogue (ND_GATE_*; the packed 2D rows with the vector epilogue
+// GE: gated epilogue (GATED_*; the packed 2D rows with the vector epilogue
 // or the 3D plane pass only, see gated_fused_ok).
-template <int DT, int MODE, int GE = ND_GATE_NONE>
+template <int DT, int MODE, int GE = GATED_NONE>
 bool inner_inv(const NdPlan& p, float2* ws, int64_t nbh, int n0, int off1, int n1out, RowInvOut o,
                const float2* tw, hipStream_t st) {
   if (plane_ok(p)) {
@@ -367,14 +367,14 @@ inline bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const 
 // *gate (x is then q; gated_nd_fwd).
 template <int DT, bool GATED = false>
 bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws, bool save,
-                const float2* tw, hipStream_t st, const NdGateIO* gate = nullptr) {
-  constexpr int GM = GATED ? ND_GATE_FWD : ND_GATE_NONE;
+                const float2* tw, hipStream_t st, const GatedIO* gate = nullptr) {
+  constexpr int GM = GATED ? GATED_FWD : GATED_NONE;
   const int64_t BH = p.B * p.H;
   float2* wsx = save ? ws + BH * p.spec : ws;
   float2* wsk = wsx + BH * p.spec;
   float2* wsy = save ? ws : wsx;
   if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-  const NdGateIO gi = GATED ? *gate : NdGateIO{};
+  const GatedIO gi = GATED ? *gate : GatedIO{};
   if (!inner_fwd<DT, GM>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st, gi)) return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rf{p.r[0], p.r[1], p.r[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
@@ -415,19 +415,19 @@ bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, v
 // gated_nd_bwd).
 template <int DT, bool GATED = false>
 bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
-                float* gs, float2* ws, bool fwd_state, const float2* tw, hipStream_t st, const NdGateIO* gate = nullptr) {
+                float* gs, float2* ws, bool fwd_state, const float2* tw, hipStream_t st, const GatedIO* gate = nullptr) {
   const int64_t BH = p.B * p.H, NK = p.kb * p.H;
   float2* wsg = ws;
   float2* wsx = wsg + BH * p.spec;
   float2* wsk = wsx + BH * p.spec;
   float2* wsq = wsk + NK * p.spec;
-  const NdGateIO gi = GATED ? *gate : NdGateIO{};
+  const GatedIO gi = GATED ? *gate : GatedIO{};
   if (!fwd_state) {
     if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-    if (!inner_fwd<DT, GATED ? ND_GATE_FWD : ND_GATE_NONE>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st, gi))
+    if (!inner_fwd<DT, GATED ? GATED_FWD : GATED_NONE>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st, gi))
       return false;
   }
-  if (!inner_fwd<DT, GATED ? ND_GATE_BWD : ND_GATE_NONE>(p, g, BH, p.S[0], p.S[1], p.S[2], true, wsg, tw, st, gi))
+  if (!inner_fwd<DT, GATED ? GATED_BWD : GATED_NONE>(p, g, BH, p.S[0], p.S[1], p.S[2], true, wsg, tw, st, gi))
     return false;
   const ColGeom cg = axis0_geom(p);
   const Ramp rp{p.c[0], p.c[1], p.c[2], p.lF[0], p.lF[1], p.lF[2], p.FH};
@@ -459,7 +459,7 @@ bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const float* k, c
   }
   const float scale = 1.f / (float(p.F[0]) * float(p.F[1]) * float(p.F[2] / 2));
   RowInvOut og{gx, g, s, nullptr, int(p.H), 0, p.S[2], 0, 0, 0, scale, gi};
-  if (!inner_inv<DT, ND_OUT_Y, GATED ? ND_GATE_BWD : ND_GATE_NONE>(p, wsg, BH, p.S[0], 0, p.S[1], og, tw, st))
+  if (!inner_inv<DT, ND_OUT_Y, GATED ? GATED_BWD : GATED_NONE>(p, wsg, BH, p.S[0], 0, p.S[1], og, tw, st))
     return false;
   RowInvOut ok_{gk, nullptr, nullptr, gs, int(p.H), 0, p.K[2], p.c[0], p.c[1], p.c[2], scale * p.gk_scale};
   return inner_inv<NSQ_DTYPE_F32, ND_OUT_GK>(p, wsq, NK, p.K[0], 0, p.K[1], ok_, tw, st);
@@ -523,10 +523,10 @@ inline size_t nd_workspace_bytes(int nd, int64_t B, int64_t H, const int64_t* S,
 // kernel instantiations build in parallel.
 #define NSQ_ND_RUN_INSTANCES(EXT, DT, GATED)                                                                       \
   EXT template bool run_nd_fwd<DT, GATED>(const NdPlan&, const void*, const float*, const void*, void*, float2*,    \
-                                          bool, const float2*, hipStream_t, const NdGateIO*);                      \
+                                          bool, const float2*, hipStream_t, const GatedIO*);                      \
   EXT template bool run_nd_bwd<DT, GATED>(const NdPlan&, const void*, const void*, const float*, const void*,      \
                                           void*, float*, float*, float2*, bool, const float2*, hipStream_t,        \
-                                          const NdGateIO*);
+                                          const GatedIO*);
 NSQ_ND_RUN_INSTANCES(extern, NSQ_DTYPE_F32, false)
 NSQ_ND_RUN_INSTANCES(extern, NSQ_DTYPE_BF16, false)
 NSQ_ND_RUN_INSTANCES(extern, NSQ_DTYPE_F16, false)

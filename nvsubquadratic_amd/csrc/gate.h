@@ -54,6 +54,65 @@ __device__ __forceinline__ float gate1(int act, float q, float k) {
   return Elem<DT>::round(q * Elem<DT>::round(gate_act(act, k)));
 }
 
+// Gates formed inside a conv pass (the N-d passes of fftconv_nd_impl.h, the
+// 4-step column passes of fftconv1d_impl.h): GATED_FWD forms z = q act1(kg)
+// as the first pass loads and applies gate 2 in the last epilogue; GATED_BWD
+// forms dy1 = g act2(v) as the g-side first pass loads and dq, dkg, dv in the
+// gx epilogue.  Roundings as gate_ew_kernel's, so the results equal the gate
+// kernels composed around the plain conv.
+enum { GATED_NONE = 0, GATED_FWD = 1, GATED_BWD = 2 };
+
+// Operands of a gated pass beyond the conv's own (every tensor with the I/O
+// layout of the conv's x).
+struct GatedIO {
+  const void* q;   // gate-1 operand (the forward's x; the backward's x-side and dq, dkg)
+  const void* kg;  // gate-1 input
+  const void* v;   // gate-2 input
+  const void* y1;  // backward: the conv output before gate 2 (for dv)
+  void* y1out;     // forward: y1 kept for the backward (may be null)
+  void* dv;        // backward: written by the gx epilogue
+  void* dkg;       // backward: written by the gx epilogue
+  int act1, act2;
+};
+
+// The first pass's input from its two loaded operands (FWD: q, kg; BWD: g, v).
+template <int DT, int GL>
+__device__ __forceinline__ float gated_input(int act1, int act2, float a, float b) {
+#pragma clang fp contract(off)
+  if constexpr (GL == GATED_FWD)
+    return gate1<DT>(act1, a, b);
+  else if constexpr (GL == GATED_BWD)
+    return Elem<DT>::round(a * Elem<DT>::round(gate_act(act2, b)));
+  else
+    return a;
+}
+
+// One output sample of a gated last pass.  `conv` is the scaled transform
+// value, `a` / `b` the operands of the gate formed here (FWD: q, kg -> z, the
+// shortcut term's input; BWD: g, v -> dy1 and dv), `c` / `d` / `e` the others
+// (FWD: v; BWD: q, kg, y1).  Returns the stored output (FWD: out; BWD: dq) and
+// sets o2 (FWD: y1; BWD: dkg) and o3 (BWD: dv).
+template <int DT, int GE>
+__device__ __forceinline__ float gated_output(float conv, bool has_s, float sv, float a, float b, float c, float d,
+                                              float e, int act1, int act2, float& o2, float& o3) {
+#pragma clang fp contract(off)
+  o3 = 0.f;
+  if constexpr (GE == GATED_FWD) {
+    const float y1 = epilogue<DT>(conv, has_s, sv, gate1<DT>(act1, a, b));
+    o2 = y1;
+    return y1 * Elem<DT>::round(gate_act(act2, c));
+  } else if constexpr (GE == GATED_BWD) {
+    const float dy1 = Elem<DT>::round(a * Elem<DT>::round(gate_act(act2, b)));
+    o3 = Elem<DT>::round(a * e) * gate_dact(act2, b);
+    const float dz = epilogue<DT>(conv, has_s, sv, dy1);
+    o2 = Elem<DT>::round(dz * c) * gate_dact(act1, d);
+    return dz * Elem<DT>::round(gate_act(act1, d));
+  } else {
+    o2 = 0.f;
+    return epilogue<DT>(conv, has_s, sv, a);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Elementwise gate kernels (flat over B*H*L; 8 elements per thread, one 16- or
 // 32-byte vector access per operand when the run of 8 is whole, else scalar).
