@@ -372,6 +372,14 @@ int nsq_mixed_fftconv_nd_bwd(int nd, const void* g, const void* x, const float* 
 int nsq_siren_mlp_fwd(const float* grid, int64_t G, int d, const float* w0, const float* b0, int E, const float* wh,
                       const float* bh, int nh, int HD, float* act, int64_t lda, void* stream);
 
+/* Readout of the same generator (kernels_nd.py:1189, SIRENKernelND's output
+ * linear): k[h][g] = b_out[h] + W_out[h] . a_nh[g] for W_out [H, HD], b_out [H]
+ * (may be null), act rows 0..HD-1 of nsq_siren_mlp_fwd's output (row stride
+ * lda), written as k [H][G] fp32: the filter in the layout the FFT convs read.
+ * HD in {16, 32, 64, 128}.  Its gradients are plain GEMMs on the caller's side. */
+int nsq_siren_readout_fwd(const float* wout, const float* bout, int64_t H, int HD, const float* act, int64_t lda,
+                          int64_t G, float* k, void* stream);
+
 size_t nsq_siren_mlp_bwd_workspace_bytes(int64_t G, int d, int E, int nh, int HD);
 
 int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_stride_g, const float* grid, int64_t G,

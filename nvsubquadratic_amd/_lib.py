@@ -153,6 +153,8 @@ _SIGNATURES = {
         [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p,
          _c_i64, _c_void_p],
     ),
+    "nsq_siren_readout_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p]),
     "nsq_siren_mlp_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "nsq_siren_mlp_bwd": (
         _c_int,

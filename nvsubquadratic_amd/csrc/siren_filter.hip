@@ -5,11 +5,12 @@
 //   a_0[g] = sin(W0 x_g + b0),  a_i[g] = sin(W_i a_{i-1}[g] + b_i) (i = 1..nh),
 //   k[h][g] = W_out[h] . a_nh[g] + b_out[h].
 // These kernels produce the last activation transposed, A_ext = [a_nh^T; 1]
-// ([HD + 1][G]), and the hidden weights' gradients from dA = W_out^T gk; the
-// readout k = [W_out | b_out] A_ext (one GEMM of K = HD + 1 that writes the
-// filter straight in the [H][G] layout the FFT convs read, bias folded in) and
-// its two gradient GEMMs are plain library GEMMs (hipBLASLt), which this
-// shape (M = H, N = G, K = 33) feeds at its own HBM roofline.
+// ([HD + 1][G]), the filter k = W_out a_nh + b_out straight in the [H][G]
+// layout the FFT convs read (siren_readout_fwd_kernel), and the hidden weights'
+// gradients from dA = W_out^T gk.  The readout's two gradient products are
+// plain library GEMMs (hipBLASLt; the ones row of A_ext gives b_out's), which
+// run this shape (K = H, and K = G split in 16 slices) at ~70% of the fp32
+// matrix rate.
 //
 // Design (MI355X):
 //  * A wave owns 16 grid points.  Every product is a v_mfma_f32_16x16x4_f32
@@ -422,6 +423,98 @@ struct SirenFwd {
   }
 };
 
+// Readout k[h][g] = b_out[h] + sum_j W_out[h][j] a[j][g] (j < HD, in order):
+// a lane owns V consecutive points and keeps their HD activations in
+// registers; a workgroup takes a block of ReadoutCfg::ROWS channels whose W_out
+// rows it stages in LDS (wave-uniform broadcast reads) and produces CH of them
+// at a time (CH x V independent FMA chains).  Each store is V consecutive
+// floats per lane, so a wave writes 64 V contiguous floats of one filter row.
+// The pass is bound by writing k (4 bytes per output: 0.63 ms for 4.3 GB on
+// MI355X) against HD fused multiply-adds per output on the VALU.
+template <int HD>
+struct ReadoutCfg {
+  static constexpr int V = HD <= 32 ? 4 : (HD == 64 ? 2 : 1);  // points per lane: V * HD activations in registers
+  static constexpr int CH = V == 4 ? 4 : 8;                      // channels per step
+  static constexpr int ROWS = (8192 / HD) < 256 ? (8192 / HD) : 256;  // channels per workgroup (32 KB of W_out)
+};
+
+// VEC: V-wide accesses (G a multiple of V, k and act 16-byte aligned, lda a
+// multiple of V); otherwise one point per lane.
+template <int HD, bool VEC>
+__global__ __launch_bounds__(256) void siren_readout_fwd_kernel(const float* __restrict__ wout,
+                                                                const float* __restrict__ bout,
+                                                                const float* __restrict__ act, int64_t lda,
+                                                                int64_t G, int64_t H, float* __restrict__ k) {
+  using C = ReadoutCfg<HD>;
+  constexpr int V = VEC ? C::V : 1;
+  constexpr int CH = C::CH, ROWS = C::ROWS;
+  __shared__ float ws[ROWS * HD];
+  __shared__ float bs[ROWS];
+  const int64_t g = (int64_t(blockIdx.x) * 256 + threadIdx.x) * V;
+  const bool gok = g < G;  // VEC: the V points are whole (G % V == 0)
+  const int64_t h0 = int64_t(blockIdx.y) * ROWS;
+  const int nrows = H - h0 < ROWS ? int(H - h0) : ROWS;
+  for (int i = threadIdx.x; i < ROWS * HD; i += 256) ws[i] = i < nrows * HD ? wout[h0 * HD + i] : 0.f;
+  for (int i = threadIdx.x; i < ROWS; i += 256) bs[i] = (bout && i < nrows) ? bout[h0 + i] : 0.f;
+  float a[HD][V];
+  const float* ap = act + (gok ? g : 0);
+#pragma unroll
+  for (int j = 0; j < HD; ++j) {
+    if constexpr (V == 4) {
+      const float4 t = *reinterpret_cast<const float4*>(ap + int64_t(j) * lda);
+      a[j][0] = t.x; a[j][1] = t.y; a[j][2] = t.z; a[j][3] = t.w;
+    } else if constexpr (V == 2) {
+      const float2 t = *reinterpret_cast<const float2*>(ap + int64_t(j) * lda);
+      a[j][0] = t.x; a[j][1] = t.y;
+    } else {
+      a[j][0] = ap[int64_t(j) * lda];
+    }
+  }
+  __syncthreads();
+  for (int hh = 0; hh < nrows; hh += CH) {
+    float acc[CH][V];
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[c][v] = bs[hh + c < ROWS ? hh + c : 0];
+#pragma unroll
+    for (int j = 0; j < HD; ++j)
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const float wv = ws[(hh + c < ROWS ? hh + c : 0) * HD + j];
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[c][v] = __builtin_fmaf(wv, a[j][v], acc[c][v]);
+      }
+    if (gok) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        if (hh + c >= nrows) break;
+        float* o = k + (h0 + hh + c) * G + g;
+        if constexpr (V == 4)
+          *reinterpret_cast<float4*>(o) = make_float4(acc[c][0], acc[c][1], acc[c][2], acc[c][3]);
+        else if constexpr (V == 2)
+          *reinterpret_cast<float2*>(o) = make_float2(acc[c][0], acc[c][1]);
+        else
+          *o = acc[c][0];
+      }
+    }
+  }
+}
+
+template <int HD>
+static void launch_readout(const float* wout, const float* bout, const float* act, int64_t lda, int64_t G, int64_t H,
+                           float* k, hipStream_t st) {
+  using C = ReadoutCfg<HD>;
+  const bool vec = G % C::V == 0 && lda % C::V == 0 && (reinterpret_cast<uintptr_t>(k) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(act) & 15) == 0;
+  const int v = vec ? C::V : 1;
+  const dim3 grd(unsigned(ceil_div(G, int64_t(256) * v)), unsigned(ceil_div(H, int64_t(C::ROWS))));
+  if (vec)
+    hipLaunchKernelGGL((siren_readout_fwd_kernel<HD, true>), grd, dim3(256), 0, st, wout, bout, act, lda, G, H, k);
+  else
+    hipLaunchKernelGGL((siren_readout_fwd_kernel<HD, false>), grd, dim3(256), 0, st, wout, bout, act, lda, G, H, k);
+}
+
 constexpr int kSirenMaxLds = 160 * 1024;
 
 // LDS bytes per wave of the backward pass 1.
@@ -543,6 +636,29 @@ int nsq_siren_mlp_fwd(const float* grid, int64_t G, int d, const float* w0, cons
   NSQ_CHECK_ARG(act && lda >= G, "siren_mlp_fwd: null output or row stride %lld < G", (long long)lda);
   const SirenNet n{w0, b0, wh, bh, d, nh};
   siren_dispatch<SirenFwd>(E, HD, grid, G, n, act, lda, (hipStream_t)stream);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+int nsq_siren_readout_fwd(const float* wout, const float* bout, int64_t H, int HD, const float* act, int64_t lda,
+                          int64_t G, float* k, void* stream) {
+  using namespace nsq;
+  clear_error();
+  NSQ_CHECK_ARG(wout && act && k, "siren_readout_fwd: null pointer argument");
+  NSQ_CHECK_ARG(G >= 1 && G <= (int64_t(1) << 30) && lda >= G, "siren_readout_fwd: G=%lld, lda=%lld", (long long)G,
+                (long long)lda);
+  NSQ_CHECK_ARG(H >= 1 && H <= (int64_t(1) << 20), "siren_readout_fwd: H=%lld out of range", (long long)H);
+  NSQ_CHECK_ARG(ceil_div(H, int64_t(64)) <= 65535, "siren_readout_fwd: H=%lld too large", (long long)H);
+  hipStream_t st = (hipStream_t)stream;
+  switch (HD) {
+    case 16: launch_readout<16>(wout, bout, act, lda, G, H, k, st); break;
+    case 32: launch_readout<32>(wout, bout, act, lda, G, H, k, st); break;
+    case 64: launch_readout<64>(wout, bout, act, lda, G, H, k, st); break;
+    case 128: launch_readout<128>(wout, bout, act, lda, G, H, k, st); break;
+    default:
+      set_error("siren_readout_fwd: mlp_hidden_dim %d must be 16, 32, 64 or 128", HD);
+      return NSQ_ERR_UNSUPPORTED;
+  }
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
 }

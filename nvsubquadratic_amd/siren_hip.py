@@ -11,9 +11,9 @@ returned as ``[1, *grid, out_dim]``; ``CKConvND`` then crops it (causal: the sec
 
 How: ``nsq_siren_mlp_fwd`` evaluates the embedding and every hidden layer for 16 grid points per wave
 on the matrix cores and writes only ``[a_nh^T; 1]`` (``[HD + 1, G]``) -- no per-layer activation reaches
-HBM.  The readout is one GEMM, ``[W_out | b_out] @ [a_nh^T; 1]``, which writes the filter straight as
-``[out_dim, G]`` -- the layout the FFT convs read -- with the bias folded in, so neither the
-``[G, out_dim]`` result nor its transpose exists; ``forward`` hands the reference's
+HBM.  The readout (``nsq_siren_readout_fwd``: one point per lane, the W_out rows wave-uniform) writes the
+filter straight as ``[out_dim, G]`` -- the layout the FFT convs read -- so neither the ``[G, out_dim]``
+result nor its transpose exists; ``forward`` hands the reference's
 ``[1, *grid, out_dim]`` shape back as a view of it.  The readout's two gradient GEMMs come from
 autograd; the MLP backward (``nsq_siren_mlp_bwd``) recomputes the layers from the grid and reduces
 every hidden weight gradient over the points in a fixed order.  fp32 throughout, as the reference
@@ -88,11 +88,11 @@ def siren_filter_op(grid: torch.Tensor, w0: torch.Tensor, b0: Optional[torch.Ten
     ``nh`` hidden layers packed back to back in ``wh`` (biases in ``bh``) and the readout ``wout [H, HD]``,
     ``bout``.  ``act = [a_nh^T; 1]`` is the forward state the backward reads."""
     HD = wout.shape[1]
+    H, G = wout.shape[0], grid.shape[0]
     act = _mlp_fwd(grid, w0, b0, wh, bh, nh, HD)
-    if bout is None:
-        k = torch.mm(wout, act[:HD])
-    else:
-        k = torch.mm(torch.cat([wout, bout[:, None]], dim=1), act)  # bias as the (HD+1)-th column
+    k = torch.empty(H, G, dtype=torch.float32, device=grid.device)
+    _lib.check(_lib.get_lib().nsq_siren_readout_fwd(wout.data_ptr(), _opt(bout), H, HD, act.data_ptr(), act.stride(0),
+                                                    G, k.data_ptr(), _lib.stream_ptr(grid.device)))
     return k, act
 
 
@@ -168,8 +168,8 @@ def siren_filter(grid: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor | None, 
 
     ``hidden_w[i]`` is the weight of hidden linear ``i`` (``[HD, E]`` then ``[HD, HD]``), ``hidden_b``
     their biases (None: no biases); every weight is read as float32, as the reference computes.  The
-    hidden stack runs in ``nsq_siren_mlp_fwd``; the readout is one GEMM of ``K = HD + 1`` with the bias
-    as the last column of the weight."""
+    hidden stack runs in ``nsq_siren_mlp_fwd``, the readout in ``nsq_siren_readout_fwd``; the readout's
+    gradients are two GEMMs (``K = H`` and, with the bias as the ones row of ``act``, ``K = G``)."""
     f = lambda t: None if t is None else t.float().contiguous()  # noqa: E731
     wh = torch.cat([w.float().reshape(-1) for w in hidden_w])
     bh = None if hidden_b is None else torch.cat([b.float().reshape(-1) for b in hidden_b])

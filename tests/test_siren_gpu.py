@@ -121,3 +121,21 @@ def test_unsupported_widths_raise():
     with pytest.raises(NotImplementedError):
         siren_filter(grid, w0.cuda(), b0.cuda(), [w.cuda() for w in hw], [b.cuda() for b in hb], wo.cuda(),
                      bo.cuda())
+
+
+@pytest.mark.parametrize("HD,H", [(16, 48), (32, 300), (64, 96), (128, 40)])
+def test_readout_vector_paths(HD, H):
+    """G a multiple of 4: the readout's 2- and 4-point-per-lane paths (HD 64 / 16, 32), and HD 128's one point per
+    lane; H not a multiple of the channel block (the last block's tail rows)."""
+    g = torch.Generator().manual_seed(HD)
+    grid = torch.rand(4096, 2, generator=g) * 2 - 1
+    w0, b0, hw, hb, wo, bo = siren_params(2, 32, HD, 2, H, bias=True, seed=HD)
+    dev = lambda t: None if t is None else t.cuda()  # noqa: E731
+    print(f"siren readout HD={HD} H={H}", flush=True)
+    k = siren_filter(grid.cuda(), dev(w0), dev(b0), [w.cuda() for w in hw], [b.cuda() for b in hb], dev(wo),
+                     dev(bo))
+    ref = siren_mlp_torch(grid, w0, b0, hw, hb, wo, bo, dtype=torch.float64).t()
+    assert rel_l2(ref, k) < 1e-5
+    k_nb = siren_filter(grid.cuda(), dev(w0), dev(b0), [w.cuda() for w in hw], [b.cuda() for b in hb], dev(wo), None)
+    ref_nb = siren_mlp_torch(grid, w0, b0, hw, hb, wo, None, dtype=torch.float64).t()
+    assert rel_l2(ref_nb, k_nb) < 1e-5
