@@ -387,6 +387,18 @@ int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_str
                       float* gw0, float* gb0, float* gwh, float* gbh, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Channels-last (BLH) layout changes (ABI 9).
+ *
+ * dst[b][c][r] = src[b][r][c] for B matrices of R x C elements of elem_bytes
+ * (2: bf16 / fp16, 4: fp32) bytes.  Replaces the materialised
+ * rearrange("b l h -> b h l") of the `_w_reshape` / `_blh` wrappers
+ * (nvsubquadratic/ops/fftconv.py:163-232, 449-538; ops/fftconv_custom.py:338-359),
+ * and its inverse with R and C swapped.  src and dst must not alias.
+ */
+int nsq_batched_transpose(const void* src, void* dst, int elem_bytes, int64_t B, int64_t R, int64_t C,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -155,6 +155,7 @@ _SIGNATURES = {
     ),
     "nsq_siren_readout_fwd": (
         _c_int, [_c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p]),
+    "nsq_batched_transpose": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_void_p]),
     "nsq_siren_mlp_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "nsq_siren_mlp_bwd": (
         _c_int,

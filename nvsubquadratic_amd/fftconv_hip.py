@@ -32,6 +32,7 @@ from einops import rearrange
 from torch.library import custom_op
 
 from . import _lib
+from .layout import channels_first_contiguous
 
 
 __all__ = [
@@ -260,7 +261,7 @@ def _take_state(ctx) -> torch.Tensor:
 def _causal_backward(ctx, gy, _gstate):
     x, k, s = ctx.saved_tensors
     state = _take_state(ctx)
-    g = gy.to(x.dtype).contiguous()
+    g = channels_first_contiguous(gy.to(x.dtype))
     gx, gk, gs = causal_fftconv1d_backward_op(g, x, k, s, state, ctx.kbatch)
     return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None
 
@@ -292,15 +293,14 @@ def _causal_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor |
     B, H, L = x.shape
     k3 = _kernel_3d(kernel, B)
     kbatch = k3.shape[0]
-    k2 = k3.reshape(kbatch * k3.shape[1], k3.shape[2])
     if k3.shape[1] != H:
         raise ValueError(f"kernel has {k3.shape[1]} channels, x has {H}")
-    if k2.shape[-1] > 2 * L:
-        raise ValueError(f"Kernel length must be less than or equal to 2 * seq_len. Got {k2.shape[-1]}.")
+    if k3.shape[2] > 2 * L:
+        raise ValueError(f"Kernel length must be less than or equal to 2 * seq_len. Got {k3.shape[2]}.")
     input_dtype = x.dtype
     compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
-    xc = x.to(compute_dtype).contiguous()
-    kc = k2.float().contiguous()
+    xc = channels_first_contiguous(x.to(compute_dtype))
+    kc = channels_first_contiguous(k3.float()).reshape(kbatch * H, k3.shape[2])
     sc = None
     if shortcut is not None:
         if shortcut.shape != (H,):
@@ -533,7 +533,7 @@ def _nd_setup(ctx, inputs, output):
 def _nd_backward(ctx, gy, _gstate):
     x, k, s = ctx.saved_tensors
     state = _take_state(ctx)
-    g = gy.to(x.dtype).contiguous()
+    g = channels_first_contiguous(gy.to(x.dtype))
     gx, gk, gs = fftconv_nd_backward_op(g, x, k, s, state, ctx.kbatch, ctx.periodic)
     return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None, None
 
@@ -565,8 +565,8 @@ def _nd_core(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor | Non
     kbatch = kernel.shape[0]
     input_dtype = x.dtype
     compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
-    xc = x.to(compute_dtype).contiguous()
-    kc = kernel.float().reshape(kbatch * H, *kernel.shape[2:]).contiguous()
+    xc = channels_first_contiguous(x.to(compute_dtype))
+    kc = channels_first_contiguous(kernel.float()).reshape(kbatch * H, *kernel.shape[2:])
     sc = None
     if shortcut is not None:
         if shortcut.shape != (H,):
@@ -662,7 +662,7 @@ def _shifted_setup(ctx, inputs, output):
 
 def _shifted_backward(ctx, gy):
     x, k, s = ctx.saved_tensors
-    g = gy.to(x.dtype).contiguous()
+    g = channels_first_contiguous(gy.to(x.dtype))
     gx, gk, gs = shifted_fftconv1d_backward_op(g, x, k, s, ctx.kbatch, ctx.periodic)
     return gx, gk, _shortcut_grad(gs, s, ctx.kbatch, x.shape[1]), None, None
 
@@ -676,8 +676,8 @@ def shifted_fftconv1d(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Ten
     kbatch = kernel.shape[0]
     input_dtype = x.dtype
     compute_dtype = input_dtype if input_dtype in _lib.NSQ_DTYPE else torch.float32
-    xc = x.to(compute_dtype).contiguous()
-    kc = kernel.float().reshape(kbatch * H, kernel.shape[-1]).contiguous()
+    xc = channels_first_contiguous(x.to(compute_dtype))
+    kc = channels_first_contiguous(kernel.float()).reshape(kbatch * H, kernel.shape[-1])
     sc = None if shortcut is None else shortcut.to(compute_dtype).contiguous()
     return shifted_fftconv1d_op(xc, kc, sc, kbatch, int(periodic)).to(input_dtype)
 

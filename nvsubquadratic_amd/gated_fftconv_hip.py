@@ -32,6 +32,7 @@ import torch
 from torch.library import custom_op
 
 from . import _lib
+from .layout import channels_first_contiguous
 from .fftconv_hip import _kernel_3d, _workspace
 from .circular_fftconv_hip import needs_extension, periodic_by_extension
 from .mixed_fftconv_hip import periodic_mask
@@ -165,7 +166,7 @@ def _gated1d_setup(ctx, inputs, output):
 def _gated1d_backward(ctx, gy, _gy1):
     q, kg, v, y1, k, s = ctx.saved_tensors
     act1, act2, kbatch = ctx.meta
-    g = gy.to(q.dtype).contiguous()
+    g = channels_first_contiguous(gy.to(q.dtype))
     dq, dkg, dv, gk, gs = gated_causal_fftconv1d_backward_op(g, q, kg, v, y1, k, s, act1, act2, kbatch,
                                                              ctx.fuse_bwd)
     return dq, dkg, dv, gk, _shortcut_grad(gs, s, kbatch, q.shape[1]), None, None, None, None, None
@@ -205,8 +206,8 @@ def hyena_gated_causal_fftconv1d_bhl(
     kbatch = k3.shape[0]
     in_dtype = query.dtype
     cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
-    q, kg, v = (t.to(cdt).contiguous() for t in (query, key, value))
-    kc = k3.float().reshape(kbatch * H, k3.shape[-1]).contiguous()
+    q, kg, v = (channels_first_contiguous(t.to(cdt)) for t in (query, key, value))
+    kc = channels_first_contiguous(k3.float()).reshape(kbatch * H, k3.shape[-1])
     sc = None
     if shortcut is not None:
         if shortcut.shape != (H,):
@@ -300,7 +301,7 @@ def _gatednd_setup(ctx, inputs, output):
 def _gatednd_backward(ctx, gy, _gy1):
     q, kg, v, y1, k, s = ctx.saved_tensors
     act1, act2, kbatch, periodic = ctx.meta
-    g = gy.to(q.dtype).contiguous()
+    g = channels_first_contiguous(gy.to(q.dtype))
     dq, dkg, dv, gk, gs = gated_fftconv_nd_backward_op(g, q, kg, v, y1, k, s, act1, act2, kbatch, periodic)
     return dq, dkg, dv, gk, _shortcut_grad(gs, s, kbatch, q.shape[1]), None, None, None, None, None
 
@@ -332,8 +333,8 @@ def hyena_gated_fftconv_nd_bhl(query, key, value, kernel, shortcut=None, gate_no
     kbatch = k.shape[0]
     in_dtype = query.dtype
     cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
-    q, kg, v = (t.to(cdt).contiguous() for t in (query, key, value))
-    kc = k.float().reshape(kbatch * H, *k.shape[2:]).contiguous()
+    q, kg, v = (channels_first_contiguous(t.to(cdt)) for t in (query, key, value))
+    kc = channels_first_contiguous(k.float()).reshape(kbatch * H, *k.shape[2:])
     sc = None
     if shortcut is not None:
         if shortcut.shape != (H,):
