@@ -25,6 +25,8 @@
 // complex points); see real_unpack/real_repack in fft_core.h.
 #pragma once
 
+#include <cstdlib>
+
 #include "fft_core.h"
 #include "gate.h"
 
@@ -252,6 +254,66 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
       __syncthreads();
     }
   }
+}
+
+// Forward, fused plan, for grids too small to fill the GPU (M == 1 lengths,
+// few (channel, batch row) pairs): fused_fwd_kernel then runs one workgroup
+// of N/16 threads per row, one wave per SIMD, and transforms the filter and
+// the row one after the other.  Here a workgroup of 2 N/16 threads owns one
+// (channel h = blockIdx.x, batch row b = blockIdx.y) and holds a
+// two-transform tile: transform 0 is the filter, transform 1 the row, both
+// transformed at once (waves 0 .. N/512 - 1 load the filter, the rest the
+// row).  The product reads both spectra from LDS slot by slot and leaves the
+// result in transform 1; the inverse transform runs over the whole tile and
+// the epilogue keeps transform 1.  Per element the arithmetic is that of
+// fused_fwd_kernel.  Plain causal conv (no fold, ramp or gates); kfilm: the
+// filter row is image b's.
+template <int LOGN, int DT>
+__global__ __launch_bounds__(2 * FusedCfg<LOGN>::T) void fused_fwd_pair_kernel(
+    const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ k,
+    const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ y, int H, int L, int K,
+    const float2* __restrict__ tw, int kfilm) {
+  using C = FusedCfg<LOGN>;
+  static_assert(C::M == 1, "fused_fwd_pair_kernel: one transform per channel");
+  constexpr int T = 2 * C::T, SL = C::N / 2 / T;  // threads; product slots per thread
+  static_assert(SL >= 1 && (C::N / 2) % T == 0, "fused_fwd_pair_kernel: slot split");
+  __shared__ float2 lds[2 * C::SP];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int64_t row = (int64_t(b) * H + h) * L;
+  const float* kr = k + (kfilm ? int64_t(b) * H + h : int64_t(h)) * K;
+
+  auto ld = [&](int m, int n) -> float2 {
+    if (m == 0) return load_pair<NSQ_DTYPE_F32>(kr, 2 * int64_t(n), K);
+    return load_pair<DT>(x + row, 2 * int64_t(n), L);
+  };
+  LdsTile<C::SP, true> st{lds};
+  fft<LOGN, false, 2, T, C::SP>(lds, ld, st, tw);
+#pragma unroll
+  for (int i = 0; i < SL; ++i) {
+    NSQ_SLOT_FENCE();
+    const int p = opaque_tid() + i * T;
+    float2 hA, hB, A, Bc;
+    lds_unpack<LOGN>(lds, 0, p, tw, hA, hB);
+    lds_unpack<LOGN>(lds, 1, p, tw, A, Bc);
+    A = slot_mul(p == 0, A, hA);
+    Bc = cmul(Bc, hB);
+    lds_repack<LOGN>(lds, 1, p, tw, A, Bc);
+  }
+  __syncthreads();
+
+  const float scale = 1.f / float(C::N);
+  const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
+  auto epi = [&](int m, int n, float2 v) {
+    if (m == 0) return;
+    const int64_t i0 = 2 * int64_t(n);
+    if (i0 < L)
+      Elem<DT>::store(y, row + i0, epilogue<DT>(v.x * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0) : 0.f));
+    if (i0 + 1 < L)
+      Elem<DT>::store(y, row + i0 + 1,
+                      epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0 + 1) : 0.f));
+  };
+  LdsTile<C::SP, true> ldl{lds};
+  fft<LOGN, true, 2, T, C::SP>(lds, ldl, epi, tw);
 }
 
 // Backward, fused plan.  grid = ceil(H/M); each workgroup loops over all
@@ -879,12 +941,39 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
 // ===========================================================================
 // Host launchers
 // ===========================================================================
+// Largest B*H that the forward runs on fused_fwd_pair_kernel (M == 1 lengths,
+// no fold): as many rows as one round of pair workgroups covers, i.e. 256 CUs
+// times the pair tiles that fit a CU's 160 KB of LDS (FFT length 4096: 1024
+// rows, 8192: 512, 16384: 256).  Measured on MI355X (kernel time, one-
+// transform -> pair kernel): length 8192 B=2 H=128 20.2 -> 16.0 us, H=512
+// 23.4 -> 21.1 us, H=2048 68.8 -> 71.7 us; length 16384 H=256 29.4 -> 23.2
+// us, H=512 39.4 -> 43.1 us.  NSQ_1D_PAIR_MAX_ROWS overrides the bound for
+// every length (0 turns the pair kernel off).
+template <int LOGN>
+inline int64_t fused_pair_max_rows() {
+  static const int64_t env = [] {
+    const char* e = std::getenv("NSQ_1D_PAIR_MAX_ROWS");
+    return e ? int64_t(std::atoll(e)) : int64_t(-1);
+  }();
+  if (env >= 0) return env;
+  constexpr int lds = 2 * FusedCfg<LOGN>::SP * int(sizeof(float2));
+  constexpr int per_cu = (160 * 1024) / lds;
+  return int64_t(256) * (per_cu < 1 ? 1 : per_cu);
+}
+
 // kfilm: per-sample filters [B*H, K]; one image per workgroup.
 template <int LOGN, int DT>
 static void launch_fused_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void* y, int B, int H,
                              int L, int K, int kfilm, const float2* tw, hipStream_t st) {
   using C = FusedCfg<LOGN>;
   using ET = typename Elem<DT>::T;
+  if constexpr (C::M == 1) {
+    if (!p.fold && int64_t(H) * B <= fused_pair_max_rows<LOGN>()) {
+      hipLaunchKernelGGL((fused_fwd_pair_kernel<LOGN, DT>), dim3(H, B), dim3(2 * C::T), 0, st, (const ET*)x, k,
+                         (const ET*)s, (ET*)y, H, L, K, tw, kfilm);
+      return;
+    }
+  }
   const int gh = int(ceil_div(H, C::M));
   int nb = int(ceil_div(2048, gh));
   nb = nb < 1 ? 1 : (nb > B ? B : nb);

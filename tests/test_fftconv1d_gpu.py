@@ -261,6 +261,31 @@ def test_config1_fp32_fwd_bwd():
     assert rel_l2(s.grad, sg.grad) < RTOL_F32_L2
 
 
+@pytest.mark.parametrize("L", [2048, 4096, 8192])
+@pytest.mark.parametrize("dtype,film", [(torch.float32, False), (torch.bfloat16, False), (torch.float32, True)])
+def test_fused_pair_and_single_kernels_agree(L, dtype, film):
+    """The fused forward runs up to 1024 / 512 / 256 rows (B*H) of FFT lengths 4096 / 8192 / 16384 on the
+    two-transform (filter | row) workgroup and larger grids on the one-transform kernel: 8 channels past that bound
+    take the latter, the bound's worth of them the former.  Same arithmetic per element, so the outputs agree bit
+    for bit; both meet the oracle."""
+    torch.manual_seed(31)
+    B = 2 if film else 1
+    rows = {2048: 1024, 4096: 512, 8192: 256}[L]
+    H, Hp = rows // B + 8, rows // B
+    x = torch.randn(B, H, L).to(dtype)
+    k = torch.randn(B if film else 1, H, L) * torch.exp(-torch.linspace(0, 8, L))
+    s = torch.randn(H).to(dtype)
+    xd, kd, sd = x.cuda(), k.cuda(), s.cuda()
+    y_single = F.causal_fftconv1d_bhl(xd, kd, sd)
+    y_pair = F.causal_fftconv1d_bhl(xd[:, :Hp].contiguous(), kd[:, :Hp].contiguous(), sd[:Hp].contiguous())
+    assert torch.equal(y_pair, y_single[:, :Hp])
+    tol = RTOL_F32_L2 if dtype == torch.float32 else RTOL_BF16_L2
+    y64 = np.concatenate([causal_fftconv1d_np(x[b:b + 1].float().numpy(), k[b if film else 0].numpy(),
+                                              s.float().numpy()) for b in range(B)])
+    assert rel_l2(y64, y_single) < tol
+    assert rel_l2(y64[:, :Hp], y_pair) < tol
+
+
 def test_config3_channel_sample_bf16_fwd_bwd():
     """BASELINE config 3 at full length L=262144 on a 4-channel sample (bf16 I/O)."""
     L = 262144
