@@ -781,6 +781,200 @@ __device__ __forceinline__ void row_repack(float2* lds, const RowSlots<LOGN1, LO
   lds[pb] = zq;
 }
 
+// ---------------------------------------------------------------------------
+// Row pairs with the spectral slots in registers (rows of N2 = 1024: forward
+// passes of radix 16, 16, 4; inverse passes of radix 4, 16, 16).
+//
+// The last forward pass (radix 4, 256 butterflies per row) gives butterfly j
+// the elements {j + 256 r}, r < 4, in and out.  Assigning the butterflies so
+// that a thread owns both Hermitian partners of each output lets the real
+// unpack, the spectral product and the repack run on registers, and the
+// inverse transform starts with the matching radix-4 pass (first pass,
+// butterfly j reads {j + 256 r}) on the same registers.  Against the tile
+// round trip of row_unpack/row_repack this saves, per transform, one LDS
+// write and read of the whole tile and two barriers.
+//
+// Thread t (of 128 per pair) owns four butterflies b = (tile row, j):
+//   q > 0 : (0, t), (1, 255 - t), (0, 255 - t), (1, t).  Row-0 element
+//           j + 256 r pairs with row-1 element (255 - j) + 256 (3 - r), so
+//           group g = {b = 2g, 2g + 1} holds slots (b0 out r, b1 out 3 - r).
+//   q == 0: rows 0 and N1/2 pair within themselves: (0, t), (0, 256 - t),
+//           (1, t), (1, 255 - t); thread 0's row-0 butterflies are (0, 0) and
+//           (0, 128), each paired with itself (out r with out (4 - r) mod 4,
+//           slot 0 = elements 0 and 512; out r with out 3 - r).
+// Slot (g, e), e < 4, is element s = j_{2g} + 256 e of row k1: frequency
+// p = k1 + N1 s, unpack root W_2N^{k1} W_2048^{j} W_16^{2e}.
+// ---------------------------------------------------------------------------
+template <bool QZ>
+struct RegPair {
+  static constexpr int LOGN2 = 10, N2 = 1024, T = 128, NB = 4, R = 4, NRL = 256;
+  bool sp;  // q == 0 and thread 0: row-0 butterflies self-paired
+  int m[NB], j[NB];
+  __device__ __forceinline__ explicit RegPair(int tl) {
+    sp = QZ && (tl == 0);
+    m[0] = 0;
+    j[0] = tl;
+    m[1] = QZ ? 0 : 1;
+    j[1] = QZ ? (tl == 0 ? NRL / 2 : NRL - tl) : NRL - 1 - tl;
+    m[2] = QZ ? 1 : 0;
+    j[2] = QZ ? tl : NRL - 1 - tl;
+    m[3] = 1;
+    j[3] = QZ ? NRL - 1 - tl : tl;
+  }
+};
+constexpr int kRegPairLogN2 = 10;
+
+// Forward passes 1 and 2 of M rows of 1024 (first pass reads through ld).
+template <int M, int T, class LD>
+__device__ __forceinline__ void rows1024_fwd_head(float2* lds, LD& ld, const float2* __restrict__ tw) {
+  LdsTile<RowCfg<10>::N2P, true> tile{lds};
+  stockham_pass<10, 4, 0, false, M, T, false>(ld, tile, tw);
+  stockham_pass<10, 4, 4, false, M, T, false>(tile, tile, tw);
+}
+
+// Inverse passes 2 and 3 of M rows of 1024 (radix 16 after the radix-4 first
+// pass), the last one storing through st.
+template <int M, int T, class ST>
+__device__ __forceinline__ void rows1024_inv_tail(float2* lds, ST& st, const float2* __restrict__ tw) {
+  LdsTile<RowCfg<10>::N2P, true> tile{lds};
+  stockham_pass<10, 4, 2, true, M, T, false>(tile, tile, tw);
+  stockham_pass<10, 4, 6, true, M, T, false>(tile, st, tw);
+}
+
+// Last forward pass of a row pair (its 2-row sub-tile `sub`) into registers.
+// Reads only; the caller's next tile write must follow a barrier.
+template <bool QZ>
+__device__ __forceinline__ void regpair_last_fwd(const float2* sub, const RegPair<QZ>& rp,
+                                                 const float2* __restrict__ tw, float2 (&v)[4][4]) {
+  using TL = LdsTile<RowCfg<10>::N2P, true>;
+  const TL tile{const_cast<float2*>(sub)};
+  const TwTable tt(tw);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    float2 w[4];
+    pass_twiddles<4>(tt, 1 << 10, rp.j[b], w);
+    const float2* p = tile.at(rp.m[b], rp.j[b]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[b][r] = p[TL::off(r * 256)];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) v[b][r] = cmul(v[b][r], w[r]);
+    dft<4, false>(v[b]);
+  }
+}
+
+// First inverse pass (radix 4, no twiddles) of the pair's registers into its
+// sub-tile: butterfly j's outputs go to elements 4 j + r.  The caller puts a
+// barrier before (the tile may still be read) and after.
+template <bool QZ>
+__device__ __forceinline__ void regpair_first_inv(float2* sub, const RegPair<QZ>& rp, float2 (&v)[4][4]) {
+  using TL = LdsTile<RowCfg<10>::N2P, true>;
+  const TL tile{sub};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    dft<4, true>(v[b]);
+    float2* p = tile.at(rp.m[b], 4 * rp.j[b]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[TL::off(r)] = v[b][r];
+  }
+}
+
+__device__ __forceinline__ float2 sel2(bool c, float2 a, float2 b) {
+  return make_float2(c ? a.x : b.x, c ? a.y : b.y);
+}
+
+// Runs f(i, s0, A, Bc) on the pair's 8 spectral slots i = 4 g + e in order
+// (slot form, see real_unpack; s0 marks slot 0 of the q == 0 pair).  With
+// REPACK the slot values f leaves in (A, Bc) are repacked into the butterfly
+// registers in place: each slot reads and writes its own two positions, which
+// no other slot touches, so slot-at-a-time is exact and holds no slot arrays.
+// Slot (g, e) is element j_{2g} + 256 e of its row: root W_2N^{k1}
+// W_2048^{j_{2g}} W_16^{2e}; for thread 0 of q == 0, group 0 holds the
+// self-paired elements 0/512 (slot 0), 256/768, 128/896 and 384/640.
+template <int LOGN1, bool QZ, bool REPACK, class F>
+__device__ __forceinline__ void regpair_slots(const RegPair<QZ>& rp, int q, float2 (&v)[4][4],
+                                              const float2* __restrict__ tw, F&& f) {
+  constexpr int LOGN = LOGN1 + 10, N1 = 1 << LOGN1;
+  const TwTable tt(tw);
+  float2 u[2], wj[2];
+  u[0] = QZ ? make_float2(1.f, 0.f) : root<LOGN + 1>(tw, uint32_t(q));
+  u[1] = QZ ? root<LOGN + 1>(tw, uint32_t(N1 / 2)) : u[0];
+  wj[0] = tt.load(2048, rp.j[0]);
+  wj[1] = tt.load(2048, rp.j[2]);
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      NSQ_SLOT_FENCE();
+      const int b0 = 2 * g, b1 = 2 * g + 1;
+      float2 zp = v[b0][e], zq = v[b1][3 - e];
+      float2 w = cmul_fixed(u[g], rot16(wj[g], 2 * e));
+      const bool spg = QZ && g == 0;  // thread 0 of q == 0 may take the self-paired form
+      if (spg) {
+        const float2 spp = e < 2 ? v[0][e] : v[1][e - 2];
+        const float2 spq = e < 2 ? v[0][e + 2] : v[1][5 - e];
+        zp = sel2(rp.sp, spp, zp);
+        zq = sel2(rp.sp, spq, zq);
+        if (e >= 2) w = sel2(rp.sp, rot16(make_float2(1.f, 0.f), 2 * e - 3), w);  // W_16^1, W_16^3
+      }
+      const bool s0 = spg && e == 0 && rp.sp;
+      float2 A, Bc;
+      real_unpack(s0, zp, zq, w, A, Bc);
+      f(4 * g + e, s0, A, Bc);
+      if constexpr (REPACK) {
+        real_repack(s0, A, Bc, w, zp, zq);
+        if (spg) {  // both position sets, the unused one keeping its value (e < 2 share v[0][e])
+          const bool S = rp.sp;
+          if (e < 2) {
+            v[0][e] = zp;
+            v[1][3 - e] = sel2(S, v[1][3 - e], zq);
+            v[0][e + 2] = sel2(S, zq, v[0][e + 2]);
+          } else {
+            v[0][e] = sel2(S, v[0][e], zp);
+            v[1][3 - e] = sel2(S, v[1][3 - e], zq);
+            v[1][e - 2] = sel2(S, zp, v[1][e - 2]);
+            v[1][5 - e] = sel2(S, zq, v[1][5 - e]);
+          }
+        } else {
+          v[b0][e] = zp;
+          v[b1][3 - e] = zq;
+        }
+      }
+    }
+  }
+}
+
+// Last forward pass and slot loop of one row pair, for a pair index q known
+// only at run time (the q == 0 pair pairs its rows within themselves).  No
+// barriers inside, so the threads of one workgroup may take either branch.
+template <int LOGN1, bool REPACK, class F>
+__device__ __forceinline__ void regpair_fwd_slots(const float2* sub, int q, int tl, const float2* __restrict__ tw,
+                                                  float2 (&v)[4][4], F&& f) {
+  if (q == 0) {
+    const RegPair<true> rp(tl);
+    regpair_last_fwd(sub, rp, tw, v);
+    regpair_slots<LOGN1, true, REPACK>(rp, q, v, tw, f);
+  } else {
+    const RegPair<false> rp(tl);
+    regpair_last_fwd(sub, rp, tw, v);
+    regpair_slots<LOGN1, false, REPACK>(rp, q, v, tw, f);
+  }
+}
+
+// The inverse transform of a row pair held in registers: first pass into the
+// pair's sub-tile, then passes 2 and 3 over the whole tile of M rows (T
+// threads), the last one storing through st.
+template <int M, int T, class ST>
+__device__ __forceinline__ void regpair_inverse(float2* lds, float2* sub, int q, int tl, float2 (&v)[4][4], ST& st,
+                                                const float2* __restrict__ tw) {
+  __syncthreads();
+  if (q == 0)
+    regpair_first_inv(sub, RegPair<true>(tl), v);
+  else
+    regpair_first_inv(sub, RegPair<false>(tl), v);
+  __syncthreads();
+  rows1024_inv_tail<M, T>(lds, st, tw);
+}
+
 // Forward row kernel.  grid = H * N1/2 (block = h * N1/2 + q).  wsx rows are
 // [B*H][N] (column-transformed x), wsk [H][N] (column-transformed k); the
 // product's inverse rows go to wsy (== wsx for in-place, or a separate region
@@ -797,6 +991,31 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
   const int q = blockIdx.x % ((1 << LOGN1) / 2);
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 hA[C::SLOTS], hB[C::SLOTS];
+  if constexpr (LOGN2 == kRegPairLogN2) {
+    constexpr int N1 = 1 << LOGN1;
+    const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
+    const int tl = opaque_tid();
+    float2 v[4][4];
+    auto head = [&](const float2* sig) {
+      auto ld = [&](int m, int n) -> float2 { return sig[int64_t(m == 0 ? ra : rb) * C::N2 + n]; };
+      rows1024_fwd_head<2, C::T>(lds, ld, tw);
+    };
+    head(wsk + int64_t(h) * N);
+    regpair_fwd_slots<LOGN1, false>(lds, q, tl, tw, v, [&](int i, bool, float2& A, float2& Bc) {
+      hA[i] = A;
+      hB[i] = Bc;
+    });
+    for (int b = 0; b < B; ++b) {
+      head(wsx + (int64_t(b) * H + h) * N);
+      regpair_fwd_slots<LOGN1, true>(lds, q, tl, tw, v, [&](int i, bool s0, float2& A, float2& Bc) {
+        A = slot_mul(s0, A, hA[i]);
+        Bc = cmul(Bc, hB[i]);
+      });
+      RowStore<C::N2> st{wsy + (int64_t(b) * H + h) * N, ra, rb};
+      regpair_inverse<2, C::T>(lds, lds, q, tl, v, st, tw);
+    }
+    return;
+  }
   row_pair_fft<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
   {
     const RS rs(q, tw);
@@ -897,6 +1116,44 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
   const int q = blockIdx.x % ((1 << LOGN1) / 2);
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 sA[C::SLOTS], sB[C::SLOTS];  // K slots, then G slots
+  if constexpr (LOGN2 == kRegPairLogN2) {
+    constexpr int N1 = 1 << LOGN1;
+    const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
+    const int tl = opaque_tid();
+    float2 v[4][4];
+    auto head = [&](const float2* sig) {
+      auto ld = [&](int m, int n) -> float2 { return sig[int64_t(m == 0 ? ra : rb) * C::N2 + n]; };
+      rows1024_fwd_head<2, C::T>(lds, ld, tw);
+    };
+    head(wsk + int64_t(h) * N);
+    regpair_fwd_slots<LOGN1, false>(lds, q, tl, tw, v, [&](int i, bool, float2& A, float2& Bc) {
+      sA[i] = A;
+      sB[i] = Bc;
+    });
+    float2* sigg = wsg + int64_t(h) * N;
+    head(sigg);
+    // gx slots G conj K; the G slots replace the K slots
+    regpair_fwd_slots<LOGN1, true>(lds, q, tl, tw, v, [&](int i, bool s0, float2& A, float2& Bc) {
+      const float2 ga = A, gb = Bc;
+      A = slot_mulc(s0, ga, sA[i]);
+      Bc = cmulc(gb, sB[i]);
+      sA[i] = ga;
+      sB[i] = gb;
+    });
+    {
+      RowStore<C::N2> st{sigg, ra, rb};
+      regpair_inverse<2, C::T>(lds, lds, q, tl, v, st, tw);
+    }
+    head(wsx + int64_t(h) * N);
+    // gk slots G conj X
+    regpair_fwd_slots<LOGN1, true>(lds, q, tl, tw, v, [&](int i, bool s0, float2& A, float2& Bc) {
+      A = slot_mulc(s0, sA[i], A);
+      Bc = cmulc(sB[i], Bc);
+    });
+    RowStore<C::N2> st{wsk + int64_t(h) * N, ra, rb};
+    regpair_inverse<2, C::T>(lds, lds, q, tl, v, st, tw);
+    return;
+  }
   row_pair_fft<LOGN1, LOGN2>(lds, wsk + int64_t(h) * N, q, tw);
   {
     const RS rs(q, tw);

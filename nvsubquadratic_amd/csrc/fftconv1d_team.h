@@ -249,6 +249,24 @@ __device__ __forceinline__ void team_rows_fwd(float2* xsig, const float2* ksig, 
   LdsTile<TC::N2P, true> tile{lds};
   const L2Signal kin(ksig, N), xin(xsig, N);
   auto ldk = [&](int m, int n) -> float2 { return kin[team_row_of<LOGN1>(q0, m) * N2 + n]; };
+  auto ldx = [&](int m, int n) -> float2 { return xin[team_row_of<LOGN1>(q0, m) * N2 + n]; };
+  auto sty = [&](int m, int n, float2 v) { xsig[int64_t(team_row_of<LOGN1>(q0, m)) * N2 + n] = v; };
+  if constexpr (LOGN2 == kRegPairLogN2) {  // the multi-kernel row_fwd_kernel's transforms, pair by pair
+    const int q = q0 + sp;
+    float2 v[4][4], hA[SLOTS], hB[SLOTS];
+    rows1024_fwd_head<TC::M, kTeamThreads>(lds, ldk, tw);
+    regpair_fwd_slots<LOGN1, false>(sub, q, tl, tw, v, [&](int i, bool, float2& A, float2& Bc) {
+      hA[i] = A;
+      hB[i] = Bc;
+    });
+    rows1024_fwd_head<TC::M, kTeamThreads>(lds, ldx, tw);
+    regpair_fwd_slots<LOGN1, true>(sub, q, tl, tw, v, [&](int i, bool s0, float2& A, float2& Bc) {
+      A = slot_mul(s0, A, hA[i]);
+      Bc = cmul(Bc, hB[i]);
+    });
+    regpair_inverse<TC::M, kTeamThreads>(lds, sub, q, tl, v, sty, tw);
+    return;
+  }
   fft<LOGN2, false, TC::M, kTeamThreads, TC::N2P>(lds, ldk, tile, tw);
   float2 hA[SLOTS], hB[SLOTS];
   {
@@ -260,7 +278,6 @@ __device__ __forceinline__ void team_rows_fwd(float2* xsig, const float2* ksig, 
     }
   }
   __syncthreads();
-  auto ldx = [&](int m, int n) -> float2 { return xin[team_row_of<LOGN1>(q0, m) * N2 + n]; };
   fft<LOGN2, false, TC::M, kTeamThreads, TC::N2P>(lds, ldx, tile, tw);
   {
     const RS rs(q0 + sp, tw, tl);
@@ -273,7 +290,6 @@ __device__ __forceinline__ void team_rows_fwd(float2* xsig, const float2* ksig, 
     }
   }
   __syncthreads();
-  auto sty = [&](int m, int n, float2 v) { xsig[int64_t(team_row_of<LOGN1>(q0, m)) * N2 + n] = v; };
   fft<LOGN2, true, TC::M, kTeamThreads, TC::N2P>(lds, tile, sty, tw);
 }
 
@@ -292,6 +308,36 @@ __device__ __forceinline__ void team_rows_bwd(const float2* gsig, float2* xsig, 
   float2* sub = lds + sp * 2 * TC::N2P;
   LdsTile<TC::N2P, true> tile{lds};
   const L2Signal kin(ksig, N), gin(gsig, N), xin(xsig, N);
+  if constexpr (LOGN2 == kRegPairLogN2) {  // the multi-kernel row_bwd1_kernel's transforms, pair by pair
+    auto ldk = [&](int m, int n) -> float2 { return kin[team_row_of<LOGN1>(q0, m) * N2 + n]; };
+    auto ldg = [&](int m, int n) -> float2 { return gin[team_row_of<LOGN1>(q0, m) * N2 + n]; };
+    auto ldx = [&](int m, int n) -> float2 { return xin[team_row_of<LOGN1>(q0, m) * N2 + n]; };
+    auto stk = [&](int m, int n, float2 v) { ksig[int64_t(team_row_of<LOGN1>(q0, m)) * N2 + n] = v; };
+    auto stx = [&](int m, int n, float2 v) { xsig[int64_t(team_row_of<LOGN1>(q0, m)) * N2 + n] = v; };
+    const int q = q0 + sp;
+    float2 v[4][4], sA[SLOTS], sB[SLOTS];
+    rows1024_fwd_head<TC::M, kTeamThreads>(lds, ldk, tw);
+    regpair_fwd_slots<LOGN1, false>(sub, q, tl, tw, v, [&](int i, bool, float2& A, float2& Bc) {
+      sA[i] = A;
+      sB[i] = Bc;
+    });
+    rows1024_fwd_head<TC::M, kTeamThreads>(lds, ldg, tw);
+    regpair_fwd_slots<LOGN1, true>(sub, q, tl, tw, v, [&](int i, bool s0, float2& A, float2& Bc) {
+      const float2 ga = A, gb = Bc;
+      A = slot_mulc(s0, ga, sA[i]);
+      Bc = cmulc(gb, sB[i]);
+      sA[i] = ga;
+      sB[i] = gb;
+    });
+    regpair_inverse<TC::M, kTeamThreads>(lds, sub, q, tl, v, stk, tw);
+    rows1024_fwd_head<TC::M, kTeamThreads>(lds, ldx, tw);
+    regpair_fwd_slots<LOGN1, true>(sub, q, tl, tw, v, [&](int i, bool s0, float2& A, float2& Bc) {
+      A = slot_mulc(s0, sA[i], A);
+      Bc = cmulc(sB[i], Bc);
+    });
+    regpair_inverse<TC::M, kTeamThreads>(lds, sub, q, tl, v, stx, tw);
+    return;
+  }
   float2 sA[SLOTS], sB[SLOTS];  // K slots, then G slots
   auto ldk = [&](int m, int n) -> float2 { return kin[team_row_of<LOGN1>(q0, m) * N2 + n]; };
   fft<LOGN2, false, TC::M, kTeamThreads, TC::N2P>(lds, ldk, tile, tw);
