@@ -1045,9 +1045,11 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
 // g; out: gx pre-image), wsx rows [B*H][N] (column-transformed x), wsk [H][N]
 // (in: column-transformed k; out: gk pre-image).  grid = H * N1/2.  Two LDS
 // tiles: G and X of one batch row are transformed side by side and the gk
-// correlation accumulates over the batch in registers.
+// correlation accumulates over the batch in registers.  The two tiles (2 x 17
+// KB per 2-wave workgroup at N2 = 1024) allow 4 workgroups per CU, i.e. 2
+// waves per SIMD, whatever the register count: the occupancy hint says so.
 template <int LOGN1, int LOGN2>
-__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(3))) void row_bwd_kernel(
+__global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(2))) void row_bwd_kernel(
     float2* __restrict__ wsg, const float2* __restrict__ wsx, float2* __restrict__ wsk, int B, int H,
     const float2* __restrict__ tw) {
   using C = RowCfg<LOGN2>;
