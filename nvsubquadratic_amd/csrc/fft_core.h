@@ -64,6 +64,11 @@ __device__ __forceinline__ float2 root(const float2* __restrict__ tw, uint32_t m
 }
 
 
+// Keeps the scheduler from hoisting the loads of every unrolled spectral slot
+// (or twiddle, or filter value) ahead of the first one, which otherwise
+// multiplies the live registers.
+#define NSQ_SLOT_FENCE() __builtin_amdgcn_sched_barrier(0)
+
 // Thread index hidden from loop-invariant code motion.  Pass twiddles and
 // addresses depend only on the thread index; inside a batch loop the compiler
 // would otherwise hoist all of them out of the loop and keep them live across

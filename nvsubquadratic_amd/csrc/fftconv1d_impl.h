@@ -32,9 +32,6 @@
 
 namespace nsq {
 
-// Keeps the scheduler from hoisting the loads of every unrolled spectral slot
-// ahead of the first one, which otherwise multiplies the live registers.
-#define NSQ_SLOT_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 // ===========================================================================
 // Plan selection

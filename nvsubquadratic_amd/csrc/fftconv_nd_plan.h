@@ -4,6 +4,9 @@
 // structure.
 #pragma once
 
+#include <cstdlib>
+
+#include "fftconv2d_image.h"
 #include "fftconv_nd_impl.h"
 
 namespace nsq {
@@ -350,6 +353,30 @@ bool inner_inv(const NdPlan& p, float2* ws, int64_t nbh, int n0, int off1, int n
 
 
 // Filter spectrum: kb*H blocks of the [kb*H][K0][K1][K2] float32 kernel.
+// Shapes the one-kernel image forward (fftconv2d_image.h) takes; the caller
+// also needs a forward that keeps no state, a shared filter and no gates.
+inline bool image_fwd_ok(const NdPlan& p, const void* x, const void* y) {
+  return p.nd == 2 && p.kb == 1 && !p.ramp && p.wm[0] == -1 && p.wm[2] == -1 && p.F[0] == 256 && p.F[2] == 256 &&
+         p.S[0] <= 128 && p.S[2] <= 128 && p.o[0] <= 128 && p.o[2] % 2 == 0 && p.S[2] % 8 == 0 && p.pack &&
+         p.RS == 128 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
+         p.B * p.H <= int64_t(1) << 30;
+}
+
+template <int DT>
+inline void launch_image_fwd(const NdPlan& p, const void* x, const float2* khat, const void* s, void* y,
+                             const float2* tw, hipStream_t st) {
+  using ET = typename Elem<DT>::T;
+  const dim3 grid(unsigned(p.B * p.H));
+  const float scale = 1.f / (float(p.F[0]) * float(p.F[2] / 2));
+  constexpr int T = kImgThreads;
+  if (s)
+    hipLaunchKernelGGL((nd2_image_fwd_kernel<DT, true, T>), grid, dim3(T), 0, st, (const ET*)x, khat, p.RS,
+                       (const ET*)s, (ET*)y, int(p.B), int(p.H), p.S[0], p.S[2], p.o[0], p.o[2], scale, tw);
+  else
+    hipLaunchKernelGGL((nd2_image_fwd_kernel<DT, false, T>), grid, dim3(T), 0, st, (const ET*)x, khat, p.RS,
+                       (const ET*)s, (ET*)y, int(p.B), int(p.H), p.S[0], p.S[2], p.o[0], p.o[2], scale, tw);
+}
+
 inline bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {
   const int64_t nk = p.kb * p.H;
   if (!inner_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], false, wsk, tw, st)) return false;
@@ -374,6 +401,17 @@ bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, v
   float2* wsk = wsx + BH * p.spec;
   float2* wsy = save ? ws : wsx;
   if (!filter_spectrum(p, k, wsk, tw, st)) return false;
+  // A forward that keeps no state for a backward runs whole images in one
+  // kernel where the shape allows (fftconv2d_image.h); NSQ_2D_IMAGE_FWD=0
+  // selects the three passes below.
+  static const bool image_on = [] {
+    const char* e = std::getenv("NSQ_2D_IMAGE_FWD");
+    return !(e && e[0] == '0');
+  }();
+  if (!GATED && !save && image_on && image_fwd_ok(p, x, y)) {
+    launch_image_fwd<DT>(p, x, wsk, s, y, tw, st);
+    return true;
+  }
   const GatedIO gi = GATED ? *gate : GatedIO{};
   if (!inner_fwd<DT, GM>(p, x, BH, p.S[0], p.S[1], p.S[2], true, wsx, tw, st, gi)) return false;
   const ColGeom cg = axis0_geom(p);
