@@ -887,7 +887,9 @@ __device__ __forceinline__ float2 sel2(bool c, float2 a, float2 b) {
 // Slot (g, e) is element j_{2g} + 256 e of its row: root W_2N^{k1}
 // W_2048^{j_{2g}} W_16^{2e}; for thread 0 of q == 0, group 0 holds the
 // self-paired elements 0/512 (slot 0), 256/768, 128/896 and 384/640.
-template <int LOGN1, bool QZ, bool REPACK, class F>
+// UNPACK = false: f sets the slot values itself (a spectrum formed from slots
+// alone, such as a sum over batch rows) and nothing is read from v.
+template <int LOGN1, bool QZ, bool REPACK, bool UNPACK = true, class F>
 __device__ __forceinline__ void regpair_slots(const RegPair<QZ>& rp, int q, float2 (&v)[4][4],
                                               const float2* __restrict__ tw, F&& f) {
   constexpr int LOGN = LOGN1 + 10, N1 = 1 << LOGN1;
@@ -914,8 +916,8 @@ __device__ __forceinline__ void regpair_slots(const RegPair<QZ>& rp, int q, floa
         if (e >= 2) w = sel2(rp.sp, rot16(make_float2(1.f, 0.f), 2 * e - 3), w);  // W_16^1, W_16^3
       }
       const bool s0 = spg && e == 0 && rp.sp;
-      float2 A, Bc;
-      real_unpack(s0, zp, zq, w, A, Bc);
+      float2 A = make_float2(0.f, 0.f), Bc = A;
+      if constexpr (UNPACK) real_unpack(s0, zp, zq, w, A, Bc);
       f(4 * g + e, s0, A, Bc);
       if constexpr (REPACK) {
         real_repack(s0, A, Bc, w, zp, zq);
@@ -955,6 +957,17 @@ __device__ __forceinline__ void regpair_fwd_slots(const float2* sub, int q, int 
     regpair_last_fwd(sub, rp, tw, v);
     regpair_slots<LOGN1, false, REPACK>(rp, q, v, tw, f);
   }
+}
+
+// Repack of slot values that f supplies (no forward pass, nothing unpacked)
+// into the butterfly registers, for a pair index q known only at run time.
+template <int LOGN1, class F>
+__device__ __forceinline__ void regpair_set_slots(int q, int tl, const float2* __restrict__ tw, float2 (&v)[4][4],
+                                                  F&& f) {
+  if (q == 0)
+    regpair_slots<LOGN1, true, true, false>(RegPair<true>(tl), q, v, tw, f);
+  else
+    regpair_slots<LOGN1, false, true, false>(RegPair<false>(tl), q, v, tw, f);
 }
 
 // The inverse transform of a row pair held in registers: first pass into the
@@ -1043,8 +1056,9 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
 // (in: column-transformed k; out: gk pre-image).  grid = H * N1/2.  Two LDS
 // tiles: G and X of one batch row are transformed side by side and the gk
 // correlation accumulates over the batch in registers.  The two tiles (2 x 17
-// KB per 2-wave workgroup at N2 = 1024) allow 4 workgroups per CU, i.e. 2
-// waves per SIMD, whatever the register count: the occupancy hint says so.
+// KB per 2-wave workgroup) allow 4 workgroups per CU, i.e. 2 waves per SIMD,
+// whatever the register count: the occupancy hint says so.  Rows of 1024 take
+// the register-pair path with one tile.
 template <int LOGN1, int LOGN2>
 __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_eu(2))) void row_bwd_kernel(
     float2* __restrict__ wsg, const float2* __restrict__ wsx, float2* __restrict__ wsk, int B, int H,
@@ -1053,10 +1067,57 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
   using RS = RowSlots<LOGN1, LOGN2>;
   constexpr int64_t N = int64_t(1) << (LOGN1 + LOGN2);
   __shared__ float2 ldsG[C::TILE_P];
-  __shared__ float2 ldsX[C::TILE_P];
+  __shared__ float2 ldsX[LOGN2 == kRegPairLogN2 ? 1 : C::TILE_P];  // the register-pair path needs one tile
   const int q = blockIdx.x % ((1 << LOGN1) / 2);
   const int h = blockIdx.x / ((1 << LOGN1) / 2);
   float2 hA[C::SLOTS], hB[C::SLOTS], qA[C::SLOTS], qB[C::SLOTS];
+  if constexpr (LOGN2 == kRegPairLogN2) {
+    // One tile, spectral slots in registers (RegPair): per batch row X's slots
+    // are held while G is transformed; the gk correlation accumulates over the
+    // batch in slot registers (fixed order b = 0, 1, ...) and is repacked and
+    // inverted after the loop.  Its ~170 live VGPRs keep it at 2 waves per
+    // SIMD (capped at 3 it spilled 88 bytes per lane and ran slower); it gains
+    // from the fewer tile round trips.  Measured at B=4 D=1024 L=K=2^18 bf16:
+    // backward 12.57 -> 12.10-12.15 ms.
+    constexpr int N1 = 1 << LOGN1;
+    const int ra = q, rb = (q == 0) ? N1 / 2 : N1 - q;
+    const int tl = opaque_tid();
+    float2 v[4][4], xA[C::SLOTS], xB[C::SLOTS];
+    auto head = [&](const float2* sig) {
+      auto ld = [&](int m, int n) -> float2 { return sig[int64_t(m == 0 ? ra : rb) * C::N2 + n]; };
+      rows1024_fwd_head<2, C::T>(ldsG, ld, tw);
+    };
+    head(wsk + int64_t(h) * N);
+    regpair_fwd_slots<LOGN1, false>(ldsG, q, tl, tw, v, [&](int i, bool, float2& A, float2& Bc) {
+      hA[i] = A;
+      hB[i] = Bc;
+      qA[i] = qB[i] = make_float2(0.f, 0.f);
+    });
+    for (int b = 0; b < B; ++b) {
+      float2* sigg = wsg + (int64_t(b) * H + h) * N;
+      head(wsx + (int64_t(b) * H + h) * N);
+      regpair_fwd_slots<LOGN1, false>(ldsG, q, tl, tw, v, [&](int i, bool, float2& A, float2& Bc) {
+        xA[i] = A;
+        xB[i] = Bc;
+      });
+      head(sigg);
+      regpair_fwd_slots<LOGN1, true>(ldsG, q, tl, tw, v, [&](int i, bool s0, float2& A, float2& Bc) {
+        qA[i] = cadd(qA[i], slot_mulc(s0, A, xA[i]));
+        qB[i] = cadd(qB[i], cmulc(Bc, xB[i]));
+        A = slot_mulc(s0, A, hA[i]);
+        Bc = cmulc(Bc, hB[i]);
+      });
+      RowStore<C::N2> st{sigg, ra, rb};
+      regpair_inverse<2, C::T>(ldsG, ldsG, q, tl, v, st, tw);
+    }
+    regpair_set_slots<LOGN1>(q, tl, tw, v, [&](int i, bool, float2& A, float2& Bc) {
+      A = qA[i];
+      Bc = qB[i];
+    });
+    RowStore<C::N2> st{wsk + int64_t(h) * N, ra, rb};
+    regpair_inverse<2, C::T>(ldsG, ldsG, q, tl, v, st, tw);
+    return;
+  }
   row_pair_fft<LOGN1, LOGN2>(ldsG, wsk + int64_t(h) * N, q, tw);
   {
     const RS rs(q, tw);
