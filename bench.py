@@ -273,7 +273,8 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
         x = torch.randn(B, 3 * C, L, device=dev, generator=gen).to(torch.bfloat16)
         wp = torch.randn(3 * C, Kp, device=dev, generator=gen)
         wm = torch.randn(C, Km, device=dev, generator=gen) / Km ** 0.5
-        phase, dtype = "fwd", "f32"
+        # fp32 accumulation; the k=128 mixer's products are three bf16 products of split operands
+        phase, dtype = "fwd", "f32 (bf16x3 mixer products)"
         nbytes = algorithmic_bytes_b2b(B, C, L, Kp, Km, 2)
         desc = "cfg2: B2B short-conv block fwd (k=3 proj -> gate -> k=128 mixer -> gate), B=4 L=8192 D=4096, bf16 I/O"
 

@@ -12,6 +12,9 @@
 //   h   = causal_conv(z; w_mixer) + skip * z      (mixer conv with skip)
 //   out = q * h                                   (post-gate)
 // The forward is one pass over HBM: 3 input rows read, 1 output row written.
+#include <cstdlib>
+#include <type_traits>
+
 #include "direct_conv.h"
 
 namespace nsq {
@@ -916,9 +919,13 @@ __global__ void b2b_wgrad_reduce_kernel(const float* __restrict__ part, int npar
 constexpr int kB2BWsThreads = 512;
 constexpr int kB2BWsSegTiles = 8;
 
-template <int NS>
+// BF (16-bit I/O): z is stored as two bf16 halves (hi, lo; ToeplitzMfmaBf16),
+// ZE padded elements each, in the words of one z buffer.
+template <int NS, bool BF = false>
 struct B2BWsLds {
-  static constexpr int ZWORDS = (conv_pad_words(mfma_src_count<NS>()) + 7) & ~7;
+  static constexpr int ZCOUNT = BF ? kConvTile + 32 * bf16_steps<NS>() - 16 : mfma_src_count<NS>();
+  static constexpr int ZE = (bpad_elems(ZCOUNT) + 15) & ~15;
+  static constexpr int ZWORDS = BF ? ZE : (conv_pad_words(mfma_src_count<NS>()) + 7) & ~7;
   static constexpr int QWORDS = kConvTile + kConvTile / 4;  // qs_pad layout
   static constexpr int z0 = 0, q0 = 2 * ZWORDS, wm = 2 * ZWORDS + 2 * QWORDS;
   static constexpr int total = wm + kConvMaxK;
@@ -939,14 +946,14 @@ __device__ __forceinline__ void conv4_from_window(float (&out)[kConvPer], const 
   }
 }
 
-template <int DT, int NS, bool AL>
+template <int DT, int NS, bool AL, bool BF = false>
 __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typename Elem<DT>::T* __restrict__ x,
                                                                     const float* __restrict__ wp,
                                                                     const float* __restrict__ wm,
                                                                     const float* __restrict__ skip,
                                                                     typename Elem<DT>::T* __restrict__ y, int B, int C,
                                                                     int L, int Kp, int Km) {
-  using LY = B2BWsLds<NS>;
+  using LY = B2BWsLds<NS, BF>;
   using ET = typename Elem<DT>::T;
   extern __shared__ __align__(16) float smem[];
   float* const zbuf = smem + LY::z0;  // buffer u: zbuf + u * ZWORDS
@@ -956,15 +963,38 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
   const int ntiles = (L + kConvTile - 1) / kConvTile;
   const int g_begin = int(blockIdx.y) * kB2BWsSegTiles;
   const int g_end = min(B * ntiles, g_begin + kB2BWsSegTiles);
-  const int d = ((Km - 1 + 3) & ~3) + 1 - Km;  // leading zero taps of the band
+  // leading zero taps of the band: the halo hz = Km - 1 + d is a multiple of 4
+  // (fp32 words) or 8 (bf16 halves), so a tile's z starts on a 16-byte boundary
+  const int d = BF ? ((Km - 1 + 7) & ~7) + 1 - Km : ((Km - 1 + 3) & ~3) + 1 - Km;
   const int hz = Km - 1 + d;
   const int t = int(threadIdx.x);
   const bool producer = t >= kB2BWsThreads / 2;
-  constexpr int ZW = mfma_src_count<NS>();
+  // z of position m of buffer zb (float words of that buffer)
+  auto zput = [&](float* zb, int m, float v) {
+    if constexpr (BF) {
+      __bf16* zh = reinterpret_cast<__bf16*>(zb);
+      __bf16 hi, lo;
+      split_bf16(v, hi, lo);
+      zh[bpad(m)] = hi;
+      zh[LY::ZE + bpad(m)] = lo;
+    } else {
+      zb[conv_pad(m)] = v;
+    }
+  };
+  auto zcopy = [&](float* zb, int m, const float* zo, int mo) {
+    if constexpr (BF) {
+      __bf16* zh = reinterpret_cast<__bf16*>(zb);
+      const __bf16* oh = reinterpret_cast<const __bf16*>(zo);
+      zh[bpad(m)] = oh[bpad(mo)];
+      zh[LY::ZE + bpad(m)] = oh[LY::ZE + bpad(mo)];
+    } else {
+      zb[conv_pad(m)] = zo[conv_pad(mo)];
+    }
+  };
   if (t < kConvThreads) stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
-  for (int m = kConvTile + hz + t; m < ZW; m += kB2BWsThreads) {
-    zbuf[conv_pad(m)] = 0.f;
-    zbuf[LY::ZWORDS + conv_pad(m)] = 0.f;
+  for (int m = kConvTile + hz + t; m < LY::ZCOUNT; m += kB2BWsThreads) {
+    zput(zbuf, m, 0.f);
+    zput(zbuf + LY::ZWORDS, m, 0.f);
   }
   // q row of batch b; k and v rows follow at C*L and 2*C*L
   auto qrow = [&](int b) -> const ET* { return x + (int64_t(b) * 3 * C + c) * L; };
@@ -1003,13 +1033,27 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
       float zv[kConvPer];
 #pragma unroll
       for (int e = 0; e < kConvPer; ++e) zv[e] = (n + e < L) ? ka[e] * va[e] : 0.f;
-      *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt)) = make_float4(zv[0], zv[1], zv[2], zv[3]);
-      *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt + 4)) = make_float4(zv[4], zv[5], zv[6], zv[7]);
+      if constexpr (BF) {
+        nsq_bf16x8_t h8, l8;
+#pragma unroll
+        for (int e = 0; e < kConvPer; ++e) {
+          __bf16 hi, lo;
+          split_bf16(zv[e], hi, lo);
+          h8[e] = hi;
+          l8[e] = lo;
+        }
+        __bf16* zh = reinterpret_cast<__bf16*>(zb);
+        *reinterpret_cast<nsq_bf16x8_t*>(zh + bpad(hz + 8 * pt)) = h8;
+        *reinterpret_cast<nsq_bf16x8_t*>(zh + LY::ZE + bpad(hz + 8 * pt)) = l8;
+      } else {
+        *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt)) = make_float4(zv[0], zv[1], zv[2], zv[3]);
+        *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt + 4)) = make_float4(zv[4], zv[5], zv[6], zv[7]);
+      }
       float* qd = qb + qs_pad(8 * pt);
       *reinterpret_cast<float4*>(qd) = make_float4(qa[0], qa[1], qa[2], qa[3]);
       *reinterpret_cast<float4*>(qd + 4) = make_float4(qa[4], qa[5], qa[6], qa[7]);
       if (ti == 0) {
-        if (pt < hz) zb[conv_pad(pt)] = 0.f;  // causal padding before the row start
+        if (pt < hz) zput(zb, pt, 0.f);  // causal padding before the row start
       } else if (g == g_begin) {
         if (8 * pt < hz) {  // z at n0 - hz + m, m < hz
           const ET* xq = qrow(b);
@@ -1022,11 +1066,11 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
           conv4_from_window(vh, hv, wv4);
 #pragma unroll
           for (int e = 0; e < kConvPer; ++e)
-            if (8 * pt + e < hz) zb[conv_pad(8 * pt + e)] = kh[e] * vh[e];
+            if (8 * pt + e < hz) zput(zb, 8 * pt + e, kh[e] * vh[e]);
         }
       } else {
         const float* zo = zbuf + ob * LY::ZWORDS;
-        if (pt < hz) zb[conv_pad(pt)] = zo[conv_pad(kConvTile + pt)];
+        if (pt < hz) zcopy(zb, pt, zo, kConvTile + pt);
       }
       if (more) {
         cq = nq; ck = nk; cv = nv;
@@ -1041,7 +1085,8 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
     }
   } else {
     __syncthreads();  // weights staged, first tile produced
-    ToeplitzMfma<NS> tm;
+    using TM = std::conditional_t<BF, ToeplitzMfmaBf16<bf16_steps<NS>()>, ToeplitzMfma<NS>>;
+    TM tm;
     tm.load_weights(wlm, Km, skip ? skip[c] : 0.f, d);
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
     for (int g = g_begin; g < g_end; ++g) {
@@ -1051,7 +1096,12 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
       const float* zb = zbuf + cb * LY::ZWORDS;
       const float* qb = qbuf + cb * LY::QWORDS;
       nsq_f32x4_t acc0, acc1;
-      tm.run2(zb, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      if constexpr (BF) {
+        const __bf16* zh = reinterpret_cast<const __bf16*>(zb);
+        tm.run2(zh, zh + LY::ZE, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      } else {
+        tm.run2(zb, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      }
       const int n0 = ti * kConvTile;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -1219,17 +1269,28 @@ static void launch_b2b_fwd_mfma(const void* x, const float* wp, const float* wm,
   const size_t lds = size_t(B2BMfmaLds<NS>(Kp, Km).total) * sizeof(float);
   if (Kp <= 4) {
     // wave-specialized kernel; vector window loads when every row starts 16-byte aligned
-    constexpr int ES = int(sizeof(ET));
     const bool al = L % (DT == NSQ_DTYPE_F32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
     dim3 gws(C, unsigned(ceil_div(int64_t(B) * ceil_div(L, kConvTile), kB2BWsSegTiles)));
-    const size_t lws = size_t(B2BWsLds<NS>::total) * sizeof(float);
-    (void)ES;
-    if (al)
-      hipLaunchKernelGGL((b2b_fwd_ws_kernel<DT, NS, true>), gws, dim3(kB2BWsThreads), lws, st, (const ET*)x, wp, wm,
-                         skip, (ET*)y, B, C, L, Kp, Km);
+    // 16-bit I/O: the mixer's products as three bf16 products (ToeplitzMfmaBf16);
+    // NSQ_B2B_BF16_SPLIT=0 keeps the fp32 matrix-core band for every dtype
+    static const bool split_env = [] {
+      const char* e = std::getenv("NSQ_B2B_BF16_SPLIT");
+      return !(e && e[0] == '0');
+    }();
+    auto go = [&](auto bf) {
+      constexpr bool BF = decltype(bf)::value;
+      const size_t lws = size_t(B2BWsLds<NS, BF>::total) * sizeof(float);
+      if (al)
+        hipLaunchKernelGGL((b2b_fwd_ws_kernel<DT, NS, true, BF>), gws, dim3(kB2BWsThreads), lws, st, (const ET*)x,
+                           wp, wm, skip, (ET*)y, B, C, L, Kp, Km);
+      else
+        hipLaunchKernelGGL((b2b_fwd_ws_kernel<DT, NS, false, BF>), gws, dim3(kB2BWsThreads), lws, st, (const ET*)x,
+                           wp, wm, skip, (ET*)y, B, C, L, Kp, Km);
+    };
+    if (DT != NSQ_DTYPE_F32 && split_env)
+      go(std::true_type{});
     else
-      hipLaunchKernelGGL((b2b_fwd_ws_kernel<DT, NS, false>), gws, dim3(kB2BWsThreads), lws, st, (const ET*)x, wp, wm,
-                         skip, (ET*)y, B, C, L, Kp, Km);
+      go(std::false_type{});
   } else {
     hipLaunchKernelGGL((b2b_fwd_mfma_kernel<DT, NS, false, true>), grid, dim3(kConvThreads), lds, st, (const ET*)x,
                        wp, wm, skip, (ET*)y, C, L, Kp, Km);

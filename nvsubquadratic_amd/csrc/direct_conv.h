@@ -285,6 +285,83 @@ struct ToeplitzMfma {
   }
 };
 
+// ---------------------------------------------------------------------------
+// The same banded Toeplitz product on v_mfma_f32_16x16x32_bf16, for 16-bit
+// I/O: src and the taps are split into bf16 halves, v = hi + lo with hi =
+// bf16(v) and lo = bf16(v - hi) (16 mantissa bits together), and each 32-column
+// step runs three products hi*hi + hi*lo + lo*hi with fp32 accumulation: a
+// product's relative error is ~2^-17 (the dropped lo*lo term and lo's rounding),
+// far below the 2^-9 of the 16-bit output it feeds, at 16x the fp32 MFMA rate
+// per product.  Lane layout (checked on MI355X with integer operands): lane l
+// supplies A[l % 16][8 (l / 16) + e] and B[8 (l / 16) + e][l % 16], e < 8, and
+// receives D[4 (l / 16) + r][l % 16] -- the accumulator of the fp32 form.
+// src halves are bf16 arrays with an 8-element pad after every 16 (bpad): a
+// lane's 8 values of one step are one 16-byte read, and the 16 lanes of a
+// read phase (blocks a .. a+15, 48 bytes apart) cover the 64 banks once.
+// ---------------------------------------------------------------------------
+typedef __bf16 nsq_bf16x8_t __attribute__((ext_vector_type(8)));
+
+__host__ __device__ __forceinline__ constexpr int bpad(int m) { return m + 8 * (m >> 4); }
+// Padded bf16 elements holding src[0, count).
+constexpr int bpad_elems(int count) { return bpad(((count + 15) / 16) * 16); }
+
+// v = hi + lo (bf16 halves, round to nearest even each).
+__device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
+  hi = static_cast<__bf16>(v);
+  lo = static_cast<__bf16>(v - static_cast<float>(hi));
+}
+
+// S32 steps of 32 window columns: 32 * S32 >= K + 15.
+template <int S32>
+struct ToeplitzMfmaBf16 {
+  nsq_bf16x8_t bh[S32], bl[S32];
+  // As ToeplitzMfma::load_weights: tap j of the band is wl[j - shift], tap K-1
+  // of wl gets last_add; T[t][i] = band[t - i], t = 32 s + 8 (l / 16) + e.
+  __device__ __forceinline__ void load_weights(const float* wl, int K, float last_add = 0.f, int shift = 0) {
+    const int l = int(threadIdx.x) & 63, kk = l >> 4, i = l & 15;
+#pragma unroll
+    for (int s = 0; s < S32; ++s) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = 32 * s + 8 * kk + e - i - shift;
+        const bool ok = j >= 0 && j < K;
+        const float v = ok ? wl[ok ? j : 0] + (j == K - 1 ? last_add : 0.f) : 0.f;
+        __bf16 h, lo;
+        split_bf16(v, h, lo);
+        bh[s][e] = h;
+        bl[s][e] = lo;
+      }
+    }
+  }
+  // Two M-tiles (blocks a0.. and a1..) of the padded bf16 src halves zh, zl:
+  // c = the lane's four outputs of each (as ToeplitzMfma::run2).
+  __device__ __forceinline__ void run2(const __bf16* zh, const __bf16* zl, int a0, int a1, nsq_f32x4_t& c0,
+                                       nsq_f32x4_t& c1) const {
+    const int l = int(threadIdx.x) & 63, kk = l >> 4, a = l & 15;
+    // bpad(16 (a0 + a) + 32 s + 8 kk) = bpad(16 (a0 + a) + 8 kk) + 48 s
+    const int o0 = bpad(16 * (a0 + a) + 8 * kk), o1 = bpad(16 * (a1 + a) + 8 * kk);
+    c0 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    c1 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < S32; ++s) {
+      const nsq_bf16x8_t h0 = *reinterpret_cast<const nsq_bf16x8_t*>(zh + o0 + 48 * s);
+      const nsq_bf16x8_t h1 = *reinterpret_cast<const nsq_bf16x8_t*>(zh + o1 + 48 * s);
+      const nsq_bf16x8_t g0 = *reinterpret_cast<const nsq_bf16x8_t*>(zl + o0 + 48 * s);
+      const nsq_bf16x8_t g1 = *reinterpret_cast<const nsq_bf16x8_t*>(zl + o1 + 48 * s);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, bh[s], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, bh[s], c1, 0, 0, 0);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, bl[s], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, bl[s], c1, 0, 0, 0);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g0, bh[s], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g1, bh[s], c1, 0, 0, 0);
+    }
+  }
+};
+// bf16 steps for the fp32 form's NS (12, 20, 36, 68 -> 2, 3, 5, 9): covers
+// K <= 4 NS - 15 taps plus up to 7 leading zero taps.
+template <int NS>
+constexpr int bf16_steps() { return (NS + 4) / 8; }
+
 // Tile geometry of the MFMA path: kConvTile outputs = kConvTile / 16 blocks,
 // in M-tiles of 16 blocks spread over the workgroup's waves.
 constexpr int kMfmaBlocks = kConvTile / 16;

@@ -312,3 +312,29 @@ def test_module_matches_reference_conv(C, L, K):
     torch.testing.assert_close(xg.grad.cpu(), x.grad, atol=1e-2, rtol=1e-3)
     torch.testing.assert_close(fast.weight.grad.cpu(), ref.weight.grad, atol=1e-2, rtol=1e-3)
     torch.testing.assert_close(fast.bias.grad.cpu(), ref.bias.grad, atol=1e-2, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 4e-3), (torch.float16, 5e-4)])
+@pytest.mark.parametrize("Km", [16, 33, 34, 65, 66, 128, 129, 256])
+def test_b2b_16bit_io_mixer_as_bf16_products(dtype, tol, Km):
+    """16-bit I/O runs the B2B mixer on v_mfma_f32_16x16x32_bf16 with z and the taps split into bf16
+    halves (three products per step, ~2^-17 relative per product).  Against float64 of the same
+    16-bit inputs the error is the output rounding: ~1e-3 (bf16) and ~1.5e-4 (fp16) rel-L2; a band
+    or split mistake (a lost lo term alone is ~2^-9) fails the fp16 bound.  Tap counts on both sides
+    of every band step boundary, ragged length, nonzero skip, the row start and a tile halo."""
+    torch.manual_seed(200 + Km)
+    B, C, L = 3, 5, 4500
+    x = torch.randn(B, 3 * C, L).to(dtype)
+    wp = torch.randn(3 * C, 3) / 3 ** 0.5
+    wm = torch.randn(C, Km) / Km ** 0.5
+    sk = torch.randn(C)
+    p = causal_conv1d_torch(x.double(), wp.double())
+    q, k, v = p[:, :C], p[:, C:2 * C], p[:, 2 * C:]
+    z = k * v
+    y64 = q * (causal_conv1d_torch(z, wm.double()) + sk.double().view(1, C, 1) * z)
+    y = b2b_causal_conv1d(x.cuda(), wp.cuda(), wm.cuda(), sk.cuda())
+    assert y.dtype == dtype
+    y = y.double().cpu()
+    assert rel_l2(y64, y) < tol
+    assert rel_l2(y64[..., :Km + 3], y[..., :Km + 3]) < tol
+    assert rel_l2(y64[..., 2048:2048 + Km], y[..., 2048:2048 + Km]) < tol
