@@ -21,16 +21,20 @@
 //      packed column 0 separates its DC and Nyquist columns with the pairing
 //      of k and -k (k = 2m <-> 2(-m mod 128), k = 2m+1 <-> 2(127-m)+1);
 //   C  inverse real FFTs of the kept rows, window [o2, o2 + S2), epilogue.
-// A column's two halves run one after the other on the same threads, which
+// A column's two halves run one after the other on the same lanes, which
 // keep the column's values for the second half, the first half's result and
 // the next half's filter values (issued ahead, so their L2 latency overlaps a
 // DFT): ~250 VGPRs.  With 1024 threads (128 VGPRs each) that spilled 320 bytes
 // per lane, so the workgroup has 512 threads (2 waves per SIMD) and phase B
 // takes the columns in two rounds of 64.
-// Measured on MI355X, config 4 (B=16 C=384 128^2, bf16): 0.99 ms for the
-// kernel, 1.037 ms with the filter spectrum, against 1.153 ms for the three
-// passes.  One workgroup per CU with barrier-separated phases keeps the VALU
-// ~27% busy (about 41 us per image against ~11 us of VALU issue).
+// Every wave owns whole lines: 8 columns in each round of phase B (8 lanes per
+// column), 16 rows in phases A and C (8 lanes per row), so the DFT exchanges
+// rely on the wave's in-order LDS operations and an image takes two
+// workgroup barriers (after A and after B).
+// Measured on MI355X, config 4 (B=16 C=384 128^2, bf16): 0.864 ms for the
+// kernel, 0.865-0.873 ms per call with the filter spectrum, against 1.145 ms
+// for the three passes; VALU 44% busy, LDS 33% busy: the latency of 2 waves
+// per SIMD bounds it.
 // HBM traffic per image is x in, y out and the channel's filter spectrum,
 // which the images of a channel read from their XCD's L2: workgroup w runs on
 // XCD w % 8 and the images of a channel take consecutive slots there.
@@ -58,10 +62,11 @@ __device__ __forceinline__ void img_of(int w, int B, int H, int& b, int& h) {
   }
 }
 
-// The per-column state of phase B: in round q (q < 2) thread t owns column
-// col = 64 q + t % 64 and first-pass butterfly jb = t / 64 of its 128-point
-// DFTs (TMAJOR passes: the 64 lanes of a wave read 64 consecutive columns of
-// one tile row).
+// The per-column state of phase B: in round q (q < 2) wave w owns the 8
+// columns col = 64 q + 8 w + (lane & 7), and lane l runs butterfly
+// jb = l >> 3 of its column's 128-point DFTs.  A column's 8 lanes sit in one
+// wave, so its exchanges need only the wave's own LDS ordering (img_wave_sync),
+// never a workgroup barrier.
 struct ImgCol {
   int col, jb;
 };
@@ -69,30 +74,130 @@ struct ImgCol {
 // Element n of column col in the tile (rows of kImgRS, pad16 inside a row).
 __device__ __forceinline__ float2& img_at(float2* tile, int n, int col) { return tile[n * kImgRS + pad16(col)]; }
 
-// Forward 128-point DFT of the thread's column inputs v[r] = c[jb + 8 r]
-// (r < 16): radix 16 in registers, exchange through the column's slots,
-// radix 8; leaves X[jj + 16 r] (r < 8) of the butterflies jj = 2 jb + q
-// (q < 2) in xo[q][r].  Starts and ends with a barrier.
-__device__ __forceinline__ void img_col_dft_fwd(float2* tile, const ImgCol& ic, float2 (&v)[16], float2 (&xo)[2][8],
-                                                const float2* __restrict__ tw) {
-  dft<16, false>(v);  // first pass: outputs at 16 jb + r
-  __syncthreads();
+// LDS operations of one wave take effect in program order; this keeps the
+// compiler from moving a lane's slot reads above its neighbours' slot writes.
+__device__ __forceinline__ void img_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Exchange slot n (0..127) of a column lives in tile row
+//   e(n) = (n & ~3) | ((gray(n & 3) ^ h(n >> 2)) & 3),  h(m) = (m >> 2) + 2 (m & 1),
+// a permutation inside each aligned quad of rows.  The tile's row stride
+// (136 complex = 272 words) moves a row 16 banks, so only e(n) mod 4 picks a
+// lane group's banks; e(n) gives the 8 lanes of a column distinct values mod 4
+// (and alternating parity) in every exchange pattern of the DFTs below
+// (n = 16 jb + K, 2 jb + q + 16 r, jb + 8 r), so a wave's 8 columns x 8 lanes
+// cover all banks once per 8-byte access.  The three patterns reduce to four
+// per-lane row pointers and a constant offset per slot.
+__device__ __forceinline__ constexpr int img_gray2(int x) { return (x ^ (x >> 1)) & 3; }
+__device__ __forceinline__ int img_swz(int n) {
+  const int h = (n >> 4) + 2 * ((n >> 2) & 1);
+  return (n & ~3) | ((img_gray2(n & 3) ^ h) & 3);
+}
+struct ImgSlots {
+  float2* p[4];
+  __device__ __forceinline__ ImgSlots(float2* tile, int col, int base, int l) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) img_at(tile, 16 * ic.jb + r, ic.col) = v[r];
-  __syncthreads();
+    for (int c = 0; c < 4; ++c) p[c] = tile + (base + (c ^ l)) * kImgRS + pad16(col);
+  }
+};
+// n = 16 jb + K (K < 16): row 16 jb + (K & 12) + (cK ^ (jb & 3))
+__device__ __forceinline__ ImgSlots img_slots_w(float2* tile, const ImgCol& ic) {
+  return ImgSlots(tile, ic.col, 16 * ic.jb, ic.jb & 3);
+}
+__device__ __forceinline__ float2& img_w(const ImgSlots& s, int K) {
+  return s.p[img_gray2(K & 3) ^ (2 * ((K >> 2) & 1))][(K & 12) * kImgRS];
+}
+// n = 2 jb + q + 16 r: row 16 r + 4 (jb >> 1) + (((q ^ r) & 3) ^ L)
+__device__ __forceinline__ ImgSlots img_slots_r1(float2* tile, const ImgCol& ic) {
+  return ImgSlots(tile, ic.col, 4 * (ic.jb >> 1), (3 * (ic.jb & 1)) ^ (2 * ((ic.jb >> 1) & 1)));
+}
+__device__ __forceinline__ float2& img_r1(const ImgSlots& s, int q, int r) { return s.p[(q ^ r) & 3][16 * r * kImgRS]; }
+// n = jb + 8 r: row 8 r + 4 (jb >> 2) + (((r >> 1) & 3) ^ L)
+__device__ __forceinline__ ImgSlots img_slots_r2(float2* tile, const ImgCol& ic) {
+  return ImgSlots(tile, ic.col, 4 * (ic.jb >> 2), img_gray2(ic.jb & 3) ^ (2 * (ic.jb >> 2)));
+}
+__device__ __forceinline__ float2& img_r2(const ImgSlots& s, int r) { return s.p[(r >> 1) & 3][8 * r * kImgRS]; }
+
+// Slot access policies of the 128-point DFTs below: slots_w() gives slot
+// 16 jb + K, slots_r1() slot 2 jb + q + 16 r, slots_r2() slot jb + 8 r.
+// ImgColX: a phase-B column (rows permuted by img_swz).
+struct ImgColX {
+  float2* tile;
+  ImgCol ic;
+  int jb;
+  struct W {
+    ImgSlots s;
+    __device__ __forceinline__ float2& operator()(int K) const { return img_w(s, K); }
+  };
+  struct R1 {
+    ImgSlots s;
+    __device__ __forceinline__ float2& operator()(int q, int r) const { return img_r1(s, q, r); }
+  };
+  struct R2 {
+    ImgSlots s;
+    __device__ __forceinline__ float2& operator()(int r) const { return img_r2(s, r); }
+  };
+  __device__ __forceinline__ W slots_w() const { return {img_slots_w(tile, ic)}; }
+  __device__ __forceinline__ R1 slots_r1() const { return {img_slots_r1(tile, ic)}; }
+  __device__ __forceinline__ R2 slots_r2() const { return {img_slots_r2(tile, ic)}; }
+};
+// ImgRowX: a tile row in its natural layout (element n at pad16(n)); the
+// slots of a pattern are constant offsets from one per-lane pointer.  With 8
+// rows per wave (lane = 8 row + jb) the 16 jb + K and jb + 8 r patterns are
+// free of bank conflicts and 2 jb + q + 16 r has 2-way conflicts.
+struct ImgRowX {
+  float2* row;
+  int jb;
+  struct W {
+    float2* b;
+    __device__ __forceinline__ float2& operator()(int K) const { return b[K]; }  // pad16(16 jb + K) = 17 jb + K
+  };
+  struct R1 {
+    float2* b;
+    __device__ __forceinline__ float2& operator()(int q, int r) const { return b[q + 17 * r]; }
+  };
+  struct R2 {
+    float2* b;
+    __device__ __forceinline__ float2& operator()(int r) const { return b[8 * r + (r >> 1)]; }
+  };
+  __device__ __forceinline__ W slots_w() const { return {row + 17 * jb}; }
+  __device__ __forceinline__ R1 slots_r1() const { return {row + 2 * jb}; }
+  __device__ __forceinline__ R2 slots_r2() const { return {row + jb}; }
+};
+
+// Forward 128-point DFT of the thread's inputs v[r] = c[jb + 8 r] (r < 16):
+// radix 16 in registers, exchange through the line's slots (SX: ImgColX or
+// ImgRowX), radix 8; leaves X[jj + 16 r] (r < 8) of the butterflies
+// jj = 2 jb + q (q < 2) in xo[q][r].  The line's earlier slot reads precede
+// it in the wave's program order.
+template <class SX>
+__device__ __forceinline__ void img_dft128_fwd(const SX& sx, float2 (&v)[16], float2 (&xo)[2][8],
+                                               const float2* __restrict__ tw) {
+  dft<16, false>(v);  // first pass: outputs at 16 jb + r
+  {
+    const auto sw = sx.slots_w();
+    img_wave_sync();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sw(r) = v[r];
+  }
+  img_wave_sync();
   const TwTable tt(tw);
+  const auto s1 = sx.slots_r1();
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int jj = 2 * ic.jb + q;  // second pass (NS = 16): butterfly jj reads jj + 16 r, k = jj
+    const int jj = 2 * sx.jb + q;  // second pass (NS = 16): butterfly jj reads jj + 16 r, k = jj
     float2 w[8];
     pass_twiddles<8>(tt, 128, jj, w);
 #pragma unroll
-    for (int r = 0; r < 8; ++r) xo[q][r] = img_at(tile, jj + 16 * r, ic.col);
+    for (int r = 0; r < 8; ++r) xo[q][r] = s1(q, r);
 #pragma unroll
     for (int r = 1; r < 8; ++r) xo[q][r] = cmul(xo[q][r], w[r]);
     dft<8, false>(xo[q]);  // outputs at jj + 16 r: natural order
   }
-  __syncthreads();
+  img_wave_sync();
 }
 
 // u[r] *= conj(W_128^{r k}), r = 1..15: the roots at r = 1, 2, 4, 8 are table
@@ -121,29 +226,35 @@ __device__ __forceinline__ void img_twiddle16_inv(float2 (&u)[16], const float2*
 }
 
 // Inverse 128-point DFT (unnormalised) of Y[jj + 16 r] in yv[q][r] (the
-// layout img_col_dft_fwd leaves): radix 8 in registers (first pass, butterfly
+// layout img_dft128_fwd leaves): radix 8 in registers (first pass, butterfly
 // jj reads jj + 16 r), exchange, radix 16 (butterfly jb reads jb + 8 r,
-// k = jb); leaves y[jb + 8 r] in u[r].  The caller's barrier precedes it;
-// ends with a barrier.
-__device__ __forceinline__ void img_col_dft_inv(float2* tile, const ImgCol& ic, float2 (&yv)[2][8], float2 (&u)[16],
-                                                const float2* __restrict__ tw) {
+// k = jb); leaves y[jb + 8 r] in u[r].
+template <class SX>
+__device__ __forceinline__ void img_dft128_inv(const SX& sx, float2 (&yv)[2][8], float2 (&u)[16],
+                                               const float2* __restrict__ tw) {
+  {
+    const auto sw = sx.slots_w();
+    img_wave_sync();
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int jj = 2 * ic.jb + q;
-    dft<8, true>(yv[q]);  // outputs at 8 jj + r
+    for (int q = 0; q < 2; ++q) {
+      dft<8, true>(yv[q]);  // outputs at 8 jj + r = 16 jb + 8 q + r
 #pragma unroll
-    for (int r = 0; r < 8; ++r) img_at(tile, 8 * jj + r, ic.col) = yv[q][r];
+      for (int r = 0; r < 8; ++r) sw(8 * q + r) = yv[q][r];
+    }
   }
-  __syncthreads();
+  img_wave_sync();
+  {
+    const auto s2 = sx.slots_r2();
 #pragma unroll
-  for (int r = 0; r < 16; ++r) u[r] = img_at(tile, ic.jb + 8 * r, ic.col);
-  img_twiddle16_inv(u, tw, ic.jb);
+    for (int r = 0; r < 16; ++r) u[r] = s2(r);
+  }
+  img_twiddle16_inv(u, tw, sx.jb);
   dft<16, true>(u);  // outputs at jb + 8 r
-  __syncthreads();
+  img_wave_sync();
 }
 
 // Filter values of one half (ODD: frequencies k = 2m + 1, else 2m) for the
-// thread's outputs m = 2 jb + q + 16 r of img_col_dft_fwd: Khat[k][col], and
+// thread's outputs m = 2 jb + q + 16 r of img_dft128_fwd: Khat[k][col], and
 // for the packed column 0 also Khat[-k][0].  Issued before the half's DFT so
 // their L2 latency overlaps it.
 template <bool ODD>
@@ -166,18 +277,19 @@ __device__ __forceinline__ void img_filter_load(const ImgCol& ic, const float2* 
 // Spectral product of one half with the values img_filter_load fetched.
 // Column 0 is the packed DC / Nyquist column: Y = Xd Kd + i Xn Kn with the
 // pairs of k and -k (pack_split); its partner values go through the column's
-// slots, so every thread takes the two barriers.
+// slots (lanes of one wave).
 template <bool ODD>
 __device__ __forceinline__ void img_col_product(float2* tile, const ImgCol& ic, float2 (&xo)[2][8],
                                                 const float2 (&kv)[2][8], const float2 (&km)[2][8]) {
   const bool c0 = ic.col == 0;
   if (c0) {
+    const ImgSlots s1 = img_slots_r1(tile, ic);
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int r = 0; r < 8; ++r) img_at(tile, 2 * ic.jb + q + 16 * r, 0) = xo[q][r];
+      for (int r = 0; r < 8; ++r) img_r1(s1, q, r) = xo[q][r];  // slot m = 2 jb + q + 16 r
   }
-  __syncthreads();
+  img_wave_sync();
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
 #pragma unroll
@@ -186,7 +298,7 @@ __device__ __forceinline__ void img_col_product(float2* tile, const ImgCol& ic, 
         const int m = 2 * ic.jb + q + 16 * r;
         const int mp = ODD ? 127 - m : (128 - m) & 127;  // -k
         float2 xd, xn, kd, kn;
-        pack_split(xo[q][r], img_at(tile, mp, 0), xd, xn);
+        pack_split(xo[q][r], img_at(tile, img_swz(mp), 0), xd, xn);
         pack_split(kv[q][r], km[q][r], kd, kn);
         xo[q][r] = cadd(cmul(xd, kd), mul_i(cmul(xn, kn)));
       } else {
@@ -194,7 +306,7 @@ __device__ __forceinline__ void img_col_product(float2* tile, const ImgCol& ic, 
       }
     }
   }
-  __syncthreads();
+  img_wave_sync();
 }
 
 // The image kernel.  kc: filter spectra [H][256][rsk] (the three-pass plan's
@@ -209,6 +321,7 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
                                                               int S0, int S2, int o0, int o2, float scale,
                                                               const float2* __restrict__ tw) {
   using ET = typename Elem<DT>::T;
+  static_assert(kImgT == 512, "phases A and C give each of the 8 waves 16 of the 128 rows");
   __shared__ float2 tile[kImgTile];
   int b, h;
   img_of(int(blockIdx.x), B, H, b, h);
@@ -220,19 +333,43 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
   // across phase B.
 
   // ---- A: real row FFTs (128 complex = 256 real points, samples >= S2 zero) ----
+  // Wave w owns rows 16 w .. 16 w + 15, 8 at a time (lane = 8 row + jb): the
+  // row DFTs and the unpack exchange only through the wave's own rows.
   {
     const int tid = opaque_tid();
-    auto ld = [&](int m, int n) -> float2 {
-      const bool ok = m < S0 && 2 * n < S2;
-      return load_pair_nb<DT, true>(xi + int64_t(ok ? m : 0) * S2, ok ? 2 * n : 0, ok ? S2 : 0);
-    };
-    HalfZeroLoad<16, true, decltype(ld)> ld1{ld};
-    LdsTile<kImgRS, true> st{tile};
-    fft<7, false, 128, kImgT, kImgRS>(tile, ld1, st, tw);
+    const int wv = tid >> 6, lane = tid & 63, jb = lane & 7;
 #pragma unroll
-    for (int i = 0; i < 8192 / kImgT; ++i) {  // unpack in place: slot (row m, p < 64) owns elements p and 128 - p (0: 0, 64)
-      const int sl = tid + i * kImgT;
-      const int m = sl >> 6, p = sl & 63;
+    for (int g = 0; g < 2; ++g) {
+      const int m = 16 * wv + 8 * g + (lane >> 3);
+      const ImgRowX rx{tile + m * kImgRS, jb};
+      float2 xo[2][8];
+      if (16 * wv + 8 * g >= S0) {  // zero-padding rows only (wave-uniform)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int r = 0; r < 8; ++r) xo[q][r] = make_float2(0.f, 0.f);
+      } else {
+        float2 v[16];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {  // complex sample n = jb + 8 r: x[m][2n], x[m][2n + 1]
+          const int n = jb + 8 * r;
+          const bool ok = m < S0 && 2 * n < S2;
+          v[r] = load_pair_nb<DT, true>(xi + int64_t(ok ? m : 0) * S2, ok ? 2 * n : 0, ok ? S2 : 0);
+        }
+#pragma unroll
+        for (int r = 8; r < 16; ++r) v[r] = make_float2(0.f, 0.f);  // n >= 64: the zero half
+        img_dft128_fwd(rx, v, xo, tw);
+      }
+      const auto s1 = rx.slots_r1();
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) s1(q, r) = xo[q][r];  // X[jj + 16 r], natural order
+    }
+    img_wave_sync();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {  // unpack in place: slot (row m, p < 64) owns elements p and 128 - p (0: 0, 64)
+      const int m = 16 * wv + i, p = lane;
       float2* z = tile + m * kImgRS;
       const bool p0 = p == 0;
       const int pb = p0 ? 64 : 128 - p;
@@ -245,10 +382,11 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
   }
 
   // ---- B: columns: two 128-point halves, product, inverse, combine, crop ----
-  constexpr int CPR = kImgT / 8;  // columns per round: 8 threads per column
+  constexpr int CPR = kImgT / 8;  // columns per round: 8 lanes per column, 8 columns per wave
   for (int round = 0; round < 128 / CPR; ++round) {
     const int tid = opaque_tid();
-    const ImgCol ic{CPR * round + tid % CPR, tid / CPR};
+    const ImgCol ic{CPR * round + 8 * (tid >> 6) + (tid & 7), (tid >> 3) & 7};
+    const ImgColX cx{tile, ic, ic.jb};
     const TwTable tt(tw);
     float2 c[16], v[16], ye[16];
     float2 xo[2][8], kv[2][8], km[2][8];
@@ -257,18 +395,18 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
     for (int r = 0; r < 16; ++r) c[r] = img_at(tile, ic.jb + 8 * r, ic.col);  // rows >= S0 are zero
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = c[r];
-    img_col_dft_fwd(tile, ic, v, xo, tw);
+    img_dft128_fwd(cx, v, xo, tw);
     img_col_product<false>(tile, ic, xo, kv, km);
     img_filter_load<true>(ic, kc, rsk, kv, km);
-    img_col_dft_inv(tile, ic, xo, ye, tw);
+    img_dft128_inv(cx, xo, ye, tw);
     float2 wt[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) wt[r] = tt.load(256, ic.jb + 8 * r);
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = cmul(c[r], wt[r]);  // c[n] W256^n
-    img_col_dft_fwd(tile, ic, v, xo, tw);
+    img_dft128_fwd(cx, v, xo, tw);
     img_col_product<true>(tile, ic, xo, kv, km);
-    img_col_dft_inv(tile, ic, xo, v, tw);
+    img_dft128_inv(cx, xo, v, tw);
     // y[n] = ye[p] + W256^-n yo[p] for the kept n = p or p + 128 in [o0, o0 + S0)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -283,16 +421,18 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
       const bool keep = n >= o0 && n < o0 + S0;
       if (keep) img_at(tile, n - o0, ic.col) = cadd(ye[r], cmulc(v[r], wt[r]));
     }
-    __syncthreads();
+    img_wave_sync();
   }
+  __syncthreads();
 
   // ---- C: inverse real row FFTs of the kept rows, window [o2, o2 + S2), epilogue ----
+  // Wave w again owns rows 16 w .. 16 w + 15 (as in A).
   {
     const int tid = opaque_tid();
+    const int wv = tid >> 6, lane = tid & 63, jb = lane & 7;
 #pragma unroll
-    for (int i = 0; i < 8192 / kImgT; ++i) {  // repack in place (three-pass plan's nd_row_inv, PACK)
-      const int sl = tid + i * kImgT;
-      const int m = sl >> 6, p = sl & 63;
+    for (int i = 0; i < 16; ++i) {  // repack in place (three-pass plan's nd_row_inv, PACK)
+      const int m = 16 * wv + i, p = lane;
       float2* z = tile + m * kImgRS;
       const bool p0 = p == 0;
       const int pb = p0 ? 64 : 128 - p;
@@ -304,28 +444,44 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
       z[pad16(p)] = zp;
       z[pad16(pb)] = zq;
     }
-    __syncthreads();
-    LdsTile<kImgRS, true> t{tile};
-    fft_rec<7, 0, true, 128, kImgT, false>(t, t, t, t, tw);
+    img_wave_sync();
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      if (16 * wv + 8 * g >= S0) continue;  // no output rows (wave-uniform)
+      const int m = 16 * wv + 8 * g + (lane >> 3);
+      const ImgRowX rx{tile + m * kImgRS, jb};
+      float2 yv[2][8], u[16];
+      const auto s1 = rx.slots_r1();
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) yv[q][r] = s1(q, r);
+      img_dft128_inv(rx, yv, u, tw);
+      const auto s2 = rx.slots_r2();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s2(r) = u[r];  // y[jb + 8 r], natural order
+    }
+    img_wave_sync();
     const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
     const int cpr = S2 >> 3;  // 8-sample chunks per output row
+    const int nr = min(16, S0 - 16 * wv);  // the wave's output rows
     const RowBuf<DT, false> ab(xi, HAS_S ? S0 * S2 : 0);
     const RowBuf<DT, true> ob(y + img, S0 * S2);
-    for (int ch = tid; ch < S0 * cpr; ch += kImgT) {
-      const int m = ch / cpr, c8 = (ch - m * cpr) * 8;
+    for (int ch = lane; ch < nr * cpr; ch += 64) {
+      const int mi = ch / cpr, m = 16 * wv + mi, c8 = (ch - mi * cpr) * 8;
       const int e0 = m * S2 + c8;
       Win8<DT, true> a;
       a.load(ab, e0);
       const float2* zr = tile + m * kImgRS;
       const int n0 = (c8 + o2) >> 1;
-      float yv[8];
+      float yo[8];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float2 z = zr[pad16(n0 + u)];
-        yv[2 * u] = epilogue<DT>(z.x * scale, HAS_S, sv, a.at(2 * u));
-        yv[2 * u + 1] = epilogue<DT>(z.y * scale, HAS_S, sv, a.at(2 * u + 1));
+        yo[2 * u] = epilogue<DT>(z.x * scale, HAS_S, sv, a.at(2 * u));
+        yo[2 * u + 1] = epilogue<DT>(z.y * scale, HAS_S, sv, a.at(2 * u + 1));
       }
-      store8<DT, true>(ob, e0, yv);
+      store8<DT, true>(ob, e0, yo);
     }
   }
 }
