@@ -419,15 +419,18 @@ __global__ __launch_bounds__(256) void nd_plane_fwd_kernel(const typename Elem<D
   // Store [F1][FH]; column 0 separates into the DC (j = 0) and Nyquist (j = N) bins.
   float2* out = ws + (plane / n0) * spec + (plane % n0) * int64_t(C::F1) * C::FH;
   const int tst = opaque_tid();
+  static_assert((C::F1 * N) % C::T == 0, "nd_plane_fwd_kernel: store batches");
 #pragma unroll 4
-  for (int e = tst; e < C::F1 * C::FH; e += C::T) {
-    const int k1 = e / C::FH, j = e - k1 * C::FH;
-    const bool edge = (j == 0) || (j == N);
-    const float2 v = P[k1 * RS + pad16(edge ? 0 : j)];
+  for (int e = tst; e < C::F1 * N; e += C::T) {  // bins 1 .. N-1 of each row as they are
+    const int k1 = e >> LOGN, j = e & (N - 1);
+    const float2 v = P[k1 * RS + pad16(j)];
+    if (j != 0) out[int64_t(k1) * C::FH + j] = v;
+  }
+  for (int k1 = tst; k1 < C::F1; k1 += C::T) {  // packed column 0 -> DC (j = 0) and Nyquist (j = N)
+    const float2 v = P[k1 * RS];
     const float2 zc = cconj(P[((C::F1 - k1) & (C::F1 - 1)) * RS]);
-    const float2 dc = cscale(cadd(v, zc), 0.5f);
-    const float2 ny = mul_neg_i(cscale(csub(v, zc), 0.5f));
-    out[int64_t(k1) * C::FH + j] = (j == 0) ? dc : ((j == N) ? ny : v);
+    out[int64_t(k1) * C::FH] = cscale(cadd(v, zc), 0.5f);
+    out[int64_t(k1) * C::FH + N] = mul_neg_i(cscale(csub(v, zc), 0.5f));
   }
 }
 
@@ -484,6 +487,9 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
   const ET* __restrict__ sh = (const ET*)o.s;
   const int h = int(bh % o.H);
   const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load(sh, h)) : 0.f;
+  // FAST epilogue: even window start, w2 a multiple of 8, 16-byte aligned rows.
+  const bool fast = (o.off2 & 1) == 0 && (o.w2 & 7) == 0 && o.w2 <= 2 * N &&
+                    ((reinterpret_cast<uintptr_t>(o.out) | (HAS_S ? reinterpret_cast<uintptr_t>(o.aux) : 0)) & 15) == 0;
   for (int r0 = 0; r0 < n1out; r0 += C::MR) {
 #pragma unroll
     for (int i = 0; i < C::SLOTS; ++i) {
@@ -504,6 +510,37 @@ __global__ __launch_bounds__(256) void nd_plane_inv_kernel(const float2* __restr
     // Epilogue over the tile's real samples: MR rows x w2 kept samples.
     const int nrows = (n1out - r0) < C::MR ? (n1out - r0) : C::MR;
     static_assert(GE == GATED_NONE || MODE == ND_OUT_Y, "nd_plane_inv_kernel: gates on y only");
+    if constexpr (MODE == ND_OUT_Y && GE == GATED_NONE) {
+      if (fast) {
+        // 8 consecutive kept samples per thread: four complex values from LDS,
+        // one 16-byte shortcut load, one 16-byte store.  Chunk ch of the tile
+        // is row ch / cpr (a float reciprocal: ch < 2^14, so the quotient's
+        // rounding error stays far below the 1 / (2 cpr) margin of ch + 1/2).
+        const int cpr = o.w2 >> 3;
+        const float rcpr = 1.f / float(cpr);
+        const int64_t row0 = plane * n1out + r0;
+        const RowBuf<DT, false> ab(aux + row0 * o.w2, HAS_S ? nrows * o.w2 : 0);
+        const RowBuf<DT, true> ob((ET*)o.out + row0 * o.w2, nrows * o.w2);
+        for (int ch = t; ch < nrows * cpr; ch += C::T) {
+          const int m = int((float(ch) + 0.5f) * rcpr), c8 = (ch - m * cpr) * 8;
+          const int e0 = m * o.w2 + c8;
+          Win8<DT, true> a{};
+          if constexpr (HAS_S) a.load(ab, e0);
+          const float2* zr = P + (r0 + m) * RS;
+          const int nc = (c8 + o.off2) >> 1;  // first complex value of the chunk
+          float yv[8];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float2 z = zr[pad16(nc + u)];
+            yv[2 * u] = epilogue<DT>(z.x * o.scale, HAS_S, sv, a.at(2 * u));
+            yv[2 * u + 1] = epilogue<DT>(z.y * o.scale, HAS_S, sv, a.at(2 * u + 1));
+          }
+          store8<DT, true>(ob, e0, yv);
+        }
+        __syncthreads();
+        continue;
+      }
+    }
     constexpr bool BWD = GE == GATED_BWD;
     const ET* __restrict__ gb = (const ET*)(GE == GATED_FWD ? o.gio.kg : o.gio.v);
     const ET* __restrict__ gc = (const ET*)(GE == GATED_FWD ? o.gio.v : o.gio.q);
