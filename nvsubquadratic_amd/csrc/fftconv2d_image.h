@@ -40,6 +40,7 @@
 // XCD w % 8 and the images of a channel take consecutive slots there.
 #pragma once
 
+#include "fft_wave128.h"
 #include "fftconv_nd_impl.h"
 
 namespace nsq {
@@ -62,88 +63,13 @@ __device__ __forceinline__ void img_of(int w, int B, int H, int& b, int& h) {
   }
 }
 
-// The per-column state of phase B: in round q (q < 2) wave w owns the 8
-// columns col = 64 q + 8 w + (lane & 7), and lane l runs butterfly
-// jb = l >> 3 of its column's 128-point DFTs.  A column's 8 lanes sit in one
-// wave, so its exchanges need only the wave's own LDS ordering (img_wave_sync),
-// never a workgroup barrier.
-struct ImgCol {
-  int col, jb;
-};
+// The per-column state of phase B (W128Col): in round q (q < 2) wave w owns
+// the 8 columns col = 64 q + 8 w + (lane & 7), and lane l runs butterfly
+// jb = l >> 3 of its column's 128-point DFTs (w128_dft_fwd / w128_dft_inv).
 
 // Element n of column col in the tile (rows of kImgRS, pad16 inside a row).
 __device__ __forceinline__ float2& img_at(float2* tile, int n, int col) { return tile[n * kImgRS + pad16(col)]; }
 
-// LDS operations of one wave take effect in program order; this keeps the
-// compiler from moving a lane's slot reads above its neighbours' slot writes.
-__device__ __forceinline__ void img_wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Exchange slot n (0..127) of a column lives in tile row
-//   e(n) = (n & ~3) | ((gray(n & 3) ^ h(n >> 2)) & 3),  h(m) = (m >> 2) + 2 (m & 1),
-// a permutation inside each aligned quad of rows.  The tile's row stride
-// (136 complex = 272 words) moves a row 16 banks, so only e(n) mod 4 picks a
-// lane group's banks; e(n) gives the 8 lanes of a column distinct values mod 4
-// (and alternating parity) in every exchange pattern of the DFTs below
-// (n = 16 jb + K, 2 jb + q + 16 r, jb + 8 r), so a wave's 8 columns x 8 lanes
-// cover all banks once per 8-byte access.  The three patterns reduce to four
-// per-lane row pointers and a constant offset per slot.
-__device__ __forceinline__ constexpr int img_gray2(int x) { return (x ^ (x >> 1)) & 3; }
-__device__ __forceinline__ int img_swz(int n) {
-  const int h = (n >> 4) + 2 * ((n >> 2) & 1);
-  return (n & ~3) | ((img_gray2(n & 3) ^ h) & 3);
-}
-struct ImgSlots {
-  float2* p[4];
-  __device__ __forceinline__ ImgSlots(float2* tile, int col, int base, int l) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) p[c] = tile + (base + (c ^ l)) * kImgRS + pad16(col);
-  }
-};
-// n = 16 jb + K (K < 16): row 16 jb + (K & 12) + (cK ^ (jb & 3))
-__device__ __forceinline__ ImgSlots img_slots_w(float2* tile, const ImgCol& ic) {
-  return ImgSlots(tile, ic.col, 16 * ic.jb, ic.jb & 3);
-}
-__device__ __forceinline__ float2& img_w(const ImgSlots& s, int K) {
-  return s.p[img_gray2(K & 3) ^ (2 * ((K >> 2) & 1))][(K & 12) * kImgRS];
-}
-// n = 2 jb + q + 16 r: row 16 r + 4 (jb >> 1) + (((q ^ r) & 3) ^ L)
-__device__ __forceinline__ ImgSlots img_slots_r1(float2* tile, const ImgCol& ic) {
-  return ImgSlots(tile, ic.col, 4 * (ic.jb >> 1), (3 * (ic.jb & 1)) ^ (2 * ((ic.jb >> 1) & 1)));
-}
-__device__ __forceinline__ float2& img_r1(const ImgSlots& s, int q, int r) { return s.p[(q ^ r) & 3][16 * r * kImgRS]; }
-// n = jb + 8 r: row 8 r + 4 (jb >> 2) + (((r >> 1) & 3) ^ L)
-__device__ __forceinline__ ImgSlots img_slots_r2(float2* tile, const ImgCol& ic) {
-  return ImgSlots(tile, ic.col, 4 * (ic.jb >> 2), img_gray2(ic.jb & 3) ^ (2 * (ic.jb >> 2)));
-}
-__device__ __forceinline__ float2& img_r2(const ImgSlots& s, int r) { return s.p[(r >> 1) & 3][8 * r * kImgRS]; }
-
-// Slot access policies of the 128-point DFTs below: slots_w() gives slot
-// 16 jb + K, slots_r1() slot 2 jb + q + 16 r, slots_r2() slot jb + 8 r.
-// ImgColX: a phase-B column (rows permuted by img_swz).
-struct ImgColX {
-  float2* tile;
-  ImgCol ic;
-  int jb;
-  struct W {
-    ImgSlots s;
-    __device__ __forceinline__ float2& operator()(int K) const { return img_w(s, K); }
-  };
-  struct R1 {
-    ImgSlots s;
-    __device__ __forceinline__ float2& operator()(int q, int r) const { return img_r1(s, q, r); }
-  };
-  struct R2 {
-    ImgSlots s;
-    __device__ __forceinline__ float2& operator()(int r) const { return img_r2(s, r); }
-  };
-  __device__ __forceinline__ W slots_w() const { return {img_slots_w(tile, ic)}; }
-  __device__ __forceinline__ R1 slots_r1() const { return {img_slots_r1(tile, ic)}; }
-  __device__ __forceinline__ R2 slots_r2() const { return {img_slots_r2(tile, ic)}; }
-};
 // ImgRowX: a tile row in its natural layout (element n at pad16(n)); the
 // slots of a pattern are constant offsets from one per-lane pointer.  With 8
 // rows per wave (lane = 8 row + jb) the 16 jb + K and jb + 8 r patterns are
@@ -168,97 +94,12 @@ struct ImgRowX {
   __device__ __forceinline__ R2 slots_r2() const { return {row + jb}; }
 };
 
-// Forward 128-point DFT of the thread's inputs v[r] = c[jb + 8 r] (r < 16):
-// radix 16 in registers, exchange through the line's slots (SX: ImgColX or
-// ImgRowX), radix 8; leaves X[jj + 16 r] (r < 8) of the butterflies
-// jj = 2 jb + q (q < 2) in xo[q][r].  The line's earlier slot reads precede
-// it in the wave's program order.
-template <class SX>
-__device__ __forceinline__ void img_dft128_fwd(const SX& sx, float2 (&v)[16], float2 (&xo)[2][8],
-                                               const float2* __restrict__ tw) {
-  dft<16, false>(v);  // first pass: outputs at 16 jb + r
-  {
-    const auto sw = sx.slots_w();
-    img_wave_sync();
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sw(r) = v[r];
-  }
-  img_wave_sync();
-  const TwTable tt(tw);
-  const auto s1 = sx.slots_r1();
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int jj = 2 * sx.jb + q;  // second pass (NS = 16): butterfly jj reads jj + 16 r, k = jj
-    float2 w[8];
-    pass_twiddles<8>(tt, 128, jj, w);
-#pragma unroll
-    for (int r = 0; r < 8; ++r) xo[q][r] = s1(q, r);
-#pragma unroll
-    for (int r = 1; r < 8; ++r) xo[q][r] = cmul(xo[q][r], w[r]);
-    dft<8, false>(xo[q]);  // outputs at jj + 16 r: natural order
-  }
-  img_wave_sync();
-}
-
-// u[r] *= conj(W_128^{r k}), r = 1..15: the roots at r = 1, 2, 4, 8 are table
-// loads and each other root the product of two (as pass_twiddles), formed
-// and applied one output at a time so that no 16-root array is live.
-__device__ __forceinline__ void img_twiddle16_inv(float2 (&u)[16], const float2* __restrict__ tw, int k) {
-  const TwTable tt(tw);
-  const float2 w1 = tt.load(128, k), w2 = tt.load(128, 2 * k), w4 = tt.load(128, 4 * k), w8 = tt.load(128, 8 * k);
-  float2 lo[8];
-  lo[1] = w1;
-  lo[2] = w2;
-  lo[3] = cmul_fixed(w2, w1);
-  lo[4] = w4;
-#pragma unroll
-  for (int r = 1; r < 8; ++r) {
-    NSQ_SLOT_FENCE();
-    if (r >= 5) lo[r] = cmul_fixed(w4, lo[r - 4]);
-    u[r] = cmulc(u[r], lo[r]);
-  }
-  u[8] = cmulc(u[8], w8);
-#pragma unroll
-  for (int r = 9; r < 16; ++r) {
-    NSQ_SLOT_FENCE();
-    u[r] = cmulc(u[r], cmul_fixed(w8, lo[r - 8]));
-  }
-}
-
-// Inverse 128-point DFT (unnormalised) of Y[jj + 16 r] in yv[q][r] (the
-// layout img_dft128_fwd leaves): radix 8 in registers (first pass, butterfly
-// jj reads jj + 16 r), exchange, radix 16 (butterfly jb reads jb + 8 r,
-// k = jb); leaves y[jb + 8 r] in u[r].
-template <class SX>
-__device__ __forceinline__ void img_dft128_inv(const SX& sx, float2 (&yv)[2][8], float2 (&u)[16],
-                                               const float2* __restrict__ tw) {
-  {
-    const auto sw = sx.slots_w();
-    img_wave_sync();
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      dft<8, true>(yv[q]);  // outputs at 8 jj + r = 16 jb + 8 q + r
-#pragma unroll
-      for (int r = 0; r < 8; ++r) sw(8 * q + r) = yv[q][r];
-    }
-  }
-  img_wave_sync();
-  {
-    const auto s2 = sx.slots_r2();
-#pragma unroll
-    for (int r = 0; r < 16; ++r) u[r] = s2(r);
-  }
-  img_twiddle16_inv(u, tw, sx.jb);
-  dft<16, true>(u);  // outputs at jb + 8 r
-  img_wave_sync();
-}
-
 // Filter values of one half (ODD: frequencies k = 2m + 1, else 2m) for the
-// thread's outputs m = 2 jb + q + 16 r of img_dft128_fwd: Khat[k][col], and
+// thread's outputs m = 2 jb + q + 16 r of w128_dft_fwd: Khat[k][col], and
 // for the packed column 0 also Khat[-k][0].  Issued before the half's DFT so
 // their L2 latency overlaps it.
 template <bool ODD>
-__device__ __forceinline__ void img_filter_load(const ImgCol& ic, const float2* __restrict__ kc, int rsk,
+__device__ __forceinline__ void img_filter_load(const W128Col& ic, const float2* __restrict__ kc, int rsk,
                                                 float2 (&kv)[2][8], float2 (&km)[2][8]) {
   const bool c0 = ic.col == 0;
 #pragma unroll
@@ -279,17 +120,17 @@ __device__ __forceinline__ void img_filter_load(const ImgCol& ic, const float2* 
 // pairs of k and -k (pack_split); its partner values go through the column's
 // slots (lanes of one wave).
 template <bool ODD>
-__device__ __forceinline__ void img_col_product(float2* tile, const ImgCol& ic, float2 (&xo)[2][8],
+__device__ __forceinline__ void img_col_product(float2* tile, const W128Col& ic, float2 (&xo)[2][8],
                                                 const float2 (&kv)[2][8], const float2 (&km)[2][8]) {
   const bool c0 = ic.col == 0;
   if (c0) {
-    const ImgSlots s1 = img_slots_r1(tile, ic);
+    const auto s1 = w128_slots_r1<kImgRS>(tile, ic);
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int r = 0; r < 8; ++r) img_r1(s1, q, r) = xo[q][r];  // slot m = 2 jb + q + 16 r
+      for (int r = 0; r < 8; ++r) w128_r1(s1, q, r) = xo[q][r];  // slot m = 2 jb + q + 16 r
   }
-  img_wave_sync();
+  w128_wave_sync();
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
 #pragma unroll
@@ -298,7 +139,7 @@ __device__ __forceinline__ void img_col_product(float2* tile, const ImgCol& ic, 
         const int m = 2 * ic.jb + q + 16 * r;
         const int mp = ODD ? 127 - m : (128 - m) & 127;  // -k
         float2 xd, xn, kd, kn;
-        pack_split(xo[q][r], img_at(tile, img_swz(mp), 0), xd, xn);
+        pack_split(xo[q][r], img_at(tile, w128_swz(mp), 0), xd, xn);
         pack_split(kv[q][r], km[q][r], kd, kn);
         xo[q][r] = cadd(cmul(xd, kd), mul_i(cmul(xn, kn)));
       } else {
@@ -306,7 +147,7 @@ __device__ __forceinline__ void img_col_product(float2* tile, const ImgCol& ic, 
       }
     }
   }
-  img_wave_sync();
+  w128_wave_sync();
 }
 
 // The image kernel.  kc: filter spectra [H][256][rsk] (the three-pass plan's
@@ -358,7 +199,7 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
         }
 #pragma unroll
         for (int r = 8; r < 16; ++r) v[r] = make_float2(0.f, 0.f);  // n >= 64: the zero half
-        img_dft128_fwd(rx, v, xo, tw);
+        w128_dft_fwd(rx, v, xo, tw);
       }
       const auto s1 = rx.slots_r1();
 #pragma unroll
@@ -366,7 +207,7 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
 #pragma unroll
         for (int r = 0; r < 8; ++r) s1(q, r) = xo[q][r];  // X[jj + 16 r], natural order
     }
-    img_wave_sync();
+    w128_wave_sync();
 #pragma unroll
     for (int i = 0; i < 16; ++i) {  // unpack in place: slot (row m, p < 64) owns elements p and 128 - p (0: 0, 64)
       const int m = 16 * wv + i, p = lane;
@@ -385,8 +226,8 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
   constexpr int CPR = kImgT / 8;  // columns per round: 8 lanes per column, 8 columns per wave
   for (int round = 0; round < 128 / CPR; ++round) {
     const int tid = opaque_tid();
-    const ImgCol ic{CPR * round + 8 * (tid >> 6) + (tid & 7), (tid >> 3) & 7};
-    const ImgColX cx{tile, ic, ic.jb};
+    const W128Col ic{CPR * round + 8 * (tid >> 6) + (tid & 7), (tid >> 3) & 7};
+    const W128ColX<kImgRS> cx{tile, ic, ic.jb};
     const TwTable tt(tw);
     float2 c[16], v[16], ye[16];
     float2 xo[2][8], kv[2][8], km[2][8];
@@ -395,18 +236,18 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
     for (int r = 0; r < 16; ++r) c[r] = img_at(tile, ic.jb + 8 * r, ic.col);  // rows >= S0 are zero
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = c[r];
-    img_dft128_fwd(cx, v, xo, tw);
+    w128_dft_fwd(cx, v, xo, tw);
     img_col_product<false>(tile, ic, xo, kv, km);
     img_filter_load<true>(ic, kc, rsk, kv, km);
-    img_dft128_inv(cx, xo, ye, tw);
+    w128_dft_inv(cx, xo, ye, tw);
     float2 wt[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) wt[r] = tt.load(256, ic.jb + 8 * r);
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = cmul(c[r], wt[r]);  // c[n] W256^n
-    img_dft128_fwd(cx, v, xo, tw);
+    w128_dft_fwd(cx, v, xo, tw);
     img_col_product<true>(tile, ic, xo, kv, km);
-    img_dft128_inv(cx, xo, v, tw);
+    w128_dft_inv(cx, xo, v, tw);
     // y[n] = ye[p] + W256^-n yo[p] for the kept n = p or p + 128 in [o0, o0 + S0)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -421,7 +262,7 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
       const bool keep = n >= o0 && n < o0 + S0;
       if (keep) img_at(tile, n - o0, ic.col) = cadd(ye[r], cmulc(v[r], wt[r]));
     }
-    img_wave_sync();
+    w128_wave_sync();
   }
   __syncthreads();
 
@@ -444,7 +285,7 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
       z[pad16(p)] = zp;
       z[pad16(pb)] = zq;
     }
-    img_wave_sync();
+    w128_wave_sync();
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       if (16 * wv + 8 * g >= S0) continue;  // no output rows (wave-uniform)
@@ -456,12 +297,12 @@ __global__ __launch_bounds__(kImgT) void nd2_image_fwd_kernel(const typename Ele
       for (int q = 0; q < 2; ++q)
 #pragma unroll
         for (int r = 0; r < 8; ++r) yv[q][r] = s1(q, r);
-      img_dft128_inv(rx, yv, u, tw);
+      w128_dft_inv(rx, yv, u, tw);
       const auto s2 = rx.slots_r2();
 #pragma unroll
       for (int r = 0; r < 16; ++r) s2(r) = u[r];  // y[jb + 8 r], natural order
     }
-    img_wave_sync();
+    w128_wave_sync();
     const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
     const int cpr = S2 >> 3;  // 8-sample chunks per output row
     const int nr = min(16, S0 - 16 * wv);  // the wave's output rows

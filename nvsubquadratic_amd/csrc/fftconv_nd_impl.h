@@ -30,6 +30,7 @@
 #pragma once
 
 #include "fft_core.h"
+#include "fft_wave128.h"
 #include "gate.h"
 
 namespace nsq {
@@ -997,6 +998,85 @@ __global__ __launch_bounds__((ColNdCfg<LOGF, TARGET>::T)) void nd_col_bwd_kernel
   LdsTile<C::S, false> ldq{ldsX};
   auto stq = [&](int mm, int k, float2 v) { qb.store(k, j0 + mm, j0 + mm < cg.inner_count && k < K0, v); };
   fft<LOGF, true, C::M, C::T, C::S, true>(ldsX, ldq, stq, tw);
+}
+
+// The adjoint above for 128-point axis-0 columns without a packed column
+// (nd_col_bwd_kernel<7, kNdBwdTile, HALF, false>: same grid, arguments and
+// results): each wave owns 8 of the workgroup's 16 columns, 8 lanes per
+// column (fft_wave128.h), in an LDS block of 128 rows x 8 columns of its own,
+// so no step waits for the other wave.  A lane holds its column's spectral
+// values at k = 2 jb + q + 16 r (q < 2, r < 8), with their filter values,
+// shift ramps and Q accumulators; G's and X's columns of an image are loaded
+// together before either transform.
+template <bool HALF>
+__global__ __launch_bounds__(128) void nd_col_bwd_w128_kernel(float2* __restrict__ wsg, const float2* __restrict__ wsx,
+                                                              const float2* __restrict__ wsk, float2* __restrict__ wsq,
+                                                              ColGeom cg, int B, int H, int kfilm, int S0, int wm0,
+                                                              int K0, Ramp rp, int jbase, int64_t qsplit,
+                                                              const float2* __restrict__ tw) {
+  constexpr int F = 128, RSX = 8, NV = HALF ? 8 : 16;  // HALF: S0 <= F/2, inputs n >= 64 are zero
+  __shared__ float2 blk[2][F * RSX];
+  const int64_t hk = blockIdx.x;
+  const int t = opaque_tid();
+  const int wv = t >> 6, lane = t & 63;
+  const W128Col ic{lane & 7, lane >> 3};
+  const int jb = ic.jb;
+  const int j = jbase + int(blockIdx.y) * 16 + 8 * wv + ic.col;
+  const bool jok = j < cg.inner_count;
+  const W128ColX<RSX> cx{blk[wv], ic, jb};
+  const ColBuf kb(wsk + hk * cg.spec, cg);
+  const TwTable tt(tw);
+  const float2 r12 = ramp_inner(rp, tt, jok ? j : 0);
+  float2 kv[2][8], rr[2][8], q[2][8];
+#pragma unroll
+  for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int k = 2 * jb + q2 + 16 * r;
+      kv[q2][r] = kb.load(k, j, jok);
+      rr[q2][r] = cmul(r12, tt.load(F, (rp.c0 * k) & (F - 1)));
+      q[q2][r] = make_float2(0.f, 0.f);
+    }
+  const int nb = kfilm ? 1 : B;
+  const int nz = int(gridDim.z), z = int(blockIdx.z);
+  for (int bi = z * nb / nz; bi < (z + 1) * nb / nz; ++bi) {
+    const int64_t bh = kfilm ? hk : (int64_t(bi) * H + hk);
+    const ColBuf gb(wsg + bh * cg.spec, cg);
+    const ColBuf xb(wsx + bh * cg.spec, cg);
+    float2 vg[16], vx[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {  // column values n = jb + 8 r
+      const int n = (jb + 8 * r) & wm0;
+      const bool ok = r < NV && jok && n < S0;
+      vg[r] = r < NV ? gb.load(n, j, ok) : make_float2(0.f, 0.f);
+      vx[r] = r < NV ? xb.load(n, j, ok) : make_float2(0.f, 0.f);
+    }
+    float2 gs[2][8], xs[2][8];
+    w128_dft_fwd(cx, vg, gs, tw);
+    w128_dft_fwd(cx, vx, xs, tw);
+#pragma unroll
+    for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float2 gsh = cmul(gs[q2][r], rr[q2][r]);
+        q[q2][r] = cadd(q[q2][r], cmulc(gsh, xs[q2][r]));
+        gs[q2][r] = cmulc(gsh, kv[q2][r]);
+      }
+    w128_dft_inv(cx, gs, vg, tw);  // P at n = jb + 8 r
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int n = jb + 8 * r;
+      gb.store(n, j, jok && n < S0, vg[r]);
+    }
+  }
+  float2 u[16];
+  w128_dft_inv(cx, q, u, tw);
+  const ColBuf qb(wsq + (z * qsplit + hk) * cg.spec, cg);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int n = jb + 8 * r;
+    qb.store(n, j, jok && n < K0, u[r]);
+  }
 }
 
 // Sum of the batch-split partial Q blocks: for h < nk, block h += blocks

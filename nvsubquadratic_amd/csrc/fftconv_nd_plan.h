@@ -448,6 +448,16 @@ bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, v
   return inner_inv<DT, ND_OUT_Y, GM>(p, wsy, BH, p.S[0], p.o[1], p.S[1], o, tw, st);
 }
 
+// The wave-local adjoint of 128-point axis-0 columns (nd_col_bwd_w128_kernel);
+// NSQ_ND_BWD_W128=0 selects the workgroup-tile kernel for every shape.
+inline bool w128_bwd_on() {
+  static const bool on = [] {
+    const char* e = std::getenv("NSQ_ND_BWD_W128");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 // GATED: the Hyena gates fused into the first and last passes, operands in
 // *gate (x is then q, g the gradient of the gated output, gx receives dq;
 // gated_nd_bwd).
@@ -476,6 +486,15 @@ bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const float* k, c
       constexpr int TGT = decltype(tile)::value;
       const dim3 grid{unsigned(NK), unsigned(gy), unsigned(nz)};
       auto go = [&](auto half, auto pack) {
+        if constexpr (LOGF == 7 && TGT == kNdBwdTile && !decltype(pack)::value) {
+          static_assert(ColNdCfg<LOGF, TGT>::M == 16 && ColNdCfg<LOGF, TGT>::T == 128, "wave-local adjoint tile");
+          if (w128_bwd_on()) {
+            hipLaunchKernelGGL((nd_col_bwd_w128_kernel<decltype(half)::value>), grid, dim3(128), 0, st, wsg,
+                               (const float2*)wsx, (const float2*)wsk, wsq, cg, int(p.B), int(p.H), int(p.kb != 1),
+                               p.S[0], p.wm[0], p.K[0], rp, jbase, NK, tw);
+            return;
+          }
+        }
         hipLaunchKernelGGL((nd_col_bwd_kernel<LOGF, TGT, decltype(half)::value, decltype(pack)::value>), grid,
                            dim3(ColNdCfg<LOGF, TGT>::T), 0, st, wsg, (const float2*)wsx, (const float2*)wsk, wsq,
                            cg, int(p.B), int(p.H), int(p.kb != 1), p.S[0], p.wm[0], p.K[0], rp, jbase, NK, tw);

@@ -127,6 +127,18 @@ def test_3d_plane_passes_film():
     _grad_check((2, 2, 6, 100, 50), (5, 21, 27), F.fftconv3d_bhl, kb=2)
 
 
+# 128-point axis-0 columns take the wave-local adjoint (nd_col_bwd_w128_kernel): shared and per-sample filters,
+# with (S0 <= 64) and without (S0 > 64) the zero-half fold, K0 > S0, and few channels (the batch loop split over
+# workgroups, partial filter gradients summed afterwards).
+W128_3D = [((3, 2, 100, 6, 8), (5, 3, 3), 1), ((2, 3, 64, 5, 9), (64, 3, 2), 1), ((2, 2, 100, 6, 8), (5, 3, 3), 2),
+           ((1, 2, 40, 4, 4), (60, 2, 2), 1)]
+
+
+@pytest.mark.parametrize("xs,ks,kb", W128_3D)
+def test_3d_axis0_128_point_adjoint(xs, ks, kb):
+    _grad_check(xs, ks, F.fftconv3d_bhl, kb=kb)
+
+
 def test_3d_film_and_chunked():
     _grad_check((2, 3, 8, 8, 8), (5, 5, 5), F.fftconv3d_bhl, kb=2)
     torch.manual_seed(6)
