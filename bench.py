@@ -25,6 +25,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
            the rayleigh_benard Well config's layer, x periodic / y zero-padded)
        python bench.py --workload hyena-gated   (report-only: the Hyena gates
            fused into the causal conv, with the unfused composition's time)
+       python bench.py --workload hyena-norm       (report-only: the Hyena output gate + RMSNorm over
+                                                    channels + channels-last layout, fwd+bwd, cfg4 shape)
        python bench.py --workload hyena-gated-2d   (report-only: the gated 2D
            conv at cfg4's shape, with torch gates around the same conv and the
            conv alone)
@@ -465,6 +467,38 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
             Fn.linear(h, wo, bo).t().backward(g)
 
         extra["torch_layers_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
+    elif name == "hyena-norm":
+        # report-only (row F2, norms): the Hyena output tail y * sigmoid(v) -> RMSNorm over channels -> channels-last
+        # (hyena_nd.py:570-583) as one HIP pass per direction, against the reference's torch ops on the same GPU
+        from nvsubquadratic_amd.norm_hip import hyena_output_norm
+
+        B, Ch, X = 16, 384, 128
+        y, v = (torch.randn(B, Ch, X, X, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+                for _ in range(2))
+        w = (torch.rand(Ch, device=dev, generator=gen) + 0.5).requires_grad_(True)
+        g = torch.randn(B, X, X, Ch, device=dev, generator=gen).to(torch.bfloat16)
+        phase, dtype = "fwd+bwd", "f32"
+        n = B * Ch * X * X
+        nbytes = 8 * n * 2  # fwd: y, v in, out; bwd: g, y, v in, dy, dv out (bf16)
+        desc = ("hyena-norm: Hyena output tail fwd+bwd, y * sigmoid(v) -> RMSNorm over C (eps 1e-6) -> [B, H, W, C], "
+                "B=16 C=384 128^2 bf16, weight fp32")
+
+        def clear():
+            for t in (y, v, w):
+                t.grad = None
+
+        def step():
+            clear()
+            hyena_output_norm(y, v, w, 1e-6, "sigmoid").backward(g)
+
+        def step_torch():
+            clear()
+            u = (y * torch.sigmoid(v)).movedim(1, -1)
+            xf = u.float()
+            out = (w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6))).to(u.dtype)
+            out.contiguous().backward(g)
+
+        extra["torch_ops_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
     else:
         raise SystemExit(f"unknown workload {name}")
     ms_list = _time_steps(step, steps, warmup)
@@ -499,7 +533,8 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
                                                               "cfg4-circular", "well-rb", "hyena-gated",
-                                                              "hyena-gated-2d", "siren-1d", "hbm-patterns"])
+                                                              "hyena-gated-2d", "siren-1d", "hyena-norm",
+                                                              "hbm-patterns"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

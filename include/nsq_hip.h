@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 9
+#define NSQ_ABI_VERSION 10
 
 enum {
   NSQ_OK = 0,
@@ -398,6 +398,35 @@ int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_str
  */
 int nsq_batched_transpose(const void* src, void* dst, int elem_bytes, int64_t B, int64_t R, int64_t C,
                           void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Hyena gate + RMSNorm over channels + layout, one pass (ABI 10).
+ *
+ * Replaces, per call, the reference's chain of elementwise ops and copies
+ *   u = y * act(v)                              (hyena_nd.py:570; :546 for gate 1)
+ *   out = RMSNorm(u.movedim(1, -1))             (hyena_nd.py:573-580 output_norm;
+ *         rms_norm.py:71-77: fp32 upcast, u * rsqrt(mean_c u^2 + eps),
+ *         (w * .).to(dtype); rms_norm_channel_first.py:71-80 along dim 1)
+ *   rearrange(out, "b c ... -> b ... c")        (hyena_nd.py:583)
+ * y, v: [B, C, S] in `dtype` (S = the flattened spatial axes); v == NULL skips
+ * the gate (u = y).  w: fp32 [C].  out_channels_last = 1 writes out as
+ * [B, S, C] (the output_norm site), 0 as [B, C, S] (the pixelhyena_norm site,
+ * hyena_nd.py:548-556).  act: NSQ_GATE_*.  C <= 7781 (forward), C <= 3536
+ * (backward); larger C returns NSQ_ERR_UNSUPPORTED.
+ *
+ * Backward: dout in the forward's output layout; writes dy (and dv when v is
+ * given; v and dv come together) as [B, C, S] and dw fp32 [C] (overwritten,
+ * summed in a fixed order).  Workspace: nsq_channel_rmsnorm_bwd_workspace_bytes
+ * (per-workgroup partial rows of dw).
+ */
+int nsq_channel_rmsnorm_fwd(const void* y, const void* v, const float* w, void* out, int dtype, int64_t B, int64_t C,
+                            int64_t S, float eps, int act, int out_channels_last, void* stream);
+
+size_t nsq_channel_rmsnorm_bwd_workspace_bytes(int64_t B, int64_t C, int64_t S);
+
+int nsq_channel_rmsnorm_bwd(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv,
+                            float* dw, int dtype, int64_t B, int64_t C, int64_t S, float eps, int act,
+                            int out_channels_last, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,533 @@
+// Hyena's output epilogue as one pass over HBM: the second gate, the RMSNorm
+// over channels and the channels-first -> channels-last rearrange
+// (nvsubquadratic/modules/hyena_nd.py:570 y * act2(v), :573-580 output_norm on
+// y.movedim(1, -1), :583 rearrange "b c ... -> b ... c"; the norm is
+// nvsubquadratic/modules/rms_norm.py:71-77 _rmsnorm_pytorch, or its
+// channels-first twin rms_norm_channel_first.py:71-80, which is the same
+// arithmetic along dim 1).  The same pass with the first gate and a
+// channels-first output is the pixelhyena_norm site (hyena_nd.py:546-556,
+// z = q * act1(k) normalised over channels).
+//
+//   u[b,c,s]   = round(y * round(act(v)))           (y alone without a gate)
+//   r[b,s]     = rsqrt(mean_c u[b,c,s]^2 + eps)     (fp32)
+//   out[b,s,c] = round(w[c] * (u[b,c,s] * r[b,s]))  (or out[b,c,s])
+//
+// Data: y, v, dy, dv are [B, C, S] (S the flattened spatial axes), out and
+// dout [B, S, C] or [B, C, S]; w and dw fp32 [C].  A workgroup owns a tile of
+// TS consecutive positions of one batch row and all C channels, staged in LDS
+// as fp32 with an odd row stride (TS + 1): the channels-first sides are read
+// and written as runs of TS positions per channel (lanes along s), the
+// channels-last side as runs of C channels per position (lanes along c), and
+// the sum over channels is a tree over the TS-wide lane groups.  Tiles that
+// share 128-byte lines of the channels-first rows sit on one XCD (the
+// workgroup index is remapped so that XCD x = blockIdx % 8 takes a contiguous
+// range of tiles), so a line is fetched from HBM once per XCD's L2.
+//
+// Backward, per tile: recompute u and r, stage dout, m[s] = mean_c(w dout
+// xhat), du = r (w dout - xhat m) rounded to the I/O dtype (the reference's
+// fp32 upcast hands its gradient back in that dtype), then the gate's
+// adjoint: dy = round(du * round(act(v))), dv = round(round(du * y) act'(v)).
+// dw = sum over positions of dout * xhat: each workgroup walks a contiguous
+// run of tiles, sums its share per channel in LDS (each channel owned by one
+// thread), writes one partial row, and a second kernel adds the rows in a
+// fixed order (deterministic).
+#include "gate.h"
+#include "nsq_common.h"
+
+#include <initializer_list>
+
+namespace nsq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxWG = 512;  // backward workgroups (partial dw rows): two per CU
+
+// workgroup index -> logical index, consecutive logical indices on one XCD
+__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
+  if (n % 8 != 0) return bid;
+  return (bid % 8) * (n / 8) + bid / 8;
+}
+
+// VW consecutive elements as floats (VW * sizeof(T) == 16: one 16-byte access; VW == 1: one element)
+template <int DT, int VW>
+__device__ __forceinline__ void ld_vec(const typename Elem<DT>::T* p, int64_t i, float (&o)[VW]) {
+  using T = typename Elem<DT>::T;
+  if constexpr (VW == 1) {
+    o[0] = Elem<DT>::load(p, i);
+  } else {
+    static_assert(VW * sizeof(T) == 16, "16-byte vectors");
+    const uint4 u = *reinterpret_cast<const uint4*>(p + i);
+    const T* e = reinterpret_cast<const T*>(&u);
+#pragma unroll
+    for (int k = 0; k < VW; ++k) o[k] = Elem<DT>::load(e, k);
+  }
+}
+
+template <int DT, int VW>
+__device__ __forceinline__ void st_vec(typename Elem<DT>::T* p, int64_t i, const float (&o)[VW]) {
+  using T = typename Elem<DT>::T;
+  if constexpr (VW == 1) {
+    Elem<DT>::store(p, i, o[0]);
+  } else {
+    uint4 u;
+    T* e = reinterpret_cast<T*>(&u);
+#pragma unroll
+    for (int k = 0; k < VW; ++k) Elem<DT>::store(e, k, o[k]);
+    *reinterpret_cast<uint4*>(p + i) = u;
+  }
+}
+
+// Channels-first side: lane (lr, g) covers positions lr*VW .. lr*VW+VW-1 of the
+// tile and channels g, g + G, ...; a thread issues the loads of kNB channels
+// before it uses any of them.
+template <int VW>
+struct CfMap {
+  static constexpr int kNB = VW == 1 ? 8 : 4;
+  int LPR, G, lr, g;
+  __device__ __forceinline__ CfMap(int TS) {
+    LPR = TS / VW;
+    G = kThreads / LPR;
+    lr = threadIdx.x % LPR;
+    g = threadIdx.x / LPR;
+  }
+};
+
+// Phase shared by both directions: u into U[c][s] (zero past S), per-position
+// r = rsqrt(mean u^2 + eps) into rs[].  red holds G x TS partial sums.
+template <int DT, int VW>
+__device__ __forceinline__ void load_tile_u(const typename Elem<DT>::T* __restrict__ y,
+                                            const typename Elem<DT>::T* __restrict__ v, bool gated, int act,
+                                            int64_t rowbase, int C, int64_t S, int64_t s0, int TS, float eps,
+                                            float* U, float* red, float* rs) {
+#pragma clang fp contract(off)
+  const CfMap<VW> m(TS);
+  constexpr int NB = CfMap<VW>::kNB;
+  const int ld = TS + 1, p0 = m.lr * VW;
+  const int64_t pos = s0 + p0;
+  const bool ok = pos < S;  // S is a multiple of VW: the whole vector is in or out
+  float ss[VW];
+#pragma unroll
+  for (int k = 0; k < VW; ++k) ss[k] = 0.f;
+  for (int c0 = m.g; c0 < C; c0 += m.G * NB) {
+    float yv[NB][VW], vv[NB][VW];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int c = c0 + j * m.G;
+      const int64_t i = rowbase + int64_t(c) * S + pos;
+      if (ok && c < C) {
+        ld_vec<DT, VW>(y, i, yv[j]);
+        if (gated) ld_vec<DT, VW>(v, i, vv[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int c = c0 + j * m.G;
+      if (c < C) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          float u = 0.f;
+          if (ok) u = gated ? Elem<DT>::round(yv[j][k] * Elem<DT>::round(gate_act(act, vv[j][k]))) : yv[j][k];
+          U[c * ld + p0 + k] = u;
+          ss[k] = fmaf(u, u, ss[k]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < VW; ++k) red[m.g * TS + p0 + k] = ss[k];
+  __syncthreads();
+  if (threadIdx.x < TS) {
+    float sum = 0.f;
+    for (int k = 0; k < m.G; ++k) sum += red[k * TS + threadIdx.x];
+    rs[threadIdx.x] = rsqrtf(sum * (1.f / float(C)) + eps);
+  }
+  __syncthreads();
+}
+
+// Channels-last side: item q = (s, cv), s = q mod TS fastest (consecutive lanes
+// read consecutive LDS words), cv a run of VW channels (one 16-byte access).
+template <int DT, int VW>
+__global__ __launch_bounds__(kThreads) void chnorm_fwd_kernel(const typename Elem<DT>::T* __restrict__ y,
+                                                              const typename Elem<DT>::T* __restrict__ v,
+                                                              const float* __restrict__ w,
+                                                              typename Elem<DT>::T* __restrict__ out, int C,
+                                                              int64_t S, int TS, int64_t tiles_per_b, int64_t ntiles,
+                                                              float eps, int gated, int act, int out_blh) {
+#pragma clang fp contract(off)
+  extern __shared__ float smem[];
+  const int ld = TS + 1;
+  float* U = smem;
+  float* red = U + C * ld;
+  float* rs = red + kThreads * VW;
+  const int64_t tile = xcd_remap(blockIdx.x, ntiles);
+  const int64_t b = tile / tiles_per_b, s0 = (tile % tiles_per_b) * TS;
+  const int64_t rowbase = b * C * S;
+  load_tile_u<DT, VW>(y, v, gated != 0, act, rowbase, C, S, s0, TS, eps, U, red, rs);
+  const int t = threadIdx.x;
+  const int nval = int(S - s0 < TS ? S - s0 : TS);
+  if (out_blh) {
+    const int nitems = TS * (C / VW);
+    for (int q = t; q < nitems; q += kThreads) {
+      const int s = q % TS, c = (q / TS) * VW;
+      if (s < nval) {
+        float o[VW];
+#pragma unroll
+        for (int k = 0; k < VW; ++k) o[k] = w[c + k] * (U[(c + k) * ld + s] * rs[s]);
+        st_vec<DT, VW>(out, (b * S + s0 + s) * int64_t(C) + c, o);
+      }
+    }
+  } else {
+    const CfMap<VW> m(TS);
+    const int p0 = m.lr * VW;
+    if (p0 < nval)
+      for (int c = m.g; c < C; c += m.G) {
+        float o[VW];
+#pragma unroll
+        for (int k = 0; k < VW; ++k) o[k] = w[c] * (U[c * ld + p0 + k] * rs[p0 + k]);
+        st_vec<DT, VW>(out, rowbase + int64_t(c) * S + s0 + p0, o);
+      }
+  }
+}
+
+template <int DT, int VW>
+__global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
+    const typename Elem<DT>::T* __restrict__ dout, const typename Elem<DT>::T* __restrict__ y,
+    const typename Elem<DT>::T* __restrict__ v, const float* __restrict__ w, typename Elem<DT>::T* __restrict__ dy,
+    typename Elem<DT>::T* __restrict__ dv, float* __restrict__ dw_part, int C, int64_t S, int TS,
+    int64_t tiles_per_b, int64_t ntiles, int64_t tiles_per_wg, float eps, int gated, int act, int in_blh) {
+#pragma clang fp contract(off)
+  extern __shared__ float smem[];
+  const int ld = TS + 1;
+  float* U = smem;                  // u, then xhat
+  float* D = U + C * ld;            // dout (fp32)
+  float* gacc = D + C * ld;         // dw share of this workgroup
+  float* red = gacc + C;            // G x TS partial sums
+  float* rs = red + kThreads * VW;  // r per position
+  float* ms = rs + TS;              // mean_c(w dout xhat) per position
+  const int t = threadIdx.x;
+  const CfMap<VW> m(TS);
+  constexpr int NB = CfMap<VW>::kNB;
+  const int p0 = m.lr * VW;
+  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  for (int c = t; c < C; c += kThreads) gacc[c] = 0.f;
+  const int64_t tb = wg * tiles_per_wg, te = tb + tiles_per_wg < ntiles ? tb + tiles_per_wg : ntiles;
+  for (int64_t tile = tb; tile < te; ++tile) {
+    const int64_t b = tile / tiles_per_b, s0 = (tile % tiles_per_b) * TS;
+    const int64_t rowbase = b * C * S;
+    const int nval = int(S - s0 < TS ? S - s0 : TS);
+    load_tile_u<DT, VW>(y, v, gated != 0, act, rowbase, C, S, s0, TS, eps, U, red, rs);
+    // dout into D[c][s] (zero past S)
+    if (in_blh) {
+      const int nitems = TS * (C / VW);
+      for (int q0 = t; q0 < nitems; q0 += kThreads * NB) {
+        float d[NB][VW];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int q = q0 + j * kThreads, s = q % TS, c = (q / TS) * VW;
+          if (q < nitems && s < nval) {
+            ld_vec<DT, VW>(dout, (b * S + s0 + s) * int64_t(C) + c, d[j]);
+          } else {
+#pragma unroll
+            for (int k = 0; k < VW; ++k) d[j][k] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int q = q0 + j * kThreads, s = q % TS, c = (q / TS) * VW;
+          if (q < nitems)
+#pragma unroll
+            for (int k = 0; k < VW; ++k) D[(c + k) * ld + s] = d[j][k];
+        }
+      }
+    } else {
+      for (int c0 = m.g; c0 < C; c0 += m.G * NB) {
+        float d[NB][VW];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int c = c0 + j * m.G;
+          if (p0 < nval && c < C) {
+            ld_vec<DT, VW>(dout, rowbase + int64_t(c) * S + s0 + p0, d[j]);
+          } else {
+#pragma unroll
+            for (int k = 0; k < VW; ++k) d[j][k] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          if (c0 + j * m.G < C)
+#pragma unroll
+            for (int k = 0; k < VW; ++k) D[(c0 + j * m.G) * ld + p0 + k] = d[j][k];
+      }
+    }
+    __syncthreads();
+    // xhat in place of u; per-position sum of (w dout) xhat
+    {
+      float dot[VW];
+#pragma unroll
+      for (int k = 0; k < VW; ++k) dot[k] = 0.f;
+      for (int c = m.g; c < C; c += m.G) {
+        const float wc = w[c];
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          const float xh = U[c * ld + p0 + k] * rs[p0 + k];
+          U[c * ld + p0 + k] = xh;
+          dot[k] = fmaf(wc * D[c * ld + p0 + k], xh, dot[k]);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < VW; ++k) red[m.g * TS + p0 + k] = dot[k];
+    }
+    __syncthreads();
+    if (t < TS) {
+      float sum = 0.f;
+      for (int k = 0; k < m.G; ++k) sum += red[k * TS + t];
+      ms[t] = sum * (1.f / float(C));
+    }
+    // dw share: each channel summed over the tile's positions by its owner thread
+    for (int c = t; c < C; c += kThreads) {
+      float a = gacc[c];
+      for (int s = 0; s < TS; ++s) a = fmaf(D[c * ld + s], U[c * ld + s], a);
+      gacc[c] = a;
+    }
+    __syncthreads();
+    if (p0 < nval) {
+      for (int c0 = m.g; c0 < C; c0 += m.G * NB) {
+        float yv[NB][VW], vv[NB][VW];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int c = c0 + j * m.G;
+          const int64_t i = rowbase + int64_t(c) * S + s0 + p0;
+          if (gated && c < C) {
+            ld_vec<DT, VW>(y, i, yv[j]);
+            ld_vec<DT, VW>(v, i, vv[j]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int c = c0 + j * m.G;
+          if (c < C) {
+            const float wc = w[c];
+            float o0[VW], o1[VW];
+#pragma unroll
+            for (int k = 0; k < VW; ++k) {
+              const float xh = U[c * ld + p0 + k];
+              const float du = Elem<DT>::round(rs[p0 + k] * (wc * D[c * ld + p0 + k] - xh * ms[p0 + k]));
+              if (gated) {
+                o0[k] = du * Elem<DT>::round(gate_act(act, vv[j][k]));
+                o1[k] = Elem<DT>::round(du * yv[j][k]) * gate_dact(act, vv[j][k]);
+              } else {
+                o0[k] = du;
+                o1[k] = 0.f;
+              }
+            }
+            const int64_t i = rowbase + int64_t(c) * S + s0 + p0;
+            st_vec<DT, VW>(dy, i, o0);
+            if (gated) st_vec<DT, VW>(dv, i, o1);
+          }
+        }
+      }
+    }
+    __syncthreads();  // U and D are reused by the next tile
+  }
+  for (int c = t; c < C; c += kThreads) dw_part[wg * C + c] = gacc[c];
+}
+
+// dw[c] = sum over the partial rows: a workgroup takes 64 channels, its four
+// lane groups rows r = 4k + q (q = 0..3, four running sums each over r mod 16),
+// combined in a fixed order (deterministic).
+__global__ __launch_bounds__(kThreads) void chnorm_dw_reduce_kernel(const float* __restrict__ part,
+                                                                    float* __restrict__ dw, int C, int64_t rows) {
+  __shared__ float acc[4][64];
+  const int t = threadIdx.x, q = t / 64;
+  const int64_t c = int64_t(blockIdx.x) * 64 + (t % 64);
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  if (c < C) {
+    int64_t r = q;
+    for (; r + 12 < rows; r += 16) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] += part[(r + 4 * j) * C + c];
+    }
+    for (; r < rows; r += 4) a[0] += part[r * C + c];
+  }
+  acc[q][t % 64] = (a[0] + a[1]) + (a[2] + a[3]);
+  __syncthreads();
+  if (q == 0 && c < C) dw[c] = (acc[0][t] + acc[1][t]) + (acc[2][t] + acc[3][t]);
+}
+
+size_t fwd_lds(int C, int TS, int VW) { return (size_t(C) * (TS + 1) + size_t(kThreads) * VW + TS) * 4; }
+size_t bwd_lds(int C, int TS, int VW) {
+  return (size_t(C) * (TS + 1) * 2 + C + size_t(kThreads) * VW + 2 * TS) * 4;
+}
+
+constexpr size_t kLdsPreferred = 64 * 1024;  // leaves room for two or more workgroups per CU
+constexpr size_t kLdsMax = 160 * 1024;       // gfx950's LDS per workgroup
+
+// Tile width: the widest of 64, 32, ..., 4 positions whose LDS fits 64 KB, else
+// 4 positions up to the whole LDS (wide C), else 0 (unsupported C).  Sized for
+// the widest vector (VW = 8), so the tile does not depend on the vector path.
+int pick_ts(int C, bool bwd) {
+  for (int ts = 64; ts >= 4; ts /= 2)
+    if ((bwd ? bwd_lds(C, ts, 8) : fwd_lds(C, ts, 8)) <= kLdsPreferred) return ts;
+  return (bwd ? bwd_lds(C, 4, 8) : fwd_lds(C, 4, 8)) <= kLdsMax ? 4 : 0;
+}
+
+struct BwdPlan {
+  int TS;
+  int64_t tiles_per_b, ntiles, nwg, tiles_per_wg;
+};
+
+BwdPlan bwd_plan(int64_t B, int C, int64_t S) {
+  BwdPlan p{};
+  p.TS = pick_ts(C, true);
+  if (!p.TS) return p;
+  p.tiles_per_b = ceil_div(S, int64_t(p.TS));
+  p.ntiles = B * p.tiles_per_b;
+  int64_t nwg = p.ntiles < kMaxWG ? p.ntiles : kMaxWG;
+  p.tiles_per_wg = ceil_div(p.ntiles, nwg);
+  p.nwg = ceil_div(p.ntiles, p.tiles_per_wg);
+  return p;
+}
+
+// 16-byte vectors when every run of VW elements the kernel moves is whole and aligned
+bool use_vec(int vw, int C, int64_t S, int TS, std::initializer_list<const void*> ptrs) {
+  if (S % vw || C % vw || TS % vw) return false;
+  for (const void* q : ptrs)
+    if (q && (reinterpret_cast<uintptr_t>(q) & 15)) return false;
+  return true;
+}
+
+template <class K>
+void allow_lds(K* kernel, size_t lds) {
+  if (lds > kLdsPreferred)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              int(lds));
+}
+
+template <int DT, int VW>
+void launch_fwd_vw(const void* y, const void* v, const float* w, void* out, int64_t B, int C, int64_t S, int TS,
+                   float eps, int gated, int act, int out_blh, hipStream_t st) {
+  using T = typename Elem<DT>::T;
+  const int64_t tpb = ceil_div(S, int64_t(TS)), nt = B * tpb;
+  const size_t lds = fwd_lds(C, TS, VW);
+  allow_lds(&chnorm_fwd_kernel<DT, VW>, lds);
+  hipLaunchKernelGGL((chnorm_fwd_kernel<DT, VW>), dim3(unsigned(nt)), dim3(kThreads), lds, st, (const T*)y,
+                     (const T*)v, w, (T*)out, C, S, TS, tpb, nt, eps, gated, act, out_blh);
+}
+
+template <int DT>
+void launch_fwd(const void* y, const void* v, const float* w, void* out, int64_t B, int C, int64_t S, float eps,
+                int gated, int act, int out_blh, hipStream_t st) {
+  constexpr int VW = 16 / int(sizeof(typename Elem<DT>::T));
+  const int TS = pick_ts(C, false);
+  if (use_vec(VW, C, S, TS, {y, v, out}))
+    launch_fwd_vw<DT, VW>(y, v, w, out, B, C, S, TS, eps, gated, act, out_blh, st);
+  else
+    launch_fwd_vw<DT, 1>(y, v, w, out, B, C, S, TS, eps, gated, act, out_blh, st);
+}
+
+template <int DT, int VW>
+void launch_bwd_vw(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv, float* part,
+                   const BwdPlan& p, int C, int64_t S, float eps, int gated, int act, int out_blh, hipStream_t st) {
+  using T = typename Elem<DT>::T;
+  const size_t lds = bwd_lds(C, p.TS, VW);
+  allow_lds(&chnorm_bwd_kernel<DT, VW>, lds);
+  hipLaunchKernelGGL((chnorm_bwd_kernel<DT, VW>), dim3(unsigned(p.nwg)), dim3(kThreads), lds, st, (const T*)dout,
+                     (const T*)y, (const T*)v, w, (T*)dy, (T*)dv, part, C, S, p.TS, p.tiles_per_b, p.ntiles,
+                     p.tiles_per_wg, eps, gated, act, out_blh);
+}
+
+template <int DT>
+void launch_bwd(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv, float* dw,
+                float* part, const BwdPlan& p, int64_t B, int C, int64_t S, float eps, int gated, int act,
+                int out_blh, hipStream_t st) {
+  (void)B;
+  constexpr int VW = 16 / int(sizeof(typename Elem<DT>::T));
+  if (use_vec(VW, C, S, p.TS, {dout, y, v, dy, dv}))
+    launch_bwd_vw<DT, VW>(dout, y, v, w, dy, dv, part, p, C, S, eps, gated, act, out_blh, st);
+  else
+    launch_bwd_vw<DT, 1>(dout, y, v, w, dy, dv, part, p, C, S, eps, gated, act, out_blh, st);
+  hipLaunchKernelGGL(chnorm_dw_reduce_kernel, dim3(unsigned(ceil_div(int64_t(C), int64_t(64)))),
+                     dim3(kThreads), 0, st, (const float*)part, dw, C, p.nwg);
+}
+
+int check_common(const char* who, int dtype, int64_t B, int C, int64_t S, float eps, int gated, int act) {
+  NSQ_CHECK_ARG(dtype == NSQ_DTYPE_F32 || dtype == NSQ_DTYPE_BF16 || dtype == NSQ_DTYPE_F16, "%s: bad dtype %d", who,
+                dtype);
+  NSQ_CHECK_ARG(B >= 1 && C >= 1 && S >= 1, "%s: sizes must be positive (B=%lld C=%d S=%lld)", who, (long long)B, C,
+                (long long)S);
+  NSQ_CHECK_ARG(eps >= 0.f, "%s: eps must be >= 0", who);
+  NSQ_CHECK_ARG(act == NSQ_GATE_IDENTITY || act == NSQ_GATE_SIGMOID || act == NSQ_GATE_SILU, "%s: bad act %d", who,
+                act);
+  (void)gated;
+  return NSQ_OK;
+}
+
+}  // namespace
+}  // namespace nsq
+
+extern "C" size_t nsq_channel_rmsnorm_bwd_workspace_bytes(int64_t B, int64_t C, int64_t S) {
+  using namespace nsq;
+  if (B < 1 || C < 1 || C > 0x7fffffff || S < 1) return 0;
+  const BwdPlan p = bwd_plan(B, int(C), S);
+  if (!p.TS) return 0;
+  return size_t(p.nwg) * size_t(C) * sizeof(float);
+}
+
+extern "C" int nsq_channel_rmsnorm_fwd(const void* y, const void* v, const float* w, void* out, int dtype, int64_t B,
+                                       int64_t C, int64_t S, float eps, int act, int out_channels_last,
+                                       void* stream) {
+  using namespace nsq;
+  clear_error();
+  NSQ_CHECK_ARG(y && w && out, "channel_rmsnorm_fwd: null pointer argument");
+  NSQ_CHECK_ARG(C >= 1 && C <= 0x7fffffff, "channel_rmsnorm_fwd: C=%lld out of range", (long long)C);
+  const int gated = v != nullptr;
+  if (int e = check_common("channel_rmsnorm_fwd", dtype, B, int(C), S, eps, gated, act)) return e;
+  const int TS = pick_ts(int(C), false);
+  if (TS == 0) {
+    set_error("channel_rmsnorm_fwd: C=%lld exceeds the LDS tile (C <= 7781)", (long long)C);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  NSQ_CHECK_ARG(B * ceil_div(S, int64_t(TS)) <= 0x7fffffff, "channel_rmsnorm_fwd: B*S too large for the grid");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NSQ_DTYPE_F32)
+    launch_fwd<NSQ_DTYPE_F32>(y, v, w, out, B, int(C), S, eps, gated, act, out_channels_last, st);
+  else if (dtype == NSQ_DTYPE_BF16)
+    launch_fwd<NSQ_DTYPE_BF16>(y, v, w, out, B, int(C), S, eps, gated, act, out_channels_last, st);
+  else
+    launch_fwd<NSQ_DTYPE_F16>(y, v, w, out, B, int(C), S, eps, gated, act, out_channels_last, st);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+extern "C" int nsq_channel_rmsnorm_bwd(const void* dout, const void* y, const void* v, const float* w, void* dy,
+                                       void* dv, float* dw, int dtype, int64_t B, int64_t C, int64_t S, float eps,
+                                       int act, int out_channels_last, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+  using namespace nsq;
+  clear_error();
+  NSQ_CHECK_ARG(dout && y && w && dy && dw, "channel_rmsnorm_bwd: null pointer argument");
+  NSQ_CHECK_ARG((v == nullptr) == (dv == nullptr), "channel_rmsnorm_bwd: v and dv must be given together");
+  NSQ_CHECK_ARG(C >= 1 && C <= 0x7fffffff, "channel_rmsnorm_bwd: C=%lld out of range", (long long)C);
+  const int gated = v != nullptr;
+  if (int e = check_common("channel_rmsnorm_bwd", dtype, B, int(C), S, eps, gated, act)) return e;
+  const BwdPlan p = bwd_plan(B, int(C), S);
+  if (p.TS == 0) {
+    set_error("channel_rmsnorm_bwd: C=%lld exceeds the LDS tiles (C <= 3536)", (long long)C);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  const size_t need = size_t(p.nwg) * size_t(C) * sizeof(float);
+  NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "channel_rmsnorm_bwd: workspace of %zu bytes needed", need);
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  if (dtype == NSQ_DTYPE_F32)
+    launch_bwd<NSQ_DTYPE_F32>(dout, y, v, w, dy, dv, dw, part, p, B, int(C), S, eps, gated, act, out_channels_last,
+                              st);
+  else if (dtype == NSQ_DTYPE_BF16)
+    launch_bwd<NSQ_DTYPE_BF16>(dout, y, v, w, dy, dv, dw, part, p, B, int(C), S, eps, gated, act, out_channels_last,
+                               st);
+  else
+    launch_bwd<NSQ_DTYPE_F16>(dout, y, v, w, dy, dv, dw, part, p, B, int(C), S, eps, gated, act, out_channels_last,
+                              st);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}

@@ -1,0 +1,166 @@
+r"""Hyena's gate + RMSNorm over channels + layout change as one HIP pass.
+
+The reference's Hyena operator normalises over channels at three sites, each a chain of elementwise ops and
+layout copies around the long convolution (``nvsubquadratic/modules/hyena_nd.py``):
+
+- ``:570-583``, the output: ``y = y * gate_nonlinear_2(value)``, then ``output_norm`` on
+  ``y.movedim(1, -1)`` (an ``RMSNorm`` over the last axis, ``modules/rms_norm.py:71-77``), then
+  ``rearrange(y, "b c ... -> b ... c")``;
+- ``:546-556``, the conv's input: ``z = query * gate_nonlinear(key)``, then ``pixelhyena_norm`` over channels,
+  handed to the conv channels-first;
+- a channels-first norm module (``modules/rms_norm_channel_first.py:71-80``, ``RMSNormChannelFirst``) is the same
+  arithmetic along dim 1.
+
+:func:`gated_channel_rmsnorm` computes ``round(w * (u * rsqrt(mean_c u^2 + eps)))`` with
+``u = round(y * round(act(v)))`` (or ``u = y``) in one read of ``y`` / ``v`` and one write of the output, in either
+layout (``nsq_channel_rmsnorm_fwd``); its backward recomputes ``u`` and the per-position scale and writes
+``dy``, ``dv`` and the weight gradient in one more pass (``nsq_channel_rmsnorm_bwd``).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch.library import custom_op
+
+from . import _lib
+from .gated_fftconv_hip import gate_code
+
+__all__ = ["HipRMSNormChannelFirst", "channel_rmsnorm", "gated_channel_rmsnorm", "hyena_output_norm"]
+
+
+def _flat(t: torch.Tensor) -> torch.Tensor:
+    """``[B, C, *S]`` -> contiguous ``[B, C, prod(S)]``."""
+    return t.contiguous().reshape(t.shape[0], t.shape[1], -1)
+
+
+@custom_op("nsq_hip::gated_channel_rmsnorm", mutates_args=())
+def gated_channel_rmsnorm_op(y: torch.Tensor, v: Optional[torch.Tensor], weight: torch.Tensor, eps: float, act: int,
+                             channels_last: bool) -> torch.Tensor:
+    """y, v ``[B, C, S]`` contiguous, weight fp32 ``[C]`` -> ``[B, S, C]`` (channels_last) or ``[B, C, S]``."""
+    lib = _lib.get_lib()
+    _lib.check_device(y)
+    B, C, S = y.shape
+    out = torch.empty((B, S, C) if channels_last else (B, C, S), dtype=y.dtype, device=y.device)
+    _lib.check(lib.nsq_channel_rmsnorm_fwd(y.data_ptr(), v.data_ptr() if v is not None else None, weight.data_ptr(),
+                                           out.data_ptr(), _lib.dtype_code(y.dtype), B, C, S, float(eps), act,
+                                           int(channels_last), _lib.stream_ptr(y.device)))
+    return out
+
+
+@gated_channel_rmsnorm_op.register_fake
+def _(y, v, weight, eps, act, channels_last):
+    B, C, S = y.shape
+    return y.new_empty((B, S, C) if channels_last else (B, C, S))
+
+
+@custom_op("nsq_hip::gated_channel_rmsnorm_backward", mutates_args=())
+def gated_channel_rmsnorm_backward_op(dout: torch.Tensor, y: torch.Tensor, v: Optional[torch.Tensor],
+                                      weight: torch.Tensor, eps: float, act: int,
+                                      channels_last: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns ``(dy, dv, dw)``; ``dv`` is empty when ``v`` is None, ``dw`` fp32 ``[C]``."""
+    lib = _lib.get_lib()
+    _lib.check_device(y)
+    B, C, S = y.shape
+    dy = torch.empty_like(y)
+    dv = torch.empty_like(v) if v is not None else y.new_empty(0)
+    dw = torch.empty(C, dtype=torch.float32, device=y.device)
+    ws = torch.empty(int(lib.nsq_channel_rmsnorm_bwd_workspace_bytes(B, C, S)), dtype=torch.uint8, device=y.device)
+    _lib.check(lib.nsq_channel_rmsnorm_bwd(
+        dout.data_ptr(), y.data_ptr(), v.data_ptr() if v is not None else None, weight.data_ptr(), dy.data_ptr(),
+        dv.data_ptr() if v is not None else None, dw.data_ptr(), _lib.dtype_code(y.dtype), B, C, S, float(eps), act,
+        int(channels_last), ws.data_ptr(), ws.numel(), _lib.stream_ptr(y.device)))
+    return dy, dv, dw
+
+
+@gated_channel_rmsnorm_backward_op.register_fake
+def _(dout, y, v, weight, eps, act, channels_last):
+    return torch.empty_like(y), (torch.empty_like(v) if v is not None else y.new_empty(0)), \
+        y.new_empty(y.shape[1], dtype=torch.float32)
+
+
+def _setup(ctx, inputs, output):
+    y, v, weight, eps, act, channels_last = inputs
+    ctx.save_for_backward(y, v, weight)
+    ctx.cfg = (eps, act, channels_last)
+
+
+def _backward(ctx, gout):
+    y, v, weight = ctx.saved_tensors
+    eps, act, channels_last = ctx.cfg
+    dy, dv, dw = gated_channel_rmsnorm_backward_op(gout.contiguous(), y, v, weight, eps, act, channels_last)
+    return dy, (dv if v is not None else None), dw, None, None, None
+
+
+gated_channel_rmsnorm_op.register_autograd(_backward, setup_context=_setup)
+
+
+class _WeightToF32(torch.autograd.Function):
+    """The norm's weight as fp32 (the reference multiplies an fp32 tensor by it, so a 16-bit weight is promoted
+    exactly); its gradient goes back in the weight's dtype."""
+
+    @staticmethod
+    def forward(ctx, w):
+        ctx.dt = w.dtype
+        return w.float()
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(ctx.dt)
+
+
+def gated_channel_rmsnorm(y: torch.Tensor, v: Optional[torch.Tensor], weight: torch.Tensor, eps: float = 1e-6,
+                          gate_nonlinear="sigmoid", channels_last_out: bool = True) -> torch.Tensor:
+    """RMSNorm over channels of ``y * act(v)`` (of ``y`` when ``v`` is None), in one pass.
+
+    Args:
+        y, v: ``[B, C, *spatial]`` in fp32 / bf16 / fp16 (same dtype and shape).
+        weight: ``[C]``, the norm's learned scale.
+        eps: added to the mean square, as ``RMSNorm(eps=...)``.
+        gate_nonlinear: ``"identity" | "sigmoid" | "silu"`` or the matching ``nn`` module.
+        channels_last_out: ``True`` returns ``[B, *spatial, C]`` (the norm over ``movedim(1, -1)`` followed by the
+            output rearrange), ``False`` returns ``[B, C, *spatial]``.
+    """
+    if y.dim() < 2:
+        raise ValueError(f"expected [B, C, *spatial], got shape {tuple(y.shape)}")
+    if v is not None and (v.shape != y.shape or v.dtype != y.dtype):
+        raise ValueError(f"v {tuple(v.shape)} {v.dtype} must match y {tuple(y.shape)} {y.dtype}")
+    if weight.shape != (y.shape[1],):
+        raise ValueError(f"weight shape {tuple(weight.shape)} != ({y.shape[1]},)")
+    shape = y.shape
+    w = _WeightToF32.apply(weight) if weight.dtype != torch.float32 else weight
+    out = gated_channel_rmsnorm_op(_flat(y), _flat(v) if v is not None else None, w.contiguous(), float(eps),
+                                   gate_code(gate_nonlinear) if v is not None else 0, bool(channels_last_out))
+    if channels_last_out:
+        return out.view(shape[0], *shape[2:], shape[1])
+    return out.view(shape)
+
+
+def channel_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``RMSNormChannelFirst`` arithmetic (``modules/rms_norm_channel_first.py:71-80``): ``x`` ``[B, C, *S]``."""
+    return gated_channel_rmsnorm(x, None, weight, eps, "identity", channels_last_out=False)
+
+
+def hyena_output_norm(y: torch.Tensor, value: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                      gate_nonlinear_2="sigmoid") -> torch.Tensor:
+    """The Hyena operator's tail (``hyena_nd.py:570-583``) with an RMSNorm ``output_norm``: ``y`` (the long
+    conv's output) and ``value`` ``[B, C, *spatial]`` -> ``[B, *spatial, C]``."""
+    return gated_channel_rmsnorm(y, value, weight, eps, gate_nonlinear_2, channels_last_out=True)
+
+
+class HipRMSNormChannelFirst(torch.nn.Module):
+    """Drop-in for ``RMSNormChannelFirst`` (``modules/rms_norm_channel_first.py:83``): normalises ``[B, C, *S]``
+    over dim 1 on the HIP kernel.  Same parameter (``weight``, ones) and ``eps``; the ``channels_first`` flag lets
+    the Hyena operator skip its ``movedim`` round trip."""
+
+    channels_first: bool = True
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.ones(dim))
+        self.weight._no_weight_decay = True
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return channel_rmsnorm(x, self.weight, self.eps)

@@ -21,6 +21,8 @@ Contents:
 * :mod:`oracle.siren_ref` -- the SIREN implicit filter generator
   (``modules/kernels_nd.py``, ``SIRENKernelND`` without FiLM) in float32 or
   float64 torch.
+* :mod:`oracle.norm_ref` -- the Hyena gate + RMSNorm over channels + layout
+  sequence at the norm sites (torch on the CPU, autograd backward).
 
 The seeded synthetic inputs of the benchmark configs are product-side
 (``nvsubquadratic_amd.workloads``): they are data, not a checker.

@@ -1,0 +1,38 @@
+"""CPU oracle for the Hyena gate + channel RMSNorm + layout pass (test infrastructure only).
+
+Restates, with torch on the CPU, the reference's op sequence at its norm sites:
+
+- gate: ``y * gate_nonlinear(v)`` on I/O-dtype tensors (``nvsubquadratic/modules/hyena_nd.py:546`` and ``:570``);
+- norm: ``_rmsnorm_pytorch`` (``nvsubquadratic/modules/rms_norm.py:71-77``): upcast to float32,
+  ``x * rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)``, ``(weight * x).to(input_dtype)``, applied to
+  ``u.movedim(1, -1)`` (``hyena_nd.py:573-580``); the channels-first module
+  (``rms_norm_channel_first.py:71-80``) is the same along dim 1;
+- layout: ``rearrange(y, "b c ... -> b ... c")`` (``hyena_nd.py:583``) for the channels-last output.
+
+The backward is torch autograd through that sequence.  Pinned in ``tests/test_oracle_norm.py`` by a closed form of
+the normalised values, scale invariance, finite-difference gradients (float64 gradcheck) and the orthogonality of
+the input gradient to ``u`` at ``eps = 0``.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+__all__ = ["gated_channel_rmsnorm_ref"]
+
+_ACTS = {0: lambda t: t, 1: torch.sigmoid, 2: torch.nn.functional.silu}
+
+
+def gated_channel_rmsnorm_ref(y: torch.Tensor, v: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                              act: int = 1, channels_last: bool = True) -> torch.Tensor:
+    """``y``, ``v`` ``[B, C, *S]`` (any dtype, CPU), ``weight`` ``[C]`` -> ``[B, *S, C]`` or ``[B, C, *S]``."""
+    u = y * _ACTS[act](v) if v is not None else y           # hyena_nd.py:570 (I/O dtype)
+    x = u.movedim(1, -1)                                     # hyena_nd.py:578
+    dt = x.dtype
+    xf = x.to(torch.float32) if dt != torch.float64 else x   # rms_norm.py:73-74
+    var = xf.pow(2).mean(-1, keepdim=True)                   # rms_norm.py:75
+    xf = xf * torch.rsqrt(var + eps)                         # rms_norm.py:76
+    out = (weight * xf).to(dt)                               # rms_norm.py:77
+    return out if channels_last else out.movedim(-1, 1)

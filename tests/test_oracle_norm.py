@@ -1,0 +1,62 @@
+"""CPU pinning of the channel-RMSNorm restatement (oracle/norm_ref.py): closed-form normalised values, scale
+invariance, finite-difference gradients in float64, orthogonality of the input gradient to u at eps = 0, the gate
+as torch's own sigmoid / silu, and the channels-first layout as the channels-last one moved back."""
+
+import math
+
+import torch
+
+from oracle.norm_ref import gated_channel_rmsnorm_ref
+
+
+def test_closed_form_ramp():
+    # u_c = a (c + 1) at every position: mean_c u^2 = a^2 (C + 1)(2C + 1) / 6
+    B, C, S, a, eps = 2, 7, 5, 0.37, 1e-3
+    ramp = torch.arange(1, C + 1, dtype=torch.float64)
+    y = (a * ramp).view(1, C, 1).expand(B, C, S).contiguous()
+    w = torch.linspace(0.5, 2.0, C, dtype=torch.float64)
+    out = gated_channel_rmsnorm_ref(y, None, w, eps)
+    ms = a * a * (C + 1) * (2 * C + 1) / 6
+    want = w * (a * ramp) / math.sqrt(ms + eps)
+    assert out.shape == (B, S, C)
+    assert torch.allclose(out, want.view(1, 1, C).expand(B, S, C), rtol=1e-12, atol=0)
+
+
+def test_scale_invariance_and_unit_rms():
+    torch.manual_seed(0)
+    y = torch.randn(3, 16, 4, 5, dtype=torch.float64)
+    w = torch.ones(16, dtype=torch.float64)
+    o1 = gated_channel_rmsnorm_ref(y, None, w, 0.0)
+    o2 = gated_channel_rmsnorm_ref(7.5 * y, None, w, 0.0)
+    assert torch.allclose(o1, o2, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(o1.pow(2).mean(-1), torch.ones(3, 4, 5, dtype=torch.float64), rtol=1e-12)
+
+
+def test_gate_and_layouts():
+    torch.manual_seed(1)
+    y, v = torch.randn(2, 6, 9, dtype=torch.float64), torch.randn(2, 6, 9, dtype=torch.float64)
+    w = torch.randn(6, dtype=torch.float64)
+    for act, f in ((1, torch.sigmoid), (2, lambda t: t * torch.sigmoid(t)), (0, lambda t: t)):
+        last = gated_channel_rmsnorm_ref(y, v, w, 1e-6, act, channels_last=True)
+        assert torch.allclose(last, gated_channel_rmsnorm_ref(y * f(v), None, w, 1e-6), rtol=1e-13, atol=0)
+        first = gated_channel_rmsnorm_ref(y, v, w, 1e-6, act, channels_last=False)
+        assert torch.equal(first, last.movedim(-1, 1))
+
+
+def test_gradcheck_float64():
+    torch.manual_seed(2)
+    y = torch.randn(2, 5, 3, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(2, 5, 3, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(5, dtype=torch.float64, requires_grad=True)
+    for act in (0, 1, 2):
+        assert torch.autograd.gradcheck(lambda a, b, c: gated_channel_rmsnorm_ref(a, b, c, 1e-3, act), (y, v, w))
+
+
+def test_input_gradient_orthogonal_to_u_at_zero_eps():
+    # out is invariant to scaling u, so d/dlambda out(lambda u) = 0  =>  sum_c du_c u_c = 0 per position
+    torch.manual_seed(3)
+    u = torch.randn(2, 8, 11, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(8, dtype=torch.float64)
+    out = gated_channel_rmsnorm_ref(u, None, w, 0.0)
+    (du,) = torch.autograd.grad(out, u, torch.randn_like(out))
+    assert (du * u).sum(1).abs().max() < 1e-12
