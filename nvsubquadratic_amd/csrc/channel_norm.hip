@@ -27,8 +27,8 @@
 // xhat), du = r (w dout - xhat m) rounded to the I/O dtype (the reference's
 // fp32 upcast hands its gradient back in that dtype), then the gate's
 // adjoint: dy = round(du * round(act(v))), dv = round(round(du * y) act'(v)).
-// dw = sum over positions of dout * xhat: each workgroup walks a contiguous
-// run of tiles, sums its share per channel in LDS (each channel owned by one
+// dw = sum over positions of dout * xhat: each workgroup walks every nwg-th
+// tile, sums its share per channel in LDS (each channel owned by one
 // thread), writes one partial row, and a second kernel adds the rows in a
 // fixed order (deterministic).
 #include "gate.h"
@@ -210,8 +210,11 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
   const int p0 = m.lr * VW;
   const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
   for (int c = t; c < C; c += kThreads) gacc[c] = 0.f;
-  const int64_t tb = wg * tiles_per_wg, te = tb + tiles_per_wg < ntiles ? tb + tiles_per_wg : ntiles;
-  for (int64_t tile = tb; tile < te; ++tile) {
+  // tiles wg, wg + nwg, ...: the workgroups of one XCD (consecutive wg) work on
+  // neighbouring tiles at the same time, so the 128-byte lines they share are
+  // read from HBM once into that XCD's L2
+  (void)tiles_per_wg;
+  for (int64_t tile = wg; tile < ntiles; tile += gridDim.x) {
     const int64_t b = tile / tiles_per_b, s0 = (tile % tiles_per_b) * TS;
     const int64_t rowbase = b * C * S;
     const int nval = int(S - s0 < TS ? S - s0 : TS);
@@ -382,9 +385,11 @@ BwdPlan bwd_plan(int64_t B, int C, int64_t S) {
   if (!p.TS) return p;
   p.tiles_per_b = ceil_div(S, int64_t(p.TS));
   p.ntiles = B * p.tiles_per_b;
+  // a multiple of 8 workgroups (when there are 8 tiles or more), so the XCD remap applies
   int64_t nwg = p.ntiles < kMaxWG ? p.ntiles : kMaxWG;
+  if (nwg >= 8) nwg -= nwg % 8;
+  p.nwg = nwg;
   p.tiles_per_wg = ceil_div(p.ntiles, nwg);
-  p.nwg = ceil_div(p.ntiles, p.tiles_per_wg);
   return p;
 }
 
