@@ -32,9 +32,6 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
            conv alone)
        python bench.py --copy-calibration   (one plain copy kernel of known size,
                                              for scaling rocprof FETCH/WRITE_SIZE)
-       python bench.py --workload hbm-patterns   (report-only: the HBM rate of config 3's
-           column-pass and row-pass access patterns with no FFT arithmetic, and of a
-           plain 16-byte copy: the ceiling those passes' traffic can reach)
 """
 
 from __future__ import annotations
@@ -71,25 +68,6 @@ def copy_calibration() -> None:
     b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
-
-
-def hbm_patterns(channels: int = 4096) -> None:
-    """Probe kernels replaying config 3's column/row pass traffic without FFT arithmetic."""
-    import ctypes
-
-    lib = ctypes.CDLL(os.path.join(ROOT, "nvsubquadratic_amd", "libnsq_probes.so"))
-    lib.nsq_probe_hbm_patterns.restype = ctypes.c_int
-    lib.nsq_probe_hbm_patterns.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
-    torch.cuda.init()
-    out = (ctypes.c_double * 6)()
-    rc = lib.nsq_probe_hbm_patterns(channels, out)
-    if rc != 0:
-        raise RuntimeError(f"nsq_probe_hbm_patterns failed with HIP error {rc}")
-    res = {}
-    for i, name in enumerate(("col_fwd_pattern", "row_pattern", "copy16")):
-        ms, nbytes = out[2 * i], out[2 * i + 1]
-        res[name] = {"ms": round(ms, 4), "bytes": int(nbytes), "TB_s": round(nbytes / (ms * 1e-3) / 1e12, 3)}
-    print(json.dumps({"workload": "hbm-patterns", "channels": channels, "report_only": True, "probes": res}), flush=True)
 
 
 def cpu_baseline(channels: int, iters: int) -> dict:
@@ -533,8 +511,7 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
                                                               "cfg4-circular", "well-rb", "hyena-gated",
-                                                              "hyena-gated-2d", "siren-1d", "hyena-norm",
-                                                              "hbm-patterns"])
+                                                              "hyena-gated-2d", "siren-1d", "hyena-norm"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -546,9 +523,6 @@ def main() -> None:
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
-        return
-    if args.workload == "hbm-patterns":
-        hbm_patterns()
         return
     if args.workload != "cfg3":
         other_workload(args.workload, args.steps, args.warmup, cpu=not args.no_cpu)

@@ -23,8 +23,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libnsq_hip.so")
-PROBES = os.path.join(HERE, "probes")
-PROBE_LIB = os.path.join(HERE, "libnsq_probes.so")
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -62,11 +60,6 @@ def build_library(jobs: int | None = None, verbose: bool = True) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)
-    # measurement probes (bench.py --workload hbm-patterns): a library of their own, not the product's
-    psrcs = sorted(glob.glob(os.path.join(PROBES, "*.hip")))
-    if psrcs:
-        _run([HIPCC, *FLAGS, "-shared", "-o", PROBE_LIB + ".tmp", *psrcs])
-        os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
     return LIB

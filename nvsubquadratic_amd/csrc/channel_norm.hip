@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
     const typename Elem<DT>::T* __restrict__ dout, const typename Elem<DT>::T* __restrict__ y,
     const typename Elem<DT>::T* __restrict__ v, const float* __restrict__ w, typename Elem<DT>::T* __restrict__ dy,
     typename Elem<DT>::T* __restrict__ dv, float* __restrict__ dw_part, int C, int64_t S, int TS,
-    int64_t tiles_per_b, int64_t ntiles, int64_t tiles_per_wg, float eps, int gated, int act, int in_blh) {
+    int64_t tiles_per_b, int64_t ntiles, float eps, int gated, int act, int in_blh) {
 #pragma clang fp contract(off)
   extern __shared__ float smem[];
   const int ld = TS + 1;
@@ -213,7 +213,6 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
   // tiles wg, wg + nwg, ...: the workgroups of one XCD (consecutive wg) work on
   // neighbouring tiles at the same time, so the 128-byte lines they share are
   // read from HBM once into that XCD's L2
-  (void)tiles_per_wg;
   for (int64_t tile = wg; tile < ntiles; tile += gridDim.x) {
     const int64_t b = tile / tiles_per_b, s0 = (tile % tiles_per_b) * TS;
     const int64_t rowbase = b * C * S;
@@ -376,7 +375,7 @@ int pick_ts(int C, bool bwd) {
 
 struct BwdPlan {
   int TS;
-  int64_t tiles_per_b, ntiles, nwg, tiles_per_wg;
+  int64_t tiles_per_b, ntiles, nwg;
 };
 
 BwdPlan bwd_plan(int64_t B, int C, int64_t S) {
@@ -389,7 +388,6 @@ BwdPlan bwd_plan(int64_t B, int C, int64_t S) {
   int64_t nwg = p.ntiles < kMaxWG ? p.ntiles : kMaxWG;
   if (nwg >= 8) nwg -= nwg % 8;
   p.nwg = nwg;
-  p.tiles_per_wg = ceil_div(p.ntiles, nwg);
   return p;
 }
 
@@ -437,8 +435,8 @@ void launch_bwd_vw(const void* dout, const void* y, const void* v, const float* 
   const size_t lds = bwd_lds(C, p.TS, VW);
   allow_lds(&chnorm_bwd_kernel<DT, VW>, lds);
   hipLaunchKernelGGL((chnorm_bwd_kernel<DT, VW>), dim3(unsigned(p.nwg)), dim3(kThreads), lds, st, (const T*)dout,
-                     (const T*)y, (const T*)v, w, (T*)dy, (T*)dv, part, C, S, p.TS, p.tiles_per_b, p.ntiles,
-                     p.tiles_per_wg, eps, gated, act, out_blh);
+                     (const T*)y, (const T*)v, w, (T*)dy, (T*)dv, part, C, S, p.TS, p.tiles_per_b, p.ntiles, eps,
+                     gated, act, out_blh);
 }
 
 template <int DT>

@@ -6,23 +6,8 @@
 #include <initializer_list>
 
 #include "fftconv1d_impl.h"
-#include "fftconv1d_team.h"
 
 namespace nsq {
-
-// Plan choice for the shapes the team plan (fftconv1d_team.h) is built for.
-// Both plans give bitwise-identical results.  The multi-kernel 4-step plan is
-// the default: it is faster on MI355X (config 3: 13.3 + 17.5 ms against 15.5 +
-// 26.0 ms), because both are bound by the row FFTs' own issue rate rather than
-// by HBM, and the team plan recomputes x's and k's column transforms in the
-// backward.  The team plan needs a workspace independent of D (384 MiB at
-// config 3 against 24 GiB including the forward state the multi-kernel
-// backward reuses); NSQ_1D_PLAN=team selects it.
-static bool use_team_plan(const Plan1D& p, int64_t B, int64_t kbatch) {
-  const char* e = std::getenv("NSQ_1D_PLAN");
-  if (!e || std::strcmp(e, "team") != 0) return false;
-  return team_plan_ok(p, B, kbatch);
-}
 
 static int validate(const void* a, const void* b, const float* k, int dtype, int64_t B, int64_t H, int64_t L,
                     int64_t K, int64_t kbatch, Plan1D& p) {
@@ -110,7 +95,6 @@ static size_t shifted_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K
 static size_t causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int64_t kbatch, int direction) {
   Plan1D p;
   if (!make_plan(L, K, p) || p.fused) return 0;
-  if (use_team_plan(p, B, kbatch)) return team_workspace_bytes(p, direction);
   const int64_t N = int64_t(1) << p.logN;
   const int64_t nk = kbatch * H;
   // 4-step blocks of N complex values: x, k (forward: y in place of x, or in a third block kept with x and k for
@@ -128,12 +112,6 @@ static int causal_fwd(const void* x, const float* k, const void* shortcut, void*
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
-  if (use_team_plan(p, B, kbatch)) {
-    const size_t need = team_workspace_bytes(p, NSQ_DIR_FWD);
-    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv1d_causal_fwd: workspace of %zu bytes required, got %zu",
-                  need, workspace_bytes);
-    return team_fwd(p, dtype, x, k, shortcut, y, int(H), int(L), int(K), workspace, tw, st);
-  }
   float2* ws = nullptr;
   bool save = false;
   if (!p.fused) {
@@ -173,12 +151,6 @@ static int causal_bwd(const void* g, const void* x, const float* k, const void* 
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
-  if (use_team_plan(p, B, kbatch)) {  // recomputes every transform: no forward state
-    const size_t need = team_workspace_bytes(p, NSQ_DIR_BWD);
-    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "fftconv1d_causal_bwd: workspace of %zu bytes required, got %zu",
-                  need, workspace_bytes);
-    return team_bwd(p, dtype, g, x, k, shortcut, gx, gk, gs, int(H), int(L), int(K), workspace, tw, st);
-  }
   float2* ws = nullptr;
   if (!p.fused) {
     const size_t need = causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD);

@@ -24,7 +24,9 @@ __global__ __launch_bounds__(256) void batched_transpose_kernel(const T* __restr
                                                                 int64_t R, int64_t C) {
   constexpr int E = 16 / int(sizeof(T));  // elements per 16-byte vector
   __shared__ T tile[kTile][kTile + kPad];
-  const int64_t c0 = int64_t(blockIdx.x) * kTile, r0 = int64_t(blockIdx.y) * kTile;
+  // row tiles on grid.x (up to 2^31 - 1 of them: R is the long axis, L or L times the spatial volume),
+  // column (channel) tiles on grid.y, the batch on grid.z
+  const int64_t r0 = int64_t(blockIdx.x) * kTile, c0 = int64_t(blockIdx.y) * kTile;
   const int64_t boff = int64_t(blockIdx.z) * R * C;
   const T* s = src + boff;
   T* d = dst + boff;
@@ -72,7 +74,7 @@ void launch_transpose(const void* src, void* dst, int64_t B, int64_t R, int64_t 
   constexpr int E = 16 / int(sizeof(T));
   const bool vec = R % E == 0 && C % E == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
-  const dim3 grid(unsigned(ceil_div(C, int64_t(kTile))), unsigned(ceil_div(R, int64_t(kTile))), unsigned(B));
+  const dim3 grid(unsigned(ceil_div(R, int64_t(kTile))), unsigned(ceil_div(C, int64_t(kTile))), unsigned(B));
   if (vec)
     hipLaunchKernelGGL((batched_transpose_kernel<T, true>), grid, dim3(256), 0, st, (const T*)src, (T*)dst, R, C);
   else
@@ -90,7 +92,7 @@ extern "C" int nsq_batched_transpose(const void* src, void* dst, int elem_bytes,
   NSQ_CHECK_ARG(src != dst, "batched_transpose: src and dst must not alias");
   NSQ_CHECK_ARG(elem_bytes == 2 || elem_bytes == 4, "batched_transpose: element size %d must be 2 or 4", elem_bytes);
   NSQ_CHECK_ARG(B >= 1 && R >= 1 && C >= 1, "batched_transpose: sizes must be positive");
-  NSQ_CHECK_ARG(B <= 65535 && ceil_div(R, int64_t(kTile)) <= 65535 && ceil_div(C, int64_t(kTile)) <= 0x7fffffff,
+  NSQ_CHECK_ARG(B <= 65535 && ceil_div(C, int64_t(kTile)) <= 65535 && ceil_div(R, int64_t(kTile)) <= 0x7fffffff,
                 "batched_transpose: B=%lld R=%lld C=%lld exceed the launch grid", (long long)B, (long long)R,
                 (long long)C);
   hipStream_t st = (hipStream_t)stream;

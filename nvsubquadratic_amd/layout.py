@@ -16,7 +16,7 @@ from torch.library import custom_op
 
 from . import _lib
 
-__all__ = ["channels_first_contiguous", "transpose_inner_op"]
+__all__ = ["channels_first_contiguous", "transpose_fits", "transpose_inner_op"]
 
 
 @custom_op("nsq_hip::transpose_inner", mutates_args=())
@@ -45,6 +45,12 @@ def _transpose_backward(ctx, g):
 transpose_inner_op.register_autograd(_transpose_backward, setup_context=lambda ctx, inputs, output: None)
 
 
+def transpose_fits(B: int, C: int) -> bool:
+    """Whether ``nsq_batched_transpose`` takes a ``[B, R, C]`` batch: the batch on grid.z and the column tiles
+    (64 channels each) on grid.y, at most 65535 each; the row tiles sit on grid.x (2^31 - 1), so R is free."""
+    return B <= 65535 and -(-C // 64) <= 65535
+
+
 def channels_first_contiguous(t: torch.Tensor) -> torch.Tensor:
     """``t`` ``[B, H, *S]`` as a contiguous tensor.  A channels-last view (``t.movedim(1, -1)`` contiguous, as a
     ``_w_reshape`` / ``_blh`` wrapper's ``rearrange`` or the gradient of its output leaves it) moves through
@@ -53,6 +59,6 @@ def channels_first_contiguous(t: torch.Tensor) -> torch.Tensor:
         return t.contiguous()
     m = t.movedim(1, -1)
     B, H = t.shape[0], t.shape[1]
-    if not m.is_contiguous() or B > 65535 or t.numel() == 0:
+    if not m.is_contiguous() or not transpose_fits(B, H) or t.numel() == 0:
         return t.contiguous()
     return transpose_inner_op(m.reshape(B, -1, H)).view(t.shape)

@@ -129,6 +129,13 @@ def gated_channel_rmsnorm(y: torch.Tensor, v: Optional[torch.Tensor], weight: to
     if weight.shape != (y.shape[1],):
         raise ValueError(f"weight shape {tuple(weight.shape)} != ({y.shape[1]},)")
     shape = y.shape
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (y, v, weight)):
+        # the backward's two LDS tiles take fewer channels than the forward's one (C <= 3536 against 7781): refuse
+        # before the forward runs rather than at loss.backward()
+        C, S = shape[1], max(1, y.numel() // max(1, shape[0] * shape[1]))
+        if _lib.get_lib().nsq_channel_rmsnorm_bwd_workspace_bytes(shape[0], C, S) == 0:
+            raise NotImplementedError(f"fft_backend='hip' channel RMSNorm backward: C={C} exceeds the backward's "
+                                      f"LDS tiles (C <= 3536); the forward alone takes C <= 7781")
     w = _WeightToF32.apply(weight) if weight.dtype != torch.float32 else weight
     out = gated_channel_rmsnorm_op(_flat(y), _flat(v) if v is not None else None, w.contiguous(), float(eps),
                                    gate_code(gate_nonlinear) if v is not None else 0, bool(channels_last_out))

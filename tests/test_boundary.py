@@ -196,3 +196,40 @@ def test_fake_implementations_propagate_shapes_without_a_gpu():
         assert y2.shape == x2.shape and st2.numel() == 0
         yb = torch.ops.nsq_hip.b2b_causal_conv1d(torch.empty(2, 12, 64), torch.empty(12, 3), torch.empty(4, 9), None)
         assert yb.shape == (2, 4, 64)
+
+
+def test_transpose_launch_limits_and_fallback():
+    """The batched transpose takes any row count (row tiles on grid.x) but at most 65535 batches and 65535
+    column tiles; beyond that the library refuses before any launch and the layout helper falls back to
+    ``Tensor.contiguous``."""
+    from nvsubquadratic_amd.layout import transpose_fits
+
+    assert transpose_fits(65535, 65535 * 64)
+    assert not transpose_fits(65536, 8)
+    assert not transpose_fits(1, 65535 * 64 + 1)
+    assert transpose_fits(1, 8)  # any R: the row tiles are not limited to 65535
+    if not os.path.exists(_lib.LIB_PATH):
+        return
+    lib = _lib.get_lib()
+    fake_src, fake_dst = 1 << 20, 2 << 20  # argument checks run before any HIP call; nothing is dereferenced
+    assert lib.nsq_batched_transpose(fake_src, fake_dst, 2, 1, 64, 65535 * 64 + 1, None) != 0
+    assert b"exceed the launch grid" in lib.nsq_last_error()
+    assert lib.nsq_batched_transpose(fake_src, fake_dst, 2, 65536, 64, 8, None) != 0
+    assert lib.nsq_batched_transpose(fake_src, fake_dst, 3, 1, 64, 8, None) != 0
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_channel_norm_backward_limit_raised_before_forward():
+    """3536 < C <= 7781: the forward would run, its backward cannot; with a gradient wanted the call refuses up
+    front (host-side query, no launch), without one it goes on to the device check."""
+    from nvsubquadratic_amd import norm_hip as N
+
+    lib = _lib.get_lib()
+    assert lib.nsq_channel_rmsnorm_bwd_workspace_bytes(2, 3536, 64) > 0
+    assert lib.nsq_channel_rmsnorm_bwd_workspace_bytes(2, 3537, 64) == 0
+    y = torch.randn(2, 4000, 8, requires_grad=True)
+    w = torch.ones(4000)
+    with pytest.raises(NotImplementedError, match="C <= 3536"):
+        N.gated_channel_rmsnorm(y, None, w)
+    with torch.no_grad(), pytest.raises(_lib.HipLibraryError):
+        N.gated_channel_rmsnorm(y, None, w)  # forward-only: passes the limit, then refuses CPU tensors

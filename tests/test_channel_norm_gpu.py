@@ -68,7 +68,8 @@ def test_ragged_shapes(B, C, spatial, channels_last):
 
 
 def test_several_tiles_per_workgroup_bf16():
-    # C = 384 backward tiles hold 16 positions: 4 x 16384 positions = 4096 tiles over 2048 workgroups
+    # C = 384 backward tiles hold 16 positions: 4 x 16384 positions = 4096 tiles over 512 workgroups (the
+    # backward grid's cap), 8 tiles each
     _case(4, 384, (128, 128), torch.bfloat16, "sigmoid", True)
 
 

@@ -22,6 +22,18 @@ def test_transpose_matches_torch(dtype, B, R, C):
     assert torch.equal(y, x.transpose(1, 2).contiguous())
 
 
+@pytest.mark.parametrize("R", [65535 * 64 + 128, 65535 * 64 + 37])
+def test_transpose_rows_beyond_65535_tiles(R):
+    """More than 65535 row tiles (R > 65535 * 64, e.g. L = 2^22 on the 4-step plan): the row tiles sit on grid.x;
+    a vector tile run and an element-path edge."""
+    print(f"transpose long rows R={R}", flush=True)
+    x = torch.randn(1, R, 8, device="cuda").to(torch.bfloat16)
+    y = transpose_inner_op(x)
+    assert torch.equal(y, x.transpose(1, 2).contiguous())
+    v = x.movedim(-1, 1)  # the channels-last view a BLH wrapper hands over
+    assert torch.equal(channels_first_contiguous(v), v.contiguous())
+
+
 def test_channels_first_contiguous_views():
     x = torch.randn(2, 48, 40, 24, device="cuda").to(torch.bfloat16)  # BLH [B, X, Y, H]
     v = x.movedim(-1, 1)                                                # the rearranged view [B, H, X, Y]
