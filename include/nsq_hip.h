@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 10
+#define NSQ_ABI_VERSION 11
 
 enum {
   NSQ_OK = 0,
@@ -376,9 +376,28 @@ int nsq_siren_mlp_fwd(const float* grid, int64_t G, int d, const float* w0, cons
  * linear): k[h][g] = b_out[h] + W_out[h] . a_nh[g] for W_out [H, HD], b_out [H]
  * (may be null), act rows 0..HD-1 of nsq_siren_mlp_fwd's output (row stride
  * lda), written as k [H][G] fp32: the filter in the layout the FFT convs read.
- * HD in {16, 32, 64, 128}.  Its gradients are plain GEMMs on the caller's side. */
+ * HD in {16, 32, 64, 128}. */
 int nsq_siren_readout_fwd(const float* wout, const float* bout, int64_t H, int HD, const float* act, int64_t lda,
                           int64_t G, float* k, void* stream);
+
+/* The readout's gradients in one pass over gk (ABI 11; the reference gets them
+ * from autograd of SIRENKernelND's out_linear, kernels_nd.py:1189, two GEMMs
+ * that each read the filter gradient):
+ *   gact[s][j][g] = sum_h W_out[h][j] gk[s][h][g]          ([nb][HD][G], row stride G)
+ *   gwout[h][j]   = sum_s sum_g gk[s][h][g] act[s][j][g]   ([H][HD])
+ *   gbout[h]      = sum_s sum_g gk[s][h][g]                ([H]; may be null)
+ * for nb samples s (1 for a shared filter): gk [nb][H][ldk], act [nb][HD + 1][lda]
+ * (nsq_siren_mlp_fwd's output; row HD is not read).  The products run on the bf16
+ * matrix cores with both operands split into bf16 halves (three products per step,
+ * fp32 accumulation: ~2^-17 relative error per product); partial sums are reduced
+ * in a fixed order (deterministic).  HD in {16, 32, 64}; 128 returns
+ * NSQ_ERR_UNSUPPORTED (the caller keeps library GEMMs there).  gact feeds
+ * nsq_siren_mlp_bwd with gact_stride_j = G, gact_stride_g = 1. */
+size_t nsq_siren_readout_bwd_workspace_bytes(int64_t H, int HD, int64_t G, int64_t nb);
+
+int nsq_siren_readout_bwd(const float* gk, int64_t ldk, const float* act, int64_t lda, const float* wout, int64_t H,
+                          int HD, int64_t G, int64_t nb, float* gact, float* gwout, float* gbout, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 size_t nsq_siren_mlp_bwd_workspace_bytes(int64_t G, int d, int E, int nh, int HD);
 

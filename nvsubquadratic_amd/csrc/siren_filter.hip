@@ -515,6 +515,339 @@ static void launch_readout(const float* wout, const float* bout, const float* ac
     hipLaunchKernelGGL((siren_readout_fwd_kernel<HD, false>), grd, dim3(256), 0, st, wout, bout, act, lda, G, H, k);
 }
 
+// ---------------------------------------------------------------------------
+// Readout backward in one pass over the filter gradient gk (read once):
+//   gact[nb][j][g] = sum_h W_out[h][j] gk[nb][h][g]            (K = h)
+//   gW[h][j]       = sum_nb sum_g gk[nb][h][g] a[nb][j][g]      (K = g)
+//   gb[h]          = sum_nb sum_g gk[nb][h][g]
+// (a = rows 0..HD-1 of act).  Both products run on v_mfma_f32_16x16x32_bf16
+// with every operand split v = hi + lo into bf16 halves (hi = bf16(v), lo =
+// bf16(v - hi)) and three products per step, hi.hi + hi.lo + lo.hi, fp32
+// accumulation: ~2^-17 relative error per product (the dropped lo.lo term and
+// lo's rounding), against ~5x the time on the fp32 matrix path (whose rate is
+// the VALU's, so a one-pass fp32 kernel would be bound by its multiply-adds,
+// not by reading gk).  Lane layout of the product (checked on MI355X):
+// A[l % 16][8 (l / 16) + e], B[8 (l / 16) + e][l % 16], D[4 (l / 16) + r][l % 16].
+//
+// Work split.  A workgroup of 8 waves owns kRbGpw * 8 consecutive points of
+// one sample nb and a slice of the channels; wave w owns kRbGpw of the points
+// and sweeps the slice in chunks of 32 channels:
+//  * gact: the wave's [HD][kRbGpw] accumulator stays in registers across the
+//    sweep (B operand: gk loaded as 8 channels x 1 point per lane);
+//  * gW, gb: each chunk's [32][HD] product over the wave's points (A operand:
+//    gk loaded as 1 channel x 8 points per lane; the second load of the same
+//    lines is an L2 hit) is summed over the 8 waves through LDS in a fixed
+//    order and written as the workgroup's partial; siren_sum_parts_kernel adds
+//    the partials of all workgroups in a fixed order.
+// With several channel slices (small G), gact is written per slice and
+// siren_sum_parts_kernel adds the slices in order.  Deterministic throughout.
+// ---------------------------------------------------------------------------
+typedef float nsq_f32x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 nsq_bf16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kRbWaves = 8;
+constexpr int kRbThreads = 64 * kRbWaves;
+constexpr int kRbGpw = 64;   // points per wave
+constexpr int kRbHc = 32;    // channels per chunk
+
+__device__ __forceinline__ void split8(const nsq_f32x8_t& v, nsq_bf16x8_t& hi, nsq_bf16x8_t& lo) {
+  hi = __builtin_convertvector(v, nsq_bf16x8_t);
+  const nsq_f32x8_t r = v - __builtin_convertvector(hi, nsq_f32x8_t);
+  lo = __builtin_convertvector(r, nsq_bf16x8_t);
+}
+
+__device__ __forceinline__ f32x4 mfma_split(const nsq_bf16x8_t& ah, const nsq_bf16x8_t& al, const nsq_bf16x8_t& bh,
+                                            const nsq_bf16x8_t& bl, f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+  return c;
+}
+
+// 8 consecutive floats p[0..7] of a row whose valid length from p is n (zeros
+// past it).  VEC: p 16-byte aligned.
+template <bool VEC>
+__device__ __forceinline__ nsq_f32x8_t load8(const float* __restrict__ p, int64_t n) {
+  nsq_f32x8_t v;
+  if (VEC && n >= 8) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+    v = nsq_f32x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = e < n ? p[e] : 0.f;
+  }
+  return v;
+}
+
+// Raw buffer resource over bytes [p, p + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rb_rsrc(const float* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, bytes, 0x00020000);
+}
+
+template <int HD, bool VEC>
+__global__ __launch_bounds__(kRbThreads) void siren_readout_bwd_kernel(
+    const float* __restrict__ gk, int64_t ldk, const float* __restrict__ act, int64_t lda,
+    const float* __restrict__ wout, int64_t G, int H, int hslice, float* __restrict__ gact, int64_t gact_slice,
+    float* __restrict__ gw_part, float* __restrict__ gb_part) {
+  constexpr int NJ = HD / 16, NGB = kRbGpw / 16, NKS = kRbGpw / 32, RS = HD + 1;
+  // TS: row stride (words) of a wave's transposition tile [32 channels][kRbGpw points]: 66 puts the 4 channel
+  // groups of a gact operand read (rows 8q + e) 16 banks apart, so a read covers the 64 banks once
+  constexpr int TS = kRbGpw + 2;
+  // chunk partials double-buffered where LDS allows (HD <= 32), else one buffer and a second barrier
+  constexpr int NBUF = (2 * kRbWaves * kRbHc * RS + kRbWaves * kRbHc * TS) * 4 <= 160 * 1024 ? 2 : 1;
+  __shared__ float red[NBUF][kRbWaves][kRbHc * RS];
+  __shared__ float tile[kRbWaves][kRbHc * TS];
+  const int wv = int(threadIdx.x) >> 6, l = int(threadIdx.x) & 63, q = l >> 4, p = l & 15;
+  const int64_t ngb = gridDim.x;
+  const int nb = int(blockIdx.z), hs = int(blockIdx.y);
+  const int64_t gw0 = (int64_t(blockIdx.x) * kRbWaves + wv) * kRbGpw;
+  const int hb = hs * hslice, he = hb + hslice < H ? hb + hslice : H;
+  const float* gkb = gk + int64_t(nb) * H * ldk;
+  const float* ab = act + int64_t(nb) * (HD + 1) * lda;
+  // every point of this wave's block is < G (wave-uniform): the gW operand loads need no per-point guard
+  const bool full = VEC && gw0 + kRbGpw <= G;
+  const int rowb = int(ldk) * 4;  // bytes per gk row (ldk <= 2^23, checked by the entry point)
+  // byte offsets of this lane inside a chunk's rows (chunk base = row h0, column 0; gw0 < G + 512 <= 2^23 + 512)
+  // (the whole offset goes in the lane's offset register, which the buffer range check covers; only compile-time
+  // steps ride in the instruction's immediate)
+  int off_w[2];  // gW operand: row 16 hbk + p, points gw0 + 32 ks + 8q + e
+#pragma unroll
+  for (int hbk = 0; hbk < 2; ++hbk) off_w[hbk] = ((16 * hbk + p) * int(ldk) + int(gw0) + 8 * q) * 4;
+  const int off_o = (8 * q * HD + p) * 4;  // W_out operand: row 8q + e, column 16 jt + p
+
+  // act as the gW product's B operand, B[k = g][n = j] = a[j][g]: held for the whole sweep
+  nsq_bf16x8_t bah[NJ][NKS], bal[NJ][NKS];
+#pragma unroll
+  for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int64_t g = gw0 + 32 * ks + 8 * q;
+      const nsq_f32x8_t v = load8<VEC>(ab + int64_t(16 * jt + p) * lda + g, G - g);
+      split8(v, bah[jt][ks], bal[jt][ks]);
+    }
+  f32x4 acc_a[NJ][NGB];  // gact^T tiles D[j][g]
+#pragma unroll
+  for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+    for (int gb = 0; gb < NGB; ++gb) acc_a[jt][gb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // gW operand of a chunk (rows h0 + 16 hbk + p, 8 points per k-step), loaded one chunk ahead
+  auto load_gw_operand = [&](int h0, int hn, nsq_f32x8_t (&v)[2][NKS]) {
+    if (full) {
+      const __amdgpu_buffer_rsrc_t r = rb_rsrc(gkb + int64_t(h0) * ldk, hn * rowb);
+#pragma unroll
+      for (int hbk = 0; hbk < 2; ++hbk)
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, off_w[hbk] + 128 * ks, 0, 0);
+          const auto y = __builtin_amdgcn_raw_buffer_load_b128(r, off_w[hbk] + 128 * ks + 16, 0, 0);
+          v[hbk][ks] = nsq_f32x8_t{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
+                                   __uint_as_float(x[3]), __uint_as_float(y[0]), __uint_as_float(y[1]),
+                                   __uint_as_float(y[2]), __uint_as_float(y[3])};
+        }
+    } else {
+#pragma unroll
+      for (int hbk = 0; hbk < 2; ++hbk) {
+        const int hh = 16 * hbk + p;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const int64_t g = gw0 + 32 * ks + 8 * q;
+          v[hbk][ks] = hh < hn ? load8<false>(gkb + int64_t(h0 + hh) * ldk + g, G - g) : nsq_f32x8_t{};
+        }
+      }
+    }
+  };
+
+  nsq_f32x8_t cur[2][NKS], nxt[2][NKS];
+  if (hb < he) load_gw_operand(hb, he - hb < kRbHc ? he - hb : kRbHc, cur);
+  int buf = 0;
+  for (int h0 = hb; h0 < he; h0 += kRbHc, buf = NBUF == 2 ? buf ^ 1 : 0) {
+    const int hn = he - h0 < kRbHc ? he - h0 : kRbHc;  // valid channels of this chunk
+    const __amdgpu_buffer_rsrc_t ro = rb_rsrc(wout + int64_t(h0) * HD, hn * HD * 4);
+    // gact's A operand, A[m = j][k = h] = W_out[h][j] (rows >= hn read as 0)
+    nsq_f32x8_t wv8[NJ];
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        wv8[jt][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ro, off_o + 64 * jt + e * HD * 4, 0, 0));
+    // the next chunk's gW operand, in flight while this chunk's products run
+    const int h1 = h0 + kRbHc;
+    if (h1 < he) load_gw_operand(h1, he - h1 < kRbHc ? he - h1 : kRbHc, nxt);
+    // the chunk's gk values (arrived during the previous chunk) into the wave's transposition tile, row 16 hbk +
+    // p, points 32 ks + 8 q + e: the gact operand reads them back as 8 channels x 1 point per lane
+    float* tw_ = tile[wv];
+#pragma unroll
+    for (int hbk = 0; hbk < 2; ++hbk)
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        float* d = tw_ + (16 * hbk + p) * TS + 32 * ks + 8 * q;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) *reinterpret_cast<float2*>(d + e) = make_float2(cur[hbk][ks][e], cur[hbk][ks][e + 1]);
+      }
+    // --- gW: A[m = h][k = g] = gk[h][g], B[k = g][n = j] = a[j][g]; gb from the same values
+    f32x4 acc_w[2][NJ];
+    float bsum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int hbk = 0; hbk < 2; ++hbk) {
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt) acc_w[hbk][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const nsq_f32x8_t v = cur[hbk][ks];
+        bsum[hbk] += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        nsq_bf16x8_t ah, al;
+        split8(v, ah, al);
+#pragma unroll
+        for (int jt = 0; jt < NJ; ++jt)
+          acc_w[hbk][jt] = mfma_split(ah, al, bah[jt][ks], bal[jt][ks], acc_w[hbk][jt]);
+      }
+    }
+    // the wave's chunk partials to LDS: D[m = h = 16 hbk + 4 q + r][n = j = 16 jt + p]; gb per channel
+    float* rw = red[buf][wv];
+#pragma unroll
+    for (int hbk = 0; hbk < 2; ++hbk) {
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rw[(16 * hbk + 4 * q + r) * RS + 16 * jt + p] = acc_w[hbk][jt][r];
+      float b = bsum[hbk];
+      b += __shfl_xor(b, 16);
+      b += __shfl_xor(b, 32);
+      if (q == 0) rw[(16 * hbk + p) * RS + HD] = b;
+    }
+    // --- gact: B[k = h][n = g] = gk[h][g] from the tile (the wave's own LDS writes above, in order); rows >= hn
+    // are zero, points >= G only reach output columns that are not stored
+    wave_lds_order();
+    nsq_bf16x8_t wah[NJ], wal[NJ];
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt) split8(wv8[jt], wah[jt], wal[jt]);
+#pragma unroll
+    for (int gb = 0; gb < NGB; ++gb) {
+      nsq_f32x8_t gv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gv[e] = tw_[(8 * q + e) * TS + 16 * gb + p];
+      nsq_bf16x8_t bh, bl;
+      split8(gv, bh, bl);
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt) acc_a[jt][gb] = mfma_split(wah[jt], wal[jt], bh, bl, acc_a[jt][gb]);
+    }
+    __syncthreads();
+    // fixed-order sum over the 8 waves; one partial row block per workgroup and chunk
+    const int64_t prow = (int64_t(nb) * ngb + blockIdx.x) * H;
+    for (int e = int(threadIdx.x); e < kRbHc * RS; e += kRbThreads) {
+      const int hh = e / RS, j = e - hh * RS;
+      if (hh >= hn) continue;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kRbWaves; ++w) sum += red[buf][w][e];
+      if (j < HD)
+        gw_part[(prow + h0 + hh) * HD + j] = sum;
+      else if (gb_part)
+        gb_part[prow + h0 + hh] = sum;
+    }
+    // double-buffered, no second barrier: the next chunk writes the other buffer, and the chunk after it follows
+    // this chunk's successor's barrier, which every reader of this buffer has passed
+    if constexpr (NBUF == 1) __syncthreads();
+#pragma unroll
+    for (int hbk = 0; hbk < 2; ++hbk)
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) cur[hbk][ks] = nxt[hbk][ks];
+  }
+  // gact^T tiles: D[m = j = 16 jt + 4 q + r][n = g = 16 gb + p]
+  float* ga = gact + int64_t(hs) * gact_slice + int64_t(nb) * HD * G;
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb) {
+    const int64_t g = gw0 + 16 * gb + p;
+    if (g < G) {
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ga[int64_t(16 * jt + 4 * q + r) * G + g] = acc_a[jt][gb][r];
+    }
+  }
+}
+
+// out[i] = sum_{s < ns} part[s * n + i] for i < n: thread i walks the parts in order with 16 interleaved running
+// sums (s = 0, 16, 32, ... / 1, 17, ...; 16 loads in flight per thread) added in a fixed tree at the end, so the
+// result is bitwise repeatable.
+__global__ __launch_bounds__(256) void siren_sum_parts_kernel(const float* __restrict__ part, int64_t ns, int64_t n,
+                                                              float* __restrict__ out) {
+  constexpr int U = 16;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  float s[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) s[u] = 0.f;
+  int64_t k = 0;
+  for (; k + U <= ns; k += U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = part[(k + u) * n + i];
+#pragma unroll
+    for (int u = 0; u < U; ++u) s[u] += v[u];
+  }
+  for (int u = 0; k < ns; ++k, ++u) s[u] += part[k * n + i];
+#pragma unroll
+  for (int w = U / 2; w >= 1; w /= 2)
+#pragma unroll
+    for (int u = 0; u < w; ++u) s[u] += s[u + w];
+  out[i] = s[0];
+}
+
+// Readout-backward launch geometry: point blocks of 8 waves x kRbGpw, channel
+// slices of whole 32-channel chunks chosen so that the grid reaches ~512
+// workgroups (two per CU) when the points alone do not.
+struct RbPlan {
+  int64_t ngb;
+  int hs, hslice;
+  size_t gw_part, gb_part, gact_part, total;  // float offsets / count
+};
+
+RbPlan rb_plan(int64_t H, int HD, int64_t G, int64_t nb) {
+  RbPlan p{};
+  p.ngb = ceil_div(G, int64_t(kRbWaves) * kRbGpw);
+  const int64_t chunks = ceil_div(H, int64_t(kRbHc));
+  int64_t hs = ceil_div(512, p.ngb * nb);
+  hs = hs < 1 ? 1 : (hs > chunks ? chunks : hs);
+  p.hslice = int(ceil_div(chunks, hs) * kRbHc);
+  p.hs = int(ceil_div(H, int64_t(p.hslice)));
+  auto al = [](size_t v) { return (v + 63) / 64 * 64; };
+  p.gw_part = 0;
+  p.gb_part = al(size_t(nb * p.ngb) * size_t(H) * HD);
+  p.gact_part = al(p.gb_part + size_t(nb * p.ngb) * size_t(H));
+  p.total = al(p.gact_part + (p.hs > 1 ? size_t(p.hs) * size_t(nb) * HD * size_t(G) : 0));
+  return p;
+}
+
+template <int HD>
+void launch_readout_bwd(const float* gk, int64_t ldk, const float* act, int64_t lda, const float* wout, int64_t H,
+                        int64_t G, int64_t nb, float* gact, float* gwout, float* gbout, float* ws, hipStream_t st) {
+  const RbPlan p = rb_plan(H, HD, G, nb);
+  const bool vec = ldk % 4 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(gk) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(act) & 15) == 0;
+  float* ga = p.hs > 1 ? ws + p.gact_part : gact;
+  const int64_t gslice = int64_t(nb) * HD * G;
+  const dim3 grd(unsigned(p.ngb), unsigned(p.hs), unsigned(nb));
+  float* gbp = gbout ? ws + p.gb_part : nullptr;
+  if (vec)
+    hipLaunchKernelGGL((siren_readout_bwd_kernel<HD, true>), grd, dim3(kRbThreads), 0, st, gk, ldk, act, lda, wout,
+                       G, int(H), p.hslice, ga, gslice, ws + p.gw_part, gbp);
+  else
+    hipLaunchKernelGGL((siren_readout_bwd_kernel<HD, false>), grd, dim3(kRbThreads), 0, st, gk, ldk, act, lda, wout,
+                       G, int(H), p.hslice, ga, gslice, ws + p.gw_part, gbp);
+  if (p.hs > 1)
+    hipLaunchKernelGGL(siren_sum_parts_kernel, dim3(unsigned(ceil_div(gslice, 256))), dim3(256), 0, st, ga,
+                       int64_t(p.hs), gslice, gact);
+  const int64_t nparts = nb * p.ngb, nw = H * HD;
+  hipLaunchKernelGGL(siren_sum_parts_kernel, dim3(unsigned(ceil_div(nw, 256))), dim3(256), 0, st, ws + p.gw_part,
+                     nparts, nw, gwout);
+  if (gbout)
+    hipLaunchKernelGGL(siren_sum_parts_kernel, dim3(unsigned(ceil_div(H, 256))), dim3(256), 0, st, gbp, nparts, H,
+                       gbout);
+}
+
 constexpr int kSirenMaxLds = 160 * 1024;
 
 // LDS bytes per wave of the backward pass 1.
@@ -658,6 +991,42 @@ int nsq_siren_readout_fwd(const float* wout, const float* bout, int64_t H, int H
     default:
       set_error("siren_readout_fwd: mlp_hidden_dim %d must be 16, 32, 64 or 128", HD);
       return NSQ_ERR_UNSUPPORTED;
+  }
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+size_t nsq_siren_readout_bwd_workspace_bytes(int64_t H, int HD, int64_t G, int64_t nb) {
+  if (H < 1 || G < 1 || G > (int64_t(1) << 23) || nb < 1 || !(HD == 16 || HD == 32 || HD == 64)) return 0;
+  return nsq::rb_plan(H, HD, G, nb).total * sizeof(float);
+}
+
+int nsq_siren_readout_bwd(const float* gk, int64_t ldk, const float* act, int64_t lda, const float* wout, int64_t H,
+                          int HD, int64_t G, int64_t nb, float* gact, float* gwout, float* gbout, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  using namespace nsq;
+  clear_error();
+  NSQ_CHECK_ARG(gk && act && wout && gact && gwout, "siren_readout_bwd: null pointer argument");
+  NSQ_CHECK_ARG(G >= 1 && ldk >= G && lda >= G && ldk <= (int64_t(1) << 23),
+                "siren_readout_bwd: G=%lld, ldk=%lld, lda=%lld (rows of at most 2^23 points)", (long long)G,
+                (long long)ldk, (long long)lda);
+  NSQ_CHECK_ARG(H >= 1 && H <= (int64_t(1) << 20), "siren_readout_bwd: H=%lld out of range", (long long)H);
+  NSQ_CHECK_ARG(nb >= 1 && nb <= 65535, "siren_readout_bwd: %lld samples out of range", (long long)nb);
+  if (!(HD == 16 || HD == 32 || HD == 64)) {
+    set_error("siren_readout_bwd: mlp_hidden_dim %d must be 16, 32 or 64", HD);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  const RbPlan p = rb_plan(H, HD, G, nb);
+  NSQ_CHECK_ARG(p.ngb <= 0x7fffffff && p.hs <= 65535, "siren_readout_bwd: launch grid too large");
+  NSQ_CHECK_ARG(workspace && workspace_bytes >= p.total * sizeof(float),
+                "siren_readout_bwd: workspace of %zu bytes required, got %zu", p.total * sizeof(float),
+                workspace_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  float* ws = static_cast<float*>(workspace);
+  switch (HD) {
+    case 16: launch_readout_bwd<16>(gk, ldk, act, lda, wout, H, G, nb, gact, gwout, gbout, ws, st); break;
+    case 32: launch_readout_bwd<32>(gk, ldk, act, lda, wout, H, G, nb, gact, gwout, gbout, ws, st); break;
+    default: launch_readout_bwd<64>(gk, ldk, act, lda, wout, H, G, nb, gact, gwout, gbout, ws, st); break;
   }
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;

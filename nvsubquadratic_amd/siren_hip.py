@@ -14,8 +14,8 @@ on the matrix cores and writes only ``[a_nh^T; 1]`` (``[HD + 1, G]``) -- no per-
 HBM.  The readout (``nsq_siren_readout_fwd``: one point per lane, the W_out rows wave-uniform) writes the
 filter straight as ``[out_dim, G]`` -- the layout the FFT convs read -- so neither the ``[G, out_dim]``
 result nor its transpose exists; ``forward`` hands the reference's
-``[1, *grid, out_dim]`` shape back as a view of it.  The readout's two gradient GEMMs come from
-autograd; the MLP backward (``nsq_siren_mlp_bwd``) recomputes the layers from the grid and reduces
+``[1, *grid, out_dim]`` shape back as a view of it.  The readout's gradients come from one pass over the
+filter gradient (``nsq_siren_readout_bwd``); the MLP backward (``nsq_siren_mlp_bwd``) recomputes the layers from the grid and reduces
 every hidden weight gradient over the points in a fixed order.  fp32 throughout, as the reference
 computes.
 
@@ -80,6 +80,31 @@ def _readout_gram(gk: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
     return out.t()
 
 
+def _readout_backward(gk: torch.Tensor, act: torch.Tensor, wout: torch.Tensor,
+                      has_bout: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(gact [HD, G], gwout [H, HD], gbout [H] or empty)`` for ``gk [H, G]`` (unit column stride).
+
+    ``nsq_siren_readout_bwd`` reads gk once (bf16-split matrix products, fp32 accumulation); at HD = 128, which
+    that kernel does not take, two library GEMMs (``K = H``, and ``K = G`` in fixed-order slices)."""
+    lib = _lib.get_lib()
+    H, HD = wout.shape
+    G = gk.shape[1]
+    dev = gk.device
+    need = lib.nsq_siren_readout_bwd_workspace_bytes(H, HD, G, 1)
+    if need == 0:
+        gact = torch.mm(gk.t(), wout).t()  # [HD, G] view of [G, HD]
+        gw_ext = _readout_gram(gk, act if has_bout else act[:HD])  # [H, HD (+1)]
+        return gact, gw_ext[:, :HD].contiguous(), (gw_ext[:, HD].contiguous() if has_bout else wout.new_empty(0))
+    gact = torch.empty(HD, G, dtype=torch.float32, device=dev)
+    gwout = torch.empty(H, HD, dtype=torch.float32, device=dev)
+    gbout = torch.empty(H if has_bout else 0, dtype=torch.float32, device=dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    _lib.check(lib.nsq_siren_readout_bwd(gk.data_ptr(), gk.stride(0), act.data_ptr(), act.stride(0), wout.data_ptr(),
+                                         H, HD, G, 1, gact.data_ptr(), gwout.data_ptr(), _opt(gbout), ws.data_ptr(),
+                                         ws.numel(), _lib.stream_ptr(dev)))
+    return gact, gwout, gbout
+
+
 @custom_op("nsq_hip::siren_filter", mutates_args=())
 def siren_filter_op(grid: torch.Tensor, w0: torch.Tensor, b0: Optional[torch.Tensor], wh: torch.Tensor,
                     bh: Optional[torch.Tensor], wout: torch.Tensor, bout: Optional[torch.Tensor],
@@ -108,8 +133,9 @@ def siren_filter_backward_op(gk: torch.Tensor, act: torch.Tensor, grid: torch.Te
                              wout: torch.Tensor, nh: int, has_bout: bool) -> tuple[torch.Tensor, torch.Tensor,
                                                                                    torch.Tensor, torch.Tensor,
                                                                                    torch.Tensor, torch.Tensor]:
-    """Gradients ``(gw0, gb0, gwh, gbh, gwout, gbout)`` for ``gk [H, G]`` (empty where a bias is absent):
-    the readout's two gradient GEMMs, then ``nsq_siren_mlp_bwd`` on ``gact = gk^T wout`` ``[G, HD]``."""
+    """Gradients ``(gw0, gb0, gwh, gbh, gwout, gbout)`` for ``gk [H, G]`` (empty where a bias is absent): the
+    readout's gradients in one pass over gk (``nsq_siren_readout_bwd``), then ``nsq_siren_mlp_bwd`` on
+    ``gact = wout^T gk`` ``[HD, G]``."""
     lib = _lib.get_lib()
     G, d = grid.shape
     H, HD = wout.shape
@@ -117,18 +143,16 @@ def siren_filter_backward_op(gk: torch.Tensor, act: torch.Tensor, grid: torch.Te
     dev = grid.device
     if gk.stride(1) != 1:
         gk = gk.contiguous()
-    gact = torch.mm(gk.t(), wout)  # [G, HD]: element (j, g) at j + g HD
-    gw_ext = _readout_gram(gk, act if has_bout else act[:HD])  # [H, HD (+1)]
-    gwout = gw_ext[:, :HD].contiguous()
-    gbout = gw_ext[:, HD].contiguous() if has_bout else wout.new_empty(0)
+    gact, gwout, gbout = _readout_backward(gk, act, wout, has_bout)
     gw0, gwh = torch.empty_like(w0), torch.empty_like(wh)
     gb0 = torch.empty(E if _has(b0) else 0, device=dev)
     gbh = torch.empty(nh * HD if _has(bh) else 0, device=dev)
     need = lib.nsq_siren_mlp_bwd_workspace_bytes(G, d, E, nh, HD)
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
-    _lib.check(lib.nsq_siren_mlp_bwd(gact.data_ptr(), 1, HD, grid.data_ptr(), G, d, w0.data_ptr(), _opt(b0), E,
-                                     wh.data_ptr(), _opt(bh), nh, HD, gw0.data_ptr(), _opt(gb0), gwh.data_ptr(),
-                                     _opt(gbh), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev)))
+    _lib.check(lib.nsq_siren_mlp_bwd(gact.data_ptr(), gact.stride(0), gact.stride(1), grid.data_ptr(), G, d,
+                                     w0.data_ptr(), _opt(b0), E, wh.data_ptr(), _opt(bh), nh, HD, gw0.data_ptr(),
+                                     _opt(gb0), gwh.data_ptr(), _opt(gbh), ws.data_ptr(), ws.numel(),
+                                     _lib.stream_ptr(dev)))
     return gw0, gb0, gwh, gbh, gwout, gbout
 
 

@@ -139,3 +139,49 @@ def test_readout_vector_paths(HD, H):
     k_nb = siren_filter(grid.cuda(), dev(w0), dev(b0), [w.cuda() for w in hw], [b.cuda() for b in hb], dev(wo), None)
     ref_nb = siren_mlp_torch(grid, w0, b0, hw, hb, wo, None, dtype=torch.float64).t()
     assert rel_l2(ref_nb, k_nb) < 1e-5
+
+
+# (H, HD, G, samples, bias): ragged channel counts (not a multiple of the 32-channel chunk) and point counts (not a
+# multiple of 8: the element path of the loads), several samples (per-sample filters), small G (several channel
+# slices, summed by the slice kernel) and a long G (one slice, many point blocks)
+RB_CASES = [(256, 32, 65541, 1, True), (100, 64, 1000, 3, True), (37, 16, 729, 2, False), (4096, 32, 4096, 1, True),
+            (64, 32, 33, 1, True), (300, 64, 131072, 1, False)]
+
+
+@pytest.mark.parametrize("H,HD,G,nb,bias", RB_CASES)
+def test_readout_backward_one_pass(H, HD, G, nb, bias):
+    """nsq_siren_readout_bwd against float64 products: gact = W^T gk per sample, gW = sum_s gk_s a_s^T,
+    gb = sum_s sum_g gk_s; bf16-split matrix products with fp32 accumulation stay within 2e-5 rel-L2; two calls
+    are bitwise equal."""
+    from nvsubquadratic_amd import _lib
+
+    print(f"readout bwd H={H} HD={HD} G={G} nb={nb} bias={bias}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(H + G)
+    gk = torch.randn(nb, H, G, device="cuda", generator=gen)
+    act = torch.rand(nb, HD + 1, G, device="cuda", generator=gen) * 2 - 1
+    act[:, HD] = 1.0
+    wout = torch.randn(H, HD, device="cuda", generator=gen) / HD ** 0.5
+    lib = _lib.get_lib()
+    need = lib.nsq_siren_readout_bwd_workspace_bytes(H, HD, G, nb)
+    assert need > 0
+
+    def run():
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        gact = torch.empty(nb, HD, G, device="cuda")
+        gw = torch.empty(H, HD, device="cuda")
+        gb = torch.empty(H, device="cuda") if bias else None
+        _lib.check(lib.nsq_siren_readout_bwd(gk.data_ptr(), G, act.data_ptr(), G, wout.data_ptr(), H, HD, G, nb,
+                                             gact.data_ptr(), gw.data_ptr(), None if gb is None else gb.data_ptr(),
+                                             ws.data_ptr(), ws.numel(), _lib.stream_ptr(gk.device)))
+        return gact, gw, gb
+
+    gact, gw, gb = run()
+    g64, a64, w64 = gk.double(), act[:, :HD].double(), wout.double()
+    assert rel_l2(torch.matmul(w64.t(), g64), gact) < 2e-5
+    assert rel_l2(torch.einsum("shg,sjg->hj", g64, a64), gw) < 2e-5
+    if bias:
+        assert rel_l2(g64.sum(dim=(0, 2)), gb) < 2e-5
+    again = run()
+    assert torch.equal(again[0], gact) and torch.equal(again[1], gw)
+    if bias:
+        assert torch.equal(again[2], gb)
