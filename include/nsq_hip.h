@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 11
+#define NSQ_ABI_VERSION 12
 
 enum {
   NSQ_OK = 0,
@@ -405,6 +405,36 @@ int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_str
                       int d, const float* w0, const float* b0, int E, const float* wh, const float* bh, int nh, int HD,
                       float* gw0, float* gb0, float* gwh, float* gbh, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/* FiLM-conditioned generator (ABI 12): kernels_nd.py:1165-1187 with the
+ * KernelFiLMGenerator output of modules/film.py:75 (its MLP runs on the
+ * caller's side; these take its (gamma, beta) pairs).  film [nb][nfilm][2][HD]
+ * fp32: for sample s and FiLM slot f, gamma = film[s][f][0], beta =
+ * film[s][f][1]; slot f modulates h = gamma * sin(z) + beta at the output of
+ * hidden layer f + 1 - film_first, and with film_first (film_after_pos_embed,
+ * needs E == HD) slot 0 modulates the positional embedding; nfilm = nh +
+ * film_first.  The filter becomes per sample:
+ *   nsq_siren_mlp_film_fwd      act [nb][HD + 1][lda] (sample s's rows at s (HD + 1) lda);
+ *   nsq_siren_film_readout_fwd  k [nb][H][G] from that act (also the plain readout's batched form);
+ *   nsq_siren_mlp_film_bwd      gact element (s, j, g) at s gact_stride_s + j gact_stride_j + g gact_stride_g
+ *                               (nsq_siren_readout_bwd's [nb][HD][G] output reads in place); the weight and bias
+ *                               gradients summed over the samples, gfilm [nb][nfilm][2][HD] per sample.
+ * film = null with nb = 1 and film_first = 0 is the plain generator (the entry
+ * points above are exactly that).  Deterministic, fixed-order reductions. */
+int nsq_siren_mlp_film_fwd(const float* grid, int64_t G, int d, const float* w0, const float* b0, int E,
+                           const float* wh, const float* bh, int nh, int HD, const float* film, int64_t nb,
+                           int film_first, float* act, int64_t lda, void* stream);
+
+int nsq_siren_film_readout_fwd(const float* wout, const float* bout, int64_t H, int HD, const float* act,
+                               int64_t lda, int64_t G, int64_t nb, float* k, void* stream);
+
+size_t nsq_siren_mlp_film_bwd_workspace_bytes(int64_t G, int d, int E, int nh, int HD, int64_t nb, int film_first);
+
+int nsq_siren_mlp_film_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_stride_g, int64_t gact_stride_s,
+                           const float* grid, int64_t G, int d, const float* w0, const float* b0, int E,
+                           const float* wh, const float* bh, int nh, int HD, const float* film, int64_t nb,
+                           int film_first, float* gw0, float* gb0, float* gwh, float* gbh, float* gfilm,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Channels-last (BLH) layout changes (ABI 9).

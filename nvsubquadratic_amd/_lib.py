@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 11
+ABI_VERSION = 12
 NSQ_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/nsq_hip.h: the fixed scratch of nsq_causal_conv1d_bwd_noalloc
 
 
@@ -171,6 +171,20 @@ _SIGNATURES = {
     "nsq_siren_readout_bwd": (
         _c_int, [_c_void_p, _c_i64, _c_void_p, _c_i64, _c_void_p, _c_i64, _c_int, _c_i64, _c_i64, _c_void_p,
                  _c_void_p, _c_void_p, _c_void_p, _c_size, _c_void_p]),
+    "nsq_siren_mlp_film_fwd": (
+        _c_int,
+        [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p,
+         _c_i64, _c_int, _c_void_p, _c_i64, _c_void_p],
+    ),
+    "nsq_siren_film_readout_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p, _c_i64, _c_i64, _c_i64, _c_void_p, _c_void_p]),
+    "nsq_siren_mlp_film_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int]),
+    "nsq_siren_mlp_film_bwd": (
+        _c_int,
+        [_c_void_p, _c_i64, _c_i64, _c_i64, _c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p,
+         _c_void_p, _c_int, _c_int, _c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_size, _c_void_p],
+    ),
     "nsq_siren_mlp_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "nsq_siren_mlp_bwd": (
         _c_int,

@@ -61,12 +61,25 @@ struct Tile {
 };
 
 // Layer geometry: layer i (i = 1..nh) maps IN -> HD, IN = E for i = 1.
+// FiLM (kernels_nd.py:1165-1187, film.py:75): per sample s, film[s][f] holds
+// (gamma[HD], beta[HD]) for FiLM slot f; slot f modulates the output of layer
+// f + 1 - film_first (layer 0 = the positional embedding, modulated only when
+// film_first, which needs E == HD): h = gamma * sin(z) + beta.  film == null:
+// no modulation.
 struct SirenNet {
   const float* w0;  // [E][d]
   const float* b0;  // [E] or null
   const float* wh;  // packed W_1 [HD][E], W_2.. [HD][HD]
   const float* bh;  // packed [nh][HD] or null
   int d, nh;
+  const float* film = nullptr;  // [nb][nfilm][2][HD]
+  int film_first = 0;
+  __device__ __forceinline__ int nfilm() const { return nh + film_first; }
+  // (gamma, beta) of layer L (0 = embedding) for sample s, or nulls
+  __device__ __forceinline__ const float* film_of(int s, int L, int HD) const {
+    const int f = L - 1 + film_first;
+    return (film && f >= 0) ? film + (int64_t(s) * nfilm() + f) * 2 * HD : nullptr;
+  }
 };
 
 __device__ __forceinline__ const float* layer_w(const SirenNet& n, int i, int E, int HD) {
@@ -93,7 +106,7 @@ __device__ __forceinline__ float embed_pre(const SirenNet& n, int e, const float
 // pre-activation into z0 if given): lane l, point l % 16, features l / 16 + 4t.
 template <int E>
 __device__ __forceinline__ void pos_embed(const SirenNet& n, const float* __restrict__ grid, int64_t G, int64_t g0,
-                                          float* a0, float* z0) {
+                                          float* a0, float* z0, const float* fm = nullptr) {
   const int l = int(threadIdx.x) & 63, p = l & 15;
   const int64_t g = g0 + p;
   float x[3];
@@ -102,7 +115,8 @@ __device__ __forceinline__ void pos_embed(const SirenNet& n, const float* __rest
   for (int t = 0; t < E / 4; ++t) {
     const int e = (l >> 4) + 4 * t;
     const float z = embed_pre(n, e, x);
-    a0[p * Tile<E>::S + e] = sinf(z);
+    const float sv = sinf(z);
+    a0[p * Tile<E>::S + e] = fm ? __builtin_fmaf(fm[e], sv, fm[E + e]) : sv;
     if (z0) z0[p * Tile<E>::S + e] = z;
   }
 }
@@ -112,7 +126,7 @@ __device__ __forceinline__ void pos_embed(const SirenNet& n, const float* __rest
 // SIN / SOUT: row strides of the input and output tiles.
 template <int IN, int HD, int SIN = Tile<IN>::S, int SOUT = Tile<HD>::S>
 __device__ __forceinline__ void hidden_layer(const float* __restrict__ w, const float* __restrict__ b, const float* in,
-                                             float* out, float* z) {
+                                             float* out, float* z, const float* fm = nullptr) {
   constexpr int KB = IN / 4;
   const int l = int(threadIdx.x) & 63, s = l >> 4, p = l & 15;
   float bv[KB];
@@ -129,7 +143,8 @@ __device__ __forceinline__ void hidden_layer(const float* __restrict__ w, const 
     for (int r = 0; r < 4; ++r) {
       const int o = o0 + 4 * s + r;
       const float zz = acc[r] + (b ? b[o] : 0.f);
-      out[p * SOUT + o] = sinf(zz);
+      const float sv = sinf(zz);
+      out[p * SOUT + o] = fm ? __builtin_fmaf(fm[o], sv, fm[HD + o]) : sv;  // FiLM: gamma sin + beta
       if (z) z[p * SOUT + o] = zz;
     }
   }
@@ -139,15 +154,16 @@ __device__ __forceinline__ void hidden_layer(const float* __restrict__ w, const 
 // only two tiles (ping-pong); the backward passes per-layer tiles (act[i],
 // zt[i]) so every layer's activation and pre-activation survive.
 template <int E, int HD>
-__device__ __forceinline__ const float* run_layers(const SirenNet& n, float* const* act, float* const* zt) {
+__device__ __forceinline__ const float* run_layers(const SirenNet& n, float* const* act, float* const* zt, int smp) {
   for (int i = 1; i <= n.nh; ++i) {
     const float* w = layer_w(n, i, E, HD);
     const float* b = n.bh ? n.bh + (i - 1) * HD : nullptr;
+    const float* fm = n.film_of(smp, i, HD);
     wave_lds_order();
     if (i == 1)
-      hidden_layer<E, HD>(w, b, act[0], act[1], zt ? zt[1] : nullptr);
+      hidden_layer<E, HD>(w, b, act[0], act[1], zt ? zt[1] : nullptr, fm);
     else
-      hidden_layer<HD, HD>(w, b, act[i - 1], act[i], zt ? zt[i] : nullptr);
+      hidden_layer<HD, HD>(w, b, act[i - 1], act[i], zt ? zt[i] : nullptr, fm);
   }
   wave_lds_order();
   return act[n.nh];
@@ -170,10 +186,12 @@ __global__ __launch_bounds__(kSirenThreads) void siren_mlp_fwd_kernel(const floa
   float* t1 = base + Tile<E>::WORDS;
   float* t2 = t1 + Tile<HD>::WORDS;
   const int64_t g0 = (int64_t(blockIdx.x) * kSirenWaves + wv) * 16;
-  pos_embed<E>(n, grid, G, g0, t0, nullptr);
+  const int smp = int(blockIdx.y);  // sample (FiLM); act rows of sample smp follow those of smp - 1
+  act += int64_t(smp) * (HD + 1) * lda;
+  pos_embed<E>(n, grid, G, g0, t0, nullptr, n.film_of(smp, 0, HD));
   // ping-pong: a_i in t1 for odd i, t2 for even i >= 2
   float* tiles[9] = {t0, t1, t2, t1, t2, t1, t2, t1, t2};
-  const float* last = run_layers<E, HD>(n, tiles, nullptr);
+  const float* last = run_layers<E, HD>(n, tiles, nullptr, smp);
   const int64_t g = g0 + p;
   if (g < G) {
     for (int j = s; j < HD; j += 4) act[int64_t(j) * lda + g] = last[p * Tile<HD>::S + j];
@@ -181,10 +199,17 @@ __global__ __launch_bounds__(kSirenThreads) void siren_mlp_fwd_kernel(const floa
   }
 }
 
+// Backward pass 1.  grid = (ceil(G / (16 waves)), nb): sample smp = blockIdx.y.
+// Rows are written for all samples side by side, column smp * Gp + g (GT = nb
+// Gp columns; points g >= G written as zeros), so the Gram reductions over the
+// GT columns sum every weight gradient over the samples.  FiLM slot f's
+// gradients are row sums over one sample's columns of fdh = dL/dh (beta) and
+// fds = dL/dh * sin(z) (gamma), rows f * HD + o.
 template <int E, int HD>
 __global__ __launch_bounds__(kSirenThreads) void siren_bwd_delta_kernel(
-    const float* __restrict__ gact, int64_t sj, int64_t sg, const float* __restrict__ grid, int64_t G, int64_t Gp,
-    SirenNet n, float* __restrict__ act, float* __restrict__ del, float* __restrict__ gridT, int nwaves_wg) {
+    const float* __restrict__ gact, int64_t sj, int64_t sg, int64_t ss, const float* __restrict__ grid, int64_t G,
+    int64_t Gp, SirenNet n, float* __restrict__ act, float* __restrict__ del, float* __restrict__ gridT,
+    float* __restrict__ fdh, float* __restrict__ fds, int nwaves_wg) {
   extern __shared__ float lds[];
   constexpr int D = E > HD ? E : HD;
   constexpr int TS = Tile<D>::S, TW = Tile<D>::WORDS;
@@ -202,42 +227,65 @@ __global__ __launch_bounds__(kSirenThreads) void siren_bwd_delta_kernel(
   const int64_t g0 = (int64_t(blockIdx.x) * nwaves_wg + wv) * 16;
   const int64_t g = g0 + p;
   const bool gok = g < G;
+  const int smp = int(blockIdx.y);
+  const int64_t GT = int64_t(gridDim.y) * Gp;
+  const int64_t col = int64_t(smp) * Gp + g;  // this point's column in the rows of all samples
+  const bool colok = g < Gp;
 
-  // dA[p][j] = gact[j sj + (g0 + p) sg], the gradient of the last layer's output (the readout's W_out^T gk)
-  for (int j = s; j < HD; j += 4) dA[p * TS + j] = gok ? gact[int64_t(j) * sj + g * sg] : 0.f;
+  // dA[p][j] = gact[smp ss + j sj + (g0 + p) sg], the gradient of the last layer's output (W_out^T gk)
+  for (int j = s; j < HD; j += 4) dA[p * TS + j] = gok ? gact[smp * ss + int64_t(j) * sj + g * sg] : 0.f;
 
   // forward recompute with pre-activations; every tile has the D-wide stride TS
   {
     float x[3];
     load_coords(grid, G, n.d, g, x);
     const float xs = s == 0 ? x[0] : (s == 1 ? x[1] : x[2]);
-    if (s < n.d && gok) gridT[int64_t(s) * Gp + g] = xs;
+    if (s < n.d && colok) gridT[int64_t(s) * GT + col] = gok ? xs : 0.f;
+    const float* fm0 = n.film_of(smp, 0, HD);
 #pragma unroll
     for (int t = 0; t < E / 4; ++t) {
       const int e = s + 4 * t;
       const float z = embed_pre(n, e, x);
-      at[0][p * TS + e] = sinf(z);
+      const float sv = sinf(z);
+      at[0][p * TS + e] = fm0 ? __builtin_fmaf(fm0[e], sv, fm0[E + e]) : sv;
       zt[0][p * TS + e] = z;
     }
     for (int i = 1; i <= n.nh; ++i) {
       const float* w = layer_w(n, i, E, HD);
       const float* b = n.bh ? n.bh + (i - 1) * HD : nullptr;
+      const float* fm = n.film_of(smp, i, HD);
       wave_lds_order();
       if (i == 1)
-        hidden_layer<E, HD, TS, TS>(w, b, at[0], at[1], zt[1]);
+        hidden_layer<E, HD, TS, TS>(w, b, at[0], at[1], zt[1], fm);
       else
-        hidden_layer<HD, HD, TS, TS>(w, b, at[i - 1], at[i], zt[i]);
+        hidden_layer<HD, HD, TS, TS>(w, b, at[i - 1], at[i], zt[i], fm);
     }
     wave_lds_order();
   }
 
-  // delta_nh = dA * cos(z_nh); for i = nh..1: delta_{i-1}[p][j] = (sum_o delta_i[p][o] W_i[o][j]) cos(z_{i-1}[p][j])
+  // Through layer L's output h = gamma sin(z) + beta (FiLM) or sin(z): from dh, delta = dh gamma cos(z); FiLM rows
+  // fdh = dh, fds = dh sin(z) at row f * HD + o, column col.
+  auto through = [&](int L, int pp, int j, float dh, float z) -> float {
+    const float* fm = n.film_of(smp, L, HD);
+    if (fm) {
+      const int64_t row = int64_t(L - 1 + n.film_first) * HD + j;
+      const int64_t c = int64_t(smp) * Gp + g0 + pp;
+      if (g0 + pp < Gp) {
+        const bool ok = g0 + pp < G;
+        fdh[row * GT + c] = ok ? dh : 0.f;
+        fds[row * GT + c] = ok ? dh * sinf(z) : 0.f;
+      }
+      dh *= fm[j];
+    }
+    return dh * cosf(z);
+  };
+  // delta_nh = through(dA); for i = nh..1: delta_{i-1}[p][j] = through(sum_o delta_i[p][o] W_i[o][j])
   // (D[m = j][n = p] = sum_o W_i^T[j][o] delta_i^T[o][p]: A[m = j][k = o] = W_i[o][j], B[k = o][n = p]).
   float* cur = dA;
   float* nxt = dB;
   for (int e = l; e < 16 * HD; e += 64) {
     const int pp = e / HD, j = e - pp * HD;
-    cur[pp * TS + j] *= cosf(zt[n.nh][pp * TS + j]);
+    cur[pp * TS + j] = through(n.nh, pp, j, cur[pp * TS + j], zt[n.nh][pp * TS + j]);
   }
   wave_lds_order();
   for (int i = n.nh; i >= 0; --i) {
@@ -245,9 +293,9 @@ __global__ __launch_bounds__(kSirenThreads) void siren_bwd_delta_kernel(
     // write a_i^T and delta_i^T rows for these 16 points
     const int64_t roff = i == 0 ? 0 : E + int64_t(i - 1) * HD;
     for (int e = s; e < rows; e += 4) {
-      if (gok) {
-        act[(roff + e) * Gp + g] = at[i][p * TS + e];
-        del[(roff + e) * Gp + g] = cur[p * TS + e];
+      if (colok) {
+        act[(roff + e) * GT + col] = gok ? at[i][p * TS + e] : 0.f;
+        del[(roff + e) * GT + col] = gok ? cur[p * TS + e] : 0.f;
       }
     }
     if (i == 0) break;
@@ -266,7 +314,7 @@ __global__ __launch_bounds__(kSirenThreads) void siren_bwd_delta_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = j0 + 4 * s + r;
-        nxt[p * TS + j] = acc[r] * cosf(zt[i - 1][p * TS + j]);
+        nxt[p * TS + j] = through(i - 1, p, j, acc[r], zt[i - 1][p * TS + j]);
       }
     }
     wave_lds_order();
@@ -414,9 +462,10 @@ bool siren_dispatch(int E, int HD, A&&... a) {
 
 template <int E, int HD>
 struct SirenFwd {
-  static void run(const float* grid, int64_t G, const SirenNet& n, float* act, int64_t lda, hipStream_t st) {
+  static void run(const float* grid, int64_t G, const SirenNet& n, float* act, int64_t lda, int64_t nb,
+                  hipStream_t st) {
     const size_t lds = size_t(kSirenWaves) * (Tile<E>::WORDS + 2 * Tile<HD>::WORDS) * sizeof(float);
-    const dim3 grd(unsigned(ceil_div(G, 16 * kSirenWaves)));
+    const dim3 grd(unsigned(ceil_div(G, 16 * kSirenWaves)), unsigned(nb));
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&siren_mlp_fwd_kernel<E, HD>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     hipLaunchKernelGGL((siren_mlp_fwd_kernel<E, HD>), grd, dim3(kSirenThreads), lds, st, grid, G, n, act, lda);
@@ -453,6 +502,8 @@ __global__ __launch_bounds__(256) void siren_readout_fwd_kernel(const float* __r
   const int64_t g = (int64_t(blockIdx.x) * 256 + threadIdx.x) * V;
   const bool gok = g < G;  // VEC: the V points are whole (G % V == 0)
   const int64_t h0 = int64_t(blockIdx.y) * ROWS;
+  act += int64_t(blockIdx.z) * (HD + 1) * lda;  // sample blockIdx.z (per-sample FiLM filters)
+  k += int64_t(blockIdx.z) * H * G;
   const int nrows = H - h0 < ROWS ? int(H - h0) : ROWS;
   for (int i = threadIdx.x; i < ROWS * HD; i += 256) ws[i] = i < nrows * HD ? wout[h0 * HD + i] : 0.f;
   for (int i = threadIdx.x; i < ROWS; i += 256) bs[i] = (bout && i < nrows) ? bout[h0 + i] : 0.f;
@@ -503,12 +554,12 @@ __global__ __launch_bounds__(256) void siren_readout_fwd_kernel(const float* __r
 
 template <int HD>
 static void launch_readout(const float* wout, const float* bout, const float* act, int64_t lda, int64_t G, int64_t H,
-                           float* k, hipStream_t st) {
+                           float* k, int64_t nb, hipStream_t st) {
   using C = ReadoutCfg<HD>;
   const bool vec = G % C::V == 0 && lda % C::V == 0 && (reinterpret_cast<uintptr_t>(k) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(act) & 15) == 0;
   const int v = vec ? C::V : 1;
-  const dim3 grd(unsigned(ceil_div(G, int64_t(256) * v)), unsigned(ceil_div(H, int64_t(C::ROWS))));
+  const dim3 grd(unsigned(ceil_div(G, int64_t(256) * v)), unsigned(ceil_div(H, int64_t(C::ROWS))), unsigned(nb));
   if (vec)
     hipLaunchKernelGGL((siren_readout_fwd_kernel<HD, true>), grd, dim3(256), 0, st, wout, bout, act, lda, G, H, k);
   else
@@ -858,19 +909,42 @@ inline int delta_lds_per_wave(int E, int HD, int nh) {
 
 template <int E, int HD>
 struct SirenDelta {
-  static void run(const float* gact, int64_t sj, int64_t sg, const float* grid, int64_t G, int64_t Gp,
-                  const SirenNet& n, float* act, float* del, float* gridT, hipStream_t st) {
+  static void run(const float* gact, int64_t sj, int64_t sg, int64_t ss, const float* grid, int64_t G, int64_t Gp,
+                  int64_t nb, const SirenNet& n, float* act, float* del, float* gridT, float* fdh, float* fds,
+                  hipStream_t st) {
     const int per = delta_lds_per_wave(E, HD, n.nh);
     int waves = kSirenMaxLds / per;
     waves = waves > kSirenWaves ? kSirenWaves : waves;
-    const dim3 grd(unsigned(ceil_div(G, 16 * waves)));
+    const dim3 grd(unsigned(ceil_div(G, 16 * waves)), unsigned(nb));
     const size_t lds = size_t(per) * waves;
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&siren_bwd_delta_kernel<E, HD>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-    hipLaunchKernelGGL((siren_bwd_delta_kernel<E, HD>), grd, dim3(64 * waves), lds, st, gact, sj, sg, grid, G, Gp, n,
-                       act, del, gridT, waves);
+    hipLaunchKernelGGL((siren_bwd_delta_kernel<E, HD>), grd, dim3(64 * waves), lds, st, gact, sj, sg, ss, grid, G,
+                       Gp, n, act, del, gridT, fdh, fds, waves);
   }
 };
+
+// FiLM gradients gfilm[s][f][c][o] (c = 0: gamma, 1: beta) = sum_{g < G} of row f * HD + o of fds (gamma) or fdh
+// (beta) over sample s's columns [s Gp, s Gp + G): one wave per output, lanes over the points, a fixed butterfly
+// adds the lanes (deterministic).
+__global__ __launch_bounds__(256) void siren_film_grad_kernel(const float* __restrict__ fdh,
+                                                              const float* __restrict__ fds, int64_t GT, int64_t Gp,
+                                                              int64_t G, int64_t nb, int nfilm, int HD,
+                                                              float* __restrict__ gfilm) {
+  const int64_t e = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = int(threadIdx.x) & 63;
+  if (e >= nb * nfilm * 2 * HD) return;  // a whole wave leaves together
+  const int o = int(e % HD);
+  const int c = int((e / HD) % 2);
+  const int f = int((e / (2 * HD)) % nfilm);
+  const int64_t smp = e / (int64_t(2) * HD * nfilm);
+  const float* row = (c == 0 ? fds : fdh) + (int64_t(f) * HD + o) * GT + smp * Gp;
+  float acc = 0.f;
+  for (int64_t g = lane; g < G; g += 64) acc += row[g];
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) acc += __shfl_xor(acc, w);
+  if (lane == 0) gfilm[e] = acc;
+}
 
 // Points per Gram workgroup: enough chunks that M/16 x chunks reaches ~2048
 // workgroups (8 per CU), at least 64 points (16 per wave) and a multiple of 64.
@@ -916,30 +990,36 @@ void gram(const float* X, int64_t ldx, const float* Y, int64_t ldy, int NY, int6
                      gram_chunks(G, M), M, NP, NY, out, rpart, rout);
 }
 
-// Workspace layout (floats): act [E + nh HD][Gp], del [same], gridT [d][Gp],
-// part [chunks][max(E, HD)][max NT*16], rpart [chunks][max(E, HD)].
+// Workspace layout (floats): act [E + nh HD][GT], del [same], gridT [d][GT],
+// part [chunks][max(E, HD)][max NT*16], rpart [chunks][max(E, HD)], and the
+// FiLM rows fdh, fds [nfilm HD][GT].  GT = nb Gp: every row holds the nb
+// samples side by side (one sample: Gp columns, its Gram launches over G).
 struct SirenWs {
-  int64_t Gp, rows;
-  size_t act, del, gridT, part, rpart, total;  // float offsets / count
+  int64_t Gp, GT, GG, rows;
+  size_t act, del, gridT, part, rpart, fdh, fds, total;  // float offsets / count
 };
 
-SirenWs siren_ws(int64_t G, int d, int E, int nh, int HD) {
+SirenWs siren_ws(int64_t G, int d, int E, int nh, int HD, int64_t nb = 1, int nfilm = 0) {
   SirenWs w;
   w.Gp = (G + 15) / 16 * 16;
+  w.GT = nb * w.Gp;
+  w.GG = nb == 1 ? G : w.GT;  // points of the Gram launches (zeros at each sample's padding)
   w.rows = E + int64_t(nh) * HD;
   // partial sums of the largest Gram launch: hidden (M = HD, N = E or HD), embedding (M = E, N = d)
-  auto psz = [&](int64_t M, int NY) { return size_t(gram_chunks(G, int(M))) * M * 16 * gram_nt(NY); };
-  auto rsz = [&](int64_t M) { return size_t(gram_chunks(G, int(M))) * M; };
+  auto psz = [&](int64_t M, int NY) { return size_t(gram_chunks(w.GG, int(M))) * M * 16 * gram_nt(NY); };
+  auto rsz = [&](int64_t M) { return size_t(gram_chunks(w.GG, int(M))) * M; };
   size_t pmax = psz(HD, E > HD ? E : HD);
   pmax = psz(E, d) > pmax ? psz(E, d) : pmax;
   size_t rmax = rsz(HD) > rsz(E) ? rsz(HD) : rsz(E);
   auto al = [](size_t v) { return (v + 63) / 64 * 64; };  // 256-byte sub-buffers
   w.act = 0;
-  w.del = al(w.act + size_t(w.rows) * w.Gp);
-  w.gridT = al(w.del + size_t(w.rows) * w.Gp);
-  w.part = al(w.gridT + size_t(d) * w.Gp);
+  w.del = al(w.act + size_t(w.rows) * w.GT);
+  w.gridT = al(w.del + size_t(w.rows) * w.GT);
+  w.part = al(w.gridT + size_t(d) * w.GT);
   w.rpart = al(w.part + pmax);
-  w.total = al(w.rpart + rmax);
+  w.fdh = al(w.rpart + rmax);
+  w.fds = al(w.fdh + size_t(nfilm) * HD * w.GT);
+  w.total = al(w.fds + size_t(nfilm) * HD * w.GT);
   return w;
 }
 
@@ -960,23 +1040,36 @@ int siren_validate(const float* grid, int64_t G, int d, const float* w0, int E, 
 
 extern "C" {
 
-int nsq_siren_mlp_fwd(const float* grid, int64_t G, int d, const float* w0, const float* b0, int E, const float* wh,
-                      const float* bh, int nh, int HD, float* act, int64_t lda, void* stream) {
+int nsq_siren_mlp_film_fwd(const float* grid, int64_t G, int d, const float* w0, const float* b0, int E,
+                           const float* wh, const float* bh, int nh, int HD, const float* film, int64_t nb,
+                           int film_first, float* act, int64_t lda, void* stream) {
   using namespace nsq;
   clear_error();
   int rc = siren_validate(grid, G, d, w0, E, wh, nh, HD);
   if (rc) return rc;
   NSQ_CHECK_ARG(act && lda >= G, "siren_mlp_fwd: null output or row stride %lld < G", (long long)lda);
-  const SirenNet n{w0, b0, wh, bh, d, nh};
-  siren_dispatch<SirenFwd>(E, HD, grid, G, n, act, lda, (hipStream_t)stream);
+  NSQ_CHECK_ARG(nb >= 1 && nb <= 65535, "siren_mlp_fwd: %lld samples out of range", (long long)nb);
+  NSQ_CHECK_ARG(film || (nb == 1 && !film_first), "siren_mlp_fwd: several samples or film_first need FiLM parameters");
+  NSQ_CHECK_ARG(!film_first || E == HD, "siren_mlp_fwd: FiLM after the embedding needs embedding_dim %d == "
+                "mlp_hidden_dim %d", E, HD);
+  SirenNet n{w0, b0, wh, bh, d, nh};
+  n.film = film;
+  n.film_first = film_first ? 1 : 0;
+  siren_dispatch<SirenFwd>(E, HD, grid, G, n, act, lda, nb, (hipStream_t)stream);
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
 }
 
-int nsq_siren_readout_fwd(const float* wout, const float* bout, int64_t H, int HD, const float* act, int64_t lda,
-                          int64_t G, float* k, void* stream) {
+int nsq_siren_mlp_fwd(const float* grid, int64_t G, int d, const float* w0, const float* b0, int E, const float* wh,
+                      const float* bh, int nh, int HD, float* act, int64_t lda, void* stream) {
+  return nsq_siren_mlp_film_fwd(grid, G, d, w0, b0, E, wh, bh, nh, HD, nullptr, 1, 0, act, lda, stream);
+}
+
+int nsq_siren_film_readout_fwd(const float* wout, const float* bout, int64_t H, int HD, const float* act,
+                               int64_t lda, int64_t G, int64_t nb, float* k, void* stream) {
   using namespace nsq;
   clear_error();
+  NSQ_CHECK_ARG(nb >= 1 && nb <= 65535, "siren_readout_fwd: %lld samples out of range", (long long)nb);
   NSQ_CHECK_ARG(wout && act && k, "siren_readout_fwd: null pointer argument");
   NSQ_CHECK_ARG(G >= 1 && G <= (int64_t(1) << 30) && lda >= G, "siren_readout_fwd: G=%lld, lda=%lld", (long long)G,
                 (long long)lda);
@@ -984,16 +1077,21 @@ int nsq_siren_readout_fwd(const float* wout, const float* bout, int64_t H, int H
   NSQ_CHECK_ARG(ceil_div(H, int64_t(64)) <= 65535, "siren_readout_fwd: H=%lld too large", (long long)H);
   hipStream_t st = (hipStream_t)stream;
   switch (HD) {
-    case 16: launch_readout<16>(wout, bout, act, lda, G, H, k, st); break;
-    case 32: launch_readout<32>(wout, bout, act, lda, G, H, k, st); break;
-    case 64: launch_readout<64>(wout, bout, act, lda, G, H, k, st); break;
-    case 128: launch_readout<128>(wout, bout, act, lda, G, H, k, st); break;
+    case 16: launch_readout<16>(wout, bout, act, lda, G, H, k, nb, st); break;
+    case 32: launch_readout<32>(wout, bout, act, lda, G, H, k, nb, st); break;
+    case 64: launch_readout<64>(wout, bout, act, lda, G, H, k, nb, st); break;
+    case 128: launch_readout<128>(wout, bout, act, lda, G, H, k, nb, st); break;
     default:
       set_error("siren_readout_fwd: mlp_hidden_dim %d must be 16, 32, 64 or 128", HD);
       return NSQ_ERR_UNSUPPORTED;
   }
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
+}
+
+int nsq_siren_readout_fwd(const float* wout, const float* bout, int64_t H, int HD, const float* act, int64_t lda,
+                          int64_t G, float* k, void* stream) {
+  return nsq_siren_film_readout_fwd(wout, bout, H, HD, act, lda, G, 1, k, stream);
 }
 
 size_t nsq_siren_readout_bwd_workspace_bytes(int64_t H, int HD, int64_t G, int64_t nb) {
@@ -1032,24 +1130,37 @@ int nsq_siren_readout_bwd(const float* gk, int64_t ldk, const float* act, int64_
   return NSQ_OK;
 }
 
+size_t nsq_siren_mlp_film_bwd_workspace_bytes(int64_t G, int d, int E, int nh, int HD, int64_t nb, int film_first) {
+  if (G < 1 || d < 1 || d > 3 || nh < 1 || nh > 8 || !nsq::siren_dims_ok(E, HD) || nb < 1 || nb > 65535) return 0;
+  if (film_first && E != HD) return 0;
+  return nsq::siren_ws(G, d, E, nh, HD, nb, nh + (film_first ? 1 : 0)).total * sizeof(float);
+}
+
 size_t nsq_siren_mlp_bwd_workspace_bytes(int64_t G, int d, int E, int nh, int HD) {
   if (G < 1 || d < 1 || d > 3 || nh < 1 || nh > 8 || !nsq::siren_dims_ok(E, HD)) return 0;
   return nsq::siren_ws(G, d, E, nh, HD).total * sizeof(float);
 }
 
-int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_stride_g, const float* grid, int64_t G,
-                      int d, const float* w0, const float* b0, int E, const float* wh, const float* bh, int nh, int HD,
-                      float* gw0, float* gb0, float* gwh, float* gbh, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+int nsq_siren_mlp_film_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_stride_g, int64_t gact_stride_s,
+                           const float* grid, int64_t G, int d, const float* w0, const float* b0, int E,
+                           const float* wh, const float* bh, int nh, int HD, const float* film, int64_t nb,
+                           int film_first, float* gw0, float* gb0, float* gwh, float* gbh, float* gfilm,
+                           void* workspace, size_t workspace_bytes, void* stream) {
   using namespace nsq;
   clear_error();
   int rc = siren_validate(grid, G, d, w0, E, wh, nh, HD);
   if (rc) return rc;
   NSQ_CHECK_ARG(gact && gw0 && gwh, "siren_mlp_bwd: null gradient pointer");
-  NSQ_CHECK_ARG(gact_stride_j >= 0 && gact_stride_g >= 0, "siren_mlp_bwd: negative gact stride");
+  NSQ_CHECK_ARG(gact_stride_j >= 0 && gact_stride_g >= 0 && gact_stride_s >= 0, "siren_mlp_bwd: negative gact stride");
   NSQ_CHECK_ARG(!b0 || gb0, "siren_mlp_bwd: gb0 required with b0");
   NSQ_CHECK_ARG(!bh || gbh, "siren_mlp_bwd: gbh required with bh");
-  const SirenWs w = siren_ws(G, d, E, nh, HD);
+  NSQ_CHECK_ARG(nb >= 1 && nb <= 65535, "siren_mlp_bwd: %lld samples out of range", (long long)nb);
+  NSQ_CHECK_ARG(film || (nb == 1 && !film_first), "siren_mlp_bwd: several samples or film_first need FiLM parameters");
+  NSQ_CHECK_ARG(!film || gfilm, "siren_mlp_bwd: gfilm required with FiLM parameters");
+  NSQ_CHECK_ARG(!film_first || E == HD, "siren_mlp_bwd: FiLM after the embedding needs embedding_dim %d == "
+                "mlp_hidden_dim %d", E, HD);
+  const int nfilm = film ? nh + (film_first ? 1 : 0) : 0;
+  const SirenWs w = siren_ws(G, d, E, nh, HD, nb, nfilm);
   NSQ_CHECK_ARG(workspace && workspace_bytes >= w.total * sizeof(float),
                 "siren_mlp_bwd: workspace of %zu bytes required, got %zu", w.total * sizeof(float), workspace_bytes);
   NSQ_CHECK_ARG(delta_lds_per_wave(E, HD, nh) <= kSirenMaxLds, "siren_mlp_bwd: %d hidden layers of %d too large", nh,
@@ -1061,20 +1172,36 @@ int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_str
   float* gridT = ws + w.gridT;
   float* part = ws + w.part;
   float* rpart = ws + w.rpart;
-  const SirenNet n{w0, b0, wh, bh, d, nh};
-  siren_dispatch<SirenDelta>(E, HD, gact, gact_stride_j, gact_stride_g, grid, G, w.Gp, n, act, del, gridT, st);
-  // hidden layers i = nh..1: X = delta_i^T [HD], Y = a_{i-1}^T [IN]
+  SirenNet n{w0, b0, wh, bh, d, nh};
+  n.film = film;
+  n.film_first = film_first ? 1 : 0;
+  siren_dispatch<SirenDelta>(E, HD, gact, gact_stride_j, gact_stride_g, gact_stride_s, grid, G, w.Gp, nb, n, act, del,
+                             gridT, ws + w.fdh, ws + w.fds, st);
+  // hidden layers i = nh..1: X = delta_i^T [HD], Y = a_{i-1}^T [IN] (summed over the samples' columns)
   for (int i = nh; i >= 1; --i) {
     const int IN = i == 1 ? E : HD;
     const int64_t xo = E + int64_t(i - 1) * HD, yo = i == 1 ? 0 : E + int64_t(i - 2) * HD;
     float* gw = gwh + (i == 1 ? 0 : int64_t(HD) * E + int64_t(i - 2) * HD * HD);
-    gram(del + xo * w.Gp, w.Gp, act + yo * w.Gp, w.Gp, IN, G, HD, gw, gbh ? gbh + (i - 1) * HD : nullptr, part,
+    gram(del + xo * w.GT, w.GT, act + yo * w.GT, w.GT, IN, w.GG, HD, gw, gbh ? gbh + (i - 1) * HD : nullptr, part,
          rpart, st);
   }
   // positional embedding: X = delta_0^T [E], Y = grid^T [d] (rows >= d read as zero)
-  gram(del, w.Gp, gridT, w.Gp, d, G, E, gw0, gb0, part, rpart, st);
+  gram(del, w.GT, gridT, w.GT, d, w.GG, E, gw0, gb0, part, rpart, st);
+  if (film) {
+    const int64_t nout = nb * nfilm * 2 * HD;
+    hipLaunchKernelGGL(siren_film_grad_kernel, dim3(unsigned(ceil_div(nout, 4))), dim3(256), 0, st, ws + w.fdh,
+                       ws + w.fds, w.GT, w.Gp, G, nb, nfilm, HD, gfilm);
+  }
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
+}
+
+int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_stride_g, const float* grid, int64_t G,
+                      int d, const float* w0, const float* b0, int E, const float* wh, const float* bh, int nh, int HD,
+                      float* gw0, float* gb0, float* gwh, float* gbh, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  return nsq_siren_mlp_film_bwd(gact, gact_stride_j, gact_stride_g, 0, grid, G, d, w0, b0, E, wh, bh, nh, HD, nullptr,
+                                1, 0, gw0, gb0, gwh, gbh, nullptr, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

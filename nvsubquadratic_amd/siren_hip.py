@@ -19,7 +19,11 @@ filter gradient (``nsq_siren_readout_bwd``); the MLP backward (``nsq_siren_mlp_b
 every hidden weight gradient over the points in a fixed order.  fp32 throughout, as the reference
 computes.
 
-Not covered: FiLM conditioning (``film_cfg``), which raises ``NotImplementedError``; hidden and
+FiLM conditioning (``film_cfg``, ``kernels_nd.py:1165-1187``): :class:`KernelFiLMGenerator` maps the conditioning
+vector to one ``(gamma, beta)`` pair per modulated layer (``modules/film.py:75``, a small torch MLP over ``[B,
+cond_dim]``); the per-point work -- ``h = gamma * sin(z) + beta`` inside the hidden stack, the per-sample readout and
+their gradients, ``gamma`` / ``beta`` gradients included -- runs in ``nsq_siren_mlp_film_{fwd,bwd}`` /
+``nsq_siren_film_readout_fwd``, the filter coming out per sample, ``[B, out_dim, *grid]``.  Not covered: hidden and
 embedding widths other than 16, 32, 64 or 128 (raised by the library).
 """
 
@@ -34,7 +38,8 @@ from torch.library import custom_op
 
 from . import _lib
 
-__all__ = ["HipSIRENKernelND", "siren_filter", "siren_filter_op", "siren_grid"]
+__all__ = ["HipSIRENKernelND", "KernelFiLMGenerator", "siren_film_filter", "siren_filter", "siren_filter_op",
+           "siren_grid"]
 
 
 def _opt(t: Optional[torch.Tensor]) -> int | None:
@@ -186,6 +191,133 @@ def _backward(ctx, gk, _gact):
 siren_filter_op.register_autograd(_backward, setup_context=_setup)
 
 
+def _readout_backward_samples(gk: torch.Tensor, act: torch.Tensor, wout: torch.Tensor,
+                              has_bout: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """:func:`_readout_backward` for per-sample filters ``gk [nb, H, G]``, ``act [nb, HD + 1, G]``: ``gact [nb, HD,
+    G]`` per sample, ``gwout`` / ``gbout`` summed over the samples."""
+    lib = _lib.get_lib()
+    nb, H, G = gk.shape
+    HD = wout.shape[1]
+    dev = gk.device
+    need = lib.nsq_siren_readout_bwd_workspace_bytes(H, HD, G, nb)
+    if need == 0:  # HD = 128: library products in float32
+        gact = torch.matmul(wout.t().contiguous(), gk)
+        gw_ext = torch.matmul(gk.transpose(0, 1).reshape(H, nb * G),
+                              (act if has_bout else act[:, :HD]).transpose(0, 1).reshape(-1, nb * G).t())
+        return gact, gw_ext[:, :HD].contiguous(), (gw_ext[:, HD].contiguous() if has_bout else wout.new_empty(0))
+    gact = torch.empty(nb, HD, G, dtype=torch.float32, device=dev)
+    gwout = torch.empty(H, HD, dtype=torch.float32, device=dev)
+    gbout = torch.empty(H if has_bout else 0, dtype=torch.float32, device=dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    _lib.check(lib.nsq_siren_readout_bwd(gk.data_ptr(), gk.stride(1), act.data_ptr(), act.stride(1), wout.data_ptr(),
+                                         H, HD, G, nb, gact.data_ptr(), gwout.data_ptr(), _opt(gbout), ws.data_ptr(),
+                                         ws.numel(), _lib.stream_ptr(dev)))
+    return gact, gwout, gbout
+
+
+@custom_op("nsq_hip::siren_film_filter", mutates_args=())
+def siren_film_filter_op(grid: torch.Tensor, w0: torch.Tensor, b0: Optional[torch.Tensor], wh: torch.Tensor,
+                         bh: Optional[torch.Tensor], wout: torch.Tensor, bout: Optional[torch.Tensor], film: torch.Tensor,
+                         nh: int, film_first: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-sample filters ``(k [nb, H, G], act [nb, HD + 1, G])`` for FiLM parameters ``film [nb, nfilm, 2, HD]``
+    (``nsq_siren_mlp_film_fwd``, ``nsq_siren_film_readout_fwd``)."""
+    lib = _lib.get_lib()
+    _lib.check_device(grid)
+    G, d = grid.shape
+    H, HD = wout.shape
+    nb = film.shape[0]
+    act = torch.empty(nb, HD + 1, G, dtype=torch.float32, device=grid.device)
+    st = _lib.stream_ptr(grid.device)
+    _lib.check(lib.nsq_siren_mlp_film_fwd(grid.data_ptr(), G, d, w0.data_ptr(), _opt(b0), w0.shape[0], wh.data_ptr(),
+                                          _opt(bh), nh, HD, film.data_ptr(), nb, int(film_first), act.data_ptr(), G,
+                                          st))
+    k = torch.empty(nb, H, G, dtype=torch.float32, device=grid.device)
+    _lib.check(lib.nsq_siren_film_readout_fwd(wout.data_ptr(), _opt(bout), H, HD, act.data_ptr(), G, G, nb,
+                                              k.data_ptr(), st))
+    return k, act
+
+
+@siren_film_filter_op.register_fake
+def _(grid, w0, b0, wh, bh, wout, bout, film, nh, film_first):
+    G, nb = grid.shape[0], film.shape[0]
+    return grid.new_empty(nb, wout.shape[0], G), grid.new_empty(nb, wout.shape[1] + 1, G)
+
+
+@custom_op("nsq_hip::siren_film_filter_backward", mutates_args=())
+def siren_film_filter_backward_op(gk: torch.Tensor, act: torch.Tensor, grid: torch.Tensor, w0: torch.Tensor,
+                                  b0: Optional[torch.Tensor], wh: torch.Tensor, bh: Optional[torch.Tensor],
+                                  wout: torch.Tensor, film: torch.Tensor, nh: int, film_first: bool,
+                                  has_bout: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                                           torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients ``(gw0, gb0, gwh, gbh, gwout, gbout, gfilm)`` of the per-sample filters (weights summed over the
+    samples, ``gfilm [nb, nfilm, 2, HD]`` per sample)."""
+    lib = _lib.get_lib()
+    G, d = grid.shape
+    H, HD = wout.shape
+    E = w0.shape[0]
+    nb = film.shape[0]
+    dev = grid.device
+    gk = gk.contiguous()
+    gact, gwout, gbout = _readout_backward_samples(gk, act, wout, has_bout)
+    gw0, gwh = torch.empty_like(w0), torch.empty_like(wh)
+    gb0 = torch.empty(E if _has(b0) else 0, device=dev)
+    gbh = torch.empty(nh * HD if _has(bh) else 0, device=dev)
+    gfilm = torch.empty_like(film)
+    need = lib.nsq_siren_mlp_film_bwd_workspace_bytes(G, d, E, nh, HD, nb, int(film_first))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    _lib.check(lib.nsq_siren_mlp_film_bwd(gact.data_ptr(), gact.stride(1), gact.stride(2), gact.stride(0),
+                                          grid.data_ptr(), G, d, w0.data_ptr(), _opt(b0), E, wh.data_ptr(), _opt(bh),
+                                          nh, HD, film.data_ptr(), nb, int(film_first), gw0.data_ptr(), _opt(gb0),
+                                          gwh.data_ptr(), _opt(gbh), gfilm.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          _lib.stream_ptr(dev)))
+    return gw0, gb0, gwh, gbh, gwout, gbout, gfilm
+
+
+@siren_film_filter_backward_op.register_fake
+def _(gk, act, grid, w0, b0, wh, bh, wout, film, nh, film_first, has_bout):
+    HD = wout.shape[1]
+    return (torch.empty_like(w0), w0.new_empty(w0.shape[0] if _has(b0) else 0), torch.empty_like(wh),
+            wh.new_empty(nh * HD if _has(bh) else 0), torch.empty_like(wout),
+            wout.new_empty(wout.shape[0] if has_bout else 0), torch.empty_like(film))
+
+
+def _film_setup(ctx, inputs, output):
+    grid, w0, b0, wh, bh, wout, bout, film, nh, film_first = inputs
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(grid, w0, b0, wh, bh, wout, film, output[1])
+    ctx.nh, ctx.film_first = nh, film_first
+    ctx.has_bout = bout is not None
+
+
+def _film_backward(ctx, gk, _gact):
+    grid, w0, b0, wh, bh, wout, film, act = ctx.saved_tensors
+    if gk is None:
+        return (None,) * 10
+    gw0, gb0, gwh, gbh, gwout, gbout, gfilm = siren_film_filter_backward_op(
+        gk.float(), act, grid, w0, b0, wh, bh, wout, film, ctx.nh, ctx.film_first, ctx.has_bout)
+    return (None, gw0, gb0 if b0 is not None else None, gwh, gbh if bh is not None else None, gwout,
+            gbout if ctx.has_bout else None, gfilm, None, None)
+
+
+siren_film_filter_op.register_autograd(_film_backward, setup_context=_film_setup)
+
+
+def siren_film_filter(grid: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor | None,
+                      hidden_w: Sequence[torch.Tensor], hidden_b: Sequence[torch.Tensor] | None, wout: torch.Tensor,
+                      bout: torch.Tensor | None, film_params: Sequence[tuple[torch.Tensor, torch.Tensor]],
+                      film_first: bool = False) -> torch.Tensor:
+    """Functional FiLM form: per-sample filters ``[B, H, G]`` for the ``(gamma, beta)`` pairs ``film_params`` (each
+    ``[B, HD]``, in :class:`KernelFiLMGenerator`'s order: with ``film_first`` the first pair modulates the positional
+    embedding, the rest the hidden layers in order)."""
+    f = lambda t: None if t is None else t.float().contiguous()  # noqa: E731
+    wh = torch.cat([w.float().reshape(-1) for w in hidden_w])
+    bh = None if hidden_b is None else torch.cat([b.float().reshape(-1) for b in hidden_b])
+    film = torch.stack([torch.stack([g.float(), b.float()], dim=1) for g, b in film_params], dim=1).contiguous()
+    return siren_film_filter_op(f(grid), f(w0), f(b0), wh, bh, f(wout), f(bout), film, len(hidden_w),
+                                bool(film_first))[0]
+
+
 def siren_filter(grid: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor | None, hidden_w: Sequence[torch.Tensor],
                  hidden_b: Sequence[torch.Tensor] | None, wout: torch.Tensor, bout: torch.Tensor | None) -> torch.Tensor:
     """Functional form: filter ``[H, G]`` (float32) at the ``G`` points of ``grid [G, d]``.
@@ -245,6 +377,73 @@ def _siren_init(layer: torch.nn.Linear, first: bool, w0: float) -> None:
             layer.bias.zero_()
 
 
+class KernelFiLMGenerator(torch.nn.Module):
+    """The FiLM conditioner of ``SIRENKernelND`` (``modules/film.py:75``): a two-layer MLP ``Linear(cond_dim,
+    film_hidden_dim) -> GELU -> Linear(film_hidden_dim, num_film_layers * 2 * kernel_hidden_dim)`` whose output,
+    split per layer, gives the ``(gamma, beta)`` pairs the generator applies as ``h <- gamma * h + beta``.
+
+    Same constructor arguments, parameter names (``mlp.0``, ``mlp.2``), initialisation (``"identity"``: output weight
+    zero, bias gamma = 1 / beta = 0, so FiLM starts as the identity; ``"small_random"``: output weight N(0,
+    ``init_std``)) and weight-decay flags (biases never decayed; ``no_weight_decay=True`` excludes the weights too, a
+    float puts them in a group with that decay).  It runs on ``[B, cond_dim]`` vectors, a few small torch ops; the
+    per-point work it conditions is in the HIP generator kernels."""
+
+    def __init__(self, cond_dim: int, kernel_hidden_dim: int, num_film_layers: int, film_hidden_dim: int = 64,
+                 no_weight_decay: bool | float = False, init_type: str = "identity", init_std: float = 1e-4):
+        if num_film_layers < 1:
+            raise ValueError(f"num_film_layers must be >= 1, got {num_film_layers}")
+        super().__init__()
+        self.num_film_layers = num_film_layers
+        self.kernel_hidden_dim = kernel_hidden_dim
+        width = num_film_layers * 2 * kernel_hidden_dim
+        self.mlp = torch.nn.Sequential(torch.nn.Linear(cond_dim, film_hidden_dim), torch.nn.GELU(),
+                                       torch.nn.Linear(film_hidden_dim, width))
+        last = self.mlp[-1]
+        with torch.no_grad():
+            if init_type == "identity":
+                last.weight.zero_()
+            elif init_type == "small_random":
+                last.weight.normal_(0.0, init_std)
+            else:
+                raise ValueError(f"Unknown init_type: {init_type!r}. Expected 'identity' or 'small_random'.")
+            pattern = torch.cat([torch.ones(kernel_hidden_dim), torch.zeros(kernel_hidden_dim)])
+            last.bias.copy_(pattern.repeat(num_film_layers))
+        for m in self.mlp.modules():
+            if isinstance(m, torch.nn.Linear) and m.bias is not None:
+                m.bias._no_weight_decay = True
+        if isinstance(no_weight_decay, float):
+            for prm in self.parameters():
+                if not getattr(prm, "_no_weight_decay", False):
+                    prm._weight_decay = no_weight_decay
+        elif no_weight_decay:
+            for prm in self.parameters():
+                prm._no_weight_decay = True
+
+    def flop_count(self) -> int:
+        """Multiply-add count of one sample's MLP, times two, plus the GELU (``film.py`` counts it this way)."""
+        a, b = self.mlp[0], self.mlp[2]
+        return 2 * a.in_features * a.out_features + a.out_features + 2 * b.in_features * b.out_features
+
+    def forward(self, conditioning: torch.Tensor) -> list[tuple[torch.Tensor, torch.Tensor]]:
+        """``conditioning [B, cond_dim]`` -> ``num_film_layers`` pairs ``(gamma [B, HD], beta [B, HD])``, shallowest
+        layer first."""
+        out = self.mlp(conditioning)
+        return [tuple(c.chunk(2, dim=-1)) for c in out.chunk(self.num_film_layers, dim=-1)]
+
+
+def _build_film(film_cfg) -> torch.nn.Module:
+    """The FiLM generator from ``film_cfg``: a module (used as is), a dict of :class:`KernelFiLMGenerator` arguments, or
+    a zero-argument factory (such as a lazy config's instantiation)."""
+    if isinstance(film_cfg, torch.nn.Module):
+        return film_cfg
+    if isinstance(film_cfg, dict):
+        return KernelFiLMGenerator(**film_cfg)
+    if callable(film_cfg):
+        return film_cfg()
+    raise TypeError(f"film_cfg must be a module, a dict of KernelFiLMGenerator arguments or a factory; got "
+                    f"{type(film_cfg).__name__}")
+
+
 class HipSIRENKernelND(torch.nn.Module):
     """``SIRENKernelND`` (``kernels_nd.py:876``) with the hidden stack in one HIP kernel.
 
@@ -258,8 +457,11 @@ class HipSIRENKernelND(torch.nn.Module):
                  omega_0: float, L_cache: int | Sequence[int], use_bias: bool, hidden_omega_0: float = 1.0,
                  film_cfg=None, film_after_pos_embed: bool = False):
         super().__init__()
-        if film_cfg is not None or film_after_pos_embed:
-            raise NotImplementedError("fft_backend='hip' SIREN filters: FiLM conditioning is not fused")
+        self.film_after_pos_embed = bool(film_after_pos_embed)
+        if film_after_pos_embed:
+            assert embedding_dim == mlp_hidden_dim, (
+                f"film_after_pos_embed requires embedding_dim == mlp_hidden_dim, got {embedding_dim} != "
+                f"{mlp_hidden_dim}")
         if num_layers < 2:
             raise ValueError(f"num_layers must be >= 2; got {num_layers}")
         self.out_dim, self.data_dim, self.mlp_hidden_dim = out_dim, data_dim, mlp_hidden_dim
@@ -277,7 +479,16 @@ class HipSIRENKernelND(torch.nn.Module):
         _siren_init(self.out_linear, first=False, w0=self.hidden_omega_0)
         with torch.no_grad():  # Wang init of the readout: unit initial energy whatever the grid volume
             self.out_linear.weight.mul_(math.sqrt(1.0 / math.prod(self.L_cache_per_axis)))
+        self.num_film_layers = len(self.hidden_linears)
         self.film_generator = None
+        if film_cfg is not None:
+            self.film_generator = _build_film(film_cfg)
+            expected = len(self.hidden_linears) + int(self.film_after_pos_embed)
+            if self.film_generator.num_film_layers != expected:
+                raise ValueError(
+                    f"film_generator.num_film_layers={self.film_generator.num_film_layers} does not match expected "
+                    f"{expected} (len(hidden_linears)={len(self.hidden_linears)} + "
+                    f"int(film_after_pos_embed)={int(self.film_after_pos_embed)})")
         # grid cache geometry: per-axis extent and limit; the step of the first cache is kept on growth
         self._cache_m = (1.0,) * data_dim
         self.step_sizes = tuple(1.0 / (L - 1) for L in self.L_cache_per_axis)
@@ -294,29 +505,35 @@ class HipSIRENKernelND(torch.nn.Module):
             self.L_cache_per_axis = new_L
         return siren_grid(self.L_cache_per_axis, self._cache_m, seq_lens, self.out_linear.weight.device)
 
-    def _filter(self, pts: torch.Tensor) -> torch.Tensor:
+    def _filter(self, pts: torch.Tensor, conditioning: torch.Tensor | None = None) -> torch.Tensor:
+        """``[nb, H, G]``: one filter (nb = 1), or one per sample of ``conditioning`` when the generator has FiLM."""
         pe = self.positional_embedding.linear
         hb = [lin.bias for lin in self.hidden_linears] if self.hidden_linears[0].bias is not None else None
-        return siren_filter(pts, pe.weight, pe.bias, [lin.weight for lin in self.hidden_linears], hb,
-                            self.out_linear.weight, self.out_linear.bias)
+        hw = [lin.weight for lin in self.hidden_linears]
+        if conditioning is not None and self.film_generator is not None:
+            film_params = self.film_generator(conditioning)
+            return siren_film_filter(pts, pe.weight, pe.bias, hw, hb, self.out_linear.weight, self.out_linear.bias,
+                                     film_params, self.film_after_pos_embed)
+        return siren_filter(pts, pe.weight, pe.bias, hw, hb, self.out_linear.weight, self.out_linear.bias)[None]
 
     def forward(self, seq_lens: tuple[int, ...], conditioning: torch.Tensor | None = None):
-        """``(kernel [1, *grid, out_dim], grid [1, *grid, data_dim])``: the kernel is a view of the
-        channel-first filter (``kernel.permute`` back to ``[1, out_dim, *grid]`` is contiguous)."""
-        if conditioning is not None:
-            raise NotImplementedError("fft_backend='hip' SIREN filters: FiLM conditioning is not fused")
+        """``(kernel [1|B, *grid, out_dim], grid [1, *grid, data_dim])``: the kernel is a view of the channel-first
+        filter (``kernel.permute`` back to ``[1|B, out_dim, *grid]`` is contiguous); per sample (``B``) when the
+        generator has FiLM and ``conditioning [B, cond_dim]`` is given (``kernels_nd.py:1149-1190``)."""
         grid = self._grid(seq_lens)
         shape = grid.shape[:-1]
-        k = self._filter(grid.reshape(-1, self.data_dim))  # [H, G]
-        kernel = k.reshape(1, self.out_dim, *shape).movedim(1, -1)
+        k = self._filter(grid.reshape(-1, self.data_dim), conditioning)  # [nb, H, G]
+        kernel = k.reshape(k.shape[0], self.out_dim, *shape).movedim(1, -1)
         return kernel, grid.unsqueeze(0)
 
-    def kernel_bhl(self, seq_lens: tuple[int, ...], causal: bool = False) -> torch.Tensor:
-        """Channel-first filter ``[1, out_dim, *grid]``; ``causal`` (1D): only the points
-        ``kernel_len // 2 ..`` that ``CKConvND``'s causal crop keeps (``ckconv_nd.py:1159-1164``)."""
+    def kernel_bhl(self, seq_lens: tuple[int, ...], causal: bool = False,
+                   conditioning: torch.Tensor | None = None) -> torch.Tensor:
+        """Channel-first filter ``[1|B, out_dim, *grid]``; ``causal`` (1D): only the points ``kernel_len // 2 ..``
+        that ``CKConvND``'s causal crop keeps (``ckconv_nd.py:1159-1164``); per sample with FiLM conditioning."""
         grid = self._grid(seq_lens)
         if causal:
             assert self.data_dim == 1, "the causal crop is 1D"
             grid = grid[grid.shape[0] // 2:]
         shape = grid.shape[:-1]
-        return self._filter(grid.reshape(-1, self.data_dim)).reshape(1, self.out_dim, *shape)
+        k = self._filter(grid.reshape(-1, self.data_dim), conditioning)
+        return k.reshape(k.shape[0], self.out_dim, *shape)

@@ -1,11 +1,14 @@
-"""SIREN implicit filter (SIRENKernelND without FiLM) restated on the CPU -- TEST INFRASTRUCTURE ONLY.
+"""SIREN implicit filter (SIRENKernelND, with and without FiLM) restated on the CPU -- TEST INFRASTRUCTURE ONLY.
 
 nvsubquadratic/modules/kernels_nd.py: the positional embedding sin(W0 x + b0) with its linear in float32
 (:855-871), the hidden layers sin(W_i h + b_i) (:1181-1183; ``Sine`` is plain ``torch.sin``, :634-638),
 the readout W_out h + b_out (:1189), for the coordinates ``grid [G, d]``; returns ``[G, H]`` (the
 reference's ``[1, *grid, H]`` flattened).  ``dtype=torch.float64`` evaluates the same network in double
-precision.  Pinned in tests/test_oracle_siren.py against a per-neuron loop evaluation, a closed form (zero
-hidden weights) and float64 finite differences of its gradients.
+precision.  FiLM (:1165-1187): per sample b, the pair (gamma_b, beta_b) of a modulated layer maps its output h to
+gamma_b * h + beta_b (broadcast over the points); with ``film_first`` the first pair modulates the positional
+embedding and the rest the hidden layers in order (``film_after_pos_embed``), else one pair per hidden layer.
+Pinned in tests/test_oracle_siren.py against a per-neuron loop evaluation (FiLM included), closed forms (zero hidden
+weights; identity FiLM = the plain network) and float64 finite differences of its gradients.
 """
 
 from __future__ import annotations
@@ -19,6 +22,29 @@ def siren_mlp_torch(grid, w0, b0, hidden_w, hidden_b, wout, bout, dtype=torch.fl
     for i, w in enumerate(hidden_w):
         h = torch.sin(torch.nn.functional.linear(h, f(w), None if hidden_b is None else f(hidden_b[i])))
     return torch.nn.functional.linear(h, f(wout), f(bout))
+
+
+def siren_film_torch(grid, w0, b0, hidden_w, hidden_b, wout, bout, film_params, film_first=False,
+                     dtype=torch.float32):
+    """Per-sample filters ``[B, G, H]`` for the FiLM pairs ``film_params`` (each ``(gamma [B, HD], beta [B, HD])``)."""
+    f = lambda t: None if t is None else t.to(dtype)  # noqa: E731
+    h = torch.sin(torch.nn.functional.linear(grid.to(dtype), f(w0), f(b0)))[None]  # [1, G, E]
+    pairs = [(f(g)[:, None, :], f(b)[:, None, :]) for g, b in film_params]
+    off = 0
+    if film_first:
+        h = pairs[0][0] * h + pairs[0][1]
+        off = 1
+    for i, w in enumerate(hidden_w):
+        h = torch.sin(torch.nn.functional.linear(h, f(w), None if hidden_b is None else f(hidden_b[i])))
+        h = pairs[i + off][0] * h + pairs[i + off][1]
+    return torch.nn.functional.linear(h, f(wout), f(bout))
+
+
+def film_pairs(B, HD, n, seed=0):
+    """Random FiLM pairs around the identity (gamma ~ 1 + U(-0.5, 0.5), beta ~ U(-0.3, 0.3)), float32."""
+    g = torch.Generator().manual_seed(seed)
+    return [(1 + torch.rand(B, HD, generator=g) - 0.5, (torch.rand(B, HD, generator=g) - 0.5) * 0.6)
+            for _ in range(n)]
 
 
 def siren_params(d, E, HD, nh, H, bias=True, omega_0=10.0, seed=0):

@@ -185,3 +185,127 @@ def test_readout_backward_one_pass(H, HD, G, nb, bias):
     assert torch.equal(again[0], gact) and torch.equal(again[1], gw)
     if bias:
         assert torch.equal(again[2], gb)
+
+
+# (d, grid shape, E, HD, nh, H, bias, samples, film_first): FiLM on the hidden layers only or also after the
+# embedding (E == HD), the widths the configs use, HD = 128 (readout gradient on library products), no biases
+FILM_CASES = [
+    (1, (599,), 32, 32, 2, 160, True, 3, False),
+    (2, (27, 27), 32, 32, 2, 384, True, 4, True),
+    (3, (9, 7, 5), 16, 64, 1, 64, False, 2, False),
+    (2, (13, 11), 128, 128, 3, 32, True, 2, True),
+    (1, (4095,), 64, 64, 3, 256, True, 2, True),
+]
+
+
+@pytest.mark.parametrize("case", FILM_CASES)
+def test_film_filter_matches_restatement(case):
+    """FiLM-conditioned per-sample filters (kernels_nd.py:1165-1190): forward rel-L2 <= 1e-5 against float64, every
+    weight, bias, gamma and beta gradient <= 1e-4 against float64 autograd, repeated backward calls bitwise equal."""
+    from nvsubquadratic_amd.siren_hip import siren_film_filter
+    from oracle.siren_ref import film_pairs, siren_film_torch
+
+    d, shape, E, HD, nh, H, bias, B, ff = case
+    print(f"siren film {case}", flush=True)
+    grid = _grid(shape).reshape(-1, d)
+    w0, b0, hw, hb, wo, bo = siren_params(d, E, HD, nh, H, bias=bias, seed=2)
+    pairs = film_pairs(B, HD, nh + int(ff), seed=3)
+    leaves = [w0, b0, *hw, *(hb or []), wo, bo] + [t for pr in pairs for t in pr]
+    nl = len(leaves) - 2 * len(pairs)
+
+    def split(ts):
+        hb_ = ts[2 + nh:2 + 2 * nh] if hb is not None else None
+        fp = [(ts[nl + 2 * i], ts[nl + 2 * i + 1]) for i in range(len(pairs))]
+        return ts[0], ts[1], ts[2:2 + nh], hb_, ts[nl - 2], ts[nl - 1], fp
+
+    ref = [None if t is None else t.double().requires_grad_(True) for t in leaves]
+    w0r, b0r, hwr, hbr, wor, bor, fpr = split(ref)
+    y = siren_film_torch(grid.double(), w0r, b0r, hwr, hbr, wor, bor, fpr, ff, dtype=torch.float64)  # [B, G, H]
+    g = torch.randn(y.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(6))
+    y.backward(g)
+    hip = [None if t is None else t.cuda().requires_grad_(True) for t in leaves]
+    w0h, b0h, hwh, hbh, woh, boh, fph = split(hip)
+    k = siren_film_filter(grid.cuda(), w0h, b0h, hwh, hbh, woh, boh, fph, ff)
+    assert k.shape == (B, H, grid.shape[0])
+    assert rel_l2(y.detach().transpose(1, 2), k.detach()) < 1e-5
+    gk = g.transpose(1, 2).float().cuda().contiguous()
+    k.backward(gk)
+    first = []
+    for r, h in zip(ref, hip):
+        if r is None:
+            continue
+        assert rel_l2(r.grad, h.grad) < 1e-4
+        first.append(h.grad.clone())
+        h.grad = None
+    siren_film_filter(grid.cuda(), w0h, b0h, hwh, hbh, woh, boh, fph, ff).backward(gk)
+    assert all(torch.equal(a, h.grad) for a, h in zip(first, [t for t in hip if t is not None]))
+
+
+def test_film_module_forward_and_kernel_bhl():
+    """HipSIRENKernelND with film_cfg: forward(seq_lens, conditioning) -> [B, *grid, out_dim], equal to the
+    restatement with the generator's own (gamma, beta); kernel_bhl gives the channel-first view; without
+    conditioning the plain [1, *grid, out_dim] filter."""
+    from oracle.siren_ref import siren_film_torch
+
+    torch.manual_seed(0)
+    m = HipSIRENKernelND(out_dim=48, data_dim=2, mlp_hidden_dim=32, num_layers=3, embedding_dim=32, omega_0=10.0,
+                         L_cache=(14, 14), use_bias=True,
+                         film_cfg=dict(cond_dim=8, kernel_hidden_dim=32, num_film_layers=3,
+                                       init_type="small_random", init_std=0.2),
+                         film_after_pos_embed=True).cuda()
+    with torch.no_grad():
+        for lin in m.hidden_linears:
+            lin.bias.uniform_(-1, 1)
+    cond = torch.randn(3, 8, device="cuda")
+    kernel, grid = m((14, 14), conditioning=cond)
+    assert kernel.shape == (3, 27, 27, 48) and grid.shape == (1, 27, 27, 2)
+    pairs = [(gm.detach().cpu(), bt.detach().cpu()) for gm, bt in m.film_generator(cond)]
+    pe = m.positional_embedding.linear
+    ref = siren_film_torch(grid[0].reshape(-1, 2).cpu().double(), pe.weight.cpu(), pe.bias.cpu(),
+                           [lin.weight.cpu() for lin in m.hidden_linears], [lin.bias.cpu() for lin in m.hidden_linears],
+                           m.out_linear.weight.cpu(), m.out_linear.bias.cpu(), pairs, True, dtype=torch.float64)
+    assert rel_l2(ref.reshape(3, 27, 27, 48), kernel.detach().cpu()) < 1e-5
+    bhl = m.kernel_bhl((14, 14), conditioning=cond)
+    assert torch.equal(bhl, kernel.movedim(-1, 1))
+    plain, _ = m((14, 14))
+    assert plain.shape == (1, 27, 27, 48)
+    # gradients reach the FiLM generator's parameters through gamma / beta
+    kernel.square().sum().backward()
+    assert m.film_generator.mlp[0].weight.grad is not None and m.film_generator.mlp[0].weight.grad.abs().sum() > 0
+
+
+def test_film_filters_drive_the_per_sample_causal_conv():
+    """End to end (rows F1 and F3): FiLM-conditioned filters [B, H, L] on the causal half of the grid feed the HIP
+    causal FFT conv as per-sample filters; output and gradients (input, SIREN weights, every gamma and beta) against
+    the same chain on the CPU oracle in float32, rel-L2 <= 1e-4."""
+    from nvsubquadratic_amd.fftconv_hip import causal_fftconv1d_bhl
+    from nvsubquadratic_amd.siren_hip import siren_film_filter
+    from oracle.fftconv_ref import causal_fftconv1d_torch
+    from oracle.siren_ref import film_pairs, siren_film_torch
+
+    B, H, L, HD = 2, 64, 1024, 32
+    print(f"film -> causal conv B={B} H={H} L={L}", flush=True)
+    grid = siren_grid((L,), (1.0,), (L,))[L - 1:].contiguous()  # the L points CKConvND's causal crop keeps
+    w0, b0, hw, hb, wo, bo = siren_params(1, 32, HD, 2, H, seed=4)
+    pairs = film_pairs(B, HD, 2, seed=5)
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(B, H, L, generator=gen)
+    s = torch.randn(H, generator=gen)
+    g = torch.randn(B, H, L, generator=gen)
+    leaves = [w0, b0, *hw, *hb, wo, bo, *[t for pr in pairs for t in pr], x, s]
+
+    def chain(ts, filt, conv, film_fn):
+        w0_, b0_, w1, w2, b1, b2, wo_, bo_ = ts[:8]
+        fp = [(ts[8], ts[9]), (ts[10], ts[11])]
+        k = filt(film_fn, w0_, b0_, [w1, w2], [b1, b2], wo_, bo_, fp)  # [B, H, L]
+        return conv(ts[12], k, ts[13])
+
+    ref = [t.clone().requires_grad_(True) for t in leaves]
+    yr = chain(ref, lambda f, *a: f(grid, *a[:6], a[6]).transpose(1, 2), causal_fftconv1d_torch, siren_film_torch)
+    yr.backward(g)
+    hip = [t.cuda().requires_grad_(True) for t in leaves]
+    yh = chain(hip, lambda f, *a: f(grid.cuda(), *a[:6], a[6]), causal_fftconv1d_bhl, siren_film_filter)
+    yh.backward(g.cuda())
+    assert rel_l2(yr.detach(), yh.detach().cpu()) < 1e-4
+    for r, h in zip(ref, hip):
+        assert rel_l2(r.grad, h.grad.cpu()) < 1e-4
