@@ -139,10 +139,10 @@ int nsq_circular_fftconv1d_bwd(const void* g, const void* x, const float* k, con
  *     fftconv1d_fp32_bhl (nvsubquadratic/ops/fftconv.py:603-660) and
  *     mixed_fftconv1d_fp32_bhl with periodic=(False,) (ops/mixed_fftconv.py:504-630,
  *     recipe :295-342):  y[n] = sum_j k[j] x[n + K/2 - j], x zero outside
- *     [0, L), n in [0, L); K <= 2L; L + ceil(K/2) <= 2^23, else
+ *     [0, L), n in [0, L); K <= 2L; L + ceil(K/2) <= 2^24, else
  *     NSQ_ERR_UNSUPPORTED.
  *   periodic = 1: the circular conv of nsq_circular_fftconv1d_fwd, for power-of-
- *     two L <= 2^23.
+ *     two L <= 2^24.
  * Then y is rounded to the I/O dtype and shortcut * x added (as the causal op).
  * kbatch 1 or B.  FFT lengths <= 16384 run the fused kernels and need no
  * workspace; longer ones the 4-step plan, with a workspace of

@@ -20,7 +20,7 @@ signature parity; both of the reference's branches give the same result and
 the kernels always apply the shift in the frequency domain.
 
 Sizes: power-of-two periodic lengths run as above (2D / 3D: up to 1024 per
-axis; 1D: up to 2^23, the fused kernels up to 16384 and the 4-step plan
+axis; 1D: up to 2^24, the fused kernels up to 16384 and the 4-step plan
 beyond; lengths below 16 on their periodic extension at FFT length 16).  A
 periodic axis of any other length S runs as a zero-padded "same" axis on the
 periodic extension of x (:func:`periodic_by_extension`): the circular sums

@@ -21,15 +21,24 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
                 (long long)(2 * L));
   NSQ_CHECK_ARG(B * H <= 0x7fffffff && L <= (int64_t(1) << 30), "fftconv1d_causal: tensor too large");
   if (!make_plan(L, K, p)) {
-    set_error("fftconv1d_causal: unsupported (L=%lld, K=%lld): FFT length beyond 2^23", (long long)L, (long long)K);
+    set_error("fftconv1d_causal: unsupported (L=%lld, K=%lld): FFT length beyond 2^24", (long long)L, (long long)K);
     return NSQ_ERR_UNSUPPORTED;
   }
-  // 4-step column grids are B*H * (N2 / columns per workgroup) <= B*H * 512; per-sample filters run the
-  // row passes over B*H channels, B*H * N1/2 <= B*H * 512 workgroups.
-  NSQ_CHECK_ARG(p.fused || B * H < (int64_t(1) << 22) + (kbatch == 1 ? 1 : 0),
+  // 4-step column grids are B*H * (N2 / columns per workgroup) <= B*H * 512 workgroups; the row passes run
+  // B*H * N1/2 (N1 <= 2048: up to B*H * 1024) workgroups: both below 2^31.
+  NSQ_CHECK_ARG(p.fused || B * H * (int64_t(1) << (p.logN1 - 1 > 9 ? p.logN1 - 1 : 9)) < (int64_t(1) << 31),
                 "fftconv1d_causal: B*H=%lld too large for the 4-step plan", (long long)(B * H));
   NSQ_CHECK_ARG(!p.fused || kbatch == 1 || B <= 65535, "fftconv1d_causal: B=%lld too large for per-sample filters",
                 (long long)B);
+  return NSQ_OK;
+}
+
+// The 4-step passes' grids: B*H * max(N1/2, 512) workgroups, below 2^31.
+static int check_4step_grid(const char* op, int64_t B, int64_t H, int logN) {
+  if (logN <= 13) return NSQ_OK;
+  const int l1 = split_log_n1(logN);
+  NSQ_CHECK_ARG(B * H * (int64_t(1) << (l1 - 1 > 9 ? l1 - 1 : 9)) < (int64_t(1) << 31),
+                "%s: B*H=%lld too large for the 4-step plan", op, (long long)(B * H));
   return NSQ_OK;
 }
 
@@ -41,7 +50,7 @@ static int validate(const void* a, const void* b, const float* k, int dtype, int
 // the fused plan up to 13, the 4-step plan (with a workspace) up to max_logn.
 static int validate_shifted(const char* op, const void* a, const void* b, const float* k, int dtype, int64_t B,
                             int64_t H, int64_t L, int64_t K, int64_t kbatch, bool zpad, int& logN,
-                            int max_logn = 22) {
+                            int max_logn = kMaxLogN) {
   NSQ_CHECK_ARG(a && b && k, "%s: null tensor pointer", op);
   NSQ_CHECK_ARG(valid_dtype(dtype), "%s: unsupported dtype code %d", op, dtype);
   NSQ_CHECK_ARG(B >= 1 && H >= 1 && L >= 1 && K >= 1, "%s: sizes must be positive (B=%lld H=%lld L=%lld K=%lld)",
@@ -63,7 +72,7 @@ static int validate_shifted(const char* op, const void* a, const void* b, const 
       return NSQ_ERR_UNSUPPORTED;
     }
     logN = (F < 16 ? 4 : ilog2_ceil(F)) - 1;
-    return NSQ_OK;
+    return check_4step_grid(op, B, H, logN);
   }
   if (L > maxF || (L & (L - 1))) {
     set_error("%s: unsupported length L=%lld: the HIP kernels take powers of two up to %lld", op, (long long)L,
@@ -71,7 +80,7 @@ static int validate_shifted(const char* op, const void* a, const void* b, const 
     return NSQ_ERR_UNSUPPORTED;
   }
   logN = (L < 16 ? 4 : ilog2_ceil(L)) - 1;
-  return NSQ_OK;
+  return check_4step_grid(op, B, H, logN);
 }
 
 // Workspace of a shifted conv: none on the fused plan; on the 4-step plan the
@@ -82,7 +91,7 @@ static size_t shifted_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K
   int logN = 0;
   if (!valid_dtype(dtype) || B < 1 || H < 1 || L < 1 || K < 1 || K > (zpad ? 2 * L : L)) return 0;
   const int64_t F = zpad ? L + (K + 1) / 2 : L;
-  if (F > (int64_t(2) << 22) || (!zpad && (L & (L - 1)))) return 0;
+  if (F > (int64_t(2) << kMaxLogN) || (!zpad && (L & (L - 1)))) return 0;
   logN = (F < 16 ? 4 : ilog2_ceil(F)) - 1;
   if (logN <= 13) return 0;
   const int64_t N = int64_t(1) << logN;
@@ -373,7 +382,7 @@ int nsq_mixed_fftconv1d_fwd(const void* x, const float* k, const void* shortcut,
   clear_error();
   NSQ_CHECK_ARG(periodic <= 1u, "mixed_fftconv1d_fwd: periodic mask 0x%x names an axis >= 1", periodic);
   return shifted_fwd(periodic ? "mixed_fftconv1d_fwd (periodic)" : "mixed_fftconv1d_fwd (zero-padded)", x, k,
-                     shortcut, y, dtype, B, H, L, K, kbatch, periodic == 0, workspace, workspace_bytes, 22, stream);
+                     shortcut, y, dtype, B, H, L, K, kbatch, periodic == 0, workspace, workspace_bytes, kMaxLogN, stream);
 }
 
 int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const void* shortcut, void* gx, float* gk,
@@ -382,7 +391,7 @@ int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const 
   clear_error();
   NSQ_CHECK_ARG(periodic <= 1u, "mixed_fftconv1d_bwd: periodic mask 0x%x names an axis >= 1", periodic);
   return shifted_bwd(periodic ? "mixed_fftconv1d_bwd (periodic)" : "mixed_fftconv1d_bwd (zero-padded)", g, x, k,
-                     shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, periodic == 0, workspace, workspace_bytes, 22,
+                     shortcut, gx, gk, gs, dtype, B, H, L, K, kbatch, periodic == 0, workspace, workspace_bytes, kMaxLogN,
                      stream);
 }
 

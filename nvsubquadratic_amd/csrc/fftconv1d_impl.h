@@ -10,7 +10,7 @@
 //    for each batch row: real FFT of x in LDS -> spectral product -> inverse
 //    FFT -> crop/cast/shortcut epilogue straight to HBM.  HBM traffic is the
 //    algorithmic minimum (x, k read once; y written once).
-//  * 4-step (2^15 <= F <= 2^23): the packed complex length N = F/2 is split as
+//  * 4-step (2^15 <= F <= 2^24): the packed complex length N = F/2 is split as
 //    N = N1 x N2 (Cooley-Tukey).  Three kernels:
 //      col_fwd  : length-N1 DFTs down the columns of each signal (x, k, g),
 //                 times the twiddle W_N^{n2 k1}, to a workspace;
@@ -46,10 +46,13 @@ struct Plan1D {
 };
 
 // 4-step split N = N1 x N2: columns of N1 <= 256 points (two LDS passes) and
-// rows of N2 <= 4096 points; N1 grows beyond 256 only when N2 would exceed 4096.
+// rows of N2 <= 4096 points; N1 grows beyond 256 only when N2 would exceed 4096,
+// up to 2048 (a column tile of 8 x 2048 points is 131 KB of LDS and 1024
+// threads): N <= 2048 x 4096 = 2^23.
 __host__ __device__ constexpr int split_log_n1(int logN) {
   return (logN - 12 > ((logN / 2) < 8 ? (logN / 2) : 8)) ? (logN - 12) : ((logN / 2) < 8 ? (logN / 2) : 8);
 }
+constexpr int kMaxLogN = 23;
 
 inline bool make_plan(int64_t L, int64_t K, Plan1D& p) {
   if (L < 1 || K < 1 || K > 2 * L) return false;
@@ -61,7 +64,7 @@ inline bool make_plan(int64_t L, int64_t K, Plan1D& p) {
   p.logN = logF - 1;
   p.fused = p.logN <= 13;
   if (!p.fused) {
-    if (p.logN > 22) return false;
+    if (p.logN > kMaxLogN) return false;
     p.logN1 = split_log_n1(p.logN);
     p.logN2 = p.logN - p.logN1;
   } else {
@@ -1705,7 +1708,7 @@ struct FourStepShift {
   };
 };
 
-// 4-step instantiations: logN in [14, 22] split by split_log_n1.
+// 4-step instantiations: logN in [14, kMaxLogN] split by split_log_n1.
 template <int DT, bool BWD>
 struct FourStep {
   template <int LOGN>
@@ -1730,7 +1733,7 @@ bool run_fwd(const Plan1D& p, const void* x, const float* k, const void* s, void
              int kfilm, float2* ws, bool save, const float2* tw, hipStream_t st) {
   if (p.fused)
     return dispatch_int<FusedFwd<DT>::template At, 3, 13>(p.logN, p, x, k, s, y, B, H, L, K, kfilm, tw, st);
-  return dispatch_int<FourStep<DT, false>::template At, 14, 22>(p.logN, x, k, s, y, B, H, L, K, kfilm, ws,
+  return dispatch_int<FourStep<DT, false>::template At, 14, kMaxLogN>(p.logN, x, k, s, y, B, H, L, K, kfilm, ws,
                                                                  save && !p.fold, tw, st, p.fold);
 }
 
@@ -1741,7 +1744,7 @@ bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, cons
   if (p.fused)
     return dispatch_int<FusedBwd<DT>::template At, 3, 13>(p.logN, p, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, tw,
                                                           st);
-  return dispatch_int<FourStep<DT, true>::template At, 14, 22>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, ws,
+  return dispatch_int<FourStep<DT, true>::template At, 14, kMaxLogN>(p.logN, g, x, k, s, gx, gk, gs, B, H, L, K, kfilm, ws,
                                                                 fwd_state && !p.fold, tw, st, p.fold);
 }
 
@@ -1811,15 +1814,15 @@ bool run_circ_bwd(int logN, const void* g, const void* x, const float* k, const 
                                                                zpad, tw, st);
 }
 
-// Shifted convs on the 4-step plan (logN in [14, 22]); `roll` holds B*H rows of
+// Shifted convs on the 4-step plan (logN in [14, kMaxLogN]); `roll` holds B*H rows of
 // F = 2^(logN+1) I/O-dtype values, `ws` the 4-step workspace without `save`.
 template <int DT>
 bool run_shift4_fwd(int logN, const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
                     int kfilm, int c, bool zpad, void* roll, float2* ws, const float2* tw, hipStream_t st) {
-  if (logN < 14 || logN > 22) return false;
+  if (logN < 14 || logN > kMaxLogN) return false;
   const int F = 2 << logN;
   launch_shift_rows<DT>(x, roll, int64_t(B) * H, L, F, c, zpad ? F : L, st);
-  return dispatch_int<FourStepShift<DT, false>::template At, 14, 22>(logN, (const void*)roll, x, k, s, y, B, H, L, K,
+  return dispatch_int<FourStepShift<DT, false>::template At, 14, kMaxLogN>(logN, (const void*)roll, x, k, s, y, B, H, L, K,
                                                                      kfilm, ws, tw, st);
 }
 
@@ -1827,10 +1830,10 @@ template <int DT>
 bool run_shift4_bwd(int logN, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
                     float* gs, int B, int H, int L, int K, int kfilm, int c, bool zpad, void* roll, float2* ws,
                     const float2* tw, hipStream_t st) {
-  if (logN < 14 || logN > 22) return false;
+  if (logN < 14 || logN > kMaxLogN) return false;
   const int F = 2 << logN;
   launch_shift_rows<DT>(g, roll, int64_t(B) * H, L, F, -c, zpad ? F : L, st);
-  return dispatch_int<FourStepShift<DT, true>::template At, 14, 22>(logN, (const void*)roll, g, x, k, s, gx, gk, gs,
+  return dispatch_int<FourStepShift<DT, true>::template At, 14, kMaxLogN>(logN, (const void*)roll, g, x, k, s, gx, gk, gs,
                                                                     B, H, L, K, kfilm, c, ws, tw, st);
 }
 

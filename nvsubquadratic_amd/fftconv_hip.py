@@ -690,7 +690,7 @@ def fftconv1d_bhl(x: torch.Tensor, kernel: torch.Tensor, shortcut: torch.Tensor 
     Runs ``nsq_mixed_fftconv1d_*`` with ``periodic=0`` at FFT length
     ``pow2(L + ceil(K/2))`` (the reference's ``L + (K+1)//2`` gives the same
     result: every length from there on keeps the output window free of
-    wrap-around): the fused kernels up to 16384, the 4-step plan up to 2^23;
+    wrap-around): the fused kernels up to 16384, the 4-step plan up to 2^24;
     longer raises ``NotImplementedError``.
     """
     batch_size, hidden_dim, seq_len = x.shape

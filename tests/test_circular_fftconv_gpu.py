@@ -159,10 +159,10 @@ def test_circular_rejects_mismatched_shortcut_dtype():
         C.circular_fftconv1d_fp32_bhl(x, k, torch.randn(4, device="cuda", dtype=torch.bfloat16))
 
 
-@pytest.mark.parametrize("xs,ks", [((1, 2, 2**24), (5,)), ((1, 2, 2048, 16), (3, 3)), ((1, 2, 1000, 12), (101, 3))])
+@pytest.mark.parametrize("xs,ks", [((1, 2, 2**25), (5,)), ((1, 2, 2048, 16), (3, 3)), ((1, 2, 1000, 12), (101, 3))])
 def test_circular_unsupported_lengths_raise(xs, ks):
-    """Out-of-range periodic lengths are refused, not approximated (1000 with 101 taps: its periodic extension
-    needs FFT length 2048 on that axis)."""
+    """Out-of-range periodic lengths are refused, not approximated (1D: beyond the 4-step plan's 2^24; 1000 with
+    101 taps: its periodic extension needs FFT length 2048 on that axis)."""
     x = torch.randn(*xs, device="cuda")
     k = torch.randn(1, xs[1], *ks, device="cuda")
     with pytest.raises(NotImplementedError):

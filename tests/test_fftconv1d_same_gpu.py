@@ -99,9 +99,9 @@ def test_same_1d_routing_chunking_and_layouts_bitwise():
 
 
 def test_same_1d_limits():
-    x = torch.randn(1, 2, 2**23 - 100, device="cuda")
+    x = torch.randn(1, 2, 2**24 - 100, device="cuda")
     with pytest.raises(NotImplementedError, match="FFT length"):
-        Z.fftconv1d_bhl(x, torch.randn(1, 2, 400, device="cuda"))  # L + ceil(K/2) > 2^23
+        Z.fftconv1d_bhl(x, torch.randn(1, 2, 400, device="cuda"))  # L + ceil(K/2) > 2^24
     with pytest.raises(AssertionError, match="2 \\* seq_len"):
         Z.fftconv1d_bhl(torch.randn(1, 2, 8, device="cuda"), torch.randn(1, 2, 17, device="cuda"))
     # the C-ABI's own checks: K > 2L and a mask naming axis 1
