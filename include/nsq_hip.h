@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 12
+#define NSQ_ABI_VERSION 13
 
 enum {
   NSQ_OK = 0,
@@ -435,6 +435,21 @@ int nsq_siren_mlp_film_bwd(const float* gact, int64_t gact_stride_j, int64_t gac
                            const float* wh, const float* bh, int nh, int HD, const float* film, int64_t nb,
                            int film_first, float* gw0, float* gb0, float* gwh, float* gbh, float* gfilm,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* QK-norm over channels (ABI 13): nvsubquadratic/utils/qk_norm.py L2Norm, i.e.
+ * F.normalize(x, p=2, dim=channels, eps) at the Hyena operator's q / k norm site
+ * (modules/hyena_nd.py:529-543): out[b,c,s] = round(x / max(round(||x[b,:,s]||), eps)),
+ * the norm over the C channels accumulated in fp32 and rounded to the I/O dtype
+ * as torch's norm of a 16-bit tensor is.  x [B, C, S] channels-first; out
+ * [B, S, C] (out_channels_last) or [B, C, S]; the backward's dout has the output's
+ * layout and dx the input's: dx = (dout - xhat sum_c(dout xhat)) / n, dout / n
+ * where n was clamped.  One pass each way, no workspace.  C <= 7781 forward,
+ * C <= 3536 backward (NSQ_ERR_UNSUPPORTED beyond). */
+int nsq_channel_l2norm_fwd(const void* x, void* out, int dtype, int64_t B, int64_t C, int64_t S, float eps,
+                           int out_channels_last, void* stream);
+
+int nsq_channel_l2norm_bwd(const void* dout, const void* x, void* dx, int dtype, int64_t B, int64_t C, int64_t S,
+                           float eps, int out_channels_last, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Channels-last (BLH) layout changes (ABI 9).

@@ -31,6 +31,12 @@
 // tile, sums its share per channel in LDS (each channel owned by one
 // thread), writes one partial row, and a second kernel adds the rows in a
 // fixed order (deterministic).
+//
+// L2 mode (the QK-norm, nvsubquadratic/utils/qk_norm.py L2Norm: F.normalize(x,
+// p=2, dim=channels, eps)): n[b,s] = max(round(sqrt(sum_c u^2)), eps) (torch's
+// norm of a 16-bit tensor returns that dtype), out = round(u / n), no weight;
+// backward du = (dout - xhat sum_c(dout xhat)) / n, or dout / n where n was
+// clamped to eps (the clamp passes no gradient to the norm).
 #include "gate.h"
 #include "nsq_common.h"
 
@@ -93,12 +99,14 @@ struct CfMap {
 };
 
 // Phase shared by both directions: u into U[c][s] (zero past S), per-position
-// r = rsqrt(mean u^2 + eps) into rs[].  red holds G x TS partial sums.
+// r = rsqrt(mean u^2 + eps) (RMS) or 1 / max(round(||u||), eps) (l2) into rs[];
+// l2 with cl: cl[s] = 0 where the norm was clamped to eps, else 1.  red holds
+// G x TS partial sums.
 template <int DT, int VW>
 __device__ __forceinline__ void load_tile_u(const typename Elem<DT>::T* __restrict__ y,
                                             const typename Elem<DT>::T* __restrict__ v, bool gated, int act,
                                             int64_t rowbase, int C, int64_t S, int64_t s0, int TS, float eps,
-                                            float* U, float* red, float* rs) {
+                                            float* U, float* red, float* rs, bool l2 = false, float* cl = nullptr) {
 #pragma clang fp contract(off)
   const CfMap<VW> m(TS);
   constexpr int NB = CfMap<VW>::kNB;
@@ -139,7 +147,13 @@ __device__ __forceinline__ void load_tile_u(const typename Elem<DT>::T* __restri
   if (threadIdx.x < TS) {
     float sum = 0.f;
     for (int k = 0; k < m.G; ++k) sum += red[k * TS + threadIdx.x];
-    rs[threadIdx.x] = rsqrtf(sum * (1.f / float(C)) + eps);
+    if (l2) {
+      const float n = Elem<DT>::round(sqrtf(sum));
+      rs[threadIdx.x] = 1.f / fmaxf(n, eps);
+      if (cl) cl[threadIdx.x] = n < eps ? 0.f : 1.f;
+    } else {
+      rs[threadIdx.x] = rsqrtf(sum * (1.f / float(C)) + eps);
+    }
   }
   __syncthreads();
 }
@@ -152,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_fwd_kernel(const typename Ele
                                                               const float* __restrict__ w,
                                                               typename Elem<DT>::T* __restrict__ out, int C,
                                                               int64_t S, int TS, int64_t tiles_per_b, int64_t ntiles,
-                                                              float eps, int gated, int act, int out_blh) {
+                                                              float eps, int gated, int act, int out_blh, int l2) {
 #pragma clang fp contract(off)
   extern __shared__ float smem[];
   const int ld = TS + 1;
@@ -162,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_fwd_kernel(const typename Ele
   const int64_t tile = xcd_remap(blockIdx.x, ntiles);
   const int64_t b = tile / tiles_per_b, s0 = (tile % tiles_per_b) * TS;
   const int64_t rowbase = b * C * S;
-  load_tile_u<DT, VW>(y, v, gated != 0, act, rowbase, C, S, s0, TS, eps, U, red, rs);
+  load_tile_u<DT, VW>(y, v, gated != 0, act, rowbase, C, S, s0, TS, eps, U, red, rs, l2 != 0);
   const int t = threadIdx.x;
   const int nval = int(S - s0 < TS ? S - s0 : TS);
   if (out_blh) {
@@ -172,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_fwd_kernel(const typename Ele
       if (s < nval) {
         float o[VW];
 #pragma unroll
-        for (int k = 0; k < VW; ++k) o[k] = w[c + k] * (U[(c + k) * ld + s] * rs[s]);
+        for (int k = 0; k < VW; ++k) o[k] = (w ? w[c + k] : 1.f) * (U[(c + k) * ld + s] * rs[s]);
         st_vec<DT, VW>(out, (b * S + s0 + s) * int64_t(C) + c, o);
       }
     }
@@ -183,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_fwd_kernel(const typename Ele
       for (int c = m.g; c < C; c += m.G) {
         float o[VW];
 #pragma unroll
-        for (int k = 0; k < VW; ++k) o[k] = w[c] * (U[c * ld + p0 + k] * rs[p0 + k]);
+        for (int k = 0; k < VW; ++k) o[k] = (w ? w[c] : 1.f) * (U[c * ld + p0 + k] * rs[p0 + k]);
         st_vec<DT, VW>(out, rowbase + int64_t(c) * S + s0 + p0, o);
       }
   }
@@ -194,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
     const typename Elem<DT>::T* __restrict__ dout, const typename Elem<DT>::T* __restrict__ y,
     const typename Elem<DT>::T* __restrict__ v, const float* __restrict__ w, typename Elem<DT>::T* __restrict__ dy,
     typename Elem<DT>::T* __restrict__ dv, float* __restrict__ dw_part, int C, int64_t S, int TS,
-    int64_t tiles_per_b, int64_t ntiles, float eps, int gated, int act, int in_blh) {
+    int64_t tiles_per_b, int64_t ntiles, float eps, int gated, int act, int in_blh, int l2) {
 #pragma clang fp contract(off)
   extern __shared__ float smem[];
   const int ld = TS + 1;
@@ -203,7 +217,8 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
   float* gacc = D + C * ld;         // dw share of this workgroup
   float* red = gacc + C;            // G x TS partial sums
   float* rs = red + kThreads * VW;  // r per position
-  float* ms = rs + TS;              // mean_c(w dout xhat) per position
+  float* ms = rs + TS;              // mean_c(w dout xhat) (RMS) or sum_c(dout xhat) unless clamped (l2)
+  float* cl = ms + TS;              // l2: 0 where the norm was clamped
   const int t = threadIdx.x;
   const CfMap<VW> m(TS);
   constexpr int NB = CfMap<VW>::kNB;
@@ -217,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
     const int64_t b = tile / tiles_per_b, s0 = (tile % tiles_per_b) * TS;
     const int64_t rowbase = b * C * S;
     const int nval = int(S - s0 < TS ? S - s0 : TS);
-    load_tile_u<DT, VW>(y, v, gated != 0, act, rowbase, C, S, s0, TS, eps, U, red, rs);
+    load_tile_u<DT, VW>(y, v, gated != 0, act, rowbase, C, S, s0, TS, eps, U, red, rs, l2 != 0, cl);
     // dout into D[c][s] (zero past S)
     if (in_blh) {
       const int nitems = TS * (C / VW);
@@ -268,7 +283,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
 #pragma unroll
       for (int k = 0; k < VW; ++k) dot[k] = 0.f;
       for (int c = m.g; c < C; c += m.G) {
-        const float wc = w[c];
+        const float wc = w ? w[c] : 1.f;
 #pragma unroll
         for (int k = 0; k < VW; ++k) {
           const float xh = U[c * ld + p0 + k] * rs[p0 + k];
@@ -283,10 +298,10 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
     if (t < TS) {
       float sum = 0.f;
       for (int k = 0; k < m.G; ++k) sum += red[k * TS + t];
-      ms[t] = sum * (1.f / float(C));
+      ms[t] = l2 ? sum * cl[t] : sum * (1.f / float(C));
     }
     // dw share: each channel summed over the tile's positions by its owner thread
-    for (int c = t; c < C; c += kThreads) {
+    for (int c = t; c < C && w; c += kThreads) {
       float a = gacc[c];
       for (int s = 0; s < TS; ++s) a = fmaf(D[c * ld + s], U[c * ld + s], a);
       gacc[c] = a;
@@ -308,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
         for (int j = 0; j < NB; ++j) {
           const int c = c0 + j * m.G;
           if (c < C) {
-            const float wc = w[c];
+            const float wc = w ? w[c] : 1.f;
             float o0[VW], o1[VW];
 #pragma unroll
             for (int k = 0; k < VW; ++k) {
@@ -331,7 +346,8 @@ __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
     }
     __syncthreads();  // U and D are reused by the next tile
   }
-  for (int c = t; c < C; c += kThreads) dw_part[wg * C + c] = gacc[c];
+  if (dw_part)
+    for (int c = t; c < C; c += kThreads) dw_part[wg * C + c] = gacc[c];
 }
 
 // dw[c] = sum over the partial rows: a workgroup takes 64 channels, its four
@@ -358,7 +374,7 @@ __global__ __launch_bounds__(kThreads) void chnorm_dw_reduce_kernel(const float*
 
 size_t fwd_lds(int C, int TS, int VW) { return (size_t(C) * (TS + 1) + size_t(kThreads) * VW + TS) * 4; }
 size_t bwd_lds(int C, int TS, int VW) {
-  return (size_t(C) * (TS + 1) * 2 + C + size_t(kThreads) * VW + 2 * TS) * 4;
+  return (size_t(C) * (TS + 1) * 2 + C + size_t(kThreads) * VW + 3 * TS) * 4;
 }
 
 constexpr size_t kLdsPreferred = 64 * 1024;  // leaves room for two or more workgroups per CU
@@ -408,49 +424,51 @@ void allow_lds(K* kernel, size_t lds) {
 
 template <int DT, int VW>
 void launch_fwd_vw(const void* y, const void* v, const float* w, void* out, int64_t B, int C, int64_t S, int TS,
-                   float eps, int gated, int act, int out_blh, hipStream_t st) {
+                   float eps, int gated, int act, int out_blh, int l2, hipStream_t st) {
   using T = typename Elem<DT>::T;
   const int64_t tpb = ceil_div(S, int64_t(TS)), nt = B * tpb;
   const size_t lds = fwd_lds(C, TS, VW);
   allow_lds(&chnorm_fwd_kernel<DT, VW>, lds);
   hipLaunchKernelGGL((chnorm_fwd_kernel<DT, VW>), dim3(unsigned(nt)), dim3(kThreads), lds, st, (const T*)y,
-                     (const T*)v, w, (T*)out, C, S, TS, tpb, nt, eps, gated, act, out_blh);
+                     (const T*)v, w, (T*)out, C, S, TS, tpb, nt, eps, gated, act, out_blh, l2);
 }
 
 template <int DT>
 void launch_fwd(const void* y, const void* v, const float* w, void* out, int64_t B, int C, int64_t S, float eps,
-                int gated, int act, int out_blh, hipStream_t st) {
+                int gated, int act, int out_blh, hipStream_t st, int l2 = 0) {
   constexpr int VW = 16 / int(sizeof(typename Elem<DT>::T));
   const int TS = pick_ts(C, false);
   if (use_vec(VW, C, S, TS, {y, v, out}))
-    launch_fwd_vw<DT, VW>(y, v, w, out, B, C, S, TS, eps, gated, act, out_blh, st);
+    launch_fwd_vw<DT, VW>(y, v, w, out, B, C, S, TS, eps, gated, act, out_blh, l2, st);
   else
-    launch_fwd_vw<DT, 1>(y, v, w, out, B, C, S, TS, eps, gated, act, out_blh, st);
+    launch_fwd_vw<DT, 1>(y, v, w, out, B, C, S, TS, eps, gated, act, out_blh, l2, st);
 }
 
 template <int DT, int VW>
 void launch_bwd_vw(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv, float* part,
-                   const BwdPlan& p, int C, int64_t S, float eps, int gated, int act, int out_blh, hipStream_t st) {
+                   const BwdPlan& p, int C, int64_t S, float eps, int gated, int act, int out_blh, int l2,
+                   hipStream_t st) {
   using T = typename Elem<DT>::T;
   const size_t lds = bwd_lds(C, p.TS, VW);
   allow_lds(&chnorm_bwd_kernel<DT, VW>, lds);
   hipLaunchKernelGGL((chnorm_bwd_kernel<DT, VW>), dim3(unsigned(p.nwg)), dim3(kThreads), lds, st, (const T*)dout,
                      (const T*)y, (const T*)v, w, (T*)dy, (T*)dv, part, C, S, p.TS, p.tiles_per_b, p.ntiles, eps,
-                     gated, act, out_blh);
+                     gated, act, out_blh, l2);
 }
 
 template <int DT>
 void launch_bwd(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv, float* dw,
                 float* part, const BwdPlan& p, int64_t B, int C, int64_t S, float eps, int gated, int act,
-                int out_blh, hipStream_t st) {
+                int out_blh, hipStream_t st, int l2 = 0) {
   (void)B;
   constexpr int VW = 16 / int(sizeof(typename Elem<DT>::T));
   if (use_vec(VW, C, S, p.TS, {dout, y, v, dy, dv}))
-    launch_bwd_vw<DT, VW>(dout, y, v, w, dy, dv, part, p, C, S, eps, gated, act, out_blh, st);
+    launch_bwd_vw<DT, VW>(dout, y, v, w, dy, dv, part, p, C, S, eps, gated, act, out_blh, l2, st);
   else
-    launch_bwd_vw<DT, 1>(dout, y, v, w, dy, dv, part, p, C, S, eps, gated, act, out_blh, st);
-  hipLaunchKernelGGL(chnorm_dw_reduce_kernel, dim3(unsigned(ceil_div(int64_t(C), int64_t(64)))),
-                     dim3(kThreads), 0, st, (const float*)part, dw, C, p.nwg);
+    launch_bwd_vw<DT, 1>(dout, y, v, w, dy, dv, part, p, C, S, eps, gated, act, out_blh, l2, st);
+  if (dw)
+    hipLaunchKernelGGL(chnorm_dw_reduce_kernel, dim3(unsigned(ceil_div(int64_t(C), int64_t(64)))),
+                       dim3(kThreads), 0, st, (const float*)part, dw, C, p.nwg);
 }
 
 int check_common(const char* who, int dtype, int64_t B, int C, int64_t S, float eps, int gated, int act) {
@@ -531,6 +549,58 @@ extern "C" int nsq_channel_rmsnorm_bwd(const void* dout, const void* y, const vo
   else
     launch_bwd<NSQ_DTYPE_F16>(dout, y, v, w, dy, dv, dw, part, p, B, int(C), S, eps, gated, act, out_channels_last,
                               st);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+extern "C" int nsq_channel_l2norm_fwd(const void* x, void* out, int dtype, int64_t B, int64_t C, int64_t S, float eps,
+                                      int out_channels_last, void* stream) {
+  using namespace nsq;
+  clear_error();
+  NSQ_CHECK_ARG(x && out, "channel_l2norm_fwd: null pointer argument");
+  NSQ_CHECK_ARG(C >= 1 && C <= 0x7fffffff, "channel_l2norm_fwd: C=%lld out of range", (long long)C);
+  if (int e = check_common("channel_l2norm_fwd", dtype, B, int(C), S, eps, 0, NSQ_GATE_IDENTITY)) return e;
+  const int TS = pick_ts(int(C), false);
+  if (TS == 0) {
+    set_error("channel_l2norm_fwd: C=%lld exceeds the LDS tile (C <= 7781)", (long long)C);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  NSQ_CHECK_ARG(B * ceil_div(S, int64_t(TS)) <= 0x7fffffff, "channel_l2norm_fwd: B*S too large for the grid");
+  hipStream_t st = (hipStream_t)stream;
+  const int oc = out_channels_last;
+  if (dtype == NSQ_DTYPE_F32)
+    launch_fwd<NSQ_DTYPE_F32>(x, nullptr, nullptr, out, B, int(C), S, eps, 0, NSQ_GATE_IDENTITY, oc, st, 1);
+  else if (dtype == NSQ_DTYPE_BF16)
+    launch_fwd<NSQ_DTYPE_BF16>(x, nullptr, nullptr, out, B, int(C), S, eps, 0, NSQ_GATE_IDENTITY, oc, st, 1);
+  else
+    launch_fwd<NSQ_DTYPE_F16>(x, nullptr, nullptr, out, B, int(C), S, eps, 0, NSQ_GATE_IDENTITY, oc, st, 1);
+  NSQ_CHECK_LAUNCH();
+  return NSQ_OK;
+}
+
+extern "C" int nsq_channel_l2norm_bwd(const void* dout, const void* x, void* dx, int dtype, int64_t B, int64_t C,
+                                      int64_t S, float eps, int out_channels_last, void* stream) {
+  using namespace nsq;
+  clear_error();
+  NSQ_CHECK_ARG(dout && x && dx, "channel_l2norm_bwd: null pointer argument");
+  NSQ_CHECK_ARG(C >= 1 && C <= 0x7fffffff, "channel_l2norm_bwd: C=%lld out of range", (long long)C);
+  if (int e = check_common("channel_l2norm_bwd", dtype, B, int(C), S, eps, 0, NSQ_GATE_IDENTITY)) return e;
+  const BwdPlan p = bwd_plan(B, int(C), S);
+  if (p.TS == 0) {
+    set_error("channel_l2norm_bwd: C=%lld exceeds the LDS tiles (C <= 3536)", (long long)C);
+    return NSQ_ERR_UNSUPPORTED;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const int oc = out_channels_last;
+  if (dtype == NSQ_DTYPE_F32)
+    launch_bwd<NSQ_DTYPE_F32>(dout, x, nullptr, nullptr, dx, nullptr, nullptr, nullptr, p, B, int(C), S, eps, 0,
+                              NSQ_GATE_IDENTITY, oc, st, 1);
+  else if (dtype == NSQ_DTYPE_BF16)
+    launch_bwd<NSQ_DTYPE_BF16>(dout, x, nullptr, nullptr, dx, nullptr, nullptr, nullptr, p, B, int(C), S, eps, 0,
+                               NSQ_GATE_IDENTITY, oc, st, 1);
+  else
+    launch_bwd<NSQ_DTYPE_F16>(dout, x, nullptr, nullptr, dx, nullptr, nullptr, nullptr, p, B, int(C), S, eps, 0,
+                              NSQ_GATE_IDENTITY, oc, st, 1);
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;
 }

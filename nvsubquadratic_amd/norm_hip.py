@@ -26,8 +26,10 @@ from torch.library import custom_op
 
 from . import _lib
 from .gated_fftconv_hip import gate_code
+from .layout import channels_first_contiguous
 
-__all__ = ["HipRMSNormChannelFirst", "channel_rmsnorm", "gated_channel_rmsnorm", "hyena_output_norm"]
+__all__ = ["HipL2Norm", "HipRMSNormChannelFirst", "channel_l2norm", "channel_rmsnorm", "gated_channel_rmsnorm",
+           "hyena_output_norm"]
 
 
 def _flat(t: torch.Tensor) -> torch.Tensor:
@@ -171,3 +173,105 @@ class HipRMSNormChannelFirst(torch.nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return channel_rmsnorm(x, self.weight, self.eps)
+
+
+# ---------------------------------------------------------------------------
+# QK-norm: L2 normalisation over channels (nvsubquadratic/utils/qk_norm.py L2Norm, the q / k norm of
+# modules/hyena_nd.py:529-543), one HIP pass each way (nsq_channel_l2norm_fwd / _bwd)
+# ---------------------------------------------------------------------------
+@custom_op("nsq_hip::channel_l2norm", mutates_args=())
+def channel_l2norm_op(x: torch.Tensor, eps: float, channels_last: bool) -> torch.Tensor:
+    """x ``[B, C, S]`` contiguous -> ``x / max(||x||_C, eps)`` as ``[B, S, C]`` (channels_last) or ``[B, C, S]``."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, C, S = x.shape
+    out = torch.empty((B, S, C) if channels_last else (B, C, S), dtype=x.dtype, device=x.device)
+    _lib.check(lib.nsq_channel_l2norm_fwd(x.data_ptr(), out.data_ptr(), _lib.dtype_code(x.dtype), B, C, S,
+                                          float(eps), int(channels_last), _lib.stream_ptr(x.device)))
+    return out
+
+
+@channel_l2norm_op.register_fake
+def _(x, eps, channels_last):
+    B, C, S = x.shape
+    return x.new_empty((B, S, C) if channels_last else (B, C, S))
+
+
+@custom_op("nsq_hip::channel_l2norm_backward", mutates_args=())
+def channel_l2norm_backward_op(dout: torch.Tensor, x: torch.Tensor, eps: float, channels_last: bool) -> torch.Tensor:
+    """dx ``[B, C, S]`` for dout in the forward output's layout."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, C, S = x.shape
+    dx = torch.empty_like(x)
+    _lib.check(lib.nsq_channel_l2norm_bwd(dout.data_ptr(), x.data_ptr(), dx.data_ptr(), _lib.dtype_code(x.dtype), B,
+                                          C, S, float(eps), int(channels_last), _lib.stream_ptr(x.device)))
+    return dx
+
+
+@channel_l2norm_backward_op.register_fake
+def _(dout, x, eps, channels_last):
+    return torch.empty_like(x)
+
+
+def _l2_setup(ctx, inputs, output):
+    x, eps, channels_last = inputs
+    ctx.save_for_backward(x)
+    ctx.cfg = (eps, channels_last)
+
+
+def _l2_backward(ctx, gout):
+    (x,) = ctx.saved_tensors
+    eps, channels_last = ctx.cfg
+    return channel_l2norm_backward_op(gout.contiguous(), x, eps, channels_last), None, None
+
+
+channel_l2norm_op.register_autograd(_l2_backward, setup_context=_l2_setup)
+
+
+def channel_l2norm(x: torch.Tensor, eps: float = 1e-12, channels_last_out: bool = False) -> torch.Tensor:
+    """``F.normalize(x, p=2, dim=1, eps)`` for ``x [B, C, *spatial]`` (fp32 / bf16 / fp16) in one pass; with
+    ``channels_last_out`` the result comes back as ``[B, *spatial, C]`` (normalised over its last axis)."""
+    if x.dim() < 2:
+        raise ValueError(f"expected [B, C, *spatial], got shape {tuple(x.shape)}")
+    shape = x.shape
+    if torch.is_grad_enabled() and x.requires_grad:
+        C, S = shape[1], max(1, x.numel() // max(1, shape[0] * shape[1]))
+        if _lib.get_lib().nsq_channel_rmsnorm_bwd_workspace_bytes(shape[0], C, S) == 0:  # same LDS tiles
+            raise NotImplementedError(f"fft_backend='hip' channel L2 norm backward: C={C} exceeds the backward's "
+                                      f"LDS tiles (C <= 3536); the forward alone takes C <= 7781")
+    out = channel_l2norm_op(_flat(x), float(eps), bool(channels_last_out))
+    if channels_last_out:
+        return out.view(shape[0], *shape[2:], shape[1])
+    return out.view(shape)
+
+
+class HipL2Norm(torch.nn.Module):
+    """Drop-in for ``L2Norm`` (``nvsubquadratic/utils/qk_norm.py``): ``F.normalize(x, p=2, dim=self.dim, eps)``
+    with no parameters, and the same ``channels_first`` duck type (``dim == 1``) the Hyena operator uses to pick the
+    layout (``hyena_nd.py:529-543``).  ``dim = 1`` normalises ``[B, C, *spatial]`` in place of layout; ``dim = -1``
+    normalises ``[..., C]``: a channels-first tensor viewed channels-last (the Hyena operator's ``movedim``) is read
+    as it lies, a contiguous channels-last one is moved channels-first once (``nsq_batched_transpose``); either way
+    the result comes back ``[..., C]`` from the kernel's channels-last store."""
+
+    def __init__(self, dim: int = -1, eps: float = 1e-12):
+        super().__init__()
+        self.dim = dim
+        self.eps = eps
+
+    @property
+    def channels_first(self) -> bool:
+        return self.dim == 1
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        d = self.dim % x.dim()
+        if d == 1 and x.dim() >= 2:
+            return channel_l2norm(x, self.eps)
+        if d == x.dim() - 1 and x.dim() >= 2:
+            xc = channels_first_contiguous(x.movedim(-1, 1))
+            return channel_l2norm(xc, self.eps, channels_last_out=True)
+        raise NotImplementedError(f"fft_backend='hip' L2Norm: dim={self.dim} on a {x.dim()}-d tensor (the HIP kernel "
+                                  f"normalises the channel axis: dim 1 or -1)")
+
+    def extra_repr(self) -> str:
+        return f"dim={self.dim}, eps={self.eps}"

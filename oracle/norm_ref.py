@@ -12,6 +12,12 @@ Restates, with torch on the CPU, the reference's op sequence at its norm sites:
 The backward is torch autograd through that sequence.  Pinned in ``tests/test_oracle_norm.py`` by a closed form of
 the normalised values, scale invariance, finite-difference gradients (float64 gradcheck) and the orthogonality of
 the input gradient to ``u`` at ``eps = 0``.
+
+The QK-norm (``nvsubquadratic/utils/qk_norm.py``, ``L2Norm``: ``F.normalize(x, p=2, dim, eps)``) is restated as the
+norm over ``dim`` accumulated in float32 and rounded to the input dtype (torch's vector norm of a 16-bit tensor),
+clamped at ``eps``, and ``x / n`` in the input dtype; pinned against torch's own ``F.normalize`` (a library routine),
+a closed form (3, 4) -> (0.6, 0.8), the clamp (a vector shorter than eps comes out as ``x / eps``) and float64
+gradcheck.
 """
 
 from __future__ import annotations
@@ -20,7 +26,7 @@ from typing import Optional
 
 import torch
 
-__all__ = ["gated_channel_rmsnorm_ref"]
+__all__ = ["gated_channel_rmsnorm_ref", "l2norm_ref"]
 
 _ACTS = {0: lambda t: t, 1: torch.sigmoid, 2: torch.nn.functional.silu}
 
@@ -36,3 +42,11 @@ def gated_channel_rmsnorm_ref(y: torch.Tensor, v: Optional[torch.Tensor], weight
     xf = xf * torch.rsqrt(var + eps)                         # rms_norm.py:76
     out = (weight * xf).to(dt)                               # rms_norm.py:77
     return out if channels_last else out.movedim(-1, 1)
+
+
+def l2norm_ref(x: torch.Tensor, dim: int = 1, eps: float = 1e-12) -> torch.Tensor:
+    """``F.normalize(x, p=2, dim=dim, eps=eps)`` restated step by step (``qk_norm.py:109``)."""
+    xf = x.to(torch.float32) if x.dtype != torch.float64 else x
+    n = torch.linalg.vector_norm(xf, dim=dim, keepdim=True).to(x.dtype)  # torch's norm returns the input dtype
+    n = n.clamp_min(eps)
+    return (xf / n.to(xf.dtype)).to(x.dtype)

@@ -147,3 +147,75 @@ def test_opcheck():
     w = torch.rand(16, device="cuda", requires_grad=True)
     torch.library.opcheck(N.gated_channel_rmsnorm_op, (y, v, w, 1e-6, 1, True))
     torch.library.opcheck(N.gated_channel_rmsnorm_op, (y, None, w, 1e-6, 0, False))
+
+
+# --- QK-norm: L2 normalisation over channels (L2Norm, F.normalize) ----------------------------------------------
+def _l2_case(B, C, spatial, dtype, channels_last, eps=1e-12, seed=0, tiny=False):
+    from oracle.norm_ref import l2norm_ref
+
+    print(f"l2 case B={B} C={C} S={spatial} {dtype} channels_last={channels_last} eps={eps}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, C, *spatial, generator=g)
+    if tiny:  # every other position far below eps: the clamped branch
+        x[..., ::2] *= 1e-6
+    x = x.to(dtype)
+    xd = x.cuda().requires_grad_()
+    out = N.channel_l2norm(xd, eps, channels_last_out=channels_last)
+    gout = torch.randn(out.shape, generator=g).to(dtype)
+    out.backward(gout.cuda())
+    x64 = x.double().requires_grad_()
+    ref = l2norm_ref(x64, 1, eps)
+    ref = ref.movedim(1, -1) if channels_last else ref
+    ref.backward(gout.double())
+    assert out.shape == ref.shape and out.dtype == dtype
+    tol = {torch.float32: 1e-6, torch.bfloat16: 5e-3, torch.float16: 1e-3}[dtype]
+    assert rel_l2(ref, out) < tol
+    if C == 1:  # out = sign(x): the exact input gradient is zero; the kernel's is rounding noise of dout / |x|
+        scale = float((gout.double() / x64.detach().reshape(gout.shape) if not channels_last else
+                       gout.double() / x64.detach().movedim(1, -1)).abs().max())
+        assert float(xd.grad.double().cpu().abs().max()) < 10 * tol * scale
+    else:
+        assert rel_l2(x64.grad, xd.grad) < tol * 4
+    if dtype != torch.float32:  # the same dtype's restatement (its norm rounded as torch rounds it)
+        xr = x.clone().requires_grad_()
+        r2 = l2norm_ref(xr, 1, eps)
+        r2 = r2.movedim(1, -1) if channels_last else r2
+        assert rel_l2(r2.float(), out.float()) < tol
+
+
+@pytest.mark.parametrize("channels_last", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,C,spatial", [(2, 384, (16, 16)), (3, 5, (7, 9)), (1, 257, (33,)), (2, 1000, (3, 5)),
+                                         (1, 1, (64,)), (4, 64, (128, 128))])
+def test_l2norm_over_channels(B, C, spatial, dtype, channels_last):
+    _l2_case(B, C, spatial, dtype, channels_last)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_l2norm_clamped_positions(dtype):
+    # eps 1e-3 against norms of ~1e-5 at every other position: out = x / eps there, dx = dout / eps
+    _l2_case(2, 48, (8, 10), dtype, False, eps=1e-3, tiny=True)
+
+
+def test_hip_l2norm_module_layouts():
+    """HipL2Norm (L2Norm's interface): dim=1 on [B, C, *S]; dim=-1 on a channels-first tensor viewed channels-last
+    (the Hyena operator's movedim) and on a contiguous channels-last tensor; all equal torch's F.normalize."""
+    torch.manual_seed(1)
+    x = torch.randn(2, 96, 12, 10, device="cuda")
+    m1, m2 = N.HipL2Norm(dim=1), N.HipL2Norm()
+    assert m1.channels_first and not m2.channels_first
+    ref = torch.nn.functional.normalize(x, dim=1)
+    assert rel_l2(ref, m1(x)) < 1e-6
+    v = x.movedim(1, -1)
+    out = m2(v)
+    assert out.shape == v.shape and rel_l2(torch.nn.functional.normalize(v, dim=-1), out) < 1e-6
+    c = v.contiguous()
+    assert rel_l2(torch.nn.functional.normalize(c, dim=-1), m2(c)) < 1e-6
+    with pytest.raises(NotImplementedError):
+        N.HipL2Norm(dim=2)(x)
+
+
+def test_l2norm_opcheck():
+    x = torch.randn(2, 40, 33, device="cuda", requires_grad=True)
+    torch.library.opcheck(N.channel_l2norm_op, (x, 1e-12, True))
+    torch.library.opcheck(N.channel_l2norm_op, (x, 1e-12, False))

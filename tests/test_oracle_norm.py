@@ -4,9 +4,10 @@ as torch's own sigmoid / silu, and the channels-first layout as the channels-las
 
 import math
 
+import pytest
 import torch
 
-from oracle.norm_ref import gated_channel_rmsnorm_ref
+from oracle.norm_ref import gated_channel_rmsnorm_ref, l2norm_ref
 
 
 def test_closed_form_ramp():
@@ -60,3 +61,29 @@ def test_input_gradient_orthogonal_to_u_at_zero_eps():
     out = gated_channel_rmsnorm_ref(u, None, w, 0.0)
     (du,) = torch.autograd.grad(out, u, torch.randn_like(out))
     assert (du * u).sum(1).abs().max() < 1e-12
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
+def test_l2norm_restatement_matches_torch_normalize(dtype):
+    """The QK-norm restatement equals torch's F.normalize (the reference's L2Norm body) on every dtype."""
+    torch.manual_seed(0)
+    x = (torch.randn(3, 40, 7, 5) * 3).to(dtype)
+    for dim in (1, -1):
+        assert torch.equal(l2norm_ref(x, dim), torch.nn.functional.normalize(x, p=2.0, dim=dim))
+
+
+def test_l2norm_closed_forms_and_clamp():
+    x = torch.tensor([[[3.0], [4.0]]], dtype=torch.float64)   # [B=1, C=2, S=1]
+    assert torch.allclose(l2norm_ref(x), torch.tensor([[[0.6], [0.8]]], dtype=torch.float64), rtol=0, atol=1e-15)
+    tiny = torch.full((1, 4, 1), 1e-5, dtype=torch.float64)   # ||x|| = 2e-5 < eps = 1e-3: x / eps
+    assert torch.allclose(l2norm_ref(tiny, eps=1e-3), tiny / 1e-3, rtol=1e-15, atol=0)
+    y = torch.randn(2, 9, 6, dtype=torch.float64)
+    assert torch.allclose(torch.linalg.vector_norm(l2norm_ref(y), dim=1), torch.ones(2, 6, dtype=torch.float64))
+    assert torch.allclose(l2norm_ref(5.0 * y), l2norm_ref(y), rtol=1e-14, atol=1e-14)
+
+
+def test_l2norm_gradcheck_float64():
+    y = torch.randn(2, 5, 3, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda t: l2norm_ref(t, 1, 1e-12), (y,))
+    small = (torch.randn(1, 3, 2, dtype=torch.float64) * 1e-4).requires_grad_(True)  # clamped branch
+    assert torch.autograd.gradcheck(lambda t: l2norm_ref(t, 1, 1e-2), (small,))
