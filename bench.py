@@ -9,7 +9,7 @@ call on inputs resident in HBM, with outputs and workspace preallocated.
 Prints one JSON line with the driver's fields plus:
   roofline     -- algorithmic HBM bytes of the fwd+bwd pair / its measured time,
                   against MI355X's 8 TB/s (the path is HBM-bound by definition
-                  of the metric; see DESIGN.md for the per-kernel view);
+                  of the metric);
   cpu_baseline -- the CPU oracle (float32 torch.fft restatement of the
                   reference path, autograd backward) on a bounded channel
                   sample of the same workload, on this host's cores.
@@ -17,7 +17,7 @@ Prints one JSON line with the driver's fields plus:
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --workload cfg1|cfg2|cfg4|cfg5   (the other benchmark
            configurations, for the per-config report; same JSON fields, value =
-           algorithmic GB/s of the phase BASELINE.md quotes for that config)
+           algorithmic GB/s of the phase the reference's benchmark quotes for that config)
        python bench.py --workload cfg2-fwd-bwd   (config 2's block with its
            backward, report-only)
        python bench.py --workload cfg4-circular|well-rb   (periodic and
@@ -25,6 +25,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
            the rayleigh_benard Well config's layer, x periodic / y zero-padded)
        python bench.py --workload hyena-gated   (report-only: the Hyena gates
            fused into the causal conv, with the unfused composition's time)
+       python bench.py --workload siren-conv-1d    (report-only: SIREN filter + causal conv fwd+bwd at config
+                                                    3's shape with the filter never formed, and the composition)
        python bench.py --workload hyena-norm       (report-only: the Hyena output gate + RMSNorm over
                                                     channels + channels-last layout, fwd+bwd, cfg4 shape)
        python bench.py --workload hyena-gated-2d   (report-only: the gated 2D
@@ -227,7 +229,7 @@ def _time_steps(step, steps: int, warmup: int) -> list[float]:
     return [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
 
 
-def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None:
+def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare: bool = True) -> None:
     """Configs 1, 2, 4, 5 of the benchmark set (inputs resident in HBM)."""
     from nvsubquadratic_amd import causal_conv1d_hip as CC
     from nvsubquadratic_amd import fftconv_hip as F
@@ -333,7 +335,7 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
                 xg.grad = kg.grad = sg.grad = None
                 fn(xg, kg, sg).backward(g)
     elif name == "hyena-gated":
-        # report-only (row F2): the Hyena layer's gated long conv, fused, against the same layer composed of torch
+        # report-only: the Hyena layer's gated long conv, fused, against the same layer composed of torch
         # gates around the HIP conv (hyena_nd.py:546,558,570), fwd+bwd
         import torch.nn.functional as Fn
 
@@ -349,8 +351,9 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
         phase, dtype = "fwd+bwd", "f32"
         nbytes = algorithmic_bytes_gated(B, Ch, L, L, 2)
         desc = ("hyena-gated: gated causal FFT conv fwd+bwd (z = q silu(k), y = (conv(z) + s z) sigmoid(v)), "
-                "B=4 D=1024 L=8192 K=8192, bf16 I/O; forward gates fused into the conv's first and last passes, "
-                "backward gates as elementwise kernels around the conv adjoint")
+                "B=4 D=1024 L=8192 K=8192, bf16 I/O; gates as elementwise HIP kernels around the fused conv kernels "
+                "both ways (at 2^25 elements they beat the gated forward kernel, which the library keeps for calls "
+                "below 2^22 elements)")
 
         def clear():
             for t in (q, kk, v, w, sh):
@@ -365,14 +368,10 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
             z = q * Fn.silu(kk)
             (F.causal_fftconv1d_bhl(z, w, sh) * torch.sigmoid(v)).backward(g)
 
-        def step_fused_bwd():
-            clear()
-            hyena_gated_causal_fftconv1d_bhl(q, kk, v, w, sh, "silu", "sigmoid", fuse_backward_gates=True).backward(g)
-
-        extra["unfused_ms_per_step"] = round(statistics.mean(_time_steps(step_unfused, steps, warmup)), 4)
-        extra["fused_backward_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_fused_bwd, steps, warmup)), 4)
+        if compare:
+            extra["unfused_ms_per_step"] = round(statistics.mean(_time_steps(step_unfused, steps, warmup)), 4)
     elif name == "hyena-gated-2d":
-        # report-only (row F2, 2D): the gates inside the N-d conv's first and last passes, against torch's gate ops
+        # report-only (2D): the gates inside the N-d conv's first and last passes, against torch's gate ops
         # around the same HIP conv (which keeps z for the backward) and the conv alone, fwd+bwd at cfg4's shape
         import torch.nn.functional as Fn
 
@@ -406,10 +405,11 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
             clear()
             F.fftconv2d_bhl(q, w, sh).backward(g)
 
-        extra["torch_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_torch_gates, steps, warmup)), 4)
-        extra["conv_only_ms_per_step"] = round(statistics.mean(_time_steps(step_conv_only, steps, warmup)), 4)
+        if compare:
+            extra["torch_gates_ms_per_step"] = round(statistics.mean(_time_steps(step_torch_gates, steps, warmup)), 4)
+            extra["conv_only_ms_per_step"] = round(statistics.mean(_time_steps(step_conv_only, steps, warmup)), 4)
     elif name == "siren-1d":
-        # report-only (row F1): the SIREN filter of a long-context Hyena layer (kernels_nd.py:876, CKConvND's causal
+        # report-only: the SIREN filter of a long-context Hyena layer (kernels_nd.py:876, CKConvND's causal
         # half): HIP hidden stack + one readout GEMM, fwd+bwd, against the reference's torch layers on the same GPU
         import torch.nn.functional as Fn
 
@@ -444,9 +444,47 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
                 h = torch.sin(Fn.linear(h, w, b))
             Fn.linear(h, wo, bo).t().backward(g)
 
-        extra["torch_layers_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
+        if compare:
+            extra["torch_layers_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
+    elif name == "siren-conv-1d":
+        # report-only: a long-context Hyena layer's SIREN filter and causal conv together (CKConvND's causal path,
+        # ckconv_nd.py:1149-1164, identity mask) at config 3's shape, the filter never formed
+        # (siren_causal_fftconv1d), against the HIP composition that forms it (siren_filter, then the conv)
+        from nvsubquadratic_amd.fftconv_hip import causal_fftconv1d_bhl
+        from nvsubquadratic_amd.siren_hip import siren_causal_fftconv1d, siren_filter, siren_grid
+
+        B, H, L, E, HD, nh = 1, 4096, 262144, 32, 32, 2
+        grid = siren_grid((L,), (1.0,), (L,), dev)[L - 1:].contiguous()
+        gen_c = torch.Generator().manual_seed(0)
+        mk = lambda *shape, b: ((torch.rand(*shape, generator=gen_c) * 2 - 1) * b).to(dev).requires_grad_(True)  # noqa
+        w0, b0 = mk(E, 1, b=2 * 3.14159 * 10.0), mk(E, b=1.0)
+        hw = [mk(HD, E, b=(6 / E) ** 0.5)] + [mk(HD, HD, b=(6 / HD) ** 0.5) for _ in range(nh - 1)]
+        hb = [mk(HD, b=1.0) for _ in range(nh)]
+        wo, bo = mk(H, HD, b=(6 / HD) ** 0.5 / 512), mk(H, b=0.1)
+        x = torch.randn(B, H, L, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+        sh = torch.randn(H, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+        g = torch.randn(B, H, L, device=dev, generator=gen).to(torch.bfloat16)
+        phase, dtype = "fwd+bwd", "f32"
+        nbytes = 5 * B * H * L * 2  # x, y (forward); g, x, gx (backward), bf16; the filter is not an operand
+        desc = ("siren-conv-1d: SIREN filter (pos-emb 32, 2 hidden layers of 32) and causal FFT conv fwd+bwd, B=1 "
+                "H=4096 L=K=262144, bf16 I/O, fp32 arithmetic; the filter [H, L] and its gradient never formed")
+
+        def clear():
+            for t in (w0, b0, *hw, *hb, wo, bo, x, sh):
+                t.grad = None
+
+        def step():
+            clear()
+            siren_causal_fftconv1d(x, grid, w0, b0, hw, hb, wo, bo, sh).backward(g)
+
+        def step_composed():
+            clear()
+            causal_fftconv1d_bhl(x, siren_filter(grid, w0, b0, hw, hb, wo, bo), sh).backward(g)
+
+        if compare:
+            extra["composed_ms_per_step"] = round(statistics.mean(_time_steps(step_composed, steps, warmup)), 4)
     elif name == "hyena-norm":
-        # report-only (row F2, norms): the Hyena output tail y * sigmoid(v) -> RMSNorm over channels -> channels-last
+        # report-only (norms): the Hyena output tail y * sigmoid(v) -> RMSNorm over channels -> channels-last
         # (hyena_nd.py:570-583) as one HIP pass per direction, against the reference's torch ops on the same GPU
         from nvsubquadratic_amd.norm_hip import hyena_output_norm
 
@@ -476,7 +514,8 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True) -> None
             out = (w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6))).to(u.dtype)
             out.contiguous().backward(g)
 
-        extra["torch_ops_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
+        if compare:
+            extra["torch_ops_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
     else:
         raise SystemExit(f"unknown workload {name}")
     ms_list = _time_steps(step, steps, warmup)
@@ -506,18 +545,21 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-compare", action="store_true",
+                    help="report-only workloads: skip the comparison variants (torch ops, unfused compositions)")
     ap.add_argument("--cpu-channels", type=int, default=1024)
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
                                                               "cfg4-circular", "well-rb", "hyena-gated",
-                                                              "hyena-gated-2d", "siren-1d", "hyena-norm"])
+                                                              "hyena-gated-2d", "siren-1d", "siren-conv-1d",
+                                                              "hyena-norm"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU only: the causal FFT conv is depthwise and shards over channels with no "
-            "communication (see DESIGN.md); multi-GPU runs are not part of this build.",
+            "communication; multi-GPU runs are not part of this build.",
             file=sys.stderr,
         )
         sys.exit(2)
@@ -525,7 +567,7 @@ def main() -> None:
         copy_calibration()
         return
     if args.workload != "cfg3":
-        other_workload(args.workload, args.steps, args.warmup, cpu=not args.no_cpu)
+        other_workload(args.workload, args.steps, args.warmup, cpu=not args.no_cpu, compare=not args.no_compare)
         return
 
     from nvsubquadratic_amd import _lib

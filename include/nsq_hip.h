@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 13
+#define NSQ_ABI_VERSION 14
 
 enum {
   NSQ_OK = 0,
@@ -162,7 +162,7 @@ int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const 
                             unsigned periodic, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Hyena-gated causal 1D FFT convolution (row F2 of the build plan): the long conv
+ * Hyena-gated causal 1D FFT convolution: the long conv
  * with the gates around it fused into its first and last passes,
  *   z = q * act1(k_gate);  y1 = causal_conv(z; k) + shortcut * z;  y = y1 * act2(v),
  * as nvsubquadratic/modules/hyena_nd.py:546 (first gate), :558 (CKConvND global
@@ -174,12 +174,11 @@ int nsq_mixed_fftconv1d_bwd(const void* g, const void* x, const float* k, const 
  * y1 != NULL (the backward needs it).  The backward returns dq, dk_gate, dv, gk, gs.
  * Forward: FFT lengths <= 16384 run one fused kernel (no workspace); longer ones
  * run elementwise gate kernels around the multi-kernel conv.  Backward: the
- * elementwise gate kernels around the plain conv adjoint, or, with fuse_gates = 1
- * and FFT lengths <= 16384, one fused kernel (no workspace).  The fused adjoint
- * carries five extra operand streams through a latency-bound kernel and measured
- * slower on MI355X at B=4 D=1024 L=8192 (see the bench's hyena-gated line), so 0
- * is the default of the Python layer.  Workspace: nsq_gated_fftconv1d_causal_
- * workspace_bytes; the unfused paths need 16-byte aligned tensors.
+ * elementwise gate kernels around the plain conv adjoint (a one-kernel gated
+ * adjoint carries five extra operand streams through a latency-bound kernel and
+ * measured slower on MI355X, so it is not built); fuse_gates is reserved and must
+ * be 0.  Workspace: nsq_gated_fftconv1d_causal_workspace_bytes; the backward and
+ * the multi-kernel forward need 16-byte aligned tensors.
  * No counterpart in the reference: there the gates are separate torch ops
  * around fft_causal_conv1d.
  */
@@ -200,7 +199,7 @@ int nsq_gated_fftconv1d_causal_bwd(const void* g, const void* q, const void* k_g
                                    void* stream);
 
 /*
- * Hyena-gated 2D/3D FFT convolution (row F2 for the N-d layers,
+ * Hyena-gated 2D/3D FFT convolution (the N-d layers,
  * nvsubquadratic/modules/hyena_nd.py:546-570 around the CKConvND global conv,
  * ckconv_nd.py:1054-1062): z = q act1(k_gate), y1 = conv_nd(z) + shortcut z,
  * y = y1 act2(v), with the N-d conv of nsq_mixed_fftconv_nd_fwd (periodic mask,
@@ -405,6 +404,45 @@ int nsq_siren_mlp_bwd(const float* gact, int64_t gact_stride_j, int64_t gact_str
                       int d, const float* w0, const float* b0, int E, const float* wh, const float* bh, int nh, int HD,
                       float* gw0, float* gb0, float* gwh, float* gbh, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/* Causal 1D FFT convolution with a SIREN filter that is never formed (ABI 14):
+ * CKConvND's causal path (nvsubquadratic/modules/ckconv_nd.py:1149-1164 with an
+ * identity mask: the SIRENKernelND filter k = W_out a + b_out of kernels_nd.py:
+ * 1181-1189 at its causal points, then the causal conv of ops/fftconv.py:546-600,
+ * the job nsq_siren_readout_fwd + nsq_fftconv1d_causal_fwd do with k in HBM):
+ *   y[b,h,:] = causal_conv(x[b,h,:]; k_h) + shortcut[h] x[b,h,:],
+ *   k_h[g] = sum_{j<HD} wout[h][j] act[j][g] + bout[h],  g < K,
+ * for act [HD + 1][lda] (nsq_siren_mlp_fwd's output: row HD is the ones row and
+ * must hold ones), wout [H][HD], bout [H] or NULL, x / y / g / gx [B, H, L] in
+ * `dtype`, shortcut [H] or NULL.  The 4-step plan's column pass is linear, so
+ * the forward transforms the HD + 1 activation rows once and forms each
+ * channel's filter transform from them (fp32, fixed order); the backward reads
+ * the filter gradient's spectrum once for gwout, gbout and wout^T times it (the
+ * inverse column pass's adjoint is the forward one / N) and inverse-transforms
+ * only those HD rows into gact [HD][K] (row stride K; feeds nsq_siren_mlp_bwd
+ * with gact_stride_j = K, gact_stride_g = 1).  gs [H] (fp32, required with a
+ * shortcut) is the shortcut gradient; gbout may be NULL.  The gradient products
+ * run as in nsq_siren_readout_bwd (bf16-split matrix cores, fp32 accumulation,
+ * fixed-order sums).  Results equal the composition's to fp32 rounding.
+ * Takes the 4-step plan only: FFT lengths 2^15 .. 2^23 (L + K above 16384,
+ * K <= L + 1) with HD in {16, 32, 64}; other shapes return NSQ_ERR_UNSUPPORTED
+ * (the fused plan reads the filter: form it with nsq_siren_readout_fwd).
+ * Workspace (one size, both directions; 256-byte aligned): the forward leaves
+ * the transformed x, filter and activations there, and the backward with
+ * fwd_state = 1 starts from them (untouched since that forward); fwd_state = 0
+ * recomputes them.  No counterpart in the reference: there the filter is a
+ * torch tensor between the generator and the conv. */
+size_t nsq_siren_fftconv1d_causal_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, int HD);
+
+int nsq_siren_fftconv1d_causal_fwd(const void* x, const float* act, int64_t lda, const float* wout,
+                                   const float* bout, int HD, const void* shortcut, void* y, int dtype, int64_t B,
+                                   int64_t H, int64_t L, int64_t K, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
+int nsq_siren_fftconv1d_causal_bwd(const void* g, const void* x, const float* act, int64_t lda, const float* wout,
+                                   const float* bout, int HD, const void* shortcut, void* gx, float* gact,
+                                   float* gwout, float* gbout, float* gs, int dtype, int64_t B, int64_t H, int64_t L,
+                                   int64_t K, void* workspace, size_t workspace_bytes, int fwd_state, void* stream);
 
 /* FiLM-conditioned generator (ABI 12): kernels_nd.py:1165-1187 with the
  * KernelFiLMGenerator output of modules/film.py:75 (its MLP runs on the

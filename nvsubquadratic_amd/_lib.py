@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 13
+ABI_VERSION = 14
 NSQ_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/nsq_hip.h: the fixed scratch of nsq_causal_conv1d_bwd_noalloc
 
 
@@ -172,6 +172,14 @@ _SIGNATURES = {
          ctypes.c_float, _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
     ),
     "nsq_siren_readout_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_i64, _c_i64]),
+    "nsq_siren_fftconv1d_causal_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "nsq_siren_fftconv1d_causal_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_i64,
+                 _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p]),
+    "nsq_siren_fftconv1d_causal_bwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                 _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p,
+                 _c_size, _c_int, _c_void_p]),
     "nsq_siren_readout_bwd": (
         _c_int, [_c_void_p, _c_i64, _c_void_p, _c_i64, _c_void_p, _c_i64, _c_int, _c_i64, _c_i64, _c_void_p,
                  _c_void_p, _c_void_p, _c_void_p, _c_size, _c_void_p]),

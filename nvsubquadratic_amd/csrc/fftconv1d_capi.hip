@@ -192,7 +192,7 @@ static size_t gated_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t K, 
                                     int direction) {
   Plan1D p;
   if (!make_plan(L, K, p) || !valid_dtype(dtype)) return 0;
-  if (p.fused && direction == NSQ_DIR_FWD) return 0;  // one fused kernel
+  if (gates_fused_1d(p, B * H * L) && direction == NSQ_DIR_FWD) return 0;  // one gated kernel
   const size_t conv = round256(causal_workspace_bytes(B, H, L, K, kbatch, direction));
   const size_t es = dtype == NSQ_DTYPE_F32 ? 4 : 2;
   return conv + size_t(direction == NSQ_DIR_BWD ? 3 : 2) * round256(size_t(B * H * L) * es);
@@ -411,13 +411,14 @@ int nsq_gated_fftconv1d_causal_fwd(const void* q, const void* kgate, const void*
   rc = validate_gate(act1, act2);
   if (rc) return rc;
   NSQ_CHECK_ARG(kgate && v, "gated_fftconv1d_fwd: null gate input pointer");
-  NSQ_CHECK_ARG(p.fused || aligned16({q, kgate, v, y, y1}), "gated_fftconv1d_fwd: tensors must be 16-byte aligned");
+  const bool one_kernel = gates_fused_1d(p, B * H * L);
+  NSQ_CHECK_ARG(one_kernel || aligned16({q, kgate, v, y, y1}), "gated_fftconv1d_fwd: tensors must be 16-byte aligned");
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
   float2* ws = nullptr;
   void* gws = nullptr;
-  if (!p.fused) {
+  if (!one_kernel) {
     const size_t need = gated_workspace_bytes(B, H, L, K, kbatch, dtype, NSQ_DIR_FWD);
     NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv1d_fwd: workspace of %zu bytes required, got %zu",
                   need, workspace_bytes);
@@ -457,36 +458,31 @@ int nsq_gated_fftconv1d_causal_bwd(const void* g, const void* q, const void* kga
   NSQ_CHECK_ARG(kgate && v && y1, "gated_fftconv1d_bwd: null gate input pointer (y1 is required)");
   NSQ_CHECK_ARG(dq && dkgate && dv && gk, "gated_fftconv1d_bwd: null gradient output pointer");
   NSQ_CHECK_ARG(!shortcut || gs, "gated_fftconv1d_bwd: gs required when a shortcut is given");
-  const bool fused_gates = p.fused && fuse_gates;
-  NSQ_CHECK_ARG(fused_gates || aligned16({g, q, kgate, v, y1, dq, dkgate, dv}),
-                "gated_fftconv1d_bwd: tensors must be 16-byte aligned");
+  NSQ_CHECK_ARG(fuse_gates == 0, "gated_fftconv1d_bwd: fuse_gates is reserved and must be 0");
+  NSQ_CHECK_ARG(aligned16({g, q, kgate, v, y1, dq, dkgate, dv}), "gated_fftconv1d_bwd: tensors must be 16-byte aligned");
   const float2* tw = twiddle_table();
   if (!tw) return NSQ_ERR_HIP;
   hipStream_t st = (hipStream_t)stream;
-  float2* ws = nullptr;
-  void* gws = nullptr;
-  if (!fused_gates) {
-    const size_t need = gated_workspace_bytes(B, H, L, K, kbatch, dtype, NSQ_DIR_BWD);
-    NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv1d_bwd: workspace of %zu bytes required, got %zu",
-                  need, workspace_bytes);
-    ws = (float2*)workspace;
-    gws = (char*)workspace + round256(causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD));
-  }
+  const size_t need = gated_workspace_bytes(B, H, L, K, kbatch, dtype, NSQ_DIR_BWD);
+  NSQ_CHECK_ARG(workspace && workspace_bytes >= need, "gated_fftconv1d_bwd: workspace of %zu bytes required, got %zu",
+                need, workspace_bytes);
+  float2* ws = (float2*)workspace;
+  void* gws = (char*)workspace + round256(causal_workspace_bytes(B, H, L, K, kbatch, NSQ_DIR_BWD));
   const GateArgs ga{kgate, v, const_cast<void*>(y1), dkgate, dv, act1, act2};
   const int kf = kbatch != 1;
   bool ok = false;
   switch (dtype) {
     case NSQ_DTYPE_F32:
       ok = run_gated_bwd<NSQ_DTYPE_F32>(p, g, q, k, shortcut, dq, gk, gs, int(B), int(H), int(L), int(K), kf, ga, gws,
-                                        ws, tw, st, fused_gates);
+                                        ws, tw, st);
       break;
     case NSQ_DTYPE_BF16:
       ok = run_gated_bwd<NSQ_DTYPE_BF16>(p, g, q, k, shortcut, dq, gk, gs, int(B), int(H), int(L), int(K), kf, ga, gws,
-                                         ws, tw, st, fused_gates);
+                                         ws, tw, st);
       break;
     default:
       ok = run_gated_bwd<NSQ_DTYPE_F16>(p, g, q, k, shortcut, dq, gk, gs, int(B), int(H), int(L), int(K), kf, ga, gws,
-                                        ws, tw, st, fused_gates);
+                                        ws, tw, st);
       break;
   }
   NSQ_CHECK_ARG(ok, "gated_fftconv1d_bwd: no kernel for logN=%d", p.logN);

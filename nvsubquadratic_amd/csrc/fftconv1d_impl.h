@@ -322,18 +322,13 @@ __global__ __launch_bounds__(2 * FusedCfg<LOGN>::T) void fused_fwd_pair_kernel(
 // filter-gradient rows are that image's.  CIRC: as the forward; the filter
 // gradient gk[j] = sum_n g[n] x[(n + c - j) mod L] is the correlation read at
 // lag (j - c) mod L; on a periodic extension (wm = L - 1) every lag repeats
-// 2N / L times, so gk and gs are scaled by gks = L / 2N (1 otherwise).  GATE:
-// g is the gradient of the gated output; the transform reads dy1 = g act2(v)
-// and writes dv = (g y1) act2'(v) as it loads; x is q (read as z = q act1(k));
-// the epilogue turns dz = conv^T(dy1) + s dy1 into gx = dq = dz act1(k) and
-// ga.dk = (dz q) act1'(k).
-template <int LOGN, int DT, bool FOLD, bool CIRC = false, bool GATE = false>
+// 2N / L times, so gk and gs are scaled by gks = L / 2N (1 otherwise).
+template <int LOGN, int DT, bool FOLD, bool CIRC = false>
 __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
     const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x,
     const float* __restrict__ k, const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ gx,
     float* __restrict__ gk, float* __restrict__ gs, int B, int H, int L, int K, const float2* __restrict__ tw, int c,
-    int kfilm, int wm, float gks, GateArgs ga) {
-  using ET = typename Elem<DT>::T;
+    int kfilm, int wm, float gks) {
   using C = FusedCfg<LOGN>;
   __shared__ float2 ldsG[C::TILE_P];
   __shared__ float2 ldsX[C::TILE_P];
@@ -362,30 +357,13 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
       const int64_t i0 = 2 * int64_t(n);
       const bool fold = FOLD && i0 >= 2 * int64_t(L);
       const int64_t i = fold ? i0 - 2 * int64_t(L) : (i0 & wm);
-      const float2 gv = load_pair<DT>(row, i, L);
-      if constexpr (GATE) {
-        const float2 vv = load_pair<DT>((const ET*)ga.v + ro, i, L);
-        const float2 yv = load_pair<DT>((const ET*)ga.y1 + ro, i, L);
-        if (!fold) {  // dv once per sample (the fold re-reads samples)
-          if (i < L) Elem<DT>::store((ET*)ga.dv, ro + i, Elem<DT>::round(gv.x * yv.x) * gate_dact(ga.act2, vv.x));
-          if (i + 1 < L)
-            Elem<DT>::store((ET*)ga.dv, ro + i + 1, Elem<DT>::round(gv.y * yv.y) * gate_dact(ga.act2, vv.y));
-        }
-        return make_float2(Elem<DT>::round(gv.x * Elem<DT>::round(gate_act(ga.act2, vv.x))),
-                           Elem<DT>::round(gv.y * Elem<DT>::round(gate_act(ga.act2, vv.y))));
-      }
-      return gv;
+      return load_pair<DT>(row, i, L);
     };
     auto ldx = [&](int m, int n) -> float2 {
       const int h = h0 + m;
       if (h >= H) return make_float2(0.f, 0.f);
       const int64_t ro = (int64_t(b) * H + h) * L, i = (2 * int64_t(n)) & wm;
-      const float2 q = load_pair<DT>(x + ro, i, L);
-      if constexpr (GATE) {
-        const float2 kk = load_pair<DT>((const ET*)ga.kg + ro, i, L);
-        return make_float2(gate1<DT>(ga.act1, q.x, kk.x), gate1<DT>(ga.act1, q.y, kk.y));
-      }
-      return q;
+      return load_pair<DT>(x + ro, i, L);
     };
     LdsTile<C::SP, true> stG{ldsG};
     LdsTile<C::SP, true> stX{ldsX};
@@ -412,18 +390,7 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_bwd_kernel(
       const float sv = s ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
       const int64_t i0 = 2 * int64_t(n);
       auto out = [&](int64_t i, float conv) {
-        if constexpr (GATE) {
-          const float dy1 =
-              s ? Elem<DT>::round(Elem<DT>::load(g, row + i) *
-                                  Elem<DT>::round(gate_act(ga.act2, Elem<DT>::load((const ET*)ga.v, row + i))))
-                : 0.f;
-          const float dz = epilogue<DT>(conv, s != nullptr, sv, dy1);
-          const float q = Elem<DT>::load(x, row + i), kk = Elem<DT>::load((const ET*)ga.kg, row + i);
-          Elem<DT>::store(gx, row + i, dz * Elem<DT>::round(gate_act(ga.act1, kk)));
-          Elem<DT>::store((ET*)ga.dk, row + i, Elem<DT>::round(dz * q) * gate_dact(ga.act1, kk));
-        } else {
-          Elem<DT>::store(gx, row + i, epilogue<DT>(conv, s != nullptr, sv, s ? Elem<DT>::load(g, row + i) : 0.f));
-        }
+        Elem<DT>::store(gx, row + i, epilogue<DT>(conv, s != nullptr, sv, s ? Elem<DT>::load(g, row + i) : 0.f));
       };
       if (i0 < L) out(i0, v.x * scale);
       if (i0 + 1 < L) out(i0 + 1, v.y * scale);
@@ -1317,13 +1284,13 @@ static void launch_fused_bwd(const Plan1D& p, const void* g, const void* x, cons
   dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
   if (p.fold)
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, GateArgs{});
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f);
   else
     hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false>), grid, dim3(C::T), 0, st, (const ET*)g, (const ET*)x, k,
-                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, GateArgs{});
+                       (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f);
 }
 
-// Gated (Hyena) fused plan: the GATE variants of the fused kernels.
+// Gated (Hyena) fused plan: the GATE variant of the fused forward kernel.
 template <int LOGN, int DT>
 static void launch_gated_fused_fwd(const Plan1D& p, const void* q, const float* k, const void* s, void* y, int B,
                                    int H, int L, int K, int kfilm, const GateArgs& ga, const float2* tw,
@@ -1342,21 +1309,6 @@ static void launch_gated_fused_fwd(const Plan1D& p, const void* q, const float* 
   else
     hipLaunchKernelGGL((fused_fwd_kernel<LOGN, DT, false, false, true>), grid, dim3(C::T), 0, st, (const ET*)q, k,
                        (const ET*)s, (ET*)y, B, H, L, K, bpw, tw, 0, kfilm, -1, ga);
-}
-
-template <int LOGN, int DT>
-static void launch_gated_fused_bwd(const Plan1D& p, const void* g, const void* q, const float* k, const void* s,
-                                   void* dq, float* gk, float* gs, int B, int H, int L, int K, int kfilm,
-                                   const GateArgs& ga, const float2* tw, hipStream_t st) {
-  using C = FusedCfg<LOGN>;
-  using ET = typename Elem<DT>::T;
-  const dim3 grid(unsigned(ceil_div(H, C::M)), unsigned(kfilm ? B : 1));
-  if (p.fold)
-    hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, true, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
-                       (const ET*)q, k, (const ET*)s, (ET*)dq, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, ga);
-  else
-    hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
-                       (const ET*)q, k, (const ET*)s, (ET*)dq, gk, gs, B, H, L, K, tw, 0, kfilm, -1, 1.f, ga);
 }
 
 // Shifted 1D convs on the fused plan, output rolled by -c through the filter
@@ -1394,7 +1346,7 @@ static void launch_circ_bwd(const void* g, const void* x, const float* k, const 
   const int wm = (!zpad && L > 1 && L < 2 * C::N) ? L - 1 : -1;
   hipLaunchKernelGGL((fused_bwd_kernel<LOGN, DT, false, true>), grid, dim3(C::T), 0, st, (const ET*)g,
                      (const ET*)x, k, (const ET*)s, (ET*)gx, gk, gs, B, H, L, K, tw, c, kfilm, wm,
-                     wm == -1 ? 1.f : float(L) / float(2 * C::N), GateArgs{});
+                     wm == -1 ? 1.f : float(L) / float(2 * C::N));
 }
 
 // Workspace layout of the 4-step plan (rows of N complex64; NK = H, or B*H for
@@ -1485,6 +1437,8 @@ static const void* launch_fold_rows(const void* src, float2* block, int64_t rows
   return block;
 }
 
+// k == nullptr: the filter's column transforms are already in the k block (the SIREN path forms them from the
+// transformed activation rows).
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_fwd(const void* x, const float* k, const void* s, void* y, int B, int H, int L, int K,
                              int kfilm, float2* ws, bool save, const float2* tw, hipStream_t st, bool fold) {
@@ -1503,12 +1457,15 @@ static void launch_4step_fwd(const void* x, const float* k, const void* s, void*
   } else {
     launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
   }
-  launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
+  if (k) launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
   hipLaunchKernelGGL((row_fwd_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)), dim3(RowCfg<LOGN2>::T),
                      0, st, (const float2*)wsx, (const float2*)wsk, wsy, rb, rh, tw);
   launch_col_inv_out<LOGN1, LOGN, DT>(wsy, x, s, y, BH, H, L, tw, st);
 }
 
+// k == nullptr: the k block already holds the filter's column transforms (recomputing x's only, when there is
+// no forward state).  gk == nullptr: the filter gradient's spectrum is left in the k block (the SIREN path reads
+// it there) and gs is not formed.
 template <int LOGN1, int LOGN2, int DT>
 static void launch_4step_bwd(const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
                              float* gs, int B, int H, int L, int K, int kfilm, float2* ws, bool fwd_state,
@@ -1531,7 +1488,7 @@ static void launch_4step_bwd(const void* g, const void* x, const float* k, const
   }
   if (!fwd_state) {
     launch_col_fwd<LOGN1, LOGN, DT>(RealRows<DT>{(const ET*)x, L, L}, BH, wsx, tw, st);
-    launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
+    if (k) launch_col_fwd<LOGN1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{k, K, K}, NK, wsk, tw, st);
   }
   if (rb == 1)
     hipLaunchKernelGGL((row_bwd1_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)),
@@ -1540,7 +1497,7 @@ static void launch_4step_bwd(const void* g, const void* x, const float* k, const
     hipLaunchKernelGGL((row_bwd_kernel<LOGN1, LOGN2>), dim3(unsigned(rh) * ((1 << LOGN1) / 2)),
                        dim3(RowCfg<LOGN2>::T), 0, st, wsg, (const float2*)wsx, wsk, rb, rh, tw);
   launch_col_inv_out<LOGN1, LOGN, DT>(wsg, g, s, gx, BH, H, L, tw, st);
-  launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, gs, int(NK), K, tw, st);
+  if (gk) launch_col_inv_gk<LOGN1, LOGN>(wsk, gk, gs, int(NK), K, tw, st);
 }
 
 // Shifted convs (circular, or zero-padded "same") beyond the fused plan, on
@@ -1664,16 +1621,13 @@ struct FusedBwd {
   };
 };
 
-template <int DT, bool BWD>
+template <int DT>
 struct GatedFused {
   template <int LOGN>
   struct At {
     template <class... A>
     static void run(A&&... a) {
-      if constexpr (BWD)
-        launch_gated_fused_bwd<LOGN, DT>(static_cast<A&&>(a)...);
-      else
-        launch_gated_fused_fwd<LOGN, DT>(static_cast<A&&>(a)...);
+      launch_gated_fused_fwd<LOGN, DT>(static_cast<A&&>(a)...);
     }
   };
 };
@@ -1748,8 +1702,57 @@ bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, cons
                                                                 fwd_state && !p.fold, tw, st, p.fold);
 }
 
-// Gated (Hyena) causal conv.  Fused plan: one gated kernel each way.  4-step
-// plan: the elementwise gate kernels around the plain conv, with the
+// Column passes of float rows on their own, at the 4-step plan of FFT length 2^(logN + 1) (logN in
+// [14, kMaxLogN]): rows of `valid` samples (row stride `stride`) into the plan's column transforms (N complex
+// values per row), and back: the inverse column pass of `rows` blocks into float rows of K samples (row stride
+// K; out[r][0] also to gs[r] when gs != nullptr), scaled by 1/N like the filter gradient.
+template <bool INV>
+struct ColRows {
+  template <int LOGN>
+  struct At {
+    static constexpr int L1 = split_log_n1(LOGN);
+    static void run(const float* src, int64_t stride, int64_t valid, const float2* spec, float* out, float* gs,
+                    int64_t rows, int K, float2* dst, const float2* tw, hipStream_t st) {
+      if constexpr (INV)
+        launch_col_inv_gk<L1, LOGN>(spec, out, gs, int(rows), K, tw, st);
+      else
+        launch_col_fwd<L1, LOGN, NSQ_DTYPE_F32>(RealRows<NSQ_DTYPE_F32>{src, stride, valid}, rows, dst, tw, st);
+    }
+  };
+};
+
+template <int UNUSED>  // a template: one definition (fftconv1d_f32.hip) across the translation units
+bool run_col_fwd_rows(int logN, const float* src, int64_t stride, int64_t valid, int64_t rows, float2* out,
+                      const float2* tw, hipStream_t st) {
+  return dispatch_int<ColRows<false>::template At, 14, kMaxLogN>(logN, src, stride, valid, nullptr, nullptr,
+                                                                 nullptr, rows, 0, out, tw, st);
+}
+
+template <int UNUSED>
+bool run_col_inv_rows(int logN, const float2* spec, float* out, float* gs, int64_t rows, int K, const float2* tw,
+                      hipStream_t st) {
+  return dispatch_int<ColRows<true>::template At, 14, kMaxLogN>(logN, nullptr, int64_t(0), int64_t(0), spec, out,
+                                                                gs, rows, K, nullptr, tw, st);
+}
+
+// Whether the fused plan's forward runs the gated kernel (gates in its first pass and epilogue) rather than the
+// gate kernels around the plain fused kernel.  Both round the same way (same bits).  The gated kernel adds four
+// operand streams (q and k in place of z, then q, k and v again in its epilogue, y1 beside y) to a kernel that
+// holds one or two workgroups per CU, so it only pays where launches dominate: measured on MI355X (bf16 fwd),
+// B=4 H=1024 L=8192 0.436 ms against 0.351 ms for the three kernels, B=1 H=1024 L=8192 0.110 / 0.100 ms,
+// B=2 H=256 L=4096 0.037 / 0.038 ms, B=1 H=64 L=2048 0.031 / 0.038 ms.  Below 2^22 elements the gated kernel;
+// NSQ_1D_GATES_FUSED=0 / 1 forces either.
+inline bool gates_fused_1d(const Plan1D& p, int64_t elems) {
+  static const int force = [] {
+    const char* e = std::getenv("NSQ_1D_GATES_FUSED");
+    return e ? (e[0] == '0' ? 0 : 1) : -1;
+  }();
+  if (!p.fused || force == 0) return false;
+  return force == 1 || elems < (int64_t(1) << 22);
+}
+
+// Gated (Hyena) causal conv.  Forward, fused plan: one gated kernel for small calls (gates_fused_1d), else, and
+// on the 4-step plan, the elementwise gate kernels around the plain conv, with the
 // intermediates in `gws` (forward: z [, y1 when the caller keeps none];
 // backward: z, dy1, dz), the conv's own workspace in `ws`.
 // Forward: y = (conv(z) + s z) act2(v), z = q act1(k_gate); ga.y1 (optional)
@@ -1757,8 +1760,8 @@ bool run_bwd(const Plan1D& p, const void* g, const void* x, const float* k, cons
 template <int DT>
 bool run_gated_fwd(const Plan1D& p, const void* q, const float* k, const void* s, void* y, int B, int H, int L,
                    int K, int kfilm, const GateArgs& ga, void* gws, float2* ws, const float2* tw, hipStream_t st) {
-  if (p.fused)
-    return dispatch_int<GatedFused<DT, false>::template At, 3, 13>(p.logN, p, q, k, s, y, B, H, L, K, kfilm, ga, tw,
+  if (gates_fused_1d(p, int64_t(B) * H * L))
+    return dispatch_int<GatedFused<DT>::template At, 3, 13>(p.logN, p, q, k, s, y, B, H, L, K, kfilm, ga, tw,
                                                                    st);
   using ET = typename Elem<DT>::T;
   const int64_t n = int64_t(B) * H * L;
@@ -1772,18 +1775,15 @@ bool run_gated_fwd(const Plan1D& p, const void* q, const float* k, const void* s
 }
 
 // The backward runs the elementwise gate kernels around the plain conv adjoint
-// for every plan: the gated fused adjoint (GATE) is correct but, with one
-// 139 KB-LDS workgroup per CU at FFT length 16384, its five extra operand
-// streams add latency that occupancy cannot hide (measured on MI355X at
-// B=4 D=1024 L=8192 bf16: 1.01 ms against 0.66 ms for the plain adjoint plus
-// ~0.17 ms of gate kernels).  `fused_gate_bwd` selects it anyway (tests).
+// for every plan.  A gated fused adjoint (gates in the fused backward kernel's
+// loads and epilogue) measured slower on MI355X: with one 139 KB-LDS workgroup
+// per CU at FFT length 16384, its five extra operand streams add latency that
+// occupancy cannot hide (B=4 D=1024 L=8192 bf16: 0.96 ms against 0.58 ms for
+// the plain adjoint plus 0.15 ms of gate kernels), so it is not built.
 template <int DT>
 bool run_gated_bwd(const Plan1D& p, const void* g, const void* q, const float* k, const void* s, void* dq, float* gk,
                    float* gs, int B, int H, int L, int K, int kfilm, const GateArgs& ga, void* gws, float2* ws,
-                   const float2* tw, hipStream_t st, bool fused_gate_bwd) {
-  if (p.fused && fused_gate_bwd)
-    return dispatch_int<GatedFused<DT, true>::template At, 3, 13>(p.logN, p, g, q, k, s, dq, gk, gs, B, H, L, K,
-                                                                  kfilm, ga, tw, st);
+                   const float2* tw, hipStream_t st) {
   using ET = typename Elem<DT>::T;
   const int64_t n = int64_t(B) * H * L;
   const int64_t stride = int64_t(round256(size_t(n) * sizeof(ET)) / sizeof(ET));  // 256-byte aligned sub-buffers
@@ -1857,7 +1857,7 @@ bool run_shift4_bwd(int logN, const void* g, const void* x, const float* k, cons
                                          hipStream_t);                                                          \
   extern template bool run_gated_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*,     \
                                          void*, float*, float*, int, int, int, int, int, const GateArgs&, void*, \
-                                         float2*, const float2*, hipStream_t, bool);
+                                         float2*, const float2*, hipStream_t);
 
 #define NSQ_INSTANTIATE_FFTCONV1D(DT)                                                                    \
   template bool run_fwd<DT>(const Plan1D&, const void*, const float*, const void*, void*, int, int, int, \
@@ -1878,10 +1878,14 @@ bool run_shift4_bwd(int logN, const void* g, const void* x, const float* k, cons
                                   int, const GateArgs&, void*, float2*, const float2*, hipStream_t);             \
   template bool run_gated_bwd<DT>(const Plan1D&, const void*, const void*, const float*, const void*, void*,      \
                                   float*, float*, int, int, int, int, int, const GateArgs&, void*, float2*,       \
-                                  const float2*, hipStream_t, bool);
+                                  const float2*, hipStream_t);
 
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_F32)
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_BF16)
 NSQ_DECLARE_FFTCONV1D(NSQ_DTYPE_F16)
+extern template bool run_col_fwd_rows<0>(int, const float*, int64_t, int64_t, int64_t, float2*, const float2*,
+                                         hipStream_t);
+extern template bool run_col_inv_rows<0>(int, const float2*, float*, float*, int64_t, int, const float2*,
+                                         hipStream_t);
 
 }  // namespace nsq

@@ -30,6 +30,7 @@
 #include <type_traits>
 
 #include "nsq_common.h"
+#include "siren_readout.h"
 
 namespace nsq {
 namespace {
@@ -636,11 +637,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rb_rsrc(const float* p, int by
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, bytes, 0x00020000);
 }
 
+// bw (optional, G floats): gb weighted by it, gb[h] = sum_g gk[h][g] bw[g], instead of the row sum.
 template <int HD, bool VEC>
 __global__ __launch_bounds__(kRbThreads) void siren_readout_bwd_kernel(
     const float* __restrict__ gk, int64_t ldk, const float* __restrict__ act, int64_t lda,
-    const float* __restrict__ wout, int64_t G, int H, int hslice, float* __restrict__ gact, int64_t gact_slice,
-    float* __restrict__ gw_part, float* __restrict__ gb_part) {
+    const float* __restrict__ bw, const float* __restrict__ wout, int64_t G, int H, int hslice,
+    float* __restrict__ gact, int64_t gact_slice, float* __restrict__ gw_part, float* __restrict__ gb_part) {
   constexpr int NJ = HD / 16, NGB = kRbGpw / 16, NKS = kRbGpw / 32, RS = HD + 1;
   // TS: row stride (words) of a wave's transposition tile [32 channels][kRbGpw points]: 66 puts the 4 channel
   // groups of a gact operand read (rows 8q + e) 16 banks apart, so a read covers the 64 banks once
@@ -677,6 +679,14 @@ __global__ __launch_bounds__(kRbThreads) void siren_readout_bwd_kernel(
       const nsq_f32x8_t v = load8<VEC>(ab + int64_t(16 * jt + p) * lda + g, G - g);
       split8(v, bah[jt][ks], bal[jt][ks]);
     }
+  nsq_f32x8_t bwv[NKS];  // gb weights at this lane's points
+  if (bw) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int64_t g = gw0 + 32 * ks + 8 * q;
+      bwv[ks] = load8<VEC>(bw + g, G - g);
+    }
+  }
   f32x4 acc_a[NJ][NGB];  // gact^T tiles D[j][g]
 #pragma unroll
   for (int jt = 0; jt < NJ; ++jt)
@@ -747,7 +757,12 @@ __global__ __launch_bounds__(kRbThreads) void siren_readout_bwd_kernel(
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
         const nsq_f32x8_t v = cur[hbk][ks];
-        bsum[hbk] += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        if (bw) {
+          const nsq_f32x8_t u = v * bwv[ks];
+          bsum[hbk] += ((u[0] + u[1]) + (u[2] + u[3])) + ((u[4] + u[5]) + (u[6] + u[7]));
+        } else {
+          bsum[hbk] += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        }
         nsq_bf16x8_t ah, al;
         split8(v, ah, al);
 #pragma unroll
@@ -820,11 +835,11 @@ __global__ __launch_bounds__(kRbThreads) void siren_readout_bwd_kernel(
   }
 }
 
-// out[i] = sum_{s < ns} part[s * n + i] for i < n: thread i walks the parts in order with 16 interleaved running
-// sums (s = 0, 16, 32, ... / 1, 17, ...; 16 loads in flight per thread) added in a fixed tree at the end, so the
-// result is bitwise repeatable.
+// out[i] = scale * sum_{s < ns} part[s * n + i] for i < n: thread i walks the parts in order with 16 interleaved
+// running sums (s = 0, 16, 32, ... / 1, 17, ...; 16 loads in flight per thread) added in a fixed tree at the end,
+// so the result is bitwise repeatable.
 __global__ __launch_bounds__(256) void siren_sum_parts_kernel(const float* __restrict__ part, int64_t ns, int64_t n,
-                                                              float* __restrict__ out) {
+                                                              float* __restrict__ out, float scale) {
   constexpr int U = 16;
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n) return;
@@ -844,7 +859,7 @@ __global__ __launch_bounds__(256) void siren_sum_parts_kernel(const float* __res
   for (int w = U / 2; w >= 1; w /= 2)
 #pragma unroll
     for (int u = 0; u < w; ++u) s[u] += s[u + w];
-  out[i] = s[0];
+  out[i] = s[0] * scale;
 }
 
 // Readout-backward launch geometry: point blocks of 8 waves x kRbGpw, channel
@@ -873,30 +888,31 @@ RbPlan rb_plan(int64_t H, int HD, int64_t G, int64_t nb) {
 }
 
 template <int HD>
-void launch_readout_bwd(const float* gk, int64_t ldk, const float* act, int64_t lda, const float* wout, int64_t H,
-                        int64_t G, int64_t nb, float* gact, float* gwout, float* gbout, float* ws, hipStream_t st) {
+void launch_readout_bwd(const float* gk, int64_t ldk, const float* act, int64_t lda, const float* bw,
+                        const float* wout, int64_t H, int64_t G, int64_t nb, float* gact, float* gwout, float* gbout,
+                        float scale, float* ws, hipStream_t st) {
   const RbPlan p = rb_plan(H, HD, G, nb);
   const bool vec = ldk % 4 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(gk) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(act) & 15) == 0;
+                   (reinterpret_cast<uintptr_t>(act) & 15) == 0 && (reinterpret_cast<uintptr_t>(bw) & 15) == 0;
   float* ga = p.hs > 1 ? ws + p.gact_part : gact;
   const int64_t gslice = int64_t(nb) * HD * G;
   const dim3 grd(unsigned(p.ngb), unsigned(p.hs), unsigned(nb));
   float* gbp = gbout ? ws + p.gb_part : nullptr;
   if (vec)
-    hipLaunchKernelGGL((siren_readout_bwd_kernel<HD, true>), grd, dim3(kRbThreads), 0, st, gk, ldk, act, lda, wout,
-                       G, int(H), p.hslice, ga, gslice, ws + p.gw_part, gbp);
+    hipLaunchKernelGGL((siren_readout_bwd_kernel<HD, true>), grd, dim3(kRbThreads), 0, st, gk, ldk, act, lda, bw,
+                       wout, G, int(H), p.hslice, ga, gslice, ws + p.gw_part, gbp);
   else
-    hipLaunchKernelGGL((siren_readout_bwd_kernel<HD, false>), grd, dim3(kRbThreads), 0, st, gk, ldk, act, lda, wout,
-                       G, int(H), p.hslice, ga, gslice, ws + p.gw_part, gbp);
+    hipLaunchKernelGGL((siren_readout_bwd_kernel<HD, false>), grd, dim3(kRbThreads), 0, st, gk, ldk, act, lda, bw,
+                       wout, G, int(H), p.hslice, ga, gslice, ws + p.gw_part, gbp);
   if (p.hs > 1)
     hipLaunchKernelGGL(siren_sum_parts_kernel, dim3(unsigned(ceil_div(gslice, 256))), dim3(256), 0, st, ga,
-                       int64_t(p.hs), gslice, gact);
+                       int64_t(p.hs), gslice, gact, 1.f);
   const int64_t nparts = nb * p.ngb, nw = H * HD;
   hipLaunchKernelGGL(siren_sum_parts_kernel, dim3(unsigned(ceil_div(nw, 256))), dim3(256), 0, st, ws + p.gw_part,
-                     nparts, nw, gwout);
+                     nparts, nw, gwout, scale);
   if (gbout)
     hipLaunchKernelGGL(siren_sum_parts_kernel, dim3(unsigned(ceil_div(H, 256))), dim3(256), 0, st, gbp, nparts, H,
-                       gbout);
+                       gbout, scale);
 }
 
 constexpr int kSirenMaxLds = 160 * 1024;
@@ -1036,6 +1052,19 @@ int siren_validate(const float* grid, int64_t G, int d, const float* w0, int E, 
 }
 
 }  // namespace
+
+size_t siren_readout_bwd_ws_floats(int64_t H, int HD, int64_t G, int64_t nb) { return rb_plan(H, HD, G, nb).total; }
+
+bool siren_readout_bwd_run(const float* gk, int64_t ldk, const float* act, int64_t lda, const float* bw,
+                           const float* wout, int64_t H, int HD, int64_t G, int64_t nb, float* gact, float* gwout,
+                           float* gbout, float scale, float* ws, hipStream_t st) {
+  switch (HD) {
+    case 16: launch_readout_bwd<16>(gk, ldk, act, lda, bw, wout, H, G, nb, gact, gwout, gbout, scale, ws, st); return true;
+    case 32: launch_readout_bwd<32>(gk, ldk, act, lda, bw, wout, H, G, nb, gact, gwout, gbout, scale, ws, st); return true;
+    case 64: launch_readout_bwd<64>(gk, ldk, act, lda, bw, wout, H, G, nb, gact, gwout, gbout, scale, ws, st); return true;
+    default: return false;
+  }
+}
 }  // namespace nsq
 
 extern "C" {
@@ -1122,9 +1151,9 @@ int nsq_siren_readout_bwd(const float* gk, int64_t ldk, const float* act, int64_
   hipStream_t st = (hipStream_t)stream;
   float* ws = static_cast<float*>(workspace);
   switch (HD) {
-    case 16: launch_readout_bwd<16>(gk, ldk, act, lda, wout, H, G, nb, gact, gwout, gbout, ws, st); break;
-    case 32: launch_readout_bwd<32>(gk, ldk, act, lda, wout, H, G, nb, gact, gwout, gbout, ws, st); break;
-    default: launch_readout_bwd<64>(gk, ldk, act, lda, wout, H, G, nb, gact, gwout, gbout, ws, st); break;
+    case 16: launch_readout_bwd<16>(gk, ldk, act, lda, nullptr, wout, H, G, nb, gact, gwout, gbout, 1.f, ws, st); break;
+    case 32: launch_readout_bwd<32>(gk, ldk, act, lda, nullptr, wout, H, G, nb, gact, gwout, gbout, 1.f, ws, st); break;
+    default: launch_readout_bwd<64>(gk, ldk, act, lda, nullptr, wout, H, G, nb, gact, gwout, gbout, 1.f, ws, st); break;
   }
   NSQ_CHECK_LAUNCH();
   return NSQ_OK;

@@ -1,4 +1,4 @@
-r"""Hyena-gated FFT convolution (causal 1D, 2D / 3D) on the HIP backend (build-plan row F2).
+r"""Hyena-gated FFT convolution (causal 1D, 2D / 3D) on the HIP backend.
 
 The reference computes a Hyena layer's gated long convolution as separate ops
 (``nvsubquadratic/modules/hyena_nd.py:546`` first gate, ``:558`` the CKConvND
@@ -12,9 +12,8 @@ Each is an HBM round trip of a ``[B, H, L]`` tensor.  Here the forward's gates
 run inside the conv's first-pass loader and last-pass epilogue (FFT lengths up
 to 16384: one kernel), or as elementwise HIP kernels around the multi-kernel
 conv (longer sequences).  The backward runs elementwise gate kernels around the
-plain conv adjoint by default; the one-kernel gated adjoint
-(``fuse_backward_gates=True``) measured slower on MI355X (a latency-bound kernel
-at one workgroup per CU gains five operand streams).  2D / 3D: both directions
+plain conv adjoint (a one-kernel gated adjoint measured slower on MI355X: a
+latency-bound kernel at one workgroup per CU gains five operand streams).  2D / 3D: both directions
 run the gates inside the N-d conv's first and last passes (z, or dy1 and dv, as
 the first pass loads; gate 2, or dq and dk, in the last pass's epilogue) where
 the plan has packed 2D rows with the vector epilogue or 3D plane passes, else as
@@ -84,11 +83,9 @@ def gated_causal_fftconv1d_fwd_raw(q, kg, v, k, s, y, y1, act1: int, act2: int, 
 
 
 def gated_causal_fftconv1d_bwd_raw(g, q, kg, v, y1, k, s, dq, dkg, dv, gk, gs, act1: int, act2: int,
-                                   kbatch: int = 1, fuse_gates: bool = False):
-    """Launch the gated backward (gk ``[kbatch*H, K]``, gs ``[kbatch*H]`` partials or None).
-
-    ``fuse_gates``: the one-kernel adjoint with the gates inside (FFT lengths <= 16384); the default runs
-    the elementwise gate kernels around the plain adjoint, measured faster on MI355X."""
+                                   kbatch: int = 1):
+    """Launch the gated backward (gk ``[kbatch*H, K]``, gs ``[kbatch*H]`` partials or None): elementwise gate
+    kernels around the plain conv adjoint."""
     lib = _lib.get_lib()
     _lib.check_device(q)
     B, H, L = q.shape
@@ -99,7 +96,7 @@ def gated_causal_fftconv1d_bwd_raw(g, q, kg, v, y1, k, s, dq, dkg, dv, gk, gs, a
     _lib.check(lib.nsq_gated_fftconv1d_causal_bwd(
         g.data_ptr(), q.data_ptr(), kg.data_ptr(), v.data_ptr(), y1.data_ptr(), k.data_ptr(), _lib.ptr(s),
         dq.data_ptr(), dkg.data_ptr(), dv.data_ptr(), gk.data_ptr(), _lib.ptr(gs), dt, act1, act2, B, H, L, K, kbatch,
-        int(bool(fuse_gates)), _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_ptr(q.device)))
+        0, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_ptr(q.device)))
 
 
 def _grad_wanted(*ts) -> bool:
@@ -114,10 +111,10 @@ def _shortcut_grad(gs, s, kbatch, H):
 
 @custom_op("nsq_hip::gated_causal_fftconv1d", mutates_args=())
 def gated_causal_fftconv1d_op(q: torch.Tensor, kg: torch.Tensor, v: torch.Tensor, k: torch.Tensor,
-                              s: Optional[torch.Tensor], act1: int, act2: int, kbatch: int, keep: bool,
-                              fuse_bwd: bool) -> tuple[torch.Tensor, torch.Tensor]:
+                              s: Optional[torch.Tensor], act1: int, act2: int, kbatch: int,
+                              keep: bool) -> tuple[torch.Tensor, torch.Tensor]:
     """Gated causal conv forward; returns ``(y, y1)``, y1 = conv(z) + s z kept for the backward when ``keep``
-    (else empty).  ``fuse_bwd`` selects the backward's one-kernel gated adjoint (recorded for the backward)."""
+    (else empty)."""
     q, kg, v = (_aligned16(t) for t in (q, kg, v))
     y = torch.empty_like(q)
     y1 = torch.empty_like(q) if keep else q.new_empty(0)
@@ -126,50 +123,47 @@ def gated_causal_fftconv1d_op(q: torch.Tensor, kg: torch.Tensor, v: torch.Tensor
 
 
 @gated_causal_fftconv1d_op.register_fake
-def _(q, kg, v, k, s, act1, act2, kbatch, keep, fuse_bwd):
+def _(q, kg, v, k, s, act1, act2, kbatch, keep):
     return torch.empty_like(q), (torch.empty_like(q) if keep else q.new_empty(0))
 
 
 @custom_op("nsq_hip::gated_causal_fftconv1d_backward", mutates_args=())
 def gated_causal_fftconv1d_backward_op(g: torch.Tensor, q: torch.Tensor, kg: torch.Tensor, v: torch.Tensor,
                                        y1: torch.Tensor, k: torch.Tensor, s: Optional[torch.Tensor], act1: int,
-                                       act2: int, kbatch: int, fuse: bool) -> tuple[torch.Tensor, torch.Tensor,
-                                                                                   torch.Tensor, torch.Tensor,
-                                                                                   torch.Tensor]:
+                                       act2: int, kbatch: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                        torch.Tensor, torch.Tensor]:
     """``(dq, dkg, dv, gk, gs)``; gs ``[kbatch*H]`` partials, empty without a shortcut."""
     g, q, kg, v = (_aligned16(t) for t in (g, q, kg, v))
     dq, dkg, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
     gk = torch.empty_like(k)
     gs = torch.empty(kbatch * q.shape[1] if s is not None else 0, dtype=torch.float32, device=q.device)
     gated_causal_fftconv1d_bwd_raw(g, q, kg, v, y1, k, s, dq, dkg, dv, gk, gs if s is not None else None, act1, act2,
-                                   kbatch, fuse)
+                                   kbatch)
     return dq, dkg, dv, gk, gs
 
 
 @gated_causal_fftconv1d_backward_op.register_fake
-def _(g, q, kg, v, y1, k, s, act1, act2, kbatch, fuse):
+def _(g, q, kg, v, y1, k, s, act1, act2, kbatch):
     return (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q), torch.empty_like(k),
             q.new_empty(kbatch * q.shape[1] if s is not None else 0, dtype=torch.float32))
 
 
 def _gated1d_setup(ctx, inputs, output):
-    q, kg, v, k, s, act1, act2, kbatch, _keep, fuse_bwd = inputs
+    q, kg, v, k, s, act1, act2, kbatch, _keep = inputs
     # the second output is internal (state kept for the backward): no gradient flows into it, and none is
     # materialized for it (autograd would otherwise fill a zero tensor of its size before every backward)
     ctx.mark_non_differentiable(output[1])
     ctx.set_materialize_grads(False)
     ctx.save_for_backward(q, kg, v, output[1], k, s)
     ctx.meta = (act1, act2, kbatch)
-    ctx.fuse_bwd = fuse_bwd
 
 
 def _gated1d_backward(ctx, gy, _gy1):
     q, kg, v, y1, k, s = ctx.saved_tensors
     act1, act2, kbatch = ctx.meta
     g = channels_first_contiguous(gy.to(q.dtype))
-    dq, dkg, dv, gk, gs = gated_causal_fftconv1d_backward_op(g, q, kg, v, y1, k, s, act1, act2, kbatch,
-                                                             ctx.fuse_bwd)
-    return dq, dkg, dv, gk, _shortcut_grad(gs, s, kbatch, q.shape[1]), None, None, None, None, None
+    dq, dkg, dv, gk, gs = gated_causal_fftconv1d_backward_op(g, q, kg, v, y1, k, s, act1, act2, kbatch)
+    return dq, dkg, dv, gk, _shortcut_grad(gs, s, kbatch, q.shape[1]), None, None, None, None
 
 
 gated_causal_fftconv1d_op.register_autograd(_gated1d_backward, setup_context=_gated1d_setup)
@@ -183,14 +177,12 @@ def hyena_gated_causal_fftconv1d_bhl(
     shortcut: torch.Tensor | None = None,
     gate_nonlinear="silu",
     gate_nonlinear_2=None,
-    fuse_backward_gates: bool = False,
 ) -> torch.Tensor:
     """``(conv(q*act1(k)) + s*(q*act1(k))) * act2(v)`` for BHL ``[B, H, L]`` q, k, v.
 
     ``kernel``: ``[1|B, H, K]`` or ``[H, K]`` fp32-castable (``K <= 2L``, the causal
     conv's rule); ``shortcut``: ``[H]`` or None.  Returns ``[B, H, L]`` in
-    ``query.dtype``.  ``fuse_backward_gates``: run the backward's gates inside the
-    fused adjoint too (FFT lengths <= 16384; slower on MI355X at the measured shapes).
+    ``query.dtype``.
     """
     if query.ndim != 3 or key.shape != query.shape or value.shape != query.shape:
         raise ValueError(f"query, key, value must share one [B, H, L] shape; got {tuple(query.shape)}, "
@@ -213,8 +205,7 @@ def hyena_gated_causal_fftconv1d_bhl(
         if shortcut.shape != (H,):
             raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
         sc = shortcut.to(in_dtype).to(cdt).contiguous()
-    y, _ = gated_causal_fftconv1d_op(q, kg, v, kc, sc, act1, act2, kbatch, _grad_wanted(q, kg, v, kc, sc),
-                                     bool(fuse_backward_gates))
+    y, _ = gated_causal_fftconv1d_op(q, kg, v, kc, sc, act1, act2, kbatch, _grad_wanted(q, kg, v, kc, sc))
     return y.to(in_dtype)
 
 

@@ -1,4 +1,4 @@
-r"""HIP implicit filter generation: the SIREN MLP of ``SIRENKernelND`` on the matrix cores (row F1).
+r"""HIP implicit filter generation: the SIREN MLP of ``SIRENKernelND`` on the matrix cores.
 
 Reference: ``nvsubquadratic/modules/kernels_nd.py`` -- ``SIRENPositionalEmbeddingND`` (:660-860) and
 ``SIRENKernelND`` (:876-1190): for the grid coordinates ``x`` (per axis ``2 * seq_len - 1`` points on
@@ -38,8 +38,8 @@ from torch.library import custom_op
 
 from . import _lib
 
-__all__ = ["HipSIRENKernelND", "KernelFiLMGenerator", "siren_film_filter", "siren_filter", "siren_filter_op",
-           "siren_grid"]
+__all__ = ["HipSIRENKernelND", "KernelFiLMGenerator", "siren_causal_fftconv1d", "siren_film_filter", "siren_filter",
+           "siren_filter_op", "siren_grid"]
 
 
 def _opt(t: Optional[torch.Tensor]) -> int | None:
@@ -141,14 +141,21 @@ def siren_filter_backward_op(gk: torch.Tensor, act: torch.Tensor, grid: torch.Te
     """Gradients ``(gw0, gb0, gwh, gbh, gwout, gbout)`` for ``gk [H, G]`` (empty where a bias is absent): the
     readout's gradients in one pass over gk (``nsq_siren_readout_bwd``), then ``nsq_siren_mlp_bwd`` on
     ``gact = wout^T gk`` ``[HD, G]``."""
-    lib = _lib.get_lib()
-    G, d = grid.shape
-    H, HD = wout.shape
-    E = w0.shape[0]
-    dev = grid.device
     if gk.stride(1) != 1:
         gk = gk.contiguous()
     gact, gwout, gbout = _readout_backward(gk, act, wout, has_bout)
+    return (*_mlp_backward(gact, grid, w0, b0, wh, bh, nh, wout.shape[1]), gwout, gbout)
+
+
+def _mlp_backward(gact: torch.Tensor, grid: torch.Tensor, w0: torch.Tensor, b0: Optional[torch.Tensor],
+                  wh: torch.Tensor, bh: Optional[torch.Tensor], nh: int,
+                  HD: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(gw0, gb0, gwh, gbh)`` of the hidden stack for ``gact [HD, G]`` (any strides; rows >= HD are not read):
+    ``nsq_siren_mlp_bwd`` recomputes the layers from the grid."""
+    lib = _lib.get_lib()
+    G, d = grid.shape
+    E = w0.shape[0]
+    dev = grid.device
     gw0, gwh = torch.empty_like(w0), torch.empty_like(wh)
     gb0 = torch.empty(E if _has(b0) else 0, device=dev)
     gbh = torch.empty(nh * HD if _has(bh) else 0, device=dev)
@@ -158,7 +165,7 @@ def siren_filter_backward_op(gk: torch.Tensor, act: torch.Tensor, grid: torch.Te
                                      w0.data_ptr(), _opt(b0), E, wh.data_ptr(), _opt(bh), nh, HD, gw0.data_ptr(),
                                      _opt(gb0), gwh.data_ptr(), _opt(gbh), ws.data_ptr(), ws.numel(),
                                      _lib.stream_ptr(dev)))
-    return gw0, gb0, gwh, gbh, gwout, gbout
+    return gw0, gb0, gwh, gbh
 
 
 @siren_filter_backward_op.register_fake
@@ -325,11 +332,194 @@ def siren_filter(grid: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor | None, 
     ``hidden_w[i]`` is the weight of hidden linear ``i`` (``[HD, E]`` then ``[HD, HD]``), ``hidden_b``
     their biases (None: no biases); every weight is read as float32, as the reference computes.  The
     hidden stack runs in ``nsq_siren_mlp_fwd``, the readout in ``nsq_siren_readout_fwd``; the readout's
-    gradients are two GEMMs (``K = H`` and, with the bias as the ones row of ``act``, ``K = G``)."""
+    gradients come from one pass over the filter gradient (``nsq_siren_readout_bwd``)."""
     f = lambda t: None if t is None else t.float().contiguous()  # noqa: E731
     wh = torch.cat([w.float().reshape(-1) for w in hidden_w])
     bh = None if hidden_b is None else torch.cat([b.float().reshape(-1) for b in hidden_b])
     return siren_filter_op(f(grid), f(w0), f(b0), wh, bh, f(wout), f(bout), len(hidden_w))[0]
+
+
+# ---------------------------------------------------------------------------
+# Causal 1D conv with the SIREN filter kept out of HBM (nsq_siren_fftconv1d_causal_*): CKConvND's causal path
+# (ckconv_nd.py:1149-1164, the generator's filter cropped to its causal half, then fftconv.py:546-600) as the
+# hidden stack, then one conv op that forms the filter's column transforms from the transformed activations
+# and returns the readout's gradients from the filter gradient's spectrum.
+# ---------------------------------------------------------------------------
+@custom_op("nsq_hip::siren_mlp", mutates_args=())
+def siren_mlp_op(grid: torch.Tensor, w0: torch.Tensor, b0: Optional[torch.Tensor], wh: torch.Tensor,
+                 bh: Optional[torch.Tensor], nh: int, HD: int) -> torch.Tensor:
+    """``[a_nh^T; 1]`` ``[HD + 1, G]`` float32: the hidden stack's output with the ones row (the readout's
+    input, bias included)."""
+    return _mlp_fwd(grid, w0, b0, wh, bh, nh, HD)
+
+
+@siren_mlp_op.register_fake
+def _(grid, w0, b0, wh, bh, nh, HD):
+    return grid.new_empty(HD + 1, grid.shape[0])
+
+
+@custom_op("nsq_hip::siren_mlp_backward", mutates_args=())
+def siren_mlp_backward_op(gact: torch.Tensor, grid: torch.Tensor, w0: torch.Tensor, b0: Optional[torch.Tensor],
+                          wh: torch.Tensor, bh: Optional[torch.Tensor], nh: int,
+                          HD: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(gw0, gb0, gwh, gbh)`` for ``gact [HD + 1, G]`` (the ones row's gradient is ignored)."""
+    return _mlp_backward(gact, grid, w0, b0, wh, bh, nh, HD)
+
+
+@siren_mlp_backward_op.register_fake
+def _(gact, grid, w0, b0, wh, bh, nh, HD):
+    return (torch.empty_like(w0), w0.new_empty(w0.shape[0] if _has(b0) else 0), torch.empty_like(wh),
+            wh.new_empty(nh * HD if _has(bh) else 0))
+
+
+def _mlp_setup(ctx, inputs, output):
+    grid, w0, b0, wh, bh, nh, HD = inputs
+    ctx.save_for_backward(grid, w0, b0, wh, bh)
+    ctx.meta = (nh, HD)
+
+
+def _mlp_backward_fn(ctx, gact):
+    grid, w0, b0, wh, bh = ctx.saved_tensors
+    nh, HD = ctx.meta
+    gw0, gb0, gwh, gbh = siren_mlp_backward_op(gact.float(), grid, w0, b0, wh, bh, nh, HD)
+    return None, gw0, gb0 if b0 is not None else None, gwh, gbh if bh is not None else None, None, None
+
+
+siren_mlp_op.register_autograd(_mlp_backward_fn, setup_context=_mlp_setup)
+
+
+def _siren_conv_ws_bytes(B: int, H: int, L: int, K: int, HD: int) -> int:
+    return int(_lib.get_lib().nsq_siren_fftconv1d_causal_workspace_bytes(B, H, L, K, HD))
+
+
+@custom_op("nsq_hip::siren_readout_causal_fftconv1d", mutates_args=())
+def siren_readout_causal_fftconv1d_op(x: torch.Tensor, act: torch.Tensor, wout: torch.Tensor,
+                                      bout: Optional[torch.Tensor], s: Optional[torch.Tensor],
+                                      keep: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Causal conv of ``x [B, H, L]`` (contiguous) with the filter ``k = wout @ act[:HD] + bout`` (``act [HD + 1,
+    K]``, last row ones), which is never formed.  Returns ``(y, state)``: with ``keep`` the workspace, in which
+    the forward leaves the transformed x, filter and activations for the backward, else empty."""
+    lib = _lib.get_lib()
+    _lib.check_device(x)
+    B, H, L = x.shape
+    HD, K = wout.shape[1], act.shape[1]
+    y = torch.empty_like(x)
+    ws = torch.empty(_siren_conv_ws_bytes(B, H, L, K, HD), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.nsq_siren_fftconv1d_causal_fwd(x.data_ptr(), act.data_ptr(), act.stride(0), wout.data_ptr(),
+                                                  _opt(bout), HD, _opt(s), y.data_ptr(), _lib.dtype_code(x.dtype), B,
+                                                  H, L, K, ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device)))
+    return y, (ws if keep else ws.new_empty(0))
+
+
+@siren_readout_causal_fftconv1d_op.register_fake
+def _(x, act, wout, bout, s, keep):
+    B, H, L = x.shape
+    n = _siren_conv_ws_bytes(B, H, L, act.shape[1], wout.shape[1]) if keep else 0
+    return torch.empty_like(x), x.new_empty(n, dtype=torch.uint8)
+
+
+@custom_op("nsq_hip::siren_readout_causal_fftconv1d_backward", mutates_args=("state",))
+def siren_readout_causal_fftconv1d_backward_op(
+        g: torch.Tensor, x: torch.Tensor, act: torch.Tensor, wout: torch.Tensor, bout: Optional[torch.Tensor],
+        s: Optional[torch.Tensor], state: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                 torch.Tensor, torch.Tensor]:
+    """``(gx, gact [HD + 1, K] (ones row zero), gwout, gbout, gs)``, gbout / gs empty without bout / s; a non-empty
+    ``state`` is the forward's workspace and is consumed (overwritten)."""
+    lib = _lib.get_lib()
+    B, H, L = x.shape
+    HD, K = wout.shape[1], act.shape[1]
+    dev = x.device
+    has = state.numel() > 0
+    ws = state if has else torch.empty(_siren_conv_ws_bytes(B, H, L, K, HD), dtype=torch.uint8, device=dev)
+    gx = torch.empty_like(x)
+    gact = torch.empty(HD + 1, K, dtype=torch.float32, device=dev)
+    gact[HD].zero_()
+    gwout = torch.empty_like(wout)
+    gbout = torch.empty(H if bout is not None else 0, dtype=torch.float32, device=dev)
+    gs = torch.empty(H if s is not None else 0, dtype=torch.float32, device=dev)
+    _lib.check(lib.nsq_siren_fftconv1d_causal_bwd(
+        g.data_ptr(), x.data_ptr(), act.data_ptr(), act.stride(0), wout.data_ptr(), _opt(bout), HD, _opt(s),
+        gx.data_ptr(), gact.data_ptr(), gwout.data_ptr(), _opt(gbout), _opt(gs), _lib.dtype_code(x.dtype), B, H, L,
+        K, ws.data_ptr(), ws.numel(), int(has), _lib.stream_ptr(dev)))
+    return gx, gact, gwout, gbout, gs
+
+
+@siren_readout_causal_fftconv1d_backward_op.register_fake
+def _(g, x, act, wout, bout, s, state):
+    H = x.shape[1]
+    return (torch.empty_like(x), act.new_empty(act.shape), torch.empty_like(wout),
+            wout.new_empty(H if bout is not None else 0), wout.new_empty(H if s is not None else 0))
+
+
+def _sconv_setup(ctx, inputs, output):
+    x, act, wout, bout, s, _keep = inputs
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(x, act, wout, bout, s)
+    ctx.state = output[1]  # consumed in place by the backward: kept on ctx, not saved (version checks)
+
+
+def _sconv_backward(ctx, gy, _gstate):
+    x, act, wout, bout, s = ctx.saved_tensors
+    if gy is None:
+        return (None,) * 6
+    state = ctx.state
+    ctx.state = state.new_empty(0)  # a second backward (retain_graph) recomputes the transforms
+    gx, gact, gwout, gbout, gs = siren_readout_causal_fftconv1d_backward_op(gy.to(x.dtype).contiguous(), x, act, wout,
+                                                                            bout, s, state)
+    return (gx, gact, gwout, gbout if bout is not None else None, gs.to(s.dtype) if s is not None else None, None)
+
+
+siren_readout_causal_fftconv1d_op.register_autograd(_sconv_backward, setup_context=_sconv_setup)
+
+
+def siren_conv_fits(B: int, H: int, L: int, K: int, HD: int) -> bool:
+    """Whether ``nsq_siren_fftconv1d_causal_*`` takes the shape: the 4-step plan (FFT lengths 2^15 .. 2^23,
+    ``K <= L + 1``) with ``HD`` in {16, 32, 64}.  Shorter convs run the fused plan, which reads the filter."""
+    return _siren_conv_ws_bytes(B, H, L, K, HD) > 0
+
+
+def siren_causal_fftconv1d(x: torch.Tensor, grid: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor | None,
+                           hidden_w: Sequence[torch.Tensor], hidden_b: Sequence[torch.Tensor] | None,
+                           wout: torch.Tensor, bout: torch.Tensor | None,
+                           shortcut: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal 1D FFT conv of ``x [B, H, L]`` with the SIREN filter at the ``K`` points of ``grid [K, 1]``:
+    ``causal_fftconv1d_bhl(x, siren_filter(grid, ...), shortcut)`` with the same arguments, computed without the
+    filter ``[H, K]`` or its gradient in HBM where :func:`siren_conv_fits` (else exactly that composition).
+
+    The forward transforms the HD + 1 activation rows once and forms each channel's filter transform as
+    ``sum_j wout[h, j] C(a_j) + bout[h] C(1)`` (the column pass C is linear); the backward reads the filter
+    gradient's spectrum once for the readout's gradients (the inverse column pass's adjoint is C / N) and
+    inverse-transforms only the HD rows of ``wout^T`` times it.  fp32 arithmetic; results equal the composition's
+    to fp32 rounding (different summation order)."""
+    if x.ndim != 3:
+        raise ValueError(f"x must be [B, H, L]; got shape {tuple(x.shape)}")
+    B, H, L = x.shape
+    K = grid.shape[0]
+    if wout.shape[0] != H:
+        raise ValueError(f"the filter has {wout.shape[0]} channels, x has {H}")
+    HD = wout.shape[1]
+    if not (x.is_cuda and siren_conv_fits(B, H, L, K, HD)):
+        from .fftconv_hip import causal_fftconv1d_bhl
+        return causal_fftconv1d_bhl(x, siren_filter(grid, w0, b0, hidden_w, hidden_b, wout, bout), shortcut)
+    from .fftconv_hip import _grad_wanted, _within_budget
+    from .layout import channels_first_contiguous
+    f = lambda t: None if t is None else t.float().contiguous()  # noqa: E731
+    wh = torch.cat([w.float().reshape(-1) for w in hidden_w])
+    bh = None if hidden_b is None else torch.cat([b.float().reshape(-1) for b in hidden_b])
+    act = siren_mlp_op(f(grid), f(w0), f(b0), wh, bh, len(hidden_w), HD)
+    in_dtype = x.dtype
+    cdt = in_dtype if in_dtype in _lib.NSQ_DTYPE else torch.float32
+    xc = channels_first_contiguous(x.to(cdt))
+    sc = None
+    if shortcut is not None:
+        if shortcut.shape != (H,):
+            raise ValueError(f"shortcut must have shape ({H},); got {tuple(shortcut.shape)}")
+        sc = shortcut.to(in_dtype).to(cdt).contiguous()
+    wo, bo = f(wout), f(bout)
+    keep = _grad_wanted(xc, act, wo, bo, sc) and _within_budget(_siren_conv_ws_bytes(B, H, L, K, HD), x.device) > 0
+    y, _ = siren_readout_causal_fftconv1d_op(xc, act, wo, bo, sc, keep)
+    return y.to(in_dtype)
 
 
 def siren_grid(cache_L: Sequence[int], cache_m: Sequence[float], seq_lens: Sequence[int], device=None) -> torch.Tensor:
@@ -537,3 +727,23 @@ class HipSIRENKernelND(torch.nn.Module):
         shape = grid.shape[:-1]
         k = self._filter(grid.reshape(-1, self.data_dim), conditioning)
         return k.reshape(k.shape[0], self.out_dim, *shape)
+
+    def causal_fftconv1d(self, x: torch.Tensor, shortcut: torch.Tensor | None = None,
+                         conditioning: torch.Tensor | None = None) -> torch.Tensor:
+        """``CKConvND``'s causal 1D conv with this generator's filter and an identity mask (``ckconv_nd.py:1149-1164``
+        then ``fftconv.py:546-600``): ``x [B, out_dim, L]`` convolved with the filter at the ``L`` causal points of
+        the ``2L - 1`` grid, plus ``shortcut * x``; equal to ``causal_fftconv1d_bhl(x, self.kernel_bhl((L,), causal=
+        True), shortcut)``.  Without FiLM conditioning the filter and its gradient never reach HBM where the shape
+        takes the 4-step plan (:func:`siren_causal_fftconv1d`); with it, the per-sample filters are formed and
+        convolved."""
+        assert self.data_dim == 1, "the causal conv is 1D"
+        L = x.shape[-1]
+        grid = self._grid((L,))
+        pts = grid[grid.shape[0] // 2:].reshape(-1, 1)
+        if conditioning is not None and self.film_generator is not None:
+            from .fftconv_hip import causal_fftconv1d_bhl
+            return causal_fftconv1d_bhl(x, self._filter(pts, conditioning), shortcut)
+        pe = self.positional_embedding.linear
+        hb = [lin.bias for lin in self.hidden_linears] if self.hidden_linears[0].bias is not None else None
+        return siren_causal_fftconv1d(x, pts, pe.weight, pe.bias, [lin.weight for lin in self.hidden_linears], hb,
+                                      self.out_linear.weight, self.out_linear.bias, shortcut)

@@ -417,7 +417,7 @@ def test_retain_graph_second_backward_matches_first():
     assert torch.equal(gx1, x.grad) and torch.equal(gk1, k.grad)
 
 
-# --- per-sample (FiLM) filters [B, H, K] ---------------------
+# --- per-sample (FiLM) filters [B, H, K] ------------------------------------------
 @pytest.mark.parametrize("B,H,L,K", [(3, 16, 256, 7), (2, 8, 1000, 2000), (2, 5, 4096, 4096), (4, 3, 64, 64),
                                      (2, 3, 16384, 16384), (3, 2, 65536, 1000), (2, 2, 20000, 9000)])
 def test_per_sample_filters_fwd_bwd(B, H, L, K):

@@ -1,9 +1,10 @@
-"""GPU parity of the Hyena-gated causal FFT conv (fused gates) against the CPU oracle composition.
+"""GPU parity of the Hyena-gated causal FFT conv against the CPU oracle composition.
 
-Covers the fused plan (FFT length <= 16384, one kernel each way, including the K > L+1 fold), the multi-kernel plan
-(elementwise gate kernels around the 4-step conv), every gate pair the reference configs use (SiLU / Sigmoid,
-Identity), per-sample filters and bf16 I/O.  Tolerances: rel-L2 <= 1e-4 fp32, <= 2e-2 bf16.  The reference
-computes gradients with autograd through the composition; the oracle does the same on the CPU.
+Covers the fused plan (FFT length <= 16384: the gated forward kernel below 2^22 elements, gate kernels around the
+plain fused kernel above, including the K > L+1 fold), the multi-kernel plan (elementwise gate kernels around the
+4-step conv), every gate pair the reference configs use (SiLU / Sigmoid, Identity), per-sample filters and bf16
+I/O.  Tolerances: rel-L2 <= 1e-4 fp32, <= 2e-2 bf16.  The reference computes gradients with autograd through the
+composition; the oracle does the same on the CPU.  The two forward routes of the fused plan give the same bits.
 """
 
 import pytest
@@ -17,7 +18,7 @@ from oracle.gated_ref import gated_causal_fftconv1d_torch
 pytestmark = pytest.mark.gpu
 
 
-def _check(B, H, L, K, g1, g2, kb=1, dtype=torch.float32, tol=1e-4, shortcut=True, fuse_bwd=False):
+def _check(B, H, L, K, g1, g2, kb=1, dtype=torch.float32, tol=1e-4, shortcut=True):
     torch.manual_seed(B * 131 + L + K)
     q, k, v = (torch.randn(B, H, L).to(dtype).requires_grad_(True) for _ in range(3))
     w = (torch.randn(kb, H, K) / K ** 0.5).requires_grad_(True)
@@ -27,7 +28,7 @@ def _check(B, H, L, K, g1, g2, kb=1, dtype=torch.float32, tol=1e-4, shortcut=Tru
     y_ref.backward(g)
     qg, kg, vg, wg = (t.detach().cuda().requires_grad_(True) for t in (q, k, v, w))
     sg = s.detach().cuda().requires_grad_(True) if shortcut else None
-    y = hyena_gated_causal_fftconv1d_bhl(qg, kg, vg, wg, sg, g1, g2, fuse_backward_gates=fuse_bwd)
+    y = hyena_gated_causal_fftconv1d_bhl(qg, kg, vg, wg, sg, g1, g2)
     y.backward(g.cuda())
     assert y.dtype == dtype
     assert rel_l2(y_ref, y) < tol
@@ -40,7 +41,6 @@ def _check(B, H, L, K, g1, g2, kb=1, dtype=torch.float32, tol=1e-4, shortcut=Tru
 @pytest.mark.parametrize("B,H,L,K", [(2, 16, 1024, 1024), (3, 8, 300, 17), (2, 4, 100, 180), (1, 4, 8192, 8192)])
 def test_fused_plan(B, H, L, K, g1, g2):
     _check(B, H, L, K, g1, g2)
-    _check(B, H, L, K, g1, g2, fuse_bwd=True)  # the one-kernel gated adjoint
 
 
 @pytest.mark.parametrize("g1,g2", [("silu", "sigmoid"), ("identity", "identity")])
@@ -54,13 +54,11 @@ def test_multi_kernel_plan(B, H, L, K, g1, g2):
 def test_per_sample_filters_and_no_shortcut(L):
     _check(3, 4, L, 257, "silu", "sigmoid", kb=3)
     _check(2, 4, L, 64, "silu", "sigmoid", shortcut=False)
-    _check(3, 4, L, 257, "silu", "sigmoid", kb=3, fuse_bwd=True)
 
 
 @pytest.mark.parametrize("L", [4096, 65536])
 def test_bf16_io(L):
     _check(2, 8, L, L, "silu", "sigmoid", dtype=torch.bfloat16, tol=2e-2)
-    _check(2, 8, L, L, "silu", "sigmoid", dtype=torch.bfloat16, tol=2e-2, fuse_bwd=True)
 
 
 def test_modules_as_gates_and_default_second_gate():
@@ -101,3 +99,33 @@ def test_multi_kernel_plan_odd_numel_bf16_and_split_views():
     with torch.no_grad():
         y0 = hyena_gated_causal_fftconv1d_bhl(q, kk, v, wg, sg, "silu", "sigmoid")
     assert torch.equal(y0, y)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_plan_forward_routes_agree(dtype):
+    """B*H*L = 2^22 runs the gate kernels around the plain fused kernel, each half (2^21) the gated kernel: the
+    same bits, outputs and gradients; and the large call against the oracle."""
+    B, H, L, K = 4, 128, 8192, 8192
+    print(f"gated routes B={B} H={H} L={L} {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(B, H, L, generator=gen).to(dtype) for _ in range(3))
+    w = torch.randn(H, K, generator=gen) / K ** 0.5
+    s = torch.randn(H, generator=gen).to(dtype)
+    g = torch.randn(B, H, L, generator=gen).to(dtype)
+
+    def run(sl):
+        ts = [t[sl].cuda().requires_grad_(True) for t in (q, k, v)]
+        wg, sg = w.cuda().requires_grad_(True), s.cuda().requires_grad_(True)
+        y = hyena_gated_causal_fftconv1d_bhl(*ts, wg, sg, "silu", "sigmoid")
+        y.backward(g[sl].cuda())
+        return y.detach(), [t.grad for t in ts], wg.grad, sg.grad
+
+    y, gq, gw, gs = run(slice(0, B))
+    halves = [run(slice(0, B // 2)), run(slice(B // 2, B))]
+    assert torch.equal(y, torch.cat([h[0] for h in halves]))
+    for i in range(3):
+        assert torch.equal(gq[i], torch.cat([h[1][i] for h in halves]))
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert rel_l2(halves[0][2] + halves[1][2], gw) < 1e-5 and rel_l2(halves[0][3] + halves[1][3], gs) < tol
+    y_ref = gated_causal_fftconv1d_torch(q, k, v, w, s, "silu", "sigmoid")
+    assert rel_l2(y_ref, y) < tol

@@ -1,4 +1,4 @@
-"""GPU parity of the HIP SIREN filter generation (row F1) against the CPU restatement (oracle/siren_ref.py).
+"""GPU parity of the HIP SIREN filter generation against the CPU restatement (oracle/siren_ref.py).
 
 The reference network (kernels_nd.py:876-1190 without FiLM) at the shapes its configs use (embedding and
 hidden width 32, 3 layers, 160-384 channels; examples/vit5_imagenet: KERNEL_* settings) and the long 1D
@@ -275,7 +275,7 @@ def test_film_module_forward_and_kernel_bhl():
 
 
 def test_film_filters_drive_the_per_sample_causal_conv():
-    """End to end (rows F1 and F3): FiLM-conditioned filters [B, H, L] on the causal half of the grid feed the HIP
+    """End to end: FiLM-conditioned filters [B, H, L] on the causal half of the grid feed the HIP
     causal FFT conv as per-sample filters; output and gradients (input, SIREN weights, every gamma and beta) against
     the same chain on the CPU oracle in float32, rel-L2 <= 1e-4."""
     from nvsubquadratic_amd.fftconv_hip import causal_fftconv1d_bhl

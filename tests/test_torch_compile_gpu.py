@@ -1,4 +1,4 @@
-"""torch.compile through the HIP ops (build-plan row A5).
+"""torch.compile through the HIP ops.
 
 The reference runs Hyena under torch.compile (experiments/run.py:193-197) and checks that compiled
 outputs and gradients match eager (tests/modules/test_torch_compile.py:153-163: rtol/atol 1e-4 for
@@ -17,6 +17,7 @@ from nvsubquadratic_amd import causal_conv1d_hip as CC
 from nvsubquadratic_amd import fftconv_hip as F
 from nvsubquadratic_amd import gated_fftconv_hip as G
 from nvsubquadratic_amd import mixed_fftconv_hip as M
+from nvsubquadratic_amd import siren_hip as S
 from nvsubquadratic_amd.modules import HipCausalConv1d
 from oracle.circular_ref import mixed_fftconv_torch
 from oracle.direct_ref import b2b_causal_conv1d_torch, causal_conv1d_torch
@@ -162,6 +163,10 @@ def _opchecks():
     xb = torch.randn(2, 12, 300, **d)
     q, kg, v = (torch.randn(2, 4, 256, **d) for _ in range(3))
     qn, kgn, vn = (torch.randn(2, 4, 12, 10, **d) for _ in range(3))
+    gs = torch.linspace(0, 1, 8200, **d).reshape(-1, 1)  # SIREN grid [G, 1]
+    w0, b0 = torch.randn(16, 1, **d), torch.randn(16, **d)
+    wh, bh = torch.randn(2 * 16 * 16, **d) / 4, torch.randn(2 * 16, **d)
+    act = torch.cat([torch.randn(16, 8200, **d), torch.ones(1, 8200, **d)])  # [a^T; 1]
     return [
         (F.causal_fftconv1d_op, (x1, k1, s1, 1, False)),
         (F.fftconv_nd_op, (x2, k2, s1, 1, 0, False)),
@@ -169,12 +174,15 @@ def _opchecks():
         (F.shifted_fftconv1d_op, (x1, k1, s1, 1, 1)),
         (CC.causal_conv1d_op, (xc, wc, bc, 1)),
         (CC.b2b_causal_conv1d_op, (xb, torch.randn(12, 3, **d), torch.randn(4, 16, **d), torch.randn(4, **d))),
-        (G.gated_causal_fftconv1d_op, (q, kg, v, k1, s1, 2, 1, 1, True, False)),
+        (G.gated_causal_fftconv1d_op, (q, kg, v, k1, s1, 2, 1, 1, True)),
         (G.gated_fftconv_nd_op, (qn, kgn, vn, k2, s1, 2, 1, 1, 0, True)),
+        (S.siren_mlp_op, (gs, w0, b0, wh, bh, 2, 16)),
+        (S.siren_readout_causal_fftconv1d_op, (torch.randn(1, 4, 8200, **d), act, torch.randn(4, 16, **d),
+                                               torch.randn(4, **d), s1, True)),
     ]
 
 
-@pytest.mark.parametrize("i", range(8))
+@pytest.mark.parametrize("i", range(10))
 def test_opcheck(i):
     op, args = _opchecks()[i]
     args = tuple(a.requires_grad_(True) if isinstance(a, torch.Tensor) and a.is_floating_point() else a
