@@ -133,6 +133,53 @@ def measured_traffic() -> int | None:
     return int(round(total)) if total else None
 
 
+# ---------------------------------------------------------------------------
+# The reference's unfused PyTorch path on the same GPU, timed beside this build's kernels (report-only fields
+# "torch_gpu_ms_per_step" and "speedup_vs_torch_gpu"): the reference publishes its fused kernels only as speedups
+# over that path (docs/benchmarks.md:47-49, 78-81).  These restate its torch ops: the causal 1D conv of
+# ops/fftconv.py:546-600, the 2D / 3D convs of :662-733 / :736-812 at the reference's own FFT sizes, and the B2B
+# block (projection conv, gate, mixer conv with skip, gate) as separate depthwise torch convs and products.
+# ---------------------------------------------------------------------------
+def _torch_causal_fftconv1d(x, k, s):
+    L, K = x.shape[-1], k.shape[-1]
+    n = min(L + K, 2 * L)
+    y = torch.fft.irfft(torch.fft.rfft(x.float(), n=n) * torch.fft.rfft(k.float(), n=n), n=n)[..., :L].to(x.dtype)
+    return y if s is None else y + s.to(x.dtype).view(1, -1, 1) * x
+
+
+def _torch_fftconv_nd(x, k, s):
+    nd = x.ndim - 2
+    S, Kd = x.shape[2:], k.shape[-nd:]
+    fs = [min(Si + (Ki + 1) // 2, 2 * Si) for Si, Ki in zip(S, Kd)]
+    dims = tuple(range(2, 2 + nd))
+    kdims = tuple(range(k.ndim - nd, k.ndim))
+    full = torch.fft.irfftn(torch.fft.rfftn(x.float(), s=fs, dim=dims) * torch.fft.rfftn(k.float(), s=fs, dim=kdims),
+                            s=fs, dim=dims)
+    y = full[(Ellipsis, *[slice(Ki // 2, Ki // 2 + Si) for Si, Ki in zip(S, Kd)])].to(x.dtype)
+    return y + s.view(1, -1, *([1] * nd)).to(x.dtype) * x
+
+
+def _torch_b2b(x, wp, wm, skip):
+    import torch.nn.functional as Fn
+
+    C, L = x.shape[1] // 3, x.shape[-1]
+    p = Fn.conv1d(x.float(), wp.unsqueeze(1), padding=wp.shape[-1] - 1, groups=3 * C)[..., :L]
+    q, kk, v = p.split(C, dim=1)
+    z = kk * v
+    h = Fn.conv1d(z, wm.unsqueeze(1), padding=wm.shape[-1] - 1, groups=C)[..., :L]
+    if skip is not None:
+        h = h + skip.view(1, -1, 1) * z
+    return (q * h).to(x.dtype)
+
+
+def _torch_gpu_ms(step, steps: int = 5, warmup: int = 1) -> float:
+    """Mean ms per step of a torch-path step on the current stream (freed afterwards)."""
+    t = statistics.mean(_time_steps(step, steps, warmup))
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return round(t, 4)
+
+
 def cpu_baseline_other(name: str, iters: int = 3) -> dict:
     """The oracle (float32 torch on all the host cores) on the whole of config 1, 2, 4 or 5, the phase the GPU line
     times: at least ``iters`` steps after a warmup, more while under ~10 s; the median step."""
@@ -250,6 +297,10 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare
 
         def step():
             F.causal_fftconv1d_fwd_raw(c.x, c.k, c.s, y)
+
+        def step_torch():
+            with torch.no_grad():
+                _torch_causal_fftconv1d(c.x, c.k, c.s)
     elif name == "cfg2":
         B, C, L, Kp, Km = 4, 4096, 8192, 3, 128
         x = torch.randn(B, 3 * C, L, device=dev, generator=gen).to(torch.bfloat16)
@@ -263,6 +314,10 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare
         def step():
             with torch.no_grad():
                 CC.b2b_causal_conv1d(x, wp, wm, None)
+
+        def step_torch():
+            with torch.no_grad():
+                _torch_b2b(x, wp, wm, None)
     elif name == "cfg2-fwd-bwd":
         # report-only: the config-2 block with its backward (autograd), skip = 0 as in config 2
         B, C, L, Kp, Km = 4, 4096, 8192, 3, 128
@@ -294,6 +349,10 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare
             def step():
                 with torch.no_grad():
                     fn(x, k, s)
+
+            def step_torch():
+                with torch.no_grad():
+                    _torch_fftconv_nd(x, k, s)
         else:
             xg, kg, sg = (t.detach().requires_grad_(True) for t in (x, k, s))
             g = torch.randn(x.shape, device=dev, generator=gen).to(torch.bfloat16)
@@ -301,6 +360,10 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare
             def step():
                 xg.grad = kg.grad = sg.grad = None
                 fn(xg, kg, sg).backward(g)
+
+            def step_torch():
+                xg.grad = kg.grad = sg.grad = None
+                _torch_fftconv_nd(xg, kg, sg).backward(g)
     elif name in ("cfg4-circular", "well-rb"):
         # periodic boundaries (report-only): cfg4's shape with fft_padding="circular" (FFT 128^2, no padding),
         # and the rayleigh_benard Hyena layer (examples/well/v2/rayleigh_benard/hyena.py: 512x128 / patch 8 =
@@ -521,6 +584,10 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare
     ms_list = _time_steps(step, steps, warmup)
     ms = statistics.mean(ms_list)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    if compare and name in ("cfg1", "cfg2", "cfg4", "cfg5"):
+        _log("reference torch path on the GPU")
+        extra["torch_gpu_ms_per_step"] = _torch_gpu_ms(step_torch)
+        extra["speedup_vs_torch_gpu"] = round(extra["torch_gpu_ms_per_step"] / ms, 2)
     if name in _COUNTER_PROFILES:
         extra["roofline_traffic_source"] = f"profiles/{_COUNTER_PROFILES[name]}"
     if cpu and name in ("cfg1", "cfg2", "cfg4", "cfg5"):
@@ -546,7 +613,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-compare", action="store_true",
-                    help="report-only workloads: skip the comparison variants (torch ops, unfused compositions)")
+                    help="skip the comparison variants (the reference's torch path on the GPU, unfused compositions)")
     ap.add_argument("--cpu-channels", type=int, default=1024)
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true")
@@ -660,6 +727,16 @@ def main() -> None:
             "fft_tflops_radix2_count": round(flops / (ms * 1e-3) / 1e12, 2),
         },
     }
+    if not args.no_compare:
+        _log("reference torch path on the GPU")
+        xg, kg, sg = (t.detach().requires_grad_(True) for t in (c.x, c.k, c.s))
+
+        def step_torch():
+            xg.grad = kg.grad = sg.grad = None
+            _torch_causal_fftconv1d(xg, kg, sg).backward(c.g)
+
+        out["torch_gpu_ms_per_step"] = _torch_gpu_ms(step_torch, steps=3)
+        out["speedup_vs_torch_gpu"] = round(out["torch_gpu_ms_per_step"] / ms, 2)
     if not args.no_cpu:
         _log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(args.cpu_channels, args.cpu_iters)
