@@ -173,3 +173,27 @@ def test_module_causal_conv_matches_kernel_bhl():
     assert rel_l2(yr, y) < 1e-5
     for a, p in zip(gm, m.parameters()):
         assert rel_l2(p.grad, a) < 1e-4
+
+
+@pytest.mark.parametrize("B,H,L,K", [(1, 8, 20000, 5000), (2, 4, 12000, 12001)])
+def test_filter_length_other_than_l(B, H, L, K):
+    """K < L (a shorter filter grid) and K = L + 1, against the reference chain."""
+    print(f"siren conv K != L B={B} H={H} L={L} K={K}", flush=True)
+    grid = siren_grid((K,), (1.0,), (K,))[K - 1:].contiguous()  # K points
+    w0, b0, hw, hb, wo, bo = siren_params(1, 32, 32, 2, H, seed=12)
+    gen = torch.Generator().manual_seed(13)
+    x = torch.randn(B, H, L, generator=gen)
+    s = torch.randn(H, generator=gen)
+    g = torch.randn(B, H, L, generator=gen)
+    assert siren_conv_fits(B, H, L, K, 32)
+    leaves = [w0, b0, *hw, *hb, wo, bo, x, s]
+    ref = [t.clone().requires_grad_(True) for t in leaves]
+    yr = causal_fftconv1d_torch(ref[8], siren_mlp_torch(grid, ref[0], ref[1], ref[2:4], ref[4:6], ref[6], ref[7]).t(),
+                                ref[9])
+    yr.backward(g)
+    hip = [t.cuda().requires_grad_(True) for t in leaves]
+    yh = siren_causal_fftconv1d(hip[8], grid.cuda(), hip[0], hip[1], hip[2:4], hip[4:6], hip[6], hip[7], hip[9])
+    yh.backward(g.cuda())
+    assert rel_l2(yr, yh) < 2e-5
+    for r, h in zip(ref, hip):
+        assert rel_l2(r.grad, h.grad) < 1e-4, r.shape
