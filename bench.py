@@ -261,11 +261,25 @@ _COUNTER_PROFILES = {"cfg1": "fftconv1d_causal_cfg1_fwd_counters.md", "cfg2": "b
                      "cfg4": "fftconv2d_cfg4_fwd_counters.md", "cfg5": "fftconv3d_cfg5_fwd_bwd_counters.md"}
 
 
-def _time_steps(step, steps: int, warmup: int) -> list[float]:
-    """Event-timed steps on the current stream (ms each) after untimed warmup."""
+def _time_steps(step, steps: int, warmup: int, min_warm_s: float = 0.25) -> list[float]:
+    """Event-timed steps on the current stream (ms each) after untimed warmup.
+
+    The warmup runs ``warmup`` steps (which hold the first-call costs), then more for at least ``min_warm_s``
+    seconds: a sub-millisecond step otherwise gets timed while the GPU clock is still ramping (0.31 against 0.27 ms
+    for config 2's forward).
+    """
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < min_warm_s and n < 10000:
+        step()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()  # count the device's time, not the enqueue rate
+    torch.cuda.synchronize()
+    _log(f"warmup: {warmup} + {n} steps")
     stream = torch.cuda.current_stream()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record(stream)

@@ -126,8 +126,8 @@ __global__ __launch_bounds__(kConvThreads) void b2b_fwd_kernel(const typename El
 // after each phase:
 //   1. the staged rows (registers, loaded during the previous tile) go to LDS,
 //      and the next tile's loads are issued;
-//   2. z = k*v for the tile's 2048 positions into the padded window buffer
-//      (zero at positions >= L), q into qs;
+//   2. z = k*v for the tile's 2048 positions into the window buffer (split
+//      layout; zero at positions >= L), q into qs;
 //   3. MFMA: two interleaved 16-block M-tiles per wave; out = q*(y + skip*z)
 //      into qs;
 //   4. row stores; the last Km - 1 z values move to the window's front.
@@ -147,7 +147,7 @@ struct B2BMfmaLds {
     k = up8(qwords);
     v = k + up8(kConvTile + hk + 2 * kConvPer);
     z = v + up8(kConvTile + hk + 2 * kConvPer);
-    wq = z + up8(conv_pad_words(mfma_src_count<NS>()));
+    wq = z + win_words(mfma_src_count<NS>());
     wk = wq + up8(Kp);
     wv = wk + up8(Kp);
     wm = wv + up8(Kp);
@@ -155,10 +155,15 @@ struct B2BMfmaLds {
   }
 };
 
-// Output-tile slot of position p: 16 words of pad per 64 so that the four
-// 64-word-apart lane groups of an MFMA epilogue use distinct banks; runs of 8
-// from a multiple of 8 stay contiguous.
-__device__ __forceinline__ int qs_pad(int p) { return p + 16 * (p >> 6); }
+// Output-tile slot of position p (kConvTile + kConvTile / 4 words per tile):
+// runs of 8 from a multiple of 8 stay contiguous; 4 words of pad per 32 put
+// the 16-byte writes of 8 consecutive lanes (stride 8) on distinct banks, and
+// a further 8 per 64 puts the 4-byte epilogue reads of two lane groups 64
+// positions apart on opposite 16-bank halves.
+__device__ __forceinline__ int qs_pad(int p) { return p + 4 * (p >> 5) + 8 * (p >> 6); }
+// qs_pad(p0 + 16 r) - qs_pad(p0) for p0 % 64 < 16, r < 4 (an MFMA lane's epilogue
+// positions: the lane's base slot plus a constant).
+__device__ __forceinline__ constexpr int qs_step(int r) { return 16 * r + 4 * (r >> 1); }
 
 // acc[e] += sum_{j<4} wl[j] xs[base + e + j] (taps >= K are zero in wl).
 __device__ __forceinline__ void slide_fma4(float (&acc)[kConvPer], const float* xs, int base, const float* wl) {
@@ -222,7 +227,10 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
   const typename Elem<DT>::T* xq = x + (int64_t(b) * 3 * C + c) * L;
   const typename Elem<DT>::T* xk = xq + int64_t(C) * L;
   const typename Elem<DT>::T* xv = xk + int64_t(C) * L;
-  const int hz = Km - 1, hp = Kp - 1, hk = lay.hk;
+  // the band gets d leading zero taps so that the z halo hz = Km - 1 + d is a
+  // multiple of 4: a thread's 8 z values are two aligned 16-byte writes
+  const int d = ((Km - 1 + 3) & ~3) + 1 - Km;
+  const int hz = Km - 1 + d, hp = Kp - 1, hk = lay.hk;
   const int t = int(threadIdx.x);
   stage_weights<false>(wlq, wp + int64_t(c) * Kp, Kp);
   stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
@@ -230,7 +238,8 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
   stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
   // the window's tail beyond the tile's last use meets zero taps: keep it finite
   constexpr int ZW = mfma_src_count<NS>();
-  for (int m = kConvTile + t; m < ZW; m += kConvThreads) zp[conv_pad(m)] = 0.f;
+  constexpr int ZR = win_half(ZW);
+  for (int m = kConvTile + t; m < ZW; m += kConvThreads) zp[win_at(m, ZR)] = 0.f;
   RowStage<DT, kConvTile + (SHORT ? 3 : kConvMaxK - 1) + 2 * kConvPer> sq;
   RowStage<DT, TF> sk, sv;
   if constexpr (PF) {
@@ -241,7 +250,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
   }
   __syncthreads();  // weights staged
   ToeplitzMfma<NS> tm;
-  tm.load_weights(wlm, Km, skip ? skip[c] : 0.f);  // h = conv(z) + skip*z: skip joins the last tap
+  tm.load_weights(wlm, Km, skip ? skip[c] : 0.f, d);  // h = conv(z) + skip*z: skip joins the last tap
   const RowBuf<DT, false> yb(y + row * L, L);
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
   const int base = t * kConvPer;
@@ -272,7 +281,8 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
       slide_proj<SHORT>(va, xs_v, bz, Kp, wlv);
       slide_proj<SHORT>(qa, xs_q, base, Kp, wlq);
 #pragma unroll
-      for (int e = 0; e < kConvPer; ++e) zp[conv_pad(hz + base + e)] = (n0 + base + e < L) ? ka[e] * va[e] : 0.f;
+      for (int e = 0; e < kConvPer; ++e) ka[e] = (n0 + base + e < L) ? ka[e] * va[e] : 0.f;
+      win_store8(zp, ZR, hz + base, ka);
       if (ti == t_begin) {
         // z at n0 - hz + m (m < hz): the causal zero padding before the row
         // start, else recomputed from the staged halo
@@ -286,7 +296,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
               vv = fmaf(wlv[j], xs_v[i0 + j], vv);
             }
           }
-          zp[conv_pad(m)] = kv * vv;
+          zp[win_at(m, ZR)] = kv * vv;
         }
       }
       __syncthreads();  // the q stage is consumed: q takes its place
@@ -301,22 +311,23 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(PF
     {
       static_assert(kMfmaTiles == 2 * kConvWaves, "b2b MFMA: two M-tiles per wave");
       nsq_f32x4_t acc0, acc1;
-      tm.run2(zp, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      tm.run2(zp, ZR, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int mt = wave + h * kConvWaves;
+        const float* ql = qs + qs_pad(16 * (16 * mt + 4 * (l >> 4)) + (l & 15));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p = 16 * (16 * mt + 4 * (l >> 4) + r) + (l & 15);
           const float hv = h ? acc1[r] : acc0[r];
-          yb.store_elem(n0 + p, qs[qs_pad(p)] * hv);
+          yb.store_elem(n0 + p, ql[qs_step(r)] * hv);
         }
       }
     }
     __syncthreads();
     // 4. z of the next tile's halo to the window front (ordered before the
     //    next tile's reads by its first barrier)
-    for (int m = t; m < hz; m += kConvThreads) zp[conv_pad(m)] = zp[conv_pad(kConvTile + m)];
+    for (int m = t; m < hz; m += kConvThreads) zp[win_at(m, ZR)] = zp[win_at(kConvTile + m, ZR)];
   }
 }
 
@@ -336,7 +347,8 @@ __device__ __forceinline__ void load_taps4(float (&w4)[4], const float* __restri
 //       workspace; and the mixer weight gradient of each tile as an MFMA
 //       product over the same windows,
 //         D[i][t] += sum_a gh[16a + i] * zwin[16a + t],  gw[j] = sum_i D[i][i + j]
-//       (zwin[m] = z[n0 - hz + m]; t = i + j < 4 NS), kept in registers over
+//       (zwin[m] = z[n0 - hz + m]; t = i + j + d < 4 NS, d the band's leading
+//       zero taps), kept in registers over
 //       the workgroup's tiles and reduced in a fixed order (waves, then the
 //       diagonal) into a per-workgroup partial;
 //  bwd2: gz = corr(gh; w_mixer) + skip*gh on the reversed band over a forward
@@ -383,14 +395,17 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
   const typename Elem<DT>::T* xq = x + (int64_t(b) * 3 * C + c) * L;
   const typename Elem<DT>::T* xk = xq + int64_t(C) * L;
   const typename Elem<DT>::T* xv = xk + int64_t(C) * L;
-  const int hz = Km - 1, hp = Kp - 1, hk = lay.f.hk;
+  // d leading zero taps: the z halo hz = Km - 1 + d is a multiple of 4 (as in the forward)
+  const int d = ((Km - 1 + 3) & ~3) + 1 - Km;
+  const int hz = Km - 1 + d, hp = Kp - 1, hk = lay.f.hk;
   const int t = int(threadIdx.x);
   stage_weights<false>(wlq, wp + int64_t(c) * Kp, Kp);
   stage_weights<false>(wlk, wp + int64_t(C + c) * Kp, Kp);
   stage_weights<false>(wlv, wp + int64_t(2 * C + c) * Kp, Kp);
   stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
   constexpr int ZW = mfma_src_count<NS>();
-  for (int m = kConvTile + t; m < ZW; m += kConvThreads) zp[conv_pad(m)] = 0.f;
+  constexpr int ZR = win_half(ZW);
+  for (int m = kConvTile + t; m < ZW; m += kConvThreads) zp[win_at(m, ZR)] = 0.f;
   RowStage<DT, kConvTile + (SHORT ? 3 : kConvMaxK - 1) + 2 * kConvPer> sq;
   RowStage<DT, TF> sk, sv;
   {
@@ -401,7 +416,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
   }
   __syncthreads();  // weights staged
   ToeplitzMfma<NS> tm;
-  tm.load_weights(wlm, Km, skip ? skip[c] : 0.f);  // h = conv(z) + skip*z
+  tm.load_weights(wlm, Km, skip ? skip[c] : 0.f, d);  // h = conv(z) + skip*z
   const RowBuf<DT, false> gb(g + row * L, L);
   const RowBuf<NSQ_DTYPE_F32, false> gqb(gp + (int64_t(b) * 3 * C + c) * L, L);
   const RowBuf<NSQ_DTYPE_F32, false> ghb(ghw + row * L, L);
@@ -433,7 +448,8 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
       slide_proj<SHORT>(va, xs_v, bz, Kp, wlv);
       slide_proj<SHORT>(qa, xs_q, base, Kp, wlq);
 #pragma unroll
-      for (int e = 0; e < kConvPer; ++e) zp[conv_pad(hz + base + e)] = (n0 + base + e < L) ? ka[e] * va[e] : 0.f;
+      for (int e = 0; e < kConvPer; ++e) ka[e] = (n0 + base + e < L) ? ka[e] * va[e] : 0.f;
+      win_store8(zp, ZR, hz + base, ka);
       if (ti == t_begin) {
         for (int m = t; m < hz; m += kConvThreads) {
           const int64_t n = n0 - hz + m;
@@ -445,7 +461,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
               vv = fmaf(wlv[j], xs_v[i0 + j], vv);
             }
           }
-          zp[conv_pad(m)] = kv * vv;
+          zp[win_at(m, ZR)] = kv * vv;
         }
       }
       __syncthreads();  // the q stage is consumed: q takes its place
@@ -457,7 +473,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
     // 3. h on the MFMA band; gq = g*h, gh = g*q (positions >= L: g reads 0)
     {
       nsq_f32x4_t acc0, acc1;
-      tm.run2(zp, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      tm.run2(zp, ZR, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
       float gv[8];
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -468,31 +484,36 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        const int ql = qs_pad(16 * (16 * (wave + h * kConvWaves) + 4 * kk) + li);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p = 16 * (16 * (wave + h * kConvWaves) + 4 * kk + r) + li;
           const float hv = h ? acc1[r] : acc0[r];
-          const float ghv = gv[4 * h + r] * qs[qs_pad(p)];
+          const float ghv = gv[4 * h + r] * qs[ql + qs_step(r)];
           gqb.store_elem(n0 + p, gv[4 * h + r] * hv);
           ghb.store_elem(n0 + p, ghv);
-          ghs[qs_pad(p)] = ghv;
+          ghs[ql + qs_step(r)] = ghv;
         }
       }
     }
     __syncthreads();
     // 4. mixer weight gradient of the tile: wave w takes blocks [32w, 32w + 32)
+    //    (qs_pad(16 (a0 + kk) + li) = 20 a0 + 16 kk + 4 (kk / 2) + li for a0 % 4 == 0)
+    //    (win_at(16 (a0 + kk + tg) + li) = win_at(16 kk + li) + 8 (a0 + tg))
+    const float* ghl = ghs + 16 * kk + 4 * (kk >> 1) + li;
+    const float* zl = zp + win_at(16 * kk + li, ZR);
 #pragma unroll 2
     for (int a0 = 32 * wave; a0 < 32 * wave + 32; a0 += 4) {
-      const float av = ghs[qs_pad(16 * (a0 + kk) + li)];
+      const float av = ghl[20 * a0];
 #pragma unroll
       for (int tg = 0; tg < TG; ++tg) {
-        const float bv = zp[20 * (a0 + kk + tg) + li];
+        const float bv = zl[8 * (a0 + tg)];
         D[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, D[tg], 0, 0, 0);
       }
     }
     __syncthreads();
     // 5. z of the next tile's halo to the window front
-    for (int m = t; m < hz; m += kConvThreads) zp[conv_pad(m)] = zp[conv_pad(kConvTile + m)];
+    for (int m = t; m < hz; m += kConvThreads) zp[win_at(m, ZR)] = zp[win_at(kConvTile + m, ZR)];
   }
   // Fixed-order reduction: D of waves 0..3 summed into red[i][t], then
   // gw[j] = sum_i red[i][i + j].
@@ -513,7 +534,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
   }
   if (t < Km) {
     float sacc = 0.f;
-    for (int i = 0; i < 16; ++i) sacc += red[i * RW + i + t];
+    for (int i = 0; i < 16; ++i) sacc += red[i * RW + i + t + d];
     const int nparts = B * int(gridDim.y);
     const int part = b * int(gridDim.y) + int(blockIdx.y);
     gw_part[(int64_t(c) * nparts + part) * Km + t] = sacc;
@@ -522,7 +543,8 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
 
 template <int DT, int NS, bool SHORT>
 struct B2BBwd2Lds {
-  static constexpr int GWORDS = (conv_pad_words(mfma_src_count<NS>()) + 7) & ~7;
+  static constexpr int GR = win_half(mfma_src_count<NS>());
+  static constexpr int GWORDS = win_words(mfma_src_count<NS>());
   int gw, k, v, ks, vs, wk, wv, wr, total;
   __host__ __device__ static int up8(int n) { return (n + 7) & ~7; }
   __host__ __device__ B2BBwd2Lds(int Kp, int Km) {
@@ -545,6 +567,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
     const float* __restrict__ skip, const float* __restrict__ ghw, float* __restrict__ gp, int C, int L, int Kp,
     int Km) {
   constexpr int ZW = mfma_src_count<NS>();
+  constexpr int GR = B2BBwd2Lds<DT, NS, SHORT>::GR;
   constexpr int GIT = (ZW + kConvThreads - 1) / kConvThreads;
   extern __shared__ __align__(16) float smem[];
   const B2BBwd2Lds<DT, NS, SHORT> lay(Kp, Km);
@@ -595,7 +618,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
     for (int it = 0; it < GIT; ++it) {
       const int m = t + it * kConvThreads;
-      if (m < ZW) gwin[conv_pad(m)] = gstage[it];
+      if (m < ZW) gwin[win_at(m, GR)] = gstage[it];
     }
     __syncthreads();
     if (ti + 1 < t_end) load_tile(n0 + kConvTile);
@@ -617,15 +640,16 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
     // 3. gz on the reversed band; gk = gz*v, gv = gz*k
     {
       nsq_f32x4_t acc0, acc1;
-      tm.run2(gwin, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      tm.run2(gwin, GR, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        const int ql = qs_pad(16 * (16 * (wave + h * kConvWaves) + 4 * kk) + li);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p = 16 * (16 * (wave + h * kConvWaves) + 4 * kk + r) + li;
           const float gz = h ? acc1[r] : acc0[r];
-          gkb.store_elem(n0 + p, gz * vs[qs_pad(p)]);
-          gvb.store_elem(n0 + p, gz * ks[qs_pad(p)]);
+          gkb.store_elem(n0 + p, gz * vs[ql + qs_step(r)]);
+          gvb.store_elem(n0 + p, gz * ks[ql + qs_step(r)]);
         }
       }
     }
@@ -645,7 +669,8 @@ constexpr int kB2BBwdExtra = 4;  // positions past the tile with gk, gv (>= Kp -
 
 template <int NS>
 struct B2BBwd2fLds {
-  static constexpr int GWORDS = (conv_pad_words(mfma_src_count<NS>() + kB2BBwdExtra) + 7) & ~7;
+  static constexpr int GR = win_half(mfma_src_count<NS>() + kB2BBwdExtra);
+  static constexpr int GWORDS = win_words(mfma_src_count<NS>() + kB2BBwdExtra);
   static constexpr int XW = kConvTile + 3 + kB2BBwdExtra + 2 * kConvPer;  // staged x / g words per row
   static constexpr int XS = (XW + 7) & ~7;
   int gw, xq, xk, xv, gq, gk, gv, ks, vs, wq, wk, wv, wr, total;
@@ -677,6 +702,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
   constexpr int ZW = mfma_src_count<NS>() + kB2BBwdExtra;
   constexpr int GIT = (ZW + kConvThreads - 1) / kConvThreads;
   using LY = B2BBwd2fLds<NS>;
+  constexpr int GR = LY::GR;
   extern __shared__ __align__(16) float smem[];
   const LY lay(Km);
   float* gwin = smem + lay.gw;
@@ -750,7 +776,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int it = 0; it < GIT; ++it) {
       const int m = t + it * kConvThreads;
-      if (m < ZW) gwin[conv_pad(m)] = gstage[it];
+      if (m < ZW) gwin[win_at(m, GR)] = gstage[it];
     }
     // The k / v windows below read x words that other waves staged: the
     // stores above must be complete in every wave first.
@@ -782,7 +808,7 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
     // 2. gz on the band; gk = gz*v, gv = gz*k at tile positions p (LDS index p + 3)
     {
       nsq_f32x4_t acc0, acc1;
-      tm.run2(gwin, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+      tm.run2(gwin, GR, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -799,11 +825,11 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
       {
         const int p = kConvTile + wave;
         float part = 0.f;
-        for (int j = l; j < Km; j += 64) part = fmaf(wlr[j], gwin[conv_pad(p + j)], part);
+        for (int j = l; j < Km; j += 64) part = fmaf(wlr[j], gwin[win_at(p + j, GR)], part);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
         if (l == 0) {
-          const float gz = fmaf(skv, gwin[conv_pad(p)], part);
+          const float gz = fmaf(skv, gwin[win_at(p, GR)], part);
           gs_k[p + 3] = gz * vs[p];
           gs_v[p + 3] = gz * ks[p];
         }
@@ -914,18 +940,20 @@ __global__ void b2b_wgrad_reduce_kernel(const float* __restrict__ part, int npar
 // One barrier per tile hands the double-buffered z/q over; on each SIMD a
 // producer wave's VALU work overlaps a consumer wave's MFMA chain.
 // The mixer band gets `d` leading zero taps so that its halo hz = Km - 1 + d
-// is a multiple of 4: z of a tile then starts at a 16-byte boundary of the
-// padded window buffer.
+// is a multiple of 4 (fp32) or 8 (bf16 halves): z of a tile then starts at a
+// 16-byte boundary of the window buffer.
 constexpr int kB2BWsThreads = 512;
-constexpr int kB2BWsSegTiles = 8;
+constexpr int kB2BWsSegTiles = 16;  // 4, 6, 8, 12, 16, 32 measured at config 2: 16 and 32 fastest
 
-// BF (16-bit I/O): z is stored as two bf16 halves (hi, lo; ToeplitzMfmaBf16),
-// ZE padded elements each, in the words of one z buffer.
+// BF (16-bit I/O): z is stored as two plain bf16 arrays (hi, lo;
+// ToeplitzMfmaBf16), ZE elements each, in the words of one z buffer; fp32: one
+// window in the split layout (region stride ZR).
 template <int NS, bool BF = false>
 struct B2BWsLds {
   static constexpr int ZCOUNT = BF ? kConvTile + 32 * bf16_steps<NS>() - 16 : mfma_src_count<NS>();
-  static constexpr int ZE = (bpad_elems(ZCOUNT) + 15) & ~15;
-  static constexpr int ZWORDS = BF ? ZE : (conv_pad_words(mfma_src_count<NS>()) + 7) & ~7;
+  static constexpr int ZE = (ZCOUNT + 15) & ~15;
+  static constexpr int ZR = win_half(mfma_src_count<NS>());
+  static constexpr int ZWORDS = BF ? ZE : win_words(mfma_src_count<NS>());
   static constexpr int QWORDS = kConvTile + kConvTile / 4;  // qs_pad layout
   static constexpr int z0 = 0, q0 = 2 * ZWORDS, wm = 2 * ZWORDS + 2 * QWORDS;
   static constexpr int total = wm + kConvMaxK;
@@ -975,20 +1003,20 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
       __bf16* zh = reinterpret_cast<__bf16*>(zb);
       __bf16 hi, lo;
       split_bf16(v, hi, lo);
-      zh[bpad(m)] = hi;
-      zh[LY::ZE + bpad(m)] = lo;
+      zh[m] = hi;
+      zh[LY::ZE + m] = lo;
     } else {
-      zb[conv_pad(m)] = v;
+      zb[win_at(m, LY::ZR)] = v;
     }
   };
   auto zcopy = [&](float* zb, int m, const float* zo, int mo) {
     if constexpr (BF) {
       __bf16* zh = reinterpret_cast<__bf16*>(zb);
       const __bf16* oh = reinterpret_cast<const __bf16*>(zo);
-      zh[bpad(m)] = oh[bpad(mo)];
-      zh[LY::ZE + bpad(m)] = oh[LY::ZE + bpad(mo)];
+      zh[m] = oh[mo];
+      zh[LY::ZE + m] = oh[LY::ZE + mo];
     } else {
-      zb[conv_pad(m)] = zo[conv_pad(mo)];
+      zb[win_at(m, LY::ZR)] = zo[win_at(mo, LY::ZR)];
     }
   };
   if (t < kConvThreads) stage_weights<false>(wlm, wm + int64_t(c) * Km, Km);
@@ -1043,11 +1071,10 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
           l8[e] = lo;
         }
         __bf16* zh = reinterpret_cast<__bf16*>(zb);
-        *reinterpret_cast<nsq_bf16x8_t*>(zh + bpad(hz + 8 * pt)) = h8;
-        *reinterpret_cast<nsq_bf16x8_t*>(zh + LY::ZE + bpad(hz + 8 * pt)) = l8;
+        *reinterpret_cast<nsq_bf16x8_t*>(zh + hz + 8 * pt) = h8;
+        *reinterpret_cast<nsq_bf16x8_t*>(zh + LY::ZE + hz + 8 * pt) = l8;
       } else {
-        *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt)) = make_float4(zv[0], zv[1], zv[2], zv[3]);
-        *reinterpret_cast<float4*>(zb + conv_pad(hz + 8 * pt + 4)) = make_float4(zv[4], zv[5], zv[6], zv[7]);
+        win_store8(zb, LY::ZR, hz + 8 * pt, zv);
       }
       float* qd = qb + qs_pad(8 * pt);
       *reinterpret_cast<float4*>(qd) = make_float4(qa[0], qa[1], qa[2], qa[3]);
@@ -1100,16 +1127,17 @@ __global__ __launch_bounds__(kB2BWsThreads) void b2b_fwd_ws_kernel(const typenam
         const __bf16* zh = reinterpret_cast<const __bf16*>(zb);
         tm.run2(zh, zh + LY::ZE, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
       } else {
-        tm.run2(zb, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+        tm.run2(zb, LY::ZR, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
       }
       const int n0 = ti * kConvTile;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int mt = wave + h * kConvWaves;
+        const float* ql = qb + qs_pad(16 * (16 * mt + 4 * (l >> 4)) + (l & 15));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p = 16 * (16 * mt + 4 * (l >> 4) + r) + (l & 15);
-          yb.store_elem(n0 + p, qb[qs_pad(p)] * (h ? acc1[r] : acc0[r]));
+          yb.store_elem(n0 + p, ql[qs_step(r)] * (h ? acc1[r] : acc0[r]));
         }
       }
       __syncthreads();

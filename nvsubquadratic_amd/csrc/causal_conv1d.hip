@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kConvThreads) void cconv_fwd_short_kernel(const typ
 // ---------------------------------------------------------------------------
 // Matrix-core path (K >= 16; used above 16 taps): a workgroup walks a segment of
 // kConvSegTiles tiles of one (b, c) row; per tile the source window (fp32,
-// padded as ToeplitzMfma reads it) is staged from registers loaded during the
+// in the split layout ToeplitzMfma reads) is staged from registers loaded during the
 // previous tile, the MFMA band gives acc[p] for the tile's 2048 outputs, and
 // the epilogue stores from the accumulator layout through a range-checked row
 // buffer.  Modes:
@@ -79,8 +79,8 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
     const typename Elem<DS>::T* __restrict__ src, const float* __restrict__ w, const float* __restrict__ bias,
     const typename Elem<DO>::T* __restrict__ gy, void* __restrict__ out, int C, int L, int K) {
   constexpr int ZW = mfma_src_count<NS>();
-  constexpr int ZWORDS = (conv_pad_words(ZW) + 7) & ~7;
-  __shared__ __align__(16) float zp[ZWORDS];
+  constexpr int ZR = win_half(ZW);
+  __shared__ __align__(16) float zp[win_words(ZW)];
   __shared__ __align__(16) float wl[kConvWeightFloats];
   const int64_t row = blockIdx.x;
   const int c = int(row % C);
@@ -109,12 +109,12 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
     for (int it = 0; it < RowStage<DS, ZW>::IT; ++it) {
       const int m = t + it * kConvThreads;
-      if (m < ZW) zp[conv_pad(m)] = RowBuf<DS, false>::bits_to_f32(sw.v[it]);
+      if (m < ZW) zp[win_at(m, ZR)] = RowBuf<DS, false>::bits_to_f32(sw.v[it]);
     }
     __syncthreads();
     if (ti + 1 < t_end) sw.load(src + row * L, n0 + kConvTile - shift, 0, L);
     nsq_f32x4_t acc0, acc1;
-    tm.run2(zp, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
+    tm.run2(zp, ZR, 16 * wave, 16 * (wave + kConvWaves), acc0, acc1);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -146,7 +146,8 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
     const typename Elem<DG>::T* __restrict__ gp, const typename Elem<DX>::T* __restrict__ x, float* __restrict__ part,
     int B, int C, int L, int K) {
   constexpr int ZW = mfma_src_count<NS>();
-  constexpr int ZWORDS = (conv_pad_words(ZW) + 7) & ~7;
+  constexpr int ZR = win_half(ZW);
+  constexpr int ZWORDS = win_words(ZW);
   constexpr int TG = NS / 4;
   constexpr int RW = 4 * NS;
   static_assert(16 * RW <= ZWORDS + kConvTile, "cconv_wgrad_mfma_kernel: reduction area");
@@ -176,19 +177,21 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
       for (int it = 0; it < RowStage<DX, ZW>::IT; ++it) {
         const int m = t + it * kConvThreads;
-        if (m < ZW) zp[conv_pad(m)] = RowBuf<DX, false>::bits_to_f32(sx.v[it]);
+        if (m < ZW) zp[win_at(m, ZR)] = RowBuf<DX, false>::bits_to_f32(sx.v[it]);
       }
       sg.store(gs, kConvTile);
 #pragma unroll
       for (int it = 0; it < RowStage<DG, kConvTile>::IT; ++it) bacc += RowBuf<DG, false>::bits_to_f32(sg.v[it]);
     }
     __syncthreads();
+    // win_at(16 (a0 + kk + tg) + li) = win_at(16 kk + li) + 8 (a0 + tg)
+    const float* zl = zp + win_at(16 * kk + li, ZR);
 #pragma unroll 2
     for (int a0 = 32 * wave; a0 < 32 * wave + 32; a0 += 4) {
       const float av = gs[16 * (a0 + kk) + li];
 #pragma unroll
       for (int tg = 0; tg < TG; ++tg) {
-        const float bv = zp[20 * (a0 + kk + tg) + li];
+        const float bv = zl[8 * (a0 + tg)];
         D[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, D[tg], 0, 0, 0);
       }
     }

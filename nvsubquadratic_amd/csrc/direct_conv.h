@@ -206,15 +206,40 @@ __device__ __forceinline__ void wgrad_finish(float (&acc)[kConvPer], float bacc,
 // words: one 16-byte LDS read.  T follows the same column order and lives in
 // NS registers per lane for the whole tile.
 //
-// src is laid out in LDS with a 4-word pad after every 16 words,
-// conv_pad(m) = m + 4 (m / 16): the 16 lanes of one read phase (blocks a ..
-// a+15, stride 20 words) then cover all 64 banks exactly once.
+// src lives in LDS in a split layout: each 16-word block is stored as two
+// 8-word halves, the first halves of all blocks in one region and the second
+// halves in another R words further on,
+//     win_at(m, R) = 8 (m / 16) + m % 8 + R ((m / 8) % 2),   R % 32 == 16.
+// The banks of gfx950 (measured with the LDS bank-conflict counters): a
+// 16-byte read is served 32 lanes at a time over 128 four-byte banks, a
+// 16-byte write 8 lanes at a time over 32 banks, a 4-byte access 32 lanes at a
+// time over 32 banks.  The A reads of a step (lanes kk = 0, 1 over 16
+// consecutive blocks, and kk = 2, 3) are then one contiguous 512-byte run of a
+// region each, the B-operand style 4-byte reads of two consecutive blocks
+// (lanes 0-15 and 16-31) fall on opposite 16-bank halves (R % 32 == 16), and
+// a step's address is the lane's base plus a constant (an immediate offset).
 // ---------------------------------------------------------------------------
 typedef float nsq_f32x4_t __attribute__((ext_vector_type(4)));
 
-__host__ __device__ __forceinline__ constexpr int conv_pad(int m) { return m + 4 * (m >> 4); }
-// Padded LDS words holding src[0, count).
-constexpr int conv_pad_words(int count) { return conv_pad(((count + 15) / 16) * 16); }
+__host__ __device__ __forceinline__ constexpr int win_at(int m, int R) {
+  return 8 * (m >> 4) + (m & 7) + R * ((m >> 3) & 1);
+}
+// Region stride for a window of count elements: the smallest R >= 8 ceil(count / 16) with R % 32 == 16.
+__host__ __device__ constexpr int win_half(int count) { return ((8 * ((count + 15) / 16) + 15) / 32) * 32 + 16; }
+// LDS words of such a window.
+__host__ __device__ constexpr int win_words(int count) { return 2 * win_half(count); }
+// Elements P .. P+7 of a split-layout window (P % 4 == 0) as two 16-byte
+// writes.  Odd lanes write their upper four first, so that the 8 lanes of a
+// write phase (lane stride 8 elements) cover the 32 banks once.
+// (Per-value selects: a select of whole float4s is lowered through scratch
+// memory.)
+__device__ __forceinline__ void win_store8(float* win, int R, int P, const float (&v)[8]) {
+  const bool sw = (threadIdx.x & 1) != 0;
+  const float4 first = make_float4(sw ? v[4] : v[0], sw ? v[5] : v[1], sw ? v[6] : v[2], sw ? v[7] : v[3]);
+  const float4 second = make_float4(sw ? v[0] : v[4], sw ? v[1] : v[5], sw ? v[2] : v[6], sw ? v[3] : v[7]);
+  *reinterpret_cast<float4*>(win + win_at(P + (sw ? 4 : 0), R)) = first;
+  *reinterpret_cast<float4*>(win + win_at(P + (sw ? 0 : 4), R)) = second;
+}
 
 // Steps for K taps: 4*NS >= K + 15 window columns, NS a multiple of 4.
 template <int NS>
@@ -238,16 +263,22 @@ struct ToeplitzMfma {
       b[s] = ok ? v : 0.f;
     }
   }
+  // Lane base of the A reads: element 16 (a0 + a) + 4 kk of the window (step
+  // group q adds 8 q words).
+  __device__ __forceinline__ static const float* a_base(const float* srcp, int R, int a0) {
+    const int l = int(threadIdx.x) & 63, kk = l >> 4, a = l & 15;
+    return srcp + 8 * (a0 + a) + 4 * (kk & 1) + R * (kk >> 1);
+  }
   // The lane's four outputs of the 16 blocks starting at block a0:
   // out[r] = y of block a0 + 4 (l / 16) + r, position l % 16 in the block.
-  // srcp: padded src; reads src[16 a0, 16 (a0 + 16) + 4 NS - 16).
-  __device__ __forceinline__ nsq_f32x4_t run(const float* srcp, int a0) const {
-    const int l = int(threadIdx.x) & 63, kk = l >> 4, a = l & 15;
-    const float* p = srcp + 20 * (a0 + a) + 4 * kk;
+  // srcp: src in the split layout with region stride R; reads src[16 a0,
+  // 16 (a0 + 16) + 4 NS - 16).
+  __device__ __forceinline__ nsq_f32x4_t run(const float* srcp, int R, int a0) const {
+    const float* p = a_base(srcp, R, a0);
     nsq_f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < NS / 4; ++q) {
-      const float4 v = *reinterpret_cast<const float4*>(p + 20 * q);
+      const float4 v = *reinterpret_cast<const float4*>(p + 8 * q);
       c = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, b[4 * q + 0], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x4f32(v.y, b[4 * q + 1], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x4f32(v.z, b[4 * q + 2], c, 0, 0, 0);
@@ -257,10 +288,10 @@ struct ToeplitzMfma {
   }
   // Two M-tiles (blocks a0.. and a1..) with their steps interleaved: two
   // independent accumulation chains keep the matrix pipeline busy.
-  __device__ __forceinline__ void run2(const float* srcp, int a0, int a1, nsq_f32x4_t& c0, nsq_f32x4_t& c1) const {
-    const int l = int(threadIdx.x) & 63, kk = l >> 4, a = l & 15;
-    const float* p0 = srcp + 20 * (a0 + a) + 4 * kk;
-    const float* p1 = srcp + 20 * (a1 + a) + 4 * kk;
+  __device__ __forceinline__ void run2(const float* srcp, int R, int a0, int a1, nsq_f32x4_t& c0,
+                                       nsq_f32x4_t& c1) const {
+    const float* p0 = a_base(srcp, R, a0);
+    const float* p1 = a_base(srcp, R, a1);
     c0 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
     c1 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
     // operands of step group q+1 are read before the MFMAs of group q issue
@@ -270,8 +301,8 @@ struct ToeplitzMfma {
     for (int q = 0; q < NS / 4; ++q) {
       const float4 u = un, v = vn;
       if (q + 1 < NS / 4) {
-        un = *reinterpret_cast<const float4*>(p0 + 20 * (q + 1));
-        vn = *reinterpret_cast<const float4*>(p1 + 20 * (q + 1));
+        un = *reinterpret_cast<const float4*>(p0 + 8 * (q + 1));
+        vn = *reinterpret_cast<const float4*>(p1 + 8 * (q + 1));
       }
       c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(u.x, b[4 * q + 0], c0, 0, 0, 0);
       c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, b[4 * q + 0], c1, 0, 0, 0);
@@ -295,15 +326,11 @@ struct ToeplitzMfma {
 // per product.  Lane layout (checked on MI355X with integer operands): lane l
 // supplies A[l % 16][8 (l / 16) + e] and B[8 (l / 16) + e][l % 16], e < 8, and
 // receives D[4 (l / 16) + r][l % 16] -- the accumulator of the fp32 form.
-// src halves are bf16 arrays with an 8-element pad after every 16 (bpad): a
-// lane's 8 values of one step are one 16-byte read, and the 16 lanes of a
-// read phase (blocks a .. a+15, 48 bytes apart) cover the 64 banks once.
+// src halves are plain bf16 arrays: a lane's 8 values of one step are one
+// 16-byte read, and the 32 lanes of a read phase (kk = 0, 1 over 16
+// consecutive blocks) read one contiguous 512-byte run: no bank conflicts.
 // ---------------------------------------------------------------------------
 typedef __bf16 nsq_bf16x8_t __attribute__((ext_vector_type(8)));
-
-__host__ __device__ __forceinline__ constexpr int bpad(int m) { return m + 8 * (m >> 4); }
-// Padded bf16 elements holding src[0, count).
-constexpr int bpad_elems(int count) { return bpad(((count + 15) / 16) * 16); }
 
 // v = hi + lo (bf16 halves, round to nearest even each).
 __device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
@@ -333,21 +360,20 @@ struct ToeplitzMfmaBf16 {
       }
     }
   }
-  // Two M-tiles (blocks a0.. and a1..) of the padded bf16 src halves zh, zl:
+  // Two M-tiles (blocks a0.. and a1..) of the bf16 src halves zh, zl:
   // c = the lane's four outputs of each (as ToeplitzMfma::run2).
   __device__ __forceinline__ void run2(const __bf16* zh, const __bf16* zl, int a0, int a1, nsq_f32x4_t& c0,
                                        nsq_f32x4_t& c1) const {
     const int l = int(threadIdx.x) & 63, kk = l >> 4, a = l & 15;
-    // bpad(16 (a0 + a) + 32 s + 8 kk) = bpad(16 (a0 + a) + 8 kk) + 48 s
-    const int o0 = bpad(16 * (a0 + a) + 8 * kk), o1 = bpad(16 * (a1 + a) + 8 * kk);
+    const int o0 = 16 * (a0 + a) + 8 * kk, o1 = 16 * (a1 + a) + 8 * kk;
     c0 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
     c1 = nsq_f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < S32; ++s) {
-      const nsq_bf16x8_t h0 = *reinterpret_cast<const nsq_bf16x8_t*>(zh + o0 + 48 * s);
-      const nsq_bf16x8_t h1 = *reinterpret_cast<const nsq_bf16x8_t*>(zh + o1 + 48 * s);
-      const nsq_bf16x8_t g0 = *reinterpret_cast<const nsq_bf16x8_t*>(zl + o0 + 48 * s);
-      const nsq_bf16x8_t g1 = *reinterpret_cast<const nsq_bf16x8_t*>(zl + o1 + 48 * s);
+      const nsq_bf16x8_t h0 = *reinterpret_cast<const nsq_bf16x8_t*>(zh + o0 + 32 * s);
+      const nsq_bf16x8_t h1 = *reinterpret_cast<const nsq_bf16x8_t*>(zh + o1 + 32 * s);
+      const nsq_bf16x8_t g0 = *reinterpret_cast<const nsq_bf16x8_t*>(zl + o0 + 32 * s);
+      const nsq_bf16x8_t g1 = *reinterpret_cast<const nsq_bf16x8_t*>(zl + o1 + 32 * s);
       c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, bh[s], c0, 0, 0, 0);
       c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, bh[s], c1, 0, 0, 0);
       c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, bl[s], c0, 0, 0, 0);
