@@ -667,6 +667,16 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(3)
 // per-workgroup partial [3][4].  (Neither gk, gv nor gx need a workspace pass.)
 constexpr int kB2BBwdExtra = 4;  // positions past the tile with gk, gv (>= Kp - 1, keeps 16-byte alignment)
 
+// A 16-byte LDS read kept whole.  Of a window read as four float4 only some
+// values may be used; the compiler then narrows the reads to those values as
+// misaligned 4- and 8-byte reads, which at a lane stride of 8 words fall 8 to
+// a bank (4-byte accesses are served 32 lanes at a time over 32 banks).
+__device__ __forceinline__ float4 lds_read16(const float* p) {
+  float4 v = *reinterpret_cast<const float4*>(p);
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+  return v;
+}
+
 template <int NS>
 struct B2BBwd2fLds {
   static constexpr int GR = win_half(mfma_src_count<NS>() + kB2BBwdExtra);
@@ -844,10 +854,10 @@ __global__ __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(2)
         // window gc[n0 + base - 3 + i], i < 16 (LDS index base + i); x at the same offsets
         float gw_[16], xw_[12];
         {
-          const float4 a = *reinterpret_cast<const float4*>(gsrc[cc] + base);
-          const float4 b4 = *reinterpret_cast<const float4*>(gsrc[cc] + base + 4);
-          const float4 c4 = *reinterpret_cast<const float4*>(gsrc[cc] + base + 8);
-          const float4 d4 = *reinterpret_cast<const float4*>(gsrc[cc] + base + 12);
+          const float4 a = lds_read16(gsrc[cc] + base);
+          const float4 b4 = lds_read16(gsrc[cc] + base + 4);
+          const float4 c4 = lds_read16(gsrc[cc] + base + 8);
+          const float4 d4 = lds_read16(gsrc[cc] + base + 12);
           const float tmp[16] = {a.x, a.y, a.z, a.w, b4.x, b4.y, b4.z, b4.w,
                                  c4.x, c4.y, c4.z, c4.w, d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
