@@ -377,23 +377,26 @@ struct HalfZeroLoad {
   }
 };
 
-template <int LOGN, int LOGNS, bool INV, int M, int T, bool TMAJOR, class LDF, class STL, class LDL, class STF>
+// LOGRMAX: the largest pass radix (log2; 4 = radix 16, E = 16 points per
+// thread; 3 = radix 8 for E = 8).
+template <int LOGN, int LOGNS, bool INV, int M, int T, bool TMAJOR, int LOGRMAX = 4, class LDF, class STL, class LDL,
+          class STF>
 __device__ __forceinline__ void fft_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last,
                                         const float2* __restrict__ tw) {
   constexpr int REM = LOGN - LOGNS;
-  constexpr int LOGR = REM < 4 ? REM : 4;
+  constexpr int LOGR = REM < LOGRMAX ? REM : LOGRMAX;
   constexpr bool FIRST = (LOGNS == 0);
   constexpr bool LAST = (LOGNS + LOGR == LOGN);
   if constexpr (FIRST && LAST) {
     stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_first, st_last, tw);
   } else if constexpr (FIRST) {
     stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_first, st_lds, tw);
-    fft_rec<LOGN, LOGNS + LOGR, INV, M, T, TMAJOR>(ld_first, st_lds, ld_lds, st_last, tw);
+    fft_rec<LOGN, LOGNS + LOGR, INV, M, T, TMAJOR, LOGRMAX>(ld_first, st_lds, ld_lds, st_last, tw);
   } else if constexpr (LAST) {
     stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_lds, st_last, tw);
   } else {
     stockham_pass<LOGN, LOGR, LOGNS, INV, M, T, TMAJOR>(ld_lds, st_lds, tw);
-    fft_rec<LOGN, LOGNS + LOGR, INV, M, T, TMAJOR>(ld_first, st_lds, ld_lds, st_last, tw);
+    fft_rec<LOGN, LOGNS + LOGR, INV, M, T, TMAJOR, LOGRMAX>(ld_first, st_lds, ld_lds, st_last, tw);
   }
 }
 
@@ -406,6 +409,12 @@ template <int LOGN, bool INV, int M, int T, int S, bool TMAJOR = false, class LD
 __device__ __forceinline__ void fft(float2* lds, LDF& ld_first, STF& st_last, const float2* __restrict__ tw) {
   LdsTile<S, !TMAJOR> tile{lds};
   fft_rec<LOGN, 0, INV, M, T, TMAJOR>(ld_first, tile, tile, st_last, tw);
+}
+// The same with passes of radix at most 2^LOGRMAX (element-major tile).
+template <int LOGRMAX, int LOGN, bool INV, int M, int T, int S, class LDF, class STF>
+__device__ __forceinline__ void fft_radix(float2* lds, LDF& ld_first, STF& st_last, const float2* __restrict__ tw) {
+  LdsTile<S, true> tile{lds};
+  fft_rec<LOGN, 0, INV, M, T, false, LOGRMAX>(ld_first, tile, tile, st_last, tw);
 }
 
 // Transform that starts and ends in LDS.

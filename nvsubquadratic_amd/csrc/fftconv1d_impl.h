@@ -259,23 +259,25 @@ __global__ __launch_bounds__(FusedCfg<LOGN>::T) void fused_fwd_kernel(
 // Forward, fused plan, for grids too small to fill the GPU (M == 1 lengths,
 // few (channel, batch row) pairs): fused_fwd_kernel then runs one workgroup
 // of N/16 threads per row, one wave per SIMD, and transforms the filter and
-// the row one after the other.  Here a workgroup of 2 N/16 threads owns one
-// (channel h = blockIdx.x, batch row b = blockIdx.y) and holds a
+// the row one after the other.  Here a workgroup of 2 N/2^LOGRMAX threads
+// owns one (channel h = blockIdx.x, batch row b = blockIdx.y) and holds a
 // two-transform tile: transform 0 is the filter, transform 1 the row, both
-// transformed at once (waves 0 .. N/512 - 1 load the filter, the rest the
-// row).  The product reads both spectra from LDS slot by slot and leaves the
-// result in transform 1; the inverse transform runs over the whole tile and
-// the epilogue keeps transform 1.  Per element the arithmetic is that of
-// fused_fwd_kernel.  Plain causal conv (no fold, ramp or gates); kfilm: the
-// filter row is image b's.
-template <int LOGN, int DT>
-__global__ __launch_bounds__(2 * FusedCfg<LOGN>::T) void fused_fwd_pair_kernel(
+// transformed at once (the first half of the threads load the filter, the
+// rest the row).  The product reads both spectra from LDS slot by slot and
+// leaves the result in transform 1; the inverse transform runs over the whole
+// tile and the epilogue keeps transform 1.  With LOGRMAX = 4 the arithmetic
+// per element is that of fused_fwd_kernel (bitwise equal outputs); LOGRMAX =
+// 3 runs radix-8 passes at 8 points per thread (agreement to fp32 rounding).
+// Plain causal conv (no fold, ramp or gates); kfilm: the filter row is image
+// b's.
+template <int LOGN, int DT, int LOGRMAX = 4>
+__global__ __launch_bounds__(2 * (FusedCfg<LOGN>::N >> LOGRMAX)) void fused_fwd_pair_kernel(
     const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ k,
     const typename Elem<DT>::T* __restrict__ s, typename Elem<DT>::T* __restrict__ y, int H, int L, int K,
     const float2* __restrict__ tw, int kfilm) {
   using C = FusedCfg<LOGN>;
   static_assert(C::M == 1, "fused_fwd_pair_kernel: one transform per channel");
-  constexpr int T = 2 * C::T, SL = C::N / 2 / T;  // threads; product slots per thread
+  constexpr int T = 2 * (C::N >> LOGRMAX), SL = C::N / 2 / T;  // threads; product slots per thread
   static_assert(SL >= 1 && (C::N / 2) % T == 0, "fused_fwd_pair_kernel: slot split");
   __shared__ float2 lds[2 * C::SP];
   const int h = blockIdx.x, b = blockIdx.y;
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(2 * FusedCfg<LOGN>::T) void fused_fwd_pair_kernel(
     return load_pair<DT>(x + row, 2 * int64_t(n), L);
   };
   LdsTile<C::SP, true> st{lds};
-  fft<LOGN, false, 2, T, C::SP>(lds, ld, st, tw);
+  fft_radix<LOGRMAX, LOGN, false, 2, T, C::SP>(lds, ld, st, tw);
 #pragma unroll
   for (int i = 0; i < SL; ++i) {
     NSQ_SLOT_FENCE();
@@ -313,7 +315,7 @@ __global__ __launch_bounds__(2 * FusedCfg<LOGN>::T) void fused_fwd_pair_kernel(
                       epilogue<DT>(v.y * scale, s != nullptr, sv, s ? Elem<DT>::load(x, row + i0 + 1) : 0.f));
   };
   LdsTile<C::SP, true> ldl{lds};
-  fft<LOGN, true, 2, T, C::SP>(lds, ldl, epi, tw);
+  fft_radix<LOGRMAX, LOGN, true, 2, T, C::SP>(lds, ldl, epi, tw);
 }
 
 // Backward, fused plan.  grid = ceil(H/M); each workgroup loops over all
@@ -1229,13 +1231,16 @@ __global__ __launch_bounds__(RowCfg<LOGN2>::T) __attribute__((amdgpu_waves_per_e
 // Host launchers
 // ===========================================================================
 // Largest B*H that the forward runs on fused_fwd_pair_kernel (M == 1 lengths,
-// no fold): as many rows as one round of pair workgroups covers, i.e. 256 CUs
-// times the pair tiles that fit a CU's 160 KB of LDS (FFT length 4096: 1024
-// rows, 8192: 512, 16384: 256).  Measured on MI355X (kernel time, one-
-// transform -> pair kernel): length 8192 B=2 H=128 20.2 -> 16.0 us, H=512
-// 23.4 -> 21.1 us, H=2048 68.8 -> 71.7 us; length 16384 H=256 29.4 -> 23.2
-// us, H=512 39.4 -> 43.1 us.  NSQ_1D_PAIR_MAX_ROWS overrides the bound for
-// every length (0 turns the pair kernel off).
+// no fold).  FFT length 16384 (radix-16 pair kernel): as many rows as one
+// round of pair workgroups covers, 256 CUs times the pair tiles that fit a
+// CU's 160 KB of LDS (256 rows; measured, one-transform -> pair kernel: H=256
+// 29.4 -> 23.2 us, H=512 39.4 -> 43.1 us).  FFT lengths 4096 and 8192
+// (radix-8 pair kernel): 1536 rows.  Measured at B=2 (kernel time, one-
+// transform -> pair kernel): length 8192, 256 rows 19.5 -> 13.5 us, 512 22.1
+// -> 20.0, 768 25.8 -> 26.3, 1024 38.4 -> 33.6, 1536 50.1 -> 48.5; length
+// 4096, 256 rows 16.2 -> 9.0 us, 1024 20.5 -> 17.8, 1536 25.7 -> 23.7, 2048
+// 28.7 -> 29.7.  NSQ_1D_PAIR_MAX_ROWS overrides the bound for every length (0
+// turns the pair kernel off).
 template <int LOGN>
 inline int64_t fused_pair_max_rows() {
   static const int64_t env = [] {
@@ -1243,6 +1248,7 @@ inline int64_t fused_pair_max_rows() {
     return e ? int64_t(std::atoll(e)) : int64_t(-1);
   }();
   if (env >= 0) return env;
+  if constexpr (LOGN <= 12) return 1536;
   constexpr int lds = 2 * FusedCfg<LOGN>::SP * int(sizeof(float2));
   constexpr int per_cu = (160 * 1024) / lds;
   return int64_t(256) * (per_cu < 1 ? 1 : per_cu);
@@ -1256,8 +1262,11 @@ static void launch_fused_fwd(const Plan1D& p, const void* x, const float* k, con
   using ET = typename Elem<DT>::T;
   if constexpr (C::M == 1) {
     if (!p.fold && int64_t(H) * B <= fused_pair_max_rows<LOGN>()) {
-      hipLaunchKernelGGL((fused_fwd_pair_kernel<LOGN, DT>), dim3(H, B), dim3(2 * C::T), 0, st, (const ET*)x, k,
-                         (const ET*)s, (ET*)y, H, L, K, tw, kfilm);
+      // radix-8 passes up to N = 4096 (2 N / 8 <= 1024 threads): twice the waves of the radix-16 form to cover
+      // the pass latencies of a grid of one round (FFT length 8192 at B=2 H=128: 17.6 -> 15.7 us per step)
+      constexpr int LOGR = LOGN <= 12 ? 3 : 4;
+      hipLaunchKernelGGL((fused_fwd_pair_kernel<LOGN, DT, LOGR>), dim3(H, B), dim3(2 * (C::N >> LOGR)), 0, st,
+                         (const ET*)x, k, (const ET*)s, (ET*)y, H, L, K, tw, kfilm);
       return;
     }
   }

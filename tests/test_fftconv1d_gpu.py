@@ -264,13 +264,15 @@ def test_config1_fp32_fwd_bwd():
 @pytest.mark.parametrize("L", [2048, 4096, 8192])
 @pytest.mark.parametrize("dtype,film", [(torch.float32, False), (torch.bfloat16, False), (torch.float32, True)])
 def test_fused_pair_and_single_kernels_agree(L, dtype, film):
-    """The fused forward runs up to 1024 / 512 / 256 rows (B*H) of FFT lengths 4096 / 8192 / 16384 on the
+    """The fused forward runs up to 1536 / 1536 / 256 rows (B*H) of FFT lengths 4096 / 8192 / 16384 on the
     two-transform (filter | row) workgroup and larger grids on the one-transform kernel: 8 channels past that bound
-    take the latter, the bound's worth of them the former.  Same arithmetic per element, so the outputs agree bit
-    for bit; both meet the oracle."""
+    take the latter, the bound's worth of them the former.  At FFT length 16384 both run radix-16 passes and agree
+    bit for bit; up to 8192 the pair kernel runs radix-8 passes (8 points per thread, twice the threads), so the two
+    agree to fp32 rounding (rel-L2 <= 1e-6 on fp32 outputs; <= 1e-3 on bf16 outputs, where a rounding difference can
+    move an output by one bf16 step) and the pair kernel repeats bit for bit.  Both meet the oracle."""
     torch.manual_seed(31)
     B = 2 if film else 1
-    rows = {2048: 1024, 4096: 512, 8192: 256}[L]
+    rows = {2048: 1536, 4096: 1536, 8192: 256}[L]
     H, Hp = rows // B + 8, rows // B
     x = torch.randn(B, H, L).to(dtype)
     k = torch.randn(B if film else 1, H, L) * torch.exp(-torch.linspace(0, 8, L))
@@ -278,7 +280,12 @@ def test_fused_pair_and_single_kernels_agree(L, dtype, film):
     xd, kd, sd = x.cuda(), k.cuda(), s.cuda()
     y_single = F.causal_fftconv1d_bhl(xd, kd, sd)
     y_pair = F.causal_fftconv1d_bhl(xd[:, :Hp].contiguous(), kd[:, :Hp].contiguous(), sd[:Hp].contiguous())
-    assert torch.equal(y_pair, y_single[:, :Hp])
+    if L == 8192:
+        assert torch.equal(y_pair, y_single[:, :Hp])
+    else:
+        assert rel_l2(y_single[:, :Hp], y_pair) < (1e-6 if dtype == torch.float32 else 1e-3)
+        y_again = F.causal_fftconv1d_bhl(xd[:, :Hp].contiguous(), kd[:, :Hp].contiguous(), sd[:Hp].contiguous())
+        assert torch.equal(y_pair, y_again)
     tol = RTOL_F32_L2 if dtype == torch.float32 else RTOL_BF16_L2
     y64 = np.concatenate([causal_fftconv1d_np(x[b:b + 1].float().numpy(), k[b if film else 0].numpy(),
                                               s.float().numpy()) for b in range(B)])
