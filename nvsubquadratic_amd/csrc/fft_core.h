@@ -560,7 +560,7 @@ __device__ __forceinline__ void store_pair_nb(typename Elem<DT>::T* __restrict__
 // byte offsets from the row start (rows here are below 2^28 elements); every
 // offset is non-negative (see elem_halo for positions before the row).
 // ALIGNED: see load_pair_nb; a pair at an even index is then one access.
-template <int DT, bool ALIGNED>
+template <int DT, bool ALIGNED, int AUX = 0>
 struct RowBuf {
   using ET = typename Elem<DT>::T;
   __amdgpu_buffer_rsrc_t r;
@@ -570,11 +570,11 @@ struct RowBuf {
   __device__ __forceinline__ float elem(int64_t i) const {
     const int off = int(i) * int(sizeof(ET));
     if constexpr (DT == NSQ_DTYPE_F32) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX));
     } else if constexpr (DT == NSQ_DTYPE_BF16) {
-      return bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+      return bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX));
     } else {
-      return __half2float(__builtin_bit_cast(__half, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+      return __half2float(__builtin_bit_cast(__half, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX)));
     }
   }
   // Element at a position that may be negative (a halo before the row start),
@@ -591,9 +591,9 @@ struct RowBuf {
     int off = n < 0 ? int(0x80000000u) : n * int(sizeof(ET));
     asm volatile("" : "+v"(off));
     if constexpr (DT == NSQ_DTYPE_F32) {
-      return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+      return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
     } else {
-      return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+      return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX);
     }
   }
   __device__ __forceinline__ static float bits_to_f32(uint32_t b) {
@@ -608,11 +608,11 @@ struct RowBuf {
   __device__ __forceinline__ void store_elem(int64_t i, float v) const {
     const int off = int(i) * int(sizeof(ET));
     if constexpr (DT == NSQ_DTYPE_F32) {
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, AUX);
     } else if constexpr (DT == NSQ_DTYPE_BF16) {
-      __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), r, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), r, off, 0, AUX);
     } else {
-      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, __float2half_rn(v)), r, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, __float2half_rn(v)), r, off, 0, AUX);
     }
   }
   // (u[i], u[i+1]); i even when ALIGNED.
@@ -620,12 +620,12 @@ struct RowBuf {
     if constexpr (ALIGNED) {
       const int off = int(i) * int(sizeof(ET));
       if constexpr (DT == NSQ_DTYPE_F32) {
-        return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+        return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX));
       } else if constexpr (DT == NSQ_DTYPE_BF16) {
-        const uint32_t u = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+        const uint32_t u = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
         return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
       } else {
-        return __half22float2(__builtin_bit_cast(__half2, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)));
+        return __half22float2(__builtin_bit_cast(__half2, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX)));
       }
     } else {
       return make_float2(elem(i), elem(i + 1));
@@ -639,16 +639,16 @@ struct RowBuf {
   __device__ __forceinline__ PairBits load_pair_bits(int64_t i) const {
     const int off = int(i) * int(sizeof(ET));
     if constexpr (ALIGNED && DT == NSQ_DTYPE_F32) {
-      const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+      const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX);
       return PairBits{u[0], u[1]};
     } else if constexpr (ALIGNED) {
-      return PairBits{__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0), 0u};
+      return PairBits{__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX), 0u};
     } else if constexpr (DT == NSQ_DTYPE_F32) {
-      return PairBits{__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0),
-                      __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, 0)};
+      return PairBits{__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX),
+                      __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, AUX)};
     } else {
-      return PairBits{__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0),
-                      __builtin_amdgcn_raw_buffer_load_b16(r, off + 2, 0, 0)};
+      return PairBits{__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX),
+                      __builtin_amdgcn_raw_buffer_load_b16(r, off + 2, 0, AUX)};
     }
   }
   __device__ __forceinline__ static float2 pair_from_bits(PairBits p) {
@@ -667,7 +667,7 @@ struct RowBuf {
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uint32_t __attribute__((ext_vector_type(2))), v), r,
                                               off, 0, 0);
       } else if constexpr (DT == NSQ_DTYPE_BF16) {
-        __builtin_amdgcn_raw_buffer_store_b32(f32x2_to_bf16x2_bits(v.x, v.y), r, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(f32x2_to_bf16x2_bits(v.x, v.y), r, off, 0, AUX);
       } else {
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, __floats2half2_rn(v.x, v.y)), r, off, 0,
                                               0);
