@@ -38,7 +38,18 @@ struct NdPlan {
   int FH;        // spectrum columns along the last axis: F2/2 + 1, or F2/2 packed
   int RS;        // spectrum row stride (complex elements), >= FH
   int64_t spec;
+  bool r3;       // mixed-radix plan (fftconv_nd_r3.h): F_d in {48, 96, 192}, lF unused
 };
+
+// The mixed-radix 3D plan is taken where it applies unless NSQ_ND_R3=0 (read
+// per call, so the workspace size and the run agree for a given setting).
+inline bool nd_r3_allowed() {
+  const char* e = std::getenv("NSQ_ND_R3");
+  return !(e && e[0] == '0');
+}
+
+// Axis-0 columns per workgroup of the mixed-radix column passes (R3ColCfg::M).
+inline int r3_col_m(int F0) { return F0 == 48 ? 32 : 16; }
 
 // `periodic`: bit d set = axis d (of the nd given axes) is periodic.
 inline bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kb,
@@ -49,6 +60,7 @@ inline bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
   p.B = B;
   p.H = H;
   p.kb = kb;
+  p.r3 = false;
   p.ramp = false;
   p.gk_scale = 1.f;
   int s[3] = {1, 1, 1}, k[3] = {1, 1, 1};
@@ -105,6 +117,30 @@ inline bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
   // keep their compile-time row stride.
   p.RS = nd == 2 ? (p.FH + 15) / 16 * 16 : p.FH;
   p.spec = int64_t(p.F[0]) * p.F[1] * p.RS;
+  // The reference's FFT sizes (ops/fftconv.py:774-778: F_d = S_d + ceil(K_d/2),
+  // mixed-radix): a 3D volume with every axis zero-padded runs the
+  // mixed-radix plan when each axis fits a length 3 * 2^m it has kernels for
+  // (48 or 96; axis 0 also 192) and the spectrum is smaller than the
+  // power-of-two one (e.g. 96^3 against 128^3 at S = K = 64).
+  if (nd == 3 && periodic == 0 && nd_r3_allowed()) {
+    int f3[3];
+    bool ok = true;
+    for (int d = 0; d < 3; ++d) {
+      const int64_t need = int64_t(s[d]) + (k[d] + 1) / 2;
+      f3[d] = need <= 48 ? 48 : need <= 96 ? 96 : (d == 0 && need <= 192) ? 192 : 0;
+      ok = ok && f3[d] != 0;
+    }
+    const int64_t spec3 = int64_t(f3[0]) * f3[1] * (f3[2] / 2 + 1);
+    if (ok && spec3 < p.spec) {
+      p.r3 = true;
+      for (int d = 0; d < 3; ++d) {
+        p.F[d] = f3[d];
+        p.lF[d] = 0;
+      }
+      p.FH = p.RS = f3[2] / 2 + 1;
+      p.spec = spec3;
+    }
+  }
   return true;
 }
 
@@ -218,6 +254,7 @@ void col_blocks(int inner, LAUNCH&& launch) {
 // `target` (col_blocks: full blocks of M columns, then blocks of 4).
 inline int64_t axis0_blocks(const NdPlan& p, int target) {
   const int inner = p.F[1] * p.FH;
+  if (p.r3) return ceil_div(inner, r3_col_m(p.F[0]));
   int m = target >> p.lF[0];
   m = m < 4 ? 4 : (m > 16 ? 16 : m);
   const int full = inner / m, rem = inner - full * m;
@@ -273,7 +310,7 @@ bool col_pass(const NdPlan& p, float2* ws, int64_t nbh, int axis, int n_valid0, 
 // Plane passes (3D, a (b, h, a0) plane fits in LDS): both inner axes in one
 // kernel.  plane_ok mirrors PlaneCfg::OK for the plan's sizes.
 inline bool plane_ok(const NdPlan& p) {
-  if (p.nd != 3) return false;
+  if (p.nd != 3 || p.r3) return false;
   const int logn = p.lF[2] - 1, logf1 = p.lF[1];
   if (logn < 4 || logn > 9 || logf1 < 4 || logf1 > kNdMaxLogF) return false;
   const int n = 1 << logn, f1 = 1 << logf1, mr = 4096 >> logn, mc = 4096 >> logf1;
@@ -377,11 +414,30 @@ inline void launch_image_fwd(const NdPlan& p, const void* x, const float2* khat,
                        (const ET*)s, (ET*)y, int(p.B), int(p.H), p.S[0], p.S[2], p.o[0], p.o[2], scale, tw);
 }
 
-inline bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {
+// (A template, so that only the units that run the plan instantiate its kernels.)
+template <int DT = NSQ_DTYPE_F32>
+bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2* tw, hipStream_t st) {
   const int64_t nk = p.kb * p.H;
-  if (!inner_fwd<NSQ_DTYPE_F32>(p, k, nk, p.K[0], p.K[1], p.K[2], false, wsk, tw, st)) return false;
+  if (!inner_fwd<DT>(p, k, nk, p.K[0], p.K[1], p.K[2], false, wsk, tw, st)) return false;
   return col_pass<false>(p, wsk, nk, 0, 1, p.K[0], 0, p.F[0], tw, st);
 }
+
+// The mixed-radix plan's passes (fftconv_nd_r3.hip, one instance per dtype),
+// same arguments, workspace layout and results as run_nd_fwd / run_nd_bwd.
+template <int DT>
+bool run_r3_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws, bool save,
+                const float2* tw, hipStream_t st);
+template <int DT>
+bool run_r3_bwd(const NdPlan& p, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
+                float* gs, float2* ws, bool fwd_state, const float2* tw, hipStream_t st);
+#define NSQ_R3_RUN_INSTANCES(EXT, DT)                                                                               \
+  EXT template bool run_r3_fwd<DT>(const NdPlan&, const void*, const float*, const void*, void*, float2*, bool,    \
+                                   const float2*, hipStream_t);                                                  \
+  EXT template bool run_r3_bwd<DT>(const NdPlan&, const void*, const void*, const float*, const void*, void*,      \
+                                   float*, float*, float2*, bool, const float2*, hipStream_t);
+NSQ_R3_RUN_INSTANCES(extern, NSQ_DTYPE_F32)
+NSQ_R3_RUN_INSTANCES(extern, NSQ_DTYPE_BF16)
+NSQ_R3_RUN_INSTANCES(extern, NSQ_DTYPE_F16)
 
 // Workspace layout (spectrum blocks of p.spec complex64):
 //   backward: [G: BH | X: BH | Khat: NK | Q: NK | (nz - 1) * NK partial Q]
@@ -396,6 +452,10 @@ template <int DT, bool GATED = false>
 bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws, bool save,
                 const float2* tw, hipStream_t st, const GatedIO* gate = nullptr) {
   constexpr int GM = GATED ? GATED_FWD : GATED_NONE;
+  if (p.r3) {  // the gated ops run their gate kernels around the plain conv on this plan
+    if constexpr (GATED) return false;
+    else return run_r3_fwd<DT>(p, x, k, s, y, ws, save, tw, st);
+  }
   const int64_t BH = p.B * p.H;
   float2* wsx = save ? ws + BH * p.spec : ws;
   float2* wsk = wsx + BH * p.spec;
@@ -464,6 +524,10 @@ inline bool w128_bwd_on() {
 template <int DT, bool GATED = false>
 bool run_nd_bwd(const NdPlan& p, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
                 float* gs, float2* ws, bool fwd_state, const float2* tw, hipStream_t st, const GatedIO* gate = nullptr) {
+  if (p.r3) {
+    if constexpr (GATED) return false;
+    else return run_r3_bwd<DT>(p, g, x, k, s, gx, gk, gs, ws, fwd_state, tw, st);
+  }
   const int64_t BH = p.B * p.H, NK = p.kb * p.H;
   float2* wsg = ws;
   float2* wsx = wsg + BH * p.spec;

@@ -54,6 +54,13 @@ void clear_error();
 // first call for the current device.  nullptr on failure (error recorded).
 const float2* twiddle_table();
 
+// Twiddle table layout (float2 entries, forward roots W_L^j = e^{-2 pi i j / L}):
+//   W_{2^b},   b <= 14:          entries 2^b + j;
+//   W_{3*2^b}, b <= kTw3MaxLog:  entries kTwPow2Entries + 3*2^b + j.
+constexpr int kTwPow2Entries = 2 << 14;
+constexpr int kTw3MaxLog = 10;
+constexpr int kTwEntries = kTwPow2Entries + (6 << kTw3MaxLog);
+
 inline bool valid_dtype(int dt) {
   return dt == NSQ_DTYPE_F32 || dt == NSQ_DTYPE_BF16 || dt == NSQ_DTYPE_F16;
 }

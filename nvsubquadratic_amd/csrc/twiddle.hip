@@ -5,7 +5,9 @@
 // buffers.  Layout (float2 = (cos, -sin), i.e. forward-transform roots):
 //   segment b (b = 0..14) at entries [2^b, 2^(b+1)): W_{2^b}^j = exp(-2*pi*i*j/2^b)
 // so a root of unity W_{2^b}^m with b <= 14 is one load, table[2^b + m], and a
-// pass of a length-2^b transform reads one contiguous 2^b-entry segment.
+// pass of a length-2^b transform reads one contiguous 2^b-entry segment;
+//   then the roots of the mixed-radix lengths 3*2^b (b = 0..kTw3MaxLog) at
+//   entries kTwPow2Entries + [3*2^b, 3*2^(b+1)).
 // Values are computed on the host in double precision and rounded once to
 // float (within 0.5 ulp of the exact root).
 #include <cmath>
@@ -43,15 +45,17 @@ const float2* twiddle_table() {
   std::lock_guard<std::mutex> lock(g_tw_mutex);
   if (g_tw[dev]) return g_tw[dev];
   constexpr int kLogMax = 14;
-  std::vector<float2> host(size_t(2) << kLogMax, make_float2(1.f, 0.f));
+  static_assert(kTwPow2Entries == (2 << kLogMax), "twiddle table: power-of-two region size");
+  std::vector<float2> host(size_t(kTwEntries), make_float2(1.f, 0.f));
   const double two_pi = 6.283185307179586476925286766559;
-  for (int b = 0; b <= kLogMax; ++b) {
-    const int n = 1 << b;
+  auto segment = [&](size_t start, int n) {
     for (int j = 0; j < n; ++j) {
       const double a = two_pi * double(j) / double(n);
-      host[size_t(n) + j] = make_float2(float(std::cos(a)), float(-std::sin(a)));
+      host[start + j] = make_float2(float(std::cos(a)), float(-std::sin(a)));
     }
-  }
+  };
+  for (int b = 0; b <= kLogMax; ++b) segment(size_t(1) << b, 1 << b);
+  for (int b = 0; b <= kTw3MaxLog; ++b) segment(size_t(kTwPow2Entries) + (size_t(3) << b), 3 << b);
   float2* d = nullptr;
   hipError_t e = hipMalloc(&d, host.size() * sizeof(float2));
   if (e != hipSuccess) {

@@ -98,6 +98,37 @@ def test_missing_library_raises_at_call_time(monkeypatch, tmp_path):
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
+def test_nd_plan_uses_the_reference_fft_sizes_where_smaller(monkeypatch):
+    """3D zero-padded axes run at the reference's F_d = S_d + ceil(K_d/2) rounded to 48 / 96 (axis 0 also 192)
+    when that spectrum is smaller than the power-of-two one (ops/fftconv.py:774-778); NSQ_ND_R3=0 selects the
+    power-of-two plan.  Read back through the workspace size: (B*H + H) spectrum blocks of F0 F1 (F2/2 + 1)."""
+    lib = _lib.get_lib()
+
+    def fwd_bytes(xs, ks):
+        S, K = _lib.i64_array(xs[2:]), _lib.i64_array(ks)
+        return lib.nsq_fftconv_nd_workspace_bytes(3, xs[0], xs[1], S, K, 1, _lib.NSQ_DIR_FWD)
+
+    def blocks(xs, f0, f1, f2):
+        return (xs[0] * xs[1] + xs[1]) * f0 * f1 * (f2 // 2 + 1) * 8
+
+    cfg5 = ((2, 128, 64, 64, 64), (64, 64, 64))
+    assert fwd_bytes(*cfg5) == blocks(cfg5[0], 96, 96, 96)
+    assert fwd_bytes((1, 2, 128, 32, 32), (128, 32, 32)) == blocks((1, 2), 192, 48, 48)
+    assert fwd_bytes((2, 3, 33, 45, 27), (29, 7, 41)) == blocks((2, 3), 48, 96, 48)
+    # power of two where it is smaller: need 11 -> 16 on axis 0 (48 would be larger)
+    assert fwd_bytes((1, 2, 9, 64, 64), (4, 64, 64)) == blocks((1, 2), 16, 128, 128)
+    # an axis past 96 (axes 1, 2) keeps the power-of-two plan: 6+3 -> 16, 100+11 -> 128, 50+14 -> 64
+    assert fwd_bytes((1, 2, 6, 100, 50), (5, 21, 27)) == blocks((1, 2), 16, 128, 64)
+    monkeypatch.setenv("NSQ_ND_R3", "0")
+    assert fwd_bytes(*cfg5) == blocks(cfg5[0], 128, 128, 128)
+    # periodic axes keep F_d = S_d
+    S, K = _lib.i64_array([64, 64, 64]), _lib.i64_array([64, 64, 64])
+    monkeypatch.delenv("NSQ_ND_R3")
+    assert lib.nsq_mixed_fftconv_nd_workspace_bytes(3, 2, 128, S, K, 1, 1, _lib.NSQ_DIR_FWD) == blocks(
+        cfg5[0], 64, 128, 128)
+
+
 def test_nd_spectrum_block_over_2gib_rejected():
     """The 2D/3D column passes address one spectrum block with 32-bit byte
     offsets; a block of 2 GiB or more (F = 1024^3: 1024*1024*513 complex) must be
