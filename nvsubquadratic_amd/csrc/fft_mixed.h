@@ -47,6 +47,27 @@ struct TwAny {
   }
 };
 
+// The roots W_Q^m (m < Q) of one length Q staged in LDS by the workgroup: a
+// pass of period L (Q a multiple of L) reads W_L^x = W_Q^{x Q / L} there,
+// an LDS read instead of a global one in every pass of every transform.
+template <int Q>
+struct TwLds {
+  const float2* s;
+  template <int L>
+  __device__ __forceinline__ float2 root(int x) const {
+    static_assert(Q % L == 0, "TwLds: the staged length must be a multiple of the pass period");
+    return s[x * (Q / L)];
+  }
+};
+
+// Stages W_Q^m for m < Q into s (all T threads; the caller synchronises).
+template <int Q, int T>
+__device__ __forceinline__ TwLds<Q> stage_roots(float2* s, const float2* __restrict__ tw) {
+  const TwAny ta(tw);
+  for (int m = int(threadIdx.x); m < Q; m += T) s[m] = ta.root<Q>(m);
+  return TwLds<Q>{s};
+}
+
 // In-register DFT of 3 points (natural order in and out), INV with conjugate
 // roots (unscaled): X0 = a + s, X1,2 = a - s/2 -/+ i sin(2 pi / 3) d, with
 // s = b + c, d = b - c.
@@ -110,8 +131,9 @@ __device__ __forceinline__ void mixed_store(ST& st, int m, int n, float2 v) {
 // elements j + r N/R, multiplies by W_{NS R}^{r (j mod NS)}, transforms, and
 // writes elements (j - j mod NS) R + j mod NS + r NS.  TMAJOR as in
 // stockham_pass.  Barriers bracket the writes, so LD and ST may alias.
-template <int N, int R, int NS, bool INV, int M, int T, bool TMAJOR, class LD, class ST>
-__device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const float2* __restrict__ tw) {
+// TW: the roots' source (TwAny: the global table; TwLds: roots staged in LDS).
+template <int N, int R, int NS, bool INV, int M, int T, bool TMAJOR, class LD, class ST, class TW>
+__device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const TW& tws) {
   constexpr int NR = N / R;
   constexpr int NB = M * NR;
   constexpr int PER = (NB + T - 1) / T;
@@ -121,14 +143,13 @@ __device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const float2* __restr
   const int tid = opaque_tid();
   float2 w[PER][R];
   if constexpr (NS > 1) {
-    const TwAny ta(tw);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int bf = EXACT ? tid + i * T : ((tid + i * T) < NB ? tid + i * T : 0);
       const int j = TMAJOR ? (bf / M) : (bf % NR);
       const int k = j % NS;
 #pragma unroll
-      for (int r = 1; r < R; ++r) w[i][r] = ta.root<L>(r * k);
+      for (int r = 1; r < R; ++r) w[i][r] = tws.template root<L>(r * k);
     }
   }
   float2 v[PER][R];
@@ -163,29 +184,29 @@ __device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const float2* __restr
 // Full transform of M length-N sequences (first pass through ld_first, last
 // through st_last, the passes between in the LDS tile st_lds / ld_lds), radix
 // at most RMAX after the radix-3 pass.  Ends with a barrier.
-template <int N, int NS, bool INV, int M, int T, bool TMAJOR, int RMAX, class LDF, class STL, class LDL, class STF>
-__device__ __forceinline__ void fft_mixed_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last,
-                                              const float2* __restrict__ tw) {
+template <int N, int NS, bool INV, int M, int T, bool TMAJOR, int RMAX, class LDF, class STL, class LDL, class STF,
+          class TW>
+__device__ __forceinline__ void fft_mixed_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last, const TW& tws) {
   constexpr int R = mixed_radix(N, NS, RMAX);
   constexpr bool FIRST = NS == 1;
   constexpr bool LAST = NS * R == N;
   if constexpr (FIRST && LAST) {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_first, st_last, tw);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_first, st_last, tws);
   } else if constexpr (FIRST) {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_first, st_lds, tw);
-    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX>(ld_first, st_lds, ld_lds, st_last, tw);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_first, st_lds, tws);
+    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX>(ld_first, st_lds, ld_lds, st_last, tws);
   } else if constexpr (LAST) {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_lds, st_last, tw);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_lds, st_last, tws);
   } else {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_lds, st_lds, tw);
-    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX>(ld_first, st_lds, ld_lds, st_last, tw);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_lds, st_lds, tws);
+    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX>(ld_first, st_lds, ld_lds, st_last, tws);
   }
 }
 
-template <int N, bool INV, int M, int T, bool TMAJOR, int RMAX, class LDF, class TILE, class STF>
-__device__ __forceinline__ void fft_mixed(LDF& ld_first, TILE& tile, STF& st_last, const float2* __restrict__ tw) {
+template <int N, bool INV, int M, int T, bool TMAJOR, int RMAX, class LDF, class TILE, class STF, class TW>
+__device__ __forceinline__ void fft_mixed(LDF& ld_first, TILE& tile, STF& st_last, const TW& tws) {
   static_assert(mixed_len(N), "fft_mixed: length must be 2^m or 3 * 2^m");
-  fft_mixed_rec<N, 1, INV, M, T, TMAJOR, RMAX>(ld_first, tile, tile, st_last, tw);
+  fft_mixed_rec<N, 1, INV, M, T, TMAJOR, RMAX>(ld_first, tile, tile, st_last, tws);
 }
 
 }  // namespace nsq

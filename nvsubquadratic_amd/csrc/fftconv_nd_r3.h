@@ -35,12 +35,16 @@ struct R3PlaneCfg {
   static constexpr int FH = N2 + 1;        // spectrum bins per row
   static constexpr int RS = N2 + N2 / 16;  // LDS row stride (pad16 positions)
   static constexpr int T = 192;
-  // rows per row tile (a divisor of F1, so every tile lies inside the plane)
-  static constexpr int MR = F1 * N2 > 2304 ? 2304 / N2 : F1;
-  static constexpr int ROWR = 4;                      // largest power-of-two radix of the row passes
-  static constexpr int COLR = F1 * N2 >= 4608 ? 8 : 4;  // ... of the column passes
-  static constexpr int SLOTS = (MR * N2 / 2 + T - 1) / T;
-  static_assert(F1 % MR == 0, "R3PlaneCfg: row tiles must tile the plane");
+  // rows per row tile: 64 for 48-point rows in a 96-row plane (a Hyena
+  // volume's 64 valid rows in one tile), else a divisor of F1; the inverse
+  // takes the rows past the last whole tile in one tile of MRB = F1 % MR rows,
+  // so no tile reaches past the plane.
+  static constexpr int MR = (N2 == 48 && F1 == 96) ? 64 : (F1 * N2 > 2304 ? 2304 / N2 : F1);
+  static constexpr int MRB = F1 % MR;
+  static constexpr int ROWR = 16;                 // largest power-of-two radix of the row passes
+  static constexpr int COLR = F1 == 48 ? 16 : 8;  // ... of the column passes
+  static constexpr int Q = F1 > 2 * N2 ? F1 : 2 * N2;  // roots staged in LDS: W_Q covers every pass and the real unpack
+  static_assert(MR <= F1, "R3PlaneCfg: row tile");
 };
 
 // THIRD: len <= 2 F2 / 3 and n1 <= 2 F1 / 3, so the third input of every
@@ -52,12 +56,17 @@ __global__ __launch_bounds__(192) void r3_plane_fwd_kernel(const typename Elem<D
   using C = R3PlaneCfg<N2, F1>;
   constexpr int N = C::N, RS = C::RS, T = C::T, MR = C::MR;
   __shared__ float2 P[F1 * RS];
+  __shared__ float2 twl[C::Q];
   const int64_t plane = blockIdx.x;  // bh * n0 + a0
   const int64_t xoff = plane * n1 * len;
-  const TwAny ta(tw);
+  const auto tws = stage_roots<C::Q, T>(twl, tw);
+  __syncthreads();
   // Axis 2: real transforms of the valid rows, unpacked in place to V (V[0]
   // = U[0] + i U[N], V[p] = U[p]); rows of a tile past n1 transform zeros.
-  for (int r0 = 0; r0 < n1; r0 += MR) {
+  // A last tile that would pass the plane's end moves back and recomputes
+  // rows already done (from the input, so with the same values).
+  for (int rb = 0; rb < n1; rb += MR) {
+    const int r0 = rb + MR <= F1 ? rb : F1 - MR;
     LdsTile<RS, true> rows{P + r0 * RS};
     auto ld = [&](int m, int n) -> float2 {
       const int a1 = r0 + m;
@@ -65,10 +74,11 @@ __global__ __launch_bounds__(192) void r3_plane_fwd_kernel(const typename Elem<D
       return load_pair_nb<DT, AL>(src + xoff + int64_t(ok ? a1 : 0) * len, 2 * int64_t(n), ok ? len : 0);
     };
     TailZeroLoad<3, 2, THIRD, decltype(ld)> ld1{ld};
-    fft_mixed<N, false, MR, T, false, C::ROWR>(ld1, rows, rows, tw);
+    fft_mixed<N, false, MR, T, false, C::ROWR>(ld1, rows, rows, tws);
     const int ts = opaque_tid();
+    constexpr int SLOTS = (MR * (N / 2) + T - 1) / T;
 #pragma unroll
-    for (int i = 0; i < C::SLOTS; ++i) {
+    for (int i = 0; i < SLOTS; ++i) {
       const int s = ts + i * T;
       if (s >= MR * (N / 2)) continue;
       const int m = s / (N / 2), p = s - m * (N / 2);
@@ -76,7 +86,7 @@ __global__ __launch_bounds__(192) void r3_plane_fwd_kernel(const typename Elem<D
       float2* z = P + (r0 + m) * RS;
       const int pb = pad16(p0 ? N / 2 : N - p);
       float2 A, Bc;
-      real_unpack(p0, z[pad16(p)], z[pb], ta.root<2 * N>(p), A, Bc);
+      real_unpack(p0, z[pad16(p)], z[pb], tws.template root<2 * N>(p), A, Bc);
       z[pad16(p)] = A;
       z[pb] = p0 ? Bc : cconj(Bc);
     }
@@ -90,7 +100,7 @@ __global__ __launch_bounds__(192) void r3_plane_fwd_kernel(const typename Elem<D
     return make_float2(ok ? v.x : 0.f, ok ? v.y : 0.f);
   };
   TailZeroLoad<3, 2, THIRD, decltype(ldc)> ldc1{ldc};
-  fft_mixed<F1, false, N, T, true, C::COLR>(ldc1, cols, cols, tw);
+  fft_mixed<F1, false, N, T, true, C::COLR>(ldc1, cols, cols, tws);
   // Store [F1][FH]; column 0 separates into the DC (j = 0) and Nyquist (j = N) bins.
   float2* out = ws + (plane / n0) * spec + (plane % n0) * int64_t(F1) * C::FH;
   const int t = opaque_tid();
@@ -124,7 +134,8 @@ __global__ __launch_bounds__(192) void r3_plane_inv_kernel(const float2* __restr
   const int64_t bh = plane / n0;
   const int a0 = int(plane - bh * n0);
   const float2* in = ws + bh * spec + int64_t(a0) * F1 * C::FH;
-  const TwAny ta(tw);
+  __shared__ float2 twl[C::Q];
+  const auto tws = stage_roots<C::Q, T>(twl, tw);
   const int t = opaque_tid();
 #pragma unroll 8
   for (int e = t; e < F1 * N; e += T) {
@@ -143,31 +154,34 @@ __global__ __launch_bounds__(192) void r3_plane_inv_kernel(const float2* __restr
     const int r = k - off1;
     if (r >= 0 && r < n1out) P[r * RS + pad16(m)] = v;
   };
-  fft_mixed<F1, true, N, T, true, C::COLR>(cols, cols, stc, tw);
+  fft_mixed<F1, true, N, T, true, C::COLR>(cols, cols, stc, tws);
   const ET* __restrict__ aux = (const ET*)o.aux;
   const int h = int(bh % o.H);
   const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load((const ET*)o.s, h)) : 0.f;
   const bool fast = MODE == ND_OUT_Y && (o.off2 & 1) == 0 && (o.w2 & 7) == 0 && o.w2 <= 2 * N &&
                     ((reinterpret_cast<uintptr_t>(o.out) | (HAS_S ? reinterpret_cast<uintptr_t>(o.aux) : 0)) & 15) == 0;
-  for (int r0 = 0; r0 < n1out; r0 += MR) {
+  // One tile of MRT rows from row r0: repack, inverse, epilogue.
+  auto row_tile = [&](auto mrc, int r0) {
+    constexpr int MRT = decltype(mrc)::value;
+    constexpr int SLOTS = (MRT * (N / 2) + T - 1) / T;
 #pragma unroll
-    for (int i = 0; i < C::SLOTS; ++i) {
+    for (int i = 0; i < SLOTS; ++i) {
       const int s = t + i * T;
-      if (s >= MR * (N / 2)) continue;
+      if (s >= MRT * (N / 2)) continue;
       const int m = s / (N / 2), p = s - m * (N / 2);
       const bool p0 = (p == 0);
       float2* z = P + (r0 + m) * RS;
       const int pb = pad16(p0 ? N / 2 : N - p);
       const float2 b = z[pb];
       float2 zp, zq;
-      real_repack(p0, z[pad16(p)], p0 ? b : cconj(b), ta.root<2 * N>(p), zp, zq);
+      real_repack(p0, z[pad16(p)], p0 ? b : cconj(b), tws.template root<2 * N>(p), zp, zq);
       z[pad16(p)] = zp;
       z[pb] = zq;
     }
     __syncthreads();
     LdsTile<RS, true> rows{P + r0 * RS};
-    fft_mixed<N, true, MR, T, false, C::ROWR>(rows, rows, rows, tw);
-    const int nrows = (n1out - r0) < MR ? (n1out - r0) : MR;
+    fft_mixed<N, true, MRT, T, false, C::ROWR>(rows, rows, rows, tws);
+    const int nrows = (n1out - r0) < MRT ? (n1out - r0) : MRT;
     if constexpr (MODE == ND_OUT_Y) {
       if (fast) {
         // 8 consecutive kept samples per thread: four complex values from
@@ -193,7 +207,7 @@ __global__ __launch_bounds__(192) void r3_plane_inv_kernel(const float2* __restr
           store8<DT, true>(ob, e0, yv);
         }
         __syncthreads();
-        continue;
+        return;
       }
     }
     for (int e = t; e < nrows * o.w2; e += T) {
@@ -211,6 +225,15 @@ __global__ __launch_bounds__(192) void r3_plane_inv_kernel(const float2* __restr
       }
     }
     __syncthreads();
+  };
+  for (int r0 = 0; r0 < n1out;) {  // in place, so tiles do not overlap: whole tiles, then MRB rows
+    if (r0 + MR <= F1) {
+      row_tile(std::integral_constant<int, MR>{}, r0);
+      r0 += MR;
+    } else {
+      if constexpr (C::MRB > 0) row_tile(std::integral_constant<int, C::MRB>{}, r0);
+      r0 += C::MRB > 0 ? C::MRB : F1;  // (MRB = 0: MR divides F1 and this branch is not reached)
+    }
   }
 }
 
@@ -224,8 +247,12 @@ struct R3ColCfg {
   static constexpr int M = F0 == 48 ? 32 : 16;
   static constexpr int S = F0 + 1;
   static constexpr int T = 128;
-  static constexpr int RMAX = F0 == 192 ? 8 : 4;
+  static constexpr int RMAX = F0 == 48 ? 16 : 8;
   static constexpr int PT = M * F0 / T;  // spectrum elements per thread (one column, stride T / M)
+  // Occupancy target of the adjoint: 3 waves/SIMD (<= 168 VGPRs) for F0 <= 96,
+  // which costs 13 spilled registers at F0 = 96 and runs 801 -> 749 us at
+  // config 5 (measured); F0 = 192 cannot reach it.
+  static constexpr int BWD_WAVES = F0 <= 96 ? 3 : 1;
   static_assert(T % M == 0 && (M * F0) % T == 0, "R3ColCfg: tile");
 };
 
@@ -236,13 +263,16 @@ __global__ __launch_bounds__(128) void r3_col_fwd_kernel(float2* __restrict__ ws
                                                          const float2* __restrict__ tw) {
   using C = R3ColCfg<F0>;
   __shared__ float2 lds[C::M * C::S];
+  __shared__ float2 twl[F0];
+  const auto tws = stage_roots<F0, C::T>(twl, tw);
+  __syncthreads();
   const ColBuf cb(ws + int64_t(blockIdx.x) * cg.spec, cg);
   const int j0 = int(blockIdx.y) * C::M;
   auto ld = [&](int m, int n) -> float2 { return cb.load(n, j0 + m, j0 + m < cg.inner_count && n < in_cnt); };
   auto st = [&](int m, int k, float2 v) { cb.store(k, j0 + m, j0 + m < cg.inner_count, v); };
   TailZeroLoad<3, 2, THIRD, decltype(ld)> ld1{ld};
   LdsTile<C::S, false> tile{lds};
-  fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ld1, tile, st, tw);
+  fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ld1, tile, st, tws);
 }
 
 // Forward conv along axis 0: FFT(x column) * Khat -> IFFT -> window [c0, c0 +
@@ -257,6 +287,9 @@ __global__ __launch_bounds__(128) void r3_col_mul_kernel(const float2* wsx, floa
                                                          const float2* __restrict__ tw) {
   using C = R3ColCfg<F0>;
   __shared__ float2 lds[C::M * C::S];
+  __shared__ float2 twl[F0];
+  const auto tws = stage_roots<F0, C::T>(twl, tw);
+  __syncthreads();
   const int64_t hk = blockIdx.x / bsplit;
   const int part = int(blockIdx.x % bsplit);
   const ColBuf kb(wsk + hk * cg.spec, cg);
@@ -276,7 +309,7 @@ __global__ __launch_bounds__(128) void r3_col_mul_kernel(const float2* wsx, floa
     const ColBuf out(wsy + blk, cg);
     auto ld = [&](int mm, int n) -> float2 { return in.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0); };
     TailZeroLoad<3, 2, THIRD, decltype(ld)> ld1{ld};
-    fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ld1, tile, tile, tw);
+    fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ld1, tile, tile, tws);
 #pragma unroll
     for (int it = 0; it < C::PT; ++it) {
       float2& z = lds[m * C::S + kfirst + it * (C::T / C::M)];
@@ -287,7 +320,7 @@ __global__ __launch_bounds__(128) void r3_col_mul_kernel(const float2* wsx, floa
       const int e = k - c0;
       out.store(e, j0 + mm, j0 + mm < cg.inner_count && uint32_t(e) < uint32_t(S0), v);
     };
-    fft_mixed<F0, true, C::M, C::T, true, C::RMAX>(tile, tile, st, tw);
+    fft_mixed<F0, true, C::M, C::T, true, C::RMAX>(tile, tile, st, tws);
   }
 }
 
@@ -310,13 +343,17 @@ __device__ __forceinline__ float2 r3_ramp_inner(const R3Ramp& rp, const TwAny& t
 // batch is split across workgroups and the partial Q blocks are summed by
 // nd_q_reduce_kernel.  THIRD: S0 <= 2 F0 / 3.
 template <int F0, bool THIRD>
-__global__ __launch_bounds__(128) void r3_col_bwd_kernel(float2* __restrict__ wsg, const float2* __restrict__ wsx,
+__global__ __launch_bounds__(128)
+__attribute__((amdgpu_waves_per_eu(R3ColCfg<F0>::BWD_WAVES))) void r3_col_bwd_kernel(float2* __restrict__ wsg, const float2* __restrict__ wsx,
                                                          const float2* __restrict__ wsk, float2* __restrict__ wsq,
                                                          ColGeom cg, int B, int H, int kfilm, int S0, int K0,
                                                          R3Ramp rp, int64_t qsplit, const float2* __restrict__ tw) {
   using C = R3ColCfg<F0>;
   __shared__ float2 ldsG[C::M * C::S];
   __shared__ float2 ldsX[C::M * C::S];  // X of the current image; at the end, Q
+  __shared__ float2 twl[F0];
+  const auto tws = stage_roots<F0, C::T>(twl, tw);
+  __syncthreads();
   const int64_t hk = blockIdx.x;
   const int j0 = int(blockIdx.y) * C::M;
   const ColBuf kb(wsk + hk * cg.spec, cg);
@@ -332,7 +369,7 @@ __global__ __launch_bounds__(128) void r3_col_bwd_kernel(float2* __restrict__ ws
   for (int it = 0; it < C::PT; ++it) {
     const int k = kfirst + it * (C::T / C::M);
     const float2 kv = kb.load(k, j, jok);
-    kr[it] = cmulc(cmul(r12, ta.root<F0>((rp.c0 * k) % F0)), kv);
+    kr[it] = cmulc(cmul(r12, tws.template root<F0>((rp.c0 * k) % F0)), kv);
     q[it] = make_float2(0.f, 0.f);
   }
   const int nb = kfilm ? 1 : B;
@@ -347,8 +384,8 @@ __global__ __launch_bounds__(128) void r3_col_bwd_kernel(float2* __restrict__ ws
     auto ldx = [&](int mm, int n) -> float2 { return xb.load(n, j0 + mm, j0 + mm < cg.inner_count && n < S0); };
     TailZeroLoad<3, 2, THIRD, decltype(ldg)> ldg1{ldg};
     TailZeroLoad<3, 2, THIRD, decltype(ldx)> ldx1{ldx};
-    fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ldg1, tG, tG, tw);
-    fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ldx1, tX, tX, tw);
+    fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ldg1, tG, tG, tws);
+    fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ldx1, tX, tX, tws);
 #pragma unroll
     for (int it = 0; it < C::PT; ++it) {
       const int a = m * C::S + kfirst + it * (C::T / C::M);
@@ -358,17 +395,17 @@ __global__ __launch_bounds__(128) void r3_col_bwd_kernel(float2* __restrict__ ws
     }
     __syncthreads();
     auto st = [&](int mm, int k, float2 v) { gb.store(k, j0 + mm, j0 + mm < cg.inner_count && k < S0, v); };
-    fft_mixed<F0, true, C::M, C::T, true, C::RMAX>(tG, tG, st, tw);  // ends with a barrier: ldsX is free
+    fft_mixed<F0, true, C::M, C::T, true, C::RMAX>(tG, tG, st, tws);  // ends with a barrier: ldsX is free
   }
 #pragma unroll
   for (int it = 0; it < C::PT; ++it) {
     const int k = kfirst + it * (C::T / C::M);
-    ldsX[m * C::S + k] = cmul(q[it], cmul(r12, ta.root<F0>((rp.c0 * k) % F0)));
+    ldsX[m * C::S + k] = cmul(q[it], cmul(r12, tws.template root<F0>((rp.c0 * k) % F0)));
   }
   __syncthreads();
   const ColBuf qb(wsq + (z * qsplit + hk) * cg.spec, cg);
   auto stq = [&](int mm, int k, float2 v) { qb.store(k, j0 + mm, j0 + mm < cg.inner_count && k < K0, v); };
-  fft_mixed<F0, true, C::M, C::T, true, C::RMAX>(tX, tX, stq, tw);
+  fft_mixed<F0, true, C::M, C::T, true, C::RMAX>(tX, tX, stq, tws);
 }
 
 }  // namespace nsq
