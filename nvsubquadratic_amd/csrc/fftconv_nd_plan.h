@@ -41,8 +41,8 @@ struct NdPlan {
   bool r3;       // mixed-radix plan (fftconv_nd_r3.h): F_d in {48, 96, 192}, lF unused
 };
 
-// The mixed-radix 3D plan is taken where it applies unless NSQ_ND_R3=0 (read
-// per call, so the workspace size and the run agree for a given setting).
+// The mixed-radix plan is taken where it applies unless NSQ_ND_R3=0 (read per
+// call, so the workspace size and the run agree for a given setting).
 inline bool nd_r3_allowed() {
   const char* e = std::getenv("NSQ_ND_R3");
   return !(e && e[0] == '0');
@@ -52,8 +52,9 @@ inline bool nd_r3_allowed() {
 inline int r3_col_m(int F0) { return F0 == 48 ? 32 : 16; }
 
 // `periodic`: bit d set = axis d (of the nd given axes) is periodic.
+// allow_r3 = false builds the power-of-two plan whatever the shape.
 inline bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const int64_t* K, int64_t kb,
-                         unsigned periodic, NdPlan& p) {
+                         unsigned periodic, NdPlan& p, bool allow_r3 = true) {
   if (nd != 2 && nd != 3) return false;
   if (periodic >> nd) return false;
   p.nd = nd;
@@ -117,17 +118,20 @@ inline bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
   // keep their compile-time row stride.
   p.RS = nd == 2 ? (p.FH + 15) / 16 * 16 : p.FH;
   p.spec = int64_t(p.F[0]) * p.F[1] * p.RS;
-  // The reference's FFT sizes (ops/fftconv.py:774-778: F_d = S_d + ceil(K_d/2),
-  // mixed-radix): a 3D volume with every axis zero-padded runs the
-  // mixed-radix plan when each axis fits a length 3 * 2^m it has kernels for
-  // (48 or 96; axis 0 also 192) and the spectrum is smaller than the
-  // power-of-two one (e.g. 96^3 against 128^3 at S = K = 64).
-  if (nd == 3 && periodic == 0 && nd_r3_allowed()) {
-    int f3[3];
+  // The reference's FFT sizes (ops/fftconv.py:699-702, 774-778: F_d = S_d +
+  // ceil(K_d/2), mixed-radix): with every axis zero-padded, the mixed-radix
+  // plan runs when each axis fits a length 3 * 2^m it has kernels for (3D:
+  // 48 or 96, axis 0 also 192; 2D: 48, 96 or 192) and the spectrum is smaller
+  // than the power-of-two one (96^3 against 128^3 at S = K = 64, 192^2
+  // against 256^2 at S = K = 128).
+  if (periodic == 0 && allow_r3 && nd_r3_allowed()) {
+    int f3[3] = {1, 1, 1};
     bool ok = true;
     for (int d = 0; d < 3; ++d) {
+      if (nd == 2 && d == 1) continue;
       const int64_t need = int64_t(s[d]) + (k[d] + 1) / 2;
-      f3[d] = need <= 48 ? 48 : need <= 96 ? 96 : (d == 0 && need <= 192) ? 192 : 0;
+      const bool long_ok = d == 0 || nd == 2;  // 192 on axis 0, and on both axes of a 2D plane
+      f3[d] = need <= 48 ? 48 : need <= 96 ? 96 : (long_ok && need <= 192) ? 192 : 0;
       ok = ok && f3[d] != 0;
     }
     const int64_t spec3 = int64_t(f3[0]) * f3[1] * (f3[2] / 2 + 1);
@@ -137,6 +141,7 @@ inline bool make_nd_plan(int nd, int64_t B, int64_t H, const int64_t* S, const i
         p.F[d] = f3[d];
         p.lF[d] = 0;
       }
+      p.pack = false;
       p.FH = p.RS = f3[2] / 2 + 1;
       p.spec = spec3;
     }
@@ -422,6 +427,25 @@ bool filter_spectrum(const NdPlan& p, const float* k, float2* wsk, const float2*
   return col_pass<false>(p, wsk, nk, 0, 1, p.K[0], 0, p.F[0], tw, st);
 }
 
+// A forward that keeps no state for a backward runs whole 2D images in one
+// kernel where the shape allows (fftconv2d_image.h); NSQ_2D_IMAGE_FWD=0
+// selects the passes of the plan instead.
+inline bool image_fwd_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("NSQ_2D_IMAGE_FWD");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+// The power-of-two plan of the shape of p (no periodic axes: the mixed-radix
+// plan has none).
+inline bool pow2_plan_of(const NdPlan& p, NdPlan& p2) {
+  const int64_t S[3] = {p.S[0], p.nd == 2 ? p.S[2] : p.S[1], p.S[2]};
+  const int64_t K[3] = {p.K[0], p.nd == 2 ? p.K[2] : p.K[1], p.K[2]};
+  return make_nd_plan(p.nd, p.B, p.H, S, K, p.kb, 0u, p2, false);
+}
+
 // The mixed-radix plan's passes (fftconv_nd_r3.hip, one instance per dtype),
 // same arguments, workspace layout and results as run_nd_fwd / run_nd_bwd.
 template <int DT>
@@ -453,22 +477,30 @@ bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, v
                 const float2* tw, hipStream_t st, const GatedIO* gate = nullptr) {
   constexpr int GM = GATED ? GATED_FWD : GATED_NONE;
   if (p.r3) {  // the gated ops run their gate kernels around the plain conv on this plan
-    if constexpr (GATED) return false;
-    else return run_r3_fwd<DT>(p, x, k, s, y, ws, save, tw, st);
+    if constexpr (GATED) {
+      return false;
+    } else {
+      // A 2D forward that keeps no state runs the one-kernel image forward of
+      // the power-of-two plan where that applies: 0.82 ms against 1.00 ms for
+      // the mixed-radix passes at config 4 (measured).  Its filter spectrum
+      // (H blocks of 256 x 128) goes to the workspace start; the mixed-radix
+      // forward workspace ((B + 1) H blocks of 192 x 97) holds it.
+      NdPlan p2;
+      if (!save && p.nd == 2 && p.kb == 1 && image_fwd_enabled() && pow2_plan_of(p, p2) && image_fwd_ok(p2, x, y) &&
+          p2.H * p2.spec <= (p.B * p.H + p.H) * p.spec) {
+        if (!filter_spectrum(p2, k, ws, tw, st)) return false;
+        launch_image_fwd<DT>(p2, x, ws, s, y, tw, st);
+        return true;
+      }
+      return run_r3_fwd<DT>(p, x, k, s, y, ws, save, tw, st);
+    }
   }
   const int64_t BH = p.B * p.H;
   float2* wsx = save ? ws + BH * p.spec : ws;
   float2* wsk = wsx + BH * p.spec;
   float2* wsy = save ? ws : wsx;
   if (!filter_spectrum(p, k, wsk, tw, st)) return false;
-  // A forward that keeps no state for a backward runs whole images in one
-  // kernel where the shape allows (fftconv2d_image.h); NSQ_2D_IMAGE_FWD=0
-  // selects the three passes below.
-  static const bool image_on = [] {
-    const char* e = std::getenv("NSQ_2D_IMAGE_FWD");
-    return !(e && e[0] == '0');
-  }();
-  if (!GATED && !save && image_on && image_fwd_ok(p, x, y)) {
+  if (!GATED && !save && image_fwd_enabled() && image_fwd_ok(p, x, y)) {
     launch_image_fwd<DT>(p, x, wsk, s, y, tw, st);
     return true;
   }

@@ -1,23 +1,25 @@
-// 3D non-causal "same" FFT convolution at the reference's own FFT sizes.
+// 2D / 3D non-causal "same" FFT convolution at the reference's own FFT sizes.
 //
-// nvsubquadratic/ops/fftconv.py:774-778 pads axis d of a 3D conv to
-// F_d = S_d + ceil(K_d / 2) points and transforms with torch.fft, whose plans
+// nvsubquadratic/ops/fftconv.py:699-702 (2D) and :774-778 (3D) pad axis d to
+// F_d = S_d + ceil(K_d / 2) points and transform with torch.fft, whose plans
 // are mixed-radix.  The power-of-two plan of fftconv_nd_impl.h rounds F_d up
 // to 2^m instead: the same results (no wrapped term reaches the cropped
 // window either way), but at the Hyena shapes S_d = K_d = 2^a the reference's
-// F_d = 3 * 2^(a-1) gives a spectrum (F0 F1 (F2/2 + 1) complex values) 2.37x
-// smaller than the power-of-two one.  This plan runs those sizes: every axis
-// of length 48, 96 (or 192 on axis 0), each the smallest such length >= S_d +
-// ceil(K_d / 2), used when its spectrum is smaller than the power-of-two
-// plan's.  Layout and passes are those of the power-of-two 3D plan:
-//   workspace block [F0][F1][FH], FH = F2/2 + 1;
-//   r3_plane_fwd : real transforms along axis 2 and complex ones along
+// F_d = 3 * 2^(a-1) gives a spectrum 2.37x (3D) or 1.76x (2D) smaller than the
+// power-of-two one.  This plan runs those sizes: every axis of length 48 or 96
+// (192 on axis 0, and on both axes of a 2D plane), each the smallest such
+// length >= S_d + ceil(K_d / 2), used when its spectrum is smaller than the
+// power-of-two plan's.  Layout and passes are those of the power-of-two plan:
+//   workspace block [F0][F1][FH], FH = F2/2 + 1 (2D: F1 = 1);
+//   r3_plane_fwd : (3D) real transforms along axis 2 and complex ones along
 //                  axis 1 of one (b, h, a0) plane in LDS;
+//   r3_row_fwd   : (2D) real transforms along the last axis;
 //   r3_col_fwd   : axis-0 forward transform (the filter);
 //   r3_col_mul   : axis-0 forward, spectral product, inverse, crop;
 //   r3_col_bwd   : axis-0 adjoint: P = G R conj(K), Q = R sum_b G conj(X),
 //                  R the shift ramp that puts gx and gk at window 0;
-//   r3_plane_inv : inverse along axis 1, crop, inverse real rows, epilogue.
+//   r3_plane_inv : (3D) inverse along axis 1, crop, inverse real rows, epilogue;
+//   r3_row_inv   : (2D) inverse real rows, crop, epilogue.
 // The transforms are fft_mixed.h's radix-3-first Stockham passes.
 #pragma once
 
@@ -238,6 +240,162 @@ __global__ __launch_bounds__(192) void r3_plane_inv_kernel(const float2* __restr
 }
 
 // ---------------------------------------------------------------------------
+// Row passes of the 2D plan: real transforms along the last axis between the
+// [rows][len] tensor (row r = (bh, a0), a0 < n0) and row a0 of spectrum block
+// bh ([F0][FH], FH = F2/2 + 1).  M rows of N2 = F2/2 packed points per
+// workgroup.
+// ---------------------------------------------------------------------------
+template <int N2>
+struct R3RowCfg {
+  static constexpr int N = N2;
+  static constexpr int FH = N2 + 1;
+  static constexpr int RS = N2 + N2 / 16;  // LDS row stride (pad16 positions)
+  static constexpr int T = 192;
+  static constexpr int M = 2304 / N2;      // 96, 48 or 24 rows
+  static constexpr int R = 16;             // largest power-of-two radix
+  static constexpr int SLOTS = (M * (N2 / 2) + T - 1) / T;
+};
+
+// THIRD: len <= 2 F2 / 3 (the third input of each first-pass radix-3
+// butterfly is zero padding).
+template <int N2, int DT, bool AL, bool THIRD>
+__global__ __launch_bounds__(192) void r3_row_fwd_kernel(const typename Elem<DT>::T* __restrict__ src, int nrows,
+                                                         int n0, int len, float2* __restrict__ ws, int64_t spec,
+                                                         const float2* __restrict__ tw) {
+  using C = R3RowCfg<N2>;
+  constexpr int N = C::N, RS = C::RS, T = C::T, M = C::M;
+  __shared__ float2 P[M * RS];
+  __shared__ float2 twl[2 * N];
+  const auto tws = stage_roots<2 * N, T>(twl, tw);
+  __syncthreads();
+  const int r0 = int(blockIdx.x) * M;
+  LdsTile<RS, true> rows{P};
+  auto ld = [&](int m, int n) -> float2 {
+    const int r = r0 + m;
+    const bool ok = r < nrows;
+    return load_pair_nb<DT, AL>(src + int64_t(ok ? r : 0) * len, 2 * int64_t(n), ok ? len : 0);
+  };
+  TailZeroLoad<3, 2, THIRD, decltype(ld)> ld1{ld};
+  fft_mixed<N, false, M, T, false, C::R>(ld1, rows, rows, tws);
+  const int ts = opaque_tid();
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    const int s = ts + i * T;
+    const int m = s / (N / 2), p = s - m * (N / 2);
+    const int r = r0 + m;
+    if (s >= M * (N / 2) || r >= nrows) continue;
+    const bool p0 = (p == 0);
+    const float2* z = P + m * RS;
+    float2 A, Bc;
+    real_unpack(p0, z[pad16(p)], z[pad16(p0 ? N / 2 : N - p)], tws.template root<2 * N>(p), A, Bc);
+    const int bh = int(uint32_t(r) / uint32_t(n0)), a0 = r - bh * n0;
+    float2* out = ws + int64_t(bh) * spec + int64_t(a0) * C::FH;
+    if (p0) {
+      out[0] = make_float2(A.x, 0.f);
+      out[N] = make_float2(A.y, 0.f);
+      out[N / 2] = Bc;
+    } else {
+      out[p] = A;
+      out[N - p] = cconj(Bc);
+    }
+  }
+}
+
+// Inverse: rows r < nrows ((bh, a0), a0 < n0) of the spectrum -> inverse
+// real transforms, window [off2, off2 + w2), epilogue (RowInvOut; output row
+// r at r * w2; ND_OUT_GK: gs[bh] = the value at (ga0, ga2)).
+template <int N2, int DT, int MODE, bool HAS_S>
+__global__ __launch_bounds__(192) void r3_row_inv_kernel(const float2* __restrict__ ws, int nrows, int n0,
+                                                         int64_t spec, RowInvOut o, const float2* __restrict__ tw) {
+  using C = R3RowCfg<N2>;
+  using ET = typename Elem<DT>::T;
+  constexpr int N = C::N, RS = C::RS, T = C::T, M = C::M;
+  __shared__ float2 P[M * RS];
+  __shared__ float2 twl[2 * N];
+  const auto tws = stage_roots<2 * N, T>(twl, tw);
+  __syncthreads();
+  const int r0 = int(blockIdx.x) * M;
+  const int t = opaque_tid();
+#pragma unroll
+  for (int i = 0; i < C::SLOTS; ++i) {
+    const int s = t + i * T;
+    if (s >= M * (N / 2)) continue;
+    const int m = s / (N / 2), p = s - m * (N / 2);
+    const int r = r0 + m;
+    const bool rok = r < nrows;
+    const int rr = rok ? r : 0;
+    const int bh = int(uint32_t(rr) / uint32_t(n0)), a0 = rr - bh * n0;
+    const float2* in = ws + int64_t(bh) * spec + int64_t(a0) * C::FH;
+    const bool p0 = (p == 0);
+    const float2 u0 = in[p0 ? 0 : p];
+    const float2 u1 = in[p0 ? N : N - p];
+    const float2 u2 = in[N / 2];
+    float2 A = p0 ? make_float2(u0.x, u1.x) : u0;
+    float2 Bc = p0 ? u2 : cconj(u1);
+    A = make_float2(rok ? A.x : 0.f, rok ? A.y : 0.f);
+    Bc = make_float2(rok ? Bc.x : 0.f, rok ? Bc.y : 0.f);
+    float2 zp, zq;
+    real_repack(p0, A, Bc, tws.template root<2 * N>(p), zp, zq);
+    float2* z = P + m * RS;
+    z[pad16(p)] = zp;
+    z[pad16(p0 ? N / 2 : N - p)] = zq;
+  }
+  __syncthreads();
+  LdsTile<RS, true> rows{P};
+  fft_mixed<N, true, M, T, false, C::R>(rows, rows, rows, tws);
+  const ET* __restrict__ aux = (const ET*)o.aux;
+  const int nr = (nrows - r0) < M ? (nrows - r0) : M;
+  const bool fast = MODE == ND_OUT_Y && (o.off2 & 1) == 0 && (o.w2 & 7) == 0 && o.w2 <= 2 * N &&
+                    ((reinterpret_cast<uintptr_t>(o.out) | (HAS_S ? reinterpret_cast<uintptr_t>(o.aux) : 0)) & 15) == 0;
+  if constexpr (MODE == ND_OUT_Y) {
+    if (fast) {
+      // 8 consecutive kept samples per thread: four complex values from LDS,
+      // one 16-byte shortcut load, one 16-byte store.
+      const int cpr = o.w2 >> 3;
+      const int64_t tb = int64_t(r0) * o.w2;
+      const RowBuf<DT, false> ab(aux + tb, HAS_S ? nr * o.w2 : 0);
+      const RowBuf<DT, true> ob((ET*)o.out + tb, nr * o.w2);
+      for (int ch = t; ch < nr * cpr; ch += T) {
+        const int m = ch / cpr, c8 = (ch - m * cpr) * 8;
+        const int e0 = m * o.w2 + c8;
+        Win8<DT, true> a{};
+        if constexpr (HAS_S) a.load(ab, e0);
+        const int bh = int(uint32_t(r0 + m) / uint32_t(n0));
+        const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load((const ET*)o.s, bh % o.H)) : 0.f;
+        const float2* zr = P + m * RS;
+        const int nc = (c8 + o.off2) >> 1;
+        float yv[8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float2 z = zr[pad16(nc + u)];
+          yv[2 * u] = epilogue<DT>(z.x * o.scale, HAS_S, sv, a.at(2 * u));
+          yv[2 * u + 1] = epilogue<DT>(z.y * o.scale, HAS_S, sv, a.at(2 * u + 1));
+        }
+        store8<DT, true>(ob, e0, yv);
+      }
+      return;
+    }
+  }
+  for (int e = t; e < nr * o.w2; e += T) {
+    const int m = e / o.w2, c = e - m * o.w2;
+    const int sidx = c + o.off2;
+    const float2 zz = P[m * RS + pad16(sidx >> 1)];
+    const float v = ((sidx & 1) ? zz.y : zz.x) * o.scale;
+    const int r = r0 + m;
+    const int bh = int(uint32_t(r) / uint32_t(n0));
+    const int64_t idx = int64_t(r) * o.w2 + c;
+    if constexpr (MODE == ND_OUT_Y) {
+      const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load((const ET*)o.s, bh % o.H)) : 0.f;
+      const float a = HAS_S ? Elem<DT>::load(aux, idx) : 0.f;
+      Elem<DT>::store((ET*)o.out, idx, epilogue<DT>(v, HAS_S, sv, a));
+    } else {
+      ((float*)o.out)[idx] = v;
+      if (o.gs && c == o.ga2 && r - bh * n0 == o.ga0) o.gs[bh] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Axis-0 column passes: M columns of a block per workgroup (lanes on
 // consecutive inner indices, so each row segment is one coalesced access),
 // transposed tile (element n of column m at m * S + n, S odd).
@@ -246,20 +404,20 @@ template <int F0>
 struct R3ColCfg {
   static constexpr int M = F0 == 48 ? 32 : 16;
   static constexpr int S = F0 + 1;
-  static constexpr int T = 128;
+  static constexpr int T = F0 == 192 ? 256 : 128;  // 12 points per thread (24 for F0 = 192 at 128 threads: 256 VGPRs)
   static constexpr int RMAX = F0 == 48 ? 16 : 8;
   static constexpr int PT = M * F0 / T;  // spectrum elements per thread (one column, stride T / M)
-  // Occupancy target of the adjoint: 3 waves/SIMD (<= 168 VGPRs) for F0 <= 96,
-  // which costs 13 spilled registers at F0 = 96 and runs 801 -> 749 us at
-  // config 5 (measured); F0 = 192 cannot reach it.
-  static constexpr int BWD_WAVES = F0 <= 96 ? 3 : 1;
+  // Occupancy target of the adjoint: 3 waves/SIMD (<= 168 VGPRs), which costs
+  // 13 spilled registers at F0 = 96 and runs 801 -> 749 us at config 5
+  // (measured).
+  static constexpr int BWD_WAVES = 3;
   static_assert(T % M == 0 && (M * F0) % T == 0, "R3ColCfg: tile");
 };
 
 // Forward transform of the first in_cnt rows (the rest zero), all F0 outputs
 // written; grid = (blocks, ceil(inner / M)).  THIRD: in_cnt <= 2 F0 / 3.
 template <int F0, bool THIRD>
-__global__ __launch_bounds__(128) void r3_col_fwd_kernel(float2* __restrict__ ws, ColGeom cg, int in_cnt,
+__global__ __launch_bounds__(R3ColCfg<F0>::T) void r3_col_fwd_kernel(float2* __restrict__ ws, ColGeom cg, int in_cnt,
                                                          const float2* __restrict__ tw) {
   using C = R3ColCfg<F0>;
   __shared__ float2 lds[C::M * C::S];
@@ -281,7 +439,7 @@ __global__ __launch_bounds__(128) void r3_col_fwd_kernel(float2* __restrict__ ws
 // loops over its share of the batch (its filter columns are read once);
 // FiLM: grid.x = B*H.  grid.y = column blocks.  THIRD: S0 <= 2 F0 / 3.
 template <int F0, bool THIRD>
-__global__ __launch_bounds__(128) void r3_col_mul_kernel(const float2* wsx, float2* wsy,
+__global__ __launch_bounds__(R3ColCfg<F0>::T) void r3_col_mul_kernel(const float2* wsx, float2* wsy,
                                                          const float2* __restrict__ wsk, ColGeom cg, int B, int H,
                                                          int kfilm, int S0, int c0, int bsplit,
                                                          const float2* __restrict__ tw) {
@@ -343,7 +501,7 @@ __device__ __forceinline__ float2 r3_ramp_inner(const R3Ramp& rp, const TwAny& t
 // batch is split across workgroups and the partial Q blocks are summed by
 // nd_q_reduce_kernel.  THIRD: S0 <= 2 F0 / 3.
 template <int F0, bool THIRD>
-__global__ __launch_bounds__(128)
+__global__ __launch_bounds__(R3ColCfg<F0>::T)
 __attribute__((amdgpu_waves_per_eu(R3ColCfg<F0>::BWD_WAVES))) void r3_col_bwd_kernel(float2* __restrict__ wsg, const float2* __restrict__ wsx,
                                                          const float2* __restrict__ wsk, float2* __restrict__ wsq,
                                                          ColGeom cg, int B, int H, int kfilm, int S0, int K0,

@@ -1,4 +1,4 @@
-// Host passes of the mixed-radix 3D plan (kernels in fftconv_nd_r3.h): the
+// Host passes of the mixed-radix 2D / 3D plan (kernels in fftconv_nd_r3.h): the
 // same pass sequence, workspace layout and results as run_nd_fwd /
 // run_nd_bwd in fftconv_nd_plan.h, at FFT lengths 3 * 2^m.
 #include "fftconv_nd_plan.h"
@@ -21,6 +21,17 @@ static bool with_r3_plane(const NdPlan& p, F&& f) {
   return true;
 }
 
+// N2 = F2 / 2 of the 2D row kernels.
+template <class F>
+static bool with_r3_row(const NdPlan& p, F&& f) {
+  switch (p.F[2] / 2) {
+    case 24: f(IC<24>{}); return true;
+    case 48: f(IC<48>{}); return true;
+    case 96: f(IC<96>{}); return true;
+    default: return false;
+  }
+}
+
 template <class F>
 static bool with_r3_col(const NdPlan& p, F&& f) {
   switch (p.F[0]) {
@@ -31,12 +42,31 @@ static bool with_r3_col(const NdPlan& p, F&& f) {
   }
 }
 
-// Forward plane passes of nbh blocks of [n0][n1][len] real planes.
+// Forward inner-axis passes of nbh blocks of [n0][n1][len] real values: the
+// plane kernels (3D), or the row kernels (2D, n1 = 1).
 template <int DT>
 static bool r3_inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, int n1, int len, float2* ws,
                          const float2* tw, hipStream_t st) {
   using ET = typename Elem<DT>::T;
   const bool al = pairs_aligned<DT>(src, len, len);
+  if (p.nd == 2) {
+    const bool third = 3 * len <= 2 * p.F[2];
+    const int rows = int(nbh * n0);
+    return with_r3_row(p, [&](auto NC) {
+      constexpr int N2 = decltype(NC)::value;
+      const dim3 grid(unsigned(ceil_div(rows, R3RowCfg<N2>::M)));
+      auto go = [&](auto a, auto th) {
+        hipLaunchKernelGGL((r3_row_fwd_kernel<N2, DT, decltype(a)::value, decltype(th)::value>), grid,
+                           dim3(R3RowCfg<N2>::T), 0, st, (const ET*)src, rows, n0, len, ws, p.spec, tw);
+      };
+      using T_ = std::true_type;
+      using F_ = std::false_type;
+      if (al)
+        third ? go(T_{}, T_{}) : go(T_{}, F_{});
+      else
+        third ? go(F_{}, T_{}) : go(F_{}, F_{});
+    });
+  }
   const bool third = 3 * len <= 2 * p.F[2] && 3 * n1 <= 2 * p.F[1];
   return with_r3_plane(p, [&](auto NC, auto FC) {
     constexpr int N2 = decltype(NC)::value, F1 = decltype(FC)::value;
@@ -60,6 +90,18 @@ template <int DT, int MODE>
 static bool r3_inner_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0, int off1, int n1out, RowInvOut o,
                          const float2* tw, hipStream_t st) {
   const bool has_s = MODE == ND_OUT_Y && o.s;
+  if (p.nd == 2) {
+    const int rows = int(nbh * n0);
+    return with_r3_row(p, [&](auto NC) {
+      constexpr int N2 = decltype(NC)::value;
+      const dim3 grid(unsigned(ceil_div(rows, R3RowCfg<N2>::M)));
+      auto go = [&](auto hs) {
+        hipLaunchKernelGGL((r3_row_inv_kernel<N2, DT, MODE, decltype(hs)::value>), grid, dim3(R3RowCfg<N2>::T), 0,
+                           st, ws, rows, n0, p.spec, o, tw);
+      };
+      has_s ? go(std::true_type{}) : go(std::false_type{});
+    });
+  }
   return with_r3_plane(p, [&](auto NC, auto FC) {
     constexpr int N2 = decltype(NC)::value, F1 = decltype(FC)::value;
     const dim3 grid(unsigned(nbh * n0));

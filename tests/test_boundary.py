@@ -98,10 +98,9 @@ def test_missing_library_raises_at_call_time(monkeypatch, tmp_path):
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
-@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libnsq_hip.so not built")
 def test_nd_plan_uses_the_reference_fft_sizes_where_smaller(monkeypatch):
-    """3D zero-padded axes run at the reference's F_d = S_d + ceil(K_d/2) rounded to 48 / 96 (axis 0 also 192)
-    when that spectrum is smaller than the power-of-two one (ops/fftconv.py:774-778); NSQ_ND_R3=0 selects the
+    """Zero-padded 2D / 3D axes run at the reference's F_d = S_d + ceil(K_d/2) rounded to 48 / 96 / 192 when that
+    spectrum is smaller than the power-of-two one (ops/fftconv.py:699-702, 774-778); NSQ_ND_R3=0 selects the
     power-of-two plan.  Read back through the workspace size: (B*H + H) spectrum blocks of F0 F1 (F2/2 + 1)."""
     lib = _lib.get_lib()
 
@@ -120,8 +119,12 @@ def test_nd_plan_uses_the_reference_fft_sizes_where_smaller(monkeypatch):
     assert fwd_bytes((1, 2, 9, 64, 64), (4, 64, 64)) == blocks((1, 2), 16, 128, 128)
     # an axis past 96 (axes 1, 2) keeps the power-of-two plan: 6+3 -> 16, 100+11 -> 128, 50+14 -> 64
     assert fwd_bytes((1, 2, 6, 100, 50), (5, 21, 27)) == blocks((1, 2), 16, 128, 64)
+    # 2D: config 4's 128^2 with K = 128 at 192^2 (rows of 97 bins) instead of 256^2 (128 packed bins)
+    S2, K2 = _lib.i64_array([128, 128]), _lib.i64_array([128, 128])
+    assert lib.nsq_fftconv_nd_workspace_bytes(2, 16, 384, S2, K2, 1, _lib.NSQ_DIR_FWD) == (16 * 384 + 384) * 192 * 97 * 8
     monkeypatch.setenv("NSQ_ND_R3", "0")
     assert fwd_bytes(*cfg5) == blocks(cfg5[0], 128, 128, 128)
+    assert lib.nsq_fftconv_nd_workspace_bytes(2, 16, 384, S2, K2, 1, _lib.NSQ_DIR_FWD) == (16 * 384 + 384) * 256 * 128 * 8
     # periodic axes keep F_d = S_d
     S, K = _lib.i64_array([64, 64, 64]), _lib.i64_array([64, 64, 64])
     monkeypatch.delenv("NSQ_ND_R3")

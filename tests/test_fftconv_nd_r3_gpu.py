@@ -1,12 +1,13 @@
-"""GPU parity of the 3D FFT conv on the reference's own FFT sizes (3 * 2^m axes).
+"""GPU parity of the 2D / 3D FFT conv on the reference's own FFT sizes (3 * 2^m axes).
 
 The reference pads each axis to F_d = S_d + ceil(K_d / 2) and lets torch.fft run
-a mixed-radix plan (nvsubquadratic/ops/fftconv.py:774-778); the HIP plan in
-csrc/fftconv_nd_r3.h runs the lengths 48, 96 and (axis 0) 192 wherever their
-spectrum is smaller than the power-of-two one.  The shapes below reach every
-plane instance ((F2/2, F1) in {24, 48} x {48, 96}), every axis-0 length, first
-passes with and without the two-thirds zero fold (S <= 2F/3), odd and unaligned
-row lengths, per-sample filters, and the batch-split adjoint (few channels).
+a mixed-radix plan (nvsubquadratic/ops/fftconv.py:699-702, 774-778); the HIP plan
+in csrc/fftconv_nd_r3.h runs the lengths 48, 96 and 192 wherever their spectrum
+is smaller than the power-of-two one.  The shapes below reach every plane
+instance ((F2/2, F1) in {24, 48} x {48, 96}), every 2D row length (F2/2 in {24,
+48, 96}), every axis-0 length, first passes with and without the two-thirds
+zero fold (S <= 2F/3), odd and unaligned row lengths, per-sample filters, and
+the batch-split adjoint (few channels).
 Oracle: fftconv_nd_torch (the reference's torch.fft formula on the CPU) and the
 float64 numpy restatement.  Tolerances: rel-L2 <= 1e-4 fp32, <= 2e-2 16-bit I/O.
 """
@@ -140,3 +141,106 @@ def test_r3_chunked_bitwise():
     x = torch.randn(1, 40, 32, 32, 32, device="cuda")
     k = torch.randn(40, 32, 32, 32, device="cuda")
     assert torch.equal(F.fftconv3d_bhl(x, k), F.fftconv3d_bhl_chunked(x, k, chunk_size=16))
+
+
+# 2D: (x shape, kernel shape, FFT lengths (F0, F2)); row kernels at F2/2 in {24, 48, 96}, axis 0 of 48 / 96 / 192.
+R3_SHAPES_2D = [
+    ((2, 3, 128, 128), (128, 128), (192, 192)),  # config 4's geometry
+    ((2, 4, 64, 64), (64, 64), (96, 96)),
+    ((3, 2, 32, 32), (32, 32), (48, 48)),
+    ((2, 3, 90, 27), (7, 41), (96, 48)),        # odd, unaligned rows, no fold on axis 0
+    ((1, 2, 120, 70), (100, 41), (192, 96)),    # no fold on the rows
+]
+
+
+def _grad_check_2d(xs, ks, kb=1, dtype=torch.float32, tol=1e-4, seed=0):
+    torch.manual_seed(seed)
+    H = xs[1]
+    x = torch.randn(*xs).to(dtype).requires_grad_(True)
+    k = torch.randn(kb, H, *ks, requires_grad=True)
+    s = torch.randn(H).to(dtype).requires_grad_(True)
+    y_ref = fftconv_nd_torch(x, k, s)
+    g = torch.randn_like(y_ref)
+    y_ref.backward(g)
+    xg, kg, sg = (t.detach().cuda().requires_grad_(True) for t in (x, k, s))
+    y = F.fftconv2d_bhl(xg, kg, sg)
+    y.backward(g.cuda())
+    assert y.dtype == dtype
+    assert rel_l2(y_ref, y) < tol
+    assert rel_l2(x.grad, xg.grad) < tol
+    assert rel_l2(k.grad, kg.grad) < tol
+    assert rel_l2(s.grad, sg.grad) < tol
+    return y
+
+
+@pytest.mark.parametrize("xs,ks,fl", R3_SHAPES_2D)
+def test_r3_2d_plan_is_taken(xs, ks, fl):
+    lib = _lib.get_lib()
+    S, K = _lib.i64_array(xs[2:]), _lib.i64_array(ks)
+    got = lib.nsq_fftconv_nd_workspace_bytes(2, xs[0], xs[1], S, K, 1, _lib.NSQ_DIR_FWD)
+    assert got == (xs[0] * xs[1] + xs[1]) * fl[0] * (fl[1] // 2 + 1) * 8
+
+
+@pytest.mark.parametrize("xs,ks,fl", R3_SHAPES_2D)
+def test_r3_2d_fwd_bwd(xs, ks, fl):
+    _grad_check_2d(xs, ks)
+
+
+@pytest.mark.parametrize("xs,ks,fl", [R3_SHAPES_2D[0], R3_SHAPES_2D[3]])
+def test_r3_2d_film_per_sample_kernel(xs, ks, fl):
+    _grad_check_2d(xs, ks, kb=xs[0], seed=1)
+
+
+def test_r3_2d_bf16_config4_geometry():
+    """Config 4's geometry (128^2, K = 128, FFT 192^2) in bf16 I/O against the float64 restatement."""
+    y = _grad_check_2d((2, 4, 128, 128), (128, 128), dtype=torch.bfloat16, tol=2e-2, seed=2)
+    torch.manual_seed(2)
+    x = torch.randn(2, 4, 128, 128).to(torch.bfloat16)
+    k = torch.randn(1, 4, 128, 128)
+    s = torch.randn(4).to(torch.bfloat16)
+    assert rel_l2(fftconv_nd_np(x.float().numpy(), k.numpy(), s.float().numpy()), y) < 5e-3
+
+
+@pytest.mark.parametrize("xs,ks,fl", [R3_SHAPES_2D[0], R3_SHAPES_2D[4]])
+def test_r3_2d_matches_power_of_two_plan(xs, ks, fl, monkeypatch):
+    torch.manual_seed(3)
+    x = torch.randn(*xs, device="cuda", requires_grad=True)
+    k = torch.randn(xs[1], *ks, device="cuda", requires_grad=True)
+    s = torch.randn(xs[1], device="cuda", requires_grad=True)
+    g = torch.randn(*xs, device="cuda")
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("NSQ_ND_R3", flag)
+        for t in (x, k, s):
+            t.grad = None
+        y = F.fftconv2d_bhl(x, k, s)
+        y.backward(g)
+        outs.append([y.detach().clone(), x.grad.clone(), k.grad.clone(), s.grad.clone()])
+    monkeypatch.delenv("NSQ_ND_R3")
+    for a, b in zip(*outs):
+        assert rel_l2(b, a) < 1e-5
+
+
+def test_r3_2d_backward_reusing_forward_state_is_bitwise_equal():
+    torch.manual_seed(4)
+    xs, ks, kb = (2, 3, 128, 128), (128, 128), 2
+    x = torch.randn(*xs, device="cuda")
+    k = torch.randn(kb * xs[1], *ks, device="cuda")
+    s = torch.randn(xs[1], device="cuda")
+    g = torch.randn(*xs, device="cuda")
+    lib = _lib.get_lib()
+    S, K = _lib.i64_array(xs[2:]), _lib.i64_array(ks)
+    need = lib.nsq_fftconv_nd_workspace_bytes(2, xs[0], xs[1], S, K, kb, _lib.NSQ_DIR_BWD)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    F.fftconv_nd_fwd_raw(x, k, s, y, kb, ws)
+    outs = []
+    for state, w in ((True, ws), (False, None)):
+        gx, gk, gs = torch.empty_like(x), torch.empty_like(k), torch.empty(kb * xs[1], device="cuda")
+        F.fftconv_nd_bwd_raw(g, x, k, s, gx, gk, gs, kb, w, fwd_state=state)
+        outs.append((gx, gk, gs))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    y2 = torch.empty_like(x)
+    F.fftconv_nd_fwd_raw(x, k, s, y2, kb)
+    assert torch.equal(y, y2)

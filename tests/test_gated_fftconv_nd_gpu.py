@@ -140,8 +140,12 @@ FUSED_CASES = [  # (S, K, periodic, gate, gate_2, dtype, kb, shortcut)
 
 
 def _gated_run(S, K, periodic, gate, gate_2, dtype, kb, shortcut, fused):
+    # The fused gates live in the power-of-two plan's passes (NSQ_ND_R3=0 keeps shapes that the mixed-radix
+    # plan would take, which runs the gate kernels around its conv, on that plan).
     old = os.environ.get("NSQ_ND_GATES_FUSED")
+    old_r3 = os.environ.get("NSQ_ND_R3")
     os.environ["NSQ_ND_GATES_FUSED"] = "1" if fused else "0"
+    os.environ["NSQ_ND_R3"] = "0"
     try:
         torch.manual_seed(7)
         B, H = 2, 4
@@ -166,6 +170,10 @@ def _gated_run(S, K, periodic, gate, gate_2, dtype, kb, shortcut, fused):
             del os.environ["NSQ_ND_GATES_FUSED"]
         else:
             os.environ["NSQ_ND_GATES_FUSED"] = old
+        if old_r3 is None:
+            del os.environ["NSQ_ND_R3"]
+        else:
+            os.environ["NSQ_ND_R3"] = old_r3
 
 
 @pytest.mark.parametrize("case", FUSED_CASES)
