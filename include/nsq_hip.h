@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 14
+#define NSQ_ABI_VERSION 15
 
 enum {
   NSQ_OK = 0,
@@ -529,6 +529,36 @@ size_t nsq_channel_rmsnorm_bwd_workspace_bytes(int64_t B, int64_t C, int64_t S);
 int nsq_channel_rmsnorm_bwd(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv,
                             float* dw, int dtype, int64_t B, int64_t C, int64_t S, float eps, int act,
                             int out_channels_last, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Hyena gate + LayerNorm over channels + layout, one pass (ABI 15).
+ *
+ * The pixelhyena_norm site with a torch.nn.LayerNorm(C) module (the reference's
+ * configs' other norm there, e.g. examples/imagenet_classification/
+ * ccnn_7_512_hyena.py: LazyConfig(torch.nn.LayerNorm)(normalized_shape=...)),
+ * which hyena_nd.py:548-556 applies to z = q * act(k) moved to channels-last
+ * and flattened: per position over the C channels,
+ *   mu = mean_c u, var = mean_c (u - mu)^2 (biased),
+ *   out = round(w[c] ((u - mu) rsqrt(var + eps)) + b[c])   (fp32 arithmetic)
+ * with u = round(y * round(act(v))) (v == NULL: u = y).  Same layouts and
+ * arguments as nsq_channel_rmsnorm_*; w and b (fp32 [C]) may be NULL (no
+ * elementwise affine: scale 1, shift 0).  C <= 7781 forward, C <= 3241
+ * backward (NSQ_ERR_UNSUPPORTED beyond).
+ *
+ * Backward: writes dy (and dv with v), and dw / db (fp32 [C], overwritten,
+ * summed in a fixed order) when given; dw needs w.  Workspace:
+ * nsq_channel_layernorm_bwd_workspace_bytes (partial rows of dw and db; none
+ * needed when dw and db are both NULL).
+ */
+int nsq_channel_layernorm_fwd(const void* y, const void* v, const float* w, const float* b, void* out, int dtype,
+                              int64_t B, int64_t C, int64_t S, float eps, int act, int out_channels_last,
+                              void* stream);
+
+size_t nsq_channel_layernorm_bwd_workspace_bytes(int64_t B, int64_t C, int64_t S);
+
+int nsq_channel_layernorm_bwd(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv,
+                              float* dw, float* db, int dtype, int64_t B, int64_t C, int64_t S, float eps, int act,
+                              int out_channels_last, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

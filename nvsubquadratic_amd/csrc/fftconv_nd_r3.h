@@ -329,7 +329,7 @@ __global__ __launch_bounds__(192) void r3_row_inv_kernel(const float2* __restric
     const bool p0 = (p == 0);
     const float2 u0 = in[p0 ? 0 : p];
     const float2 u1 = in[p0 ? N : N - p];
-    const float2 u2 = in[N / 2];
+    const float2 u2 = p0 ? in[N / 2] : make_float2(0.f, 0.f);  // slot 0 only
     float2 A = p0 ? make_float2(u0.x, u1.x) : u0;
     float2 Bc = p0 ? u2 : cconj(u1);
     A = make_float2(rok ? A.x : 0.f, rok ? A.y : 0.f);

@@ -28,8 +28,8 @@ from . import _lib
 from .gated_fftconv_hip import gate_code
 from .layout import channels_first_contiguous
 
-__all__ = ["HipL2Norm", "HipRMSNormChannelFirst", "channel_l2norm", "channel_rmsnorm", "gated_channel_rmsnorm",
-           "hyena_output_norm"]
+__all__ = ["HipL2Norm", "HipLayerNormChannels", "HipRMSNormChannelFirst", "channel_l2norm", "channel_rmsnorm",
+           "gated_channel_layernorm", "gated_channel_rmsnorm", "hyena_output_norm"]
 
 
 def _flat(t: torch.Tensor) -> torch.Tensor:
@@ -173,6 +173,152 @@ class HipRMSNormChannelFirst(torch.nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return channel_rmsnorm(x, self.weight, self.eps)
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm over channels at the pixelhyena_norm site (a torch.nn.LayerNorm(C) in the reference's configs, applied by
+# modules/hyena_nd.py:548-556 to z moved channels-last), one HIP pass each way (nsq_channel_layernorm_fwd / _bwd)
+# ---------------------------------------------------------------------------
+@custom_op("nsq_hip::gated_channel_layernorm", mutates_args=())
+def gated_channel_layernorm_op(y: torch.Tensor, v: Optional[torch.Tensor], weight: Optional[torch.Tensor],
+                               bias: Optional[torch.Tensor], eps: float, act: int,
+                               channels_last: bool) -> torch.Tensor:
+    """y, v ``[B, C, S]`` contiguous, weight / bias fp32 ``[C]`` or None -> ``[B, S, C]`` or ``[B, C, S]``."""
+    lib = _lib.get_lib()
+    _lib.check_device(y)
+    B, C, S = y.shape
+    out = torch.empty((B, S, C) if channels_last else (B, C, S), dtype=y.dtype, device=y.device)
+    _lib.check(lib.nsq_channel_layernorm_fwd(
+        y.data_ptr(), v.data_ptr() if v is not None else None, weight.data_ptr() if weight is not None else None,
+        bias.data_ptr() if bias is not None else None, out.data_ptr(), _lib.dtype_code(y.dtype), B, C, S, float(eps),
+        act, int(channels_last), _lib.stream_ptr(y.device)))
+    return out
+
+
+@gated_channel_layernorm_op.register_fake
+def _(y, v, weight, bias, eps, act, channels_last):
+    B, C, S = y.shape
+    return y.new_empty((B, S, C) if channels_last else (B, C, S))
+
+
+@custom_op("nsq_hip::gated_channel_layernorm_backward", mutates_args=())
+def gated_channel_layernorm_backward_op(dout: torch.Tensor, y: torch.Tensor, v: Optional[torch.Tensor],
+                                        weight: Optional[torch.Tensor], want_db: bool, eps: float, act: int,
+                                        channels_last: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                      torch.Tensor]:
+    """Returns ``(dy, dv, dw, db)``; ``dv`` / ``dw`` / ``db`` are empty when ``v`` / ``weight`` / ``want_db`` are
+    absent; ``dw`` and ``db`` fp32 ``[C]``."""
+    lib = _lib.get_lib()
+    _lib.check_device(y)
+    B, C, S = y.shape
+    dy = torch.empty_like(y)
+    dv = torch.empty_like(v) if v is not None else y.new_empty(0)
+    dw = torch.empty(C, dtype=torch.float32, device=y.device) if weight is not None else y.new_empty(0)
+    db = torch.empty(C, dtype=torch.float32, device=y.device) if want_db else y.new_empty(0)
+    nws = int(lib.nsq_channel_layernorm_bwd_workspace_bytes(B, C, S)) if (weight is not None or want_db) else 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=y.device)
+    _lib.check(lib.nsq_channel_layernorm_bwd(
+        dout.data_ptr(), y.data_ptr(), v.data_ptr() if v is not None else None,
+        weight.data_ptr() if weight is not None else None, dy.data_ptr(), dv.data_ptr() if v is not None else None,
+        dw.data_ptr() if weight is not None else None, db.data_ptr() if want_db else None, _lib.dtype_code(y.dtype),
+        B, C, S, float(eps), act, int(channels_last), ws.data_ptr() if nws else None, nws,
+        _lib.stream_ptr(y.device)))
+    return dy, dv, dw, db
+
+
+@gated_channel_layernorm_backward_op.register_fake
+def _(dout, y, v, weight, want_db, eps, act, channels_last):
+    C = y.shape[1]
+    return (torch.empty_like(y), (torch.empty_like(v) if v is not None else y.new_empty(0)),
+            (y.new_empty(C, dtype=torch.float32) if weight is not None else y.new_empty(0)),
+            (y.new_empty(C, dtype=torch.float32) if want_db else y.new_empty(0)))
+
+
+def _ln_setup(ctx, inputs, output):
+    y, v, weight, bias, eps, act, channels_last = inputs
+    ctx.save_for_backward(y, v, weight)
+    ctx.cfg = (bias is not None, eps, act, channels_last)
+
+
+def _ln_backward(ctx, gout):
+    y, v, weight = ctx.saved_tensors
+    has_b, eps, act, channels_last = ctx.cfg
+    dy, dv, dw, db = gated_channel_layernorm_backward_op(gout.contiguous(), y, v, weight, has_b, eps, act,
+                                                         channels_last)
+    return (dy, (dv if v is not None else None), (dw if weight is not None else None), (db if has_b else None),
+            None, None, None)
+
+
+gated_channel_layernorm_op.register_autograd(_ln_backward, setup_context=_ln_setup)
+
+
+def gated_channel_layernorm(y: torch.Tensor, v: Optional[torch.Tensor], weight: Optional[torch.Tensor],
+                            bias: Optional[torch.Tensor], eps: float = 1e-5, gate_nonlinear="sigmoid",
+                            channels_last_out: bool = False) -> torch.Tensor:
+    """``torch.nn.LayerNorm(C)`` over the channels of ``y * act(v)`` (of ``y`` when ``v`` is None), in one pass.
+
+    Args:
+        y, v: ``[B, C, *spatial]`` in fp32 / bf16 / fp16 (same dtype and shape).
+        weight, bias: ``[C]`` or None (``elementwise_affine=False`` / ``bias=False``).
+        eps: added to the variance, as ``LayerNorm(eps=...)``.
+        gate_nonlinear: ``"identity" | "sigmoid" | "silu"`` or the matching ``nn`` module.
+        channels_last_out: ``True`` returns ``[B, *spatial, C]``, ``False`` ``[B, C, *spatial]``.
+    """
+    if y.dim() < 2:
+        raise ValueError(f"expected [B, C, *spatial], got shape {tuple(y.shape)}")
+    if v is not None and (v.shape != y.shape or v.dtype != y.dtype):
+        raise ValueError(f"v {tuple(v.shape)} {v.dtype} must match y {tuple(y.shape)} {y.dtype}")
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None and t.shape != (y.shape[1],):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != ({y.shape[1]},)")
+    shape = y.shape
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (y, v, weight, bias)):
+        C, S = shape[1], max(1, y.numel() // max(1, shape[0] * shape[1]))
+        if _lib.get_lib().nsq_channel_layernorm_bwd_workspace_bytes(shape[0], C, S) == 0:
+            raise NotImplementedError(f"fft_backend='hip' channel LayerNorm backward: C={C} exceeds the backward's "
+                                      f"LDS tiles (C <= 3241); the forward alone takes C <= 7781")
+    w = _WeightToF32.apply(weight) if weight is not None and weight.dtype != torch.float32 else weight
+    b = _WeightToF32.apply(bias) if bias is not None and bias.dtype != torch.float32 else bias
+    out = gated_channel_layernorm_op(_flat(y), _flat(v) if v is not None else None,
+                                     w.contiguous() if w is not None else None, b.contiguous() if b is not None else None,
+                                     float(eps), gate_code(gate_nonlinear) if v is not None else 0,
+                                     bool(channels_last_out))
+    if channels_last_out:
+        return out.view(shape[0], *shape[2:], shape[1])
+    return out.view(shape)
+
+
+class HipLayerNormChannels(torch.nn.Module):
+    """Drop-in for ``torch.nn.LayerNorm(C)`` at the Hyena operator's norm sites: the same parameters (``weight``
+    ones, ``bias`` zeros, ``eps`` 1e-5, ``elementwise_affine``, ``bias``) and arithmetic, normalising
+    ``[B, C, *spatial]`` over dim 1 on the HIP kernel.  ``channels_first = True`` lets the operator hand it the
+    channels-first tensor (``hyena_nd.py:548-552``) instead of its ``movedim`` / ``reshape`` round trip."""
+
+    channels_first: bool = True
+
+    def __init__(self, normalized_shape, eps: float = 1e-5, elementwise_affine: bool = True, bias: bool = True,
+                 device=None, dtype=None):
+        super().__init__()
+        shape = (normalized_shape,) if isinstance(normalized_shape, int) else tuple(normalized_shape)
+        if len(shape) != 1:
+            raise NotImplementedError(f"fft_backend='hip' LayerNorm normalises the channel axis only; got "
+                                      f"normalized_shape={shape}")
+        self.normalized_shape = shape
+        self.eps = eps
+        self.elementwise_affine = elementwise_affine
+        kw = {"device": device, "dtype": dtype}
+        if elementwise_affine:
+            self.weight = torch.nn.Parameter(torch.ones(shape, **kw))
+            self.bias = torch.nn.Parameter(torch.zeros(shape, **kw)) if bias else None
+        else:
+            self.register_parameter("weight", None)
+            self.register_parameter("bias", None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return gated_channel_layernorm(x, None, self.weight, self.bias, self.eps, "identity", channels_last_out=False)
+
+    def extra_repr(self) -> str:
+        return f"{self.normalized_shape}, eps={self.eps}, elementwise_affine={self.elementwise_affine}"
 
 
 # ---------------------------------------------------------------------------

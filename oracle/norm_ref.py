@@ -18,6 +18,13 @@ norm over ``dim`` accumulated in float32 and rounded to the input dtype (torch's
 clamped at ``eps``, and ``x / n`` in the input dtype; pinned against torch's own ``F.normalize`` (a library routine),
 a closed form (3, 4) -> (0.6, 0.8), the clamp (a vector shorter than eps comes out as ``x / eps``) and float64
 gradcheck.
+
+The LayerNorm site (a ``torch.nn.LayerNorm(C)`` as ``pixelhyena_norm``, applied by ``hyena_nd.py:548-556`` to
+``z.movedim(1, -1)``) is restated as torch's layer norm computes it: float32 arithmetic (the input upcast, the
+parameters float32), the mean and the biased variance over the channels, ``(x - mean) * rsqrt(var + eps) * w + b``,
+rounded once to the input dtype.  Pinned against ``torch.nn.functional.layer_norm`` in float64 (a library routine), a
+closed form ((1, 2, 3) -> (-sqrt(3/2), 0, sqrt(3/2)) at eps = 0), shift and scale invariance of the normalised values,
+and float64 gradcheck.
 """
 
 from __future__ import annotations
@@ -26,7 +33,7 @@ from typing import Optional
 
 import torch
 
-__all__ = ["gated_channel_rmsnorm_ref", "l2norm_ref"]
+__all__ = ["gated_channel_layernorm_ref", "gated_channel_rmsnorm_ref", "l2norm_ref"]
 
 _ACTS = {0: lambda t: t, 1: torch.sigmoid, 2: torch.nn.functional.silu}
 
@@ -50,3 +57,22 @@ def l2norm_ref(x: torch.Tensor, dim: int = 1, eps: float = 1e-12) -> torch.Tenso
     n = torch.linalg.vector_norm(xf, dim=dim, keepdim=True).to(x.dtype)  # torch's norm returns the input dtype
     n = n.clamp_min(eps)
     return (xf / n.to(xf.dtype)).to(x.dtype)
+
+
+def gated_channel_layernorm_ref(y: torch.Tensor, v: Optional[torch.Tensor], weight: Optional[torch.Tensor],
+                                bias: Optional[torch.Tensor], eps: float = 1e-5, act: int = 1,
+                                channels_last: bool = False) -> torch.Tensor:
+    """``y``, ``v`` ``[B, C, *S]`` (CPU), ``weight`` / ``bias`` ``[C]`` or None -> ``[B, *S, C]`` or ``[B, C, *S]``."""
+    u = y * _ACTS[act](v) if v is not None else y           # hyena_nd.py:546 (I/O dtype)
+    x = u.movedim(1, -1)                                     # hyena_nd.py:553-554 (rows of C channels)
+    dt = x.dtype
+    xf = x.to(torch.float32) if dt != torch.float64 else x
+    mean = xf.mean(-1, keepdim=True)
+    var = (xf - mean).pow(2).mean(-1, keepdim=True)          # biased, as LayerNorm
+    out = (xf - mean) * torch.rsqrt(var + eps)
+    if weight is not None:
+        out = out * weight.to(xf.dtype)
+    if bias is not None:
+        out = out + bias.to(xf.dtype)
+    out = out.to(dt)
+    return out if channels_last else out.movedim(-1, 1)

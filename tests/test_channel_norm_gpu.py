@@ -1,4 +1,4 @@
-"""GPU parity of the gate + channel-RMSNorm + layout pass (nsq_channel_rmsnorm_fwd / _bwd through the C ABI) against
+"""GPU parity of the gate + channel-RMSNorm (and LayerNorm, L2) + layout pass (nsq_channel_*_fwd / _bwd through the C ABI) against
 the CPU restatement of the reference's op sequence (oracle/norm_ref.py) and, at the config-4 Hyena shape, against
 the same sequence in fp32 torch ops on the GPU."""
 
@@ -219,3 +219,94 @@ def test_l2norm_opcheck():
     x = torch.randn(2, 40, 33, device="cuda", requires_grad=True)
     torch.library.opcheck(N.channel_l2norm_op, (x, 1e-12, True))
     torch.library.opcheck(N.channel_l2norm_op, (x, 1e-12, False))
+
+
+# --- LayerNorm over channels (torch.nn.LayerNorm(C) at the pixelhyena_norm site) ---------------------------------
+def _ln_case(B, C, spatial, dtype, gate, channels_last, affine=True, use_bias=True, eps=1e-5, seed=0, gtol=None):
+    from oracle.norm_ref import gated_channel_layernorm_ref
+
+    print(f"ln case B={B} C={C} S={spatial} {dtype} gate={gate} channels_last={channels_last} affine={affine} "
+          f"bias={use_bias}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    y = (0.7 * torch.randn(B, C, *spatial, generator=g) + 0.3).to(dtype)  # a nonzero mean per position
+    v = torch.randn(B, C, *spatial, generator=g).to(dtype) if gate is not None else None
+    w = (1 + 0.5 * torch.randn(C, generator=g)).float() if affine else None
+    b = (0.2 * torch.randn(C, generator=g)).float() if affine and use_bias else None
+    dev = "cuda"
+    leaves = [t.to(dev).requires_grad_() if t is not None else None for t in (y, v, w, b)]
+    out = N.gated_channel_layernorm(*leaves, eps, gate or "identity", channels_last_out=channels_last)
+    gout = torch.randn(out.shape, generator=g).to(dtype)
+    out.backward(gout.to(dev))
+    torch.cuda.synchronize()
+    refs = [t.clone().requires_grad_() if t is not None else None for t in (y, v, w, b)]
+    ref = gated_channel_layernorm_ref(*refs, eps, ACT[gate] if gate else 0, channels_last)
+    ref.backward(gout)
+    tol = TOL[dtype]
+    gtol = gtol or tol
+    assert out.shape == ref.shape and out.dtype == dtype
+    assert rel_l2(ref, out) < tol
+    for r, d in zip(refs, leaves):
+        if r is not None:
+            assert rel_l2(r.grad, d.grad) < (tol if r.dtype == torch.float32 and r.dim() == 1 else gtol)
+
+
+@pytest.mark.parametrize("gate", [None, "silu"])
+@pytest.mark.parametrize("channels_last", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_layernorm_hyena_shape(gate, channels_last, dtype):
+    _ln_case(2, 384, (32, 32), dtype, gate, channels_last)
+
+
+@pytest.mark.parametrize("B,C,spatial,affine,use_bias", [(3, 40, (7, 5), True, True), (1, 257, (33,), True, False),
+                                                          (2, 64, (3, 3, 3), False, False), (2, 3, (100,), True, True)])
+def test_layernorm_ragged_shapes_and_affine(B, C, spatial, affine, use_bias):
+    _ln_case(B, C, spatial, torch.float32, "sigmoid", False, affine=affine, use_bias=use_bias, seed=1)
+
+
+def test_layernorm_module_drop_in():
+    """HipLayerNormChannels on [B, C, *S] equals torch.nn.LayerNorm(C) on the channels-last view."""
+    torch.manual_seed(7)
+    ref = torch.nn.LayerNorm(48).cuda()
+    with torch.no_grad():
+        ref.weight.copy_(1 + 0.3 * torch.randn(48))
+        ref.bias.copy_(0.1 * torch.randn(48))
+    mod = N.HipLayerNormChannels(48).cuda()
+    mod.load_state_dict(ref.state_dict())
+    assert mod.channels_first
+    x = torch.randn(2, 48, 9, 11, device="cuda", requires_grad=True)
+    xr = x.detach().clone().requires_grad_()
+    y = mod(x)
+    yr = ref(xr.movedim(1, -1)).movedim(-1, 1)
+    g = torch.randn_like(y)
+    y.backward(g)
+    yr.backward(g)
+    assert rel_l2(yr, y) < 1e-5
+    assert rel_l2(xr.grad, x.grad) < 1e-5
+    assert rel_l2(ref.weight.grad, mod.weight.grad) < 1e-5
+    assert rel_l2(ref.bias.grad, mod.bias.grad) < 1e-5
+
+
+def test_layernorm_gradients_deterministic_and_limits():
+    torch.manual_seed(8)
+    y = torch.randn(4, 64, 4096, device="cuda", dtype=torch.bfloat16)
+    w = torch.rand(64, device="cuda")
+    g = torch.randn(4, 64, 4096, device="cuda", dtype=torch.bfloat16)
+    r1 = N.gated_channel_layernorm_backward_op(g, y, None, w, True, 1e-5, 0, False)
+    r2 = N.gated_channel_layernorm_backward_op(g, y, None, w, True, 1e-5, 0, False)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+    lib = _lib.get_lib()
+    assert lib.nsq_channel_layernorm_bwd_workspace_bytes(1, 3241, 8) > 0
+    assert lib.nsq_channel_layernorm_bwd_workspace_bytes(1, 3242, 8) == 0
+    yb = torch.randn(1, 3300, 2, device="cuda", requires_grad=True)
+    with pytest.raises(NotImplementedError, match="C <= 3241"):
+        N.gated_channel_layernorm(yb, None, torch.ones(3300, device="cuda"), None)
+
+
+def test_layernorm_opcheck():
+    y = torch.randn(2, 16, 24, device="cuda", requires_grad=True)
+    v = torch.randn(2, 16, 24, device="cuda", requires_grad=True)
+    w = torch.rand(16, device="cuda", requires_grad=True)
+    b = torch.rand(16, device="cuda", requires_grad=True)
+    torch.library.opcheck(N.gated_channel_layernorm_op, (y, v, w, b, 1e-5, 2, True))
+    torch.library.opcheck(N.gated_channel_layernorm_op, (y, None, None, None, 1e-5, 0, False))

@@ -7,7 +7,7 @@ import math
 import pytest
 import torch
 
-from oracle.norm_ref import gated_channel_rmsnorm_ref, l2norm_ref
+from oracle.norm_ref import gated_channel_layernorm_ref, gated_channel_rmsnorm_ref, l2norm_ref
 
 
 def test_closed_form_ramp():
@@ -87,3 +87,44 @@ def test_l2norm_gradcheck_float64():
     assert torch.autograd.gradcheck(lambda t: l2norm_ref(t, 1, 1e-12), (y,))
     small = (torch.randn(1, 3, 2, dtype=torch.float64) * 1e-4).requires_grad_(True)  # clamped branch
     assert torch.autograd.gradcheck(lambda t: l2norm_ref(t, 1, 1e-2), (small,))
+
+
+# LayerNorm over channels (the pixelhyena_norm site with torch.nn.LayerNorm(C))
+
+@pytest.mark.parametrize("affine", [True, False])
+def test_layernorm_restatement_matches_torch_layer_norm_float64(affine):
+    torch.manual_seed(3)
+    y = torch.randn(2, 12, 5, 3, dtype=torch.float64)
+    v = torch.randn(2, 12, 5, 3, dtype=torch.float64)
+    w = torch.randn(12, dtype=torch.float64) if affine else None
+    b = torch.randn(12, dtype=torch.float64) if affine else None
+    for act, f in ((0, lambda t: t), (1, torch.sigmoid), (2, torch.nn.functional.silu)):
+        got = gated_channel_layernorm_ref(y, v, w, b, 1e-5, act, channels_last=True)
+        want = torch.nn.functional.layer_norm((y * f(v)).movedim(1, -1), (12,), w, b, 1e-5)
+        assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+    cf = gated_channel_layernorm_ref(y, None, w, b, 1e-5, 0, channels_last=False)
+    assert torch.allclose(cf, torch.nn.functional.layer_norm(y.movedim(1, -1), (12,), w, b, 1e-5).movedim(-1, 1),
+                          rtol=1e-12, atol=1e-12)
+
+
+def test_layernorm_closed_form_and_invariances():
+    y = torch.tensor([1.0, 2.0, 3.0], dtype=torch.float64).view(1, 3, 1)
+    out = gated_channel_layernorm_ref(y, None, None, None, 0.0, 0)
+    r = math.sqrt(1.5)
+    assert torch.allclose(out.view(3), torch.tensor([-r, 0.0, r], dtype=torch.float64), rtol=1e-14, atol=1e-14)
+    torch.manual_seed(4)
+    z = torch.randn(2, 9, 7, dtype=torch.float64)
+    o1 = gated_channel_layernorm_ref(z, None, None, None, 0.0, 0)
+    o2 = gated_channel_layernorm_ref(3.5 * z + 11.0, None, None, None, 0.0, 0)  # shift and scale invariant
+    assert torch.allclose(o1, o2, rtol=1e-11, atol=1e-11)
+    assert torch.allclose(o1.mean(1), torch.zeros(2, 7, dtype=torch.float64), atol=1e-13)
+    assert torch.allclose(o1.pow(2).mean(1), torch.ones(2, 7, dtype=torch.float64), rtol=1e-12)
+
+
+def test_layernorm_gradcheck_float64():
+    torch.manual_seed(5)
+    y = torch.randn(2, 6, 4, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(2, 6, 4, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(6, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(6, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda *t: gated_channel_layernorm_ref(*t, 1e-3, 2, True), (y, v, w, b))
