@@ -29,6 +29,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                                                     3's shape with the filter never formed, and the composition)
        python bench.py --workload hyena-norm       (report-only: the Hyena output gate + RMSNorm over
                                                     channels + channels-last layout, fwd+bwd, cfg4 shape)
+       python bench.py --workload hyena-groupnorm  (report-only: the Hyena conv-input gate + GroupNorm(1, C)
+                                                    channels-first, fwd+bwd, cfg4 shape)
        python bench.py --workload hyena-gated-2d   (report-only: the gated 2D
            conv at cfg4's shape, with torch gates around the same conv and the
            conv alone)
@@ -596,6 +598,38 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare
 
         if compare:
             extra["torch_ops_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
+    elif name == "hyena-groupnorm":
+        # report-only (norms): the conv's input z = q * silu(k) -> GroupNorm(1, C) channels-first (hyena_nd.py:
+        # 546-550, the reference configs' pixelhyena_norm), three HIP passes per direction, against torch's ops
+        from nvsubquadratic_amd.norm_hip import gated_channel_groupnorm
+
+        B, Ch, X = 16, 384, 128
+        y, v = (torch.randn(B, Ch, X, X, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+                for _ in range(2))
+        w = (torch.rand(Ch, device=dev, generator=gen) + 0.5).requires_grad_(True)
+        bia = (0.1 * torch.randn(Ch, device=dev, generator=gen)).requires_grad_(True)
+        g = torch.randn(B, Ch, X, X, device=dev, generator=gen).to(torch.bfloat16)
+        phase, dtype = "fwd+bwd", "f32"
+        n = B * Ch * X * X
+        nbytes = 8 * n * 2  # fwd: y, v in, out; bwd: g, y, v in, dy, dv out (bf16)
+        desc = ("hyena-groupnorm: Hyena conv input fwd+bwd, q * silu(k) -> GroupNorm(1, C) (eps 1e-5) channels-first, "
+                "B=16 C=384 128^2 bf16, weight and bias fp32")
+
+        def clear():
+            for t in (y, v, w, bia):
+                t.grad = None
+
+        def step():
+            clear()
+            gated_channel_groupnorm(y, v, w, bia, 1, 1e-5, "silu").backward(g)
+
+        def step_torch():
+            clear()
+            z = y * torch.nn.functional.silu(v)
+            torch.nn.functional.group_norm(z, 1, w.to(z.dtype), bia.to(z.dtype), 1e-5).backward(g)
+
+        if compare:
+            extra["torch_ops_ms_per_step"] = round(statistics.mean(_time_steps(step_torch, steps, warmup)), 4)
     else:
         raise SystemExit(f"unknown workload {name}")
     ms_list = _time_steps(step, steps, warmup)
@@ -637,7 +671,7 @@ def main() -> None:
     ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg2-fwd-bwd", "cfg3", "cfg4", "cfg5",
                                                               "cfg4-circular", "well-rb", "hyena-gated",
                                                               "hyena-gated-2d", "siren-1d", "siren-conv-1d",
-                                                              "hyena-norm"])
+                                                              "hyena-norm", "hyena-groupnorm"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

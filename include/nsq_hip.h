@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NSQ_ABI_VERSION 15
+#define NSQ_ABI_VERSION 16
 
 enum {
   NSQ_OK = 0,
@@ -559,6 +559,38 @@ size_t nsq_channel_layernorm_bwd_workspace_bytes(int64_t B, int64_t C, int64_t S
 int nsq_channel_layernorm_bwd(const void* dout, const void* y, const void* v, const float* w, void* dy, void* dv,
                               float* dw, float* db, int dtype, int64_t B, int64_t C, int64_t S, float eps, int act,
                               int out_channels_last, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Hyena gate + GroupNorm over channels, channels-first (ABI 16).
+ *
+ * The pixelhyena_norm site with a torch.nn.GroupNorm(num_groups, C) module
+ * (the reference's configs use num_groups = 1, e.g.
+ * examples/imagenet_classification/ccnn_7_512_hyena.py), which hyena_nd.py:
+ * 548-550 applies channels-first (modules/_channels_first_utils.py:27) to
+ * z = q * act(k): per sample b and group g of C / G consecutive channels, over
+ * those channels and all S positions,
+ *   mu, var = mean and biased variance of u,  r = rsqrt(var + eps),
+ *   out[b,c,s] = round(u a + h),  a = r w[c],  h = b[c] - mu a
+ * (fp32 arithmetic; torch's scale / shift form) with u = round(y *
+ * round(act(v))) (v == NULL: u = y).  y, v, out: [B, C, S] of dtype; w, b:
+ * fp32 [C] or NULL (scale 1, shift 0).  mean and rstd (fp32 [B, G]) receive
+ * mu and r, which the backward takes.  C must be a multiple of G.  Workspace:
+ * nsq_channel_groupnorm_workspace_bytes(B, C, G, NSQ_DIR_FWD).
+ *
+ * Backward: writes dy (and dv with v) as [B, C, S] and dw / db (fp32 [C],
+ * overwritten, summed in a fixed order) when given; dw needs w.  Workspace:
+ * nsq_channel_groupnorm_workspace_bytes(B, C, G, NSQ_DIR_BWD).
+ */
+size_t nsq_channel_groupnorm_workspace_bytes(int64_t B, int64_t C, int64_t G, int direction);
+
+int nsq_channel_groupnorm_fwd(const void* y, const void* v, const float* w, const float* b, void* out, float* mean,
+                              float* rstd, int dtype, int64_t B, int64_t C, int64_t S, int64_t G, float eps, int act,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+int nsq_channel_groupnorm_bwd(const void* dout, const void* y, const void* v, const float* w, const float* mean,
+                              const float* rstd, void* dy, void* dv, float* dw, float* db, int dtype, int64_t B,
+                              int64_t C, int64_t S, int64_t G, int act, void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 #ifdef __cplusplus
 }

@@ -36,7 +36,7 @@ NSQ_OK = 0
 NSQ_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 NSQ_DIR_FWD = 0
 NSQ_DIR_BWD = 1
-ABI_VERSION = 15
+ABI_VERSION = 16
 NSQ_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/nsq_hip.h: the fixed scratch of nsq_causal_conv1d_bwd_noalloc
 
 
@@ -176,6 +176,17 @@ _SIGNATURES = {
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64,
          _c_i64, _c_i64, ctypes.c_float, _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
+    ),
+    "nsq_channel_groupnorm_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "nsq_channel_groupnorm_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64,
+         _c_i64, ctypes.c_float, _c_int, _c_void_p, _c_size, _c_void_p],
+    ),
+    "nsq_channel_groupnorm_bwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_void_p, _c_size, _c_void_p],
     ),
     "nsq_channel_rmsnorm_bwd": (
         _c_int,

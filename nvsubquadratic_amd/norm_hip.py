@@ -28,8 +28,9 @@ from . import _lib
 from .gated_fftconv_hip import gate_code
 from .layout import channels_first_contiguous
 
-__all__ = ["HipL2Norm", "HipLayerNormChannels", "HipRMSNormChannelFirst", "channel_l2norm", "channel_rmsnorm",
-           "gated_channel_layernorm", "gated_channel_rmsnorm", "hyena_output_norm"]
+__all__ = ["HipGroupNorm", "HipL2Norm", "HipLayerNormChannels", "HipRMSNormChannelFirst", "channel_l2norm",
+           "channel_rmsnorm", "gated_channel_groupnorm", "gated_channel_layernorm", "gated_channel_rmsnorm",
+           "hyena_output_norm"]
 
 
 def _flat(t: torch.Tensor) -> torch.Tensor:
@@ -319,6 +320,153 @@ class HipLayerNormChannels(torch.nn.Module):
 
     def extra_repr(self) -> str:
         return f"{self.normalized_shape}, eps={self.eps}, elementwise_affine={self.elementwise_affine}"
+
+
+# ---------------------------------------------------------------------------
+# GroupNorm over channels, channels-first (the pixelhyena_norm site with torch.nn.GroupNorm(G, C), applied by
+# modules/hyena_nd.py:548-550 to z as it is), three passes each way (nsq_channel_groupnorm_fwd / _bwd)
+# ---------------------------------------------------------------------------
+@custom_op("nsq_hip::gated_channel_groupnorm", mutates_args=())
+def gated_channel_groupnorm_op(y: torch.Tensor, v: Optional[torch.Tensor], weight: Optional[torch.Tensor],
+                               bias: Optional[torch.Tensor], num_groups: int, eps: float,
+                               act: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """y, v ``[B, C, S]`` contiguous, weight / bias fp32 ``[C]`` or None -> ``(out [B, C, S], mean [B, G],
+    rstd [B, G])``, the statistics fp32."""
+    lib = _lib.get_lib()
+    _lib.check_device(y)
+    B, C, S = y.shape
+    out = torch.empty_like(y)
+    mean = torch.empty((B, num_groups), dtype=torch.float32, device=y.device)
+    rstd = torch.empty((B, num_groups), dtype=torch.float32, device=y.device)
+    nws = int(lib.nsq_channel_groupnorm_workspace_bytes(B, C, num_groups, _lib.NSQ_DIR_FWD))
+    ws = torch.empty(nws, dtype=torch.uint8, device=y.device)
+    _lib.check(lib.nsq_channel_groupnorm_fwd(
+        y.data_ptr(), v.data_ptr() if v is not None else None, weight.data_ptr() if weight is not None else None,
+        bias.data_ptr() if bias is not None else None, out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+        _lib.dtype_code(y.dtype), B, C, S, num_groups, float(eps), act, ws.data_ptr() if nws else None, nws,
+        _lib.stream_ptr(y.device)))
+    return out, mean, rstd
+
+
+@gated_channel_groupnorm_op.register_fake
+def _(y, v, weight, bias, num_groups, eps, act):
+    B = y.shape[0]
+    return (torch.empty_like(y), y.new_empty((B, num_groups), dtype=torch.float32),
+            y.new_empty((B, num_groups), dtype=torch.float32))
+
+
+@custom_op("nsq_hip::gated_channel_groupnorm_backward", mutates_args=())
+def gated_channel_groupnorm_backward_op(dout: torch.Tensor, y: torch.Tensor, v: Optional[torch.Tensor],
+                                        weight: Optional[torch.Tensor], mean: torch.Tensor, rstd: torch.Tensor,
+                                        want_db: bool, act: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                          torch.Tensor]:
+    """Returns ``(dy, dv, dw, db)``; ``dv`` / ``dw`` / ``db`` are empty when ``v`` / ``weight`` / ``want_db`` are
+    absent; ``dw`` and ``db`` fp32 ``[C]``."""
+    lib = _lib.get_lib()
+    _lib.check_device(y)
+    B, C, S = y.shape
+    G = mean.shape[1]
+    dy = torch.empty_like(y)
+    dv = torch.empty_like(v) if v is not None else y.new_empty(0)
+    dw = torch.empty(C, dtype=torch.float32, device=y.device) if weight is not None else y.new_empty(0)
+    db = torch.empty(C, dtype=torch.float32, device=y.device) if want_db else y.new_empty(0)
+    nws = int(lib.nsq_channel_groupnorm_workspace_bytes(B, C, G, _lib.NSQ_DIR_BWD))
+    ws = torch.empty(nws, dtype=torch.uint8, device=y.device)
+    _lib.check(lib.nsq_channel_groupnorm_bwd(
+        dout.data_ptr(), y.data_ptr(), v.data_ptr() if v is not None else None,
+        weight.data_ptr() if weight is not None else None, mean.data_ptr(), rstd.data_ptr(), dy.data_ptr(),
+        dv.data_ptr() if v is not None else None, dw.data_ptr() if weight is not None else None,
+        db.data_ptr() if want_db else None, _lib.dtype_code(y.dtype), B, C, S, G, act, ws.data_ptr(), nws,
+        _lib.stream_ptr(y.device)))
+    return dy, dv, dw, db
+
+
+@gated_channel_groupnorm_backward_op.register_fake
+def _(dout, y, v, weight, mean, rstd, want_db, act):
+    C = y.shape[1]
+    return (torch.empty_like(y), (torch.empty_like(v) if v is not None else y.new_empty(0)),
+            (y.new_empty(C, dtype=torch.float32) if weight is not None else y.new_empty(0)),
+            (y.new_empty(C, dtype=torch.float32) if want_db else y.new_empty(0)))
+
+
+def _gn_setup(ctx, inputs, output):
+    y, v, weight, bias, num_groups, eps, act = inputs
+    _, mean, rstd = output
+    ctx.save_for_backward(y, v, weight, mean, rstd)
+    ctx.cfg = (bias is not None, act)
+
+
+def _gn_backward(ctx, gout, gmean, grstd):
+    y, v, weight, mean, rstd = ctx.saved_tensors
+    has_b, act = ctx.cfg
+    dy, dv, dw, db = gated_channel_groupnorm_backward_op(gout.contiguous(), y, v, weight, mean, rstd, has_b, act)
+    return (dy, (dv if v is not None else None), (dw if weight is not None else None), (db if has_b else None),
+            None, None, None)
+
+
+gated_channel_groupnorm_op.register_autograd(_gn_backward, setup_context=_gn_setup)
+
+
+def gated_channel_groupnorm(y: torch.Tensor, v: Optional[torch.Tensor], weight: Optional[torch.Tensor],
+                            bias: Optional[torch.Tensor], num_groups: int, eps: float = 1e-5,
+                            gate_nonlinear="sigmoid") -> torch.Tensor:
+    """``torch.nn.GroupNorm(num_groups, C)`` of ``y * act(v)`` (of ``y`` when ``v`` is None), channels-first.
+
+    Args:
+        y, v: ``[B, C, *spatial]`` in fp32 / bf16 / fp16 (same dtype and shape).
+        weight, bias: ``[C]`` or None (``affine=False``).
+        num_groups: groups of ``C / num_groups`` consecutive channels; ``C`` must be a multiple of it.
+        eps: added to the variance, as ``GroupNorm(eps=...)``.
+        gate_nonlinear: ``"identity" | "sigmoid" | "silu"`` or the matching ``nn`` module.
+    """
+    if y.dim() < 2:
+        raise ValueError(f"expected [B, C, *spatial], got shape {tuple(y.shape)}")
+    if v is not None and (v.shape != y.shape or v.dtype != y.dtype):
+        raise ValueError(f"v {tuple(v.shape)} {v.dtype} must match y {tuple(y.shape)} {y.dtype}")
+    C = y.shape[1]
+    if num_groups < 1 or C % num_groups:
+        raise ValueError(f"num_channels {C} must be divisible by num_groups {num_groups}")
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None and t.shape != (C,):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != ({C},)")
+    w = _WeightToF32.apply(weight) if weight is not None and weight.dtype != torch.float32 else weight
+    b = _WeightToF32.apply(bias) if bias is not None and bias.dtype != torch.float32 else bias
+    out, _, _ = gated_channel_groupnorm_op(_flat(y), _flat(v) if v is not None else None,
+                                           w.contiguous() if w is not None else None,
+                                           b.contiguous() if b is not None else None, int(num_groups), float(eps),
+                                           gate_code(gate_nonlinear) if v is not None else 0)
+    return out.view(y.shape)
+
+
+class HipGroupNorm(torch.nn.Module):
+    """Drop-in for ``torch.nn.GroupNorm(num_groups, num_channels)`` at the Hyena operator's pixelhyena_norm site:
+    the same parameters (``weight`` ones, ``bias`` zeros, ``eps`` 1e-5, ``affine``) and arithmetic over
+    ``[B, C, *spatial]`` on the HIP kernels.  Channels-first like GroupNorm (``channels_first = True``)."""
+
+    channels_first: bool = True
+
+    def __init__(self, num_groups: int, num_channels: int, eps: float = 1e-5, affine: bool = True, device=None,
+                 dtype=None):
+        super().__init__()
+        if num_channels % num_groups:
+            raise ValueError("num_channels must be divisible by num_groups")
+        self.num_groups = num_groups
+        self.num_channels = num_channels
+        self.eps = eps
+        self.affine = affine
+        kw = {"device": device, "dtype": dtype}
+        if affine:
+            self.weight = torch.nn.Parameter(torch.ones(num_channels, **kw))
+            self.bias = torch.nn.Parameter(torch.zeros(num_channels, **kw))
+        else:
+            self.register_parameter("weight", None)
+            self.register_parameter("bias", None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return gated_channel_groupnorm(x, None, self.weight, self.bias, self.num_groups, self.eps, "identity")
+
+    def extra_repr(self) -> str:
+        return f"{self.num_groups}, {self.num_channels}, eps={self.eps}, affine={self.affine}"
 
 
 # ---------------------------------------------------------------------------

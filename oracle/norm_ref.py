@@ -25,6 +25,14 @@ parameters float32), the mean and the biased variance over the channels, ``(x - 
 rounded once to the input dtype.  Pinned against ``torch.nn.functional.layer_norm`` in float64 (a library routine), a
 closed form ((1, 2, 3) -> (-sqrt(3/2), 0, sqrt(3/2)) at eps = 0), shift and scale invariance of the normalised values,
 and float64 gradcheck.
+
+The GroupNorm site (a ``torch.nn.GroupNorm(num_groups, C)`` as ``pixelhyena_norm``, applied channels-first by
+``hyena_nd.py:548-550`` since ``modules/_channels_first_utils.py:27`` marks GroupNorm channels-first) is restated as
+torch's group norm computes it: per sample and group of ``C / G`` consecutive channels, the mean and the biased
+variance over those channels and every position (accumulated in float64 here), then per channel the float32
+scale ``a = rsqrt(var + eps) * w`` and shift ``h = b - mean * a``, ``x * a + h`` rounded once to the input dtype.
+Pinned against ``torch.nn.functional.group_norm`` in float64 (a library routine), ``instance_norm`` at ``G = C`` (a
+second library routine), a closed form at ``G = 1`` and float64 gradcheck.
 """
 
 from __future__ import annotations
@@ -33,7 +41,7 @@ from typing import Optional
 
 import torch
 
-__all__ = ["gated_channel_layernorm_ref", "gated_channel_rmsnorm_ref", "l2norm_ref"]
+__all__ = ["gated_channel_groupnorm_ref", "gated_channel_layernorm_ref", "gated_channel_rmsnorm_ref", "l2norm_ref"]
 
 _ACTS = {0: lambda t: t, 1: torch.sigmoid, 2: torch.nn.functional.silu}
 
@@ -76,3 +84,26 @@ def gated_channel_layernorm_ref(y: torch.Tensor, v: Optional[torch.Tensor], weig
         out = out + bias.to(xf.dtype)
     out = out.to(dt)
     return out if channels_last else out.movedim(-1, 1)
+
+
+def gated_channel_groupnorm_ref(y: torch.Tensor, v: Optional[torch.Tensor], weight: Optional[torch.Tensor],
+                                bias: Optional[torch.Tensor], num_groups: int, eps: float = 1e-5,
+                                act: int = 1) -> torch.Tensor:
+    """``y``, ``v`` ``[B, C, *S]`` (CPU), ``weight`` / ``bias`` ``[C]`` or None -> ``[B, C, *S]``."""
+    u = y * _ACTS[act](v) if v is not None else y           # hyena_nd.py:546 (I/O dtype)
+    B, C = u.shape[:2]
+    G = num_groups
+    assert C % G == 0
+    dt = u.dtype
+    cdt = torch.float64 if dt == torch.float64 else torch.float32
+    xg = u.reshape(B, G, -1).to(torch.float64)
+    mean = xg.mean(-1)                                        # [B, G]
+    var = (xg - mean[..., None]).pow(2).mean(-1)              # biased, as GroupNorm
+    rstd = torch.rsqrt(var + eps).to(cdt)
+    w = weight.to(cdt) if weight is not None else torch.ones(C, dtype=cdt)
+    b = bias.to(cdt) if bias is not None else torch.zeros(C, dtype=cdt)
+    a = rstd.repeat_interleave(C // G, dim=1) * w             # [B, C]
+    h = b - mean.to(cdt).repeat_interleave(C // G, dim=1) * a
+    x = u.reshape(B, C, -1).to(cdt)
+    out = x * a[..., None] + h[..., None]
+    return out.to(dt).reshape(u.shape)

@@ -195,13 +195,15 @@ def test_noalloc_backward_refuses_oversize_scratch_on_the_host():
 
 
 _OPS = ["causal_fftconv1d", "fftconv_nd", "shifted_fftconv1d", "causal_conv1d", "b2b_causal_conv1d",
-        "gated_causal_fftconv1d", "gated_fftconv_nd"]
+        "gated_causal_fftconv1d", "gated_fftconv_nd", "gated_channel_rmsnorm", "gated_channel_layernorm",
+        "gated_channel_groupnorm", "channel_l2norm"]
 
 
 def test_every_hip_op_is_a_registered_custom_op():
     """Each op and its backward are torch.library custom ops (traceable by torch.compile)."""
     import nvsubquadratic_amd.causal_conv1d_hip  # noqa: F401
     import nvsubquadratic_amd.gated_fftconv_hip  # noqa: F401
+    import nvsubquadratic_amd.norm_hip  # noqa: F401
 
     for name in _OPS:
         for n in (name, name + "_backward"):
@@ -230,6 +232,14 @@ def test_fake_implementations_propagate_shapes_without_a_gpu():
         assert y2.shape == x2.shape and st2.numel() == 0
         yb = torch.ops.nsq_hip.b2b_causal_conv1d(torch.empty(2, 12, 64), torch.empty(12, 3), torch.empty(4, 9), None)
         assert yb.shape == (2, 4, 64)
+        import nvsubquadratic_amd.norm_hip  # noqa: F401
+
+        yn = torch.empty(3, 12, 40)
+        gn, mean, rstd = torch.ops.nsq_hip.gated_channel_groupnorm(yn, yn, torch.empty(12), None, 4, 1e-5, 1)
+        assert gn.shape == yn.shape and mean.shape == (3, 4) and rstd.shape == (3, 4)
+        dyn, dvn, dwn, dbn = torch.ops.nsq_hip.gated_channel_groupnorm_backward(yn, yn, yn, torch.empty(12), mean,
+                                                                                rstd, False, 1)
+        assert dyn.shape == yn.shape and dvn.shape == yn.shape and dwn.shape == (12,) and dbn.numel() == 0
 
 
 def test_transpose_launch_limits_and_fallback():

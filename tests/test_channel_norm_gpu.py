@@ -310,3 +310,134 @@ def test_layernorm_opcheck():
     b = torch.rand(16, device="cuda", requires_grad=True)
     torch.library.opcheck(N.gated_channel_layernorm_op, (y, v, w, b, 1e-5, 2, True))
     torch.library.opcheck(N.gated_channel_layernorm_op, (y, None, None, None, 1e-5, 0, False))
+
+
+# GroupNorm over channels, channels-first (the pixelhyena_norm site with torch.nn.GroupNorm(G, C))
+
+def _gn_case(B, C, spatial, G, dtype, gate, affine=True, eps=1e-5, seed=0, offset=0.3, tol=None, gtol=None):
+    from oracle.norm_ref import gated_channel_groupnorm_ref
+
+    print(f"gn case B={B} C={C} S={spatial} G={G} {dtype} gate={gate} affine={affine}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    y = (0.7 * torch.randn(B, C, *spatial, generator=g) + offset).to(dtype)
+    v = torch.randn(B, C, *spatial, generator=g).to(dtype) if gate is not None else None
+    w = (1 + 0.5 * torch.randn(C, generator=g)).float() if affine else None
+    b = (0.2 * torch.randn(C, generator=g)).float() if affine else None
+    dev = "cuda"
+    leaves = [t.to(dev).requires_grad_() if t is not None else None for t in (y, v, w, b)]
+    out = N.gated_channel_groupnorm(*leaves, G, eps, gate or "identity")
+    gout = torch.randn(out.shape, generator=g).to(dtype)
+    out.backward(gout.to(dev))
+    torch.cuda.synchronize()
+    refs = [t.clone().requires_grad_() if t is not None else None for t in (y, v, w, b)]
+    ref = gated_channel_groupnorm_ref(*refs, G, eps, ACT[gate] if gate else 0)
+    ref.backward(gout)
+    tol = tol or TOL[dtype]
+    gtol = gtol or tol
+    assert out.shape == ref.shape and out.dtype == dtype
+    assert rel_l2(ref, out) < tol
+    for r, d in zip(refs, leaves):
+        if r is not None:
+            assert rel_l2(r.grad, d.grad) < (tol if r.dtype == torch.float32 and r.dim() == 1 else gtol)
+
+
+@pytest.mark.parametrize("gate", [None, "sigmoid"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_groupnorm_hyena_shape(gate, dtype):
+    # the reference's configs: GroupNorm(num_groups=1, C) on [B, C, H, W]
+    _gn_case(2, 384, (32, 32), 1, dtype, gate)
+
+
+@pytest.mark.parametrize("B,C,spatial,G,affine", [(3, 12, (7, 5), 4, True), (2, 8, (33,), 8, True),
+                                                   (1, 1, (70,), 1, False), (2, 6, (1,), 3, True),
+                                                   (2, 16, (3, 4, 5), 2, True), (1, 4, (100003,), 1, True),
+                                                   (2, 32, (64, 64), 1, False)])
+def test_groupnorm_ragged_shapes_and_groups(B, C, spatial, G, affine):
+    _gn_case(B, C, spatial, G, torch.float32, "silu", affine=affine, seed=1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_groupnorm_ragged_16bit(dtype):
+    # S not a multiple of the 8-wide vectors: the scalar passes
+    _gn_case(2, 24, (13, 7), 3, dtype, "silu", seed=2)
+
+
+def test_groupnorm_large_mean():
+    # A mean 1400x the spread (fp32 in and out).  torch's scale / shift form u a + (b - mean a) rounds two terms of
+    # size mean / std to fp32, so outputs of unit size carry errors near 1e-4 in any fp32 implementation of it
+    # (1 ulp of a or of mean moves them that much): 5e-4 is that bound.  E[u^2] - E[u]^2 in fp32 would lose the
+    # variance outright (an error of about 10% here); the shifted row sums keep it.
+    _gn_case(2, 16, (40, 40), 2, torch.float32, None, offset=1000.0, seed=3, tol=5e-4, gtol=5e-4)
+
+
+def test_groupnorm_misaligned_pointers():
+    # inputs at an offset of one element: the scalar passes on unaligned rows
+    from oracle.norm_ref import gated_channel_groupnorm_ref
+
+    B, C, S, G = 2, 8, 64, 2
+    base = torch.randn(B * C * S + 1, device="cuda").to(torch.bfloat16)
+    y = base[1:].view(B, C, S)
+    w = torch.rand(C, device="cuda") + 0.5
+    out, mean, rstd = N.gated_channel_groupnorm_op(y, None, w, None, G, 1e-5, 0)
+    ref = gated_channel_groupnorm_ref(y.cpu(), None, w.cpu(), None, G, 1e-5, 0)
+    assert rel_l2(ref, out) < TOL[torch.bfloat16]
+    xg = y.double().reshape(B, G, -1)
+    assert torch.allclose(mean.double(), xg.mean(-1), rtol=1e-5, atol=1e-5)
+    assert torch.allclose(rstd.double(), torch.rsqrt(xg.var(-1, unbiased=False) + 1e-5), rtol=1e-4)
+
+
+def test_groupnorm_module_drop_in():
+    """HipGroupNorm equals torch.nn.GroupNorm on [B, C, *S], outputs and every gradient."""
+    torch.manual_seed(9)
+    for G in (1, 4):
+        ref = torch.nn.GroupNorm(G, 48).cuda()
+        with torch.no_grad():
+            ref.weight.copy_(1 + 0.3 * torch.randn(48))
+            ref.bias.copy_(0.1 * torch.randn(48))
+        mod = N.HipGroupNorm(G, 48).cuda()
+        mod.load_state_dict(ref.state_dict())
+        assert mod.channels_first
+        x = torch.randn(2, 48, 9, 11, device="cuda", requires_grad=True)
+        xr = x.detach().clone().requires_grad_()
+        y = mod(x)
+        yr = ref(xr)
+        gr = torch.randn_like(y)
+        y.backward(gr)
+        yr.backward(gr)
+        assert rel_l2(yr, y) < 1e-5
+        assert rel_l2(xr.grad, x.grad) < 1e-5
+        assert rel_l2(ref.weight.grad, mod.weight.grad) < 1e-5
+        assert rel_l2(ref.bias.grad, mod.bias.grad) < 1e-5
+
+
+def test_groupnorm_gradients_deterministic():
+    torch.manual_seed(10)
+    y = torch.randn(4, 64, 4096, device="cuda", dtype=torch.bfloat16)
+    w = torch.rand(64, device="cuda")
+    g = torch.randn(4, 64, 4096, device="cuda", dtype=torch.bfloat16)
+    _, mean, rstd = N.gated_channel_groupnorm_op(y, None, w, None, 1, 1e-5, 0)
+    r1 = N.gated_channel_groupnorm_backward_op(g, y, None, w, mean, rstd, True, 0)
+    r2 = N.gated_channel_groupnorm_backward_op(g, y, None, w, mean, rstd, True, 0)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+
+
+def test_groupnorm_argument_errors():
+    y = torch.randn(2, 6, 8, device="cuda")
+    with pytest.raises(ValueError, match="divisible"):
+        N.gated_channel_groupnorm(y, None, None, None, 4)
+    with pytest.raises(ValueError, match="channel_groupnorm_fwd: num_channels 6 must be divisible"):
+        N.gated_channel_groupnorm_op(y, None, None, None, 4, 1e-5, 0)  # the library's own check
+    lib = _lib.get_lib()
+    assert lib.nsq_channel_groupnorm_workspace_bytes(2, 6, 4, _lib.NSQ_DIR_FWD) == 0
+    assert lib.nsq_channel_groupnorm_workspace_bytes(2, 6, 3, _lib.NSQ_DIR_FWD) == 2 * 6 * 8
+    assert lib.nsq_channel_groupnorm_workspace_bytes(2, 6, 3, _lib.NSQ_DIR_BWD) == 2 * 6 * 8 + 2 * 3 * 8
+
+
+def test_groupnorm_opcheck():
+    y = torch.randn(2, 16, 24, device="cuda", requires_grad=True)
+    v = torch.randn(2, 16, 24, device="cuda", requires_grad=True)
+    w = torch.rand(16, device="cuda", requires_grad=True)
+    b = torch.rand(16, device="cuda", requires_grad=True)
+    torch.library.opcheck(N.gated_channel_groupnorm_op, (y, v, w, b, 4, 1e-5, 2))
+    torch.library.opcheck(N.gated_channel_groupnorm_op, (y, None, None, None, 1, 1e-5, 0))

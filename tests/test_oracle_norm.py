@@ -7,7 +7,7 @@ import math
 import pytest
 import torch
 
-from oracle.norm_ref import gated_channel_layernorm_ref, gated_channel_rmsnorm_ref, l2norm_ref
+from oracle.norm_ref import gated_channel_groupnorm_ref, gated_channel_layernorm_ref, gated_channel_rmsnorm_ref, l2norm_ref
 
 
 def test_closed_form_ramp():
@@ -128,3 +128,63 @@ def test_layernorm_gradcheck_float64():
     w = torch.randn(6, dtype=torch.float64, requires_grad=True)
     b = torch.randn(6, dtype=torch.float64, requires_grad=True)
     assert torch.autograd.gradcheck(lambda *t: gated_channel_layernorm_ref(*t, 1e-3, 2, True), (y, v, w, b))
+
+
+# GroupNorm over channels, channels-first (the pixelhyena_norm site with torch.nn.GroupNorm(G, C))
+
+@pytest.mark.parametrize("groups", [1, 3, 12])
+@pytest.mark.parametrize("affine", [True, False])
+def test_groupnorm_restatement_matches_torch_group_norm_float64(groups, affine):
+    torch.manual_seed(6)
+    y = torch.randn(2, 12, 5, 3, dtype=torch.float64)
+    v = torch.randn(2, 12, 5, 3, dtype=torch.float64)
+    w = torch.randn(12, dtype=torch.float64) if affine else None
+    b = torch.randn(12, dtype=torch.float64) if affine else None
+    for act, f in ((0, lambda t: t), (1, torch.sigmoid), (2, torch.nn.functional.silu)):
+        got = gated_channel_groupnorm_ref(y, v, w, b, groups, 1e-5, act)
+        want = torch.nn.functional.group_norm(y * f(v), groups, w, b, 1e-5)
+        assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_groupnorm_one_group_per_channel_is_instance_norm():
+    torch.manual_seed(7)
+    y = torch.randn(3, 8, 4, 5, dtype=torch.float64)
+    w = torch.randn(8, dtype=torch.float64)
+    b = torch.randn(8, dtype=torch.float64)
+    got = gated_channel_groupnorm_ref(y, None, w, b, 8, 1e-5, 0)
+    want = torch.nn.functional.instance_norm(y, weight=w, bias=b, eps=1e-5)
+    assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_groupnorm_closed_form_one_group():
+    # one group over C = 2 channels x S = 2 positions: values 1, 2, 3, 4 -> mean 2.5, var 1.25
+    y = torch.tensor([[[1.0, 2.0], [3.0, 4.0]]], dtype=torch.float64)
+    out = gated_channel_groupnorm_ref(y, None, None, None, 1, 0.0, 0)
+    r = 1.0 / math.sqrt(1.25)
+    want = torch.tensor([[[-1.5 * r, -0.5 * r], [0.5 * r, 1.5 * r]]], dtype=torch.float64)
+    assert torch.allclose(out, want, rtol=1e-14, atol=1e-14)
+    # w, b per channel after the group statistics: channel 1 scaled by 2 and shifted by 1
+    o2 = gated_channel_groupnorm_ref(y, None, torch.tensor([1.0, 2.0], dtype=torch.float64),
+                                     torch.tensor([0.0, 1.0], dtype=torch.float64), 1, 0.0, 0)
+    assert torch.allclose(o2[0, 1], 2.0 * want[0, 1] + 1.0, rtol=1e-14, atol=1e-14)
+    assert torch.allclose(o2[0, 0], want[0, 0], rtol=1e-14, atol=1e-14)
+
+
+def test_groupnorm_float32_rounding_once():
+    # a 16-bit input: the statistics in float64, the affine in float32, one rounding to the input dtype
+    torch.manual_seed(8)
+    y = torch.randn(2, 6, 33).to(torch.bfloat16)
+    w, b = torch.randn(6), torch.randn(6)
+    got = gated_channel_groupnorm_ref(y, None, w, b, 2, 1e-5, 0)
+    assert got.dtype == torch.bfloat16
+    want = torch.nn.functional.group_norm(y.double(), 2, w.double(), b.double(), 1e-5)
+    assert (got.double() - want).abs().max() <= 2 ** -7 * want.abs().max()
+
+
+def test_groupnorm_gradcheck_float64():
+    torch.manual_seed(9)
+    y = torch.randn(2, 6, 4, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(2, 6, 4, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(6, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(6, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda *t: gated_channel_groupnorm_ref(*t, 3, 1e-3, 2), (y, v, w, b))
