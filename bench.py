@@ -359,9 +359,9 @@ def other_workload(name: str, steps: int, warmup: int, cpu: bool = True, compare
         fn = F.fftconv2d_bhl if nd == 2 else F.fftconv3d_bhl
         phase, dtype = ("fwd", "f32") if nd == 2 else ("fwd+bwd", "f32")
         nbytes = algorithmic_bytes_nd(B, C, [size] * nd, [size] * nd, 2, phase)
-        # FFT sizes: config 4's forward keeps no state and runs the one-kernel image forward on 256^2; config 5
-        # runs the reference's own F = S + K/2 = 96 per axis (mixed-radix plan)
-        fft = "FFT 256^2 (one-kernel image forward)" if nd == 2 else "FFT 96^3 per axis (mixed-radix)"
+        # FFT sizes: the reference's own F = S + K/2 per axis: config 4's forward keeps no state and runs the
+        # one-kernel image forward on 192^2; config 5 the mixed-radix plan on 96^3
+        fft = "FFT 192^2 (one-kernel image forward, mixed-radix)" if nd == 2 else "FFT 96^3 per axis (mixed-radix)"
         desc = (f"cfg{4 if nd == 2 else 5}: {nd}D non-causal FFT conv {phase}, B={B} C={C} {size}^{nd}, "
                 f"filter {size}^{nd} fp32, {fft}, bf16 I/O")
         if nd == 2:

@@ -126,21 +126,37 @@ __device__ __forceinline__ void mixed_store(ST& st, int m, int n, float2 v) {
     st(m, n, v);
 }
 
+// Pass synchronisation: a workgroup barrier, or (WAVE) the wave's own
+// in-order LDS operations when one wave owns every transform of the pass.
+template <bool WAVE>
+__device__ __forceinline__ void mixed_sync() {
+  if constexpr (WAVE) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    __syncthreads();
+  }
+}
+
 // One radix-R Stockham pass over M transforms of length N by T threads,
-// after sub-transforms of length NS: butterfly (m, j), j < N/R, reads
+// after sub-transforms of length NS (WAVE: T = 64, the lanes of one wave,
+// which owns the M transforms; no workgroup barrier): butterfly (m, j), j < N/R, reads
 // elements j + r N/R, multiplies by W_{NS R}^{r (j mod NS)}, transforms, and
 // writes elements (j - j mod NS) R + j mod NS + r NS.  TMAJOR as in
 // stockham_pass.  Barriers bracket the writes, so LD and ST may alias.
 // TW: the roots' source (TwAny: the global table; TwLds: roots staged in LDS).
-template <int N, int R, int NS, bool INV, int M, int T, bool TMAJOR, class LD, class ST, class TW>
+template <int N, int R, int NS, bool INV, int M, int T, bool TMAJOR, bool WAVE = false, class LD, class ST,
+          class TW>
 __device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const TW& tws) {
+  static_assert(!WAVE || T == 64, "mixed_pass: a wave-local pass runs on the 64 lanes of one wave");
   constexpr int NR = N / R;
   constexpr int NB = M * NR;
   constexpr int PER = (NB + T - 1) / T;
   constexpr bool EXACT = NB % T == 0;
   constexpr int L = NS * R;
   static_assert(N % R == 0 && NR % NS == 0, "mixed_pass: radix does not divide the transform");
-  const int tid = opaque_tid();
+  const int tid = WAVE ? (opaque_tid() & 63) : opaque_tid();
   float2 w[PER][R];
   if constexpr (NS > 1) {
 #pragma unroll
@@ -161,7 +177,7 @@ __device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const TW& tws) {
 #pragma unroll
     for (int r = 0; r < R; ++r) v[i][r] = mixed_load(ld, m, j + r * NR);
   }
-  __syncthreads();
+  mixed_sync<WAVE>();
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int bf = tid + i * T;
@@ -178,35 +194,43 @@ __device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const TW& tws) {
 #pragma unroll
     for (int r = 0; r < R; ++r) mixed_store(st, m, base + r * NS, v[i][r]);
   }
-  __syncthreads();
+  mixed_sync<WAVE>();
 }
 
 // Full transform of M length-N sequences (first pass through ld_first, last
 // through st_last, the passes between in the LDS tile st_lds / ld_lds), radix
-// at most RMAX after the radix-3 pass.  Ends with a barrier.
-template <int N, int NS, bool INV, int M, int T, bool TMAJOR, int RMAX, class LDF, class STL, class LDL, class STF,
-          class TW>
+// at most RMAX after the radix-3 pass.  Ends with a barrier (WAVE: a wave
+// sync).
+template <int N, int NS, bool INV, int M, int T, bool TMAJOR, int RMAX, bool WAVE, class LDF, class STL, class LDL,
+          class STF, class TW>
 __device__ __forceinline__ void fft_mixed_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last, const TW& tws) {
   constexpr int R = mixed_radix(N, NS, RMAX);
   constexpr bool FIRST = NS == 1;
   constexpr bool LAST = NS * R == N;
   if constexpr (FIRST && LAST) {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_first, st_last, tws);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_first, st_last, tws);
   } else if constexpr (FIRST) {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_first, st_lds, tws);
-    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX>(ld_first, st_lds, ld_lds, st_last, tws);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_first, st_lds, tws);
+    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX, WAVE>(ld_first, st_lds, ld_lds, st_last, tws);
   } else if constexpr (LAST) {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_lds, st_last, tws);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_lds, st_last, tws);
   } else {
-    mixed_pass<N, R, NS, INV, M, T, TMAJOR>(ld_lds, st_lds, tws);
-    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX>(ld_first, st_lds, ld_lds, st_last, tws);
+    mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_lds, st_lds, tws);
+    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX, WAVE>(ld_first, st_lds, ld_lds, st_last, tws);
   }
 }
 
 template <int N, bool INV, int M, int T, bool TMAJOR, int RMAX, class LDF, class TILE, class STF, class TW>
 __device__ __forceinline__ void fft_mixed(LDF& ld_first, TILE& tile, STF& st_last, const TW& tws) {
   static_assert(mixed_len(N), "fft_mixed: length must be 2^m or 3 * 2^m");
-  fft_mixed_rec<N, 1, INV, M, T, TMAJOR, RMAX>(ld_first, tile, tile, st_last, tws);
+  fft_mixed_rec<N, 1, INV, M, T, TMAJOR, RMAX, false>(ld_first, tile, tile, st_last, tws);
+}
+
+// fft_mixed by one wave on transforms that it alone reads and writes.
+template <int N, bool INV, int M, bool TMAJOR, int RMAX, class LDF, class TILE, class STF, class TW>
+__device__ __forceinline__ void fft_mixed_wave(LDF& ld_first, TILE& tile, STF& st_last, const TW& tws) {
+  static_assert(mixed_len(N), "fft_mixed_wave: length must be 2^m or 3 * 2^m");
+  fft_mixed_rec<N, 1, INV, M, 64, TMAJOR, RMAX, true>(ld_first, tile, tile, st_last, tws);
 }
 
 }  // namespace nsq

@@ -438,6 +438,15 @@ inline bool image_fwd_enabled() {
   return on;
 }
 
+// NSQ_2D_IMAGE192=0: no one-kernel image forward on the 192 x 192 plane.
+inline bool image192_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("NSQ_2D_IMAGE192");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 // The power-of-two plan of the shape of p (no periodic axes: the mixed-radix
 // plan has none).
 inline bool pow2_plan_of(const NdPlan& p, NdPlan& p2) {
@@ -454,9 +463,14 @@ bool run_r3_fwd(const NdPlan& p, const void* x, const float* k, const void* s, v
 template <int DT>
 bool run_r3_bwd(const NdPlan& p, const void* g, const void* x, const float* k, const void* s, void* gx, float* gk,
                 float* gs, float2* ws, bool fwd_state, const float2* tw, hipStream_t st);
+template <int DT>
+bool run_r3_image_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws,
+                      const float2* tw, hipStream_t st);
 #define NSQ_R3_RUN_INSTANCES(EXT, DT)                                                                               \
   EXT template bool run_r3_fwd<DT>(const NdPlan&, const void*, const float*, const void*, void*, float2*, bool,    \
                                    const float2*, hipStream_t);                                                  \
+  EXT template bool run_r3_image_fwd<DT>(const NdPlan&, const void*, const float*, const void*, void*, float2*,   \
+                                         const float2*, hipStream_t);                                            \
   EXT template bool run_r3_bwd<DT>(const NdPlan&, const void*, const void*, const float*, const void*, void*,      \
                                    float*, float*, float2*, bool, const float2*, hipStream_t);
 NSQ_R3_RUN_INSTANCES(extern, NSQ_DTYPE_F32)
@@ -485,6 +499,8 @@ bool run_nd_fwd(const NdPlan& p, const void* x, const float* k, const void* s, v
       // the mixed-radix passes at config 4 (measured).  Its filter spectrum
       // (H blocks of 256 x 128) goes to the workspace start; the mixed-radix
       // forward workspace ((B + 1) H blocks of 192 x 97) holds it.
+      if (!save && p.nd == 2 && p.kb == 1 && image192_enabled() && run_r3_image_fwd<DT>(p, x, k, s, y, ws, tw, st))
+        return true;
       NdPlan p2;
       if (!save && p.nd == 2 && p.kb == 1 && image_fwd_enabled() && pow2_plan_of(p, p2) && image_fwd_ok(p2, x, y) &&
           p2.H * p2.spec <= (p.B * p.H + p.H) * p.spec) {

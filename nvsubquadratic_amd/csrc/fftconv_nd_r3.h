@@ -433,6 +433,32 @@ __global__ __launch_bounds__(R3ColCfg<F0>::T) void r3_col_fwd_kernel(float2* __r
   fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ld1, tile, st, tws);
 }
 
+// The same transform written transposed, out[blk][j][k] (a column's F0
+// frequencies contiguous), through the LDS tile so the stores are coalesced:
+// the filter spectrum of the one-kernel image forward.
+template <int F0, bool THIRD>
+__global__ __launch_bounds__(R3ColCfg<F0>::T) void r3_col_fwd_t_kernel(const float2* __restrict__ ws, ColGeom cg,
+                                                           int in_cnt, float2* __restrict__ out,
+                                                           const float2* __restrict__ tw) {
+  using C = R3ColCfg<F0>;
+  __shared__ float2 lds[C::M * C::S];
+  __shared__ float2 twl[F0];
+  const auto tws = stage_roots<F0, C::T>(twl, tw);
+  __syncthreads();
+  const ColBuf cb(ws + int64_t(blockIdx.x) * cg.spec, cg);
+  const int j0 = int(blockIdx.y) * C::M;
+  auto ld = [&](int m, int n) -> float2 { return cb.load(n, j0 + m, j0 + m < cg.inner_count && n < in_cnt); };
+  TailZeroLoad<3, 2, THIRD, decltype(ld)> ld1{ld};
+  LdsTile<C::S, false> tile{lds};
+  fft_mixed<F0, false, C::M, C::T, true, C::RMAX>(ld1, tile, tile, tws);
+  float2* ob = out + (int64_t(blockIdx.x) * cg.inner_count + j0) * F0;
+  const int nm = min(C::M, cg.inner_count - j0);
+  for (int e = int(threadIdx.x); e < nm * F0; e += C::T) {
+    const int m = e / F0, k = e - m * F0;
+    ob[e] = *tile.at(m, k);
+  }
+}
+
 // Forward conv along axis 0: FFT(x column) * Khat -> IFFT -> window [c0, c0 +
 // S0) to rows [0, S0), from wsx to wsy (the same buffer for an in-place
 // product).  Shared filter (kfilm = 0): grid.x = H * bsplit, a workgroup

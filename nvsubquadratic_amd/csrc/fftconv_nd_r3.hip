@@ -1,6 +1,7 @@
 // Host passes of the mixed-radix 2D / 3D plan (kernels in fftconv_nd_r3.h): the
 // same pass sequence, workspace layout and results as run_nd_fwd /
 // run_nd_bwd in fftconv_nd_plan.h, at FFT lengths 3 * 2^m.
+#include "fftconv2d_image192.h"
 #include "fftconv_nd_plan.h"
 #include "fftconv_nd_r3.h"
 
@@ -196,6 +197,61 @@ bool run_r3_bwd(const NdPlan& p, const void* g, const void* x, const float* k, c
   if (!r3_inner_inv<DT, ND_OUT_Y>(p, wsg, BH, p.S[0], 0, p.S[1], og, tw, st)) return false;
   RowInvOut ok_{gk, nullptr, nullptr, gs, int(p.H), 0, p.K[2], p.c[0], p.c[1], p.c[2], scale * p.gk_scale};
   return r3_inner_inv<NSQ_DTYPE_F32, ND_OUT_GK>(p, wsq, NK, p.K[0], 0, p.K[1], ok_, tw, st);
+}
+
+// The one-kernel image forward on the 192 x 192 plane (fftconv2d_image192.h)
+// for a 2D forward that keeps no state: the filter spectrum's rows at the
+// workspace's Khat position, its columns transposed into the X region the
+// kernel does not use (H * 97 * 192 <= B * H * spec).
+inline bool r3_image_ok(const NdPlan& p, const void* x, const void* y) {
+  return p.r3 && p.nd == 2 && p.kb == 1 && !p.ramp && p.wm[0] == -1 && p.wm[2] == -1 && p.F[0] == kI3F &&
+         p.F[2] == kI3F && p.FH == kI3Bins && p.S[0] <= kI3Rows && p.S[2] <= kI3Rows &&
+         p.S[2] % 8 == 0 && p.o[2] % 2 == 0 && p.o[0] + p.S[0] <= kI3F && p.o[2] + p.S[2] <= kI3F &&
+         p.spec >= int64_t(kI3Bins) * kI3F && p.B * p.H <= int64_t(1) << 30 &&
+         (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+}
+
+inline int image192_threads() {
+  static const int t = [] {
+    const char* e = std::getenv("NSQ_2D_IMAGE192_T");
+    return (e && std::atoi(e) == 512) ? 512 : 1024;
+  }();
+  return t;
+}
+
+template <int DT>
+bool run_r3_image_fwd(const NdPlan& p, const void* x, const float* k, const void* s, void* y, float2* ws,
+                      const float2* tw, hipStream_t st) {
+  if (!r3_image_ok(p, x, y)) return false;
+  using ET = typename Elem<DT>::T;
+  const int64_t BH = p.B * p.H;
+  float2* wsk = ws + BH * p.spec;
+  float2* kt = ws;
+  // the filter spectrum's row passes into the Khat region, its column pass
+  // written transposed into the X region
+  if (!r3_inner_fwd<NSQ_DTYPE_F32>(p, k, p.H, p.K[0], p.K[1], p.K[2], wsk, tw, st)) return false;
+  const ColGeom cg = axis0_geom(p);
+  const dim3 kgrid{unsigned(p.H), unsigned(ceil_div(cg.inner_count, R3ColCfg<kI3F>::M))};
+  if (3 * p.K[0] <= 2 * kI3F)
+    hipLaunchKernelGGL((r3_col_fwd_t_kernel<kI3F, true>), kgrid, dim3(R3ColCfg<kI3F>::T), 0, st, (const float2*)wsk,
+                       cg, p.K[0], kt, tw);
+  else
+    hipLaunchKernelGGL((r3_col_fwd_t_kernel<kI3F, false>), kgrid, dim3(R3ColCfg<kI3F>::T), 0, st, (const float2*)wsk,
+                       cg, p.K[0], kt, tw);
+  const float scale = 1.f / (float(kI3F) * float(kI3N2));
+  const dim3 grid{unsigned(BH)};
+  auto go = [&](auto hs, auto tc) {
+    constexpr int T = decltype(tc)::value;
+    hipLaunchKernelGGL((nd2_image192_fwd_kernel<DT, decltype(hs)::value, T>), grid, dim3(T), 0, st, (const ET*)x,
+                       (const float2*)kt, (const ET*)s, (ET*)y, int(p.B), int(p.H), int(p.S[0]), int(p.S[2]),
+                       int(p.o[0]), int(p.o[2]), scale, tw);
+  };
+  const bool t512 = image192_threads() == 512;
+  if (s)
+    t512 ? go(std::true_type{}, IC<512>{}) : go(std::true_type{}, IC<1024>{});
+  else
+    t512 ? go(std::false_type{}, IC<512>{}) : go(std::false_type{}, IC<1024>{});
+  return true;
 }
 
 NSQ_R3_RUN_INSTANCES(, NSQ_DTYPE_F32)

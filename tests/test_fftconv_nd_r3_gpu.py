@@ -244,3 +244,47 @@ def test_r3_2d_backward_reusing_forward_state_is_bitwise_equal():
     y2 = torch.empty_like(x)
     F.fftconv_nd_fwd_raw(x, k, s, y2, kb)
     assert torch.equal(y, y2)
+
+
+# The one-kernel image forward on the 192 x 192 plane (fftconv2d_image192.h) runs a 2D forward that keeps no
+# state (no gradient wanted) when F0 = F2 = 192, S0, S2 <= 128, S2 % 8 == 0 and K2 // 2 is even; forwards that keep
+# a state run the three passes.  Both against the oracle, and against each other.
+IMAGE192_SHAPES = [
+    ((2, 8, 128, 128), (128, 128)),   # config 4's geometry: every row and column of the tile
+    ((3, 5, 100, 104), (100, 168)),   # a partial row group, crop offsets 50 / 84
+    ((2, 3, 128, 128), (127, 128)),   # odd K0 (o0 = 63)
+    ((1, 2, 128, 120), (65, 129)),    # o2 = 64 from an odd K2, S2 = 120
+]
+
+
+@pytest.mark.parametrize("xs,ks", IMAGE192_SHAPES)
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2), (torch.float16, 2e-2)])
+@pytest.mark.parametrize("shortcut", [True, False])
+def test_image192_forward(xs, ks, dtype, tol, shortcut):
+    print(f"image192 case {xs} {ks} {dtype} shortcut={shortcut}", flush=True)
+    torch.manual_seed(6)
+    H = xs[1]
+    x = torch.randn(*xs).to(dtype)
+    k = torch.randn(H, *ks)
+    s = torch.randn(H).to(dtype) if shortcut else None
+    y_ref = fftconv_nd_torch(x, k[None], s if s is not None else torch.zeros(H, dtype=dtype))
+    xg, kg = x.cuda(), k.cuda()
+    sg = s.cuda() if s is not None else None
+    with torch.no_grad():
+        y = F.fftconv2d_bhl(xg, kg, sg)
+    assert y.dtype == dtype
+    assert rel_l2(y_ref, y) < tol
+    # the three passes (a forward that keeps its state for the backward) on the same inputs
+    xr = xg.clone().requires_grad_(True)
+    y3 = F.fftconv2d_bhl(xr, kg, sg)
+    assert rel_l2(y3.detach(), y) < (1e-5 if dtype == torch.float32 else 1e-2)
+
+
+def test_image192_config4_fp32_against_float64():
+    torch.manual_seed(7)
+    x = torch.randn(2, 8, 128, 128)
+    k = torch.randn(8, 128, 128)
+    s = torch.randn(8)
+    with torch.no_grad():
+        y = F.fftconv2d_bhl(x.cuda(), k.cuda(), s.cuda())
+    assert rel_l2(fftconv_nd_np(x.numpy(), k[None].numpy(), s.numpy()), y) < 2e-6
