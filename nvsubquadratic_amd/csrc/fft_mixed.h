@@ -92,8 +92,9 @@ __device__ __forceinline__ void dft_mixed(float2* v) {
 
 // Radix of the pass after sub-transforms of length NS: 3 first for a 3 * 2^m
 // length, then powers of two of at most RMAX.
-constexpr int mixed_radix(int N, int NS, int RMAX) {
-  return (NS == 1 && N % 3 == 0) ? 3 : ((N / NS) < RMAX ? (N / NS) : RMAX);
+// R2 (nonzero): the radix of the pass right after the radix-3 one.
+constexpr int mixed_radix(int N, int NS, int RMAX, int R2 = 0) {
+  return (NS == 1 && N % 3 == 0) ? 3 : (R2 && NS == 3) ? R2 : ((N / NS) < RMAX ? (N / NS) : RMAX);
 }
 
 // First-pass loader that returns zero for inputs r >= RZ of each radix-R
@@ -201,36 +202,37 @@ __device__ __forceinline__ void mixed_pass(LD& ld, ST& st, const TW& tws) {
 // through st_last, the passes between in the LDS tile st_lds / ld_lds), radix
 // at most RMAX after the radix-3 pass.  Ends with a barrier (WAVE: a wave
 // sync).
-template <int N, int NS, bool INV, int M, int T, bool TMAJOR, int RMAX, bool WAVE, class LDF, class STL, class LDL,
-          class STF, class TW>
+template <int N, int NS, bool INV, int M, int T, bool TMAJOR, int RMAX, bool WAVE, int R2, class LDF, class STL,
+          class LDL, class STF, class TW>
 __device__ __forceinline__ void fft_mixed_rec(LDF& ld_first, STL& st_lds, LDL& ld_lds, STF& st_last, const TW& tws) {
-  constexpr int R = mixed_radix(N, NS, RMAX);
+  constexpr int R = mixed_radix(N, NS, RMAX, R2);
   constexpr bool FIRST = NS == 1;
   constexpr bool LAST = NS * R == N;
   if constexpr (FIRST && LAST) {
     mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_first, st_last, tws);
   } else if constexpr (FIRST) {
     mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_first, st_lds, tws);
-    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX, WAVE>(ld_first, st_lds, ld_lds, st_last, tws);
+    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX, WAVE, R2>(ld_first, st_lds, ld_lds, st_last, tws);
   } else if constexpr (LAST) {
     mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_lds, st_last, tws);
   } else {
     mixed_pass<N, R, NS, INV, M, T, TMAJOR, WAVE>(ld_lds, st_lds, tws);
-    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX, WAVE>(ld_first, st_lds, ld_lds, st_last, tws);
+    fft_mixed_rec<N, NS * R, INV, M, T, TMAJOR, RMAX, WAVE, R2>(ld_first, st_lds, ld_lds, st_last, tws);
   }
 }
 
 template <int N, bool INV, int M, int T, bool TMAJOR, int RMAX, class LDF, class TILE, class STF, class TW>
 __device__ __forceinline__ void fft_mixed(LDF& ld_first, TILE& tile, STF& st_last, const TW& tws) {
   static_assert(mixed_len(N), "fft_mixed: length must be 2^m or 3 * 2^m");
-  fft_mixed_rec<N, 1, INV, M, T, TMAJOR, RMAX, false>(ld_first, tile, tile, st_last, tws);
+  fft_mixed_rec<N, 1, INV, M, T, TMAJOR, RMAX, false, 0>(ld_first, tile, tile, st_last, tws);
 }
 
-// fft_mixed by one wave on transforms that it alone reads and writes.
-template <int N, bool INV, int M, bool TMAJOR, int RMAX, class LDF, class TILE, class STF, class TW>
+// fft_mixed by one wave on transforms that it alone reads and writes; R2 as
+// in mixed_radix.
+template <int N, bool INV, int M, bool TMAJOR, int RMAX, int R2 = 0, class LDF, class TILE, class STF, class TW>
 __device__ __forceinline__ void fft_mixed_wave(LDF& ld_first, TILE& tile, STF& st_last, const TW& tws) {
   static_assert(mixed_len(N), "fft_mixed_wave: length must be 2^m or 3 * 2^m");
-  fft_mixed_rec<N, 1, INV, M, 64, TMAJOR, RMAX, true>(ld_first, tile, tile, st_last, tws);
+  fft_mixed_rec<N, 1, INV, M, 64, TMAJOR, RMAX, true, R2>(ld_first, tile, tile, st_last, tws);
 }
 
 }  // namespace nsq

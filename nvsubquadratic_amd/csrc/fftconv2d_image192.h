@@ -46,6 +46,14 @@ struct Img192Cfg {
   static constexpr int COLS = kI3N2 / WAVES;    // slot columns per wave in phase B
   static constexpr int CM = T == 512 ? 4 : 2;   // columns per transform batch
   static constexpr int CHUNKS = COLS / CM;
+  // Column passes (measured at config 4): 3, 4, 16 for 4 columns per wave;
+  // 3, 8, 8 for 2, where 3, 4, 16 leaves 40 lanes idle in the radix-16 pass
+  // (0.73 -> 0.85 ms) and 3, 4, 4, 4 adds a pass (0.80 ms).  The rows run
+  // 3, 4, 8: a radix-4 pass after the radix-3 one stores without bank
+  // conflicts (its butterfly groups of 3 land 12 slots apart), a radix-8 one
+  // 2-way (24 apart).
+  static constexpr int CRMAX = CM == 4 ? 16 : 8;
+  static constexpr int CR2 = CM == 4 ? 4 : 0;
   static constexpr int LDS = (kI3Rows * kI3RS + WAVES * CM * kI3CS + kI3F) * 8;
   static_assert(kI3Rows % WAVES == 0 && kI3N2 % WAVES == 0 && COLS % CM == 0, "Img192Cfg: wave split");
   static_assert(LDS <= 160 * 1024, "Img192Cfg: LDS");
@@ -95,7 +103,7 @@ __global__ __launch_bounds__(T) void nd2_image192_fwd_kernel(const typename Elem
     };
     TailZeroLoad<3, 2, true, decltype(ld)> ld1{ld};
     I3Lines tl{rows, kI3RS};
-    fft_mixed_wave<kI3N2, false, C::ROWS, false, 8>(ld1, tl, tl, tws);
+    fft_mixed_wave<kI3N2, false, C::ROWS, false, 8, 4>(ld1, tl, tl, tws);
 #pragma unroll
     for (int i = 0; i < C::ROWS * (kI3N2 / 2) / 64; ++i) {  // slot pair (p, 96 - p) of row m; p = 0: (0, 48)
       const int jj = lane + 64 * i, m = jj / (kI3N2 / 2), p = jj - m * (kI3N2 / 2);
@@ -133,7 +141,7 @@ __global__ __launch_bounds__(T) void nd2_image192_fwd_kernel(const typename Elem
 #pragma unroll
         for (int r = 0; r < 3; ++r) kn[0][r] = kc[kI3N2 * kI3F + lane + 64 * r];
       }
-      fft_mixed_wave<kI3F, false, C::CM, false, 8>(ldc1, sl, sl, tws);
+      fft_mixed_wave<kI3F, false, C::CM, false, C::CRMAX, C::CR2>(ldc1, sl, sl, tws);
       // the spectral product, read by the inverse's first pass (which reads
       // every value of the batch before it writes), in its call order
       struct Prod {
@@ -159,7 +167,7 @@ __global__ __launch_bounds__(T) void nd2_image192_fwd_kernel(const typename Elem
         const int r = n - o0;
         if (r >= 0 && r < S0) tile[r * kI3RS + c0 + m] = v;
       };
-      fft_mixed_wave<kI3F, true, C::CM, false, 8>(ldp, sl, stc, tws);
+      fft_mixed_wave<kI3F, true, C::CM, false, C::CRMAX, C::CR2>(ldp, sl, stc, tws);
     }
   }
   __syncthreads();
@@ -182,7 +190,7 @@ __global__ __launch_bounds__(T) void nd2_image192_fwd_kernel(const typename Elem
     }
     mixed_sync<true>();
     I3Lines tl{rows, kI3RS};
-    fft_mixed_wave<kI3N2, true, C::ROWS, false, 8>(tl, tl, tl, tws);
+    fft_mixed_wave<kI3N2, true, C::ROWS, false, 8, 4>(tl, tl, tl, tws);
     const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load(s, h)) : 0.f;
     const int cpr = S2 >> 3;  // 8-sample chunks per output row
     const int nr = min(C::ROWS, S0 - rw0);
