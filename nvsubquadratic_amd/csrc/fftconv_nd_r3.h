@@ -120,6 +120,78 @@ __global__ __launch_bounds__(192) void r3_plane_fwd_kernel(const typename Elem<D
   }
 }
 
+// The same forward pass with wave-local transforms: 256 threads, each wave
+// owning MR / 4 rows of a row tile and N / 4 columns, so every pass
+// synchronises on the wave's own in-order LDS operations (fft_mixed_wave) and
+// a plane takes workgroup barriers only between its phases.
+template <int N2, int F1, int DT, bool AL, bool THIRD>
+__global__ __launch_bounds__(256) void r3_plane_fwd_w_kernel(const typename Elem<DT>::T* __restrict__ src, int n0,
+                                                             int n1, int len, float2* __restrict__ ws, int64_t spec,
+                                                             const float2* __restrict__ tw) {
+  using C = R3PlaneCfg<N2, F1>;
+  constexpr int N = C::N, RS = C::RS, T = 256, MR = C::MR, W = T / 64;
+  constexpr int MRW = MR / W, NW = N / W;
+  static_assert(MR % W == 0 && N % W == 0, "r3_plane_fwd_w_kernel: wave split");
+  __shared__ float2 P[F1 * RS];
+  __shared__ float2 twl[C::Q];
+  const int64_t plane = blockIdx.x;  // bh * n0 + a0
+  const int64_t xoff = plane * n1 * len;
+  const auto tws = stage_roots<C::Q, T>(twl, tw);
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  __syncthreads();
+  for (int rb = 0; rb < n1; rb += MR) {
+    const int r0 = (rb + MR <= F1 ? rb : F1 - MR) + wv * MRW;  // the wave's rows of the tile
+    LdsTile<RS, true> rows{P + r0 * RS};
+    auto ld = [&](int m, int n) -> float2 {
+      const int a1 = r0 + m;
+      const bool ok = a1 < n1;
+      return load_pair_nb<DT, AL>(src + xoff + int64_t(ok ? a1 : 0) * len, 2 * int64_t(n), ok ? len : 0);
+    };
+    TailZeroLoad<3, 2, THIRD, decltype(ld)> ld1{ld};
+    fft_mixed_wave<N, false, MRW, false, C::ROWR>(ld1, rows, rows, tws);
+    const int lane = opaque_tid() & 63;
+    constexpr int SLOTS = (MRW * (N / 2) + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+      const int s = lane + i * 64;
+      if (s >= MRW * (N / 2)) continue;
+      const int m = s / (N / 2), p = s - m * (N / 2);
+      const bool p0 = (p == 0);
+      float2* z = P + (r0 + m) * RS;
+      const int pb = pad16(p0 ? N / 2 : N - p);
+      float2 A, Bc;
+      real_unpack(p0, z[pad16(p)], z[pb], tws.template root<2 * N>(p), A, Bc);
+      z[pad16(p)] = A;
+      z[pb] = p0 ? Bc : cconj(Bc);
+    }
+    __syncthreads();  // a last tile moved back overlaps rows of other waves
+  }
+  const int c0 = wv * NW;  // the wave's packed columns
+  LdsCols<RS> cols{P, c0};
+  auto ldc = [&](int m, int n) -> float2 {
+    const bool ok = n < n1;
+    const float2 v = P[(ok ? n : 0) * RS + pad16(c0 + m)];
+    return make_float2(ok ? v.x : 0.f, ok ? v.y : 0.f);
+  };
+  TailZeroLoad<3, 2, THIRD, decltype(ldc)> ldc1{ldc};
+  fft_mixed_wave<F1, false, NW, true, C::COLR>(ldc1, cols, cols, tws);
+  __syncthreads();
+  float2* out = ws + (plane / n0) * spec + (plane % n0) * int64_t(F1) * C::FH;
+  const int t = opaque_tid();
+#pragma unroll 4
+  for (int e = t; e < F1 * N; e += T) {
+    const int k1 = e / N, j = e - k1 * N;
+    const float2 v = P[k1 * RS + pad16(j)];
+    if (j != 0) out[int64_t(k1) * C::FH + j] = v;
+  }
+  for (int k1 = t; k1 < F1; k1 += T) {
+    const float2 v = P[k1 * RS];
+    const float2 zc = cconj(P[(k1 ? F1 - k1 : 0) * RS]);
+    out[int64_t(k1) * C::FH] = cscale(cadd(v, zc), 0.5f);
+    out[int64_t(k1) * C::FH + N] = mul_neg_i(cscale(csub(v, zc), 0.5f));
+  }
+}
+
 // Inverse: plane [F1][FH] -> inverse along axis 1 keeping rows [off1, off1 +
 // n1out) (moved to the front) -> inverse real rows, crop [off2, off2 + w2),
 // epilogue (RowInvOut: ND_OUT_Y with shortcut, or ND_OUT_GK with the lag

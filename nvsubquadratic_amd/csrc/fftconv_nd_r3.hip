@@ -43,6 +43,15 @@ static bool with_r3_col(const NdPlan& p, F&& f) {
   }
 }
 
+// NSQ_R3_PLANE_WAVE=0: the plane passes with workgroup-wide transforms.
+static bool r3_plane_wave() {
+  static const bool on = [] {
+    const char* e = std::getenv("NSQ_R3_PLANE_WAVE");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 // Forward inner-axis passes of nbh blocks of [n0][n1][len] real values: the
 // plane kernels (3D), or the row kernels (2D, n1 = 1).
 template <int DT>
@@ -73,8 +82,12 @@ static bool r3_inner_fwd(const NdPlan& p, const void* src, int64_t nbh, int n0, 
     constexpr int N2 = decltype(NC)::value, F1 = decltype(FC)::value;
     const dim3 grid(unsigned(nbh * n0));
     auto go = [&](auto a, auto th) {
-      hipLaunchKernelGGL((r3_plane_fwd_kernel<N2, F1, DT, decltype(a)::value, decltype(th)::value>), grid,
-                         dim3(R3PlaneCfg<N2, F1>::T), 0, st, (const ET*)src, n0, n1, len, ws, p.spec, tw);
+      if (r3_plane_wave())
+        hipLaunchKernelGGL((r3_plane_fwd_w_kernel<N2, F1, DT, decltype(a)::value, decltype(th)::value>), grid,
+                           dim3(256), 0, st, (const ET*)src, n0, n1, len, ws, p.spec, tw);
+      else
+        hipLaunchKernelGGL((r3_plane_fwd_kernel<N2, F1, DT, decltype(a)::value, decltype(th)::value>), grid,
+                           dim3(R3PlaneCfg<N2, F1>::T), 0, st, (const ET*)src, n0, n1, len, ws, p.spec, tw);
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
