@@ -311,6 +311,129 @@ __global__ __launch_bounds__(192) void r3_plane_inv_kernel(const float2* __restr
   }
 }
 
+// The same inverse with wave-local transforms (256 threads): each wave owns
+// N / 4 packed columns, then a quarter of each row tile, so only the phase
+// boundaries take workgroup barriers.
+template <int N2, int F1, int DT, int MODE, bool HAS_S>
+__global__ __launch_bounds__(256) void r3_plane_inv_w_kernel(const float2* __restrict__ ws, int64_t spec, int n0,
+                                                             int off1, int n1out, RowInvOut o,
+                                                             const float2* __restrict__ tw) {
+  using C = R3PlaneCfg<N2, F1>;
+  using ET = typename Elem<DT>::T;
+  constexpr int N = C::N, RS = C::RS, T = 256, MR = C::MR, W = T / 64, NW = N / W;
+  static_assert(MR % W == 0 && C::MRB % W == 0 && N % W == 0, "r3_plane_inv_w_kernel: wave split");
+  __shared__ float2 P[F1 * RS];
+  const int64_t plane = blockIdx.x;  // bh * n0 + a0
+  const int64_t bh = plane / n0;
+  const int a0 = int(plane - bh * n0);
+  const float2* in = ws + bh * spec + int64_t(a0) * F1 * C::FH;
+  __shared__ float2 twl[C::Q];
+  const auto tws = stage_roots<C::Q, T>(twl, tw);
+  const int t = opaque_tid();
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int lane = t & 63;
+#pragma unroll 8
+  for (int e = t; e < F1 * N; e += T) {
+    const int k1 = e / N, j = e - k1 * N;
+    P[k1 * RS + pad16(j)] = in[int64_t(k1) * C::FH + j];
+  }
+  __syncthreads();
+  for (int k1 = t; k1 < F1; k1 += T) {  // pack DC + i Nyquist into column 0
+    const float2 w = in[int64_t(k1) * C::FH + N];
+    const float2 v = P[k1 * RS];
+    P[k1 * RS] = make_float2(v.x - w.y, v.y + w.x);
+  }
+  __syncthreads();
+  const int c0 = wv * NW;  // the wave's packed columns
+  LdsCols<RS> cols{P, c0};
+  auto stc = [&](int m, int k, float2 v) {
+    const int r = k - off1;
+    if (r >= 0 && r < n1out) P[r * RS + pad16(c0 + m)] = v;
+  };
+  fft_mixed_wave<F1, true, NW, true, C::COLR>(cols, cols, stc, tws);
+  __syncthreads();
+  const ET* __restrict__ aux = (const ET*)o.aux;
+  const int h = int(bh % o.H);
+  const float sv = HAS_S ? Elem<DT>::round(Elem<DT>::load((const ET*)o.s, h)) : 0.f;
+  const bool fast = MODE == ND_OUT_Y && (o.off2 & 1) == 0 && (o.w2 & 7) == 0 && o.w2 <= 2 * N &&
+                    ((reinterpret_cast<uintptr_t>(o.out) | (HAS_S ? reinterpret_cast<uintptr_t>(o.aux) : 0)) & 15) == 0;
+  // The wave's MRT / W rows of a tile of MRT rows from row r0t: repack,
+  // inverse, epilogue (tiles do not overlap: no barrier between them).
+  auto row_tile = [&](auto mrc, int r0t) {
+    constexpr int MRT = decltype(mrc)::value / W;
+    const int r0 = r0t + wv * MRT;
+    constexpr int SLOTS = (MRT * (N / 2) + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+      const int s = lane + i * 64;
+      if (s >= MRT * (N / 2)) continue;
+      const int m = s / (N / 2), p = s - m * (N / 2);
+      const bool p0 = (p == 0);
+      float2* z = P + (r0 + m) * RS;
+      const int pb = pad16(p0 ? N / 2 : N - p);
+      const float2 b = z[pb];
+      float2 zp, zq;
+      real_repack(p0, z[pad16(p)], p0 ? b : cconj(b), tws.template root<2 * N>(p), zp, zq);
+      z[pad16(p)] = zp;
+      z[pb] = zq;
+    }
+    mixed_sync<true>();
+    LdsTile<RS, true> rows{P + r0 * RS};
+    fft_mixed_wave<N, true, MRT, false, C::ROWR>(rows, rows, rows, tws);
+    const int nrows = (n1out - r0) < MRT ? ((n1out - r0) > 0 ? (n1out - r0) : 0) : MRT;
+    if constexpr (MODE == ND_OUT_Y) {
+      if (fast) {
+        // 8 consecutive kept samples per thread: four complex values from
+        // LDS, one 16-byte shortcut load, one 16-byte store.
+        const int cpr = o.w2 >> 3;
+        const int64_t row0 = plane * n1out + r0;
+        const RowBuf<DT, false> ab(aux + row0 * o.w2, HAS_S ? nrows * o.w2 : 0);
+        const RowBuf<DT, true> ob((ET*)o.out + row0 * o.w2, nrows * o.w2);
+        for (int ch = lane; ch < nrows * cpr; ch += 64) {
+          const int m = ch / cpr, c8 = (ch - m * cpr) * 8;
+          const int e0 = m * o.w2 + c8;
+          Win8<DT, true> a{};
+          if constexpr (HAS_S) a.load(ab, e0);
+          const float2* zr = P + (r0 + m) * RS;
+          const int nc = (c8 + o.off2) >> 1;
+          float yv[8];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float2 z = zr[pad16(nc + u)];
+            yv[2 * u] = epilogue<DT>(z.x * o.scale, HAS_S, sv, a.at(2 * u));
+            yv[2 * u + 1] = epilogue<DT>(z.y * o.scale, HAS_S, sv, a.at(2 * u + 1));
+          }
+          store8<DT, true>(ob, e0, yv);
+        }
+        return;
+      }
+    }
+    for (int e = lane; e < nrows * o.w2; e += 64) {
+      const int m = e / o.w2, c = e - m * o.w2;
+      const int sidx = c + o.off2;
+      const float2 zz = P[(r0 + m) * RS + pad16(sidx >> 1)];
+      const float v = ((sidx & 1) ? zz.y : zz.x) * o.scale;
+      const int64_t idx = (plane * n1out + r0 + m) * o.w2 + c;
+      if constexpr (MODE == ND_OUT_Y) {
+        const float a = HAS_S ? Elem<DT>::load(aux, idx) : 0.f;
+        Elem<DT>::store((ET*)o.out, idx, epilogue<DT>(v, HAS_S, sv, a));
+      } else {
+        ((float*)o.out)[idx] = v;
+        if (o.gs && c == o.ga2 && a0 == o.ga0 && r0 + m == o.ga1) o.gs[bh] = v;
+      }
+    }
+  };
+  for (int r0 = 0; r0 < n1out;) {  // in place, so tiles do not overlap: whole tiles, then MRB rows
+    if (r0 + MR <= F1) {
+      row_tile(std::integral_constant<int, MR>{}, r0);
+      r0 += MR;
+    } else {
+      if constexpr (C::MRB > 0) row_tile(std::integral_constant<int, C::MRB>{}, r0);
+      r0 += C::MRB > 0 ? C::MRB : F1;  // (MRB = 0: MR divides F1 and this branch is not reached)
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Row passes of the 2D plan: real transforms along the last axis between the
 // [rows][len] tensor (row r = (bh, a0), a0 < n0) and row a0 of spectrum block

@@ -120,8 +120,12 @@ static bool r3_inner_inv(const NdPlan& p, const float2* ws, int64_t nbh, int n0,
     constexpr int N2 = decltype(NC)::value, F1 = decltype(FC)::value;
     const dim3 grid(unsigned(nbh * n0));
     auto go = [&](auto hs) {
-      hipLaunchKernelGGL((r3_plane_inv_kernel<N2, F1, DT, MODE, decltype(hs)::value>), grid,
-                         dim3(R3PlaneCfg<N2, F1>::T), 0, st, ws, p.spec, n0, off1, n1out, o, tw);
+      if (r3_plane_wave())
+        hipLaunchKernelGGL((r3_plane_inv_w_kernel<N2, F1, DT, MODE, decltype(hs)::value>), grid, dim3(256), 0, st,
+                           ws, p.spec, n0, off1, n1out, o, tw);
+      else
+        hipLaunchKernelGGL((r3_plane_inv_kernel<N2, F1, DT, MODE, decltype(hs)::value>), grid,
+                           dim3(R3PlaneCfg<N2, F1>::T), 0, st, ws, p.spec, n0, off1, n1out, o, tw);
     };
     has_s ? go(std::true_type{}) : go(std::false_type{});
   });
