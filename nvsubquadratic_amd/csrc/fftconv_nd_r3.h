@@ -447,6 +447,7 @@ struct R3RowCfg {
   static constexpr int RS = N2 + N2 / 16;  // LDS row stride (pad16 positions)
   static constexpr int T = 192;
   static constexpr int M = 2304 / N2;      // 96, 48 or 24 rows
+  static constexpr int MW = M / (T / 64);  // rows of each wave
   static constexpr int R = 16;             // largest power-of-two radix
   static constexpr int SLOTS = (M * (N2 / 2) + T - 1) / T;
 };
@@ -464,14 +465,18 @@ __global__ __launch_bounds__(192) void r3_row_fwd_kernel(const typename Elem<DT>
   const auto tws = stage_roots<2 * N, T>(twl, tw);
   __syncthreads();
   const int r0 = int(blockIdx.x) * M;
-  LdsTile<RS, true> rows{P};
+  // each wave transforms its own M / 3 rows (fft_mixed_wave: no workgroup
+  // barrier inside the transform)
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  LdsTile<RS, true> rows{P + wv * C::MW * RS};
   auto ld = [&](int m, int n) -> float2 {
-    const int r = r0 + m;
+    const int r = r0 + wv * C::MW + m;
     const bool ok = r < nrows;
     return load_pair_nb<DT, AL>(src + int64_t(ok ? r : 0) * len, 2 * int64_t(n), ok ? len : 0);
   };
   TailZeroLoad<3, 2, THIRD, decltype(ld)> ld1{ld};
-  fft_mixed<N, false, M, T, false, C::R>(ld1, rows, rows, tws);
+  fft_mixed_wave<N, false, C::MW, false, C::R>(ld1, rows, rows, tws);
+  __syncthreads();
   const int ts = opaque_tid();
 #pragma unroll
   for (int i = 0; i < C::SLOTS; ++i) {
@@ -536,8 +541,10 @@ __global__ __launch_bounds__(192) void r3_row_inv_kernel(const float2* __restric
     z[pad16(p0 ? N / 2 : N - p)] = zq;
   }
   __syncthreads();
-  LdsTile<RS, true> rows{P};
-  fft_mixed<N, true, M, T, false, C::R>(rows, rows, rows, tws);
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  LdsTile<RS, true> rows{P + wv * C::MW * RS};
+  fft_mixed_wave<N, true, C::MW, false, C::R>(rows, rows, rows, tws);
+  __syncthreads();
   const ET* __restrict__ aux = (const ET*)o.aux;
   const int nr = (nrows - r0) < M ? (nrows - r0) : M;
   const bool fast = MODE == ND_OUT_Y && (o.off2 & 1) == 0 && (o.w2 & 7) == 0 && o.w2 <= 2 * N &&
