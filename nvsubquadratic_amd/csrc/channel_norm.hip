@@ -197,15 +197,16 @@ __device__ __forceinline__ void load_tile_u(const typename Elem<DT>::T* __restri
 
 // Channels-last side: item q = (s, cv), s = q mod TS fastest (consecutive lanes
 // read consecutive LDS words), cv a run of VW channels (one 16-byte access).
-template <int DT, int VW>
+template <int DT, int VW, int MODE>
 __global__ __launch_bounds__(kThreads) void chnorm_fwd_kernel(const typename Elem<DT>::T* __restrict__ y,
                                                               const typename Elem<DT>::T* __restrict__ v,
                                                               const float* __restrict__ w,
                                                               const float* __restrict__ bias,
                                                               typename Elem<DT>::T* __restrict__ out, int C,
                                                               int64_t S, int TS, int64_t tiles_per_b, int64_t ntiles,
-                                                              float eps, int gated, int act, int out_blh, int mode) {
+                                                              float eps, int gated, int act, int out_blh) {
 #pragma clang fp contract(off)
+  constexpr int mode = MODE;  // a compile-time norm: RMS / L2 kernels carry no LayerNorm code
   extern __shared__ float smem[];
   const int ld = TS + 1;
   float* U = smem;
@@ -246,13 +247,14 @@ __global__ __launch_bounds__(kThreads) void chnorm_fwd_kernel(const typename Ele
   }
 }
 
-template <int DT, int VW>
+template <int DT, int VW, int MODE>
 __global__ __launch_bounds__(kThreads) void chnorm_bwd_kernel(
     const typename Elem<DT>::T* __restrict__ dout, const typename Elem<DT>::T* __restrict__ y,
     const typename Elem<DT>::T* __restrict__ v, const float* __restrict__ w, typename Elem<DT>::T* __restrict__ dy,
     typename Elem<DT>::T* __restrict__ dv, float* __restrict__ dw_part, float* __restrict__ db_part, int C, int64_t S,
-    int TS, int64_t tiles_per_b, int64_t ntiles, float eps, int gated, int act, int in_blh, int mode) {
+    int TS, int64_t tiles_per_b, int64_t ntiles, float eps, int gated, int act, int in_blh) {
 #pragma clang fp contract(off)
+  constexpr int mode = MODE;
   extern __shared__ float smem[];
   const int ld = TS + 1;
   float* U = smem;                  // u, then xhat
@@ -485,15 +487,28 @@ void allow_lds(K* kernel, size_t lds) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                               int(lds));
 }
+// The kernels take the norm as a template argument.
+template <class F>
+void with_mode(int mode, F&& f) {
+  if (mode == CHN_LN)
+    f(std::integral_constant<int, CHN_LN>{});
+  else if (mode == CHN_L2)
+    f(std::integral_constant<int, CHN_L2>{});
+  else
+    f(std::integral_constant<int, CHN_RMS>{});
+}
 template <int DT, int VW>
 void launch_fwd_vw(const void* y, const void* v, const float* w, const float* bias, void* out, int64_t B, int C,
                    int64_t S, int TS, float eps, int gated, int act, int out_blh, int mode, hipStream_t st) {
   using T = typename Elem<DT>::T;
   const int64_t tpb = ceil_div(S, int64_t(TS)), nt = B * tpb;
   const size_t lds = fwd_lds(C, TS, VW);
-  allow_lds(&chnorm_fwd_kernel<DT, VW>, lds);
-  hipLaunchKernelGGL((chnorm_fwd_kernel<DT, VW>), dim3(unsigned(nt)), dim3(kThreads), lds, st, (const T*)y,
-                     (const T*)v, w, bias, (T*)out, C, S, TS, tpb, nt, eps, gated, act, out_blh, mode);
+  with_mode(mode, [&](auto mc) {
+    constexpr int M = decltype(mc)::value;
+    allow_lds(&chnorm_fwd_kernel<DT, VW, M>, lds);
+    hipLaunchKernelGGL((chnorm_fwd_kernel<DT, VW, M>), dim3(unsigned(nt)), dim3(kThreads), lds, st, (const T*)y,
+                       (const T*)v, w, bias, (T*)out, C, S, TS, tpb, nt, eps, gated, act, out_blh);
+  });
 }
 template <int DT>
 void launch_fwd(const void* y, const void* v, const float* w, void* out, int64_t B, int C, int64_t S, float eps,
@@ -511,10 +526,13 @@ void launch_bwd_vw(const void* dout, const void* y, const void* v, const float* 
                    int mode, hipStream_t st) {
   using T = typename Elem<DT>::T;
   const size_t lds = bwd_lds(C, p.TS, VW, mode == CHN_LN);
-  allow_lds(&chnorm_bwd_kernel<DT, VW>, lds);
-  hipLaunchKernelGGL((chnorm_bwd_kernel<DT, VW>), dim3(unsigned(p.nwg)), dim3(kThreads), lds, st, (const T*)dout,
-                     (const T*)y, (const T*)v, w, (T*)dy, (T*)dv, part, partb, C, S, p.TS, p.tiles_per_b, p.ntiles,
-                     eps, gated, act, out_blh, mode);
+  with_mode(mode, [&](auto mc) {
+    constexpr int M = decltype(mc)::value;
+    allow_lds(&chnorm_bwd_kernel<DT, VW, M>, lds);
+    hipLaunchKernelGGL((chnorm_bwd_kernel<DT, VW, M>), dim3(unsigned(p.nwg)), dim3(kThreads), lds, st,
+                       (const T*)dout, (const T*)y, (const T*)v, w, (T*)dy, (T*)dv, part, partb, C, S, p.TS,
+                       p.tiles_per_b, p.ntiles, eps, gated, act, out_blh);
+  });
 }
 // part: nwg rows of C dw partials (LN: then nwg rows of dbias partials, partb).
 template <int DT>
