@@ -129,45 +129,106 @@ __global__ __launch_bounds__(T) void nd2_image192_fwd_kernel(const typename Elem
         return n < S0 ? tile[n * kI3RS + c0 + m] : make_float2(0.f, 0.f);
       };
       TailZeroLoad<3, 2, true, decltype(ldc)> ldc1{ldc};
-      // The inverse's first pass (radix 3, butterfly (m, j = lane)) reads
-      // elements lane + 64 r of each column m: their filter values are issued
-      // here, so their L2 latency overlaps the forward transform.
-      float2 kf[C::CM][3], kn[C::CM][3];
-#pragma unroll
-      for (int m = 0; m < C::CM; ++m)
-#pragma unroll
-        for (int r = 0; r < 3; ++r) kf[m][r] = kc[(c0 + m) * kI3F + lane + 64 * r];
-      if (c0 == 0) {  // the packed column's Nyquist filter column (wave-uniform)
-#pragma unroll
-        for (int r = 0; r < 3; ++r) kn[0][r] = kc[kI3N2 * kI3F + lane + 64 * r];
-      }
-      fft_mixed_wave<kI3F, false, C::CM, false, C::CRMAX, C::CR2>(ldc1, sl, sl, tws);
-      // the spectral product, read by the inverse's first pass (which reads
-      // every value of the batch before it writes), in its call order
-      struct Prod {
-        const float2* sc;
-        const float2 (&kf)[C::CM][3];
-        const float2 (&kn)[C::CM][3];
-        int c0;
-        int q = 0;
-        __device__ __forceinline__ float2 operator()(int m, int n) {
-          const int r = q % 3;
-          ++q;
-          const float2 X = sc[m * kI3CS + n];
-          if (c0 + m == 0) {  // packed DC / Nyquist column: Y = Xd Kdc + i Xn Knyq
-            const float2 Xm = sc[m * kI3CS + (n == 0 ? 0 : kI3F - n)];
-            float2 xd, xn;
-            pack_split(X, Xm, xd, xn);
-            return cadd(cmul(xd, kf[0][r]), mul_i(cmul(xn, kn[0][r])));
-          }
-          return cmul(X, kf[m][r]);
-        }
-      } ldp{sc, kf, kn, c0};
       auto stc = [&](int m, int n, float2 v) {  // keep rows [o0, o0 + S0)
         const int r = n - o0;
         if (r >= 0 && r < S0) tile[r * kI3RS + c0 + m] = v;
       };
-      fft_mixed_wave<kI3F, true, C::CM, false, C::CRMAX, C::CR2>(ldp, sl, stc, tws);
+      if constexpr (C::CM == 2) {
+        // Forward passes 3, 8, then one pass in registers: the forward's last
+        // radix-8 pass (butterfly j < 24 of column m = lane / 24 reads and
+        // writes elements j + 24 r), the filter product, and the inverse's
+        // first pass, the inverse running radix 8, 8, 3 (its first pass reads
+        // the same elements j + 24 r).  One LDS round trip fewer.
+        const bool act = lane < 2 * 24;
+        const int m = act ? lane / 24 : 0, j = lane - 24 * (lane / 24);
+        const int c = c0 + m;
+        float2 kf[8], kn[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) kf[r] = act ? kc[c * kI3F + j + 24 * r] : make_float2(0.f, 0.f);
+        if (c0 == 0) {  // the packed column's Nyquist filter column (wave-uniform)
+#pragma unroll
+          for (int r = 0; r < 8; ++r) kn[r] = act ? kc[kI3N2 * kI3F + j + 24 * r] : make_float2(0.f, 0.f);
+        }
+        mixed_pass<kI3F, 3, 1, false, 2, 64, false, true>(ldc1, sl, tws);
+        mixed_pass<kI3F, 8, 3, false, 2, 64, false, true>(sl, sl, tws);
+        float2 v[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = sc[m * kI3CS + j + 24 * r];
+        mixed_sync<true>();
+#pragma unroll
+        for (int r = 1; r < 8; ++r) v[r] = cmul(v[r], tws.template root<kI3F>(r * j));
+        dft<8, false>(v);  // X[j + 24 r]
+        if (c0 == 0) {
+          // -k of k = j + 24 r: (24 - j) + 24 (7 - r) in lane 24 - j for j > 0,
+          // 24 ((8 - r) mod 8) in this lane for j = 0
+          const int src = j == 0 ? lane : 24 - j;
+          float2 pm[8];
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const float2 o = v[7 - r];
+            pm[r] = make_float2(__shfl(o.x, src), __shfl(o.y, src));
+            if (j == 0) pm[r] = v[(8 - r) & 7];
+          }
+          if (c == 0) {  // packed DC / Nyquist column: Y = Xd Kdc + i Xn Knyq
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              float2 xd, xn;
+              pack_split(v[r], pm[r], xd, xn);
+              v[r] = cadd(cmul(xd, kf[r]), mul_i(cmul(xn, kn[r])));
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) v[r] = cmul(v[r], kf[r]);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) v[r] = cmul(v[r], kf[r]);
+        }
+        dft<8, true>(v);  // the inverse's first pass (no twiddles): elements 8 j + r
+        if (act) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) sc[m * kI3CS + 8 * j + r] = v[r];
+        }
+        mixed_sync<true>();
+        mixed_pass<kI3F, 8, 8, true, 2, 64, false, true>(sl, sl, tws);
+        mixed_pass<kI3F, 3, 64, true, 2, 64, false, true>(sl, stc, tws);
+      } else {
+        // The inverse's first pass (radix 3, butterfly (m, j = lane)) reads
+        // elements lane + 64 r of each column m: their filter values are issued
+        // here, so their L2 latency overlaps the forward transform.
+        float2 kf[C::CM][3], kn[C::CM][3];
+#pragma unroll
+        for (int m = 0; m < C::CM; ++m)
+#pragma unroll
+          for (int r = 0; r < 3; ++r) kf[m][r] = kc[(c0 + m) * kI3F + lane + 64 * r];
+        if (c0 == 0) {  // the packed column's Nyquist filter column (wave-uniform)
+#pragma unroll
+          for (int r = 0; r < 3; ++r) kn[0][r] = kc[kI3N2 * kI3F + lane + 64 * r];
+        }
+        fft_mixed_wave<kI3F, false, C::CM, false, C::CRMAX, C::CR2>(ldc1, sl, sl, tws);
+        // the spectral product, read by the inverse's first pass (which reads
+        // every value of the batch before it writes), in its call order
+        struct Prod {
+          const float2* sc;
+          const float2 (&kf)[C::CM][3];
+          const float2 (&kn)[C::CM][3];
+          int c0;
+          int q = 0;
+          __device__ __forceinline__ float2 operator()(int m, int n) {
+            const int r = q % 3;
+            ++q;
+            const float2 X = sc[m * kI3CS + n];
+            if (c0 + m == 0) {  // packed DC / Nyquist column: Y = Xd Kdc + i Xn Knyq
+              const float2 Xm = sc[m * kI3CS + (n == 0 ? 0 : kI3F - n)];
+              float2 xd, xn;
+              pack_split(X, Xm, xd, xn);
+              return cadd(cmul(xd, kf[0][r]), mul_i(cmul(xn, kn[0][r])));
+            }
+            return cmul(X, kf[m][r]);
+          }
+        } ldp{sc, kf, kn, c0};
+        fft_mixed_wave<kI3F, true, C::CM, false, C::CRMAX, C::CR2>(ldp, sl, stc, tws);
+      }
     }
   }
   __syncthreads();
